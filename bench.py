@@ -1,0 +1,189 @@
+"""Benchmark of the fermix_amd hot path on one MI355X.
+
+`python bench.py [--gpus 1] [--steps K] [--warmup W]` prints ONE JSON line. A "step"
+is one pass of the hot path over one batch of synthetic input already resident in HBM:
+
+* the headline workload: fp32 slogpf forward, B = 4096,
+  n = 128, S = A - A^T with A iid N(0, 1) from numpy default_rng(0) (jax, whose
+  jax.random.key(0) the BASELINE names, is not installed here or on the GPU box);
+* reported beside it in "workloads": configs[0] (slogdet forward, B = 4096, n = 128)
+  and configs[2] (slogdet forward + VJP, B = 1024, n = 512) when the library supports
+  it.
+
+`roofline` is the dominant kernel's algorithmic bytes per launch (B (4 n^2 + 8): read
+each matrix once, write sign and logabs) divided by its average launch duration over
+the timed region, timed with HIP events on the stream the kernel is launched on.
+`cpu_baseline` times the CPU oracle (the reference's generic path restated in numpy,
+oracle/generic.py) on a bounded sample of the same workload on this host, rank 0 only,
+with one BLAS thread.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def _parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--only", default=None, help="comma list of workloads (c1,c2,c3)")
+    return p.parse_args()
+
+
+def _time_gpu(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / steps, wall
+
+
+def _inputs(B, n, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    A = rng.standard_normal((B, n, n), dtype=np.float32)
+    if scale != 1.0:
+        A *= np.float32(scale)
+    return A
+
+
+def bench_c2(steps, warmup):
+    import torch
+    import fermix_amd
+
+    B, n = 4096, 128
+    A = _inputs(B, n, 0)
+    S = torch.from_numpy(A - np.swapaxes(A, 1, 2)).cuda()
+    fn = lambda: fermix_amd.slogpf(S, skew_symmetrize=False)
+    ms, wall = _time_gpu(fn, steps, warmup)
+    return dict(name="slogpf_fwd", B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
+                bytes=B * (4 * n * n + 8), sample=S[:64].cpu().numpy())
+
+
+def bench_c1(steps, warmup):
+    import torch
+    import fermix_amd
+
+    B, n = 4096, 128
+    A = torch.from_numpy(_inputs(B, n, 0)).cuda()
+    fn = lambda: fermix_amd.slogdet(A)
+    ms, wall = _time_gpu(fn, steps, warmup)
+    return dict(name="slogdet_fwd", B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
+                bytes=B * (4 * n * n + 8), sample=A[:64].cpu().numpy())
+
+
+def cpu_baseline(sample, which):
+    """The CPU oracle on a bounded sample, one thread (matrices/s)."""
+    from threadpoolctl import threadpool_limits
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import generic as g
+
+    f = g.slogpf_generic if which == "slogpf" else g.slogdet_generic
+    with threadpool_limits(limits=1):
+        f(sample[:4])
+        reps, t = 0, 0.0
+        t0 = time.perf_counter()
+        while t < 10.0:
+            f(sample)
+            reps += 1
+            t = time.perf_counter() - t0
+    return reps * sample.shape[0] / t, reps, t
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(
+            json.dumps({"error": "fermix_amd benchmarks one GPU only (the hot path shards "
+                        "trivially over the batch; no multi-GPU run is part of this build)",
+                        "n_gpus": args.gpus}),
+            flush=True,
+        )
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm GPU visible"}), flush=True)
+        sys.exit(1)
+    only = set(args.only.split(",")) if args.only else {"c1", "c2"}
+    res = {}
+    if "c2" in only:
+        res["c2"] = bench_c2(args.steps, args.warmup)
+        print(f"# c2 slogpf fwd: {res['c2']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
+    if "c1" in only:
+        res["c1"] = bench_c1(args.steps, args.warmup)
+        print(f"# c1 slogdet fwd: {res['c1']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
+    head = res.get("c2") or res.get("c1")
+    achieved = head["bytes"] / (head["ms"] * 1e-3) / 1e9
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": None,
+    }
+    cpu = None
+    if not args.no_cpu:
+        which = "slogpf" if head["name"].startswith("slogpf") else "slogdet"
+        rate, reps, t = cpu_baseline(head["sample"], which)
+        cpu = {
+            "value": round(rate, 2),
+            "unit": "matrices/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"oracle {which}_generic (numpy restatement of the reference's generic "
+            f"path), {head['sample'].shape[0]} of the {head['B']} n={head['n']} matrices x "
+            f"{reps} reps in {t:.1f} s, one thread",
+        }
+    workloads = {
+        k: {"workload": v["name"], "B": v["B"], "n": v["n"], "ms_per_step": round(v["ms"], 5),
+            "matrices_per_s": round(v["rate"], 1),
+            "hbm_frac": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        for k, v in res.items()
+    }
+    line = {
+        "metric": "fp32 slogdet/slogpf matrices/s at B=4096,n=128; fwd+grad matrices/s at n=512",
+        "value": round(head["rate"], 1),
+        "unit": "matrices/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (numpy default_rng(0) N(0,1); jax.random absent)",
+        "config": {"workload": f"{head['name']} B={head['B']} n={head['n']}", "B": head["B"],
+                   "n": head["n"], "baseline_config": "configs[1]" if head is res.get("c2") else "configs[0]"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "workloads": workloads,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

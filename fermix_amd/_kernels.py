@@ -1,0 +1,111 @@
+"""Torch plumbing around the C ABI: allocate outputs / workspace on the input's device,
+pass raw pointers and the current HIP stream. Inputs are (B, n, n) contiguous float32
+tensors on a ROCm device; no numerics happen here."""
+
+import torch
+
+from ._lib import check, lib
+
+
+def _stream(t):
+    return ctypes_ptr(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ctypes_ptr(x):
+    return int(x) if x else None
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _workspace(nbytes, device):
+    if nbytes == 0:
+        return None, 0
+    return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+
+
+def _check_input(A):
+    if not A.is_cuda:
+        raise RuntimeError("fermix_amd kernels need a tensor on a ROCm GPU")
+    if A.dtype != torch.float32 or A.dim() != 3 or not A.is_contiguous():
+        raise RuntimeError("internal: expected a contiguous (B, n, n) float32 tensor")
+
+
+def lu_padded_size(n):
+    return int(lib().fx_lu_padded_size(n))
+
+
+def pf_padded_size(n):
+    return int(lib().fx_pf_padded_size(n))
+
+
+def slogdet(A):
+    """(sign, logabs) of each (n, n) matrix of A (B, n, n)."""
+    _check_input(A)
+    B, n, _ = A.shape
+    sign = torch.empty(B, dtype=A.dtype, device=A.device)
+    logabs = torch.empty(B, dtype=A.dtype, device=A.device)
+    L = lib()
+    ws, wsb = _workspace(L.fx_slogdet_f32_workspace(B, n), A.device)
+    st = L.fx_slogdet_f32(_ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(ws), wsb, _stream(A))
+    check(st, "fx_slogdet_f32")
+    return sign, logabs
+
+
+def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False):
+    """(sign, logabs, invT, lu, perm) with the optional outputs None when not asked for;
+    lu / perm are padded to N = lu_padded_size(n)."""
+    _check_input(A)
+    B, n, _ = A.shape
+    dev = A.device
+    sign = torch.empty(B, dtype=A.dtype, device=dev)
+    logabs = torch.empty(B, dtype=A.dtype, device=dev)
+    invT = torch.empty_like(A) if want_inv else None
+    lu = perm = None
+    if want_lu and n > 0:
+        N = lu_padded_size(n)
+        lu = torch.empty((B, N, N), dtype=A.dtype, device=dev)
+        perm = torch.empty((B, N), dtype=torch.int32, device=dev)
+    L = lib()
+    ws, wsb = _workspace(L.fx_slogdet_parts_f32_workspace(B, n), dev)
+    st = L.fx_slogdet_parts_f32(
+        _ptr(A), B, n, int(bool(zero_singular)), _ptr(sign), _ptr(logabs), _ptr(invT),
+        _ptr(lu), _ptr(perm), _ptr(ws), wsb, _stream(A),
+    )
+    check(st, "fx_slogdet_parts_f32")
+    return sign, logabs, invT, lu, perm
+
+
+def slogpf(A, skew_symmetrize):
+    _check_input(A)
+    B, n, _ = A.shape
+    sign = torch.empty(B, dtype=A.dtype, device=A.device)
+    logabs = torch.empty(B, dtype=A.dtype, device=A.device)
+    L = lib()
+    ws, wsb = _workspace(L.fx_slogpf_f32_workspace(B, n), A.device)
+    st = L.fx_slogpf_f32(
+        _ptr(A), B, n, int(bool(skew_symmetrize)), _ptr(sign), _ptr(logabs), _ptr(ws), wsb,
+        _stream(A),
+    )
+    check(st, "fx_slogpf_f32")
+    return sign, logabs
+
+
+def slogpf_factors(A, skew_symmetrize):
+    """(sign, logabs, gbuf (B, N/16, N, 16), d (B, N/2), perm (B, N))."""
+    _check_input(A)
+    B, n, _ = A.shape
+    dev = A.device
+    N = pf_padded_size(n)
+    sign = torch.empty(B, dtype=A.dtype, device=dev)
+    logabs = torch.empty(B, dtype=A.dtype, device=dev)
+    gbuf = torch.zeros((B, N // 16, N, 16), dtype=A.dtype, device=dev)
+    d = torch.empty((B, N // 2), dtype=A.dtype, device=dev)
+    perm = torch.empty((B, N), dtype=torch.int32, device=dev)
+    st = lib().fx_slogpf_factors_f32(
+        _ptr(A), B, n, int(bool(skew_symmetrize)), _ptr(sign), _ptr(logabs), _ptr(gbuf),
+        _ptr(d), _ptr(perm), _stream(A),
+    )
+    check(st, "fx_slogpf_factors_f32")
+    return sign, logabs, gbuf, d, perm

@@ -1,0 +1,67 @@
+"""ctypes binding of the in-tree HIP library ``libfermix_amd.so`` (C ABI declared in
+``include/fermix.h``). The product path has no fallback: if the library is missing the
+calls raise ``FermixLibraryError``."""
+
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfermix_amd.so")
+
+FX_OK = 0
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); every function declared in include/fermix.h
+SIGNATURES = {
+    "fx_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "fx_abi_version": (ctypes.c_int, []),
+    "fx_lu_padded_size": (_i32, [_i32]),
+    "fx_pf_padded_size": (_i32, [_i32]),
+    "fx_slogdet_f32_workspace": (_sz, [_i64, _i32]),
+    "fx_slogdet_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _sz, _p]),
+    "fx_slogdet_parts_f32_workspace": (_sz, [_i64, _i32]),
+    "fx_slogdet_parts_f32": (
+        ctypes.c_int,
+        [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _sz, _p],
+    ),
+    "fx_slogpf_f32_workspace": (_sz, [_i64, _i32]),
+    "fx_slogpf_f32": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _sz, _p]),
+    "fx_slogpf_factors_f32": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p]),
+}
+
+
+class FermixLibraryError(RuntimeError):
+    """The HIP library is missing, fails to load, or a call returned an error status."""
+
+
+_lib = None
+
+
+def lib():
+    """The loaded library (loaded once). Raises FermixLibraryError if it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FermixLibraryError(
+                f"{LIB_PATH} is missing: build it with `python -m fermix_amd.build` "
+                "(fermix_amd has no non-HIP fallback)"
+            )
+        try:
+            h = ctypes.CDLL(LIB_PATH)
+        except OSError as e:  # pragma: no cover - environment specific
+            raise FermixLibraryError(f"cannot load {LIB_PATH}: {e}") from e
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(h, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = h
+    return _lib
+
+
+def check(status, what):
+    if status != FX_OK:
+        msg = lib().fx_status_string(status).decode()
+        raise FermixLibraryError(f"{what}: {msg} (status {status})")

@@ -1,0 +1,125 @@
+"""Public API of fermix_amd: ``slogdet``, ``slogpf``, ``det``, ``pf`` -- the interface of
+ChenAo-Phys/fermix (src/fermix/api.py:148-227) on torch tensors, with the kernels
+underneath replaced by hand-written HIP kernels for gfx950 (``libfermix_amd.so``).
+
+Conventions kept from the reference:
+* input (..., n, n); every leading dimension is a batch dimension (api.py:100-103);
+* slogdet returns (sign, logabs) with sign exactly +-1 / 0 and logabs -inf for an
+  exactly zero pivot, the jnp.linalg.slogdet convention (_fallback.py:6-9);
+* slogpf skew-symmetrises its input as (a - a^T)/2 unless skew_symmetrize=False, and
+  odd n gives (0, -inf) (api.py:122-125); pf of odd n is 0;
+* unsupported dtype -> TypeError, bad shape / block / prec -> ValueError
+  (api.py:24-31,92-97; _field.py:265-275);
+* differentiable (torch.autograd, forward mode, torch.func.vmap / grad / jvp) with the
+  reference's rules (_diff.py:101-333): d logabs = tr(A^-1 dA), d sign = 0; slogpf
+  d logabs = tr(S^-1 dS)/2 (gradient w.r.t. ``a`` S^-T/2 through the
+  skew-symmetrisation); exactly singular inputs get a zero (finite) gradient; the
+  primal of a differentiated call is bit-identical to the plain forward.
+
+Device handling: the product path is the HIP library on a ROCm GPU. A CPU tensor
+raises ``FermixDeviceError`` (the reference's generic XLA fallback is not part of this
+build) -- there is no silent CPU path.
+"""
+
+import torch
+
+from . import _diff
+from ._tune import check_block, check_prec
+
+_FLOAT_KINDS = (torch.float32, torch.float64, torch.complex64, torch.complex128)
+
+
+class FermixFallbackWarning(UserWarning):
+    """Kept for API compatibility with the reference (api.py:19-21). fermix_amd never
+    falls back silently; see FermixDeviceError."""
+
+
+class FermixDeviceError(RuntimeError):
+    """The input is not on a ROCm GPU; fermix_amd runs only its HIP kernels."""
+
+
+def _prep(a):
+    if not isinstance(a, torch.Tensor):
+        raise TypeError(f"fermix_amd expects a torch.Tensor, got {type(a).__name__}")
+    if a.dtype not in _FLOAT_KINDS:
+        raise TypeError(
+            f"fermix supports float32, float64, complex64 and complex128, got {a.dtype}"
+        )
+    if a.dim() < 2 or a.shape[-1] != a.shape[-2]:
+        raise ValueError(f"expected (..., n, n), got {tuple(a.shape)}")
+    if a.dtype != torch.float32:
+        raise TypeError(
+            f"fermix_amd implements the float32 path (the north-star dtype); got {a.dtype}"
+        )
+    return a
+
+
+def _on_device(a):
+    if not a.is_cuda:
+        raise FermixDeviceError(
+            "fermix_amd runs on a ROCm GPU only (the reference's generic CPU fallback is "
+            "not part of this build); move the input to a 'cuda' device"
+        )
+
+
+def _flat(a):
+    batch = a.shape[:-2]
+    n = a.shape[-1]
+    return a.reshape((-1, n, n)).contiguous(), batch, n
+
+
+def slogdet(a, *, prec=None, unroll_steps=None, block=None):
+    """Sign and log|det| of a batch of matrices ``a`` (..., n, n) (reference
+    ``slogdet``, api.py:148-174). prec: "ieee" (default; fp32 MFMA updates) or
+    "tf32x3" (accepted for compatibility: its purpose, fp32-level accuracy, is what the
+    IEEE fp32 MFMA path gives on gfx950, which has no TF32 type). block / unroll_steps:
+    accepted for compatibility and validated; the gfx950 kernels choose their blocking
+    from n (fermix_amd._tune)."""
+    a = _prep(a)
+    check_prec(prec)
+    check_block(block)
+    _on_device(a)
+    A, batch, n = _flat(a)
+    sign, logabs = _diff.slogdet(A)
+    return sign.reshape(batch), logabs.reshape(batch)
+
+
+def slogpf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
+    """Sign and log|pf| of a batch of skew-symmetric matrices (reference ``slogpf``,
+    api.py:177-193): S = (a - a^T)/2 unless skew_symmetrize=False (then ``a`` must be
+    exactly skew); odd n gives (0, -inf)."""
+    a = _prep(a)
+    check_prec(prec)
+    _on_device(a)
+    A, batch, n = _flat(a)
+    if n % 2 == 1:
+        z = torch.zeros(batch, dtype=a.dtype, device=a.device)
+        return z, torch.full(batch, -float("inf"), dtype=a.dtype, device=a.device)
+    sign, logabs = _diff.slogpf(A, bool(skew_symmetrize))
+    return sign.reshape(batch), logabs.reshape(batch)
+
+
+def det(a, *, prec=None, unroll_steps=None, block=None):
+    """Determinant of a batch of matrices (reference ``det``, api.py:196-212):
+    sign * exp(logabs) of the same factorisation."""
+    a = _prep(a)
+    check_prec(prec)
+    check_block(block)
+    _on_device(a)
+    A, batch, n = _flat(a)
+    return _diff.det(A).reshape(batch)
+
+
+def pf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
+    """Pfaffian of a batch of skew-symmetric matrices (reference ``pf``, api.py:215-227);
+    odd n gives 0."""
+    a = _prep(a)
+    check_prec(prec)
+    _on_device(a)
+    A, batch, n = _flat(a)
+    if n % 2 == 1:
+        return torch.zeros(batch, dtype=a.dtype, device=a.device)
+    return _diff.pf(A, bool(skew_symmetrize)).reshape(batch)
+
+
+__all__ = ["slogdet", "slogpf", "det", "pf", "FermixFallbackWarning", "FermixDeviceError"]

@@ -1,0 +1,69 @@
+// Device helpers shared by the fermix_amd HIP kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fx {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// Order-preserving key of a pivot candidate: |x| as unsigned bits plus one, 0 for "not a
+// candidate". Non-negative floats order like their bit patterns, so an integer max over
+// keys is an exact max over magnitudes (the +1 lifts |x| = 0 above "no candidate").
+__device__ __forceinline__ unsigned cand_key(float x, bool ok) {
+  return ok ? (__float_as_uint(fabsf(x)) + 1u) : 0u;
+}
+
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_u32(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+// Maximum of v over the 64 lanes, returned wave-uniform: a 16-lane all-reduce with DPP
+// (quad xor 1, quad xor 2, half-row mirror, row mirror) followed by a scalar max over the
+// four rows' results.
+__device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
+  v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
+  v = max(v, dpp_u32<0x140>(v));  // row_mirror
+  unsigned r0 = __builtin_amdgcn_readlane(v, 0);
+  unsigned r1 = __builtin_amdgcn_readlane(v, 16);
+  unsigned r2 = __builtin_amdgcn_readlane(v, 32);
+  unsigned r3 = __builtin_amdgcn_readlane(v, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+
+// Lowest lane whose predicate holds (wave-uniform); 64 if none.
+__device__ __forceinline__ int first_lane(bool p) {
+  unsigned long long m = __ballot(p);
+  return m ? (int)__builtin_ctzll(m) : 64;
+}
+
+// fp32 MFMA 16x16x4: D = A(16x4) * B(4x16) + C. Lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; D/C element (4*(l/16)+v, l%16) sits in item v of lane l.
+__device__ __forceinline__ v4f mfma16(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Compiler-level ordering point for LDS traffic exchanged between the lanes of one
+// wave (the hardware executes one wave's LDS instructions in order).
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Guarded reciprocal: 1/0 -> 0 (a zero pivot contributes nothing to the multipliers).
+__device__ __forceinline__ float safe_rcp(float d) { return d != 0.0f ? 1.0f / d : 0.0f; }
+
+}  // namespace fx

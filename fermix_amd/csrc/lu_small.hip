@@ -1,0 +1,287 @@
+// Fused slogdet for n <= 128: one workgroup (4 waves) per matrix, the whole matrix
+// resident in LDS, blocked right-looking LU with partial pivoting in 16-column panels.
+//
+// Reference roles replaced (ChenAo-Phys/fermix): the LU inner panel (src/fermix/_lu.py:
+// 54-224), the inter-panel and U-row updates (_lu.py:228-330) and the trailing GEMM
+// (_lu.py:334-393), which the reference issues as 26 separate launches at n = 128
+// (_lu.py:543-611); here they are one launch.
+//
+// Per panel k (rows/cols from r0 = 16k):
+//   * wave 0 factors the m x 16 panel in registers (lane l owns rows R*l .. R*l+R-1):
+//     pivot = largest |a| among the unassigned rows (ties: lowest row), found with a
+//     DPP max over order-preserving integer keys; rows are pivoted virtually inside
+//     the panel and written back in the new order; it also forms X = L11^-1 (lane c
+//     holds column c) and the map src[new position] = old row;
+//   * the trailing 16-column strips are gathered through src, U12 = X * A12 and
+//     A22 -= L21 * U12 run on fp32 MFMA 16x16x4, and the strip is stored in the new row
+//     order (each strip is read completely before it is written, and strips own
+//     disjoint columns, so the permutation is applied in place);
+//   * look-ahead: wave 0 updates strip 0 (the next panel's columns) itself and factors
+//     the next panel while waves 1-3 update the remaining strips.
+// With FACT the left (already factored) columns are permuted along, so the LDS holds
+// the packed LU of P A in the final row order, and the composed permutation is kept.
+//
+// n < N is padded with the identity (exact: [[A,0],[0,I]] = [[L,0],[0,I]][[U,0],[0,I]]).
+#include "common.h"
+#include "fermix_internal.h"
+
+namespace fx {
+
+template <int N>
+struct LuSmall {
+  static constexpr int LDA = N + 4;        // row stride in LDS (floats)
+  static constexpr int R = (N + 63) / 64;  // panel rows per lane
+  static constexpr int NP = N / 16;        // panels
+};
+
+// Factor the 16-column panel at (r0, r0) (wave 0 only). Accumulates the pivot signs,
+// log|pivot|, zero-pivot flag and swap count into the wave-uniform state.
+template <int N, bool FACT>
+__device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, int* perm,
+                                         int lane, float& sgn, float& lab, int& zero, int& nsw) {
+  constexpr int LDA = LuSmall<N>::LDA, R = LuSmall<N>::R;
+  float a[R][16];
+  int pos[R];
+  bool valid[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int row = R * lane + i;
+    valid[i] = (row >= r0) && (row < N);
+    pos[i] = row;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) a[i][j] = valid[i] ? As[row * LDA + r0 + j] : 0.0f;
+  }
+  float xcol[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int posc = r0 + j;
+    unsigned kb = 0;
+    int ib = 0;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const unsigned k = cand_key(a[i][j], valid[i] && pos[i] >= posc);
+      if (k > kb) { kb = k; ib = i; }
+    }
+    const unsigned gk = wave_max_u32(kb);
+    const int pl = first_lane(kb == gk);
+    const int is = readlane_i(ib, pl);
+    float u[16];
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      float v = a[0][jj];
+#pragma unroll
+      for (int i = 1; i < R; ++i) v = (is == i) ? a[i][jj] : v;
+      u[jj] = readlane_f(v, pl);
+    }
+    int pv = pos[0];
+#pragma unroll
+    for (int i = 1; i < R; ++i) pv = (is == i) ? pos[i] : pv;
+    const int pp = readlane_i(pv, pl);
+    // swap positions posc <-> pp
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (valid[i] && pos[i] == posc) pos[i] = pp;
+      if (lane == pl && i == is) pos[i] = posc;
+    }
+    nsw += (pp != posc) ? 1 : 0;
+    const float piv = u[j];
+    if (piv == 0.0f) {
+      zero = 1;
+    } else {
+      lab += logf(fabsf(piv));
+      if (piv < 0.0f) sgn = -sgn;
+    }
+    const float rcp = safe_rcp(piv);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (valid[i] && pos[i] > posc) {
+        const float l = a[i][j] * rcp;
+        a[i][j] = l;
+#pragma unroll
+        for (int jj = j + 1; jj < 16; ++jj) a[i][jj] = fmaf(-l, u[jj], a[i][jj]);
+      }
+    }
+    // row j of X = L11^-1: X[j][c] = -sum_{k<j} L11[j][k] X[k][c], X[j][j] = 1
+    float x = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < j; ++kk) x = fmaf(-u[kk], xcol[kk], x);
+    xcol[j] = (lane == j) ? 1.0f : x;
+  }
+  // write the panel back in the new row order, the position map and X
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (valid[i]) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) As[pos[i] * LDA + r0 + j] = a[i][j];
+      src[pos[i]] = R * lane + i;
+    }
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) X[k * 16 + lane] = xcol[k];
+  }
+  if (FACT) {
+    int pv[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) pv[i] = valid[i] ? perm[R * lane + i] : 0;
+    wave_lds_fence();
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      if (valid[i]) perm[pos[i]] = pv[i];
+  }
+  wave_lds_fence();
+}
+
+// Update one trailing strip (columns c0 .. c0+15, rows r0 .. N-1): gather the rows
+// through src, U12 = X * A12, A22 -= L21 * U12 (fp32 MFMA), store in the new order.
+template <int N>
+__device__ __forceinline__ void lu_strip(float* As, int r0, int c0, const int* src, const float* X,
+                                         int lane) {
+  constexpr int LDA = LuSmall<N>::LDA;
+  constexpr int MAXT = (N / 16 > 1) ? N / 16 - 1 : 1;
+  const int nt = (N - r0 - 16) / 16;
+  const int li = lane & 15, g = lane >> 4;
+  const int col = c0 + li;
+  float tb[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) tb[t] = As[src[r0 + 4 * t + g] * LDA + col];
+  v4f ct[MAXT];
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    if (i < nt) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) ct[i][v] = As[src[r0 + 16 + 16 * i + 4 * g + v] * LDA + col];
+    }
+  }
+  v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) u = mfma16(X[li * 16 + 4 * t + g], tb[t], u);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) As[(r0 + 4 * g + v) * LDA + col] = u[v];
+  wave_lds_fence();
+  float ub[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) ub[t] = As[(r0 + 4 * t + g) * LDA + col];
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    if (i < nt) {
+      const int rb = r0 + 16 + 16 * i;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) ct[i] = mfma16(-As[(rb + li) * LDA + r0 + 4 * t + g], ub[t], ct[i]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) As[(rb + 4 * g + v) * LDA + col] = ct[i][v];
+    }
+  }
+}
+
+// Apply the panel's row permutation to a strip of already factored columns (FACT only).
+template <int N>
+__device__ __forceinline__ void lu_permute_strip(float* As, int r0, int c0, const int* src, int lane) {
+  constexpr int LDA = LuSmall<N>::LDA;
+  constexpr int MAXR = N / 4;
+  const int col = c0 + (lane & 15), g = lane >> 4;
+  float v[MAXR];
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) {
+    const int p = r0 + g + 4 * i;
+    if (p < N) v[i] = As[src[p] * LDA + col];
+  }
+  wave_lds_fence();
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) {
+    const int p = r0 + g + 4 * i;
+    if (p < N) As[p * LDA + col] = v[i];
+  }
+}
+
+template <int N, bool FACT>
+__global__ __launch_bounds__(256) void lu_small_kernel(const float* __restrict__ A, int n,
+                                                       float* __restrict__ sign_out,
+                                                       float* __restrict__ logabs_out,
+                                                       float* __restrict__ lu_out,
+                                                       int* __restrict__ perm_out) {
+  constexpr int LDA = LuSmall<N>::LDA, NP = LuSmall<N>::NP;
+  __shared__ float As[N * LDA];
+  __shared__ int srcs[2][N];
+  __shared__ float Xs[2][256];
+  __shared__ int perm[N];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const float* Ab = A + b * (int64_t)n * n;
+  for (int e = tid; e < N * N; e += 256) {
+    const int r = e / N, c = e - r * N;
+    As[r * LDA + c] = (r < n && c < n) ? Ab[r * n + c] : (r == c ? 1.0f : 0.0f);
+  }
+  if (FACT)
+    for (int r = tid; r < N; r += 256) perm[r] = r;
+  __syncthreads();
+
+  float sgn = 1.0f, lab = 0.0f;
+  int zero = 0, nsw = 0;
+  if (wave == 0) lu_panel<N, FACT>(As, 0, srcs[0], Xs[0], perm, lane, sgn, lab, zero, nsw);
+  __syncthreads();
+  for (int k = 0; k < NP; ++k) {
+    const int r0 = 16 * k;
+    const int S = NP - 1 - k;
+    const int* src = srcs[k & 1];
+    const float* X = Xs[k & 1];
+    if (wave == 0) {
+      if (S > 0) {
+        lu_strip<N>(As, r0, r0 + 16, src, X, lane);
+        lu_panel<N, FACT>(As, r0 + 16, srcs[(k + 1) & 1], Xs[(k + 1) & 1], perm, lane, sgn, lab,
+                          zero, nsw);
+      }
+    } else {
+      for (int s = wave; s < S; s += 3) lu_strip<N>(As, r0, r0 + 16 + 16 * s, src, X, lane);
+      if (FACT)
+        for (int q = wave - 1; q < k; q += 3) lu_permute_strip<N>(As, r0, 16 * q, src, lane);
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    sign_out[b] = zero ? 0.0f : ((nsw & 1) ? -sgn : sgn);
+    logabs_out[b] = zero ? -INFINITY : lab;
+  }
+  if (FACT) {
+    float* Lb = lu_out + b * (int64_t)N * N;
+    for (int e = tid; e < N * N; e += 256) {
+      const int r = e / N, c = e - r * N;
+      Lb[e] = As[r * LDA + c];
+    }
+    for (int r = tid; r < N; r += 256) perm_out[b * N + r] = perm[r];
+  }
+}
+
+template <int N, bool FACT>
+static int launch_n(const float* A, int n, int64_t batch, float* sign, float* logabs, float* lu,
+                    int* perm, hipStream_t s) {
+  hipLaunchKernelGGL((lu_small_kernel<N, FACT>), dim3((unsigned)batch), dim3(256), 0, s, A, n,
+                     sign, logabs, lu, perm);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+int lu_small_padded(int n) { return ((n + 15) / 16) * 16; }
+
+template <bool FACT>
+static int dispatch(const float* A, int n, int64_t batch, float* sign, float* logabs, float* lu,
+                    int* perm, hipStream_t s) {
+  switch (lu_small_padded(n)) {
+    case 16: return launch_n<16, FACT>(A, n, batch, sign, logabs, lu, perm, s);
+    case 32: return launch_n<32, FACT>(A, n, batch, sign, logabs, lu, perm, s);
+    case 48: return launch_n<48, FACT>(A, n, batch, sign, logabs, lu, perm, s);
+    case 64: return launch_n<64, FACT>(A, n, batch, sign, logabs, lu, perm, s);
+    case 80: return launch_n<80, FACT>(A, n, batch, sign, logabs, lu, perm, s);
+    case 96: return launch_n<96, FACT>(A, n, batch, sign, logabs, lu, perm, s);
+    case 112: return launch_n<112, FACT>(A, n, batch, sign, logabs, lu, perm, s);
+    case 128: return launch_n<128, FACT>(A, n, batch, sign, logabs, lu, perm, s);
+    default: return FX_ERR_UNSUPPORTED;
+  }
+}
+
+int launch_lu_small(const float* A, int n, int64_t batch, float* sign, float* logabs, float* lu,
+                    int* perm, hipStream_t s) {
+  if (lu) return dispatch<true>(A, n, batch, sign, logabs, lu, perm, s);
+  return dispatch<false>(A, n, batch, sign, logabs, nullptr, nullptr, s);
+}
+
+}  // namespace fx

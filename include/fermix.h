@@ -1,0 +1,104 @@
+/* fermix_amd C ABI: batched fp32 slogdet / slogpf (and the factors and inverses their
+ * gradients need) on AMD Instinct MI355X (gfx950), as hand-written HIP kernels.
+ *
+ * This is the drop-in boundary for the hot path of ChenAo-Phys/fermix: each entry
+ * point replaces the group of Pallas calls the reference issues through
+ * `_pcall` (src/fermix/_field.py:357-389) for one role, cited per function below. The
+ * reference binds its kernels inside JAX; the XLA FFI handler a maintainer would add on
+ * top of this header is shown in INTEGRATION.md.
+ *
+ * Conventions (all entry points):
+ *  - matrices are row-major, contiguous, batch-major: a[b * n * n + i * n + j];
+ *  - the caller owns every buffer; the library never allocates device memory, never
+ *    synchronises, and only enqueues work on `stream` (a hipStream_t; NULL = the legacy
+ *    default stream);
+ *  - `workspace` is caller-provided device memory of at least the size reported by the
+ *    matching *_workspace function (0 means no workspace is needed; NULL allowed then);
+ *  - the return value is a status code (FX_OK on success); numerical edge cases are
+ *    encoded in the values (an exactly zero pivot gives sign 0 and logabs -inf);
+ *  - calls are reentrant; the library keeps no mutable global state.
+ */
+#ifndef FERMIX_AMD_H
+#define FERMIX_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FX_OK 0
+#define FX_ERR_INVALID_ARGUMENT 1 /* bad pointer, batch < 0, n < 0, ... */
+#define FX_ERR_WORKSPACE 2        /* workspace missing or too small */
+#define FX_ERR_LAUNCH 3           /* a HIP launch failed (hipGetLastError) */
+#define FX_ERR_UNSUPPORTED 4      /* size not covered by the compiled kernels */
+
+typedef void* fx_stream_t; /* hipStream_t */
+
+/* Human-readable text of a status code (static storage). */
+const char* fx_status_string(int status);
+
+/* ABI version of this header (major * 100 + minor). */
+int fx_abi_version(void);
+
+/* Padded order N >= n of the LU factors returned by fx_slogdet_parts_f32 (identity
+ * padding; the reference pads to its block size the same way, src/fermix/_common.py:
+ * 527-539). */
+int32_t fx_lu_padded_size(int32_t n);
+
+/* Padded order N of the Parlett-Reid factors of fx_slogpf_factors_f32. */
+int32_t fx_pf_padded_size(int32_t n);
+
+/* ---------------------------------------------------------------- slogdet
+ * sign[b], logabs[b] of det(a[b]) for b < batch: sign exactly +1 / -1, or 0 with
+ * logabs = -inf for an exactly zero pivot.
+ * Replaces `_lu_core` (src/fermix/_lu.py:543-611) as called by `_slogdet_core`
+ * (src/fermix/_diff.py:42-49); kernels K1-K4 of the reference (_lu.py:54-393). */
+size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n);
+int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs,
+                   void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* The same factorisation as fx_slogdet_f32 (identical arithmetic, so sign / logabs are
+ * bit-identical to it) plus, each optional (NULL to skip):
+ *  - inv_t (batch, n, n): A^-T formed with the zero pivots of U replaced by 1; zero for
+ *    members with a non-finite result and, if zero_singular != 0, for members with an
+ *    exactly zero pivot;
+ *  - lu (batch, N, N), N = fx_lu_padded_size(n): packed L (unit, strictly lower) and U
+ *    of P A' where A' = [[A, 0], [0, I]];
+ *  - perm (batch, N): (P A')[c] = A'[perm[c]].
+ * Replaces `_lu_parts` (src/fermix/_inverse.py:502-531) as called by `_parts`
+ * (src/fermix/_diff.py:62-77); kernels K7-K10 (_inverse.py:35-499). */
+size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n);
+int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_singular,
+                         float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm,
+                         void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* ---------------------------------------------------------------- slogpf
+ * sign[b], logabs[b] of pf(S[b]), S = (a - a^T) / 2 if skew_symmetrize != 0, else
+ * S = a (which must then be exactly skew-symmetric). Odd n gives (0, -inf).
+ * Replaces `_pf_core` (src/fermix/_pf.py:497-570) as called by `_slogpf_core`
+ * (src/fermix/_diff.py:52-59), with the skew-symmetrisation of `_slogpf`
+ * (src/fermix/api.py:124-125) fused into the load; kernels K5-K6 (_pf.py:59-382). */
+size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n);
+int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign,
+                  float* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* The Parlett-Reid factors P S' P^T = L D L^T of the same run (S' = S padded with
+ * [[0,1],[-1,0]] blocks to N = fx_pf_padded_size(n)):
+ *  - gbuf (batch, N/16, N, 16): block k's tau_t (column 2t) and w_t (column 2t+1),
+ *    indexed by the original row; entries of rows assigned before the pair step are
+ *    zero, rows assigned before block k are unspecified;
+ *  - d (batch, N/2): the pair pivots d_s = (P S' P^T reduced)[2s, 2s+1];
+ *  - perm (batch, N): final position -> original row.
+ * sign / logabs are bit-identical to fx_slogpf_f32. Replaces `_pf_core_factors`
+ * (src/fermix/_pf.py:497-514). */
+int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
+                          float* sign, float* logabs, float* gbuf, float* d, int32_t* perm,
+                          fx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERMIX_AMD_H */

@@ -1,0 +1,105 @@
+"""Float64 truth from the mathematics -- TEST INFRASTRUCTURE (pins ``oracle.generic``
+and checks the GPU results). Written from the definitions, independent of the
+algorithms under test where possible:
+
+* ``slogdet64`` -- numpy's LAPACK slogdet in float64 (the reference's own tests use
+  it, ``tests/test_fermix.py:153-155``);
+* ``pf_brute`` -- the Pfaffian as a signed sum over perfect matchings (expansion along
+  the first row), exact up to float64 rounding, n <= 10;
+* ``pf_pr64`` -- a float64 Parlett-Reid (the textbook algorithm, cross-checked against
+  ``pf_brute`` and pf^2 = det);
+* ``adjT_brute`` -- d det / dA = adj(A)^T by cofactors;
+* ``pf_grad_brute`` -- d pf / dS by minor Pfaffians.
+"""
+
+import math
+import numpy as np
+
+
+def slogdet64(A):
+    s, l = np.linalg.slogdet(np.asarray(A, np.float64))
+    return s, l
+
+
+def pf_brute(S):
+    """Pfaffian of one skew matrix by the perfect-matching expansion
+    pf(S) = sum_j (-1)^(j+1) s_0j pf(S without rows/cols 0, j) (0-based j >= 1)."""
+    S = np.asarray(S, np.float64)
+    n = S.shape[0]
+    if n % 2:
+        return 0.0
+    if n == 0:
+        return 1.0
+    total = 0.0
+    rest = list(range(1, n))
+    for t, j in enumerate(rest):
+        if S[0, j] == 0.0:
+            continue
+        keep = [k for k in rest if k != j]
+        total += (-1) ** t * S[0, j] * pf_brute(S[np.ix_(keep, keep)])
+    return total
+
+
+def pf_pr64(S):
+    """(sign, log|pf|) of one skew matrix by Parlett-Reid with partial pivoting in
+    float64: pivot the largest |entry| of column k below row k into row/col k+1."""
+    A = np.array(S, np.float64)
+    n = A.shape[0]
+    if n % 2:
+        return 0.0, -math.inf
+    sign, log = 1.0, 0.0
+    for k in range(0, n - 1, 2):
+        kp = k + 1 + int(np.argmax(np.abs(A[k + 1 :, k])))
+        if kp != k + 1:
+            A[[k + 1, kp], :] = A[[kp, k + 1], :]
+            A[:, [k + 1, kp]] = A[:, [kp, k + 1]]
+            sign = -sign
+        d = A[k, k + 1]
+        if d == 0.0:
+            return 0.0, -math.inf
+        sign *= math.copysign(1.0, d)
+        log += math.log(abs(d))
+        x = A[k + 2 :, k].copy()
+        y = A[k + 2 :, k + 1].copy()
+        A[k + 2 :, k + 2 :] += (np.outer(y, x) - np.outer(x, y)) / d
+    return sign, log
+
+
+def pf64(S):
+    s, l = pf_pr64(S)
+    return s * math.exp(l) if np.isfinite(l) else 0.0
+
+
+def slogpf64(Sb):
+    """Batched (sign, log|pf|) in float64."""
+    out = [pf_pr64(S) for S in np.asarray(Sb)]
+    return np.array([o[0] for o in out]), np.array([o[1] for o in out])
+
+
+def adjT_brute(A):
+    """d det / dA = adj(A)^T by cofactors, float64."""
+    A = np.asarray(A, np.float64)
+    n = A.shape[0]
+    G = np.zeros((n, n))
+    for i in range(n):
+        for j in range(n):
+            M = np.delete(np.delete(A, i, 0), j, 1)
+            G[i, j] = (-1) ** (i + j) * (np.linalg.det(M) if n > 1 else 1.0)
+    return G
+
+
+def pf_grad_brute(S):
+    """d pf / dS with the skew extension G = (D - D^T)/2,
+    D_ij = (-1)^(i+j+1) pf(S without rows/cols i, j) for i < j (brute force)."""
+    S = np.asarray(S, np.float64)
+    n = S.shape[0]
+    D = np.zeros((n, n))
+    for i in range(n):
+        for j in range(i + 1, n):
+            keep = [k for k in range(n) if k not in (i, j)]
+            D[i, j] = (-1) ** (i + j + 1) * pf_brute(S[np.ix_(keep, keep)])
+    return 0.5 * (D - D.T)
+
+
+def inv64(A):
+    return np.linalg.inv(np.asarray(A, np.float64))

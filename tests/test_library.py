@@ -1,0 +1,74 @@
+"""CPU checks of the boundary: the HIP library is built, loads, and exports every
+entry point include/fermix.h declares (no compute calls without a GPU); the Python API
+raises the reference's error types (src/fermix/api.py:24-31,92-97; _field.py:265-275)."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import fermix_amd
+from fermix_amd import _lib, _tune
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fermix.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("fx_slogdet_f32", "fx_slogdet_parts_f32", "fx_slogpf_f32", "fx_status_string"):
+        assert s in syms
+
+
+def test_library_loads_and_exports_every_symbol():
+    assert os.path.exists(_lib.LIB_PATH), "build the library first (python -m fermix_amd.build)"
+    h = ctypes.CDLL(_lib.LIB_PATH)
+    for s in declared_symbols():
+        assert hasattr(h, s), f"{s} declared in include/fermix.h but not exported"
+    assert set(declared_symbols()) == set(_lib.SIGNATURES)
+
+
+def test_host_only_calls():
+    L = _lib.lib()
+    assert L.fx_abi_version() == 100
+    assert L.fx_status_string(0) == b"ok"
+    assert L.fx_lu_padded_size(100) == 112
+    assert L.fx_pf_padded_size(128) == 128
+    # argument validation happens before any device work
+    assert L.fx_slogdet_f32(None, -1, 4, None, None, None, 0, None) == 1
+    assert L.fx_slogdet_f32(None, 0, 4, None, None, None, 0, None) == 0
+
+
+def test_api_errors():
+    A = torch.zeros((2, 4, 4), dtype=torch.float32)
+    with pytest.raises(TypeError):
+        fermix_amd.slogdet(torch.zeros((2, 4, 4), dtype=torch.int32))
+    with pytest.raises(TypeError):
+        fermix_amd.slogdet(np.zeros((4, 4), np.float32))
+    with pytest.raises(ValueError):
+        fermix_amd.slogdet(torch.zeros((2, 4, 3)))
+    with pytest.raises(ValueError):
+        fermix_amd.slogdet(torch.zeros((4,)))
+    with pytest.raises(ValueError):
+        fermix_amd.slogdet(A, block=48)
+    with pytest.raises(ValueError):
+        fermix_amd.det(A, prec="fast")
+    with pytest.raises(fermix_amd.FermixDeviceError):
+        fermix_amd.slogdet(A)
+    with pytest.raises(fermix_amd.FermixDeviceError):
+        fermix_amd.slogpf(A)
+
+
+def test_tune_table():
+    assert _tune.check_prec(None) == "ieee"
+    assert _tune.check_prec("tf32x3") == "ieee"
+    assert _tune.kernel_family(128) == "fused-lds"
