@@ -65,7 +65,10 @@ def _on_device(a):
 def _flat(a):
     batch = a.shape[:-2]
     n = a.shape[-1]
-    return a.reshape((-1, n, n)).contiguous(), batch, n
+    B = 1
+    for d in batch:
+        B *= int(d)
+    return a.reshape((B, n, n)).contiguous(), batch, n
 
 
 def slogdet(a, *, prec=None, unroll_steps=None, block=None):
