@@ -7,6 +7,22 @@ namespace fx {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+template <int V>
+struct ic {
+  static constexpr int value = V;
+};
+
+// Compile-time loop: f(ic<B>{}), ..., f(ic<E-1>{}). Register arrays indexed by the loop
+// variable then always resolve to fixed registers (a runtime index would make the
+// compiler fall back to s_set_gpr_idx / v_movrel indexing).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(ic<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 constexpr int WAVE = 64;
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
@@ -65,5 +81,54 @@ __device__ __forceinline__ void wave_lds_fence() {
 
 // Guarded reciprocal: 1/0 -> 0 (a zero pivot contributes nothing to the multipliers).
 __device__ __forceinline__ float safe_rcp(float d) { return d != 0.0f ? 1.0f / d : 0.0f; }
+
+// Copy the row-major n x n matrix g into an N x N LDS tile (row stride LDA) with NT
+// threads, writing pad(r, c) outside the n x n block. Every global load of a chunk is
+// issued before its LDS stores, so a thread keeps several loads in flight; with n == N
+// (n a multiple of 16) the loads are 16-byte vectors.
+template <int N, int LDA, int NT, class Pad>
+__device__ __forceinline__ void load_tile(float* As, const float* __restrict__ g, int n, int tid,
+                                          Pad pad) {
+  if (n == N) {
+    constexpr int NV = N * N / 4;
+    constexpr int PER = (NV + NT - 1) / NT;
+    const float4* g4 = reinterpret_cast<const float4*>(g);
+    float4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + NT * i;
+      if (NV % NT == 0 || e < NV) v[i] = g4[e];
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + NT * i;
+      if (NV % NT == 0 || e < NV) {
+        const int r = (4 * e) / N, c = (4 * e) % N;
+        float* d = As + r * LDA + c;
+        d[0] = v[i].x;
+        d[1] = v[i].y;
+        d[2] = v[i].z;
+        d[3] = v[i].w;
+      }
+    }
+  } else {
+    constexpr int CH = 8;
+    for (int base = 0; base < N * N; base += NT * CH) {
+      float v[CH];
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int e = base + tid + NT * u;
+        const int r = e / N, c = e % N;
+        v[u] = (e < N * N && r < n && c < n) ? g[r * n + c] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int e = base + tid + NT * u;
+        const int r = e / N, c = e % N;
+        if (e < N * N) As[r * LDA + c] = (r < n && c < n) ? v[u] : pad(r, c);
+      }
+    }
+  }
+}
 
 }  // namespace fx

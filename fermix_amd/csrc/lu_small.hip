@@ -52,8 +52,8 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
     for (int j = 0; j < 16; ++j) a[i][j] = valid[i] ? As[row * LDA + r0 + j] : 0.0f;
   }
   float xcol[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  static_for<0, 16>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
     const int posc = r0 + j;
     unsigned kb = 0;
     int ib = 0;
@@ -65,18 +65,16 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
     const unsigned gk = wave_max_u32(kb);
     const int pl = first_lane(kb == gk);
     const int is = readlane_i(ib, pl);
+    // the pivot row (wave-uniform: `is` and `pl` are scalars)
     float u[16];
-#pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      float v = a[0][jj];
-#pragma unroll
-      for (int i = 1; i < R; ++i) v = (is == i) ? a[i][jj] : v;
-      u[jj] = readlane_f(v, pl);
-    }
-    int pv = pos[0];
-#pragma unroll
-    for (int i = 1; i < R; ++i) pv = (is == i) ? pos[i] : pv;
-    const int pp = readlane_i(pv, pl);
+    int pp = 0;
+    static_for<0, R>([&](auto ic_) {
+      constexpr int i = decltype(ic_)::value;
+      if (is == i) {
+        static_for<0, 16>([&](auto cc) { u[cc.value] = readlane_f(a[i][cc.value], pl); });
+        pp = readlane_i(pos[i], pl);
+      }
+    });
     // swap positions posc <-> pp
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -97,16 +95,16 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
       if (valid[i] && pos[i] > posc) {
         const float l = a[i][j] * rcp;
         a[i][j] = l;
-#pragma unroll
-        for (int jj = j + 1; jj < 16; ++jj) a[i][jj] = fmaf(-l, u[jj], a[i][jj]);
+        static_for<j + 1, 16>([&](auto cc) {
+          a[i][cc.value] = fmaf(-l, u[cc.value], a[i][cc.value]);
+        });
       }
     }
     // row j of X = L11^-1: X[j][c] = -sum_{k<j} L11[j][k] X[k][c], X[j][j] = 1
     float x = 0.0f;
-#pragma unroll
-    for (int kk = 0; kk < j; ++kk) x = fmaf(-u[kk], xcol[kk], x);
+    static_for<0, j>([&](auto kc) { x = fmaf(-u[kc.value], xcol[kc.value], x); });
     xcol[j] = (lane == j) ? 1.0f : x;
-  }
+  });
   // write the panel back in the new row order, the position map and X
 #pragma unroll
   for (int i = 0; i < R; ++i) {
@@ -208,10 +206,7 @@ __global__ __launch_bounds__(256) void lu_small_kernel(const float* __restrict__
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* Ab = A + b * (int64_t)n * n;
-  for (int e = tid; e < N * N; e += 256) {
-    const int r = e / N, c = e - r * N;
-    As[r * LDA + c] = (r < n && c < n) ? Ab[r * n + c] : (r == c ? 1.0f : 0.0f);
-  }
+  load_tile<N, LDA, 256>(As, Ab, n, tid, [](int r, int c) { return r == c ? 1.0f : 0.0f; });
   if (FACT)
     for (int r = tid; r < N; r += 256) perm[r] = r;
   __syncthreads();

@@ -55,10 +55,10 @@ __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int
 #pragma unroll
     for (int k = 0; k < 16; ++k) G[i][k] = 0.0f;
   }
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
+  static_for<0, 8>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
     const int c = r0 + 2 * t;
-    // row a: the row at position c
+    // row a: the row at position c (wave-uniform lane la, slot sa)
     bool hit = false;
     int hs = 0;
 #pragma unroll
@@ -68,24 +68,21 @@ __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int
     const int sa = readlane_i(hs, la);
     const int qa = R * la + sa;
     float ga[16];
-#pragma unroll
-    for (int k = 0; k < 2 * t; ++k) {
-      float v = G[0][k];
-#pragma unroll
-      for (int i = 1; i < R; ++i) v = (sa == i) ? G[i][k] : v;
-      ga[k] = readlane_f(v, la);
-    }
+    static_for<0, R>([&](auto ic_) {
+      constexpr int i = decltype(ic_)::value;
+      if (sa == i) static_for<0, 2 * t>([&](auto kc) { ga[kc.value] = readlane_f(G[i][kc.value], la); });
+    });
     // column a of the current matrix: M[i][qa] = -M[qa][i] plus the G corrections
     float x[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int row = R * lane + i;
       float v = valid[i] ? -As[qa * LDA + row] : 0.0f;
-#pragma unroll
-      for (int u = 0; u < t; ++u) {
+      static_for<0, t>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
         v = fmaf(G[i][2 * u], ga[2 * u + 1], v);
         v = fmaf(-G[i][2 * u + 1], ga[2 * u], v);
-      }
+      });
       x[i] = v;
     }
     unsigned kb = 0;
@@ -99,40 +96,38 @@ __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int
     const int lp = first_lane(kb == gk);
     const int sp = readlane_i(ib, lp);
     const int qp = R * lp + sp;
-    int pv = pos[0];
-#pragma unroll
-    for (int i = 1; i < R; ++i) pv = (sp == i) ? pos[i] : pv;
-    const int pp = readlane_i(pv, lp);
+    float gp[16];
+    int pp = 0;
+    static_for<0, R>([&](auto ic_) {
+      constexpr int i = decltype(ic_)::value;
+      if (sp == i) {
+        static_for<0, 2 * t>([&](auto kc) { gp[kc.value] = readlane_f(G[i][kc.value], lp); });
+        pp = readlane_i(pos[i], lp);
+      }
+    });
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       if (valid[i] && pos[i] == c + 1) pos[i] = pp;
       if (lane == lp && i == sp) pos[i] = c + 1;
     }
     nsw += (pp != c + 1) ? 1 : 0;
-    float gp[16];
-#pragma unroll
-    for (int k = 0; k < 2 * t; ++k) {
-      float v = G[0][k];
-#pragma unroll
-      for (int i = 1; i < R; ++i) v = (sp == i) ? G[i][k] : v;
-      gp[k] = readlane_f(v, lp);
-    }
     float y[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int row = R * lane + i;
       float v = valid[i] ? -As[qp * LDA + row] : 0.0f;
-#pragma unroll
-      for (int u = 0; u < t; ++u) {
+      static_for<0, t>([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
         v = fmaf(G[i][2 * u], gp[2 * u + 1], v);
         v = fmaf(-G[i][2 * u + 1], gp[2 * u], v);
-      }
+      });
       y[i] = v;
     }
-    float yv = y[0];
-#pragma unroll
-    for (int i = 1; i < R; ++i) yv = (sa == i) ? y[i] : yv;
-    const float d = readlane_f(yv, la);  // M[a][p]
+    float d = 0.0f;  // M[a][p] = y at row a
+    static_for<0, R>([&](auto ic_) {
+      constexpr int i = decltype(ic_)::value;
+      if (sa == i) d = readlane_f(y[i], la);
+    });
     if (d == 0.0f) {
       zero = 1;
     } else {
@@ -147,7 +142,7 @@ __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int
       G[i][2 * t + 1] = act ? y[i] : 0.0f;
     }
     if (FACT && lane == 0) d_k[t] = d;
-  }
+  });
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     if (valid[i]) {
@@ -192,15 +187,23 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* Ab = A + b * (int64_t)n * n;
-  for (int e = tid; e < N * N; e += 256) {
-    const int r = e / N, c = e - r * N;
-    float v;
-    if (r < n && c < n) {
-      v = skew ? (Ab[r * n + c] - Ab[c * n + r]) * 0.5f : Ab[r * n + c];
-    } else {
-      v = ((r ^ c) == 1 && r >= n) ? ((r & 1) ? -1.0f : 1.0f) : 0.0f;  // n is even
+  // [[0,1],[-1,0]] padding blocks (n is even)
+  load_tile<N, LDA, 256>(As, Ab, n, tid, [](int r, int c) {
+    return ((r ^ c) == 1) ? ((r & 1) ? -1.0f : 1.0f) : 0.0f;
+  });
+  if (skew) {
+    __syncthreads();
+    // S = (A - A^T) / 2 in place: thread pairs (r, c) with r < c
+    for (int e = tid; e < n * n; e += 256) {
+      const int r = e / n, c = e - r * n;
+      if (r < c) {
+        const float x = As[r * LDA + c], y = As[c * LDA + r];
+        As[r * LDA + c] = (x - y) * 0.5f;
+        As[c * LDA + r] = (y - x) * 0.5f;
+      } else if (r == c) {
+        As[r * LDA + c] = 0.0f;
+      }
     }
-    As[r * LDA + c] = v;
   }
   if (FACT)
     for (int r = tid; r < N; r += 256) orig[r] = r;
