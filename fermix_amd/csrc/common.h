@@ -54,6 +54,24 @@ __device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
   return max(max(r0, r1), max(r2, r3));
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum of v over the 64 lanes in a fixed order (deterministic, wave-uniform result).
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
@@ -80,7 +98,44 @@ __device__ __forceinline__ void wave_lds_fence() {
 }
 
 // Guarded reciprocal: 1/0 -> 0 (a zero pivot contributes nothing to the multipliers).
-__device__ __forceinline__ float safe_rcp(float d) { return d != 0.0f ? 1.0f / d : 0.0f; }
+// v_rcp_f32 (1 ulp) -- the multipliers it scales are within 2 ulp of a / d.
+__device__ __forceinline__ float safe_rcp(float d) {
+  return d != 0.0f ? __builtin_amdgcn_rcpf(d) : 0.0f;
+}
+
+// Pivots of one matrix collected across a wave: pivot g lives in slot g / 64 of lane
+// g % 64, so the logs and signs are formed once at the end, off the elimination's
+// dependency chain.
+template <int NS>
+struct PivotLog {
+  float v[NS];
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) v[i] = 1.0f;
+  }
+  __device__ __forceinline__ void put(int g, float d, int lane) {
+    const int sl = g >> 6;
+    const bool mine = (g & 63) == lane;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) v[i] = (mine && sl == i) ? d : v[i];
+  }
+  // (sign, logabs) of the product of the pivots times (-1)^nswap; (0, -inf) if any is 0.
+  __device__ __forceinline__ void finish(int nswap, float& sign, float& logabs) const {
+    float lg = 0.0f;
+    bool z = false, ng = false;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      z = z || (v[i] == 0.0f);
+      ng = ng != (v[i] < 0.0f);
+      lg += (v[i] != 0.0f) ? logf(fabsf(v[i])) : 0.0f;
+    }
+    lg = wave_sum_f32(lg);
+    const unsigned long long zm = __ballot(z);
+    const int negs = __popcll(__ballot(ng)) + nswap;
+    sign = zm ? 0.0f : ((negs & 1) ? -1.0f : 1.0f);
+    logabs = zm ? -INFINITY : lg;
+  }
+};
 
 // Copy the row-major n x n matrix g into an N x N LDS tile (row stride LDA) with NT
 // threads, writing pad(r, c) outside the n x n block. Every global load of a chunk is

@@ -32,13 +32,14 @@ struct LuSmall {
   static constexpr int LDA = N + 4;        // row stride in LDS (floats)
   static constexpr int R = (N + 63) / 64;  // panel rows per lane
   static constexpr int NP = N / 16;        // panels
+  static constexpr int NPV = (N + 63) / 64;  // pivot slots per lane
 };
 
 // Factor the 16-column panel at (r0, r0) (wave 0 only). Accumulates the pivot signs,
 // log|pivot|, zero-pivot flag and swap count into the wave-uniform state.
 template <int N, bool FACT>
 __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, int* perm,
-                                         int lane, float& sgn, float& lab, int& zero, int& nsw) {
+                                         int lane, PivotLog<LuSmall<N>::NPV>& piv_log, int& nsw) {
   constexpr int LDA = LuSmall<N>::LDA, R = LuSmall<N>::R;
   float a[R][16];
   int pos[R];
@@ -65,16 +66,18 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
     const unsigned gk = wave_max_u32(kb);
     const int pl = first_lane(kb == gk);
     const int is = readlane_i(ib, pl);
-    // the pivot row (wave-uniform: `is` and `pl` are scalars)
+    // the pivot row (wave-uniform: `is` and `pl` are scalars), selected without branching
     float u[16];
-    int pp = 0;
-    static_for<0, R>([&](auto ic_) {
-      constexpr int i = decltype(ic_)::value;
-      if (is == i) {
-        static_for<0, 16>([&](auto cc) { u[cc.value] = readlane_f(a[i][cc.value], pl); });
-        pp = readlane_i(pos[i], pl);
-      }
+    static_for<0, 16>([&](auto cc) {
+      float v = a[0][cc.value];
+#pragma unroll
+      for (int i = 1; i < R; ++i) v = (is == i) ? a[i][cc.value] : v;
+      u[cc.value] = readlane_f(v, pl);
     });
+    int pv = pos[0];
+#pragma unroll
+    for (int i = 1; i < R; ++i) pv = (is == i) ? pos[i] : pv;
+    const int pp = readlane_i(pv, pl);
     // swap positions posc <-> pp
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -83,12 +86,7 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
     }
     nsw += (pp != posc) ? 1 : 0;
     const float piv = u[j];
-    if (piv == 0.0f) {
-      zero = 1;
-    } else {
-      lab += logf(fabsf(piv));
-      if (piv < 0.0f) sgn = -sgn;
-    }
+    piv_log.put(posc, piv, lane);
     const float rcp = safe_rcp(piv);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -211,9 +209,10 @@ __global__ __launch_bounds__(256) void lu_small_kernel(const float* __restrict__
     for (int r = tid; r < N; r += 256) perm[r] = r;
   __syncthreads();
 
-  float sgn = 1.0f, lab = 0.0f;
-  int zero = 0, nsw = 0;
-  if (wave == 0) lu_panel<N, FACT>(As, 0, srcs[0], Xs[0], perm, lane, sgn, lab, zero, nsw);
+  PivotLog<LuSmall<N>::NPV> piv_log;
+  piv_log.init();
+  int nsw = 0;
+  if (wave == 0) lu_panel<N, FACT>(As, 0, srcs[0], Xs[0], perm, lane, piv_log, nsw);
   __syncthreads();
   for (int k = 0; k < NP; ++k) {
     const int r0 = 16 * k;
@@ -223,8 +222,8 @@ __global__ __launch_bounds__(256) void lu_small_kernel(const float* __restrict__
     if (wave == 0) {
       if (S > 0) {
         lu_strip<N>(As, r0, r0 + 16, src, X, lane);
-        lu_panel<N, FACT>(As, r0 + 16, srcs[(k + 1) & 1], Xs[(k + 1) & 1], perm, lane, sgn, lab,
-                          zero, nsw);
+        lu_panel<N, FACT>(As, r0 + 16, srcs[(k + 1) & 1], Xs[(k + 1) & 1], perm, lane, piv_log,
+                          nsw);
       }
     } else {
       for (int s = wave; s < S; s += 3) lu_strip<N>(As, r0, r0 + 16 + 16 * s, src, X, lane);
@@ -233,9 +232,13 @@ __global__ __launch_bounds__(256) void lu_small_kernel(const float* __restrict__
     }
     __syncthreads();
   }
-  if (tid == 0) {
-    sign_out[b] = zero ? 0.0f : ((nsw & 1) ? -sgn : sgn);
-    logabs_out[b] = zero ? -INFINITY : lab;
+  if (wave == 0) {
+    float sg, la;
+    piv_log.finish(nsw, sg, la);
+    if (lane == 0) {
+      sign_out[b] = sg;
+      logabs_out[b] = la;
+    }
   }
   if (FACT) {
     float* Lb = lu_out + b * (int64_t)N * N;

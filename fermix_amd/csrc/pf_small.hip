@@ -34,6 +34,7 @@ struct PfSmall {
   static constexpr int LDG = 17;
   static constexpr int R = (N + 63) / 64;
   static constexpr int NB = N / 16;
+  static constexpr int NPV = (N / 2 + 63) / 64;  // pivot slots per lane
   static constexpr int MAXNT = N / 16 - 1;                       // trailing tiles per side
   static constexpr int MAXTILES = MAXNT * (MAXNT + 1) / 2;       // lower-triangle tiles
   static constexpr int TPW = MAXTILES > 0 ? (MAXTILES + 3) / 4 : 1;  // tiles per wave
@@ -41,8 +42,8 @@ struct PfSmall {
 
 template <int N, bool FACT>
 __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int* src, int lane,
-                                         float& sgn, float& lab, int& zero, int& nsw,
-                                         int* orig, float* gbuf_k, float* d_k) {
+                                         PivotLog<PfSmall<N>::NPV>& piv_log, int& nsw, int* orig,
+                                         float* gbuf_k, float* d_k) {
   constexpr int LDA = PfSmall<N>::LDA, LDG = PfSmall<N>::LDG, R = PfSmall<N>::R;
   float G[R][16];
   int pos[R];
@@ -68,9 +69,11 @@ __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int
     const int sa = readlane_i(hs, la);
     const int qa = R * la + sa;
     float ga[16];
-    static_for<0, R>([&](auto ic_) {
-      constexpr int i = decltype(ic_)::value;
-      if (sa == i) static_for<0, 2 * t>([&](auto kc) { ga[kc.value] = readlane_f(G[i][kc.value], la); });
+    static_for<0, 2 * t>([&](auto kc) {
+      float v = G[0][kc.value];
+#pragma unroll
+      for (int i = 1; i < R; ++i) v = (sa == i) ? G[i][kc.value] : v;
+      ga[kc.value] = readlane_f(v, la);
     });
     // column a of the current matrix: M[i][qa] = -M[qa][i] plus the G corrections
     float x[R];
@@ -97,14 +100,16 @@ __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int
     const int sp = readlane_i(ib, lp);
     const int qp = R * lp + sp;
     float gp[16];
-    int pp = 0;
-    static_for<0, R>([&](auto ic_) {
-      constexpr int i = decltype(ic_)::value;
-      if (sp == i) {
-        static_for<0, 2 * t>([&](auto kc) { gp[kc.value] = readlane_f(G[i][kc.value], lp); });
-        pp = readlane_i(pos[i], lp);
-      }
+    static_for<0, 2 * t>([&](auto kc) {
+      float v = G[0][kc.value];
+#pragma unroll
+      for (int i = 1; i < R; ++i) v = (sp == i) ? G[i][kc.value] : v;
+      gp[kc.value] = readlane_f(v, lp);
     });
+    int pv = pos[0];
+#pragma unroll
+    for (int i = 1; i < R; ++i) pv = (sp == i) ? pos[i] : pv;
+    const int pp = readlane_i(pv, lp);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       if (valid[i] && pos[i] == c + 1) pos[i] = pp;
@@ -123,17 +128,11 @@ __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int
       });
       y[i] = v;
     }
-    float d = 0.0f;  // M[a][p] = y at row a
-    static_for<0, R>([&](auto ic_) {
-      constexpr int i = decltype(ic_)::value;
-      if (sa == i) d = readlane_f(y[i], la);
-    });
-    if (d == 0.0f) {
-      zero = 1;
-    } else {
-      lab += logf(fabsf(d));
-      if (d < 0.0f) sgn = -sgn;
-    }
+    float yv = y[0];  // M[a][p] = y at row a
+#pragma unroll
+    for (int i = 1; i < R; ++i) yv = (sa == i) ? y[i] : yv;
+    const float d = readlane_f(yv, la);
+    piv_log.put(c >> 1, d, lane);
     const float inv = safe_rcp(d);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -209,15 +208,16 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
     for (int r = tid; r < N; r += 256) orig[r] = r;
   __syncthreads();
 
-  float sgn = 1.0f, lab = 0.0f;
-  int zero = 0, nsw = 0;
+  PivotLog<C::NPV> piv_log;
+  piv_log.init();
+  int nsw = 0;
   const int li = lane & 15, g = lane >> 4;
   for (int k = 0; k < NB; ++k) {
     const int r0 = 16 * k;
     if (wave == 0) {
       float* gk = FACT ? gbuf_out + (b * NB + k) * (int64_t)N * 16 : nullptr;
       float* dk = FACT ? d_out + b * (N / 2) + 8 * k : nullptr;
-      pf_panel<N, FACT>(As, Gs, r0, src, lane, sgn, lab, zero, nsw, orig, gk, dk);
+      pf_panel<N, FACT>(As, Gs, r0, src, lane, piv_log, nsw, orig, gk, dk);
     }
     __syncthreads();
     const int nt = (N - r0 - 16) / 16;
@@ -273,9 +273,13 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
     }
     __syncthreads();
   }
-  if (tid == 0) {
-    sign_out[b] = zero ? 0.0f : ((nsw & 1) ? -sgn : sgn);
-    logabs_out[b] = zero ? -INFINITY : lab;
+  if (wave == 0) {
+    float sg, la;
+    piv_log.finish(nsw, sg, la);
+    if (lane == 0) {
+      sign_out[b] = sg;
+      logabs_out[b] = la;
+    }
   }
   if (FACT)
     for (int r = tid; r < N; r += 256) perm_out[b * N + r] = orig[r];
