@@ -22,6 +22,7 @@ static int fill2(float* a, float va, float* b, float vb, int64_t count, hipStrea
 }
 
 static constexpr int SMALL_MAX = 128;
+static constexpr int LARGE_MAX = 1024;
 
 }  // namespace fx
 
@@ -44,7 +45,8 @@ int fx_abi_version(void) { return 100; }
 
 int32_t fx_lu_padded_size(int32_t n) {
   if (n <= 0) return 0;
-  return n <= SMALL_MAX ? lu_small_padded(n) : -1;
+  if (n <= SMALL_MAX) return lu_small_padded(n);
+  return n <= LARGE_MAX ? lu_large_padded(n) : -1;
 }
 
 int32_t fx_pf_padded_size(int32_t n) {
@@ -53,21 +55,21 @@ int32_t fx_pf_padded_size(int32_t n) {
 }
 
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {
-  (void)batch;
-  (void)n;
-  return 0;
+  if (batch <= 0 || n <= SMALL_MAX || n > LARGE_MAX) return 0;
+  return lu_large_workspace(batch, n, false);
 }
 
 int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs,
                    void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   if (n <= SMALL_MAX) return launch_lu_small(a, n, batch, sign, logabs, nullptr, nullptr, s);
+  if (n <= LARGE_MAX)
+    return launch_lu_large(a, n, batch, sign, logabs, workspace, workspace_bytes, false, nullptr,
+                           nullptr, s);
   return FX_ERR_UNSUPPORTED;
 }
 

@@ -19,4 +19,35 @@ int launch_lu_small(const float* A, int n, int64_t batch, float* sign, float* lo
 int launch_pf_small(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
                     float* gbuf, float* d, int* perm, hipStream_t s);
 
+// 128 < n <= 1024: blocked LU in a workspace (see lu_large.hip). W_out / g0_out return
+// the packed LU (B, N, N) and, with parts, the composed row map (B, N), N = lu_large_padded.
+int lu_large_padded(int n);
+size_t lu_large_workspace(int64_t batch, int n, bool parts);
+int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
+                    size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s);
+
+// ------------------------------------------------------------------ batched GEMM
+// Masks apply to op(X) in global coordinates (row + off*r, col + off*c): elements
+// outside the triangle read as zero (unit diagonal for the *_UNIT kinds).
+enum { MASK_NONE = 0, MASK_LOWER_UNIT = 1, MASK_UPPER = 2, MASK_UPPER_UNIT = 3 };
+
+struct GemmDesc {
+  const float* A;
+  const float* B;
+  float* C;
+  int64_t sA, sB, sC;     // stride of the batch index (blockIdx.y)
+  int64_t sA2, sB2, sC2;  // stride of the second batch index (blockIdx.z)
+  int lda, ldb, ldc;
+  int M, N, K;
+  float alpha, beta;
+  int transA, transB;  // op(A) = A (M x K, row-major) or A^T (A stored K x M)
+  int maskA, maskB;
+  int offAr, offAc, offBr, offBc;
+  int lower_only;  // only tiles on/below the diagonal; C[j][i] = mirror * C[i][j]
+  float mirror;
+};
+
+// C = alpha op(A) op(B) + beta C for every (batch, second-batch) index.
+int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s);
+
 }  // namespace fx

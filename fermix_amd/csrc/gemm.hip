@@ -1,0 +1,216 @@
+// Batched fp32 GEMM on MFMA (v_mfma_f32_32x32x2f32) for the sub-block products of the
+// large-n paths: C = alpha * op(A) op(B) + beta * C over a batch of matrices (and an
+// optional second batch dimension, e.g. the block pairs of one recursion level).
+//
+// Reference role replaced: the batched sub-block GEMM `_bgemm` (ChenAo-Phys/fermix
+// src/fermix/_inverse.py:230-426) and the trailing GEMMs of the LU / Parlett-Reid
+// (src/fermix/_lu.py:334-393, src/fermix/_pf.py:287-382).
+//
+// Design (gfx950): a workgroup of 4 waves computes a BM x BN tile; each wave owns a
+// (BM/2) x (BN/2) quarter as 32x32 MFMA accumulators. K advances in BK = 16 stages
+// staged through LDS K-major (so every MFMA operand read is 32 consecutive floats),
+// double-buffered, with the next stage's global loads in flight during the current
+// stage's MFMAs.
+//
+// Options:
+//  * operand masks: op(A)(i, k) / op(B)(k, j) read as zero outside a triangle (lower
+//    with unit diagonal, or upper), compared on global indices, so packed LU storage
+//    can be used directly as L or U; the K range of each tile is trimmed to the
+//    triangle at tile granularity;
+//  * lower_only: only tiles with tile_row >= tile_col are computed, and each element
+//    is also stored mirrored, C[j][i] = mirror * C[i][j] (mirror = -1 gives an exactly
+//    skew result with a zero diagonal).
+#include "common.h"
+#include "fermix_internal.h"
+
+namespace fx {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int GBK = 16;
+
+// Element (r, c) of op(X) in the mask's global coordinates.
+__device__ __forceinline__ float mask_val(float v, int mask, int r, int c) {
+  if (mask == MASK_LOWER_UNIT) return r > c ? v : (r == c ? 1.0f : 0.0f);
+  if (mask == MASK_UPPER) return r <= c ? v : 0.0f;
+  if (mask == MASK_UPPER_UNIT) return r < c ? v : (r == c ? 1.0f : 0.0f);
+  return v;
+}
+__device__ __forceinline__ bool mask_lower(int m) { return m == MASK_LOWER_UNIT; }
+__device__ __forceinline__ bool mask_upper(int m) { return m == MASK_UPPER || m == MASK_UPPER_UNIT; }
+
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
+  constexpr int LDSA = BM + 4, LDSB = BN + 4;
+  constexpr int WM = BM / 2, WN = BN / 2;   // per-wave quarter
+  constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 tiles per wave
+  __shared__ float As[2][GBK * LDSA];
+  __shared__ float Bs[2][GBK * LDSB];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t bat = blockIdx.y, bat2 = blockIdx.z;
+  int ti, tj;
+  const int ntn = (d.N + BN - 1) / BN;
+  if (d.lower_only) {
+    // blockIdx.x enumerates the lower triangle of tiles row-major
+    const int t = blockIdx.x;
+    int I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
+    while ((I + 1) * (I + 2) / 2 <= t) ++I;
+    while (I * (I + 1) / 2 > t) --I;
+    ti = I;
+    tj = t - I * (I + 1) / 2;
+  } else {
+    ti = blockIdx.x / ntn;
+    tj = blockIdx.x % ntn;
+  }
+  const int i0 = ti * BM, j0 = tj * BN;
+  const float* A = d.A + bat * d.sA + bat2 * d.sA2;
+  const float* B = d.B + bat * d.sB + bat2 * d.sB2;
+  float* C = d.C + bat * d.sC + bat2 * d.sC2;
+
+  // K range of this tile from the operand triangles
+  int klo = 0, khi = d.K;
+  // op(A)(i, k): lower -> k <= i + offAr - offAc, upper -> k >= i + offAr - offAc;
+  // op(B)(k, j): lower -> k >= j + offBc - offBr, upper -> k <= j + offBc - offBr
+  if (mask_upper(d.maskA)) klo = max(klo, i0 + d.offAr - d.offAc);
+  if (mask_lower(d.maskA)) khi = min(khi, i0 + BM + d.offAr - d.offAc);
+  if (mask_lower(d.maskB)) klo = max(klo, j0 + d.offBc - d.offBr);
+  if (mask_upper(d.maskB)) khi = min(khi, j0 + BN + d.offBc - d.offBr);
+  klo = max(0, (klo / GBK) * GBK);
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+
+  // global -> register staging: A tile BM x GBK, B tile GBK x BN, as float (simple and
+  // general: any ld, offsets and masks); 256 threads
+  constexpr int AE = BM * GBK / 256, BE = BN * GBK / 256;
+  float ra[AE], rb[BE];
+  auto load_stage = [&](int k0) {
+#pragma unroll
+    for (int e = 0; e < AE; ++e) {
+      const int idx = tid + 256 * e;
+      int i, k;
+      if (!d.transA) { i = idx / GBK; k = idx % GBK; }   // row-major A: k fastest
+      else { k = idx / BM; i = idx % BM; }               // A^T stored: i fastest
+      const int gi = i0 + i, gk = k0 + k;
+      float v = 0.0f;
+      if (gi < d.M && gk < khi && gk < d.K) {
+        v = d.transA ? A[(int64_t)gk * d.lda + gi] : A[(int64_t)gi * d.lda + gk];
+        if (d.maskA) v = mask_val(v, d.maskA, gi + d.offAr, gk + d.offAc);
+      }
+      ra[e] = v;
+    }
+#pragma unroll
+    for (int e = 0; e < BE; ++e) {
+      const int idx = tid + 256 * e;
+      int k, j;
+      if (!d.transB) { k = idx / BN; j = idx % BN; }     // row-major B: j fastest
+      else { j = idx / GBK; k = idx % GBK; }             // B^T stored: k fastest
+      const int gk = k0 + k, gj = j0 + j;
+      float v = 0.0f;
+      if (gj < d.N && gk < khi && gk < d.K) {
+        v = d.transB ? B[(int64_t)gj * d.ldb + gk] : B[(int64_t)gk * d.ldb + gj];
+        if (d.maskB) v = mask_val(v, d.maskB, gk + d.offBr, gj + d.offBc);
+      }
+      rb[e] = v;
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < AE; ++e) {
+      const int idx = tid + 256 * e;
+      int i, k;
+      if (!d.transA) { i = idx / GBK; k = idx % GBK; }
+      else { k = idx / BM; i = idx % BM; }
+      As[buf][k * LDSA + i] = ra[e];
+    }
+#pragma unroll
+    for (int e = 0; e < BE; ++e) {
+      const int idx = tid + 256 * e;
+      int k, j;
+      if (!d.transB) { k = idx / BN; j = idx % BN; }
+      else { j = idx / GBK; k = idx % GBK; }
+      Bs[buf][k * LDSB + j] = rb[e];
+    }
+  };
+
+  const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+  const int l32 = lane & 31, lh = lane >> 5;
+  int buf = 0;
+  if (klo < khi) {
+    load_stage(klo);
+    store_stage(0);
+    __syncthreads();
+    for (int k0 = klo; k0 < khi; k0 += GBK) {
+      const bool more = k0 + GBK < khi;
+      if (more) load_stage(k0 + GBK);
+#pragma unroll
+      for (int kp = 0; kp < GBK / 2; ++kp) {
+        float av[TM], bv[TN];
+#pragma unroll
+        for (int a = 0; a < TM; ++a) av[a] = As[buf][(2 * kp + lh) * LDSA + wm + 32 * a + l32];
+#pragma unroll
+        for (int b = 0; b < TN; ++b) bv[b] = Bs[buf][(2 * kp + lh) * LDSB + wn + 32 * b + l32];
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+          for (int b = 0; b < TN; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+      }
+      if (more) {
+        store_stage(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+      }
+    }
+  }
+
+  // epilogue: C = alpha * acc + beta * C (and the mirror)
+  const bool diag_tile = d.lower_only && ti == tj;
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = i0 + wm + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
+        const int c = j0 + wn + 32 * b + l32;
+        if (r >= d.M || c >= d.N) continue;
+        if (diag_tile && r < c) continue;
+        float* cp = C + (int64_t)r * d.ldc + c;
+        float val = d.alpha * acc[a][b][v];
+        if (d.beta != 0.0f) val = fmaf(d.beta, *cp, val);
+        if (d.lower_only && r == c && d.mirror < 0.0f) val = 0.0f;
+        *cp = val;
+        if (d.lower_only && r != c) C[(int64_t)c * d.ldc + r] = d.mirror * val;
+      }
+}
+
+int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
+  if (d.M <= 0 || d.N <= 0 || batch <= 0 || nb2 <= 0) return FX_OK;
+  if (d.lower_only && d.M != d.N) return FX_ERR_INVALID_ARGUMENT;
+  const bool big = d.M >= 128 && d.N >= 128;
+  const int BM = big ? 128 : 64, BN = BM;
+  const int tm = (d.M + BM - 1) / BM, tn = (d.N + BN - 1) / BN;
+  const int tiles = d.lower_only ? tm * (tm + 1) / 2 : tm * tn;
+  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+    const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
+    GemmDesc e = d;
+    e.A += b0 * d.sA;
+    e.B += b0 * d.sB;
+    e.C += b0 * d.sC;
+    if (big)
+      hipLaunchKernelGGL((gemm_kernel<128, 128>), dim3(tiles, (unsigned)nb, nb2), dim3(256), 0, s, e);
+    else
+      hipLaunchKernelGGL((gemm_kernel<64, 64>), dim3(tiles, (unsigned)nb, nb2), dim3(256), 0, s, e);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  }
+  return FX_OK;
+}
+
+}  // namespace fx

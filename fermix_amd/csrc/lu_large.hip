@@ -1,0 +1,494 @@
+// Blocked LU with partial pivoting for 128 < n <= 1024 (any batch): per block of PW
+// columns at r0 three launches,
+//   1. lu_panel_kernel  (one workgroup per matrix): the m x PW panel (m = N - r0) is
+//      factored in LDS in 16-column sub-panels. The rows stay in place during the
+//      panel (virtual pivoting); each column step finds the pivot with a per-wave DPP
+//      max and one workgroup barrier (every wave posts its best row, all waves pick the
+//      same winner), and the sub-panel's trailing columns inside the panel are updated
+//      on MFMA (U = X * A_piv, A_rest -= L * U, stores predicated to unassigned rows).
+//      The panel is written back in the new row order, with the map
+//      src[new position] = old row and X_s = L_ss^-1 of every sub-panel;
+//   2. lu_urow_kernel   (matrix x 64-column strip): applies the row permutation to the
+//      strip, touching only the rows that move, and for trailing strips forms the U rows
+//      U12 = L11^-1 A12 by blocked forward substitution on MFMA;
+//   3. the batched MFMA GEMM A22 -= L21 U12 (gemm.hip).
+// A final kernel turns the pivots and swap counts into (sign, logabs).
+//
+// Reference roles replaced (ChenAo-Phys/fermix): _lu_core's block loop (src/fermix/
+// _lu.py:543-611) with its inner panel (_lu.py:54-224), inter-panel update (:228-296),
+// U-row solve (:300-330) and trailing GEMM (:334-393).
+#include "common.h"
+#include "fermix_internal.h"
+
+namespace fx {
+
+template <int MR, int PW>
+struct LuPanel {
+  static constexpr int NW = 4, NT = 256;
+  static constexpr int R = MR / NT;  // rows per lane
+  static constexpr int LDP = PW + 4;
+  static constexpr int NSUB = PW / 16;
+};
+
+struct Cand {
+  unsigned key;
+  int row;
+  int pos;
+  int pad;
+  float v[16];
+};
+
+// Copy A (B, n, n) into the work buffer W (B, N, N) with identity padding.
+__global__ void copy_pad_kernel(const float* __restrict__ A, int n, float* __restrict__ W, int N) {
+  const int64_t b = blockIdx.y;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)N * N) return;
+  const int r = (int)(e / N), c = (int)(e % N);
+  W[b * N * N + e] = (r < n && c < n) ? A[b * n * n + (int64_t)r * n + c] : (r == c ? 1.0f : 0.0f);
+}
+
+template <int MR, int PW>
+__global__ __launch_bounds__(256) void lu_panel_kernel(float* __restrict__ W, int N, int r0, int blk,
+                                                       float* __restrict__ piv_out,
+                                                       int* __restrict__ nsw_out, int nblk,
+                                                       int* __restrict__ src_out,
+                                                       float* __restrict__ X_out,
+                                                       int* __restrict__ g0) {
+  using C = LuPanel<MR, PW>;
+  constexpr int R = C::R, LDP = C::LDP, NSUB = C::NSUB, NW = C::NW;
+  __shared__ float P[MR * LDP];
+  __shared__ Cand cand[2][NW];
+  __shared__ float Ubuf[16 * PW];
+  __shared__ int posL[MR];
+  __shared__ int prowL[16];
+  __shared__ float Xs[256];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int m = N - r0;
+  float* Wb = W + b * (int64_t)N * N;
+
+  // load the panel: P[i][c] = W[r0 + i][r0 + c]
+  for (int e = tid; e < m * (PW / 4); e += 256) {
+    const int i = e / (PW / 4), q = e % (PW / 4);
+    const float4 v = *reinterpret_cast<const float4*>(Wb + (int64_t)(r0 + i) * N + r0 + 4 * q);
+    float* d = P + i * LDP + 4 * q;
+    d[0] = v.x;
+    d[1] = v.y;
+    d[2] = v.z;
+    d[3] = v.w;
+  }
+  int pos[R];
+  bool valid[R];
+#pragma unroll
+  for (int s = 0; s < R; ++s) {
+    const int i = R * (64 * wave + lane) + s;
+    valid[s] = i < m;
+    pos[s] = i;
+  }
+  int nsw = 0;
+  __syncthreads();
+
+  for (int sp = 0; sp < NSUB; ++sp) {
+    const int c0 = 16 * sp;
+    float a[R][16];
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      const int i = R * (64 * wave + lane) + s;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) a[s][j] = valid[s] ? P[i * LDP + c0 + j] : 0.0f;
+    }
+    float xcol[16];
+    int prow_reg[16];
+    static_for<0, 16>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      const int posc = c0 + j;
+      unsigned kb = 0;
+      int ib = 0;
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        const unsigned k = cand_key(a[s][j], valid[s] && pos[s] >= posc);
+        if (k > kb) { kb = k; ib = s; }
+      }
+      const unsigned gk = wave_max_u32(kb);
+      const int pl = first_lane(gk != 0u ? (kb == gk) : (lane == 0));
+      Cand& my = cand[j & 1][wave];
+      if (lane == pl) {
+        my.key = gk;
+        float v[16];
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) v[jj] = a[0][jj];
+        int pv = pos[0];
+#pragma unroll
+        for (int s = 1; s < R; ++s) {
+          if (ib == s) {
+#pragma unroll
+            for (int jj = 0; jj < 16; ++jj) v[jj] = a[s][jj];
+            pv = pos[s];
+          }
+        }
+        my.row = R * (64 * wave + lane) + ib;
+        my.pos = pv;
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) my.v[jj] = v[jj];
+      }
+      __syncthreads();
+      unsigned best = cand[j & 1][0].key;
+      int wb = 0;
+#pragma unroll
+      for (int w = 1; w < NW; ++w) {
+        const unsigned kw = cand[j & 1][w].key;
+        if (kw > best) { best = kw; wb = w; }
+      }
+      const Cand& win = cand[j & 1][wb];
+      float u[16];
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) u[jj] = win.v[jj];
+      const int pp = win.pos, prow = win.row;
+      prow_reg[j] = prow;
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        const int i = R * (64 * wave + lane) + s;
+        if (valid[s] && pos[s] == posc) pos[s] = pp;
+        if (i == prow) pos[s] = posc;
+      }
+      nsw += (pp != posc) ? 1 : 0;
+      const float pivv = u[j];
+      if (wave == 0 && lane == 0) piv_out[b * N + r0 + posc] = pivv;
+      const float rcp = safe_rcp(pivv);
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        if (valid[s] && pos[s] > posc) {
+          const float l = a[s][j] * rcp;
+          a[s][j] = l;
+          static_for<j + 1, 16>([&](auto cc) { a[s][cc.value] = fmaf(-l, u[cc.value], a[s][cc.value]); });
+        }
+      }
+      float x = 0.0f;
+      static_for<0, j>([&](auto kc) { x = fmaf(-u[kc.value], xcol[kc.value], x); });
+      xcol[j] = (lane == j) ? 1.0f : x;
+    });
+    // sub-panel back to LDS (rows stay in place), positions, pivot rows, X
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      const int i = R * (64 * wave + lane) + s;
+      if (valid[s]) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) P[i * LDP + c0 + j] = a[s][j];
+        posL[i] = pos[s];
+      }
+    }
+    if (wave == 0) {
+      if (lane < 16) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          Xs[k * 16 + lane] = xcol[k];
+          X_out[((b * NSUB + sp) * 16 + k) * 16 + lane] = xcol[k];
+        }
+        int pr = prow_reg[0];
+#pragma unroll
+        for (int k = 1; k < 16; ++k) pr = (lane == k) ? prow_reg[k] : pr;
+        prowL[lane] = pr;
+      }
+    }
+    __syncthreads();
+    const int nss = NSUB - sp - 1;  // strips right of the sub-panel inside the panel
+    if (nss > 0) {
+      const int li = lane & 15, g = lane >> 4;
+      // phase A: U = X * A[pivot rows, strip]
+      if (wave < nss) {
+        const int cs = c0 + 16 * (wave + 1);
+        v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          acc = mfma16(Xs[li * 16 + 4 * t + g], P[prowL[4 * t + g] * LDP + cs + li], acc);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) Ubuf[(4 * g + v) * PW + cs + li] = acc[v];
+      }
+      __syncthreads();
+      // phase B: rest -= L * U on the unassigned rows
+      const int nrt = (m + 15) / 16;
+      for (int task = wave; task < nss * nrt; task += NW) {
+        const int st = task % nss, rt = task / nss;
+        const int cs = c0 + 16 * (st + 1);
+        const int rb = 16 * rt;
+        v4f acc;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int r = rb + 4 * g + v;
+          acc[v] = r < m ? P[r * LDP + cs + li] : 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int r = rb + li;
+          const float lv = r < m ? P[r * LDP + c0 + 4 * t + g] : 0.0f;
+          acc = mfma16(-lv, Ubuf[(4 * t + g) * PW + cs + li], acc);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int r = rb + 4 * g + v;
+          if (r < m && posL[r] > c0 + 15) P[r * LDP + cs + li] = acc[v];
+        }
+      }
+      __syncthreads();
+      // phase C: the pivot rows take their U values
+      const int ncols = 16 * nss;
+      for (int e = tid; e < 16 * ncols; e += 256) {
+        const int k = e / ncols, c = c0 + 16 + e % ncols;
+        P[prowL[k] * LDP + c] = Ubuf[k * PW + c];
+      }
+      __syncthreads();
+    }
+  }
+  // write the panel back in the new row order
+  for (int e = tid; e < m * (PW / 4); e += 256) {
+    const int i = e / (PW / 4), q = e % (PW / 4);
+    const float* sp_ = P + i * LDP + 4 * q;
+    *reinterpret_cast<float4*>(Wb + (int64_t)(r0 + posL[i]) * N + r0 + 4 * q) =
+        make_float4(sp_[0], sp_[1], sp_[2], sp_[3]);
+  }
+  for (int i = tid; i < m; i += 256) src_out[b * N + r0 + posL[i]] = r0 + i;
+  if (g0) {
+    // compose the row map: g0[r0 + p] <- g0[r0 + src(p)]
+    int* gb = g0 + b * N;
+    int tmp[(MR + 255) / 256];
+#pragma unroll
+    for (int q = 0; q < (MR + 255) / 256; ++q) {
+      const int i = tid + 256 * q;
+      tmp[q] = i < m ? gb[r0 + i] : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < (MR + 255) / 256; ++q) {
+      const int i = tid + 256 * q;
+      if (i < m) gb[r0 + posL[i]] = tmp[q];
+    }
+  }
+  if (tid == 0) nsw_out[b * nblk + blk] = nsw;
+}
+
+// Row permutation of one 64-column strip and, for a trailing strip, its U rows.
+template <int PW>
+__global__ __launch_bounds__(256) void lu_urow_kernel(float* __restrict__ W, int N, int r0,
+                                                      const int* __restrict__ src,
+                                                      const float* __restrict__ Xg,
+                                                      int nleft) {
+  constexpr int NSUB = PW / 16;
+  __shared__ float buf[2 * PW * 64];
+  __shared__ int list[2 * PW];
+  __shared__ int cnt;
+  __shared__ float L11[PW * (PW + 1)];
+  __shared__ float Ub[PW * 64];
+  __shared__ float Tw[4][256];
+  const int64_t b = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int strip = blockIdx.x;
+  const bool left = strip < nleft;
+  const int cstart = left ? 64 * strip : r0 + PW + 64 * (strip - nleft);
+  const int ncol = min(64, left ? r0 - cstart : N - cstart);
+  float* Wb = W + b * (int64_t)N * N;
+  const int* sb = src + b * N;
+  const int m = N - r0;
+  if (tid == 0) cnt = 0;
+  __syncthreads();
+  for (int p = tid; p < m; p += 256) {
+    if (sb[r0 + p] != r0 + p) {
+      const int k = atomicAdd(&cnt, 1);
+      if (k < 2 * PW) list[k] = p;
+    }
+  }
+  __syncthreads();
+  const int nm = min(cnt, 2 * PW);
+  // gather everything this strip needs before anything is written: the moved rows and,
+  // for a trailing strip, A12 (rows r0 .. r0+PW-1 of the new order) and L11
+  for (int e = tid; e < nm * 64; e += 256) {
+    const int k = e / 64, c = e % 64;
+    if (c < ncol) buf[k * 64 + c] = Wb[(int64_t)sb[r0 + list[k]] * N + cstart + c];
+  }
+  if (!left) {
+    for (int e = tid; e < PW * 64; e += 256) {
+      const int i = e / 64, c = e % 64;
+      Ub[e] = c < ncol ? Wb[(int64_t)sb[r0 + i] * N + cstart + c] : 0.0f;
+    }
+    for (int e = tid; e < PW * PW; e += 256) {
+      const int i = e / PW, c = e % PW;
+      L11[i * (PW + 1) + c] = Wb[(int64_t)(r0 + i) * N + r0 + c];
+    }
+  }
+  __syncthreads();
+  // rows r0 .. r0+PW-1 of a trailing strip are written below as U12
+  for (int e = tid; e < nm * 64; e += 256) {
+    const int k = e / 64, c = e % 64;
+    if (c < ncol && (left || list[k] >= PW))
+      Wb[(int64_t)(r0 + list[k]) * N + cstart + c] = buf[k * 64 + c];
+  }
+  if (left) return;
+  // U12 = L11^-1 A12 by blocks of 16 rows: U_s = X_s (A_s - sum_{t<s} L_st U_t)
+  // wave w owns columns [16w, 16w + 16) of the strip
+  const int li = lane & 15, g = lane >> 4;
+  const int col = 16 * wave + li;
+  const float* Xb = Xg + b * NSUB * 256;
+  for (int s = 0; s < NSUB; ++s) {
+    v4f acc;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = Ub[(16 * s + 4 * g + v) * 64 + col];
+    for (int t = 0; t < s; ++t) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc = mfma16(-L11[(16 * s + li) * (PW + 1) + 16 * t + 4 * q + g],
+                     Ub[(16 * t + 4 * q + g) * 64 + col], acc);
+    }
+    // to B layout through the wave's scratch, then U_s = X_s * acc
+#pragma unroll
+    for (int v = 0; v < 4; ++v) Tw[wave][(4 * g + v) * 16 + li] = acc[v];
+    wave_lds_fence();
+    v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) u = mfma16(Xb[s * 256 + li * 16 + 4 * q + g], Tw[wave][(4 * q + g) * 16 + li], u);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) Ub[(16 * s + 4 * g + v) * 64 + col] = u[v];
+    wave_lds_fence();
+  }
+  __syncthreads();
+  for (int e = tid; e < PW * 64; e += 256) {
+    const int i = e / 64, c = e % 64;
+    if (c < ncol) Wb[(int64_t)(r0 + i) * N + cstart + c] = Ub[e];
+  }
+}
+
+// (sign, logabs) from the pivots (B, N) and the swap counts (B, nblk); one wave per
+// matrix. Also flags matrices with an exactly zero pivot (zero_out, optional).
+__global__ void lu_finish_kernel(const float* __restrict__ piv, const int* __restrict__ nsw, int N,
+                                 int nblk, float* __restrict__ sign, float* __restrict__ logabs,
+                                 int64_t batch) {
+  const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (b >= batch) return;
+  float lg = 0.0f;
+  bool z = false, ng = false;
+  for (int i = lane; i < N; i += 64) {
+    const float v = piv[b * N + i];
+    z = z || (v == 0.0f);
+    ng = ng != (v < 0.0f);
+    lg += (v != 0.0f) ? logf(fabsf(v)) : 0.0f;
+  }
+  lg = wave_sum_f32(lg);
+  int sw = 0;
+  for (int k = lane; k < nblk; k += 64) sw += nsw[b * nblk + k];
+  sw = (int)wave_sum_f32((float)sw);
+  const bool anyz = __ballot(z) != 0ull;
+  const int negs = __popcll(__ballot(ng)) + sw;
+  if (lane == 0) {
+    sign[b] = anyz ? 0.0f : ((negs & 1) ? -1.0f : 1.0f);
+    logabs[b] = anyz ? -INFINITY : lg;
+  }
+}
+
+__global__ void iota_kernel(int* g0, int N, int64_t total) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < total) g0[e] = (int)(e % N);
+}
+
+int lu_large_padded(int n) {
+  if (n <= 512) return ((n + 63) / 64) * 64;
+  return ((n + 31) / 32) * 32;
+}
+
+size_t lu_large_workspace(int64_t batch, int n, bool parts) {
+  const int N = lu_large_padded(n);
+  const int PW = N <= 512 ? 64 : 32;
+  const int nblk = N / PW;
+  size_t bytes = 0;
+  auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
+  add((size_t)batch * N * N * 4);        // W
+  add((size_t)batch * N * 4);            // pivots
+  add((size_t)batch * nblk * 4);         // swap counts
+  add((size_t)batch * N * 4);            // src
+  add((size_t)batch * (PW / 16) * 1024); // X
+  if (parts) add((size_t)batch * N * 4); // g0
+  return bytes;
+}
+
+template <int MR, int PW>
+static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int* src, float* X,
+                      int* g0, bool fact, hipStream_t s) {
+  const int nblk = N / PW;
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int r0 = blk * PW;
+    hipLaunchKernelGGL((lu_panel_kernel<MR, PW>), dim3((unsigned)batch), dim3(256), 0, s, W, N, r0,
+                       blk, piv, nsw, nblk, src, X, g0);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    const int nleft = fact ? (r0 + 63) / 64 : 0;
+    const int nright = (N - r0 - PW + 63) / 64;
+    if (nleft + nright > 0) {
+      hipLaunchKernelGGL((lu_urow_kernel<PW>), dim3(nleft + nright, (unsigned)batch), dim3(256), 0, s,
+                         W, N, r0, src, X, nleft);
+      if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    }
+    const int mt = N - r0 - PW;
+    if (mt > 0) {
+      GemmDesc d = {};
+      d.A = W + (int64_t)(r0 + PW) * N + r0;
+      d.B = W + (int64_t)r0 * N + r0 + PW;
+      d.C = W + (int64_t)(r0 + PW) * N + r0 + PW;
+      d.sA = d.sB = d.sC = (int64_t)N * N;
+      d.lda = d.ldb = d.ldc = N;
+      d.M = mt;
+      d.N = mt;
+      d.K = PW;
+      d.alpha = -1.0f;
+      d.beta = 1.0f;
+      const int st = launch_gemm(d, batch, 1, s);
+      if (st != FX_OK) return st;
+    }
+  }
+  return FX_OK;
+}
+
+// Factor a (B, n, n) into the workspace; returns the packed LU (B, N, N) through *W_out
+// and the composed row map g0 (parts only) through *g0_out.
+int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
+                    size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s) {
+  const int N = lu_large_padded(n);
+  const int PW = N <= 512 ? 64 : 32;
+  const int nblk = N / PW;
+  if (N > 1024) return FX_ERR_UNSUPPORTED;
+  if (ws_bytes < lu_large_workspace(batch, n, parts) || !ws) return FX_ERR_WORKSPACE;
+  char* p = (char*)ws;
+  auto take = [&](size_t x) {
+    char* q = p;
+    p += (x + 255) / 256 * 256;
+    return (void*)q;
+  };
+  float* W = (float*)take((size_t)batch * N * N * 4);
+  float* piv = (float*)take((size_t)batch * N * 4);
+  int* nsw = (int*)take((size_t)batch * nblk * 4);
+  int* src = (int*)take((size_t)batch * N * 4);
+  float* X = (float*)take((size_t)batch * (PW / 16) * 1024);
+  int* g0 = parts ? (int*)take((size_t)batch * N * 4) : nullptr;
+  {
+    const int64_t tot = (int64_t)N * N;
+    hipLaunchKernelGGL(copy_pad_kernel, dim3((unsigned)((tot + 255) / 256), (unsigned)batch), dim3(256),
+                       0, s, A, n, W, N);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  }
+  if (g0) {
+    const int64_t tot = batch * N;
+    hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, g0, N, tot);
+  }
+  int st;
+  if (N <= 256)
+    st = run_blocks<256, 64>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+  else if (N <= 512)
+    st = run_blocks<512, 64>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+  else
+    st = run_blocks<1024, 32>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+  if (st != FX_OK) return st;
+  hipLaunchKernelGGL(lu_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, piv, nsw, N,
+                     nblk, sign, logabs, batch);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  if (W_out) *W_out = W;
+  if (g0_out) *g0_out = g0;
+  return FX_OK;
+}
+
+}  // namespace fx
