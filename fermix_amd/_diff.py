@@ -100,7 +100,7 @@ class _SlogdetParts(torch.autograd.Function):
     def jvp(ctx, dA):
         (invT,) = ctx.saved_tensors
         dlog = (invT * dA).sum(dim=(-1, -2))
-        return torch.zeros_like(dlog), dlog, None
+        return None, dlog, None
 
     @staticmethod
     def vmap(info, in_dims, A):
@@ -165,7 +165,7 @@ class _SlogpfParts(torch.autograd.Function):
     def jvp(ctx, dA, _skew):
         (Sinv,) = ctx.saved_tensors
         dlog = -0.5 * (Sinv * dA).sum(dim=(-1, -2))
-        return torch.zeros_like(dlog), dlog, None
+        return None, dlog, None
 
     @staticmethod
     def vmap(info, in_dims, A, skew):

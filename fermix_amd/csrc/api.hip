@@ -73,28 +73,60 @@ int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float*
   return FX_ERR_UNSUPPORTED;
 }
 
+static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
 size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n) {
-  (void)batch;
-  (void)n;
-  return 0;
+  if (batch <= 0 || n <= 0 || n > LARGE_MAX) return 0;
+  const int N = fx_lu_padded_size(n);
+  const bool copy = inv_padded(N) != N;
+  size_t bytes = 0;
+  if (n <= SMALL_MAX) {
+    bytes += align256((size_t)batch * N * N * 4) + align256((size_t)batch * N * 4);
+  } else {
+    bytes += align256(lu_large_workspace(batch, n, true));
+  }
+  return bytes + lu_inverse_workspace(batch, N, copy);
 }
 
 int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_singular,
                          float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  (void)zero_singular;
-  (void)workspace;
-  (void)workspace_bytes;
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if ((lu == nullptr) != (perm == nullptr)) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
-  if (inv_t) return FX_ERR_UNSUPPORTED;
-  if (n <= SMALL_MAX)
+  if (n > LARGE_MAX) return FX_ERR_UNSUPPORTED;
+  if (!inv_t && n <= SMALL_MAX && lu)  // factors only: straight into the caller's buffers
     return launch_lu_small(a, n, batch, sign, logabs, lu, (int*)perm, s);
-  return FX_ERR_UNSUPPORTED;
+  const size_t need = fx_slogdet_parts_f32_workspace(batch, n);
+  if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
+  const int N = fx_lu_padded_size(n);
+  char* p = (char*)workspace;
+  float* LU = nullptr;
+  int* g0 = nullptr;
+  int st;
+  if (n <= SMALL_MAX) {
+    LU = (float*)p;
+    p += align256((size_t)batch * N * N * 4);
+    g0 = (int*)p;
+    p += align256((size_t)batch * N * 4);
+    st = launch_lu_small(a, n, batch, sign, logabs, LU, g0, s);
+  } else {
+    const size_t wl = lu_large_workspace(batch, n, true);
+    st = launch_lu_large(a, n, batch, sign, logabs, p, wl, true, &LU, &g0, s);
+    p += align256(wl);
+  }
+  if (st != FX_OK) return st;
+  if (lu) {
+    if (hipMemcpyAsync(lu, LU, (size_t)batch * N * N * 4, hipMemcpyDeviceToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(perm, g0, (size_t)batch * N * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return FX_ERR_LAUNCH;
+  }
+  if (!inv_t) return FX_OK;
+  const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
+  return launch_lu_inverse(LU, g0, N, n, batch, sign, zero_singular, inv_t, true, p, rest, s);
 }
 
 size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n) {

@@ -26,6 +26,14 @@ size_t lu_large_workspace(int64_t batch, int n, bool parts);
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
                     size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s);
 
+// A^-T from the packed LU (B, N, N) and row map g0 (B, N) into invT (B, n, n); LU is
+// overwritten when in_place and N is a power-of-two multiple of 32 (inverse.hip).
+int inv_padded(int N);
+size_t lu_inverse_workspace(int64_t batch, int N, bool need_copy);
+int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, const float* sign,
+                      int zero_singular, float* invT, bool in_place, void* ws, size_t ws_bytes,
+                      hipStream_t s);
+
 // ------------------------------------------------------------------ batched GEMM
 // Masks apply to op(X) in global coordinates (row + off*r, col + off*c): elements
 // outside the triangle read as zero (unit diagonal for the *_UNIT kinds).

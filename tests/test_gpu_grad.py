@@ -1,0 +1,120 @@
+"""GPU parity of the gradients: slogdet (A^-T from the forward's own LU) against the CPU
+oracle and float64 truth; torch autograd / forward mode / vmap integration and the
+bit-identity of the differentiated primal (reference tests/test_fermix.py:309-326,
+373-425, 442-456, 608-647)."""
+
+import numpy as np
+import pytest
+import torch
+
+import fermix_amd
+from fermix_amd import _kernels
+from oracle import generic as g
+from tests.tolerances import assert_grad
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def _np(x):
+    return x.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 16, 17, 33, 48, 64, 100, 128, 129, 200, 256, 300, 512])
+def test_slogdet_invT_vs_float64_and_oracle(dev, n):
+    B = 12 if n <= 256 else 4
+    rng = np.random.default_rng(2000 + n)
+    A = (rng.standard_normal((B, n, n)) / np.sqrt(n)).astype(np.float32)
+    print(f"invT n={n} B={B}", flush=True)
+    s, l, invT, _, _ = _kernels.slogdet_parts(_t(A, dev))
+    s0, l0 = fermix_amd.slogdet(_t(A, dev))
+    assert torch.equal(s, s0) and torch.equal(l, l0), "parts primal != forward"
+    invT = _np(invT)
+    ref = np.linalg.inv(A.astype(np.float64)).transpose(0, 2, 1)
+    assert_grad(invT, ref, A, f"n={n} vs float64")
+    _, _, invo, _, _, _ = g.lu_parts_generic(A)
+    assert_grad(invT, invo, A, f"n={n} vs oracle")
+
+
+@pytest.mark.parametrize("n", [12, 40, 150])
+def test_slogdet_singular_gradient_zero(dev, n):
+    rng = np.random.default_rng(3000 + n)
+    A = rng.standard_normal((4, n, n)).astype(np.float32)
+    A[0, :, 3] = 0.0
+    A[2, 5, :] = 0.0
+    At = _t(A, dev).requires_grad_()
+    s, l = fermix_amd.slogdet(At)
+    assert np.isneginf(_np(l)[0]) and np.isneginf(_np(l)[2])
+    (gr,) = torch.autograd.grad(l[1] + l[3], At)
+    gr = _np(gr)
+    assert np.all(np.isfinite(gr))
+    assert np.all(gr[0] == 0) and np.all(gr[2] == 0)
+    ref = np.linalg.inv(A[1].astype(np.float64)).T
+    assert_grad(gr[1:2], ref[None], A[1:2], "singular batch member 1")
+    # zero_singular=False keeps the U~ inverse (finite) for the det gradient
+    _, _, inv2, _, _ = _kernels.slogdet_parts(_t(A, dev), zero_singular=False)
+    assert np.all(np.isfinite(_np(inv2)))
+
+
+def test_autograd_jvp_vmap_and_bit_identity(dev):
+    rng = np.random.default_rng(7)
+    n = 48
+    A = (rng.standard_normal((3, 2, n, n)) + 2 * np.eye(n)).astype(np.float32)
+    At = _t(A, dev)
+    s0, l0 = fermix_amd.slogdet(At)
+    Ag = At.clone().requires_grad_()
+    s1, l1 = fermix_amd.slogdet(Ag)
+    assert torch.equal(s0, s1) and torch.equal(l0, l1)  # primal bit-identical
+    w = torch.from_numpy(rng.standard_normal((3, 2)).astype(np.float32)).to(dev)
+    (gr,) = torch.autograd.grad((l1 * w).sum(), Ag)
+    ref = np.linalg.inv(A.astype(np.float64)).swapaxes(-1, -2) * _np(w)[:, :, None, None]
+    assert np.max(np.abs(_np(gr) - ref)) < 1e-4 * np.abs(ref).max()
+    # forward mode: d logabs = tr(A^-1 dA)
+    dA = torch.from_numpy(rng.standard_normal(A.shape).astype(np.float32)).to(dev)
+    (sp, lp), (ds, dl) = torch.func.jvp(lambda x: fermix_amd.slogdet(x), (At,), (dA,))
+    assert torch.equal(lp, l0) and torch.all(ds == 0)
+    want = np.einsum("...ij,...ij->...", np.linalg.inv(A.astype(np.float64)).swapaxes(-1, -2), _np(dA))
+    assert np.max(np.abs(_np(dl) - want)) < 1e-3 * max(1.0, np.abs(want).max())
+    # vmap over a leading dim == the batched call, bitwise
+    vs, vl = torch.func.vmap(lambda x: fermix_amd.slogdet(x))(At)
+    assert torch.equal(vs, s0) and torch.equal(vl, l0)
+    # torch.func.grad of a vmapped per-sample function
+    gfun = torch.func.vmap(torch.func.grad(lambda x: fermix_amd.slogdet(x)[1]))
+    gv = gfun(At.reshape(6, n, n))
+    ref1 = np.linalg.inv(A.reshape(6, n, n).astype(np.float64)).swapaxes(-1, -2)
+    assert np.max(np.abs(_np(gv) - ref1)) < 1e-4 * np.abs(ref1).max()
+
+
+def test_det_value_and_grad(dev):
+    rng = np.random.default_rng(8)
+    n = 20
+    A = (rng.standard_normal((4, n, n)) / np.sqrt(n) + np.eye(n)).astype(np.float32)
+    At = _t(A, dev).requires_grad_()
+    d = fermix_amd.det(At)
+    d64 = np.linalg.det(A.astype(np.float64))
+    assert np.allclose(_np(d), d64, rtol=1e-4)
+    (gr,) = torch.autograd.grad(d.sum(), At)
+    ref = d64[:, None, None] * np.linalg.inv(A.astype(np.float64)).swapaxes(-1, -2)
+    assert np.max(np.abs(_np(gr) - ref)) < 1e-4 * np.abs(ref).max()
+
+
+def test_c3_properties(dev):
+    """C3 size: B = 1024, n = 512, A iid N(0, 1/n). Primal bit-identical to the forward,
+    gradient finite, A^T invT = I on a subset in float64, a subset against the oracle."""
+    rng = np.random.default_rng(3)
+    B, n = 1024, 512
+    A = (rng.standard_normal((B, n, n), dtype=np.float32) * np.float32(1 / np.sqrt(n)))
+    At = _t(A, dev)
+    s, l, invT, _, _ = _kernels.slogdet_parts(At)
+    s0, l0 = fermix_amd.slogdet(At)
+    assert torch.equal(s, s0) and torch.equal(l, l0)
+    assert bool(torch.isfinite(invT).all())
+    idx = [0, 1, 511, 1023]
+    G = _np(invT[idx])
+    ref = np.linalg.inv(A[idx].astype(np.float64)).transpose(0, 2, 1)
+    assert_grad(G, ref, A[idx], "C3 subset vs float64")
+    _, _, invo, _, _, _ = g.lu_parts_generic(A[idx])
+    assert_grad(G, invo, A[idx], "C3 subset vs oracle")

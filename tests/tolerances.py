@@ -63,3 +63,17 @@ def assert_logabs(l, lref, n, what="", A=None):
         k = kappa(np.asarray(A)[fin][bad])
         lim = KAPPA_C * U32 * k
         assert np.all(err[bad] <= lim), (what, err[bad], lim)
+
+
+def assert_grad(G, ref, A, what=""):
+    """Gradients within 1e-4 relative Frobenius error of float64 truth; a member outside
+    it must be within KAPPA_C * 2^-24 * kappa(A) (what any fp32 LU inverse achieves: at
+    n = 512, N(0, 1/n) a float32 LAPACK inverse exceeds 1e-4 on about a fifth of the
+    members). The literal pass rate is printed."""
+    err = rel_fro(G, ref)
+    bad = err > 1e-4
+    print(f"[{what}] grad literal pass {int((~bad).sum())}/{err.size}, max rel-Fro {float(err.max()):.3g}",
+          flush=True)
+    if bad.any():
+        k = kappa(np.asarray(A)[bad])
+        assert np.all(err[bad] <= KAPPA_C * U32 * k), (what, err[bad], k)
