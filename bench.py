@@ -92,6 +92,25 @@ def bench_c1(steps, warmup):
                 bytes=B * (4 * n * n + 8), sample=A[:64].cpu().numpy())
 
 
+def bench_c3(steps, warmup):
+    """slogdet forward + VJP (cotangent ones on logabs), B = 1024, n = 512,
+    A iid N(0, 1/n)."""
+    import torch
+    import fermix_amd
+
+    B, n = 1024, 512
+    A = torch.from_numpy(_inputs(B, n, 0, scale=1.0 / np.sqrt(n))).cuda().requires_grad_()
+
+    def fn():
+        s, l = fermix_amd.slogdet(A)
+        (g,) = torch.autograd.grad(l.sum(), A)
+        return g
+
+    ms, wall = _time_gpu(fn, steps, warmup)
+    return dict(name="slogdet_fwd_grad", B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
+                bytes=B * 8 * n * n, flops=B * 2.0 * n ** 3, sample=None)
+
+
 def cpu_baseline(sample, which):
     """The CPU oracle on a bounded sample, one thread (matrices/s)."""
     from threadpoolctl import threadpool_limits
@@ -126,7 +145,7 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm GPU visible"}), flush=True)
         sys.exit(1)
-    only = set(args.only.split(",")) if args.only else {"c1", "c2"}
+    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3"}
     res = {}
     if "c2" in only:
         res["c2"] = bench_c2(args.steps, args.warmup)
@@ -134,7 +153,10 @@ def main():
     if "c1" in only:
         res["c1"] = bench_c1(args.steps, args.warmup)
         print(f"# c1 slogdet fwd: {res['c1']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
-    head = res.get("c2") or res.get("c1")
+    if "c3" in only:
+        res["c3"] = bench_c3(max(3, args.steps // 4), max(1, args.warmup // 2))
+        print(f"# c3 slogdet fwd+grad: {res['c3']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
+    head = res.get("c2") or res.get("c1") or res.get("c3")
     achieved = head["bytes"] / (head["ms"] * 1e-3) / 1e9
     roofline = {
         "bound": "hbm",
@@ -160,7 +182,8 @@ def main():
     workloads = {
         k: {"workload": v["name"], "B": v["B"], "n": v["n"], "ms_per_step": round(v["ms"], 5),
             "matrices_per_s": round(v["rate"], 1),
-            "hbm_frac": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "hbm_frac": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            **({"tflops_2n3": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2)} if "flops" in v else {})}
         for k, v in res.items()
     }
     line = {

@@ -93,19 +93,40 @@ def slogpf(A, skew_symmetrize):
 
 
 def slogpf_factors(A, skew_symmetrize):
-    """(sign, logabs, gbuf (B, N/16, N, 16), d (B, N/2), perm (B, N))."""
+    """(sign, logabs, gbuf (B, N/PB, N, PB), d (B, N/2), perm (B, N))."""
     _check_input(A)
     B, n, _ = A.shape
     dev = A.device
+    L = lib()
     N = pf_padded_size(n)
+    PB = int(L.fx_pf_block_columns(n))
     sign = torch.empty(B, dtype=A.dtype, device=dev)
     logabs = torch.empty(B, dtype=A.dtype, device=dev)
-    gbuf = torch.zeros((B, N // 16, N, 16), dtype=A.dtype, device=dev)
+    gbuf = torch.zeros((B, N // PB, N, PB), dtype=A.dtype, device=dev)
     d = torch.empty((B, N // 2), dtype=A.dtype, device=dev)
     perm = torch.empty((B, N), dtype=torch.int32, device=dev)
-    st = lib().fx_slogpf_factors_f32(
+    ws, wsb = _workspace(L.fx_slogpf_factors_f32_workspace(B, n), dev)
+    st = L.fx_slogpf_factors_f32(
         _ptr(A), B, n, int(bool(skew_symmetrize)), _ptr(sign), _ptr(logabs), _ptr(gbuf),
-        _ptr(d), _ptr(perm), _stream(A),
+        _ptr(d), _ptr(perm), _ptr(ws), wsb, _stream(A),
     )
     check(st, "fx_slogpf_factors_f32")
     return sign, logabs, gbuf, d, perm
+
+
+def slogpf_parts(A, skew_symmetrize):
+    """(sign, logabs, Sinv) of the (skew-symmetrised) batch from one Parlett-Reid run."""
+    _check_input(A)
+    B, n, _ = A.shape
+    dev = A.device
+    L = lib()
+    sign = torch.empty(B, dtype=A.dtype, device=dev)
+    logabs = torch.empty(B, dtype=A.dtype, device=dev)
+    g = torch.empty_like(A)
+    ws, wsb = _workspace(L.fx_slogpf_parts_f32_workspace(B, n), dev)
+    st = L.fx_slogpf_parts_f32(
+        _ptr(A), B, n, int(bool(skew_symmetrize)), 0, _ptr(sign), _ptr(logabs), _ptr(g),
+        _ptr(ws), wsb, _stream(A),
+    )
+    check(st, "fx_slogpf_parts_f32")
+    return sign, logabs, g

@@ -14,6 +14,18 @@ __global__ void fill2_kernel(float* a, float va, float* b, float vb, int64_t cou
   }
 }
 
+__global__ void fill_kernel(float* a, float v, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) a[i] = v;
+}
+
+// A fill kernel rather than hipMemsetAsync, so the call stays safe under graph capture.
+static int fill(float* a, float v, int64_t count, hipStream_t s) {
+  if (count <= 0) return FX_OK;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s, a, v, count);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
 static int fill2(float* a, float va, float* b, float vb, int64_t count, hipStream_t s) {
   if (count <= 0) return FX_OK;
   const unsigned blocks = (unsigned)((count + 255) / 256);
@@ -23,6 +35,7 @@ static int fill2(float* a, float va, float* b, float vb, int64_t count, hipStrea
 
 static constexpr int SMALL_MAX = 128;
 static constexpr int LARGE_MAX = 1024;
+static constexpr int PF_LARGE_MAX = 2048;
 
 }  // namespace fx
 
@@ -51,8 +64,11 @@ int32_t fx_lu_padded_size(int32_t n) {
 
 int32_t fx_pf_padded_size(int32_t n) {
   if (n <= 0) return 0;
-  return n <= SMALL_MAX ? pf_small_padded(n) : -1;
+  if (n <= SMALL_MAX) return pf_small_padded(n);
+  return n <= PF_LARGE_MAX ? pf_large_padded(n) : -1;
 }
+
+int32_t fx_pf_block_columns(int32_t n) { return n <= SMALL_MAX ? 16 : 32; }
 
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || n <= SMALL_MAX || n > LARGE_MAX) return 0;
@@ -130,39 +146,91 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
 }
 
 size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n) {
-  (void)batch;
-  (void)n;
-  return 0;
+  if (batch <= 0 || n <= SMALL_MAX || n > PF_LARGE_MAX || n % 2) return 0;
+  return pf_large_workspace(batch, n, false);
 }
 
 int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign,
                   float* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   if (n % 2 == 1) return fill2(sign, 0.0f, logabs, -INFINITY, batch, s);
-  if (n <= SMALL_MAX)
-    return launch_pf_small(a, n, skew_symmetrize ? 1 : 0, batch, sign, logabs, nullptr, nullptr,
-                           nullptr, s);
+  const int sk = skew_symmetrize ? 1 : 0;
+  if (n <= SMALL_MAX) return launch_pf_small(a, n, sk, batch, sign, logabs, nullptr, nullptr, nullptr, s);
+  if (n <= PF_LARGE_MAX)
+    return launch_pf_large(a, n, sk, batch, sign, logabs, nullptr, nullptr, nullptr, workspace, workspace_bytes, s);
   return FX_ERR_UNSUPPORTED;
+}
+
+size_t fx_slogpf_factors_f32_workspace(int64_t batch, int32_t n) {
+  if (batch <= 0 || n <= SMALL_MAX || n > PF_LARGE_MAX || n % 2) return 0;
+  return pf_large_workspace(batch, n, true);
 }
 
 int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
                           float* sign, float* logabs, float* gbuf, float* d, int32_t* perm,
-                          fx_stream_t stream) {
+                          void* workspace, size_t workspace_bytes, fx_stream_t stream) {
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || !gbuf || !d || !perm || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if (n == 0 || n % 2 == 1) return FX_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
-  if (n <= SMALL_MAX)
-    return launch_pf_small(a, n, skew_symmetrize ? 1 : 0, batch, sign, logabs, gbuf, d, (int*)perm,
-                           s);
+  const int sk = skew_symmetrize ? 1 : 0;
+  if (n <= SMALL_MAX) return launch_pf_small(a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, s);
+  if (n <= PF_LARGE_MAX)
+    return launch_pf_large(a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, workspace, workspace_bytes, s);
   return FX_ERR_UNSUPPORTED;
+}
+
+size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n) {
+  if (batch <= 0 || n <= 0 || n % 2 || n > PF_LARGE_MAX) return 0;
+  const int N = fx_pf_padded_size(n);
+  size_t bytes = align256((size_t)batch * N * N * 4) + align256((size_t)batch * N / 2 * 4) +
+                 align256((size_t)batch * N * 4);
+  if (n > SMALL_MAX) bytes += align256(pf_large_workspace(batch, n, true));
+  return bytes + pf_inverse_workspace(batch, N);
+}
+
+int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
+                        float* sign, float* logabs, float* g, void* workspace, size_t workspace_bytes,
+                        fx_stream_t stream) {
+  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (batch == 0) return FX_OK;
+  if (!sign || !logabs || !g || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
+  if (adjugate) return FX_ERR_UNSUPPORTED;
+  hipStream_t s = (hipStream_t)stream;
+  if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
+  if (n % 2 == 1) {
+    int st = fill2(sign, 0.0f, logabs, -INFINITY, batch, s);
+    if (st != FX_OK) return st;
+    return fill(g, 0.0f, batch * (int64_t)n * n, s);
+  }
+  if (n > PF_LARGE_MAX) return FX_ERR_UNSUPPORTED;
+  const size_t need = fx_slogpf_parts_f32_workspace(batch, n);
+  if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
+  const int N = fx_pf_padded_size(n);
+  char* p = (char*)workspace;
+  float* gbuf = (float*)p;
+  p += align256((size_t)batch * N * N * 4);
+  float* d = (float*)p;
+  p += align256((size_t)batch * N / 2 * 4);
+  int* perm = (int*)p;
+  p += align256((size_t)batch * N * 4);
+  const int sk = skew_symmetrize ? 1 : 0;
+  int st;
+  if (n <= SMALL_MAX) {
+    st = launch_pf_small(a, n, sk, batch, sign, logabs, gbuf, d, perm, s);
+  } else {
+    const size_t wl = pf_large_workspace(batch, n, true);
+    st = launch_pf_large(a, n, sk, batch, sign, logabs, gbuf, d, perm, p, wl, s);
+    p += align256(wl);
+  }
+  if (st != FX_OK) return st;
+  const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
+  return launch_pf_inverse(gbuf, n <= SMALL_MAX ? 16 : 32, d, perm, N, n, batch, g, p, rest, s);
 }
 
 }  // extern "C"

@@ -34,6 +34,22 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
                       int zero_singular, float* invT, bool in_place, void* ws, size_t ws_bytes,
                       hipStream_t s);
 
+// 128 < n <= 2048 Parlett-Reid (pf_large.hip); with gbuf the factors (B, N/32, N, 32) by
+// original row, d (B, N/2) and perm (B, N).
+int pf_large_padded(int n);
+size_t pf_large_workspace(int64_t batch, int n, bool fact);
+int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
+                    float* gbuf, float* dout, int* perm, void* ws, size_t ws_bytes, hipStream_t s);
+
+// In-place unit-lower (and upper) triangular inverses of a packed (B, Ninv, Ninv) buffer.
+int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper, hipStream_t s);
+int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hipStream_t s);
+
+// S^-1 (B, n, n) from the Parlett-Reid factors (gbuf with PB columns per block, d, perm).
+size_t pf_inverse_workspace(int64_t batch, int N);
+int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm, int N, int n, int64_t batch,
+                      float* out, void* ws, size_t ws_bytes, hipStream_t s);
+
 // ------------------------------------------------------------------ batched GEMM
 // Masks apply to op(X) in global coordinates (row + off*r, col + off*c): elements
 // outside the triangle read as zero (unit diagonal for the *_UNIT kinds).

@@ -122,49 +122,11 @@ __global__ __launch_bounds__(256) void scatter_invT_kernel(const float* __restri
   }
 }
 
-int inv_padded(int N) {
-  int p = 32;
-  while (p < N) p *= 2;
-  return p;
-}
-
-size_t lu_inverse_workspace(int64_t batch, int N, bool need_copy) {
-  const int Ninv = inv_padded(N);
-  const int nt = (N + 63) / 64;
-  size_t bytes = 0;
-  auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
-  if (need_copy) add((size_t)batch * Ninv * Ninv * 4);  // T
-  add((size_t)batch * Ninv * Ninv / 4 * 4);              // Tmp (largest level: Ninv/2 x Ninv/2)
-  add((size_t)batch * Ninv * Ninv * 4);                  // Z
-  add((size_t)batch * nt * nt * 4);                      // flags
-  add((size_t)batch * 4);                                // bad
-  return bytes;
-}
-
-int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, const float* sign,
-                      int zero_singular, float* invT, bool in_place, void* ws, size_t ws_bytes,
-                      hipStream_t s) {
-  const int Ninv = inv_padded(N);
-  const bool need_copy = !(in_place && Ninv == N);
-  if (!ws || ws_bytes < lu_inverse_workspace(batch, N, need_copy)) return FX_ERR_WORKSPACE;
-  char* p = (char*)ws;
-  auto take = [&](size_t x) {
-    char* q = p;
-    p += (x + 255) / 256 * 256;
-    return (void*)q;
-  };
-  float* T = need_copy ? (float*)take((size_t)batch * Ninv * Ninv * 4) : LU;
-  float* Tmp = (float*)take((size_t)batch * Ninv * Ninv / 4 * 4);
-  float* Z = (float*)take((size_t)batch * Ninv * Ninv * 4);
-  const int nt = (N + 63) / 64;
-  int* flags = (int*)take((size_t)batch * nt * nt * 4);
-  int* bad = (int*)take((size_t)batch * 4);
+// In-place inverses of the unit-lower L (strictly lower part) and, with upper, of the
+// upper U~ (upper part incl. diagonal) packed in T (B, Ninv, Ninv); Tmp holds
+// B * Ninv^2 / 4 floats.
+int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper, hipStream_t s) {
   const int64_t NN = (int64_t)Ninv * Ninv;
-  if (need_copy) {
-    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((NN + 255) / 256), (unsigned)batch), dim3(256), 0, s,
-                       LU, N, T, Ninv);
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  }
   hipLaunchKernelGGL(leaf_inverse_kernel, dim3(Ninv / 32, (unsigned)batch), dim3(64), 0, s, T, Ninv);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   for (int sz = 32; sz < Ninv; sz *= 2) {
@@ -208,6 +170,7 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
     e.beta = 0.0f;
     st = launch_gemm(e, batch, pairs, s);
     if (st != FX_OK) return st;
+    if (!upper) continue;
     // U: Tmp = U12 * Y22
     GemmDesc f = {};
     f.M = f.N = f.K = sz;
@@ -249,6 +212,58 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
     st = launch_gemm(h, batch, pairs, s);
     if (st != FX_OK) return st;
   }
+  return FX_OK;
+}
+
+int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hipStream_t s) {
+  return launch_tri_inverse(T, Ninv, batch, Tmp, false, s);
+}
+
+int inv_padded(int N) {
+  int p = 32;
+  while (p < N) p *= 2;
+  return p;
+}
+
+size_t lu_inverse_workspace(int64_t batch, int N, bool need_copy) {
+  const int Ninv = inv_padded(N);
+  const int nt = (N + 63) / 64;
+  size_t bytes = 0;
+  auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
+  if (need_copy) add((size_t)batch * Ninv * Ninv * 4);  // T
+  add((size_t)batch * Ninv * Ninv / 4 * 4);              // Tmp (largest level: Ninv/2 x Ninv/2)
+  add((size_t)batch * Ninv * Ninv * 4);                  // Z
+  add((size_t)batch * nt * nt * 4);                      // flags
+  add((size_t)batch * 4);                                // bad
+  return bytes;
+}
+
+int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, const float* sign,
+                      int zero_singular, float* invT, bool in_place, void* ws, size_t ws_bytes,
+                      hipStream_t s) {
+  const int Ninv = inv_padded(N);
+  const bool need_copy = !(in_place && Ninv == N);
+  if (!ws || ws_bytes < lu_inverse_workspace(batch, N, need_copy)) return FX_ERR_WORKSPACE;
+  char* p = (char*)ws;
+  auto take = [&](size_t x) {
+    char* q = p;
+    p += (x + 255) / 256 * 256;
+    return (void*)q;
+  };
+  float* T = need_copy ? (float*)take((size_t)batch * Ninv * Ninv * 4) : LU;
+  float* Tmp = (float*)take((size_t)batch * Ninv * Ninv / 4 * 4);
+  float* Z = (float*)take((size_t)batch * Ninv * Ninv * 4);
+  const int nt = (N + 63) / 64;
+  int* flags = (int*)take((size_t)batch * nt * nt * 4);
+  int* bad = (int*)take((size_t)batch * 4);
+  const int64_t NN = (int64_t)Ninv * Ninv;
+  if (need_copy) {
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((NN + 255) / 256), (unsigned)batch), dim3(256), 0, s,
+                       LU, N, T, Ninv);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  }
+  int st0 = launch_tri_inverse(T, Ninv, batch, Tmp, true, s);
+  if (st0 != FX_OK) return st0;
   // Z = U~^-1 L^-1 (only the leading N x N block is used)
   {
     GemmDesc d = {};

@@ -1,0 +1,237 @@
+// S^-1 from the forward's own Parlett-Reid factors (the slogpf backward), any N. With
+// P S' P^T = L D L^T, D = diag_s(d_s J), the pivot K of smallest |d| and d~ = d with d_K
+// and exact zeros replaced by 1:
+//   L~ = L with the a-columns scaled by 1/d~ (unit lower), Y = L~^-1,
+//   DY = rows (Y[p_s], -Y[a_s]) / d~_s,   R = Y^T DY (exactly skew),
+//   S^-1 = -P^T [R + c (w v^T - v w^T)] P,  w = R e_{a_K}, v = Y^T e_{a_K},
+//   c = (1 - d_K) / d_K (0 for d_K = 0), zeroed for d_K = 0 or a non-finite result.
+// Kernels: pivot / coefficient prep (one wave per matrix), L~ assembly, the triangular
+// inverse of inverse.hip (lower half only), DY, the skew GEMM R (lower tiles + mirror),
+// the rank-2 correction with the non-finite flags, and the permutation gather.
+//
+// Reference roles replaced (ChenAo-Phys/fermix): _pf_parts (src/fermix/_pfinv.py:196-269)
+// with _pf_assemble_kernel (:80-137), _pf_maps (:140-157), the skew _bgemm for R and
+// _adj_perm_kernel (:161-192); the scalar helpers _pivot_index / _pair_scale /
+// _pf_adj_coeffs (src/fermix/_fallback.py:101-176).
+#include "common.h"
+#include "fermix_internal.h"
+
+namespace fx {
+
+struct PfCoef {
+  int K;      // pair index of the smallest |d| among the real pairs
+  int bad;    // d_K == 0 (inverse mode: zero the result)
+  float a1;   // coefficient of R
+  float a2;   // coefficient of (w v^T - v w^T)
+};
+
+// One wave per matrix: K, 1/d~, coefficients, and the inverse permutation.
+__global__ void pf_prep_kernel(const float* __restrict__ d, int H, int hreal, const int* __restrict__ perm, int N,
+                               float* __restrict__ dinv, int* __restrict__ iperm, PfCoef* __restrict__ coef,
+                               int64_t batch) {
+  const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (b >= batch) return;
+  const float* db = d + b * H;
+  // argmin |d| over s < hreal, first index on ties
+  unsigned best = 0xffffffffu;
+  int bi = 0;
+  for (int s = lane; s < hreal; s += 64) {
+    const unsigned k = __float_as_uint(fabsf(db[s]));
+    if (k < best) { best = k; bi = s; }
+  }
+  // wave argmin (key, index): reduce keys, then the lowest index holding the minimum
+  unsigned m = best;
+  for (int off = 32; off >= 1; off >>= 1) m = min(m, (unsigned)__shfl_xor((int)m, off));
+  int cand = (best == m) ? bi : 0x7fffffff;
+  for (int off = 32; off >= 1; off >>= 1) cand = min(cand, __shfl_xor(cand, off));
+  const int K = cand;
+  const float dK = db[K];
+  for (int s = lane; s < H; s += 64) {
+    const float v = db[s];
+    const float dt = (s == K || v == 0.0f) ? 1.0f : v;
+    dinv[b * H + s] = 1.0f / dt;
+  }
+  for (int f = lane; f < N; f += 64) iperm[b * N + perm[b * N + f]] = f;
+  if (lane == 0) {
+    PfCoef c;
+    c.K = K;
+    c.bad = dK == 0.0f;
+    c.a1 = 1.0f;
+    c.a2 = dK != 0.0f ? (1.0f - dK) / dK : 0.0f;
+    coef[b] = c;
+  }
+}
+
+// T[f][c] = L~[f][c] (f > c), 1 on the diagonal, 0 above; identity beyond N.
+__global__ void pf_assemble_kernel(const float* __restrict__ gbuf, int PB, int N, const int* __restrict__ perm,
+                                   const float* __restrict__ dinv, float* __restrict__ T, int Ninv) {
+  const int64_t b = blockIdx.y;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)Ninv * Ninv) return;
+  const int f = (int)(e / Ninv), c = (int)(e % Ninv);
+  float v;
+  if (f == c) {
+    v = 1.0f;
+  } else if (f < N && c < N && f > (c | 1)) {
+    const int s = c >> 1, k = c / PB, col = c % PB;
+    const int nb = N / PB;
+    const int o = perm[b * N + f];
+    const float* g = gbuf + ((b * nb + k) * (int64_t)N + o) * PB;
+    // column a = 2s holds w / d~ (w in G column 2t+1), column p = 2s+1 holds tau (G column 2t)
+    v = (c & 1) ? g[col - 1] : g[col + 1] * dinv[b * (N / 2) + s];
+  } else {
+    v = 0.0f;
+  }
+  T[b * (int64_t)Ninv * Ninv + e] = v;
+}
+
+// DY[2s] = Y[2s+1] / d~_s, DY[2s+1] = -Y[2s] / d~_s with Y the unit-lower part of T.
+__global__ void pf_dy_kernel(const float* __restrict__ T, int Ninv, int N, const float* __restrict__ dinv,
+                             float* __restrict__ DY) {
+  const int64_t b = blockIdx.y;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)N * N) return;
+  const int r = (int)(e / N), j = (int)(e % N);
+  const int src = r ^ 1;
+  const float y = src > j ? T[b * (int64_t)Ninv * Ninv + (int64_t)src * Ninv + j] : (src == j ? 1.0f : 0.0f);
+  const float sc = dinv[b * (N / 2) + (r >> 1)];
+  DY[b * (int64_t)N * N + e] = (r & 1) ? -y * sc : y * sc;
+}
+
+// PT = -(a1 R + a2 (w v^T - v w^T)); flags non-finite 64x64 tiles.
+__global__ void pf_adj_kernel(const float* __restrict__ R, float* __restrict__ PT, int N, const float* __restrict__ T,
+                              int Ninv, const PfCoef* __restrict__ coef, int* __restrict__ flags) {
+  const int64_t b = blockIdx.y;
+  const int nt = (N + 63) / 64;
+  const int tile = blockIdx.x;
+  const int f0 = (tile / nt) * 64, c0 = (tile % nt) * 64;
+  const PfCoef cf = coef[b];
+  const int aK = 2 * cf.K;
+  const float* Rb = R + b * (int64_t)N * N;
+  float* Pb = PT + b * (int64_t)N * N;
+  const float* Tb = T + b * (int64_t)Ninv * Ninv;
+  bool badv = false;
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int f = f0 + e / 64, c = c0 + e % 64;
+    if (f < N && c < N) {
+      const float wf = Rb[(int64_t)f * N + aK], wc = Rb[(int64_t)c * N + aK];
+      // v = Y^T e_aK: v[j] = Y[aK][j] (unit lower: j < aK stored, j == aK one, j > aK zero)
+      const float v_f = f < aK ? Tb[(int64_t)aK * Ninv + f] : (f == aK ? 1.0f : 0.0f);
+      const float v_c = c < aK ? Tb[(int64_t)aK * Ninv + c] : (c == aK ? 1.0f : 0.0f);
+      const float r = Rb[(int64_t)f * N + c];
+      const float val = -(cf.a1 * r + cf.a2 * (wf * v_c - v_f * wc));
+      badv = badv || !isfinite(val);
+      Pb[(int64_t)f * N + c] = val;
+    }
+  }
+  const int any = __syncthreads_or(badv ? 1 : 0);
+  if (threadIdx.x == 0) flags[b * (nt * nt) + tile] = any;
+}
+
+__global__ void pf_reduce_bad_kernel(const int* __restrict__ flags, int ntiles, const PfCoef* __restrict__ coef,
+                                     int* __restrict__ bad, int64_t batch) {
+  const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (b >= batch) return;
+  bool f = false;
+  for (int k = lane; k < ntiles; k += 64) f = f || flags[b * ntiles + k] != 0;
+  const bool any = __ballot(f) != 0ull;
+  if (lane == 0) bad[b] = (any || coef[b].bad) ? 1 : 0;
+}
+
+// out[i][j] = PT[iperm i][iperm j] for i, j < n (or 0 for a bad member).
+__global__ void pf_gather_kernel(const float* __restrict__ PT, int N, const int* __restrict__ iperm, int n,
+                                 const int* __restrict__ bad, float* __restrict__ out) {
+  const int64_t b = blockIdx.y;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)n * n) return;
+  const int i = (int)(e / n), j = (int)(e % n);
+  const int* ip = iperm + b * N;
+  out[b * (int64_t)n * n + e] = bad[b] ? 0.0f : PT[b * (int64_t)N * N + (int64_t)ip[i] * N + ip[j]];
+}
+
+size_t pf_inverse_workspace(int64_t batch, int N) {
+  const int Ninv = inv_padded(N);
+  const int nt = (N + 63) / 64;
+  size_t bytes = 0;
+  auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
+  add((size_t)batch * Ninv * Ninv * 4);  // T (L~, then Y)
+  add((size_t)batch * Ninv * Ninv);      // Tmp (Ninv/2 x Ninv/2 floats)
+  add((size_t)batch * N * N * 4);        // DY
+  add((size_t)batch * N * N * 4);        // R / PT
+  add((size_t)batch * N / 2 * 4);        // dinv
+  add((size_t)batch * N * 4);            // iperm
+  add((size_t)batch * sizeof(PfCoef));
+  add((size_t)batch * nt * nt * 4);      // flags
+  add((size_t)batch * 4);                // bad
+  return bytes;
+}
+
+int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm, int N, int n, int64_t batch,
+                      float* out, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int Ninv = inv_padded(N);
+  if (!ws || ws_bytes < pf_inverse_workspace(batch, N)) return FX_ERR_WORKSPACE;
+  char* p = (char*)ws;
+  auto take = [&](size_t x) {
+    char* q = p;
+    p += (x + 255) / 256 * 256;
+    return (void*)q;
+  };
+  float* T = (float*)take((size_t)batch * Ninv * Ninv * 4);
+  float* Tmp = (float*)take((size_t)batch * Ninv * Ninv);
+  float* DY = (float*)take((size_t)batch * N * N * 4);
+  float* R = (float*)take((size_t)batch * N * N * 4);
+  float* dinv = (float*)take((size_t)batch * N / 2 * 4);
+  int* iperm = (int*)take((size_t)batch * N * 4);
+  PfCoef* coef = (PfCoef*)take((size_t)batch * sizeof(PfCoef));
+  const int nt = (N + 63) / 64;
+  int* flags = (int*)take((size_t)batch * nt * nt * 4);
+  int* bad = (int*)take((size_t)batch * 4);
+  const int64_t NN = (int64_t)Ninv * Ninv;
+  const unsigned wb = (unsigned)((batch + 3) / 4);
+  hipLaunchKernelGGL(pf_prep_kernel, dim3(wb), dim3(256), 0, s, d, N / 2, n / 2, perm, N, dinv, iperm, coef, batch);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  hipLaunchKernelGGL(pf_assemble_kernel, dim3((unsigned)((NN + 255) / 256), (unsigned)batch), dim3(256), 0, s,
+                     gbuf, PB, N, perm, dinv, T, Ninv);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  int st = launch_unit_lower_inverse(T, Ninv, batch, Tmp, s);
+  if (st != FX_OK) return st;
+  const int64_t MM = (int64_t)N * N;
+  hipLaunchKernelGGL(pf_dy_kernel, dim3((unsigned)((MM + 255) / 256), (unsigned)batch), dim3(256), 0, s, T, Ninv, N,
+                     dinv, DY);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  {
+    // R = Y^T DY: op(A) = Y^T (upper, unit diagonal), lower tiles, mirrored skew
+    GemmDesc g = {};
+    g.M = g.N = g.K = N;
+    g.A = T;
+    g.transA = 1;
+    g.maskA = MASK_UPPER_UNIT;
+    g.lda = Ninv;
+    g.sA = NN;
+    g.B = DY;
+    g.ldb = N;
+    g.sB = MM;
+    g.C = R;
+    g.ldc = N;
+    g.sC = MM;
+    g.alpha = 1.0f;
+    g.beta = 0.0f;
+    g.lower_only = 1;
+    g.mirror = -1.0f;
+    st = launch_gemm(g, batch, 1, s);
+    if (st != FX_OK) return st;
+  }
+  float* PT = DY;  // DY is dead once R is formed
+  hipLaunchKernelGGL(pf_adj_kernel, dim3(nt * nt, (unsigned)batch), dim3(256), 0, s, R, PT, N, T, Ninv, coef, flags);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  hipLaunchKernelGGL(pf_reduce_bad_kernel, dim3(wb), dim3(256), 0, s, flags, nt * nt, coef, bad, batch);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  const int64_t nn = (int64_t)n * n;
+  hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)((nn + 255) / 256), (unsigned)batch), dim3(256), 0, s, PT, N,
+                     iperm, n, bad, out);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+}  // namespace fx

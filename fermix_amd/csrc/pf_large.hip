@@ -1,0 +1,405 @@
+// Blocked Parlett-Reid with partial pivoting for 128 < n <= 2048 (any batch). The skew
+// matrix lives in two ping-pong buffers (full storage, exactly skew). Per block of
+// PB = 16 pair steps (32 columns) at r0:
+//   1. pf_panel_kernel (one workgroup of NT = 256..1024 threads per matrix, each lane
+//      owning 2 of the m = N - r0 rows): the 16 pair steps with the tau / w vectors kept
+//      in registers as G (m x 32); column a and column p of the current matrix are read
+//      as rows of the block-start matrix (skew) plus the G corrections; each pair step
+//      has two workgroup barriers (the row at position c, the pivot). The permutation is
+//      virtual inside the block; the kernel writes G in the block's new row order and
+//      the map src[new position] = old row;
+//   2. pf_update_kernel (matrix x lower-triangle 64x64 tile): M'' = M[src, src] + G J G^T
+//      on fp32 MFMA (K = 32), reading the old buffer through the permutation and writing
+//      the new buffer in the new order, lower tile plus its mirrored (negated) transpose
+//      through LDS, so both stores are coalesced and M'' stays exactly skew.
+// Reference roles replaced (ChenAo-Phys/fermix): _pf_run / _pf_core (src/fermix/_pf.py:
+// 497-570), the pair-step panel (:59-284) and the rank-2b update (:287-382).
+#include "common.h"
+#include "fermix_internal.h"
+
+namespace fx {
+
+constexpr int PFB = 32;  // columns per block (16 pair steps)
+
+struct PfCand {
+  unsigned key;
+  int row;
+  int pos;
+  float xv;  // x at the candidate row (d = -x[p])
+  float g[PFB];
+};
+
+struct PfRowA {
+  int row;
+  int pad[3];
+  float g[PFB];
+};
+
+// Copy a (B, n, n) into M (B, N, N): S = (a - a^T)/2 (or a) with [[0,1],[-1,0]] padding.
+__global__ void pf_copy_pad_kernel(const float* __restrict__ A, int n, int skew, float* __restrict__ M, int N) {
+  const int64_t b = blockIdx.y;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)N * N) return;
+  const int r = (int)(e / N), c = (int)(e % N);
+  const float* Ab = A + b * (int64_t)n * n;
+  float v;
+  if (r < n && c < n) {
+    v = skew ? (Ab[(int64_t)r * n + c] - Ab[(int64_t)c * n + r]) * 0.5f : Ab[(int64_t)r * n + c];
+  } else {
+    v = ((r ^ c) == 1 && r >= n) ? ((r & 1) ? -1.0f : 1.0f) : 0.0f;
+  }
+  M[b * (int64_t)N * N + e] = v;
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ M, int N, int r0, int blk,
+                                                      int nblk, float* __restrict__ d_out,
+                                                      int* __restrict__ nsw_out,
+                                                      int* __restrict__ src_out,
+                                                      float* __restrict__ Gn,
+                                                      int* __restrict__ orig,
+                                                      float* __restrict__ gbuf) {
+  constexpr int R = 2, NW = NT / 64;
+  __shared__ PfRowA rowa;
+  __shared__ PfCand cand[2][NW];
+  __shared__ int posL[NT * R];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int m = N - r0;
+  const float* Mb = M + b * (int64_t)N * N + (int64_t)r0 * N + r0;  // block-start trailing matrix
+  float G[R][PFB];
+  int pos[R];
+  bool valid[R];
+#pragma unroll
+  for (int s = 0; s < R; ++s) {
+    const int i = R * tid + s;
+    valid[s] = i < m;
+    pos[s] = i;
+#pragma unroll
+    for (int k = 0; k < PFB; ++k) G[s][k] = 0.0f;
+  }
+  int nsw = 0;
+  static_for<0, PFB / 2>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
+    const int c = 2 * t;  // local position of row a
+    // 1. the row at position c publishes its index and G row
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      if (valid[s] && pos[s] == c) {
+        rowa.row = R * tid + s;
+#pragma unroll
+        for (int k = 0; k < 2 * t; ++k) rowa.g[k] = G[s][k];
+      }
+    }
+    __syncthreads();
+    const int qa = rowa.row;
+    const float* ga = rowa.g;
+    // x = column a of the current matrix on my rows: M[i][qa] = -M[qa][i] + corrections
+    float x[R];
+    {
+      const float* rowp = Mb + (int64_t)qa * N;
+      float mv[R];
+#pragma unroll
+      for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowp[R * tid + s] : 0.0f;
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        float v = -mv[s];
+#pragma unroll
+        for (int u = 0; u < t; ++u) {
+          v = fmaf(G[s][2 * u], ga[2 * u + 1], v);
+          v = fmaf(-G[s][2 * u + 1], ga[2 * u], v);
+        }
+        x[s] = v;
+      }
+    }
+    // 2. pivot: largest |x| among the rows after position c (ties: lowest row)
+    unsigned kb = 0;
+    int ib = 0;
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      const unsigned k = cand_key(x[s], valid[s] && pos[s] > c);
+      if (k > kb) { kb = k; ib = s; }
+    }
+    const unsigned gk = wave_max_u32(kb);
+    const int pl = first_lane(gk != 0u ? (kb == gk) : (lane == 0));
+    PfCand& my = cand[t & 1][wave];
+    if (lane == pl) {
+      my.key = gk;
+      my.row = R * tid + ib;
+      float xv = x[0];
+      int pv = pos[0];
+      float gv[PFB];
+#pragma unroll
+      for (int k = 0; k < 2 * t; ++k) gv[k] = G[0][k];
+#pragma unroll
+      for (int s = 1; s < R; ++s) {
+        if (ib == s) {
+          xv = x[s];
+          pv = pos[s];
+#pragma unroll
+          for (int k = 0; k < 2 * t; ++k) gv[k] = G[s][k];
+        }
+      }
+      my.pos = pv;
+      my.xv = xv;
+#pragma unroll
+      for (int k = 0; k < 2 * t; ++k) my.g[k] = gv[k];
+    }
+    __syncthreads();
+    unsigned best = cand[t & 1][0].key;
+    int wb = 0;
+    for (int w = 1; w < NW; ++w) {
+      const unsigned kw = cand[t & 1][w].key;
+      if (kw > best) { best = kw; wb = w; }
+    }
+    const PfCand& win = cand[t & 1][wb];
+    const int qp = win.row, pp = win.pos;
+    const float d = -win.xv;  // M[a][p] = -M[p][a]
+    const float* gp = win.g;
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      if (valid[s] && pos[s] == c + 1) pos[s] = pp;
+      if (R * tid + s == qp) pos[s] = c + 1;
+    }
+    nsw += (pp != c + 1) ? 1 : 0;
+    if (tid == 0) d_out[b * (N / 2) + (r0 >> 1) + t] = d;
+    // y = column p on my rows
+    float y[R];
+    {
+      const float* rowp = Mb + (int64_t)qp * N;
+      float mv[R];
+#pragma unroll
+      for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowp[R * tid + s] : 0.0f;
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        float v = -mv[s];
+#pragma unroll
+        for (int u = 0; u < t; ++u) {
+          v = fmaf(G[s][2 * u], gp[2 * u + 1], v);
+          v = fmaf(-G[s][2 * u + 1], gp[2 * u], v);
+        }
+        y[s] = v;
+      }
+    }
+    const float inv = safe_rcp(d);
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      const bool act = valid[s] && pos[s] > c + 1;
+      G[s][2 * t] = act ? -x[s] * inv : 0.0f;
+      G[s][2 * t + 1] = act ? y[s] : 0.0f;
+    }
+  });
+  // outputs: G in the new row order, the position map, factors by original row
+#pragma unroll
+  for (int s = 0; s < R; ++s) {
+    const int i = R * tid + s;
+    if (valid[s]) {
+      posL[i] = pos[s];
+      float* gr = Gn + (b * N + r0 + pos[s]) * (int64_t)PFB;
+#pragma unroll
+      for (int k = 0; k < PFB; k += 4) *reinterpret_cast<float4*>(gr + k) = make_float4(G[s][k], G[s][k + 1], G[s][k + 2], G[s][k + 3]);
+      src_out[b * N + r0 + pos[s]] = r0 + i;
+    }
+  }
+  if (gbuf) {
+    int* ob = orig + b * N;
+    int ov[R];
+#pragma unroll
+    for (int s = 0; s < R; ++s) ov[s] = valid[s] ? ob[r0 + R * tid + s] : 0;
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      if (valid[s]) {
+        float* gr = gbuf + ((b * nblk + blk) * N + ov[s]) * (int64_t)PFB;
+#pragma unroll
+        for (int k = 0; k < PFB; ++k) gr[k] = G[s][k];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < R; ++s)
+      if (valid[s]) ob[r0 + pos[s]] = ov[s];
+  }
+  // swap count: positions of this block are local, every wave counted the same swaps
+  if (tid == 0) nsw_out[b * nblk + blk] = nsw;
+}
+
+// M_new[p][q] = M_old[src p][src q] + sum_k G[p][k] (J G^T)[k][q] for the trailing
+// positions p, q >= r1 (lower tiles; the upper triangle by the negated transpose).
+__global__ __launch_bounds__(256) void pf_update_kernel(const float* __restrict__ Mo, float* __restrict__ Mn,
+                                                        int N, int r1, const int* __restrict__ src,
+                                                        const float* __restrict__ Gn) {
+  constexpr int T = 64, LD = T + 4;
+  __shared__ float Ga[PFB][LD];  // A^T: G rows of the tile rows, K-major
+  __shared__ float Hb[PFB][LD];  // (J G^T) columns of the tile columns, K-major
+  __shared__ float Ct[T][T + 1];
+  const int64_t b = blockIdx.y;
+  const int t = blockIdx.x;
+  int I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
+  while ((I + 1) * (I + 2) / 2 <= t) ++I;
+  while (I * (I + 1) / 2 > t) --I;
+  const int J = t - I * (I + 1) / 2;
+  const int p0 = r1 + T * I, q0 = r1 + T * J;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const float* G = Gn + b * (int64_t)N * PFB;
+  const int* sb = src + b * N;
+  const float* Mob = Mo + b * (int64_t)N * N;
+  float* Mnb = Mn + b * (int64_t)N * N;
+  for (int e = tid; e < T * PFB; e += 256) {
+    const int r = e / PFB, k = e % PFB;
+    const int p = p0 + r, q = q0 + r;
+    Ga[k][r] = p < N ? G[(int64_t)p * PFB + k] : 0.0f;
+    const float gq = q < N ? G[(int64_t)q * PFB + (k ^ 1)] : 0.0f;
+    Hb[k][r] = (k & 1) ? -gq : gq;
+  }
+  __syncthreads();
+  // wave (wr, wc) owns the 32x32 quarter; C starts as the gathered old matrix
+  const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
+  const int l32 = lane & 31, lh = lane >> 5;
+  typedef float v16f __attribute__((ext_vector_type(16)));
+  v16f acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int p = p0 + wr + 8 * (v >> 2) + 4 * lh + (v & 3);
+    const int q = q0 + wc + l32;
+    acc[v] = (p < N && q < N) ? Mob[(int64_t)sb[p] * N + sb[q]] : 0.0f;
+  }
+#pragma unroll
+  for (int kp = 0; kp < PFB / 2; ++kp)
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Ga[2 * kp + lh][wr + l32], Hb[2 * kp + lh][wc + l32], acc, 0, 0, 0);
+  const bool diag = I == J;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int rr = wr + 8 * (v >> 2) + 4 * lh + (v & 3), cc = wc + l32;
+    float val = acc[v];
+    if (diag && rr == cc) val = 0.0f;
+    Ct[rr][cc] = val;
+    const int p = p0 + rr, q = q0 + cc;
+    if (p < N && q < N && (!diag || rr > cc)) Mnb[(int64_t)p * N + q] = val;
+    if (diag && rr == cc && p < N) Mnb[(int64_t)p * N + q] = 0.0f;
+  }
+  __syncthreads();
+  // mirrored tile: Mn[q][p] = -C[p][q], written row-contiguous
+  for (int e = tid; e < T * T; e += 256) {
+    const int cc = e / T, rr = e % T;
+    const int p = p0 + rr, q = q0 + cc;
+    if (p < N && q < N && (!diag || rr > cc)) Mnb[(int64_t)q * N + p] = -Ct[rr][cc];
+  }
+}
+
+__global__ void pf_finish_kernel(const float* __restrict__ d, const int* __restrict__ nsw, int H, int nblk,
+                                 float* __restrict__ sign, float* __restrict__ logabs, int64_t batch) {
+  const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (b >= batch) return;
+  float lg = 0.0f;
+  bool z = false, ng = false;
+  for (int i = lane; i < H; i += 64) {
+    const float v = d[b * H + i];
+    z = z || (v == 0.0f);
+    ng = ng != (v < 0.0f);
+    lg += (v != 0.0f) ? logf(fabsf(v)) : 0.0f;
+  }
+  lg = wave_sum_f32(lg);
+  int sw = 0;
+  for (int k = lane; k < nblk; k += 64) sw += nsw[b * nblk + k];
+  sw = (int)wave_sum_f32((float)sw);
+  const bool anyz = __ballot(z) != 0ull;
+  const int negs = __popcll(__ballot(ng)) + sw;
+  if (lane == 0) {
+    sign[b] = anyz ? 0.0f : ((negs & 1) ? -1.0f : 1.0f);
+    logabs[b] = anyz ? -INFINITY : lg;
+  }
+}
+
+static __global__ void pf_iota_kernel(int* g, int N, int64_t total) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < total) g[e] = (int)(e % N);
+}
+
+int pf_large_padded(int n) { return ((n + 31) / 32) * 32; }
+
+size_t pf_large_workspace(int64_t batch, int n, bool fact) {
+  const int N = pf_large_padded(n);
+  const int nblk = N / PFB;
+  size_t bytes = 0;
+  auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
+  add((size_t)batch * N * N * 4);  // M ping
+  add((size_t)batch * N * N * 4);  // M pong
+  add((size_t)batch * N * PFB * 4);  // G (new order)
+  add((size_t)batch * N * 4);      // src
+  add((size_t)batch * nblk * 4);   // swap counts
+  add((size_t)batch * N / 2 * 4);  // d (forward only; parts uses its own)
+  if (fact) add((size_t)batch * N * 4);  // orig
+  return bytes;
+}
+
+// Forward (and, with gbuf/dout/perm, the factors: gbuf (B, N/32, N, 32) by original row,
+// d (B, N/2), perm (B, N) final position -> original row).
+int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
+                    float* gbuf, float* dout, int* perm, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int N = pf_large_padded(n);
+  if (N > 2048) return FX_ERR_UNSUPPORTED;
+  const bool fact = gbuf != nullptr;
+  if (!ws || ws_bytes < pf_large_workspace(batch, n, fact)) return FX_ERR_WORKSPACE;
+  const int nblk = N / PFB;
+  char* p = (char*)ws;
+  auto take = [&](size_t x) {
+    char* q = p;
+    p += (x + 255) / 256 * 256;
+    return (void*)q;
+  };
+  float* M0 = (float*)take((size_t)batch * N * N * 4);
+  float* M1 = (float*)take((size_t)batch * N * N * 4);
+  float* Gn = (float*)take((size_t)batch * N * PFB * 4);
+  int* src = (int*)take((size_t)batch * N * 4);
+  int* nsw = (int*)take((size_t)batch * nblk * 4);
+  float* dbuf = (float*)take((size_t)batch * N / 2 * 4);
+  int* orig = fact ? (int*)take((size_t)batch * N * 4) : nullptr;
+  float* d = dout ? dout : dbuf;
+  const int64_t NN = (int64_t)N * N;
+  hipLaunchKernelGGL(pf_copy_pad_kernel, dim3((unsigned)((NN + 255) / 256), (unsigned)batch), dim3(256), 0, s,
+                     A, n, skew, M0, N);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  if (fact) {
+    const int64_t tot = batch * N;
+    hipLaunchKernelGGL(pf_iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, orig, N, tot);
+  }
+  float* cur = M0;
+  float* nxt = M1;
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int r0 = blk * PFB;
+    const int m = N - r0;
+    if (m <= 512)
+      hipLaunchKernelGGL((pf_panel_kernel<256>), dim3((unsigned)batch), dim3(256), 0, s, cur, N, r0, blk, nblk, d,
+                         nsw, src, Gn, orig, gbuf);
+    else if (m <= 1024)
+      hipLaunchKernelGGL((pf_panel_kernel<512>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0, blk, nblk, d,
+                         nsw, src, Gn, orig, gbuf);
+    else
+      hipLaunchKernelGGL((pf_panel_kernel<1024>), dim3((unsigned)batch), dim3(1024), 0, s, cur, N, r0, blk, nblk,
+                         d, nsw, src, Gn, orig, gbuf);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    const int r1 = r0 + PFB;
+    if (r1 < N) {
+      const int nt = (N - r1 + 63) / 64;
+      for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+        const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
+        hipLaunchKernelGGL(pf_update_kernel, dim3(nt * (nt + 1) / 2, (unsigned)nb), dim3(256), 0, s,
+                           cur + b0 * NN, nxt + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PFB);
+        if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+      }
+      float* t = cur;
+      cur = nxt;
+      nxt = t;
+    }
+  }
+  hipLaunchKernelGGL(pf_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, d, nsw, N / 2, nblk,
+                     sign, logabs, batch);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  if (perm && fact)
+    if (hipMemcpyAsync(perm, orig, (size_t)batch * N * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return FX_ERR_LAUNCH;
+  return FX_OK;
+}
+
+}  // namespace fx

@@ -84,18 +84,33 @@ size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign,
                   float* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
+/* Columns per block of the Parlett-Reid factors (16 for n <= 128, 32 above). */
+int32_t fx_pf_block_columns(int32_t n);
+
 /* The Parlett-Reid factors P S' P^T = L D L^T of the same run (S' = S padded with
- * [[0,1],[-1,0]] blocks to N = fx_pf_padded_size(n)):
- *  - gbuf (batch, N/16, N, 16): block k's tau_t (column 2t) and w_t (column 2t+1),
+ * [[0,1],[-1,0]] blocks to N = fx_pf_padded_size(n)), PB = fx_pf_block_columns(n):
+ *  - gbuf (batch, N/PB, N, PB): block k's tau_t (column 2t) and w_t (column 2t+1),
  *    indexed by the original row; entries of rows assigned before the pair step are
  *    zero, rows assigned before block k are unspecified;
  *  - d (batch, N/2): the pair pivots d_s = (P S' P^T reduced)[2s, 2s+1];
  *  - perm (batch, N): final position -> original row.
  * sign / logabs are bit-identical to fx_slogpf_f32. Replaces `_pf_core_factors`
  * (src/fermix/_pf.py:497-514). */
+size_t fx_slogpf_factors_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
                           float* sign, float* logabs, float* gbuf, float* d, int32_t* perm,
-                          fx_stream_t stream);
+                          void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* The same run as fx_slogpf_f32 (bit-identical sign / logabs) plus g (batch, n, n):
+ * S^-1 formed from the run's own factors (no second factorisation), zero for members
+ * with an exactly zero pivot or a non-finite result (adjugate = 0). adjugate != 0
+ * (pf(S) S^-1, the Pfaffian adjugate) returns FX_ERR_UNSUPPORTED in this version.
+ * Replaces `_pf_parts` (src/fermix/_pfinv.py:196-269) as called by `_pf_grad_parts`
+ * (src/fermix/_diff.py:80-89); kernels K11-K12 (_pfinv.py:80-192). */
+size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n);
+int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
+                        int32_t adjugate, float* sign, float* logabs, float* g, void* workspace,
+                        size_t workspace_bytes, fx_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -118,3 +118,68 @@ def test_c3_properties(dev):
     assert_grad(G, ref, A[idx], "C3 subset vs float64")
     _, _, invo, _, _, _ = g.lu_parts_generic(A[idx])
     assert_grad(G, invo, A[idx], "C3 subset vs oracle")
+
+
+@pytest.mark.parametrize("n", [2, 4, 6, 10, 16, 34, 64, 96, 128, 130, 256, 300, 512])
+def test_slogpf_grad_vs_float64_and_oracle(dev, n):
+    B = 8 if n <= 256 else 3
+    rng = np.random.default_rng(5000 + n)
+    A = (rng.standard_normal((B, n, n)) / np.sqrt(n)).astype(np.float32)
+    S = (A - A.transpose(0, 2, 1)).astype(np.float32)
+    print(f"slogpf grad n={n} B={B}", flush=True)
+    s, l, Sinv = _kernels.slogpf_parts(_t(S, dev), False)
+    s0, l0 = fermix_amd.slogpf(_t(S, dev), skew_symmetrize=False)
+    assert torch.equal(s, s0) and torch.equal(l, l0), "parts primal != forward"
+    Sinv = _np(Sinv)
+    ref = np.linalg.inv(S.astype(np.float64))
+    assert_grad(Sinv, ref, S, f"n={n} vs float64")
+    if n <= 256:
+        _, _, So, _ = g.pf_parts_generic(S, False)
+        assert_grad(Sinv, So, S, f"n={n} vs oracle")
+
+
+def test_slogpf_autograd_and_singular(dev):
+    rng = np.random.default_rng(77)
+    n = 40
+    A = rng.standard_normal((4, n, n)).astype(np.float32)
+    A[0, 7, :] = 0.0
+    A[0, :, 7] = 0.0  # S = (A - A^T)/2 has row/column 7 exactly zero
+    At = _t(A, dev).requires_grad_()
+    s, l = fermix_amd.slogpf(At)
+    s0, l0 = fermix_amd.slogpf(_t(A, dev))
+    assert torch.equal(s, s0) and torch.equal(l, l0)
+    assert np.isneginf(_np(l)[0])
+    (gr,) = torch.autograd.grad(l[1:].sum(), At)
+    gr = _np(gr)
+    assert np.all(np.isfinite(gr)) and np.all(gr[0] == 0)
+    S = 0.5 * (A.astype(np.float64) - A.astype(np.float64).transpose(0, 2, 1))
+    ref = 0.5 * np.linalg.inv(S[1:]).transpose(0, 2, 1)  # d log|pf| / da = S^-T / 2
+    assert np.max(np.abs(gr[1:] - ref)) < 1e-4 * np.abs(ref).max()
+    # forward mode and vmap
+    dA = torch.from_numpy(rng.standard_normal(A.shape).astype(np.float32)).to(dev)
+    (_, lp), (_, dl) = torch.func.jvp(lambda x: fermix_amd.slogpf(x), (_t(A, dev),), (dA,))
+    dS = 0.5 * (_np(dA) - _np(dA).transpose(0, 2, 1)).astype(np.float64)
+    want = 0.5 * np.einsum("bij,bji->b", np.linalg.inv(S[1:]), dS[1:])
+    assert np.max(np.abs(_np(dl)[1:] - want)) < 1e-3 * max(1.0, np.abs(want).max())
+    vs, vl = torch.func.vmap(lambda x: fermix_amd.slogpf(x))(_t(A, dev)[None])
+    assert torch.equal(vs[0], s0) and torch.equal(vl[0], l0)
+
+
+def test_c4_properties(dev):
+    """C4 size: B = 64, n = 2048, S = A - A^T, A iid N(0, 1/n). Primal bit-identical to the
+    forward, gradient finite and skew, S S^-1 = I on a subset in float64."""
+    rng = np.random.default_rng(4)
+    B, n = 64, 2048
+    A = rng.standard_normal((B, n, n), dtype=np.float32) * np.float32(1 / np.sqrt(n))
+    S = A - A.transpose(0, 2, 1)
+    del A
+    St = _t(S, dev)
+    s, l, Sinv = _kernels.slogpf_parts(St, False)
+    s0, l0 = fermix_amd.slogpf(St, skew_symmetrize=False)
+    assert torch.equal(s, s0) and torch.equal(l, l0)
+    assert bool(torch.isfinite(Sinv).all())
+    idx = [0, 63]
+    G = _np(Sinv[idx])
+    assert np.max(np.abs(G + G.transpose(0, 2, 1))) <= 1e-6 * np.abs(G).max()
+    ref = np.linalg.inv(S[idx].astype(np.float64))
+    assert_grad(G, ref, S[idx], "C4 subset vs float64")

@@ -36,3 +36,28 @@ def test_slogdet_large_vs_oracle(dev, n):
     assert np.array_equal(s, so)
     assert_logabs(l, l64, n, "vs float64", A)
     assert_logabs(l, lo, n, "vs oracle", A)
+
+
+@pytest.mark.parametrize("n", [130, 160, 256, 300, 512, 1000, 1024, 2048])
+def test_slogpf_large_vs_oracle(dev, n):
+    B = 8 if n <= 512 else 3
+    rng = np.random.default_rng(4000 + n)
+    A = (rng.standard_normal((B, n, n)) / np.sqrt(n)).astype(np.float32)
+    S = (A - A.transpose(0, 2, 1)).astype(np.float32)
+    if B > 3:
+        S[1, n // 3, :] = 0.0
+        S[1, :, n // 3] = 0.0
+    print(f"slogpf large n={n} B={B}", flush=True)
+    s, l = map(_np, fermix_amd.slogpf(_t(S, dev), skew_symmetrize=False))
+    s64, l64 = ref64.slogpf64(S)
+    assert np.array_equal(s, s64)
+    assert_logabs(l, l64, n, "vs float64", S)
+    if n <= 512:
+        so, lo = g.slogpf_generic(S)
+        assert np.array_equal(s, so)
+        assert_logabs(l, lo, n, "vs oracle", S)
+    # pf^2 = det against the slogdet kernels where they exist
+    if n <= 1024:
+        sd, ld = map(_np, fermix_amd.slogdet(_t(S, dev)))
+        fin = np.isfinite(l64)
+        assert np.all(np.abs(2 * l[fin] - ld[fin]) < 1e-3 * np.maximum(1, np.abs(ld[fin])) + 1e-3)
