@@ -111,6 +111,27 @@ def bench_c3(steps, warmup):
                 bytes=B * 8 * n * n, flops=B * 2.0 * n ** 3, sample=None)
 
 
+def bench_c4(steps, warmup):
+    """slogpf forward + VJP (cotangent ones on log|pf|), B = 64, n = 2048,
+    S = A - A^T with A iid N(0, 1/n)."""
+    import torch
+    import fermix_amd
+
+    B, n = 64, 2048
+    A = _inputs(B, n, 0, scale=1.0 / np.sqrt(n))
+    S = torch.from_numpy(A - np.swapaxes(A, 1, 2)).cuda().requires_grad_()
+    del A
+
+    def fn():
+        s, l = fermix_amd.slogpf(S, skew_symmetrize=False)
+        (g,) = torch.autograd.grad(l.sum(), S)
+        return g
+
+    ms, wall = _time_gpu(fn, steps, warmup)
+    return dict(name="slogpf_fwd_grad", B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
+                bytes=B * 8 * n * n, flops=B * 1.0 * n ** 3, sample=None)
+
+
 def cpu_baseline(sample, which):
     """The CPU oracle on a bounded sample, one thread (matrices/s)."""
     from threadpoolctl import threadpool_limits
@@ -145,7 +166,7 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm GPU visible"}), flush=True)
         sys.exit(1)
-    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3"}
+    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3", "c4"}
     res = {}
     if "c2" in only:
         res["c2"] = bench_c2(args.steps, args.warmup)
@@ -156,7 +177,10 @@ def main():
     if "c3" in only:
         res["c3"] = bench_c3(max(3, args.steps // 4), max(1, args.warmup // 2))
         print(f"# c3 slogdet fwd+grad: {res['c3']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
-    head = res.get("c2") or res.get("c1") or res.get("c3")
+    if "c4" in only:
+        res["c4"] = bench_c4(max(2, args.steps // 10), 1)
+        print(f"# c4 slogpf fwd+grad: {res['c4']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
+    head = res.get("c2") or res.get("c1") or res.get("c3") or res.get("c4")
     achieved = head["bytes"] / (head["ms"] * 1e-3) / 1e9
     roofline = {
         "bound": "hbm",
@@ -183,7 +207,7 @@ def main():
         k: {"workload": v["name"], "B": v["B"], "n": v["n"], "ms_per_step": round(v["ms"], 5),
             "matrices_per_s": round(v["rate"], 1),
             "hbm_frac": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            **({"tflops_2n3": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2)} if "flops" in v else {})}
+            **({"alg_tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2)} if "flops" in v else {})}
         for k, v in res.items()
     }
     line = {
