@@ -36,8 +36,26 @@ def _parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--only", default=None, help="comma list of workloads (c1,c2,c3)")
+    p.add_argument("--only", default=None, help="comma list of workloads (c1,c2,c3,c4)")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="also run a plain 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
+
+
+HEAD_KERNEL = {"slogpf_fwd": "pf_small_kernel<128, false>", "slogdet_fwd": "lu_small_kernel<128, false>"}
+
+
+def _measured_traffic(name):
+    """HBM bytes per dispatch of the workload's kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.txt), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.txt")
+    kern = HEAD_KERNEL.get(name)
+    if kern is None or not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith(kern + " "):
+            return int(line.split()[-1])
+    return None
 
 
 def _time_gpu(fn, steps, warmup):
@@ -180,6 +198,12 @@ def main():
     if "c4" in only:
         res["c4"] = bench_c4(max(2, args.steps // 10), 1)
         print(f"# c4 slogpf fwd+grad: {res['c4']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
+    if args.copy_probe:
+        x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda").fill_(1.0)
+        for _ in range(3):
+            y = x.clone()
+        torch.cuda.synchronize()
+        del x, y
     head = res.get("c2") or res.get("c1") or res.get("c3") or res.get("c4")
     achieved = head["bytes"] / (head["ms"] * 1e-3) / 1e9
     roofline = {
@@ -188,7 +212,7 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": _measured_traffic(head["name"]),
     }
     cpu = None
     if not args.no_cpu:
