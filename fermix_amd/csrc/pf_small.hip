@@ -1,5 +1,6 @@
-// Fused slogpf for even n <= 128: one workgroup (4 waves) per matrix, the skew matrix
-// resident in LDS, blocked Parlett-Reid with partial pivoting in blocks of 8 pair steps.
+// Fused slogpf for even n <= 128: one workgroup (4 waves) per matrix, blocked Parlett-Reid
+// with partial pivoting in blocks of 8 pair steps, the skew matrix resident in LDS as its
+// strictly lower triangle.
 //
 // Reference roles replaced (ChenAo-Phys/fermix): the pair-step panel
 // (src/fermix/_pf.py:59-284) and the rank-2b trailing update (_pf.py:287-382), issued by
@@ -10,15 +11,21 @@
 // d = M[c, c+1], tau = -M[:, c] / d and w = M[:, c+1] on the rows after c+1, and the
 // trailing matrix becomes M + tau w^T - w tau^T.
 //
-// Per block (positions from r0):
-//   * wave 0 runs 8 pair steps on the block's rows (lane l owns rows R*l ..), keeping
-//     the tau / w vectors as the columns of G (m x 16); column a and column p of the
+// LDS (N = 128: exactly 40 KiB, so four matrices share a CU):
+//   * T: M[p][q] for p > q at T[p (p - 1) / 2 + q]; M[q][p] = -M[p][q], M[p][p] = 0;
+//   * Gs: the block's tau / w vectors, 16 per row, columns XOR-swizzled by row bits 2-3
+//     so 16 consecutive rows x 4 columns hit 64 distinct banks while 4-column groups
+//     stay 16-byte aligned;
+//   * src (position -> row at block start) and orig (FACT: row -> original row), bytes.
+//
+// Per block (positions from r0; rows stored in block-start order):
+//   * wave 0 runs 8 pair steps (lane l owns rows l + 64 s). Column a and column p of the
 //     current matrix are the block-start matrix plus the G corrections
-//     sum_u tau_u[i] w_u[q] - w_u[i] tau_u[q]; the permutation stays virtual;
+//     sum_u tau_u[i] w_u[q] - w_u[i] tau_u[q]; the G row of a / p is read back from Gs as
+//     an LDS broadcast; the permutation stays virtual;
 //   * all waves then form the trailing block M'' = M + G J G^T (J = diag of
-//     [[0,1],[-1,0]]) on fp32 MFMA 16x16x4, lower-triangle tiles only, gathered through
-//     the block's permutation, stored in the new order together with the mirrored
-//     (negated) upper triangle, so the LDS matrix stays exactly skew.
+//     [[0,1],[-1,0]]) on fp32 MFMA 16x16x4 over the lower-triangle tiles, gathered through
+//     the block's permutation and stored in the new order.
 // With FACT every block's G is exported indexed by the original row index, with the
 // pivots d and the final position -> original row map (the factors of P S P^T = L D L^T).
 //
@@ -30,57 +37,89 @@ namespace fx {
 
 template <int N>
 struct PfSmall {
-  static constexpr int LDA = N + 1;
-  static constexpr int LDG = 17;
-  static constexpr int R = (N + 63) / 64;
+  static constexpr int R = (N + 63) / 64;                        // panel rows per lane
+  static constexpr int NTRI = N * (N - 1) / 2;                   // strictly lower triangle
   static constexpr int NB = N / 16;
-  static constexpr int NPV = (N / 2 + 63) / 64;  // pivot slots per lane
+  static constexpr int NPV = (N / 2 + 63) / 64;                  // pivot slots per lane
   static constexpr int MAXNT = N / 16 - 1;                       // trailing tiles per side
   static constexpr int MAXTILES = MAXNT * (MAXNT + 1) / 2;       // lower-triangle tiles
   static constexpr int TPW = MAXTILES > 0 ? (MAXTILES + 3) / 4 : 1;  // tiles per wave
+  static constexpr int LDS_BYTES = NTRI * 4 + N * 16 * 4 + 2 * N;
 };
+static_assert(PfSmall<128>::LDS_BYTES <= 40960, "four n = 128 workgroups per CU");
+
+// Start of row p of the strictly lower triangle.
+__device__ __forceinline__ int tri_row(int p) { return (p * (p - 1)) >> 1; }
+
+// Index of G element (row s, column k) in Gs.
+__device__ __forceinline__ int g_idx(int s, int k) { return s * 16 + (k ^ (((s >> 2) & 3) << 2)); }
+
+// Lowest set row of a per-slot ballot pair: slot s holds rows l + 64 s.
+template <int R>
+__device__ __forceinline__ int first_row(const unsigned long long (&b)[R]) {
+  if constexpr (R == 1) {
+    return (int)__builtin_ctzll(b[0]);
+  } else {
+    return b[0] ? (int)__builtin_ctzll(b[0]) : 64 + (int)__builtin_ctzll(b[1]);
+  }
+}
 
 template <int N, bool FACT>
-__device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int* src, int lane,
-                                         PivotLog<PfSmall<N>::NPV>& piv_log, int& nsw, int* orig,
-                                         float* gbuf_k, float* d_k) {
-  constexpr int LDA = PfSmall<N>::LDA, LDG = PfSmall<N>::LDG, R = PfSmall<N>::R;
+__device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsigned char* src, int lane,
+                                         PivotLog<PfSmall<N>::NPV>& piv_log, int& nsw,
+                                         unsigned char* orig, float* gbuf_k, float* d_k) {
+  constexpr int R = PfSmall<N>::R, NTRI = PfSmall<N>::NTRI;
   float G[R][16];
-  int pos[R];
+  int pos[R], rop[R];
   bool valid[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
-    const int row = R * lane + i;
+    const int row = lane + 64 * i;
     valid[i] = (row >= r0) && (row < N);
     pos[i] = row;
+    rop[i] = row < N ? tri_row(row) : 0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) G[i][k] = 0.0f;
   }
+  // M[row][q] of the block-start matrix for the lane's rows (value for row == q unused)
+  auto column = [&](int q, float (&v)[R]) {
+    const int roq = tri_row(q);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int row = lane + 64 * i;
+      const bool below = row > q;
+      const int e = min(below ? rop[i] + q : roq + row, NTRI - 1);
+      const float t = T[e];
+      v[i] = below ? t : -t;
+    }
+  };
+  // the first 2t entries of Gs row q, broadcast to every lane
+  auto grow = [&](int q, float (&g)[16], auto tc) {
+    constexpr int t = decltype(tc)::value;
+    const int sw = ((q >> 2) & 3) << 2;
+    static_for<0, (2 * t + 3) / 4>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      const float4 v = *reinterpret_cast<const float4*>(Gs + q * 16 + ((4 * j) ^ sw));
+      g[4 * j] = v.x;
+      g[4 * j + 1] = v.y;
+      g[4 * j + 2] = v.z;
+      g[4 * j + 3] = v.w;
+    });
+  };
   static_for<0, 8>([&](auto tc) {
     constexpr int t = decltype(tc)::value;
     const int c = r0 + 2 * t;
-    // row a: the row at position c (wave-uniform lane la, slot sa)
-    bool hit = false;
-    int hs = 0;
+    // row a: the row at position c
+    unsigned long long ba[R];
 #pragma unroll
-    for (int i = 0; i < R; ++i)
-      if (valid[i] && pos[i] == c) { hit = true; hs = i; }
-    const int la = first_lane(hit);
-    const int sa = readlane_i(hs, la);
-    const int qa = R * la + sa;
-    float ga[16];
-    static_for<0, 2 * t>([&](auto kc) {
-      float v = G[0][kc.value];
-#pragma unroll
-      for (int i = 1; i < R; ++i) v = (sa == i) ? G[i][kc.value] : v;
-      ga[kc.value] = readlane_f(v, la);
-    });
-    // column a of the current matrix: M[i][qa] = -M[qa][i] plus the G corrections
-    float x[R];
+    for (int i = 0; i < R; ++i) ba[i] = __ballot(valid[i] && pos[i] == c);
+    const int qa = first_row<R>(ba);
+    float ga[16], x[R];
+    grow(qa, ga, tc);
+    column(qa, x);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const int row = R * lane + i;
-      float v = valid[i] ? -As[qa * LDA + row] : 0.0f;
+      float v = x[i];
       static_for<0, t>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
         v = fmaf(G[i][2 * u], ga[2 * u + 1], v);
@@ -88,39 +127,28 @@ __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int
       });
       x[i] = v;
     }
-    unsigned kb = 0;
-    int ib = 0;
+    unsigned key[R], kb = 0;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const unsigned k = cand_key(x[i], valid[i] && pos[i] > c);
-      if (k > kb) { kb = k; ib = i; }
+      key[i] = cand_key(x[i], valid[i] && pos[i] > c);
+      kb = max(kb, key[i]);
     }
     const unsigned gk = wave_max_u32(kb);
-    const int lp = first_lane(kb == gk);
-    const int sp = readlane_i(ib, lp);
-    const int qp = R * lp + sp;
-    float gp[16];
-    static_for<0, 2 * t>([&](auto kc) {
-      float v = G[0][kc.value];
+    unsigned long long bp[R];
 #pragma unroll
-      for (int i = 1; i < R; ++i) v = (sp == i) ? G[i][kc.value] : v;
-      gp[kc.value] = readlane_f(v, lp);
-    });
+    for (int i = 0; i < R; ++i) bp[i] = __ballot(key[i] == gk);
+    const int qp = first_row<R>(bp);
+    const int lp = qp & 63, sp = qp >> 6;
     int pv = pos[0];
 #pragma unroll
     for (int i = 1; i < R; ++i) pv = (sp == i) ? pos[i] : pv;
     const int pp = readlane_i(pv, lp);
+    float gp[16], y[R];
+    grow(qp, gp, tc);
+    column(qp, y);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      if (valid[i] && pos[i] == c + 1) pos[i] = pp;
-      if (lane == lp && i == sp) pos[i] = c + 1;
-    }
-    nsw += (pp != c + 1) ? 1 : 0;
-    float y[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const int row = R * lane + i;
-      float v = valid[i] ? -As[qp * LDA + row] : 0.0f;
+      float v = y[i];
       static_for<0, t>([&](auto uc) {
         constexpr int u = decltype(uc)::value;
         v = fmaf(G[i][2 * u], gp[2 * u + 1], v);
@@ -128,46 +156,141 @@ __device__ __forceinline__ void pf_panel(const float* As, float* Gs, int r0, int
       });
       y[i] = v;
     }
+    const int la = qa & 63, sa = qa >> 6;
     float yv = y[0];  // M[a][p] = y at row a
 #pragma unroll
     for (int i = 1; i < R; ++i) yv = (sa == i) ? y[i] : yv;
     const float d = readlane_f(yv, la);
     piv_log.put(c >> 1, d, lane);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int row = lane + 64 * i;
+      if (valid[i] && pos[i] == c + 1) pos[i] = pp;
+      if (row == qp) pos[i] = c + 1;
+    }
+    nsw += (pp != c + 1) ? 1 : 0;
     const float inv = safe_rcp(d);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
+      const int row = lane + 64 * i;
       const bool act = valid[i] && pos[i] > c + 1;
       G[i][2 * t] = act ? -x[i] * inv : 0.0f;
       G[i][2 * t + 1] = act ? y[i] : 0.0f;
+      if (row < N)
+        *reinterpret_cast<float2*>(Gs + g_idx(row, 2 * t)) = make_float2(G[i][2 * t], G[i][2 * t + 1]);
     }
+    wave_lds_fence();
     if (FACT && lane == 0) d_k[t] = d;
   });
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
-    if (valid[i]) {
-      const int row = R * lane + i;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) Gs[row * LDG + k] = G[i][k];
-      src[pos[i]] = row;
-    }
-  }
+  for (int i = 0; i < R; ++i)
+    if (valid[i]) src[pos[i]] = (unsigned char)(lane + 64 * i);
   if (FACT) {
     int ov[R];
 #pragma unroll
-    for (int i = 0; i < R; ++i) ov[i] = valid[i] ? orig[R * lane + i] : 0;
+    for (int i = 0; i < R; ++i) ov[i] = valid[i] ? orig[lane + 64 * i] : 0;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       if (valid[i]) {
+        float4* gr = reinterpret_cast<float4*>(gbuf_k + ov[i] * 16);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) gbuf_k[ov[i] * 16 + k] = G[i][k];
+        for (int j = 0; j < 4; ++j)
+          gr[j] = make_float4(G[i][4 * j], G[i][4 * j + 1], G[i][4 * j + 2], G[i][4 * j + 3]);
       }
     }
     wave_lds_fence();
 #pragma unroll
     for (int i = 0; i < R; ++i)
-      if (valid[i]) orig[pos[i]] = ov[i];
+      if (valid[i]) orig[pos[i]] = (unsigned char)ov[i];
   }
   wave_lds_fence();
+}
+
+// Load the matrix (row-major n x n, n even) into T, padded with [[0,1],[-1,0]] blocks;
+// with skew, T holds (A - A^T) / 2 formed as A[p][q] / 2 - A[q][p] / 2 (halving is exact).
+template <int N>
+__device__ __forceinline__ void pf_load(float* T, const float* __restrict__ g, int n, int skew, int tid) {
+  const float h = skew ? 0.5f : 1.0f;
+  if (n == N) {
+    constexpr int NV = N * N / 4;
+    constexpr int PER = (NV + 255) / 256;
+    const float4* g4 = reinterpret_cast<const float4*>(g);
+    float4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + 256 * i;
+      if (NV % 256 == 0 || e < NV) v[i] = g4[e];
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + 256 * i;
+      if (NV % 256 == 0 || e < NV) {
+        const int r = (4 * e) / N, c = (4 * e) % N;
+        const float vv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (c + j < r) T[tri_row(r) + c + j] = vv[j] * h;
+      }
+    }
+    if (skew) {
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int e = tid + 256 * i;
+        if (NV % 256 == 0 || e < NV) {
+          const int r = (4 * e) / N, c = (4 * e) % N;
+          const float vv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (c + j > r) {
+              float* d = T + tri_row(c + j) + r;
+              *d = *d - vv[j] * 0.5f;
+            }
+        }
+      }
+    }
+  } else {
+    // lower triangle (every entry written once), then the upper halves subtracted
+    constexpr int CH = 8;
+    for (int base = 0; base < N * N; base += 256 * CH) {
+      float v[CH];
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int e = base + tid + 256 * u;
+        const int r = e / N, c = e % N;
+        v[u] = (e < N * N && r < n && c < r) ? g[r * n + c] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int e = base + tid + 256 * u;
+        const int r = e / N, c = e % N;
+        // padding: M[2m+1][2m] = -1 below the n x n block
+        if (e < N * N && c < r)
+          T[tri_row(r) + c] = (r < n) ? v[u] * h : ((c == r - 1 && (r & 1)) ? -1.0f : 0.0f);
+      }
+    }
+    if (skew) {
+      __syncthreads();
+      for (int base = 0; base < N * N; base += 256 * CH) {
+        float v[CH];
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+          const int e = base + tid + 256 * u;
+          const int r = e / N, c = e % N;
+          v[u] = (e < N * N && c < n && r < c) ? g[r * n + c] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+          const int e = base + tid + 256 * u;
+          const int r = e / N, c = e % N;
+          if (e < N * N && c < n && r < c) {
+            float* d = T + tri_row(c) + r;
+            *d = *d - v[u] * 0.5f;
+          }
+        }
+      }
+    }
+  }
 }
 
 template <int N, bool FACT>
@@ -178,34 +301,16 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
                                                        float* __restrict__ d_out,
                                                        int* __restrict__ perm_out) {
   using C = PfSmall<N>;
-  constexpr int LDA = C::LDA, LDG = C::LDG, NB = C::NB, TPW = C::TPW;
-  __shared__ float As[N * LDA];
-  __shared__ float Gs[N * LDG];
-  __shared__ int src[N];
-  __shared__ int orig[N];
+  constexpr int NB = C::NB, TPW = C::TPW;
+  __shared__ __align__(16) float T[C::NTRI];
+  __shared__ __align__(16) float Gs[N * 16];
+  __shared__ unsigned char src[N];
+  __shared__ unsigned char orig[FACT ? N : 1];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const float* Ab = A + b * (int64_t)n * n;
-  // [[0,1],[-1,0]] padding blocks (n is even)
-  load_tile<N, LDA, 256>(As, Ab, n, tid, [](int r, int c) {
-    return ((r ^ c) == 1) ? ((r & 1) ? -1.0f : 1.0f) : 0.0f;
-  });
-  if (skew) {
-    __syncthreads();
-    // S = (A - A^T) / 2 in place: thread pairs (r, c) with r < c
-    for (int e = tid; e < n * n; e += 256) {
-      const int r = e / n, c = e - r * n;
-      if (r < c) {
-        const float x = As[r * LDA + c], y = As[c * LDA + r];
-        As[r * LDA + c] = (x - y) * 0.5f;
-        As[c * LDA + r] = (y - x) * 0.5f;
-      } else if (r == c) {
-        As[r * LDA + c] = 0.0f;
-      }
-    }
-  }
+  pf_load<N>(T, A + b * (int64_t)n * n, n, skew, tid);
   if (FACT)
-    for (int r = tid; r < N; r += 256) orig[r] = r;
+    for (int r = tid; r < N; r += 256) orig[r] = (unsigned char)r;
   __syncthreads();
 
   PivotLog<C::NPV> piv_log;
@@ -217,14 +322,16 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
     if (wave == 0) {
       float* gk = FACT ? gbuf_out + (b * NB + k) * (int64_t)N * 16 : nullptr;
       float* dk = FACT ? d_out + b * (N / 2) + 8 * k : nullptr;
-      pf_panel<N, FACT>(As, Gs, r0, src, lane, piv_log, nsw, orig, gk, dk);
+      pf_panel<N, FACT>(T, Gs, r0, src, lane, piv_log, nsw, orig, gk, dk);
     }
-    __syncthreads();
     const int nt = (N - r0 - 16) / 16;
+    if (nt == 0) break;
+    __syncthreads();
     const int ntiles = nt * (nt + 1) / 2;
     const int rb = r0 + 16;
     v4f acc[TPW];
     int ti[TPW], tj[TPW];
+    // gather the old lower tiles M[src p][src q] through the block's permutation
 #pragma unroll
     for (int s = 0; s < TPW; ++s) {
       const int t = wave + 4 * s;
@@ -240,7 +347,13 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
         const int q = rb + 16 * J + li;
         const int sq = src[q];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[s][v] = As[src[rb + 16 * I + 4 * g + v] * LDA + sq];
+        for (int v = 0; v < 4; ++v) {
+          const int p = rb + 16 * I + 4 * g + v;
+          const int sp = src[p];
+          const int hi = max(sp, sq), lo = min(sp, sq);
+          const float e = T[p > q ? tri_row(hi) + lo : 0];
+          acc[s][v] = sp > sq ? e : -e;
+        }
       }
     }
     __syncthreads();
@@ -254,20 +367,15 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int k = 4 * u + g;
-          const float av = Gs[sr * LDG + k];
-          const float bv = (k & 1) ? -Gs[sq * LDG + k - 1] : Gs[sq * LDG + k + 1];
+          const float av = Gs[g_idx(sr, k)];
+          const float bv = (k & 1) ? -Gs[g_idx(sq, k - 1)] : Gs[g_idx(sq, k + 1)];
           acc[s] = mfma16(av, bv, acc[s]);
         }
         const int q = rb + 16 * J + li;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int p = rb + 16 * I + 4 * g + v;
-          if (p > q) {
-            As[p * LDA + q] = acc[s][v];
-            As[q * LDA + p] = -acc[s][v];
-          } else if (p == q) {
-            As[p * LDA + q] = 0.0f;
-          }
+          if (p > q) T[tri_row(p) + q] = acc[s][v];
         }
       }
     }
@@ -281,8 +389,10 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
       logabs_out[b] = la;
     }
   }
-  if (FACT)
+  if (FACT) {
+    __syncthreads();
     for (int r = tid; r < N; r += 256) perm_out[b * N + r] = orig[r];
+  }
 }
 
 template <int N, bool FACT>
