@@ -55,25 +55,29 @@ __device__ __forceinline__ int tri_row(int p) { return (p * (p - 1)) >> 1; }
 __device__ __forceinline__ int g_idx(int s, int k) { return s * 16 + (k ^ (((s >> 2) & 3) << 2)); }
 
 // Lowest set row of a per-slot ballot pair: slot s holds rows l + 64 s.
-template <int R>
+// Slots below S0 hold no candidate.
+template <int R, int S0>
 __device__ __forceinline__ int first_row(const unsigned long long (&b)[R]) {
-  if constexpr (R == 1) {
-    return (int)__builtin_ctzll(b[0]);
+  if constexpr (R - S0 == 1) {
+    return 64 * S0 + (int)__builtin_ctzll(b[S0]);
   } else {
     return b[0] ? (int)__builtin_ctzll(b[0]) : 64 + (int)__builtin_ctzll(b[1]);
   }
 }
 
-template <int N, bool FACT>
+// S0: first slot with rows >= r0 (rows l + 64 s with s < S0 are all finished).
+template <int N, bool FACT, int S0>
 __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsigned char* src, int lane,
                                          PivotLog<PfSmall<N>::NPV>& piv_log, int& nsw,
                                          unsigned char* orig, float* gbuf_k, float* d_k) {
   constexpr int R = PfSmall<N>::R, NTRI = PfSmall<N>::NTRI;
+  // lane-derived addresses are recomputed per block instead of held across the loop
+  asm volatile("" : "+v"(lane));
   float G[R][16];
   int pos[R], rop[R];
   bool valid[R];
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
+  for (int i = S0; i < R; ++i) {
     const int row = lane + 64 * i;
     valid[i] = (row >= r0) && (row < N);
     pos[i] = row;
@@ -85,7 +89,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
   auto column = [&](int q, float (&v)[R]) {
     const int roq = tri_row(q);
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
+    for (int i = S0; i < R; ++i) {
       const int row = lane + 64 * i;
       const bool below = row > q;
       const int e = min(below ? rop[i] + q : roq + row, NTRI - 1);
@@ -106,64 +110,69 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
       g[4 * j + 3] = v.w;
     });
   };
+  // the row at position c (wave-uniform)
+  auto row_at = [&](int c) {
+    unsigned long long b[R];
+#pragma unroll
+    for (int i = S0; i < R; ++i) b[i] = __ballot(valid[i] && pos[i] == c);
+    return first_row<R, S0>(b);
+  };
+  // v += sum_{u < U} G[.][2u] gq[2u+1] - G[.][2u+1] gq[2u], in order of u
+  auto correct = [&](float (&v)[R], const float (&gq)[16], auto uc) {
+    constexpr int U = decltype(uc)::value;
+#pragma unroll
+    for (int i = S0; i < R; ++i) {
+      static_for<0, U>([&](auto wc) {
+        constexpr int u = decltype(wc)::value;
+        v[i] = fmaf(G[i][2 * u], gq[2 * u + 1], v[i]);
+        v[i] = fmaf(-G[i][2 * u + 1], gq[2 * u], v[i]);
+      });
+    }
+  };
+  // Row a of step t and its current column x are carried from step t - 1: while step
+  // t - 1 searches its pivot, the row at position c + 2 is read and corrected with the
+  // finished G columns; unless the pivot swap moved that row, only step t - 1's own term
+  // is added afterwards (from the owner lane's registers, same order of operations).
+  int qa = row_at(r0);
+  float x[R];
+  column(qa, x);
   static_for<0, 8>([&](auto tc) {
     constexpr int t = decltype(tc)::value;
     const int c = r0 + 2 * t;
-    // row a: the row at position c
-    unsigned long long ba[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i) ba[i] = __ballot(valid[i] && pos[i] == c);
-    const int qa = first_row<R>(ba);
-    float ga[16], x[R];
-    grow(qa, ga, tc);
-    column(qa, x);
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      float v = x[i];
-      static_for<0, t>([&](auto uc) {
-        constexpr int u = decltype(uc)::value;
-        v = fmaf(G[i][2 * u], ga[2 * u + 1], v);
-        v = fmaf(-G[i][2 * u + 1], ga[2 * u], v);
-      });
-      x[i] = v;
-    }
     unsigned key[R], kb = 0;
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
+    for (int i = S0; i < R; ++i) {
       key[i] = cand_key(x[i], valid[i] && pos[i] > c);
       kb = max(kb, key[i]);
     }
+    const int qn = t < 7 ? row_at(c + 2) : 0;  // speculative next row a
     const unsigned gk = wave_max_u32(kb);
     unsigned long long bp[R];
 #pragma unroll
-    for (int i = 0; i < R; ++i) bp[i] = __ballot(key[i] == gk);
-    const int qp = first_row<R>(bp);
+    for (int i = S0; i < R; ++i) bp[i] = __ballot(key[i] == gk);
+    const int qp = first_row<R, S0>(bp);
     const int lp = qp & 63, sp = qp >> 6;
-    int pv = pos[0];
+    int pv = pos[S0];
 #pragma unroll
-    for (int i = 1; i < R; ++i) pv = (sp == i) ? pos[i] : pv;
+    for (int i = S0 + 1; i < R; ++i) pv = (sp == i) ? pos[i] : pv;
     const int pp = readlane_i(pv, lp);
     float gp[16], y[R];
     grow(qp, gp, tc);
     column(qp, y);
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      float v = y[i];
-      static_for<0, t>([&](auto uc) {
-        constexpr int u = decltype(uc)::value;
-        v = fmaf(G[i][2 * u], gp[2 * u + 1], v);
-        v = fmaf(-G[i][2 * u + 1], gp[2 * u], v);
-      });
-      y[i] = v;
+    float gn[16], xn[R];
+    if constexpr (t < 7) {
+      grow(qn, gn, tc);
+      column(qn, xn);
     }
+    correct(y, gp, tc);
     const int la = qa & 63, sa = qa >> 6;
-    float yv = y[0];  // M[a][p] = y at row a
+    float yv = y[S0];  // M[a][p] = y at row a
 #pragma unroll
-    for (int i = 1; i < R; ++i) yv = (sa == i) ? y[i] : yv;
+    for (int i = S0 + 1; i < R; ++i) yv = (sa == i) ? y[i] : yv;
     const float d = readlane_f(yv, la);
     piv_log.put(c >> 1, d, lane);
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
+    for (int i = S0; i < R; ++i) {
       const int row = lane + 64 * i;
       if (valid[i] && pos[i] == c + 1) pos[i] = pp;
       if (row == qp) pos[i] = c + 1;
@@ -171,7 +180,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
     nsw += (pp != c + 1) ? 1 : 0;
     const float inv = safe_rcp(d);
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
+    for (int i = S0; i < R; ++i) {
       const int row = lane + 64 * i;
       const bool act = valid[i] && pos[i] > c + 1;
       G[i][2 * t] = act ? -x[i] * inv : 0.0f;
@@ -181,16 +190,41 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
     }
     wave_lds_fence();
     if (FACT && lane == 0) d_k[t] = d;
+    if constexpr (t < 7) {
+      correct(xn, gn, tc);
+      if (pp != c + 2) {
+        const int ln = qn & 63, sn = qn >> 6;
+        float g0 = G[S0][2 * t], g1 = G[S0][2 * t + 1];
+#pragma unroll
+        for (int i = S0 + 1; i < R; ++i) {
+          g0 = (sn == i) ? G[i][2 * t] : g0;
+          g1 = (sn == i) ? G[i][2 * t + 1] : g1;
+        }
+        const float h0 = readlane_f(g0, ln), h1 = readlane_f(g1, ln);
+#pragma unroll
+        for (int i = S0; i < R; ++i) {
+          x[i] = fmaf(G[i][2 * t], h1, xn[i]);
+          x[i] = fmaf(-G[i][2 * t + 1], h0, x[i]);
+        }
+        qa = qn;
+      } else {
+        qa = row_at(c + 2);
+        float ga[16];
+        grow(qa, ga, ic<t + 1>{});
+        column(qa, x);
+        correct(x, ga, ic<t + 1>{});
+      }
+    }
   });
 #pragma unroll
-  for (int i = 0; i < R; ++i)
+  for (int i = S0; i < R; ++i)
     if (valid[i]) src[pos[i]] = (unsigned char)(lane + 64 * i);
   if (FACT) {
     int ov[R];
 #pragma unroll
-    for (int i = 0; i < R; ++i) ov[i] = valid[i] ? orig[lane + 64 * i] : 0;
+    for (int i = S0; i < R; ++i) ov[i] = valid[i] ? orig[lane + 64 * i] : 0;
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
+    for (int i = S0; i < R; ++i) {
       if (valid[i]) {
         float4* gr = reinterpret_cast<float4*>(gbuf_k + ov[i] * 16);
 #pragma unroll
@@ -200,7 +234,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
     }
     wave_lds_fence();
 #pragma unroll
-    for (int i = 0; i < R; ++i)
+    for (int i = S0; i < R; ++i)
       if (valid[i]) orig[pos[i]] = (unsigned char)ov[i];
   }
   wave_lds_fence();
@@ -294,7 +328,7 @@ __device__ __forceinline__ void pf_load(float* T, const float* __restrict__ g, i
 }
 
 template <int N, bool FACT>
-__global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__ A, int n, int skew,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void pf_small_kernel(const float* __restrict__ A, int n, int skew,
                                                        float* __restrict__ sign_out,
                                                        float* __restrict__ logabs_out,
                                                        float* __restrict__ gbuf_out,
@@ -302,9 +336,10 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
                                                        int* __restrict__ perm_out) {
   using C = PfSmall<N>;
   constexpr int NB = C::NB, TPW = C::TPW;
+  static_assert(TPW <= 8, "the sign mask holds 32 entries per chunk");
   __shared__ __align__(16) float T[C::NTRI];
   __shared__ __align__(16) float Gs[N * 16];
-  __shared__ unsigned char src[N];
+  __shared__ __align__(16) unsigned char src[N];
   __shared__ unsigned char orig[FACT ? N : 1];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -316,69 +351,97 @@ __global__ __launch_bounds__(256) void pf_small_kernel(const float* __restrict__
   PivotLog<C::NPV> piv_log;
   piv_log.init();
   int nsw = 0;
-  const int li = lane & 15, g = lane >> 4;
   for (int k = 0; k < NB; ++k) {
     const int r0 = 16 * k;
     if (wave == 0) {
       float* gk = FACT ? gbuf_out + (b * NB + k) * (int64_t)N * 16 : nullptr;
       float* dk = FACT ? d_out + b * (N / 2) + 8 * k : nullptr;
-      pf_panel<N, FACT>(T, Gs, r0, src, lane, piv_log, nsw, orig, gk, dk);
+      if (C::R == 2 && r0 >= 64)
+        pf_panel<N, FACT, C::R - 1>(T, Gs, r0, src, lane, piv_log, nsw, orig, gk, dk);
+      else
+        pf_panel<N, FACT, 0>(T, Gs, r0, src, lane, piv_log, nsw, orig, gk, dk);
     }
     const int nt = (N - r0 - 16) / 16;
     if (nt == 0) break;
     __syncthreads();
     const int ntiles = nt * (nt + 1) / 2;
     const int rb = r0 + 16;
-    v4f acc[TPW];
-    int ti[TPW], tj[TPW];
-    // gather the old lower tiles M[src p][src q] through the block's permutation
+    int li = lane & 15, g = lane >> 4, wv = __builtin_amdgcn_readfirstlane(wave);
+    asm volatile("" : "+v"(li), "+v"(g), "+s"(wv));
+    // Tiles t = wv + 4 s of the lower triangle of the trailing block, row-major:
+    // t -> (I, J), I >= J; t is wave-uniform, so idle slots are skipped by scalar
+    // branches. Tiles are processed in chunks of up to 4 (register budget): each chunk reads its
+    // permutation bytes, then its old entries M[src p][src q] (raw triangle values; bit
+    // 4 j + v of `neg` marks the ones stored transposed, negated only once every read is
+    // in flight) and G rows, then runs the MFMAs and stores.
+    // No barrier separates these reads from the stores: an entry whose row and column
+    // both stay in place is read and rewritten by the same lane, and every other old
+    // entry lies in a row or column of the block just factored (positions r0..rb-1),
+    // which this update never writes.
+    static_for<0, (TPW + 3) / 4>([&](auto cc) {
+      constexpr int S0C = 4 * decltype(cc)::value;
+      constexpr int CH = (TPW - S0C) < 4 ? (TPW - S0C) : 4;
+      int P[CH], Q[CH], sr[CH], sq[CH];
+      unsigned sp4[CH];
 #pragma unroll
-    for (int s = 0; s < TPW; ++s) {
-      const int t = wave + 4 * s;
-      ti[s] = 0;
-      tj[s] = 0;
-      if (t < ntiles) {
-        // tile t -> (I, J), I >= J, row-major over the lower triangle
-        int I = 0;
-        while ((I + 1) * (I + 2) / 2 <= t) ++I;
-        const int J = t - I * (I + 1) / 2;
-        ti[s] = I;
-        tj[s] = J;
-        const int q = rb + 16 * J + li;
-        const int sq = src[q];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int p = rb + 16 * I + 4 * g + v;
-          const int sp = src[p];
-          const int hi = max(sp, sq), lo = min(sp, sq);
-          const float e = T[p > q ? tri_row(hi) + lo : 0];
-          acc[s][v] = sp > sq ? e : -e;
+      for (int j = 0; j < CH; ++j) {
+        const int t = wv + 4 * (S0C + j);
+        P[j] = Q[j] = rb;
+        sp4[j] = 0;
+        sr[j] = sq[j] = 0;
+        if (t < ntiles) {
+          int I = 0;
+          static_for<1, C::MAXNT>([&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            I += (t >= m * (m + 1) / 2) ? 1 : 0;
+          });
+          const int J = t - I * (I + 1) / 2;
+          P[j] = rb + 16 * I;
+          Q[j] = rb + 16 * J;
+          sp4[j] = *reinterpret_cast<const unsigned*>(src + P[j] + 4 * g);
+          sr[j] = src[P[j] + li];
+          sq[j] = src[Q[j] + li];
         }
       }
-    }
-    __syncthreads();
+      float raw[CH][4];
+      float4 ga[CH], gb[CH];
+      unsigned neg = 0;
 #pragma unroll
-    for (int s = 0; s < TPW; ++s) {
-      const int t = wave + 4 * s;
-      if (t < ntiles) {
-        const int I = ti[s], J = tj[s];
-        const int sr = src[rb + 16 * I + li];
-        const int sq = src[rb + 16 * J + li];
+      for (int j = 0; j < CH; ++j) {
+        if (wv + 4 * (S0C + j) < ntiles) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int k = 4 * u + g;
-          const float av = Gs[g_idx(sr, k)];
-          const float bv = (k & 1) ? -Gs[g_idx(sq, k - 1)] : Gs[g_idx(sq, k + 1)];
-          acc[s] = mfma16(av, bv, acc[s]);
-        }
-        const int q = rb + 16 * J + li;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int p = rb + 16 * I + 4 * g + v;
-          if (p > q) T[tri_row(p) + q] = acc[s][v];
+          for (int v = 0; v < 4; ++v) {
+            const int spv = (sp4[j] >> (8 * v)) & 0xFF;
+            const int hi = max(spv, sq[j]), lo = min(spv, sq[j]);
+            // p <= q (diagonal tiles) is never stored; only its address needs clamping
+            raw[j][v] = T[min(tri_row(hi) + lo, C::NTRI - 1)];
+            neg |= (spv < sq[j] ? 1u : 0u) << (4 * j + v);
+          }
+          ga[j] = *reinterpret_cast<const float4*>(Gs + g_idx(sr[j], 4 * g));
+          gb[j] = *reinterpret_cast<const float4*>(Gs + g_idx(sq[j], 4 * g));
         }
       }
-    }
+      // M'' = M + G J G^T: MFMA step u contracts k = 4 g + u, so each lane's A and B
+      // operands are one 16-byte G row group; (J G^T)[k] = G[k+1] (k even), -G[k-1] (k odd)
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        if (wv + 4 * (S0C + j) < ntiles) {
+          v4f acc;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[v] = ((neg >> (4 * j + v)) & 1) ? -raw[j][v] : raw[j][v];
+          acc = mfma16(ga[j].x, gb[j].y, acc);
+          acc = mfma16(ga[j].y, -gb[j].x, acc);
+          acc = mfma16(ga[j].z, gb[j].w, acc);
+          acc = mfma16(ga[j].w, -gb[j].z, acc);
+          const int q = Q[j] + li;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int p = P[j] + 4 * g + v;
+            if (p > q) T[tri_row(p) + q] = acc[v];
+          }
+        }
+      }
+    });
     __syncthreads();
   }
   if (wave == 0) {
