@@ -13,9 +13,10 @@
 //
 // LDS (N = 128: exactly 40 KiB, so four matrices share a CU):
 //   * T: M[p][q] for p > q at T[p (p - 1) / 2 + q]; M[q][p] = -M[p][q], M[p][p] = 0;
-//   * Gs: the block's tau / w vectors, 16 per row, columns XOR-swizzled by row bits 2-3
-//     so 16 consecutive rows x 4 columns hit 64 distinct banks while 4-column groups
-//     stay 16-byte aligned;
+//   * Gs (directly after T): the block's tau / w vectors, 16 per row, stored as four
+//     column groups Gs[k / 4][row][k % 4], so one row's group is a 16-byte vector at a
+//     constant offset from the row's first group and 16 consecutive rows' groups cover
+//     all 64 banks;
 //   * src (position -> row at block start) and orig (FACT: row -> original row), bytes.
 //
 // Per block (positions from r0; rows stored in block-start order):
@@ -52,7 +53,8 @@ static_assert(PfSmall<128>::LDS_BYTES <= 40960, "four n = 128 workgroups per CU"
 __device__ __forceinline__ int tri_row(int p) { return (p * (p - 1)) >> 1; }
 
 // Index of G element (row s, column k) in Gs.
-__device__ __forceinline__ int g_idx(int s, int k) { return s * 16 + (k ^ (((s >> 2) & 3) << 2)); }
+template <int N>
+__device__ __forceinline__ int g_idx(int s, int k) { return (k >> 2) * (4 * N) + 4 * s + (k & 3); }
 
 // Lowest set row of a per-slot ballot pair: slot s holds rows l + 64 s.
 // Slots below S0 hold no candidate.
@@ -80,7 +82,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
   for (int i = S0; i < R; ++i) {
     const int row = lane + 64 * i;
     valid[i] = (row >= r0) && (row < N);
-    pos[i] = row;
+    pos[i] = valid[i] ? row : -1;  // finished / absent rows never match a position >= r0
     rop[i] = row < N ? tri_row(row) : 0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) G[i][k] = 0.0f;
@@ -92,7 +94,8 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
     for (int i = S0; i < R; ++i) {
       const int row = lane + 64 * i;
       const bool below = row > q;
-      const int e = min(below ? rop[i] + q : roq + row, NTRI - 1);
+      // row == q == N-1 addresses T[NTRI], the first entry of Gs (value unused)
+      const int e = below ? rop[i] + q : roq + row;
       const float t = T[e];
       v[i] = below ? t : -t;
     }
@@ -100,10 +103,9 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
   // the first 2t entries of Gs row q, broadcast to every lane
   auto grow = [&](int q, float (&g)[16], auto tc) {
     constexpr int t = decltype(tc)::value;
-    const int sw = ((q >> 2) & 3) << 2;
     static_for<0, (2 * t + 3) / 4>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
-      const float4 v = *reinterpret_cast<const float4*>(Gs + q * 16 + ((4 * j) ^ sw));
+      const float4 v = *reinterpret_cast<const float4*>(Gs + 4 * q + j * (4 * N));
       g[4 * j] = v.x;
       g[4 * j + 1] = v.y;
       g[4 * j + 2] = v.z;
@@ -114,7 +116,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
   auto row_at = [&](int c) {
     unsigned long long b[R];
 #pragma unroll
-    for (int i = S0; i < R; ++i) b[i] = __ballot(valid[i] && pos[i] == c);
+    for (int i = S0; i < R; ++i) b[i] = __ballot(pos[i] == c);
     return first_row<R, S0>(b);
   };
   // v += sum_{u < U} G[.][2u] gq[2u+1] - G[.][2u+1] gq[2u], in order of u
@@ -142,7 +144,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
     unsigned key[R], kb = 0;
 #pragma unroll
     for (int i = S0; i < R; ++i) {
-      key[i] = cand_key(x[i], valid[i] && pos[i] > c);
+      key[i] = cand_key(x[i], pos[i] > c);
       kb = max(kb, key[i]);
     }
     const int qn = t < 7 ? row_at(c + 2) : 0;  // speculative next row a
@@ -174,7 +176,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
 #pragma unroll
     for (int i = S0; i < R; ++i) {
       const int row = lane + 64 * i;
-      if (valid[i] && pos[i] == c + 1) pos[i] = pp;
+      if (pos[i] == c + 1) pos[i] = pp;
       if (row == qp) pos[i] = c + 1;
     }
     nsw += (pp != c + 1) ? 1 : 0;
@@ -182,11 +184,11 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
 #pragma unroll
     for (int i = S0; i < R; ++i) {
       const int row = lane + 64 * i;
-      const bool act = valid[i] && pos[i] > c + 1;
+      const bool act = pos[i] > c + 1;
       G[i][2 * t] = act ? -x[i] * inv : 0.0f;
       G[i][2 * t + 1] = act ? y[i] : 0.0f;
       if (row < N)
-        *reinterpret_cast<float2*>(Gs + g_idx(row, 2 * t)) = make_float2(G[i][2 * t], G[i][2 * t + 1]);
+        *reinterpret_cast<float2*>(Gs + g_idx<N>(row, 2 * t)) = make_float2(G[i][2 * t], G[i][2 * t + 1]);
     }
     wave_lds_fence();
     if (FACT && lane == 0) d_k[t] = d;
@@ -337,8 +339,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   using C = PfSmall<N>;
   constexpr int NB = C::NB, TPW = C::TPW;
   static_assert(TPW <= 8, "the sign mask holds 32 entries per chunk");
-  __shared__ __align__(16) float T[C::NTRI];
-  __shared__ __align__(16) float Gs[N * 16];
+  __shared__ __align__(16) float lds[C::NTRI + N * 16];  // T, then Gs (NTRI * 4 % 16 == 0)
+  float* const T = lds;
+  float* const Gs = lds + C::NTRI;
   __shared__ __align__(16) unsigned char src[N];
   __shared__ unsigned char orig[FACT ? N : 1];
   const int64_t b = blockIdx.x;
@@ -413,12 +416,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
           for (int v = 0; v < 4; ++v) {
             const int spv = (sp4[j] >> (8 * v)) & 0xFF;
             const int hi = max(spv, sq[j]), lo = min(spv, sq[j]);
-            // p <= q (diagonal tiles) is never stored; only its address needs clamping
-            raw[j][v] = T[min(tri_row(hi) + lo, C::NTRI - 1)];
+            // p <= q (diagonal tiles) is never stored; p == q may address T[NTRI] (in Gs)
+            raw[j][v] = T[tri_row(hi) + lo];
             neg |= (spv < sq[j] ? 1u : 0u) << (4 * j + v);
           }
-          ga[j] = *reinterpret_cast<const float4*>(Gs + g_idx(sr[j], 4 * g));
-          gb[j] = *reinterpret_cast<const float4*>(Gs + g_idx(sq[j], 4 * g));
+          ga[j] = *reinterpret_cast<const float4*>(Gs + g_idx<N>(sr[j], 4 * g));
+          gb[j] = *reinterpret_cast<const float4*>(Gs + g_idx<N>(sq[j], 4 * g));
         }
       }
       // M'' = M + G J G^T: MFMA step u contracts k = 4 g + u, so each lane's A and B
