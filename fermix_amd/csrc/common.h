@@ -40,18 +40,18 @@ __device__ __forceinline__ unsigned dpp_u32(unsigned v) {
 }
 
 // Maximum of v over the 64 lanes, returned wave-uniform: a 16-lane all-reduce with DPP
-// (quad xor 1, quad xor 2, half-row mirror, row mirror) followed by a scalar max over the
-// four rows' results.
+// (quad xor 1, quad xor 2, half-row mirror, row mirror), then row_bcast:15 into rows 1
+// and 3 and row_bcast:31 into rows 2 and 3, after which lane 63 holds the maximum.
 __device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
   v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
   v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
   v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
   v = max(v, dpp_u32<0x140>(v));  // row_mirror
-  unsigned r0 = __builtin_amdgcn_readlane(v, 0);
-  unsigned r1 = __builtin_amdgcn_readlane(v, 16);
-  unsigned r2 = __builtin_amdgcn_readlane(v, 32);
-  unsigned r3 = __builtin_amdgcn_readlane(v, 48);
-  return max(max(r0, r1), max(r2, r3));
+  // rows outside the mask read 0, the identity of the max, so each step folds into one
+  // v_max_u32_dpp
+  v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false));
+  v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false));
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
 template <int CTRL>
