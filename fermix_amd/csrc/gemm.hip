@@ -39,13 +39,16 @@ __device__ __forceinline__ float mask_val(float v, int mask, int r, int c) {
 __device__ __forceinline__ bool mask_lower(int m) { return m == MASK_LOWER_UNIT; }
 __device__ __forceinline__ bool mask_upper(int m) { return m == MASK_UPPER || m == MASK_UPPER_UNIT; }
 
-template <int BM, int BN>
+// Tile loads: VEC uses 16-byte global loads along the operand's contiguous dimension
+// (requires that dimension, the leading dimensions, batch strides and base pointers to be
+// multiples of 4 floats), otherwise one float per load. Masks are applied in registers.
+template <int BM, int BN, bool VEC>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   constexpr int LDSA = BM + 4, LDSB = BN + 4;
   constexpr int WM = BM / 2, WN = BN / 2;   // per-wave quarter
   constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 tiles per wave
-  __shared__ float As[2][GBK * LDSA];
-  __shared__ float Bs[2][GBK * LDSB];
+  __shared__ __align__(16) float As[2][GBK * LDSA];
+  __shared__ __align__(16) float Bs[2][GBK * LDSB];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t bat = blockIdx.y, bat2 = blockIdx.z;
@@ -78,6 +81,137 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   if (mask_upper(d.maskB)) khi = min(khi, j0 + BN + d.offBc - d.offBr);
   klo = max(0, (klo / GBK) * GBK);
 
+  const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+  const int l32 = lane & 31, lh = lane >> 5;
+
+  // global -> register staging of one K stage: A tile BM x GBK, B tile GBK x BN
+  constexpr int AV = BM * GBK / 1024, BV = BN * GBK / 1024;  // float4 per thread
+  constexpr int AE = BM * GBK / 256, BE = BN * GBK / 256;      // floats per thread
+  float4 va[VEC ? AV : 1], vb[VEC ? BV : 1];
+  float ra[VEC ? 1 : AE], rb[VEC ? 1 : BE];
+  auto load_stage = [&](int k0) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int e = 0; e < AV; ++e) {
+        const int idx = tid + 256 * e;
+        int gi, gk;
+        if (!d.transA) { gi = i0 + idx / (GBK / 4); gk = k0 + 4 * (idx % (GBK / 4)); }
+        else { gk = k0 + idx / (BM / 4); gi = i0 + 4 * (idx % (BM / 4)); }
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (gi < d.M && gk < d.K)
+          v = *reinterpret_cast<const float4*>(d.transA ? A + (int64_t)gk * d.lda + gi
+                                                        : A + (int64_t)gi * d.lda + gk);
+        if (d.maskA) {
+          const int r = gi + d.offAr, c = gk + d.offAc, dr = d.transA, dc = 1 - d.transA;
+          v.x = mask_val(v.x, d.maskA, r, c);
+          v.y = mask_val(v.y, d.maskA, r + dr, c + dc);
+          v.z = mask_val(v.z, d.maskA, r + 2 * dr, c + 2 * dc);
+          v.w = mask_val(v.w, d.maskA, r + 3 * dr, c + 3 * dc);
+        }
+        va[e] = v;
+      }
+#pragma unroll
+      for (int e = 0; e < BV; ++e) {
+        const int idx = tid + 256 * e;
+        int gk, gj;
+        if (!d.transB) { gk = k0 + idx / (BN / 4); gj = j0 + 4 * (idx % (BN / 4)); }
+        else { gj = j0 + idx / (GBK / 4); gk = k0 + 4 * (idx % (GBK / 4)); }
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (gj < d.N && gk < d.K)
+          v = *reinterpret_cast<const float4*>(d.transB ? B + (int64_t)gj * d.ldb + gk
+                                                        : B + (int64_t)gk * d.ldb + gj);
+        if (d.maskB) {
+          const int r = gk + d.offBr, c = gj + d.offBc, dr = d.transB, dc = 1 - d.transB;
+          v.x = mask_val(v.x, d.maskB, r, c);
+          v.y = mask_val(v.y, d.maskB, r + dr, c + dc);
+          v.z = mask_val(v.z, d.maskB, r + 2 * dr, c + 2 * dc);
+          v.w = mask_val(v.w, d.maskB, r + 3 * dr, c + 3 * dc);
+        }
+        vb[e] = v;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < AE; ++e) {
+        const int idx = tid + 256 * e;
+        int i, k;
+        if (!d.transA) { i = idx / GBK; k = idx % GBK; }   // row-major A: k fastest
+        else { k = idx / BM; i = idx % BM; }               // A^T stored: i fastest
+        const int gi = i0 + i, gk = k0 + k;
+        float v = 0.0f;
+        if (gi < d.M && gk < d.K) {
+          v = d.transA ? A[(int64_t)gk * d.lda + gi] : A[(int64_t)gi * d.lda + gk];
+          if (d.maskA) v = mask_val(v, d.maskA, gi + d.offAr, gk + d.offAc);
+        }
+        ra[e] = v;
+      }
+#pragma unroll
+      for (int e = 0; e < BE; ++e) {
+        const int idx = tid + 256 * e;
+        int k, j;
+        if (!d.transB) { k = idx / BN; j = idx % BN; }     // row-major B: j fastest
+        else { j = idx / GBK; k = idx % GBK; }             // B^T stored: k fastest
+        const int gk = k0 + k, gj = j0 + j;
+        float v = 0.0f;
+        if (gj < d.N && gk < d.K) {
+          v = d.transB ? B[(int64_t)gj * d.ldb + gk] : B[(int64_t)gk * d.ldb + gj];
+          if (d.maskB) v = mask_val(v, d.maskB, gk + d.offBr, gj + d.offBc);
+        }
+        rb[e] = v;
+      }
+    }
+  };
+  // registers -> LDS, K-major (As[k][i], Bs[k][j]) so each MFMA operand read is 32
+  // consecutive floats
+  auto store_stage = [&](int buf) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int e = 0; e < AV; ++e) {
+        const int idx = tid + 256 * e;
+        if (!d.transA) {
+          const int i = idx / (GBK / 4), k = 4 * (idx % (GBK / 4));
+          As[buf][k * LDSA + i] = va[e].x;
+          As[buf][(k + 1) * LDSA + i] = va[e].y;
+          As[buf][(k + 2) * LDSA + i] = va[e].z;
+          As[buf][(k + 3) * LDSA + i] = va[e].w;
+        } else {
+          const int k = idx / (BM / 4), i = 4 * (idx % (BM / 4));
+          *reinterpret_cast<float4*>(&As[buf][k * LDSA + i]) = va[e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < BV; ++e) {
+        const int idx = tid + 256 * e;
+        if (!d.transB) {
+          const int k = idx / (BN / 4), j = 4 * (idx % (BN / 4));
+          *reinterpret_cast<float4*>(&Bs[buf][k * LDSB + j]) = vb[e];
+        } else {
+          const int j = idx / (GBK / 4), k = 4 * (idx % (GBK / 4));
+          Bs[buf][k * LDSB + j] = vb[e].x;
+          Bs[buf][(k + 1) * LDSB + j] = vb[e].y;
+          Bs[buf][(k + 2) * LDSB + j] = vb[e].z;
+          Bs[buf][(k + 3) * LDSB + j] = vb[e].w;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < AE; ++e) {
+        const int idx = tid + 256 * e;
+        int i, k;
+        if (!d.transA) { i = idx / GBK; k = idx % GBK; }
+        else { k = idx / BM; i = idx % BM; }
+        As[buf][k * LDSA + i] = ra[e];
+      }
+#pragma unroll
+      for (int e = 0; e < BE; ++e) {
+        const int idx = tid + 256 * e;
+        int k, j;
+        if (!d.transB) { k = idx / BN; j = idx % BN; }
+        else { j = idx / GBK; k = idx % GBK; }
+        Bs[buf][k * LDSB + j] = rb[e];
+      }
+    }
+  };
+
   v16f acc[TM][TN];
 #pragma unroll
   for (int a = 0; a < TM; ++a)
@@ -85,65 +219,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
     for (int b = 0; b < TN; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+  if (klo < khi) load_stage(klo);
 
-  // global -> register staging: A tile BM x GBK, B tile GBK x BN, as float (simple and
-  // general: any ld, offsets and masks); 256 threads
-  constexpr int AE = BM * GBK / 256, BE = BN * GBK / 256;
-  float ra[AE], rb[BE];
-  auto load_stage = [&](int k0) {
-#pragma unroll
-    for (int e = 0; e < AE; ++e) {
-      const int idx = tid + 256 * e;
-      int i, k;
-      if (!d.transA) { i = idx / GBK; k = idx % GBK; }   // row-major A: k fastest
-      else { k = idx / BM; i = idx % BM; }               // A^T stored: i fastest
-      const int gi = i0 + i, gk = k0 + k;
-      float v = 0.0f;
-      if (gi < d.M && gk < khi && gk < d.K) {
-        v = d.transA ? A[(int64_t)gk * d.lda + gi] : A[(int64_t)gi * d.lda + gk];
-        if (d.maskA) v = mask_val(v, d.maskA, gi + d.offAr, gk + d.offAc);
-      }
-      ra[e] = v;
-    }
-#pragma unroll
-    for (int e = 0; e < BE; ++e) {
-      const int idx = tid + 256 * e;
-      int k, j;
-      if (!d.transB) { k = idx / BN; j = idx % BN; }     // row-major B: j fastest
-      else { j = idx / GBK; k = idx % GBK; }             // B^T stored: k fastest
-      const int gk = k0 + k, gj = j0 + j;
-      float v = 0.0f;
-      if (gj < d.N && gk < khi && gk < d.K) {
-        v = d.transB ? B[(int64_t)gj * d.ldb + gk] : B[(int64_t)gk * d.ldb + gj];
-        if (d.maskB) v = mask_val(v, d.maskB, gk + d.offBr, gj + d.offBc);
-      }
-      rb[e] = v;
-    }
-  };
-  auto store_stage = [&](int buf) {
-#pragma unroll
-    for (int e = 0; e < AE; ++e) {
-      const int idx = tid + 256 * e;
-      int i, k;
-      if (!d.transA) { i = idx / GBK; k = idx % GBK; }
-      else { k = idx / BM; i = idx % BM; }
-      As[buf][k * LDSA + i] = ra[e];
-    }
-#pragma unroll
-    for (int e = 0; e < BE; ++e) {
-      const int idx = tid + 256 * e;
-      int k, j;
-      if (!d.transB) { k = idx / BN; j = idx % BN; }
-      else { j = idx / GBK; k = idx % GBK; }
-      Bs[buf][k * LDSB + j] = rb[e];
-    }
-  };
-
-  const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
-  const int l32 = lane & 31, lh = lane >> 5;
   int buf = 0;
   if (klo < khi) {
-    load_stage(klo);
     store_stage(0);
     __syncthreads();
     for (int k0 = klo; k0 < khi; k0 += GBK) {
@@ -170,26 +249,36 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
     }
   }
 
-  // epilogue: C = alpha * acc + beta * C (and the mirror)
+  // epilogue: C = alpha * acc + beta * C (and the mirror), one 32x32 accumulator at a
+  // time with its 16 reads of C issued before any store (C is read and written through
+  // the same pointer, so reads placed after a store could not be hoisted)
   const bool diag_tile = d.lower_only && ti == tj;
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
-    for (int b = 0; b < TN; ++b)
+    for (int b = 0; b < TN; ++b) {
+      const int c = j0 + wn + 32 * b + l32;
+      float cv[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = i0 + wm + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
-        const int c = j0 + wn + 32 * b + l32;
+        cv[v] = (d.beta != 0.0f && r < d.M && c < d.N) ? C[(int64_t)r * d.ldc + c] : 0.0f;
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = i0 + wm + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
         if (r >= d.M || c >= d.N) continue;
         if (diag_tile && r < c) continue;
-        float* cp = C + (int64_t)r * d.ldc + c;
         float val = d.alpha * acc[a][b][v];
-        if (d.beta != 0.0f) val = fmaf(d.beta, *cp, val);
+        if (d.beta != 0.0f) val = fmaf(d.beta, cv[v], val);
         if (d.lower_only && r == c && d.mirror < 0.0f) val = 0.0f;
-        *cp = val;
+        C[(int64_t)r * d.ldc + c] = val;
         if (d.lower_only && r != c) C[(int64_t)c * d.ldc + r] = d.mirror * val;
       }
+    }
 }
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
   if (d.M <= 0 || d.N <= 0 || batch <= 0 || nb2 <= 0) return FX_OK;
@@ -198,16 +287,23 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
   const int BM = big ? 128 : 64, BN = BM;
   const int tm = (d.M + BM - 1) / BM, tn = (d.N + BN - 1) / BN;
   const int tiles = d.lower_only ? tm * (tm + 1) / 2 : tm * tn;
+  // 16-byte loads need every contiguous extent, leading dimension, batch stride and base
+  // pointer to be a multiple of 4 floats
+  const bool vec = aligned16(d.A) && aligned16(d.B) && d.lda % 4 == 0 && d.ldb % 4 == 0 &&
+                   d.sA % 4 == 0 && d.sB % 4 == 0 && d.sA2 % 4 == 0 && d.sB2 % 4 == 0 &&
+                   d.K % 4 == 0 && (d.transA ? d.M % 4 == 0 : true) &&
+                   (d.transB ? true : d.N % 4 == 0);
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
     const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
     GemmDesc e = d;
     e.A += b0 * d.sA;
     e.B += b0 * d.sB;
     e.C += b0 * d.sC;
-    if (big)
-      hipLaunchKernelGGL((gemm_kernel<128, 128>), dim3(tiles, (unsigned)nb, nb2), dim3(256), 0, s, e);
-    else
-      hipLaunchKernelGGL((gemm_kernel<64, 64>), dim3(tiles, (unsigned)nb, nb2), dim3(256), 0, s, e);
+    const dim3 grid(tiles, (unsigned)nb, nb2);
+    if (big && vec) hipLaunchKernelGGL((gemm_kernel<128, 128, true>), grid, dim3(256), 0, s, e);
+    else if (big) hipLaunchKernelGGL((gemm_kernel<128, 128, false>), grid, dim3(256), 0, s, e);
+    else if (vec) hipLaunchKernelGGL((gemm_kernel<64, 64, true>), grid, dim3(256), 0, s, e);
+    else hipLaunchKernelGGL((gemm_kernel<64, 64, false>), grid, dim3(256), 0, s, e);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
