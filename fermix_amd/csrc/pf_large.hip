@@ -1,5 +1,5 @@
 // Blocked Parlett-Reid with partial pivoting for 128 < n <= 2048 (any batch). The skew
-// matrix lives in two ping-pong buffers (full storage, exactly skew). Per block of
+// matrix lives in one workspace buffer (full storage, exactly skew). Per block of
 // PB = 16 pair steps (32 columns) at r0:
 //   1. pf_panel_kernel (one workgroup of NT = 256..1024 threads per matrix, each lane
 //      owning 2 of the m = N - r0 rows): the 16 pair steps with the tau / w vectors kept
@@ -8,10 +8,13 @@
 //      has two workgroup barriers (the row at position c, the pivot). The permutation is
 //      virtual inside the block; the kernel writes G in the block's new row order and
 //      the map src[new position] = old row;
-//   2. pf_update_kernel (matrix x lower-triangle 64x64 tile): M'' = M[src, src] + G J G^T
-//      on fp32 MFMA (K = 32), reading the old buffer through the permutation and writing
-//      the new buffer in the new order, lower tile plus its mirrored (negated) transpose
-//      through LDS, so both stores are coalesced and M'' stays exactly skew.
+//   2. pf_update_kernel (matrix x lower-triangle 128x128 tile, in place):
+//      M'' = M[src, src] + G J G^T on fp32 MFMA (K = 32), the old entries read through the
+//      permutation, the new ones stored in the new order: the lower tile directly, its
+//      mirrored (negated) transpose through LDS, so both stores are coalesced and M'' stays
+//      exactly skew. In place is safe: a row that moves into a trailing position comes
+//      from the block just factored, whose rows and columns the update never writes, and
+//      every other old entry is read by the lane that rewrites it.
 // Reference roles replaced (ChenAo-Phys/fermix): _pf_run / _pf_core (src/fermix/_pf.py:
 // 497-570), the pair-step panel (:59-284) and the rank-2b update (:287-382).
 #include "common.h"
@@ -225,13 +228,18 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
 
 // M_new[p][q] = M_old[src p][src q] + sum_k G[p][k] (J G^T)[k][q] for the trailing
 // positions p, q >= r1 (lower tiles; the upper triangle by the negated transpose).
-__global__ __launch_bounds__(256) void pf_update_kernel(const float* __restrict__ Mo, float* __restrict__ Mn,
-                                                        int N, int r1, const int* __restrict__ src,
+__global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, int N, int r1,
+                                                        const int* __restrict__ src,
                                                         const float* __restrict__ Gn) {
-  constexpr int T = 64, LD = T + 4;
-  __shared__ float Ga[PFB][LD];  // A^T: G rows of the tile rows, K-major
-  __shared__ float Hb[PFB][LD];  // (J G^T) columns of the tile columns, K-major
-  __shared__ float Ct[T][T + 1];
+  constexpr int T = 128, LDG = T + 4, LDT = 64 + 1;
+  typedef float v16f __attribute__((ext_vector_type(16)));
+  // Ga / Hb: the G rows of the tile rows / (J G^T) columns of the tile columns, K-major;
+  // after the MFMAs the same LDS holds half of the tile transposed (128 x 64)
+  __shared__ __align__(16) float lds[2 * PFB * LDG];
+  static_assert(T * LDT <= 2 * PFB * LDG, "transpose buffer fits");
+  __shared__ int sp[T], sq[T];
+  float* Ga = lds;
+  float* Hb = lds + PFB * LDG;
   const int64_t b = blockIdx.y;
   const int t = blockIdx.x;
   int I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
@@ -242,47 +250,90 @@ __global__ __launch_bounds__(256) void pf_update_kernel(const float* __restrict_
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* G = Gn + b * (int64_t)N * PFB;
   const int* sb = src + b * N;
-  const float* Mob = Mo + b * (int64_t)N * N;
-  float* Mnb = Mn + b * (int64_t)N * N;
+  float* Mb = M + b * (int64_t)N * N;  // entries addressed by 32-bit offsets (N <= 2048)
   for (int e = tid; e < T * PFB; e += 256) {
     const int r = e / PFB, k = e % PFB;
     const int p = p0 + r, q = q0 + r;
-    Ga[k][r] = p < N ? G[(int64_t)p * PFB + k] : 0.0f;
+    Ga[k * LDG + r] = p < N ? G[(int64_t)p * PFB + k] : 0.0f;
     const float gq = q < N ? G[(int64_t)q * PFB + (k ^ 1)] : 0.0f;
-    Hb[k][r] = (k & 1) ? -gq : gq;
+    Hb[k * LDG + r] = (k & 1) ? -gq : gq;
+  }
+  if (tid < T) {
+    sp[tid] = p0 + tid < N ? sb[p0 + tid] : 0;
+    sq[tid] = q0 + tid < N ? sb[q0 + tid] : 0;
   }
   __syncthreads();
-  // wave (wr, wc) owns the 32x32 quarter; C starts as the gathered old matrix
-  const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
+  // wave (wr, wc) owns a 64x64 quarter as 2x2 32x32 accumulators, seeded with the old
+  // entries M[src p][src q]
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
   const int l32 = lane & 31, lh = lane >> 5;
-  typedef float v16f __attribute__((ext_vector_type(16)));
-  v16f acc;
+  v16f acc[2][2];
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int p = p0 + wr + 8 * (v >> 2) + 4 * lh + (v & 3);
-    const int q = q0 + wc + l32;
-    acc[v] = (p < N && q < N) ? Mob[(int64_t)sb[p] * N + sb[q]] : 0.0f;
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int cl = wc + 32 * c + l32;
+      const int scol = sq[cl];
+      const bool cin = q0 + cl < N;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int rl = wr + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
+        acc[a][c][v] = (cin && p0 + rl < N) ? Mb[(unsigned)(sp[rl] * N + scol)] : 0.0f;
+      }
+    }
+#pragma unroll
+  for (int kp = 0; kp < PFB / 2; ++kp) {
+    float av[2], bv[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) av[a] = Ga[(2 * kp + lh) * LDG + wr + 32 * a + l32];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) bv[c] = Hb[(2 * kp + lh) * LDG + wc + 32 * c + l32];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        acc[a][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[c], acc[a][c], 0, 0, 0);
   }
-#pragma unroll
-  for (int kp = 0; kp < PFB / 2; ++kp)
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Ga[2 * kp + lh][wr + l32], Hb[2 * kp + lh][wc + l32], acc, 0, 0, 0);
   const bool diag = I == J;
+  // the tile itself (a diagonal tile is stored whole: its upper half comes from the old
+  // upper entries and the negated products, i.e. exactly the mirror; diagonal forced 0)
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int rr = wr + 8 * (v >> 2) + 4 * lh + (v & 3), cc = wc + l32;
-    float val = acc[v];
-    if (diag && rr == cc) val = 0.0f;
-    Ct[rr][cc] = val;
-    const int p = p0 + rr, q = q0 + cc;
-    if (p < N && q < N && (!diag || rr > cc)) Mnb[(int64_t)p * N + q] = val;
-    if (diag && rr == cc && p < N) Mnb[(int64_t)p * N + q] = 0.0f;
-  }
-  __syncthreads();
-  // mirrored tile: Mn[q][p] = -C[p][q], written row-contiguous
-  for (int e = tid; e < T * T; e += 256) {
-    const int cc = e / T, rr = e % T;
-    const int p = p0 + rr, q = q0 + cc;
-    if (p < N && q < N && (!diag || rr > cc)) Mnb[(int64_t)q * N + p] = -Ct[rr][cc];
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int cl = wc + 32 * c + l32;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int rl = wr + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
+        const int p = p0 + rl, q = q0 + cl;
+        if (p < N && q < N) Mb[(unsigned)(p * N + q)] = (diag && rl == cl) ? 0.0f : acc[a][c][v];
+      }
+    }
+  if (diag) return;  // uniform over the workgroup
+  // mirrored tile Mn[q][p] = -C[p][q], one 64-row half of the tile at a time through LDS
+  float* Ct = lds;  // Ct[cl * LDT + rl - 64 h]
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    __syncthreads();  // previous readers of the LDS are done
+    if ((wave >> 1) == h) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int cl = wc + 32 * c + l32;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int rr = 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
+            Ct[cl * LDT + rr] = acc[a][c][v];
+          }
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < T * 64; e += 256) {
+      const int cl = e >> 6, rr = e & 63;
+      const int p = p0 + 64 * h + rr, q = q0 + cl;
+      if (p < N && q < N) Mb[(unsigned)(q * N + p)] = -Ct[cl * LDT + rr];
+    }
   }
 }
 
@@ -323,8 +374,7 @@ size_t pf_large_workspace(int64_t batch, int n, bool fact) {
   const int nblk = N / PFB;
   size_t bytes = 0;
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
-  add((size_t)batch * N * N * 4);  // M ping
-  add((size_t)batch * N * N * 4);  // M pong
+  add((size_t)batch * N * N * 4);  // M (updated in place)
   add((size_t)batch * N * PFB * 4);  // G (new order)
   add((size_t)batch * N * 4);      // src
   add((size_t)batch * nblk * 4);   // swap counts
@@ -349,7 +399,6 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     return (void*)q;
   };
   float* M0 = (float*)take((size_t)batch * N * N * 4);
-  float* M1 = (float*)take((size_t)batch * N * N * 4);
   float* Gn = (float*)take((size_t)batch * N * PFB * 4);
   int* src = (int*)take((size_t)batch * N * 4);
   int* nsw = (int*)take((size_t)batch * nblk * 4);
@@ -365,7 +414,6 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     hipLaunchKernelGGL(pf_iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, orig, N, tot);
   }
   float* cur = M0;
-  float* nxt = M1;
   for (int blk = 0; blk < nblk; ++blk) {
     const int r0 = blk * PFB;
     const int m = N - r0;
@@ -381,16 +429,13 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     const int r1 = r0 + PFB;
     if (r1 < N) {
-      const int nt = (N - r1 + 63) / 64;
+      const int nt = (N - r1 + 127) / 128;
       for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
         const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
         hipLaunchKernelGGL(pf_update_kernel, dim3(nt * (nt + 1) / 2, (unsigned)nb), dim3(256), 0, s,
-                           cur + b0 * NN, nxt + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PFB);
+                           cur + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PFB);
         if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
       }
-      float* t = cur;
-      cur = nxt;
-      nxt = t;
     }
   }
   hipLaunchKernelGGL(pf_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, d, nsw, N / 2, nblk,
