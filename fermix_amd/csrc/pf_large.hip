@@ -251,11 +251,23 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
   const float* G = Gn + b * (int64_t)N * PFB;
   const int* sb = src + b * N;
   float* Mb = M + b * (int64_t)N * N;  // entries addressed by 32-bit offsets (N <= 2048)
-  for (int e = tid; e < T * PFB; e += 256) {
+  // fixed trip count, so every load is issued before the first store
+  constexpr int GE = T * PFB / 256;
+  float ga[GE], gb[GE];
+#pragma unroll
+  for (int i = 0; i < GE; ++i) {
+    const int e = tid + 256 * i;
     const int r = e / PFB, k = e % PFB;
-    const int p = p0 + r, q = q0 + r;
-    Ga[k * LDG + r] = p < N ? G[(int64_t)p * PFB + k] : 0.0f;
-    const float gq = q < N ? G[(int64_t)q * PFB + (k ^ 1)] : 0.0f;
+    const int p = min(p0 + r, N - 1), q = min(q0 + r, N - 1);
+    ga[i] = G[(unsigned)(p * PFB + k)];
+    gb[i] = G[(unsigned)(q * PFB + (k ^ 1))];
+  }
+#pragma unroll
+  for (int i = 0; i < GE; ++i) {
+    const int e = tid + 256 * i;
+    const int r = e / PFB, k = e % PFB;
+    Ga[k * LDG + r] = p0 + r < N ? ga[i] : 0.0f;
+    const float gq = q0 + r < N ? gb[i] : 0.0f;
     Hb[k * LDG + r] = (k & 1) ? -gq : gq;
   }
   if (tid < T) {
@@ -274,11 +286,12 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
     for (int c = 0; c < 2; ++c) {
       const int cl = wc + 32 * c + l32;
       const int scol = sq[cl];
-      const bool cin = q0 + cl < N;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
+        // rows / columns beyond N hold index 0 in sp / sq: an in-bounds read whose
+        // accumulator element is never stored (MFMA output elements are independent)
         const int rl = wr + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
-        acc[a][c][v] = (cin && p0 + rl < N) ? Mb[(unsigned)(sp[rl] * N + scol)] : 0.0f;
+        acc[a][c][v] = Mb[(unsigned)(sp[rl] * N + scol)];
       }
     }
 #pragma unroll
