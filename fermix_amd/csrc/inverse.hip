@@ -19,13 +19,13 @@
 
 namespace fx {
 
+// 32-bit index math (Ninv <= 2048).
 __global__ void embed_kernel(const float* __restrict__ src, int N, float* __restrict__ T, int Ninv) {
   const int64_t b = blockIdx.y;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)Ninv * Ninv) return;
-  const int r = (int)(e / Ninv), c = (int)(e % Ninv);
-  T[b * Ninv * Ninv + e] =
-      (r < N && c < N) ? src[b * (int64_t)N * N + (int64_t)r * N + c] : (r == c ? 1.0f : 0.0f);
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= Ninv * Ninv) return;
+  const int r = e / Ninv, c = e - r * Ninv;
+  T[b * Ninv * Ninv + e] = (r < N && c < N) ? src[b * (int64_t)N * N + r * N + c] : (r == c ? 1.0f : 0.0f);
 }
 
 // In-place inverse of the 32x32 diagonal block t of the packed T: lane c (< 32) forms
@@ -37,7 +37,17 @@ __global__ __launch_bounds__(64) void leaf_inverse_kernel(float* __restrict__ T,
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   float* base = T + b * (int64_t)Ninv * Ninv + (int64_t)(32 * t) * Ninv + 32 * t;
-  for (int e = lane; e < 1024; e += 64) Bk[(e >> 5) * 33 + (e & 31)] = base[(int64_t)(e >> 5) * Ninv + (e & 31)];
+  float ld[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int e = lane + 64 * u;
+    ld[u] = base[(e >> 5) * Ninv + (e & 31)];
+  }
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int e = lane + 64 * u;
+    Bk[(e >> 5) * 33 + (e & 31)] = ld[u];
+  }
   __syncthreads();
   const int c = lane & 31;
   float x[32];
@@ -73,12 +83,19 @@ __global__ void nonfinite_kernel(const float* __restrict__ Z, int Ninv, int N, i
   const int nt = (N + 63) / 64;
   const int i0 = (tile / nt) * 64, c0 = (tile % nt) * 64;
   bool bad = false;
-  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+  const float* Zb = Z + b * (int64_t)Ninv * Ninv;
+  float v[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {  // in-bounds (clamped) reads, all in flight
+    const int e = threadIdx.x + 256 * u;
+    const int i = min(i0 + e / 64, N - 1), c = min(c0 + e % 64, N - 1);
+    v[u] = Zb[i * Ninv + c];
+  }
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int e = threadIdx.x + 256 * u;
     const int i = i0 + e / 64, c = c0 + e % 64;
-    if (i < N && c < N) {
-      const float v = Z[b * (int64_t)Ninv * Ninv + (int64_t)i * Ninv + c];
-      bad = bad || !isfinite(v);
-    }
+    bad = bad || (i < N && c < N && !isfinite(v[u]));
   }
   const int any = __syncthreads_or(bad ? 1 : 0);
   if (threadIdx.x == 0) flags[b * (nt * nt) + tile] = any;
@@ -106,17 +123,29 @@ __global__ __launch_bounds__(256) void scatter_invT_kernel(const float* __restri
   const int i0 = 32 * blockIdx.y, c0 = 32 * blockIdx.x;
   const int tid = threadIdx.x;
   const bool isbad = bad[b] != 0;
-  for (int e = tid; e < 1024; e += 256) {
-    const int ii = e >> 5, cc = e & 31;
-    const int i = i0 + ii, c = c0 + cc;
-    tile[ii * 33 + cc] = (i < N && c < N) ? Z[b * (int64_t)Ninv * Ninv + (int64_t)i * Ninv + c] : 0.0f;
+  const float* Zb = Z + b * (int64_t)Ninv * Ninv;
+  float v[4];
+  int gr[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {  // in-bounds (clamped) reads, all in flight
+    const int e = tid + 256 * u;
+    const int i = min(i0 + (e >> 5), N - 1), c = min(c0 + (e & 31), N - 1);
+    v[u] = Zb[i * Ninv + c];
+    gr[u] = g0[b * N + min(c0 + (e >> 5), N - 1)];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + 256 * u;
+    tile[(e >> 5) * 33 + (e & 31)] = v[u];
   }
   __syncthreads();
-  for (int e = tid; e < 1024; e += 256) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + 256 * u;
     const int cc = e >> 5, ii = e & 31;
     const int i = i0 + ii, c = c0 + cc;
     if (i < n && c < N) {
-      const int r = g0[b * N + c];
+      const int r = gr[u];
       if (r < n) invT[b * (int64_t)n * n + (int64_t)r * n + i] = isbad ? 0.0f : tile[ii * 33 + cc];
     }
   }

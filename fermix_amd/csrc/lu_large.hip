@@ -39,12 +39,13 @@ struct Cand {
 };
 
 // Copy A (B, n, n) into the work buffer W (B, N, N) with identity padding.
+// 32-bit index math (N <= 1024).
 __global__ void copy_pad_kernel(const float* __restrict__ A, int n, float* __restrict__ W, int N) {
   const int64_t b = blockIdx.y;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)N * N) return;
-  const int r = (int)(e / N), c = (int)(e % N);
-  W[b * N * N + e] = (r < n && c < n) ? A[b * n * n + (int64_t)r * n + c] : (r == c ? 1.0f : 0.0f);
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= N * N) return;
+  const int r = e / N, c = e - r * N;
+  W[b * N * N + e] = (r < n && c < n) ? A[b * n * n + r * n + c] : (r == c ? 1.0f : 0.0f);
 }
 
 template <int MR, int PW>
@@ -67,15 +68,28 @@ __global__ __launch_bounds__(256) void lu_panel_kernel(float* __restrict__ W, in
   const int m = N - r0;
   float* Wb = W + b * (int64_t)N * N;
 
-  // load the panel: P[i][c] = W[r0 + i][r0 + c]
-  for (int e = tid; e < m * (PW / 4); e += 256) {
-    const int i = e / (PW / 4), q = e % (PW / 4);
-    const float4 v = *reinterpret_cast<const float4*>(Wb + (int64_t)(r0 + i) * N + r0 + 4 * q);
-    float* d = P + i * LDP + 4 * q;
-    d[0] = v.x;
-    d[1] = v.y;
-    d[2] = v.z;
-    d[3] = v.w;
+  // load the panel: P[i][c] = W[r0 + i][r0 + c], 8 vector loads in flight per thread
+  // (rows past m read row r0 and are not stored)
+  for (int base = 0; base < m * (PW / 4); base += 256 * 8) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = base + tid + 256 * u;
+      const int i = e / (PW / 4), q = e % (PW / 4);
+      v[u] = *reinterpret_cast<const float4*>(Wb + (int64_t)(r0 + (i < m ? i : 0)) * N + r0 + 4 * q);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = base + tid + 256 * u;
+      const int i = e / (PW / 4), q = e % (PW / 4);
+      if (i < m) {
+        float* d = P + i * LDP + 4 * q;
+        d[0] = v[u].x;
+        d[1] = v[u].y;
+        d[2] = v[u].z;
+        d[3] = v[u].w;
+      }
+    }
   }
   int pos[R];
   bool valid[R];
@@ -275,6 +289,8 @@ __global__ __launch_bounds__(256) void lu_urow_kernel(float* __restrict__ W, int
   constexpr int NSUB = PW / 16;
   __shared__ float buf[2 * PW * 64];
   __shared__ int list[2 * PW];
+  __shared__ int srcv[2 * PW];
+  __shared__ int srcU[PW];
   __shared__ int cnt;
   __shared__ float L11[PW * (PW + 1)];
   __shared__ float Ub[PW * 64];
@@ -288,30 +304,64 @@ __global__ __launch_bounds__(256) void lu_urow_kernel(float* __restrict__ W, int
   float* Wb = W + b * (int64_t)N * N;
   const int* sb = src + b * N;
   const int m = N - r0;
+  // pass 1 (indices): the moved rows (position, source row) and the source rows of
+  // positions r0 .. r0+PW-1
   if (tid == 0) cnt = 0;
   __syncthreads();
-  for (int p = tid; p < m; p += 256) {
-    if (sb[r0 + p] != r0 + p) {
+  constexpr int MQ = 1024 / 256;  // m <= N <= 1024
+  int sv[MQ];
+#pragma unroll
+  for (int q = 0; q < MQ; ++q) {
+    const int p = tid + 256 * q;
+    sv[q] = p < m ? sb[r0 + p] : r0 + p;
+  }
+#pragma unroll
+  for (int q = 0; q < MQ; ++q) {
+    const int p = tid + 256 * q;
+    if (p < m && sv[q] != r0 + p) {
       const int k = atomicAdd(&cnt, 1);
-      if (k < 2 * PW) list[k] = p;
+      if (k < 2 * PW) {
+        list[k] = p;
+        srcv[k] = sv[q];
+      }
     }
+    if (p < PW) srcU[p] = sv[q];
   }
   __syncthreads();
   const int nm = min(cnt, 2 * PW);
-  // gather everything this strip needs before anything is written: the moved rows and,
-  // for a trailing strip, A12 (rows r0 .. r0+PW-1 of the new order) and L11
-  for (int e = tid; e < nm * 64; e += 256) {
-    const int k = e / 64, c = e % 64;
-    if (c < ncol) buf[k * 64 + c] = Wb[(int64_t)sb[r0 + list[k]] * N + cstart + c];
+  // pass 2: gather everything this strip needs before anything is written -- the moved
+  // rows and, for a trailing strip, A12 (rows r0 .. r0+PW-1 of the new order) and L11.
+  // Loads go out in fixed-count batches with in-bounds (clamped) addresses.
+  const int cl = tid & 63;  // column of this thread in every 64-wide row below
+  const int cc = min(cl, ncol - 1);
+  for (int k0 = 0; k0 < nm; k0 += 32) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + (tid >> 6) + 4 * u;
+      v[u] = Wb[(int64_t)srcv[k < nm ? k : 0] * N + cstart + cc];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + (tid >> 6) + 4 * u;
+      if (k < nm && cl < ncol) buf[k * 64 + cl] = v[u];
+    }
   }
   if (!left) {
-    for (int e = tid; e < PW * 64; e += 256) {
-      const int i = e / 64, c = e % 64;
-      Ub[e] = c < ncol ? Wb[(int64_t)sb[r0 + i] * N + cstart + c] : 0.0f;
+    float v[PW / 4], w[PW * PW / 256];
+#pragma unroll
+    for (int u = 0; u < PW / 4; ++u) v[u] = Wb[(int64_t)srcU[(tid >> 6) + 4 * u] * N + cstart + cc];
+#pragma unroll
+    for (int u = 0; u < PW * PW / 256; ++u) {
+      const int e = tid + 256 * u;
+      w[u] = Wb[(int64_t)(r0 + e / PW) * N + r0 + e % PW];
     }
-    for (int e = tid; e < PW * PW; e += 256) {
-      const int i = e / PW, c = e % PW;
-      L11[i * (PW + 1) + c] = Wb[(int64_t)(r0 + i) * N + r0 + c];
+#pragma unroll
+    for (int u = 0; u < PW / 4; ++u) Ub[((tid >> 6) + 4 * u) * 64 + cl] = cl < ncol ? v[u] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < PW * PW / 256; ++u) {
+      const int e = tid + 256 * u;
+      L11[(e / PW) * (PW + 1) + e % PW] = w[u];
     }
   }
   __syncthreads();

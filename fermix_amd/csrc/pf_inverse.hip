@@ -64,12 +64,13 @@ __global__ void pf_prep_kernel(const float* __restrict__ d, int H, int hreal, co
 }
 
 // T[f][c] = L~[f][c] (f > c), 1 on the diagonal, 0 above; identity beyond N.
+// 32-bit index math (Ninv <= 2048).
 __global__ void pf_assemble_kernel(const float* __restrict__ gbuf, int PB, int N, const int* __restrict__ perm,
                                    const float* __restrict__ dinv, float* __restrict__ T, int Ninv) {
   const int64_t b = blockIdx.y;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)Ninv * Ninv) return;
-  const int f = (int)(e / Ninv), c = (int)(e % Ninv);
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= Ninv * Ninv) return;
+  const int f = e / Ninv, c = e - f * Ninv;
   float v;
   if (f == c) {
     v = 1.0f;
@@ -90,9 +91,9 @@ __global__ void pf_assemble_kernel(const float* __restrict__ gbuf, int PB, int N
 __global__ void pf_dy_kernel(const float* __restrict__ T, int Ninv, int N, const float* __restrict__ dinv,
                              float* __restrict__ DY) {
   const int64_t b = blockIdx.y;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)N * N) return;
-  const int r = (int)(e / N), j = (int)(e % N);
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= N * N) return;
+  const int r = e / N, j = e - r * N;
   const int src = r ^ 1;
   const float y = src > j ? T[b * (int64_t)Ninv * Ninv + (int64_t)src * Ninv + j] : (src == j ? 1.0f : 0.0f);
   const float sc = dinv[b * (N / 2) + (r >> 1)];
@@ -112,17 +113,29 @@ __global__ void pf_adj_kernel(const float* __restrict__ R, float* __restrict__ P
   float* Pb = PT + b * (int64_t)N * N;
   const float* Tb = T + b * (int64_t)Ninv * Ninv;
   bool badv = false;
-  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
-    const int f = f0 + e / 64, c = c0 + e % 64;
-    if (f < N && c < N) {
-      const float wf = Rb[(int64_t)f * N + aK], wc = Rb[(int64_t)c * N + aK];
+  // this thread's column c is fixed (64 columns, 4 rows per pass); all reads are in-bounds
+  // (clamped) and issued before use
+  const int cth = c0 + (threadIdx.x & 63), ccl = min(cth, N - 1);
+  const float wc = Rb[ccl * N + aK];
+  const float tcv = Tb[aK * Ninv + ccl];
+  const float v_c = cth < aK ? tcv : (cth == aK ? 1.0f : 0.0f);
+  float rv[16], wv[16], tv[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int f = min(f0 + (threadIdx.x >> 6) + 4 * u, N - 1);
+    rv[u] = Rb[f * N + ccl];
+    wv[u] = Rb[f * N + aK];
+    tv[u] = Tb[aK * Ninv + f];
+  }
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int f = f0 + (threadIdx.x >> 6) + 4 * u;
+    if (f < N && cth < N) {
       // v = Y^T e_aK: v[j] = Y[aK][j] (unit lower: j < aK stored, j == aK one, j > aK zero)
-      const float v_f = f < aK ? Tb[(int64_t)aK * Ninv + f] : (f == aK ? 1.0f : 0.0f);
-      const float v_c = c < aK ? Tb[(int64_t)aK * Ninv + c] : (c == aK ? 1.0f : 0.0f);
-      const float r = Rb[(int64_t)f * N + c];
-      const float val = -(cf.a1 * r + cf.a2 * (wf * v_c - v_f * wc));
+      const float v_f = f < aK ? tv[u] : (f == aK ? 1.0f : 0.0f);
+      const float val = -(cf.a1 * rv[u] + cf.a2 * (wv[u] * v_c - v_f * wc));
       badv = badv || !isfinite(val);
-      Pb[(int64_t)f * N + c] = val;
+      Pb[(int64_t)f * N + cth] = val;
     }
   }
   const int any = __syncthreads_or(badv ? 1 : 0);
@@ -144,9 +157,9 @@ __global__ void pf_reduce_bad_kernel(const int* __restrict__ flags, int ntiles, 
 __global__ void pf_gather_kernel(const float* __restrict__ PT, int N, const int* __restrict__ iperm, int n,
                                  const int* __restrict__ bad, float* __restrict__ out) {
   const int64_t b = blockIdx.y;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)n * n) return;
-  const int i = (int)(e / n), j = (int)(e % n);
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n * n) return;
+  const int i = e / n, j = e - i * n;
   const int* ip = iperm + b * N;
   out[b * (int64_t)n * n + e] = bad[b] ? 0.0f : PT[b * (int64_t)N * N + (int64_t)ip[i] * N + ip[j]];
 }

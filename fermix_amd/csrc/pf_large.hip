@@ -39,11 +39,12 @@ struct PfRowA {
 };
 
 // Copy a (B, n, n) into M (B, N, N): S = (a - a^T)/2 (or a) with [[0,1],[-1,0]] padding.
+// 32-bit index math (N <= 2048).
 __global__ void pf_copy_pad_kernel(const float* __restrict__ A, int n, int skew, float* __restrict__ M, int N) {
   const int64_t b = blockIdx.y;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)N * N) return;
-  const int r = (int)(e / N), c = (int)(e % N);
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= N * N) return;
+  const int r = e / N, c = e - r * N;
   const float* Ab = A + b * (int64_t)n * n;
   float v;
   if (r < n && c < n) {
@@ -342,7 +343,9 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
         }
     }
     __syncthreads();
-    for (int e = tid; e < T * 64; e += 256) {
+#pragma unroll
+    for (int u = 0; u < T * 64 / 256; ++u) {
+      const int e = tid + 256 * u;
       const int cl = e >> 6, rr = e & 63;
       const int p = p0 + 64 * h + rr, q = q0 + cl;
       if (p < N && q < N) Mb[(unsigned)(q * N + p)] = -Ct[cl * LDT + rr];
