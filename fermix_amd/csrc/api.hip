@@ -19,6 +19,32 @@ __global__ void fill_kernel(float* a, float v, int64_t count) {
   if (i < count) a[i] = v;
 }
 
+// Streaming copy: four 16-byte loads in flight per thread (indices clamped so the loads
+// are unconditional; only in-range stores happen).
+__global__ __launch_bounds__(256) void copy4_kernel(const float4* __restrict__ src, float4* __restrict__ dst,
+                                                    int64_t n4) {
+  const int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+  float4 v[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = base + 256 * u;
+    v[u] = src[i < n4 ? i : n4 - 1];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = base + 256 * u;
+    if (i < n4) dst[i] = v[u];
+  }
+}
+
+int launch_copy(const float* src, float* dst, int64_t count, hipStream_t s) {
+  const int64_t n4 = count / 4;
+  if (n4 <= 0) return FX_OK;
+  hipLaunchKernelGGL(copy4_kernel, dim3((unsigned)((n4 + 1023) / 1024)), dim3(256), 0, s,
+                     reinterpret_cast<const float4*>(src), reinterpret_cast<float4*>(dst), n4);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
 // A fill kernel rather than hipMemsetAsync, so the call stays safe under graph capture.
 static int fill(float* a, float v, int64_t count, hipStream_t s) {
   if (count <= 0) return FX_OK;

@@ -6,6 +6,9 @@
 
 namespace fx {
 
+// dst[i] = src[i] for i < count: count a multiple of 4, both pointers 16-byte aligned.
+int launch_copy(const float* src, float* dst, int64_t count, hipStream_t s);
+
 // n <= 128 fused kernels (one workgroup per matrix).
 int lu_small_padded(int n);
 int pf_small_padded(int n);

@@ -76,31 +76,6 @@ __global__ __launch_bounds__(64) void leaf_inverse_kernel(float* __restrict__ T,
   }
 }
 
-// flags[b * ntile + tile] = tile of Z (rows/cols < N) holds a non-finite value
-__global__ void nonfinite_kernel(const float* __restrict__ Z, int Ninv, int N, int* __restrict__ flags) {
-  const int64_t b = blockIdx.y;
-  const int tile = blockIdx.x;
-  const int nt = (N + 63) / 64;
-  const int i0 = (tile / nt) * 64, c0 = (tile % nt) * 64;
-  bool bad = false;
-  const float* Zb = Z + b * (int64_t)Ninv * Ninv;
-  float v[16];
-#pragma unroll
-  for (int u = 0; u < 16; ++u) {  // in-bounds (clamped) reads, all in flight
-    const int e = threadIdx.x + 256 * u;
-    const int i = min(i0 + e / 64, N - 1), c = min(c0 + e % 64, N - 1);
-    v[u] = Zb[i * Ninv + c];
-  }
-#pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int e = threadIdx.x + 256 * u;
-    const int i = i0 + e / 64, c = c0 + e % 64;
-    bad = bad || (i < N && c < N && !isfinite(v[u]));
-  }
-  const int any = __syncthreads_or(bad ? 1 : 0);
-  if (threadIdx.x == 0) flags[b * (nt * nt) + tile] = any;
-}
-
 // bad[b] = any tile flag, or (zero_singular and sign[b] == 0)
 __global__ void reduce_bad_kernel(const int* __restrict__ flags, int ntiles, const float* __restrict__ sign,
                                   int zero_singular, int* __restrict__ bad, int64_t batch) {
@@ -113,16 +88,17 @@ __global__ void reduce_bad_kernel(const int* __restrict__ flags, int ntiles, con
   if (lane == 0) bad[b] = (any || (zero_singular && sign[b] == 0.0f)) ? 1 : 0;
 }
 
-// invT[g0[c]][i] = Z[i][c] for i < n and g0[c] < n, through a 32x32 LDS transpose.
+// invT[g0[c]][i] = Z[i][c] for i < n and g0[c] < n, through a 32x32 LDS transpose; the
+// grid covers the whole N x N block of Z so the same pass flags each 32x32 tile that
+// holds a non-finite value (flags[b][tile], tiles row-major over ceil(N/32)^2).
 __global__ __launch_bounds__(256) void scatter_invT_kernel(const float* __restrict__ Z, int Ninv, int N,
                                                            const int* __restrict__ g0, int n,
-                                                           const int* __restrict__ bad,
+                                                           int* __restrict__ flags,
                                                            float* __restrict__ invT) {
   __shared__ float tile[32 * 33];
   const int64_t b = blockIdx.z;
   const int i0 = 32 * blockIdx.y, c0 = 32 * blockIdx.x;
   const int tid = threadIdx.x;
-  const bool isbad = bad[b] != 0;
   const float* Zb = Z + b * (int64_t)Ninv * Ninv;
   float v[4];
   int gr[4];
@@ -133,12 +109,15 @@ __global__ __launch_bounds__(256) void scatter_invT_kernel(const float* __restri
     v[u] = Zb[i * Ninv + c];
     gr[u] = g0[b * N + min(c0 + (e >> 5), N - 1)];
   }
+  bool nf = false;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int e = tid + 256 * u;
     tile[(e >> 5) * 33 + (e & 31)] = v[u];
+    nf = nf || (i0 + (e >> 5) < N && c0 + (e & 31) < N && !isfinite(v[u]));
   }
-  __syncthreads();
+  const int any = __syncthreads_or(nf ? 1 : 0);
+  if (tid == 0) flags[b * (int64_t)gridDim.x * gridDim.y + blockIdx.y * gridDim.x + blockIdx.x] = any;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int e = tid + 256 * u;
@@ -146,9 +125,18 @@ __global__ __launch_bounds__(256) void scatter_invT_kernel(const float* __restri
     const int i = i0 + ii, c = c0 + cc;
     if (i < n && c < N) {
       const int r = gr[u];
-      if (r < n) invT[b * (int64_t)n * n + (int64_t)r * n + i] = isbad ? 0.0f : tile[ii * 33 + cc];
+      if (r < n) invT[b * (int64_t)n * n + (int64_t)r * n + i] = tile[ii * 33 + cc];
     }
   }
+}
+
+// invT[b] = 0 for the flagged members (one workgroup per member; others exit at once).
+__global__ __launch_bounds__(256) void zero_bad_kernel(const int* __restrict__ bad, float* __restrict__ invT,
+                                                       int64_t nn) {
+  const int64_t b = blockIdx.x;
+  if (!bad[b]) return;
+  float* o = invT + b * nn;
+  for (int64_t e = threadIdx.x; e < nn; e += 256) o[e] = 0.0f;
 }
 
 // In-place inverses of the unit-lower L (strictly lower part) and, with upper, of the
@@ -256,7 +244,7 @@ int inv_padded(int N) {
 
 size_t lu_inverse_workspace(int64_t batch, int N, bool need_copy) {
   const int Ninv = inv_padded(N);
-  const int nt = (N + 63) / 64;
+  const int nt = (N + 31) / 32;
   size_t bytes = 0;
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
   if (need_copy) add((size_t)batch * Ninv * Ninv * 4);  // T
@@ -282,7 +270,7 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
   float* T = need_copy ? (float*)take((size_t)batch * Ninv * Ninv * 4) : LU;
   float* Tmp = (float*)take((size_t)batch * Ninv * Ninv / 4 * 4);
   float* Z = (float*)take((size_t)batch * Ninv * Ninv * 4);
-  const int nt = (N + 63) / 64;
+  const int nt = (N + 31) / 32;  // 32x32 flag tiles
   int* flags = (int*)take((size_t)batch * nt * nt * 4);
   int* bad = (int*)take((size_t)batch * 4);
   const int64_t NN = (int64_t)Ninv * Ninv;
@@ -310,18 +298,19 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
     const int st = launch_gemm(d, batch, 1, s);
     if (st != FX_OK) return st;
   }
-  hipLaunchKernelGGL(nonfinite_kernel, dim3(nt * nt, (unsigned)batch), dim3(256), 0, s, Z, Ninv, N, flags);
-  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  // invT and the non-finite tile flags in one pass over Z, then the flagged members
+  // (and, with zero_singular, those with a zero pivot) are cleared
+  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+    const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
+    hipLaunchKernelGGL(scatter_invT_kernel, dim3(nt, nt, (unsigned)nb), dim3(256), 0, s, Z + b0 * NN, Ninv, N,
+                       g0 + b0 * N, n, flags + b0 * nt * nt, invT + b0 * (int64_t)n * n);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  }
   hipLaunchKernelGGL(reduce_bad_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, flags, nt * nt,
                      sign, zero_singular, bad, batch);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
-    const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
-    hipLaunchKernelGGL(scatter_invT_kernel, dim3((N + 31) / 32, (n + 31) / 32, (unsigned)nb), dim3(256), 0, s,
-                       Z + b0 * NN, Ninv, N, g0 + b0 * N, n, bad + b0, invT + b0 * (int64_t)n * n);
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  }
-  return FX_OK;
+  hipLaunchKernelGGL(zero_bad_kernel, dim3((unsigned)batch), dim3(256), 0, s, bad, invT, (int64_t)n * n);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
 }  // namespace fx

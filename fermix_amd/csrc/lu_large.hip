@@ -515,7 +515,10 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   int* src = (int*)take((size_t)batch * N * 4);
   float* X = (float*)take((size_t)batch * (PW / 16) * 1024);
   int* g0 = parts ? (int*)take((size_t)batch * N * 4) : nullptr;
-  {
+  if (n == N && ((uintptr_t)A & 15) == 0) {  // no padding: a straight streaming copy
+    const int st = launch_copy(A, W, batch * (int64_t)N * N, s);
+    if (st != FX_OK) return st;
+  } else {
     const int64_t tot = (int64_t)N * N;
     hipLaunchKernelGGL(copy_pad_kernel, dim3((unsigned)((tot + 255) / 256), (unsigned)batch), dim3(256),
                        0, s, A, n, W, N);

@@ -63,41 +63,57 @@ __global__ void pf_prep_kernel(const float* __restrict__ d, int H, int hreal, co
   }
 }
 
-// T[f][c] = L~[f][c] (f > c), 1 on the diagonal, 0 above; identity beyond N.
-// 32-bit index math (Ninv <= 2048).
-__global__ void pf_assemble_kernel(const float* __restrict__ gbuf, int PB, int N, const int* __restrict__ perm,
-                                   const float* __restrict__ dinv, float* __restrict__ T, int Ninv) {
+// T[f][c] = L~[f][c] (f > c), 1 on the diagonal, 0 above; identity beyond N. One
+// workgroup per row f (original row o = perm[f]), four columns per thread step: a group
+// of 4 columns lies in one PB-column block of gbuf, read as one 16-byte vector.
+__global__ __launch_bounds__(256) void pf_assemble_kernel(const float* __restrict__ gbuf, int PB, int N,
+                                                          const int* __restrict__ perm,
+                                                          const float* __restrict__ dinv, float* __restrict__ T,
+                                                          int Ninv) {
   const int64_t b = blockIdx.y;
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= Ninv * Ninv) return;
-  const int f = e / Ninv, c = e - f * Ninv;
-  float v;
-  if (f == c) {
-    v = 1.0f;
-  } else if (f < N && c < N && f > (c | 1)) {
-    const int s = c >> 1, k = c / PB, col = c % PB;
-    const int nb = N / PB;
-    const int o = perm[b * N + f];
-    const float* g = gbuf + ((b * nb + k) * (int64_t)N + o) * PB;
-    // column a = 2s holds w / d~ (w in G column 2t+1), column p = 2s+1 holds tau (G column 2t)
-    v = (c & 1) ? g[col - 1] : g[col + 1] * dinv[b * (N / 2) + s];
-  } else {
-    v = 0.0f;
+  const int f = blockIdx.x;
+  float4* row = reinterpret_cast<float4*>(T + b * (int64_t)Ninv * Ninv + (int64_t)f * Ninv);
+  const int nb = N / PB;
+  const int o = f < N ? perm[b * N + f] : 0;
+  const float* db = dinv + b * (N / 2);
+  for (int c4 = threadIdx.x; c4 < Ninv / 4; c4 += 256) {
+    const int c = 4 * c4;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (f < N && c < N && f > c) {
+      const int k = c / PB, col = c % PB;
+      const float4 g = *reinterpret_cast<const float4*>(gbuf + ((b * nb + k) * (int64_t)N + o) * PB + col);
+      const float2 di = *reinterpret_cast<const float2*>(db + (c >> 1));
+      // column a = 2s holds w / d~ (w in G column 2t+1), column p = 2s+1 holds tau (G column 2t)
+      v.x = f > (c | 1) ? g.y * di.x : 0.0f;
+      v.y = f > (c | 1) ? g.x : 0.0f;
+      v.z = f > ((c + 2) | 1) ? g.w * di.y : 0.0f;
+      v.w = f > ((c + 2) | 1) ? g.z : 0.0f;
+    }
+    if (f >= c && f < c + 4) (&v.x)[f - c] = 1.0f;
+    row[c4] = v;
   }
-  T[b * (int64_t)Ninv * Ninv + e] = v;
 }
 
 // DY[2s] = Y[2s+1] / d~_s, DY[2s+1] = -Y[2s] / d~_s with Y the unit-lower part of T.
-__global__ void pf_dy_kernel(const float* __restrict__ T, int Ninv, int N, const float* __restrict__ dinv,
-                             float* __restrict__ DY) {
+// One workgroup per row r, 16-byte vectors along the row.
+__global__ __launch_bounds__(256) void pf_dy_kernel(const float* __restrict__ T, int Ninv, int N,
+                                                    const float* __restrict__ dinv, float* __restrict__ DY) {
   const int64_t b = blockIdx.y;
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= N * N) return;
-  const int r = e / N, j = e - r * N;
-  const int src = r ^ 1;
-  const float y = src > j ? T[b * (int64_t)Ninv * Ninv + (int64_t)src * Ninv + j] : (src == j ? 1.0f : 0.0f);
-  const float sc = dinv[b * (N / 2) + (r >> 1)];
-  DY[b * (int64_t)N * N + e] = (r & 1) ? -y * sc : y * sc;
+  const int r = blockIdx.x, src = r ^ 1;
+  const float4* y4 = reinterpret_cast<const float4*>(T + b * (int64_t)Ninv * Ninv + (int64_t)src * Ninv);
+  float4* o4 = reinterpret_cast<float4*>(DY + b * (int64_t)N * N + (int64_t)r * N);
+  const float d = dinv[b * (N / 2) + (r >> 1)];
+  const float sc = (r & 1) ? -d : d;
+  for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) {
+    const int c = 4 * c4;
+    float4 y = c < src ? y4[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // unit lower: entries with column > src are 0, the diagonal is 1
+    y.x = c < src ? y.x : (c == src ? 1.0f : 0.0f);
+    y.y = c + 1 < src ? y.y : (c + 1 == src ? 1.0f : 0.0f);
+    y.z = c + 2 < src ? y.z : (c + 2 == src ? 1.0f : 0.0f);
+    y.w = c + 3 < src ? y.w : (c + 3 == src ? 1.0f : 0.0f);
+    o4[c4] = make_float4(y.x * sc, y.y * sc, y.z * sc, y.w * sc);
+  }
 }
 
 // PT = -(a1 R + a2 (w v^T - v w^T)); flags non-finite 64x64 tiles.
@@ -153,15 +169,25 @@ __global__ void pf_reduce_bad_kernel(const int* __restrict__ flags, int ntiles, 
   if (lane == 0) bad[b] = (any || coef[b].bad) ? 1 : 0;
 }
 
-// out[i][j] = PT[iperm i][iperm j] for i, j < n (or 0 for a bad member).
-__global__ void pf_gather_kernel(const float* __restrict__ PT, int N, const int* __restrict__ iperm, int n,
-                                 const int* __restrict__ bad, float* __restrict__ out) {
+// out[i][j] = PT[iperm i][iperm j] for i, j < n (or 0 for a bad member). One workgroup
+// per output row: source row iperm[i] is read contiguously into LDS and the column
+// permutation is applied there.
+__global__ __launch_bounds__(256) void pf_gather_kernel(const float* __restrict__ PT, int N,
+                                                        const int* __restrict__ iperm, int n,
+                                                        const int* __restrict__ bad, float* __restrict__ out) {
+  __shared__ __align__(16) float rowb[2048];
   const int64_t b = blockIdx.y;
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n * n) return;
-  const int i = e / n, j = e - i * n;
+  const int i = blockIdx.x;
+  float* o = out + b * (int64_t)n * n + (int64_t)i * n;
+  if (bad[b]) {
+    for (int j = threadIdx.x; j < n; j += 256) o[j] = 0.0f;
+    return;
+  }
   const int* ip = iperm + b * N;
-  out[b * (int64_t)n * n + e] = bad[b] ? 0.0f : PT[b * (int64_t)N * N + (int64_t)ip[i] * N + ip[j]];
+  const float4* s4 = reinterpret_cast<const float4*>(PT + b * (int64_t)N * N + (int64_t)ip[i] * N);
+  for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) reinterpret_cast<float4*>(rowb)[c4] = s4[c4];
+  __syncthreads();
+  for (int j = threadIdx.x; j < n; j += 256) o[j] = rowb[ip[j]];
 }
 
 size_t pf_inverse_workspace(int64_t batch, int N) {
@@ -205,14 +231,13 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
   const unsigned wb = (unsigned)((batch + 3) / 4);
   hipLaunchKernelGGL(pf_prep_kernel, dim3(wb), dim3(256), 0, s, d, N / 2, n / 2, perm, N, dinv, iperm, coef, batch);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  hipLaunchKernelGGL(pf_assemble_kernel, dim3((unsigned)((NN + 255) / 256), (unsigned)batch), dim3(256), 0, s,
-                     gbuf, PB, N, perm, dinv, T, Ninv);
+  hipLaunchKernelGGL(pf_assemble_kernel, dim3((unsigned)Ninv, (unsigned)batch), dim3(256), 0, s, gbuf, PB, N,
+                     perm, dinv, T, Ninv);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   int st = launch_unit_lower_inverse(T, Ninv, batch, Tmp, s);
   if (st != FX_OK) return st;
   const int64_t MM = (int64_t)N * N;
-  hipLaunchKernelGGL(pf_dy_kernel, dim3((unsigned)((MM + 255) / 256), (unsigned)batch), dim3(256), 0, s, T, Ninv, N,
-                     dinv, DY);
+  hipLaunchKernelGGL(pf_dy_kernel, dim3((unsigned)N, (unsigned)batch), dim3(256), 0, s, T, Ninv, N, dinv, DY);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   {
     // R = Y^T DY: op(A) = Y^T (upper, unit diagonal), lower tiles, mirrored skew
@@ -241,9 +266,8 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   hipLaunchKernelGGL(pf_reduce_bad_kernel, dim3(wb), dim3(256), 0, s, flags, nt * nt, coef, bad, batch);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  const int64_t nn = (int64_t)n * n;
-  hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)((nn + 255) / 256), (unsigned)batch), dim3(256), 0, s, PT, N,
-                     iperm, n, bad, out);
+  hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)n, (unsigned)batch), dim3(256), 0, s, PT, N, iperm, n, bad,
+                     out);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 

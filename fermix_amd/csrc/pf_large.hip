@@ -422,9 +422,14 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
   int* orig = fact ? (int*)take((size_t)batch * N * 4) : nullptr;
   float* d = dout ? dout : dbuf;
   const int64_t NN = (int64_t)N * N;
-  hipLaunchKernelGGL(pf_copy_pad_kernel, dim3((unsigned)((NN + 255) / 256), (unsigned)batch), dim3(256), 0, s,
-                     A, n, skew, M0, N);
-  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  if (n == N && !skew && ((uintptr_t)A & 15) == 0) {  // no padding, no symmetrisation
+    const int st = launch_copy(A, M0, batch * NN, s);
+    if (st != FX_OK) return st;
+  } else {
+    hipLaunchKernelGGL(pf_copy_pad_kernel, dim3((unsigned)((NN + 255) / 256), (unsigned)batch), dim3(256), 0, s,
+                       A, n, skew, M0, N);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  }
   if (fact) {
     const int64_t tot = batch * N;
     hipLaunchKernelGGL(pf_iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, orig, N, tot);
