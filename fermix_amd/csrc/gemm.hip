@@ -84,130 +84,143 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
   const int l32 = lane & 31, lh = lane >> 5;
 
-  // global -> register staging of one K stage: A tile BM x GBK, B tile GBK x BN
+  // global -> register staging of one K stage: A tile BM x GBK, B tile GBK x BN. The
+  // loads take clamped (always valid) addresses and nothing reads their data until
+  // store_stage, which runs after the MFMAs of the current stage; out-of-range zeros and
+  // the triangle masks are applied there.
   constexpr int AV = BM * GBK / 1024, BV = BN * GBK / 1024;  // float4 per thread
   constexpr int AE = BM * GBK / 256, BE = BN * GBK / 256;      // floats per thread
   float4 va[VEC ? AV : 1], vb[VEC ? BV : 1];
   float ra[VEC ? 1 : AE], rb[VEC ? 1 : BE];
+  // element coordinates of staging slot e (global row / k / column)
+  auto a_coord = [&](int idx, int k0, int& gi, int& gk) {
+    if (VEC) {
+      if (!d.transA) { gi = i0 + idx / (GBK / 4); gk = k0 + 4 * (idx % (GBK / 4)); }
+      else { gk = k0 + idx / (BM / 4); gi = i0 + 4 * (idx % (BM / 4)); }
+    } else {
+      if (!d.transA) { gi = i0 + idx / GBK; gk = k0 + idx % GBK; }   // row-major A: k fastest
+      else { gk = k0 + idx / BM; gi = i0 + idx % BM; }               // A^T stored: i fastest
+    }
+  };
+  auto b_coord = [&](int idx, int k0, int& gk, int& gj) {
+    if (VEC) {
+      if (!d.transB) { gk = k0 + idx / (BN / 4); gj = j0 + 4 * (idx % (BN / 4)); }
+      else { gj = j0 + idx / (GBK / 4); gk = k0 + 4 * (idx % (GBK / 4)); }
+    } else {
+      if (!d.transB) { gk = k0 + idx / BN; gj = j0 + idx % BN; }     // row-major B: j fastest
+      else { gj = j0 + idx / GBK; gk = k0 + idx % GBK; }             // B^T stored: k fastest
+    }
+  };
+  // the last valid vector / element along each dimension (K and the contiguous
+  // dimension are multiples of 4 on the VEC path)
+  const int lastA_i = d.M - (VEC && d.transA ? 4 : 1), lastA_k = d.K - (VEC && !d.transA ? 4 : 1);
+  const int lastB_j = d.N - (VEC && !d.transB ? 4 : 1), lastB_k = d.K - (VEC && d.transB ? 4 : 1);
   auto load_stage = [&](int k0) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int e = 0; e < AV; ++e) {
+        int gi, gk;
+        a_coord(tid + 256 * e, k0, gi, gk);
+        gi = min(gi, lastA_i);
+        gk = min(gk, lastA_k);
+        va[e] = *reinterpret_cast<const float4*>(d.transA ? A + (int64_t)gk * d.lda + gi
+                                                          : A + (int64_t)gi * d.lda + gk);
+      }
+#pragma unroll
+      for (int e = 0; e < BV; ++e) {
+        int gk, gj;
+        b_coord(tid + 256 * e, k0, gk, gj);
+        gj = min(gj, lastB_j);
+        gk = min(gk, lastB_k);
+        vb[e] = *reinterpret_cast<const float4*>(d.transB ? B + (int64_t)gj * d.ldb + gk
+                                                          : B + (int64_t)gk * d.ldb + gj);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < AE; ++e) {
+        int gi, gk;
+        a_coord(tid + 256 * e, k0, gi, gk);
+        gi = min(gi, lastA_i);
+        gk = min(gk, lastA_k);
+        ra[e] = d.transA ? A[(int64_t)gk * d.lda + gi] : A[(int64_t)gi * d.lda + gk];
+      }
+#pragma unroll
+      for (int e = 0; e < BE; ++e) {
+        int gk, gj;
+        b_coord(tid + 256 * e, k0, gk, gj);
+        gj = min(gj, lastB_j);
+        gk = min(gk, lastB_k);
+        rb[e] = d.transB ? B[(int64_t)gj * d.ldb + gk] : B[(int64_t)gk * d.ldb + gj];
+      }
+    }
+  };
+  // op(A)(gi, gk) after masking (zero outside the matrix)
+  auto fixA = [&](float v, int gi, int gk) {
+    if (gi >= d.M || gk >= d.K) return 0.0f;
+    return d.maskA ? mask_val(v, d.maskA, gi + d.offAr, gk + d.offAc) : v;
+  };
+  auto fixB = [&](float v, int gk, int gj) {
+    if (gj >= d.N || gk >= d.K) return 0.0f;
+    return d.maskB ? mask_val(v, d.maskB, gk + d.offBr, gj + d.offBc) : v;
+  };
+  // registers -> LDS, K-major (As[k][i], Bs[k][j]) so each MFMA operand read is 32
+  // consecutive floats
+  auto store_stage = [&](int buf, int k0) {
     if constexpr (VEC) {
 #pragma unroll
       for (int e = 0; e < AV; ++e) {
         const int idx = tid + 256 * e;
         int gi, gk;
-        if (!d.transA) { gi = i0 + idx / (GBK / 4); gk = k0 + 4 * (idx % (GBK / 4)); }
-        else { gk = k0 + idx / (BM / 4); gi = i0 + 4 * (idx % (BM / 4)); }
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (gi < d.M && gk < d.K)
-          v = *reinterpret_cast<const float4*>(d.transA ? A + (int64_t)gk * d.lda + gi
-                                                        : A + (int64_t)gi * d.lda + gk);
-        if (d.maskA) {
-          const int r = gi + d.offAr, c = gk + d.offAc, dr = d.transA, dc = 1 - d.transA;
-          v.x = mask_val(v.x, d.maskA, r, c);
-          v.y = mask_val(v.y, d.maskA, r + dr, c + dc);
-          v.z = mask_val(v.z, d.maskA, r + 2 * dr, c + 2 * dc);
-          v.w = mask_val(v.w, d.maskA, r + 3 * dr, c + 3 * dc);
+        a_coord(idx, k0, gi, gk);
+        const int dr = d.transA, dc = 1 - d.transA;  // step of the vector's components
+        float4 v = va[e];
+        v.x = fixA(v.x, gi, gk);
+        v.y = fixA(v.y, gi + dr, gk + dc);
+        v.z = fixA(v.z, gi + 2 * dr, gk + 2 * dc);
+        v.w = fixA(v.w, gi + 3 * dr, gk + 3 * dc);
+        const int i = gi - i0, k = gk - k0;
+        if (!d.transA) {
+          As[buf][k * LDSA + i] = v.x;
+          As[buf][(k + 1) * LDSA + i] = v.y;
+          As[buf][(k + 2) * LDSA + i] = v.z;
+          As[buf][(k + 3) * LDSA + i] = v.w;
+        } else {
+          *reinterpret_cast<float4*>(&As[buf][k * LDSA + i]) = v;
         }
-        va[e] = v;
       }
 #pragma unroll
       for (int e = 0; e < BV; ++e) {
         const int idx = tid + 256 * e;
         int gk, gj;
-        if (!d.transB) { gk = k0 + idx / (BN / 4); gj = j0 + 4 * (idx % (BN / 4)); }
-        else { gj = j0 + idx / (GBK / 4); gk = k0 + 4 * (idx % (GBK / 4)); }
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (gj < d.N && gk < d.K)
-          v = *reinterpret_cast<const float4*>(d.transB ? B + (int64_t)gj * d.ldb + gk
-                                                        : B + (int64_t)gk * d.ldb + gj);
-        if (d.maskB) {
-          const int r = gk + d.offBr, c = gj + d.offBc, dr = d.transB, dc = 1 - d.transB;
-          v.x = mask_val(v.x, d.maskB, r, c);
-          v.y = mask_val(v.y, d.maskB, r + dr, c + dc);
-          v.z = mask_val(v.z, d.maskB, r + 2 * dr, c + 2 * dc);
-          v.w = mask_val(v.w, d.maskB, r + 3 * dr, c + 3 * dc);
-        }
-        vb[e] = v;
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < AE; ++e) {
-        const int idx = tid + 256 * e;
-        int i, k;
-        if (!d.transA) { i = idx / GBK; k = idx % GBK; }   // row-major A: k fastest
-        else { k = idx / BM; i = idx % BM; }               // A^T stored: i fastest
-        const int gi = i0 + i, gk = k0 + k;
-        float v = 0.0f;
-        if (gi < d.M && gk < d.K) {
-          v = d.transA ? A[(int64_t)gk * d.lda + gi] : A[(int64_t)gi * d.lda + gk];
-          if (d.maskA) v = mask_val(v, d.maskA, gi + d.offAr, gk + d.offAc);
-        }
-        ra[e] = v;
-      }
-#pragma unroll
-      for (int e = 0; e < BE; ++e) {
-        const int idx = tid + 256 * e;
-        int k, j;
-        if (!d.transB) { k = idx / BN; j = idx % BN; }     // row-major B: j fastest
-        else { j = idx / GBK; k = idx % GBK; }             // B^T stored: k fastest
-        const int gk = k0 + k, gj = j0 + j;
-        float v = 0.0f;
-        if (gj < d.N && gk < d.K) {
-          v = d.transB ? B[(int64_t)gj * d.ldb + gk] : B[(int64_t)gk * d.ldb + gj];
-          if (d.maskB) v = mask_val(v, d.maskB, gk + d.offBr, gj + d.offBc);
-        }
-        rb[e] = v;
-      }
-    }
-  };
-  // registers -> LDS, K-major (As[k][i], Bs[k][j]) so each MFMA operand read is 32
-  // consecutive floats
-  auto store_stage = [&](int buf) {
-    if constexpr (VEC) {
-#pragma unroll
-      for (int e = 0; e < AV; ++e) {
-        const int idx = tid + 256 * e;
-        if (!d.transA) {
-          const int i = idx / (GBK / 4), k = 4 * (idx % (GBK / 4));
-          As[buf][k * LDSA + i] = va[e].x;
-          As[buf][(k + 1) * LDSA + i] = va[e].y;
-          As[buf][(k + 2) * LDSA + i] = va[e].z;
-          As[buf][(k + 3) * LDSA + i] = va[e].w;
-        } else {
-          const int k = idx / (BM / 4), i = 4 * (idx % (BM / 4));
-          *reinterpret_cast<float4*>(&As[buf][k * LDSA + i]) = va[e];
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < BV; ++e) {
-        const int idx = tid + 256 * e;
+        b_coord(idx, k0, gk, gj);
+        const int dk = d.transB, dj = 1 - d.transB;
+        float4 v = vb[e];
+        v.x = fixB(v.x, gk, gj);
+        v.y = fixB(v.y, gk + dk, gj + dj);
+        v.z = fixB(v.z, gk + 2 * dk, gj + 2 * dj);
+        v.w = fixB(v.w, gk + 3 * dk, gj + 3 * dj);
+        const int k = gk - k0, j = gj - j0;
         if (!d.transB) {
-          const int k = idx / (BN / 4), j = 4 * (idx % (BN / 4));
-          *reinterpret_cast<float4*>(&Bs[buf][k * LDSB + j]) = vb[e];
+          *reinterpret_cast<float4*>(&Bs[buf][k * LDSB + j]) = v;
         } else {
-          const int j = idx / (GBK / 4), k = 4 * (idx % (GBK / 4));
-          Bs[buf][k * LDSB + j] = vb[e].x;
-          Bs[buf][(k + 1) * LDSB + j] = vb[e].y;
-          Bs[buf][(k + 2) * LDSB + j] = vb[e].z;
-          Bs[buf][(k + 3) * LDSB + j] = vb[e].w;
+          Bs[buf][k * LDSB + j] = v.x;
+          Bs[buf][(k + 1) * LDSB + j] = v.y;
+          Bs[buf][(k + 2) * LDSB + j] = v.z;
+          Bs[buf][(k + 3) * LDSB + j] = v.w;
         }
       }
     } else {
 #pragma unroll
       for (int e = 0; e < AE; ++e) {
-        const int idx = tid + 256 * e;
-        int i, k;
-        if (!d.transA) { i = idx / GBK; k = idx % GBK; }
-        else { k = idx / BM; i = idx % BM; }
-        As[buf][k * LDSA + i] = ra[e];
+        int gi, gk;
+        a_coord(tid + 256 * e, k0, gi, gk);
+        As[buf][(gk - k0) * LDSA + (gi - i0)] = fixA(ra[e], gi, gk);
       }
 #pragma unroll
       for (int e = 0; e < BE; ++e) {
-        const int idx = tid + 256 * e;
-        int k, j;
-        if (!d.transB) { k = idx / BN; j = idx % BN; }
-        else { j = idx / GBK; k = idx % GBK; }
-        Bs[buf][k * LDSB + j] = rb[e];
+        int gk, gj;
+        b_coord(tid + 256 * e, k0, gk, gj);
+        Bs[buf][(gk - k0) * LDSB + (gj - j0)] = fixB(rb[e], gk, gj);
       }
     }
   };
@@ -223,7 +236,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
 
   int buf = 0;
   if (klo < khi) {
-    store_stage(0);
+    store_stage(0, klo);
     __syncthreads();
     for (int k0 = klo; k0 < khi; k0 += GBK) {
       const bool more = k0 + GBK < khi;
@@ -242,7 +255,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
             acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
       }
       if (more) {
-        store_stage(buf ^ 1);
+        store_stage(buf ^ 1, k0 + GBK);
         __syncthreads();
         buf ^= 1;
       }
