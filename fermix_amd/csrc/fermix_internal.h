@@ -72,6 +72,7 @@ struct GemmDesc {
   int offAr, offAc, offBr, offBc;
   int lower_only;  // only tiles on/below the diagonal; C[j][i] = mirror * C[i][j]
   float mirror;
+  int xcd8;  // set by launch_gemm: the batch is a multiple of 8 (XCD-aware tile order)
 };
 
 // C = alpha op(A) op(B) + beta C for every (batch, second-batch) index.

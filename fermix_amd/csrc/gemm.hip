@@ -51,20 +51,31 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   __shared__ __align__(16) float Bs[2][GBK * LDSB];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int64_t bat = blockIdx.y, bat2 = blockIdx.z;
+  int64_t bat = blockIdx.y;
+  const int64_t bat2 = blockIdx.z;
+  int tx = blockIdx.x;
+  if (d.xcd8) {
+    // Workgroups are handed to the 8 XCDs round-robin by linear id, each XCD with its own
+    // L2: renumber so that all tiles of one matrix run on one XCD and every XCD gets the
+    // same mix of (triangle-trimmed, unequal) tiles.
+    const int64_t lin = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    const int64_t slot = lin >> 3;
+    tx = (int)(slot % gridDim.x);
+    bat = (slot / gridDim.x) * 8 + (lin & 7);
+  }
   int ti, tj;
   const int ntn = (d.N + BN - 1) / BN;
   if (d.lower_only) {
     // blockIdx.x enumerates the lower triangle of tiles row-major
-    const int t = blockIdx.x;
+    const int t = tx;
     int I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
     while ((I + 1) * (I + 2) / 2 <= t) ++I;
     while (I * (I + 1) / 2 > t) --I;
     ti = I;
     tj = t - I * (I + 1) / 2;
   } else {
-    ti = blockIdx.x / ntn;
-    tj = blockIdx.x % ntn;
+    ti = tx / ntn;
+    tj = tx % ntn;
   }
   const int i0 = ti * BM, j0 = tj * BN;
   const float* A = d.A + bat * d.sA + bat2 * d.sA2;
@@ -309,6 +320,9 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
     const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
     GemmDesc e = d;
+    // XCD-aware tile order where tiles differ in length (triangle-trimmed K ranges): it
+    // balances the XCDs there, while uniform tiles run faster in launch order
+    e.xcd8 = nb % 8 == 0 && (d.maskA || d.maskB || d.lower_only);
     e.A += b0 * d.sA;
     e.B += b0 * d.sB;
     e.C += b0 * d.sC;
