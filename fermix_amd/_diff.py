@@ -7,7 +7,12 @@ fold into the kernels' batch, so vmap(f)(x) runs exactly the arithmetic of f(x))
   requested, one parts call returns the primal and A^-T from a single factorisation;
   its (sign, logabs) are bit-identical to the plain forward (same kernel arithmetic).
 * slogpf: d logabs = -1/2 sum(S^-1 * dS) (_diff.py:129-156).
-* det / pf: value sign * exp(logabs); gradient det * A^-T (regular members).
+* det: d det = sum(adj(A)^T * dA) (_diff.py:270-302), with adj(A)^T from the same LU
+  as the primal -- det(factors) * A^-T, or its rank-1 continuation for exact zero
+  pivots -- so the gradient is finite and exact for singular A.
+* pf: d pf = sum(G * dS), G = -pf(S) S^-1 / 2 (_diff.py:305-333), with the Pfaffian
+  adjugate pf(S) S^-1 from the forward's own Parlett-Reid factors (finite for singular
+  S); G is skew, so it is also the gradient w.r.t. ``a`` through S = (a - a^T)/2.
 """
 
 import torch
@@ -186,11 +191,89 @@ def slogpf(A, skew):
 # ----------------------------------------------------------------- det / pf
 
 
+class _DetParts(torch.autograd.Function):
+    """(det, adjT) from one factorisation; d det = sum(adjT * dA)."""
+
+    @staticmethod
+    def forward(A):
+        sign, logabs, adjT = _kernels.det_parts(A)
+        return sign * torch.exp(logabs), adjT
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        _, adjT = output
+        ctx.mark_non_differentiable(adjT)
+        ctx.save_for_backward(adjT)
+        ctx.save_for_forward(adjT)
+
+    @staticmethod
+    def backward(ctx, g_det, g_adj):
+        (adjT,) = ctx.saved_tensors
+        if g_det is None:
+            return None
+        return g_det[:, None, None] * adjT
+
+    @staticmethod
+    def jvp(ctx, dA):
+        (adjT,) = ctx.saved_tensors
+        return (adjT * dA).sum(dim=(-1, -2)), None
+
+    @staticmethod
+    def vmap(info, in_dims, A):
+        A2, vb = _fold(info, in_dims, A)
+        d, adj = _DetParts.apply(A2)
+        if vb is None:
+            return (d, adj), (None, None)
+        return (_unfold(d, vb), _unfold(adj, vb)), (0, 0)
+
+
 def det(A):
-    s, l = slogdet(A)
+    if _wants_grad(A):
+        d, _ = _DetParts.apply(A)
+        return d
+    s, l = _SlogdetFwd.apply(A)
     return s * torch.exp(l)
 
 
+class _PfParts(torch.autograd.Function):
+    """(pf, G) with G = -pf(S) S^-1 / 2 from one Parlett-Reid run; d pf = sum(G * dS)."""
+
+    @staticmethod
+    def forward(A, skew):
+        sign, logabs, adj = _kernels.slogpf_parts(A, skew, adjugate=True)
+        return sign * torch.exp(logabs), -0.5 * adj
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        _, G = output
+        ctx.mark_non_differentiable(G)
+        ctx.save_for_backward(G)
+        ctx.save_for_forward(G)
+
+    @staticmethod
+    def backward(ctx, g_pf, g_G):
+        (G,) = ctx.saved_tensors
+        if g_pf is None:
+            return None, None
+        return g_pf[:, None, None] * G, None
+
+    @staticmethod
+    def jvp(ctx, dA, _skew):
+        (G,) = ctx.saved_tensors
+        return (G * dA).sum(dim=(-1, -2)), None
+
+    @staticmethod
+    def vmap(info, in_dims, A, skew):
+        A2, vb = _fold(info, in_dims[:1], A)
+        p, G = _PfParts.apply(A2, skew)
+        if vb is None:
+            return (p, G), (None, None)
+        return (_unfold(p, vb), _unfold(G, vb)), (0, 0)
+
+
 def pf(A, skew):
-    s, l = slogpf(A, skew)
+    if _wants_grad(A):
+        p, _ = _PfParts.apply(A, skew)
+        return p
+    s, l = _SlogpfFwd.apply(A, skew)
     return s * torch.exp(l)

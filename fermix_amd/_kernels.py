@@ -77,6 +77,23 @@ def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False):
     return sign, logabs, invT, lu, perm
 
 
+def det_parts(A):
+    """(sign, logabs, adjT) with adjT = adj(A)^T = d det / dA from one factorisation."""
+    _check_input(A)
+    B, n, _ = A.shape
+    dev = A.device
+    sign = torch.empty(B, dtype=A.dtype, device=dev)
+    logabs = torch.empty(B, dtype=A.dtype, device=dev)
+    adjT = torch.empty_like(A)
+    L = lib()
+    ws, wsb = _workspace(L.fx_det_parts_f32_workspace(B, n), dev)
+    st = L.fx_det_parts_f32(
+        _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(adjT), _ptr(ws), wsb, _stream(A)
+    )
+    check(st, "fx_det_parts_f32")
+    return sign, logabs, adjT
+
+
 def slogpf(A, skew_symmetrize):
     _check_input(A)
     B, n, _ = A.shape
@@ -114,8 +131,9 @@ def slogpf_factors(A, skew_symmetrize):
     return sign, logabs, gbuf, d, perm
 
 
-def slogpf_parts(A, skew_symmetrize):
-    """(sign, logabs, Sinv) of the (skew-symmetrised) batch from one Parlett-Reid run."""
+def slogpf_parts(A, skew_symmetrize, adjugate=False):
+    """(sign, logabs, G) of the (skew-symmetrised) batch from one Parlett-Reid run, G = S^-1
+    or, with adjugate, pf(S) S^-1."""
     _check_input(A)
     B, n, _ = A.shape
     dev = A.device
@@ -125,7 +143,7 @@ def slogpf_parts(A, skew_symmetrize):
     g = torch.empty_like(A)
     ws, wsb = _workspace(L.fx_slogpf_parts_f32_workspace(B, n), dev)
     st = L.fx_slogpf_parts_f32(
-        _ptr(A), B, n, int(bool(skew_symmetrize)), 0, _ptr(sign), _ptr(logabs), _ptr(g),
+        _ptr(A), B, n, int(bool(skew_symmetrize)), int(bool(adjugate)), _ptr(sign), _ptr(logabs), _ptr(g),
         _ptr(ws), wsb, _stream(A),
     )
     check(st, "fx_slogpf_parts_f32")

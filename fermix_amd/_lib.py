@@ -27,6 +27,8 @@ SIGNATURES = {
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _sz, _p],
     ),
+    "fx_det_parts_f32_workspace": (_sz, [_i64, _i32]),
+    "fx_det_parts_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _sz, _p]),
     "fx_slogpf_f32_workspace": (_sz, [_i64, _i32]),
     "fx_slogpf_f32": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _sz, _p]),
     "fx_pf_block_columns": (_i32, [_i32]),

@@ -13,8 +13,10 @@ Conventions kept from the reference:
 * differentiable (torch.autograd, forward mode, torch.func.vmap / grad / jvp) with the
   reference's rules (_diff.py:101-333): d logabs = tr(A^-1 dA), d sign = 0; slogpf
   d logabs = tr(S^-1 dS)/2 (gradient w.r.t. ``a`` S^-T/2 through the
-  skew-symmetrisation); exactly singular inputs get a zero (finite) gradient; the
-  primal of a differentiated call is bit-identical to the plain forward.
+  skew-symmetrisation); exactly singular inputs get a zero (finite) slogdet / slogpf
+  gradient; det and pf differentiate through the adjugates, d det = tr(adj(A) dA) and
+  d pf = tr(pf(S) S^-1 dS)/2, finite and exact for singular inputs; the primal of a
+  differentiated call is bit-identical to the plain forward.
 
 Device handling: the product path is the HIP library on a ROCm GPU. A CPU tensor
 raises ``FermixDeviceError`` (the reference's generic XLA fallback is not part of this

@@ -80,7 +80,7 @@ const char* fx_status_string(int status) {
   }
 }
 
-int fx_abi_version(void) { return 100; }
+int fx_abi_version(void) { return 101; }
 
 int32_t fx_lu_padded_size(int32_t n) {
   if (n <= 0) return 0;
@@ -171,6 +171,50 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
   return launch_lu_inverse(LU, g0, N, n, batch, sign, zero_singular, inv_t, true, p, rest, s);
 }
 
+size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n) {
+  if (batch <= 0 || n <= 0 || n > LARGE_MAX) return 0;
+  return fx_slogdet_parts_f32_workspace(batch, n) + align256(det_adjugate_workspace(batch, n));
+}
+
+int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
+                     void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (batch == 0) return FX_OK;
+  if (!sign || !logabs || (n > 0 && (!a || !adj_t))) return FX_ERR_INVALID_ARGUMENT;
+  hipStream_t s = (hipStream_t)stream;
+  if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
+  if (n > LARGE_MAX) return FX_ERR_UNSUPPORTED;
+  const size_t need = fx_det_parts_f32_workspace(batch, n);
+  if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
+  const int N = fx_lu_padded_size(n);
+  char* p = (char*)workspace;
+  float* LU = nullptr;
+  int* g0 = nullptr;
+  int st;
+  if (n <= SMALL_MAX) {
+    LU = (float*)p;
+    p += align256((size_t)batch * N * N * 4);
+    g0 = (int*)p;
+    p += align256((size_t)batch * N * 4);
+    st = launch_lu_small(a, n, batch, sign, logabs, LU, g0, s);
+  } else {
+    const size_t wl = lu_large_workspace(batch, n, true);
+    st = launch_lu_large(a, n, batch, sign, logabs, p, wl, true, &LU, &g0, s);
+    p += align256(wl);
+  }
+  if (st != FX_OK) return st;
+  // the adjugate's scalars and vectors come from the LU before the inverse overwrites it
+  void* dws = p;
+  p += align256(det_adjugate_workspace(batch, n));
+  float* scale = nullptr;
+  st = launch_det_adjugate_prep(LU, g0, N, n, batch, dws, &scale, s);
+  if (st != FX_OK) return st;
+  const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
+  st = launch_lu_inverse(LU, g0, N, n, batch, sign, 0, adj_t, true, p, rest, s, scale);
+  if (st != FX_OK) return st;
+  return launch_det_adjugate_finish(n, batch, dws, adj_t, s);
+}
+
 size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || n <= SMALL_MAX || n > PF_LARGE_MAX || n % 2) return 0;
   return pf_large_workspace(batch, n, false);
@@ -226,7 +270,6 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || !g || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
-  if (adjugate) return FX_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   if (n % 2 == 1) {
@@ -256,7 +299,8 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
   }
   if (st != FX_OK) return st;
   const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
-  return launch_pf_inverse(gbuf, n <= SMALL_MAX ? 16 : 32, d, perm, N, n, batch, g, p, rest, s);
+  return launch_pf_inverse(gbuf, n <= SMALL_MAX ? 16 : 32, d, perm, N, n, batch, adjugate ? 1 : 0, g, p, rest,
+                           s);
 }
 
 }  // extern "C"

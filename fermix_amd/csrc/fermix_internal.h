@@ -33,9 +33,11 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
 // overwritten when in_place and N is a power-of-two multiple of 32 (inverse.hip).
 int inv_padded(int N);
 size_t lu_inverse_workspace(int64_t batch, int N, bool need_copy);
+// With scale != nullptr every member's invT is multiplied by scale[b] (the non-finite
+// check applies to the unscaled values).
 int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, const float* sign,
                       int zero_singular, float* invT, bool in_place, void* ws, size_t ws_bytes,
-                      hipStream_t s);
+                      hipStream_t s, const float* scale = nullptr);
 
 // 128 < n <= 2048 Parlett-Reid (pf_large.hip); with gbuf the factors (B, N/32, N, 32) by
 // original row, d (B, N/2) and perm (B, N).
@@ -44,14 +46,29 @@ size_t pf_large_workspace(int64_t batch, int n, bool fact);
 int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
                     float* gbuf, float* dout, int* perm, void* ws, size_t ws_bytes, hipStream_t s);
 
-// In-place unit-lower (and upper) triangular inverses of a packed (B, Ninv, Ninv) buffer.
-int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper, hipStream_t s);
-int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hipStream_t s);
+// In-place unit-lower (and upper) triangular inverses of a packed (B, Ninv, Ninv) buffer;
+// with active != nullptr only the members with active[b] != 0 are processed.
+int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper, hipStream_t s,
+                       const int* active = nullptr);
+int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hipStream_t s,
+                              const int* active = nullptr);
 
-// S^-1 (B, n, n) from the Parlett-Reid factors (gbuf with PB columns per block, d, perm).
+// S^-1 (adjugate = 0) or pf(S) S^-1 (adjugate != 0) as (B, n, n) from the Parlett-Reid
+// factors (gbuf with PB columns per block, d, perm).
 size_t pf_inverse_workspace(int64_t batch, int N);
 int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm, int N, int n, int64_t batch,
-                      float* out, void* ws, size_t ws_bytes, hipStream_t s);
+                      int adjugate, float* out, void* ws, size_t ws_bytes, hipStream_t s);
+
+// parity[b] = parity (0 even, 1 odd) of the permutation perm[b] of 0..N-1, N <= 2048.
+int launch_perm_parity(const int* perm, int N, int64_t batch, int* parity, hipStream_t s);
+
+// det adjugate (adjugate.hip): prep reads the packed LU (before the in-place inverse
+// overwrites it) and returns the per-member scale of the inverse's scatter; finish
+// turns the members with one or two zero pivots into their rank-1 adjugate.
+size_t det_adjugate_workspace(int64_t batch, int n);
+int launch_det_adjugate_prep(const float* LU, const int* g0, int N, int n, int64_t batch, void* ws,
+                             float** scale_out, hipStream_t s);
+int launch_det_adjugate_finish(int n, int64_t batch, void* ws, float* G, hipStream_t s);
 
 // ------------------------------------------------------------------ batched GEMM
 // Masks apply to op(X) in global coordinates (row + off*r, col + off*c): elements
@@ -73,6 +90,7 @@ struct GemmDesc {
   int lower_only;  // only tiles on/below the diagonal; C[j][i] = mirror * C[i][j]
   float mirror;
   int xcd8;  // set by launch_gemm: the batch is a multiple of 8 (XCD-aware tile order)
+  const int* active;  // optional (batch,) mask: members with active[b] == 0 are skipped
 };
 
 // C = alpha op(A) op(B) + beta C for every (batch, second-batch) index.

@@ -63,6 +63,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
     tx = (int)(slot % gridDim.x);
     bat = (slot / gridDim.x) * 8 + (lin & 7);
   }
+  // members switched off by the caller's mask (uniform per workgroup, before any barrier)
+  if (d.active && !d.active[bat]) return;
   int ti, tj;
   const int ntn = (d.N + BN - 1) / BN;
   if (d.lower_only) {
@@ -326,6 +328,7 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
     e.A += b0 * d.sA;
     e.B += b0 * d.sB;
     e.C += b0 * d.sC;
+    if (d.active) e.active += b0;
     const dim3 grid(tiles, (unsigned)nb, nb2);
     if (big && vec) hipLaunchKernelGGL((gemm_kernel<128, 128, true>), grid, dim3(256), 0, s, e);
     else if (big) hipLaunchKernelGGL((gemm_kernel<128, 128, false>), grid, dim3(256), 0, s, e);

@@ -31,9 +31,11 @@ __global__ void embed_kernel(const float* __restrict__ src, int N, float* __rest
 // In-place inverse of the 32x32 diagonal block t of the packed T: lane c (< 32) forms
 // column c of L^-1 by forward substitution, lane 32 + c column c of U~^-1 by back
 // substitution.
-__global__ __launch_bounds__(64) void leaf_inverse_kernel(float* __restrict__ T, int Ninv) {
+__global__ __launch_bounds__(64) void leaf_inverse_kernel(float* __restrict__ T, int Ninv,
+                                                          const int* __restrict__ active) {
   __shared__ float Bk[32 * 33];
   const int64_t b = blockIdx.y;
+  if (active && !active[b]) return;
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   float* base = T + b * (int64_t)Ninv * Ninv + (int64_t)(32 * t) * Ninv + 32 * t;
@@ -94,7 +96,8 @@ __global__ void reduce_bad_kernel(const int* __restrict__ flags, int ntiles, con
 __global__ __launch_bounds__(256) void scatter_invT_kernel(const float* __restrict__ Z, int Ninv, int N,
                                                            const int* __restrict__ g0, int n,
                                                            int* __restrict__ flags,
-                                                           float* __restrict__ invT) {
+                                                           float* __restrict__ invT,
+                                                           const float* __restrict__ scale) {
   __shared__ float tile[32 * 33];
   const int64_t b = blockIdx.z;
   const int i0 = 32 * blockIdx.y, c0 = 32 * blockIdx.x;
@@ -118,6 +121,7 @@ __global__ __launch_bounds__(256) void scatter_invT_kernel(const float* __restri
   }
   const int any = __syncthreads_or(nf ? 1 : 0);
   if (tid == 0) flags[b * (int64_t)gridDim.x * gridDim.y + blockIdx.y * gridDim.x + blockIdx.x] = any;
+  const float sc = scale ? scale[b] : 1.0f;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int e = tid + 256 * u;
@@ -125,7 +129,7 @@ __global__ __launch_bounds__(256) void scatter_invT_kernel(const float* __restri
     const int i = i0 + ii, c = c0 + cc;
     if (i < n && c < N) {
       const int r = gr[u];
-      if (r < n) invT[b * (int64_t)n * n + (int64_t)r * n + i] = tile[ii * 33 + cc];
+      if (r < n) invT[b * (int64_t)n * n + (int64_t)r * n + i] = sc * tile[ii * 33 + cc];
     }
   }
 }
@@ -142,14 +146,16 @@ __global__ __launch_bounds__(256) void zero_bad_kernel(const int* __restrict__ b
 // In-place inverses of the unit-lower L (strictly lower part) and, with upper, of the
 // upper U~ (upper part incl. diagonal) packed in T (B, Ninv, Ninv); Tmp holds
 // B * Ninv^2 / 4 floats.
-int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper, hipStream_t s) {
+int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper, hipStream_t s,
+                       const int* active) {
   const int64_t NN = (int64_t)Ninv * Ninv;
-  hipLaunchKernelGGL(leaf_inverse_kernel, dim3(Ninv / 32, (unsigned)batch), dim3(64), 0, s, T, Ninv);
+  hipLaunchKernelGGL(leaf_inverse_kernel, dim3(Ninv / 32, (unsigned)batch), dim3(64), 0, s, T, Ninv, active);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   for (int sz = 32; sz < Ninv; sz *= 2) {
     const int pairs = Ninv / (2 * sz);
     const int64_t dstride = (int64_t)2 * sz * (Ninv + 1);  // next pair along the diagonal
     GemmDesc d = {};
+    d.active = active;
     d.M = d.N = d.K = sz;
     d.sA = d.sB = NN;
     d.sC = NN;
@@ -169,6 +175,7 @@ int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper
     if (st != FX_OK) return st;
     // X21 = -X22 * Tmp
     GemmDesc e = {};
+    e.active = active;
     e.M = e.N = e.K = sz;
     e.A = T + (int64_t)sz * Ninv + sz;
     e.maskA = MASK_LOWER_UNIT;
@@ -190,6 +197,7 @@ int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper
     if (!upper) continue;
     // U: Tmp = U12 * Y22
     GemmDesc f = {};
+    f.active = active;
     f.M = f.N = f.K = sz;
     f.A = T + sz;
     f.lda = Ninv;
@@ -210,6 +218,7 @@ int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper
     if (st != FX_OK) return st;
     // Y12 = -Y11 * Tmp
     GemmDesc h = {};
+    h.active = active;
     h.M = h.N = h.K = sz;
     h.A = T;
     h.maskA = MASK_UPPER;
@@ -232,8 +241,9 @@ int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper
   return FX_OK;
 }
 
-int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hipStream_t s) {
-  return launch_tri_inverse(T, Ninv, batch, Tmp, false, s);
+int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hipStream_t s,
+                              const int* active) {
+  return launch_tri_inverse(T, Ninv, batch, Tmp, false, s, active);
 }
 
 int inv_padded(int N) {
@@ -257,7 +267,7 @@ size_t lu_inverse_workspace(int64_t batch, int N, bool need_copy) {
 
 int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, const float* sign,
                       int zero_singular, float* invT, bool in_place, void* ws, size_t ws_bytes,
-                      hipStream_t s) {
+                      hipStream_t s, const float* scale) {
   const int Ninv = inv_padded(N);
   const bool need_copy = !(in_place && Ninv == N);
   if (!ws || ws_bytes < lu_inverse_workspace(batch, N, need_copy)) return FX_ERR_WORKSPACE;
@@ -303,7 +313,8 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
     const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
     hipLaunchKernelGGL(scatter_invT_kernel, dim3(nt, nt, (unsigned)nb), dim3(256), 0, s, Z + b0 * NN, Ninv, N,
-                       g0 + b0 * N, n, flags + b0 * nt * nt, invT + b0 * (int64_t)n * n);
+                       g0 + b0 * N, n, flags + b0 * nt * nt, invT + b0 * (int64_t)n * n,
+                       scale ? scale + b0 : nullptr);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   hipLaunchKernelGGL(reduce_bad_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, flags, nt * nt,

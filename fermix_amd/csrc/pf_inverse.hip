@@ -1,10 +1,14 @@
-// S^-1 from the forward's own Parlett-Reid factors (the slogpf backward), any N. With
-// P S' P^T = L D L^T, D = diag_s(d_s J), the pivot K of smallest |d| and d~ = d with d_K
-// and exact zeros replaced by 1:
+// S^-1 (inverse mode) or pf(S) S^-1 (adjugate mode) from the forward's own Parlett-Reid
+// factors (the slogpf / pf backward), any N. With P S' P^T = L D L^T, D = diag_s(d_s J),
+// the pivot K of smallest |d| and d~ = d with d_K and exact zeros replaced by 1:
 //   L~ = L with the a-columns scaled by 1/d~ (unit lower), Y = L~^-1,
 //   DY = rows (Y[p_s], -Y[a_s]) / d~_s,   R = Y^T DY (exactly skew),
-//   S^-1 = -P^T [R + c (w v^T - v w^T)] P,  w = R e_{a_K}, v = Y^T e_{a_K},
-//   c = (1 - d_K) / d_K (0 for d_K = 0), zeroed for d_K = 0 or a non-finite result.
+//   G = -P^T [a1 R + a2 (w v^T - v w^T)] P,  w = R e_{a_K}, v = Y^T e_{a_K},
+// inverse:   (a1, a2) = (1, (1 - d_K) / d_K), zeroed for d_K = 0 or a non-finite result;
+// adjugate:  (a1, a2) = sgn(P) D_K (d_K, 1 - d_K), D_K = prod_{s != K} d_s -- finite and
+//            exact for singular S (d_K enters linearly). A second exact zero pivot z is
+//            lifted: G is affine in that pair entry, so G = (G(d_z = +1) + G(d_z = -1)) / 2,
+//            the second evaluation running only for the members that have such a pivot.
 // Kernels: pivot / coefficient prep (one wave per matrix), L~ assembly, the triangular
 // inverse of inverse.hip (lower half only), DY, the skew GEMM R (lower tiles + mirror),
 // the rank-2 correction with the non-finite flags, and the permutation gather.
@@ -12,7 +16,7 @@
 // Reference roles replaced (ChenAo-Phys/fermix): _pf_parts (src/fermix/_pfinv.py:196-269)
 // with _pf_assemble_kernel (:80-137), _pf_maps (:140-157), the skew _bgemm for R and
 // _adj_perm_kernel (:161-192); the scalar helpers _pivot_index / _pair_scale /
-// _pf_adj_coeffs (src/fermix/_fallback.py:101-176).
+// _pf_adj_coeffs / _second_zero / _lifted_mean (src/fermix/_fallback.py:101-176).
 #include "common.h"
 #include "fermix_internal.h"
 
@@ -23,11 +27,15 @@ struct PfCoef {
   int bad;    // d_K == 0 (inverse mode: zero the result)
   float a1;   // coefficient of R
   float a2;   // coefficient of (w v^T - v w^T)
+  int z;      // adjugate mode: first exact zero pivot other than K (lifted), or -1
 };
 
-// One wave per matrix: K, 1/d~, coefficients, and the inverse permutation.
+// One wave per matrix: K, 1/d~, coefficients, and the inverse permutation. In adjugate
+// mode parity[b] is the permutation's parity; lift[b] = 1 marks a member with a second
+// exact zero pivot, whose coefficients here are those of the d_z = +1 evaluation, halved.
 __global__ void pf_prep_kernel(const float* __restrict__ d, int H, int hreal, const int* __restrict__ perm, int N,
-                               float* __restrict__ dinv, int* __restrict__ iperm, PfCoef* __restrict__ coef,
+                               int adjugate, const int* __restrict__ parity, float* __restrict__ dinv,
+                               int* __restrict__ iperm, PfCoef* __restrict__ coef, int* __restrict__ lift,
                                int64_t batch) {
   const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -47,20 +55,66 @@ __global__ void pf_prep_kernel(const float* __restrict__ d, int H, int hreal, co
   for (int off = 32; off >= 1; off >>= 1) cand = min(cand, __shfl_xor(cand, off));
   const int K = cand;
   const float dK = db[K];
+  // over s != K: sum log|d_s| of the nonzero pivots, the number of negative and of zero
+  // pivots, and the first zero
+  float lg = 0.0f;
+  int negs = 0, zeros = 0, zfirst = 0x7fffffff;
   for (int s = lane; s < H; s += 64) {
     const float v = db[s];
     const float dt = (s == K || v == 0.0f) ? 1.0f : v;
     dinv[b * H + s] = 1.0f / dt;
+    if (s != K) {
+      lg += v != 0.0f ? logf(fabsf(v)) : 0.0f;
+      negs += v < 0.0f;
+      if (v == 0.0f) {
+        ++zeros;
+        zfirst = min(zfirst, s);
+      }
+    }
   }
   for (int f = lane; f < N; f += 64) iperm[b * N + perm[b * N + f]] = f;
+  if (!adjugate) {
+    if (lane == 0) {
+      PfCoef c;
+      c.K = K;
+      c.bad = dK == 0.0f;
+      c.a1 = 1.0f;
+      c.a2 = dK != 0.0f ? (1.0f - dK) / dK : 0.0f;
+      c.z = -1;
+      coef[b] = c;
+    }
+    return;
+  }
+  lg = wave_sum_f32(lg);
+  for (int off = 32; off >= 1; off >>= 1) {
+    negs += __shfl_xor(negs, off);
+    zeros += __shfl_xor(zeros, off);
+    zfirst = min(zfirst, __shfl_xor(zfirst, off));
+  }
   if (lane == 0) {
+    const bool has2 = zeros >= 1;
+    // D_K with d_z = +1: zero if a third zero pivot remains
+    const float phase = (zeros - (has2 ? 1 : 0)) > 0 ? 0.0f : ((negs & 1) ? -1.0f : 1.0f);
+    const float sgnP = parity[b] ? -1.0f : 1.0f;
+    const float D = sgnP * phase * expf(lg) * (has2 ? 0.5f : 1.0f);
     PfCoef c;
     c.K = K;
-    c.bad = dK == 0.0f;
-    c.a1 = 1.0f;
-    c.a2 = dK != 0.0f ? (1.0f - dK) / dK : 0.0f;
+    c.bad = 0;
+    c.a1 = D * dK;
+    c.a2 = D * (1.0f - dK);
+    c.z = has2 ? zfirst : -1;
     coef[b] = c;
+    lift[b] = has2 ? 1 : 0;
   }
+}
+
+// Second evaluation of the lifted members: d~_z = -1 (1/d~ flips sign at z). The
+// coefficients of that evaluation are those of the first negated (D_K flips with d_z).
+__global__ void pf_lift_kernel(const PfCoef* __restrict__ coef, int H, float* __restrict__ dinv, int64_t batch) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  const int z = coef[b].z;
+  if (z >= 0) dinv[b * H + z] = -1.0f;
 }
 
 // T[f][c] = L~[f][c] (f > c), 1 on the diagonal, 0 above; identity beyond N. One
@@ -69,8 +123,9 @@ __global__ void pf_prep_kernel(const float* __restrict__ d, int H, int hreal, co
 __global__ __launch_bounds__(256) void pf_assemble_kernel(const float* __restrict__ gbuf, int PB, int N,
                                                           const int* __restrict__ perm,
                                                           const float* __restrict__ dinv, float* __restrict__ T,
-                                                          int Ninv) {
+                                                          int Ninv, const int* __restrict__ active) {
   const int64_t b = blockIdx.y;
+  if (active && !active[b]) return;
   const int f = blockIdx.x;
   float4* row = reinterpret_cast<float4*>(T + b * (int64_t)Ninv * Ninv + (int64_t)f * Ninv);
   const int nb = N / PB;
@@ -97,8 +152,10 @@ __global__ __launch_bounds__(256) void pf_assemble_kernel(const float* __restric
 // DY[2s] = Y[2s+1] / d~_s, DY[2s+1] = -Y[2s] / d~_s with Y the unit-lower part of T.
 // One workgroup per row r, 16-byte vectors along the row.
 __global__ __launch_bounds__(256) void pf_dy_kernel(const float* __restrict__ T, int Ninv, int N,
-                                                    const float* __restrict__ dinv, float* __restrict__ DY) {
+                                                    const float* __restrict__ dinv, float* __restrict__ DY,
+                                                    const int* __restrict__ active) {
   const int64_t b = blockIdx.y;
+  if (active && !active[b]) return;
   const int r = blockIdx.x, src = r ^ 1;
   const float4* y4 = reinterpret_cast<const float4*>(T + b * (int64_t)Ninv * Ninv + (int64_t)src * Ninv);
   float4* o4 = reinterpret_cast<float4*>(DY + b * (int64_t)N * N + (int64_t)r * N);
@@ -116,14 +173,17 @@ __global__ __launch_bounds__(256) void pf_dy_kernel(const float* __restrict__ T,
   }
 }
 
-// PT = -(a1 R + a2 (w v^T - v w^T)); flags non-finite 64x64 tiles.
+// PT = -sg (a1 R + a2 (w v^T - v w^T)); flags non-finite 64x64 tiles.
 __global__ void pf_adj_kernel(const float* __restrict__ R, float* __restrict__ PT, int N, const float* __restrict__ T,
-                              int Ninv, const PfCoef* __restrict__ coef, int* __restrict__ flags) {
+                              int Ninv, const PfCoef* __restrict__ coef, float sg, int* __restrict__ flags,
+                              const int* __restrict__ active) {
   const int64_t b = blockIdx.y;
+  if (active && !active[b]) return;
   const int nt = (N + 63) / 64;
   const int tile = blockIdx.x;
   const int f0 = (tile / nt) * 64, c0 = (tile % nt) * 64;
   const PfCoef cf = coef[b];
+  const float a1 = sg * cf.a1, a2 = sg * cf.a2;
   const int aK = 2 * cf.K;
   const float* Rb = R + b * (int64_t)N * N;
   float* Pb = PT + b * (int64_t)N * N;
@@ -149,7 +209,7 @@ __global__ void pf_adj_kernel(const float* __restrict__ R, float* __restrict__ P
     if (f < N && cth < N) {
       // v = Y^T e_aK: v[j] = Y[aK][j] (unit lower: j < aK stored, j == aK one, j > aK zero)
       const float v_f = f < aK ? tv[u] : (f == aK ? 1.0f : 0.0f);
-      const float val = -(cf.a1 * rv[u] + cf.a2 * (wv[u] * v_c - v_f * wc));
+      const float val = -(a1 * rv[u] + a2 * (wv[u] * v_c - v_f * wc));
       badv = badv || !isfinite(val);
       Pb[(int64_t)f * N + cth] = val;
     }
@@ -158,25 +218,28 @@ __global__ void pf_adj_kernel(const float* __restrict__ R, float* __restrict__ P
   if (threadIdx.x == 0) flags[b * (nt * nt) + tile] = any;
 }
 
+// bad[b]: inverse mode only (the adjugate is returned as computed).
 __global__ void pf_reduce_bad_kernel(const int* __restrict__ flags, int ntiles, const PfCoef* __restrict__ coef,
-                                     int* __restrict__ bad, int64_t batch) {
+                                     int adjugate, int* __restrict__ bad, int64_t batch) {
   const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (b >= batch) return;
   bool f = false;
   for (int k = lane; k < ntiles; k += 64) f = f || flags[b * ntiles + k] != 0;
   const bool any = __ballot(f) != 0ull;
-  if (lane == 0) bad[b] = (any || coef[b].bad) ? 1 : 0;
+  if (lane == 0) bad[b] = (!adjugate && (any || coef[b].bad)) ? 1 : 0;
 }
 
-// out[i][j] = PT[iperm i][iperm j] for i, j < n (or 0 for a bad member). One workgroup
-// per output row: source row iperm[i] is read contiguously into LDS and the column
-// permutation is applied there.
+// out[i][j] = PT[iperm i][iperm j] for i, j < n (or 0 for a bad member); with accumulate
+// out[i][j] += PT[..] for the active members. One workgroup per output row: source row
+// iperm[i] is read contiguously into LDS and the column permutation is applied there.
 __global__ __launch_bounds__(256) void pf_gather_kernel(const float* __restrict__ PT, int N,
                                                         const int* __restrict__ iperm, int n,
-                                                        const int* __restrict__ bad, float* __restrict__ out) {
+                                                        const int* __restrict__ bad, float* __restrict__ out,
+                                                        const int* __restrict__ active, int accumulate) {
   __shared__ __align__(16) float rowb[2048];
   const int64_t b = blockIdx.y;
+  if (active && !active[b]) return;
   const int i = blockIdx.x;
   float* o = out + b * (int64_t)n * n + (int64_t)i * n;
   if (bad[b]) {
@@ -187,7 +250,11 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(const float* __restrict_
   const float4* s4 = reinterpret_cast<const float4*>(PT + b * (int64_t)N * N + (int64_t)ip[i] * N);
   for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) reinterpret_cast<float4*>(rowb)[c4] = s4[c4];
   __syncthreads();
-  for (int j = threadIdx.x; j < n; j += 256) o[j] = rowb[ip[j]];
+  if (accumulate) {
+    for (int j = threadIdx.x; j < n; j += 256) o[j] += rowb[ip[j]];
+  } else {
+    for (int j = threadIdx.x; j < n; j += 256) o[j] = rowb[ip[j]];
+  }
 }
 
 size_t pf_inverse_workspace(int64_t batch, int N) {
@@ -204,11 +271,13 @@ size_t pf_inverse_workspace(int64_t batch, int N) {
   add((size_t)batch * sizeof(PfCoef));
   add((size_t)batch * nt * nt * 4);      // flags
   add((size_t)batch * 4);                // bad
+  add((size_t)batch * 4);                // parity
+  add((size_t)batch * 4);                // lift
   return bytes;
 }
 
 int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm, int N, int n, int64_t batch,
-                      float* out, void* ws, size_t ws_bytes, hipStream_t s) {
+                      int adjugate, float* out, void* ws, size_t ws_bytes, hipStream_t s) {
   const int Ninv = inv_padded(N);
   if (!ws || ws_bytes < pf_inverse_workspace(batch, N)) return FX_ERR_WORKSPACE;
   char* p = (char*)ws;
@@ -227,48 +296,72 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
   const int nt = (N + 63) / 64;
   int* flags = (int*)take((size_t)batch * nt * nt * 4);
   int* bad = (int*)take((size_t)batch * 4);
+  int* parity = (int*)take((size_t)batch * 4);
+  int* lift = (int*)take((size_t)batch * 4);
   const int64_t NN = (int64_t)Ninv * Ninv;
-  const unsigned wb = (unsigned)((batch + 3) / 4);
-  hipLaunchKernelGGL(pf_prep_kernel, dim3(wb), dim3(256), 0, s, d, N / 2, n / 2, perm, N, dinv, iperm, coef, batch);
-  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  hipLaunchKernelGGL(pf_assemble_kernel, dim3((unsigned)Ninv, (unsigned)batch), dim3(256), 0, s, gbuf, PB, N,
-                     perm, dinv, T, Ninv);
-  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  int st = launch_unit_lower_inverse(T, Ninv, batch, Tmp, s);
-  if (st != FX_OK) return st;
   const int64_t MM = (int64_t)N * N;
-  hipLaunchKernelGGL(pf_dy_kernel, dim3((unsigned)N, (unsigned)batch), dim3(256), 0, s, T, Ninv, N, dinv, DY);
-  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  {
-    // R = Y^T DY: op(A) = Y^T (upper, unit diagonal), lower tiles, mirrored skew
-    GemmDesc g = {};
-    g.M = g.N = g.K = N;
-    g.A = T;
-    g.transA = 1;
-    g.maskA = MASK_UPPER_UNIT;
-    g.lda = Ninv;
-    g.sA = NN;
-    g.B = DY;
-    g.ldb = N;
-    g.sB = MM;
-    g.C = R;
-    g.ldc = N;
-    g.sC = MM;
-    g.alpha = 1.0f;
-    g.beta = 0.0f;
-    g.lower_only = 1;
-    g.mirror = -1.0f;
-    st = launch_gemm(g, batch, 1, s);
+  const unsigned wb = (unsigned)((batch + 3) / 4);
+  if (adjugate) {
+    const int st = launch_perm_parity(perm, N, batch, parity, s);
     if (st != FX_OK) return st;
   }
-  float* PT = DY;  // DY is dead once R is formed
-  hipLaunchKernelGGL(pf_adj_kernel, dim3(nt * nt, (unsigned)batch), dim3(256), 0, s, R, PT, N, T, Ninv, coef, flags);
+  hipLaunchKernelGGL(pf_prep_kernel, dim3(wb), dim3(256), 0, s, d, N / 2, n / 2, perm, N, adjugate, parity, dinv,
+                     iperm, coef, lift, batch);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  hipLaunchKernelGGL(pf_reduce_bad_kernel, dim3(wb), dim3(256), 0, s, flags, nt * nt, coef, bad, batch);
+  // One evaluation of -(a1 R + a2 (w v^T - v w^T)) for the current dinv, written to (or,
+  // with accumulate, added to) out; `active` restricts it to the marked members.
+  auto evaluate = [&](const int* active, float sg, int accumulate) -> int {
+    hipLaunchKernelGGL(pf_assemble_kernel, dim3((unsigned)Ninv, (unsigned)batch), dim3(256), 0, s, gbuf, PB, N,
+                       perm, dinv, T, Ninv, active);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    int st = launch_unit_lower_inverse(T, Ninv, batch, Tmp, s, active);
+    if (st != FX_OK) return st;
+    hipLaunchKernelGGL(pf_dy_kernel, dim3((unsigned)N, (unsigned)batch), dim3(256), 0, s, T, Ninv, N, dinv, DY,
+                       active);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    {
+      // R = Y^T DY: op(A) = Y^T (upper, unit diagonal), lower tiles, mirrored skew
+      GemmDesc g = {};
+      g.M = g.N = g.K = N;
+      g.A = T;
+      g.transA = 1;
+      g.maskA = MASK_UPPER_UNIT;
+      g.lda = Ninv;
+      g.sA = NN;
+      g.B = DY;
+      g.ldb = N;
+      g.sB = MM;
+      g.C = R;
+      g.ldc = N;
+      g.sC = MM;
+      g.alpha = 1.0f;
+      g.beta = 0.0f;
+      g.lower_only = 1;
+      g.mirror = -1.0f;
+      g.active = active;
+      st = launch_gemm(g, batch, 1, s);
+      if (st != FX_OK) return st;
+    }
+    float* PT = DY;  // DY is dead once R is formed
+    hipLaunchKernelGGL(pf_adj_kernel, dim3(nt * nt, (unsigned)batch), dim3(256), 0, s, R, PT, N, T, Ninv, coef, sg,
+                       flags, active);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    if (!accumulate) {
+      hipLaunchKernelGGL(pf_reduce_bad_kernel, dim3(wb), dim3(256), 0, s, flags, nt * nt, coef, adjugate, bad,
+                         batch);
+      if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    }
+    hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)n, (unsigned)batch), dim3(256), 0, s, PT, N, iperm, n, bad,
+                       out, active, accumulate);
+    return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+  };
+  int st = evaluate(nullptr, 1.0f, 0);
+  if (st != FX_OK || !adjugate) return st;
+  // the lifted members' second evaluation (every other member's workgroups exit at once)
+  hipLaunchKernelGGL(pf_lift_kernel, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s, coef, N / 2, dinv,
+                     batch);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)n, (unsigned)batch), dim3(256), 0, s, PT, N, iperm, n, bad,
-                     out);
-  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+  return evaluate(lift, -1.0f, 1);
 }
 
 }  // namespace fx

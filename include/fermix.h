@@ -74,6 +74,20 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
                          float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
+/* adj_t (batch, n, n) = adj(A)^T = d det(A) / dA, finite and exact for singular A, plus
+ * sign / logabs bit-identical to fx_slogdet_f32 (det = sign * exp(logabs) is the value
+ * the reference's det returns with this gradient). From the packed LU of the same run:
+ * det(factors) * A^-T for members without an exact zero pivot; with zero pivots at
+ * k1 <= ... <= km (U~ = U with them replaced by 1, d_K = product of the other pivots) the
+ * rank-1 form sgn(P) d_K c (U~^-1 e_k1)(e_km^T U~^-1 L^-1 P), c = (U~^-1)[k1, km] for
+ * m = 2 and 1 for m = 1; 0 for m >= 3. Non-finite inverses give 0.
+ * Replaces `_det_gradT` (src/fermix/_diff.py:205-246) with `_lu_det` (:184-202) and
+ * `_perm_sign` (:160-176) on top of `_parts(zero_singular=False)`, as called by the jvp
+ * rule of `_det_diff` (:288-301). */
+size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n);
+int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
+                     void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
 /* ---------------------------------------------------------------- slogpf
  * sign[b], logabs[b] of pf(S[b]), S = (a - a^T) / 2 if skew_symmetrize != 0, else
  * S = a (which must then be exactly skew-symmetric). Odd n gives (0, -inf).
@@ -101,12 +115,16 @@ int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew
                           float* sign, float* logabs, float* gbuf, float* d, int32_t* perm,
                           void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
-/* The same run as fx_slogpf_f32 (bit-identical sign / logabs) plus g (batch, n, n):
- * S^-1 formed from the run's own factors (no second factorisation), zero for members
- * with an exactly zero pivot or a non-finite result (adjugate = 0). adjugate != 0
- * (pf(S) S^-1, the Pfaffian adjugate) returns FX_ERR_UNSUPPORTED in this version.
+/* The same run as fx_slogpf_f32 (bit-identical sign / logabs) plus g (batch, n, n)
+ * formed from the run's own factors (no second factorisation):
+ *  - adjugate = 0: S^-1, zero for members with an exactly zero pivot or a non-finite
+ *    result (the slogpf gradient is -g / 2);
+ *  - adjugate != 0: pf(S) S^-1, the Pfaffian adjugate, finite and exact for singular S
+ *    (a second exact zero pivot is lifted to +1 and -1 and the two evaluations averaged;
+ *    the pf gradient is -g / 2). Odd n gives g = 0 in both modes.
  * Replaces `_pf_parts` (src/fermix/_pfinv.py:196-269) as called by `_pf_grad_parts`
- * (src/fermix/_diff.py:80-89); kernels K11-K12 (_pfinv.py:80-192). */
+ * (src/fermix/_diff.py:80-89); kernels K11-K12 (_pfinv.py:80-192) and the adjugate
+ * helpers `_pf_adj_coeffs` / `_lifted_mean` (src/fermix/_fallback.py:138-176). */
 size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
                         int32_t adjugate, float* sign, float* logabs, float* g, void* workspace,

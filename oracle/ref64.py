@@ -9,7 +9,12 @@ algorithms under test where possible:
 * ``pf_pr64`` -- a float64 Parlett-Reid (the textbook algorithm, cross-checked against
   ``pf_brute`` and pf^2 = det);
 * ``adjT_brute`` -- d det / dA = adj(A)^T by cofactors;
-* ``pf_grad_brute`` -- d pf / dS by minor Pfaffians.
+* ``adjT_svd`` -- the same from the SVD, A = U diag(sig) V^T:
+  adj(A)^T = det(U) det(V) U diag(prod_{j != i} sig_j) V^T (any n, exact continuation
+  to singular A; pinned against ``adjT_brute``);
+* ``pf_grad_brute`` -- d pf / dS by minor Pfaffians;
+* ``pf_grad64`` -- the same with the minors' Pfaffians from ``pf64`` (larger n), and
+  ``pf_grad64_rows`` for the entries in given rows only.
 """
 
 import math
@@ -103,3 +108,50 @@ def pf_grad_brute(S):
 
 def inv64(A):
     return np.linalg.inv(np.asarray(A, np.float64))
+
+
+def adjT_svd(A):
+    """d det / dA = adj(A)^T from the SVD (float64): with A = U diag(sig) Vt,
+    adj(A) = adj(Vt) adj(diag(sig)) adj(U) = det(Vt) det(U) Vt^T diag(p) U^T,
+    p_i = prod_{j != i} sig_j, so adj(A)^T = det(U) det(Vt) U diag(p) Vt. The products
+    are formed in logs (sig_j = 0 contributes an exact zero)."""
+    A = np.asarray(A, np.float64)
+    n = A.shape[0]
+    if n == 0:
+        return np.zeros((0, 0))
+    U, sig, Vt = np.linalg.svd(A)
+    with np.errstate(divide="ignore"):
+        lg = np.log(sig)
+    p = np.empty(n)
+    for i in range(n):
+        others = np.delete(lg, i)
+        p[i] = 0.0 if np.any(np.isneginf(others)) else math.exp(float(np.sum(others)))
+    return np.linalg.det(U) * np.linalg.det(Vt) * (U * p[None, :]) @ Vt
+
+
+def pf_grad64(S):
+    """d pf / dS as in ``pf_grad_brute`` with each minor's Pfaffian from ``pf64``."""
+    S = np.asarray(S, np.float64)
+    n = S.shape[0]
+    D = np.zeros((n, n))
+    for i in range(n):
+        for j in range(i + 1, n):
+            keep = [k for k in range(n) if k not in (i, j)]
+            D[i, j] = (-1) ** (i + j + 1) * pf64(S[np.ix_(keep, keep)])
+    return 0.5 * (D - D.T)
+
+
+def pf_grad64_rows(S, rows):
+    """d pf / dS restricted to the entries (i, j) with i or j in ``rows`` (the rest set to
+    zero): for S whose every other minor Pfaffian vanishes -- e.g. S with the rows and
+    columns ``rows`` exactly zero -- this is the whole gradient, at O(n |rows|) minors."""
+    S = np.asarray(S, np.float64)
+    n = S.shape[0]
+    D = np.zeros((n, n))
+    for i in range(n):
+        for j in range(i + 1, n):
+            if i not in rows and j not in rows:
+                continue
+            keep = [k for k in range(n) if k not in (i, j)]
+            D[i, j] = (-1) ** (i + j + 1) * pf64(S[np.ix_(keep, keep)])
+    return 0.5 * (D - D.T)

@@ -39,13 +39,17 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_calls():
     L = _lib.lib()
-    assert L.fx_abi_version() == 100
+    assert L.fx_abi_version() == 101
     assert L.fx_status_string(0) == b"ok"
     assert L.fx_lu_padded_size(100) == 112
     assert L.fx_pf_padded_size(128) == 128
     # argument validation happens before any device work
     assert L.fx_slogdet_f32(None, -1, 4, None, None, None, 0, None) == 1
     assert L.fx_slogdet_f32(None, 0, 4, None, None, None, 0, None) == 0
+    assert L.fx_det_parts_f32(None, -1, 4, None, None, None, None, 0, None) == 1
+    assert L.fx_det_parts_f32(None, 2, 4, None, None, None, None, 0, None) == 1
+    assert L.fx_det_parts_f32_workspace(4, 2000) == 0
+    assert L.fx_det_parts_f32_workspace(4, 64) > L.fx_slogdet_parts_f32_workspace(4, 64)
 
 
 def test_api_errors():

@@ -216,6 +216,48 @@ def test_det_gradT_brute_force(rank_def):
     assert np.allclose(d, np.linalg.det(A.astype(np.float64)), rtol=1e-4, atol=1e-6)
 
 
+@pytest.mark.parametrize("kind", ["regular", "zero_col", "zero_col_row", "two_cols", "near"])
+def test_adjT_svd_vs_cofactors(kind):
+    """The SVD adjugate (float64 truth for the GPU tests at any n) against cofactors."""
+    n = 7
+    A = randn((4, n, n)).astype(np.float64)
+    if kind == "zero_col":
+        A[:, :, 2] = 0.0
+    if kind == "zero_col_row":
+        A[:, :, 0] = 0.0
+        A[:, 1, :] = 0.0
+    if kind == "two_cols":
+        A[:, :, 0] = 0.0
+        A[:, :, 3] = 0.0
+    if kind == "near":
+        A[:, -1, :] = np.einsum("bi,bij->bj", randn((4, n - 1)).astype(np.float64), A[:, :-1, :])
+    for a in A:
+        ref = ref64.adjT_brute(a)
+        got = ref64.adjT_svd(a)
+        assert np.max(np.abs(got - ref)) <= 1e-9 * max(np.abs(ref).max(), 1.0)
+    # a transposed result (adj(A) instead of adj(A)^T) fails on a generic member
+    a = A[0]
+    if kind == "regular":
+        assert np.max(np.abs(ref64.adjT_svd(a).T - ref64.adjT_brute(a))) > 1e-3
+
+
+@pytest.mark.parametrize("n", [4, 6, 8])
+def test_pf_grad64_vs_brute(n):
+    S = skew(randn((2, n, n))).astype(np.float64)
+    S[1, 1, :] = 0.0
+    S[1, :, 1] = 0.0
+    for x in S:
+        ref = ref64.pf_grad_brute(x)
+        assert np.max(np.abs(ref64.pf_grad64(x) - ref)) <= 1e-9 * max(np.abs(ref).max(), 1.0)
+    # rows variant: S[1] has row / column 1 zero, so only those entries are nonzero
+    ref = ref64.pf_grad_brute(S[1])
+    assert np.max(np.abs(ref64.pf_grad64_rows(S[1], [1]) - ref)) <= 1e-9 * max(np.abs(ref).max(), 1.0)
+    # regular: d pf / dS = pf S^-T / 2
+    x = S[0]
+    want = 0.5 * ref64.pf64(x) * np.linalg.inv(x).T
+    assert np.max(np.abs(ref64.pf_grad64(x) - want)) <= 1e-8 * np.abs(want).max()
+
+
 def test_polynomials():
     for n in range(0, 5):
         A = randn((4, n, n))
