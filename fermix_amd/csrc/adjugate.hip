@@ -24,16 +24,19 @@ namespace fx {
 // cycles are found by pointer jumping in LDS: after r rounds lab[i] is the smallest index
 // among the 2^r orbit elements starting at i and nx[i] = perm^(2^r)(i), so after
 // ceil(log2 N) rounds every element carries its cycle's minimum and each cycle has exactly
-// one element labelled by itself. One workgroup per member, N <= 2048.
+// one element labelled by itself. One workgroup per member, N <= PARITY_MAXN.
+constexpr int PARITY_MAXN = 4096;
+
 __global__ __launch_bounds__(256) void perm_parity_kernel(const int* __restrict__ perm, int N,
                                                           int* __restrict__ parity) {
-  __shared__ int lab[2048], nx[2048];
+  constexpr int U = PARITY_MAXN / 256;
+  __shared__ int lab[PARITY_MAXN], nx[PARITY_MAXN];
   __shared__ int wcount[4];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
   const int* g = perm + b * N;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int i = tid + 256 * u;
     if (i < N) {
       lab[i] = i;
@@ -42,9 +45,9 @@ __global__ __launch_bounds__(256) void perm_parity_kernel(const int* __restrict_
   }
   __syncthreads();
   for (int span = 1; span < N; span *= 2) {
-    int nl[8], nn[8];
+    int nl[U], nn[U];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int i = tid + 256 * u;
       nl[u] = 0;
       nn[u] = 0;
@@ -56,7 +59,7 @@ __global__ __launch_bounds__(256) void perm_parity_kernel(const int* __restrict_
     }
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int i = tid + 256 * u;
       if (i < N) {
         lab[i] = nl[u];
@@ -67,7 +70,7 @@ __global__ __launch_bounds__(256) void perm_parity_kernel(const int* __restrict_
   }
   int cnt = 0;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int i = tid + 256 * u;
     cnt += __popcll(__ballot(i < N && lab[i] == i));
   }
@@ -77,7 +80,7 @@ __global__ __launch_bounds__(256) void perm_parity_kernel(const int* __restrict_
 }
 
 int launch_perm_parity(const int* perm, int N, int64_t batch, int* parity, hipStream_t s) {
-  if (N > 2048) return FX_ERR_UNSUPPORTED;
+  if (N > PARITY_MAXN) return FX_ERR_UNSUPPORTED;
   if (batch <= 0) return FX_OK;
   hipLaunchKernelGGL(perm_parity_kernel, dim3((unsigned)batch), dim3(256), 0, s, perm, N, parity);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
@@ -85,7 +88,7 @@ int launch_perm_parity(const int* perm, int N, int64_t batch, int* parity, hipSt
 
 // ------------------------------------------------------------------ det adjugate
 
-constexpr int DET_ADJ_MAXN = 1024;
+constexpr int DET_ADJ_MAXN = LU_LARGE_MAXN;
 
 // Per-member result of det_prep_kernel.
 struct DetCoef {
@@ -201,16 +204,17 @@ __global__ __launch_bounds__(256) void det_prep_kernel(const float* __restrict__
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
   const float* LUb = LU + b * (int64_t)N * N;
-  float dv[4];
+  constexpr int DU = DET_ADJ_MAXN / 256;
+  float dv[DU];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < DU; ++u) {
     const int i = min(tid + 256 * u, N - 1);
     dv[u] = LUb[(int64_t)i * (N + 1)];
   }
   int zc = 0, negs = 0, kmin = N, kmax = -1;
   float lg = 0.0f;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < DU; ++u) {
     const int i = tid + 256 * u;
     if (i < N) {
       const bool z = dv[u] == 0.0f;

@@ -60,8 +60,8 @@ static int fill2(float* a, float va, float* b, float vb, int64_t count, hipStrea
 }
 
 static constexpr int SMALL_MAX = 128;
-static constexpr int LARGE_MAX = 1024;
-static constexpr int PF_LARGE_MAX = 2048;
+static constexpr int LARGE_MAX = LU_LARGE_MAXN;
+static constexpr int PF_LARGE_MAX = PF_LARGE_MAXN;
 
 }  // namespace fx
 
@@ -94,7 +94,7 @@ int32_t fx_pf_padded_size(int32_t n) {
   return n <= PF_LARGE_MAX ? pf_large_padded(n) : -1;
 }
 
-int32_t fx_pf_block_columns(int32_t n) { return n <= SMALL_MAX ? 16 : 32; }
+int32_t fx_pf_block_columns(int32_t n) { return (n <= SMALL_MAX || pf_large_padded(n) > 2048) ? 16 : 32; }
 
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || n <= SMALL_MAX || n > LARGE_MAX) return 0;
@@ -299,8 +299,7 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
   }
   if (st != FX_OK) return st;
   const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
-  return launch_pf_inverse(gbuf, n <= SMALL_MAX ? 16 : 32, d, perm, N, n, batch, adjugate ? 1 : 0, g, p, rest,
-                           s);
+  return launch_pf_inverse(gbuf, fx_pf_block_columns(n), d, perm, N, n, batch, adjugate ? 1 : 0, g, p, rest, s);
 }
 
 }  // extern "C"

@@ -22,8 +22,10 @@ int launch_lu_small(const float* A, int n, int64_t batch, float* sign, float* lo
 int launch_pf_small(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
                     float* gbuf, float* d, int* perm, hipStream_t s);
 
-// 128 < n <= 1024: blocked LU in a workspace (see lu_large.hip). W_out / g0_out return
-// the packed LU (B, N, N) and, with parts, the composed row map (B, N), N = lu_large_padded.
+// 128 < n <= LU_LARGE_MAXN: blocked LU in a workspace (see lu_large.hip). W_out / g0_out
+// return the packed LU (B, N, N) and, with parts, the composed row map (B, N),
+// N = lu_large_padded.
+constexpr int LU_LARGE_MAXN = 4096;
 int lu_large_padded(int n);
 size_t lu_large_workspace(int64_t batch, int n, bool parts);
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
@@ -39,8 +41,9 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
                       int zero_singular, float* invT, bool in_place, void* ws, size_t ws_bytes,
                       hipStream_t s, const float* scale = nullptr);
 
-// 128 < n <= 2048 Parlett-Reid (pf_large.hip); with gbuf the factors (B, N/32, N, 32) by
-// original row, d (B, N/2) and perm (B, N).
+// 128 < n <= PF_LARGE_MAXN Parlett-Reid (pf_large.hip); with gbuf the factors
+// (B, N/PB, N, PB) by original row (PB = 32, or 16 for N > 2048), d (B, N/2) and perm (B, N).
+constexpr int PF_LARGE_MAXN = 4096;
 int pf_large_padded(int n);
 size_t pf_large_workspace(int64_t batch, int n, bool fact);
 int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,

@@ -1,7 +1,8 @@
-// Blocked LU with partial pivoting for 128 < n <= 1024 (any batch): per block of PW
+// Blocked LU with partial pivoting for 128 < n <= 4096 (any batch): per block of PW
 // columns at r0 three launches,
 //   1. lu_panel_kernel  (one workgroup per matrix): the m x PW panel (m = N - r0) is
-//      factored in LDS in 16-column sub-panels. The rows stay in place during the
+//      factored in 16-column sub-panels, in LDS (N <= 1024) or in place in the work
+//      buffer (N > 1024: 512-1024 threads, 4 rows per lane, the sub-panel in registers). The rows stay in place during the
 //      panel (virtual pivoting); each column step finds the pivot with a per-wave DPP
 //      max and one workgroup barrier (every wave posts its best row, all waves pick the
 //      same winner), and the sub-panel's trailing columns inside the panel are updated
@@ -22,9 +23,9 @@
 
 namespace fx {
 
-template <int MR, int PW>
+template <int MR, int PW, int NT>
 struct LuPanel {
-  static constexpr int NW = 4, NT = 256;
+  static constexpr int NW = NT / 64;
   static constexpr int R = MR / NT;  // rows per lane
   static constexpr int LDP = PW + 4;
   static constexpr int NSUB = PW / 16;
@@ -39,7 +40,7 @@ struct Cand {
 };
 
 // Copy A (B, n, n) into the work buffer W (B, N, N) with identity padding.
-// 32-bit index math (N <= 1024).
+// 32-bit index math within a matrix (N * N < 2^31).
 __global__ void copy_pad_kernel(const float* __restrict__ A, int n, float* __restrict__ W, int N) {
   const int64_t b = blockIdx.y;
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
@@ -48,46 +49,55 @@ __global__ void copy_pad_kernel(const float* __restrict__ A, int n, float* __res
   W[b * N * N + e] = (r < n && c < n) ? A[b * n * n + r * n + c] : (r == c ? 1.0f : 0.0f);
 }
 
-template <int MR, int PW>
-__global__ __launch_bounds__(256) void lu_panel_kernel(float* __restrict__ W, int N, int r0, int blk,
-                                                       float* __restrict__ piv_out,
-                                                       int* __restrict__ nsw_out, int nblk,
-                                                       int* __restrict__ src_out,
-                                                       float* __restrict__ X_out,
-                                                       int* __restrict__ g0) {
-  using C = LuPanel<MR, PW>;
-  constexpr int R = C::R, LDP = C::LDP, NSUB = C::NSUB, NW = C::NW;
-  __shared__ float P[MR * LDP];
+// GLOBAL = false: the panel is copied into LDS (MR * (PW + 4) floats); GLOBAL = true: the
+// panel is factored in place in the work buffer (rows in place until the final
+// permutation), for panels too tall for LDS -- the workgroup's own global accesses are
+// ordered by its barriers (one CU, workgroup-scope fences).
+template <int MR, int PW, int NT, bool GLOBAL>
+__global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int N, int r0, int blk,
+                                                      float* __restrict__ piv_out,
+                                                      int* __restrict__ nsw_out, int nblk,
+                                                      int* __restrict__ src_out,
+                                                      float* __restrict__ X_out,
+                                                      int* __restrict__ g0) {
+  using C = LuPanel<MR, PW, NT>;
+  constexpr int R = C::R, NSUB = C::NSUB, NW = C::NW;
+  __shared__ float Plds[GLOBAL ? 1 : MR * C::LDP];
   __shared__ Cand cand[2][NW];
   __shared__ float Ubuf[16 * PW];
   __shared__ int posL[MR];
   __shared__ int prowL[16];
   __shared__ float Xs[256];
+  __shared__ float L11s[256];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = N - r0;
   float* Wb = W + b * (int64_t)N * N;
+  float* const P = GLOBAL ? Wb + (int64_t)r0 * N + r0 : Plds;
+  const int LDP = GLOBAL ? N : C::LDP;
 
-  // load the panel: P[i][c] = W[r0 + i][r0 + c], 8 vector loads in flight per thread
-  // (rows past m read row r0 and are not stored)
-  for (int base = 0; base < m * (PW / 4); base += 256 * 8) {
-    float4 v[8];
+  if (!GLOBAL) {
+    // load the panel: P[i][c] = W[r0 + i][r0 + c], 8 vector loads in flight per thread
+    // (rows past m read row r0 and are not stored)
+    for (int base = 0; base < m * (PW / 4); base += NT * 8) {
+      float4 v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int e = base + tid + 256 * u;
-      const int i = e / (PW / 4), q = e % (PW / 4);
-      v[u] = *reinterpret_cast<const float4*>(Wb + (int64_t)(r0 + (i < m ? i : 0)) * N + r0 + 4 * q);
-    }
+      for (int u = 0; u < 8; ++u) {
+        const int e = base + tid + NT * u;
+        const int i = e / (PW / 4), q = e % (PW / 4);
+        v[u] = *reinterpret_cast<const float4*>(Wb + (int64_t)(r0 + (i < m ? i : 0)) * N + r0 + 4 * q);
+      }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int e = base + tid + 256 * u;
-      const int i = e / (PW / 4), q = e % (PW / 4);
-      if (i < m) {
-        float* d = P + i * LDP + 4 * q;
-        d[0] = v[u].x;
-        d[1] = v[u].y;
-        d[2] = v[u].z;
-        d[3] = v[u].w;
+      for (int u = 0; u < 8; ++u) {
+        const int e = base + tid + NT * u;
+        const int i = e / (PW / 4), q = e % (PW / 4);
+        if (i < m) {
+          float* d = P + i * LDP + 4 * q;
+          d[0] = v[u].x;
+          d[1] = v[u].y;
+          d[2] = v[u].z;
+          d[3] = v[u].w;
+        }
       }
     }
   }
@@ -105,14 +115,29 @@ __global__ __launch_bounds__(256) void lu_panel_kernel(float* __restrict__ W, in
   for (int sp = 0; sp < NSUB; ++sp) {
     const int c0 = 16 * sp;
     float a[R][16];
+    if (GLOBAL) {
+      // 16-byte loads (r0, c0 and N are multiples of 16); rows past m read row 0
 #pragma unroll
-    for (int s = 0; s < R; ++s) {
-      const int i = R * (64 * wave + lane) + s;
+      for (int s = 0; s < R; ++s) {
+        const int i = R * tid + s;
+        const float4* rp = reinterpret_cast<const float4*>(P + (int64_t)(valid[s] ? i : 0) * LDP + c0);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) a[s][j] = valid[s] ? P[i * LDP + c0 + j] : 0.0f;
+        for (int q = 0; q < 4; ++q) {
+          const float4 v = rp[q];
+          a[s][4 * q] = valid[s] ? v.x : 0.0f;
+          a[s][4 * q + 1] = valid[s] ? v.y : 0.0f;
+          a[s][4 * q + 2] = valid[s] ? v.z : 0.0f;
+          a[s][4 * q + 3] = valid[s] ? v.w : 0.0f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        const int i = R * (64 * wave + lane) + s;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) a[s][j] = valid[s] ? P[i * LDP + c0 + j] : 0.0f;
+      }
     }
-    float xcol[16];
-    int prow_reg[16];
     static_for<0, 16>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       const int posc = c0 + j;
@@ -158,7 +183,9 @@ __global__ __launch_bounds__(256) void lu_panel_kernel(float* __restrict__ W, in
 #pragma unroll
       for (int jj = 0; jj < 16; ++jj) u[jj] = win.v[jj];
       const int pp = win.pos, prow = win.row;
-      prow_reg[j] = prow;
+      // the pivot row and its L entries (row j of L11) for X = L11^-1 after the steps
+      if (tid == 0) prowL[j] = prow;
+      if (tid < j) L11s[j * 16 + tid] = win.v[tid];
 #pragma unroll
       for (int s = 0; s < R; ++s) {
         const int i = R * (64 * wave + lane) + s;
@@ -177,31 +204,39 @@ __global__ __launch_bounds__(256) void lu_panel_kernel(float* __restrict__ W, in
           static_for<j + 1, 16>([&](auto cc) { a[s][cc.value] = fmaf(-l, u[cc.value], a[s][cc.value]); });
         }
       }
-      float x = 0.0f;
-      static_for<0, j>([&](auto kc) { x = fmaf(-u[kc.value], xcol[kc.value], x); });
-      xcol[j] = (lane == j) ? 1.0f : x;
     });
-    // sub-panel back to LDS (rows stay in place), positions, pivot rows, X
+    // sub-panel back (rows stay in place), positions, pivot rows, X
 #pragma unroll
     for (int s = 0; s < R; ++s) {
       const int i = R * (64 * wave + lane) + s;
       if (valid[s]) {
+        if (GLOBAL) {
+          float4* rp = reinterpret_cast<float4*>(P + (int64_t)i * LDP + c0);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) P[i * LDP + c0 + j] = a[s][j];
+          for (int q = 0; q < 4; ++q)
+            rp[q] = make_float4(a[s][4 * q], a[s][4 * q + 1], a[s][4 * q + 2], a[s][4 * q + 3]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) P[i * LDP + c0 + j] = a[s][j];
+        }
         posL[i] = pos[s];
       }
     }
-    if (wave == 0) {
-      if (lane < 16) {
+    __syncthreads();
+    // X = L11^-1 (unit lower): lane c < 16 of wave 0 forms column c,
+    // X[j][c] = -sum_{k<j} L11[j][k] X[k][c], X[c][c] = 1, X[j][c] = 0 for j < c
+    if (wave == 0 && lane < 16) {
+      float xcol[16];
+      static_for<0, 16>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        float x = 0.0f;
+        static_for<0, j>([&](auto kc) { x = fmaf(-L11s[j * 16 + kc.value], xcol[kc.value], x); });
+        xcol[j] = (lane == j) ? 1.0f : x;
+      });
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          Xs[k * 16 + lane] = xcol[k];
-          X_out[((b * NSUB + sp) * 16 + k) * 16 + lane] = xcol[k];
-        }
-        int pr = prow_reg[0];
-#pragma unroll
-        for (int k = 1; k < 16; ++k) pr = (lane == k) ? prow_reg[k] : pr;
-        prowL[lane] = pr;
+      for (int k = 0; k < 16; ++k) {
+        Xs[k * 16 + lane] = xcol[k];
+        X_out[((b * NSUB + sp) * 16 + k) * 16 + lane] = xcol[k];
       }
     }
     __syncthreads();
@@ -214,7 +249,7 @@ __global__ __launch_bounds__(256) void lu_panel_kernel(float* __restrict__ W, in
         v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          acc = mfma16(Xs[li * 16 + 4 * t + g], P[prowL[4 * t + g] * LDP + cs + li], acc);
+          acc = mfma16(Xs[li * 16 + 4 * t + g], P[(int64_t)prowL[4 * t + g] * LDP + cs + li], acc);
 #pragma unroll
         for (int v = 0; v < 4; ++v) Ubuf[(4 * g + v) * PW + cs + li] = acc[v];
       }
@@ -229,51 +264,76 @@ __global__ __launch_bounds__(256) void lu_panel_kernel(float* __restrict__ W, in
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int r = rb + 4 * g + v;
-          acc[v] = r < m ? P[r * LDP + cs + li] : 0.0f;
+          acc[v] = r < m ? P[(int64_t)r * LDP + cs + li] : 0.0f;
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int r = rb + li;
-          const float lv = r < m ? P[r * LDP + c0 + 4 * t + g] : 0.0f;
+          const float lv = r < m ? P[(int64_t)r * LDP + c0 + 4 * t + g] : 0.0f;
           acc = mfma16(-lv, Ubuf[(4 * t + g) * PW + cs + li], acc);
         }
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int r = rb + 4 * g + v;
-          if (r < m && posL[r] > c0 + 15) P[r * LDP + cs + li] = acc[v];
+          if (r < m && posL[r] > c0 + 15) P[(int64_t)r * LDP + cs + li] = acc[v];
         }
       }
       __syncthreads();
       // phase C: the pivot rows take their U values
       const int ncols = 16 * nss;
-      for (int e = tid; e < 16 * ncols; e += 256) {
+      for (int e = tid; e < 16 * ncols; e += NT) {
         const int k = e / ncols, c = c0 + 16 + e % ncols;
-        P[prowL[k] * LDP + c] = Ubuf[k * PW + c];
+        P[(int64_t)prowL[k] * LDP + c] = Ubuf[k * PW + c];
       }
       __syncthreads();
     }
   }
   // write the panel back in the new row order
-  for (int e = tid; e < m * (PW / 4); e += 256) {
-    const int i = e / (PW / 4), q = e % (PW / 4);
-    const float* sp_ = P + i * LDP + 4 * q;
-    *reinterpret_cast<float4*>(Wb + (int64_t)(r0 + posL[i]) * N + r0 + 4 * q) =
-        make_float4(sp_[0], sp_[1], sp_[2], sp_[3]);
+  if (GLOBAL) {
+    // in place, 16 columns at a time: every row of a pass is read before any is written
+    for (int q = 0; q < NSUB; ++q) {
+      float4 v[R][4];
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        const int i = R * tid + s;
+        const float4* rp = reinterpret_cast<const float4*>(P + (int64_t)(i < m ? i : 0) * LDP + 16 * q);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[s][k] = rp[k];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        const int i = R * tid + s;
+        if (i < m) {
+          float4* wp = reinterpret_cast<float4*>(P + (int64_t)posL[i] * LDP + 16 * q);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) wp[k] = v[s][k];
+        }
+      }
+      __syncthreads();
+    }
+  } else {
+    for (int e = tid; e < m * (PW / 4); e += NT) {
+      const int i = e / (PW / 4), q = e % (PW / 4);
+      const float* sp_ = P + i * LDP + 4 * q;
+      *reinterpret_cast<float4*>(Wb + (int64_t)(r0 + posL[i]) * N + r0 + 4 * q) =
+          make_float4(sp_[0], sp_[1], sp_[2], sp_[3]);
+    }
   }
-  for (int i = tid; i < m; i += 256) src_out[b * N + r0 + posL[i]] = r0 + i;
+  for (int i = tid; i < m; i += NT) src_out[b * N + r0 + posL[i]] = r0 + i;
   if (g0) {
     // compose the row map: g0[r0 + p] <- g0[r0 + src(p)]
     int* gb = g0 + b * N;
-    int tmp[(MR + 255) / 256];
+    int tmp[(MR + NT - 1) / NT];
 #pragma unroll
-    for (int q = 0; q < (MR + 255) / 256; ++q) {
-      const int i = tid + 256 * q;
+    for (int q = 0; q < (MR + NT - 1) / NT; ++q) {
+      const int i = tid + NT * q;
       tmp[q] = i < m ? gb[r0 + i] : 0;
     }
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < (MR + 255) / 256; ++q) {
-      const int i = tid + 256 * q;
+    for (int q = 0; q < (MR + NT - 1) / NT; ++q) {
+      const int i = tid + NT * q;
       if (i < m) gb[r0 + posL[i]] = tmp[q];
     }
   }
@@ -281,7 +341,7 @@ __global__ __launch_bounds__(256) void lu_panel_kernel(float* __restrict__ W, in
 }
 
 // Row permutation of one 64-column strip and, for a trailing strip, its U rows.
-template <int PW>
+template <int PW, int MAXM>
 __global__ __launch_bounds__(256) void lu_urow_kernel(float* __restrict__ W, int N, int r0,
                                                       const int* __restrict__ src,
                                                       const float* __restrict__ Xg,
@@ -308,7 +368,7 @@ __global__ __launch_bounds__(256) void lu_urow_kernel(float* __restrict__ W, int
   // positions r0 .. r0+PW-1
   if (tid == 0) cnt = 0;
   __syncthreads();
-  constexpr int MQ = 1024 / 256;  // m <= N <= 1024
+  constexpr int MQ = MAXM / 256;  // m <= N <= MAXM
   int sv[MQ];
 #pragma unroll
   for (int q = 0; q < MQ; ++q) {
@@ -439,13 +499,16 @@ __global__ void iota_kernel(int* g0, int N, int64_t total) {
 }
 
 int lu_large_padded(int n) {
-  if (n <= 512) return ((n + 63) / 64) * 64;
+  if (n <= 512 || n > 1024) return ((n + 63) / 64) * 64;
   return ((n + 31) / 32) * 32;
 }
 
+// Panel width: 64 columns, except 32 for 512 < N <= 1024 (the LDS panel of 1024 rows).
+static int lu_panel_width(int N) { return (N > 512 && N <= 1024) ? 32 : 64; }
+
 size_t lu_large_workspace(int64_t batch, int n, bool parts) {
   const int N = lu_large_padded(n);
-  const int PW = N <= 512 ? 64 : 32;
+  const int PW = lu_panel_width(N);
   const int nblk = N / PW;
   size_t bytes = 0;
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
@@ -458,19 +521,20 @@ size_t lu_large_workspace(int64_t batch, int n, bool parts) {
   return bytes;
 }
 
-template <int MR, int PW>
+template <int MR, int PW, int NT, bool GLOBAL>
 static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int* src, float* X,
                       int* g0, bool fact, hipStream_t s) {
   const int nblk = N / PW;
+  constexpr int MAXM = MR < 1024 ? 1024 : MR;
   for (int blk = 0; blk < nblk; ++blk) {
     const int r0 = blk * PW;
-    hipLaunchKernelGGL((lu_panel_kernel<MR, PW>), dim3((unsigned)batch), dim3(256), 0, s, W, N, r0,
+    hipLaunchKernelGGL((lu_panel_kernel<MR, PW, NT, GLOBAL>), dim3((unsigned)batch), dim3(NT), 0, s, W, N, r0,
                        blk, piv, nsw, nblk, src, X, g0);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     const int nleft = fact ? (r0 + 63) / 64 : 0;
     const int nright = (N - r0 - PW + 63) / 64;
     if (nleft + nright > 0) {
-      hipLaunchKernelGGL((lu_urow_kernel<PW>), dim3(nleft + nright, (unsigned)batch), dim3(256), 0, s,
+      hipLaunchKernelGGL((lu_urow_kernel<PW, MAXM>), dim3(nleft + nright, (unsigned)batch), dim3(256), 0, s,
                          W, N, r0, src, X, nleft);
       if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     }
@@ -499,9 +563,9 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
                     size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s) {
   const int N = lu_large_padded(n);
-  const int PW = N <= 512 ? 64 : 32;
+  const int PW = lu_panel_width(N);
   const int nblk = N / PW;
-  if (N > 1024) return FX_ERR_UNSUPPORTED;
+  if (N > LU_LARGE_MAXN) return FX_ERR_UNSUPPORTED;
   if (ws_bytes < lu_large_workspace(batch, n, parts) || !ws) return FX_ERR_WORKSPACE;
   char* p = (char*)ws;
   auto take = [&](size_t x) {
@@ -530,11 +594,15 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   }
   int st;
   if (N <= 256)
-    st = run_blocks<256, 64>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<256, 64, 256, false>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   else if (N <= 512)
-    st = run_blocks<512, 64>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<512, 64, 256, false>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+  else if (N <= 1024)
+    st = run_blocks<1024, 32, 256, false>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+  else if (N <= 2048)
+    st = run_blocks<2048, 64, 512, true>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   else
-    st = run_blocks<1024, 32>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<4096, 64, 1024, true>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   if (st != FX_OK) return st;
   hipLaunchKernelGGL(lu_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, piv, nsw, N,
                      nblk, sign, logabs, batch);

@@ -237,7 +237,7 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(const float* __restrict_
                                                         const int* __restrict__ iperm, int n,
                                                         const int* __restrict__ bad, float* __restrict__ out,
                                                         const int* __restrict__ active, int accumulate) {
-  __shared__ __align__(16) float rowb[2048];
+  __shared__ __align__(16) float rowb[PF_LARGE_MAXN];
   const int64_t b = blockIdx.y;
   if (active && !active[b]) return;
   const int i = blockIdx.x;

@@ -1,15 +1,15 @@
-// Blocked Parlett-Reid with partial pivoting for 128 < n <= 2048 (any batch). The skew
-// matrix lives in one workspace buffer (full storage, exactly skew). Per block of
-// PB = 16 pair steps (32 columns) at r0:
+// Blocked Parlett-Reid with partial pivoting for 128 < n <= 4096 (any batch). The skew
+// matrix lives in one workspace buffer (full storage, exactly skew). Per block of PB
+// columns (PB / 2 pair steps; PB = 32, or 16 for N > 2048) at r0:
 //   1. pf_panel_kernel (one workgroup of NT = 256..1024 threads per matrix, each lane
-//      owning 2 of the m = N - r0 rows): the 16 pair steps with the tau / w vectors kept
-//      in registers as G (m x 32); column a and column p of the current matrix are read
+//      owning R = 2 (PB = 32) or 4 (PB = 16) of the m = N - r0 rows): the pair steps with
+//      the tau / w vectors kept in registers as G (m x PB); column a and column p of the current matrix are read
 //      as rows of the block-start matrix (skew) plus the G corrections; each pair step
 //      has two workgroup barriers (the row at position c, the pivot). The permutation is
 //      virtual inside the block; the kernel writes G in the block's new row order and
 //      the map src[new position] = old row;
 //   2. pf_update_kernel (matrix x lower-triangle 128x128 tile, in place):
-//      M'' = M[src, src] + G J G^T on fp32 MFMA (K = 32), the old entries read through the
+//      M'' = M[src, src] + G J G^T on fp32 MFMA (K = PB), the old entries read through the
 //      permutation, the new ones stored in the new order: the lower tile directly, its
 //      mirrored (negated) transpose through LDS, so both stores are coalesced and M'' stays
 //      exactly skew. In place is safe: a row that moves into a trailing position comes
@@ -22,7 +22,11 @@
 
 namespace fx {
 
-constexpr int PFB = 32;  // columns per block (16 pair steps)
+constexpr int PFB = 32;  // columns per block (16 pair steps) for N <= 2048
+constexpr int PFB_XL = 16;  // for 2048 < N <= PF_LARGE_MAXN
+
+// Columns per block for padded order N.
+static int pf_block_cols(int N) { return N > 2048 ? PFB_XL : PFB; }
 
 struct PfCand {
   unsigned key;
@@ -39,7 +43,7 @@ struct PfRowA {
 };
 
 // Copy a (B, n, n) into M (B, N, N): S = (a - a^T)/2 (or a) with [[0,1],[-1,0]] padding.
-// 32-bit index math (N <= 2048).
+// 32-bit index math within a matrix (N * N < 2^31).
 __global__ void pf_copy_pad_kernel(const float* __restrict__ A, int n, int skew, float* __restrict__ M, int N) {
   const int64_t b = blockIdx.y;
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
@@ -55,7 +59,7 @@ __global__ void pf_copy_pad_kernel(const float* __restrict__ A, int n, int skew,
   M[b * (int64_t)N * N + e] = v;
 }
 
-template <int NT>
+template <int NT, int R, int PB>
 __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ M, int N, int r0, int blk,
                                                       int nblk, float* __restrict__ d_out,
                                                       int* __restrict__ nsw_out,
@@ -63,7 +67,7 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
                                                       float* __restrict__ Gn,
                                                       int* __restrict__ orig,
                                                       float* __restrict__ gbuf) {
-  constexpr int R = 2, NW = NT / 64;
+  constexpr int NW = NT / 64;
   __shared__ PfRowA rowa;
   __shared__ PfCand cand[2][NW];
   __shared__ int posL[NT * R];
@@ -71,7 +75,7 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = N - r0;
   const float* Mb = M + b * (int64_t)N * N + (int64_t)r0 * N + r0;  // block-start trailing matrix
-  float G[R][PFB];
+  float G[R][PB];
   int pos[R];
   bool valid[R];
 #pragma unroll
@@ -80,10 +84,10 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     valid[s] = i < m;
     pos[s] = i;
 #pragma unroll
-    for (int k = 0; k < PFB; ++k) G[s][k] = 0.0f;
+    for (int k = 0; k < PB; ++k) G[s][k] = 0.0f;
   }
   int nsw = 0;
-  static_for<0, PFB / 2>([&](auto tc) {
+  static_for<0, PB / 2>([&](auto tc) {
     constexpr int t = decltype(tc)::value;
     const int c = 2 * t;  // local position of row a
     // 1. the row at position c publishes its index and G row
@@ -132,7 +136,7 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
       my.row = R * tid + ib;
       float xv = x[0];
       int pv = pos[0];
-      float gv[PFB];
+      float gv[PB];
 #pragma unroll
       for (int k = 0; k < 2 * t; ++k) gv[k] = G[0][k];
 #pragma unroll
@@ -199,9 +203,9 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     const int i = R * tid + s;
     if (valid[s]) {
       posL[i] = pos[s];
-      float* gr = Gn + (b * N + r0 + pos[s]) * (int64_t)PFB;
+      float* gr = Gn + (b * N + r0 + pos[s]) * (int64_t)PB;
 #pragma unroll
-      for (int k = 0; k < PFB; k += 4) *reinterpret_cast<float4*>(gr + k) = make_float4(G[s][k], G[s][k + 1], G[s][k + 2], G[s][k + 3]);
+      for (int k = 0; k < PB; k += 4) *reinterpret_cast<float4*>(gr + k) = make_float4(G[s][k], G[s][k + 1], G[s][k + 2], G[s][k + 3]);
       src_out[b * N + r0 + pos[s]] = r0 + i;
     }
   }
@@ -213,9 +217,9 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
 #pragma unroll
     for (int s = 0; s < R; ++s) {
       if (valid[s]) {
-        float* gr = gbuf + ((b * nblk + blk) * N + ov[s]) * (int64_t)PFB;
+        float* gr = gbuf + ((b * nblk + blk) * N + ov[s]) * (int64_t)PB;
 #pragma unroll
-        for (int k = 0; k < PFB; ++k) gr[k] = G[s][k];
+        for (int k = 0; k < PB; ++k) gr[k] = G[s][k];
       }
     }
     __syncthreads();
@@ -229,18 +233,19 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
 
 // M_new[p][q] = M_old[src p][src q] + sum_k G[p][k] (J G^T)[k][q] for the trailing
 // positions p, q >= r1 (lower tiles; the upper triangle by the negated transpose).
+template <int PB>
 __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, int N, int r1,
                                                         const int* __restrict__ src,
                                                         const float* __restrict__ Gn) {
   constexpr int T = 128, LDG = T + 4, LDT = 64 + 1;
+  constexpr int LDS_N = 2 * PB * LDG > T * LDT ? 2 * PB * LDG : T * LDT;
   typedef float v16f __attribute__((ext_vector_type(16)));
   // Ga / Hb: the G rows of the tile rows / (J G^T) columns of the tile columns, K-major;
   // after the MFMAs the same LDS holds half of the tile transposed (128 x 64)
-  __shared__ __align__(16) float lds[2 * PFB * LDG];
-  static_assert(T * LDT <= 2 * PFB * LDG, "transpose buffer fits");
+  __shared__ __align__(16) float lds[LDS_N];
   __shared__ int sp[T], sq[T];
   float* Ga = lds;
-  float* Hb = lds + PFB * LDG;
+  float* Hb = lds + PB * LDG;
   const int64_t b = blockIdx.y;
   const int t = blockIdx.x;
   int I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
@@ -249,24 +254,24 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
   const int J = t - I * (I + 1) / 2;
   const int p0 = r1 + T * I, q0 = r1 + T * J;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const float* G = Gn + b * (int64_t)N * PFB;
+  const float* G = Gn + b * (int64_t)N * PB;
   const int* sb = src + b * N;
-  float* Mb = M + b * (int64_t)N * N;  // entries addressed by 32-bit offsets (N <= 2048)
+  float* Mb = M + b * (int64_t)N * N;  // entries addressed by 32-bit offsets (N * N < 2^32)
   // fixed trip count, so every load is issued before the first store
-  constexpr int GE = T * PFB / 256;
+  constexpr int GE = T * PB / 256;
   float ga[GE], gb[GE];
 #pragma unroll
   for (int i = 0; i < GE; ++i) {
     const int e = tid + 256 * i;
-    const int r = e / PFB, k = e % PFB;
+    const int r = e / PB, k = e % PB;
     const int p = min(p0 + r, N - 1), q = min(q0 + r, N - 1);
-    ga[i] = G[(unsigned)(p * PFB + k)];
-    gb[i] = G[(unsigned)(q * PFB + (k ^ 1))];
+    ga[i] = G[(unsigned)(p * PB + k)];
+    gb[i] = G[(unsigned)(q * PB + (k ^ 1))];
   }
 #pragma unroll
   for (int i = 0; i < GE; ++i) {
     const int e = tid + 256 * i;
-    const int r = e / PFB, k = e % PFB;
+    const int r = e / PB, k = e % PB;
     Ga[k * LDG + r] = p0 + r < N ? ga[i] : 0.0f;
     const float gq = q0 + r < N ? gb[i] : 0.0f;
     Hb[k * LDG + r] = (k & 1) ? -gq : gq;
@@ -296,7 +301,7 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
       }
     }
 #pragma unroll
-  for (int kp = 0; kp < PFB / 2; ++kp) {
+  for (int kp = 0; kp < PB / 2; ++kp) {
     float av[2], bv[2];
 #pragma unroll
     for (int a = 0; a < 2; ++a) av[a] = Ga[(2 * kp + lh) * LDG + wr + 32 * a + l32];
@@ -387,11 +392,12 @@ int pf_large_padded(int n) { return ((n + 31) / 32) * 32; }
 
 size_t pf_large_workspace(int64_t batch, int n, bool fact) {
   const int N = pf_large_padded(n);
-  const int nblk = N / PFB;
+  const int PB = pf_block_cols(N);
+  const int nblk = N / PB;
   size_t bytes = 0;
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
   add((size_t)batch * N * N * 4);  // M (updated in place)
-  add((size_t)batch * N * PFB * 4);  // G (new order)
+  add((size_t)batch * N * PB * 4);  // G (new order)
   add((size_t)batch * N * 4);      // src
   add((size_t)batch * nblk * 4);   // swap counts
   add((size_t)batch * N / 2 * 4);  // d (forward only; parts uses its own)
@@ -399,15 +405,16 @@ size_t pf_large_workspace(int64_t batch, int n, bool fact) {
   return bytes;
 }
 
-// Forward (and, with gbuf/dout/perm, the factors: gbuf (B, N/32, N, 32) by original row,
+// Forward (and, with gbuf/dout/perm, the factors: gbuf (B, N/PB, N, PB) by original row,
 // d (B, N/2), perm (B, N) final position -> original row).
 int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
                     float* gbuf, float* dout, int* perm, void* ws, size_t ws_bytes, hipStream_t s) {
   const int N = pf_large_padded(n);
-  if (N > 2048) return FX_ERR_UNSUPPORTED;
+  if (N > PF_LARGE_MAXN) return FX_ERR_UNSUPPORTED;
   const bool fact = gbuf != nullptr;
   if (!ws || ws_bytes < pf_large_workspace(batch, n, fact)) return FX_ERR_WORKSPACE;
-  const int nblk = N / PFB;
+  const int PB = pf_block_cols(N);
+  const int nblk = N / PB;
   char* p = (char*)ws;
   auto take = [&](size_t x) {
     char* q = p;
@@ -415,7 +422,7 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     return (void*)q;
   };
   float* M0 = (float*)take((size_t)batch * N * N * 4);
-  float* Gn = (float*)take((size_t)batch * N * PFB * 4);
+  float* Gn = (float*)take((size_t)batch * N * PB * 4);
   int* src = (int*)take((size_t)batch * N * 4);
   int* nsw = (int*)take((size_t)batch * nblk * 4);
   float* dbuf = (float*)take((size_t)batch * N / 2 * 4);
@@ -436,25 +443,41 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
   }
   float* cur = M0;
   for (int blk = 0; blk < nblk; ++blk) {
-    const int r0 = blk * PFB;
+    const int r0 = blk * PB;
     const int m = N - r0;
-    if (m <= 512)
-      hipLaunchKernelGGL((pf_panel_kernel<256>), dim3((unsigned)batch), dim3(256), 0, s, cur, N, r0, blk, nblk, d,
-                         nsw, src, Gn, orig, gbuf);
-    else if (m <= 1024)
-      hipLaunchKernelGGL((pf_panel_kernel<512>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0, blk, nblk, d,
-                         nsw, src, Gn, orig, gbuf);
-    else
-      hipLaunchKernelGGL((pf_panel_kernel<1024>), dim3((unsigned)batch), dim3(1024), 0, s, cur, N, r0, blk, nblk,
-                         d, nsw, src, Gn, orig, gbuf);
+    if (PB == PFB) {
+      if (m <= 512)
+        hipLaunchKernelGGL((pf_panel_kernel<256, 2, PFB>), dim3((unsigned)batch), dim3(256), 0, s, cur, N, r0, blk,
+                           nblk, d, nsw, src, Gn, orig, gbuf);
+      else if (m <= 1024)
+        hipLaunchKernelGGL((pf_panel_kernel<512, 2, PFB>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0, blk,
+                           nblk, d, nsw, src, Gn, orig, gbuf);
+      else
+        hipLaunchKernelGGL((pf_panel_kernel<1024, 2, PFB>), dim3((unsigned)batch), dim3(1024), 0, s, cur, N, r0,
+                           blk, nblk, d, nsw, src, Gn, orig, gbuf);
+    } else {
+      if (m <= 1024)
+        hipLaunchKernelGGL((pf_panel_kernel<256, 4, PFB_XL>), dim3((unsigned)batch), dim3(256), 0, s, cur, N, r0,
+                           blk, nblk, d, nsw, src, Gn, orig, gbuf);
+      else if (m <= 2048)
+        hipLaunchKernelGGL((pf_panel_kernel<512, 4, PFB_XL>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0,
+                           blk, nblk, d, nsw, src, Gn, orig, gbuf);
+      else
+        hipLaunchKernelGGL((pf_panel_kernel<1024, 4, PFB_XL>), dim3((unsigned)batch), dim3(1024), 0, s, cur, N,
+                           r0, blk, nblk, d, nsw, src, Gn, orig, gbuf);
+    }
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    const int r1 = r0 + PFB;
+    const int r1 = r0 + PB;
     if (r1 < N) {
       const int nt = (N - r1 + 127) / 128;
       for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
         const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
-        hipLaunchKernelGGL(pf_update_kernel, dim3(nt * (nt + 1) / 2, (unsigned)nb), dim3(256), 0, s,
-                           cur + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PFB);
+        if (PB == PFB)
+          hipLaunchKernelGGL(pf_update_kernel<PFB>, dim3(nt * (nt + 1) / 2, (unsigned)nb), dim3(256), 0, s,
+                             cur + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PB);
+        else
+          hipLaunchKernelGGL(pf_update_kernel<PFB_XL>, dim3(nt * (nt + 1) / 2, (unsigned)nb), dim3(256), 0, s,
+                             cur + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PB);
         if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
       }
     }

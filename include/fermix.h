@@ -52,7 +52,8 @@ int32_t fx_pf_padded_size(int32_t n);
 
 /* ---------------------------------------------------------------- slogdet
  * sign[b], logabs[b] of det(a[b]) for b < batch: sign exactly +1 / -1, or 0 with
- * logabs = -inf for an exactly zero pivot.
+ * logabs = -inf for an exactly zero pivot. Sizes: every entry point of this header
+ * covers 0 <= n <= 4096 and returns FX_ERR_UNSUPPORTED above.
  * Replaces `_lu_core` (src/fermix/_lu.py:543-611) as called by `_slogdet_core`
  * (src/fermix/_diff.py:42-49); kernels K1-K4 of the reference (_lu.py:54-393). */
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n);
@@ -98,7 +99,7 @@ size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign,
                   float* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
-/* Columns per block of the Parlett-Reid factors (16 for n <= 128, 32 above). */
+/* Columns per block of the Parlett-Reid factors (16 for n <= 128, 32 for n <= 2048, 16 above). */
 int32_t fx_pf_block_columns(int32_t n);
 
 /* The Parlett-Reid factors P S' P^T = L D L^T of the same run (S' = S padded with
