@@ -32,11 +32,18 @@ def check_block(block):
 
 
 # n ranges -> kernel family (mirrors fx_slogdet_f32 / fx_slogpf_f32 dispatch)
+TINY_MAX_N = {"slogdet": 32, "slogpf": 16}  # several matrices per wave, one lane per row
 SMALL_MAX_N = 128  # fused one-workgroup-per-matrix kernels, matrix resident in LDS
+LARGE_MAX_N = 4096  # blocked kernels; larger n is unsupported
 
 
-def kernel_family(n):
-    """Name of the kernel family the library runs for order n."""
+def kernel_family(n, op="slogdet"):
+    """Name of the kernel family the library runs for order n ("slogdet" / "slogpf", the
+    same for their gradients)."""
+    if n <= TINY_MAX_N[op]:
+        return "tiny-wave"
     if n <= SMALL_MAX_N:
         return "fused-lds"
-    return "blocked"
+    if n <= LARGE_MAX_N:
+        return "blocked"
+    return "unsupported"

@@ -9,6 +9,18 @@ namespace fx {
 // dst[i] = src[i] for i < count: count a multiple of 4, both pointers 16-byte aligned.
 int launch_copy(const float* src, float* dst, int64_t count, hipStream_t s);
 
+// n <= TINY_MAXN (LU) / PF_TINY_MAXN (Parlett-Reid): several matrices per wave, one lane
+// per row (tiny.hip). Same outputs
+// and factor formats as the n <= 128 kernels below (N = tiny_padded(n) = 16 or 32),
+// which dispatch to them for these n.
+constexpr int TINY_MAXN = 32;     // LU
+constexpr int PF_TINY_MAXN = 16;  // Parlett-Reid
+int tiny_padded(int n);
+int launch_lu_tiny(const float* A, int n, int64_t batch, float* sign, float* logabs, float* lu, int* perm,
+                   hipStream_t s);
+int launch_pf_tiny(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs, float* gbuf, float* d,
+                   int* perm, hipStream_t s);
+
 // n <= 128 fused kernels (one workgroup per matrix).
 int lu_small_padded(int n);
 int pf_small_padded(int n);

@@ -264,8 +264,6 @@ template <bool FACT>
 static int dispatch(const float* A, int n, int64_t batch, float* sign, float* logabs, float* lu,
                     int* perm, hipStream_t s) {
   switch (lu_small_padded(n)) {
-    case 16: return launch_n<16, FACT>(A, n, batch, sign, logabs, lu, perm, s);
-    case 32: return launch_n<32, FACT>(A, n, batch, sign, logabs, lu, perm, s);
     case 48: return launch_n<48, FACT>(A, n, batch, sign, logabs, lu, perm, s);
     case 64: return launch_n<64, FACT>(A, n, batch, sign, logabs, lu, perm, s);
     case 80: return launch_n<80, FACT>(A, n, batch, sign, logabs, lu, perm, s);
@@ -278,6 +276,7 @@ static int dispatch(const float* A, int n, int64_t batch, float* sign, float* lo
 
 int launch_lu_small(const float* A, int n, int64_t batch, float* sign, float* logabs, float* lu,
                     int* perm, hipStream_t s) {
+  if (n <= TINY_MAXN) return launch_lu_tiny(A, n, batch, sign, logabs, lu, perm, s);
   if (lu) return dispatch<true>(A, n, batch, sign, logabs, lu, perm, s);
   return dispatch<false>(A, n, batch, sign, logabs, nullptr, nullptr, s);
 }

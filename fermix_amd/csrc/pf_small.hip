@@ -475,7 +475,6 @@ template <bool FACT>
 static int dispatch(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
                     float* gbuf, float* d, int* perm, hipStream_t s) {
   switch (pf_small_padded(n)) {
-    case 16: return launch_n<16, FACT>(A, n, skew, batch, sign, logabs, gbuf, d, perm, s);
     case 32: return launch_n<32, FACT>(A, n, skew, batch, sign, logabs, gbuf, d, perm, s);
     case 48: return launch_n<48, FACT>(A, n, skew, batch, sign, logabs, gbuf, d, perm, s);
     case 64: return launch_n<64, FACT>(A, n, skew, batch, sign, logabs, gbuf, d, perm, s);
@@ -489,6 +488,7 @@ static int dispatch(const float* A, int n, int skew, int64_t batch, float* sign,
 
 int launch_pf_small(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
                     float* gbuf, float* d, int* perm, hipStream_t s) {
+  if (n <= PF_TINY_MAXN) return launch_pf_tiny(A, n, skew, batch, sign, logabs, gbuf, d, perm, s);
   if (gbuf) return dispatch<true>(A, n, skew, batch, sign, logabs, gbuf, d, perm, s);
   return dispatch<false>(A, n, skew, batch, sign, logabs, nullptr, nullptr, nullptr, s);
 }

@@ -76,3 +76,5 @@ def test_tune_table():
     assert _tune.check_prec(None) == "ieee"
     assert _tune.check_prec("tf32x3") == "ieee"
     assert _tune.kernel_family(128) == "fused-lds"
+    assert _tune.kernel_family(32) == "tiny-wave" and _tune.kernel_family(32, "slogpf") == "fused-lds"
+    assert _tune.kernel_family(4096, "slogpf") == "blocked" and _tune.kernel_family(4097) == "unsupported"
