@@ -80,7 +80,7 @@ const char* fx_status_string(int status) {
   }
 }
 
-int fx_abi_version(void) { return 101; }
+int fx_abi_version(void) { return 102; }
 
 int32_t fx_lu_padded_size(int32_t n) {
   if (n <= 0) return 0;
