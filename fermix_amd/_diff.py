@@ -91,6 +91,7 @@ class _SlogdetParts(torch.autograd.Function):
     def setup_context(ctx, inputs, output):
         sign, logabs, invT = output
         ctx.mark_non_differentiable(sign, invT)
+        ctx.set_materialize_grads(False)  # no zero fills for the unused outputs
         ctx.save_for_backward(invT)
         ctx.save_for_forward(invT)
 
@@ -156,6 +157,7 @@ class _SlogpfParts(torch.autograd.Function):
     def setup_context(ctx, inputs, output):
         sign, logabs, Sinv = output
         ctx.mark_non_differentiable(sign, Sinv)
+        ctx.set_materialize_grads(False)  # no zero fills for the unused outputs
         ctx.save_for_backward(Sinv)
         ctx.save_for_forward(Sinv)
 
@@ -203,6 +205,7 @@ class _DetParts(torch.autograd.Function):
     def setup_context(ctx, inputs, output):
         _, adjT = output
         ctx.mark_non_differentiable(adjT)
+        ctx.set_materialize_grads(False)  # no zero fills for the unused outputs
         ctx.save_for_backward(adjT)
         ctx.save_for_forward(adjT)
 
@@ -247,6 +250,7 @@ class _PfParts(torch.autograd.Function):
     def setup_context(ctx, inputs, output):
         _, G = output
         ctx.mark_non_differentiable(G)
+        ctx.set_materialize_grads(False)  # no zero fills for the unused outputs
         ctx.save_for_backward(G)
         ctx.save_for_forward(G)
 

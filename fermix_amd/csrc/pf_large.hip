@@ -2,8 +2,8 @@
 // matrix lives in one workspace buffer (full storage, exactly skew). Per block of PB
 // columns (PB / 2 pair steps; PB = 32, or 16 for N > 2048) at r0:
 //   1. pf_panel_kernel (one workgroup of NT = 256..1024 threads per matrix, each lane
-//      owning R = 2 (PB = 32) or 4 (PB = 16) of the m = N - r0 rows): the pair steps with
-//      the tau / w vectors kept in registers as G (m x PB); column a and column p of the current matrix are read
+//      owning R = 2 or 4 of the m = N - r0 rows): the pair steps with the tau / w vectors
+//      kept in registers as G (m x PB); column a and column p of the current matrix are read
 //      as rows of the block-start matrix (skew) plus the G corrections; each pair step
 //      has two workgroup barriers (the row at position c, the pivot). The permutation is
 //      virtual inside the block; the kernel writes G in the block's new row order and
@@ -134,24 +134,16 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     if (lane == pl) {
       my.key = gk;
       my.row = R * tid + ib;
-      float xv = x[0];
-      int pv = pos[0];
-      float gv[PB];
+      // the winning slot's x, position and G row, written straight from that slot
 #pragma unroll
-      for (int k = 0; k < 2 * t; ++k) gv[k] = G[0][k];
-#pragma unroll
-      for (int s = 1; s < R; ++s) {
+      for (int s = 0; s < R; ++s) {
         if (ib == s) {
-          xv = x[s];
-          pv = pos[s];
+          my.pos = pos[s];
+          my.xv = x[s];
 #pragma unroll
-          for (int k = 0; k < 2 * t; ++k) gv[k] = G[s][k];
+          for (int k = 0; k < 2 * t; ++k) my.g[k] = G[s][k];
         }
       }
-      my.pos = pv;
-      my.xv = xv;
-#pragma unroll
-      for (int k = 0; k < 2 * t; ++k) my.g[k] = gv[k];
     }
     __syncthreads();
     unsigned best = cand[t & 1][0].key;
@@ -453,7 +445,7 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
         hipLaunchKernelGGL((pf_panel_kernel<512, 2, PFB>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0, blk,
                            nblk, d, nsw, src, Gn, orig, gbuf);
       else
-        hipLaunchKernelGGL((pf_panel_kernel<1024, 2, PFB>), dim3((unsigned)batch), dim3(1024), 0, s, cur, N, r0,
+        hipLaunchKernelGGL((pf_panel_kernel<512, 4, PFB>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0,
                            blk, nblk, d, nsw, src, Gn, orig, gbuf);
     } else {
       if (m <= 1024)
