@@ -50,7 +50,7 @@ struct PfSmall {
 static_assert(PfSmall<128>::LDS_BYTES <= 40960, "four n = 128 workgroups per CU");
 
 // Start of row p of the strictly lower triangle.
-__device__ __forceinline__ int tri_row(int p) { return (p * (p - 1)) >> 1; }
+__device__ __forceinline__ int tri_row(int p) { return (int)(__umul24((unsigned)p, (unsigned)(p - 1)) >> 1); }
 
 // Index of G element (row s, column k) in Gs.
 template <int N>
@@ -437,10 +437,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
           acc = mfma16(ga[j].z, gb[j].w, acc);
           acc = mfma16(ga[j].w, -gb[j].z, acc);
           const int q = Q[j] + li;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int p = P[j] + 4 * g + v;
-            if (p > q) T[tri_row(p) + q] = acc[v];
+          const int p0 = P[j] + 4 * g;
+          const int e0 = tri_row(p0) + q;  // tri_row(p0 + v) = tri_row(p0) + v p0 + v (v - 1) / 2
+          if (P[j] != Q[j]) {
+            // off-diagonal tile: every element lies below the diagonal
+            T[e0] = acc[0];
+            T[e0 + p0] = acc[1];
+            T[e0 + 2 * p0 + 1] = acc[2];
+            T[e0 + 3 * p0 + 3] = acc[3];
+          } else {
+            if (p0 > q) T[e0] = acc[0];
+            if (p0 + 1 > q) T[e0 + p0] = acc[1];
+            if (p0 + 2 > q) T[e0 + 2 * p0 + 1] = acc[2];
+            if (p0 + 3 > q) T[e0 + 3 * p0 + 3] = acc[3];
           }
         }
       }
