@@ -142,6 +142,8 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
   if (n > LARGE_MAX) return FX_ERR_UNSUPPORTED;
   if (!inv_t && n <= SMALL_MAX && lu)  // factors only: straight into the caller's buffers
     return launch_lu_small(a, n, batch, sign, logabs, lu, (int*)perm, s);
+  if (inv_t && !lu && n <= TINY_MAXN)  // one Gauss-Jordan pass, no workspace
+    return launch_lu_tiny_inv(a, n, batch, zero_singular ? 1 : 0, sign, logabs, inv_t, s);
   const size_t need = fx_slogdet_parts_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_lu_padded_size(n);

@@ -20,6 +20,9 @@ int launch_lu_tiny(const float* A, int n, int64_t batch, float* sign, float* log
                    hipStream_t s);
 int launch_pf_tiny(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs, float* gbuf, float* d,
                    int* perm, hipStream_t s);
+// sign / logabs (bit-identical to launch_lu_tiny) and A^-T in one pass (Gauss-Jordan).
+int launch_lu_tiny_inv(const float* A, int n, int64_t batch, int zero_singular, float* sign, float* logabs,
+                       float* invT, hipStream_t s);
 
 // n <= 128 fused kernels (one workgroup per matrix).
 int lu_small_padded(int n);

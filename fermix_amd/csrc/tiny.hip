@@ -154,6 +154,109 @@ __global__ __launch_bounds__(256) void lu_tiny_kernel(const float* __restrict__ 
   }
 }
 
+// Gauss-Jordan on [A | I] with the pivots of lu_tiny_kernel: sign / logabs bit-identical
+// to it (the unassigned rows take exactly its update) plus A^-T. Every other row i takes
+// row_i -= m_i row_p with m_i = a_i[j] / d~ (d~ = the pivot, 1 for an exact zero, as in
+// U~): for the unassigned rows this is the LU step, for the assigned ones the upward
+// elimination, and the augmented half collects E with E A~ = diag(d~) Pi, so row pos_i of
+// A~^-1 is (row i of E) / d~_{pos_i}. zero_singular zeroes members with a zero pivot;
+// members with a non-finite result are zeroed always (the slogdet gradient convention).
+template <int G>
+__global__ __launch_bounds__(256) void lu_tiny_inv_kernel(const float* __restrict__ A, int n, int vec, int64_t batch,
+                                                          int zero_singular, float* __restrict__ sign_out,
+                                                          float* __restrict__ logabs_out, float* __restrict__ invT) {
+  constexpr int MPW = 256 / G;
+  __shared__ __align__(16) float ubuf[256];
+  __shared__ __align__(16) float ebuf[256];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int r = tid % G;
+  const int gbase = lane - r;
+  float* const ub = ubuf + (tid - r);
+  float* const eb = ebuf + (tid - r);
+  const int64_t mi = (int64_t)blockIdx.x * MPW + tid / G;
+  const bool live = mi < batch;
+  const float* Ab = A + (live ? mi : 0) * (int64_t)n * n;
+  float a[G], e[G];
+  load_row<G>(a, Ab, n, r, live, vec);
+#pragma unroll
+  for (int k = 0; k < G; ++k) {
+    if (r >= n && k == r) a[k] = 1.0f;
+    e[k] = (k == r) ? 1.0f : 0.0f;
+  }
+  int pos = r;
+  int nsw = 0;
+  float mypiv = 1.0f;
+  static_for<0, G>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if (j < n) {
+      const bool cand = r < n && pos >= j;
+      const unsigned key = cand_key(a[j], cand);
+      const unsigned gk = group_max_u32<G>(key);
+      const int prow = group_first<G>(cand && key == gk, gbase);
+      const int pl = gbase + prow;
+      const float piv = __shfl(a[j], pl);
+      const int pp = __shfl(pos, pl);
+      if (r == prow) {
+#pragma unroll
+        for (int k = j + 1; k < G; ++k) ub[k] = a[k];
+#pragma unroll
+        for (int k = 0; k < G; k += 4) *reinterpret_cast<float4*>(eb + k) = make_float4(e[k], e[k + 1], e[k + 2], e[k + 3]);
+      }
+      wave_lds_fence();
+      const bool was_assigned = pos < j;
+      if (pos == j) pos = pp;
+      if (r == prow) pos = j;
+      nsw += (pp != j) ? 1 : 0;
+      if (r == j) mypiv = piv;
+      // d~: 1 for an exact zero pivot; a zero pivot column is zero on every unassigned
+      // row, so their multipliers stay 0 as in the LU
+      const float rcp = piv != 0.0f ? __builtin_amdgcn_rcpf(piv) : 1.0f;
+      if (r < n && r != prow && (pos > j || was_assigned)) {
+        const float l = a[j] * rcp;
+        a[j] = l;
+#pragma unroll
+        for (int k = j + 1; k < G; ++k) a[k] = fmaf(-l, ub[k], a[k]);
+#pragma unroll
+        for (int k = 0; k < G; k += 4) {
+          const float4 ev = *reinterpret_cast<const float4*>(eb + k);
+          e[k] = fmaf(-l, ev.x, e[k]);
+          e[k + 1] = fmaf(-l, ev.y, e[k + 1]);
+          e[k + 2] = fmaf(-l, ev.z, e[k + 2]);
+          e[k + 3] = fmaf(-l, ev.w, e[k + 3]);
+        }
+      }
+      wave_lds_fence();
+    }
+  });
+  const bool real = r < n;
+  const bool z = real && mypiv == 0.0f;
+  const float lg = group_sum_f32<G>((real && mypiv != 0.0f) ? logf(fabsf(mypiv)) : 0.0f);
+  const int anyz = group_first<G>(z, gbase) < G;
+  const unsigned long long nm = __ballot(real && mypiv < 0.0f);
+  const int negs = __popc((unsigned)(nm >> gbase) & (G == 32 ? 0xFFFFFFFFu : 0xFFFFu)) + nsw;
+  if (live && r == 0) {
+    sign_out[mi] = anyz ? 0.0f : ((negs & 1) ? -1.0f : 1.0f);
+    logabs_out[mi] = anyz ? -INFINITY : lg;
+  }
+  // row pos of A~^-1 = e / d~_pos, written as column pos of A^-T; d~_pos comes from the
+  // lane that holds pivot pos
+  const float dpos = __shfl(mypiv, gbase + pos);
+  const float s = dpos != 0.0f ? 1.0f / dpos : 1.0f;
+  bool nf = false;
+#pragma unroll
+  for (int k = 0; k < G; ++k) {
+    e[k] *= s;
+    nf = nf || (real && k < n && !isfinite(e[k]));
+  }
+  const bool bad = (group_first<G>(nf, gbase) < G) || (zero_singular && anyz);
+  if (live && real) {
+    float* ob = invT + mi * (int64_t)n * n + pos;
+#pragma unroll
+    for (int k = 0; k < G; ++k)
+      if (k < n) ob[(int64_t)k * n] = bad ? 0.0f : e[k];
+  }
+}
+
 // Skew row r of S (n x n): S = (A - A^T) / 2 if skew, else A; rows >= n (n even) are the
 // [[0, 1], [-1, 0]] padding.
 template <int G>
@@ -301,6 +404,20 @@ int launch_lu_tiny(const float* A, int n, int64_t batch, float* sign, float* log
 
 // Parlett-Reid for n <= PF_TINY_MAXN only: at G = 32 (two matrices per wave, three LDS
 // round trips per pair step) the one-workgroup-per-matrix kernel is faster.
+int launch_lu_tiny_inv(const float* A, int n, int64_t batch, int zero_singular, float* sign, float* logabs,
+                       float* invT, hipStream_t s) {
+  if (n < 1 || n > TINY_MAXN) return FX_ERR_UNSUPPORTED;
+  const int G = tiny_padded(n), vec = tiny_vec(A, n);
+  const unsigned blocks = (unsigned)((batch * G + 255) / 256);
+  if (G == 16)
+    hipLaunchKernelGGL((lu_tiny_inv_kernel<16>), dim3(blocks), dim3(256), 0, s, A, n, vec, batch, zero_singular, sign,
+                       logabs, invT);
+  else
+    hipLaunchKernelGGL((lu_tiny_inv_kernel<32>), dim3(blocks), dim3(256), 0, s, A, n, vec, batch, zero_singular, sign,
+                       logabs, invT);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
 int launch_pf_tiny(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs, float* gbuf, float* d,
                    int* perm, hipStream_t s) {
   if (n < 2 || n > PF_TINY_MAXN || (n & 1)) return FX_ERR_UNSUPPORTED;

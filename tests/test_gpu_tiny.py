@@ -13,7 +13,7 @@ import fermix_amd
 from fermix_amd import _kernels
 from oracle import generic as g
 from oracle import ref64
-from tests.tolerances import assert_logabs
+from tests.tolerances import assert_grad, assert_logabs
 
 pytestmark = pytest.mark.gpu
 
@@ -177,3 +177,53 @@ def test_pf_tiny_factors_reconstruct(dev, n):
             L[rows, a] = gbuf[b, k, og, 2 * t + 1] / d[b, s_]
             L[rows, p] = gbuf[b, k, og, 2 * t]
         assert np.abs(L @ D @ L.T - P).max() < 1e-4 * max(1.0, n / 16), (n, b)
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 8, 16, 20, 31, 32])
+@pytest.mark.parametrize("B", [1, 9, 33])
+def test_slogdet_tiny_gradient(dev, n, B):
+    """A^-T from the one-pass Gauss-Jordan kernel: against float64 and the oracle, the
+    primal bit-identical to the forward, unaligned input giving the same bits."""
+    rng = np.random.default_rng(9940 + 10 * n + B)
+    A = (rng.standard_normal((B, n, n)) + 2 * np.eye(n)).astype(np.float32)
+    s, l, invT, _, _ = _kernels.slogdet_parts(_t(A, dev))
+    s0, l0 = fermix_amd.slogdet(_t(A, dev))
+    assert torch.equal(s, s0) and torch.equal(l, l0), "parts primal != forward"
+    su, lu_, invu, _, _ = _kernels.slogdet_parts(_unaligned(A, dev))
+    assert torch.equal(su, s) and torch.equal(lu_, l) and torch.equal(invu, invT)
+    ref = np.linalg.inv(A.astype(np.float64)).swapaxes(-1, -2)
+    assert_grad(_np(invT), ref, A, f"tiny invT n={n} B={B}")
+    _, _, invo, _, _, _ = g.lu_parts_generic(A)
+    assert_grad(_np(invT), invo, A, f"tiny invT n={n} vs oracle")
+
+
+def test_slogdet_tiny_gradient_singular(dev):
+    """Exact zero pivots: zero gradient (zero_singular), or (zero_singular=False) the
+    finite inverse of A~ = P^T L U~. A~ depends on which row takes the zero pivot (this
+    library, like the reference's kernels, picks the lowest original row; LAPACK the
+    lowest current position), so it is checked against this library's LU -> inverse path
+    on the same pivots, and through the factorization-free property that A~ differs from
+    A in one column: I - A A~^-1 has rank one."""
+    rng = np.random.default_rng(9950)
+    for n in (4, 13, 16, 27):
+        A = rng.standard_normal((4, n, n)).astype(np.float32)
+        A[0, :, 2] = 0.0
+        A[2, n - 1, :] = 0.0
+        At = _t(A, dev).requires_grad_()
+        _, l = fermix_amd.slogdet(At)
+        (gr,) = torch.autograd.grad(l[1] + l[3], At)
+        gr = _np(gr)
+        assert np.all(np.isfinite(gr)) and np.all(gr[0] == 0) and np.all(gr[2] == 0)
+        ref = np.linalg.inv(A[[1, 3]].astype(np.float64)).swapaxes(-1, -2)
+        assert_grad(gr[[1, 3]], ref, A[[1, 3]], f"tiny singular batch n={n}")
+        _, _, inv2, _, _ = _kernels.slogdet_parts(_t(A, dev), zero_singular=False)
+        inv2 = _np(inv2)
+        # the general path (LU factors requested) runs the same pivots
+        _, _, inv3, _, _ = _kernels.slogdet_parts(_t(A, dev), zero_singular=False, want_lu=True)
+        inv3 = _np(inv3)
+        assert np.all(np.isfinite(inv2))
+        for b in (0, 2):
+            assert np.max(np.abs(inv2[b] - inv3[b])) <= 1e-4 * max(1.0, np.abs(inv3[b]).max())
+            D = np.eye(n) - A[b].astype(np.float64) @ inv2[b].T.astype(np.float64)
+            sv = np.linalg.svd(D, compute_uv=False)
+            assert sv[1] <= 1e-4 * (1.0 + sv[0]), (n, b, sv[:3])
