@@ -1,8 +1,9 @@
 // Blocked LU with partial pivoting for 128 < n <= 4096 (any batch): per block of PW
 // columns at r0 three launches,
 //   1. lu_panel_kernel  (one workgroup per matrix): the m x PW panel (m = N - r0) is
-//      factored in 16-column sub-panels, in LDS (N <= 1024) or in place in the work
-//      buffer (N > 1024: 512-1024 threads, 4 rows per lane, the sub-panel in registers). The rows stay in place during the
+//      factored in 16-column sub-panels, in LDS (N <= 256) or in place in the work
+//      buffer (512-1024 threads, 1-4 rows per lane, the sub-panel in registers; a few
+//      KiB of LDS, so several matrices share a CU). The rows stay in place during the
 //      panel (virtual pivoting); each column step finds the pivot with a per-wave DPP
 //      max and one workgroup barrier (every wave posts its best row, all waves pick the
 //      same winner), and the sub-panel's trailing columns inside the panel are updated
@@ -498,13 +499,10 @@ __global__ void iota_kernel(int* g0, int N, int64_t total) {
   if (e < total) g0[e] = (int)(e % N);
 }
 
-int lu_large_padded(int n) {
-  if (n <= 512 || n > 1024) return ((n + 63) / 64) * 64;
-  return ((n + 31) / 32) * 32;
-}
+int lu_large_padded(int n) { return ((n + 63) / 64) * 64; }
 
-// Panel width: 64 columns, except 32 for 512 < N <= 1024 (the LDS panel of 1024 rows).
-static int lu_panel_width(int N) { return (N > 512 && N <= 1024) ? 32 : 64; }
+// Panel width: 64 columns (the trailing products run at K = 64).
+static int lu_panel_width(int) { return 64; }
 
 size_t lu_large_workspace(int64_t batch, int n, bool parts) {
   const int N = lu_large_padded(n);
@@ -596,9 +594,9 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   if (N <= 256)
     st = run_blocks<256, 64, 256, false>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   else if (N <= 512)
-    st = run_blocks<512, 64, 256, false>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<512, 64, 512, true>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   else if (N <= 1024)
-    st = run_blocks<1024, 32, 256, false>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<1024, 64, 512, true>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   else if (N <= 2048)
     st = run_blocks<2048, 64, 512, true>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   else
