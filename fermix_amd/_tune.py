@@ -9,6 +9,9 @@ arithmetic). The table lives in the C library's dispatch (``fermix_amd/csrc/api.
 this module mirrors it for introspection and tests.
 """
 
+import contextlib
+import os
+
 # prec values accepted by the public API. "ieee": fp32 MFMA / FMA updates (the only
 # arithmetic of this build). "tf32x3" is accepted for drop-in compatibility with the
 # reference's float32 default: it exists there to reach fp32-level accuracy on tensor
@@ -36,10 +39,26 @@ TINY_MAX_N = {"slogdet": 32, "slogpf": 16}  # several matrices per wave, one lan
 SMALL_MAX_N = 128  # fused one-workgroup-per-matrix kernels, matrix resident in LDS
 LARGE_MAX_N = 4096  # blocked kernels; larger n is unsupported
 
+# The library's family override (read by every C entry point; the counterpart of the
+# reference's OVERRIDE hook, src/fermix/_common.py:363-378, which its tests use to force
+# a dispatch path, tests/test_fermix.py:720-762).
+ENV = "FERMIX_AMD_KERNELS"
+FAMILIES = {"tiny": "tiny-wave", "fused": "fused-lds", "blocked": "blocked"}
+
 
 def kernel_family(n, op="slogdet"):
     """Name of the kernel family the library runs for order n ("slogdet" / "slogpf", the
-    same for their gradients)."""
+    same for their gradients), honouring an active override."""
+    forced = os.environ.get(ENV, "")
+    if forced in FAMILIES:
+        if n > LARGE_MAX_N:
+            return "unsupported"
+        ok = {
+            "tiny": n <= TINY_MAX_N[op],
+            "fused": TINY_MAX_N[op] < n <= SMALL_MAX_N,
+            "blocked": True,
+        }[forced]
+        return FAMILIES[forced] if ok else "unsupported"
     if n <= TINY_MAX_N[op]:
         return "tiny-wave"
     if n <= SMALL_MAX_N:
@@ -47,3 +66,21 @@ def kernel_family(n, op="slogdet"):
     if n <= LARGE_MAX_N:
         return "blocked"
     return "unsupported"
+
+
+@contextlib.contextmanager
+def override(family):
+    """Force a kernel family ("tiny", "fused" or "blocked") for the calls made inside the
+    block (a size the family does not cover then raises FermixLibraryError). Sets the
+    library's environment variable for the process and restores it on exit."""
+    if family not in FAMILIES:
+        raise ValueError(f"family must be one of {sorted(FAMILIES)}, got {family!r}")
+    old = os.environ.get(ENV)
+    os.environ[ENV] = family
+    try:
+        yield
+    finally:
+        if old is None:
+            os.environ.pop(ENV, None)
+        else:
+            os.environ[ENV] = old

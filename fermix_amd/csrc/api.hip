@@ -1,6 +1,9 @@
 // C ABI entry points of the fermix_amd library: argument validation, size dispatch
 // (by n only, never by the batch, so a batched call and a vmapped one run the same
 // arithmetic), workspace accounting and kernel sequencing on the caller's stream.
+#include <stdlib.h>
+#include <string.h>
+
 #include "common.h"
 #include "fermix_internal.h"
 
@@ -63,6 +66,40 @@ static constexpr int SMALL_MAX = 128;
 static constexpr int LARGE_MAX = LU_LARGE_MAXN;
 static constexpr int PF_LARGE_MAX = PF_LARGE_MAXN;
 
+// Kernel families. The choice depends on n only (never on the batch), so a batched call
+// and a vmapped one run the same arithmetic: several matrices per wave (n <= 32 for the
+// LU, 16 for Parlett-Reid), one fused workgroup per matrix (n <= 128), blocked kernels
+// with workspace (n <= 4096). The environment variable FERMIX_AMD_KERNELS = tiny | fused
+// | blocked forces a family where it covers n (for cross-checks and tuning sweeps; an
+// uncovered n then reports FX_ERR_UNSUPPORTED). It is read on every call and the library
+// keeps no state of its own.
+enum { FAM_NONE = -1, FAM_TINY = 0, FAM_FUSED = 1, FAM_BLOCKED = 2 };
+
+static int family_override() {
+  const char* e = getenv("FERMIX_AMD_KERNELS");
+  if (!e || !*e) return FAM_NONE;
+  if (!strcmp(e, "tiny")) return FAM_TINY;
+  if (!strcmp(e, "fused")) return FAM_FUSED;
+  if (!strcmp(e, "blocked")) return FAM_BLOCKED;
+  return FAM_NONE;
+}
+
+// tiny_max: largest n of the tiny family for this factorisation; large_max: of the blocked.
+static int family(int n, int tiny_max, int large_max) {
+  if (n <= 0 || n > large_max) return FAM_NONE;
+  switch (family_override()) {
+    case FAM_TINY: return n <= tiny_max ? FAM_TINY : FAM_NONE;
+    case FAM_FUSED: return (n > tiny_max && n <= SMALL_MAX) ? FAM_FUSED : FAM_NONE;
+    case FAM_BLOCKED: return FAM_BLOCKED;
+    default: break;
+  }
+  if (n <= tiny_max) return FAM_TINY;
+  return n <= SMALL_MAX ? FAM_FUSED : FAM_BLOCKED;
+}
+
+static int lu_family(int n) { return family(n, TINY_MAXN, LARGE_MAX); }
+static int pf_family(int n) { return family(n, PF_TINY_MAXN, PF_LARGE_MAX); }
+
 }  // namespace fx
 
 using namespace fx;
@@ -84,20 +121,24 @@ int fx_abi_version(void) { return 102; }
 
 int32_t fx_lu_padded_size(int32_t n) {
   if (n <= 0) return 0;
-  if (n <= SMALL_MAX) return lu_small_padded(n);
-  return n <= LARGE_MAX ? lu_large_padded(n) : -1;
+  const int f = lu_family(n);
+  if (f == FAM_NONE) return -1;
+  return f == FAM_BLOCKED ? lu_large_padded(n) : lu_small_padded(n);
 }
 
 int32_t fx_pf_padded_size(int32_t n) {
   if (n <= 0) return 0;
-  if (n <= SMALL_MAX) return pf_small_padded(n);
-  return n <= PF_LARGE_MAX ? pf_large_padded(n) : -1;
+  const int f = pf_family(n);
+  if (f == FAM_NONE) return -1;
+  return f == FAM_BLOCKED ? pf_large_padded(n) : pf_small_padded(n);
 }
 
-int32_t fx_pf_block_columns(int32_t n) { return (n <= SMALL_MAX || pf_large_padded(n) > 2048) ? 16 : 32; }
+int32_t fx_pf_block_columns(int32_t n) {
+  return (pf_family(n) != FAM_BLOCKED || pf_large_padded(n) > 2048) ? 16 : 32;
+}
 
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {
-  if (batch <= 0 || n <= SMALL_MAX || n > LARGE_MAX) return 0;
+  if (batch <= 0 || lu_family(n) != FAM_BLOCKED) return 0;
   return lu_large_workspace(batch, n, false);
 }
 
@@ -108,21 +149,31 @@ int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float*
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
-  if (n <= SMALL_MAX) return launch_lu_small(a, n, batch, sign, logabs, nullptr, nullptr, s);
-  if (n <= LARGE_MAX)
-    return launch_lu_large(a, n, batch, sign, logabs, workspace, workspace_bytes, false, nullptr,
-                           nullptr, s);
-  return FX_ERR_UNSUPPORTED;
+  switch (lu_family(n)) {
+    case FAM_TINY: return launch_lu_tiny(a, n, batch, sign, logabs, nullptr, nullptr, s);
+    case FAM_FUSED: return launch_lu_small(a, n, batch, sign, logabs, nullptr, nullptr, s);
+    case FAM_BLOCKED:
+      return launch_lu_large(a, n, batch, sign, logabs, workspace, workspace_bytes, false, nullptr, nullptr, s);
+    default: return FX_ERR_UNSUPPORTED;
+  }
+}
+
+// The packed LU and row map of the tiny / fused families (no workspace; N = lu_small_padded).
+static int lu_fused_factors(int fam, const float* a, int n, int64_t batch, float* sign, float* logabs, float* lu,
+                            int* perm, hipStream_t s) {
+  return fam == FAM_TINY ? launch_lu_tiny(a, n, batch, sign, logabs, lu, perm, s)
+                         : launch_lu_small(a, n, batch, sign, logabs, lu, perm, s);
 }
 
 static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n) {
-  if (batch <= 0 || n <= 0 || n > LARGE_MAX) return 0;
+  const int fam = lu_family(n);
+  if (batch <= 0 || fam == FAM_NONE) return 0;
   const int N = fx_lu_padded_size(n);
   const bool copy = inv_padded(N) != N;
   size_t bytes = 0;
-  if (n <= SMALL_MAX) {
+  if (fam != FAM_BLOCKED) {
     bytes += align256((size_t)batch * N * N * 4) + align256((size_t)batch * N * 4);
   } else {
     bytes += align256(lu_large_workspace(batch, n, true));
@@ -139,10 +190,11 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
   if ((lu == nullptr) != (perm == nullptr)) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
-  if (n > LARGE_MAX) return FX_ERR_UNSUPPORTED;
-  if (!inv_t && n <= SMALL_MAX && lu)  // factors only: straight into the caller's buffers
-    return launch_lu_small(a, n, batch, sign, logabs, lu, (int*)perm, s);
-  if (inv_t && !lu && n <= TINY_MAXN)  // one Gauss-Jordan pass, no workspace
+  const int fam = lu_family(n);
+  if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (!inv_t && fam != FAM_BLOCKED && lu)  // factors only: straight into the caller's buffers
+    return lu_fused_factors(fam, a, n, batch, sign, logabs, lu, (int*)perm, s);
+  if (inv_t && !lu && fam == FAM_TINY)  // one Gauss-Jordan pass, no workspace
     return launch_lu_tiny_inv(a, n, batch, zero_singular ? 1 : 0, sign, logabs, inv_t, s);
   const size_t need = fx_slogdet_parts_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
@@ -151,12 +203,12 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
   float* LU = nullptr;
   int* g0 = nullptr;
   int st;
-  if (n <= SMALL_MAX) {
+  if (fam != FAM_BLOCKED) {
     LU = (float*)p;
     p += align256((size_t)batch * N * N * 4);
     g0 = (int*)p;
     p += align256((size_t)batch * N * 4);
-    st = launch_lu_small(a, n, batch, sign, logabs, LU, g0, s);
+    st = lu_fused_factors(fam, a, n, batch, sign, logabs, LU, g0, s);
   } else {
     const size_t wl = lu_large_workspace(batch, n, true);
     st = launch_lu_large(a, n, batch, sign, logabs, p, wl, true, &LU, &g0, s);
@@ -174,7 +226,7 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
 }
 
 size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n) {
-  if (batch <= 0 || n <= 0 || n > LARGE_MAX) return 0;
+  if (batch <= 0 || lu_family(n) == FAM_NONE) return 0;
   return fx_slogdet_parts_f32_workspace(batch, n) + align256(det_adjugate_workspace(batch, n));
 }
 
@@ -185,7 +237,8 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
   if (!sign || !logabs || (n > 0 && (!a || !adj_t))) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
-  if (n > LARGE_MAX) return FX_ERR_UNSUPPORTED;
+  const int fam = lu_family(n);
+  if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
   const size_t need = fx_det_parts_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_lu_padded_size(n);
@@ -193,12 +246,12 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
   float* LU = nullptr;
   int* g0 = nullptr;
   int st;
-  if (n <= SMALL_MAX) {
+  if (fam != FAM_BLOCKED) {
     LU = (float*)p;
     p += align256((size_t)batch * N * N * 4);
     g0 = (int*)p;
     p += align256((size_t)batch * N * 4);
-    st = launch_lu_small(a, n, batch, sign, logabs, LU, g0, s);
+    st = lu_fused_factors(fam, a, n, batch, sign, logabs, LU, g0, s);
   } else {
     const size_t wl = lu_large_workspace(batch, n, true);
     st = launch_lu_large(a, n, batch, sign, logabs, p, wl, true, &LU, &g0, s);
@@ -218,8 +271,14 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
 }
 
 size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n) {
-  if (batch <= 0 || n <= SMALL_MAX || n > PF_LARGE_MAX || n % 2) return 0;
+  if (batch <= 0 || n % 2 || pf_family(n) != FAM_BLOCKED) return 0;
   return pf_large_workspace(batch, n, false);
+}
+
+static int pf_fused(int fam, const float* a, int n, int sk, int64_t batch, float* sign, float* logabs, float* gbuf,
+                    float* d, int* perm, hipStream_t s) {
+  return fam == FAM_TINY ? launch_pf_tiny(a, n, sk, batch, sign, logabs, gbuf, d, perm, s)
+                         : launch_pf_small(a, n, sk, batch, sign, logabs, gbuf, d, perm, s);
 }
 
 int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign,
@@ -231,14 +290,14 @@ int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetr
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   if (n % 2 == 1) return fill2(sign, 0.0f, logabs, -INFINITY, batch, s);
   const int sk = skew_symmetrize ? 1 : 0;
-  if (n <= SMALL_MAX) return launch_pf_small(a, n, sk, batch, sign, logabs, nullptr, nullptr, nullptr, s);
-  if (n <= PF_LARGE_MAX)
-    return launch_pf_large(a, n, sk, batch, sign, logabs, nullptr, nullptr, nullptr, workspace, workspace_bytes, s);
-  return FX_ERR_UNSUPPORTED;
+  const int fam = pf_family(n);
+  if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (fam != FAM_BLOCKED) return pf_fused(fam, a, n, sk, batch, sign, logabs, nullptr, nullptr, nullptr, s);
+  return launch_pf_large(a, n, sk, batch, sign, logabs, nullptr, nullptr, nullptr, workspace, workspace_bytes, s);
 }
 
 size_t fx_slogpf_factors_f32_workspace(int64_t batch, int32_t n) {
-  if (batch <= 0 || n <= SMALL_MAX || n > PF_LARGE_MAX || n % 2) return 0;
+  if (batch <= 0 || n % 2 || pf_family(n) != FAM_BLOCKED) return 0;
   return pf_large_workspace(batch, n, true);
 }
 
@@ -251,18 +310,19 @@ int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew
   if (n == 0 || n % 2 == 1) return FX_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
   const int sk = skew_symmetrize ? 1 : 0;
-  if (n <= SMALL_MAX) return launch_pf_small(a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, s);
-  if (n <= PF_LARGE_MAX)
-    return launch_pf_large(a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, workspace, workspace_bytes, s);
-  return FX_ERR_UNSUPPORTED;
+  const int fam = pf_family(n);
+  if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (fam != FAM_BLOCKED) return pf_fused(fam, a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, s);
+  return launch_pf_large(a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, workspace, workspace_bytes, s);
 }
 
 size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n) {
-  if (batch <= 0 || n <= 0 || n % 2 || n > PF_LARGE_MAX) return 0;
+  const int fam = pf_family(n);
+  if (batch <= 0 || n % 2 || fam == FAM_NONE) return 0;
   const int N = fx_pf_padded_size(n);
   size_t bytes = align256((size_t)batch * N * N * 4) + align256((size_t)batch * N / 2 * 4) +
                  align256((size_t)batch * N * 4);
-  if (n > SMALL_MAX) bytes += align256(pf_large_workspace(batch, n, true));
+  if (fam == FAM_BLOCKED) bytes += align256(pf_large_workspace(batch, n, true));
   return bytes + pf_inverse_workspace(batch, N);
 }
 
@@ -279,7 +339,8 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
     if (st != FX_OK) return st;
     return fill(g, 0.0f, batch * (int64_t)n * n, s);
   }
-  if (n > PF_LARGE_MAX) return FX_ERR_UNSUPPORTED;
+  const int fam = pf_family(n);
+  if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
   const size_t need = fx_slogpf_parts_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_pf_padded_size(n);
@@ -292,8 +353,8 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
   p += align256((size_t)batch * N * 4);
   const int sk = skew_symmetrize ? 1 : 0;
   int st;
-  if (n <= SMALL_MAX) {
-    st = launch_pf_small(a, n, sk, batch, sign, logabs, gbuf, d, perm, s);
+  if (fam != FAM_BLOCKED) {
+    st = pf_fused(fam, a, n, sk, batch, sign, logabs, gbuf, d, perm, s);
   } else {
     const size_t wl = pf_large_workspace(batch, n, true);
     st = launch_pf_large(a, n, sk, batch, sign, logabs, gbuf, d, perm, p, wl, s);

@@ -16,7 +16,15 @@
  *    matching *_workspace function (0 means no workspace is needed; NULL allowed then);
  *  - the return value is a status code (FX_OK on success); numerical edge cases are
  *    encoded in the values (an exactly zero pivot gives sign 0 and logabs -inf);
- *  - calls are reentrant; the library keeps no mutable global state.
+ *  - calls are reentrant; the library keeps no mutable global state;
+ *  - the kernel family is chosen from n alone (never from the batch): several matrices
+ *    per wave (n <= 32 for slogdet, 16 for slogpf), one fused workgroup per matrix
+ *    (n <= 128), blocked kernels with workspace (n <= 4096). The environment variable
+ *    FERMIX_AMD_KERNELS = tiny | fused | blocked, read on every call, forces a family
+ *    where it covers n (FX_ERR_UNSUPPORTED elsewhere); the padded orders, block widths
+ *    and workspace sizes reported below follow it, so query them under the same setting
+ *    as the call. This replaces the reference's tuning-table OVERRIDE hook
+ *    (src/fermix/_common.py:363-378).
  */
 #ifndef FERMIX_AMD_H
 #define FERMIX_AMD_H

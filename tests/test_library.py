@@ -52,6 +52,20 @@ def test_host_only_calls():
     assert L.fx_det_parts_f32_workspace(4, 64) > L.fx_slogdet_parts_f32_workspace(4, 64)
 
 
+def test_family_override_sizes():
+    """The padded orders and workspaces follow the forced family (host-only queries)."""
+    L = _lib.lib()
+    assert L.fx_lu_padded_size(20) == 32 and L.fx_slogdet_f32_workspace(4, 20) == 0
+    with _tune.override("blocked"):
+        assert L.fx_lu_padded_size(20) == 64 and L.fx_pf_padded_size(20) == 32
+        assert L.fx_slogdet_f32_workspace(4, 20) > 0 and L.fx_pf_block_columns(20) == 32
+    with _tune.override("tiny"):
+        assert L.fx_lu_padded_size(40) == -1 and L.fx_pf_padded_size(20) == -1
+    with _tune.override("fused"):
+        assert L.fx_lu_padded_size(20) == -1 and L.fx_lu_padded_size(100) == 112
+    assert L.fx_lu_padded_size(20) == 32
+
+
 def test_api_errors():
     A = torch.zeros((2, 4, 4), dtype=torch.float32)
     with pytest.raises(TypeError):
