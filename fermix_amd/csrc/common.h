@@ -103,6 +103,19 @@ __device__ __forceinline__ float safe_rcp(float d) {
   return d != 0.0f ? __builtin_amdgcn_rcpf(d) : 0.0f;
 }
 
+// x unchanged, through an empty register constraint the optimiser cannot look into. Used
+// on values copied out of one of several per-row register arrays under a per-row
+// predicate: without it the copies merge into one copy from a selected address, which
+// indexes the arrays dynamically and moves them to scratch memory.
+__device__ __forceinline__ float opaque(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Materialise a running counter where it stands: otherwise the increments of a fully
+// unrolled loop can sink to the counter's single use, keeping every operand live.
+__device__ __forceinline__ void pin(int& x) { asm volatile("" : "+v"(x)); }
+
 // Pivots of one matrix collected across a wave: pivot g lives in slot g / 64 of lane
 // g % 64, so the logs and signs are formed once at the end, off the elimination's
 // dependency chain.

@@ -1,14 +1,18 @@
-// Blocked LU with partial pivoting for 128 < n <= 4096 (any batch): per block of PW
+// Blocked LU with partial pivoting for 128 < n <= 4096 (any batch): per block of PW = 64
 // columns at r0 three launches,
-//   1. lu_panel_kernel  (one workgroup per matrix): the m x PW panel (m = N - r0) is
-//      factored in 16-column sub-panels, in LDS (N <= 256) or in place in the work
-//      buffer (512-1024 threads, 1-4 rows per lane, the sub-panel in registers; a few
-//      KiB of LDS, so several matrices share a CU). The rows stay in place during the
-//      panel (virtual pivoting); each column step finds the pivot with a per-wave DPP
-//      max and one workgroup barrier (every wave posts its best row, all waves pick the
-//      same winner), and the sub-panel's trailing columns inside the panel are updated
-//      on MFMA (U = X * A_piv, A_rest -= L * U, stores predicated to unassigned rows).
-//      The panel is written back in the new row order, with the map
+//   1. the panel (one workgroup per matrix), factored in place in the work buffer; the
+//      rows stay in place during the panel (virtual pivoting) and each column step finds
+//      the pivot with a per-wave DPP max and one workgroup barrier (every wave posts its
+//      best row, all waves pick the same winner):
+//      - lu_panel_reg_kernel for m = N - r0 <= 1024: one row per lane (64..1024 threads,
+//        the smallest count that covers m), the whole 64-column row in registers; after
+//        each 16-column sub-panel the pivot rows publish their remaining columns in LDS,
+//        U = X * A_piv is formed there and every unassigned row applies A_rest -= L U
+//        with its own FMAs, so the panel is read once and written once;
+//      - lu_panel_kernel for taller panels: 2-4 rows per lane, one 16-column sub-panel in
+//        registers at a time, the trailing columns inside the panel updated on MFMA
+//        (stores predicated to unassigned rows);
+//      both write the panel back in the new row order, with the map
 //      src[new position] = old row and X_s = L_ss^-1 of every sub-panel;
 //   2. lu_urow_kernel   (matrix x 64-column strip): applies the row permutation to the
 //      strip, touching only the rows that move, and for trailing strips forms the U rows
@@ -28,7 +32,6 @@ template <int MR, int PW, int NT>
 struct LuPanel {
   static constexpr int NW = NT / 64;
   static constexpr int R = MR / NT;  // rows per lane
-  static constexpr int LDP = PW + 4;
   static constexpr int NSUB = PW / 16;
 };
 
@@ -50,11 +53,11 @@ __global__ void copy_pad_kernel(const float* __restrict__ A, int n, float* __res
   W[b * N * N + e] = (r < n && c < n) ? A[b * n * n + r * n + c] : (r == c ? 1.0f : 0.0f);
 }
 
-// GLOBAL = false: the panel is copied into LDS (MR * (PW + 4) floats); GLOBAL = true: the
-// panel is factored in place in the work buffer (rows in place until the final
-// permutation), for panels too tall for LDS -- the workgroup's own global accesses are
-// ordered by its barriers (one CU, workgroup-scope fences).
-template <int MR, int PW, int NT, bool GLOBAL>
+// Panels taller than one row per lane (m > 1024): factored in place in the work buffer
+// (rows in place until the final permutation), 16 columns at a time in registers -- the
+// workgroup's own global accesses are ordered by its barriers (one CU, workgroup-scope
+// fences).
+template <int MR, int PW, int NT>
 __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int N, int r0, int blk,
                                                       float* __restrict__ piv_out,
                                                       int* __restrict__ nsw_out, int nblk,
@@ -63,7 +66,6 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
                                                       int* __restrict__ g0) {
   using C = LuPanel<MR, PW, NT>;
   constexpr int R = C::R, NSUB = C::NSUB, NW = C::NW;
-  __shared__ float Plds[GLOBAL ? 1 : MR * C::LDP];
   __shared__ Cand cand[2][NW];
   __shared__ float Ubuf[16 * PW];
   __shared__ int posL[MR];
@@ -74,34 +76,9 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = N - r0;
   float* Wb = W + b * (int64_t)N * N;
-  float* const P = GLOBAL ? Wb + (int64_t)r0 * N + r0 : Plds;
-  const int LDP = GLOBAL ? N : C::LDP;
+  float* const P = Wb + (int64_t)r0 * N + r0;
+  const int LDP = N;
 
-  if (!GLOBAL) {
-    // load the panel: P[i][c] = W[r0 + i][r0 + c], 8 vector loads in flight per thread
-    // (rows past m read row r0 and are not stored)
-    for (int base = 0; base < m * (PW / 4); base += NT * 8) {
-      float4 v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int e = base + tid + NT * u;
-        const int i = e / (PW / 4), q = e % (PW / 4);
-        v[u] = *reinterpret_cast<const float4*>(Wb + (int64_t)(r0 + (i < m ? i : 0)) * N + r0 + 4 * q);
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int e = base + tid + NT * u;
-        const int i = e / (PW / 4), q = e % (PW / 4);
-        if (i < m) {
-          float* d = P + i * LDP + 4 * q;
-          d[0] = v[u].x;
-          d[1] = v[u].y;
-          d[2] = v[u].z;
-          d[3] = v[u].w;
-        }
-      }
-    }
-  }
   int pos[R];
   bool valid[R];
 #pragma unroll
@@ -116,27 +93,18 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
   for (int sp = 0; sp < NSUB; ++sp) {
     const int c0 = 16 * sp;
     float a[R][16];
-    if (GLOBAL) {
-      // 16-byte loads (r0, c0 and N are multiples of 16); rows past m read row 0
+    // 16-byte loads (r0, c0 and N are multiples of 16); rows past m read row 0
 #pragma unroll
-      for (int s = 0; s < R; ++s) {
-        const int i = R * tid + s;
-        const float4* rp = reinterpret_cast<const float4*>(P + (int64_t)(valid[s] ? i : 0) * LDP + c0);
+    for (int s = 0; s < R; ++s) {
+      const int i = R * tid + s;
+      const float4* rp = reinterpret_cast<const float4*>(P + (int64_t)(valid[s] ? i : 0) * LDP + c0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 v = rp[q];
-          a[s][4 * q] = valid[s] ? v.x : 0.0f;
-          a[s][4 * q + 1] = valid[s] ? v.y : 0.0f;
-          a[s][4 * q + 2] = valid[s] ? v.z : 0.0f;
-          a[s][4 * q + 3] = valid[s] ? v.w : 0.0f;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < R; ++s) {
-        const int i = R * (64 * wave + lane) + s;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) a[s][j] = valid[s] ? P[i * LDP + c0 + j] : 0.0f;
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = rp[q];
+        a[s][4 * q] = valid[s] ? v.x : 0.0f;
+        a[s][4 * q + 1] = valid[s] ? v.y : 0.0f;
+        a[s][4 * q + 2] = valid[s] ? v.z : 0.0f;
+        a[s][4 * q + 3] = valid[s] ? v.w : 0.0f;
       }
     }
     static_for<0, 16>([&](auto jc) {
@@ -154,22 +122,15 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
       Cand& my = cand[j & 1][wave];
       if (lane == pl) {
         my.key = gk;
-        float v[16];
+        my.row = R * (64 * wave + lane) + ib;
 #pragma unroll
-        for (int jj = 0; jj < 16; ++jj) v[jj] = a[0][jj];
-        int pv = pos[0];
-#pragma unroll
-        for (int s = 1; s < R; ++s) {
+        for (int s = 0; s < R; ++s) {
           if (ib == s) {
+            my.pos = pos[s];
 #pragma unroll
-            for (int jj = 0; jj < 16; ++jj) v[jj] = a[s][jj];
-            pv = pos[s];
+            for (int jj = 0; jj < 16; ++jj) my.v[jj] = opaque(a[s][jj]);
           }
         }
-        my.row = R * (64 * wave + lane) + ib;
-        my.pos = pv;
-#pragma unroll
-        for (int jj = 0; jj < 16; ++jj) my.v[jj] = v[jj];
       }
       __syncthreads();
       unsigned best = cand[j & 1][0].key;
@@ -194,6 +155,7 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
         if (i == prow) pos[s] = posc;
       }
       nsw += (pp != posc) ? 1 : 0;
+      pin(nsw);
       const float pivv = u[j];
       if (wave == 0 && lane == 0) piv_out[b * N + r0 + posc] = pivv;
       const float rcp = safe_rcp(pivv);
@@ -211,15 +173,10 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
     for (int s = 0; s < R; ++s) {
       const int i = R * (64 * wave + lane) + s;
       if (valid[s]) {
-        if (GLOBAL) {
-          float4* rp = reinterpret_cast<float4*>(P + (int64_t)i * LDP + c0);
+        float4* rp = reinterpret_cast<float4*>(P + (int64_t)i * LDP + c0);
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            rp[q] = make_float4(a[s][4 * q], a[s][4 * q + 1], a[s][4 * q + 2], a[s][4 * q + 3]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) P[i * LDP + c0 + j] = a[s][j];
-        }
+        for (int q = 0; q < 4; ++q)
+          rp[q] = make_float4(a[s][4 * q], a[s][4 * q + 1], a[s][4 * q + 2], a[s][4 * q + 3]);
         posL[i] = pos[s];
       }
     }
@@ -289,37 +246,34 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
       __syncthreads();
     }
   }
-  // write the panel back in the new row order
-  if (GLOBAL) {
-    // in place, 16 columns at a time: every row of a pass is read before any is written
-    for (int q = 0; q < NSUB; ++q) {
-      float4 v[R][4];
+  // write the panel back in the new row order, in place, 16 columns at a time: every row
+  // of a pass is read before any is written
+  for (int q = 0; q < NSUB; ++q) {
+    float v[R][16];  // plain floats: an array of float4 stays in scratch memory
 #pragma unroll
-      for (int s = 0; s < R; ++s) {
-        const int i = R * tid + s;
-        const float4* rp = reinterpret_cast<const float4*>(P + (int64_t)(i < m ? i : 0) * LDP + 16 * q);
+    for (int s = 0; s < R; ++s) {
+      const int i = R * tid + s;
+      const float4* rp = reinterpret_cast<const float4*>(P + (int64_t)(i < m ? i : 0) * LDP + 16 * q);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) v[s][k] = rp[k];
+      for (int k = 0; k < 4; ++k) {
+        const float4 t = rp[k];
+        v[s][4 * k] = t.x;
+        v[s][4 * k + 1] = t.y;
+        v[s][4 * k + 2] = t.z;
+        v[s][4 * k + 3] = t.w;
       }
-      __syncthreads();
+    }
+    __syncthreads();
 #pragma unroll
-      for (int s = 0; s < R; ++s) {
-        const int i = R * tid + s;
-        if (i < m) {
-          float4* wp = reinterpret_cast<float4*>(P + (int64_t)posL[i] * LDP + 16 * q);
+    for (int s = 0; s < R; ++s) {
+      const int i = R * tid + s;
+      if (i < m) {
+        float4* wp = reinterpret_cast<float4*>(P + (int64_t)posL[i] * LDP + 16 * q);
 #pragma unroll
-          for (int k = 0; k < 4; ++k) wp[k] = v[s][k];
-        }
+        for (int k = 0; k < 4; ++k) wp[k] = make_float4(v[s][4 * k], v[s][4 * k + 1], v[s][4 * k + 2], v[s][4 * k + 3]);
       }
-      __syncthreads();
     }
-  } else {
-    for (int e = tid; e < m * (PW / 4); e += NT) {
-      const int i = e / (PW / 4), q = e % (PW / 4);
-      const float* sp_ = P + i * LDP + 4 * q;
-      *reinterpret_cast<float4*>(Wb + (int64_t)(r0 + posL[i]) * N + r0 + 4 * q) =
-          make_float4(sp_[0], sp_[1], sp_[2], sp_[3]);
-    }
+    __syncthreads();
   }
   for (int i = tid; i < m; i += NT) src_out[b * N + r0 + posL[i]] = r0 + i;
   if (g0) {
@@ -337,6 +291,171 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
       const int i = tid + NT * q;
       if (i < m) gb[r0 + posL[i]] = tmp[q];
     }
+  }
+  if (tid == 0) nsw_out[b * nblk + blk] = nsw;
+}
+
+// The same panel (PW = 64, in place in the work buffer) for m <= NT with one row per lane
+// and the whole 64-column row in registers: the column steps are those of
+// lu_panel_kernel, but after each sub-panel the 16 pivot rows publish their remaining
+// columns in LDS, U = X * (those columns) is formed there, and every unassigned row
+// applies A_rest -= L U with its own FMAs (pivot rows take their U row). The panel is
+// read once and written once, in the new row order, with no global round trip between.
+template <int NT>
+__global__ __launch_bounds__(NT) void lu_panel_reg_kernel(float* __restrict__ W, int N, int r0, int blk,
+                                                          float* __restrict__ piv_out,
+                                                          int* __restrict__ nsw_out, int nblk,
+                                                          int* __restrict__ src_out,
+                                                          float* __restrict__ X_out,
+                                                          int* __restrict__ g0) {
+  constexpr int NW = NT / 64, PW = 64, NSUB = 4;
+  __shared__ Cand cand[2][NW];
+  __shared__ __align__(16) float Prow[16 * PW];  // pivot rows of the sub-panel, all columns
+  __shared__ __align__(16) float Ubuf[16 * PW];
+  __shared__ float Xs[256];
+  __shared__ float L11s[256];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int m = N - r0;
+  float* Wb = W + b * (int64_t)N * N;
+  float* const P = Wb + (int64_t)r0 * N + r0;
+  const bool valid = tid < m;
+  int pos = tid;
+  float a[PW];
+  {
+    // 16-byte loads (r0 and N are multiples of 64); lanes past m read row 0
+    const float4* rp = reinterpret_cast<const float4*>(P + (int64_t)(valid ? tid : 0) * N);
+#pragma unroll
+    for (int q = 0; q < PW / 4; ++q) {
+      const float4 v = rp[q];
+      a[4 * q] = valid ? v.x : 0.0f;
+      a[4 * q + 1] = valid ? v.y : 0.0f;
+      a[4 * q + 2] = valid ? v.z : 0.0f;
+      a[4 * q + 3] = valid ? v.w : 0.0f;
+    }
+  }
+  int nsw = 0;
+  static_for<0, NSUB>([&](auto spc) {
+    constexpr int c0 = 16 * decltype(spc)::value;
+    static_for<0, 16>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      constexpr int col = c0 + j;
+      const unsigned kb = cand_key(a[col], valid && pos >= col);
+      const unsigned gk = wave_max_u32(kb);
+      const int pl = first_lane(gk != 0u ? (kb == gk) : (lane == 0));
+      Cand& my = cand[j & 1][wave];
+      if (lane == pl) {
+        my.key = gk;
+        my.row = tid;
+        my.pos = pos;
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) my.v[jj] = a[c0 + jj];
+      }
+      __syncthreads();
+      unsigned best = cand[j & 1][0].key;
+      int wb = 0;
+#pragma unroll
+      for (int w = 1; w < NW; ++w) {
+        const unsigned kw = cand[j & 1][w].key;
+        if (kw > best) { best = kw; wb = w; }
+      }
+      const Cand& win = cand[j & 1][wb];
+      float u[16];
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) u[jj] = win.v[jj];
+      const int pp = win.pos, prow = win.row;
+      if (tid < j) L11s[j * 16 + tid] = win.v[tid];
+      if (valid && pos == col) pos = pp;
+      if (tid == prow) pos = col;
+      nsw += (pp != col) ? 1 : 0;
+      pin(nsw);
+      const float pivv = u[j];
+      if (tid == 0) piv_out[b * N + r0 + col] = pivv;
+      const float rcp = safe_rcp(pivv);
+      if (valid && pos > col) {
+        const float l = a[col] * rcp;
+        a[col] = l;
+        static_for<j + 1, 16>([&](auto cc) { a[c0 + cc.value] = fmaf(-l, u[cc.value], a[c0 + cc.value]); });
+      }
+    });
+    if constexpr (c0 + 16 < PW) {
+      // the sub-panel's pivot rows publish their remaining columns
+      if (valid && pos >= c0 && pos < c0 + 16) {
+        float* pr = Prow + (pos - c0) * PW;
+#pragma unroll
+        for (int c = c0 + 16; c < PW; c += 4) *reinterpret_cast<float4*>(pr + c) = make_float4(a[c], a[c + 1], a[c + 2], a[c + 3]);
+      }
+    }
+    __syncthreads();
+    // X = L11^-1 (unit lower): lane c < 16 of wave 0 forms column c,
+    // X[j][c] = -sum_{k<j} L11[j][k] X[k][c], X[c][c] = 1, X[j][c] = 0 for j < c
+    if (wave == 0 && lane < 16) {
+      float xcol[16];
+      static_for<0, 16>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        float x = 0.0f;
+        static_for<0, j>([&](auto kc) { x = fmaf(-L11s[j * 16 + kc.value], xcol[kc.value], x); });
+        xcol[j] = (lane == j) ? 1.0f : x;
+      });
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        Xs[k * 16 + lane] = xcol[k];
+        X_out[((b * NSUB + c0 / 16) * 16 + k) * 16 + lane] = xcol[k];
+      }
+    }
+    if constexpr (c0 + 16 < PW) {
+      constexpr int NC = PW - c0 - 16;  // columns right of the sub-panel
+      __syncthreads();
+      // U = X * Prow[:, c0+16 ..] (X unit lower: terms t <= k)
+      for (int e = tid; e < 16 * NC; e += NT) {
+        const int k = e / NC, c = c0 + 16 + e % NC;
+        float s = Prow[k * PW + c];
+        for (int t = 0; t < k; ++t) s = fmaf(Xs[k * 16 + t], Prow[t * PW + c], s);
+        Ubuf[k * PW + c] = s;
+      }
+      __syncthreads();
+      if (valid && pos > c0 + 15) {
+        // A_rest -= L U on the unassigned rows (U rows broadcast from LDS)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const float l = a[c0 + k];
+#pragma unroll
+          for (int c = c0 + 16; c < PW; c += 4) {
+            const float4 uv = *reinterpret_cast<const float4*>(Ubuf + k * PW + c);
+            a[c] = fmaf(-l, uv.x, a[c]);
+            a[c + 1] = fmaf(-l, uv.y, a[c + 1]);
+            a[c + 2] = fmaf(-l, uv.z, a[c + 2]);
+            a[c + 3] = fmaf(-l, uv.w, a[c + 3]);
+          }
+        }
+      } else if (valid && pos >= c0) {
+        // pivot rows take their U row
+        const float* ur = Ubuf + (pos - c0) * PW;
+#pragma unroll
+        for (int c = c0 + 16; c < PW; c += 4) {
+          const float4 uv = *reinterpret_cast<const float4*>(ur + c);
+          a[c] = uv.x;
+          a[c + 1] = uv.y;
+          a[c + 2] = uv.z;
+          a[c + 3] = uv.w;
+        }
+      }
+    }
+  });
+  // the panel back in the new row order (every row was read at the start, many barriers
+  // ago, so the in-place stores cannot overwrite an unread row)
+  if (valid) {
+    float4* wp = reinterpret_cast<float4*>(P + (int64_t)pos * N);
+#pragma unroll
+    for (int q = 0; q < PW / 4; ++q) wp[q] = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+    src_out[b * N + r0 + pos] = r0 + tid;
+  }
+  if (g0) {
+    // compose the row map: g0[r0 + p] <- g0[r0 + src(p)]
+    int* gb = g0 + b * N;
+    const int t0 = valid ? gb[r0 + tid] : 0;
+    __syncthreads();
+    if (valid) gb[r0 + pos] = t0;
   }
   if (tid == 0) nsw_out[b * nblk + blk] = nsw;
 }
@@ -519,15 +638,31 @@ size_t lu_large_workspace(int64_t batch, int n, bool parts) {
   return bytes;
 }
 
-template <int MR, int PW, int NT, bool GLOBAL>
+// MR: the largest m of the matrix's panels; panels with m > 1024 (MR > 1024 only) use
+// lu_panel_kernel with NT threads, the others lu_panel_reg_kernel.
+template <int MR, int NT>
 static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int* src, float* X,
                       int* g0, bool fact, hipStream_t s) {
+  constexpr int PW = 64;
   const int nblk = N / PW;
   constexpr int MAXM = MR < 1024 ? 1024 : MR;
   for (int blk = 0; blk < nblk; ++blk) {
     const int r0 = blk * PW;
-    hipLaunchKernelGGL((lu_panel_kernel<MR, PW, NT, GLOBAL>), dim3((unsigned)batch), dim3(NT), 0, s, W, N, r0,
-                       blk, piv, nsw, nblk, src, X, g0);
+    const int m = N - r0;
+    if (m <= 1024) {
+#define FX_PANEL_REG(T)                                                                                       \
+  hipLaunchKernelGGL((lu_panel_reg_kernel<T>), dim3((unsigned)batch), dim3(T), 0, s, W, N, r0, blk, piv, nsw, \
+                     nblk, src, X, g0)
+      if (m <= 64) FX_PANEL_REG(64);
+      else if (m <= 128) FX_PANEL_REG(128);
+      else if (m <= 256) FX_PANEL_REG(256);
+      else if (m <= 512) FX_PANEL_REG(512);
+      else FX_PANEL_REG(1024);
+#undef FX_PANEL_REG
+    } else if constexpr (MR > 1024) {
+      hipLaunchKernelGGL((lu_panel_kernel<MR, PW, NT>), dim3((unsigned)batch), dim3(NT), 0, s, W, N, r0, blk, piv,
+                         nsw, nblk, src, X, g0);
+    }
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     const int nleft = fact ? (r0 + 63) / 64 : 0;
     const int nright = (N - r0 - PW + 63) / 64;
@@ -591,16 +726,12 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
     hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, g0, N, tot);
   }
   int st;
-  if (N <= 256)
-    st = run_blocks<256, 64, 256, false>(W, N, batch, piv, nsw, src, X, g0, parts, s);
-  else if (N <= 512)
-    st = run_blocks<512, 64, 512, true>(W, N, batch, piv, nsw, src, X, g0, parts, s);
-  else if (N <= 1024)
-    st = run_blocks<1024, 64, 512, true>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+  if (N <= 1024)
+    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   else if (N <= 2048)
-    st = run_blocks<2048, 64, 512, true>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   else
-    st = run_blocks<4096, 64, 1024, true>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, src, X, g0, parts, s);
   if (st != FX_OK) return st;
   hipLaunchKernelGGL(lu_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, piv, nsw, N,
                      nblk, sign, logabs, batch);

@@ -100,7 +100,7 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
       if (valid[s] && pos[s] == c) {
         rowa.row = R * tid + s;
 #pragma unroll
-        for (int k = 0; k < 2 * t; ++k) rowa.g[k] = G[s][k];
+        for (int k = 0; k < 2 * t; ++k) rowa.g[k] = opaque(G[s][k]);
       }
     }
     __syncthreads();
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
           my.pos = pos[s];
           my.xv = x[s];
 #pragma unroll
-          for (int k = 0; k < 2 * t; ++k) my.g[k] = G[s][k];
+          for (int k = 0; k < 2 * t; ++k) my.g[k] = opaque(G[s][k]);
         }
       }
     }
@@ -166,6 +166,7 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
       if (R * tid + s == qp) pos[s] = c + 1;
     }
     nsw += (pp != c + 1) ? 1 : 0;
+    pin(nsw);
     if (tid == 0) d_out[b * (N / 2) + (r0 >> 1) + t] = d;
     // y = column p on my rows
     float y[R];
