@@ -6,8 +6,9 @@
 // src/fermix/_inverse.py:230-426) and the trailing GEMMs of the LU / Parlett-Reid
 // (src/fermix/_lu.py:334-393, src/fermix/_pf.py:287-382).
 //
-// Design (gfx950): a workgroup of 4 waves computes a BM x BN tile (64 x 64 in use); each
-// wave owns a (BM/2) x (BN/2) quarter as 32x32 MFMA accumulators. K advances in BK = 16 stages
+// Design (gfx950): a workgroup of 4 waves computes a BM x BN tile (64 x 64, or 128 x 128
+// in gemm128_kernel for the products with M, N >= 1024); each wave owns a (BM/2) x (BN/2)
+// quarter as 32x32 MFMA accumulators. K advances in BK = 16 stages
 // staged through LDS K-major (so every MFMA operand read is 32 consecutive floats),
 // double-buffered, with the next stage's global loads in flight during the current
 // stage's MFMAs.
@@ -42,7 +43,9 @@ __device__ __forceinline__ bool mask_upper(int m) { return m == MASK_UPPER || m 
 // Tile loads: VEC uses 16-byte global loads along the operand's contiguous dimension
 // (requires that dimension, the leading dimensions, batch strides and base pointers to be
 // multiples of 4 floats), otherwise one float per load. Masks are applied in registers.
-template <int BM, int BN, bool VEC>
+// PREC: beta != 0 with C read before the K loop, so the read latency overlaps the
+// products (the LU trailing update, K = 64: 12 % faster at m = 448).
+template <int BM, int BN, bool VEC, bool PREC>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   constexpr int LDSA = BM + 4, LDSB = BN + 4;
   constexpr int WM = BM / 2, WN = BN / 2;   // per-wave quarter
@@ -93,6 +96,23 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   if (mask_lower(d.maskB)) klo = max(klo, j0 + d.offBc - d.offBr);
   if (mask_upper(d.maskB)) khi = min(khi, j0 + BN + d.offBc - d.offBr);
   klo = max(0, (klo / GBK) * GBK);
+
+  // A stage is plain when no element of it needs a bound or mask fix (a uniform test):
+  // an interior tile, a full K stage, and both operands' stage blocks strictly inside
+  // their triangles. Plain stages skip the per-element fixes, which otherwise dominate
+  // the instruction count of a stage.
+  const bool interior = i0 + BM <= d.M && j0 + BN <= d.N;
+  auto plain_stage = [&](int k0) {
+    if (!VEC || !interior || k0 + GBK > d.K) return false;
+    bool ok = true;
+    if (d.maskA == MASK_LOWER_UNIT) ok = ok && i0 + d.offAr > k0 + GBK - 1 + d.offAc;
+    if (d.maskA == MASK_UPPER) ok = ok && i0 + BM - 1 + d.offAr <= k0 + d.offAc;
+    if (d.maskA == MASK_UPPER_UNIT) ok = ok && i0 + BM - 1 + d.offAr < k0 + d.offAc;
+    if (d.maskB == MASK_LOWER_UNIT) ok = ok && k0 + d.offBr > j0 + BN - 1 + d.offBc;
+    if (d.maskB == MASK_UPPER) ok = ok && k0 + GBK - 1 + d.offBr <= j0 + d.offBc;
+    if (d.maskB == MASK_UPPER_UNIT) ok = ok && k0 + GBK - 1 + d.offBr < j0 + d.offBc;
+    return ok;
+  };
 
   const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
   const int l32 = lane & 31, lh = lane >> 5;
@@ -178,7 +198,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   };
   // registers -> LDS, K-major (As[k][i], Bs[k][j]) so each MFMA operand read is 32
   // consecutive floats
-  auto store_stage = [&](int buf, int k0) {
+  auto store_stage = [&](int buf, int k0, bool plain) {
     if constexpr (VEC) {
 #pragma unroll
       for (int e = 0; e < AV; ++e) {
@@ -187,10 +207,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
         a_coord(idx, k0, gi, gk);
         const int dr = d.transA, dc = 1 - d.transA;  // step of the vector's components
         float4 v = va[e];
-        v.x = fixA(v.x, gi, gk);
-        v.y = fixA(v.y, gi + dr, gk + dc);
-        v.z = fixA(v.z, gi + 2 * dr, gk + 2 * dc);
-        v.w = fixA(v.w, gi + 3 * dr, gk + 3 * dc);
+        if (!plain) {
+          v.x = fixA(v.x, gi, gk);
+          v.y = fixA(v.y, gi + dr, gk + dc);
+          v.z = fixA(v.z, gi + 2 * dr, gk + 2 * dc);
+          v.w = fixA(v.w, gi + 3 * dr, gk + 3 * dc);
+        }
         const int i = gi - i0, k = gk - k0;
         if (!d.transA) {
           As[buf][k * LDSA + i] = v.x;
@@ -208,10 +230,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
         b_coord(idx, k0, gk, gj);
         const int dk = d.transB, dj = 1 - d.transB;
         float4 v = vb[e];
-        v.x = fixB(v.x, gk, gj);
-        v.y = fixB(v.y, gk + dk, gj + dj);
-        v.z = fixB(v.z, gk + 2 * dk, gj + 2 * dj);
-        v.w = fixB(v.w, gk + 3 * dk, gj + 3 * dj);
+        if (!plain) {
+          v.x = fixB(v.x, gk, gj);
+          v.y = fixB(v.y, gk + dk, gj + dj);
+          v.z = fixB(v.z, gk + 2 * dk, gj + 2 * dj);
+          v.w = fixB(v.w, gk + 3 * dk, gj + 3 * dj);
+        }
         const int k = gk - k0, j = gj - j0;
         if (!d.transB) {
           *reinterpret_cast<float4*>(&Bs[buf][k * LDSB + j]) = v;
@@ -245,11 +269,25 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
     for (int b = 0; b < TN; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+  float cpre[PREC ? TM : 1][PREC ? TN : 1][16];
+  if (PREC) {
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int b = 0; b < TN; ++b) {
+        const int c = j0 + wn + 32 * b + l32;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = i0 + wm + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
+          cpre[a][b][v] = (r < d.M && c < d.N) ? C[(int64_t)r * d.ldc + c] : 0.0f;
+        }
+      }
+  }
   if (klo < khi) load_stage(klo);
 
   int buf = 0;
   if (klo < khi) {
-    store_stage(0, klo);
+    store_stage(0, klo, plain_stage(klo));
     __syncthreads();
     for (int k0 = klo; k0 < khi; k0 += GBK) {
       const bool more = k0 + GBK < khi;
@@ -268,7 +306,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
             acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
       }
       if (more) {
-        store_stage(buf ^ 1, k0 + GBK);
+        store_stage(buf ^ 1, k0 + GBK, plain_stage(k0 + GBK));
         __syncthreads();
         buf ^= 1;
       }
@@ -288,7 +326,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = i0 + wm + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
-        cv[v] = (d.beta != 0.0f && r < d.M && c < d.N) ? C[(int64_t)r * d.ldc + c] : 0.0f;
+        if (PREC) cv[v] = cpre[PREC ? a : 0][PREC ? b : 0][v];
+        else cv[v] = (d.beta != 0.0f && r < d.M && c < d.N) ? C[(int64_t)r * d.ldc + c] : 0.0f;
       }
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -300,6 +339,204 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
         if (d.lower_only && r == c && d.mirror < 0.0f) val = 0.0f;
         C[(int64_t)r * d.ldc + c] = val;
         if (d.lower_only && r != c) C[(int64_t)c * d.ldc + r] = d.mirror * val;
+      }
+    }
+}
+
+// 128 x 128 tiles for the large products (16-byte aligned operands, op(B) = B, op(A) = A
+// or A^T by TA): each wave owns a 64 x 64 quarter as 2 x 2 32x32 accumulators, so a
+// K = 16 stage is 32 MFMAs per wave against four 16-byte loads per thread. The staging
+// code carries no per-element work: offsets are formed once per tile, loads use clamped
+// (always valid) addresses, and the raw values go to LDS. Only a stage that touches a
+// matrix edge or an operand triangle's diagonal (tested uniformly) is then fixed in LDS
+// -- zeros outside the matrix, the triangle masks -- between two barriers.
+// Launch bound of 4 waves per SIMD: the compiler then fits the kernel in 116 VGPRs
+// (accumulators included) without scratch, against 168 + 64 left to itself.
+template <bool TA>
+__global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
+  constexpr int BM = 128, BN = 128, LDA_ = BM + 4, LDB_ = BN + 4;
+  __shared__ __align__(16) float As[2][GBK * LDA_];
+  __shared__ __align__(16) float Bs[2][GBK * LDB_];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  int64_t bat = blockIdx.y;
+  const int64_t bat2 = blockIdx.z;
+  int tx = blockIdx.x;
+  if (d.xcd8) {
+    const int64_t lin = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    const int64_t slot = lin >> 3;
+    tx = (int)(slot % gridDim.x);
+    bat = (slot / gridDim.x) * 8 + (lin & 7);
+  }
+  if (d.active && !d.active[bat]) return;
+  int ti, tj;
+  if (d.lower_only) {
+    const int t = tx;
+    int I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
+    while ((I + 1) * (I + 2) / 2 <= t) ++I;
+    while (I * (I + 1) / 2 > t) --I;
+    ti = I;
+    tj = t - I * (I + 1) / 2;
+  } else {
+    const int ntn = (d.N + BN - 1) / BN;
+    ti = tx / ntn;
+    tj = tx % ntn;
+  }
+  const int i0 = ti * BM, j0 = tj * BN;
+  const float* A = d.A + bat * d.sA + bat2 * d.sA2;
+  const float* B = d.B + bat * d.sB + bat2 * d.sB2;
+  float* C = d.C + bat * d.sC + bat2 * d.sC2;
+
+  int klo = 0, khi = d.K;
+  if (mask_upper(d.maskA)) klo = max(klo, i0 + d.offAr - d.offAc);
+  if (mask_lower(d.maskA)) khi = min(khi, i0 + BM + d.offAr - d.offAc);
+  if (mask_lower(d.maskB)) klo = max(klo, j0 + d.offBc - d.offBr);
+  if (mask_upper(d.maskB)) khi = min(khi, j0 + BN + d.offBc - d.offBr);
+  klo = max(0, (klo / GBK) * GBK);
+
+  const bool interior = i0 + BM <= d.M && j0 + BN <= d.N;
+  auto plain_stage = [&](int k0) {
+    bool ok = interior && k0 + GBK <= d.K;
+    if (d.maskA == MASK_LOWER_UNIT) ok = ok && i0 + d.offAr > k0 + GBK - 1 + d.offAc;
+    if (d.maskA == MASK_UPPER) ok = ok && i0 + BM - 1 + d.offAr <= k0 + d.offAc;
+    if (d.maskA == MASK_UPPER_UNIT) ok = ok && i0 + BM - 1 + d.offAr < k0 + d.offAc;
+    if (d.maskB == MASK_LOWER_UNIT) ok = ok && k0 + d.offBr > j0 + BN - 1 + d.offBc;
+    if (d.maskB == MASK_UPPER) ok = ok && k0 + GBK - 1 + d.offBr <= j0 + d.offBc;
+    if (d.maskB == MASK_UPPER_UNIT) ok = ok && k0 + GBK - 1 + d.offBr < j0 + d.offBc;
+    return ok;
+  };
+
+  // this thread's staging slots (two float4 of A, two of B per stage), 32-bit offsets
+  // within a matrix (N * N < 2^31); rows / columns past the matrix clamped once here
+  // A (not TA): rows ra + 64 e, columns k0 + ka .. +3;  A^T (TA): k rows k0 + ka + 8 e,
+  // columns ia .. +3;  B: k rows k0 + kb + 8 e, columns jb .. +3
+  const int ra = tid >> 2, ka = TA ? (tid >> 5) : 4 * (tid & 3);
+  const int ia = min(i0 + 4 * (tid & 31), d.M - 4);
+  const int kb = tid >> 5, jb = min(j0 + 4 * (tid & 31), d.N - 4);
+  int aoff[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) aoff[e] = TA ? ia : min(i0 + ra + 64 * e, d.M - 1) * d.lda;
+  float va[2][4], vb[2][4];  // plain floats: arrays of float4 are not kept in registers
+  auto load_stage = [&](int k0) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float4 x = !TA ? *reinterpret_cast<const float4*>(A + aoff[e] + min(k0 + ka, d.K - 4))
+                           : *reinterpret_cast<const float4*>(A + min(k0 + ka + 8 * e, d.K - 1) * d.lda + aoff[e]);
+      const float4 y = *reinterpret_cast<const float4*>(B + min(k0 + kb + 8 * e, d.K - 1) * d.ldb + jb);
+      va[e][0] = x.x;
+      va[e][1] = x.y;
+      va[e][2] = x.z;
+      va[e][3] = x.w;
+      vb[e][0] = y.x;
+      vb[e][1] = y.y;
+      vb[e][2] = y.z;
+      vb[e][3] = y.w;
+    }
+  };
+  // registers -> LDS, K-major (As[k][i], Bs[k][j]); clamped columns land in the slots of
+  // the columns past the matrix, which the fix pass zeroes
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      if (!TA) {
+        float* p = &As[buf][ka * LDA_ + ra + 64 * e];
+        p[0] = va[e][0];
+        p[LDA_] = va[e][1];
+        p[2 * LDA_] = va[e][2];
+        p[3 * LDA_] = va[e][3];
+      } else {
+        *reinterpret_cast<float4*>(&As[buf][(ka + 8 * e) * LDA_ + 4 * (tid & 31)]) =
+            make_float4(va[e][0], va[e][1], va[e][2], va[e][3]);
+      }
+      *reinterpret_cast<float4*>(&Bs[buf][(kb + 8 * e) * LDB_ + 4 * (tid & 31)]) =
+          make_float4(vb[e][0], vb[e][1], vb[e][2], vb[e][3]);
+    }
+  };
+  auto fix_stage = [&](int buf, int k0) {
+    for (int e = tid; e < GBK * BM; e += 256) {
+      const int k = e / BM, i = e % BM, gi = i0 + i, gk = k0 + k;
+      float* p = &As[buf][k * LDA_ + i];
+      *p = (gi >= d.M || gk >= d.K) ? 0.0f : (d.maskA ? mask_val(*p, d.maskA, gi + d.offAr, gk + d.offAc) : *p);
+    }
+    for (int e = tid; e < GBK * BN; e += 256) {
+      const int k = e / BN, j = e % BN, gj = j0 + j, gk = k0 + k;
+      float* p = &Bs[buf][k * LDB_ + j];
+      *p = (gj >= d.N || gk >= d.K) ? 0.0f : (d.maskB ? mask_val(*p, d.maskB, gk + d.offBr, gj + d.offBc) : *p);
+    }
+  };
+
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int l32 = lane & 31, lh = lane >> 5;
+  v16f acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+  if (klo < khi) {
+    load_stage(klo);
+    store_stage(0);
+    if (!plain_stage(klo)) {
+      __syncthreads();
+      fix_stage(0, klo);
+    }
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = klo; k0 < khi; k0 += GBK) {
+      const bool more = k0 + GBK < khi;
+      if (more) load_stage(k0 + GBK);
+#pragma unroll
+      for (int kp = 0; kp < GBK / 2; ++kp) {
+        float av[2], bv[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) av[a] = As[buf][(2 * kp + lh) * LDA_ + wm + 32 * a + l32];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) bv[b] = Bs[buf][(2 * kp + lh) * LDB_ + wn + 32 * b + l32];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+      }
+      if (more) {
+        store_stage(buf ^ 1);
+        if (!plain_stage(k0 + GBK)) {
+          __syncthreads();
+          fix_stage(buf ^ 1, k0 + GBK);
+        }
+        __syncthreads();
+        buf ^= 1;
+      }
+    }
+  }
+
+  // epilogue as in gemm_kernel, with 32-bit offsets within the matrix: element v of an
+  // accumulator is row r0 + dv, dv = 8 (v / 4) + v % 4, so its offsets step by the
+  // uniform dv * ldc (and dv for the mirrored store)
+  const bool diag_tile = d.lower_only && ti == tj;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int c = j0 + wn + 32 * b + l32;
+      const int r0 = i0 + wm + 32 * a + 4 * lh;
+      const int o = r0 * d.ldc + c, om = c * d.ldc + r0;
+      float cv[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int dv = 8 * (v >> 2) + (v & 3);
+        cv[v] = (d.beta != 0.0f && r0 + dv < d.M && c < d.N) ? C[o + dv * d.ldc] : 0.0f;
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int dv = 8 * (v >> 2) + (v & 3), r = r0 + dv;
+        if (r >= d.M || c >= d.N) continue;
+        if (diag_tile && r < c) continue;
+        float val = d.alpha * acc[a][b][v];
+        if (d.beta != 0.0f) val = fmaf(d.beta, cv[v], val);
+        if (d.lower_only && r == c && d.mirror < 0.0f) val = 0.0f;
+        C[o + dv * d.ldc] = val;
+        if (d.lower_only && r != c) C[om + dv] = d.mirror * val;
       }
     }
 }
@@ -323,6 +560,13 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
                    d.sA % 4 == 0 && d.sB % 4 == 0 && d.sA2 % 4 == 0 && d.sB2 % 4 == 0 &&
                    d.K % 4 == 0 && (d.transA ? d.M % 4 == 0 : true) &&
                    (d.transB ? true : d.N % 4 == 0);
+  // 128 x 128 tiles for the large products (measured at batch 64: the n = 2048 top
+  // triangular-inverse level 18 % and the skew R product 15 % faster); at M = 512 and
+  // below, and for short K, the coarser triangle trimming and the longer prologue /
+  // epilogue per K stage make the 64 x 64 tiles faster
+  const bool big = vec && !d.transB && d.M >= 1024 && d.N >= 1024 && d.K >= 512;
+  const int tm2 = (d.M + 127) / 128, tn2 = (d.N + 127) / 128;
+  const int tiles2 = d.lower_only ? tm2 * (tm2 + 1) / 2 : tm2 * tn2;
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
     const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
     GemmDesc e = d;
@@ -333,9 +577,17 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
     e.B += b0 * d.sB;
     e.C += b0 * d.sC;
     if (d.active) e.active += b0;
+    if (big) {
+      const dim3 grid2(tiles2, (unsigned)nb, nb2);
+      if (d.transA) hipLaunchKernelGGL((gemm128_kernel<true>), grid2, dim3(256), 0, s, e);
+      else hipLaunchKernelGGL((gemm128_kernel<false>), grid2, dim3(256), 0, s, e);
+      if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+      continue;
+    }
     const dim3 grid(tiles, (unsigned)nb, nb2);
-    if (vec) hipLaunchKernelGGL((gemm_kernel<BM, BN, true>), grid, dim3(256), 0, s, e);
-    else hipLaunchKernelGGL((gemm_kernel<BM, BN, false>), grid, dim3(256), 0, s, e);
+    if (vec && d.beta != 0.0f) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, true>), grid, dim3(256), 0, s, e);
+    else if (vec) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, false>), grid, dim3(256), 0, s, e);
+    else hipLaunchKernelGGL((gemm_kernel<BM, BN, false, false>), grid, dim3(256), 0, s, e);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
