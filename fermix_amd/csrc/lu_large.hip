@@ -460,21 +460,25 @@ __global__ __launch_bounds__(NT) void lu_panel_reg_kernel(float* __restrict__ W,
   if (tid == 0) nsw_out[b * nblk + blk] = nsw;
 }
 
-// Row permutation of one 64-column strip and, for a trailing strip, its U rows.
+// Row permutation of one 64-column strip and, for a trailing strip, its U rows
+// U12 = L11^-1 A12. Everything is read before anything is written (the moved rows into
+// registers, 32 per thread; A12, L11 and the panel's X straight into MFMA operand
+// layout), then the moved rows are stored and each wave solves for its 16 columns of U12
+// in registers: U_s = X_s (A_s - sum_{t<s} L_st U_t), the right operands in accumulator
+// layout (lane (g, c) holding rows 4g + v) taken as they stand, one MFMA per v over the
+// K indices {4g + v}. About 1.3 KiB of LDS and (launch bound) at most 128 registers, so
+// 4 waves per SIMD.
 template <int PW, int MAXM>
-__global__ __launch_bounds__(256) void lu_urow_kernel(float* __restrict__ W, int N, int r0,
+__global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, int N, int r0,
                                                       const int* __restrict__ src,
                                                       const float* __restrict__ Xg,
                                                       int nleft) {
+  static_assert(PW == 64, "one 16-column slice of the strip per wave");
   constexpr int NSUB = PW / 16;
-  __shared__ float buf[2 * PW * 64];
   __shared__ int list[2 * PW];
   __shared__ int srcv[2 * PW];
   __shared__ int srcU[PW];
   __shared__ int cnt;
-  __shared__ float L11[PW * (PW + 1)];
-  __shared__ float Ub[PW * 64];
-  __shared__ float Tw[4][256];
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int strip = blockIdx.x;
@@ -485,8 +489,12 @@ __global__ __launch_bounds__(256) void lu_urow_kernel(float* __restrict__ W, int
   const int* sb = src + b * N;
   const int m = N - r0;
   // pass 1 (indices): the moved rows (position, source row) and the source rows of
-  // positions r0 .. r0+PW-1
-  if (tid == 0) cnt = 0;
+  // positions r0 .. r0+PW-1. srcv[0] starts as a valid row: the gathers below read
+  // srcv[0] for every slot k >= nm, including when no row moved (nm = 0).
+  if (tid == 0) {
+    cnt = 0;
+    srcv[0] = r0;
+  }
   __syncthreads();
   constexpr int MQ = MAXM / 256;  // m <= N <= MAXM
   int sv[MQ];
@@ -509,79 +517,62 @@ __global__ __launch_bounds__(256) void lu_urow_kernel(float* __restrict__ W, int
   }
   __syncthreads();
   const int nm = min(cnt, 2 * PW);
-  // pass 2: gather everything this strip needs before anything is written -- the moved
-  // rows and, for a trailing strip, A12 (rows r0 .. r0+PW-1 of the new order) and L11.
-  // Loads go out in fixed-count batches with in-bounds (clamped) addresses.
-  const int cl = tid & 63;  // column of this thread in every 64-wide row below
+  // pass 2: every read. Moved row k (< nm) column cl: thread (k % 4 = tid >> 6, cl).
+  const int cl = tid & 63;
   const int cc = min(cl, ncol - 1);
-  for (int k0 = 0; k0 < nm; k0 += 32) {
-    float v[8];
+  float mv[2 * PW / 4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int k = k0 + (tid >> 6) + 4 * u;
-      v[u] = Wb[(int64_t)srcv[k < nm ? k : 0] * N + cstart + cc];
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int k = k0 + (tid >> 6) + 4 * u;
-      if (k < nm && cl < ncol) buf[k * 64 + cl] = v[u];
-    }
+  for (int u = 0; u < 2 * PW / 4; ++u) {
+    const int k = (tid >> 6) + 4 * u;
+    mv[u] = Wb[(int64_t)srcv[k < nm ? k : 0] * N + cstart + cc];
   }
+  // operands of the U12 solve (trailing strips): lane (g, li) of wave w, column 16w + li
+  const int li = lane & 15, g = lane >> 4;
+  const int col = min(16 * wave + li, ncol - 1);
+  v4f a12[NSUB];
+  float lv[NSUB * (NSUB - 1) / 2][4], xv[NSUB][4];
   if (!left) {
-    float v[PW / 4], w[PW * PW / 256];
+    const float* Xb = Xg + b * NSUB * 256;
 #pragma unroll
-    for (int u = 0; u < PW / 4; ++u) v[u] = Wb[(int64_t)srcU[(tid >> 6) + 4 * u] * N + cstart + cc];
+    for (int s = 0; s < NSUB; ++s)
 #pragma unroll
-    for (int u = 0; u < PW * PW / 256; ++u) {
-      const int e = tid + 256 * u;
-      w[u] = Wb[(int64_t)(r0 + e / PW) * N + r0 + e % PW];
-    }
+      for (int v = 0; v < 4; ++v) {
+        a12[s][v] = Wb[(int64_t)srcU[16 * s + 4 * g + v] * N + cstart + col];
+        xv[s][v] = Xb[s * 256 + li * 16 + 4 * g + v];
+      }
 #pragma unroll
-    for (int u = 0; u < PW / 4; ++u) Ub[((tid >> 6) + 4 * u) * 64 + cl] = cl < ncol ? v[u] : 0.0f;
+    for (int s = 1, q = 0; s < NSUB; ++s)
 #pragma unroll
-    for (int u = 0; u < PW * PW / 256; ++u) {
-      const int e = tid + 256 * u;
-      L11[(e / PW) * (PW + 1) + e % PW] = w[u];
-    }
+      for (int t = 0; t < s; ++t, ++q)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) lv[q][v] = Wb[(int64_t)(r0 + 16 * s + li) * N + r0 + 16 * t + 4 * g + v];
   }
-  __syncthreads();
-  // rows r0 .. r0+PW-1 of a trailing strip are written below as U12
-  for (int e = tid; e < nm * 64; e += 256) {
-    const int k = e / 64, c = e % 64;
-    if (c < ncol && (left || list[k] >= PW))
-      Wb[(int64_t)(r0 + list[k]) * N + cstart + c] = buf[k * 64 + c];
+  __syncthreads();  // no row is written before every thread has read what it needs
+  // the moved rows; rows r0 .. r0+PW-1 of a trailing strip are written below as U12
+#pragma unroll
+  for (int u = 0; u < 2 * PW / 4; ++u) {
+    const int k = (tid >> 6) + 4 * u;
+    if (k < nm && cl < ncol && (left || list[k] >= PW)) Wb[(int64_t)(r0 + list[k]) * N + cstart + cl] = mv[u];
   }
   if (left) return;
-  // U12 = L11^-1 A12 by blocks of 16 rows: U_s = X_s (A_s - sum_{t<s} L_st U_t)
-  // wave w owns columns [16w, 16w + 16) of the strip
-  const int li = lane & 15, g = lane >> 4;
-  const int col = 16 * wave + li;
-  const float* Xb = Xg + b * NSUB * 256;
-  for (int s = 0; s < NSUB; ++s) {
-    v4f acc;
+  v4f U[NSUB];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] = Ub[(16 * s + 4 * g + v) * 64 + col];
-    for (int t = 0; t < s; ++t) {
+  for (int s = 0, q0 = 0; s < NSUB; q0 += s, ++s) {
+    v4f acc = a12[s];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        acc = mfma16(-L11[(16 * s + li) * (PW + 1) + 16 * t + 4 * q + g],
-                     Ub[(16 * t + 4 * q + g) * 64 + col], acc);
-    }
-    // to B layout through the wave's scratch, then U_s = X_s * acc
+    for (int t = 0; t < s; ++t)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) Tw[wave][(4 * g + v) * 16 + li] = acc[v];
-    wave_lds_fence();
+      for (int v = 0; v < 4; ++v) acc = mfma16(-lv[q0 + t][v], U[t][v], acc);
     v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) u = mfma16(Xb[s * 256 + li * 16 + 4 * q + g], Tw[wave][(4 * q + g) * 16 + li], u);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) Ub[(16 * s + 4 * g + v) * 64 + col] = u[v];
-    wave_lds_fence();
+    for (int v = 0; v < 4; ++v) u = mfma16(xv[s][v], acc[v], u);
+    U[s] = u;
   }
-  __syncthreads();
-  for (int e = tid; e < PW * 64; e += 256) {
-    const int i = e / 64, c = e % 64;
-    if (c < ncol) Wb[(int64_t)(r0 + i) * N + cstart + c] = Ub[e];
+  if (16 * wave + li < ncol) {
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) Wb[(int64_t)(r0 + 16 * s + 4 * g + v) * N + cstart + 16 * wave + li] = U[s][v];
   }
 }
 

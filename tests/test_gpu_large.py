@@ -61,3 +61,25 @@ def test_slogpf_large_vs_oracle(dev, n):
         sd, ld = map(_np, fermix_amd.slogdet(_t(S, dev)))
         fin = np.isfinite(l64)
         assert np.all(np.abs(2 * l[fin] - ld[fin]) < 1e-3 * np.maximum(1, np.abs(ld[fin])) + 1e-3)
+
+
+@pytest.mark.parametrize("n", [192, 512, 1024, 1536])
+def test_no_row_moves(dev, n):
+    """Column-diagonally-dominant matrices: the diagonal entry is the largest of its column
+    throughout the elimination, so no panel moves a row and every row-permutation step
+    runs with an empty move list. slogdet and A^-T against float64."""
+    from fermix_amd import _kernels
+    from tests.tolerances import assert_grad
+
+    B = 3
+    rng = np.random.default_rng(6000 + n)
+    A = (rng.standard_normal((B, n, n)) / n).astype(np.float32) + np.float32(4.0) * np.eye(n, dtype=np.float32)
+    print(f"no row moves n={n}", flush=True)
+    s, l, invT, _, _ = _kernels.slogdet_parts(_t(A, dev))
+    s0, l0 = fermix_amd.slogdet(_t(A, dev))
+    assert torch.equal(s, s0) and torch.equal(l, l0)
+    s64, l64 = ref64.slogdet64(A)
+    assert np.array_equal(_np(s), s64)
+    assert_logabs(_np(l), l64, n, "vs float64", A)
+    ref = np.linalg.inv(A.astype(np.float64)).swapaxes(-1, -2)
+    assert_grad(_np(invT), ref, A, f"n={n} A^-T vs float64")
