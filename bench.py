@@ -42,7 +42,7 @@ def _parse():
     return p.parse_args()
 
 
-HEAD_KERNEL = {"slogpf_fwd": "pf_small_kernel<128, false>", "slogdet_fwd": "lu_small_kernel<128, false>"}
+HEAD_KERNEL = {"slogpf_fwd": "pf_small_kernel<128, false>", "slogdet_fwd": "lu_split_kernel<128, 64, false>"}
 
 
 def _measured_traffic(name):
