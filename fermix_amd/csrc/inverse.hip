@@ -1,9 +1,9 @@
 // A^-T from the packed LU of P A' (the slogdet backward), any N: the factors are
 // embedded in T (Ninv x Ninv, Ninv = 32 * 2^k >= N, identity padded) and
-//   1. the 32x32 diagonal blocks are inverted in place: strictly-lower part of L^-1,
-//      upper part of U~^-1 (U~ = U with exact zero pivots replaced by 1, so singular
-//      inputs stay finite);
-//   2. the block-recursive levels s = 32, 64, .., Ninv/2 complete L^-1 and U~^-1 with
+//   1. the 128x128 (or Ninv x Ninv, if smaller) diagonal blocks are inverted in place in
+//      LDS: strictly-lower part of L^-1, upper part of U~^-1 (U~ = U with exact zero
+//      pivots replaced by 1, so singular inputs stay finite);
+//   2. the block-recursive levels s = 128, 256, .., Ninv/2 complete L^-1 and U~^-1 with
 //      four batched MFMA GEMMs per level (all block pairs of a level in one launch):
 //        X21 = -X22 (L21 X11),   Y12 = -Y11 (U12 Y22);
 //   3. Z = U~^-1 L^-1 by one GEMM whose tiles only run over k >= max(row, col);
@@ -28,54 +28,167 @@ __global__ void embed_kernel(const float* __restrict__ src, int N, float* __rest
   T[b * Ninv * Ninv + e] = (r < N && c < N) ? src[b * (int64_t)N * N + r * N + c] : (r == c ? 1.0f : 0.0f);
 }
 
-// In-place inverse of the 32x32 diagonal block t of the packed T: lane c (< 32) forms
-// column c of L^-1 by forward substitution, lane 32 + c column c of U~^-1 by back
-// substitution.
-__global__ __launch_bounds__(64) void leaf_inverse_kernel(float* __restrict__ T, int Ninv,
-                                                          const int* __restrict__ active) {
-  __shared__ float Bk[32 * 33];
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// op values of the packed block in LDS: the unit-lower factor (strictly lower entries,
+// 1 on the diagonal) and the upper factor (upper entries incl. the diagonal)
+__device__ __forceinline__ float lunit_at(const float* Ts, int ld, int r, int c) {
+  return r > c ? Ts[r * ld + c] : (r == c ? 1.0f : 0.0f);
+}
+__device__ __forceinline__ float upper_at(const float* Ts, int ld, int r, int c) {
+  return r <= c ? Ts[r * ld + c] : 0.0f;
+}
+
+// In-place inverses of the D x D diagonal blocks of the packed T (D = min(128, Ninv)):
+// the strictly-lower part becomes L^-1, and with upper the upper part U~^-1, over the
+// whole block, in one workgroup with the block in LDS:
+//   1. the 32x32 leaves by substitution, one wave per leaf: lane c (< 32) forms column c
+//      of L^-1 by forward substitution, lane 32 + c column c of U~^-1 by back
+//      substitution (zero pivots divided as 1);
+//   2. the recursion levels s = 32, 64 < D on MFMA (32x32x2): X21 = -X22 (L21 X11) and
+//      Y12 = -Y11 (U12 Y22), one (pair, factor, 32-column block) per wave. The inner
+//      product stays in registers and enters the outer one as it stands (lane (h, c)
+//      holding rows 8 (v / 4) + 4 h + v % 4: one MFMA per v over those K indices, the
+//      left operand read from LDS in that order); a barrier separates the reads of
+//      L21 / U12 from the in-place stores of X21 / Y12.
+template <int D>
+__global__ __launch_bounds__(256) void diag_inverse_kernel(float* __restrict__ T, int Ninv,
+                                                           const int* __restrict__ active, int upper) {
+  constexpr int LDT = D + 1;
+  __shared__ float Ts[D * LDT];
   const int64_t b = blockIdx.y;
   if (active && !active[b]) return;
-  const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  float* base = T + b * (int64_t)Ninv * Ninv + (int64_t)(32 * t) * Ninv + 32 * t;
-  float ld[16];
+  const int t0 = D * blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  float* base = T + b * (int64_t)Ninv * Ninv + (int64_t)t0 * Ninv + t0;
+  {
+    constexpr int NV = D * D / 4, PER = (NV + 255) / 256;
+    float4 v[PER];
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int e = lane + 64 * u;
-    ld[u] = base[(e >> 5) * Ninv + (e & 31)];
-  }
-#pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int e = lane + 64 * u;
-    Bk[(e >> 5) * 33 + (e & 31)] = ld[u];
-  }
-  __syncthreads();
-  const int c = lane & 31;
-  float x[32];
-  if (lane < 32) {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int k = 0; k < i; ++k) acc = fmaf(Bk[i * 33 + k], x[k], acc);
-      x[i] = (i == c) ? 1.0f : (i > c ? -acc : 0.0f);
+    for (int u = 0; u < PER; ++u) {
+      const int e = tid + 256 * u;
+      if (NV % 256 == 0 || e < NV) v[u] = *reinterpret_cast<const float4*>(base + (e / (D / 4)) * Ninv + 4 * (e % (D / 4)));
     }
-  } else {
 #pragma unroll
-    for (int i = 31; i >= 0; --i) {
-      float acc = (i == c) ? 1.0f : 0.0f;
-#pragma unroll
-      for (int k = i + 1; k < 32; ++k) acc = fmaf(-Bk[i * 33 + k], x[k], acc);
-      const float dg = Bk[i * 33 + i];
-      x[i] = (i > c) ? 0.0f : acc / (dg == 0.0f ? 1.0f : dg);
+    for (int u = 0; u < PER; ++u) {
+      const int e = tid + 256 * u;
+      if (NV % 256 == 0 || e < NV) {
+        float* d = Ts + (e / (D / 4)) * LDT + 4 * (e % (D / 4));
+        d[0] = v[u].x;
+        d[1] = v[u].y;
+        d[2] = v[u].z;
+        d[3] = v[u].w;
+      }
     }
   }
   __syncthreads();
+  // 1. leaves
+  if (wave < D / 32) {
+    const int lo = 32 * wave, c = lane & 31;
+    float x[32];
+    if (lane < 32) {
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    if (lane < 32 ? (i > c) : (i <= c)) base[(int64_t)i * Ninv + c] = x[i];
+      for (int i = 0; i < 32; ++i) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < i; ++k) acc = fmaf(Ts[(lo + i) * LDT + lo + k], x[k], acc);
+        x[i] = (i == c) ? 1.0f : (i > c ? -acc : 0.0f);
+      }
+    } else if (upper) {
+#pragma unroll
+      for (int i = 31; i >= 0; --i) {
+        float acc = (i == c) ? 1.0f : 0.0f;
+#pragma unroll
+        for (int k = i + 1; k < 32; ++k) acc = fmaf(-Ts[(lo + i) * LDT + lo + k], x[k], acc);
+        const float dg = Ts[(lo + i) * LDT + lo + i];
+        x[i] = (i > c) ? 0.0f : acc / (dg == 0.0f ? 1.0f : dg);
+      }
+    }
+    // both halves of the wave have read the leaf (the branches run one after the other)
+    if (lane < 32 || upper) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        if (lane < 32 ? (i > c) : (i <= c)) Ts[(lo + i) * LDT + lo + c] = x[i];
+    }
   }
+  __syncthreads();
+  // 2. levels s = 32, 64 below D
+  const int l32 = lane & 31, lh = lane >> 5;
+  static_for<0, 2>([&](auto lc) {
+    constexpr int s = 32 << decltype(lc)::value;
+    if constexpr (s < D) {
+      constexpr int NCB = s / 32;  // 32-column blocks (and 32-row tiles) of an s x s block
+      const int chains = upper ? 2 : 1;
+      const int items = (D / (2 * s)) * chains * NCB;  // <= 4
+      const bool act = wave < items;
+      const int J = wave % NCB, rest = wave / NCB;
+      const int chain = rest % chains, o = (rest / chains) * 2 * s;
+      v16f tacc[NCB];
+#pragma unroll
+      for (int I = 0; I < NCB; ++I)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) tacc[I][v] = 0.0f;
+      if (act) {
+        if (chain == 0) {
+          // T = L21 X11, column block J: k >= 32 J (X11 unit lower)
+          for (int k0 = 32 * J; k0 < s; k0 += 2) {
+            const float bv = lunit_at(Ts, LDT, o + k0 + lh, o + 32 * J + l32);
+#pragma unroll
+            for (int I = 0; I < NCB; ++I)
+              tacc[I] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ts[(o + s + 32 * I + l32) * LDT + o + k0 + lh], bv,
+                                                              tacc[I], 0, 0, 0);
+          }
+        } else {
+          // T = U12 Y22, column block J: k < 32 J + 32 (Y22 upper)
+          for (int k0 = 0; k0 < 32 * J + 32; k0 += 2) {
+            const float bv = upper_at(Ts, LDT, o + s + k0 + lh, o + s + 32 * J + l32);
+#pragma unroll
+            for (int I = 0; I < NCB; ++I)
+              tacc[I] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ts[(o + 32 * I + l32) * LDT + o + s + k0 + lh], bv,
+                                                              tacc[I], 0, 0, 0);
+          }
+        }
+      }
+      __syncthreads();  // every read of L21 / U12 is done
+      if (act) {
+#pragma unroll
+        for (int I = 0; I < NCB; ++I) {
+          v16f out;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) out[v] = 0.0f;
+          if (chain == 0) {
+            // X21 = -X22 T, row tile I: k <= 32 I + 31 (X22 unit lower)
+#pragma unroll
+            for (int K = 0; K <= I; ++K)
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                const int k = 32 * K + 8 * (v >> 2) + 4 * lh + (v & 3);
+                out = __builtin_amdgcn_mfma_f32_32x32x2f32(lunit_at(Ts, LDT, o + s + 32 * I + l32, o + s + k),
+                                                           tacc[K][v], out, 0, 0, 0);
+              }
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              Ts[(o + s + 32 * I + 8 * (v >> 2) + 4 * lh + (v & 3)) * LDT + o + 32 * J + l32] = -out[v];
+          } else {
+            // Y12 = -Y11 T, row tile I: k >= 32 I (Y11 upper)
+#pragma unroll
+            for (int K = I; K < NCB; ++K)
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                const int k = 32 * K + 8 * (v >> 2) + 4 * lh + (v & 3);
+                out = __builtin_amdgcn_mfma_f32_32x32x2f32(upper_at(Ts, LDT, o + 32 * I + l32, o + k), tacc[K][v],
+                                                           out, 0, 0, 0);
+              }
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              Ts[(o + 32 * I + 8 * (v >> 2) + 4 * lh + (v & 3)) * LDT + o + s + 32 * J + l32] = -out[v];
+          }
+        }
+      }
+      __syncthreads();
+    }
+  });
+  for (int e = tid; e < D * D; e += 256) base[(e / D) * Ninv + e % D] = Ts[(e / D) * LDT + e % D];
 }
 
 // bad[b] = any tile flag, or (zero_singular and sign[b] == 0)
@@ -149,9 +262,18 @@ __global__ __launch_bounds__(256) void zero_bad_kernel(const int* __restrict__ b
 int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper, hipStream_t s,
                        const int* active) {
   const int64_t NN = (int64_t)Ninv * Ninv;
-  hipLaunchKernelGGL(leaf_inverse_kernel, dim3(Ninv / 32, (unsigned)batch), dim3(64), 0, s, T, Ninv, active);
+  const int D = Ninv < 128 ? Ninv : 128;  // diagonal blocks inverted whole in LDS
+  if (D == 32)
+    hipLaunchKernelGGL((diag_inverse_kernel<32>), dim3(Ninv / 32, (unsigned)batch), dim3(256), 0, s, T, Ninv, active,
+                       (int)upper);
+  else if (D == 64)
+    hipLaunchKernelGGL((diag_inverse_kernel<64>), dim3(Ninv / 64, (unsigned)batch), dim3(256), 0, s, T, Ninv, active,
+                       (int)upper);
+  else
+    hipLaunchKernelGGL((diag_inverse_kernel<128>), dim3(Ninv / 128, (unsigned)batch), dim3(256), 0, s, T, Ninv,
+                       active, (int)upper);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  for (int sz = 32; sz < Ninv; sz *= 2) {
+  for (int sz = D; sz < Ninv; sz *= 2) {
     const int pairs = Ninv / (2 * sz);
     const int64_t dstride = (int64_t)2 * sz * (Ninv + 1);  // next pair along the diagonal
     GemmDesc d = {};
