@@ -17,7 +17,8 @@
 //   2. lu_urow_kernel   (matrix x 64-column strip): applies the row permutation to the
 //      strip, touching only the rows that move, and for trailing strips forms the U rows
 //      U12 = L11^-1 A12 by blocked forward substitution on MFMA;
-//   3. the batched MFMA GEMM A22 -= L21 U12 (gemm.hip).
+//   3. lu_update_kernel: the trailing update A22 -= L21 U12 on MFMA (K = 64, one LDS stage
+//      per 64 x 64 tile).
 // A final kernel turns the pivots and swap counts into (sign, logabs).
 //
 // Reference roles replaced (ChenAo-Phys/fermix): _lu_core's block loop (src/fermix/
@@ -629,6 +630,63 @@ size_t lu_large_workspace(int64_t batch, int n, bool parts) {
   return bytes;
 }
 
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// The trailing update A22 -= L21 U12 of one block (K = PW = 64) over the 64 x 64 tiles of
+// the mt x mt trailing block (mt a multiple of 64, every tile interior). The whole K
+// range is one LDS stage, so every load of a tile -- its C (straight into the
+// accumulators, which the MFMAs then reduce: C - L21 U12 with no epilogue arithmetic),
+// L21 rows and U12 columns -- is issued up front and the tile needs one barrier: more
+// bytes in flight per workgroup than a K-pipelined GEMM at this short K, where the
+// update is bound by reading and writing C. XCD-aware tile order when the batch is a
+// multiple of 8 (one matrix's L21 / U12 fetched into one L2).
+__global__ __launch_bounds__(256) void lu_update_kernel(float* __restrict__ W, int N, int r0, int nt) {
+  constexpr int PW = 64, LDA_ = PW + 1, LDB_ = 64 + 4;
+  __shared__ float As[64 * LDA_];                 // L21 tile, (i, k)
+  __shared__ __align__(16) float Bs[PW * LDB_];  // U12 tile, (k, j)
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  int64_t b = blockIdx.y;
+  int tx = blockIdx.x;
+  if ((gridDim.y & 7) == 0) {
+    const int64_t lin = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    const int64_t slot = lin >> 3;
+    tx = (int)(slot % gridDim.x);
+    b = (slot / gridDim.x) * 8 + (lin & 7);
+  }
+  float* Wb = W + b * (int64_t)N * N;  // offsets below are 32-bit (N * N < 2^31)
+  const int r1 = r0 + PW;
+  const int i0 = r1 + 64 * (tx / nt), j0 = r1 + 64 * (tx % nt);
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+  const int l32 = lane & 31, lh = lane >> 5;
+  v16f acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32];
+  float4 a4[4], b4[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + 256 * u, r = e >> 4, q = 4 * (e & 15);
+    a4[u] = *reinterpret_cast<const float4*>(Wb + (i0 + r) * N + r0 + q);
+    b4[u] = *reinterpret_cast<const float4*>(Wb + (r0 + r) * N + j0 + q);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + 256 * u, r = e >> 4, q = 4 * (e & 15);
+    float* pa = As + r * LDA_ + q;
+    pa[0] = a4[u].x;
+    pa[1] = a4[u].y;
+    pa[2] = a4[u].z;
+    pa[3] = a4[u].w;
+    *reinterpret_cast<float4*>(Bs + r * LDB_ + q) = b4[u];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int kp = 0; kp < PW / 2; ++kp)
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(-As[(wm + l32) * LDA_ + 2 * kp + lh], Bs[(2 * kp + lh) * LDB_ + wn + l32],
+                                               acc, 0, 0, 0);
+#pragma unroll
+  for (int v = 0; v < 16; ++v) Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32] = acc[v];
+}
+
 // MR: the largest m of the matrix's panels; panels with m > 1024 (MR > 1024 only) use
 // lu_panel_kernel with NT threads, the others lu_panel_reg_kernel.
 template <int MR, int NT>
@@ -662,21 +720,15 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
                          W, N, r0, src, X, nleft);
       if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     }
-    const int mt = N - r0 - PW;
+    const int mt = N - r0 - PW;  // a multiple of 64
     if (mt > 0) {
-      GemmDesc d = {};
-      d.A = W + (int64_t)(r0 + PW) * N + r0;
-      d.B = W + (int64_t)r0 * N + r0 + PW;
-      d.C = W + (int64_t)(r0 + PW) * N + r0 + PW;
-      d.sA = d.sB = d.sC = (int64_t)N * N;
-      d.lda = d.ldb = d.ldc = N;
-      d.M = mt;
-      d.N = mt;
-      d.K = PW;
-      d.alpha = -1.0f;
-      d.beta = 1.0f;
-      const int st = launch_gemm(d, batch, 1, s);
-      if (st != FX_OK) return st;
+      const int nt = mt / 64;
+      for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+        const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
+        hipLaunchKernelGGL(lu_update_kernel, dim3(nt * nt, (unsigned)nb), dim3(256), 0, s, W + b0 * (int64_t)N * N, N,
+                           r0, nt);
+        if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+      }
     }
   }
   return FX_OK;
