@@ -308,7 +308,8 @@ __global__ __launch_bounds__(NT) void lu_panel_reg_kernel(float* __restrict__ W,
                                                           int* __restrict__ nsw_out, int nblk,
                                                           int* __restrict__ src_out,
                                                           float* __restrict__ X_out,
-                                                          int* __restrict__ g0) {
+                                                          int* __restrict__ g0,
+                                                          const float* __restrict__ A0) {
   constexpr int NW = NT / 64, PW = 64, NSUB = 4;
   __shared__ Cand cand[2][NW];
   __shared__ __align__(16) float Prow[16 * PW];  // pivot rows of the sub-panel, all columns
@@ -324,8 +325,10 @@ __global__ __launch_bounds__(NT) void lu_panel_reg_kernel(float* __restrict__ W,
   int pos = tid;
   float a[PW];
   {
-    // 16-byte loads (r0 and N are multiples of 64); lanes past m read row 0
-    const float4* rp = reinterpret_cast<const float4*>(P + (int64_t)(valid ? tid : 0) * N);
+    // 16-byte loads (r0 and N are multiples of 64); lanes past m read row 0. A0 (first
+    // block only, in place of the input copy): the panel is read from the input itself.
+    const float* Ps = A0 ? A0 + b * (int64_t)N * N : P;
+    const float4* rp = reinterpret_cast<const float4*>(Ps + (int64_t)(valid ? tid : 0) * N);
 #pragma unroll
     for (int q = 0; q < PW / 4; ++q) {
       const float4 v = rp[q];
@@ -473,7 +476,7 @@ template <int PW, int MAXM>
 __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, int N, int r0,
                                                       const int* __restrict__ src,
                                                       const float* __restrict__ Xg,
-                                                      int nleft) {
+                                                      int nleft, const float* __restrict__ A0) {
   static_assert(PW == 64, "one 16-column slice of the strip per wave");
   constexpr int NSUB = PW / 16;
   __shared__ int list[2 * PW];
@@ -487,6 +490,10 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
   const int cstart = left ? 64 * strip : r0 + PW + 64 * (strip - nleft);
   const int ncol = min(64, left ? r0 - cstart : N - cstart);
   float* Wb = W + b * (int64_t)N * N;
+  // A0 (first block, in place of the input copy): the rows are read from the input, and
+  // the trailing update writes every row below the block (from the input, through the
+  // row map), so only U12 is stored here
+  const float* Rb = A0 ? A0 + b * (int64_t)N * N : Wb;
   const int* sb = src + b * N;
   const int m = N - r0;
   // pass 1 (indices): the moved rows (position, source row) and the source rows of
@@ -525,7 +532,7 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
 #pragma unroll
   for (int u = 0; u < 2 * PW / 4; ++u) {
     const int k = (tid >> 6) + 4 * u;
-    mv[u] = Wb[(int64_t)srcv[k < nm ? k : 0] * N + cstart + cc];
+    mv[u] = Rb[(int64_t)srcv[k < nm ? k : 0] * N + cstart + cc];
   }
   // operands of the U12 solve (trailing strips): lane (g, li) of wave w, column 16w + li
   const int li = lane & 15, g = lane >> 4;
@@ -538,7 +545,7 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        a12[s][v] = Wb[(int64_t)srcU[16 * s + 4 * g + v] * N + cstart + col];
+        a12[s][v] = Rb[(int64_t)srcU[16 * s + 4 * g + v] * N + cstart + col];
         xv[s][v] = Xb[s * 256 + li * 16 + 4 * g + v];
       }
 #pragma unroll
@@ -553,7 +560,7 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
 #pragma unroll
   for (int u = 0; u < 2 * PW / 4; ++u) {
     const int k = (tid >> 6) + 4 * u;
-    if (k < nm && cl < ncol && (left || list[k] >= PW)) Wb[(int64_t)(r0 + list[k]) * N + cstart + cl] = mv[u];
+    if (!A0 && k < nm && cl < ncol && (left || list[k] >= PW)) Wb[(int64_t)(r0 + list[k]) * N + cstart + cl] = mv[u];
   }
   if (left) return;
   v4f U[NSUB];
@@ -640,7 +647,8 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // bytes in flight per workgroup than a K-pipelined GEMM at this short K, where the
 // update is bound by reading and writing C. XCD-aware tile order when the batch is a
 // multiple of 8 (one matrix's L21 / U12 fetched into one L2).
-__global__ __launch_bounds__(256) void lu_update_kernel(float* __restrict__ W, int N, int r0, int nt) {
+__global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W, int N, int r0, int nt,
+                                                        const float* __restrict__ A0, const int* __restrict__ rmap) {
   constexpr int PW = 64, LDA_ = PW + 1, LDB_ = 64 + 4;
   __shared__ float As[64 * LDA_];                 // L21 tile, (i, k)
   __shared__ __align__(16) float Bs[PW * LDB_];  // U12 tile, (k, j)
@@ -659,8 +667,16 @@ __global__ __launch_bounds__(256) void lu_update_kernel(float* __restrict__ W, i
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const int l32 = lane & 31, lh = lane >> 5;
   v16f acc;
+  if (A0) {
+    // first block, in place of the input copy: C from the input through the row map
+    const float* Ab = A0 + b * (int64_t)N * N;
+    const int* rb = rmap + b * N;
 #pragma unroll
-  for (int v = 0; v < 16; ++v) acc[v] = Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32];
+    for (int v = 0; v < 16; ++v) acc[v] = Ab[rb[i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)] * N + j0 + wn + l32];
+  } else {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32];
+  }
   float4 a4[4], b4[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -691,17 +707,18 @@ __global__ __launch_bounds__(256) void lu_update_kernel(float* __restrict__ W, i
 // lu_panel_kernel with NT threads, the others lu_panel_reg_kernel.
 template <int MR, int NT>
 static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int* src, float* X,
-                      int* g0, bool fact, hipStream_t s) {
+                      int* g0, bool fact, const float* A_in, hipStream_t s) {
   constexpr int PW = 64;
   const int nblk = N / PW;
   constexpr int MAXM = MR < 1024 ? 1024 : MR;
   for (int blk = 0; blk < nblk; ++blk) {
     const int r0 = blk * PW;
     const int m = N - r0;
+    const float* A0 = blk == 0 ? A_in : nullptr;  // input read in place of a copy
     if (m <= 1024) {
 #define FX_PANEL_REG(T)                                                                                       \
   hipLaunchKernelGGL((lu_panel_reg_kernel<T>), dim3((unsigned)batch), dim3(T), 0, s, W, N, r0, blk, piv, nsw, \
-                     nblk, src, X, g0)
+                     nblk, src, X, g0, A0)
       if (m <= 64) FX_PANEL_REG(64);
       else if (m <= 128) FX_PANEL_REG(128);
       else if (m <= 256) FX_PANEL_REG(256);
@@ -717,7 +734,7 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
     const int nright = (N - r0 - PW + 63) / 64;
     if (nleft + nright > 0) {
       hipLaunchKernelGGL((lu_urow_kernel<PW, MAXM>), dim3(nleft + nright, (unsigned)batch), dim3(256), 0, s,
-                         W, N, r0, src, X, nleft);
+                         W, N, r0, src, X, nleft, A0);
       if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     }
     const int mt = N - r0 - PW;  // a multiple of 64
@@ -726,7 +743,7 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
       for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
         const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
         hipLaunchKernelGGL(lu_update_kernel, dim3(nt * nt, (unsigned)nb), dim3(256), 0, s, W + b0 * (int64_t)N * N, N,
-                           r0, nt);
+                           r0, nt, A0 ? A0 + b0 * (int64_t)N * N : nullptr, src + b0 * N);
         if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
       }
     }
@@ -755,14 +772,20 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   int* src = (int*)take((size_t)batch * N * 4);
   float* X = (float*)take((size_t)batch * (PW / 16) * 1024);
   int* g0 = parts ? (int*)take((size_t)batch * N * 4) : nullptr;
-  if (n == N && ((uintptr_t)A & 15) == 0) {  // no padding: a straight streaming copy
-    const int st = launch_copy(A, W, batch * (int64_t)N * N, s);
-    if (st != FX_OK) return st;
-  } else {
-    const int64_t tot = (int64_t)N * N;
-    hipLaunchKernelGGL(copy_pad_kernel, dim3((unsigned)((tot + 255) / 256), (unsigned)batch), dim3(256),
-                       0, s, A, n, W, N);
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  // No padding and panels held in registers throughout (N <= 1024): the first block's
+  // kernels read the input directly and together write all of W, so no copy is made.
+  // Otherwise the input is copied (identity-padded) into W first.
+  const bool direct = n == N && N <= 1024 && ((uintptr_t)A & 15) == 0;
+  if (!direct) {
+    if (n == N && ((uintptr_t)A & 15) == 0) {  // no padding: a straight streaming copy
+      const int st = launch_copy(A, W, batch * (int64_t)N * N, s);
+      if (st != FX_OK) return st;
+    } else {
+      const int64_t tot = (int64_t)N * N;
+      hipLaunchKernelGGL(copy_pad_kernel, dim3((unsigned)((tot + 255) / 256), (unsigned)batch), dim3(256),
+                         0, s, A, n, W, N);
+      if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    }
   }
   if (g0) {
     const int64_t tot = batch * N;
@@ -770,11 +793,11 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   }
   int st;
   if (N <= 1024)
-    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, src, X, g0, parts, direct ? A : nullptr, s);
   else if (N <= 2048)
-    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, src, X, g0, parts, nullptr, s);
   else
-    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, src, X, g0, parts, s);
+    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, src, X, g0, parts, nullptr, s);
   if (st != FX_OK) return st;
   hipLaunchKernelGGL(lu_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, piv, nsw, N,
                      nblk, sign, logabs, batch);
