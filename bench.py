@@ -169,6 +169,27 @@ def cpu_baseline(sample, which):
     return reps * sample.shape[0] / t, reps, t
 
 
+def cpu_library():
+    """numpy.linalg.slogdet (LAPACK getrf per matrix) on the full C1 batch on the host cores:
+    the CPU library figure beside the oracle port (jax, whose jnp.linalg.slogdet the
+    reference would time, is not installed). One thread, then up to 16 (the box's CPU
+    share for one GPU). Returns {threads: matrices/s}."""
+    from threadpoolctl import threadpool_limits
+
+    A = _inputs(4096, 128, 0)
+    out = {}
+    for threads in (1, min(16, os.cpu_count() or 1)):
+        with threadpool_limits(limits=threads):
+            np.linalg.slogdet(A[:64])
+            reps, t, t0 = 0, 0.0, time.perf_counter()
+            while t < 3.0:
+                np.linalg.slogdet(A)
+                reps += 1
+                t = time.perf_counter() - t0
+        out[threads] = A.shape[0] * reps / t
+    return out
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -227,6 +248,19 @@ def main():
             f"path), {head['sample'].shape[0]} of the {head['B']} n={head['n']} matrices x "
             f"{reps} reps in {t:.1f} s, one thread",
         }
+    lib = None
+    if not args.no_cpu and "c1" in only:
+        rates = cpu_library()
+        t1, tn = sorted(rates)[0], sorted(rates)[-1]
+        lib = {
+            "value": round(rates[t1], 1),
+            "unit": "matrices/s",
+            "cores": t1,
+            "kind": "library",
+            "value_threads": {str(k): round(v, 1) for k, v in rates.items()},
+            "sample": f"numpy.linalg.slogdet (LAPACK getrf) on the full C1 batch (B = 4096, n = 128), "
+            f"{t1} and {tn} threads; compare workloads.c1",
+        }
     workloads = {
         k: {"workload": v["name"], "B": v["B"], "n": v["n"], "ms_per_step": round(v["ms"], 5),
             "matrices_per_s": round(v["rate"], 1),
@@ -251,6 +285,7 @@ def main():
                    "n": head["n"], "baseline_config": "configs[1]" if head is res.get("c2") else "configs[0]"},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_library": lib,
         "workloads": workloads,
     }
     print(json.dumps(line), flush=True)

@@ -43,9 +43,7 @@ __device__ __forceinline__ bool mask_upper(int m) { return m == MASK_UPPER || m 
 // Tile loads: VEC uses 16-byte global loads along the operand's contiguous dimension
 // (requires that dimension, the leading dimensions, batch strides and base pointers to be
 // multiples of 4 floats), otherwise one float per load. Masks are applied in registers.
-// PREC: beta != 0 with C read before the K loop, so the read latency overlaps the
-// products (the LU trailing update, K = 64: 12 % faster at m = 448).
-template <int BM, int BN, bool VEC, bool PREC>
+template <int BM, int BN, bool VEC>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   constexpr int LDSA = BM + 4, LDSB = BN + 4;
   constexpr int WM = BM / 2, WN = BN / 2;   // per-wave quarter
@@ -269,20 +267,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
     for (int b = 0; b < TN; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
-  float cpre[PREC ? TM : 1][PREC ? TN : 1][16];
-  if (PREC) {
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-      for (int b = 0; b < TN; ++b) {
-        const int c = j0 + wn + 32 * b + l32;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int r = i0 + wm + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
-          cpre[a][b][v] = (r < d.M && c < d.N) ? C[(int64_t)r * d.ldc + c] : 0.0f;
-        }
-      }
-  }
   if (klo < khi) load_stage(klo);
 
   int buf = 0;
@@ -326,8 +310,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = i0 + wm + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
-        if (PREC) cv[v] = cpre[PREC ? a : 0][PREC ? b : 0][v];
-        else cv[v] = (d.beta != 0.0f && r < d.M && c < d.N) ? C[(int64_t)r * d.ldc + c] : 0.0f;
+        cv[v] = (d.beta != 0.0f && r < d.M && c < d.N) ? C[(int64_t)r * d.ldc + c] : 0.0f;
       }
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -586,9 +569,8 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
       continue;
     }
     const dim3 grid(tiles, (unsigned)nb, nb2);
-    if (vec && d.beta != 0.0f) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, true>), grid, dim3(256), 0, s, e);
-    else if (vec) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, false>), grid, dim3(256), 0, s, e);
-    else hipLaunchKernelGGL((gemm_kernel<BM, BN, false, false>), grid, dim3(256), 0, s, e);
+    if (vec) hipLaunchKernelGGL((gemm_kernel<BM, BN, true>), grid, dim3(256), 0, s, e);
+    else hipLaunchKernelGGL((gemm_kernel<BM, BN, false>), grid, dim3(256), 0, s, e);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
