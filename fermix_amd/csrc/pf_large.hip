@@ -41,8 +41,10 @@ struct PfCand {
 };
 
 struct PfRowA {
-  int row;
-  int pad[3];
+  int row;    // at position c
+  int next1;  // at position c + 1
+  int next2;  // at position c + 2
+  int pad;
   float g[PFB];
 };
 
@@ -91,10 +93,12 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     for (int k = 0; k < PB; ++k) G[s][k] = 0.0f;
   }
   int nsw = 0;
+  float mv_next[R];  // row a of the next pair step, loaded ahead (see below)
   static_for<0, PB / 2>([&](auto tc) {
     constexpr int t = decltype(tc)::value;
     const int c = 2 * t;  // local position of row a
-    // 1. the row at position c publishes its index and G row
+    // 1. the row at position c publishes its index and G row; the rows at c + 1 and c + 2
+    //    their indices (the next step's row a is one of them)
 #pragma unroll
     for (int s = 0; s < R; ++s) {
       if (valid[s] && pos[s] == c) {
@@ -102,17 +106,24 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
 #pragma unroll
         for (int k = 0; k < 2 * t; ++k) rowa.g[k] = opaque(G[s][k]);
       }
+      if (valid[s] && pos[s] == c + 1) rowa.next1 = R * tid + s;
+      if (valid[s] && pos[s] == c + 2) rowa.next2 = R * tid + s;
     }
     __syncthreads();
-    const int qa = rowa.row;
+    const int qa = rowa.row, qn1 = rowa.next1, qn2 = rowa.next2;
     const float* ga = rowa.g;
     // x = column a of the current matrix on my rows: M[i][qa] = -M[qa][i] + corrections
     float x[R];
     {
-      const float* rowp = Mb + (int64_t)qa * N;
       float mv[R];
+      if constexpr (t == 0) {
+        const float* rowp = Mb + (int64_t)qa * N;
 #pragma unroll
-      for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowp[R * tid + s] : 0.0f;
+        for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowp[R * tid + s] : 0.0f;
+      } else {
+#pragma unroll
+        for (int s = 0; s < R; ++s) mv[s] = mv_next[s];
+      }
 #pragma unroll
       for (int s = 0; s < R; ++s) {
         float v = -mv[s];
@@ -168,6 +179,14 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     nsw += (pp != c + 1) ? 1 : 0;
     pin(nsw);
     if (tid == 0) d_out[b * (N / 2) + (r0 >> 1) + t] = d;
+    // the next step's row a sits at position c + 2 after this step's swap: the old row
+    // at c + 1 if the pivot came from c + 2, else the row at c + 2. Its load goes out
+    // now, beside the pivot row's (the block-start matrix is read-only in the panel).
+    if constexpr (t + 1 < PB / 2) {
+      const float* rown = Mb + (int64_t)(pp == c + 2 ? qn1 : qn2) * N;
+#pragma unroll
+      for (int s = 0; s < R; ++s) mv_next[s] = valid[s] ? rown[R * tid + s] : 0.0f;
+    }
     // y = column p on my rows
     float y[R];
     {
@@ -453,7 +472,7 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
         hipLaunchKernelGGL((pf_panel_kernel<512, 2, PFB>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0, blk,
                            nblk, d, nsw, src, Gn, orig, gbuf);
       else
-        hipLaunchKernelGGL((pf_panel_kernel<512, 4, PFB>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0,
+        hipLaunchKernelGGL((pf_panel_kernel<1024, 2, PFB>), dim3((unsigned)batch), dim3(1024), 0, s, cur, N, r0,
                            blk, nblk, d, nsw, src, Gn, orig, gbuf);
     } else {
       if (m <= 1024)
