@@ -134,7 +134,7 @@ int32_t fx_pf_padded_size(int32_t n) {
 }
 
 int32_t fx_pf_block_columns(int32_t n) {
-  return (pf_family(n) != FAM_BLOCKED || pf_large_padded(n) > 2048) ? 16 : 32;
+  return pf_family(n) != FAM_BLOCKED ? 16 : pf_large_block_cols(pf_large_padded(n));
 }
 
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {

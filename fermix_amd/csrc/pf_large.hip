@@ -1,6 +1,7 @@
 // Blocked Parlett-Reid with partial pivoting for 128 < n <= 4096 (any batch). The skew
 // matrix lives in one workspace buffer (full storage, exactly skew). Per block of PB
-// columns (PB / 2 pair steps; PB = 32, or 16 for N > 2048) at r0:
+// columns (PB / 2 pair steps; PB = 64 for 512 <= N <= 1024 a multiple of 64, 32 for the other
+// N <= 2048, 16 above) at r0:
 //   1. pf_panel_kernel (one workgroup of NT = 256..1024 threads per matrix, each lane
 //      owning R = 2 or 4 of the m = N - r0 rows): the pair steps with the tau / w vectors
 //      kept in registers as G (m x PB); column a and column p of the current matrix are read
@@ -26,18 +27,21 @@ namespace fx {
 // SIMD resident, against two for 128 x 128 tiles, and the in-place update streams
 // M about 10 % faster at n = 1200 .. 2048.
 constexpr int PF_UPDATE_TILE = 64;
-constexpr int PFB = 32;  // columns per block (16 pair steps) for N <= 2048
+constexpr int PFB_L = 64;   // columns per block (32 pair steps) for 512 <= N <= 1024, N % 64 == 0
+constexpr int PFB = 32;     // for the other N <= 2048
 constexpr int PFB_XL = 16;  // for 2048 < N <= PF_LARGE_MAXN
 
 // Columns per block for padded order N.
-static int pf_block_cols(int N) { return N > 2048 ? PFB_XL : PFB; }
+int pf_large_block_cols(int N) {
+  return N > 2048 ? PFB_XL : (N >= 512 && N <= 1024 && N % PFB_L == 0 ? PFB_L : PFB);
+}
 
 struct PfCand {
   unsigned key;
   int row;
   int pos;
   float xv;  // x at the candidate row (d = -x[p])
-  float g[PFB];
+  float g[PFB_L];
 };
 
 struct PfRowA {
@@ -45,7 +49,7 @@ struct PfRowA {
   int next1;  // at position c + 1
   int next2;  // at position c + 2
   int pad;
-  float g[PFB];
+  float g[PFB_L];
 };
 
 // Copy a (B, n, n) into M (B, N, N): S = (a - a^T)/2 (or a) with [[0,1],[-1,0]] padding.
@@ -411,7 +415,7 @@ int pf_large_padded(int n) { return ((n + 31) / 32) * 32; }
 
 size_t pf_large_workspace(int64_t batch, int n, bool fact) {
   const int N = pf_large_padded(n);
-  const int PB = pf_block_cols(N);
+  const int PB = pf_large_block_cols(N);
   const int nblk = N / PB;
   size_t bytes = 0;
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
@@ -424,6 +428,39 @@ size_t pf_large_workspace(int64_t batch, int n, bool fact) {
   return bytes;
 }
 
+// One block of PB columns at r0 = blk * PB: the panel (NT = 256, 512 or 1024 threads, R
+// rows per lane) and, unless it is the last block, the in-place trailing update.
+template <int PB, int R>
+static int pf_block(float* M, int N, int blk, int nblk, int64_t batch, float* d, int* nsw, int* src, float* Gn,
+                    int* orig, float* gbuf, hipStream_t s) {
+  const int r0 = blk * PB;
+  const int m = N - r0;
+  if (m <= 256 * R)
+    hipLaunchKernelGGL((pf_panel_kernel<256, R, PB>), dim3((unsigned)batch), dim3(256), 0, s, M, N, r0, blk, nblk,
+                       d, nsw, src, Gn, orig, gbuf);
+  else if (m <= 512 * R)
+    hipLaunchKernelGGL((pf_panel_kernel<512, R, PB>), dim3((unsigned)batch), dim3(512), 0, s, M, N, r0, blk, nblk,
+                       d, nsw, src, Gn, orig, gbuf);
+  else if constexpr (PB * R <= 64)  // G[R][PB] fits the 128 VGPRs of a 1024-thread workgroup
+    hipLaunchKernelGGL((pf_panel_kernel<1024, R, PB>), dim3((unsigned)batch), dim3(1024), 0, s, M, N, r0, blk,
+                       nblk, d, nsw, src, Gn, orig, gbuf);
+  else
+    return FX_ERR_UNSUPPORTED;
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  const int r1 = r0 + PB;
+  if (r1 >= N) return FX_OK;
+  constexpr int TU = PF_UPDATE_TILE;
+  const int nt = (N - r1 + TU - 1) / TU;
+  const int64_t NN = (int64_t)N * N;
+  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+    const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
+    hipLaunchKernelGGL((pf_update_kernel<PB, TU>), dim3(nt * (nt + 1) / 2, (unsigned)nb), dim3(256), 0, s,
+                       M + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PB);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  }
+  return FX_OK;
+}
+
 // Forward (and, with gbuf/dout/perm, the factors: gbuf (B, N/PB, N, PB) by original row,
 // d (B, N/2), perm (B, N) final position -> original row).
 int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
@@ -432,7 +469,7 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
   if (N > PF_LARGE_MAXN) return FX_ERR_UNSUPPORTED;
   const bool fact = gbuf != nullptr;
   if (!ws || ws_bytes < pf_large_workspace(batch, n, fact)) return FX_ERR_WORKSPACE;
-  const int PB = pf_block_cols(N);
+  const int PB = pf_large_block_cols(N);
   const int nblk = N / PB;
   char* p = (char*)ws;
   auto take = [&](size_t x) {
@@ -460,47 +497,11 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     const int64_t tot = batch * N;
     hipLaunchKernelGGL(pf_iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, orig, N, tot);
   }
-  float* cur = M0;
   for (int blk = 0; blk < nblk; ++blk) {
-    const int r0 = blk * PB;
-    const int m = N - r0;
-    if (PB == PFB) {
-      if (m <= 512)
-        hipLaunchKernelGGL((pf_panel_kernel<256, 2, PFB>), dim3((unsigned)batch), dim3(256), 0, s, cur, N, r0, blk,
-                           nblk, d, nsw, src, Gn, orig, gbuf);
-      else if (m <= 1024)
-        hipLaunchKernelGGL((pf_panel_kernel<512, 2, PFB>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0, blk,
-                           nblk, d, nsw, src, Gn, orig, gbuf);
-      else
-        hipLaunchKernelGGL((pf_panel_kernel<1024, 2, PFB>), dim3((unsigned)batch), dim3(1024), 0, s, cur, N, r0,
-                           blk, nblk, d, nsw, src, Gn, orig, gbuf);
-    } else {
-      if (m <= 1024)
-        hipLaunchKernelGGL((pf_panel_kernel<256, 4, PFB_XL>), dim3((unsigned)batch), dim3(256), 0, s, cur, N, r0,
-                           blk, nblk, d, nsw, src, Gn, orig, gbuf);
-      else if (m <= 2048)
-        hipLaunchKernelGGL((pf_panel_kernel<512, 4, PFB_XL>), dim3((unsigned)batch), dim3(512), 0, s, cur, N, r0,
-                           blk, nblk, d, nsw, src, Gn, orig, gbuf);
-      else
-        hipLaunchKernelGGL((pf_panel_kernel<1024, 4, PFB_XL>), dim3((unsigned)batch), dim3(1024), 0, s, cur, N,
-                           r0, blk, nblk, d, nsw, src, Gn, orig, gbuf);
-    }
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    const int r1 = r0 + PB;
-    if (r1 < N) {
-      constexpr int TU = PF_UPDATE_TILE;
-      const int nt = (N - r1 + TU - 1) / TU;
-      for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
-        const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
-        if (PB == PFB)
-          hipLaunchKernelGGL((pf_update_kernel<PFB, TU>), dim3(nt * (nt + 1) / 2, (unsigned)nb), dim3(256), 0, s,
-                             cur + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PB);
-        else
-          hipLaunchKernelGGL((pf_update_kernel<PFB_XL, TU>), dim3(nt * (nt + 1) / 2, (unsigned)nb), dim3(256), 0,
-                             s, cur + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PB);
-        if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-      }
-    }
+    const int st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, s)
+                   : PB == PFB ? pf_block<PFB, 2>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, s)
+                               : pf_block<PFB_XL, 4>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, s);
+    if (st != FX_OK) return st;
   }
   hipLaunchKernelGGL(pf_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, d, nsw, N / 2, nblk,
                      sign, logabs, batch);

@@ -107,7 +107,8 @@ size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign,
                   float* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
-/* Columns per block of the Parlett-Reid factors (16 for n <= 128, 32 for n <= 2048, 16 above). */
+/* Columns per block of the Parlett-Reid factors: 16 for n <= 128; 64 for 480 < n <= 1024
+ * when fx_pf_padded_size(n) is a multiple of 64; 32 for the other n <= 2048; 16 above. */
 int32_t fx_pf_block_columns(int32_t n);
 
 /* The Parlett-Reid factors P S' P^T = L D L^T of the same run (S' = S padded with

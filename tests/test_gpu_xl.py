@@ -110,9 +110,10 @@ def test_slogpf_xl(dev, n):
     assert sz[1] == 0 and np.isneginf(lz[1]) and sz[0] == sgn[0]
 
 
-@pytest.mark.parametrize("n", [2176, 4096])
+@pytest.mark.parametrize("n", [1000, 2176, 4096])
 def test_slogpf_grad_xl(dev, n):
-    """S^-1 (inverse mode) and pf S^-1 (adjugate mode) from the 16-column-block factors."""
+    """S^-1 (inverse mode) and pf S^-1 (adjugate mode) from the 64-column-block (n = 1000,
+    padded to 1024) and 16-column-block factors."""
     B = 2
     rng = np.random.default_rng(8400 + n)
     S, sgn, lab, S64 = _bjb(rng, B, n)
