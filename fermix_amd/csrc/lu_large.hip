@@ -1,5 +1,6 @@
 // Blocked LU with partial pivoting for 128 < n <= 4096 (any batch): per block of PW = 64
-// columns at r0 three launches,
+// columns at r0 three launches (blocks go in pairs, see run_blocks: the first block's
+// trailing update is deferred and merged into the second's at K = 128),
 //   1. the panel (one workgroup per matrix), factored in place in the work buffer; the
 //      rows stay in place during the panel (virtual pivoting) and each column step finds
 //      the pivot with a per-wave DPP max and one workgroup barrier (every wave posts its
@@ -16,9 +17,11 @@
 //      src[new position] = old row and X_s = L_ss^-1 of every sub-panel;
 //   2. lu_urow_kernel   (matrix x 64-column strip): applies the row permutation to the
 //      strip, touching only the rows that move, and for trailing strips forms the U rows
-//      U12 = L11^-1 A12 by blocked forward substitution on MFMA;
-//   3. lu_update_kernel: the trailing update A22 -= L21 U12 on MFMA (K = 64, one LDS stage
-//      per 64 x 64 tile).
+//      U12 = L11^-1 A12 by blocked forward substitution on MFMA (in a pair's second block
+//      after subtracting the first block's deferred update from the pivot rows);
+//   3. lu_update_kernel: the trailing update A22 -= L21 U12 on MFMA, one LDS stage of
+//      K = 64 per 64 x 64 tile at a time: a pair's first block updates only the second
+//      block's 64 columns, the second block the whole trailing matrix at K = 128.
 // A final kernel turns the pivots and swap counts into (sign, logabs).
 //
 // Reference roles replaced (ChenAo-Phys/fermix): _lu_core's block loop (src/fermix/
@@ -475,25 +478,30 @@ __global__ __launch_bounds__(NT) void lu_panel_reg_kernel(float* __restrict__ W,
 template <int PW, int MAXM>
 __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, int N, int r0,
                                                       const int* __restrict__ src,
-                                                      const float* __restrict__ Xg,
-                                                      int nleft, const float* __restrict__ A0) {
+                                                      const float* __restrict__ Xg, int lfirst,
+                                                      int nleft, const float* __restrict__ A0,
+                                                      const int* __restrict__ rmap, int rc,
+                                                      int* __restrict__ comp_out) {
   static_assert(PW == 64, "one 16-column slice of the strip per wave");
   constexpr int NSUB = PW / 16;
   __shared__ int list[2 * PW];
   __shared__ int srcv[2 * PW];
   __shared__ int srcU[PW];
+  __shared__ int srcUr[PW];
   __shared__ int cnt;
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int strip = blockIdx.x;
   const bool left = strip < nleft;
-  const int cstart = left ? 64 * strip : r0 + PW + 64 * (strip - nleft);
+  const int cstart = left ? 64 * (lfirst + strip) : r0 + PW + 64 * (strip - nleft);
   const int ncol = min(64, left ? r0 - cstart : N - cstart);
   float* Wb = W + b * (int64_t)N * N;
-  // A0 (first block, in place of the input copy): the rows are read from the input, and
-  // the trailing update writes every row below the block (from the input, through the
-  // row map), so only U12 is stored here
-  const float* Rb = A0 ? A0 + b * (int64_t)N * N : Wb;
+  // A0 (first block pair, in place of the input copy): the trailing rows are read from
+  // the input (position p of the first block's order is input row rmap[p] when rmap is
+  // given), and the trailing update writes every row below the block (from the input,
+  // through the row maps), so only U12 is stored here
+  const float* Rb = A0 && !left ? A0 + b * (int64_t)N * N : Wb;
+  const int* rm = rmap && !left ? rmap + b * N : nullptr;
   const int* sb = src + b * N;
   const int m = N - r0;
   // pass 1 (indices): the moved rows (position, source row) and the source rows of
@@ -514,14 +522,27 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
 #pragma unroll
   for (int q = 0; q < MQ; ++q) {
     const int p = tid + 256 * q;
+    // srcv / srcUr index the rows of Rb (through rmap), srcU those of W
+    const int sr = rm && p < m ? rm[sv[q]] : sv[q];
     if (p < m && sv[q] != r0 + p) {
       const int k = atomicAdd(&cnt, 1);
       if (k < 2 * PW) {
         list[k] = p;
-        srcv[k] = sv[q];
+        srcv[k] = sr;
       }
     }
-    if (p < PW) srcU[p] = sv[q];
+    if (p < PW) {
+      srcU[p] = sv[q];
+      srcUr[p] = sr;
+    }
+  }
+  // the composed map of the first block pair (position -> input row), for its update
+  if (comp_out && rm && blockIdx.x == nleft) {  // the first trailing strip
+#pragma unroll
+    for (int q = 0; q < MQ; ++q) {
+      const int p = tid + 256 * q;
+      if (p < m) comp_out[b * N + r0 + p] = rm[sv[q]];
+    }
   }
   __syncthreads();
   const int nm = min(cnt, 2 * PW);
@@ -545,7 +566,7 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        a12[s][v] = Rb[(int64_t)srcU[16 * s + 4 * g + v] * N + cstart + col];
+        a12[s][v] = Rb[(int64_t)srcUr[16 * s + 4 * g + v] * N + cstart + col];
         xv[s][v] = Xb[s * 256 + li * 16 + 4 * g + v];
       }
 #pragma unroll
@@ -560,9 +581,34 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
 #pragma unroll
   for (int u = 0; u < 2 * PW / 4; ++u) {
     const int k = (tid >> 6) + 4 * u;
-    if (!A0 && k < nm && cl < ncol && (left || list[k] >= PW)) Wb[(int64_t)(r0 + list[k]) * N + cstart + cl] = mv[u];
+    if ((left || !A0) && k < nm && cl < ncol && (left || list[k] >= PW)) Wb[(int64_t)(r0 + list[k]) * N + cstart + cl] = mv[u];
   }
   if (left) return;
+  if (rc >= 0) {
+    // deferred update of the previous block (rows / columns rc .. rc+63, not yet applied
+    // to these columns): A12 -= L21' U12' on the pivot rows, with L21' read at the pivot
+    // rows' current (pre-move) slots and U12' from rows rc .. rc+63. MFMA c takes
+    // k = 16 g + c on lane (g, li): four 16-byte L21' loads per row block, one U12' row
+    // element per c.
+    float uv[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) uv[c] = Wb[(int64_t)(rc + 16 * g + c) * N + cstart + col];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+      const float* Lr = Wb + (int64_t)srcU[16 * s + li] * N + rc + 16 * g;
+      float lw[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 t = *reinterpret_cast<const float4*>(Lr + 4 * q);
+        lw[4 * q] = t.x;
+        lw[4 * q + 1] = t.y;
+        lw[4 * q + 2] = t.z;
+        lw[4 * q + 3] = t.w;
+      }
+#pragma unroll
+      for (int c = 0; c < 16; ++c) a12[s] = mfma16(-lw[c], uv[c], a12[s]);
+    }
+  }
   v4f U[NSUB];
 #pragma unroll
   for (int s = 0, q0 = 0; s < NSUB; q0 += s, ++s) {
@@ -631,7 +677,9 @@ size_t lu_large_workspace(int64_t batch, int n, bool parts) {
   add((size_t)batch * N * N * 4);        // W
   add((size_t)batch * N * 4);            // pivots
   add((size_t)batch * nblk * 4);         // swap counts
-  add((size_t)batch * N * 4);            // src
+  add((size_t)batch * N * 4);            // src (even blocks)
+  add((size_t)batch * N * 4);            // src (odd blocks)
+  add((size_t)batch * N * 4);            // composed map of the first block pair
   add((size_t)batch * (PW / 16) * 1024); // X
   if (parts) add((size_t)batch * N * 4); // g0
   return bytes;
@@ -639,19 +687,27 @@ size_t lu_large_workspace(int64_t batch, int n, bool parts) {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// The trailing update A22 -= L21 U12 of one block (K = PW = 64) over the 64 x 64 tiles of
-// the mt x mt trailing block (mt a multiple of 64, every tile interior). The whole K
-// range is one LDS stage, so every load of a tile -- its C (straight into the
-// accumulators, which the MFMAs then reduce: C - L21 U12 with no epilogue arithmetic),
-// L21 rows and U12 columns -- is issued up front and the tile needs one barrier: more
-// bytes in flight per workgroup than a K-pipelined GEMM at this short K, where the
-// update is bound by reading and writing C. XCD-aware tile order when the batch is a
-// multiple of 8 (one matrix's L21 / U12 fetched into one L2).
-__global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W, int N, int r0, int nt,
-                                                        const float* __restrict__ A0, const int* __restrict__ rmap) {
-  constexpr int PW = 64, LDA_ = PW + 1, LDB_ = 64 + 4;
-  __shared__ float As[64 * LDA_];                 // L21 tile, (i, k)
-  __shared__ __align__(16) float Bs[PW * LDB_];  // U12 tile, (k, j)
+// The trailing update A22 -= L21 U12 over K = 64 KC columns from r0 (KC = 1: one block,
+// KC = 2: a block pair whose first update was deferred), on the 64 x 64 tiles of rows
+// >= r1 = r0 + 64 KC and of ntc tile columns from r1. Every K chunk of 64 is one LDS
+// stage; every load of a tile -- its C (straight into the accumulators, which the MFMAs
+// then reduce: C - L21 U12 with no epilogue arithmetic), the first chunk's L21 rows and
+// U12 columns -- is issued up front, the next chunk's while the current chunk's MFMAs
+// run: more bytes in flight per workgroup than a K-pipelined GEMM at this short K.
+// Row gathers:
+//  * rmapL (KC = 2): L21 of the first block at row rmapL[p] (its rows were permuted by the
+//    second block's pivots only in the other columns);
+//  * A0 (first block pair, in place of the input copy): C of position p is input row
+//    rmapC[p].
+// XCD-aware tile order when the batch is a multiple of 8 (one matrix's L21 / U12 fetched
+// into one L2).
+template <int KC>
+__global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W, int N, int r0, int ntc,
+                                                        const float* __restrict__ A0, const int* __restrict__ rmapC,
+                                                        const int* __restrict__ rmapL) {
+  constexpr int LDA_ = 64 + 1, LDB_ = 64 + 4;
+  __shared__ float As[64 * LDA_];                 // L21 chunk, (i, k)
+  __shared__ __align__(16) float Bs[64 * LDB_];  // U12 chunk, (k, j)
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   int64_t b = blockIdx.y;
   int tx = blockIdx.x;
@@ -662,58 +718,110 @@ __global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W
     b = (slot / gridDim.x) * 8 + (lin & 7);
   }
   float* Wb = W + b * (int64_t)N * N;  // offsets below are 32-bit (N * N < 2^31)
-  const int r1 = r0 + PW;
-  const int i0 = r1 + 64 * (tx / nt), j0 = r1 + 64 * (tx % nt);
+  const int r1 = r0 + 64 * KC;
+  const int i0 = r1 + 64 * (tx / ntc), j0 = r1 + 64 * (tx % ntc);
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const int l32 = lane & 31, lh = lane >> 5;
   v16f acc;
   if (A0) {
-    // first block, in place of the input copy: C from the input through the row map
     const float* Ab = A0 + b * (int64_t)N * N;
-    const int* rb = rmap + b * N;
+    const int* rb = rmapC + b * N;
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[v] = Ab[rb[i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)] * N + j0 + wn + l32];
   } else {
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[v] = Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32];
   }
-  float4 a4[4], b4[4];
+  // staging of one chunk: thread (r = e / 16, q = 4 (e % 16)) of e = tid + 256 u holds
+  // L21 (i0 + r, q .. q+3) and U12 (r, j0 + q .. q+3) of the chunk; float arrays stay in
+  // registers
+  float av[16], bw[16];
+  auto load = [&](int c) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int e = tid + 256 * u, r = e >> 4, q = 4 * (e & 15);
-    a4[u] = *reinterpret_cast<const float4*>(Wb + (i0 + r) * N + r0 + q);
-    b4[u] = *reinterpret_cast<const float4*>(Wb + (r0 + r) * N + j0 + q);
+    for (int u = 0; u < 4; ++u) {
+      const int e = tid + 256 * u, r = e >> 4, q = 4 * (e & 15);
+      const int ra = (KC == 2 && c == 0 && rmapL) ? rmapL[b * N + i0 + r] : i0 + r;
+      const float4 x = *reinterpret_cast<const float4*>(Wb + ra * N + r0 + 64 * c + q);
+      const float4 y = *reinterpret_cast<const float4*>(Wb + (r0 + 64 * c + r) * N + j0 + q);
+      av[4 * u] = x.x;
+      av[4 * u + 1] = x.y;
+      av[4 * u + 2] = x.z;
+      av[4 * u + 3] = x.w;
+      bw[4 * u] = y.x;
+      bw[4 * u + 1] = y.y;
+      bw[4 * u + 2] = y.z;
+      bw[4 * u + 3] = y.w;
+    }
+  };
+  load(0);
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+    if (c > 0) __syncthreads();  // every wave is done with the previous chunk
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = tid + 256 * u, r = e >> 4, q = 4 * (e & 15);
+      float* pa = As + r * LDA_ + q;
+      pa[0] = av[4 * u];
+      pa[1] = av[4 * u + 1];
+      pa[2] = av[4 * u + 2];
+      pa[3] = av[4 * u + 3];
+      *reinterpret_cast<float4*>(Bs + r * LDB_ + q) = make_float4(bw[4 * u], bw[4 * u + 1], bw[4 * u + 2], bw[4 * u + 3]);
+    }
+    __syncthreads();
+    if (c + 1 < KC) load(c + 1);
+#pragma unroll
+    for (int kp = 0; kp < 32; ++kp)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(-As[(wm + l32) * LDA_ + 2 * kp + lh], Bs[(2 * kp + lh) * LDB_ + wn + l32],
+                                                 acc, 0, 0, 0);
   }
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int e = tid + 256 * u, r = e >> 4, q = 4 * (e & 15);
-    float* pa = As + r * LDA_ + q;
-    pa[0] = a4[u].x;
-    pa[1] = a4[u].y;
-    pa[2] = a4[u].z;
-    pa[3] = a4[u].w;
-    *reinterpret_cast<float4*>(Bs + r * LDB_ + q) = b4[u];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int kp = 0; kp < PW / 2; ++kp)
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(-As[(wm + l32) * LDA_ + 2 * kp + lh], Bs[(2 * kp + lh) * LDB_ + wn + l32],
-                                               acc, 0, 0, 0);
 #pragma unroll
   for (int v = 0; v < 16; ++v) Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32] = acc[v];
 }
 
+// Grid of the trailing update: ntr x ntc tiles per matrix, batches of at most 65535.
+template <int KC>
+static int launch_update(float* W, int N, int64_t batch, int r0, int ntr, int ntc, const float* A0,
+                         const int* rmapC, const int* rmapL, hipStream_t s) {
+  const int64_t NN = (int64_t)N * N;
+  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+    const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
+    hipLaunchKernelGGL((lu_update_kernel<KC>), dim3(ntr * ntc, (unsigned)nb), dim3(256), 0, s, W + b0 * NN, N, r0,
+                       ntc, A0 ? A0 + b0 * NN : nullptr, rmapC ? rmapC + b0 * N : nullptr,
+                       rmapL ? rmapL + b0 * N : nullptr);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  }
+  return FX_OK;
+}
+
 // MR: the largest m of the matrix's panels; panels with m > 1024 (MR > 1024 only) use
 // lu_panel_kernel with NT threads, the others lu_panel_reg_kernel.
+//
+// Blocks go in pairs (r0, r0 + 64): after the first block's U rows, only the next 64
+// columns get its update (the second panel's columns); the second block's U rows take
+// the first block's update themselves, and one K = 128 update then applies both blocks
+// to the trailing matrix, at twice the arithmetic intensity of two K = 64 updates (the
+// update is bound by reading and writing the trailing matrix at K = 64). The first
+// block's L columns are permuted by the second block's pivots only in the parts run,
+// after the K = 128 update (which reads them through the second block's row map).
+// The panels' row maps alternate between srcs[0] (even blocks) and srcs[1] (odd); the
+// first pair, reading the input in place of a copy, composes both into srcs[2].
 template <int MR, int NT>
-static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int* src, float* X,
+static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int* const srcs[3], float* X,
                       int* g0, bool fact, const float* A_in, hipStream_t s) {
   constexpr int PW = 64;
   const int nblk = N / PW;
   constexpr int MAXM = MR < 1024 ? 1024 : MR;
+  auto urow = [&](int r0, const int* src, int lfirst, int nleft, int nright, const float* A0, const int* rmap,
+                  int rc, int* comp) {
+    if (nleft + nright == 0) return FX_OK;
+    hipLaunchKernelGGL((lu_urow_kernel<PW, MAXM>), dim3(nleft + nright, (unsigned)batch), dim3(256), 0, s, W, N, r0,
+                       src, X, lfirst, nleft, A0, rmap, rc, comp);
+    return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+  };
   for (int blk = 0; blk < nblk; ++blk) {
     const int r0 = blk * PW;
     const int m = N - r0;
+    int* src = srcs[blk & 1];
     const float* A0 = blk == 0 ? A_in : nullptr;  // input read in place of a copy
     if (m <= 1024) {
 #define FX_PANEL_REG(T)                                                                                       \
@@ -730,23 +838,25 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
                          nsw, nblk, src, X, g0);
     }
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    const int nleft = fact ? (r0 + 63) / 64 : 0;
-    const int nright = (N - r0 - PW + 63) / 64;
-    if (nleft + nright > 0) {
-      hipLaunchKernelGGL((lu_urow_kernel<PW, MAXM>), dim3(nleft + nright, (unsigned)batch), dim3(256), 0, s,
-                         W, N, r0, src, X, nleft, A0);
-      if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    const int nright = (N - r0 - PW) / 64;  // trailing strips / tile rows (N a multiple of 64)
+    int st;
+    if ((blk & 1) == 0) {
+      // first block of a pair: U rows, then the update of the next panel's columns only
+      st = urow(r0, src, 0, fact ? r0 / 64 : 0, nright, A0, nullptr, -1, nullptr);
+      if (st == FX_OK && nright > 0)
+        st = launch_update<1>(W, N, batch, r0, nright, 1, A0, A0 ? src : nullptr, nullptr, s);
+    } else {
+      // second block: U rows with the first block's deferred update, then both blocks'
+      // update of the trailing matrix; the first pair reads the input through both maps
+      const int rp = r0 - PW;
+      const float* Ain = blk == 1 ? A_in : nullptr;
+      st = urow(r0, src, 0, fact ? rp / 64 : 0, nright, Ain, Ain ? srcs[0] : nullptr, rp,
+                Ain && nright > 0 ? srcs[2] : nullptr);
+      if (st == FX_OK && nright > 0)
+        st = launch_update<2>(W, N, batch, rp, nright, nright, Ain, Ain ? srcs[2] : nullptr, src, s);
+      if (st == FX_OK && fact) st = urow(r0, src, rp / 64, 1, 0, nullptr, nullptr, -1, nullptr);
     }
-    const int mt = N - r0 - PW;  // a multiple of 64
-    if (mt > 0) {
-      const int nt = mt / 64;
-      for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
-        const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
-        hipLaunchKernelGGL(lu_update_kernel, dim3(nt * nt, (unsigned)nb), dim3(256), 0, s, W + b0 * (int64_t)N * N, N,
-                           r0, nt, A0 ? A0 + b0 * (int64_t)N * N : nullptr, src + b0 * N);
-        if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-      }
-    }
+    if (st != FX_OK) return st;
   }
   return FX_OK;
 }
@@ -769,7 +879,8 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   float* W = (float*)take((size_t)batch * N * N * 4);
   float* piv = (float*)take((size_t)batch * N * 4);
   int* nsw = (int*)take((size_t)batch * nblk * 4);
-  int* src = (int*)take((size_t)batch * N * 4);
+  int* const srcs[3] = {(int*)take((size_t)batch * N * 4), (int*)take((size_t)batch * N * 4),
+                        (int*)take((size_t)batch * N * 4)};
   float* X = (float*)take((size_t)batch * (PW / 16) * 1024);
   int* g0 = parts ? (int*)take((size_t)batch * N * 4) : nullptr;
   // No padding and panels held in registers throughout (N <= 1024): the first block's
@@ -793,11 +904,11 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   }
   int st;
   if (N <= 1024)
-    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, src, X, g0, parts, direct ? A : nullptr, s);
+    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, srcs, X, g0, parts, direct ? A : nullptr, s);
   else if (N <= 2048)
-    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, src, X, g0, parts, nullptr, s);
+    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s);
   else
-    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, src, X, g0, parts, nullptr, s);
+    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s);
   if (st != FX_OK) return st;
   hipLaunchKernelGGL(lu_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, piv, nsw, N,
                      nblk, sign, logabs, batch);
