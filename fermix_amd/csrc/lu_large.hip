@@ -67,7 +67,7 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
                                                       int* __restrict__ nsw_out, int nblk,
                                                       int* __restrict__ src_out,
                                                       float* __restrict__ X_out,
-                                                      int* __restrict__ g0) {
+                                                      int* __restrict__ g0, int lmove) {
   using C = LuPanel<MR, PW, NT>;
   constexpr int R = C::R, NSUB = C::NSUB, NW = C::NW;
   __shared__ Cand cand[2][NW];
@@ -251,8 +251,9 @@ __global__ __launch_bounds__(NT) void lu_panel_kernel(float* __restrict__ W, int
     }
   }
   // write the panel back in the new row order, in place, 16 columns at a time: every row
-  // of a pass is read before any is written
-  for (int q = 0; q < NSUB; ++q) {
+  // of a pass is read before any is written. With lmove the previous block's 64 L
+  // columns (left of the panel) go along.
+  for (int q = lmove ? -4 : 0; q < NSUB; ++q) {
     float v[R][16];  // plain floats: an array of float4 stays in scratch memory
 #pragma unroll
     for (int s = 0; s < R; ++s) {
@@ -312,7 +313,7 @@ __global__ __launch_bounds__(NT) void lu_panel_reg_kernel(float* __restrict__ W,
                                                           int* __restrict__ src_out,
                                                           float* __restrict__ X_out,
                                                           int* __restrict__ g0,
-                                                          const float* __restrict__ A0) {
+                                                          const float* __restrict__ A0, int lmove) {
   constexpr int NW = NT / 64, PW = 64, NSUB = 4;
   __shared__ Cand cand[2][NW];
   __shared__ __align__(16) float Prow[16 * PW];  // pivot rows of the sub-panel, all columns
@@ -457,6 +458,28 @@ __global__ __launch_bounds__(NT) void lu_panel_reg_kernel(float* __restrict__ W,
     for (int q = 0; q < PW / 4; ++q) wp[q] = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
     src_out[b * N + r0 + pos] = r0 + tid;
   }
+  if (lmove) {
+    // the previous block's 64 L columns (left of the panel) follow the rows that moved:
+    // all read, one barrier, all written (a moved row's slot belongs to another moved row)
+    const bool mv = valid && pos != tid;
+    if (mv) {
+      const float4* rp = reinterpret_cast<const float4*>(P - PW + (int64_t)tid * N);
+#pragma unroll
+      for (int q = 0; q < PW / 4; ++q) {
+        const float4 t = rp[q];
+        a[4 * q] = t.x;
+        a[4 * q + 1] = t.y;
+        a[4 * q + 2] = t.z;
+        a[4 * q + 3] = t.w;
+      }
+    }
+    __syncthreads();
+    if (mv) {
+      float4* wp = reinterpret_cast<float4*>(P - PW + (int64_t)pos * N);
+#pragma unroll
+      for (int q = 0; q < PW / 4; ++q) wp[q] = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+    }
+  }
   if (g0) {
     // compose the row map: g0[r0 + p] <- g0[r0 + src(p)]
     int* gb = g0 + b * N;
@@ -586,16 +609,16 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
   if (left) return;
   if (rc >= 0) {
     // deferred update of the previous block (rows / columns rc .. rc+63, not yet applied
-    // to these columns): A12 -= L21' U12' on the pivot rows, with L21' read at the pivot
-    // rows' current (pre-move) slots and U12' from rows rc .. rc+63. MFMA c takes
-    // k = 16 g + c on lane (g, li): four 16-byte L21' loads per row block, one U12' row
-    // element per c.
+    // to these columns): A12 -= L21' U12' on the pivot rows, with L21' at the pivot rows'
+    // new positions r0 .. r0+63 (the panel moved those columns along) and U12' from rows
+    // rc .. rc+63. MFMA c takes k = 16 g + c on lane (g, li): four 16-byte L21' loads
+    // per row block, one U12' row element per c.
     float uv[16];
 #pragma unroll
     for (int c = 0; c < 16; ++c) uv[c] = Wb[(int64_t)(rc + 16 * g + c) * N + cstart + col];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
-      const float* Lr = Wb + (int64_t)srcU[16 * s + li] * N + rc + 16 * g;
+      const float* Lr = Wb + (int64_t)(r0 + 16 * s + li) * N + rc + 16 * g;
       float lw[16];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -694,17 +717,13 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // then reduce: C - L21 U12 with no epilogue arithmetic), the first chunk's L21 rows and
 // U12 columns -- is issued up front, the next chunk's while the current chunk's MFMAs
 // run: more bytes in flight per workgroup than a K-pipelined GEMM at this short K.
-// Row gathers:
-//  * rmapL (KC = 2): L21 of the first block at row rmapL[p] (its rows were permuted by the
-//    second block's pivots only in the other columns);
-//  * A0 (first block pair, in place of the input copy): C of position p is input row
-//    rmapC[p].
+// A0 (first block pair, in place of the input copy): C of position p is input row
+// rmapC[p].
 // XCD-aware tile order when the batch is a multiple of 8 (one matrix's L21 / U12 fetched
 // into one L2).
 template <int KC>
 __global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W, int N, int r0, int ntc,
-                                                        const float* __restrict__ A0, const int* __restrict__ rmapC,
-                                                        const int* __restrict__ rmapL) {
+                                                        const float* __restrict__ A0, const int* __restrict__ rmapC) {
   constexpr int LDA_ = 64 + 1, LDB_ = 64 + 4;
   __shared__ float As[64 * LDA_];                 // L21 chunk, (i, k)
   __shared__ __align__(16) float Bs[64 * LDB_];  // U12 chunk, (k, j)
@@ -740,8 +759,7 @@ __global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int e = tid + 256 * u, r = e >> 4, q = 4 * (e & 15);
-      const int ra = (KC == 2 && c == 0 && rmapL) ? rmapL[b * N + i0 + r] : i0 + r;
-      const float4 x = *reinterpret_cast<const float4*>(Wb + ra * N + r0 + 64 * c + q);
+      const float4 x = *reinterpret_cast<const float4*>(Wb + (i0 + r) * N + r0 + 64 * c + q);
       const float4 y = *reinterpret_cast<const float4*>(Wb + (r0 + 64 * c + r) * N + j0 + q);
       av[4 * u] = x.x;
       av[4 * u + 1] = x.y;
@@ -781,13 +799,12 @@ __global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W
 // Grid of the trailing update: ntr x ntc tiles per matrix, batches of at most 65535.
 template <int KC>
 static int launch_update(float* W, int N, int64_t batch, int r0, int ntr, int ntc, const float* A0,
-                         const int* rmapC, const int* rmapL, hipStream_t s) {
+                         const int* rmapC, hipStream_t s) {
   const int64_t NN = (int64_t)N * N;
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
     const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
     hipLaunchKernelGGL((lu_update_kernel<KC>), dim3(ntr * ntc, (unsigned)nb), dim3(256), 0, s, W + b0 * NN, N, r0,
-                       ntc, A0 ? A0 + b0 * NN : nullptr, rmapC ? rmapC + b0 * N : nullptr,
-                       rmapL ? rmapL + b0 * N : nullptr);
+                       ntc, A0 ? A0 + b0 * NN : nullptr, rmapC ? rmapC + b0 * N : nullptr);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
@@ -800,9 +817,9 @@ static int launch_update(float* W, int N, int64_t batch, int r0, int ntr, int nt
 // columns get its update (the second panel's columns); the second block's U rows take
 // the first block's update themselves, and one K = 128 update then applies both blocks
 // to the trailing matrix, at twice the arithmetic intensity of two K = 64 updates (the
-// update is bound by reading and writing the trailing matrix at K = 64). The first
-// block's L columns are permuted by the second block's pivots only in the parts run,
-// after the K = 128 update (which reads them through the second block's row map).
+// update is bound by reading and writing the trailing matrix at K = 64). The second
+// panel moves the first block's L columns along with the rows it moves, so both blocks'
+// L columns are in the final row order for the U-row correction and the K = 128 update.
 // The panels' row maps alternate between srcs[0] (even blocks) and srcs[1] (odd); the
 // first pair, reading the input in place of a copy, composes both into srcs[2].
 template <int MR, int NT>
@@ -811,6 +828,9 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
   constexpr int PW = 64;
   const int nblk = N / PW;
   constexpr int MAXM = MR < 1024 ? 1024 : MR;
+  // unpaired blocks at N <= 256 (measured: the pairs' extra launches and the U-row
+  // correction cost more there than the K = 128 update saves)
+  const bool paired = N > 256;
   auto urow = [&](int r0, const int* src, int lfirst, int nleft, int nright, const float* A0, const int* rmap,
                   int rc, int* comp) {
     if (nleft + nright == 0) return FX_OK;
@@ -823,10 +843,11 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
     const int m = N - r0;
     int* src = srcs[blk & 1];
     const float* A0 = blk == 0 ? A_in : nullptr;  // input read in place of a copy
+    const int lmove = paired && (blk & 1);  // a pair's second panel moves the first block's L along
     if (m <= 1024) {
 #define FX_PANEL_REG(T)                                                                                       \
   hipLaunchKernelGGL((lu_panel_reg_kernel<T>), dim3((unsigned)batch), dim3(T), 0, s, W, N, r0, blk, piv, nsw, \
-                     nblk, src, X, g0, A0)
+                     nblk, src, X, g0, A0, lmove)
       if (m <= 64) FX_PANEL_REG(64);
       else if (m <= 128) FX_PANEL_REG(128);
       else if (m <= 256) FX_PANEL_REG(256);
@@ -835,16 +856,20 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
 #undef FX_PANEL_REG
     } else if constexpr (MR > 1024) {
       hipLaunchKernelGGL((lu_panel_kernel<MR, PW, NT>), dim3((unsigned)batch), dim3(NT), 0, s, W, N, r0, blk, piv,
-                         nsw, nblk, src, X, g0);
+                         nsw, nblk, src, X, g0, lmove);
     }
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     const int nright = (N - r0 - PW) / 64;  // trailing strips / tile rows (N a multiple of 64)
     int st;
-    if ((blk & 1) == 0) {
+    if (!paired) {
+      st = urow(r0, src, 0, fact ? r0 / 64 : 0, nright, A0, nullptr, -1, nullptr);
+      if (st == FX_OK && nright > 0)
+        st = launch_update<1>(W, N, batch, r0, nright, nright, A0, A0 ? src : nullptr, s);
+    } else if ((blk & 1) == 0) {
       // first block of a pair: U rows, then the update of the next panel's columns only
       st = urow(r0, src, 0, fact ? r0 / 64 : 0, nright, A0, nullptr, -1, nullptr);
       if (st == FX_OK && nright > 0)
-        st = launch_update<1>(W, N, batch, r0, nright, 1, A0, A0 ? src : nullptr, nullptr, s);
+        st = launch_update<1>(W, N, batch, r0, nright, 1, A0, A0 ? src : nullptr, s);
     } else {
       // second block: U rows with the first block's deferred update, then both blocks'
       // update of the trailing matrix; the first pair reads the input through both maps
@@ -853,8 +878,7 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
       st = urow(r0, src, 0, fact ? rp / 64 : 0, nright, Ain, Ain ? srcs[0] : nullptr, rp,
                 Ain && nright > 0 ? srcs[2] : nullptr);
       if (st == FX_OK && nright > 0)
-        st = launch_update<2>(W, N, batch, rp, nright, nright, Ain, Ain ? srcs[2] : nullptr, src, s);
-      if (st == FX_OK && fact) st = urow(r0, src, rp / 64, 1, 0, nullptr, nullptr, -1, nullptr);
+        st = launch_update<2>(W, N, batch, rp, nright, nright, Ain, Ain ? srcs[2] : nullptr, s);
     }
     if (st != FX_OK) return st;
   }
