@@ -110,6 +110,16 @@ struct GemmDesc {
   float mirror;
   int xcd8;  // set by launch_gemm: the batch is a multiple of 8 (XCD-aware tile order)
   const int* active;  // optional (batch,) mask: members with active[b] == 0 are skipped
+  // Optional transposed, row-permuted output in place of C (64 x 64 tiles, one batch
+  // index, not lower_only): tout[b][g0[b][j]][i] = scale[b] * alpha (op(A) op(B))[i][j]
+  // for i < nout and g0[b][j] < nout (tout (batch, nout, nout), g0 (batch, N)), and
+  // flags[b][tile] = the tile holds a non-finite value (tiles row-major, ceil(M/64) x
+  // ceil(N/64) per member). scale is optional.
+  float* tout;
+  const int* g0;
+  int nout;
+  const float* scale;
+  int* flags;
 };
 
 // C = alpha op(A) op(B) + beta C for every (batch, second-batch) index.

@@ -48,8 +48,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   constexpr int LDSA = BM + 4, LDSB = BN + 4;
   constexpr int WM = BM / 2, WN = BN / 2;   // per-wave quarter
   constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 tiles per wave
-  __shared__ __align__(16) float As[2][GBK * LDSA];
-  __shared__ __align__(16) float Bs[2][GBK * LDSB];
+  // one LDS block: the two operand stages, reused by the transposed-output epilogue
+  constexpr int LDS_AB = 2 * GBK * LDSA + 2 * GBK * LDSB;
+  static_assert(LDS_AB >= BN * (BM + 1), "transposed tile fits the operand stages");
+  __shared__ __align__(16) float smem[LDS_AB];
+  float(*As)[GBK * LDSA] = reinterpret_cast<float(*)[GBK * LDSA]>(smem);
+  float(*Bs)[GBK * LDSB] = reinterpret_cast<float(*)[GBK * LDSB]>(smem + 2 * GBK * LDSA);
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   int64_t bat = blockIdx.y;
@@ -295,6 +299,38 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
         buf ^= 1;
       }
     }
+  }
+
+  if (d.tout) {
+    // transposed, row-permuted output: the tile goes through LDS transposed (Ts[c][r])
+    // so that each tile column j is stored as one contiguous run of row g0[j] of tout
+    constexpr int LDT = BM + 1;
+    float* Ts = smem;
+    __syncthreads();  // every wave is done with the last stage's operands
+    bool nf = false;
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int b = 0; b < TN; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = wm + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3), c = wn + 32 * b + l32;
+          Ts[c * LDT + r] = acc[a][b][v];
+          nf = nf || (i0 + r < d.M && j0 + c < d.N && !isfinite(acc[a][b][v]));
+        }
+    const int any = __syncthreads_or(nf ? 1 : 0);
+    if (tid == 0) d.flags[bat * (int64_t)gridDim.x + tx] = any;
+    const int* gb = d.g0 + bat * d.N;
+    const float sc = d.scale ? d.alpha * d.scale[bat] : d.alpha;
+    float* ob = d.tout + bat * (int64_t)d.nout * d.nout;
+    for (int e = tid; e < BM * BN; e += 256) {
+      const int cc = e / BM, ii = e % BM, i = i0 + ii, c = j0 + cc;
+      if (i < d.nout && c < d.N) {
+        const int r = gb[c];
+        if (r < d.nout) ob[(int64_t)r * d.nout + i] = sc * Ts[cc * LDT + ii];
+      }
+    }
+    return;
   }
 
   // epilogue: C = alpha * acc + beta * C (and the mirror), one 32x32 accumulator at a
@@ -547,7 +583,8 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
   // triangular-inverse level 18 % and the skew R product 15 % faster); at M = 512 and
   // below, and for short K, the coarser triangle trimming and the longer prologue /
   // epilogue per K stage make the 64 x 64 tiles faster
-  const bool big = vec && !d.transB && d.M >= 1024 && d.N >= 1024 && d.K >= 512;
+  const bool big = vec && !d.transB && d.M >= 1024 && d.N >= 1024 && d.K >= 512 && !d.tout;
+  if (d.tout && (d.lower_only || nb2 != 1 || d.active)) return FX_ERR_INVALID_ARGUMENT;
   const int tm2 = (d.M + 127) / 128, tn2 = (d.N + 127) / 128;
   const int tiles2 = d.lower_only ? tm2 * (tm2 + 1) / 2 : tm2 * tn2;
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
@@ -559,8 +596,14 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
     e.xcd8 = nb % 8 == 0;
     e.A += b0 * d.sA;
     e.B += b0 * d.sB;
-    e.C += b0 * d.sC;
+    if (d.C) e.C += b0 * d.sC;
     if (d.active) e.active += b0;
+    if (d.tout) {
+      e.tout += b0 * (int64_t)d.nout * d.nout;
+      e.g0 += b0 * d.N;
+      e.flags += b0 * tiles;
+      if (d.scale) e.scale += b0;
+    }
     if (big) {
       const dim3 grid2(tiles2, (unsigned)nb, nb2);
       if (d.transA) hipLaunchKernelGGL((gemm128_kernel<true>), grid2, dim3(256), 0, s, e);

@@ -6,9 +6,11 @@
 //   2. the block-recursive levels s = 128, 256, .., Ninv/2 complete L^-1 and U~^-1 with
 //      four batched MFMA GEMMs per level (all block pairs of a level in one launch):
 //        X21 = -X22 (L21 X11),   Y12 = -Y11 (U12 Y22);
-//   3. Z = U~^-1 L^-1 by one GEMM whose tiles only run over k >= max(row, col);
-//   4. invT[g0[c]][i] = Z[i][c] (transpose + row permutation), zeroed for members with
-//      a non-finite Z or, if requested, an exactly zero pivot.
+//   3. Z = U~^-1 L^-1 by one GEMM whose tiles only run over k >= max(row, col), its
+//      epilogue storing invT[g0[c]][i] = Z[i][c] (transpose + row permutation through
+//      LDS) and flagging tiles with a non-finite value; Z itself is never stored;
+//   4. invT is zeroed for members with a non-finite Z or, if requested, an exactly zero
+//      pivot.
 // Total 4/3 N^3 of MFMA work (L^-1 and U^-1 N^3/3 each, the triangular product 2N^3/3).
 //
 // Reference roles replaced (ChenAo-Phys/fermix): _packed_lu / _diag_kernel leaf
@@ -203,50 +205,6 @@ __global__ void reduce_bad_kernel(const int* __restrict__ flags, int ntiles, con
   if (lane == 0) bad[b] = (any || (zero_singular && sign[b] == 0.0f)) ? 1 : 0;
 }
 
-// invT[g0[c]][i] = Z[i][c] for i < n and g0[c] < n, through a 32x32 LDS transpose; the
-// grid covers the whole N x N block of Z so the same pass flags each 32x32 tile that
-// holds a non-finite value (flags[b][tile], tiles row-major over ceil(N/32)^2).
-__global__ __launch_bounds__(256) void scatter_invT_kernel(const float* __restrict__ Z, int Ninv, int N,
-                                                           const int* __restrict__ g0, int n,
-                                                           int* __restrict__ flags,
-                                                           float* __restrict__ invT,
-                                                           const float* __restrict__ scale) {
-  __shared__ float tile[32 * 33];
-  const int64_t b = blockIdx.z;
-  const int i0 = 32 * blockIdx.y, c0 = 32 * blockIdx.x;
-  const int tid = threadIdx.x;
-  const float* Zb = Z + b * (int64_t)Ninv * Ninv;
-  float v[4];
-  int gr[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {  // in-bounds (clamped) reads, all in flight
-    const int e = tid + 256 * u;
-    const int i = min(i0 + (e >> 5), N - 1), c = min(c0 + (e & 31), N - 1);
-    v[u] = Zb[i * Ninv + c];
-    gr[u] = g0[b * N + min(c0 + (e >> 5), N - 1)];
-  }
-  bool nf = false;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int e = tid + 256 * u;
-    tile[(e >> 5) * 33 + (e & 31)] = v[u];
-    nf = nf || (i0 + (e >> 5) < N && c0 + (e & 31) < N && !isfinite(v[u]));
-  }
-  const int any = __syncthreads_or(nf ? 1 : 0);
-  if (tid == 0) flags[b * (int64_t)gridDim.x * gridDim.y + blockIdx.y * gridDim.x + blockIdx.x] = any;
-  const float sc = scale ? scale[b] : 1.0f;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int e = tid + 256 * u;
-    const int cc = e >> 5, ii = e & 31;
-    const int i = i0 + ii, c = c0 + cc;
-    if (i < n && c < N) {
-      const int r = gr[u];
-      if (r < n) invT[b * (int64_t)n * n + (int64_t)r * n + i] = sc * tile[ii * 33 + cc];
-    }
-  }
-}
-
 // invT[b] = 0 for the flagged members (one workgroup per member; others exit at once).
 __global__ __launch_bounds__(256) void zero_bad_kernel(const int* __restrict__ bad, float* __restrict__ invT,
                                                        int64_t nn) {
@@ -376,12 +334,11 @@ int inv_padded(int N) {
 
 size_t lu_inverse_workspace(int64_t batch, int N, bool need_copy) {
   const int Ninv = inv_padded(N);
-  const int nt = (N + 31) / 32;
+  const int nt = (N + 63) / 64;  // 64x64 tiles of the Z product
   size_t bytes = 0;
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
   if (need_copy) add((size_t)batch * Ninv * Ninv * 4);  // T
   add((size_t)batch * Ninv * Ninv / 4 * 4);              // Tmp (largest level: Ninv/2 x Ninv/2)
-  add((size_t)batch * Ninv * Ninv * 4);                  // Z
   add((size_t)batch * nt * nt * 4);                      // flags
   add((size_t)batch * 4);                                // bad
   return bytes;
@@ -401,8 +358,7 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
   };
   float* T = need_copy ? (float*)take((size_t)batch * Ninv * Ninv * 4) : LU;
   float* Tmp = (float*)take((size_t)batch * Ninv * Ninv / 4 * 4);
-  float* Z = (float*)take((size_t)batch * Ninv * Ninv * 4);
-  const int nt = (N + 31) / 32;  // 32x32 flag tiles
+  const int nt = (N + 63) / 64;  // 64x64 tiles of the Z product, one non-finite flag each
   int* flags = (int*)take((size_t)batch * nt * nt * 4);
   int* bad = (int*)take((size_t)batch * 4);
   const int64_t NN = (int64_t)Ninv * Ninv;
@@ -413,7 +369,8 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
   }
   int st0 = launch_tri_inverse(T, Ninv, batch, Tmp, true, s);
   if (st0 != FX_OK) return st0;
-  // Z = U~^-1 L^-1 (only the leading N x N block is used)
+  // Z = U~^-1 L^-1 (the leading N x N block) stored straight as invT = P^T Z^T:
+  // invT[g0[c]][i] = Z[i][c] for i < n and g0[c] < n, with the non-finite tile flags
   {
     GemmDesc d = {};
     d.M = d.N = N;
@@ -422,23 +379,19 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
     d.maskA = MASK_UPPER;
     d.B = T;
     d.maskB = MASK_LOWER_UNIT;
-    d.C = Z;
-    d.lda = d.ldb = d.ldc = Ninv;
-    d.sA = d.sB = d.sC = NN;
+    d.lda = d.ldb = Ninv;
+    d.sA = d.sB = NN;
     d.alpha = 1.0f;
     d.beta = 0.0f;
+    d.tout = invT;
+    d.g0 = g0;
+    d.nout = n;
+    d.scale = scale;
+    d.flags = flags;
     const int st = launch_gemm(d, batch, 1, s);
     if (st != FX_OK) return st;
   }
-  // invT and the non-finite tile flags in one pass over Z, then the flagged members
-  // (and, with zero_singular, those with a zero pivot) are cleared
-  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
-    const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
-    hipLaunchKernelGGL(scatter_invT_kernel, dim3(nt, nt, (unsigned)nb), dim3(256), 0, s, Z + b0 * NN, Ninv, N,
-                       g0 + b0 * N, n, flags + b0 * nt * nt, invT + b0 * (int64_t)n * n,
-                       scale ? scale + b0 : nullptr);
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  }
+  // the flagged members (and, with zero_singular, those with a zero pivot) are cleared
   hipLaunchKernelGGL(reduce_bad_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, flags, nt * nt,
                      sign, zero_singular, bad, batch);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
