@@ -4,9 +4,12 @@ reverse mode (backward), forward mode (jvp) and a vmap rule (all leading dimensi
 fold into the kernels' batch, so vmap(f)(x) runs exactly the arithmetic of f(x)).
 
 * slogdet: d logabs = sum(A^-T * dA), d sign = 0 (_diff.py:101-126). With a gradient
-  requested, one parts call returns the primal and A^-T from a single factorisation;
-  its (sign, logabs) are bit-identical to the plain forward (same kernel arithmetic).
-* slogpf: d logabs = -1/2 sum(S^-1 * dS) (_diff.py:129-156).
+  requested, the forward runs the factorisation alone (its (sign, logabs) bit-identical
+  to the plain forward: same kernel arithmetic) and keeps the packed LU; the backward
+  forms g_logabs * A^-T from it in one pass. For n <= 32 one parts call forms the primal
+  and A^-T together (a single Gauss-Jordan pass).
+* slogpf: d logabs = -1/2 sum(S^-1 * dS) (_diff.py:129-156), likewise from the forward's
+  kept Parlett-Reid factors with the cotangent applied by the inverse.
 * det: d det = sum(adj(A)^T * dA) (_diff.py:270-302), with adj(A)^T from the same LU
   as the primal -- det(factors) * A^-T, or its rank-1 continuation for exact zero
   pivots -- so the gradient is finite and exact for singular A.
@@ -38,6 +41,23 @@ def _wants_grad(A):
     if fx is not None and fx.is_functorch_wrapped_tensor(A):
         return not fx.is_batchedtensor(A)
     return False
+
+
+def _plain_reverse(A):
+    """A plain autograd tensor (requires_grad, no forward-mode dual, no torch.func
+    wrapper): its derivative can only come from a backward pass on real tensors, so
+    the factors may be kept and the inverse formed in the backward."""
+    if not A.requires_grad:
+        return False
+    try:
+        import torch.autograd.forward_ad as fwAD
+
+        if fwAD.unpack_dual(A).tangent is not None:
+            return False
+    except Exception:  # pragma: no cover - no dual level active
+        pass
+    fx = getattr(torch._C, "_functorch", None)
+    return not (fx is not None and fx.is_functorch_wrapped_tensor(A))
 
 
 def _fold(info, in_dims, A):
@@ -117,9 +137,62 @@ class _SlogdetParts(torch.autograd.Function):
         return (_unfold(s, vb), _unfold(l, vb), _unfold(inv, vb)), (0, 0, 0)
 
 
+class _SlogdetSplit(torch.autograd.Function):
+    """(sign, logabs) with the factors (lu, perm) kept for the derivative: the backward
+    forms g_logabs * A^-T in one pass from them (the cotangent is the inverse kernel's
+    per-member scale, so no separate product over B n^2). Used for plain reverse mode;
+    the jvp (real tensors only) forms A^-T from a copy of lu.
+    The backward overwrites lu (the inverse's scratch); a second backward of the same
+    graph refactors the saved input."""
+
+    @staticmethod
+    def forward(A):
+        return _kernels.slogdet_factors(A)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        sign, logabs, lu, perm = output
+        ctx.mark_non_differentiable(sign, lu, perm)
+        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(inputs[0], sign, lu, perm)
+        ctx.save_for_forward(sign, lu, perm)
+        ctx.n = inputs[0].shape[-1]
+        ctx.lu_used = False
+
+    @staticmethod
+    def backward(ctx, g_sign, g_logabs, g_lu, g_perm):
+        A, sign, lu, perm = ctx.saved_tensors
+        if g_logabs is None:
+            return None
+        if ctx.lu_used:  # retained graph, second backward: lu was overwritten
+            sign, _, lu, perm = _kernels.slogdet_factors(A.detach())
+        ctx.lu_used = True
+        return _kernels.slogdet_inverse(lu, perm, sign, ctx.n, scale=g_logabs)
+
+    @staticmethod
+    def jvp(ctx, dA):
+        sign, lu, perm = ctx.saved_tensors
+        invT = _kernels.slogdet_inverse(lu.clone(), perm, sign, ctx.n)
+        dlog = (invT * dA).sum(dim=(-1, -2))
+        return None, dlog, None, None
+
+    @staticmethod
+    def vmap(info, in_dims, A):
+        A2, vb = _fold(info, in_dims, A)
+        out = _SlogdetSplit.apply(A2)
+        if vb is None:
+            return out, (None,) * 4
+        return tuple(_unfold(x, vb) for x in out), (0,) * 4
+
+
 def slogdet(A):
     if _wants_grad(A):
-        s, l, _ = _SlogdetParts.apply(A)
+        # n <= 32: one Gauss-Jordan pass forms A^-T with the factors; forward mode and
+        # torch.func transforms: the parts call (their rules run on wrapped tensors)
+        if A.shape[-1] > 32 and _plain_reverse(A):
+            s, l, _, _ = _SlogdetSplit.apply(A)
+        else:
+            s, l, _ = _SlogdetParts.apply(A)
         return s, l
     return _SlogdetFwd.apply(A)
 
@@ -183,9 +256,55 @@ class _SlogpfParts(torch.autograd.Function):
         return (_unfold(s, vb), _unfold(l, vb), _unfold(inv, vb)), (0, 0, 0)
 
 
+class _SlogpfSplit(torch.autograd.Function):
+    """(sign, logabs) with the Parlett-Reid factors kept for the derivative: the backward
+    forms (-g_logabs / 2) S^-1 in one pass from them (the scale applied in the inverse's
+    final gather). Used for plain reverse mode; the jvp (real tensors only) forms S^-1.
+    The factors are only read."""
+
+    @staticmethod
+    def forward(A, skew):
+        return _kernels.slogpf_factors(A, skew)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        sign, logabs, gbuf, d, perm = output
+        ctx.mark_non_differentiable(sign, gbuf, d, perm)
+        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(gbuf, d, perm)
+        ctx.save_for_forward(gbuf, d, perm)
+        ctx.n = inputs[0].shape[-1]
+
+    @staticmethod
+    def backward(ctx, g_sign, g_logabs, g_gbuf, g_d, g_perm):
+        gbuf, d, perm = ctx.saved_tensors
+        if g_logabs is None:
+            return None, None
+        return _kernels.slogpf_inverse(gbuf, d, perm, ctx.n, scale=-0.5 * g_logabs), None
+
+    @staticmethod
+    def jvp(ctx, dA, _skew):
+        gbuf, d, perm = ctx.saved_tensors
+        Sinv = _kernels.slogpf_inverse(gbuf, d, perm, ctx.n)
+        dlog = -0.5 * (Sinv * dA).sum(dim=(-1, -2))
+        return None, dlog, None, None, None
+
+    @staticmethod
+    def vmap(info, in_dims, A, skew):
+        A2, vb = _fold(info, in_dims[:1], A)
+        out = _SlogpfSplit.apply(A2, skew)
+        if vb is None:
+            return out, (None,) * 5
+        return tuple(_unfold(x, vb) for x in out), (0,) * 5
+
+
 def slogpf(A, skew):
     if _wants_grad(A):
-        s, l, _ = _SlogpfParts.apply(A, skew)
+        n = A.shape[-1]
+        if n > 0 and n % 2 == 0 and _plain_reverse(A):
+            s, l, _, _, _ = _SlogpfSplit.apply(A, skew)
+        else:
+            s, l, _ = _SlogpfParts.apply(A, skew)
         return s, l
     return _SlogpfFwd.apply(A, skew)
 

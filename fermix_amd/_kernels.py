@@ -77,6 +77,43 @@ def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False):
     return sign, logabs, invT, lu, perm
 
 
+def slogdet_factors(A):
+    """(sign, logabs, lu (B, N, N), perm (B, N)): the packed LU of fx_slogdet_parts_f32
+    alone, N = lu_padded_size(n)."""
+    _check_input(A)
+    B, n, _ = A.shape
+    dev = A.device
+    N = lu_padded_size(n) if n > 0 else 0
+    sign = torch.empty(B, dtype=A.dtype, device=dev)
+    logabs = torch.empty(B, dtype=A.dtype, device=dev)
+    lu = torch.empty((B, N, N), dtype=A.dtype, device=dev)
+    perm = torch.empty((B, N), dtype=torch.int32, device=dev)
+    L = lib()
+    ws, wsb = _workspace(L.fx_slogdet_factors_f32_workspace(B, n), dev)
+    st = L.fx_slogdet_factors_f32(
+        _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(lu), _ptr(perm), _ptr(ws), wsb, _stream(A)
+    )
+    check(st, "fx_slogdet_factors_f32")
+    return sign, logabs, lu, perm
+
+
+def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True):
+    """scale[b] * A^-T (B, n, n) from slogdet_factors' outputs; lu is overwritten."""
+    B = sign.shape[0]
+    dev = sign.device
+    out = torch.empty((B, n, n), dtype=sign.dtype, device=dev)
+    if scale is not None:
+        scale = scale.to(dtype=sign.dtype).contiguous()
+    L = lib()
+    ws, wsb = _workspace(L.fx_slogdet_inverse_f32_workspace(B, n), dev)
+    st = L.fx_slogdet_inverse_f32(
+        _ptr(lu), _ptr(perm), _ptr(sign), _ptr(scale), B, n, int(bool(zero_singular)), _ptr(out),
+        _ptr(ws), wsb, _stream(sign),
+    )
+    check(st, "fx_slogdet_inverse_f32")
+    return out
+
+
 def det_parts(A):
     """(sign, logabs, adjT) with adjT = adj(A)^T = d det / dA from one factorisation."""
     _check_input(A)
@@ -119,7 +156,7 @@ def slogpf_factors(A, skew_symmetrize):
     PB = int(L.fx_pf_block_columns(n))
     sign = torch.empty(B, dtype=A.dtype, device=dev)
     logabs = torch.empty(B, dtype=A.dtype, device=dev)
-    gbuf = torch.zeros((B, N // PB, N, PB), dtype=A.dtype, device=dev)
+    gbuf = torch.empty((B, N // PB, N, PB), dtype=A.dtype, device=dev)  # unspecified entries stay unset
     d = torch.empty((B, N // 2), dtype=A.dtype, device=dev)
     perm = torch.empty((B, N), dtype=torch.int32, device=dev)
     ws, wsb = _workspace(L.fx_slogpf_factors_f32_workspace(B, n), dev)
@@ -129,6 +166,24 @@ def slogpf_factors(A, skew_symmetrize):
     )
     check(st, "fx_slogpf_factors_f32")
     return sign, logabs, gbuf, d, perm
+
+
+def slogpf_inverse(gbuf, d, perm, n, scale=None, adjugate=False):
+    """scale[b] * S^-1 (or scale[b] * pf(S) S^-1) (B, n, n) from slogpf_factors' outputs,
+    which are read only."""
+    B = d.shape[0]
+    dev = d.device
+    out = torch.empty((B, n, n), dtype=d.dtype, device=dev)
+    if scale is not None:
+        scale = scale.to(dtype=d.dtype).contiguous()
+    L = lib()
+    ws, wsb = _workspace(L.fx_slogpf_inverse_f32_workspace(B, n), dev)
+    st = L.fx_slogpf_inverse_f32(
+        _ptr(gbuf), _ptr(d), _ptr(perm), _ptr(scale), B, n, int(bool(adjugate)), _ptr(out),
+        _ptr(ws), wsb, _stream(d),
+    )
+    check(st, "fx_slogpf_inverse_f32")
+    return out
 
 
 def slogpf_parts(A, skew_symmetrize, adjugate=False):

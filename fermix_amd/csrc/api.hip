@@ -225,6 +225,44 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
   return launch_lu_inverse(LU, g0, N, n, batch, sign, zero_singular, inv_t, true, p, rest, s);
 }
 
+size_t fx_slogdet_factors_f32_workspace(int64_t batch, int32_t n) {
+  if (batch <= 0 || lu_family(n) != FAM_BLOCKED) return 0;
+  return lu_large_workspace(batch, n, true, true);
+}
+
+int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* lu,
+                           int32_t* perm, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (batch == 0) return FX_OK;
+  if (!sign || !logabs || (n > 0 && (!a || !lu || !perm))) return FX_ERR_INVALID_ARGUMENT;
+  hipStream_t s = (hipStream_t)stream;
+  if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
+  const int fam = lu_family(n);
+  if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (fam != FAM_BLOCKED) return lu_fused_factors(fam, a, n, batch, sign, logabs, lu, (int*)perm, s);
+  return launch_lu_large(a, n, batch, sign, logabs, workspace, workspace_bytes, true, nullptr, nullptr, s, lu,
+                         (int*)perm);
+}
+
+size_t fx_slogdet_inverse_f32_workspace(int64_t batch, int32_t n) {
+  if (batch <= 0 || n <= 0 || lu_family(n) == FAM_NONE) return 0;
+  const int N = fx_lu_padded_size(n);
+  return lu_inverse_workspace(batch, N, inv_padded(N) != N);
+}
+
+int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, const float* scale, int64_t batch,
+                           int32_t n, int32_t zero_singular, float* inv_t, void* workspace, size_t workspace_bytes,
+                           fx_stream_t stream) {
+  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (batch == 0 || n == 0) return FX_OK;
+  if (!lu || !perm || !sign || !inv_t) return FX_ERR_INVALID_ARGUMENT;
+  if (lu_family(n) == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  const size_t need = fx_slogdet_inverse_f32_workspace(batch, n);
+  if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
+  return launch_lu_inverse(lu, (const int*)perm, fx_lu_padded_size(n), n, batch, sign, zero_singular ? 1 : 0, inv_t,
+                           true, workspace, workspace_bytes, (hipStream_t)stream, scale);
+}
+
 size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || lu_family(n) == FAM_NONE) return 0;
   return fx_slogdet_parts_f32_workspace(batch, n) + align256(det_adjugate_workspace(batch, n));
@@ -314,6 +352,27 @@ int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew
   if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
   if (fam != FAM_BLOCKED) return pf_fused(fam, a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, s);
   return launch_pf_large(a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, workspace, workspace_bytes, s);
+}
+
+size_t fx_slogpf_inverse_f32_workspace(int64_t batch, int32_t n) {
+  if (batch <= 0 || n <= 0 || n % 2 || pf_family(n) == FAM_NONE) return 0;
+  return pf_inverse_workspace(batch, fx_pf_padded_size(n));
+}
+
+int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm, const float* scale,
+                          int64_t batch, int32_t n, int32_t adjugate, float* g, void* workspace,
+                          size_t workspace_bytes, fx_stream_t stream) {
+  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (batch == 0 || n == 0) return FX_OK;
+  if (!g) return FX_ERR_INVALID_ARGUMENT;
+  hipStream_t s = (hipStream_t)stream;
+  if (n % 2 == 1) return fill(g, 0.0f, batch * (int64_t)n * n, s);
+  if (!gbuf || !d || !perm) return FX_ERR_INVALID_ARGUMENT;
+  if (pf_family(n) == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  const size_t need = fx_slogpf_inverse_f32_workspace(batch, n);
+  if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
+  return launch_pf_inverse(gbuf, fx_pf_block_columns(n), d, (const int*)perm, fx_pf_padded_size(n), n, batch,
+                           adjugate ? 1 : 0, g, workspace, workspace_bytes, s, scale);
 }
 
 size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n) {

@@ -39,12 +39,14 @@ int launch_pf_small(const float* A, int n, int skew, int64_t batch, float* sign,
 
 // 128 < n <= LU_LARGE_MAXN: blocked LU in a workspace (see lu_large.hip). W_out / g0_out
 // return the packed LU (B, N, N) and, with parts, the composed row map (B, N),
-// N = lu_large_padded.
+// N = lu_large_padded. With W_ext (and, with parts, g0_ext) the LU and the row map are
+// formed in those caller buffers instead of the workspace (external = true sizes it).
 constexpr int LU_LARGE_MAXN = 4096;
 int lu_large_padded(int n);
-size_t lu_large_workspace(int64_t batch, int n, bool parts);
+size_t lu_large_workspace(int64_t batch, int n, bool parts, bool external = false);
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
-                    size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s);
+                    size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s,
+                    float* W_ext = nullptr, int* g0_ext = nullptr);
 
 // A^-T from the packed LU (B, N, N) and row map g0 (B, N) into invT (B, n, n); LU is
 // overwritten when in_place and N is a power-of-two multiple of 32 (inverse.hip).
@@ -73,10 +75,12 @@ int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hip
                               const int* active = nullptr);
 
 // S^-1 (adjugate = 0) or pf(S) S^-1 (adjugate != 0) as (B, n, n) from the Parlett-Reid
-// factors (gbuf with PB columns per block, d, perm).
+// factors (gbuf with PB columns per block, d, perm), read only; every member multiplied
+// by scale[b] when scale is given.
 size_t pf_inverse_workspace(int64_t batch, int N);
 int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm, int N, int n, int64_t batch,
-                      int adjugate, float* out, void* ws, size_t ws_bytes, hipStream_t s);
+                      int adjugate, float* out, void* ws, size_t ws_bytes, hipStream_t s,
+                      const float* scale = nullptr);
 
 // parity[b] = parity (0 even, 1 odd) of the permutation perm[b] of 0..N-1, N <= 2048.
 int launch_perm_parity(const int* perm, int N, int64_t batch, int* parity, hipStream_t s);

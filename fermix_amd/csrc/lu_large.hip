@@ -691,20 +691,20 @@ int lu_large_padded(int n) { return ((n + 63) / 64) * 64; }
 // Panel width: 64 columns (the trailing products run at K = 64).
 static int lu_panel_width(int) { return 64; }
 
-size_t lu_large_workspace(int64_t batch, int n, bool parts) {
+size_t lu_large_workspace(int64_t batch, int n, bool parts, bool external) {
   const int N = lu_large_padded(n);
   const int PW = lu_panel_width(N);
   const int nblk = N / PW;
   size_t bytes = 0;
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
-  add((size_t)batch * N * N * 4);        // W
+  if (!external) add((size_t)batch * N * N * 4);  // W
   add((size_t)batch * N * 4);            // pivots
   add((size_t)batch * nblk * 4);         // swap counts
   add((size_t)batch * N * 4);            // src (even blocks)
   add((size_t)batch * N * 4);            // src (odd blocks)
   add((size_t)batch * N * 4);            // composed map of the first block pair
   add((size_t)batch * (PW / 16) * 1024); // X
-  if (parts) add((size_t)batch * N * 4); // g0
+  if (parts && !external) add((size_t)batch * N * 4);  // g0
   return bytes;
 }
 
@@ -888,25 +888,28 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
 // Factor a (B, n, n) into the workspace; returns the packed LU (B, N, N) through *W_out
 // and the composed row map g0 (parts only) through *g0_out.
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
-                    size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s) {
+                    size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s, float* W_ext,
+                    int* g0_ext) {
   const int N = lu_large_padded(n);
   const int PW = lu_panel_width(N);
   const int nblk = N / PW;
   if (N > LU_LARGE_MAXN) return FX_ERR_UNSUPPORTED;
-  if (ws_bytes < lu_large_workspace(batch, n, parts) || !ws) return FX_ERR_WORKSPACE;
+  const bool external = W_ext != nullptr;
+  if (external && parts && !g0_ext) return FX_ERR_INVALID_ARGUMENT;
+  if (ws_bytes < lu_large_workspace(batch, n, parts, external) || !ws) return FX_ERR_WORKSPACE;
   char* p = (char*)ws;
   auto take = [&](size_t x) {
     char* q = p;
     p += (x + 255) / 256 * 256;
     return (void*)q;
   };
-  float* W = (float*)take((size_t)batch * N * N * 4);
+  float* W = external ? W_ext : (float*)take((size_t)batch * N * N * 4);
   float* piv = (float*)take((size_t)batch * N * 4);
   int* nsw = (int*)take((size_t)batch * nblk * 4);
   int* const srcs[3] = {(int*)take((size_t)batch * N * 4), (int*)take((size_t)batch * N * 4),
                         (int*)take((size_t)batch * N * 4)};
   float* X = (float*)take((size_t)batch * (PW / 16) * 1024);
-  int* g0 = parts ? (int*)take((size_t)batch * N * 4) : nullptr;
+  int* g0 = parts ? (external ? g0_ext : (int*)take((size_t)batch * N * 4)) : nullptr;
   // No padding and panels held in registers throughout (N <= 1024): the first block's
   // kernels read the input directly and together write all of W, so no copy is made.
   // Otherwise the input is copied (identity-padded) into W first.

@@ -230,13 +230,15 @@ __global__ void pf_reduce_bad_kernel(const int* __restrict__ flags, int ntiles, 
   if (lane == 0) bad[b] = (!adjugate && (any || coef[b].bad)) ? 1 : 0;
 }
 
-// out[i][j] = PT[iperm i][iperm j] for i, j < n (or 0 for a bad member); with accumulate
-// out[i][j] += PT[..] for the active members. One workgroup per output row: source row
-// iperm[i] is read contiguously into LDS and the column permutation is applied there.
+// out[i][j] = sc PT[iperm i][iperm j] for i, j < n (or 0 for a bad member), sc = scale[b]
+// or 1; with accumulate out[i][j] += sc PT[..] for the active members. One workgroup per
+// output row: source row iperm[i] is read contiguously into LDS and the column
+// permutation is applied there.
 __global__ __launch_bounds__(256) void pf_gather_kernel(const float* __restrict__ PT, int N,
                                                         const int* __restrict__ iperm, int n,
                                                         const int* __restrict__ bad, float* __restrict__ out,
-                                                        const int* __restrict__ active, int accumulate) {
+                                                        const int* __restrict__ active, int accumulate,
+                                                        const float* __restrict__ scale) {
   __shared__ __align__(16) float rowb[PF_LARGE_MAXN];
   const int64_t b = blockIdx.y;
   if (active && !active[b]) return;
@@ -250,7 +252,14 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(const float* __restrict_
   const float4* s4 = reinterpret_cast<const float4*>(PT + b * (int64_t)N * N + (int64_t)ip[i] * N);
   for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) reinterpret_cast<float4*>(rowb)[c4] = s4[c4];
   __syncthreads();
-  if (accumulate) {
+  if (scale) {
+    const float sc = scale[b];
+    if (accumulate) {
+      for (int j = threadIdx.x; j < n; j += 256) o[j] += sc * rowb[ip[j]];
+    } else {
+      for (int j = threadIdx.x; j < n; j += 256) o[j] = sc * rowb[ip[j]];
+    }
+  } else if (accumulate) {
     for (int j = threadIdx.x; j < n; j += 256) o[j] += rowb[ip[j]];
   } else {
     for (int j = threadIdx.x; j < n; j += 256) o[j] = rowb[ip[j]];
@@ -277,7 +286,7 @@ size_t pf_inverse_workspace(int64_t batch, int N) {
 }
 
 int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm, int N, int n, int64_t batch,
-                      int adjugate, float* out, void* ws, size_t ws_bytes, hipStream_t s) {
+                      int adjugate, float* out, void* ws, size_t ws_bytes, hipStream_t s, const float* scale) {
   const int Ninv = inv_padded(N);
   if (!ws || ws_bytes < pf_inverse_workspace(batch, N)) return FX_ERR_WORKSPACE;
   char* p = (char*)ws;
@@ -352,7 +361,7 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
       if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     }
     hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)n, (unsigned)batch), dim3(256), 0, s, PT, N, iperm, n, bad,
-                       out, active, accumulate);
+                       out, active, accumulate, scale);
     return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
   };
   int st = evaluate(nullptr, 1.0f, 0);

@@ -83,6 +83,27 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
                          float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
+/* The factors of fx_slogdet_parts_f32 alone, formed straight in the caller's lu
+ * (batch, N, N) and perm (batch, N) (N = fx_lu_padded_size(n); same layout), with sign /
+ * logabs bit-identical to fx_slogdet_f32. Together with fx_slogdet_inverse_f32 this
+ * splits `_lu_parts` (src/fermix/_inverse.py:502-531) into its factorisation, run by the
+ * forward pass, and the inverse, run by the backward pass once the cotangent is known. */
+size_t fx_slogdet_factors_f32_workspace(int64_t batch, int32_t n);
+int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* lu,
+                           int32_t* perm, void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* inv_t (batch, n, n) = scale[b] * A^-T (scale NULL: 1) from the factors lu / perm of
+ * fx_slogdet_factors_f32 (or fx_slogdet_parts_f32) and their sign, with the guards of
+ * fx_slogdet_parts_f32's inv_t (zero pivots of U replaced by 1; zero for non-finite
+ * results and, if zero_singular != 0, for members with sign 0). lu is used as scratch
+ * and overwritten. With scale = the logabs cotangent, inv_t is the slogdet VJP itself:
+ * `_permT` with the guard of `_lu_parts` (src/fermix/_inverse.py:478-531) and the
+ * cotangent product of the jvp rule (src/fermix/_diff.py:92-126) in one pass. */
+size_t fx_slogdet_inverse_f32_workspace(int64_t batch, int32_t n);
+int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, const float* scale, int64_t batch,
+                           int32_t n, int32_t zero_singular, float* inv_t, void* workspace, size_t workspace_bytes,
+                           fx_stream_t stream);
+
 /* adj_t (batch, n, n) = adj(A)^T = d det(A) / dA, finite and exact for singular A, plus
  * sign / logabs bit-identical to fx_slogdet_f32 (det = sign * exp(logabs) is the value
  * the reference's det returns with this gradient). From the packed LU of the same run:
@@ -124,6 +145,16 @@ size_t fx_slogpf_factors_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
                           float* sign, float* logabs, float* gbuf, float* d, int32_t* perm,
                           void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* g (batch, n, n) = scale[b] * S^-1 (adjugate = 0) or scale[b] * pf(S) S^-1 (adjugate
+ * != 0) from the factors of fx_slogpf_factors_f32 (read only; scale NULL: 1), with the
+ * guards of fx_slogpf_parts_f32's g. With scale = -cotangent / 2 it is the slogpf VJP:
+ * `_pf_parts` (src/fermix/_pfinv.py:196-269) on saved factors, with the cotangent
+ * product of the jvp rule (src/fermix/_diff.py:129-156) in its final gather. */
+size_t fx_slogpf_inverse_f32_workspace(int64_t batch, int32_t n);
+int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm, const float* scale,
+                          int64_t batch, int32_t n, int32_t adjugate, float* g, void* workspace,
+                          size_t workspace_bytes, fx_stream_t stream);
 
 /* The same run as fx_slogpf_f32 (bit-identical sign / logabs) plus g (batch, n, n)
  * formed from the run's own factors (no second factorisation):

@@ -183,3 +183,56 @@ def test_c4_properties(dev):
     assert np.max(np.abs(G + G.transpose(0, 2, 1))) <= 1e-6 * np.abs(G).max()
     ref = np.linalg.inv(S[idx].astype(np.float64))
     assert_grad(G, ref, S[idx], "C4 subset vs float64")
+
+
+@pytest.mark.parametrize("n", [40, 129, 200, 512])
+def test_slogdet_inverse_from_factors(dev, n):
+    """fx_slogdet_factors_f32 + fx_slogdet_inverse_f32 (scale = a cotangent) against the
+    one-call parts route times the cotangent: the same LU, the same inverse, and the scale
+    applied once either way, so bit-identical; the primal bit-identical to the forward."""
+    B = 5
+    rng = np.random.default_rng(9100 + n)
+    A = (rng.standard_normal((B, n, n)) / np.sqrt(n)).astype(np.float32)
+    A[2, :, n // 3] = 0.0  # exactly singular member: zero gradient
+    At = _t(A, dev)
+    w = _t(rng.standard_normal(B).astype(np.float32), dev)
+    print(f"inverse from factors n={n}", flush=True)
+    s, l, lu, perm = _kernels.slogdet_factors(At)
+    s0, l0 = fermix_amd.slogdet(At)
+    assert torch.equal(s, s0) and torch.equal(l, l0)
+    _, _, invT, _, _ = _kernels.slogdet_parts(At)
+    g = _kernels.slogdet_inverse(lu, perm, s, n, scale=w)
+    assert torch.equal(g, w[:, None, None] * invT)
+    assert torch.all(g[2] == 0)
+    # the autograd route (factors in the forward, the scaled inverse in the backward),
+    # including a second backward of a retained graph (the first overwrote the LU)
+    Ag = At.clone().requires_grad_()
+    _, la = fermix_amd.slogdet(Ag)
+    (g1,) = torch.autograd.grad((la * w).sum(), Ag, retain_graph=True)
+    (g2,) = torch.autograd.grad((la * w).sum(), Ag)
+    assert torch.equal(g1, g) and torch.equal(g2, g)
+
+
+@pytest.mark.parametrize("n", [34, 130, 512, 1000])
+def test_slogpf_inverse_from_factors(dev, n):
+    """fx_slogpf_factors_f32 + fx_slogpf_inverse_f32 (scale = -cotangent / 2) against the
+    parts route times the same scale (bit-identical), both modes; the autograd route."""
+    B = 4
+    rng = np.random.default_rng(9200 + n)
+    A = (rng.standard_normal((B, n, n)) / np.sqrt(n)).astype(np.float32)
+    S = (A - A.transpose(0, 2, 1)).astype(np.float32)
+    S[1, n // 5, :] = 0.0
+    S[1, :, n // 5] = 0.0
+    St = _t(S, dev)
+    w = _t(rng.standard_normal(B).astype(np.float32), dev)
+    print(f"pf inverse from factors n={n}", flush=True)
+    s, l, gbuf, d, perm = _kernels.slogpf_factors(St, False)
+    for adj in (False, True):
+        _, _, G = _kernels.slogpf_parts(St, False, adjugate=adj)
+        g = _kernels.slogpf_inverse(gbuf, d, perm, n, scale=-0.5 * w, adjugate=adj)
+        assert torch.equal(g, (-0.5 * w)[:, None, None] * G), f"adjugate={adj}"
+    Sg = St.clone().requires_grad_()
+    _, la = fermix_amd.slogpf(Sg, skew_symmetrize=False)
+    (g1,) = torch.autograd.grad((la * w).sum(), Sg)
+    _, _, G = _kernels.slogpf_parts(St, False)
+    assert torch.equal(g1, (-0.5 * w)[:, None, None] * G)
