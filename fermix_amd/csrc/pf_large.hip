@@ -258,7 +258,8 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
 template <int PB, int T>
 __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, int N, int r1,
                                                         const int* __restrict__ src,
-                                                        const float* __restrict__ Gn) {
+                                                        const float* __restrict__ Gn,
+                                                        const float* __restrict__ Min) {
   constexpr int H = T / 2, AW = H / 32;       // quarter size, accumulators per side
   constexpr int LDG = T + 4, LDT = H + 1;
   constexpr int LDS_N = 2 * PB * LDG > T * LDT ? 2 * PB * LDG : T * LDT;
@@ -280,6 +281,8 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
   const float* G = Gn + b * (int64_t)N * PB;
   const int* sb = src + b * N;
   float* Mb = M + b * (int64_t)N * N;  // entries addressed by 32-bit offsets (N * N < 2^32)
+  // old entries: M itself, or the input for the first block (in place of a copy into M)
+  const float* Cb = Min ? Min + b * (int64_t)N * N : Mb;
   // fixed trip count, so every load is issued before the first store
   constexpr int GE = T * PB / 256;
   float ga[GE], gb[GE];
@@ -320,7 +323,7 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
         // rows / columns beyond N hold index 0 in sp / sq: an in-bounds read whose
         // accumulator element is never stored (MFMA output elements are independent)
         const int rl = wr + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
-        acc[a][c][v] = Mb[(unsigned)(sp[rl] * N + scol)];
+        acc[a][c][v] = Cb[(unsigned)(sp[rl] * N + scol)];
       }
     }
 #pragma unroll
@@ -432,17 +435,18 @@ size_t pf_large_workspace(int64_t batch, int n, bool fact) {
 // rows per lane) and, unless it is the last block, the in-place trailing update.
 template <int PB, int R>
 static int pf_block(float* M, int N, int blk, int nblk, int64_t batch, float* d, int* nsw, int* src, float* Gn,
-                    int* orig, float* gbuf, hipStream_t s) {
+                    int* orig, float* gbuf, const float* A0, hipStream_t s) {
   const int r0 = blk * PB;
   const int m = N - r0;
+  const float* Mp = A0 ? A0 : M;  // A0 (first block): the input itself, same layout
   if (m <= 256 * R)
-    hipLaunchKernelGGL((pf_panel_kernel<256, R, PB>), dim3((unsigned)batch), dim3(256), 0, s, M, N, r0, blk, nblk,
+    hipLaunchKernelGGL((pf_panel_kernel<256, R, PB>), dim3((unsigned)batch), dim3(256), 0, s, Mp, N, r0, blk, nblk,
                        d, nsw, src, Gn, orig, gbuf);
   else if (m <= 512 * R)
-    hipLaunchKernelGGL((pf_panel_kernel<512, R, PB>), dim3((unsigned)batch), dim3(512), 0, s, M, N, r0, blk, nblk,
+    hipLaunchKernelGGL((pf_panel_kernel<512, R, PB>), dim3((unsigned)batch), dim3(512), 0, s, Mp, N, r0, blk, nblk,
                        d, nsw, src, Gn, orig, gbuf);
   else if constexpr (PB * R <= 64)  // G[R][PB] fits the 128 VGPRs of a 1024-thread workgroup
-    hipLaunchKernelGGL((pf_panel_kernel<1024, R, PB>), dim3((unsigned)batch), dim3(1024), 0, s, M, N, r0, blk,
+    hipLaunchKernelGGL((pf_panel_kernel<1024, R, PB>), dim3((unsigned)batch), dim3(1024), 0, s, Mp, N, r0, blk,
                        nblk, d, nsw, src, Gn, orig, gbuf);
   else
     return FX_ERR_UNSUPPORTED;
@@ -455,7 +459,7 @@ static int pf_block(float* M, int N, int blk, int nblk, int64_t batch, float* d,
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
     const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
     hipLaunchKernelGGL((pf_update_kernel<PB, TU>), dim3(nt * (nt + 1) / 2, (unsigned)nb), dim3(256), 0, s,
-                       M + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PB);
+                       M + b0 * NN, N, r1, src + b0 * N, Gn + b0 * N * PB, A0 ? A0 + b0 * NN : nullptr);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
@@ -485,10 +489,11 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
   int* orig = fact ? (int*)take((size_t)batch * N * 4) : nullptr;
   float* d = dout ? dout : dbuf;
   const int64_t NN = (int64_t)N * N;
-  if (n == N && !skew && ((uintptr_t)A & 15) == 0) {  // no padding, no symmetrisation
-    const int st = launch_copy(A, M0, batch * NN, s);
-    if (st != FX_OK) return st;
-  } else {
+  // No padding and no symmetrisation: the first block's panel and update read the input
+  // itself, and the update writes every trailing entry of M (later blocks never read the
+  // first block's rows), so no copy is made. Otherwise the padded copy comes first.
+  const bool direct = n == N && !skew && ((uintptr_t)A & 15) == 0;
+  if (!direct) {
     hipLaunchKernelGGL(pf_copy_pad_kernel, dim3((unsigned)((NN + 255) / 256), (unsigned)batch), dim3(256), 0, s,
                        A, n, skew, M0, N);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
@@ -498,9 +503,10 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     hipLaunchKernelGGL(pf_iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, orig, N, tot);
   }
   for (int blk = 0; blk < nblk; ++blk) {
-    const int st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, s)
-                   : PB == PFB ? pf_block<PFB, 2>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, s)
-                               : pf_block<PFB_XL, 4>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, s);
+    const float* A0 = direct && blk == 0 ? A : nullptr;
+    const int st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                   : PB == PFB ? pf_block<PFB, 2>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                               : pf_block<PFB_XL, 4>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
     if (st != FX_OK) return st;
   }
   hipLaunchKernelGGL(pf_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, d, nsw, N / 2, nblk,
