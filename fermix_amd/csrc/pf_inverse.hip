@@ -11,7 +11,8 @@
 //            the second evaluation running only for the members that have such a pivot.
 // Kernels: pivot / coefficient prep (one wave per matrix), L~ assembly, the triangular
 // inverse of inverse.hip (lower half only), DY, the skew GEMM R (lower tiles + mirror),
-// the rank-2 correction with the non-finite flags, and the permutation gather.
+// and the permutation gather with the rank-2 correction and the non-finite flags formed
+// on the way (no corrected matrix is stored between them).
 //
 // Reference roles replaced (ChenAo-Phys/fermix): _pf_parts (src/fermix/_pfinv.py:196-269)
 // with _pf_assemble_kernel (:80-137), _pf_maps (:140-157), the skew _bgemm for R and
@@ -173,49 +174,13 @@ __global__ __launch_bounds__(256) void pf_dy_kernel(const float* __restrict__ T,
   }
 }
 
-// PT = -sg (a1 R + a2 (w v^T - v w^T)); flags non-finite 64x64 tiles.
-__global__ void pf_adj_kernel(const float* __restrict__ R, float* __restrict__ PT, int N, const float* __restrict__ T,
-                              int Ninv, const PfCoef* __restrict__ coef, float sg, int* __restrict__ flags,
-                              const int* __restrict__ active) {
+// w[c] = R[c][2K] (the column of R that the rank-2 correction uses), one thread per c.
+__global__ void pf_wvec_kernel(const float* __restrict__ R, int N, const PfCoef* __restrict__ coef,
+                               float* __restrict__ w, const int* __restrict__ active) {
   const int64_t b = blockIdx.y;
   if (active && !active[b]) return;
-  const int nt = (N + 63) / 64;
-  const int tile = blockIdx.x;
-  const int f0 = (tile / nt) * 64, c0 = (tile % nt) * 64;
-  const PfCoef cf = coef[b];
-  const float a1 = sg * cf.a1, a2 = sg * cf.a2;
-  const int aK = 2 * cf.K;
-  const float* Rb = R + b * (int64_t)N * N;
-  float* Pb = PT + b * (int64_t)N * N;
-  const float* Tb = T + b * (int64_t)Ninv * Ninv;
-  bool badv = false;
-  // this thread's column c is fixed (64 columns, 4 rows per pass); all reads are in-bounds
-  // (clamped) and issued before use
-  const int cth = c0 + (threadIdx.x & 63), ccl = min(cth, N - 1);
-  const float wc = Rb[ccl * N + aK];
-  const float tcv = Tb[aK * Ninv + ccl];
-  const float v_c = cth < aK ? tcv : (cth == aK ? 1.0f : 0.0f);
-  float rv[16], wv[16], tv[16];
-#pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int f = min(f0 + (threadIdx.x >> 6) + 4 * u, N - 1);
-    rv[u] = Rb[f * N + ccl];
-    wv[u] = Rb[f * N + aK];
-    tv[u] = Tb[aK * Ninv + f];
-  }
-#pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int f = f0 + (threadIdx.x >> 6) + 4 * u;
-    if (f < N && cth < N) {
-      // v = Y^T e_aK: v[j] = Y[aK][j] (unit lower: j < aK stored, j == aK one, j > aK zero)
-      const float v_f = f < aK ? tv[u] : (f == aK ? 1.0f : 0.0f);
-      const float val = -(a1 * rv[u] + a2 * (wv[u] * v_c - v_f * wc));
-      badv = badv || !isfinite(val);
-      Pb[(int64_t)f * N + cth] = val;
-    }
-  }
-  const int any = __syncthreads_or(badv ? 1 : 0);
-  if (threadIdx.x == 0) flags[b * (nt * nt) + tile] = any;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c < N) w[b * N + c] = R[b * (int64_t)N * N + (int64_t)c * N + 2 * coef[b].K];
 }
 
 // bad[b]: inverse mode only (the adjugate is returned as computed).
@@ -230,55 +195,77 @@ __global__ void pf_reduce_bad_kernel(const int* __restrict__ flags, int ntiles, 
   if (lane == 0) bad[b] = (!adjugate && (any || coef[b].bad)) ? 1 : 0;
 }
 
-// out[i][j] = sc PT[iperm i][iperm j] for i, j < n (or 0 for a bad member), sc = scale[b]
-// or 1; with accumulate out[i][j] += sc PT[..] for the active members. One workgroup per
-// output row: source row iperm[i] is read contiguously into LDS and the column
-// permutation is applied there.
-__global__ __launch_bounds__(256) void pf_gather_kernel(const float* __restrict__ PT, int N,
-                                                        const int* __restrict__ iperm, int n,
-                                                        const int* __restrict__ bad, float* __restrict__ out,
-                                                        const int* __restrict__ active, int accumulate,
-                                                        const float* __restrict__ scale) {
+// The final matrix straight from R (skew, both triangles stored): with f = iperm[i],
+// c = iperm[j] (the factor order of output row i / column j),
+//   out[i][j] = sc * -(a1 R[f][c] + a2 (w_f v_c - v_f w_c)),
+// w = R[:, 2K] (wvec), v = Y^T e_2K (v_c = Y[2K][c] for c < 2K, 1 at 2K, 0 after), a1 / a2
+// the member's coefficients times sg, sc = scale[b] or 1; with accumulate the value is
+// added for the active members. One workgroup per row i < N: source row f of R is read
+// contiguously into LDS and the column permutation applied there; rows / columns >= n
+// are evaluated (flags[b][i] marks a non-finite value in row i) but not stored.
+__global__ __launch_bounds__(256) void pf_adj_gather_kernel(const float* __restrict__ R, int N,
+                                                            const float* __restrict__ T, int Ninv,
+                                                            const PfCoef* __restrict__ coef, float sg,
+                                                            const float* __restrict__ wvec,
+                                                            const int* __restrict__ iperm, int n,
+                                                            int* __restrict__ flags, float* __restrict__ out,
+                                                            const int* __restrict__ active, int accumulate,
+                                                            const float* __restrict__ scale) {
   __shared__ __align__(16) float rowb[PF_LARGE_MAXN];
   const int64_t b = blockIdx.y;
   if (active && !active[b]) return;
   const int i = blockIdx.x;
-  float* o = out + b * (int64_t)n * n + (int64_t)i * n;
-  if (bad[b]) {
-    for (int j = threadIdx.x; j < n; j += 256) o[j] = 0.0f;
-    return;
-  }
   const int* ip = iperm + b * N;
-  const float4* s4 = reinterpret_cast<const float4*>(PT + b * (int64_t)N * N + (int64_t)ip[i] * N);
+  const int f = ip[i];
+  const float4* s4 = reinterpret_cast<const float4*>(R + b * (int64_t)N * N + (int64_t)f * N);
   for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) reinterpret_cast<float4*>(rowb)[c4] = s4[c4];
+  const PfCoef cf = coef[b];
+  const float a1 = sg * cf.a1, a2 = sg * cf.a2;
+  const int aK = 2 * cf.K;
+  const float* Tk = T + b * (int64_t)Ninv * Ninv + (int64_t)aK * Ninv;  // row 2K of Y
+  const float* wb = wvec + b * N;
+  const float v_f = f < aK ? Tk[f] : (f == aK ? 1.0f : 0.0f);
+  const float sc = scale ? scale[b] : 1.0f;
   __syncthreads();
-  if (scale) {
-    const float sc = scale[b];
-    if (accumulate) {
-      for (int j = threadIdx.x; j < n; j += 256) o[j] += sc * rowb[ip[j]];
-    } else {
-      for (int j = threadIdx.x; j < n; j += 256) o[j] = sc * rowb[ip[j]];
+  const float w_f = rowb[aK];
+  float* o = out + b * (int64_t)n * n + (int64_t)i * n;
+  bool nf = false;
+  for (int j = threadIdx.x; j < N; j += 256) {
+    const int c = ip[j];
+    const float v_c = c < aK ? Tk[c] : (c == aK ? 1.0f : 0.0f);
+    const float val = -(a1 * rowb[c] + a2 * (w_f * v_c - v_f * wb[c]));
+    nf = nf || !isfinite(val);
+    if (i < n && j < n) {
+      if (accumulate) o[j] += sc * val;
+      else o[j] = sc * val;
     }
-  } else if (accumulate) {
-    for (int j = threadIdx.x; j < n; j += 256) o[j] += rowb[ip[j]];
-  } else {
-    for (int j = threadIdx.x; j < n; j += 256) o[j] = rowb[ip[j]];
   }
+  const int any = __syncthreads_or(nf ? 1 : 0);
+  if (threadIdx.x == 0) flags[b * N + i] = any;
+}
+
+// out[b] = 0 for the flagged members (one workgroup per member; others exit at once).
+__global__ __launch_bounds__(256) void pf_zero_bad_kernel(const int* __restrict__ bad, float* __restrict__ out,
+                                                          int64_t nn) {
+  const int64_t b = blockIdx.x;
+  if (!bad[b]) return;
+  float* o = out + b * nn;
+  for (int64_t e = threadIdx.x; e < nn; e += 256) o[e] = 0.0f;
 }
 
 size_t pf_inverse_workspace(int64_t batch, int N) {
   const int Ninv = inv_padded(N);
-  const int nt = (N + 63) / 64;
   size_t bytes = 0;
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
   add((size_t)batch * Ninv * Ninv * 4);  // T (L~, then Y)
   add((size_t)batch * Ninv * Ninv);      // Tmp (Ninv/2 x Ninv/2 floats)
   add((size_t)batch * N * N * 4);        // DY
-  add((size_t)batch * N * N * 4);        // R / PT
+  add((size_t)batch * N * N * 4);        // R
+  add((size_t)batch * N * 4);            // wvec
   add((size_t)batch * N / 2 * 4);        // dinv
   add((size_t)batch * N * 4);            // iperm
   add((size_t)batch * sizeof(PfCoef));
-  add((size_t)batch * nt * nt * 4);      // flags
+  add((size_t)batch * N * 4);            // flags (one per row)
   add((size_t)batch * 4);                // bad
   add((size_t)batch * 4);                // parity
   add((size_t)batch * 4);                // lift
@@ -299,11 +286,11 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
   float* Tmp = (float*)take((size_t)batch * Ninv * Ninv);
   float* DY = (float*)take((size_t)batch * N * N * 4);
   float* R = (float*)take((size_t)batch * N * N * 4);
+  float* wvec = (float*)take((size_t)batch * N * 4);
   float* dinv = (float*)take((size_t)batch * N / 2 * 4);
   int* iperm = (int*)take((size_t)batch * N * 4);
   PfCoef* coef = (PfCoef*)take((size_t)batch * sizeof(PfCoef));
-  const int nt = (N + 63) / 64;
-  int* flags = (int*)take((size_t)batch * nt * nt * 4);
+  int* flags = (int*)take((size_t)batch * N * 4);
   int* bad = (int*)take((size_t)batch * 4);
   int* parity = (int*)take((size_t)batch * 4);
   int* lift = (int*)take((size_t)batch * 4);
@@ -351,17 +338,17 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
       st = launch_gemm(g, batch, 1, s);
       if (st != FX_OK) return st;
     }
-    float* PT = DY;  // DY is dead once R is formed
-    hipLaunchKernelGGL(pf_adj_kernel, dim3(nt * nt, (unsigned)batch), dim3(256), 0, s, R, PT, N, T, Ninv, coef, sg,
-                       flags, active);
+    hipLaunchKernelGGL(pf_wvec_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)batch), dim3(256), 0, s, R, N,
+                       coef, wvec, active);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    if (!accumulate) {
-      hipLaunchKernelGGL(pf_reduce_bad_kernel, dim3(wb), dim3(256), 0, s, flags, nt * nt, coef, adjugate, bad,
-                         batch);
-      if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    }
-    hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)n, (unsigned)batch), dim3(256), 0, s, PT, N, iperm, n, bad,
-                       out, active, accumulate, scale);
+    hipLaunchKernelGGL(pf_adj_gather_kernel, dim3((unsigned)N, (unsigned)batch), dim3(256), 0, s, R, N, T, Ninv,
+                       coef, sg, wvec, iperm, n, flags, out, active, accumulate, scale);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    if (accumulate) return FX_OK;
+    // inverse mode: members with d_K = 0 or a non-finite value anywhere are zeroed
+    hipLaunchKernelGGL(pf_reduce_bad_kernel, dim3(wb), dim3(256), 0, s, flags, N, coef, adjugate, bad, batch);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    hipLaunchKernelGGL(pf_zero_bad_kernel, dim3((unsigned)batch), dim3(256), 0, s, bad, out, (int64_t)n * n);
     return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
   };
   int st = evaluate(nullptr, 1.0f, 0);
