@@ -43,8 +43,13 @@ __device__ __forceinline__ bool mask_upper(int m) { return m == MASK_UPPER || m 
 // Tile loads: VEC uses 16-byte global loads along the operand's contiguous dimension
 // (requires that dimension, the leading dimensions, batch strides and base pointers to be
 // multiples of 4 floats), otherwise one float per load. Masks are applied in registers.
-template <int BM, int BN, bool VEC>
+template <int BM, int BN, bool VEC, int MK>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
+  // operand masks: MK = 4 maskA + maskB fixed at compile time (the combinations this
+  // library uses), so each mask test folds to one compare per element; MK < 0 reads them
+  // from the descriptor
+  const int maskA = MK >= 0 ? (MK >> 2) : maskA;
+  const int maskB = MK >= 0 ? (MK & 3) : maskB;
   constexpr int LDSA = BM + 4, LDSB = BN + 4;
   constexpr int WM = BM / 2, WN = BN / 2;   // per-wave quarter
   constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 tiles per wave
@@ -93,10 +98,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   int klo = 0, khi = d.K;
   // op(A)(i, k): lower -> k <= i + offAr - offAc, upper -> k >= i + offAr - offAc;
   // op(B)(k, j): lower -> k >= j + offBc - offBr, upper -> k <= j + offBc - offBr
-  if (mask_upper(d.maskA)) klo = max(klo, i0 + d.offAr - d.offAc);
-  if (mask_lower(d.maskA)) khi = min(khi, i0 + BM + d.offAr - d.offAc);
-  if (mask_lower(d.maskB)) klo = max(klo, j0 + d.offBc - d.offBr);
-  if (mask_upper(d.maskB)) khi = min(khi, j0 + BN + d.offBc - d.offBr);
+  if (mask_upper(maskA)) klo = max(klo, i0 + d.offAr - d.offAc);
+  if (mask_lower(maskA)) khi = min(khi, i0 + BM + d.offAr - d.offAc);
+  if (mask_lower(maskB)) klo = max(klo, j0 + d.offBc - d.offBr);
+  if (mask_upper(maskB)) khi = min(khi, j0 + BN + d.offBc - d.offBr);
   klo = max(0, (klo / GBK) * GBK);
 
   // A stage is plain when no element of it needs a bound or mask fix (a uniform test):
@@ -107,12 +112,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   auto plain_stage = [&](int k0) {
     if (!VEC || !interior || k0 + GBK > d.K) return false;
     bool ok = true;
-    if (d.maskA == MASK_LOWER_UNIT) ok = ok && i0 + d.offAr > k0 + GBK - 1 + d.offAc;
-    if (d.maskA == MASK_UPPER) ok = ok && i0 + BM - 1 + d.offAr <= k0 + d.offAc;
-    if (d.maskA == MASK_UPPER_UNIT) ok = ok && i0 + BM - 1 + d.offAr < k0 + d.offAc;
-    if (d.maskB == MASK_LOWER_UNIT) ok = ok && k0 + d.offBr > j0 + BN - 1 + d.offBc;
-    if (d.maskB == MASK_UPPER) ok = ok && k0 + GBK - 1 + d.offBr <= j0 + d.offBc;
-    if (d.maskB == MASK_UPPER_UNIT) ok = ok && k0 + GBK - 1 + d.offBr < j0 + d.offBc;
+    if (maskA == MASK_LOWER_UNIT) ok = ok && i0 + d.offAr > k0 + GBK - 1 + d.offAc;
+    if (maskA == MASK_UPPER) ok = ok && i0 + BM - 1 + d.offAr <= k0 + d.offAc;
+    if (maskA == MASK_UPPER_UNIT) ok = ok && i0 + BM - 1 + d.offAr < k0 + d.offAc;
+    if (maskB == MASK_LOWER_UNIT) ok = ok && k0 + d.offBr > j0 + BN - 1 + d.offBc;
+    if (maskB == MASK_UPPER) ok = ok && k0 + GBK - 1 + d.offBr <= j0 + d.offBc;
+    if (maskB == MASK_UPPER_UNIT) ok = ok && k0 + GBK - 1 + d.offBr < j0 + d.offBc;
     return ok;
   };
 
@@ -192,11 +197,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   // op(A)(gi, gk) after masking (zero outside the matrix)
   auto fixA = [&](float v, int gi, int gk) {
     if (gi >= d.M || gk >= d.K) return 0.0f;
-    return d.maskA ? mask_val(v, d.maskA, gi + d.offAr, gk + d.offAc) : v;
+    return maskA ? mask_val(v, maskA, gi + d.offAr, gk + d.offAc) : v;
   };
   auto fixB = [&](float v, int gk, int gj) {
     if (gj >= d.N || gk >= d.K) return 0.0f;
-    return d.maskB ? mask_val(v, d.maskB, gk + d.offBr, gj + d.offBc) : v;
+    return maskB ? mask_val(v, maskB, gk + d.offBr, gj + d.offBc) : v;
   };
   // registers -> LDS, K-major (As[k][i], Bs[k][j]) so each MFMA operand read is 32
   // consecutive floats
@@ -612,8 +617,22 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
       continue;
     }
     const dim3 grid(tiles, (unsigned)nb, nb2);
-    if (vec) hipLaunchKernelGGL((gemm_kernel<BM, BN, true>), grid, dim3(256), 0, s, e);
-    else hipLaunchKernelGGL((gemm_kernel<BM, BN, false>), grid, dim3(256), 0, s, e);
+#define FX_GEMM_MK(K) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, K>), grid, dim3(256), 0, s, e)
+    if (vec) {
+      switch (4 * d.maskA + d.maskB) {
+        case 4 * MASK_NONE + MASK_NONE: FX_GEMM_MK(4 * MASK_NONE + MASK_NONE); break;
+        case 4 * MASK_NONE + MASK_LOWER_UNIT: FX_GEMM_MK(4 * MASK_NONE + MASK_LOWER_UNIT); break;
+        case 4 * MASK_NONE + MASK_UPPER: FX_GEMM_MK(4 * MASK_NONE + MASK_UPPER); break;
+        case 4 * MASK_LOWER_UNIT + MASK_NONE: FX_GEMM_MK(4 * MASK_LOWER_UNIT + MASK_NONE); break;
+        case 4 * MASK_UPPER + MASK_NONE: FX_GEMM_MK(4 * MASK_UPPER + MASK_NONE); break;
+        case 4 * MASK_UPPER + MASK_LOWER_UNIT: FX_GEMM_MK(4 * MASK_UPPER + MASK_LOWER_UNIT); break;
+        case 4 * MASK_UPPER_UNIT + MASK_NONE: FX_GEMM_MK(4 * MASK_UPPER_UNIT + MASK_NONE); break;
+        default: FX_GEMM_MK(-1); break;
+      }
+    } else {
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, false, -1>), grid, dim3(256), 0, s, e);
+    }
+#undef FX_GEMM_MK
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
