@@ -376,8 +376,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
 // -- zeros outside the matrix, the triangle masks -- between two barriers.
 // Launch bound of 4 waves per SIMD: the compiler then fits the kernel in 116 VGPRs
 // (accumulators included) without scratch, against 168 + 64 left to itself.
-template <bool TA>
+template <bool TA, int MK>
 __global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
+  const int maskA = MK >= 0 ? (MK >> 2) : maskA;  // compile-time masks as in gemm_kernel
+  const int maskB = MK >= 0 ? (MK & 3) : maskB;
   constexpr int BM = 128, BN = 128, LDA_ = BM + 4, LDB_ = BN + 4;
   __shared__ __align__(16) float As[2][GBK * LDA_];
   __shared__ __align__(16) float Bs[2][GBK * LDB_];
@@ -411,21 +413,21 @@ __global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
   float* C = d.C + bat * d.sC + bat2 * d.sC2;
 
   int klo = 0, khi = d.K;
-  if (mask_upper(d.maskA)) klo = max(klo, i0 + d.offAr - d.offAc);
-  if (mask_lower(d.maskA)) khi = min(khi, i0 + BM + d.offAr - d.offAc);
-  if (mask_lower(d.maskB)) klo = max(klo, j0 + d.offBc - d.offBr);
-  if (mask_upper(d.maskB)) khi = min(khi, j0 + BN + d.offBc - d.offBr);
+  if (mask_upper(maskA)) klo = max(klo, i0 + d.offAr - d.offAc);
+  if (mask_lower(maskA)) khi = min(khi, i0 + BM + d.offAr - d.offAc);
+  if (mask_lower(maskB)) klo = max(klo, j0 + d.offBc - d.offBr);
+  if (mask_upper(maskB)) khi = min(khi, j0 + BN + d.offBc - d.offBr);
   klo = max(0, (klo / GBK) * GBK);
 
   const bool interior = i0 + BM <= d.M && j0 + BN <= d.N;
   auto plain_stage = [&](int k0) {
     bool ok = interior && k0 + GBK <= d.K;
-    if (d.maskA == MASK_LOWER_UNIT) ok = ok && i0 + d.offAr > k0 + GBK - 1 + d.offAc;
-    if (d.maskA == MASK_UPPER) ok = ok && i0 + BM - 1 + d.offAr <= k0 + d.offAc;
-    if (d.maskA == MASK_UPPER_UNIT) ok = ok && i0 + BM - 1 + d.offAr < k0 + d.offAc;
-    if (d.maskB == MASK_LOWER_UNIT) ok = ok && k0 + d.offBr > j0 + BN - 1 + d.offBc;
-    if (d.maskB == MASK_UPPER) ok = ok && k0 + GBK - 1 + d.offBr <= j0 + d.offBc;
-    if (d.maskB == MASK_UPPER_UNIT) ok = ok && k0 + GBK - 1 + d.offBr < j0 + d.offBc;
+    if (maskA == MASK_LOWER_UNIT) ok = ok && i0 + d.offAr > k0 + GBK - 1 + d.offAc;
+    if (maskA == MASK_UPPER) ok = ok && i0 + BM - 1 + d.offAr <= k0 + d.offAc;
+    if (maskA == MASK_UPPER_UNIT) ok = ok && i0 + BM - 1 + d.offAr < k0 + d.offAc;
+    if (maskB == MASK_LOWER_UNIT) ok = ok && k0 + d.offBr > j0 + BN - 1 + d.offBc;
+    if (maskB == MASK_UPPER) ok = ok && k0 + GBK - 1 + d.offBr <= j0 + d.offBc;
+    if (maskB == MASK_UPPER_UNIT) ok = ok && k0 + GBK - 1 + d.offBr < j0 + d.offBc;
     return ok;
   };
 
@@ -479,12 +481,12 @@ __global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
     for (int e = tid; e < GBK * BM; e += 256) {
       const int k = e / BM, i = e % BM, gi = i0 + i, gk = k0 + k;
       float* p = &As[buf][k * LDA_ + i];
-      *p = (gi >= d.M || gk >= d.K) ? 0.0f : (d.maskA ? mask_val(*p, d.maskA, gi + d.offAr, gk + d.offAc) : *p);
+      *p = (gi >= d.M || gk >= d.K) ? 0.0f : (maskA ? mask_val(*p, maskA, gi + d.offAr, gk + d.offAc) : *p);
     }
     for (int e = tid; e < GBK * BN; e += 256) {
       const int k = e / BN, j = e % BN, gj = j0 + j, gk = k0 + k;
       float* p = &Bs[buf][k * LDB_ + j];
-      *p = (gj >= d.N || gk >= d.K) ? 0.0f : (d.maskB ? mask_val(*p, d.maskB, gk + d.offBr, gj + d.offBc) : *p);
+      *p = (gj >= d.N || gk >= d.K) ? 0.0f : (maskB ? mask_val(*p, maskB, gk + d.offBr, gj + d.offBc) : *p);
     }
   };
 
@@ -611,8 +613,24 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
     }
     if (big) {
       const dim3 grid2(tiles2, (unsigned)nb, nb2);
-      if (d.transA) hipLaunchKernelGGL((gemm128_kernel<true>), grid2, dim3(256), 0, s, e);
-      else hipLaunchKernelGGL((gemm128_kernel<false>), grid2, dim3(256), 0, s, e);
+#define FX_GEMM128(T, K) hipLaunchKernelGGL((gemm128_kernel<T, K>), grid2, dim3(256), 0, s, e)
+      const int mk = 4 * d.maskA + d.maskB;
+      if (d.transA) {
+        if (mk == 4 * MASK_UPPER_UNIT + MASK_NONE) FX_GEMM128(true, 4 * MASK_UPPER_UNIT + MASK_NONE);
+        else if (mk == 0) FX_GEMM128(true, 0);
+        else FX_GEMM128(true, -1);
+      } else {
+        switch (mk) {
+          case 4 * MASK_NONE + MASK_NONE: FX_GEMM128(false, 4 * MASK_NONE + MASK_NONE); break;
+          case 4 * MASK_NONE + MASK_LOWER_UNIT: FX_GEMM128(false, 4 * MASK_NONE + MASK_LOWER_UNIT); break;
+          case 4 * MASK_NONE + MASK_UPPER: FX_GEMM128(false, 4 * MASK_NONE + MASK_UPPER); break;
+          case 4 * MASK_LOWER_UNIT + MASK_NONE: FX_GEMM128(false, 4 * MASK_LOWER_UNIT + MASK_NONE); break;
+          case 4 * MASK_UPPER + MASK_NONE: FX_GEMM128(false, 4 * MASK_UPPER + MASK_NONE); break;
+          case 4 * MASK_UPPER + MASK_LOWER_UNIT: FX_GEMM128(false, 4 * MASK_UPPER + MASK_LOWER_UNIT); break;
+          default: FX_GEMM128(false, -1); break;
+        }
+      }
+#undef FX_GEMM128
       if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
       continue;
     }
