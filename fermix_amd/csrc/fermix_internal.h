@@ -62,7 +62,7 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
 // (B, N/PB, N, PB) by original row (PB = pf_large_block_cols(N)), d (B, N/2) and perm (B, N).
 constexpr int PF_LARGE_MAXN = 4096;
 int pf_large_padded(int n);
-int pf_large_block_cols(int N);  // 64 for 512 <= N <= 1024 and N % 64 == 0, 32 for the other N <= 2048, 16 above
+int pf_large_block_cols(int N);  // columns per factor chunk: 32 for N <= 2048, 16 above
 size_t pf_large_workspace(int64_t batch, int n, bool fact);
 int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
                     float* gbuf, float* dout, int* perm, void* ws, size_t ws_bytes, hipStream_t s);

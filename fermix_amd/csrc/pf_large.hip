@@ -1,7 +1,7 @@
 // Blocked Parlett-Reid with partial pivoting for 128 < n <= 4096 (any batch). The skew
 // matrix lives in one workspace buffer (full storage, exactly skew). Per block of PB
-// columns (PB / 2 pair steps; PB = 64 for 512 <= N <= 1024 a multiple of 64, 32 for the other
-// N <= 2048, 16 above) at r0:
+// columns (PB / 2 pair steps; PB = 64 once the trailing order m = N - r0 is at most 1024
+// for N >= 512 a multiple of 64, else 32; 16 above N = 2048) at r0:
 //   1. pf_panel_kernel (one workgroup of NT = 256..1024 threads per matrix, each lane
 //      owning R = 2 or 4 of the m = N - r0 rows): the pair steps with the tau / w vectors
 //      kept in registers as G (m x PB); column a and column p of the current matrix are read
@@ -27,13 +27,20 @@ namespace fx {
 // SIMD resident, against two for 128 x 128 tiles, and the in-place update streams
 // M about 10 % faster at n = 1200 .. 2048.
 constexpr int PF_UPDATE_TILE = 64;
-constexpr int PFB_L = 64;   // columns per block (32 pair steps) for 512 <= N <= 1024, N % 64 == 0
-constexpr int PFB = 32;     // for the other N <= 2048
-constexpr int PFB_XL = 16;  // for 2048 < N <= PF_LARGE_MAXN
+constexpr int PFB_L = 64;   // columns per block (32 pair steps) where m <= 1024 (see pf_block_width)
+constexpr int PFB = 32;     // the other blocks of N <= 2048
+constexpr int PFB_XL = 16;  // every block of 2048 < N <= PF_LARGE_MAXN
 
-// Columns per block for padded order N.
-int pf_large_block_cols(int N) {
-  return N > 2048 ? PFB_XL : (N >= 512 && N <= 1024 && N % PFB_L == 0 ? PFB_L : PFB);
+// Columns per chunk of the exported factors gbuf (B, N / CW, N, CW) for padded order N:
+// the 32 (16 above N = 2048) columns of a block, or one half of a 64-column block.
+int pf_large_block_cols(int N) { return N > 2048 ? PFB_XL : PFB; }
+
+// Columns of the block at r0: 64 once the trailing order m = N - r0 is at most 1024, for
+// N >= 512 a multiple of 64 (G (m x 64) in the registers of 256 / 512 threads; the
+// trailing updates' HBM traffic halves), else 32; 16 above N = 2048.
+static int pf_block_width(int N, int r0) {
+  if (N > 2048) return PFB_XL;
+  return (N >= 512 && N % PFB_L == 0 && N - r0 <= 1024 && r0 % PFB_L == 0) ? PFB_L : PFB;
 }
 
 struct PfCand {
@@ -70,14 +77,16 @@ __global__ void pf_copy_pad_kernel(const float* __restrict__ A, int n, int skew,
 }
 
 template <int NT, int R, int PB>
-__global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ M, int N, int r0, int blk,
-                                                      int nblk, float* __restrict__ d_out,
+__global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ M, int N, int r0, int nch,
+                                                      float* __restrict__ d_out,
                                                       int* __restrict__ nsw_out,
                                                       int* __restrict__ src_out,
                                                       float* __restrict__ Gn,
                                                       int* __restrict__ orig,
                                                       float* __restrict__ gbuf) {
   constexpr int NW = NT / 64;
+  constexpr int CW = PB < 32 ? PB : 32;  // factor chunk width
+  static_assert(PB % CW == 0 && PB / CW <= 2, "a block spans one or two chunks");
   __shared__ PfRowA rowa;
   __shared__ PfCand cand[2][NW];
   __shared__ int posL[NT * R];
@@ -237,9 +246,10 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
 #pragma unroll
     for (int s = 0; s < R; ++s) {
       if (valid[s]) {
-        float* gr = gbuf + ((b * nblk + blk) * N + ov[s]) * (int64_t)PB;
+        // chunks of CW columns: chunk r0 / CW + k / CW, column k % CW
 #pragma unroll
-        for (int k = 0; k < PB; ++k) gr[k] = G[s][k];
+        for (int k = 0; k < PB; ++k)
+          gbuf[((b * nch + r0 / CW + k / CW) * N + ov[s]) * (int64_t)CW + k % CW] = G[s][k];
       }
     }
     __syncthreads();
@@ -247,8 +257,12 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     for (int s = 0; s < R; ++s)
       if (valid[s]) ob[r0 + pos[s]] = ov[s];
   }
-  // swap count: positions of this block are local, every wave counted the same swaps
-  if (tid == 0) nsw_out[b * nblk + blk] = nsw;
+  // swap count per chunk: positions of this block are local, every wave counted the same
+  // swaps (a 64-column block's second chunk counts none)
+  if (tid == 0) {
+    nsw_out[b * nch + r0 / CW] = nsw;
+    if (PB > CW) nsw_out[b * nch + r0 / CW + 1] = 0;
+  }
 }
 
 // M_new[p][q] = M_old[src p][src q] + sum_k G[p][k] (J G^T)[k][q] for the trailing
@@ -384,7 +398,7 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
   }
 }
 
-__global__ void pf_finish_kernel(const float* __restrict__ d, const int* __restrict__ nsw, int H, int nblk,
+__global__ void pf_finish_kernel(const float* __restrict__ d, const int* __restrict__ nsw, int H, int nch,
                                  float* __restrict__ sign, float* __restrict__ logabs, int64_t batch) {
   const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -399,7 +413,7 @@ __global__ void pf_finish_kernel(const float* __restrict__ d, const int* __restr
   }
   lg = wave_sum_f32(lg);
   int sw = 0;
-  for (int k = lane; k < nblk; k += 64) sw += nsw[b * nblk + k];
+  for (int k = lane; k < nch; k += 64) sw += nsw[b * nch + k];
   sw = (int)wave_sum_f32((float)sw);
   const bool anyz = __ballot(z) != 0ull;
   const int negs = __popcll(__ballot(ng)) + sw;
@@ -416,38 +430,40 @@ static __global__ void pf_iota_kernel(int* g, int N, int64_t total) {
 
 int pf_large_padded(int n) { return ((n + 31) / 32) * 32; }
 
+// Widest block of padded order N (the block at m = min(N, 1024) is the first that can be
+// 64 columns wide).
+static int pf_max_width(int N) { return pf_block_width(N, N > 1024 ? N - 1024 : 0); }
+
 size_t pf_large_workspace(int64_t batch, int n, bool fact) {
   const int N = pf_large_padded(n);
-  const int PB = pf_large_block_cols(N);
-  const int nblk = N / PB;
+  const int nch = N / pf_large_block_cols(N);
   size_t bytes = 0;
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
   add((size_t)batch * N * N * 4);  // M (updated in place)
-  add((size_t)batch * N * PB * 4);  // G (new order)
+  add((size_t)batch * N * pf_max_width(N) * 4);  // G (new order) of the current block
   add((size_t)batch * N * 4);      // src
-  add((size_t)batch * nblk * 4);   // swap counts
+  add((size_t)batch * nch * 4);    // swap counts per chunk
   add((size_t)batch * N / 2 * 4);  // d (forward only; parts uses its own)
   if (fact) add((size_t)batch * N * 4);  // orig
   return bytes;
 }
 
-// One block of PB columns at r0 = blk * PB: the panel (NT = 256, 512 or 1024 threads, R
-// rows per lane) and, unless it is the last block, the in-place trailing update.
+// One block of PB columns at r0: the panel (NT = 256, 512 or 1024 threads, R rows per
+// lane) and, unless it is the last block, the in-place trailing update.
 template <int PB, int R>
-static int pf_block(float* M, int N, int blk, int nblk, int64_t batch, float* d, int* nsw, int* src, float* Gn,
+static int pf_block(float* M, int N, int r0, int nch, int64_t batch, float* d, int* nsw, int* src, float* Gn,
                     int* orig, float* gbuf, const float* A0, hipStream_t s) {
-  const int r0 = blk * PB;
   const int m = N - r0;
   const float* Mp = A0 ? A0 : M;  // A0 (first block): the input itself, same layout
   if (m <= 256 * R)
-    hipLaunchKernelGGL((pf_panel_kernel<256, R, PB>), dim3((unsigned)batch), dim3(256), 0, s, Mp, N, r0, blk, nblk,
-                       d, nsw, src, Gn, orig, gbuf);
+    hipLaunchKernelGGL((pf_panel_kernel<256, R, PB>), dim3((unsigned)batch), dim3(256), 0, s, Mp, N, r0, nch, d,
+                       nsw, src, Gn, orig, gbuf);
   else if (m <= 512 * R)
-    hipLaunchKernelGGL((pf_panel_kernel<512, R, PB>), dim3((unsigned)batch), dim3(512), 0, s, Mp, N, r0, blk, nblk,
-                       d, nsw, src, Gn, orig, gbuf);
+    hipLaunchKernelGGL((pf_panel_kernel<512, R, PB>), dim3((unsigned)batch), dim3(512), 0, s, Mp, N, r0, nch, d,
+                       nsw, src, Gn, orig, gbuf);
   else if constexpr (PB * R <= 64)  // G[R][PB] fits the 128 VGPRs of a 1024-thread workgroup
-    hipLaunchKernelGGL((pf_panel_kernel<1024, R, PB>), dim3((unsigned)batch), dim3(1024), 0, s, Mp, N, r0, blk,
-                       nblk, d, nsw, src, Gn, orig, gbuf);
+    hipLaunchKernelGGL((pf_panel_kernel<1024, R, PB>), dim3((unsigned)batch), dim3(1024), 0, s, Mp, N, r0, nch,
+                       d, nsw, src, Gn, orig, gbuf);
   else
     return FX_ERR_UNSUPPORTED;
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
@@ -473,8 +489,7 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
   if (N > PF_LARGE_MAXN) return FX_ERR_UNSUPPORTED;
   const bool fact = gbuf != nullptr;
   if (!ws || ws_bytes < pf_large_workspace(batch, n, fact)) return FX_ERR_WORKSPACE;
-  const int PB = pf_large_block_cols(N);
-  const int nblk = N / PB;
+  const int nch = N / pf_large_block_cols(N);
   char* p = (char*)ws;
   auto take = [&](size_t x) {
     char* q = p;
@@ -482,9 +497,9 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     return (void*)q;
   };
   float* M0 = (float*)take((size_t)batch * N * N * 4);
-  float* Gn = (float*)take((size_t)batch * N * PB * 4);
+  float* Gn = (float*)take((size_t)batch * N * pf_max_width(N) * 4);
   int* src = (int*)take((size_t)batch * N * 4);
-  int* nsw = (int*)take((size_t)batch * nblk * 4);
+  int* nsw = (int*)take((size_t)batch * nch * 4);
   float* dbuf = (float*)take((size_t)batch * N / 2 * 4);
   int* orig = fact ? (int*)take((size_t)batch * N * 4) : nullptr;
   float* d = dout ? dout : dbuf;
@@ -502,14 +517,16 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     const int64_t tot = batch * N;
     hipLaunchKernelGGL(pf_iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, orig, N, tot);
   }
-  for (int blk = 0; blk < nblk; ++blk) {
-    const float* A0 = direct && blk == 0 ? A : nullptr;
-    const int st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
-                   : PB == PFB ? pf_block<PFB, 2>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
-                               : pf_block<PFB_XL, 4>(M0, N, blk, nblk, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
+  for (int r0 = 0; r0 < N;) {
+    const float* A0 = direct && r0 == 0 ? A : nullptr;
+    const int PB = pf_block_width(N, r0);
+    const int st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                   : PB == PFB ? pf_block<PFB, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                               : pf_block<PFB_XL, 4>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
     if (st != FX_OK) return st;
+    r0 += PB;
   }
-  hipLaunchKernelGGL(pf_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, d, nsw, N / 2, nblk,
+  hipLaunchKernelGGL(pf_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, d, nsw, N / 2, nch,
                      sign, logabs, batch);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   if (perm && fact)

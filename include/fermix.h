@@ -128,15 +128,16 @@ size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign,
                   float* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
-/* Columns per block of the Parlett-Reid factors: 16 for n <= 128; 64 for 480 < n <= 1024
- * when fx_pf_padded_size(n) is a multiple of 64; 32 for the other n <= 2048; 16 above. */
+/* Columns per chunk of the Parlett-Reid factors: 16 for n <= 128, 32 for n <= 2048, 16
+ * above (a chunk holds 16 or 8 pair steps; a 64-column block of the factorisation spans
+ * two chunks). */
 int32_t fx_pf_block_columns(int32_t n);
 
 /* The Parlett-Reid factors P S' P^T = L D L^T of the same run (S' = S padded with
  * [[0,1],[-1,0]] blocks to N = fx_pf_padded_size(n)), PB = fx_pf_block_columns(n):
- *  - gbuf (batch, N/PB, N, PB): block k's tau_t (column 2t) and w_t (column 2t+1),
- *    indexed by the original row; entries of rows assigned before the pair step are
- *    zero, rows assigned before block k are unspecified;
+ *  - gbuf (batch, N/PB, N, PB): chunk k's tau_t (column 2t) and w_t (column 2t+1) of the
+ *    pair steps PB/2 k + t, indexed by the original row; entries of rows assigned before
+ *    the pair step are zero, rows assigned before chunk k are unspecified;
  *  - d (batch, N/2): the pair pivots d_s = (P S' P^T reduced)[2s, 2s+1];
  *  - perm (batch, N): final position -> original row.
  * sign / logabs are bit-identical to fx_slogpf_f32. Replaces `_pf_core_factors`

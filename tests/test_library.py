@@ -59,8 +59,8 @@ def test_family_override_sizes():
     with _tune.override("blocked"):
         assert L.fx_lu_padded_size(20) == 64 and L.fx_pf_padded_size(20) == 32
         assert L.fx_slogdet_f32_workspace(4, 20) > 0 and L.fx_pf_block_columns(20) == 32
-    # blocked Parlett-Reid: 64-column blocks for 512 <= N <= 1024 where the padded order allows
-    assert [L.fx_pf_block_columns(n) for n in (100, 200, 256, 500, 512, 1024, 1025, 2048, 2049)] == [16, 32, 32, 64, 64, 64, 32, 32, 16]
+    # factor chunks: 32 columns for the blocked Parlett-Reid up to 2048, 16 above
+    assert [L.fx_pf_block_columns(n) for n in (100, 200, 256, 500, 512, 1024, 1025, 2048, 2049)] == [16, 32, 32, 32, 32, 32, 32, 32, 16]
     with _tune.override("tiny"):
         assert L.fx_lu_padded_size(40) == -1 and L.fx_pf_padded_size(20) == -1
     with _tune.override("fused"):
