@@ -512,6 +512,8 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
   __shared__ int srcU[PW];
   __shared__ int srcUr[PW];
   __shared__ int cnt;
+  constexpr int LDL = PW + 4;
+  __shared__ __align__(16) float Ls[PW * LDL];  // L21' of the pivot rows (deferred update)
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int strip = blockIdx.x;
@@ -533,6 +535,22 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
   if (tid == 0) {
     cnt = 0;
     srcv[0] = r0;
+  }
+  // deferred update (rc >= 0): the pivot rows' L21' (rows r0 .. r0+63 -- the panel moved
+  // those columns along -- columns rc .. rc+63) is read once per workgroup, here, so its
+  // latency overlaps the index pass; it reaches LDS before the read barrier below
+  float lr[16];
+  const bool corr = rc >= 0 && !left;
+  if (corr) {
+    const float4* lp = reinterpret_cast<const float4*>(Wb + (int64_t)(r0 + (tid >> 2)) * N + rc + 16 * (tid & 3));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 t = lp[q];
+      lr[4 * q] = t.x;
+      lr[4 * q + 1] = t.y;
+      lr[4 * q + 2] = t.z;
+      lr[4 * q + 3] = t.w;
+    }
   }
   __syncthreads();
   constexpr int MQ = MAXM / 256;  // m <= N <= MAXM
@@ -599,6 +617,12 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
 #pragma unroll
         for (int v = 0; v < 4; ++v) lv[q][v] = Wb[(int64_t)(r0 + 16 * s + li) * N + r0 + 16 * t + 4 * g + v];
   }
+  if (corr) {
+    float* lq = Ls + (tid >> 2) * LDL + 16 * (tid & 3);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<float4*>(lq + 4 * q) = make_float4(lr[4 * q], lr[4 * q + 1], lr[4 * q + 2], lr[4 * q + 3]);
+  }
   __syncthreads();  // no row is written before every thread has read what it needs
   // the moved rows; rows r0 .. r0+PW-1 of a trailing strip are written below as U12
 #pragma unroll
@@ -607,18 +631,17 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
     if ((left || !A0) && k < nm && cl < ncol && (left || list[k] >= PW)) Wb[(int64_t)(r0 + list[k]) * N + cstart + cl] = mv[u];
   }
   if (left) return;
-  if (rc >= 0) {
+  if (corr) {
     // deferred update of the previous block (rows / columns rc .. rc+63, not yet applied
-    // to these columns): A12 -= L21' U12' on the pivot rows, with L21' at the pivot rows'
-    // new positions r0 .. r0+63 (the panel moved those columns along) and U12' from rows
-    // rc .. rc+63. MFMA c takes k = 16 g + c on lane (g, li): four 16-byte L21' loads
-    // per row block, one U12' row element per c.
+    // to these columns): A12 -= L21' U12' on the pivot rows, with L21' from LDS (staged
+    // above) and U12' from rows rc .. rc+63. MFMA c takes k = 16 g + c on lane (g, li):
+    // four 16-byte L21' reads per row block, one U12' row element per c.
     float uv[16];
 #pragma unroll
     for (int c = 0; c < 16; ++c) uv[c] = Wb[(int64_t)(rc + 16 * g + c) * N + cstart + col];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
-      const float* Lr = Wb + (int64_t)(r0 + 16 * s + li) * N + rc + 16 * g;
+      const float* Lr = Ls + (16 * s + li) * LDL + 16 * g;
       float lw[16];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
