@@ -23,7 +23,7 @@ def _np(x):
     return x.detach().cpu().numpy()
 
 
-@pytest.mark.parametrize("n", [1, 2, 5, 16, 17, 33, 48, 64, 100, 128, 129, 200, 256, 300, 512])
+@pytest.mark.parametrize("n", [1, 2, 5, 16, 17, 33, 48, 64, 100, 128, 129, 200, 256, 300, 320, 512])
 def test_slogdet_invT_vs_float64_and_oracle(dev, n):
     B = 12 if n <= 256 else 4
     rng = np.random.default_rng(2000 + n)

@@ -21,7 +21,7 @@ def _np(x):
     return x.detach().cpu().numpy()
 
 
-@pytest.mark.parametrize("n", [129, 160, 192, 200, 256, 300, 384, 512, 640, 1000, 1024])
+@pytest.mark.parametrize("n", [129, 160, 192, 200, 256, 300, 320, 384, 448, 512, 640, 1000, 1024])
 def test_slogdet_large_vs_oracle(dev, n):
     B = 16 if n <= 512 else 6
     rng = np.random.default_rng(1000 + n)
