@@ -325,15 +325,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
         }
     const int any = __syncthreads_or(nf ? 1 : 0);
     if (tid == 0) d.flags[bat * (int64_t)gridDim.x + tx] = any;
+    // lane l holds the target row of tile column l (BN == 64: one per lane), so each store
+    // pass takes its row with a lane read instead of a load; column cc = wave + 4 u
+    static_assert(BN == 64 && BM == 64, "one tile column per lane");
     const int* gb = d.g0 + bat * d.N;
+    const int rl = j0 + lane < d.N ? gb[j0 + lane] : d.nout;
     const float sc = d.scale ? d.alpha * d.scale[bat] : d.alpha;
     float* ob = d.tout + bat * (int64_t)d.nout * d.nout;
-    for (int e = tid; e < BM * BN; e += 256) {
-      const int cc = e / BM, ii = e % BM, i = i0 + ii, c = j0 + cc;
-      if (i < d.nout && c < d.N) {
-        const int r = gb[c];
-        if (r < d.nout) ob[(int64_t)r * d.nout + i] = sc * Ts[cc * LDT + ii];
-      }
+    const int i = i0 + lane;
+#pragma unroll
+    for (int u = 0; u < BN / 4; ++u) {
+      const int cc = wave + 4 * u;
+      const int r = __builtin_amdgcn_readlane(rl, cc);
+      if (i < d.nout && r < d.nout) ob[(int64_t)r * d.nout + i] = sc * Ts[cc * LDT + lane];
     }
     return;
   }
