@@ -124,6 +124,9 @@ struct GemmDesc {
   int nout;
   const float* scale;
   int* flags;
+  // Optional row transform of B (maskB must be MASK_NONE, transB 0): op(B) row k is
+  // s_k B[k ^ 1] with s_k = bscale[b][k / 2], negated for odd k (bscale (batch, K / 2)).
+  const float* bscale;
 };
 
 // C = alpha op(A) op(B) + beta C for every (batch, second-batch) index.

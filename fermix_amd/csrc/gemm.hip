@@ -43,7 +43,7 @@ __device__ __forceinline__ bool mask_upper(int m) { return m == MASK_UPPER || m 
 // Tile loads: VEC uses 16-byte global loads along the operand's contiguous dimension
 // (requires that dimension, the leading dimensions, batch strides and base pointers to be
 // multiples of 4 floats), otherwise one float per load. Masks are applied in registers.
-template <int BM, int BN, bool VEC, int MK>
+template <int BM, int BN, bool VEC, int MK, bool BS = false>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   // operand masks: MK = 4 maskA + maskB fixed at compile time (the combinations this
   // library uses), so each mask test folds to one compare per element; MK < 0 reads them
@@ -131,6 +131,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   constexpr int AV = BM * GBK / 1024, BV = BN * GBK / 1024;  // float4 per thread
   constexpr int AE = BM * GBK / 256, BE = BN * GBK / 256;      // floats per thread
   float4 va[VEC ? AV : 1], vb[VEC ? BV : 1];
+  float bsv[VEC ? BV : 1];  // B row scales (bscale), loaded with the stage
   float ra[VEC ? 1 : AE], rb[VEC ? 1 : BE];
   // element coordinates of staging slot e (global row / k / column)
   auto a_coord = [&](int idx, int k0, int& gi, int& gk) {
@@ -172,6 +173,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
         b_coord(tid + 256 * e, k0, gk, gj);
         gj = min(gj, lastB_j);
         gk = min(gk, lastB_k);
+        if (BS) {  // row pair swap (K is even) and the row's scale
+          bsv[e] = d.bscale[bat * (d.K / 2) + (gk >> 1)];
+          gk ^= 1;
+        }
         vb[e] = *reinterpret_cast<const float4*>(d.transB ? B + (int64_t)gj * d.ldb + gk
                                                           : B + (int64_t)gk * d.ldb + gj);
       }
@@ -237,6 +242,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
         b_coord(idx, k0, gk, gj);
         const int dk = d.transB, dj = 1 - d.transB;
         float4 v = vb[e];
+        if (BS) {  // row gk of op(B) = s_gk B[gk ^ 1] (one row per vector: transB is 0)
+          const float sg = (gk & 1) ? -bsv[e] : bsv[e];
+          v.x *= sg;
+          v.y *= sg;
+          v.z *= sg;
+          v.w *= sg;
+        }
         if (!plain) {
           v.x = fixB(v.x, gk, gj);
           v.y = fixB(v.y, gk + dk, gj + dj);
@@ -380,7 +392,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
 // -- zeros outside the matrix, the triangle masks -- between two barriers.
 // Launch bound of 4 waves per SIMD: the compiler then fits the kernel in 116 VGPRs
 // (accumulators included) without scratch, against 168 + 64 left to itself.
-template <bool TA, int MK>
+template <bool TA, int MK, bool BS = false>
 __global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
   const int maskA = MK >= 0 ? (MK >> 2) : maskA;  // compile-time masks as in gemm_kernel
   const int maskB = MK >= 0 ? (MK & 3) : maskB;
@@ -446,12 +458,15 @@ __global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
 #pragma unroll
   for (int e = 0; e < 2; ++e) aoff[e] = TA ? ia : min(i0 + ra + 64 * e, d.M - 1) * d.lda;
   float va[2][4], vb[2][4];  // plain floats: arrays of float4 are not kept in registers
+  float bsv[2];              // B row scales (bscale), signed, loaded with the stage
   auto load_stage = [&](int k0) {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const float4 x = !TA ? *reinterpret_cast<const float4*>(A + aoff[e] + min(k0 + ka, d.K - 4))
                            : *reinterpret_cast<const float4*>(A + min(k0 + ka + 8 * e, d.K - 1) * d.lda + aoff[e]);
-      const float4 y = *reinterpret_cast<const float4*>(B + min(k0 + kb + 8 * e, d.K - 1) * d.ldb + jb);
+      const int kr = min(k0 + kb + 8 * e, d.K - 1);
+      if (BS) bsv[e] = d.bscale[bat * (d.K / 2) + (kr >> 1)];
+      const float4 y = *reinterpret_cast<const float4*>(B + (BS ? kr ^ 1 : kr) * d.ldb + jb);
       va[e][0] = x.x;
       va[e][1] = x.y;
       va[e][2] = x.z;
@@ -477,8 +492,14 @@ __global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
         *reinterpret_cast<float4*>(&As[buf][(ka + 8 * e) * LDA_ + 4 * (tid & 31)]) =
             make_float4(va[e][0], va[e][1], va[e][2], va[e][3]);
       }
-      *reinterpret_cast<float4*>(&Bs[buf][(kb + 8 * e) * LDB_ + 4 * (tid & 31)]) =
-          make_float4(vb[e][0], vb[e][1], vb[e][2], vb[e][3]);
+      if (BS) {  // row k of op(B) = s_k B[k ^ 1]: the sign of odd rows (kb + 8 e = k mod 2)
+        const float sg = (kb & 1) ? -bsv[e] : bsv[e];
+        *reinterpret_cast<float4*>(&Bs[buf][(kb + 8 * e) * LDB_ + 4 * (tid & 31)]) =
+            make_float4(sg * vb[e][0], sg * vb[e][1], sg * vb[e][2], sg * vb[e][3]);
+      } else {
+        *reinterpret_cast<float4*>(&Bs[buf][(kb + 8 * e) * LDB_ + 4 * (tid & 31)]) =
+            make_float4(vb[e][0], vb[e][1], vb[e][2], vb[e][3]);
+      }
     }
   };
   auto fix_stage = [&](int buf, int k0) {
@@ -596,6 +617,7 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
   // epilogue per K stage make the 64 x 64 tiles faster
   const bool big = vec && !d.transB && d.M >= 1024 && d.N >= 1024 && d.K >= 512 && !d.tout;
   if (d.tout && (d.lower_only || nb2 != 1 || d.active)) return FX_ERR_INVALID_ARGUMENT;
+  if (d.bscale && (d.maskB != MASK_NONE || d.transB || d.K % 2 || nb2 != 1 || !vec)) return FX_ERR_INVALID_ARGUMENT;
   const int tm2 = (d.M + 127) / 128, tn2 = (d.N + 127) / 128;
   const int tiles2 = d.lower_only ? tm2 * (tm2 + 1) / 2 : tm2 * tn2;
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
@@ -614,6 +636,22 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
       e.g0 += b0 * d.N;
       e.flags += b0 * tiles;
       if (d.scale) e.scale += b0;
+    }
+    if (d.bscale) e.bscale += b0 * (d.K / 2);
+    if (d.bscale) {  // the B row transform: its own instantiations (A^T unit upper, or any mask)
+      const bool ua = d.transA && d.maskA == MASK_UPPER_UNIT;
+      if (big) {
+        const dim3 grid2(tiles2, (unsigned)nb, nb2);
+        if (ua) hipLaunchKernelGGL((gemm128_kernel<true, 4 * MASK_UPPER_UNIT, true>), grid2, dim3(256), 0, s, e);
+        else if (d.transA) hipLaunchKernelGGL((gemm128_kernel<true, -1, true>), grid2, dim3(256), 0, s, e);
+        else hipLaunchKernelGGL((gemm128_kernel<false, -1, true>), grid2, dim3(256), 0, s, e);
+      } else {
+        const dim3 grid(tiles, (unsigned)nb, nb2);
+        if (ua) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, 4 * MASK_UPPER_UNIT, true>), grid, dim3(256), 0, s, e);
+        else hipLaunchKernelGGL((gemm_kernel<BM, BN, true, -1, true>), grid, dim3(256), 0, s, e);
+      }
+      if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+      continue;
     }
     if (big) {
       const dim3 grid2(tiles2, (unsigned)nb, nb2);

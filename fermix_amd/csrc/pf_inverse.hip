@@ -10,7 +10,9 @@
 //            lifted: G is affine in that pair entry, so G = (G(d_z = +1) + G(d_z = -1)) / 2,
 //            the second evaluation running only for the members that have such a pivot.
 // Kernels: pivot / coefficient prep (one wave per matrix), L~ assembly, the triangular
-// inverse of inverse.hip (lower half only), DY, the skew GEMM R (lower tiles + mirror),
+// inverse of inverse.hip (lower half only), the skew GEMM R (lower tiles + mirror; its
+// B operand DY is read from Y through the GEMM's row pair swap and per-row scale, so DY
+// is never stored),
 // and the permutation gather with the rank-2 correction and the non-finite flags formed
 // on the way (no corrected matrix is stored between them).
 //
@@ -150,30 +152,6 @@ __global__ __launch_bounds__(256) void pf_assemble_kernel(const float* __restric
   }
 }
 
-// DY[2s] = Y[2s+1] / d~_s, DY[2s+1] = -Y[2s] / d~_s with Y the unit-lower part of T.
-// One workgroup per row r, 16-byte vectors along the row.
-__global__ __launch_bounds__(256) void pf_dy_kernel(const float* __restrict__ T, int Ninv, int N,
-                                                    const float* __restrict__ dinv, float* __restrict__ DY,
-                                                    const int* __restrict__ active) {
-  const int64_t b = blockIdx.y;
-  if (active && !active[b]) return;
-  const int r = blockIdx.x, src = r ^ 1;
-  const float4* y4 = reinterpret_cast<const float4*>(T + b * (int64_t)Ninv * Ninv + (int64_t)src * Ninv);
-  float4* o4 = reinterpret_cast<float4*>(DY + b * (int64_t)N * N + (int64_t)r * N);
-  const float d = dinv[b * (N / 2) + (r >> 1)];
-  const float sc = (r & 1) ? -d : d;
-  for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) {
-    const int c = 4 * c4;
-    float4 y = c < src ? y4[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    // unit lower: entries with column > src are 0, the diagonal is 1
-    y.x = c < src ? y.x : (c == src ? 1.0f : 0.0f);
-    y.y = c + 1 < src ? y.y : (c + 1 == src ? 1.0f : 0.0f);
-    y.z = c + 2 < src ? y.z : (c + 2 == src ? 1.0f : 0.0f);
-    y.w = c + 3 < src ? y.w : (c + 3 == src ? 1.0f : 0.0f);
-    o4[c4] = make_float4(y.x * sc, y.y * sc, y.z * sc, y.w * sc);
-  }
-}
-
 // w[c] = R[c][2K] (the column of R that the rank-2 correction uses), one thread per c.
 __global__ void pf_wvec_kernel(const float* __restrict__ R, int N, const PfCoef* __restrict__ coef,
                                float* __restrict__ w, const int* __restrict__ active) {
@@ -259,7 +237,6 @@ size_t pf_inverse_workspace(int64_t batch, int N) {
   auto add = [&](size_t x) { bytes += (x + 255) / 256 * 256; };
   add((size_t)batch * Ninv * Ninv * 4);  // T (L~, then Y)
   add((size_t)batch * Ninv * Ninv);      // Tmp (Ninv/2 x Ninv/2 floats)
-  add((size_t)batch * N * N * 4);        // DY
   add((size_t)batch * N * N * 4);        // R
   add((size_t)batch * N * 4);            // wvec
   add((size_t)batch * N / 2 * 4);        // dinv
@@ -284,7 +261,6 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
   };
   float* T = (float*)take((size_t)batch * Ninv * Ninv * 4);
   float* Tmp = (float*)take((size_t)batch * Ninv * Ninv);
-  float* DY = (float*)take((size_t)batch * N * N * 4);
   float* R = (float*)take((size_t)batch * N * N * 4);
   float* wvec = (float*)take((size_t)batch * N * 4);
   float* dinv = (float*)take((size_t)batch * N / 2 * 4);
@@ -312,9 +288,6 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     int st = launch_unit_lower_inverse(T, Ninv, batch, Tmp, s, active);
     if (st != FX_OK) return st;
-    hipLaunchKernelGGL(pf_dy_kernel, dim3((unsigned)N, (unsigned)batch), dim3(256), 0, s, T, Ninv, N, dinv, DY,
-                       active);
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     {
       // R = Y^T DY: op(A) = Y^T (upper, unit diagonal), lower tiles, mirrored skew
       GemmDesc g = {};
@@ -324,9 +297,12 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
       g.maskA = MASK_UPPER_UNIT;
       g.lda = Ninv;
       g.sA = NN;
-      g.B = DY;
-      g.ldb = N;
-      g.sB = MM;
+      // B = DY = rows (Y[p_s], -Y[a_s]) / d~_s, read from Y by the GEMM's row transform
+      // (Y keeps exact zeros above and ones on its diagonal)
+      g.B = T;
+      g.ldb = Ninv;
+      g.sB = NN;
+      g.bscale = dinv;
       g.C = R;
       g.ldc = N;
       g.sC = MM;
