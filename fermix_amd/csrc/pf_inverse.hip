@@ -189,29 +189,43 @@ __global__ __launch_bounds__(256) void pf_adj_gather_kernel(const float* __restr
                                                             int* __restrict__ flags, float* __restrict__ out,
                                                             const int* __restrict__ active, int accumulate,
                                                             const float* __restrict__ scale) {
-  __shared__ __align__(16) float rowb[PF_LARGE_MAXN];
+  // the source row of R, row 2K of Y and w, each read contiguously into LDS; the column
+  // permutation then gathers from LDS only
+  extern __shared__ __align__(16) float pf_gather_lds[];  // 3 N floats (launch-time size)
+  float* const rowb = pf_gather_lds;
+  float* const vrow = pf_gather_lds + N;
+  float* const wrow = pf_gather_lds + 2 * N;
   const int64_t b = blockIdx.y;
   if (active && !active[b]) return;
   const int i = blockIdx.x;
   const int* ip = iperm + b * N;
   const int f = ip[i];
-  const float4* s4 = reinterpret_cast<const float4*>(R + b * (int64_t)N * N + (int64_t)f * N);
-  for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) reinterpret_cast<float4*>(rowb)[c4] = s4[c4];
   const PfCoef cf = coef[b];
   const float a1 = sg * cf.a1, a2 = sg * cf.a2;
   const int aK = 2 * cf.K;
-  const float* Tk = T + b * (int64_t)Ninv * Ninv + (int64_t)aK * Ninv;  // row 2K of Y
-  const float* wb = wvec + b * N;
-  const float v_f = f < aK ? Tk[f] : (f == aK ? 1.0f : 0.0f);
+  const float4* s4 = reinterpret_cast<const float4*>(R + b * (int64_t)N * N + (int64_t)f * N);
+  const float4* t4 = reinterpret_cast<const float4*>(T + b * (int64_t)Ninv * Ninv + (int64_t)aK * Ninv);
+  const float4* w4 = reinterpret_cast<const float4*>(wvec + b * N);
+  for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) {
+    reinterpret_cast<float4*>(rowb)[c4] = s4[c4];
+    // v = Y^T e_2K: Y[2K][c] for c < 2K, 1 at 2K, 0 after
+    float4 t = t4[c4];
+    const int c = 4 * c4;
+    t.x = c < aK ? t.x : (c == aK ? 1.0f : 0.0f);
+    t.y = c + 1 < aK ? t.y : (c + 1 == aK ? 1.0f : 0.0f);
+    t.z = c + 2 < aK ? t.z : (c + 2 == aK ? 1.0f : 0.0f);
+    t.w = c + 3 < aK ? t.w : (c + 3 == aK ? 1.0f : 0.0f);
+    reinterpret_cast<float4*>(vrow)[c4] = t;
+    reinterpret_cast<float4*>(wrow)[c4] = w4[c4];
+  }
   const float sc = scale ? scale[b] : 1.0f;
   __syncthreads();
-  const float w_f = rowb[aK];
+  const float w_f = rowb[aK], v_f = vrow[f];
   float* o = out + b * (int64_t)n * n + (int64_t)i * n;
   bool nf = false;
   for (int j = threadIdx.x; j < N; j += 256) {
     const int c = ip[j];
-    const float v_c = c < aK ? Tk[c] : (c == aK ? 1.0f : 0.0f);
-    const float val = -(a1 * rowb[c] + a2 * (w_f * v_c - v_f * wb[c]));
+    const float val = -(a1 * rowb[c] + a2 * (w_f * vrow[c] - v_f * wrow[c]));
     nf = nf || !isfinite(val);
     if (i < n && j < n) {
       if (accumulate) o[j] += sc * val;
@@ -317,8 +331,8 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
     hipLaunchKernelGGL(pf_wvec_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)batch), dim3(256), 0, s, R, N,
                        coef, wvec, active);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    hipLaunchKernelGGL(pf_adj_gather_kernel, dim3((unsigned)N, (unsigned)batch), dim3(256), 0, s, R, N, T, Ninv,
-                       coef, sg, wvec, iperm, n, flags, out, active, accumulate, scale);
+    hipLaunchKernelGGL(pf_adj_gather_kernel, dim3((unsigned)N, (unsigned)batch), dim3(256), 3 * N * sizeof(float), s,
+                       R, N, T, Ninv, coef, sg, wvec, iperm, n, flags, out, active, accumulate, scale);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     if (accumulate) return FX_OK;
     // inverse mode: members with d_K = 0 or a non-finite value anywhere are zeroed
