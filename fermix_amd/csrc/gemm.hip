@@ -20,7 +20,14 @@
 //    triangle at tile granularity;
 //  * lower_only: only tiles with tile_row >= tile_col are computed, and each element
 //    is also stored mirrored, C[j][i] = mirror * C[i][j] (mirror = -1 gives an exactly
-//    skew result with a zero diagonal).
+//    skew result with a zero diagonal);
+//  * tout (64 x 64 tiles): the product is stored transposed and row-permuted,
+//    tout[g0[j]][i] = scale[b] alpha C[i][j], through an LDS transpose in the epilogue,
+//    with a non-finite flag per tile (the slogdet backward's A^-T = P^T Z^T);
+//  * bscale: op(B) row k is +-bscale[k / 2] B[k ^ 1] (pair swap and per-row scale,
+//    applied between the stage load and the LDS store), a compile-time variant.
+// The mask combination is a template parameter for the combinations the library uses,
+// so a masked element costs one compare and a plain stage carries no mask code.
 #include "common.h"
 #include "fermix_internal.h"
 
