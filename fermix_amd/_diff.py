@@ -16,6 +16,9 @@ fold into the kernels' batch, so vmap(f)(x) runs exactly the arithmetic of f(x))
 * pf: d pf = sum(G * dS), G = -pf(S) S^-1 / 2 (_diff.py:305-333), with the Pfaffian
   adjugate pf(S) S^-1 from the forward's own Parlett-Reid factors (finite for singular
   S); G is skew, so it is also the gradient w.r.t. ``a`` through S = (a - a^T)/2.
+
+float64 inputs take the parts route (A^-T / S^-1 formed with the primal by the f64
+kernels); their det / pf derivatives (the exact adjugates) raise NotImplementedError.
 """
 
 import torch
@@ -189,7 +192,7 @@ def slogdet(A):
     if _wants_grad(A):
         # n <= 32: one Gauss-Jordan pass forms A^-T with the factors; forward mode and
         # torch.func transforms: the parts call (their rules run on wrapped tensors)
-        if A.shape[-1] > 32 and _plain_reverse(A):
+        if A.dtype == torch.float32 and A.shape[-1] > 32 and _plain_reverse(A):
             s, l, _, _ = _SlogdetSplit.apply(A)
         else:
             s, l, _ = _SlogdetParts.apply(A)
@@ -301,7 +304,7 @@ class _SlogpfSplit(torch.autograd.Function):
 def slogpf(A, skew):
     if _wants_grad(A):
         n = A.shape[-1]
-        if n > 0 and n % 2 == 0 and _plain_reverse(A):
+        if A.dtype == torch.float32 and n > 0 and n % 2 == 0 and _plain_reverse(A):
             s, l, _, _, _ = _SlogpfSplit.apply(A, skew)
         else:
             s, l, _ = _SlogpfParts.apply(A, skew)

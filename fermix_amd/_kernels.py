@@ -1,6 +1,6 @@
 """Torch plumbing around the C ABI: allocate outputs / workspace on the input's device,
 pass raw pointers and the current HIP stream. Inputs are (B, n, n) contiguous float32
-tensors on a ROCm device; no numerics happen here."""
+tensors (float64 for the f64 entry points) on a ROCm device; no numerics happen here."""
 
 import torch
 
@@ -25,11 +25,22 @@ def _workspace(nbytes, device):
     return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
 
 
-def _check_input(A):
+def _check_input(A, f64_ok=False):
+    """Returns True for a float64 input (the f64 entry points), False for float32."""
     if not A.is_cuda:
         raise RuntimeError("fermix_amd kernels need a tensor on a ROCm GPU")
-    if A.dtype != torch.float32 or A.dim() != 3 or not A.is_contiguous():
-        raise RuntimeError("internal: expected a contiguous (B, n, n) float32 tensor")
+    ok = (torch.float32, torch.float64) if f64_ok else (torch.float32,)
+    if A.dtype not in ok or A.dim() != 3 or not A.is_contiguous():
+        raise RuntimeError(f"internal: expected a contiguous (B, n, n) tensor of {ok}")
+    return A.dtype == torch.float64
+
+
+def _no_f64(A, what):
+    if A.dtype == torch.float64:
+        raise NotImplementedError(
+            f"fermix_amd: {what} is implemented for float32 only (float64 has slogdet / "
+            "slogpf / det / pf values and the slogdet / slogpf derivatives)"
+        )
 
 
 def lu_padded_size(n):
@@ -42,11 +53,16 @@ def pf_padded_size(n):
 
 def slogdet(A):
     """(sign, logabs) of each (n, n) matrix of A (B, n, n)."""
-    _check_input(A)
+    f64 = _check_input(A, f64_ok=True)
     B, n, _ = A.shape
     sign = torch.empty(B, dtype=A.dtype, device=A.device)
     logabs = torch.empty(B, dtype=A.dtype, device=A.device)
     L = lib()
+    if f64:
+        ws, wsb = _workspace(L.fx_slogdet_f64_workspace(B, n), A.device)
+        st = L.fx_slogdet_f64(_ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(ws), wsb, _stream(A))
+        check(st, "fx_slogdet_f64")
+        return sign, logabs
     ws, wsb = _workspace(L.fx_slogdet_f32_workspace(B, n), A.device)
     st = L.fx_slogdet_f32(_ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(ws), wsb, _stream(A))
     check(st, "fx_slogdet_f32")
@@ -55,13 +71,24 @@ def slogdet(A):
 
 def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False):
     """(sign, logabs, invT, lu, perm) with the optional outputs None when not asked for;
-    lu / perm are padded to N = lu_padded_size(n)."""
-    _check_input(A)
+    lu / perm are padded to N = lu_padded_size(n). float64: invT only (zero for exactly
+    singular members), no packed factors."""
+    f64 = _check_input(A, f64_ok=True)
     B, n, _ = A.shape
     dev = A.device
     sign = torch.empty(B, dtype=A.dtype, device=dev)
     logabs = torch.empty(B, dtype=A.dtype, device=dev)
     invT = torch.empty_like(A) if want_inv else None
+    if f64:
+        if want_lu or not zero_singular:
+            _no_f64(A, "the packed LU / unguarded inverse")
+        L = lib()
+        ws, wsb = _workspace(L.fx_slogdet_parts_f64_workspace(B, n), dev)
+        st = L.fx_slogdet_parts_f64(
+            _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(invT), _ptr(ws), wsb, _stream(A)
+        )
+        check(st, "fx_slogdet_parts_f64")
+        return sign, logabs, invT, None, None
     lu = perm = None
     if want_lu and n > 0:
         N = lu_padded_size(n)
@@ -116,6 +143,7 @@ def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True):
 
 def det_parts(A):
     """(sign, logabs, adjT) with adjT = adj(A)^T = d det / dA from one factorisation."""
+    _no_f64(A, "the det gradient (exact adjugate)")
     _check_input(A)
     B, n, _ = A.shape
     dev = A.device
@@ -132,11 +160,19 @@ def det_parts(A):
 
 
 def slogpf(A, skew_symmetrize):
-    _check_input(A)
+    f64 = _check_input(A, f64_ok=True)
     B, n, _ = A.shape
     sign = torch.empty(B, dtype=A.dtype, device=A.device)
     logabs = torch.empty(B, dtype=A.dtype, device=A.device)
     L = lib()
+    if f64:
+        ws, wsb = _workspace(L.fx_slogpf_f64_workspace(B, n), A.device)
+        st = L.fx_slogpf_f64(
+            _ptr(A), B, n, int(bool(skew_symmetrize)), _ptr(sign), _ptr(logabs), _ptr(ws), wsb,
+            _stream(A),
+        )
+        check(st, "fx_slogpf_f64")
+        return sign, logabs
     ws, wsb = _workspace(L.fx_slogpf_f32_workspace(B, n), A.device)
     st = L.fx_slogpf_f32(
         _ptr(A), B, n, int(bool(skew_symmetrize)), _ptr(sign), _ptr(logabs), _ptr(ws), wsb,
@@ -188,14 +224,24 @@ def slogpf_inverse(gbuf, d, perm, n, scale=None, adjugate=False):
 
 def slogpf_parts(A, skew_symmetrize, adjugate=False):
     """(sign, logabs, G) of the (skew-symmetrised) batch from one Parlett-Reid run, G = S^-1
-    or, with adjugate, pf(S) S^-1."""
-    _check_input(A)
+    or, with adjugate, pf(S) S^-1 (float32 only)."""
+    if adjugate:
+        _no_f64(A, "the pf gradient (Pfaffian adjugate)")
+    f64 = _check_input(A, f64_ok=True)
     B, n, _ = A.shape
     dev = A.device
     L = lib()
     sign = torch.empty(B, dtype=A.dtype, device=dev)
     logabs = torch.empty(B, dtype=A.dtype, device=dev)
     g = torch.empty_like(A)
+    if f64:
+        ws, wsb = _workspace(L.fx_slogpf_parts_f64_workspace(B, n), dev)
+        st = L.fx_slogpf_parts_f64(
+            _ptr(A), B, n, int(bool(skew_symmetrize)), 0, _ptr(sign), _ptr(logabs), _ptr(g),
+            _ptr(ws), wsb, _stream(A),
+        )
+        check(st, "fx_slogpf_parts_f64")
+        return sign, logabs, g
     ws, wsb = _workspace(L.fx_slogpf_parts_f32_workspace(B, n), dev)
     st = L.fx_slogpf_parts_f32(
         _ptr(A), B, n, int(bool(skew_symmetrize)), int(bool(adjugate)), _ptr(sign), _ptr(logabs), _ptr(g),

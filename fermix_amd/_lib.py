@@ -42,6 +42,14 @@ SIGNATURES = {
     "fx_slogpf_inverse_f32": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _sz, _p]),
     "fx_slogpf_parts_f32_workspace": (_sz, [_i64, _i32]),
     "fx_slogpf_parts_f32": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _sz, _p]),
+    "fx_slogdet_f64_workspace": (_sz, [_i64, _i32]),
+    "fx_slogdet_f64": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _sz, _p]),
+    "fx_slogdet_parts_f64_workspace": (_sz, [_i64, _i32]),
+    "fx_slogdet_parts_f64": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _sz, _p]),
+    "fx_slogpf_f64_workspace": (_sz, [_i64, _i32]),
+    "fx_slogpf_f64": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _sz, _p]),
+    "fx_slogpf_parts_f64_workspace": (_sz, [_i64, _i32]),
+    "fx_slogpf_parts_f64": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _sz, _p]),
 }
 
 

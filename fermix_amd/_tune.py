@@ -12,6 +12,8 @@ this module mirrors it for introspection and tests.
 import contextlib
 import os
 
+import torch
+
 # prec values accepted by the public API. "ieee": fp32 MFMA / FMA updates (the only
 # arithmetic of this build). "tf32x3" is accepted for drop-in compatibility with the
 # reference's float32 default: it exists there to reach fp32-level accuracy on tensor
@@ -19,11 +21,18 @@ import os
 PREC = ("ieee", "tf32x3")
 
 
-def check_prec(prec):
+def check_prec(prec, dtype=None):
+    """"tf32x3" is accepted for float32 only (the reference rejects it for 64-bit types,
+    src/fermix/_field.py:265-275)."""
     if prec is None:
         return "ieee"
     if prec not in PREC:
         raise ValueError(f"prec must be 'tf32x3' or 'ieee', got {prec!r}")
+    if prec == "tf32x3" and dtype is not None and dtype != torch.float32:
+        raise ValueError(
+            "prec='tf32x3' applies to float32 / complex64 only; float64 and "
+            "complex128 run in IEEE fp64 (prec='ieee')"
+        )
     return "ieee"
 
 

@@ -49,9 +49,9 @@ def _prep(a):
         )
     if a.dim() < 2 or a.shape[-1] != a.shape[-2]:
         raise ValueError(f"expected (..., n, n), got {tuple(a.shape)}")
-    if a.dtype != torch.float32:
+    if a.dtype not in (torch.float32, torch.float64):
         raise TypeError(
-            f"fermix_amd implements the float32 path (the north-star dtype); got {a.dtype}"
+            f"fermix_amd implements the float32 and float64 paths; got {a.dtype}"
         )
     return a
 
@@ -81,7 +81,7 @@ def slogdet(a, *, prec=None, unroll_steps=None, block=None):
     accepted for compatibility and validated; the gfx950 kernels choose their blocking
     from n (fermix_amd._tune)."""
     a = _prep(a)
-    check_prec(prec)
+    check_prec(prec, a.dtype)
     check_block(block)
     _on_device(a)
     A, batch, n = _flat(a)
@@ -94,7 +94,7 @@ def slogpf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
     api.py:177-193): S = (a - a^T)/2 unless skew_symmetrize=False (then ``a`` must be
     exactly skew); odd n gives (0, -inf)."""
     a = _prep(a)
-    check_prec(prec)
+    check_prec(prec, a.dtype)
     _on_device(a)
     A, batch, n = _flat(a)
     if n % 2 == 1:
@@ -108,7 +108,7 @@ def det(a, *, prec=None, unroll_steps=None, block=None):
     """Determinant of a batch of matrices (reference ``det``, api.py:196-212):
     sign * exp(logabs) of the same factorisation."""
     a = _prep(a)
-    check_prec(prec)
+    check_prec(prec, a.dtype)
     check_block(block)
     _on_device(a)
     A, batch, n = _flat(a)
@@ -119,7 +119,7 @@ def pf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
     """Pfaffian of a batch of skew-symmetric matrices (reference ``pf``, api.py:215-227);
     odd n gives 0."""
     a = _prep(a)
-    check_prec(prec)
+    check_prec(prec, a.dtype)
     _on_device(a)
     A, batch, n = _flat(a)
     if n % 2 == 1:

@@ -1,0 +1,376 @@
+// float64 path: slogdet / slogpf forward and their gradients (A^-T, S^-1) for
+// 0 <= n <= 4096, one workgroup per matrix.
+//
+// The reference takes float64 through the same entry points as float32 (dtype check
+// `_prep`, src/fermix/api.py:24-31; 64-bit fields in src/fermix/_field.py:20-120, where
+// "tf32x3" is rejected for 64-bit types, :265-275). Its arithmetic for these types is
+// the generic path: LU with partial pivoting (`_slogdet_generic` / `_slog_from_lu`,
+// src/fermix/_fallback.py:36-60), the inverse for the gradient (`_lu_parts_generic`,
+// :63-97) and Parlett-Reid with the pivot swapped into column c + 1 and the rank-2
+// update tau w^T - w tau^T (`_slogpf_generic`, :266-300).
+//
+// Kernels (each a single workgroup per matrix; the matrix in LDS when it fits in 60 KiB,
+// else in a per-matrix slice of the workspace, where its rows stay in L2):
+//  - gj64_kernel<NT, INV>: Gauss-Jordan with virtual partial pivoting (the pivot row of
+//    column j is the unassigned row of largest |x|, lowest row index on ties). Without
+//    INV only the unassigned rows are updated (an LU); with INV the assigned rows and an
+//    identity block [A | I] are eliminated too, and row j of A^-1 is row prow[j] of the
+//    right block over pivot j. The unassigned rows see the same operations in both modes,
+//    so sign / logabs of the gradient call are bit-identical to the forward.
+//  - pr64_kernel<NT>: Parlett-Reid on the full matrix with physical row / column swaps;
+//    the update adds round(tau_r w_k) - round(w_r tau_k) (no contraction), so the matrix
+//    stays exactly skew-symmetric and its diagonal exactly zero.
+// Both are latency-bound per matrix (a workgroup barrier per column / pair step); they
+// are a correct, device-resident float64 path, not tuned like the float32 families.
+#include "fermix_internal.h"
+
+namespace fx {
+namespace {
+
+constexpr int F64_MAXN = 4096;
+constexpr size_t F64_LDS_MAX = 60 * 1024;  // matrix bytes kept in LDS
+
+size_t align_up_256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Order-preserving key of a pivot candidate: |x| bits plus one (0 = no candidate).
+__device__ __forceinline__ unsigned long long key64(double x) {
+  return (unsigned long long)__double_as_longlong(fabs(x)) + 1ull;
+}
+
+__device__ __forceinline__ void take_better(unsigned long long& k, int& r, unsigned long long k2, int r2) {
+  if (k2 > k || (k2 == k && r2 < r)) {
+    k = k2;
+    r = r2;
+  }
+}
+
+// Workgroup argmax of (key, row), larger key first, then lower row; every thread returns
+// the winning row (-1 if no thread had a candidate). redk / redr: NT / 64 slots; the
+// caller alternates two slot sets between consecutive calls, so no extra barrier guards
+// their reuse.
+template <int NT>
+__device__ __forceinline__ int block_argmax(unsigned long long k, int r, unsigned long long* redk, int* redr) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long k2 = __shfl_xor(k, off);
+    const int r2 = __shfl_xor(r, off);
+    take_better(k, r, k2, r2);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    redk[w] = k;
+    redr[w] = r;
+  }
+  __syncthreads();
+  k = redk[0];
+  r = redr[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) take_better(k, r, redk[i], redr[i]);
+  return k ? r : -1;
+}
+
+// Loads S (skew != 0: (a - a^T) / 2) into M with row stride ld; with ident, M[:, n:2n] = I.
+template <int NT>
+__device__ __forceinline__ void load_matrix(const double* __restrict__ a, int n, int skew, double* M, int ld,
+                                            bool ident) {
+  for (int e = threadIdx.x; e < n * n; e += NT) {
+    const int r = e / n, k = e - r * n;
+    double v = a[e];
+    if (skew) v = (v - a[(size_t)k * n + r]) * 0.5;
+    M[(size_t)r * ld + k] = v;
+    if (ident) M[(size_t)r * ld + n + k] = (r == k) ? 1.0 : 0.0;
+  }
+}
+
+template <int NT, bool INV>
+__global__ __launch_bounds__(NT) void gj64_kernel(const double* __restrict__ a, int n, int skew, double* Wg,
+                                                 int use_lds, double* __restrict__ sign_out,
+                                                 double* __restrict__ logabs_out, double* __restrict__ out, int out_t,
+                                                 const double* __restrict__ gate) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ unsigned long long redk[2][NT / 64];
+  __shared__ int redr[2][NT / 64];
+  const int ld = INV ? 2 * n : n;
+  const size_t mat = (size_t)n * ld;
+  const int64_t b = blockIdx.x;
+  double* M = use_lds ? (double*)smem : Wg + (size_t)b * mat;
+  int* prow = (int*)(smem + (use_lds ? mat * sizeof(double) : 0));
+  unsigned char* asg = (unsigned char*)(prow + n);
+  const double* A = a + (size_t)b * n * n;
+
+  load_matrix<NT>(A, n, skew, M, ld, INV);
+  for (int r = threadIdx.x; r < n; r += NT) asg[r] = 0;
+  __syncthreads();
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  double logabs = 0.0, sgn = 1.0;
+  bool singular = false;
+  for (int j = 0; j < n; ++j) {
+    unsigned long long k = 0;
+    int row = 0x7fffffff;
+    for (int r = threadIdx.x; r < n; r += NT)
+      if (!asg[r]) take_better(k, row, key64(M[(size_t)r * ld + j]), r);
+    const int p = block_argmax<NT>(k, row, redk[j & 1], redr[j & 1]);
+    const double piv = M[(size_t)p * ld + j];
+    double rinv = 0.0;  // recip(0) = 0: a zero pivot updates nothing
+    if (piv == 0.0) {
+      singular = true;
+    } else {
+      rinv = 1.0 / piv;
+      logabs += log(fabs(piv));
+      if (piv < 0.0) sgn = -sgn;
+    }
+    if (threadIdx.x == 0) {
+      prow[j] = p;
+      asg[p] = 1;
+    }
+    const double* P = M + (size_t)p * ld;
+    for (int r = wave; r < n; r += NT / 64) {
+      if (r == p || (!INV && asg[r])) continue;
+      double* R = M + (size_t)r * ld;
+      const double l = R[j] * rinv;
+      for (int c = j + 1 + lane; c < ld; c += 64) R[c] = fma(-l, P[c], R[c]);
+    }
+    __syncthreads();
+  }
+
+  // parity of j -> prow[j] (n - number of cycles), by thread 0; asg reused as the marks
+  if (threadIdx.x == 0) {
+    for (int r = 0; r < n; ++r) asg[r] = 0;
+    int cycles = 0;
+    for (int s = 0; s < n; ++s) {
+      if (asg[s]) continue;
+      ++cycles;
+      for (int t = s; !asg[t]; t = prow[t]) asg[t] = 1;
+    }
+    if ((n - cycles) & 1) sgn = -sgn;
+    if (singular) {
+      sign_out[b] = 0.0;
+      logabs_out[b] = -INFINITY;
+    } else {
+      sign_out[b] = sgn;
+      logabs_out[b] = logabs;
+    }
+  }
+  if constexpr (INV) {
+    double* O = out + (size_t)b * n * n;
+    const bool zero = singular || (gate && gate[b] == 0.0);
+    bool bad = false;
+    if (!zero) {
+      // A^-1[j, c] = M[prow[j], n + c] / pivot_j; out_t: O[c, j], else O[j, c]
+      for (int e = threadIdx.x; e < n * n; e += NT) {
+        const int r = e / n, c = e - r * n;
+        const int j = out_t ? c : r, col = out_t ? r : c;
+        const double* Pj = M + (size_t)prow[j] * ld;
+        const double v = Pj[n + col] / Pj[j];
+        bad |= !isfinite(v);
+        O[e] = v;
+      }
+    }
+    if (zero || __syncthreads_or(bad))
+      for (int e = threadIdx.x; e < n * n; e += NT) O[e] = 0.0;
+  }
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void pr64_kernel(const double* __restrict__ a, int n, int skew, double* Wg,
+                                                 int use_lds, double* __restrict__ sign_out,
+                                                 double* __restrict__ logabs_out) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ unsigned long long redk[2][NT / 64];
+  __shared__ int redr[2][NT / 64];
+  const size_t mat = (size_t)n * n;
+  const int64_t b = blockIdx.x;
+  if (n & 1) {  // odd n: pf = 0
+    if (threadIdx.x == 0) {
+      sign_out[b] = 0.0;
+      logabs_out[b] = -INFINITY;
+    }
+    return;
+  }
+  double* M = use_lds ? (double*)smem : Wg + (size_t)b * mat;
+  load_matrix<NT>(a + (size_t)b * mat, n, skew, M, n, false);
+  __syncthreads();
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  double logabs = 0.0, sgn = 1.0;
+  bool singular = false;
+  for (int c = 0; c + 1 < n; c += 2) {
+    unsigned long long k = 0;
+    int row = 0x7fffffff;
+    // |S[r, c]| = |S[c, r]|: the candidates read along row c
+    for (int r = c + 1 + threadIdx.x; r < n; r += NT) take_better(k, row, key64(M[(size_t)c * n + r]), r);
+    const int p = block_argmax<NT>(k, row, redk[(c >> 1) & 1], redr[(c >> 1) & 1]);
+    const int q = c + 1;
+    if (p != q) {  // swap rows p, q over columns >= c, then columns p, q over rows >= c
+      sgn = -sgn;
+      for (int x = c + threadIdx.x; x < n; x += NT) {
+        const double u = M[(size_t)p * n + x], v = M[(size_t)q * n + x];
+        M[(size_t)p * n + x] = v;
+        M[(size_t)q * n + x] = u;
+      }
+      __syncthreads();
+      for (int x = c + threadIdx.x; x < n; x += NT) {
+        const double u = M[(size_t)x * n + p], v = M[(size_t)x * n + q];
+        M[(size_t)x * n + p] = v;
+        M[(size_t)x * n + q] = u;
+      }
+      __syncthreads();
+    }
+    const double d = M[(size_t)c * n + q];
+    if (d == 0.0) {
+      singular = true;
+      break;
+    }
+    logabs += log(fabs(d));
+    if (d < 0.0) sgn = -sgn;
+    const double rd = 1.0 / d;
+    // tau = -S[:, c] / d = S[c, :] / d, w = S[:, q] = -S[q, :] (rows c and q contiguous)
+    const double* Rc = M + (size_t)c * n;
+    const double* Rq = M + (size_t)q * n;
+    for (int r = q + 1 + wave; r < n; r += NT / 64) {
+      double* R = M + (size_t)r * n;
+      const double tr = Rc[r] * rd, wr = -Rq[r];
+      for (int x = q + 1 + lane; x < n; x += 64) {
+#pragma clang fp contract(off)
+        const double t = tr * (-Rq[x]) - wr * (Rc[x] * rd);
+        R[x] = R[x] + t;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    sign_out[b] = singular ? 0.0 : sgn;
+    logabs_out[b] = singular ? -INFINITY : logabs;
+  }
+}
+
+bool f64_in_lds(int n, int ld) { return (size_t)n * ld * sizeof(double) <= F64_LDS_MAX; }
+
+size_t f64_matrix_ws(int64_t batch, int n, int ld) {
+  if (batch <= 0 || n <= 0 || f64_in_lds(n, ld)) return 0;
+  return (size_t)batch * n * ld * sizeof(double);
+}
+
+size_t f64_lds_bytes(int n, int ld, bool lds, bool maps) {
+  size_t bytes = lds ? (size_t)n * ld * sizeof(double) : 0;
+  if (maps) bytes += (size_t)n * sizeof(int) + ((n + 15) / 16) * 16;
+  return bytes ? bytes : 16;
+}
+
+int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, double* logabs, double* out,
+                int out_t, const double* gate, void* ws, size_t ws_bytes, hipStream_t s) {
+  const bool inv = out != nullptr;
+  const int ld = inv ? 2 * n : n;
+  const bool lds = f64_in_lds(n, ld);
+  if (!lds && (!ws || ws_bytes < f64_matrix_ws(batch, n, ld))) return FX_ERR_WORKSPACE;
+  const size_t shm = f64_lds_bytes(n, ld, lds, true);
+  const dim3 grid((unsigned)batch);
+  double* W = (double*)ws;
+  if (n <= 128) {
+    if (inv)
+      gj64_kernel<256, true><<<grid, 256, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
+    else
+      gj64_kernel<256, false><<<grid, 256, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
+  } else {
+    if (inv)
+      gj64_kernel<1024, true><<<grid, 1024, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
+    else
+      gj64_kernel<1024, false><<<grid, 1024, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
+  }
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
+                size_t ws_bytes, hipStream_t s) {
+  const bool lds = f64_in_lds(n, n);
+  if (!lds && (!ws || ws_bytes < f64_matrix_ws(batch, n, n))) return FX_ERR_WORKSPACE;
+  const size_t shm = f64_lds_bytes(n, n, lds, false);
+  const dim3 grid((unsigned)batch);
+  if (n <= 128)
+    pr64_kernel<256><<<grid, 256, shm, s>>>(a, n, skew, (double*)ws, lds, sign, logabs);
+  else
+    pr64_kernel<1024><<<grid, 1024, shm, s>>>(a, n, skew, (double*)ws, lds, sign, logabs);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+int check_f64_args(const void* a, int64_t batch, int n, const void* sign, const void* logabs) {
+  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (n > F64_MAXN) return FX_ERR_UNSUPPORTED;
+  if (batch > 0 && (!sign || !logabs || (n > 0 && !a))) return FX_ERR_INVALID_ARGUMENT;
+  if (batch > 0x7fffffff) return FX_ERR_UNSUPPORTED;
+  return FX_OK;
+}
+
+}  // namespace
+}  // namespace fx
+
+using namespace fx;
+
+extern "C" {
+
+size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n) {
+  return n > F64_MAXN ? 0 : f64_matrix_ws(batch, n, n);
+}
+
+int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
+                   size_t workspace_bytes, fx_stream_t stream) {
+  const int st = check_f64_args(a, batch, n, sign, logabs);
+  if (st != FX_OK || batch == 0) return st;
+  return launch_gj64(a, n, 0, batch, sign, logabs, nullptr, 0, nullptr, workspace, workspace_bytes,
+                     (hipStream_t)stream);
+}
+
+size_t fx_slogdet_parts_f64_workspace(int64_t batch, int32_t n) {
+  return n > F64_MAXN ? 0 : f64_matrix_ws(batch, n, 2 * n);
+}
+
+int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
+                         void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  const int st = check_f64_args(a, batch, n, sign, logabs);
+  if (st != FX_OK || batch == 0) return st;
+  if (!inv_t) return fx_slogdet_f64(a, batch, n, sign, logabs, workspace, workspace_bytes, stream);
+  return launch_gj64(a, n, 0, batch, sign, logabs, inv_t, 1, nullptr, workspace, workspace_bytes,
+                     (hipStream_t)stream);
+}
+
+size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n) {
+  return n > F64_MAXN ? 0 : f64_matrix_ws(batch, n, n);
+}
+
+int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign, double* logabs,
+                  void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  const int st = check_f64_args(a, batch, n, sign, logabs);
+  if (st != FX_OK || batch == 0) return st;
+  return launch_pr64(a, n, skew_symmetrize != 0, batch, sign, logabs, workspace, workspace_bytes,
+                     (hipStream_t)stream);
+}
+
+size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n) {
+  if (n > F64_MAXN || batch <= 0) return 0;
+  const size_t pr = f64_matrix_ws(batch, n, n), gj = f64_matrix_ws(batch, n, 2 * n);
+  return align_up_256(pr) + align_up_256(gj) + align_up_256((size_t)batch * 2 * sizeof(double));
+}
+
+int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
+                        double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
+                        fx_stream_t stream) {
+  int st = check_f64_args(a, batch, n, sign, logabs);
+  if (st != FX_OK || batch == 0) return st;
+  if (adjugate) return FX_ERR_UNSUPPORTED;
+  hipStream_t s = (hipStream_t)stream;
+  if (!g) return fx_slogpf_f64(a, batch, n, skew_symmetrize, sign, logabs, workspace, workspace_bytes, stream);
+  if (workspace_bytes < fx_slogpf_parts_f64_workspace(batch, n) || !workspace) return FX_ERR_WORKSPACE;
+  const size_t pr = align_up_256(f64_matrix_ws(batch, n, n));
+  const size_t gj = align_up_256(f64_matrix_ws(batch, n, 2 * n));
+  char* base = (char*)workspace;
+  st = launch_pr64(a, n, skew_symmetrize != 0, batch, sign, logabs, base, pr, s);
+  if (st != FX_OK || n == 0) return st;
+  // S^-1 by Gauss-Jordan on the same S, zeroed where the Parlett-Reid run found pf = 0
+  // (every member for odd n)
+  double* gsign = (double*)(base + pr + gj);
+  double* glog = gsign + batch;
+  return launch_gj64(a, n, skew_symmetrize != 0, batch, gsign, glog, g, 0, sign, base + pr, gj, s);
+}
+
+}  // extern "C"

@@ -1,4 +1,4 @@
-/* fermix_amd C ABI: batched fp32 slogdet / slogpf (and the factors and inverses their
+/* fermix_amd C ABI: batched fp32 (and fp64) slogdet / slogpf (and the factors and inverses their
  * gradients need) on AMD Instinct MI355X (gfx950), as hand-written HIP kernels.
  *
  * This is the drop-in boundary for the hot path of ChenAo-Phys/fermix: each entry
@@ -171,6 +171,39 @@ size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
                         int32_t adjugate, float* sign, float* logabs, float* g, void* workspace,
                         size_t workspace_bytes, fx_stream_t stream);
+
+/* ---------------------------------------------------------------- float64
+ * The reference takes float64 through the same API (`_prep`, src/fermix/api.py:24-31,
+ * with 64-bit fields, src/fermix/_field.py:20-120 and :265-275). These entry points are
+ * the float64 counterparts of the ones above, with the same argument meaning, outputs
+ * in float64 and 0 <= n <= 4096. Unblocked kernels, one workgroup per matrix: an LU /
+ * Gauss-Jordan with partial pivoting (`_slogdet_generic`, `_lu_parts_generic`,
+ * src/fermix/_fallback.py:36-97) and Parlett-Reid (`_slogpf_generic`, :266-300). The
+ * workspace is 0 where the matrix fits in LDS (n <= 87 for the forward, n <= 61 with the
+ * inverse), else one matrix copy per member (twice that with the inverse). The kernel
+ * family override FERMIX_AMD_KERNELS does not apply to them. */
+size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n);
+int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
+                   size_t workspace_bytes, fx_stream_t stream);
+
+/* sign / logabs bit-identical to fx_slogdet_f64, plus inv_t (batch, n, n) = A^-T (NULL to
+ * skip), zero for members with an exactly zero pivot or a non-finite inverse (the
+ * zero_singular = 1 convention of fx_slogdet_parts_f32). */
+size_t fx_slogdet_parts_f64_workspace(int64_t batch, int32_t n);
+int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
+                         void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n);
+int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign, double* logabs,
+                  void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* sign / logabs bit-identical to fx_slogpf_f64, plus g (batch, n, n) = S^-1 (NULL to
+ * skip), zero where pf(S) = 0 (odd n, an exactly zero pivot) or S^-1 is not finite.
+ * adjugate != 0 (the Pfaffian adjugate) returns FX_ERR_UNSUPPORTED for float64. */
+size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n);
+int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
+                        double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
+                        fx_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -86,6 +86,16 @@ def test_api_errors():
         fermix_amd.slogdet(A)
     with pytest.raises(fermix_amd.FermixDeviceError):
         fermix_amd.slogpf(A)
+    # float64 is a supported dtype (device check next); tf32x3 is float32-only
+    # (reference src/fermix/_field.py:265-275); complex is not built
+    with pytest.raises(fermix_amd.FermixDeviceError):
+        fermix_amd.slogdet(A.double())
+    with pytest.raises(ValueError):
+        fermix_amd.slogdet(A.double(), prec="tf32x3")
+    with pytest.raises(ValueError):
+        fermix_amd.pf(A.double(), prec="tf32x3")
+    with pytest.raises(TypeError):
+        fermix_amd.slogdet(A.to(torch.complex64))
 
 
 def test_tune_table():

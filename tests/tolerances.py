@@ -77,3 +77,36 @@ def assert_grad(G, ref, A, what=""):
     if bad.any():
         k = kappa(np.asarray(A)[bad])
         assert np.all(err[bad] <= KAPPA_C * U32 * k), (what, err[bad], k)
+
+
+# float64 (the f64 entry points): the same contract scaled to double precision --
+# logabs within 1e-12 max(1, |ref|) + 1e-13 n, gradients within 1e-10 relative
+# Frobenius error, each with the fallback KAPPA_C * 2^-53 * kappa(A).
+U64 = 2.0**-53
+
+
+def assert_logabs64(l, lref, n, what="", A=None):
+    l = np.asarray(l, np.float64)
+    lref = np.asarray(lref, np.float64)
+    fin = np.isfinite(lref)
+    assert np.array_equal(np.isneginf(l), np.isneginf(lref)), (what, l, lref)
+    err = np.abs(l[fin] - lref[fin])
+    tol = 1e-12 * np.maximum(1.0, np.abs(lref[fin])) + 1e-13 * n
+    bad = err > tol
+    if err.size:
+        print(f"[{what}] f64 n={n}: literal logabs pass {int((~bad).sum())}/{err.size}, "
+              f"max err/tol {float((err / tol).max()):.3g}", flush=True)
+    if bad.any():
+        assert A is not None, (what, float(err.max()))
+        lim = KAPPA_C * U64 * kappa(np.asarray(A)[fin][bad])
+        assert np.all(err[bad] <= lim), (what, err[bad], lim)
+
+
+def assert_grad64(G, ref, A, what=""):
+    err = rel_fro(G, ref)
+    bad = err > 1e-10
+    print(f"[{what}] f64 grad literal pass {int((~bad).sum())}/{err.size}, max rel-Fro {float(err.max()):.3g}",
+          flush=True)
+    if bad.any():
+        k = kappa(np.asarray(A)[bad])
+        assert np.all(err[bad] <= KAPPA_C * U64 * k), (what, err[bad], k)
