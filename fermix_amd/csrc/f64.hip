@@ -22,6 +22,7 @@
 //    stays exactly skew-symmetric and its diagonal exactly zero.
 // Both are latency-bound per matrix (a workgroup barrier per column / pair step); they
 // are a correct, device-resident float64 path, not tuned like the float32 families.
+#include "common.h"
 #include "fermix_internal.h"
 
 namespace fx {
@@ -172,6 +173,142 @@ __global__ __launch_bounds__(NT) void gj64_kernel(const double* __restrict__ a, 
   }
 }
 
+// n <= RW (64 or 128): the same Gauss-Jordan with the matrix in registers. Thread t owns
+// row r = t % RW, columns [q NC, q NC + NC) of [A | I] (q = t / RW, CH chunks); per column
+// j the chunk holding column j posts its values (the multipliers' sources and the pivot
+// candidates) and, after the pivot is known, the pivot row's owners post that row: two
+// workgroup barriers per column, every element updated by its owner with the formula of
+// gj64_kernel (fma(-l, P[c], M[r, c]), l = M[r, j] * rinv), so sign / logabs equal its
+// bits, and the forward (INV = false) and the inverse (INV = true) agree bit for bit.
+template <int RW, int NC, int CH, bool INV>
+__global__ __launch_bounds__(RW* CH) void gjreg64_kernel(const double* __restrict__ a, int n, int skew,
+                                                         double* __restrict__ sign_out,
+                                                         double* __restrict__ logabs_out, double* __restrict__ out,
+                                                         int out_t, const double* __restrict__ gate) {
+  constexpr int NW = RW / 64;
+  __shared__ double colj[2][RW];
+  __shared__ double prowv[2][NC * CH];
+  __shared__ unsigned long long redk[2][NW];
+  __shared__ int redr[2][NW];
+  __shared__ int pidx[RW];      // pivot row of column j
+  __shared__ int pos[RW];       // column whose pivot row is r
+  __shared__ double pivs[RW];   // pivot of column j
+  const int t = threadIdx.x, r = t % RW, q = t / RW;
+  const int64_t b = blockIdx.x;
+  const double* A = a + (size_t)b * n * n;
+
+  double M[NC];
+  static_for<0, NC>([&](auto I) {
+    const int c = q * NC + I.value;
+    double v = 0.0;
+    if (r < n) {
+      if (c < n) {
+        v = A[(size_t)r * n + c];
+        if (skew) v = (v - A[(size_t)c * n + r]) * 0.5;
+      } else if (INV && c < 2 * n) {
+        v = (c - n == r) ? 1.0 : 0.0;
+      }
+    }
+    M[I.value] = v;
+  });
+
+  bool asg = false, singular = false;
+  double logabs = 0.0, sgn = 1.0;
+  for (int j = 0; j < n; ++j) {
+    const int buf = j & 1, qj = j / NC, ij = j - qj * NC;
+    if (q == qj) {
+      double v = 0.0;
+      static_for<0, NC>([&](auto I) {
+        if (I.value == ij) v = M[I.value];
+      });
+      // exact wave argmax of the 64-bit keys: the high words' maximum, then the low
+      // words' maximum among the lanes holding it (DPP reductions), then the lowest such
+      // lane (a ballot; lanes are consecutive rows)
+      const unsigned long long k = (r < n && !asg) ? key64(v) : 0ull;
+      const unsigned hi = (unsigned)(k >> 32), lo = (unsigned)k;
+      const unsigned mh = wave_max_u32(hi);
+      const unsigned ml = wave_max_u32(hi == mh ? lo : 0u);
+      const unsigned long long win = __ballot(hi == mh && lo == ml);
+      if ((r & 63) == 0) {
+        redk[buf][r >> 6] = ((unsigned long long)mh << 32) | ml;
+        redr[buf][r >> 6] = r + __ffsll((long long)win) - 1;
+      }
+      colj[buf][r] = v;
+    }
+    __syncthreads();
+    unsigned long long k = redk[buf][0];
+    int p = redr[buf][0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) take_better(k, p, redk[buf][i], redr[buf][i]);
+    const double piv = colj[buf][p];
+    double rinv = 0.0;  // the logs of the pivots are taken after the loop
+    if (piv == 0.0) {
+      singular = true;
+    } else {
+      rinv = 1.0 / piv;
+      if (piv < 0.0) sgn = -sgn;
+    }
+    if (r == p) static_for<0, NC>([&](auto I) { prowv[buf][q * NC + I.value] = M[I.value]; });
+    if (t == 0) {
+      pidx[j] = p;
+      pivs[j] = piv;
+    }
+    __syncthreads();
+    if (r < n && r != p && (INV || !asg)) {
+      const double l = colj[buf][r] * rinv;
+      static_for<0, NC>([&](auto I) {
+        const int c = q * NC + I.value;
+        if (c > j) M[I.value] = fma(-l, prowv[buf][c], M[I.value]);
+      });
+    }
+    if (r == p) asg = true;
+  }
+
+  // log|pivot_j| in parallel into colj[0] (free after the loop), summed in order by
+  // thread 0 (sequential pivot order, as the reference's running logabs)
+  __syncthreads();
+  double* lg = colj[0];
+  for (int j = t; j < n; j += RW * CH) lg[j] = log(fabs(pivs[j]));
+  __syncthreads();
+  if (t == 0) {  // parity of j -> pidx[j]; pos doubles as the visit marks first
+    if (!singular)
+      for (int j = 0; j < n; ++j) logabs += lg[j];
+    for (int s = 0; s < n; ++s) pos[s] = 0;
+    int cycles = 0;
+    for (int s = 0; s < n; ++s) {
+      if (pos[s]) continue;
+      ++cycles;
+      for (int u = s; !pos[u]; u = pidx[u]) pos[u] = 1;
+    }
+    if ((n - cycles) & 1) sgn = -sgn;
+    sign_out[b] = singular ? 0.0 : sgn;
+    logabs_out[b] = singular ? -INFINITY : logabs;
+  }
+  if constexpr (INV) {
+    __syncthreads();
+    for (int j = t; j < n; j += RW * CH) pos[pidx[j]] = j;
+    __syncthreads();
+    double* O = out + (size_t)b * n * n;
+    const bool zero = singular || (gate && gate[b] == 0.0);
+    bool bad = false;
+    if (!zero && r < n) {
+      // row r of the right block is row pos[r] of A^-1 times its pivot
+      const int j = pos[r];
+      const double pj = pivs[j];
+      static_for<0, NC>([&](auto I) {
+        const int c = q * NC + I.value - n;
+        if (c >= 0 && c < n) {
+          const double v = M[I.value] / pj;
+          bad |= !isfinite(v);
+          O[out_t ? (size_t)c * n + j : (size_t)j * n + c] = v;
+        }
+      });
+    }
+    if (zero || __syncthreads_or(bad))
+      for (int e = t; e < n * n; e += RW * CH) O[e] = 0.0;
+  }
+}
+
 template <int NT>
 __global__ __launch_bounds__(NT) void pr64_kernel(const double* __restrict__ a, int n, int skew, double* Wg,
                                                  int use_lds, double* __restrict__ sign_out,
@@ -262,6 +399,21 @@ int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, d
                 int out_t, const double* gate, void* ws, size_t ws_bytes, hipStream_t s) {
   const bool inv = out != nullptr;
   const int ld = inv ? 2 * n : n;
+  if (n <= 128) {  // register-resident
+    const dim3 grid((unsigned)batch);
+    if (n <= 64) {
+      if (inv)
+        gjreg64_kernel<64, 32, 4, true><<<grid, 256, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
+      else
+        gjreg64_kernel<64, 32, 2, false><<<grid, 128, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
+    } else {
+      if (inv)
+        gjreg64_kernel<128, 32, 8, true><<<grid, 1024, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
+      else
+        gjreg64_kernel<128, 32, 4, false><<<grid, 512, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
+    }
+    return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+  }
   const bool lds = f64_in_lds(n, ld);
   if (!lds && (!ws || ws_bytes < f64_matrix_ws(batch, n, ld))) return FX_ERR_WORKSPACE;
   const size_t shm = f64_lds_bytes(n, ld, lds, true);
@@ -309,8 +461,13 @@ using namespace fx;
 
 extern "C" {
 
+// Workspace of the Gauss-Jordan path: none in registers (n <= 128) or LDS.
+size_t gj64_ws(int64_t batch, int n, bool inv) {
+  return n <= 128 ? 0 : f64_matrix_ws(batch, n, inv ? 2 * n : n);
+}
+
 size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n) {
-  return n > F64_MAXN ? 0 : f64_matrix_ws(batch, n, n);
+  return n > F64_MAXN ? 0 : gj64_ws(batch, n, false);
 }
 
 int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
@@ -322,7 +479,7 @@ int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, doub
 }
 
 size_t fx_slogdet_parts_f64_workspace(int64_t batch, int32_t n) {
-  return n > F64_MAXN ? 0 : f64_matrix_ws(batch, n, 2 * n);
+  return n > F64_MAXN ? 0 : gj64_ws(batch, n, true);
 }
 
 int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
@@ -348,7 +505,7 @@ int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmet
 
 size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n) {
   if (n > F64_MAXN || batch <= 0) return 0;
-  const size_t pr = f64_matrix_ws(batch, n, n), gj = f64_matrix_ws(batch, n, 2 * n);
+  const size_t pr = f64_matrix_ws(batch, n, n), gj = gj64_ws(batch, n, true);
   return align_up_256(pr) + align_up_256(gj) + align_up_256((size_t)batch * 2 * sizeof(double));
 }
 
@@ -362,7 +519,7 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
   if (!g) return fx_slogpf_f64(a, batch, n, skew_symmetrize, sign, logabs, workspace, workspace_bytes, stream);
   if (workspace_bytes < fx_slogpf_parts_f64_workspace(batch, n) || !workspace) return FX_ERR_WORKSPACE;
   const size_t pr = align_up_256(f64_matrix_ws(batch, n, n));
-  const size_t gj = align_up_256(f64_matrix_ws(batch, n, 2 * n));
+  const size_t gj = align_up_256(gj64_ws(batch, n, true));
   char* base = (char*)workspace;
   st = launch_pr64(a, n, skew_symmetrize != 0, batch, sign, logabs, base, pr, s);
   if (st != FX_OK || n == 0) return st;
