@@ -9,19 +9,23 @@
 // :63-97) and Parlett-Reid with the pivot swapped into column c + 1 and the rank-2
 // update tau w^T - w tau^T (`_slogpf_generic`, :266-300).
 //
-// Kernels (each a single workgroup per matrix; the matrix in LDS when it fits in 60 KiB,
-// else in a per-matrix slice of the workspace, where its rows stay in L2):
-//  - gj64_kernel<NT, INV>: Gauss-Jordan with virtual partial pivoting (the pivot row of
-//    column j is the unassigned row of largest |x|, lowest row index on ties). Without
-//    INV only the unassigned rows are updated (an LU); with INV the assigned rows and an
-//    identity block [A | I] are eliminated too, and row j of A^-1 is row prow[j] of the
-//    right block over pivot j. The unassigned rows see the same operations in both modes,
-//    so sign / logabs of the gradient call are bit-identical to the forward.
-//  - pr64_kernel<NT>: Parlett-Reid on the full matrix with physical row / column swaps;
-//    the update adds round(tau_r w_k) - round(w_r tau_k) (no contraction), so the matrix
-//    stays exactly skew-symmetric and its diagonal exactly zero.
-// Both are latency-bound per matrix (a workgroup barrier per column / pair step); they
-// are a correct, device-resident float64 path, not tuned like the float32 families.
+// Kernels (each a single workgroup per matrix):
+//  - n <= 128, gjreg64_kernel<RW, NC, CH, INV> / pfreg64_kernel<RW, NC, CH>: the matrix in
+//    registers, each thread a 32-column strip of one row; per column (pair) step the
+//    owners post the pivot candidates and the pivot row(s) through LDS, two barriers;
+//  - n > 128, gj64_kernel<NT, INV> / pr64_kernel<NT>: the matrix in LDS when it fits in
+//    60 KiB, else in a per-matrix slice of the workspace (rows served from L2).
+// Gauss-Jordan (gj*): virtual partial pivoting (the pivot row of column j is the
+// unassigned row of largest |x|, lowest row index on ties). Without INV only the
+// unassigned rows are updated (an LU); with INV the assigned rows and an identity block
+// [A | I] are eliminated too, and row j of A^-1 is row prow[j] of the right block over
+// pivot j. Every element update is fma(-l, P[c], M[r, c]), l = M[r, j] * (1 / pivot), in
+// both modes, so sign / logabs of the gradient call are bit-identical to the forward.
+// Parlett-Reid (p*): pr64_kernel swaps the pivot row / column into position c + 1 as
+// the reference's generic path does; pfreg64_kernel pivots virtually (pair a = the lowest
+// unassigned index, p = argmax |S[p, a]|; pf = sgn(pi) prod d_k). Both add
+// round(tau_r w_x) - round(w_r tau_x) (no contraction), so the matrix stays exactly
+// skew-symmetric. All four are latency-bound per matrix (barriers per column step).
 #include "common.h"
 #include "fermix_internal.h"
 
@@ -309,6 +313,135 @@ __global__ __launch_bounds__(RW* CH) void gjreg64_kernel(const double* __restric
   }
 }
 
+// Exact wave argmax of 64-bit keys over the 64 lanes of a wave whose lanes hold the
+// consecutive rows r0 .. r0 + 63: the high words' maximum, then the low words' maximum
+// among the lanes holding it (DPP reductions), then the lowest such lane (ballot).
+__device__ __forceinline__ void wave_argmax64(unsigned long long k, int r0, unsigned long long& kout, int& rout) {
+  const unsigned hi = (unsigned)(k >> 32), lo = (unsigned)k;
+  const unsigned mh = wave_max_u32(hi);
+  const unsigned ml = wave_max_u32(hi == mh ? lo : 0u);
+  const unsigned long long win = __ballot(hi == mh && lo == ml);
+  kout = ((unsigned long long)mh << 32) | ml;
+  rout = r0 + __ffsll((long long)win) - 1;
+}
+
+// Even n <= RW: Parlett-Reid with the matrix in registers (layout of gjreg64_kernel) and
+// virtual pivoting: pair step k takes a = the lowest unassigned index and p = the
+// unassigned row != a of largest |S[p, a]| (lowest index on ties); rows a and p are
+// posted, d = S[a, p], and every unassigned row r adds
+// round(tau_r w_x) - round(w_r tau_x) (tau = S[a, :] / d, w = -S[p, :], no contraction)
+// to its entries, so the unassigned block stays exactly skew. pf(S) = sgn(pi) prod d_k
+// for pi = (a_0, p_0, a_1, p_1, ...).
+template <int RW, int NC, int CH>
+__global__ __launch_bounds__(RW* CH) void pfreg64_kernel(const double* __restrict__ a, int n, int skew,
+                                                         double* __restrict__ sign_out,
+                                                         double* __restrict__ logabs_out) {
+  constexpr int NW = RW / 64;
+  __shared__ double rowa[2][NC * CH];
+  __shared__ double rowp[2][NC * CH];
+  __shared__ unsigned long long redk[2][NW];
+  __shared__ int redr[2][NW];
+  __shared__ int perm[RW];
+  __shared__ double dv[RW / 2];
+  const int t = threadIdx.x, r = t % RW, q = t / RW;
+  const int64_t b = blockIdx.x;
+  if (n & 1) {
+    if (t == 0) {
+      sign_out[b] = 0.0;
+      logabs_out[b] = -INFINITY;
+    }
+    return;
+  }
+  const double* A = a + (size_t)b * n * n;
+  double M[NC];
+  static_for<0, NC>([&](auto I) {
+    const int c = q * NC + I.value;
+    double v = 0.0;
+    if (r < n && c < n) {
+      v = A[(size_t)r * n + c];
+      if (skew) v = (v - A[(size_t)c * n + r]) * 0.5;
+    }
+    M[I.value] = v;
+  });
+
+  unsigned long long used0 = 0, used1 = 0;  // assigned indices (uniform)
+  bool asg = false, singular = false;
+  double sgn = 1.0;
+  int steps = 0;
+  for (int k = 0; 2 * k < n; ++k) {
+    const int buf = k & 1;
+    const int ai = ~used0 ? __ffsll((long long)~used0) - 1 : 64 + __ffsll((long long)~used1) - 1;
+    const int qa = ai / NC, ia = ai - qa * NC;
+    if (q == qa) {
+      double v = 0.0;
+      static_for<0, NC>([&](auto I) {
+        if (I.value == ia) v = M[I.value];
+      });
+      unsigned long long kw;
+      int rw;
+      wave_argmax64((r < n && !asg && r != ai) ? key64(v) : 0ull, r & ~63, kw, rw);
+      if ((r & 63) == 0) {
+        redk[buf][r >> 6] = kw;
+        redr[buf][r >> 6] = rw;
+      }
+    }
+    if (r == ai) static_for<0, NC>([&](auto I) { rowa[buf][q * NC + I.value] = M[I.value]; });
+    __syncthreads();
+    unsigned long long kk = redk[buf][0];
+    int p = redr[buf][0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) take_better(kk, p, redk[buf][i], redr[buf][i]);
+    if (r == p) static_for<0, NC>([&](auto I) { rowp[buf][q * NC + I.value] = M[I.value]; });
+    const double d = rowa[buf][p];
+    if (t == 0) {
+      perm[2 * k] = ai;
+      perm[2 * k + 1] = p;
+      dv[k] = d;
+    }
+    steps = k + 1;
+    if (d == 0.0) {
+      singular = true;
+      break;
+    }
+    if (d < 0.0) sgn = -sgn;
+    const double rd = 1.0 / d;
+    __syncthreads();
+    if (r < n && !asg && r != ai && r != p) {
+      const double tr = rowa[buf][r] * rd, wr = -rowp[buf][r];
+      static_for<0, NC>([&](auto I) {
+#pragma clang fp contract(off)
+        const int x = q * NC + I.value;
+        const double tt = tr * (-rowp[buf][x]) - wr * (rowa[buf][x] * rd);
+        M[I.value] = M[I.value] + tt;
+      });
+    }
+    if (r == ai || r == p) asg = true;
+    if (ai < 64) used0 |= 1ull << ai; else used1 |= 1ull << (ai - 64);
+    if (p < 64) used0 |= 1ull << p; else used1 |= 1ull << (p - 64);
+  }
+  __syncthreads();
+  if (t == 0) {
+    double logabs = 0.0;
+    if (!singular) {
+      for (int k = 0; k < steps; ++k) logabs += log(fabs(dv[k]));
+      // parity of i -> perm[i]: marks in the sign bit of a copy (perm values < n)
+      int cycles = 0;
+      for (int s = 0; s < n; ++s) {
+        if (perm[s] < 0) continue;
+        ++cycles;
+        for (int u = s; perm[u] >= 0;) {
+          const int nx = perm[u];
+          perm[u] = -1;
+          u = nx;
+        }
+      }
+      if ((n - cycles) & 1) sgn = -sgn;
+    }
+    sign_out[b] = singular ? 0.0 : sgn;
+    logabs_out[b] = singular ? -INFINITY : logabs;
+  }
+}
+
 template <int NT>
 __global__ __launch_bounds__(NT) void pr64_kernel(const double* __restrict__ a, int n, int skew, double* Wg,
                                                  int use_lds, double* __restrict__ sign_out,
@@ -435,6 +568,14 @@ int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, d
 
 int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
                 size_t ws_bytes, hipStream_t s) {
+  if (n <= 128) {  // register-resident
+    const dim3 grid((unsigned)batch);
+    if (n <= 64)
+      pfreg64_kernel<64, 32, 2><<<grid, 128, 0, s>>>(a, n, skew, sign, logabs);
+    else
+      pfreg64_kernel<128, 32, 4><<<grid, 512, 0, s>>>(a, n, skew, sign, logabs);
+    return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+  }
   const bool lds = f64_in_lds(n, n);
   if (!lds && (!ws || ws_bytes < f64_matrix_ws(batch, n, n))) return FX_ERR_WORKSPACE;
   const size_t shm = f64_lds_bytes(n, n, lds, false);
@@ -492,7 +633,7 @@ int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign
 }
 
 size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n) {
-  return n > F64_MAXN ? 0 : f64_matrix_ws(batch, n, n);
+  return n > F64_MAXN || n <= 128 ? 0 : f64_matrix_ws(batch, n, n);
 }
 
 int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign, double* logabs,
@@ -505,7 +646,7 @@ int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmet
 
 size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n) {
   if (n > F64_MAXN || batch <= 0) return 0;
-  const size_t pr = f64_matrix_ws(batch, n, n), gj = gj64_ws(batch, n, true);
+  const size_t pr = fx_slogpf_f64_workspace(batch, n), gj = gj64_ws(batch, n, true);
   return align_up_256(pr) + align_up_256(gj) + align_up_256((size_t)batch * 2 * sizeof(double));
 }
 
@@ -518,7 +659,7 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
   hipStream_t s = (hipStream_t)stream;
   if (!g) return fx_slogpf_f64(a, batch, n, skew_symmetrize, sign, logabs, workspace, workspace_bytes, stream);
   if (workspace_bytes < fx_slogpf_parts_f64_workspace(batch, n) || !workspace) return FX_ERR_WORKSPACE;
-  const size_t pr = align_up_256(f64_matrix_ws(batch, n, n));
+  const size_t pr = align_up_256(fx_slogpf_f64_workspace(batch, n));
   const size_t gj = align_up_256(gj64_ws(batch, n, true));
   char* base = (char*)workspace;
   st = launch_pr64(a, n, skew_symmetrize != 0, batch, sign, logabs, base, pr, s);
