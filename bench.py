@@ -36,7 +36,8 @@ def _parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--only", default=None, help="comma list of workloads (c1,c2,c3,c4)")
+    p.add_argument("--only", default=None, help="comma list of workloads (c1,c2,c3,c4; f64 adds the float64 "
+                   "n = 128 workloads, reported on stderr)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
@@ -190,6 +191,35 @@ def cpu_library():
     return out
 
 
+def bench_f64(steps, warmup):
+    """float64 counterparts of the n = 128 workloads (B = 4096, the C1 / C2 inputs in
+    float64): slogpf and slogdet forward, and slogdet forward + gradient."""
+    import torch
+    import fermix_amd
+
+    B, n = 4096, 128
+    A64 = _inputs(B, n, 0).astype(np.float64)
+    A = torch.from_numpy(A64).cuda()
+    S = torch.from_numpy(A64 - np.swapaxes(A64, 1, 2)).cuda()
+    Ag = A.clone().requires_grad_()
+
+    def grad():
+        s, l = fermix_amd.slogdet(Ag)
+        (g,) = torch.autograd.grad(l.sum(), Ag)
+        return g
+
+    out = {}
+    for name, fn, nbytes in [
+        ("f64_slogpf_fwd", lambda: fermix_amd.slogpf(S, skew_symmetrize=False), 8 * n * n + 16),
+        ("f64_slogdet_fwd", lambda: fermix_amd.slogdet(A), 8 * n * n + 16),
+        ("f64_slogdet_fwd_grad", grad, 16 * n * n),
+    ]:
+        ms, wall = _time_gpu(fn, steps, warmup)
+        out[name] = dict(name=name, B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
+                         bytes=B * nbytes, sample=None)
+    return out
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -219,13 +249,19 @@ def main():
     if "c4" in only:
         res["c4"] = bench_c4(max(2, args.steps // 10), 1)
         print(f"# c4 slogpf fwd+grad: {res['c4']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
+    if "f64" in only:
+        for k, r in bench_f64(args.steps, args.warmup).items():
+            res[k] = r
+            print(f"# {k}: {r['ms']:.4f} ms/step ({r['rate']:.4g} matrices/s)", file=sys.stderr,
+                  flush=True)
     if args.copy_probe:
         x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda").fill_(1.0)
         for _ in range(3):
             y = x.clone()
         torch.cuda.synchronize()
         del x, y
-    head = res.get("c2") or res.get("c1") or res.get("c3") or res.get("c4")
+    head = (res.get("c2") or res.get("c1") or res.get("c3") or res.get("c4")
+            or res.get("f64_slogpf_fwd"))
     achieved = head["bytes"] / (head["ms"] * 1e-3) / 1e9
     roofline = {
         "bound": "hbm",
@@ -279,7 +315,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f64" if head["name"].startswith("f64") else "f32",
         "data": "synthetic (numpy default_rng(0) N(0,1); jax.random absent)",
         "config": {"workload": f"{head['name']} B={head['B']} n={head['n']}", "B": head["B"],
                    "n": head["n"], "baseline_config": "configs[1]" if head is res.get("c2") else "configs[0]"},
