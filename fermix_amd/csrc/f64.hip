@@ -11,7 +11,7 @@
 //
 // Kernels (each a single workgroup per matrix):
 //  - n <= 128, gjreg64_kernel<RW, NC, CH, INV> / pfreg64_kernel<RW, NC, CH>: the matrix in
-//    registers, each thread a 32-column strip of one row; per column (pair) step the
+//    registers, each thread a 16- or 32-column strip of one row; per column (pair) step the
 //    owners post the pivot candidates and the pivot row(s) through LDS, two barriers;
 //  - n > 128, gj64_kernel<NT, INV> / pr64_kernel<NT>: the matrix in LDS when it fits in
 //    60 KiB, else in a per-matrix slice of the workspace (rows served from L2).
@@ -538,7 +538,7 @@ int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, d
       if (inv)
         gjreg64_kernel<64, 32, 4, true><<<grid, 256, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
       else
-        gjreg64_kernel<64, 32, 2, false><<<grid, 128, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
+        gjreg64_kernel<64, 16, 4, false><<<grid, 256, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
     } else {
       if (inv)
         gjreg64_kernel<128, 32, 8, true><<<grid, 1024, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
