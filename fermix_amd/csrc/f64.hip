@@ -536,7 +536,7 @@ int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, d
     const dim3 grid((unsigned)batch);
     if (n <= 64) {
       if (inv)
-        gjreg64_kernel<64, 32, 4, true><<<grid, 256, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
+        gjreg64_kernel<64, 16, 8, true><<<grid, 512, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
       else
         gjreg64_kernel<64, 16, 4, false><<<grid, 256, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
     } else {
