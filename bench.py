@@ -14,8 +14,10 @@ is one pass of the hot path over one batch of synthetic input already resident i
 each matrix once, write sign and logabs) divided by its average launch duration over
 the timed region, timed with HIP events on the stream the kernel is launched on.
 `cpu_baseline` times the CPU oracle (the reference's generic path restated in numpy,
-oracle/generic.py) on a bounded sample of the same workload on this host, rank 0 only,
-with one BLAS thread.
+oracle/generic.py) on a bounded sample of the same workload on this host, rank 0 only:
+`value` with one BLAS thread, `value_all_cores` with one single-threaded process per
+host CPU (at most 16, the box's CPU share of one GPU), with the CPU model, CPU count and
+thread environment beside it. The CPU legs run before the GPU is initialised.
 """
 
 import argparse
@@ -86,16 +88,20 @@ def _inputs(B, n, seed, scale=1.0):
     return A
 
 
-def bench_c2(steps, warmup):
+def bench_c2(steps, warmup, skew_symmetrize=True):
+    """slogpf forward, B = 4096, n = 128, S = A - A^T. The headline calls the
+    API default (skew_symmetrize=True, fused into the kernel's load; (S - S^T) / 2 = S
+    bitwise here); skew_symmetrize=False is reported beside it."""
     import torch
     import fermix_amd
 
     B, n = 4096, 128
     A = _inputs(B, n, 0)
     S = torch.from_numpy(A - np.swapaxes(A, 1, 2)).cuda()
-    fn = lambda: fermix_amd.slogpf(S, skew_symmetrize=False)
+    fn = lambda: fermix_amd.slogpf(S, skew_symmetrize=skew_symmetrize)
     ms, wall = _time_gpu(fn, steps, warmup)
-    return dict(name="slogpf_fwd", B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
+    name = "slogpf_fwd" if skew_symmetrize else "slogpf_fwd_noskew"
+    return dict(name=name, B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
                 bytes=B * (4 * n * n + 8), sample=S[:64].cpu().numpy())
 
 
@@ -151,23 +157,64 @@ def bench_c4(steps, warmup):
                 bytes=B * 8 * n * n, flops=B * 1.0 * n ** 3, sample=None)
 
 
-def cpu_baseline(sample, which):
-    """The CPU oracle on a bounded sample, one thread (matrices/s)."""
-    from threadpoolctl import threadpool_limits
-
+def _oracle_fn(which):
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import generic as g
 
-    f = g.slogpf_generic if which == "slogpf" else g.slogdet_generic
+    return g.slogpf_generic if which == "slogpf" else g.slogdet_generic
+
+
+def _cpu_worker(args):
+    """One process of the all-core leg: the oracle on its slice for about `secs` seconds,
+    one BLAS thread; returns (matrices done, seconds)."""
+    sample, which, secs = args
+    from threadpoolctl import threadpool_limits
+
+    f = _oracle_fn(which)
     with threadpool_limits(limits=1):
-        f(sample[:4])
-        reps, t = 0, 0.0
-        t0 = time.perf_counter()
-        while t < 10.0:
+        f(sample[:1])
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < secs:
             f(sample)
-            reps += 1
-            t = time.perf_counter() - t0
-    return reps * sample.shape[0] / t, reps, t
+            done += sample.shape[0]
+    return done, time.perf_counter() - t0
+
+
+def cpu_baseline(sample, which, workers):
+    """The CPU oracle on a bounded sample: one thread (matrices/s), then `workers`
+    processes of one thread each over slices of the sample (the all-core figure)."""
+    from concurrent.futures import ProcessPoolExecutor
+
+    done, t = _cpu_worker((sample, which, 10.0))
+    one = done / t
+    reps = done // sample.shape[0]
+    allc = None
+    if workers > 1:
+        parts = [sample[i::workers] for i in range(workers)]
+        parts = [p for p in parts if p.shape[0]]
+        with ProcessPoolExecutor(len(parts)) as ex:
+            res = list(ex.map(_cpu_worker, [(p, which, 8.0) for p in parts]))
+        allc = sum(d for d, _ in res) / max(tt for _, tt in res)
+    return one, reps, t, allc
+
+
+def host_info():
+    """CPU model, logical CPU count and the thread environment of this host."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    env = {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS",
+                                          "XLA_FLAGS") if os.environ.get(k) is not None}
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = None
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": aff, "thread_env": env}
 
 
 def cpu_library():
@@ -230,24 +277,65 @@ def main():
             flush=True,
         )
         sys.exit(2)
+    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3", "c4"}
+    # The CPU legs run first, before anything initialises the GPU, so that the worker
+    # processes of the all-core leg fork from a process without GPU state.
+    cpu = None
+    lib = None
+    if not args.no_cpu and ("c2" in only or "c1" in only):
+        which = "slogpf" if "c2" in only else "slogdet"
+        A = _inputs(4096, 128, 0)[:64]
+        sample = A - np.swapaxes(A, 1, 2) if which == "slogpf" else A
+        info = host_info()
+        workers = min(16, info["affinity_cpus"] or info["os_cpu_count"] or 1)
+        rate, reps, t, allc = cpu_baseline(sample, which, workers)
+        cpu = {
+            "value": round(rate, 2),
+            "unit": "matrices/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"oracle {which}_generic (numpy restatement of the reference's generic "
+            f"path), the first {sample.shape[0]} of the 4096 n=128 matrices x "
+            f"{reps} reps in {t:.1f} s, one thread; value_all_cores: {workers} processes of one "
+            f"thread each over slices of the same sample for about 8 s",
+            "value_all_cores": round(allc, 2) if allc else None,
+            "cores_all": workers,
+            **info,
+        }
+        print(f"# cpu baseline ({which}): {rate:.1f} matrices/s one thread, "
+              f"{allc or 0:.1f} with {workers} processes", file=sys.stderr, flush=True)
+    if not args.no_cpu and "c1" in only:
+        rates = cpu_library()
+        t1, tn = sorted(rates)[0], sorted(rates)[-1]
+        lib = {
+            "value": round(rates[t1], 1),
+            "unit": "matrices/s",
+            "cores": t1,
+            "kind": "library",
+            "value_threads": {str(k): round(v, 1) for k, v in rates.items()},
+            "sample": f"numpy.linalg.slogdet (LAPACK getrf) on the full C1 batch (B = 4096, n = 128), "
+            f"{t1} and {tn} threads; compare workloads.c1",
+        }
     import torch
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm GPU visible"}), flush=True)
         sys.exit(1)
-    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3", "c4"}
     res = {}
     if "c2" in only:
         res["c2"] = bench_c2(args.steps, args.warmup)
         print(f"# c2 slogpf fwd: {res['c2']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
+        res["c2_noskew"] = bench_c2(args.steps, args.warmup, skew_symmetrize=False)
+        print(f"# c2 slogpf fwd (skew_symmetrize=False): {res['c2_noskew']['ms']:.4f} ms/step",
+              file=sys.stderr, flush=True)
     if "c1" in only:
         res["c1"] = bench_c1(args.steps, args.warmup)
         print(f"# c1 slogdet fwd: {res['c1']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
     if "c3" in only:
-        res["c3"] = bench_c3(max(3, args.steps // 4), max(1, args.warmup // 2))
+        res["c3"] = bench_c3(max(10, args.steps), max(2, args.warmup // 2))
         print(f"# c3 slogdet fwd+grad: {res['c3']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
     if "c4" in only:
-        res["c4"] = bench_c4(max(2, args.steps // 10), 1)
+        res["c4"] = bench_c4(max(10, args.steps // 2), 2)
         print(f"# c4 slogpf fwd+grad: {res['c4']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
     if "f64" in only:
         for k, r in bench_f64(args.steps, args.warmup).items():
@@ -271,32 +359,6 @@ def main():
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": _measured_traffic(head["name"]),
     }
-    cpu = None
-    if not args.no_cpu:
-        which = "slogpf" if head["name"].startswith("slogpf") else "slogdet"
-        rate, reps, t = cpu_baseline(head["sample"], which)
-        cpu = {
-            "value": round(rate, 2),
-            "unit": "matrices/s",
-            "cores": 1,
-            "kind": "port",
-            "sample": f"oracle {which}_generic (numpy restatement of the reference's generic "
-            f"path), {head['sample'].shape[0]} of the {head['B']} n={head['n']} matrices x "
-            f"{reps} reps in {t:.1f} s, one thread",
-        }
-    lib = None
-    if not args.no_cpu and "c1" in only:
-        rates = cpu_library()
-        t1, tn = sorted(rates)[0], sorted(rates)[-1]
-        lib = {
-            "value": round(rates[t1], 1),
-            "unit": "matrices/s",
-            "cores": t1,
-            "kind": "library",
-            "value_threads": {str(k): round(v, 1) for k, v in rates.items()},
-            "sample": f"numpy.linalg.slogdet (LAPACK getrf) on the full C1 batch (B = 4096, n = 128), "
-            f"{t1} and {tn} threads; compare workloads.c1",
-        }
     workloads = {
         k: {"workload": v["name"], "B": v["B"], "n": v["n"], "ms_per_step": round(v["ms"], 5),
             "matrices_per_s": round(v["rate"], 1),
@@ -318,7 +380,8 @@ def main():
         "dtype": "f64" if head["name"].startswith("f64") else "f32",
         "data": "synthetic (numpy default_rng(0) N(0,1); jax.random absent)",
         "config": {"workload": f"{head['name']} B={head['B']} n={head['n']}", "B": head["B"],
-                   "n": head["n"], "baseline_config": "configs[1]" if head is res.get("c2") else "configs[0]"},
+                   "n": head["n"], "skew_symmetrize": True if head is res.get("c2") else None,
+                   "baseline_config": "configs[1]" if head is res.get("c2") else "configs[0]"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "cpu_library": lib,

@@ -35,6 +35,12 @@ def _check_input(A, f64_ok=False):
     return A.dtype == torch.float64
 
 
+def _aligned(A):
+    """A itself when its data is 16-byte aligned (the C ABI's contract), else an aligned
+    copy: a view into a batch at an odd member offset of an odd-n batch is not."""
+    return A if A.data_ptr() % 16 == 0 else A.clone()
+
+
 def _no_f64(A, what):
     if A.dtype == torch.float64:
         raise NotImplementedError(
@@ -54,6 +60,7 @@ def pf_padded_size(n):
 def slogdet(A):
     """(sign, logabs) of each (n, n) matrix of A (B, n, n)."""
     f64 = _check_input(A, f64_ok=True)
+    A = _aligned(A)
     B, n, _ = A.shape
     sign = torch.empty(B, dtype=A.dtype, device=A.device)
     logabs = torch.empty(B, dtype=A.dtype, device=A.device)
@@ -74,6 +81,7 @@ def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False):
     lu / perm are padded to N = lu_padded_size(n). float64: invT only (zero for exactly
     singular members), no packed factors."""
     f64 = _check_input(A, f64_ok=True)
+    A = _aligned(A)
     B, n, _ = A.shape
     dev = A.device
     sign = torch.empty(B, dtype=A.dtype, device=dev)
@@ -108,6 +116,7 @@ def slogdet_factors(A):
     """(sign, logabs, lu (B, N, N), perm (B, N)): the packed LU of fx_slogdet_parts_f32
     alone, N = lu_padded_size(n)."""
     _check_input(A)
+    A = _aligned(A)
     B, n, _ = A.shape
     dev = A.device
     N = lu_padded_size(n) if n > 0 else 0
@@ -145,6 +154,7 @@ def det_parts(A):
     """(sign, logabs, adjT) with adjT = adj(A)^T = d det / dA from one factorisation."""
     _no_f64(A, "the det gradient (exact adjugate)")
     _check_input(A)
+    A = _aligned(A)
     B, n, _ = A.shape
     dev = A.device
     sign = torch.empty(B, dtype=A.dtype, device=dev)
@@ -161,6 +171,7 @@ def det_parts(A):
 
 def slogpf(A, skew_symmetrize):
     f64 = _check_input(A, f64_ok=True)
+    A = _aligned(A)
     B, n, _ = A.shape
     sign = torch.empty(B, dtype=A.dtype, device=A.device)
     logabs = torch.empty(B, dtype=A.dtype, device=A.device)
@@ -185,6 +196,7 @@ def slogpf(A, skew_symmetrize):
 def slogpf_factors(A, skew_symmetrize):
     """(sign, logabs, gbuf (B, N/PB, N, PB), d (B, N/2), perm (B, N))."""
     _check_input(A)
+    A = _aligned(A)
     B, n, _ = A.shape
     dev = A.device
     L = lib()
@@ -228,6 +240,7 @@ def slogpf_parts(A, skew_symmetrize, adjugate=False):
     if adjugate:
         _no_f64(A, "the pf gradient (Pfaffian adjugate)")
     f64 = _check_input(A, f64_ok=True)
+    A = _aligned(A)
     B, n, _ = A.shape
     dev = A.device
     L = lib()

@@ -26,6 +26,8 @@ HIP_FLAGS = [
     "-Xclang",
     "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # a variable read before it is set is a build error, not a warning
+    "-Werror=uninitialized",
 ]
 
 

@@ -100,6 +100,29 @@ static int family(int n, int tiny_max, int large_max) {
 static int lu_family(int n) { return family(n, TINY_MAXN, LARGE_MAX); }
 static int pf_family(int n) { return family(n, PF_TINY_MAXN, PF_LARGE_MAX); }
 
+// Alignment contract of the ABI: every matrix-shaped or workspace pointer is 16-byte
+// aligned (the kernels move rows as 16-byte vectors), per-member scalars (sign, logabs,
+// scale) 4-byte aligned. Checked before any work is enqueued.
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+static bool al4(const void* p) { return ((uintptr_t)p & 3) == 0; }
+
+// Batch chunking: several kernels put the batch on gridDim.y (at most 65535), so the
+// entry points that reach them run the batch in chunks of BATCH_CHUNK members (a multiple
+// of 8, which keeps the XCD-aware tile order and 16-byte alignment of every chunk's
+// slices), one after another on the stream, each reusing the same workspace. Workspace
+// sizes are those of one chunk.
+static constexpr int64_t BATCH_CHUNK = 65528;
+static int64_t chunk_batch(int64_t batch) { return batch < BATCH_CHUNK ? batch : BATCH_CHUNK; }
+
+template <class F>
+static int for_chunks(int64_t batch, F&& f) {
+  for (int64_t b0 = 0; b0 < batch; b0 += BATCH_CHUNK) {
+    const int st = f(b0, chunk_batch(batch - b0));
+    if (st != FX_OK) return st;
+  }
+  return FX_OK;
+}
+
 }  // namespace fx
 
 using namespace fx;
@@ -117,7 +140,7 @@ const char* fx_status_string(int status) {
   }
 }
 
-int fx_abi_version(void) { return 102; }
+int fx_abi_version(void) { return 103; }
 
 int32_t fx_lu_padded_size(int32_t n) {
   if (n <= 0) return 0;
@@ -139,7 +162,7 @@ int32_t fx_pf_block_columns(int32_t n) {
 
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || lu_family(n) != FAM_BLOCKED) return 0;
-  return lu_large_workspace(batch, n, false);
+  return lu_large_workspace(chunk_batch(batch), n, false);
 }
 
 int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs,
@@ -147,13 +170,17 @@ int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float*
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
+  if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(workspace)) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   switch (lu_family(n)) {
     case FAM_TINY: return launch_lu_tiny(a, n, batch, sign, logabs, nullptr, nullptr, s);
     case FAM_FUSED: return launch_lu_small(a, n, batch, sign, logabs, nullptr, nullptr, s);
     case FAM_BLOCKED:
-      return launch_lu_large(a, n, batch, sign, logabs, workspace, workspace_bytes, false, nullptr, nullptr, s);
+      return for_chunks(batch, [&](int64_t b0, int64_t nb) {
+        return launch_lu_large(a + b0 * n * n, n, nb, sign + b0, logabs + b0, workspace, workspace_bytes, false,
+                               nullptr, nullptr, s);
+      });
     default: return FX_ERR_UNSUPPORTED;
   }
 }
@@ -167,18 +194,23 @@ static int lu_fused_factors(int fam, const float* a, int n, int64_t batch, float
 
 static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n) {
-  const int fam = lu_family(n);
-  if (batch <= 0 || fam == FAM_NONE) return 0;
+// Workspace of one chunk of nb members of fx_slogdet_parts_f32.
+static size_t slogdet_parts_ws(int64_t nb, int n, int fam) {
   const int N = fx_lu_padded_size(n);
   const bool copy = inv_padded(N) != N;
   size_t bytes = 0;
   if (fam != FAM_BLOCKED) {
-    bytes += align256((size_t)batch * N * N * 4) + align256((size_t)batch * N * 4);
+    bytes += align256((size_t)nb * N * N * 4) + align256((size_t)nb * N * 4);
   } else {
-    bytes += align256(lu_large_workspace(batch, n, true));
+    bytes += align256(lu_large_workspace(nb, n, true));
   }
-  return bytes + lu_inverse_workspace(batch, N, copy);
+  return bytes + lu_inverse_workspace(nb, N, copy);
+}
+
+size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n) {
+  const int fam = lu_family(n);
+  if (batch <= 0 || fam == FAM_NONE) return 0;
+  return slogdet_parts_ws(chunk_batch(batch), n, fam);
 }
 
 int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_singular,
@@ -188,6 +220,8 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if ((lu == nullptr) != (perm == nullptr)) return FX_ERR_INVALID_ARGUMENT;
+  if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(inv_t) || !al16(lu) || !al16(perm) || !al16(workspace))
+    return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   const int fam = lu_family(n);
@@ -199,35 +233,40 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
   const size_t need = fx_slogdet_parts_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_lu_padded_size(n);
-  char* p = (char*)workspace;
-  float* LU = nullptr;
-  int* g0 = nullptr;
-  int st;
-  if (fam != FAM_BLOCKED) {
-    LU = (float*)p;
-    p += align256((size_t)batch * N * N * 4);
-    g0 = (int*)p;
-    p += align256((size_t)batch * N * 4);
-    st = lu_fused_factors(fam, a, n, batch, sign, logabs, LU, g0, s);
-  } else {
-    const size_t wl = lu_large_workspace(batch, n, true);
-    st = launch_lu_large(a, n, batch, sign, logabs, p, wl, true, &LU, &g0, s);
-    p += align256(wl);
-  }
-  if (st != FX_OK) return st;
-  if (lu) {
-    if (hipMemcpyAsync(lu, LU, (size_t)batch * N * N * 4, hipMemcpyDeviceToDevice, s) != hipSuccess ||
-        hipMemcpyAsync(perm, g0, (size_t)batch * N * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
-      return FX_ERR_LAUNCH;
-  }
-  if (!inv_t) return FX_OK;
-  const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
-  return launch_lu_inverse(LU, g0, N, n, batch, sign, zero_singular, inv_t, true, p, rest, s);
+  return for_chunks(batch, [&](int64_t b0, int64_t nb) {
+    const float* ab = a + b0 * n * n;
+    float* sg = sign + b0;
+    float* lg = logabs + b0;
+    char* p = (char*)workspace;
+    float* LU = nullptr;
+    int* g0 = nullptr;
+    int st;
+    if (fam != FAM_BLOCKED) {
+      LU = (float*)p;
+      p += align256((size_t)nb * N * N * 4);
+      g0 = (int*)p;
+      p += align256((size_t)nb * N * 4);
+      st = lu_fused_factors(fam, ab, n, nb, sg, lg, LU, g0, s);
+    } else {
+      const size_t wl = lu_large_workspace(nb, n, true);
+      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s);
+      p += align256(wl);
+    }
+    if (st != FX_OK) return st;
+    if (lu) {
+      if (hipMemcpyAsync(lu + b0 * N * N, LU, (size_t)nb * N * N * 4, hipMemcpyDeviceToDevice, s) != hipSuccess ||
+          hipMemcpyAsync(perm + b0 * N, g0, (size_t)nb * N * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
+        return FX_ERR_LAUNCH;
+    }
+    if (!inv_t) return FX_OK;
+    const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
+    return launch_lu_inverse(LU, g0, N, n, nb, sg, zero_singular, inv_t + b0 * n * n, true, p, rest, s);
+  });
 }
 
 size_t fx_slogdet_factors_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || lu_family(n) != FAM_BLOCKED) return 0;
-  return lu_large_workspace(batch, n, true, true);
+  return lu_large_workspace(chunk_batch(batch), n, true, true);
 }
 
 int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* lu,
@@ -235,19 +274,24 @@ int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && (!a || !lu || !perm))) return FX_ERR_INVALID_ARGUMENT;
+  if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(lu) || !al16(perm) || !al16(workspace))
+    return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   const int fam = lu_family(n);
   if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
   if (fam != FAM_BLOCKED) return lu_fused_factors(fam, a, n, batch, sign, logabs, lu, (int*)perm, s);
-  return launch_lu_large(a, n, batch, sign, logabs, workspace, workspace_bytes, true, nullptr, nullptr, s, lu,
-                         (int*)perm);
+  const int N = fx_lu_padded_size(n);
+  return for_chunks(batch, [&](int64_t b0, int64_t nb) {
+    return launch_lu_large(a + b0 * n * n, n, nb, sign + b0, logabs + b0, workspace, workspace_bytes, true, nullptr,
+                           nullptr, s, lu + b0 * N * N, (int*)perm + b0 * N);
+  });
 }
 
 size_t fx_slogdet_inverse_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || n <= 0 || lu_family(n) == FAM_NONE) return 0;
   const int N = fx_lu_padded_size(n);
-  return lu_inverse_workspace(batch, N, inv_padded(N) != N);
+  return lu_inverse_workspace(chunk_batch(batch), N, inv_padded(N) != N);
 }
 
 int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, const float* scale, int64_t batch,
@@ -256,16 +300,22 @@ int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, co
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0 || n == 0) return FX_OK;
   if (!lu || !perm || !sign || !inv_t) return FX_ERR_INVALID_ARGUMENT;
+  if (!al16(lu) || !al16(perm) || !al4(sign) || !al4(scale) || !al16(inv_t) || !al16(workspace))
+    return FX_ERR_INVALID_ARGUMENT;
   if (lu_family(n) == FAM_NONE) return FX_ERR_UNSUPPORTED;
   const size_t need = fx_slogdet_inverse_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
-  return launch_lu_inverse(lu, (const int*)perm, fx_lu_padded_size(n), n, batch, sign, zero_singular ? 1 : 0, inv_t,
-                           true, workspace, workspace_bytes, (hipStream_t)stream, scale);
+  const int N = fx_lu_padded_size(n);
+  return for_chunks(batch, [&](int64_t b0, int64_t nb) {
+    return launch_lu_inverse(lu + b0 * N * N, (const int*)perm + b0 * N, N, n, nb, sign + b0, zero_singular ? 1 : 0,
+                             inv_t + b0 * n * n, true, workspace, workspace_bytes, (hipStream_t)stream,
+                             scale ? scale + b0 : nullptr);
+  });
 }
 
 size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || lu_family(n) == FAM_NONE) return 0;
-  return fx_slogdet_parts_f32_workspace(batch, n) + align256(det_adjugate_workspace(batch, n));
+  return fx_slogdet_parts_f32_workspace(batch, n) + align256(det_adjugate_workspace(chunk_batch(batch), n));
 }
 
 int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
@@ -273,6 +323,7 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && (!a || !adj_t))) return FX_ERR_INVALID_ARGUMENT;
+  if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(adj_t) || !al16(workspace)) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   const int fam = lu_family(n);
@@ -280,37 +331,43 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
   const size_t need = fx_det_parts_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_lu_padded_size(n);
-  char* p = (char*)workspace;
-  float* LU = nullptr;
-  int* g0 = nullptr;
-  int st;
-  if (fam != FAM_BLOCKED) {
-    LU = (float*)p;
-    p += align256((size_t)batch * N * N * 4);
-    g0 = (int*)p;
-    p += align256((size_t)batch * N * 4);
-    st = lu_fused_factors(fam, a, n, batch, sign, logabs, LU, g0, s);
-  } else {
-    const size_t wl = lu_large_workspace(batch, n, true);
-    st = launch_lu_large(a, n, batch, sign, logabs, p, wl, true, &LU, &g0, s);
-    p += align256(wl);
-  }
-  if (st != FX_OK) return st;
-  // the adjugate's scalars and vectors come from the LU before the inverse overwrites it
-  void* dws = p;
-  p += align256(det_adjugate_workspace(batch, n));
-  float* scale = nullptr;
-  st = launch_det_adjugate_prep(LU, g0, N, n, batch, dws, &scale, s);
-  if (st != FX_OK) return st;
-  const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
-  st = launch_lu_inverse(LU, g0, N, n, batch, sign, 0, adj_t, true, p, rest, s, scale);
-  if (st != FX_OK) return st;
-  return launch_det_adjugate_finish(n, batch, dws, adj_t, s);
+  return for_chunks(batch, [&](int64_t b0, int64_t nb) {
+    const float* ab = a + b0 * n * n;
+    float* sg = sign + b0;
+    float* lg = logabs + b0;
+    float* adj = adj_t + b0 * n * n;
+    char* p = (char*)workspace;
+    float* LU = nullptr;
+    int* g0 = nullptr;
+    int st;
+    if (fam != FAM_BLOCKED) {
+      LU = (float*)p;
+      p += align256((size_t)nb * N * N * 4);
+      g0 = (int*)p;
+      p += align256((size_t)nb * N * 4);
+      st = lu_fused_factors(fam, ab, n, nb, sg, lg, LU, g0, s);
+    } else {
+      const size_t wl = lu_large_workspace(nb, n, true);
+      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s);
+      p += align256(wl);
+    }
+    if (st != FX_OK) return st;
+    // the adjugate's scalars and vectors come from the LU before the inverse overwrites it
+    void* dws = p;
+    p += align256(det_adjugate_workspace(nb, n));
+    float* scale = nullptr;
+    st = launch_det_adjugate_prep(LU, g0, N, n, nb, dws, &scale, s);
+    if (st != FX_OK) return st;
+    const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
+    st = launch_lu_inverse(LU, g0, N, n, nb, sg, 0, adj, true, p, rest, s, scale);
+    if (st != FX_OK) return st;
+    return launch_det_adjugate_finish(n, nb, dws, adj, s);
+  });
 }
 
 size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || n % 2 || pf_family(n) != FAM_BLOCKED) return 0;
-  return pf_large_workspace(batch, n, false);
+  return pf_large_workspace(chunk_batch(batch), n, false);
 }
 
 static int pf_fused(int fam, const float* a, int n, int sk, int64_t batch, float* sign, float* logabs, float* gbuf,
@@ -324,6 +381,7 @@ int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetr
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
+  if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(workspace)) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   if (n % 2 == 1) return fill2(sign, 0.0f, logabs, -INFINITY, batch, s);
@@ -331,12 +389,15 @@ int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetr
   const int fam = pf_family(n);
   if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
   if (fam != FAM_BLOCKED) return pf_fused(fam, a, n, sk, batch, sign, logabs, nullptr, nullptr, nullptr, s);
-  return launch_pf_large(a, n, sk, batch, sign, logabs, nullptr, nullptr, nullptr, workspace, workspace_bytes, s);
+  return for_chunks(batch, [&](int64_t b0, int64_t nb) {
+    return launch_pf_large(a + b0 * n * n, n, sk, nb, sign + b0, logabs + b0, nullptr, nullptr, nullptr, workspace,
+                           workspace_bytes, s);
+  });
 }
 
 size_t fx_slogpf_factors_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || n % 2 || pf_family(n) != FAM_BLOCKED) return 0;
-  return pf_large_workspace(batch, n, true);
+  return pf_large_workspace(chunk_batch(batch), n, true);
 }
 
 int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
@@ -345,18 +406,24 @@ int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || !gbuf || !d || !perm || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
+  if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(gbuf) || !al16(d) || !al16(perm) || !al16(workspace))
+    return FX_ERR_INVALID_ARGUMENT;
   if (n == 0 || n % 2 == 1) return FX_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
   const int sk = skew_symmetrize ? 1 : 0;
   const int fam = pf_family(n);
   if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
   if (fam != FAM_BLOCKED) return pf_fused(fam, a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, s);
-  return launch_pf_large(a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, workspace, workspace_bytes, s);
+  const int N = fx_pf_padded_size(n);
+  return for_chunks(batch, [&](int64_t b0, int64_t nb) {
+    return launch_pf_large(a + b0 * n * n, n, sk, nb, sign + b0, logabs + b0, gbuf + b0 * N * N, d + b0 * (N / 2),
+                           (int*)perm + b0 * N, workspace, workspace_bytes, s);
+  });
 }
 
 size_t fx_slogpf_inverse_f32_workspace(int64_t batch, int32_t n) {
   if (batch <= 0 || n <= 0 || n % 2 || pf_family(n) == FAM_NONE) return 0;
-  return pf_inverse_workspace(batch, fx_pf_padded_size(n));
+  return pf_inverse_workspace(chunk_batch(batch), fx_pf_padded_size(n));
 }
 
 int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm, const float* scale,
@@ -365,24 +432,34 @@ int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0 || n == 0) return FX_OK;
   if (!g) return FX_ERR_INVALID_ARGUMENT;
+  if (!al16(gbuf) || !al16(d) || !al16(perm) || !al4(scale) || !al16(g) || !al16(workspace))
+    return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n % 2 == 1) return fill(g, 0.0f, batch * (int64_t)n * n, s);
   if (!gbuf || !d || !perm) return FX_ERR_INVALID_ARGUMENT;
   if (pf_family(n) == FAM_NONE) return FX_ERR_UNSUPPORTED;
   const size_t need = fx_slogpf_inverse_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
-  return launch_pf_inverse(gbuf, fx_pf_block_columns(n), d, (const int*)perm, fx_pf_padded_size(n), n, batch,
-                           adjugate ? 1 : 0, g, workspace, workspace_bytes, s, scale);
+  const int N = fx_pf_padded_size(n);
+  return for_chunks(batch, [&](int64_t b0, int64_t nb) {
+    return launch_pf_inverse(gbuf + b0 * N * N, fx_pf_block_columns(n), d + b0 * (N / 2), (const int*)perm + b0 * N,
+                             N, n, nb, adjugate ? 1 : 0, g + b0 * n * n, workspace, workspace_bytes, s,
+                             scale ? scale + b0 : nullptr);
+  });
+}
+
+// Workspace of one chunk of nb members of fx_slogpf_parts_f32.
+static size_t slogpf_parts_ws(int64_t nb, int n, int fam) {
+  const int N = fx_pf_padded_size(n);
+  size_t bytes = align256((size_t)nb * N * N * 4) + align256((size_t)nb * N / 2 * 4) + align256((size_t)nb * N * 4);
+  if (fam == FAM_BLOCKED) bytes += align256(pf_large_workspace(nb, n, true));
+  return bytes + pf_inverse_workspace(nb, N);
 }
 
 size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n) {
   const int fam = pf_family(n);
   if (batch <= 0 || n % 2 || fam == FAM_NONE) return 0;
-  const int N = fx_pf_padded_size(n);
-  size_t bytes = align256((size_t)batch * N * N * 4) + align256((size_t)batch * N / 2 * 4) +
-                 align256((size_t)batch * N * 4);
-  if (fam == FAM_BLOCKED) bytes += align256(pf_large_workspace(batch, n, true));
-  return bytes + pf_inverse_workspace(batch, N);
+  return slogpf_parts_ws(chunk_batch(batch), n, fam);
 }
 
 int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
@@ -391,6 +468,7 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || !g || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
+  if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(g) || !al16(workspace)) return FX_ERR_INVALID_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   if (n % 2 == 1) {
@@ -403,25 +481,31 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
   const size_t need = fx_slogpf_parts_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_pf_padded_size(n);
-  char* p = (char*)workspace;
-  float* gbuf = (float*)p;
-  p += align256((size_t)batch * N * N * 4);
-  float* d = (float*)p;
-  p += align256((size_t)batch * N / 2 * 4);
-  int* perm = (int*)p;
-  p += align256((size_t)batch * N * 4);
   const int sk = skew_symmetrize ? 1 : 0;
-  int st;
-  if (fam != FAM_BLOCKED) {
-    st = pf_fused(fam, a, n, sk, batch, sign, logabs, gbuf, d, perm, s);
-  } else {
-    const size_t wl = pf_large_workspace(batch, n, true);
-    st = launch_pf_large(a, n, sk, batch, sign, logabs, gbuf, d, perm, p, wl, s);
-    p += align256(wl);
-  }
-  if (st != FX_OK) return st;
-  const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
-  return launch_pf_inverse(gbuf, fx_pf_block_columns(n), d, perm, N, n, batch, adjugate ? 1 : 0, g, p, rest, s);
+  return for_chunks(batch, [&](int64_t b0, int64_t nb) {
+    const float* ab = a + b0 * n * n;
+    float* sg = sign + b0;
+    float* lg = logabs + b0;
+    char* p = (char*)workspace;
+    float* gbuf = (float*)p;
+    p += align256((size_t)nb * N * N * 4);
+    float* d = (float*)p;
+    p += align256((size_t)nb * N / 2 * 4);
+    int* perm = (int*)p;
+    p += align256((size_t)nb * N * 4);
+    int st;
+    if (fam != FAM_BLOCKED) {
+      st = pf_fused(fam, ab, n, sk, nb, sg, lg, gbuf, d, perm, s);
+    } else {
+      const size_t wl = pf_large_workspace(nb, n, true);
+      st = launch_pf_large(ab, n, sk, nb, sg, lg, gbuf, d, perm, p, wl, s);
+      p += align256(wl);
+    }
+    if (st != FX_OK) return st;
+    const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
+    return launch_pf_inverse(gbuf, fx_pf_block_columns(n), d, perm, N, n, nb, adjugate ? 1 : 0, g + b0 * n * n, p,
+                             rest, s);
+  });
 }
 
 }  // extern "C"

@@ -552,17 +552,10 @@ int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, d
   const size_t shm = f64_lds_bytes(n, ld, lds, true);
   const dim3 grid((unsigned)batch);
   double* W = (double*)ws;
-  if (n <= 128) {
-    if (inv)
-      gj64_kernel<256, true><<<grid, 256, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
-    else
-      gj64_kernel<256, false><<<grid, 256, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
-  } else {
-    if (inv)
-      gj64_kernel<1024, true><<<grid, 1024, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
-    else
-      gj64_kernel<1024, false><<<grid, 1024, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
-  }
+  if (inv)
+    gj64_kernel<1024, true><<<grid, 1024, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
+  else
+    gj64_kernel<1024, false><<<grid, 1024, shm, s>>>(a, n, skew, W, lds, sign, logabs, out, out_t, gate);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
@@ -580,17 +573,24 @@ int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, d
   if (!lds && (!ws || ws_bytes < f64_matrix_ws(batch, n, n))) return FX_ERR_WORKSPACE;
   const size_t shm = f64_lds_bytes(n, n, lds, false);
   const dim3 grid((unsigned)batch);
-  if (n <= 128)
-    pr64_kernel<256><<<grid, 256, shm, s>>>(a, n, skew, (double*)ws, lds, sign, logabs);
-  else
-    pr64_kernel<1024><<<grid, 1024, shm, s>>>(a, n, skew, (double*)ws, lds, sign, logabs);
+  pr64_kernel<1024><<<grid, 1024, shm, s>>>(a, n, skew, (double*)ws, lds, sign, logabs);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
-int check_f64_args(const void* a, int64_t batch, int n, const void* sign, const void* logabs) {
+// Workspace of the Gauss-Jordan path: none in registers (n <= 128) or LDS.
+size_t gj64_ws(int64_t batch, int n, bool inv) {
+  return n <= 128 ? 0 : f64_matrix_ws(batch, n, inv ? 2 * n : n);
+}
+
+// Argument checks shared by the float64 entry points: the alignment contract of the ABI
+// (matrix-shaped and workspace pointers 16-byte aligned, sign / logabs 8-byte aligned).
+int check_f64_args(const void* a, int64_t batch, int n, const void* sign, const void* logabs, const void* out,
+                   const void* ws) {
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (n > F64_MAXN) return FX_ERR_UNSUPPORTED;
   if (batch > 0 && (!sign || !logabs || (n > 0 && !a))) return FX_ERR_INVALID_ARGUMENT;
+  auto mis = [](const void* p, uintptr_t m) { return ((uintptr_t)p & m) != 0; };
+  if (mis(a, 15) || mis(out, 15) || mis(ws, 15) || mis(sign, 7) || mis(logabs, 7)) return FX_ERR_INVALID_ARGUMENT;
   if (batch > 0x7fffffff) return FX_ERR_UNSUPPORTED;
   return FX_OK;
 }
@@ -602,10 +602,6 @@ using namespace fx;
 
 extern "C" {
 
-// Workspace of the Gauss-Jordan path: none in registers (n <= 128) or LDS.
-size_t gj64_ws(int64_t batch, int n, bool inv) {
-  return n <= 128 ? 0 : f64_matrix_ws(batch, n, inv ? 2 * n : n);
-}
 
 size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n) {
   return n > F64_MAXN ? 0 : gj64_ws(batch, n, false);
@@ -613,7 +609,7 @@ size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n) {
 
 int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream) {
-  const int st = check_f64_args(a, batch, n, sign, logabs);
+  const int st = check_f64_args(a, batch, n, sign, logabs, nullptr, workspace);
   if (st != FX_OK || batch == 0) return st;
   return launch_gj64(a, n, 0, batch, sign, logabs, nullptr, 0, nullptr, workspace, workspace_bytes,
                      (hipStream_t)stream);
@@ -625,7 +621,7 @@ size_t fx_slogdet_parts_f64_workspace(int64_t batch, int32_t n) {
 
 int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  const int st = check_f64_args(a, batch, n, sign, logabs);
+  const int st = check_f64_args(a, batch, n, sign, logabs, inv_t, workspace);
   if (st != FX_OK || batch == 0) return st;
   if (!inv_t) return fx_slogdet_f64(a, batch, n, sign, logabs, workspace, workspace_bytes, stream);
   return launch_gj64(a, n, 0, batch, sign, logabs, inv_t, 1, nullptr, workspace, workspace_bytes,
@@ -638,7 +634,7 @@ size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n) {
 
 int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign, double* logabs,
                   void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  const int st = check_f64_args(a, batch, n, sign, logabs);
+  const int st = check_f64_args(a, batch, n, sign, logabs, nullptr, workspace);
   if (st != FX_OK || batch == 0) return st;
   return launch_pr64(a, n, skew_symmetrize != 0, batch, sign, logabs, workspace, workspace_bytes,
                      (hipStream_t)stream);
@@ -653,7 +649,7 @@ size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n) {
 int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
                         fx_stream_t stream) {
-  int st = check_f64_args(a, batch, n, sign, logabs);
+  int st = check_f64_args(a, batch, n, sign, logabs, g, workspace);
   if (st != FX_OK || batch == 0) return st;
   if (adjugate) return FX_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;

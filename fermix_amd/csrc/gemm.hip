@@ -55,8 +55,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   // operand masks: MK = 4 maskA + maskB fixed at compile time (the combinations this
   // library uses), so each mask test folds to one compare per element; MK < 0 reads them
   // from the descriptor
-  const int maskA = MK >= 0 ? (MK >> 2) : maskA;
-  const int maskB = MK >= 0 ? (MK & 3) : maskB;
+  const int maskA = MK >= 0 ? (MK >> 2) : d.maskA;
+  const int maskB = MK >= 0 ? (MK & 3) : d.maskB;
   constexpr int LDSA = BM + 4, LDSB = BN + 4;
   constexpr int WM = BM / 2, WN = BN / 2;   // per-wave quarter
   constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 tiles per wave
@@ -401,8 +401,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
 // (accumulators included) without scratch, against 168 + 64 left to itself.
 template <bool TA, int MK, bool BS = false>
 __global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
-  const int maskA = MK >= 0 ? (MK >> 2) : maskA;  // compile-time masks as in gemm_kernel
-  const int maskB = MK >= 0 ? (MK & 3) : maskB;
+  const int maskA = MK >= 0 ? (MK >> 2) : d.maskA;  // compile-time masks as in gemm_kernel
+  const int maskB = MK >= 0 ? (MK & 3) : d.maskB;
   constexpr int BM = 128, BN = 128, LDA_ = BM + 4, LDB_ = BN + 4;
   __shared__ __align__(16) float As[2][GBK * LDA_];
   __shared__ __align__(16) float Bs[2][GBK * LDB_];

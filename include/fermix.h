@@ -14,6 +14,14 @@
  *    default stream);
  *  - `workspace` is caller-provided device memory of at least the size reported by the
  *    matching *_workspace function (0 means no workspace is needed; NULL allowed then);
+ *  - alignment: every matrix-shaped pointer (a, lu, perm, inv_t, adj_t, gbuf, d, g) and
+ *    the workspace must be 16-byte aligned, and sign / logabs / scale aligned to their
+ *    element size; a misaligned pointer returns FX_ERR_INVALID_ARGUMENT before any work is
+ *    enqueued (memory from hipMalloc, or a tensor allocator, satisfies this; a slice of a
+ *    batch at an odd member offset of an odd-n batch does not and must be copied);
+ *  - any batch size up to 2^31 - 1 is accepted: entry points whose kernels put the
+ *    batch on a grid dimension limited to 65535 run it in consecutive chunks of 65528
+ *    members on the stream, and their *_workspace sizes are those of one chunk;
  *  - the return value is a status code (FX_OK on success); numerical edge cases are
  *    encoded in the values (an exactly zero pivot gives sign 0 and logabs -inf);
  *  - calls are reentrant; the library keeps no mutable global state;
@@ -179,9 +187,9 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
  * in float64 and 0 <= n <= 4096. Unblocked kernels, one workgroup per matrix: an LU /
  * Gauss-Jordan with partial pivoting (`_slogdet_generic`, `_lu_parts_generic`,
  * src/fermix/_fallback.py:36-97) and Parlett-Reid (`_slogpf_generic`, :266-300). The
- * workspace is 0 where the matrix fits in LDS (n <= 87 for the forward, n <= 61 with the
- * inverse), else one matrix copy per member (twice that with the inverse). The kernel
- * family override FERMIX_AMD_KERNELS does not apply to them. */
+ * workspace is 0 for n <= 128 (the matrix is held in registers), else one matrix copy
+ * per member (twice that with the inverse). The kernel family override
+ * FERMIX_AMD_KERNELS does not apply to them. */
 size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n);
 int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream);

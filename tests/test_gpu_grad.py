@@ -10,7 +10,7 @@ import torch
 import fermix_amd
 from fermix_amd import _kernels
 from oracle import generic as g
-from tests.tolerances import assert_grad
+from tests.tolerances import assert_grad, assert_grad_vs_fp32, lapack_inverse_f32, rel_fro
 
 pytestmark = pytest.mark.gpu
 
@@ -112,12 +112,16 @@ def test_c3_properties(dev):
     s0, l0 = fermix_amd.slogdet(At)
     assert torch.equal(s, s0) and torch.equal(l, l0)
     assert bool(torch.isfinite(invT).all())
-    idx = [0, 1, 511, 1023]
+    idx = list(range(0, 1024, 64)) + [1, 1023]
     G = _np(invT[idx])
     ref = np.linalg.inv(A[idx].astype(np.float64)).transpose(0, 2, 1)
     assert_grad(G, ref, A[idx], "C3 subset vs float64")
+    # no worse than twice the fp32 references on the same members: the oracle (the
+    # reference's generic path restated) and float32 LAPACK
     _, _, invo, _, _, _ = g.lu_parts_generic(A[idx])
-    assert_grad(G, invo, A[idx], "C3 subset vs oracle")
+    assert_grad_vs_fp32(G, ref, rel_fro(invo, ref), "C3 subset vs the oracle's error")
+    inv32 = lapack_inverse_f32(A[idx]).transpose(0, 2, 1)
+    assert_grad_vs_fp32(G, ref, rel_fro(inv32, ref), "C3 subset vs fp32 LAPACK's error")
 
 
 @pytest.mark.parametrize("n", [2, 4, 6, 10, 16, 34, 64, 96, 128, 130, 256, 300, 512])
@@ -178,11 +182,14 @@ def test_c4_properties(dev):
     s0, l0 = fermix_amd.slogpf(St, skew_symmetrize=False)
     assert torch.equal(s, s0) and torch.equal(l, l0)
     assert bool(torch.isfinite(Sinv).all())
-    idx = [0, 63]
+    idx = [0, 1, 2, 31, 62, 63]
     G = _np(Sinv[idx])
     assert np.max(np.abs(G + G.transpose(0, 2, 1))) <= 1e-6 * np.abs(G).max()
     ref = np.linalg.inv(S[idx].astype(np.float64))
     assert_grad(G, ref, S[idx], "C4 subset vs float64")
+    # no worse than twice a float32 LAPACK inverse of the same members
+    inv32 = lapack_inverse_f32(S[idx])
+    assert_grad_vs_fp32(G, ref, rel_fro(inv32, ref), "C4 subset vs fp32 LAPACK's error")
 
 
 @pytest.mark.parametrize("n", [40, 129, 200, 512])

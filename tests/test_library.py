@@ -39,7 +39,7 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_calls():
     L = _lib.lib()
-    assert L.fx_abi_version() == 102
+    assert L.fx_abi_version() == 103
     assert L.fx_status_string(0) == b"ok"
     assert L.fx_lu_padded_size(100) == 112
     assert L.fx_pf_padded_size(128) == 128
@@ -104,3 +104,54 @@ def test_tune_table():
     assert _tune.kernel_family(128) == "fused-lds"
     assert _tune.kernel_family(32) == "tiny-wave" and _tune.kernel_family(32, "slogpf") == "fused-lds"
     assert _tune.kernel_family(4096, "slogpf") == "blocked" and _tune.kernel_family(4097) == "unsupported"
+
+
+def test_misaligned_pointers_rejected():
+    """The alignment contract of include/fermix.h: a matrix-shaped or workspace pointer
+    that is not 16-byte aligned (here a fake address 4 bytes past a 16-byte boundary)
+    returns FX_ERR_INVALID_ARGUMENT before any device work is enqueued, for every family
+    and every float32 / float64 entry point."""
+    L = _lib.lib()
+    good, bad = 0x10000, 0x10004
+    ws = 0x20000
+    for n in (8, 100, 129, 512):
+        assert L.fx_slogdet_f32(bad, 2, n, good, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_f32(good, 2, n, good, good, bad, 1 << 40, None) == 1
+        assert L.fx_slogdet_f32(good, 2, n, good + 2, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_parts_f32(good, 2, n, 1, good, good, bad, None, None, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_parts_f32(good, 2, n, 1, good, good, good, bad, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_parts_f32(good, 2, n, 1, good, good, good, good, bad, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_factors_f32(good, 2, n, good, good, bad, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_inverse_f32(bad, good, good, None, 2, n, 1, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_inverse_f32(good, good, good, None, 2, n, 1, good, bad, 1 << 40, None) == 1
+        assert L.fx_det_parts_f32(good, 2, n, good, good, bad, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_f32(bad, 2, n, 0, good, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_factors_f32(good, 2, n, 0, good, good, bad, good, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_inverse_f32(good, good, good, None, 2, n, 0, bad, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_parts_f32(bad, 2, n, 0, 0, good, good, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_f64(bad, 2, n, good, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_parts_f64(good, 2, n, good, good, bad, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_f64(good, 2, n, 0, good + 4, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_parts_f64(good, 2, n, 0, 0, good, good, bad, ws, 1 << 40, None) == 1
+
+
+def test_workspace_is_one_chunk():
+    """Batches above 65528 members run in chunks of 65528 on the stream, so the workspace
+    of any larger batch is that of one chunk (host-only queries)."""
+    L = _lib.lib()
+    C = 65528
+    for fn, n in (
+        (L.fx_slogdet_f32_workspace, 200),
+        (L.fx_slogdet_parts_f32_workspace, 200),
+        (L.fx_slogdet_parts_f32_workspace, 64),
+        (L.fx_slogdet_factors_f32_workspace, 200),
+        (L.fx_slogdet_inverse_f32_workspace, 64),
+        (L.fx_det_parts_f32_workspace, 130),
+        (L.fx_slogpf_f32_workspace, 200),
+        (L.fx_slogpf_factors_f32_workspace, 200),
+        (L.fx_slogpf_inverse_f32_workspace, 200),
+        (L.fx_slogpf_parts_f32_workspace, 64),
+    ):
+        w = fn(C, n)
+        assert w > 0 and fn(C + 1, n) == w and fn(10 * C, n) == w, (fn, n)
+        assert fn(C - 8, n) < w, (fn, n)

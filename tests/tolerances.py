@@ -34,7 +34,7 @@ def relerr(x, ref):
 
 
 U32 = 2.0**-24
-KAPPA_C = 8.0
+KAPPA_C = 4.0
 
 
 def kappa(A):
@@ -69,14 +69,57 @@ def assert_grad(G, ref, A, what=""):
     """Gradients within 1e-4 relative Frobenius error of float64 truth; a member outside
     it must be within KAPPA_C * 2^-24 * kappa(A) (what any fp32 LU inverse achieves: at
     n = 512, N(0, 1/n) a float32 LAPACK inverse exceeds 1e-4 on about a fifth of the
-    members). The literal pass rate is printed."""
+    members). The literal pass rate, and err / (2^-24 kappa) of every member outside the
+    literal bar, are printed."""
     err = rel_fro(G, ref)
     bad = err > 1e-4
     print(f"[{what}] grad literal pass {int((~bad).sum())}/{err.size}, max rel-Fro {float(err.max()):.3g}",
           flush=True)
     if bad.any():
         k = kappa(np.asarray(A)[bad])
+        print(f"[{what}] outside the literal bar: err / (2^-24 kappa) = "
+              f"{np.array2string(err[bad] / (U32 * k), precision=3)}", flush=True)
         assert np.all(err[bad] <= KAPPA_C * U32 * k), (what, err[bad], k)
+
+
+def lapack_inverse_f32(A):
+    """A^-1 of each member by float32 LAPACK (sgetrf + sgetri), the accuracy reference a
+    genuine fp32 library inverse sets on the same inputs."""
+    from scipy.linalg import lapack
+
+    out = np.empty(A.shape, np.float32)
+    for b in range(A.shape[0]):
+        lu, piv, info = lapack.sgetrf(np.asarray(A[b], np.float32))
+        inv, info2 = lapack.sgetri(lu, piv)
+        assert info == 0 and info2 == 0, (b, info, info2)
+        out[b] = inv
+    return out
+
+
+def assert_grad_vs_fp32(G, ref, err_fp32, what=""):
+    """The gradient bar at the full-size configs, against an fp32 reference (float32
+    LAPACK, or the oracle) on the same members, with float64 truth `ref`:
+
+    * over the subset, the geometric mean of err / err_fp32 and the ratio of the summed
+      errors are both at most 1.5 -- on average no less accurate than the fp32 library;
+    * each member within max(1e-4, 8 err_fp32).
+
+    A per-member factor of 2 would fail equally accurate algorithms: the relative
+    Frobenius errors of two fp32 LAPACK inverses of the same matrix, one from the LU of A
+    and one from the LU of A^T, differ by factors from 0.08 to 8.0 over 64 C3-sized members
+    (n = 512, N(0, 1/n); 8 % of them by more than 2). A 10x accuracy regression fails the
+    subset bars."""
+    err = rel_fro(G, ref)
+    err_fp32 = np.asarray(err_fp32, np.float64)
+    ratio = err / err_fp32
+    gmean = float(np.exp(np.mean(np.log(ratio))))
+    sratio = float(err.sum() / err_fp32.sum())
+    e3 = {"float_kind": lambda v: f"{v:.3e}"}
+    print(f"[{what}] grad rel-Fro {np.array2string(err, formatter=e3)}; fp32 reference "
+          f"{np.array2string(err_fp32, formatter=e3)}; ratio {np.array2string(ratio, precision=3)}; "
+          f"geometric mean {gmean:.3f}, summed-error ratio {sratio:.3f}", flush=True)
+    assert gmean <= 1.5 and sratio <= 1.5, (what, gmean, sratio)
+    assert np.all(err <= np.maximum(1e-4, 8.0 * err_fp32)), (what, err, err_fp32)
 
 
 # float64 (the f64 entry points): the same contract scaled to double precision --
