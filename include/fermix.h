@@ -24,7 +24,8 @@
  *    members on the stream, and their *_workspace sizes are those of one chunk;
  *  - the return value is a status code (FX_OK on success); numerical edge cases are
  *    encoded in the values (an exactly zero pivot gives sign 0 and logabs -inf);
- *  - calls are reentrant; the library keeps no mutable global state;
+ *  - calls are reentrant; the library keeps no mutable global state (apart from the
+ *    once-per-device address of the scratch array of fx_slogdet_f32_noalloc);
  *  - the kernel family is chosen from n alone (never from the batch): several matrices
  *    per wave (n <= 32 for slogdet, 16 for slogpf), one fused workgroup per matrix
  *    (n <= 128), blocked kernels with workspace (n <= 4096). The environment variable
@@ -125,6 +126,18 @@ int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, co
 size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n);
 int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
                      void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* No counterpart in the reference: fx_slogdet_f32 for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments without the workspace; sign / logabs bit-identical to
+ * fx_slogdet_f32. The blocked kernels' workspace (n > 128) is a device array of the
+ * library of FX_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends); a batch whose
+ * workspace exceeds it runs in consecutive sub-batches that fit. n whose single-matrix
+ * workspace exceeds the array (n > 4032) returns FX_ERR_UNSUPPORTED. The call allocates
+ * nothing. Calls that overlap on one GPU share its array and race: serialise them. */
+#define FX_NOALLOC_SCRATCH_BYTES (64u << 20)
+int fx_slogdet_f32_noalloc(const float* a, int64_t batch, int32_t n, float* sign, float* logabs,
+                           fx_stream_t stream);
 
 /* ---------------------------------------------------------------- slogpf
  * sign[b], logabs[b] of pf(S[b]), S = (a - a^T) / 2 if skew_symmetrize != 0, else

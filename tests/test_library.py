@@ -155,3 +155,18 @@ def test_workspace_is_one_chunk():
         w = fn(C, n)
         assert w > 0 and fn(C + 1, n) == w and fn(10 * C, n) == w, (fn, n)
         assert fn(C - 8, n) < w, (fn, n)
+
+
+def test_noalloc_host_checks():
+    """fx_slogdet_f32_noalloc validates its arguments and rejects n whose one-matrix
+    workspace exceeds the scratch array before any device work (host-only)."""
+    L = _lib.lib()
+    good = 0x10000
+    assert L.fx_slogdet_f32_noalloc(None, -1, 300, None, None, None) == 1
+    assert L.fx_slogdet_f32_noalloc(None, 0, 300, None, None, None) == 0
+    assert L.fx_slogdet_f32_noalloc(None, 4, 300, None, None, None) == 1
+    limit = 64 << 20
+    assert L.fx_slogdet_f32_workspace(1, 4032) <= limit < L.fx_slogdet_f32_workspace(1, 4033)
+    for n in (4033, 4096):
+        assert L.fx_slogdet_f32_noalloc(good, 4, n, good, good, None) == 4
+    assert L.fx_slogdet_f32_noalloc(good, 4, 5000, good, good, None) == 4
