@@ -27,6 +27,8 @@
 //   * all waves then form the trailing block M'' = M + G J G^T (J = diag of
 //     [[0,1],[-1,0]]) on fp32 MFMA 16x16x4 over the lower-triangle tiles, gathered through
 //     the block's permutation and stored in the new order.
+// The load reads each matrix once in 4 x 4 block pairs and forms (A - A^T) / 2 in
+// registers (n == N).
 // With FACT every block's G is exported indexed by the original row index, with the
 // pivots d and the final position -> original row map (the factors of P S P^T = L D L^T).
 //
@@ -242,50 +244,90 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
   wave_lds_fence();
 }
 
+// Load of a full N x N matrix (n == N) into T in one pass over 4 x 4 block pairs: pair
+// (I, J), I >= J, owns T(p, q) for p in rows 4I..4I+3, q in columns 4J..4J+3, p > q. A
+// thread reads the block A[I][J] as four 16-byte rows and, with skew, the transposed block
+// A[J][I] the same way, and forms every entry in registers: T(p, q) = A[p][q] / 2 -
+// A[q][p] / 2 (fma(-A[q][p], 1/2, A[p][q] / 2): halving is exact, one rounding), or
+// A[p][q] without skew. No LDS read-modify-write and no barrier. Pairs are numbered by
+// folded block rows: rows f and NB4 - 1 - f together hold NB4 + 1 pairs, so consecutive
+// threads read consecutive 16-byte pieces of the same rows of A[I][J].
+template <int N>
+__device__ __forceinline__ void pf_load_full(float* T, const float* __restrict__ g, int skew, int tid) {
+  constexpr int NB4 = N / 4;
+  static_assert(NB4 % 2 == 0, "folded block rows");
+  constexpr int NPAIR = NB4 * (NB4 + 1) / 2;
+  constexpr int ITER = (NPAIR + 255) / 256;
+  float4 lo[ITER][4], up[ITER][4];
+  int bi[ITER], bj[ITER];
+#pragma unroll
+  for (int it = 0; it < ITER; ++it) {
+    const int t = tid + 256 * it;
+    const int f = t / (NB4 + 1), x = t - f * (NB4 + 1);
+    bi[it] = x <= f ? f : NB4 - 1 - f;
+    bj[it] = x <= f ? x : x - f - 1;
+    if (NPAIR % 256 == 0 || t < NPAIR) {
+      const float4* a = reinterpret_cast<const float4*>(g + (4 * bi[it]) * N + 4 * bj[it]);
+      const float4* u = reinterpret_cast<const float4*>(g + (4 * bj[it]) * N + 4 * bi[it]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lo[it][i] = a[i * (N / 4)];
+      if (skew && bi[it] != bj[it]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) up[it][i] = u[i * (N / 4)];
+      }
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < ITER; ++it) {
+    const int t = tid + 256 * it;
+    if (NPAIR % 256 == 0 || t < NPAIR) {
+      const int p0 = 4 * bi[it], q0 = 4 * bj[it];
+      float v[4][4];  // v[i][j] = T(p0 + i, q0 + j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float r[4] = {lo[it][i].x, lo[it][i].y, lo[it][i].z, lo[it][i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[i][j] = r[j];
+      }
+      if (bi[it] != bj[it]) {
+        if (skew) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float c[4] = {up[it][j].x, up[it][j].y, up[it][j].z, up[it][j].w};  // A[q0 + j][p0 + i]
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i][j] = fmaf(-c[i], 0.5f, v[i][j] * 0.5f);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float* d = T + tri_row(p0 + i) + q0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) d[j] = v[i][j];
+        }
+      } else {
+        // diagonal block: T(p0 + i, p0 + j) for i > j; the transposed entries are this
+        // block's own
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+          float* d = T + tri_row(p0 + i) + q0;
+#pragma unroll
+          for (int j = 0; j < i; ++j) d[j] = skew ? fmaf(-v[j][i], 0.5f, v[i][j] * 0.5f) : v[i][j];
+        }
+      }
+    }
+  }
+}
+
 // Load the matrix (row-major n x n, n even) into T, padded with [[0,1],[-1,0]] blocks;
 // with skew, T holds (A - A^T) / 2 formed as A[p][q] / 2 - A[q][p] / 2 (halving is exact).
 template <int N>
 __device__ __forceinline__ void pf_load(float* T, const float* __restrict__ g, int n, int skew, int tid) {
   const float h = skew ? 0.5f : 1.0f;
   if (n == N) {
-    constexpr int NV = N * N / 4;
-    constexpr int PER = (NV + 255) / 256;
-    const float4* g4 = reinterpret_cast<const float4*>(g);
-    float4 v[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = tid + 256 * i;
-      if (NV % 256 == 0 || e < NV) v[i] = g4[e];
-    }
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int e = tid + 256 * i;
-      if (NV % 256 == 0 || e < NV) {
-        const int r = (4 * e) / N, c = (4 * e) % N;
-        const float vv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (c + j < r) T[tri_row(r) + c + j] = vv[j] * h;
-      }
-    }
-    if (skew) {
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int e = tid + 256 * i;
-        if (NV % 256 == 0 || e < NV) {
-          const int r = (4 * e) / N, c = (4 * e) % N;
-          const float vv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (c + j > r) {
-              float* d = T + tri_row(c + j) + r;
-              *d = *d - vv[j] * 0.5f;
-            }
-        }
-      }
-    }
-  } else {
+    pf_load_full<N>(T, g, skew, tid);
+    return;
+  }
+  {
     // lower triangle (every entry written once), then the upper halves subtracted
     constexpr int CH = 8;
     for (int base = 0; base < N * N; base += 256 * CH) {
