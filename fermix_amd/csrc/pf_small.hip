@@ -44,9 +44,6 @@ struct PfSmall {
   static constexpr int NTRI = N * (N - 1) / 2;                   // strictly lower triangle
   static constexpr int NB = N / 16;
   static constexpr int NPV = (N / 2 + 63) / 64;                  // pivot slots per lane
-  static constexpr int MAXNT = N / 16 - 1;                       // trailing tiles per side
-  static constexpr int MAXTILES = MAXNT * (MAXNT + 1) / 2;       // lower-triangle tiles
-  static constexpr int TPW = MAXTILES > 0 ? (MAXTILES + 3) / 4 : 1;  // tiles per wave
   static constexpr int LDS_BYTES = NTRI * 4 + N * 16 * 4 + 2 * N;
 };
 static_assert(PfSmall<128>::LDS_BYTES <= 40960, "four n = 128 workgroups per CU");
@@ -371,6 +368,98 @@ __device__ __forceinline__ void pf_load(float* T, const float* __restrict__ g, i
   }
 }
 
+// Trailing update of one block: M'' = M + G J G^T (J = diag of [[0,1],[-1,0]]) over the
+// lower-triangle 16 x 16 tiles of the positions >= rb, fp32 MFMA 16x16x4. Entry (P, Q) of
+// the new order is read as M_old(src[P], src[Q]) from the triangle (negated when stored
+// transposed) and written in place at (P, Q); G is indexed by block-start row.
+// No barrier separates the reads from the stores: an entry whose row and column both stay
+// in place is read and rewritten by the same lane, and every other old entry lies in a row
+// or column of the block just factored (positions r0..rb-1), which this update never
+// writes. Tiles t = wv, wv + 4, ... (row-major over (I, J), I >= J) go to wave wv, two per
+// iteration so the second tile's LDS reads overlap the first's; (I, J) advance in scalar
+// registers.
+template <int N>
+__device__ __forceinline__ void pf_update(float* T, const float* Gs, const unsigned char* src, int rb, int nt, int wv,
+                                          int li, int g) {
+  const int ntiles = nt * (nt + 1) / 2;
+  int I = wv == 0 ? 0 : (wv < 3 ? 1 : 2);
+  int J = wv - I * (I + 1) / 2;
+  auto advance = [&]() {
+    J += 4;
+    while (J > I) {
+      J -= I + 1;
+      ++I;
+    }
+  };
+  struct Tile {
+    int P0, Q0, sq, sr;
+    unsigned sp4;
+    float raw[4];
+    float4 ga, gb;
+    unsigned below;
+  };
+  auto read_src = [&](Tile& x) {
+    x.sp4 = *reinterpret_cast<const unsigned*>(src + x.P0 + 4 * g);
+    x.sq = src[x.Q0 + li];
+    x.sr = src[x.P0 + li];
+  };
+  auto read_old = [&](Tile& x) {
+    x.below = 0;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      // branch-free addressing: the entry lives in the row of the larger index
+      const int sv = (x.sp4 >> (8 * v)) & 0xFF;
+      const int hi = max(sv, x.sq), lo = min(sv, x.sq);
+      // p == q (diagonal tiles; never stored) may address T[NTRI], the first entry of Gs
+      x.raw[v] = T[tri_row(hi) + lo];
+      x.below |= (sv > x.sq ? 1u : 0u) << v;
+    }
+    x.ga = *reinterpret_cast<const float4*>(Gs + g_idx<N>(x.sr, 4 * g));
+    x.gb = *reinterpret_cast<const float4*>(Gs + g_idx<N>(x.sq, 4 * g));
+  };
+  // MFMA step u contracts k = 4 g + u, so each lane's A and B operands are one 16-byte G
+  // row group; (J G^T)[k] = G[k+1] (k even), -G[k-1] (k odd)
+  auto finish = [&](const Tile& x) {
+    v4f acc;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = ((x.below >> v) & 1) ? x.raw[v] : -x.raw[v];
+    acc = mfma16(x.ga.x, x.gb.y, acc);
+    acc = mfma16(x.ga.y, -x.gb.x, acc);
+    acc = mfma16(x.ga.z, x.gb.w, acc);
+    acc = mfma16(x.ga.w, -x.gb.z, acc);
+    const int q = x.Q0 + li;
+    const int p0 = x.P0 + 4 * g;
+    const int e0 = tri_row(p0) + q;  // tri_row(p0 + v) = tri_row(p0) + v p0 + v (v - 1) / 2
+    if (x.P0 != x.Q0) {
+      T[e0] = acc[0];
+      T[e0 + p0] = acc[1];
+      T[e0 + 2 * p0 + 1] = acc[2];
+      T[e0 + 3 * p0 + 3] = acc[3];
+    } else {
+      if (p0 > q) T[e0] = acc[0];
+      if (p0 + 1 > q) T[e0 + p0] = acc[1];
+      if (p0 + 2 > q) T[e0 + 2 * p0 + 1] = acc[2];
+      if (p0 + 3 > q) T[e0 + 3 * p0 + 3] = acc[3];
+    }
+  };
+  for (int t = wv; t < ntiles; t += 8) {
+    Tile a, b;
+    a.P0 = rb + 16 * I;
+    a.Q0 = rb + 16 * J;
+    advance();
+    const bool two = t + 4 < ntiles;
+    b.P0 = rb + 16 * I;
+    b.Q0 = rb + 16 * J;
+    advance();
+    read_src(a);
+    if (two) read_src(b);
+    read_old(a);
+    if (two) read_old(b);
+    finish(a);
+    if (two) finish(b);
+  }
+}
+
 template <int N, bool FACT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void pf_small_kernel(const float* __restrict__ A, int n, int skew,
                                                        float* __restrict__ sign_out,
@@ -379,8 +468,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
                                                        float* __restrict__ d_out,
                                                        int* __restrict__ perm_out) {
   using C = PfSmall<N>;
-  constexpr int NB = C::NB, TPW = C::TPW;
-  static_assert(TPW <= 8, "the sign mask holds 32 entries per chunk");
+  constexpr int NB = C::NB;
   __shared__ __align__(16) float lds[C::NTRI + N * 16];  // T, then Gs (NTRI * 4 % 16 == 0)
   float* const T = lds;
   float* const Gs = lds + C::NTRI;
@@ -409,93 +497,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     const int nt = (N - r0 - 16) / 16;
     if (nt == 0) break;
     __syncthreads();
-    const int ntiles = nt * (nt + 1) / 2;
     const int rb = r0 + 16;
     int li = lane & 15, g = lane >> 4, wv = __builtin_amdgcn_readfirstlane(wave);
     asm volatile("" : "+v"(li), "+v"(g), "+s"(wv));
-    // Tiles t = wv + 4 s of the lower triangle of the trailing block, row-major:
-    // t -> (I, J), I >= J; t is wave-uniform, so idle slots are skipped by scalar
-    // branches. Tiles are processed in chunks of up to 4 (register budget): each chunk reads its
-    // permutation bytes, then its old entries M[src p][src q] (raw triangle values; bit
-    // 4 j + v of `neg` marks the ones stored transposed, negated only once every read is
-    // in flight) and G rows, then runs the MFMAs and stores.
-    // No barrier separates these reads from the stores: an entry whose row and column
-    // both stay in place is read and rewritten by the same lane, and every other old
-    // entry lies in a row or column of the block just factored (positions r0..rb-1),
-    // which this update never writes.
-    static_for<0, (TPW + 3) / 4>([&](auto cc) {
-      constexpr int S0C = 4 * decltype(cc)::value;
-      constexpr int CH = (TPW - S0C) < 4 ? (TPW - S0C) : 4;
-      int P[CH], Q[CH], sr[CH], sq[CH];
-      unsigned sp4[CH];
-#pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        const int t = wv + 4 * (S0C + j);
-        P[j] = Q[j] = rb;
-        sp4[j] = 0;
-        sr[j] = sq[j] = 0;
-        if (t < ntiles) {
-          int I = 0;
-          static_for<1, C::MAXNT>([&](auto mc) {
-            constexpr int m = decltype(mc)::value;
-            I += (t >= m * (m + 1) / 2) ? 1 : 0;
-          });
-          const int J = t - I * (I + 1) / 2;
-          P[j] = rb + 16 * I;
-          Q[j] = rb + 16 * J;
-          sp4[j] = *reinterpret_cast<const unsigned*>(src + P[j] + 4 * g);
-          sr[j] = src[P[j] + li];
-          sq[j] = src[Q[j] + li];
-        }
-      }
-      float raw[CH][4];
-      float4 ga[CH], gb[CH];
-      unsigned neg = 0;
-#pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        if (wv + 4 * (S0C + j) < ntiles) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int spv = (sp4[j] >> (8 * v)) & 0xFF;
-            const int hi = max(spv, sq[j]), lo = min(spv, sq[j]);
-            // p <= q (diagonal tiles) is never stored; p == q may address T[NTRI] (in Gs)
-            raw[j][v] = T[tri_row(hi) + lo];
-            neg |= (spv < sq[j] ? 1u : 0u) << (4 * j + v);
-          }
-          ga[j] = *reinterpret_cast<const float4*>(Gs + g_idx<N>(sr[j], 4 * g));
-          gb[j] = *reinterpret_cast<const float4*>(Gs + g_idx<N>(sq[j], 4 * g));
-        }
-      }
-      // M'' = M + G J G^T: MFMA step u contracts k = 4 g + u, so each lane's A and B
-      // operands are one 16-byte G row group; (J G^T)[k] = G[k+1] (k even), -G[k-1] (k odd)
-#pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        if (wv + 4 * (S0C + j) < ntiles) {
-          v4f acc;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[v] = ((neg >> (4 * j + v)) & 1) ? -raw[j][v] : raw[j][v];
-          acc = mfma16(ga[j].x, gb[j].y, acc);
-          acc = mfma16(ga[j].y, -gb[j].x, acc);
-          acc = mfma16(ga[j].z, gb[j].w, acc);
-          acc = mfma16(ga[j].w, -gb[j].z, acc);
-          const int q = Q[j] + li;
-          const int p0 = P[j] + 4 * g;
-          const int e0 = tri_row(p0) + q;  // tri_row(p0 + v) = tri_row(p0) + v p0 + v (v - 1) / 2
-          if (P[j] != Q[j]) {
-            // off-diagonal tile: every element lies below the diagonal
-            T[e0] = acc[0];
-            T[e0 + p0] = acc[1];
-            T[e0 + 2 * p0 + 1] = acc[2];
-            T[e0 + 3 * p0 + 3] = acc[3];
-          } else {
-            if (p0 > q) T[e0] = acc[0];
-            if (p0 + 1 > q) T[e0 + p0] = acc[1];
-            if (p0 + 2 > q) T[e0 + 2 * p0 + 1] = acc[2];
-            if (p0 + 3 > q) T[e0 + 3 * p0 + 3] = acc[3];
-          }
-        }
-      }
-    });
+    pf_update<N>(T, Gs, src, rb, nt, wv, li, g);
     __syncthreads();
   }
   if (wave == 0) {
