@@ -117,9 +117,9 @@ def bench_c1(steps, warmup):
                 bytes=B * (4 * n * n + 8), sample=A[:64].cpu().numpy())
 
 
-def bench_c3(steps, warmup):
+def bench_c3(steps, warmup, prec="ieee"):
     """slogdet forward + VJP (cotangent ones on logabs), B = 1024, n = 512,
-    A iid N(0, 1/n)."""
+    A iid N(0, 1/n); prec "ieee" (fp32 MFMA) or "bf16x3"."""
     import torch
     import fermix_amd
 
@@ -127,18 +127,19 @@ def bench_c3(steps, warmup):
     A = torch.from_numpy(_inputs(B, n, 0, scale=1.0 / np.sqrt(n))).cuda().requires_grad_()
 
     def fn():
-        s, l = fermix_amd.slogdet(A)
+        s, l = fermix_amd.slogdet(A, prec=prec)
         (g,) = torch.autograd.grad(l.sum(), A)
         return g
 
     ms, wall = _time_gpu(fn, steps, warmup)
-    return dict(name="slogdet_fwd_grad", B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
+    name = "slogdet_fwd_grad" + ("" if prec == "ieee" else "_" + prec)
+    return dict(name=name, B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
                 bytes=B * 8 * n * n, flops=B * 2.0 * n ** 3, sample=None)
 
 
-def bench_c4(steps, warmup):
+def bench_c4(steps, warmup, prec="ieee"):
     """slogpf forward + VJP (cotangent ones on log|pf|), B = 64, n = 2048,
-    S = A - A^T with A iid N(0, 1/n)."""
+    S = A - A^T with A iid N(0, 1/n); prec "ieee" or "bf16x3"."""
     import torch
     import fermix_amd
 
@@ -148,12 +149,13 @@ def bench_c4(steps, warmup):
     del A
 
     def fn():
-        s, l = fermix_amd.slogpf(S, skew_symmetrize=False)
+        s, l = fermix_amd.slogpf(S, skew_symmetrize=False, prec=prec)
         (g,) = torch.autograd.grad(l.sum(), S)
         return g
 
     ms, wall = _time_gpu(fn, steps, warmup)
-    return dict(name="slogpf_fwd_grad", B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
+    name = "slogpf_fwd_grad" + ("" if prec == "ieee" else "_" + prec)
+    return dict(name=name, B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
                 bytes=B * 8 * n * n, flops=B * 1.0 * n ** 3, sample=None)
 
 
@@ -334,9 +336,15 @@ def main():
     if "c3" in only:
         res["c3"] = bench_c3(max(10, args.steps), max(2, args.warmup // 2))
         print(f"# c3 slogdet fwd+grad: {res['c3']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
+        res["c3_bf16x3"] = bench_c3(max(10, args.steps), max(2, args.warmup // 2), prec="bf16x3")
+        print(f"# c3 slogdet fwd+grad (prec=bf16x3): {res['c3_bf16x3']['ms']:.4f} ms/step", file=sys.stderr,
+              flush=True)
     if "c4" in only:
         res["c4"] = bench_c4(max(10, args.steps // 2), 2)
         print(f"# c4 slogpf fwd+grad: {res['c4']['ms']:.4f} ms/step", file=sys.stderr, flush=True)
+        res["c4_bf16x3"] = bench_c4(max(10, args.steps // 2), 2, prec="bf16x3")
+        print(f"# c4 slogpf fwd+grad (prec=bf16x3): {res['c4_bf16x3']['ms']:.4f} ms/step", file=sys.stderr,
+              flush=True)
     if "f64" in only:
         for k, r in bench_f64(args.steps, args.warmup).items():
             res[k] = r

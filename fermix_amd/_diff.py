@@ -86,17 +86,17 @@ class _SlogdetFwd(torch.autograd.Function):
     """Forward only (no derivative requested)."""
 
     @staticmethod
-    def forward(A):
-        return _kernels.slogdet(A)
+    def forward(A, x3):
+        return _kernels.slogdet(A, x3)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
         ctx.mark_non_differentiable(*output)
 
     @staticmethod
-    def vmap(info, in_dims, A):
-        A2, vb = _fold(info, in_dims, A)
-        s, l = _SlogdetFwd.apply(A2)
+    def vmap(info, in_dims, A, x3):
+        A2, vb = _fold(info, in_dims[:1], A)
+        s, l = _SlogdetFwd.apply(A2, x3)
         if vb is None:
             return (s, l), (None, None)
         return (_unfold(s, vb), _unfold(l, vb)), (0, 0)
@@ -106,8 +106,8 @@ class _SlogdetParts(torch.autograd.Function):
     """(sign, logabs, invT) from one factorisation; d logabs = sum(invT * dA)."""
 
     @staticmethod
-    def forward(A):
-        sign, logabs, invT, _, _ = _kernels.slogdet_parts(A)
+    def forward(A, x3):
+        sign, logabs, invT, _, _ = _kernels.slogdet_parts(A, x3=x3)
         return sign, logabs, invT
 
     @staticmethod
@@ -122,19 +122,19 @@ class _SlogdetParts(torch.autograd.Function):
     def backward(ctx, g_sign, g_logabs, g_invT):
         (invT,) = ctx.saved_tensors
         if g_logabs is None:
-            return None
-        return g_logabs[:, None, None] * invT
+            return None, None
+        return g_logabs[:, None, None] * invT, None
 
     @staticmethod
-    def jvp(ctx, dA):
+    def jvp(ctx, dA, _x3):
         (invT,) = ctx.saved_tensors
         dlog = (invT * dA).sum(dim=(-1, -2))
         return None, dlog, None
 
     @staticmethod
-    def vmap(info, in_dims, A):
-        A2, vb = _fold(info, in_dims, A)
-        s, l, inv = _SlogdetParts.apply(A2)
+    def vmap(info, in_dims, A, x3):
+        A2, vb = _fold(info, in_dims[:1], A)
+        s, l, inv = _SlogdetParts.apply(A2, x3)
         if vb is None:
             return (s, l, inv), (None, None, None)
         return (_unfold(s, vb), _unfold(l, vb), _unfold(inv, vb)), (0, 0, 0)
@@ -149,8 +149,8 @@ class _SlogdetSplit(torch.autograd.Function):
     graph refactors the saved input."""
 
     @staticmethod
-    def forward(A):
-        return _kernels.slogdet_factors(A)
+    def forward(A, x3):
+        return _kernels.slogdet_factors(A, x3)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -160,44 +160,46 @@ class _SlogdetSplit(torch.autograd.Function):
         ctx.save_for_backward(inputs[0], sign, lu, perm)
         ctx.save_for_forward(sign, lu, perm)
         ctx.n = inputs[0].shape[-1]
+        ctx.x3 = inputs[1]
         ctx.lu_used = False
 
     @staticmethod
     def backward(ctx, g_sign, g_logabs, g_lu, g_perm):
         A, sign, lu, perm = ctx.saved_tensors
         if g_logabs is None:
-            return None
+            return None, None
         if ctx.lu_used:  # retained graph, second backward: lu was overwritten
-            sign, _, lu, perm = _kernels.slogdet_factors(A.detach())
+            sign, _, lu, perm = _kernels.slogdet_factors(A.detach(), ctx.x3)
         ctx.lu_used = True
-        return _kernels.slogdet_inverse(lu, perm, sign, ctx.n, scale=g_logabs)
+        return _kernels.slogdet_inverse(lu, perm, sign, ctx.n, scale=g_logabs, x3=ctx.x3), None
 
     @staticmethod
-    def jvp(ctx, dA):
+    def jvp(ctx, dA, _x3):
         sign, lu, perm = ctx.saved_tensors
-        invT = _kernels.slogdet_inverse(lu.clone(), perm, sign, ctx.n)
+        invT = _kernels.slogdet_inverse(lu.clone(), perm, sign, ctx.n, x3=ctx.x3)
         dlog = (invT * dA).sum(dim=(-1, -2))
         return None, dlog, None, None
 
     @staticmethod
-    def vmap(info, in_dims, A):
-        A2, vb = _fold(info, in_dims, A)
-        out = _SlogdetSplit.apply(A2)
+    def vmap(info, in_dims, A, x3):
+        A2, vb = _fold(info, in_dims[:1], A)
+        out = _SlogdetSplit.apply(A2, x3)
         if vb is None:
             return out, (None,) * 4
         return tuple(_unfold(x, vb) for x in out), (0,) * 4
 
 
-def slogdet(A):
+def slogdet(A, x3=0):
+    """x3: the split-bf16x3 product mode of the blocked kernels (0: fp32 MFMA)."""
     if _wants_grad(A):
         # n <= 32: one Gauss-Jordan pass forms A^-T with the factors; forward mode and
         # torch.func transforms: the parts call (their rules run on wrapped tensors)
         if A.dtype == torch.float32 and A.shape[-1] > 32 and _plain_reverse(A):
-            s, l, _, _ = _SlogdetSplit.apply(A)
+            s, l, _, _ = _SlogdetSplit.apply(A, x3)
         else:
-            s, l, _ = _SlogdetParts.apply(A)
+            s, l, _ = _SlogdetParts.apply(A, x3)
         return s, l
-    return _SlogdetFwd.apply(A)
+    return _SlogdetFwd.apply(A, x3)
 
 
 # ----------------------------------------------------------------- slogpf
@@ -226,8 +228,8 @@ class _SlogpfParts(torch.autograd.Function):
     derivative w.r.t. ``a`` through S = (a - a^T)/2 (Sinv is skew)."""
 
     @staticmethod
-    def forward(A, skew):
-        return _kernels.slogpf_parts(A, skew)
+    def forward(A, skew, x3):
+        return _kernels.slogpf_parts(A, skew, x3=x3)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -241,19 +243,19 @@ class _SlogpfParts(torch.autograd.Function):
     def backward(ctx, g_sign, g_logabs, g_sinv):
         (Sinv,) = ctx.saved_tensors
         if g_logabs is None:
-            return None, None
-        return (-0.5 * g_logabs)[:, None, None] * Sinv, None
+            return None, None, None
+        return (-0.5 * g_logabs)[:, None, None] * Sinv, None, None
 
     @staticmethod
-    def jvp(ctx, dA, _skew):
+    def jvp(ctx, dA, _skew, _x3):
         (Sinv,) = ctx.saved_tensors
         dlog = -0.5 * (Sinv * dA).sum(dim=(-1, -2))
         return None, dlog, None
 
     @staticmethod
-    def vmap(info, in_dims, A, skew):
+    def vmap(info, in_dims, A, skew, x3):
         A2, vb = _fold(info, in_dims[:1], A)
-        s, l, inv = _SlogpfParts.apply(A2, skew)
+        s, l, inv = _SlogpfParts.apply(A2, skew, x3)
         if vb is None:
             return (s, l, inv), (None, None, None)
         return (_unfold(s, vb), _unfold(l, vb), _unfold(inv, vb)), (0, 0, 0)
@@ -266,7 +268,7 @@ class _SlogpfSplit(torch.autograd.Function):
     The factors are only read."""
 
     @staticmethod
-    def forward(A, skew):
+    def forward(A, skew, x3):
         return _kernels.slogpf_factors(A, skew)
 
     @staticmethod
@@ -277,37 +279,40 @@ class _SlogpfSplit(torch.autograd.Function):
         ctx.save_for_backward(gbuf, d, perm)
         ctx.save_for_forward(gbuf, d, perm)
         ctx.n = inputs[0].shape[-1]
+        ctx.x3 = inputs[2]
 
     @staticmethod
     def backward(ctx, g_sign, g_logabs, g_gbuf, g_d, g_perm):
         gbuf, d, perm = ctx.saved_tensors
         if g_logabs is None:
-            return None, None
-        return _kernels.slogpf_inverse(gbuf, d, perm, ctx.n, scale=-0.5 * g_logabs), None
+            return None, None, None
+        return _kernels.slogpf_inverse(gbuf, d, perm, ctx.n, scale=-0.5 * g_logabs, x3=ctx.x3), None, None
 
     @staticmethod
-    def jvp(ctx, dA, _skew):
+    def jvp(ctx, dA, _skew, _x3):
         gbuf, d, perm = ctx.saved_tensors
-        Sinv = _kernels.slogpf_inverse(gbuf, d, perm, ctx.n)
+        Sinv = _kernels.slogpf_inverse(gbuf, d, perm, ctx.n, x3=ctx.x3)
         dlog = -0.5 * (Sinv * dA).sum(dim=(-1, -2))
         return None, dlog, None, None, None
 
     @staticmethod
-    def vmap(info, in_dims, A, skew):
+    def vmap(info, in_dims, A, skew, x3):
         A2, vb = _fold(info, in_dims[:1], A)
-        out = _SlogpfSplit.apply(A2, skew)
+        out = _SlogpfSplit.apply(A2, skew, x3)
         if vb is None:
             return out, (None,) * 5
         return tuple(_unfold(x, vb) for x in out), (0,) * 5
 
 
-def slogpf(A, skew):
+def slogpf(A, skew, x3=0):
+    """x3: the split-bf16x3 product mode of the gradient's GEMMs (the forward's trailing
+    update is memory-bound and runs in fp32 in both modes)."""
     if _wants_grad(A):
         n = A.shape[-1]
         if A.dtype == torch.float32 and n > 0 and n % 2 == 0 and _plain_reverse(A):
-            s, l, _, _, _ = _SlogpfSplit.apply(A, skew)
+            s, l, _, _, _ = _SlogpfSplit.apply(A, skew, x3)
         else:
-            s, l, _ = _SlogpfParts.apply(A, skew)
+            s, l, _ = _SlogpfParts.apply(A, skew, x3)
         return s, l
     return _SlogpfFwd.apply(A, skew)
 
@@ -319,8 +324,8 @@ class _DetParts(torch.autograd.Function):
     """(det, adjT) from one factorisation; d det = sum(adjT * dA)."""
 
     @staticmethod
-    def forward(A):
-        sign, logabs, adjT = _kernels.det_parts(A)
+    def forward(A, x3):
+        sign, logabs, adjT = _kernels.det_parts(A, x3)
         return sign * torch.exp(logabs), adjT
 
     @staticmethod
@@ -335,28 +340,28 @@ class _DetParts(torch.autograd.Function):
     def backward(ctx, g_det, g_adj):
         (adjT,) = ctx.saved_tensors
         if g_det is None:
-            return None
-        return g_det[:, None, None] * adjT
+            return None, None
+        return g_det[:, None, None] * adjT, None
 
     @staticmethod
-    def jvp(ctx, dA):
+    def jvp(ctx, dA, _x3):
         (adjT,) = ctx.saved_tensors
         return (adjT * dA).sum(dim=(-1, -2)), None
 
     @staticmethod
-    def vmap(info, in_dims, A):
-        A2, vb = _fold(info, in_dims, A)
-        d, adj = _DetParts.apply(A2)
+    def vmap(info, in_dims, A, x3):
+        A2, vb = _fold(info, in_dims[:1], A)
+        d, adj = _DetParts.apply(A2, x3)
         if vb is None:
             return (d, adj), (None, None)
         return (_unfold(d, vb), _unfold(adj, vb)), (0, 0)
 
 
-def det(A):
+def det(A, x3=0):
     if _wants_grad(A):
-        d, _ = _DetParts.apply(A)
+        d, _ = _DetParts.apply(A, x3)
         return d
-    s, l = _SlogdetFwd.apply(A)
+    s, l = _SlogdetFwd.apply(A, x3)
     return s * torch.exp(l)
 
 
@@ -364,8 +369,8 @@ class _PfParts(torch.autograd.Function):
     """(pf, G) with G = -pf(S) S^-1 / 2 from one Parlett-Reid run; d pf = sum(G * dS)."""
 
     @staticmethod
-    def forward(A, skew):
-        sign, logabs, adj = _kernels.slogpf_parts(A, skew, adjugate=True)
+    def forward(A, skew, x3):
+        sign, logabs, adj = _kernels.slogpf_parts(A, skew, adjugate=True, x3=x3)
         return sign * torch.exp(logabs), -0.5 * adj
 
     @staticmethod
@@ -380,26 +385,26 @@ class _PfParts(torch.autograd.Function):
     def backward(ctx, g_pf, g_G):
         (G,) = ctx.saved_tensors
         if g_pf is None:
-            return None, None
-        return g_pf[:, None, None] * G, None
+            return None, None, None
+        return g_pf[:, None, None] * G, None, None
 
     @staticmethod
-    def jvp(ctx, dA, _skew):
+    def jvp(ctx, dA, _skew, _x3):
         (G,) = ctx.saved_tensors
         return (G * dA).sum(dim=(-1, -2)), None
 
     @staticmethod
-    def vmap(info, in_dims, A, skew):
+    def vmap(info, in_dims, A, skew, x3):
         A2, vb = _fold(info, in_dims[:1], A)
-        p, G = _PfParts.apply(A2, skew)
+        p, G = _PfParts.apply(A2, skew, x3)
         if vb is None:
             return (p, G), (None, None)
         return (_unfold(p, vb), _unfold(G, vb)), (0, 0)
 
 
-def pf(A, skew):
+def pf(A, skew, x3=0):
     if _wants_grad(A):
-        p, _ = _PfParts.apply(A, skew)
+        p, _ = _PfParts.apply(A, skew, x3)
         return p
     s, l = _SlogpfFwd.apply(A, skew)
     return s * torch.exp(l)

@@ -57,8 +57,9 @@ def pf_padded_size(n):
     return int(lib().fx_pf_padded_size(n))
 
 
-def slogdet(A):
-    """(sign, logabs) of each (n, n) matrix of A (B, n, n)."""
+def slogdet(A, x3=0):
+    """(sign, logabs) of each (n, n) matrix of A (B, n, n); x3: FX_PREC_BF16X3 products
+    (float32 only)."""
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape
@@ -71,12 +72,12 @@ def slogdet(A):
         check(st, "fx_slogdet_f64")
         return sign, logabs
     ws, wsb = _workspace(L.fx_slogdet_f32_workspace(B, n), A.device)
-    st = L.fx_slogdet_f32(_ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(ws), wsb, _stream(A))
+    st = L.fx_slogdet_f32(_ptr(A), B, n, _ptr(sign), _ptr(logabs), int(x3), _ptr(ws), wsb, _stream(A))
     check(st, "fx_slogdet_f32")
     return sign, logabs
 
 
-def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False):
+def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False, x3=0):
     """(sign, logabs, invT, lu, perm) with the optional outputs None when not asked for;
     lu / perm are padded to N = lu_padded_size(n). float64: invT only (zero for exactly
     singular members), no packed factors."""
@@ -106,13 +107,13 @@ def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False):
     ws, wsb = _workspace(L.fx_slogdet_parts_f32_workspace(B, n), dev)
     st = L.fx_slogdet_parts_f32(
         _ptr(A), B, n, int(bool(zero_singular)), _ptr(sign), _ptr(logabs), _ptr(invT),
-        _ptr(lu), _ptr(perm), _ptr(ws), wsb, _stream(A),
+        _ptr(lu), _ptr(perm), int(x3), _ptr(ws), wsb, _stream(A),
     )
     check(st, "fx_slogdet_parts_f32")
     return sign, logabs, invT, lu, perm
 
 
-def slogdet_factors(A):
+def slogdet_factors(A, x3=0):
     """(sign, logabs, lu (B, N, N), perm (B, N)): the packed LU of fx_slogdet_parts_f32
     alone, N = lu_padded_size(n)."""
     _check_input(A)
@@ -127,13 +128,13 @@ def slogdet_factors(A):
     L = lib()
     ws, wsb = _workspace(L.fx_slogdet_factors_f32_workspace(B, n), dev)
     st = L.fx_slogdet_factors_f32(
-        _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(lu), _ptr(perm), _ptr(ws), wsb, _stream(A)
+        _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(lu), _ptr(perm), int(x3), _ptr(ws), wsb, _stream(A)
     )
     check(st, "fx_slogdet_factors_f32")
     return sign, logabs, lu, perm
 
 
-def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True):
+def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True, x3=0):
     """scale[b] * A^-T (B, n, n) from slogdet_factors' outputs; lu is overwritten."""
     B = sign.shape[0]
     dev = sign.device
@@ -144,13 +145,13 @@ def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True):
     ws, wsb = _workspace(L.fx_slogdet_inverse_f32_workspace(B, n), dev)
     st = L.fx_slogdet_inverse_f32(
         _ptr(lu), _ptr(perm), _ptr(sign), _ptr(scale), B, n, int(bool(zero_singular)), _ptr(out),
-        _ptr(ws), wsb, _stream(sign),
+        int(x3), _ptr(ws), wsb, _stream(sign),
     )
     check(st, "fx_slogdet_inverse_f32")
     return out
 
 
-def det_parts(A):
+def det_parts(A, x3=0):
     """(sign, logabs, adjT) with adjT = adj(A)^T = d det / dA from one factorisation."""
     _no_f64(A, "the det gradient (exact adjugate)")
     _check_input(A)
@@ -163,7 +164,7 @@ def det_parts(A):
     L = lib()
     ws, wsb = _workspace(L.fx_det_parts_f32_workspace(B, n), dev)
     st = L.fx_det_parts_f32(
-        _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(adjT), _ptr(ws), wsb, _stream(A)
+        _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(adjT), int(x3), _ptr(ws), wsb, _stream(A)
     )
     check(st, "fx_det_parts_f32")
     return sign, logabs, adjT
@@ -216,7 +217,7 @@ def slogpf_factors(A, skew_symmetrize):
     return sign, logabs, gbuf, d, perm
 
 
-def slogpf_inverse(gbuf, d, perm, n, scale=None, adjugate=False):
+def slogpf_inverse(gbuf, d, perm, n, scale=None, adjugate=False, x3=0):
     """scale[b] * S^-1 (or scale[b] * pf(S) S^-1) (B, n, n) from slogpf_factors' outputs,
     which are read only."""
     B = d.shape[0]
@@ -228,13 +229,13 @@ def slogpf_inverse(gbuf, d, perm, n, scale=None, adjugate=False):
     ws, wsb = _workspace(L.fx_slogpf_inverse_f32_workspace(B, n), dev)
     st = L.fx_slogpf_inverse_f32(
         _ptr(gbuf), _ptr(d), _ptr(perm), _ptr(scale), B, n, int(bool(adjugate)), _ptr(out),
-        _ptr(ws), wsb, _stream(d),
+        int(x3), _ptr(ws), wsb, _stream(d),
     )
     check(st, "fx_slogpf_inverse_f32")
     return out
 
 
-def slogpf_parts(A, skew_symmetrize, adjugate=False):
+def slogpf_parts(A, skew_symmetrize, adjugate=False, x3=0):
     """(sign, logabs, G) of the (skew-symmetrised) batch from one Parlett-Reid run, G = S^-1
     or, with adjugate, pf(S) S^-1 (float32 only)."""
     if adjugate:
@@ -258,7 +259,7 @@ def slogpf_parts(A, skew_symmetrize, adjugate=False):
     ws, wsb = _workspace(L.fx_slogpf_parts_f32_workspace(B, n), dev)
     st = L.fx_slogpf_parts_f32(
         _ptr(A), B, n, int(bool(skew_symmetrize)), int(bool(adjugate)), _ptr(sign), _ptr(logabs), _ptr(g),
-        _ptr(ws), wsb, _stream(A),
+        int(x3), _ptr(ws), wsb, _stream(A),
     )
     check(st, "fx_slogpf_parts_f32")
     return sign, logabs, g

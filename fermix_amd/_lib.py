@@ -21,28 +21,28 @@ SIGNATURES = {
     "fx_lu_padded_size": (_i32, [_i32]),
     "fx_pf_padded_size": (_i32, [_i32]),
     "fx_slogdet_f32_workspace": (_sz, [_i64, _i32]),
-    "fx_slogdet_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _sz, _p]),
+    "fx_slogdet_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _i32, _p, _sz, _p]),
     "fx_slogdet_parts_f32_workspace": (_sz, [_i64, _i32]),
     "fx_slogdet_parts_f32": (
         ctypes.c_int,
-        [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _sz, _p],
+        [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _i32, _p, _sz, _p],
     ),
     "fx_slogdet_factors_f32_workspace": (_sz, [_i64, _i32]),
-    "fx_slogdet_factors_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _p, _sz, _p]),
+    "fx_slogdet_factors_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _i32, _p, _sz, _p]),
     "fx_slogdet_inverse_f32_workspace": (_sz, [_i64, _i32]),
-    "fx_slogdet_inverse_f32": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _sz, _p]),
+    "fx_slogdet_inverse_f32": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _i32, _p, _i32, _p, _sz, _p]),
     "fx_slogdet_f32_noalloc": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p]),
     "fx_det_parts_f32_workspace": (_sz, [_i64, _i32]),
-    "fx_det_parts_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _sz, _p]),
+    "fx_det_parts_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _i32, _p, _sz, _p]),
     "fx_slogpf_f32_workspace": (_sz, [_i64, _i32]),
     "fx_slogpf_f32": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _sz, _p]),
     "fx_pf_block_columns": (_i32, [_i32]),
     "fx_slogpf_factors_f32_workspace": (_sz, [_i64, _i32]),
     "fx_slogpf_factors_f32": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _sz, _p]),
     "fx_slogpf_inverse_f32_workspace": (_sz, [_i64, _i32]),
-    "fx_slogpf_inverse_f32": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _sz, _p]),
+    "fx_slogpf_inverse_f32": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _i32, _p, _i32, _p, _sz, _p]),
     "fx_slogpf_parts_f32_workspace": (_sz, [_i64, _i32]),
-    "fx_slogpf_parts_f32": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _sz, _p]),
+    "fx_slogpf_parts_f32": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _sz, _p]),
     "fx_slogdet_f64_workspace": (_sz, [_i64, _i32]),
     "fx_slogdet_f64": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _sz, _p]),
     "fx_slogdet_parts_f64_workspace": (_sz, [_i64, _i32]),

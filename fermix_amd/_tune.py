@@ -14,26 +14,37 @@ import os
 
 import torch
 
-# prec values accepted by the public API. "ieee": fp32 MFMA / FMA updates (the only
-# arithmetic of this build). "tf32x3" is accepted for drop-in compatibility with the
-# reference's float32 default: it exists there to reach fp32-level accuracy on tensor
-# cores; gfx950 has no TF32 type, and its IEEE fp32 MFMA path is that accuracy.
-PREC = ("ieee", "tf32x3")
+# prec values accepted by the public API (the reference's PREC, src/fermix/_field.py:20-23):
+#  * "ieee": fp32 MFMA products;
+#  * "bf16x3": each fp32 operand split into three bf16 parts and six bf16 MFMA products,
+#    fp32 accumulation (fp32-level accuracy, several times the MFMA rate of fp32);
+#  * "tf32x3": the reference's name for its three-pass fp32-accuracy mode on tensor cores;
+#    gfx950 has no TF32 type, so it selects the gfx950 counterpart, "bf16x3".
+# The mode applies to the blocked kernels' trailing LU updates and to the inverse /
+# adjugate GEMMs (include/fermix.h, FX_PREC_*); the default is "ieee".
+PREC = ("ieee", "tf32x3", "bf16x3")
+DEFAULT_PREC = "ieee"
 
 
 def check_prec(prec, dtype=None):
-    """"tf32x3" is accepted for float32 only (the reference rejects it for 64-bit types,
+    """The mode a `prec` argument selects ("ieee" or "bf16x3"). The reduced-precision
+    modes are float32-only (the reference rejects "tf32x3" for 64-bit types,
     src/fermix/_field.py:265-275)."""
     if prec is None:
-        return "ieee"
+        return DEFAULT_PREC
     if prec not in PREC:
-        raise ValueError(f"prec must be 'tf32x3' or 'ieee', got {prec!r}")
-    if prec == "tf32x3" and dtype is not None and dtype != torch.float32:
+        raise ValueError(f"prec must be one of {PREC}, got {prec!r}")
+    if prec != "ieee" and dtype is not None and dtype != torch.float32:
         raise ValueError(
-            "prec='tf32x3' applies to float32 / complex64 only; float64 and "
+            f"prec={prec!r} applies to float32 / complex64 only; float64 and "
             "complex128 run in IEEE fp64 (prec='ieee')"
         )
-    return "ieee"
+    return "ieee" if prec == "ieee" else "bf16x3"
+
+
+def prec_flag(mode):
+    """The C ABI's prec value of a mode returned by check_prec."""
+    return 1 if mode == "bf16x3" else 0
 
 
 def check_block(block):

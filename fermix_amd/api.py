@@ -26,7 +26,7 @@ build) -- there is no silent CPU path.
 import torch
 
 from . import _diff
-from ._tune import check_block, check_prec
+from ._tune import check_block, check_prec, prec_flag
 
 _FLOAT_KINDS = (torch.float32, torch.float64, torch.complex64, torch.complex128)
 
@@ -75,32 +75,36 @@ def _flat(a):
 
 def slogdet(a, *, prec=None, unroll_steps=None, block=None):
     """Sign and log|det| of a batch of matrices ``a`` (..., n, n) (reference
-    ``slogdet``, api.py:148-174). prec: "ieee" (default; fp32 MFMA updates) or
-    "tf32x3" (accepted for compatibility: its purpose, fp32-level accuracy, is what the
-    IEEE fp32 MFMA path gives on gfx950, which has no TF32 type). block / unroll_steps:
-    accepted for compatibility and validated; the gfx950 kernels choose their blocking
-    from n (fermix_amd._tune)."""
+    ``slogdet``, api.py:148-174). prec: "ieee" (default; fp32 MFMA products), "bf16x3"
+    (three-way bf16 split, six bf16 MFMA products, fp32 accumulation) or "tf32x3" (the
+    reference's fp32-accuracy three-pass mode; on gfx950, which has no TF32 type, it
+    selects "bf16x3"). The mode applies to the blocked kernels (n > 128): the trailing
+    updates and the inverse's GEMMs. block / unroll_steps: accepted for compatibility
+    and validated, without effect: the gfx950 kernels choose their blocking from n
+    (fermix_amd._tune)."""
     a = _prep(a)
-    check_prec(prec, a.dtype)
+    x3 = prec_flag(check_prec(prec, a.dtype))
     check_block(block)
     _on_device(a)
     A, batch, n = _flat(a)
-    sign, logabs = _diff.slogdet(A)
+    sign, logabs = _diff.slogdet(A, x3)
     return sign.reshape(batch), logabs.reshape(batch)
 
 
 def slogpf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
     """Sign and log|pf| of a batch of skew-symmetric matrices (reference ``slogpf``,
     api.py:177-193): S = (a - a^T)/2 unless skew_symmetrize=False (then ``a`` must be
-    exactly skew); odd n gives (0, -inf)."""
+    exactly skew); odd n gives (0, -inf). prec as for slogdet; it applies to the
+    gradient's GEMMs (the forward's trailing update is memory-bound and runs in fp32).
+    upd_warps: accepted for compatibility, without effect."""
     a = _prep(a)
-    check_prec(prec, a.dtype)
+    x3 = prec_flag(check_prec(prec, a.dtype))
     _on_device(a)
     A, batch, n = _flat(a)
     if n % 2 == 1:
         z = torch.zeros(batch, dtype=a.dtype, device=a.device)
         return z, torch.full(batch, -float("inf"), dtype=a.dtype, device=a.device)
-    sign, logabs = _diff.slogpf(A, bool(skew_symmetrize))
+    sign, logabs = _diff.slogpf(A, bool(skew_symmetrize), x3)
     return sign.reshape(batch), logabs.reshape(batch)
 
 
@@ -108,23 +112,23 @@ def det(a, *, prec=None, unroll_steps=None, block=None):
     """Determinant of a batch of matrices (reference ``det``, api.py:196-212):
     sign * exp(logabs) of the same factorisation."""
     a = _prep(a)
-    check_prec(prec, a.dtype)
+    x3 = prec_flag(check_prec(prec, a.dtype))
     check_block(block)
     _on_device(a)
     A, batch, n = _flat(a)
-    return _diff.det(A).reshape(batch)
+    return _diff.det(A, x3).reshape(batch)
 
 
 def pf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
     """Pfaffian of a batch of skew-symmetric matrices (reference ``pf``, api.py:215-227);
     odd n gives 0."""
     a = _prep(a)
-    check_prec(prec, a.dtype)
+    x3 = prec_flag(check_prec(prec, a.dtype))
     _on_device(a)
     A, batch, n = _flat(a)
     if n % 2 == 1:
         return torch.zeros(batch, dtype=a.dtype, device=a.device)
-    return _diff.pf(A, bool(skew_symmetrize)).reshape(batch)
+    return _diff.pf(A, bool(skew_symmetrize), x3).reshape(batch)
 
 
 __all__ = ["slogdet", "slogpf", "det", "pf", "FermixFallbackWarning", "FermixDeviceError"]

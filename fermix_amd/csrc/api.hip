@@ -114,6 +114,9 @@ static bool al4(const void* p) { return ((uintptr_t)p & 3) == 0; }
 static constexpr int64_t BATCH_CHUNK = 65528;
 static int64_t chunk_batch(int64_t batch) { return batch < BATCH_CHUNK ? batch : BATCH_CHUNK; }
 
+// prec argument of the entry points: FX_PREC_IEEE (fp32 MFMA) or FX_PREC_BF16X3.
+static bool bad_prec(int32_t prec) { return prec != FX_PREC_IEEE && prec != FX_PREC_BF16X3; }
+
 template <class F>
 static int for_chunks(int64_t batch, F&& f) {
   for (int64_t b0 = 0; b0 < batch; b0 += BATCH_CHUNK) {
@@ -140,7 +143,7 @@ const char* fx_status_string(int status) {
   }
 }
 
-int fx_abi_version(void) { return 103; }
+int fx_abi_version(void) { return 200; }
 
 int32_t fx_lu_padded_size(int32_t n) {
   if (n <= 0) return 0;
@@ -165,9 +168,9 @@ size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {
   return lu_large_workspace(chunk_batch(batch), n, false);
 }
 
-int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs,
+int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, int32_t prec,
                    void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(workspace)) return FX_ERR_INVALID_ARGUMENT;
@@ -179,7 +182,7 @@ int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float*
     case FAM_BLOCKED:
       return for_chunks(batch, [&](int64_t b0, int64_t nb) {
         return launch_lu_large(a + b0 * n * n, n, nb, sign + b0, logabs + b0, workspace, workspace_bytes, false,
-                               nullptr, nullptr, s);
+                               nullptr, nullptr, s, nullptr, nullptr, prec);
       });
     default: return FX_ERR_UNSUPPORTED;
   }
@@ -214,9 +217,9 @@ size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n) {
 }
 
 int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_singular,
-                         float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm,
+                         float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm, int32_t prec,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if ((lu == nullptr) != (perm == nullptr)) return FX_ERR_INVALID_ARGUMENT;
@@ -249,7 +252,7 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
       st = lu_fused_factors(fam, ab, n, nb, sg, lg, LU, g0, s);
     } else {
       const size_t wl = lu_large_workspace(nb, n, true);
-      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s);
+      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s, nullptr, nullptr, prec);
       p += align256(wl);
     }
     if (st != FX_OK) return st;
@@ -260,7 +263,8 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
     }
     if (!inv_t) return FX_OK;
     const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
-    return launch_lu_inverse(LU, g0, N, n, nb, sg, zero_singular, inv_t + b0 * n * n, true, p, rest, s);
+    return launch_lu_inverse(LU, g0, N, n, nb, sg, zero_singular, inv_t + b0 * n * n, true, p, rest, s, nullptr,
+                             prec);
   });
 }
 
@@ -270,8 +274,8 @@ size_t fx_slogdet_factors_f32_workspace(int64_t batch, int32_t n) {
 }
 
 int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* lu,
-                           int32_t* perm, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+                           int32_t* perm, int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && (!a || !lu || !perm))) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(lu) || !al16(perm) || !al16(workspace))
@@ -284,7 +288,7 @@ int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign
   const int N = fx_lu_padded_size(n);
   return for_chunks(batch, [&](int64_t b0, int64_t nb) {
     return launch_lu_large(a + b0 * n * n, n, nb, sign + b0, logabs + b0, workspace, workspace_bytes, true, nullptr,
-                           nullptr, s, lu + b0 * N * N, (int*)perm + b0 * N);
+                           nullptr, s, lu + b0 * N * N, (int*)perm + b0 * N, prec);
   });
 }
 
@@ -295,9 +299,9 @@ size_t fx_slogdet_inverse_f32_workspace(int64_t batch, int32_t n) {
 }
 
 int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, const float* scale, int64_t batch,
-                           int32_t n, int32_t zero_singular, float* inv_t, void* workspace, size_t workspace_bytes,
-                           fx_stream_t stream) {
-  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+                           int32_t n, int32_t zero_singular, float* inv_t, int32_t prec, void* workspace,
+                           size_t workspace_bytes, fx_stream_t stream) {
+  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0 || n == 0) return FX_OK;
   if (!lu || !perm || !sign || !inv_t) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(lu) || !al16(perm) || !al4(sign) || !al4(scale) || !al16(inv_t) || !al16(workspace))
@@ -309,7 +313,7 @@ int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, co
   return for_chunks(batch, [&](int64_t b0, int64_t nb) {
     return launch_lu_inverse(lu + b0 * N * N, (const int*)perm + b0 * N, N, n, nb, sign + b0, zero_singular ? 1 : 0,
                              inv_t + b0 * n * n, true, workspace, workspace_bytes, (hipStream_t)stream,
-                             scale ? scale + b0 : nullptr);
+                             scale ? scale + b0 : nullptr, prec);
   });
 }
 
@@ -319,8 +323,8 @@ size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n) {
 }
 
 int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
-                     void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+                     int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && (!a || !adj_t))) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(adj_t) || !al16(workspace)) return FX_ERR_INVALID_ARGUMENT;
@@ -348,7 +352,7 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
       st = lu_fused_factors(fam, ab, n, nb, sg, lg, LU, g0, s);
     } else {
       const size_t wl = lu_large_workspace(nb, n, true);
-      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s);
+      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s, nullptr, nullptr, prec);
       p += align256(wl);
     }
     if (st != FX_OK) return st;
@@ -359,7 +363,7 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
     st = launch_det_adjugate_prep(LU, g0, N, n, nb, dws, &scale, s);
     if (st != FX_OK) return st;
     const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
-    st = launch_lu_inverse(LU, g0, N, n, nb, sg, 0, adj, true, p, rest, s, scale);
+    st = launch_lu_inverse(LU, g0, N, n, nb, sg, 0, adj, true, p, rest, s, scale, prec);
     if (st != FX_OK) return st;
     return launch_det_adjugate_finish(n, nb, dws, adj, s);
   });
@@ -427,9 +431,9 @@ size_t fx_slogpf_inverse_f32_workspace(int64_t batch, int32_t n) {
 }
 
 int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm, const float* scale,
-                          int64_t batch, int32_t n, int32_t adjugate, float* g, void* workspace,
+                          int64_t batch, int32_t n, int32_t adjugate, float* g, int32_t prec, void* workspace,
                           size_t workspace_bytes, fx_stream_t stream) {
-  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0 || n == 0) return FX_OK;
   if (!g) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(gbuf) || !al16(d) || !al16(perm) || !al4(scale) || !al16(g) || !al16(workspace))
@@ -444,7 +448,7 @@ int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm
   return for_chunks(batch, [&](int64_t b0, int64_t nb) {
     return launch_pf_inverse(gbuf + b0 * N * N, fx_pf_block_columns(n), d + b0 * (N / 2), (const int*)perm + b0 * N,
                              N, n, nb, adjugate ? 1 : 0, g + b0 * n * n, workspace, workspace_bytes, s,
-                             scale ? scale + b0 : nullptr);
+                             scale ? scale + b0 : nullptr, prec);
   });
 }
 
@@ -463,9 +467,9 @@ size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n) {
 }
 
 int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
-                        float* sign, float* logabs, float* g, void* workspace, size_t workspace_bytes,
+                        float* sign, float* logabs, float* g, int32_t prec, void* workspace, size_t workspace_bytes,
                         fx_stream_t stream) {
-  if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || !g || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(g) || !al16(workspace)) return FX_ERR_INVALID_ARGUMENT;
@@ -504,7 +508,7 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
     if (st != FX_OK) return st;
     const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
     return launch_pf_inverse(gbuf, fx_pf_block_columns(n), d, perm, N, n, nb, adjugate ? 1 : 0, g + b0 * n * n, p,
-                             rest, s);
+                             rest, s, nullptr, prec);
   });
 }
 

@@ -83,6 +83,41 @@ __device__ __forceinline__ int first_lane(bool p) {
   return m ? (int)__builtin_ctzll(m) : 64;
 }
 
+// Split-bf16x3 products (the fp32-accuracy reduced-precision MFMA mode): x = hi + mid + lo,
+// each part the round-to-nearest bf16 of what the previous parts leave (the residues are
+// exact in fp32), so the three parts hold x to about 24 significant bits. A product over
+// a K = 16 slice takes the six bf16 MFMAs whose terms are at least 2^-16 of the leading
+// one (hi*hi, hi*mid, mid*hi, hi*lo, mid*mid, lo*hi; smallest first), accumulated in fp32:
+// about 2^-24 relative per term, against 2^-24 for the fp32 MFMA.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void split_bf16x3(const float (&x)[8], bf16x8 (&p)[3]) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const __bf16 h = (__bf16)x[u];
+    const float r1 = x[u] - (float)h;
+    const __bf16 m = (__bf16)r1;
+    const float r2 = r1 - (float)m;
+    p[0][u] = h;
+    p[1][u] = m;
+    p[2][u] = (__bf16)r2;
+  }
+}
+
+// acc += A B over K = 16 with v_mfma_f32_32x32x16_bf16: lane l supplies the parts of
+// A[l % 32][8 (l / 32) + u] and B[8 (l / 32) + u][l % 32], u < 8; D is the 32x32 fp32
+// accumulator layout of the 32x32x2 fp32 MFMA.
+__device__ __forceinline__ v16f_t mfma_bf16x3(const bf16x8 (&a)[3], const bf16x8 (&b)[3], v16f_t acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+  return acc;
+}
+
 // fp32 MFMA 16x16x4: D = A(16x4) * B(4x16) + C. Lane l supplies A[l%16][l/16] and
 // B[l/16][l%16]; D/C element (4*(l/16)+v, l%16) sits in item v of lane l.
 __device__ __forceinline__ v4f mfma16(float a, float b, v4f c) {

@@ -44,9 +44,10 @@ int launch_pf_small(const float* A, int n, int skew, int64_t batch, float* sign,
 constexpr int LU_LARGE_MAXN = 4096;
 int lu_large_padded(int n);
 size_t lu_large_workspace(int64_t batch, int n, bool parts, bool external = false);
+// x3 != 0 runs the trailing updates in the split-bf16x3 mode (FX_PREC_BF16X3).
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
                     size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s,
-                    float* W_ext = nullptr, int* g0_ext = nullptr);
+                    float* W_ext = nullptr, int* g0_ext = nullptr, int x3 = 0);
 
 // A^-T from the packed LU (B, N, N) and row map g0 (B, N) into invT (B, n, n); LU is
 // overwritten when in_place and N is a power-of-two multiple of 32 (inverse.hip).
@@ -54,9 +55,10 @@ int inv_padded(int N);
 size_t lu_inverse_workspace(int64_t batch, int N, bool need_copy);
 // With scale != nullptr every member's invT is multiplied by scale[b] (the non-finite
 // check applies to the unscaled values).
+// x3 != 0 runs the GEMMs in the split-bf16x3 mode.
 int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, const float* sign,
                       int zero_singular, float* invT, bool in_place, void* ws, size_t ws_bytes,
-                      hipStream_t s, const float* scale = nullptr);
+                      hipStream_t s, const float* scale = nullptr, int x3 = 0);
 
 // 128 < n <= PF_LARGE_MAXN Parlett-Reid (pf_large.hip); with gbuf the factors
 // (B, N/PB, N, PB) by original row (PB = pf_large_block_cols(N)), d (B, N/2) and perm (B, N).
@@ -70,9 +72,9 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
 // In-place unit-lower (and upper) triangular inverses of a packed (B, Ninv, Ninv) buffer;
 // with active != nullptr only the members with active[b] != 0 are processed.
 int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper, hipStream_t s,
-                       const int* active = nullptr);
+                       const int* active = nullptr, int x3 = 0);
 int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hipStream_t s,
-                              const int* active = nullptr);
+                              const int* active = nullptr, int x3 = 0);
 
 // S^-1 (adjugate = 0) or pf(S) S^-1 (adjugate != 0) as (B, n, n) from the Parlett-Reid
 // factors (gbuf with PB columns per block, d, perm), read only; every member multiplied
@@ -80,7 +82,7 @@ int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hip
 size_t pf_inverse_workspace(int64_t batch, int N);
 int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm, int N, int n, int64_t batch,
                       int adjugate, float* out, void* ws, size_t ws_bytes, hipStream_t s,
-                      const float* scale = nullptr);
+                      const float* scale = nullptr, int x3 = 0);
 
 // parity[b] = parity (0 even, 1 odd) of the permutation perm[b] of 0..N-1, N <= 2048.
 int launch_perm_parity(const int* perm, int N, int64_t batch, int* parity, hipStream_t s);
@@ -113,6 +115,7 @@ struct GemmDesc {
   int lower_only;  // only tiles on/below the diagonal; C[j][i] = mirror * C[i][j]
   float mirror;
   int xcd8;  // set by launch_gemm: the batch is a multiple of 8 (XCD-aware tile order)
+  int x3;    // products in the split-bf16x3 mode (FX_PREC_BF16X3) instead of fp32 MFMA
   const int* active;  // optional (batch,) mask: members with active[b] == 0 are skipped
   // Optional transposed, row-permuted output in place of C (64 x 64 tiles, one batch
   // index, not lower_only): tout[b][g0[b][j]][i] = scale[b] * alpha (op(A) op(B))[i][j]

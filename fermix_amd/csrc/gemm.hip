@@ -50,7 +50,7 @@ __device__ __forceinline__ bool mask_upper(int m) { return m == MASK_UPPER || m 
 // Tile loads: VEC uses 16-byte global loads along the operand's contiguous dimension
 // (requires that dimension, the leading dimensions, batch strides and base pointers to be
 // multiples of 4 floats), otherwise one float per load. Masks are applied in registers.
-template <int BM, int BN, bool VEC, int MK, bool BS = false>
+template <int BM, int BN, bool VEC, int MK, bool BS = false, bool X3 = false>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
   // operand masks: MK = 4 maskA + maskB fixed at compile time (the combinations this
   // library uses), so each mask test folds to one compare per element; MK < 0 reads them
@@ -304,18 +304,42 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
     for (int k0 = klo; k0 < khi; k0 += GBK) {
       const bool more = k0 + GBK < khi;
       if (more) load_stage(k0 + GBK);
+      if constexpr (X3) {
+        // the stage's K = 16 in one bf16x3 product per accumulator: lane operands are the
+        // eight k = 8 lh + u of its row (A) / column (B), split in registers
+        bf16x8 ap[TM][3], bp[TN][3];
 #pragma unroll
-      for (int kp = 0; kp < GBK / 2; ++kp) {
-        float av[TM], bv[TN];
+        for (int a = 0; a < TM; ++a) {
+          float f[8];
 #pragma unroll
-        for (int a = 0; a < TM; ++a) av[a] = As[buf][(2 * kp + lh) * LDSA + wm + 32 * a + l32];
+          for (int u = 0; u < 8; ++u) f[u] = As[buf][(8 * lh + u) * LDSA + wm + 32 * a + l32];
+          split_bf16x3(f, ap[a]);
+        }
 #pragma unroll
-        for (int b = 0; b < TN; ++b) bv[b] = Bs[buf][(2 * kp + lh) * LDSB + wn + 32 * b + l32];
+        for (int b = 0; b < TN; ++b) {
+          float f[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) f[u] = Bs[buf][(8 * lh + u) * LDSB + wn + 32 * b + l32];
+          split_bf16x3(f, bp[b]);
+        }
 #pragma unroll
         for (int a = 0; a < TM; ++a)
 #pragma unroll
-          for (int b = 0; b < TN; ++b)
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+          for (int b = 0; b < TN; ++b) acc[a][b] = mfma_bf16x3(ap[a], bp[b], acc[a][b]);
+      } else {
+#pragma unroll
+        for (int kp = 0; kp < GBK / 2; ++kp) {
+          float av[TM], bv[TN];
+#pragma unroll
+          for (int a = 0; a < TM; ++a) av[a] = As[buf][(2 * kp + lh) * LDSA + wm + 32 * a + l32];
+#pragma unroll
+          for (int b = 0; b < TN; ++b) bv[b] = Bs[buf][(2 * kp + lh) * LDSB + wn + 32 * b + l32];
+#pragma unroll
+          for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+              acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+        }
       }
       if (more) {
         store_stage(buf ^ 1, k0 + GBK, plain_stage(k0 + GBK));
@@ -399,8 +423,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
 // -- zeros outside the matrix, the triangle masks -- between two barriers.
 // Launch bound of 4 waves per SIMD: the compiler then fits the kernel in 116 VGPRs
 // (accumulators included) without scratch, against 168 + 64 left to itself.
-template <bool TA, int MK, bool BS = false>
-__global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
+template <bool TA, int MK, bool BS = false, bool X3 = false>
+__global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
   const int maskA = MK >= 0 ? (MK >> 2) : d.maskA;  // compile-time masks as in gemm_kernel
   const int maskB = MK >= 0 ? (MK & 3) : d.maskB;
   constexpr int BM = 128, BN = 128, LDA_ = BM + 4, LDB_ = BN + 4;
@@ -543,18 +567,41 @@ __global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
     for (int k0 = klo; k0 < khi; k0 += GBK) {
       const bool more = k0 + GBK < khi;
       if (more) load_stage(k0 + GBK);
+      if constexpr (X3) {
+        // as in gemm_kernel: the stage's K = 16 in one bf16x3 product per accumulator;
+        // A's parts first, then each B column block's, used by both A row blocks
+        bf16x8 ap[2][3];
 #pragma unroll
-      for (int kp = 0; kp < GBK / 2; ++kp) {
-        float av[2], bv[2];
+        for (int a = 0; a < 2; ++a) {
+          float f[8];
 #pragma unroll
-        for (int a = 0; a < 2; ++a) av[a] = As[buf][(2 * kp + lh) * LDA_ + wm + 32 * a + l32];
+          for (int u = 0; u < 8; ++u) f[u] = As[buf][(8 * lh + u) * LDA_ + wm + 32 * a + l32];
+          split_bf16x3(f, ap[a]);
+        }
 #pragma unroll
-        for (int b = 0; b < 2; ++b) bv[b] = Bs[buf][(2 * kp + lh) * LDB_ + wn + 32 * b + l32];
+        for (int b = 0; b < 2; ++b) {
+          float f[8];
+          bf16x8 bp[3];
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+          for (int u = 0; u < 8; ++u) f[u] = Bs[buf][(8 * lh + u) * LDB_ + wn + 32 * b + l32];
+          split_bf16x3(f, bp);
 #pragma unroll
-          for (int b = 0; b < 2; ++b)
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+          for (int a = 0; a < 2; ++a) acc[a][b] = mfma_bf16x3(ap[a], bp, acc[a][b]);
+        }
+      } else {
+#pragma unroll
+        for (int kp = 0; kp < GBK / 2; ++kp) {
+          float av[2], bv[2];
+#pragma unroll
+          for (int a = 0; a < 2; ++a) av[a] = As[buf][(2 * kp + lh) * LDA_ + wm + 32 * a + l32];
+#pragma unroll
+          for (int b = 0; b < 2; ++b) bv[b] = Bs[buf][(2 * kp + lh) * LDB_ + wn + 32 * b + l32];
+#pragma unroll
+          for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+              acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+        }
       }
       if (more) {
         store_stage(buf ^ 1);
@@ -601,8 +648,8 @@ __global__ __launch_bounds__(256, 4) void gemm128_kernel(GemmDesc d) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
-  if (d.M <= 0 || d.N <= 0 || batch <= 0 || nb2 <= 0) return FX_OK;
+template <bool X3>
+static int launch_gemm_t(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
   if (d.lower_only && d.M != d.N) return FX_ERR_INVALID_ARGUMENT;
   // 64 x 64 tiles throughout: with one 32x32 accumulator per wave many more workgroups
   // stay resident per CU than with 128 x 128 tiles, which hides the operand and C
@@ -649,20 +696,20 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
       const bool ua = d.transA && d.maskA == MASK_UPPER_UNIT;
       if (big) {
         const dim3 grid2(tiles2, (unsigned)nb, nb2);
-        if (ua) hipLaunchKernelGGL((gemm128_kernel<true, 4 * MASK_UPPER_UNIT, true>), grid2, dim3(256), 0, s, e);
-        else if (d.transA) hipLaunchKernelGGL((gemm128_kernel<true, -1, true>), grid2, dim3(256), 0, s, e);
-        else hipLaunchKernelGGL((gemm128_kernel<false, -1, true>), grid2, dim3(256), 0, s, e);
+        if (ua) hipLaunchKernelGGL((gemm128_kernel<true, 4 * MASK_UPPER_UNIT, true, X3>), grid2, dim3(256), 0, s, e);
+        else if (d.transA) hipLaunchKernelGGL((gemm128_kernel<true, -1, true, X3>), grid2, dim3(256), 0, s, e);
+        else hipLaunchKernelGGL((gemm128_kernel<false, -1, true, X3>), grid2, dim3(256), 0, s, e);
       } else {
         const dim3 grid(tiles, (unsigned)nb, nb2);
-        if (ua) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, 4 * MASK_UPPER_UNIT, true>), grid, dim3(256), 0, s, e);
-        else hipLaunchKernelGGL((gemm_kernel<BM, BN, true, -1, true>), grid, dim3(256), 0, s, e);
+        if (ua) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, 4 * MASK_UPPER_UNIT, true, X3>), grid, dim3(256), 0, s, e);
+        else hipLaunchKernelGGL((gemm_kernel<BM, BN, true, -1, true, X3>), grid, dim3(256), 0, s, e);
       }
       if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
       continue;
     }
     if (big) {
       const dim3 grid2(tiles2, (unsigned)nb, nb2);
-#define FX_GEMM128(T, K) hipLaunchKernelGGL((gemm128_kernel<T, K>), grid2, dim3(256), 0, s, e)
+#define FX_GEMM128(T, K) hipLaunchKernelGGL((gemm128_kernel<T, K, false, X3>), grid2, dim3(256), 0, s, e)
       const int mk = 4 * d.maskA + d.maskB;
       if (d.transA) {
         if (mk == 4 * MASK_UPPER_UNIT + MASK_NONE) FX_GEMM128(true, 4 * MASK_UPPER_UNIT + MASK_NONE);
@@ -684,7 +731,7 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
       continue;
     }
     const dim3 grid(tiles, (unsigned)nb, nb2);
-#define FX_GEMM_MK(K) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, K>), grid, dim3(256), 0, s, e)
+#define FX_GEMM_MK(K) hipLaunchKernelGGL((gemm_kernel<BM, BN, true, K, false, X3>), grid, dim3(256), 0, s, e)
     if (vec) {
       switch (4 * d.maskA + d.maskB) {
         case 4 * MASK_NONE + MASK_NONE: FX_GEMM_MK(4 * MASK_NONE + MASK_NONE); break;
@@ -697,12 +744,17 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
         default: FX_GEMM_MK(-1); break;
       }
     } else {
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, false, -1>), grid, dim3(256), 0, s, e);
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, false, -1, false, X3>), grid, dim3(256), 0, s, e);
     }
 #undef FX_GEMM_MK
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
+}
+
+int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s) {
+  if (d.M <= 0 || d.N <= 0 || batch <= 0 || nb2 <= 0) return FX_OK;
+  return d.x3 ? launch_gemm_t<true>(d, batch, nb2, s) : launch_gemm_t<false>(d, batch, nb2, s);
 }
 
 }  // namespace fx

@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void zero_bad_kernel(const int* __restrict__ b
 // upper U~ (upper part incl. diagonal) packed in T (B, Ninv, Ninv); Tmp holds
 // B * Ninv^2 / 4 floats.
 int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper, hipStream_t s,
-                       const int* active) {
+                       const int* active, int x3) {
   const int64_t NN = (int64_t)Ninv * Ninv;
   const int D = Ninv < 128 ? Ninv : 128;  // diagonal blocks inverted whole in LDS
   if (D == 32)
@@ -236,6 +236,7 @@ int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper
     const int64_t dstride = (int64_t)2 * sz * (Ninv + 1);  // next pair along the diagonal
     GemmDesc d = {};
     d.active = active;
+    d.x3 = x3;
     d.M = d.N = d.K = sz;
     d.sA = d.sB = NN;
     d.sC = NN;
@@ -256,6 +257,7 @@ int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper
     // X21 = -X22 * Tmp
     GemmDesc e = {};
     e.active = active;
+    e.x3 = x3;
     e.M = e.N = e.K = sz;
     e.A = T + (int64_t)sz * Ninv + sz;
     e.maskA = MASK_LOWER_UNIT;
@@ -278,6 +280,7 @@ int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper
     // U: Tmp = U12 * Y22
     GemmDesc f = {};
     f.active = active;
+    f.x3 = x3;
     f.M = f.N = f.K = sz;
     f.A = T + sz;
     f.lda = Ninv;
@@ -299,6 +302,7 @@ int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper
     // Y12 = -Y11 * Tmp
     GemmDesc h = {};
     h.active = active;
+    h.x3 = x3;
     h.M = h.N = h.K = sz;
     h.A = T;
     h.maskA = MASK_UPPER;
@@ -322,8 +326,8 @@ int launch_tri_inverse(float* T, int Ninv, int64_t batch, float* Tmp, bool upper
 }
 
 int launch_unit_lower_inverse(float* T, int Ninv, int64_t batch, float* Tmp, hipStream_t s,
-                              const int* active) {
-  return launch_tri_inverse(T, Ninv, batch, Tmp, false, s, active);
+                              const int* active, int x3) {
+  return launch_tri_inverse(T, Ninv, batch, Tmp, false, s, active, x3);
 }
 
 int inv_padded(int N) {
@@ -346,7 +350,7 @@ size_t lu_inverse_workspace(int64_t batch, int N, bool need_copy) {
 
 int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, const float* sign,
                       int zero_singular, float* invT, bool in_place, void* ws, size_t ws_bytes,
-                      hipStream_t s, const float* scale) {
+                      hipStream_t s, const float* scale, int x3) {
   const int Ninv = inv_padded(N);
   const bool need_copy = !(in_place && Ninv == N);
   if (!ws || ws_bytes < lu_inverse_workspace(batch, N, need_copy)) return FX_ERR_WORKSPACE;
@@ -367,12 +371,13 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
                        LU, N, T, Ninv);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
-  int st0 = launch_tri_inverse(T, Ninv, batch, Tmp, true, s);
+  int st0 = launch_tri_inverse(T, Ninv, batch, Tmp, true, s, nullptr, x3);
   if (st0 != FX_OK) return st0;
   // Z = U~^-1 L^-1 (the leading N x N block) stored straight as invT = P^T Z^T:
   // invT[g0[c]][i] = Z[i][c] for i < n and g0[c] < n, with the non-finite tile flags
   {
     GemmDesc d = {};
+    d.x3 = x3;
     d.M = d.N = N;
     d.K = Ninv;
     d.A = T;

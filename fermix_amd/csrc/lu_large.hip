@@ -744,8 +744,8 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // rmapC[p].
 // XCD-aware tile order when the batch is a multiple of 8 (one matrix's L21 / U12 fetched
 // into one L2).
-template <int KC>
-__global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W, int N, int r0, int ntc,
+template <int KC, bool X3 = false>
+__global__ __launch_bounds__(256, X3 ? 3 : 4) void lu_update_kernel(float* __restrict__ W, int N, int r0, int ntc,
                                                         const float* __restrict__ A0, const int* __restrict__ rmapC) {
   constexpr int LDA_ = 64 + 1, LDB_ = 64 + 4;
   __shared__ float As[64 * LDA_];                 // L21 chunk, (i, k)
@@ -810,10 +810,28 @@ __global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W
     }
     __syncthreads();
     if (c + 1 < KC) load(c + 1);
+    if constexpr (X3) {
+      // split-bf16x3: four K = 16 slices, lane operands the eight k = 16 q + 8 lh + u of
+      // its row of -L21 and its column of U12
 #pragma unroll
-    for (int kp = 0; kp < 32; ++kp)
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(-As[(wm + l32) * LDA_ + 2 * kp + lh], Bs[(2 * kp + lh) * LDB_ + wn + l32],
-                                                 acc, 0, 0, 0);
+      for (int q = 0; q < 4; ++q) {
+        float fa[8], fb[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          fa[u] = -As[(wm + l32) * LDA_ + 16 * q + 8 * lh + u];
+          fb[u] = Bs[(16 * q + 8 * lh + u) * LDB_ + wn + l32];
+        }
+        bf16x8 pa[3], pb[3];
+        split_bf16x3(fa, pa);
+        split_bf16x3(fb, pb);
+        acc = mfma_bf16x3(pa, pb, acc);
+      }
+    } else {
+#pragma unroll
+      for (int kp = 0; kp < 32; ++kp)
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(-As[(wm + l32) * LDA_ + 2 * kp + lh],
+                                                   Bs[(2 * kp + lh) * LDB_ + wn + l32], acc, 0, 0, 0);
+    }
   }
 #pragma unroll
   for (int v = 0; v < 16; ++v) Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32] = acc[v];
@@ -822,12 +840,16 @@ __global__ __launch_bounds__(256, 4) void lu_update_kernel(float* __restrict__ W
 // Grid of the trailing update: ntr x ntc tiles per matrix, batches of at most 65535.
 template <int KC>
 static int launch_update(float* W, int N, int64_t batch, int r0, int ntr, int ntc, const float* A0,
-                         const int* rmapC, hipStream_t s) {
+                         const int* rmapC, hipStream_t s, int x3) {
   const int64_t NN = (int64_t)N * N;
   for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
     const int64_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
-    hipLaunchKernelGGL((lu_update_kernel<KC>), dim3(ntr * ntc, (unsigned)nb), dim3(256), 0, s, W + b0 * NN, N, r0,
-                       ntc, A0 ? A0 + b0 * NN : nullptr, rmapC ? rmapC + b0 * N : nullptr);
+    if (x3)
+      hipLaunchKernelGGL((lu_update_kernel<KC, true>), dim3(ntr * ntc, (unsigned)nb), dim3(256), 0, s, W + b0 * NN, N,
+                         r0, ntc, A0 ? A0 + b0 * NN : nullptr, rmapC ? rmapC + b0 * N : nullptr);
+    else
+      hipLaunchKernelGGL((lu_update_kernel<KC, false>), dim3(ntr * ntc, (unsigned)nb), dim3(256), 0, s, W + b0 * NN, N,
+                         r0, ntc, A0 ? A0 + b0 * NN : nullptr, rmapC ? rmapC + b0 * N : nullptr);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
@@ -847,7 +869,7 @@ static int launch_update(float* W, int N, int64_t batch, int r0, int ntr, int nt
 // first pair, reading the input in place of a copy, composes both into srcs[2].
 template <int MR, int NT>
 static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int* const srcs[3], float* X,
-                      int* g0, bool fact, const float* A_in, hipStream_t s) {
+                      int* g0, bool fact, const float* A_in, hipStream_t s, int x3) {
   constexpr int PW = 64;
   const int nblk = N / PW;
   constexpr int MAXM = MR < 1024 ? 1024 : MR;
@@ -887,12 +909,12 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
     if (!paired) {
       st = urow(r0, src, 0, fact ? r0 / 64 : 0, nright, A0, nullptr, -1, nullptr);
       if (st == FX_OK && nright > 0)
-        st = launch_update<1>(W, N, batch, r0, nright, nright, A0, A0 ? src : nullptr, s);
+        st = launch_update<1>(W, N, batch, r0, nright, nright, A0, A0 ? src : nullptr, s, x3);
     } else if ((blk & 1) == 0) {
       // first block of a pair: U rows, then the update of the next panel's columns only
       st = urow(r0, src, 0, fact ? r0 / 64 : 0, nright, A0, nullptr, -1, nullptr);
       if (st == FX_OK && nright > 0)
-        st = launch_update<1>(W, N, batch, r0, nright, 1, A0, A0 ? src : nullptr, s);
+        st = launch_update<1>(W, N, batch, r0, nright, 1, A0, A0 ? src : nullptr, s, x3);
     } else {
       // second block: U rows with the first block's deferred update, then both blocks'
       // update of the trailing matrix; the first pair reads the input through both maps
@@ -901,7 +923,7 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
       st = urow(r0, src, 0, fact ? rp / 64 : 0, nright, Ain, Ain ? srcs[0] : nullptr, rp,
                 Ain && nright > 0 ? srcs[2] : nullptr);
       if (st == FX_OK && nright > 0)
-        st = launch_update<2>(W, N, batch, rp, nright, nright, Ain, Ain ? srcs[2] : nullptr, s);
+        st = launch_update<2>(W, N, batch, rp, nright, nright, Ain, Ain ? srcs[2] : nullptr, s, x3);
     }
     if (st != FX_OK) return st;
   }
@@ -912,7 +934,7 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
 // and the composed row map g0 (parts only) through *g0_out.
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
                     size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s, float* W_ext,
-                    int* g0_ext) {
+                    int* g0_ext, int x3) {
   const int N = lu_large_padded(n);
   const int PW = lu_panel_width(N);
   const int nblk = N / PW;
@@ -954,11 +976,11 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   }
   int st;
   if (N <= 1024)
-    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, srcs, X, g0, parts, direct ? A : nullptr, s);
+    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, srcs, X, g0, parts, direct ? A : nullptr, s, x3);
   else if (N <= 2048)
-    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s);
+    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3);
   else
-    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s);
+    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3);
   if (st != FX_OK) return st;
   hipLaunchKernelGGL(lu_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, piv, nsw, N,
                      nblk, sign, logabs, batch);

@@ -70,7 +70,7 @@ extern "C" int fx_slogdet_f32_noalloc(const float* a, int64_t batch, int32_t n, 
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if (fx_slogdet_f32_workspace(batch, n) == 0)  // no workspace needed (or n unsupported)
-    return fx_slogdet_f32(a, batch, n, sign, logabs, nullptr, 0, stream);
+    return fx_slogdet_f32(a, batch, n, sign, logabs, FX_PREC_IEEE, nullptr, 0, stream);
   const int64_t m = fitting_batch(batch, n);
   if (m == 0) return FX_ERR_UNSUPPORTED;  // one matrix's workspace exceeds the scratch array
   void* ws = nullptr;
@@ -78,8 +78,8 @@ extern "C" int fx_slogdet_f32_noalloc(const float* a, int64_t batch, int32_t n, 
   if (st != FX_OK) return st;
   for (int64_t b0 = 0; b0 < batch; b0 += m) {
     const int64_t nb = batch - b0 < m ? batch - b0 : m;
-    const int r = fx_slogdet_f32(a + b0 * n * n, nb, n, sign + b0, logabs + b0, ws, FX_NOALLOC_SCRATCH_BYTES,
-                                 stream);
+    const int r = fx_slogdet_f32(a + b0 * n * n, nb, n, sign + b0, logabs + b0, FX_PREC_IEEE, ws,
+                                 FX_NOALLOC_SCRATCH_BYTES, stream);
     if (r != FX_OK) return r;
   }
   return FX_OK;

@@ -264,7 +264,8 @@ size_t pf_inverse_workspace(int64_t batch, int N) {
 }
 
 int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm, int N, int n, int64_t batch,
-                      int adjugate, float* out, void* ws, size_t ws_bytes, hipStream_t s, const float* scale) {
+                      int adjugate, float* out, void* ws, size_t ws_bytes, hipStream_t s, const float* scale,
+                      int x3) {
   const int Ninv = inv_padded(N);
   if (!ws || ws_bytes < pf_inverse_workspace(batch, N)) return FX_ERR_WORKSPACE;
   char* p = (char*)ws;
@@ -300,11 +301,12 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
     hipLaunchKernelGGL(pf_assemble_kernel, dim3((unsigned)Ninv, (unsigned)batch), dim3(256), 0, s, gbuf, PB, N,
                        perm, dinv, T, Ninv, active);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    int st = launch_unit_lower_inverse(T, Ninv, batch, Tmp, s, active);
+    int st = launch_unit_lower_inverse(T, Ninv, batch, Tmp, s, active, x3);
     if (st != FX_OK) return st;
     {
       // R = Y^T DY: op(A) = Y^T (upper, unit diagonal), lower tiles, mirrored skew
       GemmDesc g = {};
+      g.x3 = x3;
       g.M = g.N = g.K = N;
       g.A = T;
       g.transA = 1;

@@ -53,6 +53,21 @@ extern "C" {
 
 typedef void* fx_stream_t; /* hipStream_t */
 
+/* prec: the arithmetic of the MFMA products (the reference's `prec`, src/fermix/_field.py:
+ * 20-23, 173-190, 262-275, whose fp32 modes are "ieee" and "tf32x3"):
+ *  - FX_PREC_IEEE: fp32 MFMA (v_mfma_f32_32x32x2f32 / 16x16x4f32);
+ *  - FX_PREC_BF16X3: every fp32 operand split as hi + mid + lo bf16 (round to nearest, the
+ *    residues exact in fp32) and the six products with terms down to 2^-16 of the leading
+ *    one on v_mfma_f32_32x32x16_bf16, fp32 accumulation -- gfx950's counterpart of the
+ *    reference's tf32x3 (three reduced-precision passes at fp32 accuracy).
+ * It applies to the blocked (n > 128) LU trailing updates and to every GEMM of the
+ * inverses (A^-T, S^-1, the adjugates). The n <= 128 kernels, the panels, the U-row solves,
+ * the diagonal-block inverses and the Parlett-Reid trailing update (bound by memory
+ * traffic, not by the MFMA rate) compute in fp32 in both modes; the slogpf forward entry
+ * points therefore take no prec. */
+#define FX_PREC_IEEE 0
+#define FX_PREC_BF16X3 1
+
 /* Human-readable text of a status code (static storage). */
 const char* fx_status_string(int status);
 
@@ -74,7 +89,7 @@ int32_t fx_pf_padded_size(int32_t n);
  * Replaces `_lu_core` (src/fermix/_lu.py:543-611) as called by `_slogdet_core`
  * (src/fermix/_diff.py:42-49); kernels K1-K4 of the reference (_lu.py:54-393). */
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n);
-int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs,
+int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, int32_t prec,
                    void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
 /* The same factorisation as fx_slogdet_f32 (identical arithmetic, so sign / logabs are
@@ -89,7 +104,7 @@ int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float*
  * (src/fermix/_diff.py:62-77); kernels K7-K10 (_inverse.py:35-499). */
 size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n);
 int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_singular,
-                         float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm,
+                         float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm, int32_t prec,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
 /* The factors of fx_slogdet_parts_f32 alone, formed straight in the caller's lu
@@ -99,7 +114,7 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
  * forward pass, and the inverse, run by the backward pass once the cotangent is known. */
 size_t fx_slogdet_factors_f32_workspace(int64_t batch, int32_t n);
 int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* lu,
-                           int32_t* perm, void* workspace, size_t workspace_bytes, fx_stream_t stream);
+                           int32_t* perm, int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
 /* inv_t (batch, n, n) = scale[b] * A^-T (scale NULL: 1) from the factors lu / perm of
  * fx_slogdet_factors_f32 (or fx_slogdet_parts_f32) and their sign, with the guards of
@@ -110,8 +125,8 @@ int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign
  * cotangent product of the jvp rule (src/fermix/_diff.py:92-126) in one pass. */
 size_t fx_slogdet_inverse_f32_workspace(int64_t batch, int32_t n);
 int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, const float* scale, int64_t batch,
-                           int32_t n, int32_t zero_singular, float* inv_t, void* workspace, size_t workspace_bytes,
-                           fx_stream_t stream);
+                           int32_t n, int32_t zero_singular, float* inv_t, int32_t prec, void* workspace,
+                           size_t workspace_bytes, fx_stream_t stream);
 
 /* adj_t (batch, n, n) = adj(A)^T = d det(A) / dA, finite and exact for singular A, plus
  * sign / logabs bit-identical to fx_slogdet_f32 (det = sign * exp(logabs) is the value
@@ -125,12 +140,12 @@ int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, co
  * rule of `_det_diff` (:288-301). */
 size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n);
 int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
-                     void* workspace, size_t workspace_bytes, fx_stream_t stream);
+                     int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
 /* No counterpart in the reference: fx_slogdet_f32 for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). Same arguments without the workspace; sign / logabs bit-identical to
- * fx_slogdet_f32. The blocked kernels' workspace (n > 128) is a device array of the
+ * hipMalloc). Same arguments without the workspace (and prec: FX_PREC_IEEE); sign / logabs
+ * bit-identical to fx_slogdet_f32 with FX_PREC_IEEE. The blocked kernels' workspace (n > 128) is a device array of the
  * library of FX_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends); a batch whose
  * workspace exceeds it runs in consecutive sub-batches that fit. n whose single-matrix
  * workspace exceeds the array (n > 4032) returns FX_ERR_UNSUPPORTED. The call allocates
@@ -175,7 +190,7 @@ int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew
  * product of the jvp rule (src/fermix/_diff.py:129-156) in its final gather. */
 size_t fx_slogpf_inverse_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm, const float* scale,
-                          int64_t batch, int32_t n, int32_t adjugate, float* g, void* workspace,
+                          int64_t batch, int32_t n, int32_t adjugate, float* g, int32_t prec, void* workspace,
                           size_t workspace_bytes, fx_stream_t stream);
 
 /* The same run as fx_slogpf_f32 (bit-identical sign / logabs) plus g (batch, n, n)
@@ -190,7 +205,7 @@ int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm
  * helpers `_pf_adj_coeffs` / `_lifted_mean` (src/fermix/_fallback.py:138-176). */
 size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
-                        int32_t adjugate, float* sign, float* logabs, float* g, void* workspace,
+                        int32_t adjugate, float* sign, float* logabs, float* g, int32_t prec, void* workspace,
                         size_t workspace_bytes, fx_stream_t stream);
 
 /* ---------------------------------------------------------------- float64

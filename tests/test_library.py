@@ -39,15 +39,15 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_calls():
     L = _lib.lib()
-    assert L.fx_abi_version() == 103
+    assert L.fx_abi_version() == 200
     assert L.fx_status_string(0) == b"ok"
     assert L.fx_lu_padded_size(100) == 112
     assert L.fx_pf_padded_size(128) == 128
     # argument validation happens before any device work
-    assert L.fx_slogdet_f32(None, -1, 4, None, None, None, 0, None) == 1
-    assert L.fx_slogdet_f32(None, 0, 4, None, None, None, 0, None) == 0
-    assert L.fx_det_parts_f32(None, -1, 4, None, None, None, None, 0, None) == 1
-    assert L.fx_det_parts_f32(None, 2, 4, None, None, None, None, 0, None) == 1
+    assert L.fx_slogdet_f32(None, -1, 4, None, None, 0, None, 0, None) == 1
+    assert L.fx_slogdet_f32(None, 0, 4, None, None, 0, None, 0, None) == 0
+    assert L.fx_det_parts_f32(None, -1, 4, None, None, None, 0, None, 0, None) == 1
+    assert L.fx_det_parts_f32(None, 2, 4, None, None, None, 0, None, 0, None) == 1
     assert L.fx_det_parts_f32_workspace(4, 5000) == 0 and L.fx_det_parts_f32_workspace(4, 4096) > 0
     assert L.fx_det_parts_f32_workspace(4, 64) > L.fx_slogdet_parts_f32_workspace(4, 64)
 
@@ -100,7 +100,13 @@ def test_api_errors():
 
 def test_tune_table():
     assert _tune.check_prec(None) == "ieee"
-    assert _tune.check_prec("tf32x3") == "ieee"
+    assert _tune.check_prec("ieee") == "ieee"
+    assert _tune.check_prec("tf32x3") == "bf16x3" and _tune.check_prec("bf16x3") == "bf16x3"
+    assert _tune.prec_flag("bf16x3") == 1 and _tune.prec_flag("ieee") == 0
+    with pytest.raises(ValueError):
+        _tune.check_prec("bf16x3", torch.float64)
+    with pytest.raises(ValueError):
+        _tune.check_prec("fp16")
     assert _tune.kernel_family(128) == "fused-lds"
     assert _tune.kernel_family(32) == "tiny-wave" and _tune.kernel_family(32, "slogpf") == "fused-lds"
     assert _tune.kernel_family(4096, "slogpf") == "blocked" and _tune.kernel_family(4097) == "unsupported"
@@ -115,20 +121,20 @@ def test_misaligned_pointers_rejected():
     good, bad = 0x10000, 0x10004
     ws = 0x20000
     for n in (8, 100, 129, 512):
-        assert L.fx_slogdet_f32(bad, 2, n, good, good, ws, 1 << 40, None) == 1
-        assert L.fx_slogdet_f32(good, 2, n, good, good, bad, 1 << 40, None) == 1
-        assert L.fx_slogdet_f32(good, 2, n, good + 2, good, ws, 1 << 40, None) == 1
-        assert L.fx_slogdet_parts_f32(good, 2, n, 1, good, good, bad, None, None, ws, 1 << 40, None) == 1
-        assert L.fx_slogdet_parts_f32(good, 2, n, 1, good, good, good, bad, good, ws, 1 << 40, None) == 1
-        assert L.fx_slogdet_parts_f32(good, 2, n, 1, good, good, good, good, bad, ws, 1 << 40, None) == 1
-        assert L.fx_slogdet_factors_f32(good, 2, n, good, good, bad, good, ws, 1 << 40, None) == 1
-        assert L.fx_slogdet_inverse_f32(bad, good, good, None, 2, n, 1, good, ws, 1 << 40, None) == 1
-        assert L.fx_slogdet_inverse_f32(good, good, good, None, 2, n, 1, good, bad, 1 << 40, None) == 1
-        assert L.fx_det_parts_f32(good, 2, n, good, good, bad, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_f32(bad, 2, n, good, good, 0, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_f32(good, 2, n, good, good, 0, bad, 1 << 40, None) == 1
+        assert L.fx_slogdet_f32(good, 2, n, good + 2, good, 0, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_parts_f32(good, 2, n, 1, good, good, bad, None, None, 0, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_parts_f32(good, 2, n, 1, good, good, good, bad, good, 0, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_parts_f32(good, 2, n, 1, good, good, good, good, bad, 0, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_factors_f32(good, 2, n, good, good, bad, good, 0, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_inverse_f32(bad, good, good, None, 2, n, 1, good, 0, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_inverse_f32(good, good, good, None, 2, n, 1, good, 0, bad, 1 << 40, None) == 1
+        assert L.fx_det_parts_f32(good, 2, n, good, good, bad, 0, ws, 1 << 40, None) == 1
         assert L.fx_slogpf_f32(bad, 2, n, 0, good, good, ws, 1 << 40, None) == 1
         assert L.fx_slogpf_factors_f32(good, 2, n, 0, good, good, bad, good, good, ws, 1 << 40, None) == 1
-        assert L.fx_slogpf_inverse_f32(good, good, good, None, 2, n, 0, bad, ws, 1 << 40, None) == 1
-        assert L.fx_slogpf_parts_f32(bad, 2, n, 0, 0, good, good, good, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_inverse_f32(good, good, good, None, 2, n, 0, bad, 0, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_parts_f32(bad, 2, n, 0, 0, good, good, good, 0, ws, 1 << 40, None) == 1
         assert L.fx_slogdet_f64(bad, 2, n, good, good, ws, 1 << 40, None) == 1
         assert L.fx_slogdet_parts_f64(good, 2, n, good, good, bad, ws, 1 << 40, None) == 1
         assert L.fx_slogpf_f64(good, 2, n, 0, good + 4, good, ws, 1 << 40, None) == 1
@@ -170,3 +176,17 @@ def test_noalloc_host_checks():
     for n in (4033, 4096):
         assert L.fx_slogdet_f32_noalloc(good, 4, n, good, good, None) == 4
     assert L.fx_slogdet_f32_noalloc(good, 4, 5000, good, good, None) == 4
+
+
+def test_prec_argument_validated():
+    """prec outside {FX_PREC_IEEE, FX_PREC_BF16X3} is rejected before any device work."""
+    L = _lib.lib()
+    good, ws = 0x10000, 0x20000
+    for bad_prec in (-1, 2, 7):
+        assert L.fx_slogdet_f32(good, 2, 300, good, good, bad_prec, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_parts_f32(good, 2, 300, 1, good, good, good, None, None, bad_prec, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_factors_f32(good, 2, 300, good, good, good, good, bad_prec, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_inverse_f32(good, good, good, None, 2, 300, 1, good, bad_prec, ws, 1 << 40, None) == 1
+        assert L.fx_det_parts_f32(good, 2, 300, good, good, good, bad_prec, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_inverse_f32(good, good, good, None, 2, 300, 0, good, bad_prec, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_parts_f32(good, 2, 300, 0, 0, good, good, good, bad_prec, ws, 1 << 40, None) == 1

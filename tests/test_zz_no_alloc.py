@@ -20,7 +20,8 @@ def _call_pair(dev, A):
     l0 = torch.empty(B, device=dev)
     nb = L.fx_slogdet_f32_workspace(B, n)
     ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
-    st = L.fx_slogdet_f32(A.data_ptr(), B, n, s0.data_ptr(), l0.data_ptr(), ws.data_ptr() if nb else None, nb, stream)
+    st = L.fx_slogdet_f32(A.data_ptr(), B, n, s0.data_ptr(), l0.data_ptr(), 0, ws.data_ptr() if nb else None, nb,
+                          stream)
     assert st == 0, st
     s1 = torch.full((B,), 7.0, device=dev)
     l1 = torch.full((B,), 7.0, device=dev)
