@@ -105,6 +105,47 @@ __device__ __forceinline__ void split_bf16x3(const float (&x)[8], bf16x8 (&p)[3]
   }
 }
 
+// The same split of four values (one staged group of consecutive k), for operands that
+// are split once when a K stage goes to LDS.
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void split4_bf16x3(const float (&x)[4], bf16x4 (&p)[3]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const __bf16 h = (__bf16)x[u];
+    const float r1 = x[u] - (float)h;
+    const __bf16 m = (__bf16)r1;
+    const float r2 = r1 - (float)m;
+    p[0][u] = h;
+    p[1][u] = m;
+    p[2][u] = (__bf16)r2;
+  }
+}
+
+// Split operand planes in LDS: a staged operand is three bf16 planes (hi, mid, lo) of
+// rows of consecutive k (one row per i of A / j of B), so an MFMA operand -- eight k of
+// one row -- is one 16-byte read per plane. Rows of 16 k (32 bytes) swap their two
+// 16-byte halves on every other group of four rows, rows of 64 k (128 bytes) permute
+// their eight 16-byte chunks by the row's low three bits: either way the 16-byte reads of
+// eight consecutive rows at one k fall on distinct banks. Offsets in bf16 elements of
+// the group of k .. k+3 (k % 4 == 0) or k .. k+7 (k % 8 == 0) of row r.
+__device__ __forceinline__ int x3_off16(int r, int k) { return 16 * r + ((((k >> 3) ^ (r >> 2)) & 1) << 3) + (k & 7); }
+__device__ __forceinline__ int x3_off64(int r, int k) { return 64 * r + ((((k >> 3) ^ r) & 7) << 3) + (k & 7); }
+
+// Store one split group to the three planes (plane stride PS elements) / read one
+// operand's eight k from them.
+template <int PS>
+__device__ __forceinline__ void x3_put(__bf16* planes, int off, const float (&x)[4]) {
+  bf16x4 p[3];
+  split4_bf16x3(x, p);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) *reinterpret_cast<bf16x4*>(planes + s * PS + off) = p[s];
+}
+template <int PS>
+__device__ __forceinline__ void x3_get(const __bf16* planes, int off, bf16x8 (&p)[3]) {
+#pragma unroll
+  for (int s = 0; s < 3; ++s) p[s] = *reinterpret_cast<const bf16x8*>(planes + s * PS + off);
+}
+
 // acc += A B over K = 16 with v_mfma_f32_32x32x16_bf16: lane l supplies the parts of
 // A[l % 32][8 (l / 32) + u] and B[8 (l / 32) + u][l % 32], u < 8; D is the 32x32 fp32
 // accumulator layout of the 32x32x2 fp32 MFMA.

@@ -11,7 +11,8 @@
 // quarter as 32x32 MFMA accumulators. K advances in BK = 16 stages
 // staged through LDS K-major (so every MFMA operand read is 32 consecutive floats),
 // double-buffered, with the next stage's global loads in flight during the current
-// stage's MFMAs.
+// stage's MFMAs. The split-bf16x3 mode (X3) runs each K = 16 stage as six bf16 MFMAs
+// (v_mfma_f32_32x32x16_bf16) per accumulator.
 //
 // Options:
 //  * operand masks: op(A)(i, k) / op(B)(k, j) read as zero outside a triangle (lower
@@ -423,13 +424,23 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmDesc d) {
 // -- zeros outside the matrix, the triangle masks -- between two barriers.
 // Launch bound of 4 waves per SIMD: the compiler then fits the kernel in 116 VGPRs
 // (accumulators included) without scratch, against 168 + 64 left to itself.
+// The split-bf16x3 variant (X3) splits each staged element once, into three bf16 planes
+// (48 KiB of LDS for two stages), and reads each MFMA operand as one 16-byte read per
+// plane: measured 17-30 % faster than the fp32 MFMA on the n = 2048 slogpf backward's
+// products. (The 64 x 64 kernel keeps the split at the point of use: with one
+// accumulator per wave its products are bound by latency, and the larger staged LDS
+// footprint made them slower.)
 template <bool TA, int MK, bool BS = false, bool X3 = false>
 __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
   const int maskA = MK >= 0 ? (MK >> 2) : d.maskA;  // compile-time masks as in gemm_kernel
   const int maskB = MK >= 0 ? (MK & 3) : d.maskB;
   constexpr int BM = 128, BN = 128, LDA_ = BM + 4, LDB_ = BN + 4;
-  __shared__ __align__(16) float As[2][GBK * LDA_];
-  __shared__ __align__(16) float Bs[2][GBK * LDB_];
+  // fp32 stages K-major, or (X3) three split bf16 planes per operand and stage
+  constexpr int XPA = BM * GBK, XPB = BN * GBK;  // bf16 per plane
+  constexpr int SMEM = X3 ? 2 * 3 * (XPA + XPB) * 2 : 2 * GBK * (LDA_ + LDB_) * 4;
+  __shared__ __align__(16) char smem[SMEM];
+  float(*As)[GBK * LDA_] = reinterpret_cast<float(*)[GBK * LDA_]>(smem);
+  float(*Bs)[GBK * LDB_] = reinterpret_cast<float(*)[GBK * LDB_]>(smem + 2 * GBK * LDA_ * 4);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   int64_t bat = blockIdx.y;
   const int64_t bat2 = blockIdx.z;
@@ -546,6 +557,66 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
     }
   };
 
+  // split-bf16x3 staging (X3): each thread holds two groups of four consecutive k -- of
+  // rows ra, ra + 64 of A (one 16-byte load each), or of columns 2 p, 2 p + 1 (p = tid %
+  // 64) of A^T / B (four 8-byte loads along k) -- fixed in registers when the stage is
+  // not plain, then split once into the planes
+  auto xA = [&](int b) { return reinterpret_cast<__bf16*>(smem) + b * 3 * (XPA + XPB); };
+  auto xB = [&](int b) { return reinterpret_cast<__bf16*>(smem) + b * 3 * (XPA + XPB) + 3 * XPA; };
+  const int xp = tid & 63, xk = 4 * (tid >> 6);
+  const int xia = min(i0 + 2 * xp, d.M - 2), xjb = min(j0 + 2 * xp, d.N - 2);
+  float xa[2][4], xb[2][4], xs[4];
+  auto load_x3 = [&](int k0) {
+    if (!TA) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float4 x = *reinterpret_cast<const float4*>(A + aoff[e] + min(k0 + ka, d.K - 4));
+        xa[e][0] = x.x;
+        xa[e][1] = x.y;
+        xa[e][2] = x.z;
+        xa[e][3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float2 x = *reinterpret_cast<const float2*>(A + min(k0 + xk + r, d.K - 1) * d.lda + xia);
+        xa[0][r] = x.x;
+        xa[1][r] = x.y;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kr = min(k0 + xk + r, d.K - 1);
+      if (BS) xs[r] = d.bscale[bat * (d.K / 2) + (kr >> 1)];
+      const float2 y = *reinterpret_cast<const float2*>(B + (BS ? kr ^ 1 : kr) * d.ldb + xjb);
+      xb[0][r] = y.x;
+      xb[1][r] = y.y;
+    }
+  };
+  auto store_x3 = [&](int b, int k0, bool plain) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      // A: row gi, k from gk; B: column gj, k from k0 + xk
+      const int gi = TA ? i0 + 2 * xp + e : i0 + ra + 64 * e, gk = TA ? k0 + xk : k0 + ka;
+      const int gj = j0 + 2 * xp + e;
+      float va4[4], vb4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = xa[e][r];
+        if (!plain)
+          v = (gi >= d.M || gk + r >= d.K) ? 0.0f : (maskA ? mask_val(v, maskA, gi + d.offAr, gk + r + d.offAc) : v);
+        va4[r] = v;
+        const int k = k0 + xk + r;
+        float w = xb[e][r];
+        if (BS) w *= (k & 1) ? -xs[r] : xs[r];
+        if (!plain) w = (gj >= d.N || k >= d.K) ? 0.0f : (maskB ? mask_val(w, maskB, k + d.offBr, gj + d.offBc) : w);
+        vb4[r] = w;
+      }
+      x3_put<XPA>(xA(b), x3_off16(gi - i0, gk - k0), va4);
+      x3_put<XPB>(xB(b), x3_off16(gj - j0, xk), vb4);
+    }
+  };
+
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const int l32 = lane & 31, lh = lane >> 5;
   v16f acc[2][2];
@@ -555,7 +626,35 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
-  if (klo < khi) {
+  if constexpr (X3) {
+   if (klo < khi) {
+    load_x3(klo);
+    store_x3(0, klo, plain_stage(klo));
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = klo; k0 < khi; k0 += GBK) {
+      const bool more = k0 + GBK < khi;
+      if (more) load_x3(k0 + GBK);
+      // the stage's K = 16 in one bf16x3 product per accumulator; A's parts first, then
+      // each B column block's, used by both A row blocks
+      bf16x8 ap[2][3];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) x3_get<XPA>(xA(buf), x3_off16(wm + 32 * a + l32, 8 * lh), ap[a]);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        bf16x8 bp[3];
+        x3_get<XPB>(xB(buf), x3_off16(wn + 32 * b + l32, 8 * lh), bp);
+#pragma unroll
+        for (int a = 0; a < 2; ++a) acc[a][b] = mfma_bf16x3(ap[a], bp, acc[a][b]);
+      }
+      if (more) {
+        store_x3(buf ^ 1, k0 + GBK, plain_stage(k0 + GBK));
+        __syncthreads();
+        buf ^= 1;
+      }
+    }
+   }
+  } else if (klo < khi) {
     load_stage(klo);
     store_stage(0);
     if (!plain_stage(klo)) {
@@ -567,41 +666,18 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
     for (int k0 = klo; k0 < khi; k0 += GBK) {
       const bool more = k0 + GBK < khi;
       if (more) load_stage(k0 + GBK);
-      if constexpr (X3) {
-        // as in gemm_kernel: the stage's K = 16 in one bf16x3 product per accumulator;
-        // A's parts first, then each B column block's, used by both A row blocks
-        bf16x8 ap[2][3];
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
-          float f[8];
+      for (int kp = 0; kp < GBK / 2; ++kp) {
+        float av[2], bv[2];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) f[u] = As[buf][(8 * lh + u) * LDA_ + wm + 32 * a + l32];
-          split_bf16x3(f, ap[a]);
-        }
+        for (int a = 0; a < 2; ++a) av[a] = As[buf][(2 * kp + lh) * LDA_ + wm + 32 * a + l32];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          float f[8];
-          bf16x8 bp[3];
+        for (int b = 0; b < 2; ++b) bv[b] = Bs[buf][(2 * kp + lh) * LDB_ + wn + 32 * b + l32];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) f[u] = Bs[buf][(8 * lh + u) * LDB_ + wn + 32 * b + l32];
-          split_bf16x3(f, bp);
+        for (int a = 0; a < 2; ++a)
 #pragma unroll
-          for (int a = 0; a < 2; ++a) acc[a][b] = mfma_bf16x3(ap[a], bp, acc[a][b]);
-        }
-      } else {
-#pragma unroll
-        for (int kp = 0; kp < GBK / 2; ++kp) {
-          float av[2], bv[2];
-#pragma unroll
-          for (int a = 0; a < 2; ++a) av[a] = As[buf][(2 * kp + lh) * LDA_ + wm + 32 * a + l32];
-#pragma unroll
-          for (int b = 0; b < 2; ++b) bv[b] = Bs[buf][(2 * kp + lh) * LDB_ + wn + 32 * b + l32];
-#pragma unroll
-          for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-              acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
-        }
+          for (int b = 0; b < 2; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
       }
       if (more) {
         store_stage(buf ^ 1);
