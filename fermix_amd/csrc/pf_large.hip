@@ -1,7 +1,11 @@
 // Blocked Parlett-Reid with partial pivoting for 128 < n <= 4096 (any batch). The skew
-// matrix lives in one workspace buffer (full storage, exactly skew). Per block of PB
-// columns (PB / 2 pair steps; PB = 64 once the trailing order m = N - r0 is at most 1024
-// for N >= 512 a multiple of 64, else 32; 16 above N = 2048) at r0:
+// matrix lives in one workspace buffer as its strictly lower triangle, in strips of four
+// rows stored column-major (entry (p, q), p > q, at ((p / 4) N + q) 4 + p % 4): an MFMA
+// accumulator's four consecutive rows of one column are one 16-byte store, and a row of
+// the skew matrix is its stored part (columns q < p, 16-byte strided) and the negated
+// column below the diagonal (whole 16-byte strip pieces). Per block of PB columns (PB / 2
+// pair steps; PB = 64 once the trailing order m = N - r0 is at most 1024 for N >= 512 a
+// multiple of 64, else 32; 16 above N = 2048) at r0:
 //   1. pf_panel_kernel (one workgroup of NT = 256..1024 threads per matrix, each lane
 //      owning R = 2 or 4 of the m = N - r0 rows): the pair steps with the tau / w vectors
 //      kept in registers as G (m x PB); column a and column p of the current matrix are read
@@ -11,11 +15,11 @@
 //      the map src[new position] = old row;
 //   2. pf_update_kernel (matrix x lower-triangle 64x64 tile, in place):
 //      M'' = M[src, src] + G J G^T on fp32 MFMA (K = PB), the old entries read through the
-//      permutation, the new ones stored in the new order: the lower tile directly, its
-//      mirrored (negated) transpose through LDS, so both stores are coalesced and M'' stays
-//      exactly skew. In place is safe: a row that moves into a trailing position comes
-//      from the block just factored, whose rows and columns the update never writes, and
-//      every other old entry is read by the lane that rewrites it.
+//      permutation (from the stored triangle, negated where the pair is transposed), the
+//      new lower entries stored in the new order, four rows of a column per 16-byte
+//      store; the upper half is never formed. In place is safe: a row that moves into a
+//      trailing position comes from the block just factored, whose columns the update
+//      never writes, and every other old entry is read by the lane that rewrites it.
 // Reference roles replaced (ChenAo-Phys/fermix): _pf_run / _pf_core (src/fermix/_pf.py:
 // 497-570), the pair-step panel (:59-284) and the rank-2b update (:287-382).
 #include "common.h"
@@ -59,19 +63,27 @@ struct PfRowA {
   float g[PFB_L];
 };
 
-// Copy a (B, n, n) into M (B, N, N): S = (a - a^T)/2 (or a) with [[0,1],[-1,0]] padding.
-// 32-bit index math within a matrix (N * N < 2^31).
+// Offset of the stored entry (p, q), p > q, in a matrix of the lower-triangle strip
+// layout (32-bit: N * N < 2^31).
+__device__ __forceinline__ unsigned l4(int p, int q, int N) {
+  return ((unsigned)(p >> 2) * (unsigned)N + (unsigned)q) * 4u + (unsigned)(p & 3);
+}
+
+// Copy a (B, n, n) into M (B, N, N) in the strip layout: S = (a - a^T)/2 (or a) with
+// [[0,1],[-1,0]] padding, the strictly lower entries only (the rest of each strip is never
+// read). Thread e writes strip e / (4 N), column (e / 4) % N, row 4 (e / (4 N)) + e % 4.
 __global__ void pf_copy_pad_kernel(const float* __restrict__ A, int n, int skew, float* __restrict__ M, int N) {
   const int64_t b = blockIdx.y;
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= N * N) return;
-  const int r = e / N, c = e - r * N;
+  const int r = 4 * (e / (4 * N)) + (e & 3), c = (e >> 2) % N;
+  if (r <= c) return;
   const float* Ab = A + b * (int64_t)n * n;
   float v;
   if (r < n && c < n) {
     v = skew ? (Ab[(int64_t)r * n + c] - Ab[(int64_t)c * n + r]) * 0.5f : Ab[(int64_t)r * n + c];
   } else {
-    v = ((r ^ c) == 1 && r >= n) ? ((r & 1) ? -1.0f : 1.0f) : 0.0f;
+    v = ((r ^ c) == 1 && r >= n) ? -1.0f : 0.0f;  // r odd, c = r - 1: M[r][r-1] = -1
   }
   M[b * (int64_t)N * N + e] = v;
 }
@@ -83,17 +95,24 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
                                                       int* __restrict__ src_out,
                                                       float* __restrict__ Gn,
                                                       int* __restrict__ orig,
-                                                      float* __restrict__ gbuf) {
+                                                      float* __restrict__ gbuf, int full) {
   constexpr int NW = NT / 64;
   constexpr int CW = PB < 32 ? PB : 32;  // factor chunk width
   static_assert(PB % CW == 0 && PB / CW <= 2, "a block spans one or two chunks");
   __shared__ PfRowA rowa;
   __shared__ PfCand cand[2][NW];
-  __shared__ int posL[NT * R];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = N - r0;
-  const float* Mb = M + b * (int64_t)N * N + (int64_t)r0 * N + r0;  // block-start trailing matrix
+  // M[r0 + q][r0 + i] of the block-start matrix: the input itself in full storage (full:
+  // the first block reading it in place of a copy), else the strip layout's triangle
+  const float* Mm = M + b * (int64_t)N * N;
+  auto rowv = [&](int q, int i) {
+    if (full) return Mm[(unsigned)((r0 + q) * N + r0 + i)];
+    const int gq = r0 + q, gi = r0 + i;
+    const float v = Mm[l4(max(gq, gi), min(gq, gi), N)];
+    return gi < gq ? v : (gi > gq ? -v : 0.0f);
+  };
   float G[R][PB];
   int pos[R];
   bool valid[R];
@@ -130,9 +149,8 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     {
       float mv[R];
       if constexpr (t == 0) {
-        const float* rowp = Mb + (int64_t)qa * N;
 #pragma unroll
-        for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowp[R * tid + s] : 0.0f;
+        for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowv(qa, R * tid + s) : 0.0f;
       } else {
 #pragma unroll
         for (int s = 0; s < R; ++s) mv[s] = mv_next[s];
@@ -196,17 +214,16 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     // at c + 1 if the pivot came from c + 2, else the row at c + 2. Its load goes out
     // now, beside the pivot row's (the block-start matrix is read-only in the panel).
     if constexpr (t + 1 < PB / 2) {
-      const float* rown = Mb + (int64_t)(pp == c + 2 ? qn1 : qn2) * N;
+      const int qn = pp == c + 2 ? qn1 : qn2;
 #pragma unroll
-      for (int s = 0; s < R; ++s) mv_next[s] = valid[s] ? rown[R * tid + s] : 0.0f;
+      for (int s = 0; s < R; ++s) mv_next[s] = valid[s] ? rowv(qn, R * tid + s) : 0.0f;
     }
     // y = column p on my rows
     float y[R];
     {
-      const float* rowp = Mb + (int64_t)qp * N;
       float mv[R];
 #pragma unroll
-      for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowp[R * tid + s] : 0.0f;
+      for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowv(qp, R * tid + s) : 0.0f;
 #pragma unroll
       for (int s = 0; s < R; ++s) {
         float v = -mv[s];
@@ -231,7 +248,6 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
   for (int s = 0; s < R; ++s) {
     const int i = R * tid + s;
     if (valid[s]) {
-      posL[i] = pos[s];
       float* gr = Gn + (b * N + r0 + pos[s]) * (int64_t)PB;
 #pragma unroll
       for (int k = 0; k < PB; k += 4) *reinterpret_cast<float4*>(gr + k) = make_float4(G[s][k], G[s][k + 1], G[s][k + 2], G[s][k + 3]);
@@ -266,22 +282,26 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
 }
 
 // M_new[p][q] = M_old[src p][src q] + sum_k G[p][k] (J G^T)[k][q] for the trailing
-// positions p, q >= r1 (lower tiles of T x T; the upper triangle by the negated
-// transpose). Four waves, each owning a (T/2) x (T/2) quarter as AW x AW 32x32 MFMA
-// accumulators.
+// positions p > q >= r1 (lower tiles of T x T). Four waves, each owning a (T/2) x (T/2)
+// quarter as AW x AW 32x32 MFMA accumulators (the rows 8 (v / 4) + 4 lh + v % 4 of
+// accumulator elements v = 4 g .. 4 g + 3 form one strip of the layout). Old entries: for
+// the first block read through src from the full-storage input Min; for the others from
+// the strip layout: a strip of four rows none of which moved is one 16-byte load at
+// column src q (a moved column's source is a block row, below every trailing row, so the
+// entry is stored there), a strip with a moved row (at most PB per block) entry by entry.
+// New entries: the strip layout, four rows of a column per 16-byte store.
 template <int PB, int T>
 __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, int N, int r1,
                                                         const int* __restrict__ src,
                                                         const float* __restrict__ Gn,
                                                         const float* __restrict__ Min) {
   constexpr int H = T / 2, AW = H / 32;       // quarter size, accumulators per side
-  constexpr int LDG = T + 4, LDT = H + 1;
-  constexpr int LDS_N = 2 * PB * LDG > T * LDT ? 2 * PB * LDG : T * LDT;
+  constexpr int LDG = T + 4;
   typedef float v16f __attribute__((ext_vector_type(16)));
-  // Ga / Hb: the G rows of the tile rows / (J G^T) columns of the tile columns, K-major;
-  // after the MFMAs the same LDS holds half of the tile transposed (T x T/2)
-  __shared__ __align__(16) float lds[LDS_N];
+  // Ga / Hb: the G rows of the tile rows / (J G^T) columns of the tile columns, K-major
+  __shared__ __align__(16) float lds[2 * PB * LDG];
   __shared__ int sp[T], sq[T];
+  __shared__ int smv[T / 4];  // strip of the tile rows with a moved row
   float* Ga = lds;
   float* Hb = lds + PB * LDG;
   const int64_t b = blockIdx.y;
@@ -294,9 +314,7 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* G = Gn + b * (int64_t)N * PB;
   const int* sb = src + b * N;
-  float* Mb = M + b * (int64_t)N * N;  // entries addressed by 32-bit offsets (N * N < 2^32)
-  // old entries: M itself, or the input for the first block (in place of a copy into M)
-  const float* Cb = Min ? Min + b * (int64_t)N * N : Mb;
+  float* Mb = M + b * (int64_t)N * N;  // entries addressed by 32-bit offsets (N * N < 2^31)
   // fixed trip count, so every load is issued before the first store
   constexpr int GE = T * PB / 256;
   float ga[GE], gb[GE];
@@ -319,10 +337,19 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
   if (tid < T) {
     sp[tid] = p0 + tid < N ? sb[p0 + tid] : 0;
     sq[tid] = q0 + tid < N ? sb[q0 + tid] : 0;
+  } else if (tid < T + T / 4) {
+    const int r = p0 + 4 * (tid - T);  // rows beyond N (whole strips: N % 4 == 0) count as unmoved
+    bool mv = false;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) mv = mv || (r < N && sb[r + u] != r + u);
+    smv[tid - T] = mv;
   }
   __syncthreads();
   // wave (wr, wc) owns an H x H quarter as AW x AW 32x32 accumulators, seeded with the
-  // old entries M[src p][src q]
+  // old entries M[src p][src q]; rows / columns beyond N and the upper half of a
+  // diagonal tile are seeded with zeros and never stored (MFMA output elements are
+  // independent)
+  const bool diag = I == J;
   const int wr = (wave >> 1) * H, wc = (wave & 1) * H;
   const int l32 = lane & 31, lh = lane >> 5;
   v16f acc[AW][AW];
@@ -330,14 +357,35 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
   for (int a = 0; a < AW; ++a)
 #pragma unroll
     for (int c = 0; c < AW; ++c) {
-      const int cl = wc + 32 * c + l32;
-      const int scol = sq[cl];
+      const int cl = wc + 32 * c + l32, q = q0 + cl;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        // rows / columns beyond N hold index 0 in sp / sq: an in-bounds read whose
-        // accumulator element is never stored (MFMA output elements are independent)
-        const int rl = wr + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
-        acc[a][c][v] = Cb[(unsigned)(sp[rl] * N + scol)];
+      for (int g = 0; g < 4; ++g) {
+        const int rl = wr + 32 * a + 8 * g + 4 * lh, p = p0 + rl;  // p % 4 == 0
+        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (Min) {
+          // rows / columns beyond N hold index 0 in sp / sq: in-bounds reads
+          const float* Ab = Min + b * (int64_t)N * N;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) x[u] = Ab[(unsigned)(sp[rl + u] * N + sq[cl])];
+        } else if (p < N && q < N) {
+          const int scol = sq[cl];
+          if (!diag && !smv[rl >> 2]) {  // uniform per half-wave
+            const float4 y = *reinterpret_cast<const float4*>(Mb + l4(p, scol, N));
+            x[0] = y.x;
+            x[1] = y.y;
+            x[2] = y.z;
+            x[3] = y.w;
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int srow = sp[rl + u];
+              const float y = Mb[l4(max(srow, scol), min(srow, scol), N)];
+              x[u] = (diag && p + u <= q) ? 0.0f : (srow > scol ? y : -y);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[a][c][4 * g + u] = x[u];
       }
     }
 #pragma unroll
@@ -353,49 +401,29 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
       for (int c = 0; c < AW; ++c)
         acc[a][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[c], acc[a][c], 0, 0, 0);
   }
-  const bool diag = I == J;
-  // the tile itself (a diagonal tile is stored whole: its upper half comes from the old
-  // upper entries and the negated products, i.e. exactly the mirror; diagonal forced 0)
+  // the lower entries: whole strips off the diagonal tiles (N is a multiple of 4, so a
+  // strip is inside the matrix or outside it), entry by entry below the diagonal of a
+  // diagonal tile
 #pragma unroll
   for (int a = 0; a < AW; ++a)
 #pragma unroll
     for (int c = 0; c < AW; ++c) {
-      const int cl = wc + 32 * c + l32;
+      const int q = q0 + wc + 32 * c + l32;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int rl = wr + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
-        const int p = p0 + rl, q = q0 + cl;
-        if (p < N && q < N) Mb[(unsigned)(p * N + q)] = (diag && rl == cl) ? 0.0f : acc[a][c][v];
+      for (int g = 0; g < 4; ++g) {
+        const int p = p0 + wr + 32 * a + 8 * g + 4 * lh;  // a multiple of 4
+        if (p >= N || q >= N) continue;
+        float* dst = Mb + l4(p, q, N);
+        if (!diag) {
+          *reinterpret_cast<float4*>(dst) =
+              make_float4(acc[a][c][4 * g], acc[a][c][4 * g + 1], acc[a][c][4 * g + 2], acc[a][c][4 * g + 3]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (p + u > q) dst[u] = acc[a][c][4 * g + u];
+        }
       }
     }
-  if (diag) return;  // uniform over the workgroup
-  // mirrored tile Mn[q][p] = -C[p][q], one H-row half of the tile at a time through LDS
-  float* Ct = lds;  // Ct[cl * LDT + rl - H h]
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    __syncthreads();  // previous readers of the LDS are done
-    if ((wave >> 1) == h) {
-#pragma unroll
-      for (int a = 0; a < AW; ++a)
-#pragma unroll
-        for (int c = 0; c < AW; ++c) {
-          const int cl = wc + 32 * c + l32;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int rr = 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3);
-            Ct[cl * LDT + rr] = acc[a][c][v];
-          }
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < T * H / 256; ++u) {
-      const int e = tid + 256 * u;
-      const int cl = e / H, rr = e % H;
-      const int p = p0 + H * h + rr, q = q0 + cl;
-      if (p < N && q < N) Mb[(unsigned)(q * N + p)] = -Ct[cl * LDT + rr];
-    }
-  }
 }
 
 __global__ void pf_finish_kernel(const float* __restrict__ d, const int* __restrict__ nsw, int H, int nch,
@@ -454,20 +482,21 @@ template <int PB, int R>
 static int pf_block(float* M, int N, int r0, int nch, int64_t batch, float* d, int* nsw, int* src, float* Gn,
                     int* orig, float* gbuf, const float* A0, hipStream_t s) {
   const int m = N - r0;
-  const float* Mp = A0 ? A0 : M;  // A0 (first block): the input itself, same layout
+  const float* Mp = A0 ? A0 : M;  // A0 (first block): the input itself, full storage
+  const int full = A0 != nullptr;
+  const int r1 = r0 + PB;
   if (m <= 256 * R)
     hipLaunchKernelGGL((pf_panel_kernel<256, R, PB>), dim3((unsigned)batch), dim3(256), 0, s, Mp, N, r0, nch, d,
-                       nsw, src, Gn, orig, gbuf);
+                       nsw, src, Gn, orig, gbuf, full);
   else if (m <= 512 * R)
     hipLaunchKernelGGL((pf_panel_kernel<512, R, PB>), dim3((unsigned)batch), dim3(512), 0, s, Mp, N, r0, nch, d,
-                       nsw, src, Gn, orig, gbuf);
+                       nsw, src, Gn, orig, gbuf, full);
   else if constexpr (PB * R <= 64)  // G[R][PB] fits the 128 VGPRs of a 1024-thread workgroup
     hipLaunchKernelGGL((pf_panel_kernel<1024, R, PB>), dim3((unsigned)batch), dim3(1024), 0, s, Mp, N, r0, nch,
-                       d, nsw, src, Gn, orig, gbuf);
+                       d, nsw, src, Gn, orig, gbuf, full);
   else
     return FX_ERR_UNSUPPORTED;
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  const int r1 = r0 + PB;
   if (r1 >= N) return FX_OK;
   constexpr int TU = PF_UPDATE_TILE;
   const int nt = (N - r1 + TU - 1) / TU;

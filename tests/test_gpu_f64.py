@@ -32,9 +32,10 @@ def _skew(A):
     return (A - np.swapaxes(A, -1, -2)) * 0.5
 
 
-# n spans the LDS-resident sizes (forward n <= 87, inverse n <= 61) and the workspace
-# sizes on 256 and 1024 threads (n > 128)
-@pytest.mark.parametrize("n", [0, 1, 2, 3, 5, 16, 31, 61, 62, 87, 88, 128, 129, 200, 300])
+# n spans the register-resident kernels (n <= 128: 16-column strips up to n = 64, 32-column
+# strips from n = 65, no workspace) and the workspace kernels on 256 and 1024 threads
+# (n > 128)
+@pytest.mark.parametrize("n", [0, 1, 2, 3, 5, 16, 31, 61, 62, 64, 65, 87, 88, 128, 129, 200, 300])
 def test_f64_slogdet_and_inverse(dev, n):
     B = 8 if n <= 128 else 3
     rng = np.random.default_rng(7000 + n)
