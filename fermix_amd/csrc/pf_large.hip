@@ -304,8 +304,17 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
   __shared__ int smv[T / 4];  // strip of the tile rows with a moved row
   float* Ga = lds;
   float* Hb = lds + PB * LDG;
-  const int64_t b = blockIdx.y;
-  const int t = blockIdx.x;
+  int64_t b = blockIdx.y;
+  int t = blockIdx.x;
+  if (PB >= 64 && (gridDim.y & 7) == 0) {
+    // workgroups go to the 8 XCDs round-robin by linear id: renumber so that all tiles
+    // of one matrix run on one XCD and its G block is fetched into one L2 (measured at
+    // n = 2048: 10 % faster with 64-column blocks, 8 % slower with 32-column ones)
+    const int64_t lin = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    const int64_t slot = lin >> 3;
+    t = (int)(slot % gridDim.x);
+    b = (slot / gridDim.x) * 8 + (lin & 7);
+  }
   int I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
   while ((I + 1) * (I + 2) / 2 <= t) ++I;
   while (I * (I + 1) / 2 > t) --I;
