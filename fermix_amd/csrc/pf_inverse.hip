@@ -206,6 +206,14 @@ __global__ __launch_bounds__(256) void pf_adj_gather_kernel(const float* __restr
   const float4* s4 = reinterpret_cast<const float4*>(R + b * (int64_t)N * N + (int64_t)f * N);
   const float4* t4 = reinterpret_cast<const float4*>(T + b * (int64_t)Ninv * Ninv + (int64_t)aK * Ninv);
   const float4* w4 = reinterpret_cast<const float4*>(wvec + b * N);
+  // the column permutation of this thread's outputs, loaded with the rows (one round trip)
+  constexpr int MAXJ = PF_LARGE_MAXN / 256;
+  int cj[MAXJ];
+#pragma unroll
+  for (int u = 0; u < MAXJ; ++u) {
+    const int j = threadIdx.x + 256 * u;
+    cj[u] = j < N ? ip[j] : 0;
+  }
   for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) {
     reinterpret_cast<float4*>(rowb)[c4] = s4[c4];
     // v = Y^T e_2K: Y[2K][c] for c < 2K, 1 at 2K, 0 after
@@ -223,13 +231,17 @@ __global__ __launch_bounds__(256) void pf_adj_gather_kernel(const float* __restr
   const float w_f = rowb[aK], v_f = vrow[f];
   float* o = out + b * (int64_t)n * n + (int64_t)i * n;
   bool nf = false;
-  for (int j = threadIdx.x; j < N; j += 256) {
-    const int c = ip[j];
-    const float val = -(a1 * rowb[c] + a2 * (w_f * vrow[c] - v_f * wrow[c]));
-    nf = nf || !isfinite(val);
-    if (i < n && j < n) {
-      if (accumulate) o[j] += sc * val;
-      else o[j] = sc * val;
+#pragma unroll
+  for (int u = 0; u < MAXJ; ++u) {
+    const int j = threadIdx.x + 256 * u;
+    if (j < N) {
+      const int c = cj[u];
+      const float val = -(a1 * rowb[c] + a2 * (w_f * vrow[c] - v_f * wrow[c]));
+      nf = nf || !isfinite(val);
+      if (i < n && j < n) {
+        if (accumulate) o[j] += sc * val;
+        else o[j] = sc * val;
+      }
     }
   }
   const int any = __syncthreads_or(nf ? 1 : 0);
