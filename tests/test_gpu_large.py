@@ -83,3 +83,37 @@ def test_no_row_moves(dev, n):
     assert_logabs(_np(l), l64, n, "vs float64", A)
     ref = np.linalg.inv(A.astype(np.float64)).swapaxes(-1, -2)
     assert_grad(_np(invT), ref, A, f"n={n} A^-T vs float64")
+
+
+@pytest.mark.parametrize("n", [160, 512, 1056, 2080])
+def test_slogpf_first_block_paths_agree(dev, n):
+    """The blocked Parlett-Reid keeps the trailing matrix as its lower triangle in 4-row
+    strips. With skew_symmetrize=False and n a multiple of 32 the first block reads the
+    full-storage input in place of a copy (its update gathering the old entries through
+    the permutation); with skew_symmetrize=True the input is first copied into the strip
+    layout ((S - S^T) / 2 = S exactly for an exactly skew S, so both runs factor the same
+    numbers). The two runs must agree bit for bit, in the forward and in the factors of
+    the gradient route; n covers 32- and 64-column blocks and the 16-column blocks above
+    2048."""
+    from fermix_amd import _kernels
+
+    B = 4 if n <= 1056 else 2
+    rng = np.random.default_rng(9100 + n)
+    A = (rng.standard_normal((B, n, n)) / np.sqrt(n)).astype(np.float32)
+    S = (A - A.transpose(0, 2, 1)).astype(np.float32)
+    S[0, 3, :] = 0.0  # an exactly singular member: (0, -inf) on both paths
+    S[0, :, 3] = 0.0
+    print(f"slogpf first-block paths n={n} B={B}", flush=True)
+    St = _t(S, dev)
+    s1, l1 = fermix_amd.slogpf(St, skew_symmetrize=False)
+    s2, l2 = fermix_amd.slogpf(St, skew_symmetrize=True)
+    assert torch.equal(s1, s2) and torch.equal(l1, l2)
+    assert _np(s1)[0] == 0 and np.isneginf(_np(l1)[0])
+    sp1, lp1, G1 = _kernels.slogpf_parts(St, False)
+    sp2, lp2, G2 = _kernels.slogpf_parts(St, True)
+    assert torch.equal(sp1, s1) and torch.equal(lp1, l1)
+    assert torch.equal(sp2, s2) and torch.equal(lp2, l2)
+    assert torch.equal(G1, G2)
+    s64, l64 = ref64.slogpf64(S[1:])
+    assert np.array_equal(_np(s1)[1:], s64)
+    assert_logabs(_np(l1)[1:], l64, n, "vs float64", S[1:])
