@@ -99,19 +99,43 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
   constexpr int NW = NT / 64;
   constexpr int CW = PB < 32 ? PB : 32;  // factor chunk width
   static_assert(PB % CW == 0 && PB / CW <= 2, "a block spans one or two chunks");
-  __shared__ PfRowA rowa;
-  __shared__ PfCand cand[2][NW];
+  __shared__ __align__(16) PfRowA rowa;
+  __shared__ __align__(16) PfCand cand[2][NW];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = N - r0;
   // M[r0 + q][r0 + i] of the block-start matrix: the input itself in full storage (full:
   // the first block reading it in place of a copy), else the strip layout's triangle
   const float* Mm = M + b * (int64_t)N * N;
-  auto rowv = [&](int q, int i) {
-    if (full) return Mm[(unsigned)((r0 + q) * N + r0 + i)];
-    const int gq = r0 + q, gi = r0 + i;
-    const float v = Mm[l4(max(gq, gi), min(gq, gi), N)];
-    return gi < gq ? v : (gi > gq ? -v : 0.0f);
+  // The lane's R consecutive entries M[r0 + q][r0 + R tid + s] (zero beyond m). r0 and m
+  // are multiples of 16, so a lane's rows are one strip piece: the part below the diagonal
+  // (rows > r0 + q) is one 8- or 16-byte load, the part right of it R loads 16 bytes apart.
+  typedef float vR __attribute__((ext_vector_type(R)));
+  auto rowr = [&](int q, float (&v)[R]) {
+    const int i0 = R * tid;
+    const int gq = r0 + q, gi = r0 + i0;
+    if (i0 >= m) {
+#pragma unroll
+      for (int s = 0; s < R; ++s) v[s] = 0.0f;
+    } else if (full) {
+      const vR y = *reinterpret_cast<const vR*>(Mm + (unsigned)(gq * N + gi));
+#pragma unroll
+      for (int s = 0; s < R; ++s) v[s] = y[s];
+    } else if (gi > gq) {
+      const vR y = *reinterpret_cast<const vR*>(Mm + l4(gi, gq, N));
+#pragma unroll
+      for (int s = 0; s < R; ++s) v[s] = -y[s];
+    } else if (gi + R <= gq) {
+#pragma unroll
+      for (int s = 0; s < R; ++s) v[s] = Mm[l4(gq, gi + s, N)];
+    } else {
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        const int g = gi + s;
+        const float y = Mm[l4(max(gq, g), min(gq, g), N)];
+        v[s] = g < gq ? y : (g > gq ? -y : 0.0f);
+      }
+    }
   };
   float G[R][PB];
   int pos[R];
@@ -135,8 +159,10 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     for (int s = 0; s < R; ++s) {
       if (valid[s] && pos[s] == c) {
         rowa.row = R * tid + s;
+        // 16-byte stores; the columns from 2 t on are still zero and never read
 #pragma unroll
-        for (int k = 0; k < 2 * t; ++k) rowa.g[k] = opaque(G[s][k]);
+        for (int k = 0; k < 2 * t; k += 4)
+          *reinterpret_cast<float4*>(rowa.g + k) = make_float4(opaque(G[s][k]), opaque(G[s][k + 1]), opaque(G[s][k + 2]), opaque(G[s][k + 3]));
       }
       if (valid[s] && pos[s] == c + 1) rowa.next1 = R * tid + s;
       if (valid[s] && pos[s] == c + 2) rowa.next2 = R * tid + s;
@@ -149,8 +175,7 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     {
       float mv[R];
       if constexpr (t == 0) {
-#pragma unroll
-        for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowv(qa, R * tid + s) : 0.0f;
+        rowr(qa, mv);
       } else {
 #pragma unroll
         for (int s = 0; s < R; ++s) mv[s] = mv_next[s];
@@ -187,7 +212,8 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
           my.pos = pos[s];
           my.xv = x[s];
 #pragma unroll
-          for (int k = 0; k < 2 * t; ++k) my.g[k] = opaque(G[s][k]);
+          for (int k = 0; k < 2 * t; k += 4)
+            *reinterpret_cast<float4*>(my.g + k) = make_float4(opaque(G[s][k]), opaque(G[s][k + 1]), opaque(G[s][k + 2]), opaque(G[s][k + 3]));
         }
       }
     }
@@ -215,15 +241,13 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
     // now, beside the pivot row's (the block-start matrix is read-only in the panel).
     if constexpr (t + 1 < PB / 2) {
       const int qn = pp == c + 2 ? qn1 : qn2;
-#pragma unroll
-      for (int s = 0; s < R; ++s) mv_next[s] = valid[s] ? rowv(qn, R * tid + s) : 0.0f;
+      rowr(qn, mv_next);
     }
     // y = column p on my rows
     float y[R];
     {
       float mv[R];
-#pragma unroll
-      for (int s = 0; s < R; ++s) mv[s] = valid[s] ? rowv(qp, R * tid + s) : 0.0f;
+      rowr(qp, mv);
 #pragma unroll
       for (int s = 0; s < R; ++s) {
         float v = -mv[s];
