@@ -152,13 +152,20 @@ __global__ __launch_bounds__(256) void pf_assemble_kernel(const float* __restric
   }
 }
 
-// w[c] = R[c][2K] (the column of R that the rank-2 correction uses), one thread per c.
-__global__ void pf_wvec_kernel(const float* __restrict__ R, int N, const PfCoef* __restrict__ coef,
-                               float* __restrict__ w, const int* __restrict__ active) {
+// The two vectors of the rank-2 correction in output order, vw (B, 2, N): w_c = R[c][2K]
+// (a column of R) and v_c = Y[2K][c] for c < 2K, 1 at 2K, 0 after (v = Y^T e_2K), stored
+// at j with c = iperm[j]; one thread per j.
+__global__ void pf_wvec_kernel(const float* __restrict__ R, int N, const float* __restrict__ T, int Ninv,
+                               const PfCoef* __restrict__ coef, const int* __restrict__ iperm,
+                               float* __restrict__ vw, const int* __restrict__ active) {
   const int64_t b = blockIdx.y;
   if (active && !active[b]) return;
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c < N) w[b * N + c] = R[b * (int64_t)N * N + (int64_t)c * N + 2 * coef[b].K];
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= N) return;
+  const int aK = 2 * coef[b].K, c = iperm[b * N + j];
+  vw[2 * b * N + j] = R[b * (int64_t)N * N + (int64_t)c * N + aK];
+  const float y = T[b * (int64_t)Ninv * Ninv + (int64_t)aK * Ninv + c];
+  vw[(2 * b + 1) * N + j] = c < aK ? y : (c == aK ? 1.0f : 0.0f);
 }
 
 // bad[b]: inverse mode only (the adjugate is returned as computed).
@@ -176,76 +183,80 @@ __global__ void pf_reduce_bad_kernel(const int* __restrict__ flags, int ntiles, 
 // The final matrix straight from R (skew, both triangles stored): with f = iperm[i],
 // c = iperm[j] (the factor order of output row i / column j),
 //   out[i][j] = sc * -(a1 R[f][c] + a2 (w_f v_c - v_f w_c)),
-// w = R[:, 2K] (wvec), v = Y^T e_2K (v_c = Y[2K][c] for c < 2K, 1 at 2K, 0 after), a1 / a2
-// the member's coefficients times sg, sc = scale[b] or 1; with accumulate the value is
-// added for the active members. One workgroup per row i < N: source row f of R is read
+// w = R[:, 2K], v = Y^T e_2K (both in output order in vw), a1 / a2 the member's
+// coefficients times sg, sc = scale[b] or 1; with accumulate the value is added for the
+// active members. One workgroup per RPW rows i < N: the source rows f of R are read
 // contiguously into LDS and the column permutation applied there; rows / columns >= n
-// are evaluated (flags[b][i] marks a non-finite value in row i) but not stored.
+// are evaluated (flags[b][i] marks a non-finite value among the workgroup's rows) but
+// not stored.
+template <int RPW>
 __global__ __launch_bounds__(256) void pf_adj_gather_kernel(const float* __restrict__ R, int N,
-                                                            const float* __restrict__ T, int Ninv,
                                                             const PfCoef* __restrict__ coef, float sg,
-                                                            const float* __restrict__ wvec,
+                                                            const float* __restrict__ vw,
                                                             const int* __restrict__ iperm, int n,
                                                             int* __restrict__ flags, float* __restrict__ out,
                                                             const int* __restrict__ active, int accumulate,
                                                             const float* __restrict__ scale) {
-  // the source row of R, row 2K of Y and w, each read contiguously into LDS; the column
-  // permutation then gathers from LDS only
-  extern __shared__ __align__(16) float pf_gather_lds[];  // 3 N floats (launch-time size)
-  float* const rowb = pf_gather_lds;
-  float* const vrow = pf_gather_lds + N;
-  float* const wrow = pf_gather_lds + 2 * N;
+  extern __shared__ __align__(16) float pf_gather_lds[];  // RPW N floats (launch-time size)
   const int64_t b = blockIdx.y;
   if (active && !active[b]) return;
-  const int i = blockIdx.x;
+  const int i0 = RPW * blockIdx.x;
   const int* ip = iperm + b * N;
-  const int f = ip[i];
+  const float* wp = vw + 2 * b * N;
+  const float* vp = wp + N;
+  int f[RPW];
+  float wf[RPW], vf[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int i = min(i0 + r, N - 1);
+    f[r] = ip[i];
+    wf[r] = wp[i];
+    vf[r] = vp[i];
+  }
   const PfCoef cf = coef[b];
   const float a1 = sg * cf.a1, a2 = sg * cf.a2;
-  const int aK = 2 * cf.K;
-  const float4* s4 = reinterpret_cast<const float4*>(R + b * (int64_t)N * N + (int64_t)f * N);
-  const float4* t4 = reinterpret_cast<const float4*>(T + b * (int64_t)Ninv * Ninv + (int64_t)aK * Ninv);
-  const float4* w4 = reinterpret_cast<const float4*>(wvec + b * N);
-  // the column permutation of this thread's outputs, loaded with the rows (one round trip)
+  const float* Rb = R + b * (int64_t)N * N;
+  // the column permutation and the correction vectors of this thread's outputs, loaded
+  // with the rows (one round trip)
   constexpr int MAXJ = PF_LARGE_MAXN / 256;
   int cj[MAXJ];
+  float wj[MAXJ], vj[MAXJ];
 #pragma unroll
   for (int u = 0; u < MAXJ; ++u) {
-    const int j = threadIdx.x + 256 * u;
-    cj[u] = j < N ? ip[j] : 0;
+    const int j = min((int)threadIdx.x + 256 * u, N - 1);
+    cj[u] = ip[j];
+    wj[u] = wp[j];
+    vj[u] = vp[j];
   }
   for (int c4 = threadIdx.x; c4 < N / 4; c4 += 256) {
-    reinterpret_cast<float4*>(rowb)[c4] = s4[c4];
-    // v = Y^T e_2K: Y[2K][c] for c < 2K, 1 at 2K, 0 after
-    float4 t = t4[c4];
-    const int c = 4 * c4;
-    t.x = c < aK ? t.x : (c == aK ? 1.0f : 0.0f);
-    t.y = c + 1 < aK ? t.y : (c + 1 == aK ? 1.0f : 0.0f);
-    t.z = c + 2 < aK ? t.z : (c + 2 == aK ? 1.0f : 0.0f);
-    t.w = c + 3 < aK ? t.w : (c + 3 == aK ? 1.0f : 0.0f);
-    reinterpret_cast<float4*>(vrow)[c4] = t;
-    reinterpret_cast<float4*>(wrow)[c4] = w4[c4];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+      reinterpret_cast<float4*>(pf_gather_lds + r * N)[c4] = reinterpret_cast<const float4*>(Rb + (int64_t)f[r] * N)[c4];
   }
   const float sc = scale ? scale[b] : 1.0f;
   __syncthreads();
-  const float w_f = rowb[aK], v_f = vrow[f];
-  float* o = out + b * (int64_t)n * n + (int64_t)i * n;
   bool nf = false;
 #pragma unroll
-  for (int u = 0; u < MAXJ; ++u) {
-    const int j = threadIdx.x + 256 * u;
-    if (j < N) {
-      const int c = cj[u];
-      const float val = -(a1 * rowb[c] + a2 * (w_f * vrow[c] - v_f * wrow[c]));
-      nf = nf || !isfinite(val);
-      if (i < n && j < n) {
-        if (accumulate) o[j] += sc * val;
-        else o[j] = sc * val;
+  for (int r = 0; r < RPW; ++r) {
+    const int i = i0 + r;
+    if (i >= N) break;
+    const float* rowb = pf_gather_lds + r * N;
+    float* o = out + b * (int64_t)n * n + (int64_t)i * n;
+#pragma unroll
+    for (int u = 0; u < MAXJ; ++u) {
+      const int j = threadIdx.x + 256 * u;
+      if (j < N) {
+        const float val = -(a1 * rowb[cj[u]] + a2 * (wf[r] * vj[u] - vf[r] * wj[u]));
+        nf = nf || !isfinite(val);
+        if (i < n && j < n) {
+          if (accumulate) o[j] += sc * val;
+          else o[j] = sc * val;
+        }
       }
     }
   }
   const int any = __syncthreads_or(nf ? 1 : 0);
-  if (threadIdx.x == 0) flags[b * N + i] = any;
+  if (threadIdx.x < RPW && i0 + threadIdx.x < N) flags[b * N + i0 + threadIdx.x] = any;
 }
 
 // out[b] = 0 for the flagged members (one workgroup per member; others exit at once).
@@ -264,7 +275,7 @@ size_t pf_inverse_workspace(int64_t batch, int N) {
   add((size_t)batch * Ninv * Ninv * 4);  // T (L~, then Y)
   add((size_t)batch * Ninv * Ninv);      // Tmp (Ninv/2 x Ninv/2 floats)
   add((size_t)batch * N * N * 4);        // R
-  add((size_t)batch * N * 4);            // wvec
+  add((size_t)batch * 2 * N * 4);        // vw: w and v in output order
   add((size_t)batch * N / 2 * 4);        // dinv
   add((size_t)batch * N * 4);            // iperm
   add((size_t)batch * sizeof(PfCoef));
@@ -289,7 +300,7 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
   float* T = (float*)take((size_t)batch * Ninv * Ninv * 4);
   float* Tmp = (float*)take((size_t)batch * Ninv * Ninv);
   float* R = (float*)take((size_t)batch * N * N * 4);
-  float* wvec = (float*)take((size_t)batch * N * 4);
+  float* vw = (float*)take((size_t)batch * 2 * N * 4);
   float* dinv = (float*)take((size_t)batch * N / 2 * 4);
   int* iperm = (int*)take((size_t)batch * N * 4);
   PfCoef* coef = (PfCoef*)take((size_t)batch * sizeof(PfCoef));
@@ -343,10 +354,13 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
       if (st != FX_OK) return st;
     }
     hipLaunchKernelGGL(pf_wvec_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)batch), dim3(256), 0, s, R, N,
-                       coef, wvec, active);
+                       T, Ninv, coef, iperm, vw, active);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    hipLaunchKernelGGL(pf_adj_gather_kernel, dim3((unsigned)N, (unsigned)batch), dim3(256), 3 * N * sizeof(float), s,
-                       R, N, T, Ninv, coef, sg, wvec, iperm, n, flags, out, active, accumulate, scale);
+    // two rows per workgroup: measured 383 us at B = 64, N = 2048 against 520 (one), 463 (four)
+    constexpr int RPW = 2;
+    hipLaunchKernelGGL((pf_adj_gather_kernel<RPW>), dim3((unsigned)((N + RPW - 1) / RPW), (unsigned)batch), dim3(256),
+                       RPW * N * sizeof(float), s, R, N, coef, sg, vw, iperm, n, flags, out, active, accumulate,
+                       scale);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     if (accumulate) return FX_OK;
     // inverse mode: members with d_K = 0 or a non-finite value anywhere are zeroed
