@@ -2,6 +2,14 @@
 (gfx950) with hand-written HIP kernels behind a C ABI (include/fermix.h), keeping the
 Python interface of ChenAo-Phys/fermix."""
 
-from .api import FermixDeviceError, FermixFallbackWarning, det, pf, slogdet, slogpf
+from .api import FermixDeviceError, FermixFallbackWarning, FermixTuneWarning, det, pf, slogdet, slogpf
 
-__all__ = ["slogdet", "slogpf", "det", "pf", "FermixFallbackWarning", "FermixDeviceError"]
+__all__ = [
+    "slogdet",
+    "slogpf",
+    "det",
+    "pf",
+    "FermixFallbackWarning",
+    "FermixDeviceError",
+    "FermixTuneWarning",
+]

@@ -4,7 +4,7 @@ tensors (float64 for the f64 entry points) on a ROCm device; no numerics happen 
 
 import torch
 
-from ._lib import check, lib
+from ._lib import FX_PREC_MASK, check, lib
 
 
 def _stream(t):
@@ -58,8 +58,8 @@ def pf_padded_size(n):
 
 
 def slogdet(A, x3=0):
-    """(sign, logabs) of each (n, n) matrix of A (B, n, n); x3: FX_PREC_BF16X3 products
-    (float32 only)."""
+    """(sign, logabs) of each (n, n) matrix of A (B, n, n); x3: the C ABI's prec word
+    (FX_PREC_BF16X3 products, FX_LU_BLOCK_* options; float32 only)."""
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape
@@ -145,7 +145,7 @@ def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True, x3=0):
     ws, wsb = _workspace(L.fx_slogdet_inverse_f32_workspace(B, n), dev)
     st = L.fx_slogdet_inverse_f32(
         _ptr(lu), _ptr(perm), _ptr(sign), _ptr(scale), B, n, int(bool(zero_singular)), _ptr(out),
-        int(x3), _ptr(ws), wsb, _stream(sign),
+        int(x3) & FX_PREC_MASK, _ptr(ws), wsb, _stream(sign),
     )
     check(st, "fx_slogdet_inverse_f32")
     return out

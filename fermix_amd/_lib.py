@@ -9,6 +9,31 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfermix_a
 
 FX_OK = 0
 
+# option bits of the prec argument of the slogdet / det entry points (include/fermix.h)
+FX_PREC_MASK = 0x0F
+FX_LU_BLOCK_64 = 0x100
+FX_LU_BLOCK_128 = 0x200
+
+# fields of struct fx_tune, in order (int32 each; 7 reserved int32 follow)
+TUNE_FIELDS = (
+    "fused_max_n",
+    "lu_pair_above_n",
+    "lu_direct_max_n",
+    "pf_block64_min_n",
+    "pf_block64_max_m",
+    "gemm128_min_mn",
+    "gemm128_min_k",
+    "f64_reg_max_n",
+    "f64_strip16_max_n",
+)
+
+
+class FxTune(ctypes.Structure):
+    """struct fx_tune of include/fermix.h."""
+
+    _fields_ = [(f, ctypes.c_int32) for f in TUNE_FIELDS] + [("reserved", ctypes.c_int32 * 7)]
+
+
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -20,6 +45,9 @@ SIGNATURES = {
     "fx_abi_version": (ctypes.c_int, []),
     "fx_lu_padded_size": (_i32, [_i32]),
     "fx_pf_padded_size": (_i32, [_i32]),
+    "fx_tune_table": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(FxTune)]),
+    "fx_tune_override": (ctypes.c_int, [ctypes.POINTER(FxTune)]),
+    "fx_tune_active": (ctypes.c_int, [ctypes.POINTER(FxTune)]),
     "fx_slogdet_f32_workspace": (_sz, [_i64, _i32]),
     "fx_slogdet_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _i32, _p, _sz, _p]),
     "fx_slogdet_parts_f32_workspace": (_sz, [_i64, _i32]),

@@ -26,7 +26,7 @@ build) -- there is no silent CPU path.
 import torch
 
 from . import _diff
-from ._tune import check_block, check_prec, prec_flag
+from ._tune import FermixTuneWarning, block_flag, check_block, check_prec, note_ignored, prec_flag
 
 _FLOAT_KINDS = (torch.float32, torch.float64, torch.complex64, torch.complex128)
 
@@ -73,18 +73,28 @@ def _flat(a):
     return a.reshape((B, n, n)).contiguous(), batch, n
 
 
+def _lu_opts(a, prec, unroll_steps, block):
+    """The C ABI's prec word of a slogdet / det call: the product mode and, for float32,
+    the LU block option."""
+    x3 = prec_flag(check_prec(prec, a.dtype))
+    check_block(block)
+    note_ignored("unroll_steps", unroll_steps)
+    return x3 | (block_flag(block) if a.dtype == torch.float32 else 0)
+
+
 def slogdet(a, *, prec=None, unroll_steps=None, block=None):
     """Sign and log|det| of a batch of matrices ``a`` (..., n, n) (reference
     ``slogdet``, api.py:148-174). prec: "ieee" (default; fp32 MFMA products), "bf16x3"
     (three-way bf16 split, six bf16 MFMA products, fp32 accumulation) or "tf32x3" (the
     reference's fp32-accuracy three-pass mode; on gfx950, which has no TF32 type, it
     selects "bf16x3"). The mode applies to the blocked kernels (n > 128): the trailing
-    updates and the inverse's GEMMs. block / unroll_steps: accepted for compatibility
-    and validated, without effect: the gfx950 kernels choose their blocking from n
-    (fermix_amd._tune)."""
+    updates and the inverse's GEMMs. block: the outer LU block of the blocked kernels
+    (float32): None (the tuning table: block pairs above N = 256), 64 (single 64-column
+    blocks, K = 64 trailing updates) or 128 (blocks in pairs, K = 128 updates); 32 runs
+    64 with a FermixTuneWarning. unroll_steps: accepted, without effect on gfx950 (the
+    panels are always unrolled), with a FermixTuneWarning when given."""
     a = _prep(a)
-    x3 = prec_flag(check_prec(prec, a.dtype))
-    check_block(block)
+    x3 = _lu_opts(a, prec, unroll_steps, block)
     _on_device(a)
     A, batch, n = _flat(a)
     sign, logabs = _diff.slogdet(A, x3)
@@ -96,9 +106,12 @@ def slogpf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
     api.py:177-193): S = (a - a^T)/2 unless skew_symmetrize=False (then ``a`` must be
     exactly skew); odd n gives (0, -inf). prec as for slogdet; it applies to the
     gradient's GEMMs (the forward's trailing update is memory-bound and runs in fp32).
-    upd_warps: accepted for compatibility, without effect."""
+    upd_warps: accepted, without effect on gfx950 (the trailing update's shape is fixed;
+    its blocking follows the tuning table, fermix_amd._tune), with a FermixTuneWarning
+    when given."""
     a = _prep(a)
     x3 = prec_flag(check_prec(prec, a.dtype))
+    note_ignored("upd_warps", upd_warps)
     _on_device(a)
     A, batch, n = _flat(a)
     if n % 2 == 1:
@@ -110,10 +123,9 @@ def slogpf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
 
 def det(a, *, prec=None, unroll_steps=None, block=None):
     """Determinant of a batch of matrices (reference ``det``, api.py:196-212):
-    sign * exp(logabs) of the same factorisation."""
+    sign * exp(logabs) of the same factorisation. Options as for slogdet."""
     a = _prep(a)
-    x3 = prec_flag(check_prec(prec, a.dtype))
-    check_block(block)
+    x3 = _lu_opts(a, prec, unroll_steps, block)
     _on_device(a)
     A, batch, n = _flat(a)
     return _diff.det(A, x3).reshape(batch)
@@ -121,9 +133,10 @@ def det(a, *, prec=None, unroll_steps=None, block=None):
 
 def pf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
     """Pfaffian of a batch of skew-symmetric matrices (reference ``pf``, api.py:215-227);
-    odd n gives 0."""
+    odd n gives 0. Options as for slogpf."""
     a = _prep(a)
     x3 = prec_flag(check_prec(prec, a.dtype))
+    note_ignored("upd_warps", upd_warps)
     _on_device(a)
     A, batch, n = _flat(a)
     if n % 2 == 1:
@@ -131,4 +144,12 @@ def pf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
     return _diff.pf(A, bool(skew_symmetrize), x3).reshape(batch)
 
 
-__all__ = ["slogdet", "slogpf", "det", "pf", "FermixFallbackWarning", "FermixDeviceError"]
+__all__ = [
+    "slogdet",
+    "slogpf",
+    "det",
+    "pf",
+    "FermixFallbackWarning",
+    "FermixDeviceError",
+    "FermixTuneWarning",
+]

@@ -46,17 +46,31 @@ def _compile(hipcc, src, obj):
     return obj
 
 
-def build(verbose=False, jobs=None):
-    """Compile and link the library; returns its path."""
+def _stale(src, obj, deps_mtime):
+    """True when obj is missing or older than its source or any shared header."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return t < os.path.getmtime(src) or t < deps_mtime
+
+
+def build(verbose=False, jobs=None, incremental=False):
+    """Compile and link the library; returns its path. incremental=True recompiles only
+    the sources whose object is older than the source or a header (the default compiles
+    everything)."""
     hipcc = _hipcc()
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(
         os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip")
     )
     objs = [os.path.join(BUILD, os.path.basename(s)[:-4] + ".o") for s in srcs]
-    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)))
+    headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    headers.append(os.path.join(os.path.dirname(HERE), "include", "fermix.h"))
+    deps = max(os.path.getmtime(h) for h in headers if os.path.exists(h))
+    todo = [(s, o) for s, o in zip(srcs, objs) if not incremental or _stale(s, o, deps)]
+    jobs = jobs or min(max(1, len(todo)), max(1, (os.cpu_count() or 4)))
     with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
-        futs = [ex.submit(_compile, hipcc, s, o) for s, o in zip(srcs, objs)]
+        futs = [ex.submit(_compile, hipcc, s, o) for s, o in todo]
         for f in futs:
             o = f.result()
             if verbose:
@@ -73,5 +87,5 @@ def build(verbose=False, jobs=None):
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv[1:])
     sys.exit(0)

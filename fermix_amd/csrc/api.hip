@@ -94,7 +94,8 @@ static int family(int n, int tiny_max, int large_max) {
     default: break;
   }
   if (n <= tiny_max) return FAM_TINY;
-  return n <= SMALL_MAX ? FAM_FUSED : FAM_BLOCKED;
+  const int fused_max = tune().fused_max_n < SMALL_MAX ? tune().fused_max_n : SMALL_MAX;
+  return n <= fused_max ? FAM_FUSED : FAM_BLOCKED;
 }
 
 static int lu_family(int n) { return family(n, TINY_MAXN, LARGE_MAX); }
@@ -114,8 +115,15 @@ static bool al4(const void* p) { return ((uintptr_t)p & 3) == 0; }
 static constexpr int64_t BATCH_CHUNK = 65528;
 static int64_t chunk_batch(int64_t batch) { return batch < BATCH_CHUNK ? batch : BATCH_CHUNK; }
 
-// prec argument of the entry points: FX_PREC_IEEE (fp32 MFMA) or FX_PREC_BF16X3.
+// prec argument of the entry points: FX_PREC_IEEE (fp32 MFMA) or FX_PREC_BF16X3; the
+// LU factorisations also take an FX_LU_BLOCK_* option in the same word.
 static bool bad_prec(int32_t prec) { return prec != FX_PREC_IEEE && prec != FX_PREC_BF16X3; }
+static bool bad_lu_prec(int32_t prec) {
+  return (prec & ~(FX_PREC_MASK | FX_LU_BLOCK_MASK)) != 0 || bad_prec(prec & FX_PREC_MASK) ||
+         (prec & FX_LU_BLOCK_MASK) == FX_LU_BLOCK_MASK;
+}
+static int x3_of(int32_t prec) { return prec & FX_PREC_MASK; }
+static int block_of(int32_t prec) { return prec & FX_LU_BLOCK_MASK; }
 
 template <class F>
 static int for_chunks(int64_t batch, F&& f) {
@@ -143,7 +151,7 @@ const char* fx_status_string(int status) {
   }
 }
 
-int fx_abi_version(void) { return 200; }
+int fx_abi_version(void) { return 201; }
 
 int32_t fx_lu_padded_size(int32_t n) {
   if (n <= 0) return 0;
@@ -170,7 +178,7 @@ size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {
 
 int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, int32_t prec,
                    void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || n < 0 || bad_lu_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(workspace)) return FX_ERR_INVALID_ARGUMENT;
@@ -182,7 +190,7 @@ int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float*
     case FAM_BLOCKED:
       return for_chunks(batch, [&](int64_t b0, int64_t nb) {
         return launch_lu_large(a + b0 * n * n, n, nb, sign + b0, logabs + b0, workspace, workspace_bytes, false,
-                               nullptr, nullptr, s, nullptr, nullptr, prec);
+                               nullptr, nullptr, s, nullptr, nullptr, x3_of(prec), block_of(prec));
       });
     default: return FX_ERR_UNSUPPORTED;
   }
@@ -219,7 +227,7 @@ size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n) {
 int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_singular,
                          float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm, int32_t prec,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || n < 0 || bad_lu_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if ((lu == nullptr) != (perm == nullptr)) return FX_ERR_INVALID_ARGUMENT;
@@ -252,7 +260,8 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
       st = lu_fused_factors(fam, ab, n, nb, sg, lg, LU, g0, s);
     } else {
       const size_t wl = lu_large_workspace(nb, n, true);
-      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s, nullptr, nullptr, prec);
+      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s, nullptr, nullptr, x3_of(prec),
+                           block_of(prec));
       p += align256(wl);
     }
     if (st != FX_OK) return st;
@@ -264,7 +273,7 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
     if (!inv_t) return FX_OK;
     const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
     return launch_lu_inverse(LU, g0, N, n, nb, sg, zero_singular, inv_t + b0 * n * n, true, p, rest, s, nullptr,
-                             prec);
+                             x3_of(prec));
   });
 }
 
@@ -275,7 +284,7 @@ size_t fx_slogdet_factors_f32_workspace(int64_t batch, int32_t n) {
 
 int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* lu,
                            int32_t* perm, int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || n < 0 || bad_lu_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && (!a || !lu || !perm))) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(lu) || !al16(perm) || !al16(workspace))
@@ -288,7 +297,7 @@ int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign
   const int N = fx_lu_padded_size(n);
   return for_chunks(batch, [&](int64_t b0, int64_t nb) {
     return launch_lu_large(a + b0 * n * n, n, nb, sign + b0, logabs + b0, workspace, workspace_bytes, true, nullptr,
-                           nullptr, s, lu + b0 * N * N, (int*)perm + b0 * N, prec);
+                           nullptr, s, lu + b0 * N * N, (int*)perm + b0 * N, x3_of(prec), block_of(prec));
   });
 }
 
@@ -324,7 +333,7 @@ size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n) {
 
 int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
                      int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || n < 0 || bad_lu_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && (!a || !adj_t))) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(a) || !al4(sign) || !al4(logabs) || !al16(adj_t) || !al16(workspace)) return FX_ERR_INVALID_ARGUMENT;
@@ -352,7 +361,8 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
       st = lu_fused_factors(fam, ab, n, nb, sg, lg, LU, g0, s);
     } else {
       const size_t wl = lu_large_workspace(nb, n, true);
-      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s, nullptr, nullptr, prec);
+      st = launch_lu_large(ab, n, nb, sg, lg, p, wl, true, &LU, &g0, s, nullptr, nullptr, x3_of(prec),
+                           block_of(prec));
       p += align256(wl);
     }
     if (st != FX_OK) return st;
@@ -363,7 +373,7 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
     st = launch_det_adjugate_prep(LU, g0, N, n, nb, dws, &scale, s);
     if (st != FX_OK) return st;
     const size_t rest = workspace_bytes - (size_t)(p - (char*)workspace);
-    st = launch_lu_inverse(LU, g0, N, n, nb, sg, 0, adj, true, p, rest, s, scale, prec);
+    st = launch_lu_inverse(LU, g0, N, n, nb, sg, 0, adj, true, p, rest, s, scale, x3_of(prec));
     if (st != FX_OK) return st;
     return launch_det_adjugate_finish(n, nb, dws, adj, s);
   });

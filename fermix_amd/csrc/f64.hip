@@ -10,10 +10,11 @@
 // update tau w^T - w tau^T (`_slogpf_generic`, :266-300).
 //
 // Kernels (each a single workgroup per matrix):
-//  - n <= 128, gjreg64_kernel<RW, NC, CH, INV> / pfreg64_kernel<RW, NC, CH>: the matrix in
-//    registers, each thread a 16- or 32-column strip of one row; per column (pair) step the
+//  - n <= 128 (fx_tune.f64_reg_max_n), gjreg64_kernel<RW, NC, CH, INV> /
+//    pfreg64_kernel<RW, NC, CH>: the matrix in registers, each thread a 16-column (n <= 64,
+//    fx_tune.f64_strip16_max_n) or 32-column strip of one row; per column (pair) step the
 //    owners post the pivot candidates and the pivot row(s) through LDS, two barriers;
-//  - n > 128, gj64_kernel<NT, INV> / pr64_kernel<NT>: the matrix in LDS when it fits in
+//  - larger n, gj64_kernel<NT, INV> / pr64_kernel<NT>: the matrix in LDS when it fits in
 //    60 KiB, else in a per-matrix slice of the workspace (rows served from L2).
 // Gauss-Jordan (gj*): virtual partial pivoting (the pivot row of column j is the
 // unassigned row of largest |x|, lowest row index on ties). Without INV only the
@@ -532,9 +533,9 @@ int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, d
                 int out_t, const double* gate, void* ws, size_t ws_bytes, hipStream_t s) {
   const bool inv = out != nullptr;
   const int ld = inv ? 2 * n : n;
-  if (n <= 128) {  // register-resident
+  if (n <= tune().f64_reg_max_n) {  // register-resident
     const dim3 grid((unsigned)batch);
-    if (n <= 64) {
+    if (n <= tune().f64_strip16_max_n) {
       if (inv)
         gjreg64_kernel<64, 16, 8, true><<<grid, 512, 0, s>>>(a, n, skew, sign, logabs, out, out_t, gate);
       else
@@ -561,9 +562,9 @@ int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, d
 
 int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
                 size_t ws_bytes, hipStream_t s) {
-  if (n <= 128) {  // register-resident
+  if (n <= tune().f64_reg_max_n) {  // register-resident
     const dim3 grid((unsigned)batch);
-    if (n <= 64)
+    if (n <= tune().f64_strip16_max_n)
       pfreg64_kernel<64, 32, 2><<<grid, 128, 0, s>>>(a, n, skew, sign, logabs);
     else
       pfreg64_kernel<128, 32, 4><<<grid, 512, 0, s>>>(a, n, skew, sign, logabs);
@@ -577,9 +578,9 @@ int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, d
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
-// Workspace of the Gauss-Jordan path: none in registers (n <= 128) or LDS.
+// Workspace of the Gauss-Jordan path: none in registers (n <= f64_reg_max_n) or LDS.
 size_t gj64_ws(int64_t batch, int n, bool inv) {
-  return n <= 128 ? 0 : f64_matrix_ws(batch, n, inv ? 2 * n : n);
+  return n <= tune().f64_reg_max_n ? 0 : f64_matrix_ws(batch, n, inv ? 2 * n : n);
 }
 
 // Argument checks shared by the float64 entry points: the alignment contract of the ABI
@@ -629,7 +630,7 @@ int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign
 }
 
 size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n) {
-  return n > F64_MAXN || n <= 128 ? 0 : f64_matrix_ws(batch, n, n);
+  return n > F64_MAXN || n <= tune().f64_reg_max_n ? 0 : f64_matrix_ws(batch, n, n);
 }
 
 int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign, double* logabs,

@@ -6,6 +6,9 @@
 
 namespace fx {
 
+// The tuning values in effect (tune.hip): the gfx950 table, or the fx_tune_override.
+const fx_tune& tune();
+
 // dst[i] = src[i] for i < count: count a multiple of 4, both pointers 16-byte aligned.
 int launch_copy(const float* src, float* dst, int64_t count, hipStream_t s);
 
@@ -44,10 +47,12 @@ int launch_pf_small(const float* A, int n, int skew, int64_t batch, float* sign,
 constexpr int LU_LARGE_MAXN = 4096;
 int lu_large_padded(int n);
 size_t lu_large_workspace(int64_t batch, int n, bool parts, bool external = false);
-// x3 != 0 runs the trailing updates in the split-bf16x3 mode (FX_PREC_BF16X3).
+// x3 != 0 runs the trailing updates in the split-bf16x3 mode (FX_PREC_BF16X3); lu_block is
+// FX_LU_BLOCK_TABLE, FX_LU_BLOCK_64 or FX_LU_BLOCK_128 (block pairs from the table, never,
+// always).
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
                     size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s,
-                    float* W_ext = nullptr, int* g0_ext = nullptr, int x3 = 0);
+                    float* W_ext = nullptr, int* g0_ext = nullptr, int x3 = 0, int lu_block = FX_LU_BLOCK_TABLE);
 
 // A^-T from the packed LU (B, N, N) and row map g0 (B, N) into invT (B, n, n); LU is
 // overwritten when in_place and N is a power-of-two multiple of 32 (inverse.hip).

@@ -745,7 +745,9 @@ static int launch_gemm_t(const GemmDesc& d, int64_t batch, int nb2, hipStream_t 
   // triangular-inverse level 18 % and the skew R product 15 % faster); at M = 512 and
   // below, and for short K, the coarser triangle trimming and the longer prologue /
   // epilogue per K stage make the 64 x 64 tiles faster
-  const bool big = vec && !d.transB && d.M >= 1024 && d.N >= 1024 && d.K >= 512 && !d.tout;
+  const fx_tune& tu = tune();
+  const bool big = vec && !d.transB && d.M >= tu.gemm128_min_mn && d.N >= tu.gemm128_min_mn &&
+                   d.K >= tu.gemm128_min_k && !d.tout;
   if (d.tout && (d.lower_only || nb2 != 1 || d.active)) return FX_ERR_INVALID_ARGUMENT;
   if (d.bscale && (d.maskB != MASK_NONE || d.transB || d.K % 2 || nb2 != 1 || !vec)) return FX_ERR_INVALID_ARGUMENT;
   const int tm2 = (d.M + 127) / 128, tn2 = (d.N + 127) / 128;

@@ -888,13 +888,10 @@ static int launch_update(float* W, int N, int64_t batch, int r0, int ntr, int nt
 // first pair, reading the input in place of a copy, composes both into srcs[2].
 template <int MR, int NT>
 static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int* const srcs[3], float* X,
-                      int* g0, bool fact, const float* A_in, hipStream_t s, int x3) {
+                      int* g0, bool fact, const float* A_in, hipStream_t s, int x3, bool paired) {
   constexpr int PW = 64;
   const int nblk = N / PW;
   constexpr int MAXM = MR < 1024 ? 1024 : MR;
-  // unpaired blocks at N <= 256 (measured: the pairs' extra launches and the U-row
-  // correction cost more there than the K = 128 update saves)
-  const bool paired = N > 256;
   auto urow = [&](int r0, const int* src, int lfirst, int nleft, int nright, const float* A0, const int* rmap,
                   int rc, int* comp) {
     if (nleft + nright == 0) return FX_OK;
@@ -953,7 +950,7 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
 // and the composed row map g0 (parts only) through *g0_out.
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
                     size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s, float* W_ext,
-                    int* g0_ext, int x3) {
+                    int* g0_ext, int x3, int lu_block) {
   const int N = lu_large_padded(n);
   const int PW = lu_panel_width(N);
   const int nblk = N / PW;
@@ -977,7 +974,11 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   // No padding and panels held in registers throughout (N <= 1024): the first block's
   // kernels read the input directly and together write all of W, so no copy is made.
   // Otherwise the input is copied (identity-padded) into W first.
-  const bool direct = n == N && N <= 1024 && ((uintptr_t)A & 15) == 0;
+  const fx_tune& tn = tune();
+  const bool direct = n == N && N <= tn.lu_direct_max_n && N <= 1024 && ((uintptr_t)A & 15) == 0;
+  // block pairs (one K = 128 update per pair) per the call's option, else the table (at
+  // N <= 256 the pairs' extra launches and U-row correction cost more than they save)
+  const bool paired = lu_block == FX_LU_BLOCK_128 || (lu_block != FX_LU_BLOCK_64 && N > tn.lu_pair_above_n);
   if (!direct) {
     if (n == N && ((uintptr_t)A & 15) == 0) {  // no padding: a straight streaming copy
       const int st = launch_copy(A, W, batch * (int64_t)N * N, s);
@@ -995,11 +996,11 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
   }
   int st;
   if (N <= 1024)
-    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, srcs, X, g0, parts, direct ? A : nullptr, s, x3);
+    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, srcs, X, g0, parts, direct ? A : nullptr, s, x3, paired);
   else if (N <= 2048)
-    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3);
+    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3, paired);
   else
-    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3);
+    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3, paired);
   if (st != FX_OK) return st;
   hipLaunchKernelGGL(lu_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, piv, nsw, N,
                      nblk, sign, logabs, batch);

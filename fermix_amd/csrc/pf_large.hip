@@ -39,12 +39,15 @@ constexpr int PFB_XL = 16;  // every block of 2048 < N <= PF_LARGE_MAXN
 // the 32 (16 above N = 2048) columns of a block, or one half of a 64-column block.
 int pf_large_block_cols(int N) { return N > 2048 ? PFB_XL : PFB; }
 
-// Columns of the block at r0: 64 once the trailing order m = N - r0 is at most 1024, for
-// N >= 512 a multiple of 64 (G (m x 64) in the registers of 256 / 512 threads; the
-// trailing updates' HBM traffic halves), else 32; 16 above N = 2048.
+// Columns of the block at r0: 64 once the trailing order m = N - r0 is at most
+// fx_tune.pf_block64_max_m (1024 in the table, the register limit: G (m x 64) in the
+// registers of 256 / 512 threads; the trailing updates' HBM traffic halves), for N >=
+// fx_tune.pf_block64_min_n (512) a multiple of 64, else 32; 16 above N = 2048.
 static int pf_block_width(int N, int r0) {
   if (N > 2048) return PFB_XL;
-  return (N >= 512 && N % PFB_L == 0 && N - r0 <= 1024 && r0 % PFB_L == 0) ? PFB_L : PFB;
+  const fx_tune& t = tune();
+  const int max_m = t.pf_block64_max_m < 1024 ? t.pf_block64_max_m : 1024;
+  return (N >= t.pf_block64_min_n && N % PFB_L == 0 && N - r0 <= max_m && r0 % PFB_L == 0) ? PFB_L : PFB;
 }
 
 struct PfCand {
@@ -491,9 +494,16 @@ static __global__ void pf_iota_kernel(int* g, int N, int64_t total) {
 
 int pf_large_padded(int n) { return ((n + 31) / 32) * 32; }
 
-// Widest block of padded order N (the block at m = min(N, 1024) is the first that can be
-// 64 columns wide).
-static int pf_max_width(int N) { return pf_block_width(N, N > 1024 ? N - 1024 : 0); }
+// Widest block of padded order N, over the block sequence launch_pf_large runs.
+static int pf_max_width(int N) {
+  int w = 0;
+  for (int r0 = 0; r0 < N;) {
+    const int pb = pf_block_width(N, r0);
+    w = pb > w ? pb : w;
+    r0 += pb;
+  }
+  return w;
+}
 
 size_t pf_large_workspace(int64_t batch, int n, bool fact) {
   const int N = pf_large_padded(n);

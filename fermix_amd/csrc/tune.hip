@@ -1,0 +1,96 @@
+// The gfx950 tuning table and its override (fx_tune_table / fx_tune_override /
+// fx_tune_active): the launch choices the host code makes from n alone. Counterpart of
+// the reference's Tune / TUNES[arch][kind] / OVERRIDE / _tune (src/fermix/_common.py:
+// 17-378), whose per-architecture values are Triton tiles and warps; the values here
+// are the size thresholds of this library's own dispatch decisions, each measured on
+// MI355X:
+//  - fused_max_n 128: the one-workgroup-per-matrix kernels hold an n <= 128 matrix in
+//    LDS (40 KiB at n = 128, four matrices per CU) and beat the blocked kernels there;
+//  - lu_pair_above_n 256: LU blocks in pairs (one K = 128 trailing update per pair)
+//    lost 1.6 % at N = 256 (their extra U-row correction and launches) and win above
+//    (slogdet B = 1024, n = 512 2.54 -> 2.46 ms; B = 64, n = 2048 11.48 -> 10.40 ms);
+//  - lu_direct_max_n 1024: the largest order whose panels are held in registers, so the
+//    first block pair can read the input in place of a copy;
+//  - pf_block64_min_n 512 / pf_block64_max_m 1024: 64-column Parlett-Reid blocks halve
+//    the trailing updates' traffic (B = 256, n = 1024 5.33 -> 3.97 ms) but at N = 256 the
+//    panel's halved occupancy loses (2.44 -> 3.20 ms); m <= 1024 is the register limit
+//    of the 64-column panel;
+//  - gemm128_min_mn 1024 / gemm128_min_k 512: 128 x 128 GEMM tiles won on the n = 2048
+//    products (triangular-inverse top level -18 %, R = Y^T D Y -15 %) and lost at
+//    M = 512 and for short K (coarser triangle trimming, longer prologue per stage);
+//  - f64_reg_max_n 128 / f64_strip16_max_n 64: float64 matrices in registers for
+//    n <= 128 (slogdet n = 128 8.66 -> 3.16 ms against the LDS kernel), in 16-column strips
+//    for n <= 64 (n = 64 1.37 ms; at n = 128 they lose, 3.97 against 3.16 ms).
+#include <atomic>
+#include <string.h>
+
+#include "common.h"
+#include "fermix_internal.h"
+
+namespace fx {
+namespace {
+
+constexpr fx_tune GFX950 = {
+    /* fused_max_n */ 128,
+    /* lu_pair_above_n */ 256,
+    /* lu_direct_max_n */ 1024,
+    /* pf_block64_min_n */ 512,
+    /* pf_block64_max_m */ 1024,
+    /* gemm128_min_mn */ 1024,
+    /* gemm128_min_k */ 512,
+    /* f64_reg_max_n */ 128,
+    /* f64_strip16_max_n */ 64,
+    /* reserved */ {0, 0, 0, 0, 0, 0, 0},
+};
+
+fx_tune g_override;
+std::atomic<bool> g_has_override{false};
+
+bool valid(const fx_tune& t) {
+  auto in = [](int32_t v, int32_t lo, int32_t hi) { return v >= lo && v <= hi; };
+  for (int32_t r : t.reserved)
+    if (r != 0) return false;
+  return in(t.fused_max_n, TINY_MAXN, 128) && in(t.lu_pair_above_n, 0, 1 << 30) &&
+         in(t.lu_direct_max_n, 0, 1024) && in(t.pf_block64_min_n, 128, 1 << 30) &&
+         in(t.pf_block64_max_m, 0, 1024) && in(t.gemm128_min_mn, 128, 1 << 30) &&
+         in(t.gemm128_min_k, 64, 1 << 30) && in(t.f64_reg_max_n, 0, 128) && in(t.f64_strip16_max_n, 0, 64);
+}
+
+}  // namespace
+
+const fx_tune& tune() { return g_has_override.load(std::memory_order_acquire) ? g_override : GFX950; }
+
+}  // namespace fx
+
+using namespace fx;
+
+extern "C" {
+
+int fx_tune_table(const char* arch, fx_tune* out) {
+  if (!arch || !out) return FX_ERR_INVALID_ARGUMENT;
+  // a full device name may carry target features ("gfx950:sramecc+:xnack-")
+  const size_t len = strcspn(arch, ":");
+  if (len != 6 || strncmp(arch, "gfx950", 6) != 0) return FX_ERR_UNSUPPORTED;
+  *out = GFX950;
+  return FX_OK;
+}
+
+int fx_tune_override(const fx_tune* t) {
+  if (!t) {
+    g_has_override.store(false, std::memory_order_release);
+    return FX_OK;
+  }
+  if (!valid(*t)) return FX_ERR_INVALID_ARGUMENT;
+  g_has_override.store(false, std::memory_order_release);
+  g_override = *t;
+  g_has_override.store(true, std::memory_order_release);
+  return FX_OK;
+}
+
+int fx_tune_active(fx_tune* out) {
+  if (!out) return FX_ERR_INVALID_ARGUMENT;
+  *out = tune();
+  return FX_OK;
+}
+
+}  // extern "C"

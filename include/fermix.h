@@ -24,16 +24,19 @@
  *    members on the stream, and their *_workspace sizes are those of one chunk;
  *  - the return value is a status code (FX_OK on success); numerical edge cases are
  *    encoded in the values (an exactly zero pivot gives sign 0 and logabs -inf);
- *  - calls are reentrant; the library keeps no mutable global state (apart from the
- *    once-per-device address of the scratch array of fx_slogdet_f32_noalloc);
+ *  - calls are reentrant; the library keeps no mutable global state apart from the
+ *    once-per-device address of the scratch array of fx_slogdet_f32_noalloc and the
+ *    tuning-table override of fx_tune_override;
  *  - the kernel family is chosen from n alone (never from the batch): several matrices
  *    per wave (n <= 32 for slogdet, 16 for slogpf), one fused workgroup per matrix
- *    (n <= 128), blocked kernels with workspace (n <= 4096). The environment variable
+ *    (n <= fx_tune.fused_max_n, 128 in the gfx950 table), blocked kernels with workspace
+ *    (n <= 4096); the blocked kernels' own choices follow the tuning table below, whose
+ *    fx_tune_override is the reference's OVERRIDE hook. The environment variable
  *    FERMIX_AMD_KERNELS = tiny | fused | blocked, read on every call, forces a family
  *    where it covers n (FX_ERR_UNSUPPORTED elsewhere); the padded orders, block widths
  *    and workspace sizes reported below follow it, so query them under the same setting
- *    as the call. This replaces the reference's tuning-table OVERRIDE hook
- *    (src/fermix/_common.py:363-378).
+ *    as the call (a test hook like the reference's OVERRIDE, src/fermix/_common.py:
+ *    363-378).
  */
 #ifndef FERMIX_AMD_H
 #define FERMIX_AMD_H
@@ -67,6 +70,74 @@ typedef void* fx_stream_t; /* hipStream_t */
  * points therefore take no prec. */
 #define FX_PREC_IEEE 0
 #define FX_PREC_BF16X3 1
+
+/* Option bits or-ed into the prec argument of the slogdet / det entry points (float32):
+ * the outer LU block of the blocked family (n > 128), the reference's per-call `block`
+ * (src/fermix/api.py:92-97, _common.py:31-41). The factorisation is built from 64-column
+ * panels whose trailing updates go either one block at a time (K = 64) or in pairs of
+ * blocks (one K = 128 update per pair):
+ *  - FX_LU_BLOCK_TABLE (0): the tuning table's choice (pairs for padded N above
+ *    fx_tune.lu_pair_above_n);
+ *  - FX_LU_BLOCK_64: single 64-column blocks;
+ *  - FX_LU_BLOCK_128: blocks in pairs, K = 128 updates.
+ * The choice changes the rounding of the factorisation, so a gradient call must pass the
+ * option of the forward call it differentiates (sign / logabs are then bit-identical).
+ * fx_slogdet_inverse_f32 and the slogpf entry points accept prec values without option
+ * bits only. */
+#define FX_PREC_MASK 0x0f
+#define FX_LU_BLOCK_TABLE 0x000
+#define FX_LU_BLOCK_64 0x100
+#define FX_LU_BLOCK_128 0x200
+#define FX_LU_BLOCK_MASK 0x300
+
+/* ---------------------------------------------------------------- tuning table
+ * The library's launch choices for one GPU architecture: the counterpart of the
+ * reference's Tune / TUNES[arch][kind] / OVERRIDE (src/fermix/_common.py:17-378), whose
+ * fields are Triton tiles and warps; here every field is a size threshold of a dispatch
+ * decision the host code makes from n alone (never from the batch). The float32 fields
+ * steer the fp32 kernels, the f64_ fields the float64 ones. Ranges are those the compiled
+ * kernels support; values outside them are rejected by fx_tune_override. */
+typedef struct fx_tune {
+  /* float32 families: n <= fused_max_n (above the several-matrices-per-wave sizes,
+   * n <= 32 for slogdet and n <= 16 for slogpf, which are fixed) runs one workgroup per
+   * matrix with the matrix in LDS; larger n runs the blocked kernels. 32 .. 128 */
+  int32_t fused_max_n;
+  /* blocked LU: 64-column blocks in pairs (one K = 128 trailing update per pair) for
+   * padded order N > lu_pair_above_n (FX_LU_BLOCK_TABLE). >= 0 */
+  int32_t lu_pair_above_n;
+  /* blocked LU: the first block pair reads the input in place of a copy into the
+   * workspace when n = N <= lu_direct_max_n (16-byte aligned input). 0 .. 1024 */
+  int32_t lu_direct_max_n;
+  /* blocked Parlett-Reid (N <= 2048): 64-column blocks once the trailing order is at most
+   * pf_block64_max_m, for padded orders N >= pf_block64_min_n that are multiples of 64;
+   * 32-column blocks otherwise (16 above N = 2048). 128 .. 4096 / 0 .. 1024 */
+  int32_t pf_block64_min_n;
+  int32_t pf_block64_max_m;
+  /* GEMMs of the inverses and adjugates: 128 x 128 tiles when M, N >= gemm128_min_mn
+   * and K >= gemm128_min_k, else 64 x 64 (bit-identical results). >= 128 / >= 64 */
+  int32_t gemm128_min_mn;
+  int32_t gemm128_min_k;
+  /* float64: the matrix in registers for n <= f64_reg_max_n (0 .. 128), with rows split
+   * in 16-column strips for n <= f64_strip16_max_n (0 .. 64) and 32-column ones above;
+   * larger n runs one workgroup per matrix in LDS or in the workspace */
+  int32_t f64_reg_max_n;
+  int32_t f64_strip16_max_n;
+  int32_t reserved[7]; /* zero */
+} fx_tune;
+
+/* The table of an architecture ("gfx950"; FX_ERR_UNSUPPORTED for any other name: the
+ * library holds gfx950 code only). */
+int fx_tune_table(const char* arch, fx_tune* out);
+
+/* Replace the table for every later call in the process (NULL: back to the table) -- the
+ * reference's OVERRIDE hook, for tuning sweeps and tests. FX_ERR_INVALID_ARGUMENT (and no
+ * change) for a field outside its range. Workspace sizes follow the active values, so
+ * query them after setting an override. Not to be changed while another thread is inside
+ * an entry point of the library. */
+int fx_tune_override(const fx_tune* t);
+
+/* The values in effect (the override if one is set, else the gfx950 table). */
+int fx_tune_active(fx_tune* out);
 
 /* Human-readable text of a status code (static storage). */
 const char* fx_status_string(int status);

@@ -28,7 +28,7 @@ def _np(x):
 def _families(n, op):
     out = []
     for f in ("tiny", "fused", "blocked"):
-        with _tune.override(f):
+        with _tune.force_family(f):
             if _tune.kernel_family(n, op) != "unsupported":
                 out.append(f)
     return out
@@ -46,7 +46,7 @@ def test_slogdet_families_agree(dev, n):
     assert "blocked" in fams and (len(fams) >= 2 or n > 128)
     res = {}
     for f in fams:
-        with _tune.override(f):
+        with _tune.force_family(f):
             print(f"slogdet n={n} family={f}", flush=True)
             s, l = fermix_amd.slogdet(_t(A, dev))
             sp, lp, invT, _, _ = _kernels.slogdet_parts(_t(A, dev))
@@ -74,7 +74,7 @@ def test_slogpf_families_agree(dev, n):
     fams = _families(n, "slogpf")
     assert "blocked" in fams and (len(fams) >= 2 or n > 128)
     for f in fams:
-        with _tune.override(f):
+        with _tune.force_family(f):
             print(f"slogpf n={n} family={f}", flush=True)
             s, l = fermix_amd.slogpf(_t(S, dev), skew_symmetrize=False)
             sp, lp, Sinv = _kernels.slogpf_parts(_t(S, dev), False)
@@ -96,7 +96,7 @@ def test_det_adjugate_any_family(dev, family):
     A[0, :, 3] = 0.0
     A[1, :, 0] = 0.0
     A[1, :, 1] = 0.0
-    with _tune.override(family):
+    with _tune.force_family(family):
         At = _t(A, dev).requires_grad_()
         d = fermix_amd.det(At)
         (g,) = torch.autograd.grad(d.sum(), At)
@@ -110,6 +110,6 @@ def test_det_adjugate_any_family(dev, family):
 
 def test_unsupported_family_raises(dev):
     A = torch.zeros((2, 40, 40), device=dev)
-    with _tune.override("tiny"):
+    with _tune.force_family("tiny"):
         with pytest.raises(fermix_amd._lib.FermixLibraryError):
             fermix_amd.slogdet(A)

@@ -3,8 +3,10 @@ entry point include/fermix.h declares (no compute calls without a GPU); the Pyth
 raises the reference's error types (src/fermix/api.py:24-31,92-97; _field.py:265-275)."""
 
 import ctypes
+import dataclasses
 import os
 import re
+import warnings
 
 import numpy as np
 import pytest
@@ -39,7 +41,7 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_calls():
     L = _lib.lib()
-    assert L.fx_abi_version() == 200
+    assert L.fx_abi_version() == 201
     assert L.fx_status_string(0) == b"ok"
     assert L.fx_lu_padded_size(100) == 112
     assert L.fx_pf_padded_size(128) == 128
@@ -56,14 +58,14 @@ def test_family_override_sizes():
     """The padded orders and workspaces follow the forced family (host-only queries)."""
     L = _lib.lib()
     assert L.fx_lu_padded_size(20) == 32 and L.fx_slogdet_f32_workspace(4, 20) == 0
-    with _tune.override("blocked"):
+    with _tune.force_family("blocked"):
         assert L.fx_lu_padded_size(20) == 64 and L.fx_pf_padded_size(20) == 32
         assert L.fx_slogdet_f32_workspace(4, 20) > 0 and L.fx_pf_block_columns(20) == 32
     # factor chunks: 32 columns for the blocked Parlett-Reid up to 2048, 16 above
     assert [L.fx_pf_block_columns(n) for n in (100, 200, 256, 500, 512, 1024, 1025, 2048, 2049)] == [16, 32, 32, 32, 32, 32, 32, 32, 16]
-    with _tune.override("tiny"):
+    with _tune.force_family("tiny"):
         assert L.fx_lu_padded_size(40) == -1 and L.fx_pf_padded_size(20) == -1
-    with _tune.override("fused"):
+    with _tune.force_family("fused"):
         assert L.fx_lu_padded_size(20) == -1 and L.fx_lu_padded_size(100) == 112
     assert L.fx_lu_padded_size(20) == 32
 
@@ -190,3 +192,104 @@ def test_prec_argument_validated():
         assert L.fx_det_parts_f32(good, 2, 300, good, good, good, bad_prec, ws, 1 << 40, None) == 1
         assert L.fx_slogpf_inverse_f32(good, good, good, None, 2, 300, 0, good, bad_prec, ws, 1 << 40, None) == 1
         assert L.fx_slogpf_parts_f32(good, 2, 300, 0, 0, good, good, good, bad_prec, ws, 1 << 40, None) == 1
+
+
+def test_lu_block_option_validated():
+    """The FX_LU_BLOCK_* option bits are accepted by the LU factorisations only, and
+    FX_LU_BLOCK_64 | FX_LU_BLOCK_128 together, or unknown bits, are rejected before any
+    device work (batch 0 returns FX_OK once the arguments pass)."""
+    L = _lib.lib()
+    good, ws = 0x10000, 0x20000
+    for opt in (_lib.FX_LU_BLOCK_64, _lib.FX_LU_BLOCK_128, _lib.FX_LU_BLOCK_128 | 1):
+        assert L.fx_slogdet_f32(good, 0, 300, good, good, opt, ws, 1 << 40, None) == 0
+        assert L.fx_slogdet_parts_f32(good, 0, 300, 1, good, good, good, None, None, opt, ws, 1 << 40, None) == 0
+        assert L.fx_slogdet_factors_f32(good, 0, 300, good, good, good, good, opt, ws, 1 << 40, None) == 0
+        assert L.fx_det_parts_f32(good, 0, 300, good, good, good, opt, ws, 1 << 40, None) == 0
+        # the inverse and the Parlett-Reid entry points take no option bits
+        assert L.fx_slogdet_inverse_f32(good, good, good, None, 2, 300, 1, good, opt, ws, 1 << 40, None) == 1
+        assert L.fx_slogpf_parts_f32(good, 2, 300, 0, 0, good, good, good, opt, ws, 1 << 40, None) == 1
+    for bad in (_lib.FX_LU_BLOCK_64 | _lib.FX_LU_BLOCK_128, 0x400, 0x10, _lib.FX_LU_BLOCK_64 | 2):
+        assert L.fx_slogdet_f32(good, 0, 300, good, good, bad, ws, 1 << 40, None) == 1
+        assert L.fx_slogdet_parts_f32(good, 0, 300, 1, good, good, good, None, None, bad, ws, 1 << 40, None) == 1
+        assert L.fx_det_parts_f32(good, 0, 300, good, good, good, bad, ws, 1 << 40, None) == 1
+
+
+def test_tuning_table_in_library():
+    """The gfx950 table the C library holds is the one fermix_amd._tune states; other
+    architecture names are refused; target features after ':' are ignored."""
+    assert _tune.library_table("gfx950") == _tune.TUNES["gfx950"] == _tune.table()
+    assert _tune.library_table("gfx950:sramecc+:xnack-") == _tune.TUNES["gfx950"]
+    L = _lib.lib()
+    t = _lib.FxTune()
+    assert L.fx_tune_table(b"gfx942", t) == 4 and L.fx_tune_table(b"gfx9500", t) == 4
+    assert _tune.active() == _tune.table()
+    with pytest.raises(ValueError):
+        _tune.table("gfx90a")
+
+
+def test_tuning_override():
+    """The override hook replaces the table for later calls (dispatch and workspace
+    queries follow it), rejects values outside the compiled kernels' ranges without
+    changing anything, and the context manager restores the table."""
+    L = _lib.lib()
+    base = _tune.table()
+    # fused family up to 128 by the table; lowered, n = 100 goes to the blocked kernels
+    assert L.fx_lu_padded_size(100) == 112 and L.fx_slogdet_f32_workspace(4, 100) == 0
+    assert _tune.kernel_family(100) == "fused-lds"
+    with _tune.override(fused_max_n=64) as t:
+        assert t.fused_max_n == 64 and _tune.active() == t
+        assert L.fx_lu_padded_size(100) == 128 and L.fx_slogdet_f32_workspace(4, 100) > 0
+        assert L.fx_pf_padded_size(100) == 128 and L.fx_pf_block_columns(100) == 32
+        assert _tune.kernel_family(100) == "blocked" and _tune.kernel_family(64) == "fused-lds"
+    assert _tune.active() == base and L.fx_lu_padded_size(100) == 112
+    # 64-column Parlett-Reid blocks need a G buffer twice as wide: the workspace follows
+    w64 = L.fx_slogpf_f32_workspace(4, 1024)
+    with _tune.override(pf_block64_max_m=0):
+        w32 = L.fx_slogpf_f32_workspace(4, 1024)
+    with _tune.override(pf_block64_min_n=2048):
+        assert L.fx_slogpf_f32_workspace(4, 1024) == w32
+    assert w32 < w64 == L.fx_slogpf_f32_workspace(4, 1024)
+    # float64: the register kernels need no workspace; lowered, n = 100 takes the LDS /
+    # workspace kernel (n * 2n doubles do not fit its LDS for the inverse)
+    assert L.fx_slogdet_parts_f64_workspace(4, 100) == 0
+    with _tune.override(f64_reg_max_n=64):
+        assert L.fx_slogdet_parts_f64_workspace(4, 100) > 0
+    for bad in (
+        dict(fused_max_n=129),
+        dict(fused_max_n=16),
+        dict(lu_direct_max_n=2048),
+        dict(pf_block64_max_m=2048),
+        dict(pf_block64_min_n=64),
+        dict(gemm128_min_mn=64),
+        dict(f64_reg_max_n=256),
+        dict(f64_strip16_max_n=128),
+        dict(lu_pair_above_n=-1),
+    ):
+        with pytest.raises(_lib.FermixLibraryError):
+            _tune.set_override(dataclasses.replace(base, **bad))
+        assert _tune.active() == base
+    t = _lib.FxTune()
+    assert L.fx_tune_active(t) == 0
+    t.reserved[3] = 1
+    assert L.fx_tune_override(t) == 1 and _tune.active() == base
+
+
+def test_knob_warnings():
+    """The reference's knobs without a gfx950 counterpart warn (FermixTuneWarning) instead
+    of passing silently; block=32 maps to 64 with a warning; valid block values do not
+    warn. (The device check comes after: CPU tensors still raise FermixDeviceError.)"""
+    A = torch.zeros((2, 4, 4), dtype=torch.float32)
+    with pytest.warns(fermix_amd.FermixTuneWarning, match="unroll_steps"):
+        with pytest.raises(fermix_amd.FermixDeviceError):
+            fermix_amd.slogdet(A, unroll_steps=True)
+    with pytest.warns(fermix_amd.FermixTuneWarning, match="upd_warps"):
+        with pytest.raises(fermix_amd.FermixDeviceError):
+            fermix_amd.slogpf(A, upd_warps=8)
+    with pytest.warns(fermix_amd.FermixTuneWarning, match="block=32"):
+        assert _tune.block_flag(32) == _lib.FX_LU_BLOCK_64
+    assert _tune.block_flag(None) == 0 and _tune.block_flag(128) == _lib.FX_LU_BLOCK_128
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        for blk in (None, 64, 128):
+            with pytest.raises(fermix_amd.FermixDeviceError):
+                fermix_amd.det(A, block=blk)
