@@ -17,8 +17,10 @@ fold into the kernels' batch, so vmap(f)(x) runs exactly the arithmetic of f(x))
   adjugate pf(S) S^-1 from the forward's own Parlett-Reid factors (finite for singular
   S); G is skew, so it is also the gradient w.r.t. ``a`` through S = (a - a^T)/2.
 
-float64 inputs take the parts route (A^-T / S^-1 formed with the primal by the f64
-kernels); their det / pf derivatives (the exact adjugates) raise NotImplementedError.
+float64 and complex inputs take the parts route (A^-T / S^-1 formed with the primal by
+the float64 / complex kernels); for complex kinds the sign is differentiable too, with
+the reference's conventions (see _log_tangents below). Their det / pf derivatives (the
+exact adjugates) raise NotImplementedError.
 """
 
 import torch
@@ -79,6 +81,49 @@ def _unfold(x, vb):
     return x.reshape(vb + tuple(x.shape[1:]))
 
 
+# complex kinds (the reference's _log_tangents, src/fermix/_diff.py:92-98): with
+# t = tr(A^-1 dA) (tr(S^-1 dS) / 2 for slogpf), d logabs = Re t and d sign = i Im(t) sign --
+# jnp.linalg.slogdet's convention -- and for real kinds d sign = 0. In torch's reverse
+# mode (the gradient of a real loss L is the conjugate Wirtinger one, dL = Re(conj(g) dz))
+# a sign cotangent g_s and a logabs cotangent g_l give g_A = (g_l - i Im(conj(g_s) sign))
+# conj(M), where t = sum(M * dA).
+
+
+def _keep_sign(ctx, sign, M):
+    """setup_context of the parts rules: M is the gradient matrix (sum(M * dA) = t); the
+    sign is differentiable for complex kinds only."""
+    if sign.is_complex():
+        ctx.mark_non_differentiable(M)
+    else:
+        ctx.mark_non_differentiable(sign, M)
+    ctx.set_materialize_grads(False)  # no zero fills for the unused outputs
+    ctx.save_for_backward(sign, M)
+    ctx.save_for_forward(sign, M)
+
+
+def _log_cotangent(sign, g_sign, g_logabs):
+    """The per-member factor k with g_A = k conj(M) (real kinds: g_logabs); None if no
+    cotangent reaches the derivative."""
+    if not sign.is_complex():
+        return g_logabs
+    k = None if g_logabs is None else g_logabs.to(sign.dtype)
+    if g_sign is not None:
+        ks = -1j * (g_sign.conj() * sign).imag
+        k = ks if k is None else k + ks
+    return k
+
+
+def _apply_cotangent(k, M):
+    return k[:, None, None] * (M.conj() if M.is_complex() else M)
+
+
+def _log_tangents(sign, t):
+    """(d sign, d logabs) from t: None and t for real kinds."""
+    if not sign.is_complex():
+        return None, t
+    return 1j * t.imag * sign, t.real
+
+
 # ----------------------------------------------------------------- slogdet
 
 
@@ -113,23 +158,21 @@ class _SlogdetParts(torch.autograd.Function):
     @staticmethod
     def setup_context(ctx, inputs, output):
         sign, logabs, invT = output
-        ctx.mark_non_differentiable(sign, invT)
-        ctx.set_materialize_grads(False)  # no zero fills for the unused outputs
-        ctx.save_for_backward(invT)
-        ctx.save_for_forward(invT)
+        _keep_sign(ctx, sign, invT)
 
     @staticmethod
     def backward(ctx, g_sign, g_logabs, g_invT):
-        (invT,) = ctx.saved_tensors
-        if g_logabs is None:
+        sign, invT = ctx.saved_tensors
+        k = _log_cotangent(sign, g_sign, g_logabs)
+        if k is None:
             return None, None
-        return g_logabs[:, None, None] * invT, None
+        return _apply_cotangent(k, invT), None
 
     @staticmethod
     def jvp(ctx, dA, _x3):
-        (invT,) = ctx.saved_tensors
-        dlog = (invT * dA).sum(dim=(-1, -2))
-        return None, dlog, None
+        sign, invT = ctx.saved_tensors
+        ds, dlog = _log_tangents(sign, (invT * dA).sum(dim=(-1, -2)))
+        return ds, dlog, None
 
     @staticmethod
     def vmap(info, in_dims, A, x3):
@@ -234,23 +277,21 @@ class _SlogpfParts(torch.autograd.Function):
     @staticmethod
     def setup_context(ctx, inputs, output):
         sign, logabs, Sinv = output
-        ctx.mark_non_differentiable(sign, Sinv)
-        ctx.set_materialize_grads(False)  # no zero fills for the unused outputs
-        ctx.save_for_backward(Sinv)
-        ctx.save_for_forward(Sinv)
+        _keep_sign(ctx, sign, Sinv)
 
     @staticmethod
     def backward(ctx, g_sign, g_logabs, g_sinv):
-        (Sinv,) = ctx.saved_tensors
-        if g_logabs is None:
+        sign, Sinv = ctx.saved_tensors
+        k = _log_cotangent(sign, g_sign, g_logabs)
+        if k is None:
             return None, None, None
-        return (-0.5 * g_logabs)[:, None, None] * Sinv, None, None
+        return _apply_cotangent(-0.5 * k, Sinv), None, None
 
     @staticmethod
     def jvp(ctx, dA, _skew, _x3):
-        (Sinv,) = ctx.saved_tensors
-        dlog = -0.5 * (Sinv * dA).sum(dim=(-1, -2))
-        return None, dlog, None
+        sign, Sinv = ctx.saved_tensors
+        ds, dlog = _log_tangents(sign, -0.5 * (Sinv * dA).sum(dim=(-1, -2)))
+        return ds, dlog, None
 
     @staticmethod
     def vmap(info, in_dims, A, skew, x3):

@@ -25,6 +25,9 @@ def _workspace(nbytes, device):
     return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
 
 
+_CPLX = {torch.complex64: "c64", torch.complex128: "c128"}
+
+
 def _check_input(A, f64_ok=False):
     """Returns True for a float64 input (the f64 entry points), False for float32."""
     if not A.is_cuda:
@@ -35,6 +38,49 @@ def _check_input(A, f64_ok=False):
     return A.dtype == torch.float64
 
 
+def _real_dtype(dt):
+    return torch.float32 if dt == torch.complex64 else torch.float64
+
+
+def _cplx_input(A):
+    """The kind suffix ("c64" / "c128") of a complex input, else None."""
+    k = _CPLX.get(A.dtype)
+    if k is None:
+        return None
+    if not A.is_cuda:
+        raise RuntimeError("fermix_amd kernels need a tensor on a ROCm GPU")
+    if A.dim() != 3 or not A.is_contiguous():
+        raise RuntimeError("internal: expected a contiguous (B, n, n) complex tensor")
+    return k
+
+
+def _cplx_call(A, name, skew=None, want_out=False, adjugate=False):
+    """complex64 / complex128: (sign, logabs[, out]) from fx_<name>_<kind>; sign complex
+    (B,), logabs real (B,), out (B, n, n) complex (A^-T for slogdet_parts, S^-1 for
+    slogpf_parts)."""
+    k = _cplx_input(A)
+    A = _aligned(A)
+    B, n, _ = A.shape
+    dev = A.device
+    sign = torch.empty(B, dtype=A.dtype, device=dev)
+    logabs = torch.empty(B, dtype=_real_dtype(A.dtype), device=dev)
+    out = torch.empty_like(A) if want_out else None
+    L = lib()
+    fn = f"fx_{name}_{k}"
+    ws, wsb = _workspace(getattr(L, fn + "_workspace")(B, n), dev)
+    args = [_ptr(A), B, n]
+    if skew is not None:
+        args.append(int(bool(skew)))
+    if name == "slogpf_parts":
+        args.append(int(bool(adjugate)))
+    args += [_ptr(sign), _ptr(logabs)]
+    if name.endswith("_parts"):
+        args.append(_ptr(out))
+    args += [_ptr(ws), wsb, _stream(A)]
+    check(getattr(L, fn)(*args), fn)
+    return (sign, logabs, out) if name.endswith("_parts") else (sign, logabs)
+
+
 def _aligned(A):
     """A itself when its data is 16-byte aligned (the C ABI's contract), else an aligned
     copy: a view into a batch at an odd member offset of an odd-n batch is not."""
@@ -42,10 +88,11 @@ def _aligned(A):
 
 
 def _no_f64(A, what):
-    if A.dtype == torch.float64:
+    if A.dtype != torch.float32:
         raise NotImplementedError(
-            f"fermix_amd: {what} is implemented for float32 only (float64 has slogdet / "
-            "slogpf / det / pf values and the slogdet / slogpf derivatives)"
+            f"fermix_amd: {what} is implemented for float32 only (float64 / complex64 / "
+            "complex128 have slogdet / slogpf / det / pf values and the slogdet / slogpf "
+            "derivatives)"
         )
 
 
@@ -60,6 +107,8 @@ def pf_padded_size(n):
 def slogdet(A, x3=0):
     """(sign, logabs) of each (n, n) matrix of A (B, n, n); x3: the C ABI's prec word
     (FX_PREC_BF16X3 products, FX_LU_BLOCK_* options; float32 only)."""
+    if A.is_complex():
+        return _cplx_call(A, "slogdet")
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape
@@ -79,8 +128,13 @@ def slogdet(A, x3=0):
 
 def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False, x3=0):
     """(sign, logabs, invT, lu, perm) with the optional outputs None when not asked for;
-    lu / perm are padded to N = lu_padded_size(n). float64: invT only (zero for exactly
-    singular members), no packed factors."""
+    lu / perm are padded to N = lu_padded_size(n). float64 and complex: invT only (zero
+    for exactly singular members), no packed factors."""
+    if A.is_complex():
+        if want_lu or not zero_singular:
+            _no_f64(A, "the packed LU / unguarded inverse")
+        sign, logabs, invT = _cplx_call(A, "slogdet_parts", want_out=want_inv)
+        return sign, logabs, invT, None, None
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape
@@ -171,6 +225,8 @@ def det_parts(A, x3=0):
 
 
 def slogpf(A, skew_symmetrize):
+    if A.is_complex():
+        return _cplx_call(A, "slogpf", skew=skew_symmetrize)
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape
@@ -240,6 +296,8 @@ def slogpf_parts(A, skew_symmetrize, adjugate=False, x3=0):
     or, with adjugate, pf(S) S^-1 (float32 only)."""
     if adjugate:
         _no_f64(A, "the pf gradient (Pfaffian adjugate)")
+    if A.is_complex():
+        return _cplx_call(A, "slogpf_parts", skew=skew_symmetrize, want_out=True)
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape

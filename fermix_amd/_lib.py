@@ -80,6 +80,18 @@ SIGNATURES = {
     "fx_slogpf_parts_f64_workspace": (_sz, [_i64, _i32]),
     "fx_slogpf_parts_f64": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _sz, _p]),
 }
+# complex64 / complex128: the float64 signatures with interleaved (re, im) buffers
+for _k in ("c64", "c128"):
+    SIGNATURES.update({
+        f"fx_slogdet_{_k}_workspace": (_sz, [_i64, _i32]),
+        f"fx_slogdet_{_k}": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _sz, _p]),
+        f"fx_slogdet_parts_{_k}_workspace": (_sz, [_i64, _i32]),
+        f"fx_slogdet_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _sz, _p]),
+        f"fx_slogpf_{_k}_workspace": (_sz, [_i64, _i32]),
+        f"fx_slogpf_{_k}": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _sz, _p]),
+        f"fx_slogpf_parts_{_k}_workspace": (_sz, [_i64, _i32]),
+        f"fx_slogpf_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _sz, _p]),
+    })
 
 
 class FermixLibraryError(RuntimeError):

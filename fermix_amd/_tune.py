@@ -40,13 +40,14 @@ class FermixTuneWarning(UserWarning):
 
 def check_prec(prec, dtype=None):
     """The mode a `prec` argument selects ("ieee" or "bf16x3"). The reduced-precision
-    modes are float32-only (the reference rejects "tf32x3" for 64-bit types,
-    src/fermix/_field.py:265-275)."""
+    modes apply to the 32-bit kinds only (the reference rejects "tf32x3" for float64 /
+    complex128, src/fermix/_field.py:265-275); complex64 accepts them but runs no MFMA
+    product (its kernels are unblocked), so they do not change its results."""
     if prec is None:
         return DEFAULT_PREC
     if prec not in PREC:
         raise ValueError(f"prec must be one of {PREC}, got {prec!r}")
-    if prec != "ieee" and dtype is not None and dtype != torch.float32:
+    if prec != "ieee" and dtype is not None and dtype not in (torch.float32, torch.complex64):
         raise ValueError(
             f"prec={prec!r} applies to float32 / complex64 only; float64 and "
             "complex128 run in IEEE fp64 (prec='ieee')"

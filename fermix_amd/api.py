@@ -18,6 +18,12 @@ Conventions kept from the reference:
   d pf = tr(pf(S) S^-1 dS)/2, finite and exact for singular inputs; the primal of a
   differentiated call is bit-identical to the plain forward.
 
+dtypes: float32, float64, complex64 and complex128 (the reference's four kinds); for
+complex inputs sign is a unit complex number (prod(d / |d|) times the parity) and
+logabs real, and the derivatives follow jnp.linalg's convention (d logabs = Re t,
+d sign = i Im(t) sign with t = tr(A^-1 dA)); torch's reverse mode then gives the
+gradient of logabs as conj(A^-T).
+
 Device handling: the product path is the HIP library on a ROCm GPU. A CPU tensor
 raises ``FermixDeviceError`` (the reference's generic XLA fallback is not part of this
 build) -- there is no silent CPU path.
@@ -49,10 +55,6 @@ def _prep(a):
         )
     if a.dim() < 2 or a.shape[-1] != a.shape[-2]:
         raise ValueError(f"expected (..., n, n), got {tuple(a.shape)}")
-    if a.dtype not in (torch.float32, torch.float64):
-        raise TypeError(
-            f"fermix_amd implements the float32 and float64 paths; got {a.dtype}"
-        )
     return a
 
 

@@ -275,4 +275,43 @@ __device__ __forceinline__ void load_tile(float* As, const float* __restrict__ g
   }
 }
 
+// ---- 64-bit workgroup argmax (the float64 and complex kernels)
+
+// Order-preserving key of a pivot candidate: |x| bits plus one (0 = no candidate).
+__device__ __forceinline__ unsigned long long key64(double x) {
+  return (unsigned long long)__double_as_longlong(fabs(x)) + 1ull;
+}
+
+__device__ __forceinline__ void take_better(unsigned long long& k, int& r, unsigned long long k2, int r2) {
+  if (k2 > k || (k2 == k && r2 < r)) {
+    k = k2;
+    r = r2;
+  }
+}
+
+// Workgroup argmax of (key, row), larger key first, then lower row; every thread returns
+// the winning row (-1 if no thread had a candidate). redk / redr: NT / 64 slots; the
+// caller alternates two slot sets between consecutive calls, so no extra barrier guards
+// their reuse.
+template <int NT>
+__device__ __forceinline__ int block_argmax(unsigned long long k, int r, unsigned long long* redk, int* redr) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long k2 = __shfl_xor(k, off);
+    const int r2 = __shfl_xor(r, off);
+    take_better(k, r, k2, r2);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    redk[w] = k;
+    redr[w] = r;
+  }
+  __syncthreads();
+  k = redk[0];
+  r = redr[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) take_better(k, r, redk[i], redr[i]);
+  return k ? r : -1;
+}
+
 }  // namespace fx

@@ -312,6 +312,56 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
                         double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
                         fx_stream_t stream);
 
+/* ---------------------------------------------------------------- complex
+ * The reference's complex kinds (complex64 / complex128 through the same API: `_prep`,
+ * src/fermix/api.py:24-31; the complex field, src/fermix/_field.py:32-120, 129-162). A
+ * complex matrix is interleaved (re, im) pairs, row-major and batch-major (the memory of
+ * a C99 complex array, or of torch's complex tensors): a[2 (b n n + i n + j) + {0, 1}];
+ * sign is one complex value per member (2 floats / doubles), logabs real. Conventions of
+ * the generic path (src/fermix/_fallback.py:36-55, 266-300): the pivot is the candidate
+ * of largest |re| + |im| (LAPACK's cabs1, the reference's `abs1`), sign = parity *
+ * prod(d / |d|), logabs = sum log|d|, an exactly zero pivot gives sign 0 and logabs -inf;
+ * inv_t = A^-T without conjugation (the holomorphic derivative of log det, as in
+ * `_lu_parts_generic`, :63-97). Unblocked kernels, one workgroup per matrix, the matrix in
+ * LDS when it fits (else one copy per member in the workspace; twice that with the
+ * inverse), 0 <= n <= 4096. The pf adjugate mode returns FX_ERR_UNSUPPORTED. */
+size_t fx_slogdet_c64_workspace(int64_t batch, int32_t n);
+int fx_slogdet_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, void* workspace,
+                   size_t workspace_bytes, fx_stream_t stream);
+size_t fx_slogdet_c128_workspace(int64_t batch, int32_t n);
+int fx_slogdet_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
+                    size_t workspace_bytes, fx_stream_t stream);
+
+/* sign / logabs bit-identical to fx_slogdet_c64 / _c128, plus inv_t (batch, n, n) = A^-T
+ * (NULL to skip), zero for members with an exactly zero pivot or a non-finite inverse. */
+size_t fx_slogdet_parts_c64_workspace(int64_t batch, int32_t n);
+int fx_slogdet_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* inv_t,
+                         void* workspace, size_t workspace_bytes, fx_stream_t stream);
+size_t fx_slogdet_parts_c128_workspace(int64_t batch, int32_t n);
+int fx_slogdet_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
+                          void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* pf of complex skew-symmetric S (S^T = -S; S = (a - a^T) / 2 if skew_symmetrize != 0):
+ * Parlett-Reid with the pivot swapped into column c + 1 (`_slogpf_generic`,
+ * src/fermix/_fallback.py:266-300); odd n gives (0, -inf). */
+size_t fx_slogpf_c64_workspace(int64_t batch, int32_t n);
+int fx_slogpf_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign, float* logabs,
+                  void* workspace, size_t workspace_bytes, fx_stream_t stream);
+size_t fx_slogpf_c128_workspace(int64_t batch, int32_t n);
+int fx_slogpf_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign,
+                   double* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
+/* sign / logabs bit-identical to fx_slogpf_c64 / _c128, plus g (batch, n, n) = S^-1 (NULL
+ * to skip), zero where pf(S) = 0 (odd n, an exactly zero pivot) or S^-1 is not finite. */
+size_t fx_slogpf_parts_c64_workspace(int64_t batch, int32_t n);
+int fx_slogpf_parts_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
+                        float* sign, float* logabs, float* g, void* workspace, size_t workspace_bytes,
+                        fx_stream_t stream);
+size_t fx_slogpf_parts_c128_workspace(int64_t batch, int32_t n);
+int fx_slogpf_parts_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
+                         double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
+                         fx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,7 +1,8 @@
 """The reference's generic (jax.numpy) path restated in numpy -- TEST INFRASTRUCTURE.
 
 Every function works on a batch (B, n, n) and keeps the input dtype (float32 in,
-float32 arithmetic), citing the reference function it follows. The LU is LAPACK
+float32 arithmetic; slogdet / slogpf and lu_parts also take float64, complex64 and
+complex128, the reference's other kinds), citing the reference function it follows. The LU is LAPACK
 ``?getrf`` (the routine ``lax.linalg.lu`` calls on the CPU) and the triangular solves
 are LAPACK ``?trtrs`` (``lax.linalg.triangular_solve``'s CPU routine); the rest --
 pivot bookkeeping, pairwise reductions, the masked Parlett-Reid, the gradient
@@ -40,7 +41,12 @@ def lu_factor(A):
     the permutation with (P A)[c] = A[perm[c]]."""
     A = np.asarray(A)
     B, n, _ = A.shape
-    getrf = _lapack.sgetrf if A.dtype == np.float32 else _lapack.dgetrf
+    getrf = {
+        np.dtype(np.float32): _lapack.sgetrf,
+        np.dtype(np.float64): _lapack.dgetrf,
+        np.dtype(np.complex64): _lapack.cgetrf,
+        np.dtype(np.complex128): _lapack.zgetrf,
+    }[A.dtype]
     lu = np.empty_like(A)
     piv = np.empty((B, n), np.int32)
     for b in range(B):
@@ -60,18 +66,25 @@ def lu_factor(A):
 def slog_from_lu(lu, piv):
     """(sign, logabs) of P L U from the diagonal of U and the swap sequence (reference
     ``_fallback.py:36-55``): parity = number of non-trivial swaps + number of negative
-    pivots; a zero pivot gives (0, -inf); log|det| is a pairwise sum of log|d|."""
+    pivots (real), or the pairwise product of the pivots' unit phases d / |d| with the
+    swap parity's sign flip (complex); a zero pivot gives (0, -inf); log|det| is a
+    pairwise sum of log|d| in the real dtype."""
     d = np.diagonal(lu, axis1=-2, axis2=-1)
     iota = np.arange(lu.shape[-1])
     swaps = np.sum(piv != iota, axis=-1)
     zero = np.any(d == 0, axis=-1)
     dsafe = np.where(d == 0, np.ones_like(d), d)
-    parity = swaps + np.sum(d < 0, axis=-1)
-    sign = np.where(parity % 2 == 1, -1.0, 1.0).astype(lu.dtype)
+    rdt = np.finfo(lu.dtype).dtype
+    if np.iscomplexobj(lu):
+        sign = pairwise((dsafe / np.abs(dsafe)).astype(lu.dtype), np.multiply, 1)
+        sign = np.where(swaps % 2 == 1, -sign, sign)
+    else:
+        parity = swaps + np.sum(d < 0, axis=-1)
+        sign = np.where(parity % 2 == 1, -1.0, 1.0).astype(lu.dtype)
     sign = np.where(zero, np.zeros_like(sign), sign)
     with np.errstate(divide="ignore"):
-        logsum = pairwise(np.log(np.abs(dsafe)), np.add, 0)
-    logabs = np.where(zero, -np.inf, logsum).astype(lu.dtype)
+        logsum = pairwise(np.log(np.abs(dsafe)).astype(rdt), np.add, 0)
+    logabs = np.where(zero, -np.inf, logsum).astype(rdt)
     return sign, logabs
 
 
@@ -151,14 +164,15 @@ def slogpf_generic(S):
     dt = A.dtype
     idx = np.arange(n)[None, :]
     sign = np.ones(B, dt)
-    log = np.zeros(B, dt)
+    log = np.zeros(B, np.finfo(dt).dtype)
     with np.errstate(divide="ignore", invalid="ignore"):
         for k in range(n // 2):
             c = 2 * k
             A, kp, _, d, _, _ = _pr_step(A, c, idx)
             sign = np.where(kp != c + 1, -sign, sign)
+            # sign(d): d / |d| for complex d (numpy >= 2 and jnp.sign alike)
             sign = sign * np.sign(d)
-            log = (log + np.log(np.abs(d))).astype(dt)
+            log = (log + np.log(np.abs(d))).astype(log.dtype)
     return sign.astype(dt), log
 
 

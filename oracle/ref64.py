@@ -2,8 +2,8 @@
 and checks the GPU results). Written from the definitions, independent of the
 algorithms under test where possible:
 
-* ``slogdet64`` -- numpy's LAPACK slogdet in float64 (the reference's own tests use
-  it, ``tests/test_fermix.py:153-155``);
+* ``slogdet64`` -- numpy's LAPACK slogdet in float64 / complex128 (the reference's own
+  tests use it, ``tests/test_fermix.py:153-155``);
 * ``pf_brute`` -- the Pfaffian as a signed sum over perfect matchings (expansion along
   the first row), exact up to float64 rounding, n <= 10;
 * ``pf_pr64`` -- a float64 Parlett-Reid (the textbook algorithm, cross-checked against
@@ -21,15 +21,22 @@ import math
 import numpy as np
 
 
+def _wide(x):
+    """float64, or complex128 for complex input."""
+    x = np.asarray(x)
+    return x.astype(np.complex128 if np.iscomplexobj(x) else np.float64)
+
+
 def slogdet64(A):
-    s, l = np.linalg.slogdet(np.asarray(A, np.float64))
+    s, l = np.linalg.slogdet(_wide(A))
     return s, l
 
 
 def pf_brute(S):
     """Pfaffian of one skew matrix by the perfect-matching expansion
-    pf(S) = sum_j (-1)^(j+1) s_0j pf(S without rows/cols 0, j) (0-based j >= 1)."""
-    S = np.asarray(S, np.float64)
+    pf(S) = sum_j (-1)^(j+1) s_0j pf(S without rows/cols 0, j) (0-based j >= 1); float64
+    or complex128."""
+    S = _wide(S)
     n = S.shape[0]
     if n % 2:
         return 0.0
@@ -47,12 +54,14 @@ def pf_brute(S):
 
 def pf_pr64(S):
     """(sign, log|pf|) of one skew matrix by Parlett-Reid with partial pivoting in
-    float64: pivot the largest |entry| of column k below row k into row/col k+1."""
-    A = np.array(S, np.float64)
+    float64 (complex128 for complex S, the sign then the unit phase): pivot the largest
+    |entry| of column k below row k into row/col k+1."""
+    A = _wide(S).copy()
+    cplx = np.iscomplexobj(A)
     n = A.shape[0]
     if n % 2:
         return 0.0, -math.inf
-    sign, log = 1.0, 0.0
+    sign, log = (1.0 + 0.0j if cplx else 1.0), 0.0
     for k in range(0, n - 1, 2):
         kp = k + 1 + int(np.argmax(np.abs(A[k + 1 :, k])))
         if kp != k + 1:
@@ -62,7 +71,7 @@ def pf_pr64(S):
         d = A[k, k + 1]
         if d == 0.0:
             return 0.0, -math.inf
-        sign *= math.copysign(1.0, d)
+        sign *= d / abs(d) if cplx else math.copysign(1.0, d)
         log += math.log(abs(d))
         x = A[k + 2 :, k].copy()
         y = A[k + 2 :, k + 1].copy()
@@ -76,9 +85,9 @@ def pf64(S):
 
 
 def slogpf64(Sb):
-    """Batched (sign, log|pf|) in float64."""
+    """Batched (sign, log|pf|) in float64 (complex128 sign for complex input)."""
     out = [pf_pr64(S) for S in np.asarray(Sb)]
-    return np.array([o[0] for o in out]), np.array([o[1] for o in out])
+    return np.array([o[0] for o in out]), np.array([o[1] for o in out], np.float64)
 
 
 def adjT_brute(A):

@@ -88,16 +88,23 @@ def test_api_errors():
         fermix_amd.slogdet(A)
     with pytest.raises(fermix_amd.FermixDeviceError):
         fermix_amd.slogpf(A)
-    # float64 is a supported dtype (device check next); tf32x3 is float32-only
-    # (reference src/fermix/_field.py:265-275); complex is not built
+    # float64 and complex are supported dtypes (device check next); tf32x3 is for the
+    # 32-bit kinds only (reference src/fermix/_field.py:265-275)
     with pytest.raises(fermix_amd.FermixDeviceError):
         fermix_amd.slogdet(A.double())
     with pytest.raises(ValueError):
         fermix_amd.slogdet(A.double(), prec="tf32x3")
     with pytest.raises(ValueError):
         fermix_amd.pf(A.double(), prec="tf32x3")
+    for dt in (torch.complex64, torch.complex128):
+        with pytest.raises(fermix_amd.FermixDeviceError):
+            fermix_amd.slogpf(A.to(dt))
+    with pytest.raises(fermix_amd.FermixDeviceError):
+        fermix_amd.slogdet(A.to(torch.complex64), prec="tf32x3")
+    with pytest.raises(ValueError):
+        fermix_amd.slogdet(A.to(torch.complex128), prec="tf32x3")
     with pytest.raises(TypeError):
-        fermix_amd.slogdet(A.to(torch.complex64))
+        fermix_amd.slogdet(A.to(torch.float16))
 
 
 def test_tune_table():
@@ -293,3 +300,26 @@ def test_knob_warnings():
         for blk in (None, 64, 128):
             with pytest.raises(fermix_amd.FermixDeviceError):
                 fermix_amd.det(A, block=blk)
+
+
+def test_complex_entry_points_host_checks():
+    """The complex entry points validate alignment (16 bytes for matrices / workspace,
+    the value size for sign / logabs), batch and n before any device work, and size
+    their workspace (none while the matrix fits the LDS limit)."""
+    L = _lib.lib()
+    good, bad, ws = 0x10000, 0x10008, 0x20000
+    for k, esz in (("c64", 4), ("c128", 8)):
+        f = getattr(L, f"fx_slogdet_{k}")
+        assert f(bad, 2, 40, good, good, ws, 1 << 40, None) == 1
+        assert f(good, 2, 40, good + esz, good, ws, 1 << 40, None) == 1  # sign: one complex value
+        assert f(good, -1, 40, good, good, ws, 1 << 40, None) == 1
+        assert f(good, 0, 40, good, good, ws, 1 << 40, None) == 0
+        assert f(good, 2, 5000, good, good, ws, 1 << 40, None) == 4
+        assert getattr(L, f"fx_slogdet_parts_{k}")(good, 2, 40, good, good, bad, ws, 1 << 40, None) == 1
+        assert getattr(L, f"fx_slogpf_{k}")(bad, 2, 40, 0, good, good, ws, 1 << 40, None) == 1
+        assert getattr(L, f"fx_slogpf_parts_{k}")(good, 2, 40, 0, 0, good, good, bad, ws, 1 << 40, None) == 1
+        assert getattr(L, f"fx_slogpf_parts_{k}")(good, 2, 40, 0, 1, good, good, good, ws, 1 << 40, None) == 4
+        assert getattr(L, f"fx_slogdet_{k}_workspace")(4, 40) == 0
+        w = getattr(L, f"fx_slogdet_{k}_workspace")(4, 300)
+        assert w == 4 * 300 * 300 * 2 * esz
+        assert getattr(L, f"fx_slogdet_parts_{k}_workspace")(4, 300) == 2 * w

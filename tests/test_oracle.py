@@ -320,3 +320,87 @@ def test_planted_mistakes_are_caught():
     _, _, invT, _, _, _ = g.lu_parts_generic(A)
     ref = np.linalg.inv(A.astype(np.float64)).transpose(0, 2, 1)
     assert relerr(np.swapaxes(invT, 1, 2), ref) > 1e-2
+
+
+# --------------------------------------------------------------- complex kinds
+def crandn(shape, dtype=np.complex64):
+    return (rng.standard_normal(shape) + 1j * rng.standard_normal(shape)).astype(dtype)
+
+
+@pytest.mark.parametrize("dtype", [np.complex64, np.complex128])
+def test_complex_oracle_slogdet_and_inverse(dtype):
+    """Complex slogdet of the oracle (reference _slog_from_lu's complex branch,
+    _fallback.py:36-55: sign = parity * prod(d / |d|)) against numpy's complex128 slogdet,
+    with sign of the input dtype and logabs of its real dtype; the closed form of a
+    permuted diagonal (sign = parity * prod of the phases, logabs = sum log|d_i|); A^-T
+    without conjugation (lu_parts, _fallback.py:63-97) against numpy's inverse; and a zero
+    column gives (0, -inf) and a zero gradient."""
+    tol = 1e-4 if dtype == np.complex64 else 1e-11
+    for n in (1, 4, 17, 40):
+        A = crandn((5, n, n), dtype)
+        s, l = g.slogdet_generic(A)
+        s64, l64 = ref64.slogdet64(A)
+        assert s.dtype == dtype and l.dtype == np.finfo(dtype).dtype
+        assert np.max(np.abs(s - s64)) < tol * max(1, n / 8)
+        assert np.max(np.abs(l - l64)) < tol * max(1, n / 8)
+        _, _, invT, _, _, _ = g.lu_parts_generic(A)
+        ref = np.linalg.inv(A.astype(np.complex128)).transpose(0, 2, 1)
+        assert relerr(invT, ref) < 100 * tol
+        assert relerr(invT, ref.conj()) > 0.1  # not the conjugate
+    n = 7
+    d = crandn((n,), np.complex128)
+    p = rng.permutation(n)
+    M = (np.eye(n)[p] * d[p][:, None]).astype(dtype)  # row i = d[p[i]] e_p[i]
+    s, l = g.slogdet_generic(M[None])
+    inv = sum(1 for i, j in itertools.combinations(range(n), 2) if p[i] > p[j])
+    phase = np.prod(d / np.abs(d)) * (-1) ** inv
+    assert abs(s[0] - phase) < tol and abs(l[0] - np.sum(np.log(np.abs(d)))) < tol * n
+    A = crandn((2, 6, 6), dtype)
+    A[0, :, 2] = 0
+    s, l, invT, _, _, _ = g.lu_parts_generic(A)
+    assert s[0] == 0 and l[0] == -np.inf and np.all(invT[0] == 0) and abs(abs(s[1]) - 1) < tol
+
+
+@pytest.mark.parametrize("dtype", [np.complex64, np.complex128])
+def test_complex_oracle_slogpf(dtype):
+    """Complex slogpf of the oracle (reference _slogpf_generic, _fallback.py:266-300, with
+    sign(d) = d / |d|) against the perfect-matching Pfaffian (n <= 8), pf^2 = det at larger
+    n, the closed form pf(a_1 J + ... + a_k J) = prod a_i, and a zero row / column (0, -inf)."""
+    tol = 1e-4 if dtype == np.complex64 else 1e-11
+    for n in (2, 4, 8):
+        S = skew(crandn((4, n, n), dtype))
+        s, l = g.slogpf_generic(S)
+        brute = np.array([ref64.pf_brute(x) for x in S])
+        assert np.max(np.abs(s * np.exp(l) - brute)) < tol * np.max(np.abs(brute)) * n
+    S = skew(crandn((3, 30, 30), dtype))
+    s, l = g.slogpf_generic(S)
+    sd, ld = ref64.slogdet64(S)
+    assert np.max(np.abs(s * s - sd)) < 10 * tol and np.max(np.abs(2 * l - ld)) < 10 * tol * 30
+    a = crandn((4,), np.complex128)
+    D = np.zeros((8, 8), np.complex128)
+    for i in range(4):
+        D[2 * i, 2 * i + 1], D[2 * i + 1, 2 * i] = a[i], -a[i]
+    s, l = g.slogpf_generic(D.astype(dtype)[None])
+    assert abs(s[0] * np.exp(l[0]) - np.prod(a)) < tol * abs(np.prod(a)) * 8
+    S = skew(crandn((1, 6, 6), dtype))
+    S[0, 3, :] = 0
+    S[0, :, 3] = 0
+    s, l = g.slogpf_generic(S)
+    assert s[0] == 0 and l[0] == -np.inf
+
+
+def test_complex_planted_mistakes_are_caught():
+    """A complex sign without the pivot phases (the real parity rule applied to complex
+    pivots) and a conjugated inverse fail the complex pins."""
+    A = crandn((3, 6, 6), np.complex128)
+    lu, piv, _ = g.lu_factor(A)
+    s, _ = g.slog_from_lu(lu, piv)
+    s64, _ = ref64.slogdet64(A)
+    assert np.max(np.abs(s - s64)) < 1e-10
+    d = np.diagonal(lu, axis1=-2, axis2=-1)
+    no_phase = np.where(np.sum(piv != np.arange(6), -1) % 2, -1.0, 1.0)
+    assert np.max(np.abs(no_phase - s64)) > 0.1
+    _, _, invT, _, _, _ = g.lu_parts_generic(A)
+    ref = np.linalg.inv(A).transpose(0, 2, 1)
+    assert relerr(invT.conj(), ref) > 0.1 and relerr(invT, ref) < 1e-10
+    assert np.all(np.abs(d) > 0)

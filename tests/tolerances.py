@@ -19,17 +19,24 @@ def ref_log_tol(n):
     return 2e-3 * max(1.0, n / 64)
 
 
+def _wide(x):
+    """float64, or complex128 when x is complex (a cast to float64 would drop the
+    imaginary part)."""
+    x = np.asarray(x)
+    return x.astype(np.complex128 if np.iscomplexobj(x) else np.float64)
+
+
 def rel_fro(x, ref):
-    x = np.asarray(x, np.float64)
-    ref = np.asarray(ref, np.float64)
+    x = _wide(x)
+    ref = _wide(ref)
     den = np.linalg.norm(ref.reshape(ref.shape[0], -1), axis=1)
     num = np.linalg.norm((x - ref).reshape(ref.shape[0], -1), axis=1)
     return num / np.maximum(den, 1e-300)
 
 
 def relerr(x, ref):
-    x = np.asarray(x, np.float64)
-    ref = np.asarray(ref, np.float64)
+    x = _wide(x)
+    ref = _wide(ref)
     return float(np.max(np.abs(x - ref)) / max(np.max(np.abs(ref)), 1e-30))
 
 
@@ -39,7 +46,7 @@ KAPPA_C = 4.0
 
 def kappa(A):
     """2-norm condition numbers of a batch, in float64."""
-    return np.linalg.cond(np.asarray(A, np.float64))
+    return np.linalg.cond(_wide(A))
 
 
 def assert_logabs(l, lref, n, what="", A=None):
