@@ -19,8 +19,9 @@ fold into the kernels' batch, so vmap(f)(x) runs exactly the arithmetic of f(x))
 
 float64 and complex inputs take the parts route (A^-T / S^-1 formed with the primal by
 the float64 / complex kernels); for complex kinds the sign is differentiable too, with
-the reference's conventions (see _log_tangents below). Their det / pf derivatives (the
-exact adjugates) raise NotImplementedError.
+the reference's conventions (see _log_tangents below). Their det derivative is the exact
+adjugate of the same Gauss-Jordan run (fx_det_parts_f64 / _c64 / _c128); their pf
+derivative (the Pfaffian adjugate) raises NotImplementedError.
 """
 
 import torch
@@ -382,7 +383,9 @@ class _DetParts(torch.autograd.Function):
         (adjT,) = ctx.saved_tensors
         if g_det is None:
             return None, None
-        return g_det[:, None, None] * adjT, None
+        # det is holomorphic: with dL = Re(conj(g) d det), the conjugate-Wirtinger
+        # gradient is g conj(adj(A)^T) (adj(A)^T itself for real kinds)
+        return _apply_cotangent(g_det, adjT), None
 
     @staticmethod
     def jvp(ctx, dA, _x3):

@@ -206,8 +206,25 @@ def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True, x3=0):
 
 
 def det_parts(A, x3=0):
-    """(sign, logabs, adjT) with adjT = adj(A)^T = d det / dA from one factorisation."""
-    _no_f64(A, "the det gradient (exact adjugate)")
+    """(sign, logabs, adjT) with adjT = adj(A)^T = d det / dA from one factorisation
+    (holomorphic, no conjugation, for complex A)."""
+    if A.dtype != torch.float32:
+        k = {torch.float64: "f64", torch.complex64: "c64", torch.complex128: "c128"}[A.dtype]
+        if not A.is_cuda:
+            raise RuntimeError("fermix_amd kernels need a tensor on a ROCm GPU")
+        A = _aligned(A.contiguous())
+        B, n, _ = A.shape
+        dev = A.device
+        sign = torch.empty(B, dtype=A.dtype, device=dev)
+        logabs = torch.empty(B, dtype=_real_dtype(A.dtype) if A.is_complex() else A.dtype, device=dev)
+        adjT = torch.empty_like(A)
+        L = lib()
+        ws, wsb = _workspace(getattr(L, f"fx_det_parts_{k}_workspace")(B, n), dev)
+        st = getattr(L, f"fx_det_parts_{k}")(
+            _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(adjT), _ptr(ws), wsb, _stream(A)
+        )
+        check(st, f"fx_det_parts_{k}")
+        return sign, logabs, adjT
     _check_input(A)
     A = _aligned(A)
     B, n, _ = A.shape

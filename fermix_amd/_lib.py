@@ -92,6 +92,12 @@ for _k in ("c64", "c128"):
         f"fx_slogpf_parts_{_k}_workspace": (_sz, [_i64, _i32]),
         f"fx_slogpf_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _sz, _p]),
     })
+# det's gradient (the exact adjugate) for the 64-bit and complex kinds
+for _k in ("f64", "c64", "c128"):
+    SIGNATURES.update({
+        f"fx_det_parts_{_k}_workspace": (_sz, [_i64, _i32]),
+        f"fx_det_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _sz, _p]),
+    })
 
 
 class FermixLibraryError(RuntimeError):

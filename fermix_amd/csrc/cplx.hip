@@ -11,12 +11,14 @@
 //
 // Kernels (one workgroup of 1024 threads per matrix; the matrix in LDS when it fits in
 // 60 KiB, else in a per-matrix slice of the workspace, served from L2):
-//  - cgj_kernel<T, INV>: Gauss-Jordan with virtual partial pivoting (the pivot of column
-//    j is the unassigned row of largest |re| + |im|, lowest row on ties). Without INV only
-//    the unassigned rows are updated (an LU); with INV the assigned rows and the identity
-//    block [A | I] too, and row j of A^-1 is row prow[j] of the right block times the
-//    pivot's reciprocal. The element update is the same in both, so the forward and the
-//    inverse call give bit-identical sign / logabs;
+//  - cgj_kernel<F, MODE>: Gauss-Jordan with virtual partial pivoting (the pivot of column
+//    j is the unassigned row of largest |re| + |im|, lowest row on ties), generic over the
+//    field F (cx<float>, cx<double>, and double for the float64 det gradient). GJ_FWD
+//    updates only the unassigned rows (an LU); GJ_INV / GJ_ADJ also the assigned rows and
+//    the identity block [A | I], and row j of A^-1 is row prow[j] of the right block times
+//    the pivot's reciprocal; GJ_ADJ forms det's gradient adj(A)^T from it, continued to
+//    exactly singular A. The element update is the same in every mode, so the gradient
+//    calls give bit-identical sign / logabs;
 //  - cpr_kernel<T>: Parlett-Reid with the pivot row / column swapped into position c + 1,
 //    d = S[c, c+1], tau = -S[:, c] / d, w = S[:, c+1] and the rank-2 update
 //    tau w^T - w tau^T on the rows and columns after c + 1.
@@ -36,144 +38,225 @@ struct cx {
   T re, im;
 };
 
+// ---- field operations: F = cx<float> / cx<double> (complex kinds) or double (the
+// float64 adjugate, which shares the Gauss-Jordan kernel below)
+template <class F>
+struct Fd;
 template <class T>
-__device__ __forceinline__ cx<T> cmul(cx<T> a, cx<T> b) {
-  return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
-}
+struct Fd<cx<T>> {
+  using R = T;  // real component type (logabs)
+  static __device__ __forceinline__ cx<T> zero() { return {T(0), T(0)}; }
+  static __device__ __forceinline__ cx<T> one() { return {T(1), T(0)}; }
+  static __device__ __forceinline__ bool is0(cx<T> x) { return x.re == T(0) && x.im == T(0); }
+  // pivot magnitude |re| + |im| (LAPACK's cabs1), exact in double for both kinds
+  static __device__ __forceinline__ unsigned long long key(cx<T> x) {
+    return key64((double)(fabs(x.re) + fabs(x.im)));
+  }
+  static __device__ __forceinline__ cx<T> mul(cx<T> a, cx<T> b) {
+    return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
+  }
+  // r - l p with fused products
+  static __device__ __forceinline__ cx<T> fms(cx<T> r, cx<T> l, cx<T> p) {
+    return {fma(-l.re, p.re, fma(l.im, p.im, r.re)), fma(-l.re, p.im, fma(-l.im, p.re, r.im))};
+  }
+  // 1 / x = conj(x) / |x|^2, 0 -> 0
+  static __device__ __forceinline__ cx<T> rcp(cx<T> x) {
+    const T s = x.re * x.re + x.im * x.im;
+    const T inv = s != T(0) ? T(1) / s : T(0);
+    return {x.re * inv, -(x.im * inv)};
+  }
+  static __device__ __forceinline__ bool finite(cx<T> x) { return isfinite(x.re) && isfinite(x.im); }
+  // the pivot's phase and log-modulus, accumulated in double
+  static __device__ __forceinline__ void acc(double2& sgn, double& logabs, cx<T> x) {
+    const double re = x.re, im = x.im, m = hypot(re, im);
+    logabs += log(m);
+    const double ur = re / m, ui = im / m;
+    sgn = make_double2(sgn.x * ur - sgn.y * ui, sgn.x * ui + sgn.y * ur);
+  }
+  static __device__ __forceinline__ cx<T> from(double2 v) { return {T(v.x), T(v.y)}; }
+};
+template <>
+struct Fd<double> {
+  using R = double;
+  static __device__ __forceinline__ double zero() { return 0.0; }
+  static __device__ __forceinline__ double one() { return 1.0; }
+  static __device__ __forceinline__ bool is0(double x) { return x == 0.0; }
+  static __device__ __forceinline__ unsigned long long key(double x) { return key64(x); }
+  static __device__ __forceinline__ double mul(double a, double b) { return a * b; }
+  static __device__ __forceinline__ double fms(double r, double l, double p) { return fma(-l, p, r); }
+  static __device__ __forceinline__ double rcp(double x) { return x != 0.0 ? 1.0 / x : 0.0; }
+  static __device__ __forceinline__ bool finite(double x) { return isfinite(x); }
+  // the float64 kernels' order: log|d| added in pivot order, the sign flipped per
+  // negative pivot
+  static __device__ __forceinline__ void acc(double2& sgn, double& logabs, double x) {
+    logabs += log(fabs(x));
+    if (x < 0.0) sgn.x = -sgn.x;
+  }
+  static __device__ __forceinline__ double from(double2 v) { return v.x; }
+};
 
-// r - l p with fused products
-template <class T>
-__device__ __forceinline__ cx<T> cfms(cx<T> r, cx<T> l, cx<T> p) {
-  return {fma(-l.re, p.re, fma(l.im, p.im, r.re)), fma(-l.re, p.im, fma(-l.im, p.re, r.im))};
-}
-
-// 1 / x = conj(x) / |x|^2, 0 -> 0
-template <class T>
-__device__ __forceinline__ cx<T> crecip(cx<T> x) {
-  const T s = x.re * x.re + x.im * x.im;
-  const T inv = s != T(0) ? T(1) / s : T(0);
-  return {x.re * inv, -(x.im * inv)};
-}
-
-template <class T>
-__device__ __forceinline__ bool czero(cx<T> x) {
-  return x.re == T(0) && x.im == T(0);
-}
-
-// pivot key: |re| + |im| (exact in double for both kinds), order-preserving bits + 1
-template <class T>
-__device__ __forceinline__ unsigned long long ckey(cx<T> x) {
-  return key64((double)(fabs(x.re) + fabs(x.im)));
-}
-
-// the pivot's phase and log-modulus, accumulated in double
-__device__ __forceinline__ void acc_pivot(double2& sgn, double& logabs, double re, double im) {
-  const double m = hypot(re, im);
-  logabs += log(m);
-  const double ur = re / m, ui = im / m;
-  sgn = make_double2(sgn.x * ur - sgn.y * ui, sgn.x * ui + sgn.y * ur);
-}
-
-template <class T>
-__device__ __forceinline__ void write_sl(cx<T>* sign_out, T* logabs_out, int64_t b, bool singular, double2 sgn,
-                                         double logabs) {
-  sign_out[b] = singular ? cx<T>{T(0), T(0)} : cx<T>{T(sgn.x), T(sgn.y)};
-  logabs_out[b] = singular ? T(-INFINITY) : T(logabs);
+template <class F>
+__device__ __forceinline__ void write_sl(F* sign_out, typename Fd<F>::R* logabs_out, int64_t b, bool singular,
+                                         double2 sgn, double logabs) {
+  using R = typename Fd<F>::R;
+  sign_out[b] = singular ? Fd<F>::zero() : Fd<F>::from(sgn);
+  logabs_out[b] = singular ? R(-INFINITY) : R(logabs);
 }
 
 // S (skew != 0: (a - a^T) / 2) into M with row stride ld; with ident, M[:, n:2n] = I.
 template <class T>
-__device__ __forceinline__ void cload(const cx<T>* __restrict__ a, int n, int skew, cx<T>* M, int ld, bool ident) {
+__device__ __forceinline__ cx<T> half_diff(cx<T> v, cx<T> u) {
+  return {(v.re - u.re) * T(0.5), (v.im - u.im) * T(0.5)};
+}
+__device__ __forceinline__ double half_diff(double v, double u) { return (v - u) * 0.5; }
+
+template <class F>
+__device__ __forceinline__ void cload(const F* __restrict__ a, int n, int skew, F* M, int ld, bool ident) {
   for (int e = threadIdx.x; e < n * n; e += CX_NT) {
     const int r = e / n, k = e - r * n;
-    cx<T> v = a[e];
-    if (skew) {
-      const cx<T> u = a[(size_t)k * n + r];
-      v = {(v.re - u.re) * T(0.5), (v.im - u.im) * T(0.5)};
-    }
+    F v = a[e];
+    if (skew) v = half_diff(v, a[(size_t)k * n + r]);
     M[(size_t)r * ld + k] = v;
-    if (ident) M[(size_t)r * ld + n + k] = cx<T>{(r == k) ? T(1) : T(0), T(0)};
+    if (ident) M[(size_t)r * ld + n + k] = (r == k) ? Fd<F>::one() : Fd<F>::zero();
   }
 }
 
-template <class T, bool INV>
-__global__ __launch_bounds__(CX_NT) void cgj_kernel(const cx<T>* __restrict__ a, int n, int skew, cx<T>* Wg,
-                                                    int use_lds, cx<T>* __restrict__ sign_out,
-                                                    T* __restrict__ logabs_out, cx<T>* __restrict__ out,
-                                                    int out_t, const cx<T>* __restrict__ gate) {
+enum { GJ_FWD = 0, GJ_INV = 1, GJ_ADJ = 2 };
+
+// Gauss-Jordan on [A | I] (MODE != GJ_FWD) or A. A zero pivot is taken as 1 for the
+// elimination (the U~ convention: its column has no nonzero candidate, so only the
+// assigned rows change), which leaves the forward unchanged and makes the right block
+// X~ = (P^T L U~)^-1 in GJ_ADJ.
+//  - GJ_INV: out = A^-1 (out_t: A^-T), zero for a zero pivot, a zero `gate` value or a
+//    non-finite result;
+//  - GJ_ADJ: out = adj(A)^T = d det / dA, from the same pivots: det(A) A^-T when no pivot
+//    is zero; with zero pivots at columns k1 <= ... <= km (km the last) the rank-1
+//    continuation s X~[km, i] X~[j, g(k1)] at (i, j), s = sgn(P) d_K (times
+//    X~[k1, g(km)] for m = 2), g(k) = the row assigned at column k, d_K the product of
+//    the nonzero pivots; m >= 3 gives 0 -- reference _det_gradT (src/fermix/_diff.py:
+//    205-246) with U~^-1 e_k1 = X~ P^T L e_k1 = X~[:, g(k1)] (a zero pivot's multipliers
+//    are zero) and (U~^-1)[k1, km] = X~[k1, g(km)]; a non-finite result gives 0.
+template <class F, int MODE>
+__global__ __launch_bounds__(CX_NT) void cgj_kernel(const F* __restrict__ a, int n, int skew, F* Wg, int use_lds,
+                                                    F* __restrict__ sign_out, typename Fd<F>::R* __restrict__ logabs_out,
+                                                    F* __restrict__ out, int out_t, const F* __restrict__ gate) {
+  using D = Fd<F>;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ unsigned long long redk[2][CX_NT / 64];
   __shared__ int redr[2][CX_NT / 64];
-  const int ld = INV ? 2 * n : n;
+  constexpr bool RIGHT = MODE != GJ_FWD;
+  const int ld = RIGHT ? 2 * n : n;
   const size_t mat = (size_t)n * ld;
   const int64_t b = blockIdx.x;
-  cx<T>* M = use_lds ? (cx<T>*)smem : Wg + (size_t)b * mat;
-  int* prow = (int*)(smem + (use_lds ? mat * sizeof(cx<T>) : 0));
+  F* M = use_lds ? (F*)smem : Wg + (size_t)b * mat;
+  int* prow = (int*)(smem + (use_lds ? mat * sizeof(F) : 0));
   unsigned char* asg = (unsigned char*)(prow + n);
 
-  cload<T>(a + (size_t)b * n * n, n, skew, M, ld, INV);
+  cload<F>(a + (size_t)b * n * n, n, skew, M, ld, RIGHT);
   for (int r = threadIdx.x; r < n; r += CX_NT) asg[r] = 0;
   __syncthreads();
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   double logabs = 0.0;
   double2 sgn = make_double2(1.0, 0.0);
-  bool singular = false;
+  int nzero = 0, k1 = 0, km = 0;  // zero pivots: count, first and last column
   for (int j = 0; j < n; ++j) {
     unsigned long long k = 0;
     int row = 0x7fffffff;
     for (int r = threadIdx.x; r < n; r += CX_NT)
-      if (!asg[r]) take_better(k, row, ckey<T>(M[(size_t)r * ld + j]), r);
+      if (!asg[r]) take_better(k, row, D::key(M[(size_t)r * ld + j]), r);
     const int p = block_argmax<CX_NT>(k, row, redk[j & 1], redr[j & 1]);
-    const cx<T> piv = M[(size_t)p * ld + j];
-    if (czero(piv))
-      singular = true;
-    else
-      acc_pivot(sgn, logabs, (double)piv.re, (double)piv.im);
-    const cx<T> rinv = crecip(piv);  // recip(0) = 0: a zero pivot updates nothing
+    const F piv = M[(size_t)p * ld + j];
+    F rinv;
+    if (D::is0(piv)) {
+      k1 = nzero ? k1 : j;
+      km = j;
+      ++nzero;
+      rinv = D::one();
+    } else {
+      D::acc(sgn, logabs, piv);
+      rinv = D::rcp(piv);
+    }
     if (threadIdx.x == 0) {
       prow[j] = p;
       asg[p] = 1;
     }
-    const cx<T>* P = M + (size_t)p * ld;
+    const F* P = M + (size_t)p * ld;
     for (int r = wave; r < n; r += CX_NT / 64) {
-      if (r == p || (!INV && asg[r])) continue;
-      cx<T>* R = M + (size_t)r * ld;
-      const cx<T> l = cmul(R[j], rinv);
-      for (int c = j + 1 + lane; c < ld; c += 64) R[c] = cfms(R[c], l, P[c]);
+      if (r == p || (!RIGHT && asg[r])) continue;
+      F* R = M + (size_t)r * ld;
+      const F l = D::mul(R[j], rinv);
+      for (int c = j + 1 + lane; c < ld; c += 64) R[c] = D::fms(R[c], l, P[c]);
     }
     __syncthreads();
   }
 
   // parity of j -> prow[j] (n - number of cycles) by thread 0; asg reused as the marks
   if (threadIdx.x == 0) {
-    for (int r = 0; r < n; ++r) asg[r] = 0;
     int cycles = 0;
+    for (int r = 0; r < n; ++r) asg[r] = 0;
     for (int s = 0; s < n; ++s) {
       if (asg[s]) continue;
       ++cycles;
       for (int t = s; !asg[t]; t = prow[t]) asg[t] = 1;
     }
-    if ((n - cycles) & 1) sgn = make_double2(-sgn.x, -sgn.y);
-    write_sl<T>(sign_out, logabs_out, b, singular, sgn, logabs);
+    const bool odd = (n - cycles) & 1;
+    write_sl<F>(sign_out, logabs_out, b, nzero > 0, odd ? make_double2(-sgn.x, -sgn.y) : sgn, logabs);
+    if (MODE == GJ_ADJ) redk[0][0] = odd ? 1ull : 0ull;
   }
-  if constexpr (INV) {
-    cx<T>* O = out + (size_t)b * n * n;
-    const bool zero = singular || (gate && czero(gate[b]));
+  if constexpr (MODE == GJ_INV) {
+    F* O = out + (size_t)b * n * n;
+    const bool zero = nzero > 0 || (gate && D::is0(gate[b]));
     bool bad = false;
     if (!zero) {
-      // A^-1[j, c] = M[prow[j], n + c] / pivot_j; out_t: O[c, j] (A^-T), else O[j, c]
+      // A^-1[j, c] = M[prow[j], n + c] / pivot_j; out_t: O[c, j], else O[j, c]
       for (int e = threadIdx.x; e < n * n; e += CX_NT) {
         const int r = e / n, q = e - r * n;
         const int j = out_t ? q : r, c = out_t ? r : q;
-        const cx<T>* Pj = M + (size_t)prow[j] * ld;
-        const cx<T> v = cmul(Pj[n + c], crecip(Pj[j]));
-        bad |= !(isfinite(v.re) && isfinite(v.im));
+        const F* Pj = M + (size_t)prow[j] * ld;
+        const F v = D::mul(Pj[n + c], D::rcp(Pj[j]));
+        bad |= !D::finite(v);
         O[e] = v;
       }
     }
     if (zero || __syncthreads_or(bad))
-      for (int e = threadIdx.x; e < n * n; e += CX_NT) O[e] = cx<T>{T(0), T(0)};
+      for (int e = threadIdx.x; e < n * n; e += CX_NT) O[e] = D::zero();
+  }
+  if constexpr (MODE == GJ_ADJ) {
+    __syncthreads();
+    const bool odd = redk[0][0] != 0;
+    // X~[j, c] = M[g(j), n + c] / pivot_j, with a zero pivot taken as 1
+    auto X = [&](int j, int c) {
+      const F* Pj = M + (size_t)prow[j] * ld;
+      const F pj = Pj[j];
+      return D::mul(Pj[n + c], D::is0(pj) ? D::one() : D::rcp(pj));
+    };
+    // s = sgn(P) prod of the nonzero pivots (det itself when none is zero)
+    const double e = exp(logabs);
+    double2 sd = make_double2(sgn.x * e, sgn.y * e);
+    if (odd) sd = make_double2(-sd.x, -sd.y);
+    F s = D::from(sd);
+    F* O = out + (size_t)b * n * n;
+    bool bad = false;
+    if (nzero == 0) {
+      for (int q = threadIdx.x; q < n * n; q += CX_NT) {
+        const int i = q / n, j = q - i * n;
+        const F v = D::mul(s, X(j, i));
+        bad |= !D::finite(v);
+        O[q] = v;
+      }
+    } else if (nzero <= 2) {
+      if (nzero == 2) s = D::mul(s, X(k1, prow[km]));
+      const int g1 = prow[k1];
+      for (int q = threadIdx.x; q < n * n; q += CX_NT) {
+        const int i = q / n, j = q - i * n;
+        const F v = D::mul(D::mul(s, X(km, i)), X(j, g1));
+        bad |= !D::finite(v);
+        O[q] = v;
+      }
+    }
+    if (nzero > 2 || __syncthreads_or(bad))
+      for (int q = threadIdx.x; q < n * n; q += CX_NT) O[q] = D::zero();
   }
 }
 
@@ -181,17 +264,19 @@ template <class T>
 __global__ __launch_bounds__(CX_NT) void cpr_kernel(const cx<T>* __restrict__ a, int n, int skew, cx<T>* Wg,
                                                     int use_lds, cx<T>* __restrict__ sign_out,
                                                     T* __restrict__ logabs_out) {
+  using F = cx<T>;
+  using D = Fd<F>;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ unsigned long long redk[2][CX_NT / 64];
   __shared__ int redr[2][CX_NT / 64];
   const size_t mat = (size_t)n * n;
   const int64_t b = blockIdx.x;
   if (n & 1) {  // odd n: pf = 0
-    if (threadIdx.x == 0) write_sl<T>(sign_out, logabs_out, b, true, make_double2(0.0, 0.0), 0.0);
+    if (threadIdx.x == 0) write_sl<F>(sign_out, logabs_out, b, true, make_double2(0.0, 0.0), 0.0);
     return;
   }
-  cx<T>* M = use_lds ? (cx<T>*)smem : Wg + (size_t)b * mat;
-  cload<T>(a + (size_t)b * mat, n, skew, M, n, false);
+  F* M = use_lds ? (F*)smem : Wg + (size_t)b * mat;
+  cload<F>(a + (size_t)b * mat, n, skew, M, n, false);
   __syncthreads();
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -202,60 +287,60 @@ __global__ __launch_bounds__(CX_NT) void cpr_kernel(const cx<T>* __restrict__ a,
     unsigned long long k = 0;
     int row = 0x7fffffff;
     // |S[r, c]| = |S[c, r]|: the candidates read along row c
-    for (int r = c + 1 + threadIdx.x; r < n; r += CX_NT) take_better(k, row, ckey<T>(M[(size_t)c * n + r]), r);
+    for (int r = c + 1 + threadIdx.x; r < n; r += CX_NT) take_better(k, row, D::key(M[(size_t)c * n + r]), r);
     const int p = block_argmax<CX_NT>(k, row, redk[(c >> 1) & 1], redr[(c >> 1) & 1]);
     const int q = c + 1;
     if (p != q) {  // swap rows p, q over columns >= c, then columns p, q over rows >= c
       sgn = make_double2(-sgn.x, -sgn.y);
       for (int x = c + threadIdx.x; x < n; x += CX_NT) {
-        const cx<T> u = M[(size_t)p * n + x], v = M[(size_t)q * n + x];
+        const F u = M[(size_t)p * n + x], v = M[(size_t)q * n + x];
         M[(size_t)p * n + x] = v;
         M[(size_t)q * n + x] = u;
       }
       __syncthreads();
       for (int x = c + threadIdx.x; x < n; x += CX_NT) {
-        const cx<T> u = M[(size_t)x * n + p], v = M[(size_t)x * n + q];
+        const F u = M[(size_t)x * n + p], v = M[(size_t)x * n + q];
         M[(size_t)x * n + p] = v;
         M[(size_t)x * n + q] = u;
       }
       __syncthreads();
     }
-    const cx<T> d = M[(size_t)c * n + q];
-    if (czero(d)) {
+    const F d = M[(size_t)c * n + q];
+    if (D::is0(d)) {
       singular = true;
       break;
     }
-    acc_pivot(sgn, logabs, (double)d.re, (double)d.im);
-    const cx<T> rd = crecip(d);
+    D::acc(sgn, logabs, d);
+    const F rd = D::rcp(d);
     // tau = -S[:, c] / d = S[c, :] / d, w = S[:, q] = -S[q, :] (rows c and q contiguous);
     // S[r, x] += tau_r w_x - w_r tau_x
-    const cx<T>* Rc = M + (size_t)c * n;
-    const cx<T>* Rq = M + (size_t)q * n;
+    const F* Rc = M + (size_t)c * n;
+    const F* Rq = M + (size_t)q * n;
     for (int r = q + 1 + wave; r < n; r += CX_NT / 64) {
-      cx<T>* R = M + (size_t)r * n;
-      const cx<T> tr = cmul(Rc[r], rd);
-      const cx<T> wr = {-Rq[r].re, -Rq[r].im};
+      F* R = M + (size_t)r * n;
+      const F tr = D::mul(Rc[r], rd);
+      const F wr = {-Rq[r].re, -Rq[r].im};
       for (int x = q + 1 + lane; x < n; x += 64) {
-        const cx<T> wx = {-Rq[x].re, -Rq[x].im};
-        const cx<T> tx = cmul(Rc[x], rd);
-        const cx<T> t1 = cmul(tr, wx), t2 = cmul(wr, tx);
-        R[x] = cx<T>{R[x].re + (t1.re - t2.re), R[x].im + (t1.im - t2.im)};
+        const F wx = {-Rq[x].re, -Rq[x].im};
+        const F tx = D::mul(Rc[x], rd);
+        const F t1 = D::mul(tr, wx), t2 = D::mul(wr, tx);
+        R[x] = F{R[x].re + (t1.re - t2.re), R[x].im + (t1.im - t2.im)};
       }
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) write_sl<T>(sign_out, logabs_out, b, singular, sgn, logabs);
+  if (threadIdx.x == 0) write_sl<F>(sign_out, logabs_out, b, singular, sgn, logabs);
 }
 
-template <class T>
+template <class F>
 bool cx_in_lds(int n, int ld) {
-  return (size_t)n * ld * sizeof(cx<T>) <= CX_LDS_MAX;
+  return (size_t)n * ld * sizeof(F) <= CX_LDS_MAX;
 }
 
-template <class T>
+template <class F>
 size_t cx_matrix_ws(int64_t batch, int n, int ld) {
-  if (batch <= 0 || n <= 0 || cx_in_lds<T>(n, ld)) return 0;
-  return (size_t)batch * n * ld * sizeof(cx<T>);
+  if (batch <= 0 || n <= 0 || cx_in_lds<F>(n, ld)) return 0;
+  return (size_t)batch * n * ld * sizeof(F);
 }
 
 size_t cx_lds_bytes(size_t mat_bytes, int n, bool lds, bool maps) {
@@ -266,112 +351,139 @@ size_t cx_lds_bytes(size_t mat_bytes, int n, bool lds, bool maps) {
 
 size_t align_up(size_t x) { return (x + 255) / 256 * 256; }
 
+// The element type of a kind's buffers (interleaved pairs for complex) and its real type.
+template <class F>
+struct Kind;
 template <class T>
-int launch_cgj(const T* a, int n, int skew, int64_t batch, T* sign, T* logabs, T* out, int out_t, const T* gate,
-               void* ws, size_t ws_bytes, hipStream_t s) {
-  const bool inv = out != nullptr;
-  const int ld = inv ? 2 * n : n;
-  const bool lds = cx_in_lds<T>(n, ld);
-  if (!lds && (!ws || ws_bytes < cx_matrix_ws<T>(batch, n, ld))) return FX_ERR_WORKSPACE;
-  const size_t shm = cx_lds_bytes((size_t)n * ld * sizeof(cx<T>), n, lds, true);
+struct Kind<cx<T>> {
+  using R = T;
+};
+template <>
+struct Kind<double> {
+  using R = double;
+};
+
+template <class F>
+int launch_cgj(const void* a, int n, int skew, int64_t batch, void* sign, void* logabs, void* out, int mode,
+               int out_t, const void* gate, void* ws, size_t ws_bytes, hipStream_t s) {
+  using R = typename Kind<F>::R;
+  const int ld = mode != GJ_FWD ? 2 * n : n;
+  const bool lds = cx_in_lds<F>(n, ld);
+  if (!lds && (!ws || ws_bytes < cx_matrix_ws<F>(batch, n, ld))) return FX_ERR_WORKSPACE;
+  const size_t shm = cx_lds_bytes((size_t)n * ld * sizeof(F), n, lds, true);
   const dim3 grid((unsigned)batch);
-  const cx<T>* A = reinterpret_cast<const cx<T>*>(a);
-  cx<T>* W = (cx<T>*)ws;
-  cx<T>* sg = reinterpret_cast<cx<T>*>(sign);
-  if (inv)
-    cgj_kernel<T, true><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, logabs, reinterpret_cast<cx<T>*>(out),
-                                                 out_t, reinterpret_cast<const cx<T>*>(gate));
+  const F* A = (const F*)a;
+  F* W = (F*)ws;
+  F* sg = (F*)sign;
+  R* lg = (R*)logabs;
+  if (mode == GJ_INV)
+    cgj_kernel<F, GJ_INV><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, (F*)out, out_t, (const F*)gate);
+  else if (mode == GJ_ADJ)
+    cgj_kernel<F, GJ_ADJ><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, (F*)out, 1, nullptr);
   else
-    cgj_kernel<T, false><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, logabs, nullptr, 0, nullptr);
+    cgj_kernel<F, GJ_FWD><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, nullptr, 0, nullptr);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
 template <class T>
-int launch_cpr(const T* a, int n, int skew, int64_t batch, T* sign, T* logabs, void* ws, size_t ws_bytes,
+int launch_cpr(const void* a, int n, int skew, int64_t batch, void* sign, void* logabs, void* ws, size_t ws_bytes,
                hipStream_t s) {
-  const bool lds = cx_in_lds<T>(n, n);
-  if (!lds && (!ws || ws_bytes < cx_matrix_ws<T>(batch, n, n))) return FX_ERR_WORKSPACE;
-  const size_t shm = cx_lds_bytes((size_t)n * n * sizeof(cx<T>), n, lds, false);
-  cpr_kernel<T><<<dim3((unsigned)batch), CX_NT, shm, s>>>(reinterpret_cast<const cx<T>*>(a), n, skew, (cx<T>*)ws,
-                                                          lds, reinterpret_cast<cx<T>*>(sign), logabs);
+  using F = cx<T>;
+  const bool lds = cx_in_lds<F>(n, n);
+  if (!lds && (!ws || ws_bytes < cx_matrix_ws<F>(batch, n, n))) return FX_ERR_WORKSPACE;
+  const size_t shm = cx_lds_bytes((size_t)n * n * sizeof(F), n, lds, false);
+  cpr_kernel<T><<<dim3((unsigned)batch), CX_NT, shm, s>>>((const F*)a, n, skew, (F*)ws, lds, (F*)sign, (T*)logabs);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
 // The alignment contract of the ABI (matrix-shaped and workspace pointers 16-byte
 // aligned; sign / logabs aligned to their element size) and the size limits.
-template <class T>
+template <class F>
 int check_cx_args(const void* a, int64_t batch, int n, const void* sign, const void* logabs, const void* out,
                   const void* ws) {
+  using R = typename Kind<F>::R;
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (n > CX_MAXN) return FX_ERR_UNSUPPORTED;
   if (batch > 0 && (!sign || !logabs || (n > 0 && !a))) return FX_ERR_INVALID_ARGUMENT;
   auto mis = [](const void* p, uintptr_t m) { return ((uintptr_t)p & m) != 0; };
-  if (mis(a, 15) || mis(out, 15) || mis(ws, 15) || mis(sign, 2 * sizeof(T) - 1) || mis(logabs, sizeof(T) - 1))
+  if (mis(a, 15) || mis(out, 15) || mis(ws, 15) || mis(sign, sizeof(F) - 1) || mis(logabs, sizeof(R) - 1))
     return FX_ERR_INVALID_ARGUMENT;
   if (batch > 0x7fffffff) return FX_ERR_UNSUPPORTED;
   return FX_OK;
 }
 
 // sign = 1, logabs = 0 for every member (n = 0)
-template <class T>
-__global__ void cx_empty_kernel(T* sign, T* logabs, int64_t batch) {
+template <class F>
+__global__ void cx_empty_kernel(F* sign, typename Kind<F>::R* logabs, int64_t batch) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < batch) {
-    sign[2 * i] = T(1);
-    sign[2 * i + 1] = T(0);
-    logabs[i] = T(0);
+    sign[i] = Fd<F>::one();
+    logabs[i] = 0;
   }
 }
 
-template <class T>
-int cx_empty(T* sign, T* logabs, int64_t batch, hipStream_t s) {
-  cx_empty_kernel<T><<<dim3((unsigned)((batch + 255) / 256)), 256, 0, s>>>(sign, logabs, batch);
+template <class F>
+int cx_empty(void* sign, void* logabs, int64_t batch, hipStream_t s) {
+  cx_empty_kernel<F><<<dim3((unsigned)((batch + 255) / 256)), 256, 0, s>>>((F*)sign, (typename Kind<F>::R*)logabs,
+                                                                          batch);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
-template <class T>
+template <class F>
 size_t slogdet_ws(int64_t batch, int n) {
-  return n > CX_MAXN ? 0 : cx_matrix_ws<T>(batch, n, n);
+  return n > CX_MAXN ? 0 : cx_matrix_ws<F>(batch, n, n);
 }
-template <class T>
+template <class F>
 size_t slogdet_parts_ws(int64_t batch, int n) {
-  return n > CX_MAXN ? 0 : cx_matrix_ws<T>(batch, n, 2 * n);
+  return n > CX_MAXN ? 0 : cx_matrix_ws<F>(batch, n, 2 * n);
 }
 
-template <class T>
-int slogdet(const T* a, int64_t batch, int n, T* sign, T* logabs, void* ws, size_t wsb, hipStream_t s) {
-  const int st = check_cx_args<T>(a, batch, n, sign, logabs, nullptr, ws);
+template <class F>
+int slogdet(const void* a, int64_t batch, int n, void* sign, void* logabs, void* ws, size_t wsb, hipStream_t s) {
+  const int st = check_cx_args<F>(a, batch, n, sign, logabs, nullptr, ws);
   if (st != FX_OK || batch == 0) return st;
-  if (n == 0) return cx_empty<T>(sign, logabs, batch, s);
-  return launch_cgj<T>(a, n, 0, batch, sign, logabs, nullptr, 0, nullptr, ws, wsb, s);
+  if (n == 0) return cx_empty<F>(sign, logabs, batch, s);
+  return launch_cgj<F>(a, n, 0, batch, sign, logabs, nullptr, GJ_FWD, 0, nullptr, ws, wsb, s);
 }
 
-template <class T>
-int slogdet_parts(const T* a, int64_t batch, int n, T* sign, T* logabs, T* inv_t, void* ws, size_t wsb,
+template <class F>
+int slogdet_parts(const void* a, int64_t batch, int n, void* sign, void* logabs, void* inv_t, void* ws, size_t wsb,
                   hipStream_t s) {
-  const int st = check_cx_args<T>(a, batch, n, sign, logabs, inv_t, ws);
+  const int st = check_cx_args<F>(a, batch, n, sign, logabs, inv_t, ws);
   if (st != FX_OK || batch == 0) return st;
-  if (n == 0) return cx_empty<T>(sign, logabs, batch, s);
-  return launch_cgj<T>(a, n, 0, batch, sign, logabs, inv_t, 1, nullptr, ws, wsb, s);
+  if (n == 0) return cx_empty<F>(sign, logabs, batch, s);
+  if (!inv_t) return launch_cgj<F>(a, n, 0, batch, sign, logabs, nullptr, GJ_FWD, 0, nullptr, ws, wsb, s);
+  return launch_cgj<F>(a, n, 0, batch, sign, logabs, inv_t, GJ_INV, 1, nullptr, ws, wsb, s);
+}
+
+// det's gradient adj(A)^T with sign / logabs of the same run
+template <class F>
+int det_parts(const void* a, int64_t batch, int n, void* sign, void* logabs, void* adj_t, void* ws, size_t wsb,
+              hipStream_t s) {
+  const int st = check_cx_args<F>(a, batch, n, sign, logabs, adj_t, ws);
+  if (st != FX_OK || batch == 0) return st;
+  if (n > 0 && !adj_t) return FX_ERR_INVALID_ARGUMENT;
+  if (n == 0) return cx_empty<F>(sign, logabs, batch, s);
+  return launch_cgj<F>(a, n, 0, batch, sign, logabs, adj_t, GJ_ADJ, 1, nullptr, ws, wsb, s);
 }
 
 template <class T>
 size_t slogpf_ws(int64_t batch, int n) {
-  return n > CX_MAXN ? 0 : cx_matrix_ws<T>(batch, n, n);
+  return n > CX_MAXN ? 0 : cx_matrix_ws<cx<T>>(batch, n, n);
 }
 
 template <class T>
 size_t slogpf_parts_ws(int64_t batch, int n) {
   if (n > CX_MAXN || batch <= 0) return 0;
-  return align_up(slogpf_ws<T>(batch, n)) + align_up(cx_matrix_ws<T>(batch, n, 2 * n)) +
+  return align_up(slogpf_ws<T>(batch, n)) + align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n)) +
          align_up((size_t)batch * 3 * sizeof(T));
 }
 
 template <class T>
 int slogpf(const T* a, int64_t batch, int n, int skew, T* sign, T* logabs, void* ws, size_t wsb, hipStream_t s) {
-  const int st = check_cx_args<T>(a, batch, n, sign, logabs, nullptr, ws);
+  const int st = check_cx_args<cx<T>>(a, batch, n, sign, logabs, nullptr, ws);
   if (st != FX_OK || batch == 0) return st;
-  if (n == 0) return cx_empty<T>(sign, logabs, batch, s);
+  if (n == 0) return cx_empty<cx<T>>(sign, logabs, batch, s);
   return launch_cpr<T>(a, n, skew != 0, batch, sign, logabs, ws, wsb, s);
 }
 
@@ -380,20 +492,20 @@ int slogpf(const T* a, int64_t batch, int n, int skew, T* sign, T* logabs, void*
 template <class T>
 int slogpf_parts(const T* a, int64_t batch, int n, int skew, int adjugate, T* sign, T* logabs, T* g, void* ws,
                  size_t wsb, hipStream_t s) {
-  int st = check_cx_args<T>(a, batch, n, sign, logabs, g, ws);
+  int st = check_cx_args<cx<T>>(a, batch, n, sign, logabs, g, ws);
   if (st != FX_OK || batch == 0) return st;
   if (adjugate) return FX_ERR_UNSUPPORTED;
   if (!g) return slogpf<T>(a, batch, n, skew, sign, logabs, ws, wsb, s);
-  if (n == 0) return cx_empty<T>(sign, logabs, batch, s);
+  if (n == 0) return cx_empty<cx<T>>(sign, logabs, batch, s);
   if (wsb < slogpf_parts_ws<T>(batch, n) || (!ws && slogpf_parts_ws<T>(batch, n))) return FX_ERR_WORKSPACE;
   const size_t pr = align_up(slogpf_ws<T>(batch, n));
-  const size_t gj = align_up(cx_matrix_ws<T>(batch, n, 2 * n));
+  const size_t gj = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n));
   char* base = (char*)ws;
   st = launch_cpr<T>(a, n, skew != 0, batch, sign, logabs, base, pr, s);
   if (st != FX_OK) return st;
   T* gsign = (T*)(base + pr + gj);
   T* glog = gsign + 2 * batch;
-  return launch_cgj<T>(a, n, skew != 0, batch, gsign, glog, g, 0, sign, base + pr, gj, s);
+  return launch_cgj<cx<T>>(a, n, skew != 0, batch, gsign, glog, g, GJ_INV, 0, sign, base + pr, gj, s);
 }
 
 }  // namespace
@@ -403,28 +515,28 @@ using namespace fx;
 
 extern "C" {
 
-size_t fx_slogdet_c64_workspace(int64_t batch, int32_t n) { return slogdet_ws<float>(batch, n); }
-size_t fx_slogdet_c128_workspace(int64_t batch, int32_t n) { return slogdet_ws<double>(batch, n); }
+size_t fx_slogdet_c64_workspace(int64_t batch, int32_t n) { return slogdet_ws<cx<float>>(batch, n); }
+size_t fx_slogdet_c128_workspace(int64_t batch, int32_t n) { return slogdet_ws<cx<double>>(batch, n); }
 
 int fx_slogdet_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream) {
-  return slogdet<float>(a, batch, n, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
+  return slogdet<cx<float>>(a, batch, n, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_slogdet_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
                     size_t workspace_bytes, fx_stream_t stream) {
-  return slogdet<double>(a, batch, n, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
+  return slogdet<cx<double>>(a, batch, n, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
-size_t fx_slogdet_parts_c64_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<float>(batch, n); }
-size_t fx_slogdet_parts_c128_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<double>(batch, n); }
+size_t fx_slogdet_parts_c64_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<float>>(batch, n); }
+size_t fx_slogdet_parts_c128_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<double>>(batch, n); }
 
 int fx_slogdet_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* inv_t,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  return slogdet_parts<float>(a, batch, n, sign, logabs, inv_t, workspace, workspace_bytes, (hipStream_t)stream);
+  return slogdet_parts<cx<float>>(a, batch, n, sign, logabs, inv_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_slogdet_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
                           void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  return slogdet_parts<double>(a, batch, n, sign, logabs, inv_t, workspace, workspace_bytes, (hipStream_t)stream);
+  return slogdet_parts<cx<double>>(a, batch, n, sign, logabs, inv_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 size_t fx_slogpf_c64_workspace(int64_t batch, int32_t n) { return slogpf_ws<float>(batch, n); }
@@ -454,6 +566,23 @@ int fx_slogpf_parts_c128(const double* a, int64_t batch, int32_t n, int32_t skew
                          fx_stream_t stream) {
   return slogpf_parts<double>(a, batch, n, skew_symmetrize, adjugate, sign, logabs, g, workspace,
                               workspace_bytes, (hipStream_t)stream);
+}
+
+size_t fx_det_parts_c64_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<float>>(batch, n); }
+size_t fx_det_parts_c128_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<double>>(batch, n); }
+size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<double>(batch, n); }
+
+int fx_det_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
+                     void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  return det_parts<cx<float>>(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, (hipStream_t)stream);
+}
+int fx_det_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
+                      void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  return det_parts<cx<double>>(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, (hipStream_t)stream);
+}
+int fx_det_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
+                     void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  return det_parts<double>(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -362,6 +362,27 @@ int fx_slogpf_parts_c128(const double* a, int64_t batch, int32_t n, int32_t skew
                          double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
                          fx_stream_t stream);
 
+/* adj_t (batch, n, n) = adj(A)^T = d det(A) / dA (holomorphic for complex A, no
+ * conjugation) plus sign / logabs of the same Gauss-Jordan run, for float64, complex64
+ * and complex128 -- fx_det_parts_f32's contract: det(A) A^-T from the run's own pivots
+ * when no pivot is exactly zero; with zero pivots at columns k1 <= ... <= km (U~ = U with
+ * them taken as 1, d_K = the product of the other pivots) the rank-1 continuation
+ * sgn(P) d_K c (U~^-1 e_k1)(e_km^T U~^-1 L^-1 P) with c = (U~^-1)[k1, km] for m = 2 and 1
+ * for m = 1; 0 for m >= 3 and for a non-finite result. Replaces `_det_gradT` with `_lu_det`
+ * and `_perm_sign` (src/fermix/_diff.py:160-246) for the 64-bit and complex kinds. One
+ * workgroup per matrix; the workspace is that of the _parts entry points (none while
+ * [A | I] fits in 60 KiB of LDS). For float64 the sign / logabs equal fx_slogdet_f64's
+ * bits (the same pivots and per-element updates). */
+size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n);
+int fx_det_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
+                     void* workspace, size_t workspace_bytes, fx_stream_t stream);
+size_t fx_det_parts_c64_workspace(int64_t batch, int32_t n);
+int fx_det_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
+                     void* workspace, size_t workspace_bytes, fx_stream_t stream);
+size_t fx_det_parts_c128_workspace(int64_t batch, int32_t n);
+int fx_det_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
+                      void* workspace, size_t workspace_bytes, fx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

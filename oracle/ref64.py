@@ -91,10 +91,11 @@ def slogpf64(Sb):
 
 
 def adjT_brute(A):
-    """d det / dA = adj(A)^T by cofactors, float64."""
-    A = np.asarray(A, np.float64)
+    """d det / dA = adj(A)^T by cofactors, float64 (complex128 for complex A: the
+    holomorphic derivative, no conjugation)."""
+    A = _wide(A)
     n = A.shape[0]
-    G = np.zeros((n, n))
+    G = np.zeros((n, n), A.dtype)
     for i in range(n):
         for j in range(n):
             M = np.delete(np.delete(A, i, 0), j, 1)
@@ -120,14 +121,15 @@ def inv64(A):
 
 
 def adjT_svd(A):
-    """d det / dA = adj(A)^T from the SVD (float64): with A = U diag(sig) Vt,
-    adj(A) = adj(Vt) adj(diag(sig)) adj(U) = det(Vt) det(U) Vt^T diag(p) U^T,
-    p_i = prod_{j != i} sig_j, so adj(A)^T = det(U) det(Vt) U diag(p) Vt. The products
-    are formed in logs (sig_j = 0 contributes an exact zero)."""
-    A = np.asarray(A, np.float64)
+    """d det / dA = adj(A)^T from the SVD (float64, or complex128 for complex A): with
+    A = U diag(sig) Vt (U, Vt unitary, adj(U) = det(U) U^H), adj(A) = adj(Vt) adj(diag(sig))
+    adj(U) = det(Vt) det(U) Vt^H diag(p) U^H, p_i = prod_{j != i} sig_j, so adj(A)^T =
+    det(U) det(Vt) conj(U) diag(p) conj(Vt) (U diag(p) Vt for real A). The products are
+    formed in logs (sig_j = 0 contributes an exact zero)."""
+    A = _wide(A)
     n = A.shape[0]
     if n == 0:
-        return np.zeros((0, 0))
+        return np.zeros((0, 0), A.dtype)
     U, sig, Vt = np.linalg.svd(A)
     with np.errstate(divide="ignore"):
         lg = np.log(sig)
@@ -135,7 +137,7 @@ def adjT_svd(A):
     for i in range(n):
         others = np.delete(lg, i)
         p[i] = 0.0 if np.any(np.isneginf(others)) else math.exp(float(np.sum(others)))
-    return np.linalg.det(U) * np.linalg.det(Vt) * (U * p[None, :]) @ Vt
+    return np.linalg.det(U) * np.linalg.det(Vt) * (U.conj() * p[None, :]) @ Vt.conj()
 
 
 def pf_grad64(S):

@@ -162,13 +162,18 @@ def test_f64_autograd(dev, n):
     assert np.allclose(_np(dl), ref, rtol=1e-9, atol=1e-9)
     sv, lv = torch.func.vmap(fermix_amd.slogdet)(_t(A, dev)[:, None])
     assert torch.equal(lv[:, 0], l0)
-    # det / pf values in float64; their gradients (exact adjugates) are float32-only
+    # det / pf values in float64; det's gradient is the exact adjugate of the same run
+    # (tests/test_gpu_adjugate64.py covers the singular cases); pf's is float32-only
     d = fermix_amd.det(_t(A, dev))
     assert np.allclose(_np(d), np.linalg.det(A), rtol=1e-10, atol=0)
     p = fermix_amd.pf(_t(A, dev))
     sr, lr = ref64.slogpf64(S)
     assert np.allclose(_np(p), sr * np.exp(lr), rtol=1e-10, atol=0)
-    with pytest.raises(NotImplementedError):
-        fermix_amd.det(_t(A, dev).requires_grad_())
+    Ad = _t(A, dev).requires_grad_()
+    dd = fermix_amd.det(Ad)
+    assert torch.equal(dd.detach(), d)
+    (gd,) = torch.autograd.grad(dd.sum(), Ad)
+    assert_grad64(_np(gd), np.linalg.det(A)[:, None, None] * np.swapaxes(ref64.inv64(A), 1, 2), A,
+                  "det autograd")
     with pytest.raises(NotImplementedError):
         fermix_amd.pf(_t(A, dev).requires_grad_())

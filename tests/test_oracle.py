@@ -404,3 +404,27 @@ def test_complex_planted_mistakes_are_caught():
     ref = np.linalg.inv(A).transpose(0, 2, 1)
     assert relerr(invT.conj(), ref) > 0.1 and relerr(invT, ref) < 1e-10
     assert np.all(np.abs(d) > 0)
+
+
+@pytest.mark.parametrize("case", ["regular", "rank n-1", "rank n-2"])
+def test_complex_adjT_svd_vs_cofactors(case):
+    """The complex SVD adjugate (the float64 / complex truth of the det gradient) against
+    cofactors, the closed form det(A) A^-T for regular A, and 0 at rank n - 2; a
+    conjugated continuation fails the check."""
+    n = 6
+    A = crandn((n, n), np.complex128)
+    if case != "regular":
+        A[:, 2] = 0.3 * A[:, 0] - 1j * A[:, 4]
+    if case == "rank n-2":
+        A[:, 3] = A[:, 1]
+    S = ref64.adjT_svd(A)
+    C = ref64.adjT_brute(A)
+    assert np.max(np.abs(S - C)) < 1e-10 * max(1.0, np.max(np.abs(C)))
+    if case == "regular":
+        ref = np.linalg.det(A) * np.linalg.inv(A).T
+        assert np.max(np.abs(C - ref)) < 1e-10 * np.max(np.abs(ref))
+        assert np.max(np.abs(C.conj() - ref)) > 0.1 * np.max(np.abs(ref))
+    elif case == "rank n-1":
+        assert np.max(np.abs(C)) > 1e-3
+    else:
+        assert np.max(np.abs(C)) < 1e-10
