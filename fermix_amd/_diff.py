@@ -27,6 +27,7 @@ derivative (the Pfaffian adjugate) raises NotImplementedError.
 import torch
 
 from . import _kernels
+from ._kernels import DEFAULT_X3
 
 # ----------------------------------------------------------------- helpers
 
@@ -233,7 +234,7 @@ class _SlogdetSplit(torch.autograd.Function):
         return tuple(_unfold(x, vb) for x in out), (0,) * 4
 
 
-def slogdet(A, x3=0):
+def slogdet(A, x3=DEFAULT_X3):
     """x3: the split-bf16x3 product mode of the blocked kernels (0: fp32 MFMA)."""
     if _wants_grad(A):
         # n <= 32: one Gauss-Jordan pass forms A^-T with the factors; forward mode and
@@ -346,7 +347,7 @@ class _SlogpfSplit(torch.autograd.Function):
         return tuple(_unfold(x, vb) for x in out), (0,) * 5
 
 
-def slogpf(A, skew, x3=0):
+def slogpf(A, skew, x3=DEFAULT_X3):
     """x3: the split-bf16x3 product mode of the gradient's GEMMs (the forward's trailing
     update is memory-bound and runs in fp32 in both modes)."""
     if _wants_grad(A):
@@ -401,7 +402,7 @@ class _DetParts(torch.autograd.Function):
         return (_unfold(d, vb), _unfold(adj, vb)), (0, 0)
 
 
-def det(A, x3=0):
+def det(A, x3=DEFAULT_X3):
     if _wants_grad(A):
         d, _ = _DetParts.apply(A, x3)
         return d
@@ -446,7 +447,7 @@ class _PfParts(torch.autograd.Function):
         return (_unfold(p, vb), _unfold(G, vb)), (0, 0)
 
 
-def pf(A, skew, x3=0):
+def pf(A, skew, x3=DEFAULT_X3):
     if _wants_grad(A):
         p, _ = _PfParts.apply(A, skew, x3)
         return p

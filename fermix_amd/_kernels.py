@@ -5,6 +5,11 @@ tensors (float64 for the f64 entry points) on a ROCm device; no numerics happen 
 import torch
 
 from ._lib import FX_PREC_MASK, check, lib
+from ._tune import DEFAULT_PREC, prec_flag
+
+# the C ABI's prec word of the library's default product mode (the public API's default
+# for float32); the float64 and complex entry points take no prec
+DEFAULT_X3 = prec_flag(DEFAULT_PREC)
 
 
 def _stream(t):
@@ -104,7 +109,7 @@ def pf_padded_size(n):
     return int(lib().fx_pf_padded_size(n))
 
 
-def slogdet(A, x3=0):
+def slogdet(A, x3=DEFAULT_X3):
     """(sign, logabs) of each (n, n) matrix of A (B, n, n); x3: the C ABI's prec word
     (FX_PREC_BF16X3 products, FX_LU_BLOCK_* options; float32 only)."""
     if A.is_complex():
@@ -126,7 +131,7 @@ def slogdet(A, x3=0):
     return sign, logabs
 
 
-def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False, x3=0):
+def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False, x3=DEFAULT_X3):
     """(sign, logabs, invT, lu, perm) with the optional outputs None when not asked for;
     lu / perm are padded to N = lu_padded_size(n). float64 and complex: invT only (zero
     for exactly singular members), no packed factors."""
@@ -167,7 +172,7 @@ def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False, x3=0):
     return sign, logabs, invT, lu, perm
 
 
-def slogdet_factors(A, x3=0):
+def slogdet_factors(A, x3=DEFAULT_X3):
     """(sign, logabs, lu (B, N, N), perm (B, N)): the packed LU of fx_slogdet_parts_f32
     alone, N = lu_padded_size(n)."""
     _check_input(A)
@@ -188,7 +193,7 @@ def slogdet_factors(A, x3=0):
     return sign, logabs, lu, perm
 
 
-def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True, x3=0):
+def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True, x3=DEFAULT_X3):
     """scale[b] * A^-T (B, n, n) from slogdet_factors' outputs; lu is overwritten."""
     B = sign.shape[0]
     dev = sign.device
@@ -205,7 +210,7 @@ def slogdet_inverse(lu, perm, sign, n, scale=None, zero_singular=True, x3=0):
     return out
 
 
-def det_parts(A, x3=0):
+def det_parts(A, x3=DEFAULT_X3):
     """(sign, logabs, adjT) with adjT = adj(A)^T = d det / dA from one factorisation
     (holomorphic, no conjugation, for complex A)."""
     if A.dtype != torch.float32:
@@ -290,7 +295,7 @@ def slogpf_factors(A, skew_symmetrize):
     return sign, logabs, gbuf, d, perm
 
 
-def slogpf_inverse(gbuf, d, perm, n, scale=None, adjugate=False, x3=0):
+def slogpf_inverse(gbuf, d, perm, n, scale=None, adjugate=False, x3=DEFAULT_X3):
     """scale[b] * S^-1 (or scale[b] * pf(S) S^-1) (B, n, n) from slogpf_factors' outputs,
     which are read only."""
     B = d.shape[0]
@@ -308,7 +313,7 @@ def slogpf_inverse(gbuf, d, perm, n, scale=None, adjugate=False, x3=0):
     return out
 
 
-def slogpf_parts(A, skew_symmetrize, adjugate=False, x3=0):
+def slogpf_parts(A, skew_symmetrize, adjugate=False, x3=DEFAULT_X3):
     """(sign, logabs, G) of the (skew-symmetrised) batch from one Parlett-Reid run, G = S^-1
     or, with adjugate, pf(S) S^-1 (float32 only)."""
     if adjugate:

@@ -14,7 +14,7 @@ FX_PREC_MASK = 0x0F
 FX_LU_BLOCK_64 = 0x100
 FX_LU_BLOCK_128 = 0x200
 
-# fields of struct fx_tune, in order (int32 each; 7 reserved int32 follow)
+# fields of struct fx_tune, in order (int32 each; 3 reserved int32 follow)
 TUNE_FIELDS = (
     "fused_max_n",
     "lu_pair_above_n",
@@ -23,6 +23,10 @@ TUNE_FIELDS = (
     "pf_block64_max_m",
     "gemm128_min_mn",
     "gemm128_min_k",
+    "gemm128_tout",
+    "gemm128_x3_min_mn",
+    "gemm128_x3_min_k",
+    "gemm128_x3_tout",
     "f64_reg_max_n",
     "f64_strip16_max_n",
 )
@@ -31,7 +35,7 @@ TUNE_FIELDS = (
 class FxTune(ctypes.Structure):
     """struct fx_tune of include/fermix.h."""
 
-    _fields_ = [(f, ctypes.c_int32) for f in TUNE_FIELDS] + [("reserved", ctypes.c_int32 * 7)]
+    _fields_ = [(f, ctypes.c_int32) for f in TUNE_FIELDS] + [("reserved", ctypes.c_int32 * 3)]
 
 
 _p = ctypes.c_void_p

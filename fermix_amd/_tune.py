@@ -28,9 +28,13 @@ import torch
 #  * "tf32x3": the reference's name for its three-pass fp32-accuracy mode on tensor cores;
 #    gfx950 has no TF32 type, so it selects the gfx950 counterpart, "bf16x3".
 # The mode applies to the blocked kernels' trailing LU updates and to the inverse /
-# adjugate GEMMs (include/fermix.h, FX_PREC_*); the default is "ieee".
+# adjugate GEMMs (include/fermix.h, FX_PREC_*). The default is the three-pass mode for
+# the 32-bit kinds and "ieee" for the 64-bit ones, as the reference's Field.default_prec
+# (src/fermix/_field.py:262-263): on MI355X "bf16x3" is also the faster mode of the
+# blocked gradients (128 x 128 GEMM tiles with the operands split once in LDS), with the
+# same accuracy bar as "ieee" (tests/test_gpu_prec.py).
 PREC = ("ieee", "tf32x3", "bf16x3")
-DEFAULT_PREC = "ieee"
+DEFAULT_PREC = "bf16x3"
 
 
 class FermixTuneWarning(UserWarning):
@@ -44,7 +48,7 @@ def check_prec(prec, dtype=None):
     complex128, src/fermix/_field.py:265-275); complex64 accepts them but runs no MFMA
     product (its kernels are unblocked), so they do not change its results."""
     if prec is None:
-        return DEFAULT_PREC
+        return "ieee" if dtype in (torch.float64, torch.complex128) else DEFAULT_PREC
     if prec not in PREC:
         raise ValueError(f"prec must be one of {PREC}, got {prec!r}")
     if prec != "ieee" and dtype is not None and dtype not in (torch.float32, torch.complex64):
@@ -122,9 +126,15 @@ class Tune:
     # once the trailing order is <= pf_block64_max_m
     pf_block64_min_n: int = 512
     pf_block64_max_m: int = 1024
-    # GEMMs: 128 x 128 tiles for M, N >= gemm128_min_mn and K >= gemm128_min_k
+    # GEMMs (fp32 MFMA): 128 x 128 tiles for M, N >= gemm128_min_mn and K >=
+    # gemm128_min_k, also for the product with A^-T's transposed, row-permuted output
+    # if gemm128_tout; the gemm128_x3_* fields are the same for prec="bf16x3"
     gemm128_min_mn: int = 1024
     gemm128_min_k: int = 512
+    gemm128_tout: int = 0
+    gemm128_x3_min_mn: int = 128
+    gemm128_x3_min_k: int = 128
+    gemm128_x3_tout: int = 1
     # float64: registers for n <= f64_reg_max_n, 16-column strips for n <= f64_strip16_max_n
     f64_reg_max_n: int = 128
     f64_strip16_max_n: int = 64

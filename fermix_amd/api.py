@@ -86,11 +86,12 @@ def _lu_opts(a, prec, unroll_steps, block):
 
 def slogdet(a, *, prec=None, unroll_steps=None, block=None):
     """Sign and log|det| of a batch of matrices ``a`` (..., n, n) (reference
-    ``slogdet``, api.py:148-174). prec: "ieee" (default; fp32 MFMA products), "bf16x3"
-    (three-way bf16 split, six bf16 MFMA products, fp32 accumulation) or "tf32x3" (the
-    reference's fp32-accuracy three-pass mode; on gfx950, which has no TF32 type, it
-    selects "bf16x3"). The mode applies to the blocked kernels (n > 128): the trailing
-    updates and the inverse's GEMMs. block: the outer LU block of the blocked kernels
+    ``slogdet``, api.py:148-174). prec: "bf16x3" (the float32 / complex64 default: three-way
+    bf16 split, six bf16 MFMA products, fp32 accumulation, fp32 accuracy), "tf32x3" (the
+    reference's name for its default fp32-accuracy three-pass mode; on gfx950, which has
+    no TF32 type, it selects "bf16x3") or "ieee" (fp32 MFMA products; the only mode, and
+    the default, of float64 / complex128). The mode applies to the blocked kernels
+    (n > 128): the trailing updates and the inverse's GEMMs. block: the outer LU block of the blocked kernels
     (float32): None (the tuning table: block pairs above N = 256), 64 (single 64-column
     blocks, K = 64 trailing updates) or 128 (blocks in pairs, K = 128 updates); 32 runs
     64 with a FermixTuneWarning. unroll_steps: accepted, without effect on gfx950 (the

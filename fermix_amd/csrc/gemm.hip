@@ -691,6 +691,60 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
     }
   }
 
+  if (d.tout) {
+    // transposed, row-permuted output as in gemm_kernel, in two passes of 64 tile columns
+    // (a 64 x 128 transposed half fits the operand LDS): the two waves holding the pass's
+    // columns stage them as Ts[c][r], then each of the 64 columns is stored as one
+    // contiguous run of 128 rows (two per lane) of row g0[j] of tout
+    constexpr int LDT = BM + 1;
+    static_assert(64 * LDT * 4 <= SMEM, "half tile fits the operand stages");
+    float* Ts = reinterpret_cast<float*>(smem);
+    const int* gb = d.g0 + bat * d.N;
+    const float sc = d.scale ? d.alpha * d.scale[bat] : d.alpha;
+    float* ob = d.tout + bat * (int64_t)d.nout * d.nout;
+    bool nf = false;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      __syncthreads();  // the operands (pass 0) / the previous pass's stores are done
+      if ((wave & 1) == pass) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int r = wm + 32 * a + 8 * (v >> 2) + 4 * lh + (v & 3), c = 32 * b + l32;
+              Ts[c * LDT + r] = acc[a][b][v];
+              nf = nf || (i0 + r < d.M && j0 + 64 * pass + c < d.N && !isfinite(acc[a][b][v]));
+            }
+      }
+      __syncthreads();
+      const int jc = j0 + 64 * pass;
+      const int rl = jc + lane < d.N ? gb[jc + lane] : d.nout;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int cc = wave + 4 * u;
+        const int r = __builtin_amdgcn_readlane(rl, cc);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int i = i0 + lane + 64 * h;
+          if (i < d.nout && r < d.nout) ob[(int64_t)r * d.nout + i] = sc * Ts[cc * LDT + lane + 64 * h];
+        }
+      }
+    }
+    // one flag per 64 x 64 tile (the layout of gemm_kernel's flags): this tile's value
+    // goes to the (up to four) 64-tiles it covers
+    const int any = __syncthreads_or(nf ? 1 : 0);
+    if (tid == 0) {
+      const int ntm = (d.M + 63) / 64, ntn = (d.N + 63) / 64;
+      int* fb = d.flags + bat * (int64_t)ntm * ntn;
+      for (int a = 0; a < 2; ++a)
+        for (int b = 0; b < 2; ++b)
+          if (2 * ti + a < ntm && 2 * tj + b < ntn) fb[(2 * ti + a) * ntn + 2 * tj + b] = any;
+    }
+    return;
+  }
+
   // epilogue as in gemm_kernel, with 32-bit offsets within the matrix: element v of an
   // accumulator is row r0 + dv, dv = 8 (v / 4) + v % 4, so its offsets step by the
   // uniform dv * ldc (and dv for the mirrored store)
@@ -746,8 +800,10 @@ static int launch_gemm_t(const GemmDesc& d, int64_t batch, int nb2, hipStream_t 
   // below, and for short K, the coarser triangle trimming and the longer prologue /
   // epilogue per K stage make the 64 x 64 tiles faster
   const fx_tune& tu = tune();
-  const bool big = vec && !d.transB && d.M >= tu.gemm128_min_mn && d.N >= tu.gemm128_min_mn &&
-                   d.K >= tu.gemm128_min_k && !d.tout;
+  const int mn128 = X3 ? tu.gemm128_x3_min_mn : tu.gemm128_min_mn;
+  const int k128 = X3 ? tu.gemm128_x3_min_k : tu.gemm128_min_k;
+  const int tout128 = X3 ? tu.gemm128_x3_tout : tu.gemm128_tout;
+  const bool big = vec && !d.transB && d.M >= mn128 && d.N >= mn128 && d.K >= k128 && (!d.tout || tout128);
   if (d.tout && (d.lower_only || nb2 != 1 || d.active)) return FX_ERR_INVALID_ARGUMENT;
   if (d.bscale && (d.maskB != MASK_NONE || d.transB || d.K % 2 || nb2 != 1 || !vec)) return FX_ERR_INVALID_ARGUMENT;
   const int tm2 = (d.M + 127) / 128, tn2 = (d.N + 127) / 128;

@@ -73,22 +73,84 @@ __device__ __forceinline__ unsigned l4(int p, int q, int N) {
 }
 
 // Copy a (B, n, n) into M (B, N, N) in the strip layout: S = (a - a^T)/2 (or a) with
-// [[0,1],[-1,0]] padding, the strictly lower entries only (the rest of each strip is never
-// read). Thread e writes strip e / (4 N), column (e / 4) % N, row 4 (e / (4 N)) + e % 4.
-__global__ void pf_copy_pad_kernel(const float* __restrict__ A, int n, int skew, float* __restrict__ M, int N) {
+// [[0,1],[-1,0]] padding, the strictly lower entries (the rest of each strip is never
+// read; the diagonal tiles' upper entries are written as zeros). One workgroup per 64 x 64
+// tile pair (I, J), I >= J: the blocks A[I][J] and, with skew, A[J][I] are read once each
+// along their rows into LDS (each wave a 256-byte row segment), the entries formed there
+// (fma(-A[c][r], 1/2, A[r][c] / 2): halving is exact, one rounding), and the strips of the
+// tile written as 16-byte vectors -- four rows of one column are one strip piece, so a
+// strip of the tile is 1 KiB of consecutive memory.
+constexpr int PCT = 64;  // tile of the copy
+__global__ __launch_bounds__(256) void pf_copy_pad_kernel(const float* __restrict__ A, int n, int skew,
+                                                         float* __restrict__ M, int N) {
+  __shared__ float Tl[PCT][PCT + 1], Tu[PCT][PCT + 1];
   const int64_t b = blockIdx.y;
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= N * N) return;
-  const int r = 4 * (e / (4 * N)) + (e & 3), c = (e >> 2) % N;
-  if (r <= c) return;
+  const int t = blockIdx.x;
+  int I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
+  while ((I + 1) * (I + 2) / 2 <= t) ++I;
+  while (I * (I + 1) / 2 > t) --I;
+  const int J = t - I * (I + 1) / 2;
+  const int r0 = PCT * I, c0 = PCT * J;
   const float* Ab = A + b * (int64_t)n * n;
-  float v;
-  if (r < n && c < n) {
-    v = skew ? (Ab[(int64_t)r * n + c] - Ab[(int64_t)c * n + r]) * 0.5f : Ab[(int64_t)r * n + c];
-  } else {
-    v = ((r ^ c) == 1 && r >= n) ? -1.0f : 0.0f;  // r odd, c = r - 1: M[r][r-1] = -1
+  const int tid = threadIdx.x;
+  // Tl[i][j] = A[r0 + i][c0 + j], Tu[j][i] = A[c0 + j][r0 + i] (0 outside the n x n input):
+  // thread t reads columns 4 (t % 16) .. + 3 of rows t / 16 + 16 k, one 16-byte load per
+  // row piece when the rows are 16-byte aligned (n % 4 == 0) and the piece is inside the
+  // input, so each wave reads four 256-byte row segments per load, all eight in flight
+  const int c4 = 4 * (tid & 15), rr = tid >> 4;
+  const bool vec = (n & 3) == 0;
+  float4 lo[4], up[4];
+  auto ld4 = [&](int gr, int gc) {
+    if (gr >= n) return make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float* p = Ab + (int64_t)gr * n + gc;
+    if (vec && gc + 3 < n) return *reinterpret_cast<const float4*>(p);
+    return make_float4(gc < n ? p[0] : 0.0f, gc + 1 < n ? p[1] : 0.0f, gc + 2 < n ? p[2] : 0.0f,
+                       gc + 3 < n ? p[3] : 0.0f);
+  };
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    lo[k] = ld4(r0 + rr + 16 * k, c0 + c4);
+    if (skew) up[k] = ld4(c0 + rr + 16 * k, r0 + c4);
   }
-  M[b * (int64_t)N * N + e] = v;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float* d = &Tl[rr + 16 * k][c4];
+    d[0] = lo[k].x;
+    d[1] = lo[k].y;
+    d[2] = lo[k].z;
+    d[3] = lo[k].w;
+    if (skew) {
+      float* e = &Tu[rr + 16 * k][c4];
+      e[0] = up[k].x;
+      e[1] = up[k].y;
+      e[2] = up[k].z;
+      e[3] = up[k].w;
+    }
+  }
+  __syncthreads();
+  float* Mb = M + b * (int64_t)N * N;
+  // (strip s of the tile, column q): rows r0 + 4 s .. + 3 of column c0 + q
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + 256 * u, s = e >> 6, q = e & 63;
+    const int gr = r0 + 4 * s, gc = c0 + q;
+    if (gr >= N || gc >= N) continue;
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = gr + k, i = 4 * s + k;
+      float x;
+      if (r <= gc) {
+        x = 0.0f;  // upper entries of a diagonal tile: never read
+      } else if (r < n && gc < n) {
+        x = skew ? fmaf(-Tu[q][i], 0.5f, Tl[i][q] * 0.5f) : Tl[i][q];
+      } else {
+        x = ((r ^ gc) == 1 && r >= n) ? -1.0f : 0.0f;  // r odd, c = r - 1: M[r][r-1] = -1
+      }
+      v[k] = x;
+    }
+    *reinterpret_cast<float4*>(Mb + l4(gr, gc, N)) = make_float4(v[0], v[1], v[2], v[3]);
+  }
 }
 
 template <int NT, int R, int PB>
@@ -581,7 +643,8 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
   // first block's rows), so no copy is made. Otherwise the padded copy comes first.
   const bool direct = n == N && !skew && ((uintptr_t)A & 15) == 0;
   if (!direct) {
-    hipLaunchKernelGGL(pf_copy_pad_kernel, dim3((unsigned)((NN + 255) / 256), (unsigned)batch), dim3(256), 0, s,
+    const int ntc = (N + PCT - 1) / PCT;
+    hipLaunchKernelGGL(pf_copy_pad_kernel, dim3((unsigned)(ntc * (ntc + 1) / 2), (unsigned)batch), dim3(256), 0, s,
                        A, n, skew, M0, N);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }

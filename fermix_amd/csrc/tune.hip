@@ -15,9 +15,15 @@
 //    the trailing updates' traffic (B = 256, n = 1024 5.33 -> 3.97 ms) but at N = 256 the
 //    panel's halved occupancy loses (2.44 -> 3.20 ms); m <= 1024 is the register limit
 //    of the 64-column panel;
-//  - gemm128_min_mn 1024 / gemm128_min_k 512: 128 x 128 GEMM tiles won on the n = 2048
-//    products (triangular-inverse top level -18 %, R = Y^T D Y -15 %) and lost at
-//    M = 512 and for short K (coarser triangle trimming, longer prologue per stage);
+//  - gemm128_min_mn 1024 / gemm128_min_k 512 / gemm128_tout 0 (fp32 MFMA): 128 x 128
+//    GEMM tiles won on the n = 2048 products (triangular-inverse top level -18 %,
+//    R = Y^T D Y -15 %) and lost at M = 512 and for short K (coarser triangle trimming,
+//    longer prologue per stage); for the A^-T product they lose at n = 512 / 1024
+//    (slogdet fwd + grad B = 1024, n = 512: 6.23 -> 6.56 ms) and tie at 2048;
+//  - gemm128_x3_*: 128 / 128 / 1 (bf16x3): there the 128 x 128 kernel, which splits each
+//    operand once into LDS planes, wins on every product from 128 on: slogdet fwd + grad
+//    n = 512 6.32 -> 5.78 ms, n = 1024 9.74 -> 8.64, n = 2048 19.68 -> 17.64, n = 256
+//    4.56 -> 4.41; slogpf fwd + grad 1-4 %;
 //  - f64_reg_max_n 128 / f64_strip16_max_n 64: float64 matrices in registers for
 //    n <= 128 (slogdet n = 128 8.66 -> 3.16 ms against the LDS kernel), in 16-column strips
 //    for n <= 64 (n = 64 1.37 ms; at n = 128 they lose, 3.97 against 3.16 ms).
@@ -38,9 +44,13 @@ constexpr fx_tune GFX950 = {
     /* pf_block64_max_m */ 1024,
     /* gemm128_min_mn */ 1024,
     /* gemm128_min_k */ 512,
+    /* gemm128_tout */ 0,
+    /* gemm128_x3_min_mn */ 128,
+    /* gemm128_x3_min_k */ 128,
+    /* gemm128_x3_tout */ 1,
     /* f64_reg_max_n */ 128,
     /* f64_strip16_max_n */ 64,
-    /* reserved */ {0, 0, 0, 0, 0, 0, 0},
+    /* reserved */ {0, 0, 0},
 };
 
 fx_tune g_override;
@@ -53,7 +63,9 @@ bool valid(const fx_tune& t) {
   return in(t.fused_max_n, TINY_MAXN, 128) && in(t.lu_pair_above_n, 0, 1 << 30) &&
          in(t.lu_direct_max_n, 0, 1024) && in(t.pf_block64_min_n, 128, 1 << 30) &&
          in(t.pf_block64_max_m, 0, 1024) && in(t.gemm128_min_mn, 128, 1 << 30) &&
-         in(t.gemm128_min_k, 64, 1 << 30) && in(t.f64_reg_max_n, 0, 128) && in(t.f64_strip16_max_n, 0, 64);
+         in(t.gemm128_min_k, 64, 1 << 30) && in(t.gemm128_tout, 0, 1) &&
+         in(t.gemm128_x3_min_mn, 128, 1 << 30) && in(t.gemm128_x3_min_k, 64, 1 << 30) && in(t.gemm128_x3_tout, 0, 1) && in(t.f64_reg_max_n, 0, 128) &&
+         in(t.f64_strip16_max_n, 0, 64);
 }
 
 }  // namespace

@@ -113,16 +113,24 @@ typedef struct fx_tune {
    * 32-column blocks otherwise (16 above N = 2048). 128 .. 4096 / 0 .. 1024 */
   int32_t pf_block64_min_n;
   int32_t pf_block64_max_m;
-  /* GEMMs of the inverses and adjugates: 128 x 128 tiles when M, N >= gemm128_min_mn
-   * and K >= gemm128_min_k, else 64 x 64 (bit-identical results). >= 128 / >= 64 */
+  /* GEMMs of the inverses and adjugates in FX_PREC_IEEE: 128 x 128 tiles when M, N >=
+   * gemm128_min_mn and K >= gemm128_min_k, else 64 x 64 (bit-identical results); the
+   * product with A^-T's transposed, row-permuted output too if gemm128_tout (0 / 1).
+   * >= 128 / >= 64 */
   int32_t gemm128_min_mn;
   int32_t gemm128_min_k;
+  int32_t gemm128_tout;
+  /* the same three for FX_PREC_BF16X3 (the 128 x 128 kernel splits each operand once
+   * into bf16 planes in LDS, the 64 x 64 one at every use) */
+  int32_t gemm128_x3_min_mn;
+  int32_t gemm128_x3_min_k;
+  int32_t gemm128_x3_tout;
   /* float64: the matrix in registers for n <= f64_reg_max_n (0 .. 128), with rows split
    * in 16-column strips for n <= f64_strip16_max_n (0 .. 64) and 32-column ones above;
    * larger n runs one workgroup per matrix in LDS or in the workspace */
   int32_t f64_reg_max_n;
   int32_t f64_strip16_max_n;
-  int32_t reserved[7]; /* zero */
+  int32_t reserved[3]; /* zero */
 } fx_tune;
 
 /* The table of an architecture ("gfx950"; FX_ERR_UNSUPPORTED for any other name: the

@@ -90,19 +90,29 @@ def test_lu_override_pairs_and_direct(dev, n):
 
 @pytest.mark.parametrize("n", [256, 512])
 def test_gemm_tile_override_bit_identical(dev, n):
-    """128 x 128 GEMM tiles (gemm128_min_mn / _k lowered so that the n <= 512 inverse GEMMs
-    take them) give the same bits as the 64 x 64 tiles of the table, for A^-T and S^-1."""
+    """fp32 MFMA: 128 x 128 GEMM tiles (gemm128_min_mn / _k lowered and gemm128_tout set, so
+    that every n <= 512 inverse GEMM, the A^-T product with its transposed output included,
+    takes them) give the same bits as the 64 x 64 tiles of the table, for A^-T and S^-1."""
     A = _mats(n, 4, 7300 + n)
     At = _t(A, dev)
     S = _t(A - A.transpose(0, 2, 1), dev)
-    ref_inv = fermix_amd._kernels.slogdet_parts(At)[2]
-    ref_sinv = fermix_amd._kernels.slogpf_parts(S, False)[2]
+    ref_inv = fermix_amd._kernels.slogdet_parts(At, x3=0)[2]
+    ref_sinv = fermix_amd._kernels.slogpf_parts(S, False, x3=0)[2]
     print(f"gemm128 override n={n}", flush=True)
-    with _tune.override(gemm128_min_mn=128, gemm128_min_k=64):
-        inv = fermix_amd._kernels.slogdet_parts(At)[2]
-        sinv = fermix_amd._kernels.slogpf_parts(S, False)[2]
+    with _tune.override(gemm128_min_mn=128, gemm128_min_k=64, gemm128_tout=1):
+        inv = fermix_amd._kernels.slogdet_parts(At, x3=0)[2]
+        sinv = fermix_amd._kernels.slogpf_parts(S, False, x3=0)[2]
     assert torch.equal(inv, ref_inv)
     assert torch.equal(sinv, ref_sinv)
+    # bf16x3: the table's 128 x 128 tiles (operands split once in LDS) against 64 x 64
+    # tiles (split at every use): the same split values and products, the same bits
+    ref3 = fermix_amd._kernels.slogdet_parts(At, x3=1)[2]
+    ref3s = fermix_amd._kernels.slogpf_parts(S, False, x3=1)[2]
+    with _tune.override(gemm128_x3_min_mn=1 << 20, gemm128_x3_tout=0):
+        inv3 = fermix_amd._kernels.slogdet_parts(At, x3=1)[2]
+        sinv3 = fermix_amd._kernels.slogpf_parts(S, False, x3=1)[2]
+    assert torch.equal(inv3, ref3)
+    assert torch.equal(sinv3, ref3s)
 
 
 @pytest.mark.parametrize("n,override", [(1024, dict(pf_block64_max_m=0)), (256, dict(pf_block64_min_n=256)),

@@ -108,7 +108,11 @@ def test_api_errors():
 
 
 def test_tune_table():
-    assert _tune.check_prec(None) == "ieee"
+    # default: the three-pass mode for the 32-bit kinds, "ieee" for the 64-bit ones
+    # (reference Field.default_prec, src/fermix/_field.py:262-263)
+    assert _tune.check_prec(None) == "bf16x3" and _tune.check_prec(None, torch.float32) == "bf16x3"
+    assert _tune.check_prec(None, torch.complex64) == "bf16x3"
+    assert _tune.check_prec(None, torch.float64) == "ieee" and _tune.check_prec(None, torch.complex128) == "ieee"
     assert _tune.check_prec("ieee") == "ieee"
     assert _tune.check_prec("tf32x3") == "bf16x3" and _tune.check_prec("bf16x3") == "bf16x3"
     assert _tune.prec_flag("bf16x3") == 1 and _tune.prec_flag("ieee") == 0
@@ -277,7 +281,7 @@ def test_tuning_override():
         assert _tune.active() == base
     t = _lib.FxTune()
     assert L.fx_tune_active(t) == 0
-    t.reserved[3] = 1
+    t.reserved[2] = 1
     assert L.fx_tune_override(t) == 1 and _tune.active() == base
 
 
