@@ -21,7 +21,10 @@ float64 and complex inputs take the parts route (A^-T / S^-1 formed with the pri
 the float64 / complex kernels); for complex kinds the sign is differentiable too, with
 the reference's conventions (see _log_tangents below). Their det derivative is the exact
 adjugate of the same Gauss-Jordan run (fx_det_parts_f64 / _c64 / _c128); their pf
-derivative (the Pfaffian adjugate) raises NotImplementedError.
+derivative is the Pfaffian adjugate of fx_slogpf_parts_f64 / _c64 / _c128 (adjugate
+mode), with the primal from the plain forward's own kernel. For complex kinds the
+backward applies torch's conjugate convention (cotangent times the conjugate of the
+holomorphic derivative), the jvp the holomorphic derivative itself.
 """
 
 import torch
@@ -431,7 +434,7 @@ class _PfParts(torch.autograd.Function):
         (G,) = ctx.saved_tensors
         if g_pf is None:
             return None, None, None
-        return g_pf[:, None, None] * G, None, None
+        return _apply_cotangent(g_pf, G), None, None
 
     @staticmethod
     def jvp(ctx, dA, _skew, _x3):
@@ -453,3 +456,52 @@ def pf(A, skew, x3=DEFAULT_X3):
         return p
     s, l = _SlogpfFwd.apply(A, skew)
     return s * torch.exp(l)
+
+
+# ------------------------------------------------------------------- odd n
+
+
+class _OddConst(torch.autograd.Function):
+    """Odd n: the reference's constant branch (api.py:122-123, 141-142) -- pf = 0, slogpf
+    (0, -inf) -- as a function of the input with a zero derivative, so that reverse mode,
+    forward mode and vmap see what the reference's constant differentiates to."""
+
+    generate_vmap_rule = True
+
+    @staticmethod
+    def forward(A, what):
+        B = A.shape[0]
+        zero = torch.zeros(B, dtype=A.dtype, device=A.device)
+        if what == "pf":
+            return zero
+        real = A.real.dtype if A.is_complex() else A.dtype
+        return zero, torch.full((B,), -float("inf"), dtype=real, device=A.device)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        A, what = inputs
+        ctx.what = what
+        ctx.set_materialize_grads(False)
+        ctx.meta = (A.shape, A.dtype, A.device)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        shape, dtype, device = ctx.meta
+        return torch.zeros(shape, dtype=dtype, device=device), None
+
+    @staticmethod
+    def jvp(ctx, dA, _what):
+        B = dA.shape[0]
+        zero = torch.zeros(B, dtype=dA.dtype, device=dA.device)
+        if ctx.what == "pf":
+            return zero
+        real = dA.real.dtype if dA.is_complex() else dA.dtype
+        return zero, torch.zeros(B, dtype=real, device=dA.device)
+
+
+def odd_pf(A):
+    return _OddConst.apply(A, "pf")
+
+
+def odd_slogpf(A):
+    return _OddConst.apply(A, "slogpf")

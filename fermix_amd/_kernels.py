@@ -96,8 +96,7 @@ def _no_f64(A, what):
     if A.dtype != torch.float32:
         raise NotImplementedError(
             f"fermix_amd: {what} is implemented for float32 only (float64 / complex64 / "
-            "complex128 have slogdet / slogpf / det / pf values and the slogdet / slogpf "
-            "derivatives)"
+            "complex128 have the values and every derivative, formed by their own kernels)"
         )
 
 
@@ -315,11 +314,9 @@ def slogpf_inverse(gbuf, d, perm, n, scale=None, adjugate=False, x3=DEFAULT_X3):
 
 def slogpf_parts(A, skew_symmetrize, adjugate=False, x3=DEFAULT_X3):
     """(sign, logabs, G) of the (skew-symmetrised) batch from one Parlett-Reid run, G = S^-1
-    or, with adjugate, pf(S) S^-1 (float32 only)."""
-    if adjugate:
-        _no_f64(A, "the pf gradient (Pfaffian adjugate)")
+    or, with adjugate, pf(S) S^-1 (the Pfaffian adjugate)."""
     if A.is_complex():
-        return _cplx_call(A, "slogpf_parts", skew=skew_symmetrize, want_out=True)
+        return _cplx_call(A, "slogpf_parts", skew=skew_symmetrize, want_out=True, adjugate=adjugate)
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape
@@ -331,7 +328,7 @@ def slogpf_parts(A, skew_symmetrize, adjugate=False, x3=DEFAULT_X3):
     if f64:
         ws, wsb = _workspace(L.fx_slogpf_parts_f64_workspace(B, n), dev)
         st = L.fx_slogpf_parts_f64(
-            _ptr(A), B, n, int(bool(skew_symmetrize)), 0, _ptr(sign), _ptr(logabs), _ptr(g),
+            _ptr(A), B, n, int(bool(skew_symmetrize)), int(bool(adjugate)), _ptr(sign), _ptr(logabs), _ptr(g),
             _ptr(ws), wsb, _stream(A),
         )
         check(st, "fx_slogpf_parts_f64")

@@ -118,8 +118,8 @@ def slogpf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
     _on_device(a)
     A, batch, n = _flat(a)
     if n % 2 == 1:
-        z = torch.zeros(batch, dtype=a.dtype, device=a.device)
-        return z, torch.full(batch, -float("inf"), dtype=a.dtype, device=a.device)
+        sign, logabs = _diff.odd_slogpf(A)
+        return sign.reshape(batch), logabs.reshape(batch)
     sign, logabs = _diff.slogpf(A, bool(skew_symmetrize), x3)
     return sign.reshape(batch), logabs.reshape(batch)
 
@@ -143,7 +143,7 @@ def pf(a, *, prec=None, skew_symmetrize=True, upd_warps=None):
     _on_device(a)
     A, batch, n = _flat(a)
     if n % 2 == 1:
-        return torch.zeros(batch, dtype=a.dtype, device=a.device)
+        return _diff.odd_pf(A).reshape(batch)
     return _diff.pf(A, bool(skew_symmetrize), x3).reshape(batch)
 
 

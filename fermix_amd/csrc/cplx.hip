@@ -1,4 +1,5 @@
-// complex64 / complex128 slogdet and slogpf (values, A^-T and S^-1) -- the reference's
+// complex64 / complex128 slogdet and slogpf (values, A^-T, S^-1, the det and pf adjugates;
+// the latter two also for float64) -- the reference's
 // complex kinds (src/fermix/_field.py:32-120: a complex value as a (re, im) pair, the
 // pivot magnitude |re| + |im| (`abs1`, LAPACK's cabs1), the guarded reciprocal
 // conj(x) / |x|^2 (`recip`), the pivot phase x / |x| (`unit`) and log of the modulus
@@ -21,8 +22,15 @@
 //    calls give bit-identical sign / logabs;
 //  - cpr_kernel<T>: Parlett-Reid with the pivot row / column swapped into position c + 1,
 //    d = S[c, c+1], tau = -S[:, c] / d, w = S[:, c+1] and the rank-2 update
-//    tau w^T - w tau^T on the rows and columns after c + 1.
+//    tau w^T - w tau^T on the rows and columns after c + 1;
+//  - the Pfaffian adjugate pf(S) S^-1 (pf's gradient) of the float64 and complex kinds:
+//    cpfa_factor_kernel<F> (Parlett-Reid keeping the permutation, the pivots and the
+//    factor column of the smallest pivot) and cgj_kernel<F, GJ_PFA> (the inverse of the
+//    factorisation with that pivot and the zero pivots replaced by 1, formed from S while
+//    it is loaded, and the reference's rank-2 correction on the way out).
 // The phase and the log are accumulated in double for both kinds.
+#include <algorithm>
+
 #include "common.h"
 #include "fermix_internal.h"
 
@@ -74,6 +82,11 @@ struct Fd<cx<T>> {
     sgn = make_double2(sgn.x * ur - sgn.y * ui, sgn.x * ui + sgn.y * ur);
   }
   static __device__ __forceinline__ cx<T> from(double2 v) { return {T(v.x), T(v.y)}; }
+  static __device__ __forceinline__ double2 to2(cx<T> x) { return make_double2(x.re, x.im); }
+  // the modulus |x| (the Pfaffian adjugate's choice of the smallest pivot), in double
+  static __device__ __forceinline__ double mag(cx<T> x) { return hypot((double)x.re, (double)x.im); }
+  static __device__ __forceinline__ cx<T> add(cx<T> a, cx<T> b) { return {a.re + b.re, a.im + b.im}; }
+  static __device__ __forceinline__ cx<T> sub(cx<T> a, cx<T> b) { return {a.re - b.re, a.im - b.im}; }
 };
 template <>
 struct Fd<double> {
@@ -93,7 +106,15 @@ struct Fd<double> {
     if (x < 0.0) sgn.x = -sgn.x;
   }
   static __device__ __forceinline__ double from(double2 v) { return v.x; }
+  static __device__ __forceinline__ double2 to2(double x) { return make_double2(x, 0.0); }
+  static __device__ __forceinline__ double mag(double x) { return fabs(x); }
+  static __device__ __forceinline__ double add(double a, double b) { return a + b; }
+  static __device__ __forceinline__ double sub(double a, double b) { return a - b; }
 };
+
+__device__ __forceinline__ double2 c2mul(double2 a, double2 b) {
+  return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
 
 template <class F>
 __device__ __forceinline__ void write_sl(F* sign_out, typename Fd<F>::R* logabs_out, int64_t b, bool singular,
@@ -121,7 +142,51 @@ __device__ __forceinline__ void cload(const F* __restrict__ a, int n, int skew, 
   }
 }
 
-enum { GJ_FWD = 0, GJ_INV = 1, GJ_ADJ = 2 };
+enum { GJ_FWD = 0, GJ_INV = 1, GJ_ADJ = 2, GJ_PFA = 3 };
+
+// ---- the Pfaffian adjugate pf(S) S^-1 (the pf gradient) of the 64-bit and complex kinds.
+// Parlett-Reid with the rows and columns permuted (P), P S P^T = L D L^T with D = diag_s(
+// d_s J); K = the pair of the smallest |d| (the first exact zero if any); d~ = d with d_K
+// and the exact zeros replaced by 1; L~ = L with the a-columns scaled by 1/d~ (columns
+// a_s = 2s: w_s / d~_s, p_s = 2s + 1: tau_s). The reference's formula (src/fermix/
+// _fallback.py:101-192, _pfinv.py:196-269) is
+//   G = -P^T [a1 R + a2 (w v^T - v w^T)] P,  R = Y^T DY, Y = L~^-1,
+//   w = R e_aK, v = Y^T e_aK, (a1, a2) = sgn(P) D_K (d_K, 1 - d_K), D_K = prod_{s != K} d_s.
+// Here R comes from one inverse: R = -(T~)^-1 with T~ = L~ D~ L~^T, and T~ differs from
+// P S P^T only in pair K (its entry d_K -> 1, its a-row / column beyond p_K scaled by 1/d_K:
+// + (1 - d_K)(e_a e_p^T + e_a tau^T - transposes)) and at the zero pivots' pair entries
+// (0 -> 1), so T~ is formed from S while it is loaded; v = Y^T e_aK is row a_K of L~^-1,
+// = (L~^T X~)[p_K, :] = X~^T l with l = L~ e_pK (l = e_pK + tau_K) and X~ = (T~)^-1. With
+// X~: G' = a1 X~ - a2 (w v^T - v w^T), w = -X~ e_aK, and G = P^T G' P. A second exact zero
+// pivot z is lifted as in the reference: G = (G(d_z = 1) + G(d_z = -1)) / 2 (two
+// evaluations, the second only for the members that have one); three or more give G = 0.
+template <class F>
+struct PfaHead {
+  int K;     // pair of the smallest |d|
+  int z;     // second zero pivot (lifted), -1 none, -2 three or more zero pivots (G = 0)
+  int pad[2];
+  F dK;
+  F a1[2], a2[2];  // per evaluation (z = +1, z = -1), the 1/2 of the mean included
+};
+
+// byte offsets inside one member's slice of the adjugate's metadata
+struct PfaLayout {
+  size_t perm, ell, d, v, w, rp, stride;
+};
+
+template <class F>
+PfaLayout pfa_layout(int n) {
+  auto up = [](size_t x) { return (x + 15) / 16 * 16; };
+  PfaLayout L;
+  L.perm = up(sizeof(PfaHead<F>));
+  L.ell = L.perm + up((size_t)n * sizeof(int));
+  L.d = L.ell + up((size_t)n * sizeof(F));
+  L.v = L.d + up((size_t)(n / 2) * sizeof(F));
+  L.w = L.v + up((size_t)n * sizeof(F));
+  L.rp = L.w + up((size_t)n * sizeof(F));
+  L.stride = (L.rp + (size_t)n * sizeof(F) + 255) / 256 * 256;
+  return L;
+}
 
 // Gauss-Jordan on [A | I] (MODE != GJ_FWD) or A. A zero pivot is taken as 1 for the
 // elimination (the U~ convention: its column has no nonzero candidate, so only the
@@ -139,7 +204,8 @@ enum { GJ_FWD = 0, GJ_INV = 1, GJ_ADJ = 2 };
 template <class F, int MODE>
 __global__ __launch_bounds__(CX_NT) void cgj_kernel(const F* __restrict__ a, int n, int skew, F* Wg, int use_lds,
                                                     F* __restrict__ sign_out, typename Fd<F>::R* __restrict__ logabs_out,
-                                                    F* __restrict__ out, int out_t, const F* __restrict__ gate) {
+                                                    F* __restrict__ out, int out_t, const F* __restrict__ gate,
+                                                    unsigned char* __restrict__ meta, PfaLayout PL, int eval) {
   using D = Fd<F>;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ unsigned long long redk[2][CX_NT / 64];
@@ -152,7 +218,44 @@ __global__ __launch_bounds__(CX_NT) void cgj_kernel(const F* __restrict__ a, int
   int* prow = (int*)(smem + (use_lds ? mat * sizeof(F) : 0));
   unsigned char* asg = (unsigned char*)(prow + n);
 
-  cload<F>(a + (size_t)b * n * n, n, skew, M, ld, RIGHT);
+  if constexpr (MODE == GJ_PFA) {
+    unsigned char* mb = meta + (size_t)b * PL.stride;
+    const PfaHead<F>& h = *(const PfaHead<F>*)mb;
+    if (h.z == -2) {  // three or more zero pivots: G = 0
+      if (eval == 0)
+        for (int e = threadIdx.x; e < n * n; e += CX_NT) out[(size_t)b * n * n + e] = D::zero();
+      return;
+    }
+    if (eval == 1 && h.z < 0) return;
+    // T~ (rows and columns permuted, pair K and the zero pivots' entries replaced)
+    const int* perm = (const int*)(mb + PL.perm);
+    const F* ell = (const F*)(mb + PL.ell);
+    const F* dm = (const F*)(mb + PL.d);
+    const int aK = 2 * h.K, pK = aK + 1;
+    const F eK = D::sub(D::one(), h.dK);
+    const F lift = eval ? D::sub(D::zero(), D::one()) : D::one();
+    const F* A = a + (size_t)b * n * n;
+    for (int e = threadIdx.x; e < n * n; e += CX_NT) {
+      const int r = e / n, k = e - r * n;
+      const int pr = perm[r], pk = perm[k];
+      F v = A[(size_t)pr * n + pk];
+      if (skew) v = half_diff(v, A[(size_t)pk * n + pr]);
+      if (r == aK) {
+        if (k == pK) v = D::add(v, eK);
+        else if (k > pK) v = D::add(v, D::mul(eK, ell[k]));
+      } else if (k == aK) {
+        if (r == pK) v = D::sub(v, eK);
+        else if (r > pK) v = D::sub(v, D::mul(eK, ell[r]));
+      } else if ((r ^ k) == 1 && D::is0(dm[r >> 1])) {
+        const F val = (r >> 1) == h.z ? lift : D::one();
+        v = (r & 1) ? D::sub(v, val) : D::add(v, val);
+      }
+      M[(size_t)r * ld + k] = v;
+      M[(size_t)r * ld + n + k] = (r == k) ? D::one() : D::zero();
+    }
+  } else {
+    cload<F>(a + (size_t)b * n * n, n, skew, M, ld, RIGHT);
+  }
   for (int r = threadIdx.x; r < n; r += CX_NT) asg[r] = 0;
   __syncthreads();
 
@@ -189,6 +292,45 @@ __global__ __launch_bounds__(CX_NT) void cgj_kernel(const F* __restrict__ a, int
       for (int c = j + 1 + lane; c < ld; c += 64) R[c] = D::fms(R[c], l, P[c]);
     }
     __syncthreads();
+  }
+
+  if constexpr (MODE == GJ_PFA) {
+    // X~[i, c] = M[prow[i], n + c] rp[i] (a zero pivot of T~, which exact arithmetic
+    // excludes, taken as 1); v = X~^T l over the rows i >= p_K; w = -X~[:, a_K]
+    unsigned char* mb = meta + (size_t)b * PL.stride;
+    const PfaHead<F>& h = *(const PfaHead<F>*)mb;
+    const int* perm = (const int*)(mb + PL.perm);
+    const F* ell = (const F*)(mb + PL.ell);
+    F* vv = (F*)(mb + PL.v);
+    F* ww = (F*)(mb + PL.w);
+    F* rp = (F*)(mb + PL.rp);
+    const int aK = 2 * h.K, pK = aK + 1;
+    for (int i = threadIdx.x; i < n; i += CX_NT) {
+      const F* Pi = M + (size_t)prow[i] * ld;
+      const F pv = Pi[i];
+      const F r = D::is0(pv) ? D::one() : D::rcp(pv);
+      rp[i] = r;
+      ww[i] = D::sub(D::zero(), D::mul(Pi[n + aK], r));
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < n; j += CX_NT) {
+      F acc = D::zero();
+      for (int i = pK; i < n; ++i) acc = D::add(acc, D::mul(D::mul(ell[i], rp[i]), M[(size_t)prow[i] * ld + n + j]));
+      vv[j] = acc;
+    }
+    __syncthreads();
+    const F a1 = eval ? h.a1[1] : h.a1[0], a2 = eval ? h.a2[1] : h.a2[0];
+    F* O = out + (size_t)b * n * n;
+    for (int e = threadIdx.x; e < n * n; e += CX_NT) {
+      const int i = e / n, j = e - i * n;
+      const F x = D::mul(M[(size_t)prow[i] * ld + n + j], rp[i]);
+      const F c = D::sub(D::mul(ww[i], vv[j]), D::mul(vv[i], ww[j]));
+      F g = D::sub(D::mul(a1, x), D::mul(a2, c));
+      F* o = O + (size_t)perm[i] * n + perm[j];
+      if (eval) g = D::add(*o, g);
+      *o = g;
+    }
+    return;
   }
 
   // parity of j -> prow[j] (n - number of cycles) by thread 0; asg reused as the marks
@@ -332,6 +474,133 @@ __global__ __launch_bounds__(CX_NT) void cpr_kernel(const cx<T>* __restrict__ a,
   if (threadIdx.x == 0) write_sl<F>(sign_out, logabs_out, b, singular, sgn, logabs);
 }
 
+// Parlett-Reid of the Pfaffian adjugate (any field): the pair steps of cpr_kernel with
+// whole rows swapped (so the factor's columns below each pair, which the L~ formula reads,
+// move with the permutation), the permutation kept, and no stop at a zero pivot (tau = 0
+// there: the step changes nothing, as in the reference's masked step). Thread 0 keeps the
+// pivot statistics; the end writes the member's PfaHead, the permutation, d and
+// l = L~ e_pK (e_pK + tau_K).
+template <class F>
+__global__ __launch_bounds__(CX_NT) void cpfa_factor_kernel(const F* __restrict__ a, int n, int skew, F* Wg,
+                                                            int use_lds, unsigned char* __restrict__ meta,
+                                                            PfaLayout PL) {
+  using D = Fd<F>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ unsigned long long redk[2][CX_NT / 64];
+  __shared__ int redr[2][CX_NT / 64];
+  __shared__ int sK;
+  const size_t mat = (size_t)n * n;
+  const int64_t b = blockIdx.x;
+  F* M = use_lds ? (F*)smem : Wg + (size_t)b * mat;
+  int* perm = (int*)(smem + (use_lds ? mat * sizeof(F) : 0));
+  unsigned char* mb = meta + (size_t)b * PL.stride;
+  F* dm = (F*)(mb + PL.d);
+  cload<F>(a + (size_t)b * mat, n, skew, M, n, false);
+  for (int r = threadIdx.x; r < n; r += CX_NT) perm[r] = r;
+  __syncthreads();
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int par = 0, nzero = 0, z2 = -1, K = 0;  // thread 0's statistics
+  double best = INFINITY, lsum = 0.0;
+  double2 ph = make_double2(1.0, 0.0);
+  for (int c = 0; c + 1 < n; c += 2) {
+    unsigned long long k = 0;
+    int row = 0x7fffffff;
+    for (int r = c + 1 + threadIdx.x; r < n; r += CX_NT) take_better(k, row, D::key(M[(size_t)c * n + r]), r);
+    const int p = block_argmax<CX_NT>(k, row, redk[(c >> 1) & 1], redr[(c >> 1) & 1]);
+    const int q = c + 1;
+    if (p != q) {
+      par ^= 1;
+      for (int x = threadIdx.x; x < n; x += CX_NT) {
+        const F u = M[(size_t)p * n + x], v = M[(size_t)q * n + x];
+        M[(size_t)p * n + x] = v;
+        M[(size_t)q * n + x] = u;
+      }
+      if (threadIdx.x == 0) {
+        const int t = perm[p];
+        perm[p] = perm[q];
+        perm[q] = t;
+      }
+      __syncthreads();
+      for (int x = c + threadIdx.x; x < n; x += CX_NT) {
+        const F u = M[(size_t)x * n + p], v = M[(size_t)x * n + q];
+        M[(size_t)x * n + p] = v;
+        M[(size_t)x * n + q] = u;
+      }
+      __syncthreads();
+    }
+    const F d = M[(size_t)c * n + q];
+    if (threadIdx.x == 0) {
+      dm[c >> 1] = d;
+      const double m = D::mag(d);
+      if (m < best) {  // first index on ties; the first zero pivot once there is one
+        best = m;
+        K = c >> 1;
+      }
+      if (D::is0(d)) {
+        if (nzero == 1) z2 = c >> 1;
+        ++nzero;
+      } else {
+        D::acc(ph, lsum, d);
+      }
+    }
+    if (D::is0(d)) continue;  // tau = 0: the step leaves the matrix as it is
+    const F rd = D::rcp(d);
+    const F* Rc = M + (size_t)c * n;
+    const F* Rq = M + (size_t)q * n;
+    for (int r = q + 1 + wave; r < n; r += CX_NT / 64) {
+      F* R = M + (size_t)r * n;
+      const F tr = D::mul(Rc[r], rd);
+      const F wr = D::sub(D::zero(), Rq[r]);
+      for (int x = q + 1 + lane; x < n; x += 64) {
+        const F wx = D::sub(D::zero(), Rq[x]);
+        const F tx = D::mul(Rc[x], rd);
+        R[x] = D::add(R[x], D::sub(D::mul(tr, wx), D::mul(wr, tx)));
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    PfaHead<F>& h = *(PfaHead<F>*)mb;
+    h.K = K;
+    h.pad[0] = h.pad[1] = 0;
+    const F dK = dm[K];
+    h.dK = dK;
+    // D_K = prod_{s != K} d_s as phase * exp(log sum), without d_K (a zero d_K was never
+    // accumulated) and without the lifted zero
+    if (!D::is0(dK)) {
+      lsum -= log(D::mag(dK));
+      const double2 u = D::to2(dK);
+      const double m = D::mag(dK);
+      ph = c2mul(ph, make_double2(u.x / m, -u.y / m));
+    }
+    const double e = exp(lsum);
+    const double sP = par ? -1.0 : 1.0;
+    const double2 DK = make_double2(sP * ph.x * e, sP * ph.y * e);
+    const double2 dK2 = D::to2(dK);
+    double2 a1 = c2mul(DK, dK2), a2 = c2mul(DK, make_double2(1.0 - dK2.x, -dK2.y));
+    h.z = nzero >= 3 ? -2 : nzero == 2 ? z2 : -1;
+    if (nzero == 2) {  // mean of the lifted evaluations d_z = +1 and d_z = -1
+      a1 = make_double2(0.5 * a1.x, 0.5 * a1.y);
+      a2 = make_double2(0.5 * a2.x, 0.5 * a2.y);
+    }
+    h.a1[0] = D::from(a1);
+    h.a2[0] = D::from(a2);
+    h.a1[1] = D::from(make_double2(-a1.x, -a1.y));
+    h.a2[1] = D::from(make_double2(-a2.x, -a2.y));
+    sK = K;
+  }
+  __syncthreads();
+  const int aK = 2 * sK, pK = aK + 1;
+  const F rK = D::rcp(M[(size_t)aK * n + pK]);  // d_K (0 -> 0: tau_K = 0)
+  int* po = (int*)(mb + PL.perm);
+  F* ell = (F*)(mb + PL.ell);
+  for (int r = threadIdx.x; r < n; r += CX_NT) {
+    po[r] = perm[r];
+    ell[r] = r < pK ? D::zero() : r == pK ? D::one() : D::sub(D::zero(), D::mul(M[(size_t)r * n + aK], rK));
+  }
+}
+
 template <class F>
 bool cx_in_lds(int n, int ld) {
   return (size_t)n * ld * sizeof(F) <= CX_LDS_MAX;
@@ -377,11 +646,12 @@ int launch_cgj(const void* a, int n, int skew, int64_t batch, void* sign, void* 
   F* sg = (F*)sign;
   R* lg = (R*)logabs;
   if (mode == GJ_INV)
-    cgj_kernel<F, GJ_INV><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, (F*)out, out_t, (const F*)gate);
+    cgj_kernel<F, GJ_INV><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, (F*)out, out_t, (const F*)gate, nullptr, PfaLayout{}, 0);
   else if (mode == GJ_ADJ)
-    cgj_kernel<F, GJ_ADJ><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, (F*)out, 1, nullptr);
+    cgj_kernel<F, GJ_ADJ><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, (F*)out, 1, nullptr, nullptr, PfaLayout{}, 0);
   else
-    cgj_kernel<F, GJ_FWD><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, nullptr, 0, nullptr);
+    cgj_kernel<F, GJ_FWD><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, nullptr, 0, nullptr, nullptr,
+                                                  PfaLayout{}, 0);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
@@ -472,11 +742,61 @@ size_t slogpf_ws(int64_t batch, int n) {
   return n > CX_MAXN ? 0 : cx_matrix_ws<cx<T>>(batch, n, n);
 }
 
+// The Pfaffian adjugate's workspace: the Parlett-Reid matrix and then [T~ | I] (the same
+// bytes; none while they fit in LDS) and the per-member metadata.
+template <class F>
+size_t pf_adjugate_ws(int64_t batch, int n) {
+  if (batch <= 0 || n <= 0 || (n & 1) || n > CX_MAXN) return 0;
+  const size_t mats = std::max(cx_matrix_ws<F>(batch, n, n), cx_matrix_ws<F>(batch, n, 2 * n));
+  return align_up(mats) + align_up((size_t)batch * pfa_layout<F>(n).stride);
+}
+
+template <class F>
+__global__ void cx_zero_kernel(F* g, int64_t count) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < count; e += (int64_t)gridDim.x * blockDim.x)
+    g[e] = Fd<F>::zero();
+}
+
+template <class F>
+int cx_zero(F* g, int64_t count, hipStream_t s) {
+  if (count <= 0) return FX_OK;
+  const int64_t blocks = std::min<int64_t>((count + 255) / 256, 65536);
+  cx_zero_kernel<F><<<dim3((unsigned)blocks), 256, 0, s>>>(g, count);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+// g = pf(S) S^-1 for even n > 0: the Parlett-Reid factor, then one [T~ | I] Gauss-Jordan
+// per evaluation (the second returns at once for the members without a lifted pivot).
+template <class F>
+int pf_adjugate(const F* a, int64_t batch, int n, int skew, F* g, void* ws, size_t wsb, hipStream_t s) {
+  const size_t need = pf_adjugate_ws<F>(batch, n);
+  if (need && (!ws || wsb < need)) return FX_ERR_WORKSPACE;
+  const PfaLayout PL = pfa_layout<F>(n);
+  char* base = (char*)ws;
+  const size_t mats = align_up(std::max(cx_matrix_ws<F>(batch, n, n), cx_matrix_ws<F>(batch, n, 2 * n)));
+  F* W = (F*)base;
+  unsigned char* meta = (unsigned char*)(base + mats);
+  const dim3 grid((unsigned)batch);
+  {
+    const bool lds = cx_in_lds<F>(n, n);
+    const size_t shm = cx_lds_bytes((size_t)n * n * sizeof(F), n, lds, true);
+    cpfa_factor_kernel<F><<<grid, CX_NT, shm, s>>>(a, n, skew, W, lds, meta, PL);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  }
+  const bool lds = cx_in_lds<F>(n, 2 * n);
+  const size_t shm = cx_lds_bytes((size_t)n * 2 * n * sizeof(F), n, lds, true);
+  for (int ev = 0; ev < 2; ++ev) {
+    cgj_kernel<F, GJ_PFA><<<grid, CX_NT, shm, s>>>(a, n, skew, W, lds, nullptr, nullptr, g, 0, nullptr, meta, PL, ev);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  }
+  return FX_OK;
+}
+
 template <class T>
 size_t slogpf_parts_ws(int64_t batch, int n) {
   if (n > CX_MAXN || batch <= 0) return 0;
-  return align_up(slogpf_ws<T>(batch, n)) + align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n)) +
-         align_up((size_t)batch * 3 * sizeof(T));
+  const size_t inv = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n)) + align_up((size_t)batch * 3 * sizeof(T));
+  return align_up(slogpf_ws<T>(batch, n)) + std::max(inv, pf_adjugate_ws<cx<T>>(batch, n));
 }
 
 template <class T>
@@ -487,28 +807,42 @@ int slogpf(const T* a, int64_t batch, int n, int skew, T* sign, T* logabs, void*
   return launch_cpr<T>(a, n, skew != 0, batch, sign, logabs, ws, wsb, s);
 }
 
-// S^-1 by Gauss-Jordan on the same S (zeroed where the Parlett-Reid run found pf = 0;
-// every member for odd n), after the Parlett-Reid run for sign / logabs.
+// The Parlett-Reid run for sign / logabs, then g: S^-1 by Gauss-Jordan on the same S
+// (zeroed where the Parlett-Reid run found pf = 0; every member for odd n), or the
+// Pfaffian adjugate pf(S) S^-1 (zero for odd n).
 template <class T>
 int slogpf_parts(const T* a, int64_t batch, int n, int skew, int adjugate, T* sign, T* logabs, T* g, void* ws,
                  size_t wsb, hipStream_t s) {
   int st = check_cx_args<cx<T>>(a, batch, n, sign, logabs, g, ws);
   if (st != FX_OK || batch == 0) return st;
-  if (adjugate) return FX_ERR_UNSUPPORTED;
   if (!g) return slogpf<T>(a, batch, n, skew, sign, logabs, ws, wsb, s);
   if (n == 0) return cx_empty<cx<T>>(sign, logabs, batch, s);
   if (wsb < slogpf_parts_ws<T>(batch, n) || (!ws && slogpf_parts_ws<T>(batch, n))) return FX_ERR_WORKSPACE;
   const size_t pr = align_up(slogpf_ws<T>(batch, n));
-  const size_t gj = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n));
   char* base = (char*)ws;
   st = launch_cpr<T>(a, n, skew != 0, batch, sign, logabs, base, pr, s);
   if (st != FX_OK) return st;
+  if (adjugate) {
+    if (n & 1) return cx_zero<cx<T>>((cx<T>*)g, batch * (int64_t)n * n, s);
+    return pf_adjugate<cx<T>>((const cx<T>*)a, batch, n, skew != 0, (cx<T>*)g, base + pr, wsb - pr, s);
+  }
+  const size_t gj = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n));
   T* gsign = (T*)(base + pr + gj);
   T* glog = gsign + 2 * batch;
   return launch_cgj<cx<T>>(a, n, skew != 0, batch, gsign, glog, g, GJ_INV, 0, sign, base + pr, gj, s);
 }
 
 }  // namespace
+
+// the float64 Pfaffian adjugate (fx_slogpf_parts_f64 with adjugate != 0): zero for odd n
+size_t pf_adjugate_f64_ws(int64_t batch, int n) { return pf_adjugate_ws<double>(batch, n); }
+int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, void* ws, size_t wsb,
+                    hipStream_t s) {
+  if (batch <= 0 || n == 0) return FX_OK;
+  if (n & 1) return cx_zero<double>(g, batch * (int64_t)n * n, s);
+  return pf_adjugate<double>(a, batch, n, skew, g, ws, wsb, s);
+}
+
 }  // namespace fx
 
 using namespace fx;

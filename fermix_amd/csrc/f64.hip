@@ -27,6 +27,8 @@
 // unassigned index, p = argmax |S[p, a]|; pf = sgn(pi) prod d_k). Both add
 // round(tau_r w_x) - round(w_r tau_x) (no contraction), so the matrix stays exactly
 // skew-symmetric. All four are latency-bound per matrix (barriers per column step).
+#include <algorithm>
+
 #include "common.h"
 #include "fermix_internal.h"
 
@@ -607,7 +609,8 @@ int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmet
 size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n) {
   if (n > F64_MAXN || batch <= 0) return 0;
   const size_t pr = fx_slogpf_f64_workspace(batch, n), gj = gj64_ws(batch, n, true);
-  return align_up_256(pr) + align_up_256(gj) + align_up_256((size_t)batch * 2 * sizeof(double));
+  const size_t inv = align_up_256(gj) + align_up_256((size_t)batch * 2 * sizeof(double));
+  return align_up_256(pr) + std::max(inv, pf_adjugate_f64_ws(batch, n));
 }
 
 int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
@@ -615,15 +618,18 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
                         fx_stream_t stream) {
   int st = check_f64_args(a, batch, n, sign, logabs, g, workspace);
   if (st != FX_OK || batch == 0) return st;
-  if (adjugate) return FX_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
   if (!g) return fx_slogpf_f64(a, batch, n, skew_symmetrize, sign, logabs, workspace, workspace_bytes, stream);
-  if (workspace_bytes < fx_slogpf_parts_f64_workspace(batch, n) || !workspace) return FX_ERR_WORKSPACE;
+  const size_t need = fx_slogpf_parts_f64_workspace(batch, n);
+  if (workspace_bytes < need || (!workspace && need)) return FX_ERR_WORKSPACE;
   const size_t pr = align_up_256(fx_slogpf_f64_workspace(batch, n));
   const size_t gj = align_up_256(gj64_ws(batch, n, true));
   char* base = (char*)workspace;
   st = launch_pr64(a, n, skew_symmetrize != 0, batch, sign, logabs, base, pr, s);
   if (st != FX_OK || n == 0) return st;
+  // the Pfaffian adjugate from its own Parlett-Reid run (cplx.hip)
+  if (adjugate)
+    return pf_adjugate_f64(a, batch, n, skew_symmetrize != 0, g, base + pr, workspace_bytes - pr, s);
   // S^-1 by Gauss-Jordan on the same S, zeroed where the Parlett-Reid run found pf = 0
   // (every member for odd n)
   double* gsign = (double*)(base + pr + gj);

@@ -140,4 +140,9 @@ struct GemmDesc {
 // C = alpha op(A) op(B) + beta C for every (batch, second-batch) index.
 int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s);
 
+// float64 Pfaffian adjugate pf(S) S^-1 (cplx.hip; zero for odd n)
+size_t pf_adjugate_f64_ws(int64_t batch, int n);
+int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, void* ws, size_t wsb,
+                    hipStream_t s);
+
 }  // namespace fx

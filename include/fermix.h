@@ -312,9 +312,16 @@ size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n);
 int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign, double* logabs,
                   void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
-/* sign / logabs bit-identical to fx_slogpf_f64, plus g (batch, n, n) = S^-1 (NULL to
- * skip), zero where pf(S) = 0 (odd n, an exactly zero pivot) or S^-1 is not finite.
- * adjugate != 0 (the Pfaffian adjugate) returns FX_ERR_UNSUPPORTED for float64. */
+/* sign / logabs bit-identical to fx_slogpf_f64, plus g (batch, n, n) (NULL to skip):
+ * adjugate = 0: g = S^-1, zero where pf(S) = 0 (odd n, an exactly zero pivot) or S^-1 is
+ * not finite;
+ * adjugate != 0: g = pf(S) S^-1, the Pfaffian adjugate (pf's gradient, -g / 2 = d pf / dS),
+ * finite and exact for singular S (rank n - 2: the rank-2 adjugate; rank <= n - 4: 0),
+ * zero for odd n: the reference's formula (_pf_adj_blocks / _pf_adj_coeffs / _second_zero,
+ * src/fermix/_fallback.py:101-192) from a Parlett-Reid run of its own (the smallest
+ * pivot K by modulus, exact zero pivots and d_K replaced by 1) and one Gauss-Jordan
+ * inverse of the replaced factorisation, a second exact zero pivot lifted to +1 and -1
+ * (two inverses for those members); sign / logabs stay those of the plain forward. */
 size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
@@ -332,7 +339,7 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
  * inv_t = A^-T without conjugation (the holomorphic derivative of log det, as in
  * `_lu_parts_generic`, :63-97). Unblocked kernels, one workgroup per matrix, the matrix in
  * LDS when it fits (else one copy per member in the workspace; twice that with the
- * inverse), 0 <= n <= 4096. The pf adjugate mode returns FX_ERR_UNSUPPORTED. */
+ * inverse), 0 <= n <= 4096. */
 size_t fx_slogdet_c64_workspace(int64_t batch, int32_t n);
 int fx_slogdet_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream);
@@ -359,8 +366,16 @@ size_t fx_slogpf_c128_workspace(int64_t batch, int32_t n);
 int fx_slogpf_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign,
                    double* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 
-/* sign / logabs bit-identical to fx_slogpf_c64 / _c128, plus g (batch, n, n) = S^-1 (NULL
- * to skip), zero where pf(S) = 0 (odd n, an exactly zero pivot) or S^-1 is not finite. */
+/* sign / logabs bit-identical to fx_slogpf_c64 / _c128, plus g (batch, n, n) (NULL to
+ * skip): adjugate = 0: g = S^-1, zero where pf(S) = 0 (odd n, an exactly zero pivot) or
+ * S^-1 is not finite;
+ * adjugate != 0: g = pf(S) S^-1, the Pfaffian adjugate (pf's gradient, -g / 2 = d pf / dS),
+ * finite and exact for singular S (rank n - 2: the rank-2 adjugate; rank <= n - 4: 0),
+ * zero for odd n: the reference's formula (_pf_adj_blocks / _pf_adj_coeffs / _second_zero,
+ * src/fermix/_fallback.py:101-192) from a Parlett-Reid run of its own (the smallest
+ * pivot K by modulus, exact zero pivots and d_K replaced by 1) and one Gauss-Jordan
+ * inverse of the replaced factorisation, a second exact zero pivot lifted to +1 and -1
+ * (two inverses for those members); sign / logabs stay those of the plain forward. */
 size_t fx_slogpf_parts_c64_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         float* sign, float* logabs, float* g, void* workspace, size_t workspace_bytes,

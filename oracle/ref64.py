@@ -105,10 +105,11 @@ def adjT_brute(A):
 
 def pf_grad_brute(S):
     """d pf / dS with the skew extension G = (D - D^T)/2,
-    D_ij = (-1)^(i+j+1) pf(S without rows/cols i, j) for i < j (brute force)."""
-    S = np.asarray(S, np.float64)
+    D_ij = (-1)^(i+j+1) pf(S without rows/cols i, j) for i < j (brute force); float64 or
+    complex128 (the holomorphic derivative)."""
+    S = _wide(S)
     n = S.shape[0]
-    D = np.zeros((n, n))
+    D = np.zeros((n, n), S.dtype)
     for i in range(n):
         for j in range(i + 1, n):
             keep = [k for k in range(n) if k not in (i, j)]
@@ -142,9 +143,9 @@ def adjT_svd(A):
 
 def pf_grad64(S):
     """d pf / dS as in ``pf_grad_brute`` with each minor's Pfaffian from ``pf64``."""
-    S = np.asarray(S, np.float64)
+    S = _wide(S)
     n = S.shape[0]
-    D = np.zeros((n, n))
+    D = np.zeros((n, n), S.dtype)
     for i in range(n):
         for j in range(i + 1, n):
             keep = [k for k in range(n) if k not in (i, j)]
@@ -156,9 +157,9 @@ def pf_grad64_rows(S, rows):
     """d pf / dS restricted to the entries (i, j) with i or j in ``rows`` (the rest set to
     zero): for S whose every other minor Pfaffian vanishes -- e.g. S with the rows and
     columns ``rows`` exactly zero -- this is the whole gradient, at O(n |rows|) minors."""
-    S = np.asarray(S, np.float64)
+    S = _wide(S)
     n = S.shape[0]
-    D = np.zeros((n, n))
+    D = np.zeros((n, n), S.dtype)
     for i in range(n):
         for j in range(i + 1, n):
             if i not in rows and j not in rows:

@@ -162,8 +162,9 @@ def test_f64_autograd(dev, n):
     assert np.allclose(_np(dl), ref, rtol=1e-9, atol=1e-9)
     sv, lv = torch.func.vmap(fermix_amd.slogdet)(_t(A, dev)[:, None])
     assert torch.equal(lv[:, 0], l0)
-    # det / pf values in float64; det's gradient is the exact adjugate of the same run
-    # (tests/test_gpu_adjugate64.py covers the singular cases); pf's is float32-only
+    # det / pf values in float64; det's gradient is the exact adjugate of the same run,
+    # pf's the Pfaffian adjugate (tests/test_gpu_adjugate64.py and
+    # tests/test_gpu_pf_adjugate64.py cover the singular cases)
     d = fermix_amd.det(_t(A, dev))
     assert np.allclose(_np(d), np.linalg.det(A), rtol=1e-10, atol=0)
     p = fermix_amd.pf(_t(A, dev))
@@ -175,5 +176,9 @@ def test_f64_autograd(dev, n):
     (gd,) = torch.autograd.grad(dd.sum(), Ad)
     assert_grad64(_np(gd), np.linalg.det(A)[:, None, None] * np.swapaxes(ref64.inv64(A), 1, 2), A,
                   "det autograd")
-    with pytest.raises(NotImplementedError):
-        fermix_amd.pf(_t(A, dev).requires_grad_())
+    Ap = _t(A, dev).requires_grad_()
+    pp = fermix_amd.pf(Ap)
+    assert torch.equal(pp.detach(), p)
+    (gp,) = torch.autograd.grad(pp.sum(), Ap)
+    pf_ref = sr * np.exp(lr)
+    assert_grad64(_np(gp), 0.5 * pf_ref[:, None, None] * np.swapaxes(ref64.inv64(S), 1, 2), S, "pf autograd")

@@ -1,0 +1,154 @@
+"""GPU parity of pf's gradient, the Pfaffian adjugate pf(S) S^-1, for the float64 and
+complex kinds (fx_slogpf_parts_f64 / _c64 / _c128 with adjugate != 0): regular members
+against pf(S) S^-1 in float64 / complex128, singular ones (one and two exact zero pivots,
+rank n - 2; three, rank n - 4) against minor Pfaffians, and the autograd / jvp rules with
+torch's conjugate convention -- the reference's pf gradient tests for every dtype
+(tests/test_fermix.py:522-610)."""
+
+import numpy as np
+import pytest
+import torch
+
+import fermix_amd
+from fermix_amd import _kernels
+from oracle import generic as g
+from oracle import ref64
+from tests.tolerances import relerr
+
+pytestmark = pytest.mark.gpu
+
+KINDS = {"f64": (np.float64, 1e-10), "c64": (np.complex64, 5e-5), "c128": (np.complex128, 1e-10)}
+
+
+def _np(x):
+    return x.detach().cpu().numpy()
+
+
+def _jmat(n):
+    J = np.zeros((n, n))
+    for i in range(0, n - 1, 2):
+        J[i, i + 1], J[i + 1, i] = 1.0, -1.0
+    return J
+
+
+def _near_j(rng, B, n, dt):
+    """X J X^T with X = I + N(0, 1/(4n)) (complex: both parts): pf = det(X) = O(1)."""
+    X = rng.standard_normal((B, n, n))
+    if np.dtype(dt).kind == "c":
+        X = X + 1j * rng.standard_normal((B, n, n))
+    X = np.eye(n) + 0.5 * X / np.sqrt(n)
+    S = X @ _jmat(n) @ np.swapaxes(X, 1, 2)
+    return (0.5 * (S - np.swapaxes(S, 1, 2))).astype(dt)
+
+
+def _wide(x):
+    return x.astype(np.complex128 if np.iscomplexobj(x) else np.float64)
+
+
+def _pf_adj(S, dev):
+    """(sign, logabs, pf(S) S^-1) through the C ABI's adjugate mode (input already skew)."""
+    St = torch.from_numpy(S).to(dev)
+    sign, logabs, G = _kernels.slogpf_parts(St, False, adjugate=True)
+    return St, sign, logabs, _np(G)
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+@pytest.mark.parametrize("n", [2, 4, 16, 30, 64, 100, 130, 256])
+def test_pf_adjugate_regular(dev, kind, n):
+    """pf(S) S^-1 against float64 / complex128; the primal bit-identical to the plain
+    slogpf forward; the pf gradient (autograd, with skew_symmetrize on a skew input) is
+    -pf(S) S^-1 / 2, conjugated for the complex kinds, and the jvp is sum(G * dS)."""
+    if kind == "c128" and n > 130:
+        pytest.skip("complex128 at n = 256 adds run time without a new code path")
+    dt, tol = KINDS[kind]
+    rng = np.random.default_rng(9300 + n)
+    S = _near_j(rng, 3, n, dt)
+    print(f"pf adjugate {kind} n={n}", flush=True)
+    St, sign, logabs, G = _pf_adj(S, dev)
+    s0, l0 = fermix_amd.slogpf(St, skew_symmetrize=False)
+    assert torch.equal(sign, s0) and torch.equal(logabs, l0), "pf primal != forward"
+    W = _wide(S)
+    pf_ref = np.array([ref64.pf64(x) for x in W])
+    ref = pf_ref[:, None, None] * np.linalg.inv(W)
+    err = relerr(G, ref)
+    print(f"  relerr {err:.3g}", flush=True)
+    assert err < tol * max(1.0, n / 16)
+    X = St.clone().requires_grad_(True)
+    p = fermix_amd.pf(X)
+    assert torch.equal(p.detach(), s0 * torch.exp(l0))
+    (gr,) = torch.autograd.grad(p.real.sum() if p.is_complex() else p.sum(), X)
+    gr = _np(gr)
+    if kind != "f64":
+        gr = gr.conj()  # torch's conjugate-Wirtinger gradient -> d pf / dS
+    assert relerr(gr, -0.5 * ref) < tol * max(1.0, n / 16)
+    dS = _near_j(rng, 3, n, dt) - _near_j(rng, 3, n, dt)
+    _, dp = torch.func.jvp(fermix_amd.pf, (St,), (torch.from_numpy(dS).to(dev),))
+    want = (-0.5 * ref * _wide(dS)).sum(axis=(1, 2))
+    assert np.max(np.abs(_np(dp) - want)) < tol * max(1.0, n / 16) * np.abs(want).max() * 10
+
+
+def _zero_rows(S, b, rows):
+    for r in rows:
+        S[b, r % S.shape[1], :] = 0.0
+        S[b, :, r % S.shape[1]] = 0.0
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+@pytest.mark.parametrize("n", [4, 8, 10, 40, 130])
+def test_pf_adjugate_singular(dev, kind, n):
+    """Members: one zero row / column (one exact zero pivot, rank n - 2), rows 0 and 2
+    zero (two exact zero pivots, rank n - 2: the lifted evaluations), rows 0, 2 and 4
+    zero (rank n - 4: zero adjugate; for n = 4 the zero matrix), and a regular member,
+    against minor Pfaffians (all entries for n <= 10, the zeroed rows' entries, which are
+    then the only nonzero ones, above) and the oracle's generic formula."""
+    dt, tol = KINDS[kind]
+    rng = np.random.default_rng(9400 + n)
+    S = _near_j(rng, 4, n, dt)
+    _zero_rows(S, 0, [3])
+    _zero_rows(S, 1, [0, 2])
+    _zero_rows(S, 2, [0, 2, 4] if n > 4 else [0, 1, 2, 3])
+    print(f"pf adjugate singular {kind} n={n}", flush=True)
+    St, sign, logabs, G = _pf_adj(S, dev)
+    assert np.all(np.isfinite(G)) and np.all(_np(sign)[:3] == 0)
+    W = _wide(S)
+    grad = -0.5 * G
+    if n <= 10:
+        ref = [ref64.pf_grad64(x) for x in W[:3]]
+    else:
+        ref = [ref64.pf_grad64_rows(W[0], [3]), ref64.pf_grad64_rows(W[1], [0, 2]), np.zeros((n, n), W.dtype)]
+    ref.append(0.5 * ref64.pf64(W[3]) * np.linalg.inv(W[3]).T)
+    ref = np.stack(ref)
+    assert np.all(grad[2] == 0), "rank n - 4: zero adjugate"
+    for k in (0, 1, 3):
+        assert np.abs(ref[k]).max() > 0
+        err = relerr(grad[k], ref[k])
+        print(f"  member {k}: relerr {err:.3g}", flush=True)
+        assert err < tol * max(1.0, n / 16), (k, err)
+    if n <= 40:
+        _, _, Go, _ = g.pf_parts_generic(W, True)
+        assert relerr(G, Go) < tol * max(1.0, n / 16)
+    # autograd through pf: finite, equal to the adjugate (conjugated for complex)
+    X = St.clone().requires_grad_(True)
+    p = fermix_amd.pf(X)
+    (gr,) = torch.autograd.grad(p.real.sum() if p.is_complex() else p.sum(), X)
+    gr = _np(gr)
+    if kind != "f64":
+        gr = gr.conj()
+    assert np.array_equal(gr, grad)
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+def test_pf_adjugate_odd_and_empty(dev, kind):
+    """Odd n: pf = 0 and a zero gradient; n = 0: pf = 1 and an empty gradient."""
+    dt, _ = KINDS[kind]
+    rng = np.random.default_rng(9500)
+    for n in (3, 7):
+        A = rng.standard_normal((2, n, n)).astype(dt)
+        X = torch.from_numpy(A).to(dev).requires_grad_(True)
+        p = fermix_amd.pf(X)
+        assert np.all(_np(p) == 0)
+        (gr,) = torch.autograd.grad(p.real.sum() if p.is_complex() else p.sum(), X)
+        assert np.all(_np(gr) == 0)
+    X = torch.zeros((2, 0, 0), dtype=torch.from_numpy(np.zeros(1, dt)).dtype, device=dev).requires_grad_(True)
+    p = fermix_amd.pf(X)
+    assert np.all(_np(p) == 1)

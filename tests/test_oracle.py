@@ -428,3 +428,39 @@ def test_complex_adjT_svd_vs_cofactors(case):
         assert np.max(np.abs(C)) > 1e-3
     else:
         assert np.max(np.abs(C)) < 1e-10
+
+
+@pytest.mark.parametrize("case", ["regular", "one_zero", "two_zero", "three_zero"])
+def test_complex_pf_adjugate_vs_minors(case):
+    """The complex Pfaffian adjugate of the oracle (reference _pf_parts_generic with the
+    complex pivots' phases, _fallback.py:101-263) against minor Pfaffians by the
+    perfect-matching expansion (the holomorphic d pf / dS) -- the truth of the complex pf
+    gradient -- with a conjugated result failing it."""
+    n = 8
+    S = crandn((3, n, n), np.complex128)
+    S = S - np.swapaxes(S, 1, 2)
+    if case == "one_zero":
+        S[:, 2, :] = 0.0
+        S[:, :, 2] = 0.0
+    if case == "two_zero":  # rows 0 and 2 null: two exact zero pivots, rank n - 2
+        for r in (0, 2):
+            S[:, r, :] = 0.0
+            S[:, :, r] = 0.0
+    if case == "three_zero":  # rank n - 4: the adjugate is zero
+        for r in (0, 2, 4):
+            S[:, r, :] = 0.0
+            S[:, :, r] = 0.0
+    _, _, G, pfv = g.pf_parts_generic(S, True)
+    grad = -0.5 * G
+    ref = np.stack([ref64.pf_grad_brute(x) for x in S])
+    assert np.allclose(pfv, [ref64.pf_brute(x) for x in S], atol=1e-10 * max(1, np.abs(pfv).max()))
+    if case == "three_zero":
+        assert np.all(ref == 0) and np.max(np.abs(grad)) == 0
+        return
+    scale = np.abs(ref).max()
+    assert scale > 0
+    assert np.max(np.abs(grad - ref)) < 1e-10 * scale
+    assert np.max(np.abs(grad.conj() - ref)) > 1e-3 * scale
+    if case == "regular":
+        want = 0.5 * pfv[:, None, None] * np.linalg.inv(S).transpose(0, 2, 1)
+        assert np.max(np.abs(ref - want)) < 1e-10 * scale
