@@ -92,32 +92,44 @@ __device__ __forceinline__ int first_lane(bool p) {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float v16f_t __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ void split_bf16x3(const float (&x)[8], bf16x8 (&p)[3]) {
+// The split of four values (one staged group of consecutive k, for operands that are
+// split once when a K stage goes to LDS) and of eight (an operand split at its use).
+// Two values per conversion (v_cvt_pk_bf16_f32 rounds a pair into one register; the
+// parts come back to fp32 by a shift or a mask), the same bits as the scalar split.
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split4_bf16x3(const float (&x)[4], bf16x4 (&p)[3]) {
+  // residues of the values as given: no contraction with a product that formed them
+#pragma clang fp contract(off)
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const __bf16 h = (__bf16)x[u];
-    const float r1 = x[u] - (float)h;
-    const __bf16 m = (__bf16)r1;
-    const float r2 = r1 - (float)m;
-    p[0][u] = h;
-    p[1][u] = m;
-    p[2][u] = (__bf16)r2;
+  for (int u = 0; u < 4; u += 2) {
+    const f32x2_t v = {x[u], x[u + 1]};
+    const bf16x2_t h = __builtin_convertvector(v, bf16x2_t);
+    const f32x2_t hf = __builtin_convertvector(h, f32x2_t);
+    const f32x2_t r1 = {v[0] - hf[0], v[1] - hf[1]};
+    const bf16x2_t m = __builtin_convertvector(r1, bf16x2_t);
+    const f32x2_t mf = __builtin_convertvector(m, f32x2_t);
+    const f32x2_t r2 = {r1[0] - mf[0], r1[1] - mf[1]};
+    const bf16x2_t l = __builtin_convertvector(r2, bf16x2_t);
+    p[0][u] = h[0];
+    p[0][u + 1] = h[1];
+    p[1][u] = m[0];
+    p[1][u + 1] = m[1];
+    p[2][u] = l[0];
+    p[2][u + 1] = l[1];
   }
 }
-
-// The same split of four values (one staged group of consecutive k), for operands that
-// are split once when a K stage goes to LDS.
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void split4_bf16x3(const float (&x)[4], bf16x4 (&p)[3]) {
+__device__ __forceinline__ void split_bf16x3(const float (&x)[8], bf16x8 (&p)[3]) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const __bf16 h = (__bf16)x[u];
-    const float r1 = x[u] - (float)h;
-    const __bf16 m = (__bf16)r1;
-    const float r2 = r1 - (float)m;
-    p[0][u] = h;
-    p[1][u] = m;
-    p[2][u] = (__bf16)r2;
+  for (int q = 0; q < 2; ++q) {
+    const float y[4] = {x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+    bf16x4 t[3];
+    split4_bf16x3(y, t);
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) p[s][4 * q + u] = t[s][u];
   }
 }
 

@@ -29,6 +29,8 @@
 //    applied between the stage load and the LDS store), a compile-time variant.
 // The mask combination is a template parameter for the combinations the library uses,
 // so a masked element costs one compare and a plain stage carries no mask code.
+#include <type_traits>
+
 #include "common.h"
 #include "fermix_internal.h"
 
@@ -478,16 +480,23 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
   klo = max(0, (klo / GBK) * GBK);
 
   const bool interior = i0 + BM <= d.M && j0 + BN <= d.N;
-  auto plain_stage = [&](int k0) {
-    bool ok = interior && k0 + GBK <= d.K;
-    if (maskA == MASK_LOWER_UNIT) ok = ok && i0 + d.offAr > k0 + GBK - 1 + d.offAc;
-    if (maskA == MASK_UPPER) ok = ok && i0 + BM - 1 + d.offAr <= k0 + d.offAc;
-    if (maskA == MASK_UPPER_UNIT) ok = ok && i0 + BM - 1 + d.offAr < k0 + d.offAc;
-    if (maskB == MASK_LOWER_UNIT) ok = ok && k0 + d.offBr > j0 + BN - 1 + d.offBc;
-    if (maskB == MASK_UPPER) ok = ok && k0 + GBK - 1 + d.offBr <= j0 + d.offBc;
-    if (maskB == MASK_UPPER_UNIT) ok = ok && k0 + GBK - 1 + d.offBr < j0 + d.offBc;
-    return ok;
+  // a stage is plain for an operand when none of its elements meets the operand's
+  // triangle diagonal (the K range is trimmed to the triangle per tile), and inside the
+  // matrices when no element is past M, N or K
+  auto plain_a = [&](int k0) {
+    if (maskA == MASK_LOWER_UNIT) return i0 + d.offAr > k0 + GBK - 1 + d.offAc;
+    if (maskA == MASK_UPPER) return i0 + BM - 1 + d.offAr <= k0 + d.offAc;
+    if (maskA == MASK_UPPER_UNIT) return i0 + BM - 1 + d.offAr < k0 + d.offAc;
+    return true;
   };
+  auto plain_b = [&](int k0) {
+    if (maskB == MASK_LOWER_UNIT) return k0 + d.offBr > j0 + BN - 1 + d.offBc;
+    if (maskB == MASK_UPPER) return k0 + GBK - 1 + d.offBr <= j0 + d.offBc;
+    if (maskB == MASK_UPPER_UNIT) return k0 + GBK - 1 + d.offBr < j0 + d.offBc;
+    return true;
+  };
+  auto inside = [&](int k0) { return interior && k0 + GBK <= d.K; };
+  auto plain_stage = [&](int k0) { return inside(k0) && plain_a(k0) && plain_b(k0); };
 
   // this thread's staging slots (two float4 of A, two of B per stage), 32-bit offsets
   // within a matrix (N * N < 2^31); rows / columns past the matrix clamped once here
@@ -565,35 +574,44 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
   auto xB = [&](int b) { return reinterpret_cast<__bf16*>(smem) + b * 3 * (XPA + XPB) + 3 * XPA; };
   const int xp = tid & 63, xk = 4 * (tid >> 6);
   const int xia = min(i0 + 2 * xp, d.M - 2), xjb = min(j0 + 2 * xp, d.N - 2);
-  float xa[2][4], xb[2][4], xs[4];
-  auto load_x3 = [&](int k0) {
+  // a stage's loaded values (a second set, with the loads two stages ahead, measured
+  // 26 % slower on the n = 512 slogdet backward: 194 VGPRs leave two workgroups per CU
+  // against three)
+  struct X3Regs {
+    float a[2][4], b[2][4], s[4];
+  };
+  X3Regs rg0;
+  auto load_x3 = [&](int k0, X3Regs& R) {
     if (!TA) {
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const float4 x = *reinterpret_cast<const float4*>(A + aoff[e] + min(k0 + ka, d.K - 4));
-        xa[e][0] = x.x;
-        xa[e][1] = x.y;
-        xa[e][2] = x.z;
-        xa[e][3] = x.w;
+        R.a[e][0] = x.x;
+        R.a[e][1] = x.y;
+        R.a[e][2] = x.z;
+        R.a[e][3] = x.w;
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float2 x = *reinterpret_cast<const float2*>(A + min(k0 + xk + r, d.K - 1) * d.lda + xia);
-        xa[0][r] = x.x;
-        xa[1][r] = x.y;
+        R.a[0][r] = x.x;
+        R.a[1][r] = x.y;
       }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int kr = min(k0 + xk + r, d.K - 1);
-      if (BS) xs[r] = d.bscale[bat * (d.K / 2) + (kr >> 1)];
+      if (BS) R.s[r] = d.bscale[bat * (d.K / 2) + (kr >> 1)];
       const float2 y = *reinterpret_cast<const float2*>(B + (BS ? kr ^ 1 : kr) * d.ldb + xjb);
-      xb[0][r] = y.x;
-      xb[1][r] = y.y;
+      R.b[0][r] = y.x;
+      R.b[1][r] = y.y;
     }
   };
-  auto store_x3 = [&](int b, int k0, bool plain) {
+  // the stage's masks: each operand's triangle only where its stage meets the diagonal,
+  // the matrix edges only in edge tiles and a partial last stage (all uniform)
+  auto put_x3 = [&](int b, int k0, const X3Regs& R, auto ma_c, auto mb_c, auto edge_c) {
+    constexpr bool ma = decltype(ma_c)::value, mb = decltype(mb_c)::value, edge = decltype(edge_c)::value;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       // A: row gi, k from gk; B: column gj, k from k0 + xk
@@ -602,19 +620,30 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
       float va4[4], vb4[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float v = xa[e][r];
-        if (!plain)
-          v = (gi >= d.M || gk + r >= d.K) ? 0.0f : (maskA ? mask_val(v, maskA, gi + d.offAr, gk + r + d.offAc) : v);
+        float v = R.a[e][r];
+        if (ma) v = mask_val(v, maskA, gi + d.offAr, gk + r + d.offAc);
+        if (edge) v = (gi >= d.M || gk + r >= d.K) ? 0.0f : v;
         va4[r] = v;
         const int k = k0 + xk + r;
-        float w = xb[e][r];
-        if (BS) w *= (k & 1) ? -xs[r] : xs[r];
-        if (!plain) w = (gj >= d.N || k >= d.K) ? 0.0f : (maskB ? mask_val(w, maskB, k + d.offBr, gj + d.offBc) : w);
+        float w = R.b[e][r];
+        if (BS) w *= (k & 1) ? -R.s[r] : R.s[r];
+        if (mb) w = mask_val(w, maskB, k + d.offBr, gj + d.offBc);
+        if (edge) w = (gj >= d.N || k >= d.K) ? 0.0f : w;
         vb4[r] = w;
       }
       x3_put<XPA>(xA(b), x3_off16(gi - i0, gk - k0), va4);
       x3_put<XPB>(xB(b), x3_off16(gj - j0, xk), vb4);
     }
+  };
+  auto store_x3 = [&](int b, int k0, const X3Regs& R) {
+    using T = std::true_type;
+    using F = std::false_type;
+    const bool ma = !plain_a(k0), mb = !plain_b(k0), edge = !inside(k0);
+    if (edge) put_x3(b, k0, R, T{}, T{}, T{});
+    else if (ma && mb) put_x3(b, k0, R, T{}, T{}, F{});
+    else if (ma) put_x3(b, k0, R, T{}, F{}, F{});
+    else if (mb) put_x3(b, k0, R, F{}, T{}, F{});
+    else put_x3(b, k0, R, F{}, F{}, F{});
   };
 
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
@@ -628,13 +657,13 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
   if constexpr (X3) {
    if (klo < khi) {
-    load_x3(klo);
-    store_x3(0, klo, plain_stage(klo));
+    load_x3(klo, rg0);
+    store_x3(0, klo, rg0);
     __syncthreads();
     int buf = 0;
     for (int k0 = klo; k0 < khi; k0 += GBK) {
       const bool more = k0 + GBK < khi;
-      if (more) load_x3(k0 + GBK);
+      if (more) load_x3(k0 + GBK, rg0);
       // the stage's K = 16 in one bf16x3 product per accumulator; A's parts first, then
       // each B column block's, used by both A row blocks
       bf16x8 ap[2][3];
@@ -648,7 +677,7 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
         for (int a = 0; a < 2; ++a) acc[a][b] = mfma_bf16x3(ap[a], bp, acc[a][b]);
       }
       if (more) {
-        store_x3(buf ^ 1, k0 + GBK, plain_stage(k0 + GBK));
+        store_x3(buf ^ 1, k0 + GBK, rg0);
         __syncthreads();
         buf ^= 1;
       }
