@@ -214,7 +214,7 @@ def override(t=None, **changes):
 # n ranges -> kernel family (mirrors fx_slogdet_f32 / fx_slogpf_f32 dispatch)
 TINY_MAX_N = {"slogdet": 32, "slogpf": 16}  # several matrices per wave, one lane per row
 SMALL_MAX_N = 128  # largest n the fused one-workgroup-per-matrix kernels are built for
-LARGE_MAX_N = 4096  # blocked kernels; larger n is unsupported
+LARGE_MAX_N = 8192  # blocked kernels (float32); larger n is unsupported
 
 # The library's family override (read by every C entry point; a test hook like the
 # reference's OVERRIDE, src/fermix/_common.py:363-378, which its tests use to force a

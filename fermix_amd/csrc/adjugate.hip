@@ -25,7 +25,7 @@ namespace fx {
 // among the 2^r orbit elements starting at i and nx[i] = perm^(2^r)(i), so after
 // ceil(log2 N) rounds every element carries its cycle's minimum and each cycle has exactly
 // one element labelled by itself. One workgroup per member, N <= PARITY_MAXN.
-constexpr int PARITY_MAXN = 4096;
+constexpr int PARITY_MAXN = 8192;
 
 __global__ __launch_bounds__(256) void perm_parity_kernel(const int* __restrict__ perm, int N,
                                                           int* __restrict__ parity) {

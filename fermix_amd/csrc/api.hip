@@ -69,7 +69,7 @@ static constexpr int PF_LARGE_MAX = PF_LARGE_MAXN;
 // Kernel families. The choice depends on n only (never on the batch), so a batched call
 // and a vmapped one run the same arithmetic: several matrices per wave (n <= 32 for the
 // LU, 16 for Parlett-Reid), one fused workgroup per matrix (n <= 128), blocked kernels
-// with workspace (n <= 4096). The environment variable FERMIX_AMD_KERNELS = tiny | fused
+// with workspace (n <= 8192). The environment variable FERMIX_AMD_KERNELS = tiny | fused
 // | blocked forces a family where it covers n (for cross-checks and tuning sweeps; an
 // uncovered n then reports FX_ERR_UNSUPPORTED). It is read on every call and the library
 // keeps no state of its own.

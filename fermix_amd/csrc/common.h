@@ -171,6 +171,21 @@ __device__ __forceinline__ v16f_t mfma_bf16x3(const bf16x8 (&a)[3], const bf16x8
   return acc;
 }
 
+// The same six products into two accumulators: hh += hi*hi, sm += the five smaller terms.
+// The bf16 MFMA adds each product to its accumulator truncated to about three bits
+// below the accumulator's last place (measured on gfx950: sixteen products of 0.1 ulp
+// each leave a 1.0 accumulator unchanged), so small terms added to a large accumulator
+// are biased toward zero; in their own accumulator, about 2^-8 of hh, that loss is
+// 2^-8 smaller, and the caller adds the accumulators (and any seed) in fp32.
+__device__ __forceinline__ void mfma_bf16x3_2(const bf16x8 (&a)[3], const bf16x8 (&b)[3], v16f_t& hh, v16f_t& sm) {
+  sm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], sm, 0, 0, 0);
+  sm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], sm, 0, 0, 0);
+  sm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], sm, 0, 0, 0);
+  sm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], sm, 0, 0, 0);
+  sm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], sm, 0, 0, 0);
+  hh = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], hh, 0, 0, 0);
+}
+
 // fp32 MFMA 16x16x4: D = A(16x4) * B(4x16) + C. Lane l supplies A[l%16][l/16] and
 // B[l/16][l%16]; D/C element (4*(l/16)+v, l%16) sits in item v of lane l.
 __device__ __forceinline__ v4f mfma16(float a, float b, v4f c) {

@@ -44,7 +44,7 @@ int launch_pf_small(const float* A, int n, int skew, int64_t batch, float* sign,
 // return the packed LU (B, N, N) and, with parts, the composed row map (B, N),
 // N = lu_large_padded. With W_ext (and, with parts, g0_ext) the LU and the row map are
 // formed in those caller buffers instead of the workspace (external = true sizes it).
-constexpr int LU_LARGE_MAXN = 4096;
+constexpr int LU_LARGE_MAXN = 8192;
 int lu_large_padded(int n);
 size_t lu_large_workspace(int64_t batch, int n, bool parts, bool external = false);
 // x3 != 0 runs the trailing updates in the split-bf16x3 mode (FX_PREC_BF16X3); lu_block is
@@ -67,9 +67,9 @@ int launch_lu_inverse(float* LU, const int* g0, int N, int n, int64_t batch, con
 
 // 128 < n <= PF_LARGE_MAXN Parlett-Reid (pf_large.hip); with gbuf the factors
 // (B, N/PB, N, PB) by original row (PB = pf_large_block_cols(N)), d (B, N/2) and perm (B, N).
-constexpr int PF_LARGE_MAXN = 4096;
+constexpr int PF_LARGE_MAXN = 8192;
 int pf_large_padded(int n);
-int pf_large_block_cols(int N);  // columns per factor chunk: 32 for N <= 2048, 16 above
+int pf_large_block_cols(int N);  // columns per factor chunk: 32 for N <= 2048, 16 to 4096, 8 above
 size_t pf_large_workspace(int64_t batch, int n, bool fact);
 int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
                     float* gbuf, float* dout, int* perm, void* ws, size_t ws_bytes, hipStream_t s);

@@ -1,4 +1,4 @@
-// Blocked LU with partial pivoting for 128 < n <= 4096 (any batch): per block of PW = 64
+// Blocked LU with partial pivoting for 128 < n <= 8192 (any batch): per block of PW = 64
 // columns at r0 three launches (blocks go in pairs, see run_blocks: the first block's
 // trailing update is deferred and merged into the second's at K = 128),
 //   1. the panel (one workgroup per matrix), factored in place in the work buffer; the
@@ -736,10 +736,9 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // The trailing update A22 -= L21 U12 over K = 64 KC columns from r0 (KC = 1: one block,
 // KC = 2: a block pair whose first update was deferred), on the 64 x 64 tiles of rows
 // >= r1 = r0 + 64 KC and of ntc tile columns from r1. Every K chunk of 64 is one LDS
-// stage; every load of a tile -- its C (straight into the accumulators, which the MFMAs
-// then reduce: C - L21 U12 with no epilogue arithmetic), the first chunk's L21 rows and
-// U12 columns -- is issued up front, the next chunk's while the current chunk's MFMAs
-// run: more bytes in flight per workgroup than a K-pipelined GEMM at this short K.
+// stage; the first chunk's L21 rows and U12 columns are loaded up front, the next chunk's
+// while the current chunk's MFMAs run, and the products -L21 U12 are summed in
+// accumulators of their own, C read and added in fp32 at the end.
 // A0 (first block pair, in place of the input copy): C of position p is input row
 // rmapC[p].
 // XCD-aware tile order when the batch is a multiple of 8 (one matrix's L21 / U12 fetched
@@ -774,22 +773,20 @@ __global__ __launch_bounds__(256, X3 ? 3 : 4) void lu_update_kernel(float* __res
   const int i0 = r1 + 64 * (tx / ntc), j0 = r1 + 64 * (tx % ntc);
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
   const int l32 = lane & 31, lh = lane >> 5;
-  v16f acc;
-  if (A0) {
-    const float* Ab = A0 + b * (int64_t)N * N;
-    const int* rb = rmapC + b * N;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] = Ab[rb[i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)] * N + j0 + wn + l32];
-  } else {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] = Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32];
-  }
   // staging of one chunk: thread (r = e / 16, q = 4 (e % 16)) of e = tid + 256 u holds
   // L21 (i0 + r, q .. q+3) and U12 (r, j0 + q .. q+3) of the chunk; float arrays stay in
   // registers. X3 takes U12 column-wise instead: thread (j = tid % 64, kq = tid / 64)
   // holds U12 (16 u + 4 kq .. +3, j0 + j), so that each staged group is four
   // consecutive k of one column.
   float av[16], bw[16];
+  // the products' accumulators, added to C (in acc) at the end: the MFMAs truncate what
+  // they add to an accumulator below about three bits under its last place, so products
+  // summed on their own lose far less than products added to C one by one (measured at
+  // n = 4160: logabs error 1.1e-4 -> 1.7e-5 for the bf16x3 mode). fp32 mode: xhh only;
+  // X3: hi*hi in xhh, the smaller terms in xsm.
+  v16f xhh, xsm;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) xhh[v] = xsm[v] = 0.0f;
   auto load = [&](int c) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -837,21 +834,35 @@ __global__ __launch_bounds__(256, X3 ? 3 : 4) void lu_update_kernel(float* __res
     if (c + 1 < KC) load(c + 1);
     if constexpr (X3) {
       // split-bf16x3: four K = 16 slices, lane operands the eight k = 16 q + 8 lh + u of
-      // its row of -L21 and its column of U12, one 16-byte read per plane
+      // its row of -L21 and its column of U12, one 16-byte read per plane; the products
+      // in their own accumulators (hi*hi and the smaller terms), added to C at the end
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         bf16x8 pa[3], pb[3];
         x3_get<XP>(xA, x3_off64(wm + l32, 16 * q + 8 * lh), pa);
         x3_get<XP>(xB, x3_off64(wn + l32, 16 * q + 8 * lh), pb);
-        acc = mfma_bf16x3(pa, pb, acc);
+        mfma_bf16x3_2(pa, pb, xhh, xsm);
       }
     } else {
 #pragma unroll
       for (int kp = 0; kp < 32; ++kp)
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(-As[(wm + l32) * LDA_ + 2 * kp + lh],
-                                                   Bs[(2 * kp + lh) * LDB_ + wn + l32], acc, 0, 0, 0);
+        xhh = __builtin_amdgcn_mfma_f32_32x32x2f32(-As[(wm + l32) * LDA_ + 2 * kp + lh],
+                                                   Bs[(2 * kp + lh) * LDB_ + wn + l32], xhh, 0, 0, 0);
     }
   }
+  // C, read after the products (its registers are free during them)
+  v16f acc;
+  if (A0) {
+    const float* Ab = A0 + b * (int64_t)N * N;
+    const int* rb = rmapC + b * N;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = Ab[rb[i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)] * N + j0 + wn + l32];
+  } else {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32];
+  }
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] += X3 ? xhh[v] + xsm[v] : xhh[v];
 #pragma unroll
   for (int v = 0; v < 16; ++v) Wb[(i0 + wm + 8 * (v >> 2) + 4 * lh + (v & 3)) * N + j0 + wn + l32] = acc[v];
 }
@@ -999,8 +1010,10 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
     st = run_blocks<1024, 0>(W, N, batch, piv, nsw, srcs, X, g0, parts, direct ? A : nullptr, s, x3, paired);
   else if (N <= 2048)
     st = run_blocks<2048, 512>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3, paired);
-  else
+  else if (N <= 4096)
     st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3, paired);
+  else
+    st = run_blocks<8192, 1024>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3, paired);
   if (st != FX_OK) return st;
   hipLaunchKernelGGL(lu_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, piv, nsw, N,
                      nblk, sign, logabs, batch);

@@ -1,11 +1,11 @@
-// Blocked Parlett-Reid with partial pivoting for 128 < n <= 4096 (any batch). The skew
+// Blocked Parlett-Reid with partial pivoting for 128 < n <= 8192 (any batch). The skew
 // matrix lives in one workspace buffer as its strictly lower triangle, in strips of four
 // rows stored column-major (entry (p, q), p > q, at ((p / 4) N + q) 4 + p % 4): an MFMA
 // accumulator's four consecutive rows of one column are one 16-byte store, and a row of
 // the skew matrix is its stored part (columns q < p, 16-byte strided) and the negated
 // column below the diagonal (whole 16-byte strip pieces). Per block of PB columns (PB / 2
 // pair steps; PB = 64 once the trailing order m = N - r0 is at most 1024 for N >= 512 a
-// multiple of 64, else 32; 16 above N = 2048) at r0:
+// multiple of 64, else 32; 16 above N = 2048, 8 above N = 4096) at r0:
 //   1. pf_panel_kernel (one workgroup of NT = 256..1024 threads per matrix, each lane
 //      owning R = 2 or 4 of the m = N - r0 rows): the pair steps with the tau / w vectors
 //      kept in registers as G (m x PB); column a and column p of the current matrix are read
@@ -33,17 +33,21 @@ namespace fx {
 constexpr int PF_UPDATE_TILE = 64;
 constexpr int PFB_L = 64;   // columns per block (32 pair steps) where m <= 1024 (see pf_block_width)
 constexpr int PFB = 32;     // the other blocks of N <= 2048
-constexpr int PFB_XL = 16;  // every block of 2048 < N <= PF_LARGE_MAXN
+constexpr int PFB_XL = 16;  // every block of 2048 < N <= 4096
+constexpr int PFB_XXL = 8;  // every block of 4096 < N <= PF_LARGE_MAXN (R = 8 rows per lane)
 
 // Columns per chunk of the exported factors gbuf (B, N / CW, N, CW) for padded order N:
-// the 32 (16 above N = 2048) columns of a block, or one half of a 64-column block.
-int pf_large_block_cols(int N) { return N > 2048 ? PFB_XL : PFB; }
+// the 32 (16 above N = 2048, 8 above 4096) columns of a block, or one half of a 64-column
+// block.
+int pf_large_block_cols(int N) { return N > 4096 ? PFB_XXL : N > 2048 ? PFB_XL : PFB; }
 
 // Columns of the block at r0: 64 once the trailing order m = N - r0 is at most
 // fx_tune.pf_block64_max_m (1024 in the table, the register limit: G (m x 64) in the
 // registers of 256 / 512 threads; the trailing updates' HBM traffic halves), for N >=
-// fx_tune.pf_block64_min_n (512) a multiple of 64, else 32; 16 above N = 2048.
+// fx_tune.pf_block64_min_n (512) a multiple of 64, else 32; 16 above N = 2048, 8 above
+// N = 4096 (G (m x PB) in the registers of a 1024-thread workgroup).
 static int pf_block_width(int N, int r0) {
+  if (N > 4096) return PFB_XXL;
   if (N > 2048) return PFB_XL;
   const fx_tune& t = tune();
   const int max_m = t.pf_block64_max_m < 1024 ? t.pf_block64_max_m : 1024;
@@ -173,9 +177,12 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
   // the first block reading it in place of a copy), else the strip layout's triangle
   const float* Mm = M + b * (int64_t)N * N;
   // The lane's R consecutive entries M[r0 + q][r0 + R tid + s] (zero beyond m). r0 and m
-  // are multiples of 16, so a lane's rows are one strip piece: the part below the diagonal
-  // (rows > r0 + q) is one 8- or 16-byte load, the part right of it R loads 16 bytes apart.
+  // are multiples of 8, so a lane's rows are whole strip pieces (R <= 4: one, R = 8: two
+  // strips): the part below the diagonal (rows > r0 + q) is one 8- or 16-byte load per
+  // strip, the part right of it R loads 16 bytes apart.
   typedef float vR __attribute__((ext_vector_type(R)));
+  typedef float vS __attribute__((ext_vector_type(R < 4 ? R : 4)));
+  constexpr int SR = R < 4 ? R : 4;  // rows of one strip piece
   auto rowr = [&](int q, float (&v)[R]) {
     const int i0 = R * tid;
     const int gq = r0 + q, gi = r0 + i0;
@@ -187,9 +194,12 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
 #pragma unroll
       for (int s = 0; s < R; ++s) v[s] = y[s];
     } else if (gi > gq) {
-      const vR y = *reinterpret_cast<const vR*>(Mm + l4(gi, gq, N));
 #pragma unroll
-      for (int s = 0; s < R; ++s) v[s] = -y[s];
+      for (int h = 0; h < R / SR; ++h) {
+        const vS y = *reinterpret_cast<const vS*>(Mm + l4(gi + SR * h, gq, N));
+#pragma unroll
+        for (int s = 0; s < SR; ++s) v[SR * h + s] = -y[s];
+      }
     } else if (gi + R <= gq) {
 #pragma unroll
       for (int s = 0; s < R; ++s) v[s] = Mm[l4(gq, gi + s, N)];
@@ -657,7 +667,8 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     const int PB = pf_block_width(N, r0);
     const int st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
                    : PB == PFB ? pf_block<PFB, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
-                               : pf_block<PFB_XL, 4>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
+                   : PB == PFB_XL ? pf_block<PFB_XL, 4>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                                  : pf_block<PFB_XXL, 8>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
     if (st != FX_OK) return st;
     r0 += PB;
   }

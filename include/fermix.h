@@ -30,7 +30,7 @@
  *  - the kernel family is chosen from n alone (never from the batch): several matrices
  *    per wave (n <= 32 for slogdet, 16 for slogpf), one fused workgroup per matrix
  *    (n <= fx_tune.fused_max_n, 128 in the gfx950 table), blocked kernels with workspace
- *    (n <= 4096); the blocked kernels' own choices follow the tuning table below, whose
+ *    (n <= 8192 for float32); the blocked kernels' own choices follow the tuning table below, whose
  *    fx_tune_override is the reference's OVERRIDE hook. The environment variable
  *    FERMIX_AMD_KERNELS = tiny | fused | blocked, read on every call, forces a family
  *    where it covers n (FX_ERR_UNSUPPORTED elsewhere); the padded orders, block widths
@@ -110,7 +110,7 @@ typedef struct fx_tune {
   int32_t lu_direct_max_n;
   /* blocked Parlett-Reid (N <= 2048): 64-column blocks once the trailing order is at most
    * pf_block64_max_m, for padded orders N >= pf_block64_min_n that are multiples of 64;
-   * 32-column blocks otherwise (16 above N = 2048). 128 .. 4096 / 0 .. 1024 */
+   * 32-column blocks otherwise (16 above N = 2048, 8 above N = 4096). 128 .. 4096 / 0 .. 1024 */
   int32_t pf_block64_min_n;
   int32_t pf_block64_max_m;
   /* GEMMs of the inverses and adjugates in FX_PREC_IEEE: 128 x 128 tiles when M, N >=
@@ -163,8 +163,11 @@ int32_t fx_pf_padded_size(int32_t n);
 
 /* ---------------------------------------------------------------- slogdet
  * sign[b], logabs[b] of det(a[b]) for b < batch: sign exactly +1 / -1, or 0 with
- * logabs = -inf for an exactly zero pivot. Sizes: every entry point of this header
- * covers 0 <= n <= 4096 and returns FX_ERR_UNSUPPORTED above.
+ * logabs = -inf for an exactly zero pivot. Sizes: every float32 entry point of this
+ * header covers 0 <= n <= 8192 (the float64 and complex ones 0 <= n <= 4096) and returns
+ * FX_ERR_UNSUPPORTED above. Above n = 4096 the LU panels spill registers and the
+ * Parlett-Reid blocks are 8 columns wide (latency-bound; the trailing updates and GEMMs
+ * are those of the smaller orders).
  * Replaces `_lu_core` (src/fermix/_lu.py:543-611) as called by `_slogdet_core`
  * (src/fermix/_diff.py:42-49); kernels K1-K4 of the reference (_lu.py:54-393). */
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n);

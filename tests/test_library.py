@@ -50,7 +50,8 @@ def test_host_only_calls():
     assert L.fx_slogdet_f32(None, 0, 4, None, None, 0, None, 0, None) == 0
     assert L.fx_det_parts_f32(None, -1, 4, None, None, None, 0, None, 0, None) == 1
     assert L.fx_det_parts_f32(None, 2, 4, None, None, None, 0, None, 0, None) == 1
-    assert L.fx_det_parts_f32_workspace(4, 5000) == 0 and L.fx_det_parts_f32_workspace(4, 4096) > 0
+    assert L.fx_det_parts_f32_workspace(4, 8193) == 0 and L.fx_det_parts_f32_workspace(4, 8192) > 0
+    assert L.fx_slogpf_parts_f32_workspace(1, 8192) > 0 and L.fx_slogpf_parts_f32_workspace(1, 8194) == 0
     assert L.fx_det_parts_f32_workspace(4, 64) > L.fx_slogdet_parts_f32_workspace(4, 64)
 
 
@@ -122,7 +123,7 @@ def test_tune_table():
         _tune.check_prec("fp16")
     assert _tune.kernel_family(128) == "fused-lds"
     assert _tune.kernel_family(32) == "tiny-wave" and _tune.kernel_family(32, "slogpf") == "fused-lds"
-    assert _tune.kernel_family(4096, "slogpf") == "blocked" and _tune.kernel_family(4097) == "unsupported"
+    assert _tune.kernel_family(8192, "slogpf") == "blocked" and _tune.kernel_family(8193) == "unsupported"
 
 
 def test_misaligned_pointers_rejected():
