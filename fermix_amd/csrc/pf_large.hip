@@ -453,14 +453,15 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
     smv[tid - T] = mv;
   }
   __syncthreads();
-  // wave (wr, wc) owns an H x H quarter as AW x AW 32x32 accumulators, seeded with the
-  // old entries M[src p][src q]; rows / columns beyond N and the upper half of a
-  // diagonal tile are seeded with zeros and never stored (MFMA output elements are
-  // independent)
+  // wave (wr, wc) owns an H x H quarter: the old entries M[src p][src q] (zeros for rows
+  // / columns beyond N and the upper half of a diagonal tile, which are never stored),
+  // loaded first, and G J G^T in AW x AW 32x32 accumulators of its own, added in fp32:
+  // the MFMAs truncate what they add below about three bits under the accumulator's
+  // last place, so small products added to the old entries one by one would lose more
   const bool diag = I == J;
   const int wr = (wave >> 1) * H, wc = (wave & 1) * H;
   const int l32 = lane & 31, lh = lane >> 5;
-  v16f acc[AW][AW];
+  v16f acc[AW][AW], prod[AW][AW];
 #pragma unroll
   for (int a = 0; a < AW; ++a)
 #pragma unroll
@@ -497,6 +498,12 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
       }
     }
 #pragma unroll
+  for (int a = 0; a < AW; ++a)
+#pragma unroll
+    for (int c = 0; c < AW; ++c)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) prod[a][c][v] = 0.0f;
+#pragma unroll
   for (int kp = 0; kp < PB / 2; ++kp) {
     float av[AW], bv[AW];
 #pragma unroll
@@ -507,8 +514,14 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
     for (int a = 0; a < AW; ++a)
 #pragma unroll
       for (int c = 0; c < AW; ++c)
-        acc[a][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[c], acc[a][c], 0, 0, 0);
+        prod[a][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[c], prod[a][c], 0, 0, 0);
   }
+#pragma unroll
+  for (int a = 0; a < AW; ++a)
+#pragma unroll
+    for (int c = 0; c < AW; ++c)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][c][v] += prod[a][c][v];
   // the lower entries: whole strips off the diagonal tiles (N is a multiple of 4, so a
   // strip is inside the matrix or outside it), entry by entry below the diagonal of a
   // diagonal tile
