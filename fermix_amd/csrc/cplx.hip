@@ -737,6 +737,31 @@ int det_parts(const void* a, int64_t batch, int n, void* sign, void* logabs, voi
   return launch_cgj<F>(a, n, 0, batch, sign, logabs, adj_t, GJ_ADJ, 1, nullptr, ws, wsb, s);
 }
 
+// float64 above the register kernels' orders: sign / logabs from the blocked LU (the
+// forward's bits), the adjugate from the Gauss-Jordan run, its own values in scratch.
+size_t det_parts_f64_ws(int64_t batch, int n) {
+  if (n > CX_MAXN || batch <= 0) return 0;
+  if (n <= tune().f64_reg_max_n) return slogdet_parts_ws<double>(batch, n);
+  return align_up(lu64_workspace(batch, n)) + align_up(slogdet_parts_ws<double>(batch, n)) +
+         align_up((size_t)batch * 2 * sizeof(double));
+}
+
+int det_parts_f64(const double* a, int64_t batch, int n, double* sign, double* logabs, double* adj_t, void* ws,
+                  size_t wsb, hipStream_t s) {
+  if (n <= tune().f64_reg_max_n) return det_parts<double>(a, batch, n, sign, logabs, adj_t, ws, wsb, s);
+  const int st = check_cx_args<double>(a, batch, n, sign, logabs, adj_t, ws);
+  if (st != FX_OK || batch == 0) return st;
+  if (!adj_t) return FX_ERR_INVALID_ARGUMENT;
+  const size_t need = det_parts_f64_ws(batch, n);
+  if (!ws || wsb < need) return FX_ERR_WORKSPACE;
+  const size_t lw = align_up(lu64_workspace(batch, n)), gw = align_up(slogdet_parts_ws<double>(batch, n));
+  char* base = (char*)ws;
+  const int r = launch_lu64(a, n, batch, sign, logabs, base, lw, s);
+  if (r != FX_OK) return r;
+  double* gsign = (double*)(base + lw + gw);
+  return launch_cgj<double>(a, n, 0, batch, gsign, gsign + batch, adj_t, GJ_ADJ, 1, nullptr, base + lw, gw, s);
+}
+
 template <class T>
 size_t slogpf_ws(int64_t batch, int n) {
   return n > CX_MAXN ? 0 : cx_matrix_ws<cx<T>>(batch, n, n);
@@ -904,7 +929,7 @@ int fx_slogpf_parts_c128(const double* a, int64_t batch, int32_t n, int32_t skew
 
 size_t fx_det_parts_c64_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<float>>(batch, n); }
 size_t fx_det_parts_c128_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<double>>(batch, n); }
-size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<double>(batch, n); }
+size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n) { return det_parts_f64_ws(batch, n); }
 
 int fx_det_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
                      void* workspace, size_t workspace_bytes, fx_stream_t stream) {
@@ -916,7 +941,7 @@ int fx_det_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, d
 }
 int fx_det_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
                      void* workspace, size_t workspace_bytes, fx_stream_t stream) {
-  return det_parts<double>(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, (hipStream_t)stream);
+  return det_parts_f64(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 }  // extern "C"

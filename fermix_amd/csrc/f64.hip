@@ -569,20 +569,30 @@ using namespace fx;
 extern "C" {
 
 
+// Above the register kernels the values come from the blocked LU (lu64.hip); the
+// gradient's A^-T from the Gauss-Jordan kernel, whose own sign / logabs go to scratch, so
+// that a gradient call returns the forward's bits.
+static bool lu64_path(int n) { return n > tune().f64_reg_max_n; }
+
 size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n) {
-  return n > F64_MAXN ? 0 : gj64_ws(batch, n, false);
+  if (n > F64_MAXN) return 0;
+  return lu64_path(n) ? lu64_workspace(batch, n) : gj64_ws(batch, n, false);
 }
 
 int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream) {
   const int st = check_f64_args(a, batch, n, sign, logabs, nullptr, workspace);
   if (st != FX_OK || batch == 0) return st;
+  if (lu64_path(n)) return launch_lu64(a, n, batch, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
   return launch_gj64(a, n, 0, batch, sign, logabs, nullptr, 0, nullptr, workspace, workspace_bytes,
                      (hipStream_t)stream);
 }
 
 size_t fx_slogdet_parts_f64_workspace(int64_t batch, int32_t n) {
-  return n > F64_MAXN ? 0 : gj64_ws(batch, n, true);
+  if (n > F64_MAXN) return 0;
+  if (!lu64_path(n)) return gj64_ws(batch, n, true);
+  return align_up_256(lu64_workspace(batch, n)) + align_up_256(gj64_ws(batch, n, true)) +
+         align_up_256((size_t)batch * 2 * sizeof(double));
 }
 
 int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
@@ -590,8 +600,17 @@ int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign
   const int st = check_f64_args(a, batch, n, sign, logabs, inv_t, workspace);
   if (st != FX_OK || batch == 0) return st;
   if (!inv_t) return fx_slogdet_f64(a, batch, n, sign, logabs, workspace, workspace_bytes, stream);
-  return launch_gj64(a, n, 0, batch, sign, logabs, inv_t, 1, nullptr, workspace, workspace_bytes,
-                     (hipStream_t)stream);
+  hipStream_t s = (hipStream_t)stream;
+  if (!lu64_path(n))
+    return launch_gj64(a, n, 0, batch, sign, logabs, inv_t, 1, nullptr, workspace, workspace_bytes, s);
+  const size_t need = fx_slogdet_parts_f64_workspace(batch, n);
+  if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
+  const size_t lw = align_up_256(lu64_workspace(batch, n)), gw = align_up_256(gj64_ws(batch, n, true));
+  char* base = (char*)workspace;
+  int r = launch_lu64(a, n, batch, sign, logabs, base, lw, s);
+  if (r != FX_OK) return r;
+  double* gsign = (double*)(base + lw + gw);
+  return launch_gj64(a, n, 0, batch, gsign, gsign + batch, inv_t, 1, nullptr, base + lw, gw, s);
 }
 
 size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n) {

@@ -140,6 +140,11 @@ struct GemmDesc {
 // C = alpha op(A) op(B) + beta C for every (batch, second-batch) index.
 int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s);
 
+// float64 blocked LU (sign, logabs) for the orders above the register kernels (lu64.hip)
+size_t lu64_workspace(int64_t batch, int n);
+int launch_lu64(const double* A, int n, int64_t batch, double* sign, double* logabs, void* ws, size_t ws_bytes,
+                hipStream_t s);
+
 // float64 Pfaffian adjugate pf(S) S^-1 (cplx.hip; zero for odd n)
 size_t pf_adjugate_f64_ws(int64_t batch, int n);
 int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, void* ws, size_t wsb,

@@ -33,11 +33,11 @@ def _skew(A):
 
 
 # n spans the register-resident kernels (n <= 128: 16-column strips up to n = 64, 32-column
-# strips from n = 65, no workspace) and the workspace kernels on 256 and 1024 threads
-# (n > 128)
-@pytest.mark.parametrize("n", [0, 1, 2, 3, 5, 16, 31, 61, 62, 64, 65, 87, 88, 128, 129, 200, 300])
+# strips from n = 65, no workspace) and, above, the blocked LU for the values (32-column
+# panels, padded orders 160 .. 1024) with the Gauss-Jordan workspace kernel for A^-T
+@pytest.mark.parametrize("n", [0, 1, 2, 3, 5, 16, 31, 61, 62, 64, 65, 87, 88, 128, 129, 200, 300, 520, 1024])
 def test_f64_slogdet_and_inverse(dev, n):
-    B = 8 if n <= 128 else 3
+    B = 8 if n <= 128 else (3 if n <= 300 else 2)
     rng = np.random.default_rng(7000 + n)
     A = rng.standard_normal((B, n, n)) / np.sqrt(max(n, 1))
     print(f"f64 slogdet n={n} B={B}", flush=True)
@@ -111,7 +111,7 @@ def test_f64_closed_forms(dev):
     assert np.allclose(_np(l), np.log(np.abs(a)).sum(axis=1), rtol=1e-14, atol=1e-13)
 
 
-@pytest.mark.parametrize("n", [12, 70, 150])
+@pytest.mark.parametrize("n", [12, 70, 150, 300])
 def test_f64_singular_and_odd(dev, n):
     rng = np.random.default_rng(7300 + n)
     A = rng.standard_normal((4, n, n))
