@@ -254,6 +254,9 @@ __global__ __launch_bounds__(CX_NT) void cgj_kernel(const F* __restrict__ a, int
       M[(size_t)r * ld + n + k] = (r == k) ? D::one() : D::zero();
     }
   } else {
+    // GJ_ADJ with a gate: only the members whose gate value is 0 (exactly singular ones,
+    // the others' adjugate formed by the caller)
+    if (MODE == GJ_ADJ && gate && !Fd<F>::is0(gate[b])) return;
     cload<F>(a + (size_t)b * n * n, n, skew, M, ld, RIGHT);
   }
   for (int r = threadIdx.x; r < n; r += CX_NT) asg[r] = 0;
@@ -648,7 +651,8 @@ int launch_cgj(const void* a, int n, int skew, int64_t batch, void* sign, void* 
   if (mode == GJ_INV)
     cgj_kernel<F, GJ_INV><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, (F*)out, out_t, (const F*)gate, nullptr, PfaLayout{}, 0);
   else if (mode == GJ_ADJ)
-    cgj_kernel<F, GJ_ADJ><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, (F*)out, 1, nullptr, nullptr, PfaLayout{}, 0);
+    cgj_kernel<F, GJ_ADJ><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, (F*)out, 1, (const F*)gate, nullptr,
+                                                   PfaLayout{}, 0);
   else
     cgj_kernel<F, GJ_FWD><<<grid, CX_NT, shm, s>>>(A, n, skew, W, lds, sg, lg, nullptr, 0, nullptr, nullptr,
                                                   PfaLayout{}, 0);
@@ -737,12 +741,13 @@ int det_parts(const void* a, int64_t batch, int n, void* sign, void* logabs, voi
   return launch_cgj<F>(a, n, 0, batch, sign, logabs, adj_t, GJ_ADJ, 1, nullptr, ws, wsb, s);
 }
 
-// float64 above the register kernels' orders: sign / logabs from the blocked LU (the
-// forward's bits), the adjugate from the Gauss-Jordan run, its own values in scratch.
+// float64 above the register kernels' orders: sign / logabs (the forward's bits) and the
+// regular members' adjugate det(A) A^-T from the blocked LU and its solves, the exactly
+// singular members' from a Gauss-Jordan run gated to them (its values in scratch).
 size_t det_parts_f64_ws(int64_t batch, int n) {
   if (n > CX_MAXN || batch <= 0) return 0;
   if (n <= tune().f64_reg_max_n) return slogdet_parts_ws<double>(batch, n);
-  return align_up(lu64_workspace(batch, n)) + align_up(slogdet_parts_ws<double>(batch, n)) +
+  return align_up(lu64_inverse_workspace(batch, n)) + align_up(slogdet_parts_ws<double>(batch, n)) +
          align_up((size_t)batch * 2 * sizeof(double));
 }
 
@@ -754,12 +759,12 @@ int det_parts_f64(const double* a, int64_t batch, int n, double* sign, double* l
   if (!adj_t) return FX_ERR_INVALID_ARGUMENT;
   const size_t need = det_parts_f64_ws(batch, n);
   if (!ws || wsb < need) return FX_ERR_WORKSPACE;
-  const size_t lw = align_up(lu64_workspace(batch, n)), gw = align_up(slogdet_parts_ws<double>(batch, n));
+  const size_t lw = align_up(lu64_inverse_workspace(batch, n)), gw = align_up(slogdet_parts_ws<double>(batch, n));
   char* base = (char*)ws;
-  const int r = launch_lu64(a, n, batch, sign, logabs, base, lw, s);
+  const int r = launch_lu64_inverse(a, n, 0, batch, sign, logabs, nullptr, 1, adj_t, 1, base, lw, s);
   if (r != FX_OK) return r;
   double* gsign = (double*)(base + lw + gw);
-  return launch_cgj<double>(a, n, 0, batch, gsign, gsign + batch, adj_t, GJ_ADJ, 1, nullptr, base + lw, gw, s);
+  return launch_cgj<double>(a, n, 0, batch, gsign, gsign + batch, adj_t, GJ_ADJ, 1, sign, base + lw, gw, s);
 }
 
 template <class T>

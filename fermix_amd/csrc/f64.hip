@@ -569,9 +569,9 @@ using namespace fx;
 extern "C" {
 
 
-// Above the register kernels the values come from the blocked LU (lu64.hip); the
-// gradient's A^-T from the Gauss-Jordan kernel, whose own sign / logabs go to scratch, so
-// that a gradient call returns the forward's bits.
+// Above the register kernels the values come from the blocked LU (lu64.hip) and the
+// gradient's A^-T from the blocked solves of the same factorisation, so that a gradient
+// call returns the forward's bits.
 static bool lu64_path(int n) { return n > tune().f64_reg_max_n; }
 
 size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n) {
@@ -590,9 +590,7 @@ int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, doub
 
 size_t fx_slogdet_parts_f64_workspace(int64_t batch, int32_t n) {
   if (n > F64_MAXN) return 0;
-  if (!lu64_path(n)) return gj64_ws(batch, n, true);
-  return align_up_256(lu64_workspace(batch, n)) + align_up_256(gj64_ws(batch, n, true)) +
-         align_up_256((size_t)batch * 2 * sizeof(double));
+  return lu64_path(n) ? lu64_inverse_workspace(batch, n) : gj64_ws(batch, n, true);
 }
 
 int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
@@ -603,14 +601,7 @@ int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign
   hipStream_t s = (hipStream_t)stream;
   if (!lu64_path(n))
     return launch_gj64(a, n, 0, batch, sign, logabs, inv_t, 1, nullptr, workspace, workspace_bytes, s);
-  const size_t need = fx_slogdet_parts_f64_workspace(batch, n);
-  if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
-  const size_t lw = align_up_256(lu64_workspace(batch, n)), gw = align_up_256(gj64_ws(batch, n, true));
-  char* base = (char*)workspace;
-  int r = launch_lu64(a, n, batch, sign, logabs, base, lw, s);
-  if (r != FX_OK) return r;
-  double* gsign = (double*)(base + lw + gw);
-  return launch_gj64(a, n, 0, batch, gsign, gsign + batch, inv_t, 1, nullptr, base + lw, gw, s);
+  return launch_lu64_inverse(a, n, 0, batch, sign, logabs, nullptr, 0, inv_t, 1, workspace, workspace_bytes, s);
 }
 
 size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n) {
@@ -627,8 +618,9 @@ int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmet
 
 size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n) {
   if (n > F64_MAXN || batch <= 0) return 0;
-  const size_t pr = fx_slogpf_f64_workspace(batch, n), gj = gj64_ws(batch, n, true);
-  const size_t inv = align_up_256(gj) + align_up_256((size_t)batch * 2 * sizeof(double));
+  const size_t pr = fx_slogpf_f64_workspace(batch, n);
+  const size_t inv = (lu64_path(n) ? align_up_256(lu64_inverse_workspace(batch, n)) : align_up_256(gj64_ws(batch, n, true))) +
+                     align_up_256((size_t)batch * 2 * sizeof(double));
   return align_up_256(pr) + std::max(inv, pf_adjugate_f64_ws(batch, n));
 }
 
@@ -649,8 +641,14 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
   // the Pfaffian adjugate from its own Parlett-Reid run (cplx.hip)
   if (adjugate)
     return pf_adjugate_f64(a, batch, n, skew_symmetrize != 0, g, base + pr, workspace_bytes - pr, s);
-  // S^-1 by Gauss-Jordan on the same S, zeroed where the Parlett-Reid run found pf = 0
-  // (every member for odd n)
+  // S^-1 by Gauss-Jordan (register kernels' orders) or the blocked LU solves on the same S,
+  // zeroed where the Parlett-Reid run found pf = 0 (every member for odd n)
+  if (lu64_path(n)) {
+    const size_t lw = align_up_256(lu64_inverse_workspace(batch, n));
+    double* gsign = (double*)(base + pr + lw);
+    return launch_lu64_inverse(a, n, skew_symmetrize != 0, batch, gsign, gsign + batch, sign, 0, g, 0, base + pr, lw,
+                               s);
+  }
   double* gsign = (double*)(base + pr + gj);
   double* glog = gsign + batch;
   return launch_gj64(a, n, skew_symmetrize != 0, batch, gsign, glog, g, 0, sign, base + pr, gj, s);

@@ -144,6 +144,13 @@ int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s);
 size_t lu64_workspace(int64_t batch, int n);
 int launch_lu64(const double* A, int n, int64_t batch, double* sign, double* logabs, void* ws, size_t ws_bytes,
                 hipStream_t s);
+// ... and the inverse from the same factorisation (A skew-symmetrised when skew): out =
+// A^-T (out_t) or A^-1, times det A when det, zero where gate (default: the factorisation's
+// own sign) is 0 or the result is not finite; sign / logabs those of the factorisation.
+size_t lu64_inverse_workspace(int64_t batch, int n);
+int launch_lu64_inverse(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs,
+                        const double* gate, int det, double* out, int out_t, void* ws, size_t ws_bytes,
+                        hipStream_t s);
 
 // float64 Pfaffian adjugate pf(S) S^-1 (cplx.hip; zero for odd n)
 size_t pf_adjugate_f64_ws(int64_t batch, int n);

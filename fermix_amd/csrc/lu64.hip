@@ -7,14 +7,15 @@
 //      column step at a time -- the pivot is the row of largest |x| among rows >= c
 //      (lowest row on ties), swapped into row c over the panel's columns, then the
 //      multipliers and the rank-1 update of the panel's remaining columns;
-//   2. lu64_urow_kernel (matrix x 256 trailing columns): the panel's row swaps on the
+//   2. lu64_rows_kernel<0> (matrix x 256 trailing columns): the panel's row swaps on the
 //      trailing columns and U12 = L11^-1 A12 by forward substitution (L11 in LDS);
-//   3. lu64_update_kernel (matrix x 64 x 64 tile): A22 -= L21 U12 at K = 32, the products
+//   3. lu64_gemm_kernel (matrix x 64 x 64 tile): A22 -= L21 U12 at K = 32, the products
 //      in an accumulator of their own, subtracted from A22 in fp64 at the end;
 //   4. lu64_finish_kernel: sign = (-1)^swaps * prod sign(d), logabs = sum log|d| in
 //      pivot order (one wave, lane-strided partial sums and a fixed tree).
 // The column steps of a panel are latency-bound (three workgroup barriers each); the
-// work that grows as n^3 runs on the MFMA in many workgroups per matrix.
+// work that grows as n^3 runs on the MFMA in many workgroups per matrix. The inverse
+// (launch_lu64_inverse: A^-T, S^-1, det A^-T) solves with the same row and GEMM kernels.
 #include <algorithm>
 
 #include "common.h"
@@ -30,15 +31,19 @@ typedef double v4d __attribute__((ext_vector_type(4)));
 
 int lu64_padded(int n) { return (n + P64 - 1) / P64 * P64; }
 
-// W (B, N, N) = A (B, n, n) with identity padding; a grid-stride loop over B N N elements.
-__global__ void lu64_copy_kernel(const double* __restrict__ A, int n, double* __restrict__ W, int N,
+// W (B, N, N) = A (B, n, n) with identity padding (skew: (A - A^T) / 2); a grid-stride
+// loop over B N N elements.
+__global__ void lu64_copy_kernel(const double* __restrict__ A, int n, int skew, double* __restrict__ W, int N,
                                  int64_t total) {
   const int64_t NN = (int64_t)N * N;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t b = e / NN;
     const int64_t f = e - b * NN;
     const int r = (int)(f / N), c = (int)(f - (int64_t)r * N);
-    W[e] = (r < n && c < n) ? A[b * (int64_t)n * n + (int64_t)r * n + c] : (r == c ? 1.0 : 0.0);
+    const double* Ab = A + b * (int64_t)n * n;
+    double v = r == c ? 1.0 : 0.0;
+    if (r < n && c < n) v = skew ? (Ab[(int64_t)r * n + c] - Ab[(int64_t)c * n + r]) * 0.5 : Ab[(int64_t)r * n + c];
+    W[e] = v;
   }
 }
 
@@ -90,83 +95,104 @@ __global__ __launch_bounds__(NT64) void lu64_panel_kernel(double* __restrict__ W
   if (tid == 0) nsw[b * (N / P64) + r0 / P64] = swaps;
 }
 
-// Trailing columns r0 + 32 + 256 cb + tid: the panel's swaps, then U12 = L11^-1 A12.
-__global__ __launch_bounds__(NT64) void lu64_urow_kernel(double* __restrict__ W, int N, int r0,
-                                                         const int* __restrict__ ipiv, int ncb) {
-  __shared__ double L11[P64][P64 + 1];
+// 32 rows r0 .. r0 + 31 of a target matrix T, columns c0 + 256 cb + tid (< cend), against
+// the diagonal block D = W[r0 .. r0 + 31][r0 .. r0 + 31] of the factorisation:
+//   MODE 0 / 1: the panel's row swaps (row r0 + j with ipiv[r0 + j] >= r0 + j, in order),
+//     then the forward substitution with the unit lower part of D (MODE 0: T = W, the
+//     U rows of the trailing columns; MODE 1: T = Y, the forward solve of L Y = P I);
+//   MODE 2: the backward substitution with the upper part of D (the solve U X = Y).
+template <int MODE>
+__global__ __launch_bounds__(NT64) void lu64_rows_kernel(const double* __restrict__ W, double* __restrict__ T,
+                                                         int N, int r0, const int* __restrict__ ipiv, int c0,
+                                                         int cend, int ncb) {
+  __shared__ double D[P64][P64 + 1];
   const int64_t b = blockIdx.x / ncb;
   const int cb = (int)(blockIdx.x - b * ncb);
-  double* Wb = W + b * (int64_t)N * N;
+  const double* Wb = W + b * (int64_t)N * N;
+  double* Tb = T + b * (int64_t)N * N;
   const int tid = threadIdx.x;
   for (int e = tid; e < P64 * P64; e += NT64) {
     const int i = e / P64, k = e % P64;
-    L11[i][k] = Wb[(int64_t)(r0 + i) * N + r0 + k];
+    D[i][k] = Wb[(int64_t)(r0 + i) * N + r0 + k];
   }
   __syncthreads();
-  const int col = r0 + P64 + NT64 * cb + tid;
-  if (col >= N) return;
-  const int* ip = ipiv + b * N + r0;
+  const int col = c0 + NT64 * cb + tid;
+  if (col >= cend) return;
   double x[P64];
 #pragma unroll
-  for (int i = 0; i < P64; ++i) x[i] = Wb[(int64_t)(r0 + i) * N + col];
-  // swaps in column order: row r0 + j with row ip[j] (>= r0 + j); rows beyond the panel
-  // rows exchange with the column's entries below
+  for (int i = 0; i < P64; ++i) x[i] = Tb[(int64_t)(r0 + i) * N + col];
+  if constexpr (MODE != 2) {
+    const int* ip = ipiv + b * N + r0;
+    // rows beyond the block rows exchange with the column's entries below
 #pragma unroll
-  for (int j = 0; j < P64; ++j) {
-    const int p = ip[j];
-    if (p != r0 + j) {
-      if (p < r0 + P64) {
-        // both rows inside the panel rows: exchange x[j] and x[p - r0]
-        double t = x[j];
+    for (int j = 0; j < P64; ++j) {
+      const int p = ip[j];
+      if (p != r0 + j) {
+        if (p < r0 + P64) {
+          double t = x[j];
 #pragma unroll
-        for (int i = j + 1; i < P64; ++i)
-          if (p - r0 == i) {
-            const double u = x[i];
-            x[i] = t;
-            t = u;
-          }
-        x[j] = t;
-      } else {
-        double* e = Wb + (int64_t)p * N + col;
-        const double u = *e;
-        *e = x[j];
-        x[j] = u;
+          for (int i = j + 1; i < P64; ++i)
+            if (p - r0 == i) {
+              const double u = x[i];
+              x[i] = t;
+              t = u;
+            }
+          x[j] = t;
+        } else {
+          double* e = Tb + (int64_t)p * N + col;
+          const double u = *e;
+          *e = x[j];
+          x[j] = u;
+        }
       }
     }
+#pragma unroll
+    for (int i = 1; i < P64; ++i) {
+      double v = x[i];
+#pragma unroll
+      for (int k = 0; k < i; ++k) v = fma(-D[i][k], x[k], v);
+      x[i] = v;
+    }
+  } else {
+#pragma unroll
+    for (int i = P64 - 1; i >= 0; --i) {
+      double v = x[i];
+#pragma unroll
+      for (int k = i + 1; k < P64; ++k) v = fma(-D[i][k], x[k], v);
+      x[i] = v / D[i][i];
+    }
   }
-  // forward substitution with the unit lower L11
 #pragma unroll
-  for (int i = 1; i < P64; ++i) {
-    double v = x[i];
-#pragma unroll
-    for (int k = 0; k < i; ++k) v = fma(-L11[i][k], x[k], v);
-    x[i] = v;
-  }
-#pragma unroll
-  for (int i = 0; i < P64; ++i) Wb[(int64_t)(r0 + i) * N + col] = x[i];
+  for (int i = 0; i < P64; ++i) Tb[(int64_t)(r0 + i) * N + col] = x[i];
 }
 
-// A22 -= L21 U12 over the trailing rows / columns >= r1 = r0 + 32, one 64 x 64 tile per
-// workgroup (tiles t = tile row * ntl + tile column), four waves of 32 x 32, each as
-// 2 x 2 16 x 16 fp64 MFMA accumulators over K = 32 (eight K = 4 steps). Lane l supplies
-// A[l % 16][l / 16] and B[l / 16][l % 16]; accumulator element v of lane l is row
-// l / 16 + 4 v, column l % 16 (measured with a one-wave probe: unlike the fp32 16x16x4
-// layout, the four rows of a lane are 4 apart).
-__global__ __launch_bounds__(256) void lu64_update_kernel(double* __restrict__ W, int N, int r0, int ntl) {
-  __shared__ double As[64][P64 + 1];  // L21 tile rows
-  __shared__ double Bs[P64][64 + 1];  // U12 tile columns
-  const int nt = ntl * ntl;
+// C -= A B with K = 32: A = rows 0 .. M - 1 of a 32-column block, B = its 32 rows of
+// columns 0 .. NC - 1, C = M x NC (every operand given at its first element in matrix 0;
+// row stride ld, matrix stride NN). One 64 x 64 tile per workgroup (tiles t = tile row *
+// ntc + tile column), four waves of 32 x 32, each as 2 x 2 16 x 16 fp64 MFMA
+// accumulators over eight K = 4 steps; the products in accumulators of their own,
+// subtracted from C in fp64 at the end. Lane l supplies A[l % 16][l / 16] and
+// B[l / 16][l % 16]; accumulator element v of lane l is row l / 16 + 4 v, column l % 16
+// (measured with a one-wave probe: unlike the fp32 16x16x4 layout, a lane's four rows
+// are 4 apart). Serves the trailing update A22 -= L21 U12 and both solves' updates.
+__global__ __launch_bounds__(256) void lu64_gemm_kernel(const double* __restrict__ A, const double* __restrict__ Bm,
+                                                        double* __restrict__ C, int ld, int64_t NN, int M, int NC,
+                                                        int ntr, int ntc) {
+  __shared__ double As[64][P64 + 1];
+  __shared__ double Bs[P64][64 + 1];
+  const int nt = ntr * ntc;
   const int64_t b = blockIdx.x / nt;
   const int t = (int)(blockIdx.x - b * nt);
-  const int r1 = r0 + P64;
-  const int i0 = r1 + 64 * (t / ntl), j0 = r1 + 64 * (t % ntl);
-  double* Wb = W + b * (int64_t)N * N;
+  const int i0 = 64 * (t / ntc), j0 = 64 * (t % ntc);
+  const double* Ab = A + b * NN;
+  const double* Bb = Bm + b * NN;
+  double* Cb = C + b * NN;
   const int tid = threadIdx.x;
   for (int e = tid; e < 64 * P64; e += 256) {
     const int i = e / P64, k = e % P64;
-    As[i][k] = i0 + i < N ? Wb[(int64_t)(i0 + i) * N + r0 + k] : 0.0;
+    As[i][k] = i0 + i < M ? Ab[(int64_t)(i0 + i) * ld + k] : 0.0;
     const int kk = e / 64, j = e % 64;
-    Bs[kk][j] = j0 + j < N ? Wb[(int64_t)(r0 + kk) * N + j0 + j] : 0.0;
+    Bs[kk][j] = j0 + j < NC ? Bb[(int64_t)kk * ld + j0 + j] : 0.0;
   }
   __syncthreads();
   const int wave = tid >> 6, lane = tid & 63;
@@ -199,8 +225,8 @@ __global__ __launch_bounds__(256) void lu64_update_kernel(double* __restrict__ W
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = i0 + wm + 16 * a + lk + 4 * v;
-        if (row < N && col < N) {
-          double* e = Wb + (int64_t)row * N + col;
+        if (row < M && col < NC) {
+          double* e = Cb + (int64_t)row * ld + col;
           *e = *e - acc[a][c][v];
         }
       }
@@ -237,6 +263,105 @@ __global__ void lu64_finish_kernel(const double* __restrict__ dpiv, const int* _
   }
 }
 
+// out[b][i][j] (i, j < n) = scale_b X[j][i] (out_t) or scale_b X[i][j], X the solve's
+// N x N result; zero where gate[b] == 0 (the member's own sign, or a caller's gate); any
+// non-finite value of a member raises flag[b] (every writer stores 1).
+__global__ void lu64_out_kernel(const double* __restrict__ X, int N, int n, int out_t,
+                                const double* __restrict__ gate, const double* __restrict__ ssign,
+                                const double* __restrict__ slog, double* __restrict__ out, int* __restrict__ flag,
+                                int64_t total) {
+  const int64_t nn = (int64_t)n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = e / nn;
+    const int64_t f = e - b * nn;
+    const int i = (int)(f / n), j = (int)(f - (int64_t)i * n);
+    double v = 0.0;
+    if (gate[b] != 0.0) {
+      v = X[b * (int64_t)N * N + (out_t ? (int64_t)j * N + i : (int64_t)i * N + j)];
+      if (ssign) v *= ssign[b] * exp(slog[b]);
+      if (!isfinite(v)) flag[b] = 1;
+    }
+    out[e] = v;
+  }
+}
+
+__global__ void lu64_zero_kernel(double* __restrict__ out, int n, const int* __restrict__ flag, int64_t total) {
+  const int64_t nn = (int64_t)n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x)
+    if (flag[e / nn]) out[e] = 0.0;
+}
+
+__global__ void lu64_fill_kernel(double* __restrict__ Y, int N, int* __restrict__ flag, int64_t batch,
+                                 int64_t total) {
+  const int64_t NN = (int64_t)N * N;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t f = e % NN;
+    Y[e] = (f / N == f % N) ? 1.0 : 0.0;
+    if (f == 0) flag[e / NN] = 0;
+  }
+}
+
+unsigned grid_of(int64_t total) { return (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 20); }
+
+struct Lu64Bufs {
+  double* W;
+  int* ipiv;
+  double* dpiv;
+  int* nsw;
+};
+
+Lu64Bufs lu64_take(char*& p, int64_t batch, int N) {
+  auto take = [&](size_t x) {
+    char* q = p;
+    p += (x + 255) / 256 * 256;
+    return (void*)q;
+  };
+  Lu64Bufs f;
+  f.W = (double*)take((size_t)batch * N * N * 8);
+  f.ipiv = (int*)take((size_t)batch * N * 4);
+  f.dpiv = (double*)take((size_t)batch * N * 8);
+  f.nsw = (int*)take((size_t)batch * (N / P64) * 4);
+  return f;
+}
+
+// C -= A B (K = 32) over M x NC, operands at their first elements of matrix 0
+int lu64_gemm(const double* A, const double* Bm, double* C, int N, int M, int NC, int64_t batch, hipStream_t s) {
+  if (M <= 0 || NC <= 0) return FX_OK;
+  const int ntr = (M + 63) / 64, ntc = (NC + 63) / 64;
+  lu64_gemm_kernel<<<dim3((unsigned)(batch * ntr * ntc)), 256, 0, s>>>(A, Bm, C, N, (int64_t)N * N, M, NC, ntr, ntc);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+template <int MODE>
+int lu64_rows(const double* W, double* T, int N, int r0, const int* ipiv, int c0, int cend, int64_t batch,
+              hipStream_t s) {
+  if (cend <= c0) return FX_OK;
+  const int ncb = (cend - c0 + NT64 - 1) / NT64;
+  lu64_rows_kernel<MODE><<<dim3((unsigned)(batch * ncb)), NT64, 0, s>>>(W, T, N, r0, ipiv, c0, cend, ncb);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+// Copy (with skew symmetrisation) and factor in place; sign / logabs of the factorisation.
+int lu64_factor(const double* A, int n, int skew, int64_t batch, const Lu64Bufs& f, int N, double* sign,
+                double* logabs, hipStream_t s) {
+  const int64_t total = batch * (int64_t)N * N;
+  lu64_copy_kernel<<<dim3(grid_of(total)), 256, 0, s>>>(A, n, skew, f.W, N, total);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  for (int r0 = 0; r0 < N; r0 += P64) {
+    lu64_panel_kernel<<<dim3((unsigned)batch), NT64, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    const int r1 = r0 + P64;
+    if (r1 >= N) break;
+    int st = lu64_rows<0>(f.W, f.W, N, r0, f.ipiv, r1, N, batch, s);
+    if (st == FX_OK)
+      st = lu64_gemm(f.W + (int64_t)r1 * N + r0, f.W + (int64_t)r0 * N + r1, f.W + (int64_t)r1 * N + r1, N, N - r1,
+                     N - r1, batch, s);
+    if (st != FX_OK) return st;
+  }
+  lu64_finish_kernel<<<dim3((unsigned)((batch + 3) / 4)), 256, 0, s>>>(f.dpiv, f.nsw, N, sign, logabs, batch);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
 }  // namespace
 
 size_t lu64_workspace(int64_t batch, int n) {
@@ -254,32 +379,58 @@ int launch_lu64(const double* A, int n, int64_t batch, double* sign, double* log
   if (!ws || ws_bytes < lu64_workspace(batch, n)) return FX_ERR_WORKSPACE;
   const int N = lu64_padded(n);
   char* p = (char*)ws;
-  auto take = [&](size_t x) {
-    char* q = p;
-    p += (x + 255) / 256 * 256;
-    return (void*)q;
-  };
-  double* W = (double*)take((size_t)batch * N * N * 8);
-  int* ipiv = (int*)take((size_t)batch * N * 4);
-  double* dpiv = (double*)take((size_t)batch * N * 8);
-  int* nsw = (int*)take((size_t)batch * (N / P64) * 4);
-  const int64_t total = batch * (int64_t)N * N;
-  const int64_t cblocks = std::min<int64_t>((total + 255) / 256, 1 << 20);
-  lu64_copy_kernel<<<dim3((unsigned)cblocks), 256, 0, s>>>(A, n, W, N, total);
+  const Lu64Bufs f = lu64_take(p, batch, N);
+  return lu64_factor(A, n, 0, batch, f, N, sign, logabs, s);
+}
+
+size_t lu64_inverse_workspace(int64_t batch, int n) {
+  if (batch <= 0 || n <= 0) return 0;
+  const int N = lu64_padded(n);
+  auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+  return lu64_workspace(batch, n) + al((size_t)batch * N * N * 8) + al((size_t)batch * 4);
+}
+
+// The factorisation of A (skew: of (A - A^T) / 2) with its sign / logabs, then X = A^-1 by
+// the blocked solves L Y = P I (the panels' swaps applied to Y as they were to A, column
+// by column, rows in the order of their panel) and U X = Y (bottom block first), each a
+// 32-row substitution per column and a K = 32 fp64 MFMA update of the rows below / above
+// per block. out = X^T (out_t) or X, times sign exp(logabs) with `det` (the adjugate of a
+// regular member), zero where gate is 0 (default: the member's own sign) or X is not
+// finite. 2 n^3 flops of the solves on the MFMA against 2 n^3 of a Gauss-Jordan run on
+// one workgroup per matrix.
+int launch_lu64_inverse(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs,
+                        const double* gate, int det, double* out, int out_t, void* ws, size_t ws_bytes,
+                        hipStream_t s) {
+  if (batch <= 0) return FX_OK;
+  if (n <= 0 || n > 4096) return FX_ERR_UNSUPPORTED;
+  if (!ws || ws_bytes < lu64_inverse_workspace(batch, n)) return FX_ERR_WORKSPACE;
+  const int N = lu64_padded(n);
+  char* p = (char*)ws;
+  const Lu64Bufs f = lu64_take(p, batch, N);
+  double* Y = (double*)p;
+  p += ((size_t)batch * N * N * 8 + 255) / 256 * 256;
+  int* flag = (int*)p;
+  int st = lu64_factor(A, n, skew, batch, f, N, sign, logabs, s);
+  if (st != FX_OK) return st;
+  const int64_t tot = batch * (int64_t)N * N;
+  lu64_fill_kernel<<<dim3(grid_of(tot)), 256, 0, s>>>(Y, N, flag, batch, tot);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  for (int r0 = 0; r0 < N; r0 += P64) {
-    lu64_panel_kernel<<<dim3((unsigned)batch), NT64, 0, s>>>(W, N, r0, ipiv, dpiv, nsw);
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    const int rest = N - r0 - P64;
-    if (rest <= 0) break;
-    const int ncb = (rest + NT64 - 1) / NT64;
-    lu64_urow_kernel<<<dim3((unsigned)(batch * ncb)), NT64, 0, s>>>(W, N, r0, ipiv, ncb);
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    const int ntl = (rest + 63) / 64;
-    lu64_update_kernel<<<dim3((unsigned)(batch * ntl * ntl)), 256, 0, s>>>(W, N, r0, ntl);
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  for (int r0 = 0; r0 < N && st == FX_OK; r0 += P64) {
+    const int r1 = r0 + P64;
+    st = lu64_rows<1>(f.W, Y, N, r0, f.ipiv, 0, N, batch, s);
+    if (st == FX_OK && r1 < N)
+      st = lu64_gemm(f.W + (int64_t)r1 * N + r0, Y + (int64_t)r0 * N, Y + (int64_t)r1 * N, N, N - r1, N, batch, s);
   }
-  lu64_finish_kernel<<<dim3((unsigned)((batch + 3) / 4)), 256, 0, s>>>(dpiv, nsw, N, sign, logabs, batch);
+  for (int r0 = N - P64; r0 >= 0 && st == FX_OK; r0 -= P64) {
+    st = lu64_rows<2>(f.W, Y, N, r0, f.ipiv, 0, N, batch, s);
+    if (st == FX_OK && r0 > 0) st = lu64_gemm(f.W + r0, Y + (int64_t)r0 * N, Y, N, r0, N, batch, s);
+  }
+  if (st != FX_OK) return st;
+  const int64_t on = batch * (int64_t)n * n;
+  lu64_out_kernel<<<dim3(grid_of(on)), 256, 0, s>>>(Y, N, n, out_t, gate ? gate : sign, det ? sign : nullptr,
+                                                     det ? logabs : nullptr, out, flag, on);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  lu64_zero_kernel<<<dim3(grid_of(on)), 256, 0, s>>>(out, n, flag, on);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
