@@ -294,12 +294,14 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
  * The reference takes float64 through the same API (`_prep`, src/fermix/api.py:24-31,
  * with 64-bit fields, src/fermix/_field.py:20-120 and :265-275). These entry points are
  * the float64 counterparts of the ones above, with the same argument meaning, outputs
- * in float64 and 0 <= n <= 4096. Unblocked kernels, one workgroup per matrix: an LU /
- * Gauss-Jordan with partial pivoting (`_slogdet_generic`, `_lu_parts_generic`,
- * src/fermix/_fallback.py:36-97) and Parlett-Reid (`_slogpf_generic`, :266-300). The
- * workspace is 0 for n <= 128 (the matrix is held in registers), else one matrix copy
- * per member (twice that with the inverse). The kernel family override
- * FERMIX_AMD_KERNELS does not apply to them. */
+ * in float64 and 0 <= n <= 4096. For n <= fx_tune.f64_reg_max_n (128) one workgroup per
+ * matrix holds it in registers: an LU / Gauss-Jordan with partial pivoting
+ * (`_slogdet_generic`, `_lu_parts_generic`, src/fermix/_fallback.py:36-97) and
+ * Parlett-Reid (`_slogpf_generic`, :266-300), no workspace. Above, slogdet / det and the
+ * inverses run a blocked LU (32-column panels, the trailing updates on the fp64 MFMA) and
+ * blocked solves of it in a workspace of two padded matrix copies per member; the
+ * Parlett-Reid stays one workgroup per matrix (one matrix copy). The kernel family
+ * override FERMIX_AMD_KERNELS does not apply to them. */
 size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n);
 int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream);
@@ -398,7 +400,9 @@ int fx_slogpf_parts_c128(const double* a, int64_t batch, int32_t n, int32_t skew
  * and `_perm_sign` (src/fermix/_diff.py:160-246) for the 64-bit and complex kinds. One
  * workgroup per matrix; the workspace is that of the _parts entry points (none while
  * [A | I] fits in 60 KiB of LDS). For float64 the sign / logabs equal fx_slogdet_f64's
- * bits (the same pivots and per-element updates). */
+ * bits (the same pivots and per-element updates; above n = 128 the blocked LU's, whose
+ * solves give the regular members' det(A) A^-T, the Gauss-Jordan continuation then
+ * running only for the exactly singular members). */
 size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n);
 int fx_det_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
                      void* workspace, size_t workspace_bytes, fx_stream_t stream);
