@@ -219,6 +219,9 @@ __global__ __launch_bounds__(CX_NT) void cgj_kernel(const F* __restrict__ a, int
   unsigned char* asg = (unsigned char*)(prow + n);
 
   if constexpr (MODE == GJ_PFA) {
+    // with a gate: only the members whose gate value is 0 (pf = 0; the others' adjugate
+    // formed by the caller)
+    if (gate && !Fd<F>::is0(gate[b])) return;
     unsigned char* mb = meta + (size_t)b * PL.stride;
     const PfaHead<F>& h = *(const PfaHead<F>*)mb;
     if (h.z == -2) {  // three or more zero pivots: G = 0
@@ -486,7 +489,7 @@ __global__ __launch_bounds__(CX_NT) void cpr_kernel(const cx<T>* __restrict__ a,
 template <class F>
 __global__ __launch_bounds__(CX_NT) void cpfa_factor_kernel(const F* __restrict__ a, int n, int skew, F* Wg,
                                                             int use_lds, unsigned char* __restrict__ meta,
-                                                            PfaLayout PL) {
+                                                            PfaLayout PL, const F* __restrict__ gate) {
   using D = Fd<F>;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ unsigned long long redk[2][CX_NT / 64];
@@ -494,6 +497,7 @@ __global__ __launch_bounds__(CX_NT) void cpfa_factor_kernel(const F* __restrict_
   __shared__ int sK;
   const size_t mat = (size_t)n * n;
   const int64_t b = blockIdx.x;
+  if (gate && !D::is0(gate[b])) return;  // formed by the caller
   F* M = use_lds ? (F*)smem : Wg + (size_t)b * mat;
   int* perm = (int*)(smem + (use_lds ? mat * sizeof(F) : 0));
   unsigned char* mb = meta + (size_t)b * PL.stride;
@@ -761,7 +765,7 @@ int det_parts_f64(const double* a, int64_t batch, int n, double* sign, double* l
   if (!ws || wsb < need) return FX_ERR_WORKSPACE;
   const size_t lw = align_up(lu64_inverse_workspace(batch, n)), gw = align_up(slogdet_parts_ws<double>(batch, n));
   char* base = (char*)ws;
-  const int r = launch_lu64_inverse(a, n, 0, batch, sign, logabs, nullptr, 1, adj_t, 1, base, lw, s);
+  const int r = launch_lu64_inverse(a, n, 0, batch, sign, logabs, nullptr, sign, logabs, adj_t, 1, base, lw, s);
   if (r != FX_OK) return r;
   double* gsign = (double*)(base + lw + gw);
   return launch_cgj<double>(a, n, 0, batch, gsign, gsign + batch, adj_t, GJ_ADJ, 1, sign, base + lw, gw, s);
@@ -796,9 +800,11 @@ int cx_zero(F* g, int64_t count, hipStream_t s) {
 }
 
 // g = pf(S) S^-1 for even n > 0: the Parlett-Reid factor, then one [T~ | I] Gauss-Jordan
-// per evaluation (the second returns at once for the members without a lifted pivot).
+// per evaluation (the second returns at once for the members without a lifted pivot);
+// with a gate, only the members whose gate value is 0.
 template <class F>
-int pf_adjugate(const F* a, int64_t batch, int n, int skew, F* g, void* ws, size_t wsb, hipStream_t s) {
+int pf_adjugate(const F* a, int64_t batch, int n, int skew, F* g, void* ws, size_t wsb, hipStream_t s,
+                const F* gate = nullptr) {
   const size_t need = pf_adjugate_ws<F>(batch, n);
   if (need && (!ws || wsb < need)) return FX_ERR_WORKSPACE;
   const PfaLayout PL = pfa_layout<F>(n);
@@ -810,13 +816,13 @@ int pf_adjugate(const F* a, int64_t batch, int n, int skew, F* g, void* ws, size
   {
     const bool lds = cx_in_lds<F>(n, n);
     const size_t shm = cx_lds_bytes((size_t)n * n * sizeof(F), n, lds, true);
-    cpfa_factor_kernel<F><<<grid, CX_NT, shm, s>>>(a, n, skew, W, lds, meta, PL);
+    cpfa_factor_kernel<F><<<grid, CX_NT, shm, s>>>(a, n, skew, W, lds, meta, PL, gate);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   const bool lds = cx_in_lds<F>(n, 2 * n);
   const size_t shm = cx_lds_bytes((size_t)n * 2 * n * sizeof(F), n, lds, true);
   for (int ev = 0; ev < 2; ++ev) {
-    cgj_kernel<F, GJ_PFA><<<grid, CX_NT, shm, s>>>(a, n, skew, W, lds, nullptr, nullptr, g, 0, nullptr, meta, PL, ev);
+    cgj_kernel<F, GJ_PFA><<<grid, CX_NT, shm, s>>>(a, n, skew, W, lds, nullptr, nullptr, g, 0, gate, meta, PL, ev);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   }
   return FX_OK;
@@ -864,13 +870,29 @@ int slogpf_parts(const T* a, int64_t batch, int n, int skew, int adjugate, T* si
 
 }  // namespace
 
-// the float64 Pfaffian adjugate (fx_slogpf_parts_f64 with adjugate != 0): zero for odd n
-size_t pf_adjugate_f64_ws(int64_t batch, int n) { return pf_adjugate_ws<double>(batch, n); }
-int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, void* ws, size_t wsb,
-                    hipStream_t s) {
+// the float64 Pfaffian adjugate (fx_slogpf_parts_f64 with adjugate != 0): zero for odd n.
+// Above the register kernels (n > f64_reg_max_n) the members with pf != 0 (psign, the
+// Parlett-Reid run's sign, and plog its log|pf|) take pf(S) S^-1 from the blocked LU
+// solves, and only those with pf = 0 run the Parlett-Reid factor and Gauss-Jordan above.
+static size_t pf_adjugate_f64_lu_ws(int64_t batch, int n) {
+  return align_up(lu64_inverse_workspace(batch, n)) + align_up((size_t)batch * 2 * sizeof(double));
+}
+size_t pf_adjugate_f64_ws(int64_t batch, int n) {
+  const size_t gj = pf_adjugate_ws<double>(batch, n);
+  if (n <= tune().f64_reg_max_n || batch <= 0 || (n & 1)) return gj;
+  return std::max(gj, pf_adjugate_f64_lu_ws(batch, n));
+}
+int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, const double* psign,
+                    const double* plog, void* ws, size_t wsb, hipStream_t s) {
   if (batch <= 0 || n == 0) return FX_OK;
   if (n & 1) return cx_zero<double>(g, batch * (int64_t)n * n, s);
-  return pf_adjugate<double>(a, batch, n, skew, g, ws, wsb, s);
+  if (n <= tune().f64_reg_max_n) return pf_adjugate<double>(a, batch, n, skew, g, ws, wsb, s);
+  if (!ws || wsb < pf_adjugate_f64_ws(batch, n)) return FX_ERR_WORKSPACE;
+  const size_t lw = align_up(lu64_inverse_workspace(batch, n));
+  double* lsign = (double*)((char*)ws + lw);
+  const int r = launch_lu64_inverse(a, n, skew, batch, lsign, lsign + batch, psign, psign, plog, g, 0, ws, lw, s);
+  if (r != FX_OK) return r;
+  return pf_adjugate<double>(a, batch, n, skew, g, ws, wsb, s, psign);
 }
 
 }  // namespace fx

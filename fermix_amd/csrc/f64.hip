@@ -1,5 +1,6 @@
 // float64 path: slogdet / slogpf forward and their gradients (A^-T, S^-1) for
-// 0 <= n <= 4096, one workgroup per matrix.
+// 0 <= n <= 4096: one workgroup per matrix up to n = 128, the blocked kernels of lu64.hip
+// above.
 //
 // The reference takes float64 through the same entry points as float32 (dtype check
 // `_prep`, src/fermix/api.py:24-31; 64-bit fields in src/fermix/_field.py:20-120, where
@@ -14,19 +15,22 @@
 //    pfreg64_kernel<RW, NC, CH>: the matrix in registers, each thread a 16-column (n <= 64,
 //    fx_tune.f64_strip16_max_n) or 32-column strip of one row; per column (pair) step the
 //    owners post the pivot candidates and the pivot row(s) through LDS, two barriers;
-//  - larger n, gj64_kernel<NT, INV> / pr64_kernel<NT>: the matrix in LDS when it fits in
-//    60 KiB, else in a per-matrix slice of the workspace (rows served from L2).
+//  - larger n, gj64_kernel<NT, INV>: the matrix in LDS when it fits in 60 KiB, else in a
+//    per-matrix slice of the workspace (rows served from L2); it serves the inverse and
+//    adjugate runs that the blocked kernels of lu64.hip (LU, Parlett-Reid and the solves,
+//    used above 128 for sign / logabs and A^-T, S^-1) leave to it.
 // Gauss-Jordan (gj*): virtual partial pivoting (the pivot row of column j is the
 // unassigned row of largest |x|, lowest row index on ties). Without INV only the
 // unassigned rows are updated (an LU); with INV the assigned rows and an identity block
 // [A | I] are eliminated too, and row j of A^-1 is row prow[j] of the right block over
 // pivot j. Every element update is fma(-l, P[c], M[r, c]), l = M[r, j] * (1 / pivot), in
 // both modes, so sign / logabs of the gradient call are bit-identical to the forward.
-// Parlett-Reid (p*): pr64_kernel swaps the pivot row / column into position c + 1 as
-// the reference's generic path does; pfreg64_kernel pivots virtually (pair a = the lowest
-// unassigned index, p = argmax |S[p, a]|; pf = sgn(pi) prod d_k). Both add
-// round(tau_r w_x) - round(w_r tau_x) (no contraction), so the matrix stays exactly
-// skew-symmetric. All four are latency-bound per matrix (barriers per column step).
+// Parlett-Reid (pfreg64_kernel): virtual pivoting (pair a = the lowest unassigned index,
+// p = argmax |S[p, a]|; pf = sgn(pi) prod d_k); it adds round(tau_r w_x) - round(w_r
+// tau_x) (no contraction), so the matrix stays exactly skew-symmetric. Above n = 128 the
+// blocked Parlett-Reid of lu64.hip swaps the pivot row / column into position c + 1 as the
+// reference's generic path does. The register kernels are latency-bound per matrix
+// (barriers per column step).
 #include <algorithm>
 
 #include "common.h"
@@ -408,79 +412,6 @@ __global__ __launch_bounds__(RW* CH) void pfreg64_kernel(const double* __restric
   }
 }
 
-template <int NT>
-__global__ __launch_bounds__(NT) void pr64_kernel(const double* __restrict__ a, int n, int skew, double* Wg,
-                                                 int use_lds, double* __restrict__ sign_out,
-                                                 double* __restrict__ logabs_out) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ unsigned long long redk[2][NT / 64];
-  __shared__ int redr[2][NT / 64];
-  const size_t mat = (size_t)n * n;
-  const int64_t b = blockIdx.x;
-  if (n & 1) {  // odd n: pf = 0
-    if (threadIdx.x == 0) {
-      sign_out[b] = 0.0;
-      logabs_out[b] = -INFINITY;
-    }
-    return;
-  }
-  double* M = use_lds ? (double*)smem : Wg + (size_t)b * mat;
-  load_matrix<NT>(a + (size_t)b * mat, n, skew, M, n, false);
-  __syncthreads();
-
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  double logabs = 0.0, sgn = 1.0;
-  bool singular = false;
-  for (int c = 0; c + 1 < n; c += 2) {
-    unsigned long long k = 0;
-    int row = 0x7fffffff;
-    // |S[r, c]| = |S[c, r]|: the candidates read along row c
-    for (int r = c + 1 + threadIdx.x; r < n; r += NT) take_better(k, row, key64(M[(size_t)c * n + r]), r);
-    const int p = block_argmax<NT>(k, row, redk[(c >> 1) & 1], redr[(c >> 1) & 1]);
-    const int q = c + 1;
-    if (p != q) {  // swap rows p, q over columns >= c, then columns p, q over rows >= c
-      sgn = -sgn;
-      for (int x = c + threadIdx.x; x < n; x += NT) {
-        const double u = M[(size_t)p * n + x], v = M[(size_t)q * n + x];
-        M[(size_t)p * n + x] = v;
-        M[(size_t)q * n + x] = u;
-      }
-      __syncthreads();
-      for (int x = c + threadIdx.x; x < n; x += NT) {
-        const double u = M[(size_t)x * n + p], v = M[(size_t)x * n + q];
-        M[(size_t)x * n + p] = v;
-        M[(size_t)x * n + q] = u;
-      }
-      __syncthreads();
-    }
-    const double d = M[(size_t)c * n + q];
-    if (d == 0.0) {
-      singular = true;
-      break;
-    }
-    logabs += log(fabs(d));
-    if (d < 0.0) sgn = -sgn;
-    const double rd = 1.0 / d;
-    // tau = -S[:, c] / d = S[c, :] / d, w = S[:, q] = -S[q, :] (rows c and q contiguous)
-    const double* Rc = M + (size_t)c * n;
-    const double* Rq = M + (size_t)q * n;
-    for (int r = q + 1 + wave; r < n; r += NT / 64) {
-      double* R = M + (size_t)r * n;
-      const double tr = Rc[r] * rd, wr = -Rq[r];
-      for (int x = q + 1 + lane; x < n; x += 64) {
-#pragma clang fp contract(off)
-        const double t = tr * (-Rq[x]) - wr * (Rc[x] * rd);
-        R[x] = R[x] + t;
-      }
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    sign_out[b] = singular ? 0.0 : sgn;
-    logabs_out[b] = singular ? -INFINITY : logabs;
-  }
-}
-
 bool f64_in_lds(int n, int ld) { return (size_t)n * ld * sizeof(double) <= F64_LDS_MAX; }
 
 size_t f64_matrix_ws(int64_t batch, int n, int ld) {
@@ -535,12 +466,7 @@ int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, d
       pfreg64_kernel<128, 32, 4><<<grid, 512, 0, s>>>(a, n, skew, sign, logabs);
     return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
   }
-  const bool lds = f64_in_lds(n, n);
-  if (!lds && (!ws || ws_bytes < f64_matrix_ws(batch, n, n))) return FX_ERR_WORKSPACE;
-  const size_t shm = f64_lds_bytes(n, n, lds, false);
-  const dim3 grid((unsigned)batch);
-  pr64_kernel<1024><<<grid, 1024, shm, s>>>(a, n, skew, (double*)ws, lds, sign, logabs);
-  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+  return launch_pr64_blocked(a, n, skew, batch, sign, logabs, ws, ws_bytes, s);  // lu64.hip
 }
 
 // Workspace of the Gauss-Jordan path: none in registers (n <= f64_reg_max_n) or LDS.
@@ -601,11 +527,12 @@ int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign
   hipStream_t s = (hipStream_t)stream;
   if (!lu64_path(n))
     return launch_gj64(a, n, 0, batch, sign, logabs, inv_t, 1, nullptr, workspace, workspace_bytes, s);
-  return launch_lu64_inverse(a, n, 0, batch, sign, logabs, nullptr, 0, inv_t, 1, workspace, workspace_bytes, s);
+  return launch_lu64_inverse(a, n, 0, batch, sign, logabs, nullptr, nullptr, nullptr, inv_t, 1, workspace,
+                             workspace_bytes, s);
 }
 
 size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n) {
-  return n > F64_MAXN || n <= tune().f64_reg_max_n ? 0 : f64_matrix_ws(batch, n, n);
+  return n > F64_MAXN || n <= tune().f64_reg_max_n ? 0 : pr64_workspace(batch, n);
 }
 
 int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign, double* logabs,
@@ -640,14 +567,14 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
   if (st != FX_OK || n == 0) return st;
   // the Pfaffian adjugate from its own Parlett-Reid run (cplx.hip)
   if (adjugate)
-    return pf_adjugate_f64(a, batch, n, skew_symmetrize != 0, g, base + pr, workspace_bytes - pr, s);
+    return pf_adjugate_f64(a, batch, n, skew_symmetrize != 0, g, sign, logabs, base + pr, workspace_bytes - pr, s);
   // S^-1 by Gauss-Jordan (register kernels' orders) or the blocked LU solves on the same S,
   // zeroed where the Parlett-Reid run found pf = 0 (every member for odd n)
   if (lu64_path(n)) {
     const size_t lw = align_up_256(lu64_inverse_workspace(batch, n));
     double* gsign = (double*)(base + pr + lw);
-    return launch_lu64_inverse(a, n, skew_symmetrize != 0, batch, gsign, gsign + batch, sign, 0, g, 0, base + pr, lw,
-                               s);
+    return launch_lu64_inverse(a, n, skew_symmetrize != 0, batch, gsign, gsign + batch, sign, nullptr, nullptr, g, 0,
+                               base + pr, lw, s);
   }
   double* gsign = (double*)(base + pr + gj);
   double* glog = gsign + batch;

@@ -145,16 +145,23 @@ size_t lu64_workspace(int64_t batch, int n);
 int launch_lu64(const double* A, int n, int64_t batch, double* sign, double* logabs, void* ws, size_t ws_bytes,
                 hipStream_t s);
 // ... and the inverse from the same factorisation (A skew-symmetrised when skew): out =
-// A^-T (out_t) or A^-1, times det A when det, zero where gate (default: the factorisation's
-// own sign) is 0 or the result is not finite; sign / logabs those of the factorisation.
+// A^-T (out_t) or A^-1, times ssign exp(slog) when ssign is given, zero where gate
+// (default: the factorisation's own sign) is 0 or the result is not finite; sign / logabs
+// those of the factorisation.
 size_t lu64_inverse_workspace(int64_t batch, int n);
 int launch_lu64_inverse(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs,
-                        const double* gate, int det, double* out, int out_t, void* ws, size_t ws_bytes,
-                        hipStream_t s);
+                        const double* gate, const double* ssign, const double* slog, double* out, int out_t,
+                        void* ws, size_t ws_bytes, hipStream_t s);
+// float64 Parlett-Reid sign / logabs for n above the register kernels (lu64.hip): 16 pair
+// steps per panel, the trailing update on the fp64 MFMA
+size_t pr64_workspace(int64_t batch, int n);
+int launch_pr64_blocked(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
+                        size_t ws_bytes, hipStream_t s);
 
-// float64 Pfaffian adjugate pf(S) S^-1 (cplx.hip; zero for odd n)
+// float64 Pfaffian adjugate pf(S) S^-1 (cplx.hip; zero for odd n); psign / plog: the
+// Parlett-Reid run's sign and log|pf| of the same S
 size_t pf_adjugate_f64_ws(int64_t batch, int n);
-int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, void* ws, size_t wsb,
-                    hipStream_t s);
+int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, const double* psign,
+                    const double* plog, void* ws, size_t wsb, hipStream_t s);
 
 }  // namespace fx

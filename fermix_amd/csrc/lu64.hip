@@ -15,7 +15,9 @@
 //      pivot order (one wave, lane-strided partial sums and a fixed tree).
 // The column steps of a panel are latency-bound (three workgroup barriers each); the
 // work that grows as n^3 runs on the MFMA in many workgroups per matrix. The inverse
-// (launch_lu64_inverse: A^-T, S^-1, det A^-T) solves with the same row and GEMM kernels.
+// (launch_lu64_inverse: A^-T, S^-1, det A^-T) solves with the same row and GEMM kernels,
+// and the blocked Parlett-Reid below (launch_pr64_blocked: float64 slogpf) updates its
+// trailing matrix with the same GEMM.
 #include <algorithm>
 
 #include "common.h"
@@ -31,17 +33,18 @@ typedef double v4d __attribute__((ext_vector_type(4)));
 
 int lu64_padded(int n) { return (n + P64 - 1) / P64 * P64; }
 
-// W (B, N, N) = A (B, n, n) with identity padding (skew: (A - A^T) / 2); a grid-stride
-// loop over B N N elements.
+// W (B, N, N) = A (B, n, n) with identity padding (skew: (A - A^T) / 2), or, with pfpad
+// (n even), padding by 2 x 2 blocks [[0, 1], [-1, 0]] on the diagonal (skew, Pfaffian 1);
+// a grid-stride loop over B N N elements.
 __global__ void lu64_copy_kernel(const double* __restrict__ A, int n, int skew, double* __restrict__ W, int N,
-                                 int64_t total) {
+                                 int64_t total, int pfpad = 0) {
   const int64_t NN = (int64_t)N * N;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t b = e / NN;
     const int64_t f = e - b * NN;
     const int r = (int)(f / N), c = (int)(f - (int64_t)r * N);
     const double* Ab = A + b * (int64_t)n * n;
-    double v = r == c ? 1.0 : 0.0;
+    double v = pfpad ? (c == (r ^ 1) ? ((r & 1) ? -1.0 : 1.0) : 0.0) : (r == c ? 1.0 : 0.0);
     if (r < n && c < n) v = skew ? (Ab[(int64_t)r * n + c] - Ab[(int64_t)c * n + r]) * 0.5 : Ab[(int64_t)r * n + c];
     W[e] = v;
   }
@@ -49,11 +52,12 @@ __global__ void lu64_copy_kernel(const double* __restrict__ A, int n, int skew, 
 
 // Panel of columns r0 .. r0 + 31, rows r0 .. N - 1, in place; ipiv / d: the pivot row and
 // pivot of each column; nsw: the block's row swaps.
-__global__ __launch_bounds__(NT64) void lu64_panel_kernel(double* __restrict__ W, int N, int r0,
-                                                          int* __restrict__ ipiv, double* __restrict__ dpiv,
-                                                          int* __restrict__ nsw) {
-  __shared__ unsigned long long redk[2][NT64 / 64];
-  __shared__ int redr[2][NT64 / 64];
+template <int NT>
+__global__ __launch_bounds__(NT) void lu64_panel_kernel(double* __restrict__ W, int N, int r0,
+                                                        int* __restrict__ ipiv, double* __restrict__ dpiv,
+                                                        int* __restrict__ nsw) {
+  __shared__ unsigned long long redk[2][NT / 64];
+  __shared__ int redr[2][NT / 64];
   __shared__ double prow[P64];
   const int64_t b = blockIdx.x;
   double* Wb = W + b * (int64_t)N * N;
@@ -63,8 +67,8 @@ __global__ __launch_bounds__(NT64) void lu64_panel_kernel(double* __restrict__ W
     const int c = r0 + j;
     unsigned long long k = 0;
     int row = 0x7fffffff;
-    for (int r = c + tid; r < N; r += NT64) take_better(k, row, key64(Wb[(int64_t)r * N + c]), r);
-    const int p = block_argmax<NT64>(k, row, redk[j & 1], redr[j & 1]);  // >= c: every key is >= 1
+    for (int r = c + tid; r < N; r += NT) take_better(k, row, key64(Wb[(int64_t)r * N + c]), r);
+    const int p = block_argmax<NT>(k, row, redk[j & 1], redr[j & 1]);  // >= c: every key is >= 1
     if (p != c) {
       if (tid < P64) {
         double* Rc = Wb + (int64_t)c * N + r0;
@@ -84,7 +88,7 @@ __global__ __launch_bounds__(NT64) void lu64_panel_kernel(double* __restrict__ W
       dpiv[b * N + c] = d;
     }
     const double rd = d != 0.0 ? 1.0 / d : 0.0;  // a zero pivot: its column is zero below
-    for (int r = c + 1 + tid; r < N; r += NT64) {
+    for (int r = c + 1 + tid; r < N; r += NT) {
       double* R = Wb + (int64_t)r * N + r0;
       const double l = R[j] * rd;
       R[j] = l;
@@ -167,16 +171,17 @@ __global__ __launch_bounds__(NT64) void lu64_rows_kernel(const double* __restric
 }
 
 // C -= A B with K = 32: A = rows 0 .. M - 1 of a 32-column block, B = its 32 rows of
-// columns 0 .. NC - 1, C = M x NC (every operand given at its first element in matrix 0;
-// row stride ld, matrix stride NN). One 64 x 64 tile per workgroup (tiles t = tile row *
+// columns 0 .. NC - 1, C = M x NC (every operand given at its first element in matrix 0,
+// with its own row and matrix strides). One 64 x 64 tile per workgroup (tiles t = tile row *
 // ntc + tile column), four waves of 32 x 32, each as 2 x 2 16 x 16 fp64 MFMA
 // accumulators over eight K = 4 steps; the products in accumulators of their own,
 // subtracted from C in fp64 at the end. Lane l supplies A[l % 16][l / 16] and
 // B[l / 16][l % 16]; accumulator element v of lane l is row l / 16 + 4 v, column l % 16
 // (measured with a one-wave probe: unlike the fp32 16x16x4 layout, a lane's four rows
 // are 4 apart). Serves the trailing update A22 -= L21 U12 and both solves' updates.
-__global__ __launch_bounds__(256) void lu64_gemm_kernel(const double* __restrict__ A, const double* __restrict__ Bm,
-                                                        double* __restrict__ C, int ld, int64_t NN, int M, int NC,
+__global__ __launch_bounds__(256) void lu64_gemm_kernel(const double* __restrict__ A, int lda, int64_t sA,
+                                                        const double* __restrict__ Bm, int ldb, int64_t sB,
+                                                        double* __restrict__ C, int ldc, int64_t sC, int M, int NC,
                                                         int ntr, int ntc) {
   __shared__ double As[64][P64 + 1];
   __shared__ double Bs[P64][64 + 1];
@@ -184,15 +189,15 @@ __global__ __launch_bounds__(256) void lu64_gemm_kernel(const double* __restrict
   const int64_t b = blockIdx.x / nt;
   const int t = (int)(blockIdx.x - b * nt);
   const int i0 = 64 * (t / ntc), j0 = 64 * (t % ntc);
-  const double* Ab = A + b * NN;
-  const double* Bb = Bm + b * NN;
-  double* Cb = C + b * NN;
+  const double* Ab = A + b * sA;
+  const double* Bb = Bm + b * sB;
+  double* Cb = C + b * sC;
   const int tid = threadIdx.x;
   for (int e = tid; e < 64 * P64; e += 256) {
     const int i = e / P64, k = e % P64;
-    As[i][k] = i0 + i < M ? Ab[(int64_t)(i0 + i) * ld + k] : 0.0;
+    As[i][k] = i0 + i < M ? Ab[(int64_t)(i0 + i) * lda + k] : 0.0;
     const int kk = e / 64, j = e % 64;
-    Bs[kk][j] = j0 + j < NC ? Bb[(int64_t)kk * ld + j0 + j] : 0.0;
+    Bs[kk][j] = j0 + j < NC ? Bb[(int64_t)kk * ldb + j0 + j] : 0.0;
   }
   __syncthreads();
   const int wave = tid >> 6, lane = tid & 63;
@@ -226,7 +231,7 @@ __global__ __launch_bounds__(256) void lu64_gemm_kernel(const double* __restrict
       for (int v = 0; v < 4; ++v) {
         const int row = i0 + wm + 16 * a + lk + 4 * v;
         if (row < M && col < NC) {
-          double* e = Cb + (int64_t)row * ld + col;
+          double* e = Cb + (int64_t)row * ldc + col;
           *e = *e - acc[a][c][v];
         }
       }
@@ -325,11 +330,19 @@ Lu64Bufs lu64_take(char*& p, int64_t batch, int N) {
 }
 
 // C -= A B (K = 32) over M x NC, operands at their first elements of matrix 0
-int lu64_gemm(const double* A, const double* Bm, double* C, int N, int M, int NC, int64_t batch, hipStream_t s) {
+int lu64_gemm_strided(const double* A, int lda, int64_t sA, const double* Bm, int ldb, int64_t sB, double* C,
+                      int ldc, int64_t sC, int M, int NC, int64_t batch, hipStream_t s) {
   if (M <= 0 || NC <= 0) return FX_OK;
   const int ntr = (M + 63) / 64, ntc = (NC + 63) / 64;
-  lu64_gemm_kernel<<<dim3((unsigned)(batch * ntr * ntc)), 256, 0, s>>>(A, Bm, C, N, (int64_t)N * N, M, NC, ntr, ntc);
+  lu64_gemm_kernel<<<dim3((unsigned)(batch * ntr * ntc)), 256, 0, s>>>(A, lda, sA, Bm, ldb, sB, C, ldc, sC, M, NC,
+                                                                      ntr, ntc);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+// the same with every operand inside an N x N matrix of the batch
+int lu64_gemm(const double* A, const double* Bm, double* C, int N, int M, int NC, int64_t batch, hipStream_t s) {
+  const int64_t NN = (int64_t)N * N;
+  return lu64_gemm_strided(A, N, NN, Bm, N, NN, C, N, NN, M, NC, batch, s);
 }
 
 template <int MODE>
@@ -348,7 +361,10 @@ int lu64_factor(const double* A, int n, int skew, int64_t batch, const Lu64Bufs&
   lu64_copy_kernel<<<dim3(grid_of(total)), 256, 0, s>>>(A, n, skew, f.W, N, total);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   for (int r0 = 0; r0 < N; r0 += P64) {
-    lu64_panel_kernel<<<dim3((unsigned)batch), NT64, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
+    if (N > 512)  // latency-bound column steps: more threads per matrix
+      lu64_panel_kernel<1024><<<dim3((unsigned)batch), 1024, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
+    else
+      lu64_panel_kernel<NT64><<<dim3((unsigned)batch), NT64, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     const int r1 = r0 + P64;
     if (r1 >= N) break;
@@ -360,6 +376,178 @@ int lu64_factor(const double* A, int n, int skew, int64_t batch, const Lu64Bufs&
   }
   lu64_finish_kernel<<<dim3((unsigned)((batch + 3) / 4)), 256, 0, s>>>(f.dpiv, f.nsw, N, sign, logabs, batch);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+// ---- blocked Parlett-Reid (float64 slogpf above the register kernels)
+//
+// The reference's Parlett-Reid block loop (src/fermix/_pf.py:59-382: pair steps with a
+// pivot search in the eliminated column, a symmetric row / column swap and the rank-2
+// skew update S22 -= u v^T - v u^T, u = S[c, :] / S[c, c + 1], v = S[c + 1, :]) with the
+// updates of 16 pair steps deferred: within a panel each pair step forms its two rows
+// left-looking from the panel's earlier (u, v), and after the panel the trailing matrix
+// takes all 16 at once, S22 -= [U, -V] [V, U]^T, a K = 32 product on the fp64 MFMA
+// (lu64_gemm_kernel). The pair's Pfaffian factor is d = S[c, c + 1] after the swap; pf =
+// (-1)^swaps prod d.
+constexpr int PRB = P64 / 2;  // pair steps per panel
+
+// Panel of positions r0 .. r0 + 31 (one workgroup per matrix), W the full skew matrix of
+// padded order N (rows and columns >= c + 1 swapped symmetrically, in place). Ar (B, N,
+// 32): row x = (U[x][0..15], -V[x][0..15]); Bk (B, 32, N): rows 0..15 = V^T, 16..31 =
+// U^T (the two operands of the trailing product, and the left-looking coefficients).
+// rc: the current row c of the pair step; lacc / sacc / stat: log|pf| and sign so far and
+// the zero-pivot flag (a flagged member skips its later panels).
+template <int NT>
+__global__ __launch_bounds__(NT) void pr64_panel_kernel(double* __restrict__ W, int N, int r0,
+                                                        double* __restrict__ Ar, double* __restrict__ Bk,
+                                                        double* __restrict__ rcg, double* __restrict__ lacc,
+                                                        double* __restrict__ sacc, int* __restrict__ stat) {
+  __shared__ unsigned long long redk[2][NT / 64];
+  __shared__ int redr[2][NT / 64];
+  __shared__ double cu[PRB], cv[PRB];
+  const int64_t b = blockIdx.x;
+  if (stat[b]) return;
+  const int tid = threadIdx.x;
+  double* Wb = W + b * (int64_t)N * N;
+  double* Ab = Ar + b * (int64_t)N * P64;
+  double* Bb = Bk + b * (int64_t)P64 * N;
+  double* rc = rcg + b * (int64_t)N;
+  double lg = 0.0, sg = 1.0;  // thread 0's running sums, in pivot order
+  bool sing = false;
+  for (int p = 0; p < PRB; ++p) {
+    const int c = r0 + 2 * p, q = c + 1;
+    // row c: S[c][x] - sum_j (U[c][j] V[x][j] - V[c][j] U[x][j]) for x > c
+    if (tid < p) {
+      cu[tid] = Bb[(int64_t)(PRB + tid) * N + c];
+      cv[tid] = Bb[(int64_t)tid * N + c];
+    }
+    __syncthreads();
+    unsigned long long k = 0;
+    int row = 0x7fffffff;
+    for (int x = q + tid; x < N; x += NT) {
+      double a = Wb[(int64_t)c * N + x];
+      for (int j = 0; j < p; ++j) {
+        a = fma(-cu[j], Bb[(int64_t)j * N + x], a);
+        a = fma(cv[j], Bb[(int64_t)(PRB + j) * N + x], a);
+      }
+      rc[x] = a;
+      take_better(k, row, key64(a), x);
+    }
+    // |S[x][c]| = |S[c][x]|: the largest, lowest index on ties, moves to position q
+    const int pv = block_argmax<NT>(k, row, redk[p & 1], redr[p & 1]);
+    if (pv != q) {
+      for (int x = q + tid; x < N; x += NT) {
+        const double u = Wb[(int64_t)pv * N + x], v = Wb[(int64_t)q * N + x];
+        Wb[(int64_t)pv * N + x] = v;
+        Wb[(int64_t)q * N + x] = u;
+      }
+      if (tid < P64) {
+        const double u = Ab[(int64_t)pv * P64 + tid], v = Ab[(int64_t)q * P64 + tid];
+        Ab[(int64_t)pv * P64 + tid] = v;
+        Ab[(int64_t)q * P64 + tid] = u;
+        const double y = Bb[(int64_t)tid * N + pv], z = Bb[(int64_t)tid * N + q];
+        Bb[(int64_t)tid * N + pv] = z;
+        Bb[(int64_t)tid * N + q] = y;
+      }
+      if (tid == 0) {
+        const double u = rc[pv];
+        rc[pv] = rc[q];
+        rc[q] = u;
+        sg = -sg;
+      }
+      __syncthreads();
+      for (int r = q + tid; r < N; r += NT) {
+        const double u = Wb[(int64_t)r * N + pv], v = Wb[(int64_t)r * N + q];
+        Wb[(int64_t)r * N + pv] = v;
+        Wb[(int64_t)r * N + q] = u;
+      }
+    }
+    __syncthreads();
+    if (tid < p) {
+      cu[tid] = Bb[(int64_t)(PRB + tid) * N + q];
+      cv[tid] = Bb[(int64_t)tid * N + q];
+    }
+    __syncthreads();
+    const double d = rc[q];
+    if (d == 0.0) {  // row c is zero beyond c: pf = 0
+      sing = true;
+      break;
+    }
+    const double rd = 1.0 / d;
+    // u = row c / d, v = row q (left-looking like row c) beyond q; zero at positions <= q
+    for (int x = r0 + tid; x < N; x += NT) {
+      double u = 0.0, v = 0.0;
+      if (x > q) {
+        double a = Wb[(int64_t)q * N + x];
+        for (int j = 0; j < p; ++j) {
+          a = fma(-cu[j], Bb[(int64_t)j * N + x], a);
+          a = fma(cv[j], Bb[(int64_t)(PRB + j) * N + x], a);
+        }
+        v = a;
+        u = rc[x] * rd;
+      }
+      Ab[(int64_t)x * P64 + p] = u;
+      Ab[(int64_t)x * P64 + PRB + p] = -v;
+      Bb[(int64_t)p * N + x] = v;
+      Bb[(int64_t)(PRB + p) * N + x] = u;
+    }
+    if (tid == 0) {
+      lg += log(fabs(d));
+      if (d < 0.0) sg = -sg;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    if (sing) stat[b] = 1;
+    lacc[b] += lg;
+    sacc[b] *= sg;
+  }
+}
+
+__global__ void pr64_init_kernel(double* __restrict__ lacc, double* __restrict__ sacc, int* __restrict__ stat,
+                                 int64_t batch) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  lacc[b] = 0.0;
+  sacc[b] = 1.0;
+  stat[b] = 0;
+}
+
+// (sign, logabs): the running sums, (0, -inf) for flagged members and for odd n (odd)
+__global__ void pr64_finish_kernel(const double* __restrict__ lacc, const double* __restrict__ sacc,
+                                   const int* __restrict__ stat, int odd, double* __restrict__ sign,
+                                   double* __restrict__ logabs, int64_t batch) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  const bool zero = odd || stat[b];
+  sign[b] = zero ? 0.0 : sacc[b];
+  logabs[b] = zero ? -INFINITY : lacc[b];
+}
+
+struct Pr64Bufs {
+  double* W;
+  double* Ar;
+  double* Bk;
+  double* rc;
+  double* lacc;
+  double* sacc;
+  int* stat;
+};
+
+Pr64Bufs pr64_take(char* p, int64_t batch, int N) {
+  auto take = [&](size_t x) {
+    char* q = p;
+    p += (x + 255) / 256 * 256;
+    return (void*)q;
+  };
+  Pr64Bufs f;
+  f.W = (double*)take((size_t)batch * N * N * 8);
+  f.Ar = (double*)take((size_t)batch * N * P64 * 8);
+  f.Bk = (double*)take((size_t)batch * N * P64 * 8);
+  f.rc = (double*)take((size_t)batch * N * 8);
+  f.lacc = (double*)take((size_t)batch * 8);
+  f.sacc = (double*)take((size_t)batch * 8);
+  f.stat = (int*)take((size_t)batch * 4);
+  return f;
 }
 
 }  // namespace
@@ -394,13 +582,14 @@ size_t lu64_inverse_workspace(int64_t batch, int n) {
 // the blocked solves L Y = P I (the panels' swaps applied to Y as they were to A, column
 // by column, rows in the order of their panel) and U X = Y (bottom block first), each a
 // 32-row substitution per column and a K = 32 fp64 MFMA update of the rows below / above
-// per block. out = X^T (out_t) or X, times sign exp(logabs) with `det` (the adjugate of a
-// regular member), zero where gate is 0 (default: the member's own sign) or X is not
-// finite. 2 n^3 flops of the solves on the MFMA against 2 n^3 of a Gauss-Jordan run on
-// one workgroup per matrix.
+// per block. out = X^T (out_t) or X, times ssign exp(slog) when ssign is given (the
+// factorisation's own sign / logabs: the det adjugate of a regular member; a Parlett-Reid
+// run's: the Pfaffian adjugate), zero where gate is 0 (default: the member's own sign) or
+// X is not finite. 2 n^3 flops of the solves on the MFMA against 2 n^3 of a Gauss-Jordan
+// run on one workgroup per matrix.
 int launch_lu64_inverse(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs,
-                        const double* gate, int det, double* out, int out_t, void* ws, size_t ws_bytes,
-                        hipStream_t s) {
+                        const double* gate, const double* ssign, const double* slog, double* out, int out_t,
+                        void* ws, size_t ws_bytes, hipStream_t s) {
   if (batch <= 0) return FX_OK;
   if (n <= 0 || n > 4096) return FX_ERR_UNSUPPORTED;
   if (!ws || ws_bytes < lu64_inverse_workspace(batch, n)) return FX_ERR_WORKSPACE;
@@ -427,10 +616,57 @@ int launch_lu64_inverse(const double* A, int n, int skew, int64_t batch, double*
   }
   if (st != FX_OK) return st;
   const int64_t on = batch * (int64_t)n * n;
-  lu64_out_kernel<<<dim3(grid_of(on)), 256, 0, s>>>(Y, N, n, out_t, gate ? gate : sign, det ? sign : nullptr,
-                                                     det ? logabs : nullptr, out, flag, on);
+  lu64_out_kernel<<<dim3(grid_of(on)), 256, 0, s>>>(Y, N, n, out_t, gate ? gate : sign, ssign, slog, out, flag, on);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   lu64_zero_kernel<<<dim3(grid_of(on)), 256, 0, s>>>(out, n, flag, on);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+size_t pr64_workspace(int64_t batch, int n) {
+  if (batch <= 0 || n <= 0 || (n & 1)) return 0;
+  const int N = lu64_padded(n);
+  auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+  return al((size_t)batch * N * N * 8) + 2 * al((size_t)batch * N * P64 * 8) + al((size_t)batch * N * 8) +
+         2 * al((size_t)batch * 8) + al((size_t)batch * 4);
+}
+
+// sign / logabs of pf(A) (skew: of (A - A^T) / 2) by the blocked Parlett-Reid: copy with
+// [[0, 1], [-1, 0]] padding to order N (a multiple of 32), 16 pair steps per panel
+// kernel, the K = 32 trailing update after each; (0, -inf) for odd n.
+int launch_pr64_blocked(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
+                        size_t ws_bytes, hipStream_t s) {
+  if (batch <= 0) return FX_OK;
+  if (n <= 0 || n > 4096) return FX_ERR_UNSUPPORTED;
+  const unsigned gb = (unsigned)((batch + 255) / 256);
+  if (n & 1) {
+    pr64_finish_kernel<<<dim3(gb), 256, 0, s>>>(nullptr, nullptr, nullptr, 1, sign, logabs, batch);
+    return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+  }
+  if (!ws || ws_bytes < pr64_workspace(batch, n)) return FX_ERR_WORKSPACE;
+  const int N = lu64_padded(n);
+  const Pr64Bufs f = pr64_take((char*)ws, batch, N);
+  const int64_t total = batch * (int64_t)N * N;
+  lu64_copy_kernel<<<dim3(grid_of(total)), 256, 0, s>>>(A, n, skew, f.W, N, total, 1);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  pr64_init_kernel<<<dim3(gb), 256, 0, s>>>(f.lacc, f.sacc, f.stat, batch);
+  if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+  const int64_t NN = (int64_t)N * N, NP = (int64_t)N * P64;
+  for (int r0 = 0; r0 < N; r0 += P64) {
+    if (N > 512)  // latency-bound column loops: more threads per matrix
+      pr64_panel_kernel<1024><<<dim3((unsigned)batch), 1024, 0, s>>>(f.W, N, r0, f.Ar, f.Bk, f.rc, f.lacc, f.sacc,
+                                                                     f.stat);
+    else
+      pr64_panel_kernel<NT64><<<dim3((unsigned)batch), NT64, 0, s>>>(f.W, N, r0, f.Ar, f.Bk, f.rc, f.lacc, f.sacc,
+                                                                     f.stat);
+    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+    const int r1 = r0 + P64;
+    if (r1 >= N) break;
+    // S22 -= [U, -V] [V, U]^T over positions r1 .. N - 1
+    const int st = lu64_gemm_strided(f.Ar + (int64_t)r1 * P64, P64, NP, f.Bk + r1, N, NP, f.W + (int64_t)r1 * N + r1,
+                                     N, NN, N - r1, N - r1, batch, s);
+    if (st != FX_OK) return st;
+  }
+  pr64_finish_kernel<<<dim3(gb), 256, 0, s>>>(f.lacc, f.sacc, f.stat, 0, sign, logabs, batch);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 

@@ -299,9 +299,11 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
  * (`_slogdet_generic`, `_lu_parts_generic`, src/fermix/_fallback.py:36-97) and
  * Parlett-Reid (`_slogpf_generic`, :266-300), no workspace. Above, slogdet / det and the
  * inverses run a blocked LU (32-column panels, the trailing updates on the fp64 MFMA) and
- * blocked solves of it in a workspace of two padded matrix copies per member; the
- * Parlett-Reid stays one workgroup per matrix (one matrix copy). The kernel family
- * override FERMIX_AMD_KERNELS does not apply to them. */
+ * blocked solves of it in a workspace of two padded matrix copies per member, and slogpf
+ * a blocked Parlett-Reid (16 pair steps per panel, the pivot swapped into c + 1 as the
+ * generic path does, the K = 32 trailing update on the fp64 MFMA; one padded matrix copy
+ * plus 64 columns per member). The kernel family override FERMIX_AMD_KERNELS does not
+ * apply to them. */
 size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n);
 int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream);
@@ -326,7 +328,9 @@ int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmet
  * src/fermix/_fallback.py:101-192) from a Parlett-Reid run of its own (the smallest
  * pivot K by modulus, exact zero pivots and d_K replaced by 1) and one Gauss-Jordan
  * inverse of the replaced factorisation, a second exact zero pivot lifted to +1 and -1
- * (two inverses for those members); sign / logabs stay those of the plain forward. */
+ * (two inverses for those members); above n = 128 only the members with pf = 0 take that
+ * route, the others pf(S) times S^-1 from the blocked LU solves; sign / logabs stay those
+ * of the plain forward. */
 size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
@@ -380,7 +384,9 @@ int fx_slogpf_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symme
  * src/fermix/_fallback.py:101-192) from a Parlett-Reid run of its own (the smallest
  * pivot K by modulus, exact zero pivots and d_K replaced by 1) and one Gauss-Jordan
  * inverse of the replaced factorisation, a second exact zero pivot lifted to +1 and -1
- * (two inverses for those members); sign / logabs stay those of the plain forward. */
+ * (two inverses for those members); above n = 128 only the members with pf = 0 take that
+ * route, the others pf(S) times S^-1 from the blocked LU solves; sign / logabs stay those
+ * of the plain forward. */
 size_t fx_slogpf_parts_c64_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         float* sign, float* logabs, float* g, void* workspace, size_t workspace_bytes,

@@ -52,7 +52,8 @@ def test_f64_slogdet_and_inverse(dev, n):
         assert_grad64(_np(invT), np.swapaxes(ref64.inv64(A), 1, 2), A, f"A^-T n={n}")
 
 
-@pytest.mark.parametrize("n", [0, 2, 4, 6, 8, 16, 30, 62, 64, 86, 88, 128, 130, 200, 256])
+# above n = 128 the blocked Parlett-Reid (16 pair steps per panel, padded orders 160 .. 544)
+@pytest.mark.parametrize("n", [0, 2, 4, 6, 8, 16, 30, 62, 64, 86, 88, 128, 130, 200, 256, 520])
 def test_f64_slogpf_and_inverse(dev, n):
     B = 8 if n <= 128 else 3
     rng = np.random.default_rng(7100 + n)
@@ -182,3 +183,48 @@ def test_f64_autograd(dev, n):
     (gp,) = torch.autograd.grad(pp.sum(), Ap)
     pf_ref = sr * np.exp(lr)
     assert_grad64(_np(gp), 0.5 * pf_ref[:, None, None] * np.swapaxes(ref64.inv64(S), 1, 2), S, "pf autograd")
+
+
+def _jmat(n):
+    J = np.zeros((n, n))
+    for i in range(0, n - 1, 2):
+        J[i, i + 1], J[i + 1, i] = 1.0, -1.0
+    return J
+
+
+@pytest.mark.parametrize("n", [1030, 2048, 4096])
+def test_f64_slogpf_blocked_large(dev, n):
+    """The blocked Parlett-Reid at large n: pf(X J X^T) = det(X) (X = I + N(0, 1/(4n)), well
+    conditioned) against float64 slogdet(X) on the GPU; a member with a zero row / column
+    (pf = 0), odd n (pf = 0), and the same matrices with their order reversed (a symmetric
+    permutation P S P^T, other pivots: pf changes by det P). n = 4096 runs unpadded."""
+    B = 2 if n < 4096 else 1
+    g = torch.Generator(device="cpu").manual_seed(9900 + n)
+    X = torch.eye(n, dtype=torch.float64) + 0.5 * torch.randn((B, n, n), generator=g, dtype=torch.float64) / np.sqrt(n)
+    X = X.to(dev)
+    S = X @ torch.from_numpy(_jmat(n)).to(dev) @ X.transpose(1, 2)
+    S = (0.5 * (S - S.transpose(1, 2))).contiguous()
+    sgn, lab = torch.linalg.slogdet(X)
+    print(f"f64 slogpf blocked n={n} B={B}", flush=True)
+    s, l = fermix_amd.slogpf(S, skew_symmetrize=False)
+    assert torch.equal(s.cpu(), sgn.cpu())
+    err = np.abs(_np(l) - _np(lab))
+    print(f"  logabs err {err}", flush=True)
+    assert np.all(err < 1e-12 * n)
+    # a symmetric permutation reverses the order: pf(P S P^T) = det(P) pf(S)
+    perm = torch.arange(n - 1, -1, -1, device=dev)
+    Sp = S[:, perm][:, :, perm].contiguous()
+    sp, lp = fermix_amd.slogpf(Sp, skew_symmetrize=False)
+    dP = (-1.0) ** ((n * (n - 1) // 2) % 2)
+    assert torch.equal(sp.cpu(), dP * sgn.cpu())
+    assert np.all(np.abs(_np(lp) - _np(lab)) < 1e-12 * n)
+    if n < 4096:
+        Sz = S.clone()
+        Sz[0, n // 3, :] = 0.0
+        Sz[0, :, n // 3] = 0.0
+        sz, lz = fermix_amd.slogpf(Sz, skew_symmetrize=False)
+        assert _np(sz)[0] == 0 and np.isneginf(_np(lz)[0])
+        assert torch.equal(sz[1:], s[1:]) and torch.equal(lz[1:], l[1:])
+        o = torch.randn((2, n - 1, n - 1), generator=g, dtype=torch.float64).to(dev)
+        so, lo = fermix_amd.slogpf(o)
+        assert np.all(_np(so) == 0) and np.all(np.isneginf(_np(lo)))

@@ -152,3 +152,37 @@ def test_pf_adjugate_odd_and_empty(dev, kind):
     X = torch.zeros((2, 0, 0), dtype=torch.from_numpy(np.zeros(1, dt)).dtype, device=dev).requires_grad_(True)
     p = fermix_amd.pf(X)
     assert np.all(_np(p) == 1)
+
+
+def test_pf_adjugate_f64_blocked(dev):
+    """float64 above the register kernels (n = 520): a regular member takes pf(S) S^-1 from
+    the blocked LU solves scaled by the Parlett-Reid pf (against float64 numpy), a member
+    with a zero row / column k takes the Parlett-Reid adjugate (rank n - 2: only row and
+    column k nonzero; entries against minor Pfaffians, G[i][j] = (-1)^(i+j) pf(S without
+    i, j) for i < j)."""
+    n, k = 520, 77
+    rng = np.random.default_rng(9600)
+    S = _near_j(rng, 2, n, np.float64)
+    _zero_rows(S, 1, [k])
+    print(f"pf adjugate f64 blocked n={n}", flush=True)
+    St, sign, logabs, G = _pf_adj(S, dev)
+    s0, l0 = fermix_amd.slogpf(St, skew_symmetrize=False)
+    assert torch.equal(sign, s0) and torch.equal(logabs, l0)
+    assert _np(sign)[1] == 0 and np.all(np.isfinite(G))
+    ref = ref64.pf64(S[0]) * np.linalg.inv(S[0])
+    err = relerr(G[0], ref)
+    print(f"  regular relerr {err:.3g}", flush=True)
+    assert err < 1e-10 * n / 16
+    G1 = G[1]
+    off = G1.copy()
+    off[k, :] = 0.0
+    off[:, k] = 0.0
+    assert np.abs(off).max() <= 1e-10 * np.abs(G1).max()
+    assert np.allclose(G1, -G1.T, rtol=0, atol=1e-10 * np.abs(G1).max())
+    for j in (0, 300, n - 1):
+        i, jj = min(k, j), max(k, j)
+        keep = [x for x in range(n) if x not in (i, jj)]
+        want = (-1.0) ** (i + jj) * ref64.pf64(S[1][np.ix_(keep, keep)])
+        got = G1[i, jj]
+        print(f"  G[{i}][{jj}] {got:.10g} vs {want:.10g}", flush=True)
+        assert abs(got - want) <= 1e-9 * abs(want)
