@@ -30,9 +30,11 @@
 //    it is loaded, and the reference's rank-2 correction on the way out).
 // The phase and the log are accumulated in double for both kinds.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "fermix_internal.h"
+#include "field.h"
 
 namespace fx {
 namespace {
@@ -40,81 +42,15 @@ namespace {
 constexpr int CX_MAXN = 4096;
 constexpr size_t CX_LDS_MAX = 60 * 1024;  // matrix bytes kept in LDS
 constexpr int CX_NT = 1024;
+// complex orders above this run the blocked kernels of lu64.hip (LU, solves, Parlett-Reid
+// with the trailing updates on the fp64 MFMA); up to it, the one-workgroup kernels here
+constexpr int CX_BLK_MIN = 64;
 
-template <class T>
-struct cx {
-  T re, im;
-};
-
-// ---- field operations: F = cx<float> / cx<double> (complex kinds) or double (the
-// float64 adjugate, which shares the Gauss-Jordan kernel below)
 template <class F>
-struct Fd;
-template <class T>
-struct Fd<cx<T>> {
-  using R = T;  // real component type (logabs)
-  static __device__ __forceinline__ cx<T> zero() { return {T(0), T(0)}; }
-  static __device__ __forceinline__ cx<T> one() { return {T(1), T(0)}; }
-  static __device__ __forceinline__ bool is0(cx<T> x) { return x.re == T(0) && x.im == T(0); }
-  // pivot magnitude |re| + |im| (LAPACK's cabs1), exact in double for both kinds
-  static __device__ __forceinline__ unsigned long long key(cx<T> x) {
-    return key64((double)(fabs(x.re) + fabs(x.im)));
-  }
-  static __device__ __forceinline__ cx<T> mul(cx<T> a, cx<T> b) {
-    return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
-  }
-  // r - l p with fused products
-  static __device__ __forceinline__ cx<T> fms(cx<T> r, cx<T> l, cx<T> p) {
-    return {fma(-l.re, p.re, fma(l.im, p.im, r.re)), fma(-l.re, p.im, fma(-l.im, p.re, r.im))};
-  }
-  // 1 / x = conj(x) / |x|^2, 0 -> 0
-  static __device__ __forceinline__ cx<T> rcp(cx<T> x) {
-    const T s = x.re * x.re + x.im * x.im;
-    const T inv = s != T(0) ? T(1) / s : T(0);
-    return {x.re * inv, -(x.im * inv)};
-  }
-  static __device__ __forceinline__ bool finite(cx<T> x) { return isfinite(x.re) && isfinite(x.im); }
-  // the pivot's phase and log-modulus, accumulated in double
-  static __device__ __forceinline__ void acc(double2& sgn, double& logabs, cx<T> x) {
-    const double re = x.re, im = x.im, m = hypot(re, im);
-    logabs += log(m);
-    const double ur = re / m, ui = im / m;
-    sgn = make_double2(sgn.x * ur - sgn.y * ui, sgn.x * ui + sgn.y * ur);
-  }
-  static __device__ __forceinline__ cx<T> from(double2 v) { return {T(v.x), T(v.y)}; }
-  static __device__ __forceinline__ double2 to2(cx<T> x) { return make_double2(x.re, x.im); }
-  // the modulus |x| (the Pfaffian adjugate's choice of the smallest pivot), in double
-  static __device__ __forceinline__ double mag(cx<T> x) { return hypot((double)x.re, (double)x.im); }
-  static __device__ __forceinline__ cx<T> add(cx<T> a, cx<T> b) { return {a.re + b.re, a.im + b.im}; }
-  static __device__ __forceinline__ cx<T> sub(cx<T> a, cx<T> b) { return {a.re - b.re, a.im - b.im}; }
-};
-template <>
-struct Fd<double> {
-  using R = double;
-  static __device__ __forceinline__ double zero() { return 0.0; }
-  static __device__ __forceinline__ double one() { return 1.0; }
-  static __device__ __forceinline__ bool is0(double x) { return x == 0.0; }
-  static __device__ __forceinline__ unsigned long long key(double x) { return key64(x); }
-  static __device__ __forceinline__ double mul(double a, double b) { return a * b; }
-  static __device__ __forceinline__ double fms(double r, double l, double p) { return fma(-l, p, r); }
-  static __device__ __forceinline__ double rcp(double x) { return x != 0.0 ? 1.0 / x : 0.0; }
-  static __device__ __forceinline__ bool finite(double x) { return isfinite(x); }
-  // the float64 kernels' order: log|d| added in pivot order, the sign flipped per
-  // negative pivot
-  static __device__ __forceinline__ void acc(double2& sgn, double& logabs, double x) {
-    logabs += log(fabs(x));
-    if (x < 0.0) sgn.x = -sgn.x;
-  }
-  static __device__ __forceinline__ double from(double2 v) { return v.x; }
-  static __device__ __forceinline__ double2 to2(double x) { return make_double2(x, 0.0); }
-  static __device__ __forceinline__ double mag(double x) { return fabs(x); }
-  static __device__ __forceinline__ double add(double a, double b) { return a + b; }
-  static __device__ __forceinline__ double sub(double a, double b) { return a - b; }
-};
-
-__device__ __forceinline__ double2 c2mul(double2 a, double2 b) {
-  return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+bool blocked(int n) {
+  return !std::is_same<F, double>::value && n > CX_BLK_MIN;
 }
+
 
 template <class F>
 __device__ __forceinline__ void write_sl(F* sign_out, typename Fd<F>::R* logabs_out, int64_t b, bool singular,
@@ -125,11 +61,6 @@ __device__ __forceinline__ void write_sl(F* sign_out, typename Fd<F>::R* logabs_
 }
 
 // S (skew != 0: (a - a^T) / 2) into M with row stride ld; with ident, M[:, n:2n] = I.
-template <class T>
-__device__ __forceinline__ cx<T> half_diff(cx<T> v, cx<T> u) {
-  return {(v.re - u.re) * T(0.5), (v.im - u.im) * T(0.5)};
-}
-__device__ __forceinline__ double half_diff(double v, double u) { return (v - u) * 0.5; }
 
 template <class F>
 __device__ __forceinline__ void cload(const F* __restrict__ a, int n, int skew, F* M, int ld, bool ident) {
@@ -709,11 +640,21 @@ int cx_empty(void* sign, void* logabs, int64_t batch, hipStream_t s) {
 
 template <class F>
 size_t slogdet_ws(int64_t batch, int n) {
-  return n > CX_MAXN ? 0 : cx_matrix_ws<F>(batch, n, n);
+  if (n > CX_MAXN) return 0;
+  return blocked<F>(n) ? blk_lu_workspace<F>(batch, n) : cx_matrix_ws<F>(batch, n, n);
 }
 template <class F>
 size_t slogdet_parts_ws(int64_t batch, int n) {
-  return n > CX_MAXN ? 0 : cx_matrix_ws<F>(batch, n, 2 * n);
+  if (n > CX_MAXN) return 0;
+  return blocked<F>(n) ? blk_lu_inverse_workspace<F>(batch, n) : cx_matrix_ws<F>(batch, n, 2 * n);
+}
+// det's gradient: blocked, the LU solves plus the Gauss-Jordan run for the singular members
+// (its [A | I] and its sign / logabs in scratch)
+template <class F>
+size_t det_parts_ws(int64_t batch, int n) {
+  if (n > CX_MAXN || !blocked<F>(n) || batch <= 0) return slogdet_parts_ws<F>(batch, n);
+  return align_up(blk_lu_inverse_workspace<F>(batch, n)) + align_up(cx_matrix_ws<F>(batch, n, 2 * n)) +
+         align_up((size_t)batch * 2 * sizeof(F));
 }
 
 template <class F>
@@ -721,6 +662,8 @@ int slogdet(const void* a, int64_t batch, int n, void* sign, void* logabs, void*
   const int st = check_cx_args<F>(a, batch, n, sign, logabs, nullptr, ws);
   if (st != FX_OK || batch == 0) return st;
   if (n == 0) return cx_empty<F>(sign, logabs, batch, s);
+  using R = typename Kind<F>::R;
+  if (blocked<F>(n)) return blk_lu<F>((const F*)a, n, batch, (F*)sign, (R*)logabs, ws, wsb, s);
   return launch_cgj<F>(a, n, 0, batch, sign, logabs, nullptr, GJ_FWD, 0, nullptr, ws, wsb, s);
 }
 
@@ -730,6 +673,12 @@ int slogdet_parts(const void* a, int64_t batch, int n, void* sign, void* logabs,
   const int st = check_cx_args<F>(a, batch, n, sign, logabs, inv_t, ws);
   if (st != FX_OK || batch == 0) return st;
   if (n == 0) return cx_empty<F>(sign, logabs, batch, s);
+  using R = typename Kind<F>::R;
+  if (blocked<F>(n)) {
+    if (!inv_t) return blk_lu<F>((const F*)a, n, batch, (F*)sign, (R*)logabs, ws, wsb, s);
+    return blk_lu_inverse<F>((const F*)a, n, 0, batch, (F*)sign, (R*)logabs, nullptr, nullptr, nullptr, (F*)inv_t, 1,
+                             ws, wsb, s);
+  }
   if (!inv_t) return launch_cgj<F>(a, n, 0, batch, sign, logabs, nullptr, GJ_FWD, 0, nullptr, ws, wsb, s);
   return launch_cgj<F>(a, n, 0, batch, sign, logabs, inv_t, GJ_INV, 1, nullptr, ws, wsb, s);
 }
@@ -742,6 +691,17 @@ int det_parts(const void* a, int64_t batch, int n, void* sign, void* logabs, voi
   if (st != FX_OK || batch == 0) return st;
   if (n > 0 && !adj_t) return FX_ERR_INVALID_ARGUMENT;
   if (n == 0) return cx_empty<F>(sign, logabs, batch, s);
+  if (blocked<F>(n)) {  // as det_parts_f64 below: the regular members from the LU solves
+    using R = typename Kind<F>::R;
+    if (!ws || wsb < det_parts_ws<F>(batch, n)) return FX_ERR_WORKSPACE;
+    const size_t lw = align_up(blk_lu_inverse_workspace<F>(batch, n)), gw = align_up(cx_matrix_ws<F>(batch, n, 2 * n));
+    char* base = (char*)ws;
+    const int r = blk_lu_inverse<F>((const F*)a, n, 0, batch, (F*)sign, (R*)logabs, nullptr, (const F*)sign,
+                                    (const R*)logabs, (F*)adj_t, 1, base, lw, s);
+    if (r != FX_OK) return r;
+    F* gsign = (F*)(base + lw + gw);
+    return launch_cgj<F>(a, n, 0, batch, gsign, gsign + batch, adj_t, GJ_ADJ, 1, sign, base + lw, gw, s);
+  }
   return launch_cgj<F>(a, n, 0, batch, sign, logabs, adj_t, GJ_ADJ, 1, nullptr, ws, wsb, s);
 }
 
@@ -773,7 +733,14 @@ int det_parts_f64(const double* a, int64_t batch, int n, double* sign, double* l
 
 template <class T>
 size_t slogpf_ws(int64_t batch, int n) {
-  return n > CX_MAXN ? 0 : cx_matrix_ws<cx<T>>(batch, n, n);
+  if (n > CX_MAXN) return 0;
+  return blocked<cx<T>>(n) ? blk_pr_workspace<cx<T>>(batch, n) : cx_matrix_ws<cx<T>>(batch, n, n);
+}
+
+template <class T>
+int launch_pf(const T* a, int n, int skew, int64_t batch, T* sign, T* logabs, void* ws, size_t wsb, hipStream_t s) {
+  if (blocked<cx<T>>(n)) return blk_pr<cx<T>>((const cx<T>*)a, n, skew, batch, (cx<T>*)sign, logabs, ws, wsb, s);
+  return launch_cpr<T>(a, n, skew, batch, sign, logabs, ws, wsb, s);
 }
 
 // The Pfaffian adjugate's workspace: the Parlett-Reid matrix and then [T~ | I] (the same
@@ -831,7 +798,12 @@ int pf_adjugate(const F* a, int64_t batch, int n, int skew, F* g, void* ws, size
 template <class T>
 size_t slogpf_parts_ws(int64_t batch, int n) {
   if (n > CX_MAXN || batch <= 0) return 0;
-  const size_t inv = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n)) + align_up((size_t)batch * 3 * sizeof(T));
+  const size_t scratch = align_up((size_t)batch * 3 * sizeof(T));
+  if (blocked<cx<T>>(n)) {
+    const size_t inv = align_up(blk_lu_inverse_workspace<cx<T>>(batch, n)) + scratch;
+    return align_up(slogpf_ws<T>(batch, n)) + std::max(inv, pf_adjugate_ws<cx<T>>(batch, n));
+  }
+  const size_t inv = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n)) + scratch;
   return align_up(slogpf_ws<T>(batch, n)) + std::max(inv, pf_adjugate_ws<cx<T>>(batch, n));
 }
 
@@ -840,7 +812,7 @@ int slogpf(const T* a, int64_t batch, int n, int skew, T* sign, T* logabs, void*
   const int st = check_cx_args<cx<T>>(a, batch, n, sign, logabs, nullptr, ws);
   if (st != FX_OK || batch == 0) return st;
   if (n == 0) return cx_empty<cx<T>>(sign, logabs, batch, s);
-  return launch_cpr<T>(a, n, skew != 0, batch, sign, logabs, ws, wsb, s);
+  return launch_pf<T>(a, n, skew != 0, batch, sign, logabs, ws, wsb, s);
 }
 
 // The Parlett-Reid run for sign / logabs, then g: S^-1 by Gauss-Jordan on the same S
@@ -856,12 +828,24 @@ int slogpf_parts(const T* a, int64_t batch, int n, int skew, int adjugate, T* si
   if (wsb < slogpf_parts_ws<T>(batch, n) || (!ws && slogpf_parts_ws<T>(batch, n))) return FX_ERR_WORKSPACE;
   const size_t pr = align_up(slogpf_ws<T>(batch, n));
   char* base = (char*)ws;
-  st = launch_cpr<T>(a, n, skew != 0, batch, sign, logabs, base, pr, s);
+  st = launch_pf<T>(a, n, skew != 0, batch, sign, logabs, base, pr, s);
   if (st != FX_OK) return st;
-  if (adjugate) {
-    if (n & 1) return cx_zero<cx<T>>((cx<T>*)g, batch * (int64_t)n * n, s);
-    return pf_adjugate<cx<T>>((const cx<T>*)a, batch, n, skew != 0, (cx<T>*)g, base + pr, wsb - pr, s);
+  if (adjugate && (n & 1)) return cx_zero<cx<T>>((cx<T>*)g, batch * (int64_t)n * n, s);
+  if (blocked<cx<T>>(n)) {
+    // S^-1 (adjugate: pf(S) S^-1 of the members with pf != 0) from the blocked LU solves,
+    // zero where pf = 0; the adjugate of those from the Parlett-Reid run below
+    const cx<T>* A = (const cx<T>*)a;
+    const cx<T>* sg = (const cx<T>*)sign;
+    const size_t lw = align_up(blk_lu_inverse_workspace<cx<T>>(batch, n));
+    cx<T>* gsign = (cx<T>*)(base + pr + lw);
+    T* glog = (T*)(gsign + batch);
+    st = blk_lu_inverse<cx<T>>(A, n, skew != 0, batch, gsign, glog, sg, adjugate ? sg : nullptr,
+                               adjugate ? logabs : nullptr, (cx<T>*)g, 0, base + pr, lw, s);
+    if (st != FX_OK || !adjugate) return st;
+    return pf_adjugate<cx<T>>(A, batch, n, skew != 0, (cx<T>*)g, base + pr, wsb - pr, s, sg);
   }
+  if (adjugate)
+    return pf_adjugate<cx<T>>((const cx<T>*)a, batch, n, skew != 0, (cx<T>*)g, base + pr, wsb - pr, s);
   const size_t gj = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n));
   T* gsign = (T*)(base + pr + gj);
   T* glog = gsign + 2 * batch;
@@ -954,8 +938,8 @@ int fx_slogpf_parts_c128(const double* a, int64_t batch, int32_t n, int32_t skew
                               workspace_bytes, (hipStream_t)stream);
 }
 
-size_t fx_det_parts_c64_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<float>>(batch, n); }
-size_t fx_det_parts_c128_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<double>>(batch, n); }
+size_t fx_det_parts_c64_workspace(int64_t batch, int32_t n) { return det_parts_ws<cx<float>>(batch, n); }
+size_t fx_det_parts_c128_workspace(int64_t batch, int32_t n) { return det_parts_ws<cx<double>>(batch, n); }
 size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n) { return det_parts_f64_ws(batch, n); }
 
 int fx_det_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,

@@ -189,3 +189,45 @@ def test_complex_singular_odd_and_det_pf(dev, kind):
     assert torch.equal(s4.reshape(-1), st) and torch.equal(l4.reshape(-1), lt)
     sv, lv = torch.func.vmap(fermix_amd.slogdet)(A4)
     assert torch.equal(sv.reshape(-1), st) and torch.equal(lv.reshape(-1), lt)
+
+
+@pytest.mark.parametrize("kind", ["c64", "c128"])
+def test_complex_blocked_large(dev, kind):
+    """The blocked complex kernels at n = 1030 (padded order 1056, 1024-thread panels):
+    slogdet of X = I + N(0, 1/(4n)) (both parts) against numpy's complex128 slogdet, A^-T
+    through its residual X^T A^-T - I (complex128 on the CPU), and pf(X J X^T) = det(X)
+    with its S^-1 residual; a zero row / column gives pf = 0 and leaves the other member's
+    bits unchanged."""
+    nd, td = DT[kind]
+    n = 1030
+    rng = np.random.default_rng(9800)
+    X = (np.eye(n) + 0.5 * _crandn(rng, (2, n, n), np.complex128) / np.sqrt(n)).astype(nd)
+    Xw = X.astype(np.complex128)
+    tol, gtol = _tols(kind, n)
+    print(f"complex blocked {kind} n={n}", flush=True)
+    s, l = fermix_amd.slogdet(torch.from_numpy(X).to(dev))
+    sr, lr = np.linalg.slogdet(Xw)
+    assert np.all(np.abs(_np(s) - sr) < tol) and np.all(np.abs(_np(l) - lr) < tol * max(1.0, np.abs(lr).max()))
+    from fermix_amd import _kernels
+    _, _, invT = _kernels.slogdet_parts(torch.from_numpy(X).to(dev))[:3]
+    res = np.swapaxes(Xw, 1, 2) @ _np(invT).astype(np.complex128) - np.eye(n)
+    print(f"  A^-T residual {np.abs(res).max():.3g}", flush=True)
+    assert np.abs(res).max() < gtol
+    J = np.zeros((n, n))
+    J[np.arange(0, n, 2), np.arange(1, n, 2)] = 1.0
+    J[np.arange(1, n, 2), np.arange(0, n, 2)] = -1.0
+    S = Xw @ J @ np.swapaxes(Xw, 1, 2)
+    S = (0.5 * (S - np.swapaxes(S, 1, 2))).astype(nd)
+    St = torch.from_numpy(S).to(dev)
+    ps, pl = fermix_amd.slogpf(St, skew_symmetrize=False)
+    assert np.all(np.abs(_np(ps) - sr) < 10 * tol) and np.all(np.abs(_np(pl) - lr) < 10 * tol * max(1.0, np.abs(lr).max()))
+    _, _, Sinv = _kernels.slogpf_parts(St, False)
+    res = S.astype(np.complex128) @ _np(Sinv).astype(np.complex128) - np.eye(n)
+    print(f"  S^-1 residual {np.abs(res).max():.3g}", flush=True)
+    assert np.abs(res).max() < 10 * gtol
+    Sz = St.clone()
+    Sz[0, 7, :] = 0
+    Sz[0, :, 7] = 0
+    zs, zl = fermix_amd.slogpf(Sz, skew_symmetrize=False)
+    assert _np(zs)[0] == 0 and np.isneginf(_np(zl)[0])
+    assert torch.equal(zs[1], ps[1]) and torch.equal(zl[1], pl[1])
