@@ -346,9 +346,11 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
  * of largest |re| + |im| (LAPACK's cabs1, the reference's `abs1`), sign = parity *
  * prod(d / |d|), logabs = sum log|d|, an exactly zero pivot gives sign 0 and logabs -inf;
  * inv_t = A^-T without conjugation (the holomorphic derivative of log det, as in
- * `_lu_parts_generic`, :63-97). Unblocked kernels, one workgroup per matrix, the matrix in
- * LDS when it fits (else one copy per member in the workspace; twice that with the
- * inverse), 0 <= n <= 4096. */
+ * `_lu_parts_generic`, :63-97). 0 <= n <= 4096. Up to n = 64 one workgroup per matrix,
+ * the matrix in LDS when it fits (else one copy per member in the workspace; twice that
+ * with the inverse); above, the blocked kernels of the float64 path on the complex field
+ * (32-column LU panels, 16-pair Parlett-Reid panels, the trailing updates as four real
+ * fp64 MFMA products per complex one, complex64 operands widened to double in them). */
 size_t fx_slogdet_c64_workspace(int64_t batch, int32_t n);
 int fx_slogdet_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream);
@@ -404,11 +406,11 @@ int fx_slogpf_parts_c128(const double* a, int64_t batch, int32_t n, int32_t skew
  * sgn(P) d_K c (U~^-1 e_k1)(e_km^T U~^-1 L^-1 P) with c = (U~^-1)[k1, km] for m = 2 and 1
  * for m = 1; 0 for m >= 3 and for a non-finite result. Replaces `_det_gradT` with `_lu_det`
  * and `_perm_sign` (src/fermix/_diff.py:160-246) for the 64-bit and complex kinds. One
- * workgroup per matrix; the workspace is that of the _parts entry points (none while
- * [A | I] fits in 60 KiB of LDS). For float64 the sign / logabs equal fx_slogdet_f64's
- * bits (the same pivots and per-element updates; above n = 128 the blocked LU's, whose
- * solves give the regular members' det(A) A^-T, the Gauss-Jordan continuation then
- * running only for the exactly singular members). */
+ * workgroup per matrix up to n = 128 (float64) / 64 (complex; no workspace while [A | I]
+ * fits in 60 KiB of LDS); above, the blocked LU, whose solves give the regular members'
+ * det(A) A^-T, the Gauss-Jordan continuation then running only for the exactly singular
+ * members. The sign / logabs equal those of fx_slogdet_f64 / _c64 / _c128 (the same
+ * pivots and per-element updates). */
 size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n);
 int fx_det_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
                      void* workspace, size_t workspace_bytes, fx_stream_t stream);
