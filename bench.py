@@ -39,7 +39,8 @@ def _parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--only", default=None, help="comma list of workloads (c1,c2,c3,c4; f64 adds the float64 "
-                   "n = 128 workloads, reported on stderr)")
+                   "n = 128 workloads, blk the blocked float64 / complex ones at n = 512, both reported "
+                   "on stderr)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
@@ -271,6 +272,32 @@ def bench_f64(steps, warmup):
     return out
 
 
+def bench_blocked(steps, warmup):
+    """The blocked float64 / complex kernels (lu64.hip) at B = 32, n = 512: the value and
+    gradient factors (sign, logabs and A^-T or S^-1) of slogdet and slogpf in float64,
+    complex64 and complex128, on the C3-shaped inputs (complex: a second draw as the
+    imaginary part)."""
+    import torch
+    from fermix_amd import _kernels
+
+    B, n = 32, 512
+    re = _inputs(B, n, 0).astype(np.float64)
+    im = _inputs(B, n, 1).astype(np.float64)
+    out = {}
+    for kind, arr in [("f64", re), ("c64", (re + 1j * im).astype(np.complex64)),
+                      ("c128", re + 1j * im)]:
+        A = torch.from_numpy(np.ascontiguousarray(arr)).cuda()
+        S = (A - A.transpose(1, 2)).contiguous()
+        esz = A.element_size()
+        for name, fn in [(f"blk_{kind}_slogdet_parts", lambda: _kernels.slogdet_parts(A)),
+                         (f"blk_{kind}_slogpf_parts", lambda: _kernels.slogpf_parts(S, False))]:
+            ms, wall = _time_gpu(fn, steps, warmup)
+            out[name] = dict(name=name, B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
+                             bytes=B * 2 * esz * n * n, sample=None)
+        del A, S
+    return out
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -354,6 +381,11 @@ def main():
             res[k] = r
             print(f"# {k}: {r['ms']:.4f} ms/step ({r['rate']:.4g} matrices/s)", file=sys.stderr,
                   flush=True)
+    if "blk" in only:
+        for k, r in bench_blocked(max(3, args.steps // 4), max(1, args.warmup // 2)).items():
+            res[k] = r
+            print(f"# {k}: {r['ms']:.4f} ms/step ({r['rate']:.4g} matrices/s)", file=sys.stderr,
+                  flush=True)
     if args.copy_probe:
         x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda").fill_(1.0)
         for _ in range(3):
@@ -361,7 +393,7 @@ def main():
         torch.cuda.synchronize()
         del x, y
     head = (res.get("c2") or res.get("c1") or res.get("c3") or res.get("c4")
-            or res.get("f64_slogpf_fwd"))
+            or res.get("f64_slogpf_fwd") or res.get("blk_f64_slogdet_parts"))
     achieved = head["bytes"] / (head["ms"] * 1e-3) / 1e9
     roofline = {
         "bound": "hbm",
@@ -389,7 +421,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64" if head["name"].startswith("f64") else "f32",
+        "dtype": "f64" if head["name"].startswith(("f64", "blk_f64")) else "f32",
         "data": "synthetic (numpy default_rng(0) N(0,1); jax.random absent)",
         "config": {"workload": f"{head['name']} B={head['B']} n={head['n']}", "B": head["B"],
                    "n": head["n"], "skew_symmetrize": True if head is res.get("c2") else None,

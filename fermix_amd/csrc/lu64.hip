@@ -114,6 +114,74 @@ __global__ __launch_bounds__(NT) void lu64_panel_kernel(F* __restrict__ W, int N
   if (tid == 0) nsw[b * (N / P64) + r0 / P64] = swaps;
 }
 
+// The same panel with its rows in registers (m = N - r0 <= NTR: thread t holds row r0 + t,
+// columns r0 .. r0 + 31; NTR = 1024 only for 8-byte elements, whose 32-entry rows fit the
+// 128 registers of a 1024-thread workgroup): per column step one workgroup argmax, the
+// pivot row and row c
+// posted through LDS and exchanged by their owners, then the multipliers and the rank-1
+// update in registers -- the arithmetic of lu64_panel_kernel element for element (same
+// pivots, same rounding), without its global stores and reloads between column steps.
+template <class F, int NTR>
+__global__ __launch_bounds__(NTR) void lu64_panel_reg_kernel(F* __restrict__ W, int N, int r0,
+                                                             int* __restrict__ ipiv, F* __restrict__ dpiv,
+                                                             int* __restrict__ nsw) {
+  using D = Fd<F>;
+  __shared__ unsigned long long redk[2][NTR / 64];
+  __shared__ int redr[2][NTR / 64];
+  __shared__ F prow[P64], crow[P64];
+  const int64_t b = blockIdx.x;
+  F* Wb = W + b * (int64_t)N * N;
+  const int tid = threadIdx.x;
+  const int r = r0 + tid;
+  const bool own = r < N;
+  F a[P64];
+#pragma unroll
+  for (int q = 0; q < P64; ++q) a[q] = own ? Wb[(int64_t)r * N + r0 + q] : D::zero();
+  int swaps = 0;
+  // column steps with compile-time j (the row stays in registers, no dynamic index)
+  static_for<0, P64>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    const int c = r0 + j;
+    const unsigned long long k = own && tid >= j ? D::key(a[j]) : 0ull;
+    const int p = block_argmax<NTR>(k, own ? r : 0x7fffffff, redk[j & 1], redr[j & 1]);  // >= c
+    if (r == p) {
+#pragma unroll
+      for (int q = 0; q < P64; ++q) prow[q] = a[q];
+    }
+    if (tid == j && p != c) {
+#pragma unroll
+      for (int q = 0; q < P64; ++q) crow[q] = a[q];
+    }
+    __syncthreads();
+    if (p != c) {
+      ++swaps;
+      if (tid == j) {
+#pragma unroll
+        for (int q = 0; q < P64; ++q) a[q] = prow[q];
+      } else if (r == p) {
+#pragma unroll
+        for (int q = 0; q < P64; ++q) a[q] = crow[q];
+      }
+    }
+    const F d = prow[j];
+    if (tid == 0) {
+      ipiv[b * N + c] = p;
+      dpiv[b * N + c] = d;
+    }
+    if (own && tid > j) {
+      const F l = D::mul(a[j], D::rcp(d));
+      a[j] = l;
+#pragma unroll
+      for (int q = j + 1; q < P64; ++q) a[q] = D::fms(a[q], l, prow[q]);
+    }
+  });
+  if (own) {
+#pragma unroll
+    for (int q = 0; q < P64; ++q) Wb[(int64_t)r * N + r0 + q] = a[q];
+  }
+  if (tid == 0) nsw[b * (N / P64) + r0 / P64] = swaps;
+}
+
 // 32 rows r0 .. r0 + 31 of a target matrix T, columns c0 + 256 cb + tid (< cend), against
 // the diagonal block D = W[r0 .. r0 + 31][r0 .. r0 + 31] of the factorisation:
 //   MODE 0 / 1: the panel's row swaps (row r0 + j with ipiv[r0 + j] >= r0 + j, in order),
@@ -492,10 +560,16 @@ int lu64_factor(const F* A, int n, int skew, int64_t batch, const Lu64Bufs<F>& f
   lu64_copy_kernel<F><<<dim3(grid_of(total)), 256, 0, s>>>(A, n, skew, f.W, N, total, 0);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   for (int r0 = 0; r0 < N; r0 += P64) {
-    if (N > 512)  // latency-bound column steps: more threads per matrix
+    bool in_regs = N - r0 <= 512;  // the panel's rows in registers
+    if (in_regs) {
+      lu64_panel_reg_kernel<F, 512><<<dim3((unsigned)batch), 512, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
+    } else if constexpr (sizeof(F) == 8) {
+      in_regs = N - r0 <= 1024;
+      if (in_regs)
+        lu64_panel_reg_kernel<F, 1024><<<dim3((unsigned)batch), 1024, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
+    }
+    if (!in_regs)  // latency-bound column steps on rows in memory: more threads per matrix
       lu64_panel_kernel<F, 1024><<<dim3((unsigned)batch), 1024, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
-    else
-      lu64_panel_kernel<F, NT64><<<dim3((unsigned)batch), NT64, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     const int r1 = r0 + P64;
     if (r1 >= N) break;
