@@ -228,3 +228,28 @@ def test_f64_slogpf_blocked_large(dev, n):
         o = torch.randn((2, n - 1, n - 1), generator=g, dtype=torch.float64).to(dev)
         so, lo = fermix_amd.slogpf(o)
         assert np.all(_np(so) == 0) and np.all(np.isneginf(_np(lo)))
+
+
+def test_f64_slogdet_blocked_large(dev):
+    """n = 2050 (padded order 2080): the LU panels with their rows in memory (m > 1024) and
+    then in registers, slogdet against torch's float64 slogdet on the GPU, A^-T through its
+    float64 residual A^T A^-T - I, and the det adjugate det(A) A^-T of the same run."""
+    n = 2050
+    g = torch.Generator(device="cpu").manual_seed(9950)
+    A = (torch.eye(n, dtype=torch.float64) + 0.5 * torch.randn((1, n, n), generator=g, dtype=torch.float64)
+         / np.sqrt(n)).to(dev)
+    print(f"f64 slogdet blocked n={n}", flush=True)
+    s, l = fermix_amd.slogdet(A)
+    sr, lr = torch.linalg.slogdet(A)
+    assert torch.equal(s.cpu(), sr.cpu())
+    assert abs(l.item() - lr.item()) < 1e-12 * n
+    s2, l2, invT, _, _ = _kernels.slogdet_parts(A)
+    assert torch.equal(s2, s) and torch.equal(l2, l)
+    R = A[0].transpose(0, 1) @ invT[0] - torch.eye(n, dtype=torch.float64, device=dev)
+    err = (torch.linalg.norm(R) / np.sqrt(n)).item()
+    print(f"  A^-T residual {err:.3g}", flush=True)
+    assert err < 1e-12
+    Ad = A.clone().requires_grad_()
+    d = fermix_amd.det(Ad)
+    (gd,) = torch.autograd.grad(d.sum(), Ad)
+    assert np.allclose(_np(gd), _np(d)[:, None, None] * _np(invT), rtol=1e-10, atol=0)
