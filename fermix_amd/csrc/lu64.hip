@@ -708,6 +708,140 @@ __global__ __launch_bounds__(NT) void pr64_panel_kernel(F* __restrict__ W, int N
   }
 }
 
+// The same panel with the panel's (U, V) entries in registers (m = N - r0 <= NTR: thread
+// t owns position r0 + t, its U / V entries of the pair steps so far and its entry of the
+// current row c): the left-looking sums read registers instead of the (U, V) block, the
+// swap exchanges the two positions' registers through LDS, and the block is written once
+// at the end -- the arithmetic of pr64_panel_kernel element for element.
+template <class F, int NTR>
+__global__ __launch_bounds__(NTR) void pr64_panel_reg_kernel(F* __restrict__ W, int N, int r0, F* __restrict__ Ar,
+                                                             F* __restrict__ Bk, double* __restrict__ lacc,
+                                                             double2* __restrict__ sacc, int* __restrict__ stat) {
+  using D = Fd<F>;
+  __shared__ unsigned long long redk[2][NTR / 64];
+  __shared__ int redr[2][NTR / 64];
+  __shared__ F cu[PRB], cv[PRB];
+  __shared__ F xs[2][2 * PRB + 1];
+  __shared__ F dsh;
+  const int64_t b = blockIdx.x;
+  if (stat[b]) return;
+  const int tid = threadIdx.x;
+  const int x = r0 + tid;
+  const bool own = x < N;
+  F* Wb = W + b * (int64_t)N * N;
+  F u[PRB], v[PRB];
+#pragma unroll
+  for (int j = 0; j < PRB; ++j) u[j] = v[j] = D::zero();
+  F rcx = D::zero();
+  double lg = 0.0;  // thread 0's running sums, in pivot order
+  double2 sg = make_double2(1.0, 0.0);
+  bool sing = false;
+  static_for<0, PRB>([&](auto pc) {
+    constexpr int p = decltype(pc)::value;
+    if (sing) return;
+    const int c = r0 + 2 * p, q = c + 1;
+    if (x == c) {
+#pragma unroll
+      for (int j = 0; j < p; ++j) {
+        cu[j] = u[j];
+        cv[j] = v[j];
+      }
+    }
+    __syncthreads();
+    unsigned long long k = 0;
+    if (own && x > c) {
+      F a = Wb[(int64_t)c * N + x];
+#pragma unroll
+      for (int j = 0; j < p; ++j) {
+        a = D::fms(a, cu[j], v[j]);
+        a = D::fms(a, D::neg(cv[j]), u[j]);
+      }
+      rcx = a;
+      k = D::key(a);
+    }
+    const int pv = block_argmax<NTR>(k, own && x > c ? x : 0x7fffffff, redk[p & 1], redr[p & 1]);
+    if (pv != q) {
+      for (int y = q + tid; y < N; y += NTR) {
+        const F a = Wb[(int64_t)pv * N + y], e = Wb[(int64_t)q * N + y];
+        Wb[(int64_t)pv * N + y] = e;
+        Wb[(int64_t)q * N + y] = a;
+      }
+      if (x == pv || x == q) {
+        F* o = xs[x == q];
+#pragma unroll
+        for (int j = 0; j < p; ++j) {
+          o[j] = u[j];
+          o[PRB + j] = v[j];
+        }
+        o[2 * PRB] = rcx;
+      }
+      if (tid == 0) sg = make_double2(-sg.x, -sg.y);
+      __syncthreads();
+      if (x == pv || x == q) {
+        const F* o = xs[x == pv];
+#pragma unroll
+        for (int j = 0; j < p; ++j) {
+          u[j] = o[j];
+          v[j] = o[PRB + j];
+        }
+        rcx = o[2 * PRB];
+      }
+      for (int r = q + tid; r < N; r += NTR) {
+        const F a = Wb[(int64_t)r * N + pv], e = Wb[(int64_t)r * N + q];
+        Wb[(int64_t)r * N + pv] = e;
+        Wb[(int64_t)r * N + q] = a;
+      }
+    }
+    __syncthreads();
+    if (x == q) {
+#pragma unroll
+      for (int j = 0; j < p; ++j) {
+        cu[j] = u[j];
+        cv[j] = v[j];
+      }
+      dsh = rcx;
+    }
+    __syncthreads();
+    const F d = dsh;
+    if (D::is0(d)) {  // row c is zero beyond c: pf = 0
+      sing = true;
+      return;
+    }
+    const F rd = D::rcp(d);
+    F un = D::zero(), vn = D::zero();
+    if (own && x > q) {
+      F a = Wb[(int64_t)q * N + x];
+#pragma unroll
+      for (int j = 0; j < p; ++j) {
+        a = D::fms(a, cu[j], v[j]);
+        a = D::fms(a, D::neg(cv[j]), u[j]);
+      }
+      vn = a;
+      un = D::mul(rcx, rd);
+    }
+    u[p] = un;
+    v[p] = vn;
+    if (tid == 0) D::acc(sg, lg, d);
+    __syncthreads();
+  });
+  if (own && !sing) {
+    F* Ab = Ar + b * (int64_t)N * P64;
+    F* Bb = Bk + b * (int64_t)P64 * N;
+#pragma unroll
+    for (int j = 0; j < PRB; ++j) {
+      Ab[(int64_t)x * P64 + j] = u[j];
+      Ab[(int64_t)x * P64 + PRB + j] = D::neg(v[j]);
+      Bb[(int64_t)j * N + x] = v[j];
+      Bb[(int64_t)(PRB + j) * N + x] = u[j];
+    }
+  }
+  if (tid == 0) {
+    if (sing) stat[b] = 1;
+    lacc[b] += lg;
+    sacc[b] = c2mul(sacc[b], sg);
+  }
+}
+
 __global__ void pr64_init_kernel(double* __restrict__ lacc, double2* __restrict__ sacc, int* __restrict__ stat,
                                  int64_t batch) {
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -862,11 +996,17 @@ int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logab
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   const int64_t NN = (int64_t)N * N, NP = (int64_t)N * P64;
   for (int r0 = 0; r0 < N; r0 += P64) {
-    if (N > 512)  // latency-bound column loops: more threads per matrix
+    // the panel's (U, V) in registers for 8-byte elements up to 512 rows (the 16-byte
+    // complex128 entries, and 1024-thread workgroups, would spill)
+    bool in_regs = false;
+    if constexpr (sizeof(F) == 8) {
+      in_regs = N - r0 <= 512;
+      if (in_regs)
+        pr64_panel_reg_kernel<F, 512><<<dim3((unsigned)batch), 512, 0, s>>>(f.W, N, r0, f.Ar, f.Bk, f.lacc, f.sacc,
+                                                                            f.stat);
+    }
+    if (!in_regs)  // latency-bound column loops: more threads per matrix
       pr64_panel_kernel<F, 1024><<<dim3((unsigned)batch), 1024, 0, s>>>(f.W, N, r0, f.Ar, f.Bk, f.rc, f.lacc, f.sacc,
-                                                                        f.stat);
-    else
-      pr64_panel_kernel<F, NT64><<<dim3((unsigned)batch), NT64, 0, s>>>(f.W, N, r0, f.Ar, f.Bk, f.rc, f.lacc, f.sacc,
                                                                         f.stat);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     const int r1 = r0 + P64;
