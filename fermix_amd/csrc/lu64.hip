@@ -7,21 +7,23 @@
 // magnitude of a complex value is |re| + |im|, its sign the product of the pivots'
 // phases d / |d|. The matrix is copied into a workspace of padded order N (a
 // multiple of 32, identity padding) and factored in place, 32 columns per block:
-//   1. lu64_panel_kernel (one workgroup per matrix): the 32 columns of rows >= r0, one
-//      column step at a time -- the pivot is the row of largest |x| among rows >= c
-//      (lowest row on ties), swapped into row c over the panel's columns, then the
-//      multipliers and the rank-1 update of the panel's remaining columns;
+//   1. lu64_panel_reg_kernel / lu64_panel_kernel (one workgroup per matrix): the 32
+//      columns of rows >= r0, one column step at a time -- the pivot is the row of
+//      largest |x| among rows >= c (lowest row on ties), swapped into row c over the
+//      panel's columns, then the multipliers and the rank-1 update of the panel's
+//      remaining columns; with the rows in registers up to 512 rows (1024 for 8-byte
+//      elements), else in memory;
 //   2. lu64_rows_kernel<0> (matrix x 256 trailing columns): the panel's row swaps on the
 //      trailing columns and U12 = L11^-1 A12 by forward substitution (L11 in LDS);
-//   3. lu64_gemm_kernel (matrix x 64 x 64 tile): A22 -= L21 U12 at K = 32, the products
-//      in an accumulator of their own, subtracted from A22 in fp64 at the end;
+//   3. lu64_gemm_kernel / lucx_gemm_kernel (matrix x 64 x 64 tile): A22 -= L21 U12 at
+//      K = 32, the products in accumulators of their own, subtracted from A22 at the end;
 //   4. lu64_finish_kernel: sign = (-1)^swaps * prod sign(d), logabs = sum log|d| in
 //      pivot order (one wave, lane-strided partial sums and a fixed tree).
-// The column steps of a panel are latency-bound (three workgroup barriers each); the
-// work that grows as n^3 runs on the MFMA in many workgroups per matrix. The inverse
-// (launch_lu64_inverse: A^-T, S^-1, det A^-T) solves with the same row and GEMM kernels,
-// and the blocked Parlett-Reid below (launch_pr64_blocked: float64 slogpf) updates its
-// trailing matrix with the same GEMM.
+// The column steps of a panel are latency-bound (two or three workgroup barriers each);
+// the work that grows as n^3 runs on the MFMA in many workgroups per matrix. The inverse
+// (blk_lu_inverse: A^-T, S^-1, det A^-T, pf S^-1) solves with the same row and GEMM
+// kernels, and the blocked Parlett-Reid below (blk_pr: slogpf) updates its trailing
+// matrix with the same GEMMs.
 #include <algorithm>
 
 #include "common.h"
