@@ -64,6 +64,7 @@ SIGNATURES = {
     "fx_slogdet_inverse_f32_workspace": (_sz, [_i64, _i32]),
     "fx_slogdet_inverse_f32": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _i32, _p, _i32, _p, _sz, _p]),
     "fx_slogdet_f32_noalloc": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p]),
+    "fx_slogdet_f32_noalloc_batch": (_i64, [_i64, _i32]),
     "fx_det_parts_f32_workspace": (_sz, [_i64, _i32]),
     "fx_det_parts_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _i32, _p, _sz, _p]),
     "fx_slogpf_f32_workspace": (_sz, [_i64, _i32]),

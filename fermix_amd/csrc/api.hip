@@ -154,6 +154,7 @@ const char* fx_status_string(int status) {
 int fx_abi_version(void) { return 201; }
 
 int32_t fx_lu_padded_size(int32_t n) {
+  fx::TunePin pin_;
   if (n <= 0) return 0;
   const int f = lu_family(n);
   if (f == FAM_NONE) return -1;
@@ -161,6 +162,7 @@ int32_t fx_lu_padded_size(int32_t n) {
 }
 
 int32_t fx_pf_padded_size(int32_t n) {
+  fx::TunePin pin_;
   if (n <= 0) return 0;
   const int f = pf_family(n);
   if (f == FAM_NONE) return -1;
@@ -168,16 +170,19 @@ int32_t fx_pf_padded_size(int32_t n) {
 }
 
 int32_t fx_pf_block_columns(int32_t n) {
+  fx::TunePin pin_;
   return pf_family(n) != FAM_BLOCKED ? 16 : pf_large_block_cols(pf_large_padded(n));
 }
 
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (batch <= 0 || lu_family(n) != FAM_BLOCKED) return 0;
   return lu_large_workspace(chunk_batch(batch), n, false);
 }
 
 int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, int32_t prec,
                    void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0 || bad_lu_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
@@ -219,6 +224,7 @@ static size_t slogdet_parts_ws(int64_t nb, int n, int fam) {
 }
 
 size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   const int fam = lu_family(n);
   if (batch <= 0 || fam == FAM_NONE) return 0;
   return slogdet_parts_ws(chunk_batch(batch), n, fam);
@@ -227,6 +233,7 @@ size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n) {
 int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_singular,
                          float* sign, float* logabs, float* inv_t, float* lu, int32_t* perm, int32_t prec,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0 || bad_lu_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
@@ -278,12 +285,14 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
 }
 
 size_t fx_slogdet_factors_f32_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (batch <= 0 || lu_family(n) != FAM_BLOCKED) return 0;
   return lu_large_workspace(chunk_batch(batch), n, true, true);
 }
 
 int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* lu,
                            int32_t* perm, int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0 || bad_lu_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && (!a || !lu || !perm))) return FX_ERR_INVALID_ARGUMENT;
@@ -302,6 +311,7 @@ int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign
 }
 
 size_t fx_slogdet_inverse_f32_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (batch <= 0 || n <= 0 || lu_family(n) == FAM_NONE) return 0;
   const int N = fx_lu_padded_size(n);
   return lu_inverse_workspace(chunk_batch(batch), N, inv_padded(N) != N);
@@ -310,6 +320,7 @@ size_t fx_slogdet_inverse_f32_workspace(int64_t batch, int32_t n) {
 int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, const float* scale, int64_t batch,
                            int32_t n, int32_t zero_singular, float* inv_t, int32_t prec, void* workspace,
                            size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0 || n == 0) return FX_OK;
   if (!lu || !perm || !sign || !inv_t) return FX_ERR_INVALID_ARGUMENT;
@@ -327,12 +338,14 @@ int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, co
 }
 
 size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (batch <= 0 || lu_family(n) == FAM_NONE) return 0;
   return fx_slogdet_parts_f32_workspace(batch, n) + align256(det_adjugate_workspace(chunk_batch(batch), n));
 }
 
 int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
                      int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0 || bad_lu_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && (!a || !adj_t))) return FX_ERR_INVALID_ARGUMENT;
@@ -380,6 +393,7 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
 }
 
 size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (batch <= 0 || n % 2 || pf_family(n) != FAM_BLOCKED) return 0;
   return pf_large_workspace(chunk_batch(batch), n, false);
 }
@@ -392,6 +406,7 @@ static int pf_fused(int fam, const float* a, int n, int sk, int64_t batch, float
 
 int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign,
                   float* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
@@ -410,6 +425,7 @@ int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetr
 }
 
 size_t fx_slogpf_factors_f32_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (batch <= 0 || n % 2 || pf_family(n) != FAM_BLOCKED) return 0;
   return pf_large_workspace(chunk_batch(batch), n, true);
 }
@@ -417,6 +433,7 @@ size_t fx_slogpf_factors_f32_workspace(int64_t batch, int32_t n) {
 int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize,
                           float* sign, float* logabs, float* gbuf, float* d, int32_t* perm,
                           void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || !gbuf || !d || !perm || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
@@ -436,6 +453,7 @@ int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew
 }
 
 size_t fx_slogpf_inverse_f32_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (batch <= 0 || n <= 0 || n % 2 || pf_family(n) == FAM_NONE) return 0;
   return pf_inverse_workspace(chunk_batch(batch), fx_pf_padded_size(n));
 }
@@ -443,6 +461,7 @@ size_t fx_slogpf_inverse_f32_workspace(int64_t batch, int32_t n) {
 int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm, const float* scale,
                           int64_t batch, int32_t n, int32_t adjugate, float* g, int32_t prec, void* workspace,
                           size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0 || n == 0) return FX_OK;
   if (!g) return FX_ERR_INVALID_ARGUMENT;
@@ -471,6 +490,7 @@ static size_t slogpf_parts_ws(int64_t nb, int n, int fam) {
 }
 
 size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   const int fam = pf_family(n);
   if (batch <= 0 || n % 2 || fam == FAM_NONE) return 0;
   return slogpf_parts_ws(chunk_batch(batch), n, fam);
@@ -479,6 +499,7 @@ size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n) {
 int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         float* sign, float* logabs, float* g, int32_t prec, void* workspace, size_t workspace_bytes,
                         fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0 || bad_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || !g || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;

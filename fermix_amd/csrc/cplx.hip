@@ -885,73 +885,84 @@ using namespace fx;
 
 extern "C" {
 
-size_t fx_slogdet_c64_workspace(int64_t batch, int32_t n) { return slogdet_ws<cx<float>>(batch, n); }
-size_t fx_slogdet_c128_workspace(int64_t batch, int32_t n) { return slogdet_ws<cx<double>>(batch, n); }
+size_t fx_slogdet_c64_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogdet_ws<cx<float>>(batch, n); }
+size_t fx_slogdet_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogdet_ws<cx<double>>(batch, n); }
 
 int fx_slogdet_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   return slogdet<cx<float>>(a, batch, n, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_slogdet_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
                     size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   return slogdet<cx<double>>(a, batch, n, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
-size_t fx_slogdet_parts_c64_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<float>>(batch, n); }
-size_t fx_slogdet_parts_c128_workspace(int64_t batch, int32_t n) { return slogdet_parts_ws<cx<double>>(batch, n); }
+size_t fx_slogdet_parts_c64_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogdet_parts_ws<cx<float>>(batch, n); }
+size_t fx_slogdet_parts_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogdet_parts_ws<cx<double>>(batch, n); }
 
 int fx_slogdet_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* inv_t,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   return slogdet_parts<cx<float>>(a, batch, n, sign, logabs, inv_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_slogdet_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
                           void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   return slogdet_parts<cx<double>>(a, batch, n, sign, logabs, inv_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
-size_t fx_slogpf_c64_workspace(int64_t batch, int32_t n) { return slogpf_ws<float>(batch, n); }
-size_t fx_slogpf_c128_workspace(int64_t batch, int32_t n) { return slogpf_ws<double>(batch, n); }
+size_t fx_slogpf_c64_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogpf_ws<float>(batch, n); }
+size_t fx_slogpf_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogpf_ws<double>(batch, n); }
 
 int fx_slogpf_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign, float* logabs,
                   void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   return slogpf<float>(a, batch, n, skew_symmetrize, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_slogpf_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign,
                    double* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   return slogpf<double>(a, batch, n, skew_symmetrize, sign, logabs, workspace, workspace_bytes,
                         (hipStream_t)stream);
 }
 
-size_t fx_slogpf_parts_c64_workspace(int64_t batch, int32_t n) { return slogpf_parts_ws<float>(batch, n); }
-size_t fx_slogpf_parts_c128_workspace(int64_t batch, int32_t n) { return slogpf_parts_ws<double>(batch, n); }
+size_t fx_slogpf_parts_c64_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogpf_parts_ws<float>(batch, n); }
+size_t fx_slogpf_parts_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogpf_parts_ws<double>(batch, n); }
 
 int fx_slogpf_parts_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         float* sign, float* logabs, float* g, void* workspace, size_t workspace_bytes,
                         fx_stream_t stream) {
+  fx::TunePin pin_;
   return slogpf_parts<float>(a, batch, n, skew_symmetrize, adjugate, sign, logabs, g, workspace, workspace_bytes,
                              (hipStream_t)stream);
 }
 int fx_slogpf_parts_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                          double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
                          fx_stream_t stream) {
+  fx::TunePin pin_;
   return slogpf_parts<double>(a, batch, n, skew_symmetrize, adjugate, sign, logabs, g, workspace,
                               workspace_bytes, (hipStream_t)stream);
 }
 
-size_t fx_det_parts_c64_workspace(int64_t batch, int32_t n) { return det_parts_ws<cx<float>>(batch, n); }
-size_t fx_det_parts_c128_workspace(int64_t batch, int32_t n) { return det_parts_ws<cx<double>>(batch, n); }
-size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n) { return det_parts_f64_ws(batch, n); }
+size_t fx_det_parts_c64_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return det_parts_ws<cx<float>>(batch, n); }
+size_t fx_det_parts_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return det_parts_ws<cx<double>>(batch, n); }
+size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return det_parts_f64_ws(batch, n); }
 
 int fx_det_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
                      void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   return det_parts<cx<float>>(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_det_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
                       void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   return det_parts<cx<double>>(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_det_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
                      void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   return det_parts_f64(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 

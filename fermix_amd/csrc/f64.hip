@@ -501,12 +501,14 @@ extern "C" {
 static bool lu64_path(int n) { return n > tune().f64_reg_max_n; }
 
 size_t fx_slogdet_f64_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (n > F64_MAXN) return 0;
   return lu64_path(n) ? lu64_workspace(batch, n) : gj64_ws(batch, n, false);
 }
 
 int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
                    size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   const int st = check_f64_args(a, batch, n, sign, logabs, nullptr, workspace);
   if (st != FX_OK || batch == 0) return st;
   if (lu64_path(n)) return launch_lu64(a, n, batch, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
@@ -515,12 +517,14 @@ int fx_slogdet_f64(const double* a, int64_t batch, int32_t n, double* sign, doub
 }
 
 size_t fx_slogdet_parts_f64_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (n > F64_MAXN) return 0;
   return lu64_path(n) ? lu64_inverse_workspace(batch, n) : gj64_ws(batch, n, true);
 }
 
 int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
                          void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   const int st = check_f64_args(a, batch, n, sign, logabs, inv_t, workspace);
   if (st != FX_OK || batch == 0) return st;
   if (!inv_t) return fx_slogdet_f64(a, batch, n, sign, logabs, workspace, workspace_bytes, stream);
@@ -532,11 +536,13 @@ int fx_slogdet_parts_f64(const double* a, int64_t batch, int32_t n, double* sign
 }
 
 size_t fx_slogpf_f64_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   return n > F64_MAXN || n <= tune().f64_reg_max_n ? 0 : pr64_workspace(batch, n);
 }
 
 int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign, double* logabs,
                   void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+  fx::TunePin pin_;
   const int st = check_f64_args(a, batch, n, sign, logabs, nullptr, workspace);
   if (st != FX_OK || batch == 0) return st;
   return launch_pr64(a, n, skew_symmetrize != 0, batch, sign, logabs, workspace, workspace_bytes,
@@ -544,6 +550,7 @@ int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmet
 }
 
 size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
   if (n > F64_MAXN || batch <= 0) return 0;
   const size_t pr = fx_slogpf_f64_workspace(batch, n);
   const size_t inv = (lu64_path(n) ? align_up_256(lu64_inverse_workspace(batch, n)) : align_up_256(gj64_ws(batch, n, true))) +
@@ -554,6 +561,7 @@ size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n) {
 int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
                         fx_stream_t stream) {
+  fx::TunePin pin_;
   int st = check_f64_args(a, batch, n, sign, logabs, g, workspace);
   if (st != FX_OK || batch == 0) return st;
   hipStream_t s = (hipStream_t)stream;

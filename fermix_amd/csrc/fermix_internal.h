@@ -8,6 +8,18 @@ namespace fx {
 
 // The tuning values in effect (tune.hip): the gfx950 table, or the fx_tune_override.
 const fx_tune& tune();
+// Held by every C entry point for the length of the call: pins the tuning table that is
+// active when the call begins (nested entry points keep the outer pin), so a concurrent
+// fx_tune_override takes effect at a thread's next call, never part-way through one.
+struct TunePin {
+  TunePin();
+  ~TunePin();
+  TunePin(const TunePin&) = delete;
+  TunePin& operator=(const TunePin&) = delete;
+
+ private:
+  bool own_;
+};
 
 // dst[i] = src[i] for i < count: count a multiple of 4, both pointers 16-byte aligned.
 int launch_copy(const float* src, float* dst, int64_t count, hipStream_t s);

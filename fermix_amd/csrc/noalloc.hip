@@ -4,7 +4,8 @@
 // `scratch`, of FX_NOALLOC_SCRATCH_BYTES; a batch whose workspace exceeds it runs in
 // consecutive sub-batches that each fit (every kernel is per matrix, so the results are
 // those of fx_slogdet_f32 bitwise). n <= 128 needs no workspace and runs fx_slogdet_f32
-// directly.
+// directly. The plan (sub-batch size) is fixed and every argument checked before the
+// first sub-batch is enqueued.
 //
 // Each GPU the library runs on holds its own copy of the array until the process ends;
 // its address on a device is looked up once, with that device current
@@ -56,6 +57,7 @@ int64_t fitting_batch(int64_t batch, int n) {
     else
       hi = mid - 1;
   }
+  if (lo >= batch) return batch;
   return lo >= 8 ? lo / 8 * 8 : lo;
 }
 
@@ -64,22 +66,36 @@ int64_t fitting_batch(int64_t batch, int n) {
 
 using namespace fx;
 
+extern "C" int64_t fx_slogdet_f32_noalloc_batch(int64_t batch, int32_t n) {
+  fx::TunePin pin_;
+  if (batch <= 0 || n < 0) return 0;
+  if (fx_slogdet_f32_workspace(batch, n) == 0) return batch;
+  return fitting_batch(batch, n);
+}
+
 extern "C" int fx_slogdet_f32_noalloc(const float* a, int64_t batch, int32_t n, float* sign, float* logabs,
                                       fx_stream_t stream) {
+  fx::TunePin pin_;
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
   if (batch == 0) return FX_OK;
   if (!sign || !logabs || (n > 0 && !a)) return FX_ERR_INVALID_ARGUMENT;
   if (fx_slogdet_f32_workspace(batch, n) == 0)  // no workspace needed (or n unsupported)
     return fx_slogdet_f32(a, batch, n, sign, logabs, FX_PREC_IEEE, nullptr, 0, stream);
+  // the whole plan is checked before the first sub-batch is enqueued
+  if (((uintptr_t)a & 15) || ((uintptr_t)sign & 3) || ((uintptr_t)logabs & 3)) return FX_ERR_INVALID_ARGUMENT;
   const int64_t m = fitting_batch(batch, n);
-  if (m == 0) return FX_ERR_UNSUPPORTED;  // one matrix's workspace exceeds the scratch array
+  if (m == 0) return FX_ERR_UNSUPPORTED;  // the workspace of one sub-batch exceeds the array
   void* ws = nullptr;
   const int st = scratch_address(&ws);
   if (st != FX_OK) return st;
+  // Sub-batches go straight to the blocked LU, which reads each member's rows with
+  // 4-byte loads whenever the matrices are not 16-byte aligned: for odd n a sub-batch
+  // starts at a + b0 n^2 floats, 4-byte aligned only (n^2 = 1 mod 4). Same arguments as
+  // fx_slogdet_f32 with FX_PREC_IEEE and the table's block choice, so bit-identical.
   for (int64_t b0 = 0; b0 < batch; b0 += m) {
     const int64_t nb = batch - b0 < m ? batch - b0 : m;
-    const int r = fx_slogdet_f32(a + b0 * n * n, nb, n, sign + b0, logabs + b0, FX_PREC_IEEE, ws,
-                                 FX_NOALLOC_SCRATCH_BYTES, stream);
+    const int r = launch_lu_large(a + b0 * n * n, n, nb, sign + b0, logabs + b0, ws, FX_NOALLOC_SCRATCH_BYTES,
+                                  false, nullptr, nullptr, (hipStream_t)stream, nullptr, nullptr, FX_PREC_IEEE, 0);
     if (r != FX_OK) return r;
   }
   return FX_OK;

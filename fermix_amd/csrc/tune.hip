@@ -28,6 +28,8 @@
 //    n <= 128 (slogdet n = 128 8.66 -> 3.16 ms against the LDS kernel), in 16-column strips
 //    for n <= 64 (n = 64 1.37 ms; at n = 128 they lose, 3.97 against 3.16 ms).
 #include <atomic>
+#include <deque>
+#include <mutex>
 #include <string.h>
 
 #include "common.h"
@@ -53,8 +55,21 @@ constexpr fx_tune GFX950 = {
     /* reserved */ {0, 0, 0},
 };
 
-fx_tune g_override;
-std::atomic<bool> g_has_override{false};
+// Every table an override publishes is kept, unchanged, until the process ends (a few
+// dozen bytes each; an identical table is published once), so a pointer to the active
+// table stays valid for as long as any call holds it.
+std::mutex g_store_mu;
+std::deque<fx_tune> g_store;
+std::atomic<const fx_tune*> g_active{&GFX950};
+thread_local const fx_tune* t_pinned = nullptr;
+
+const fx_tune* publish(const fx_tune& t) {
+  std::lock_guard<std::mutex> lock(g_store_mu);
+  for (const fx_tune& x : g_store)
+    if (memcmp(&x, &t, sizeof t) == 0) return &x;
+  g_store.push_back(t);
+  return &g_store.back();
+}
 
 bool valid(const fx_tune& t) {
   auto in = [](int32_t v, int32_t lo, int32_t hi) { return v >= lo && v <= hi; };
@@ -70,7 +85,18 @@ bool valid(const fx_tune& t) {
 
 }  // namespace
 
-const fx_tune& tune() { return g_has_override.load(std::memory_order_acquire) ? g_override : GFX950; }
+// The table of the current call: the one pinned when the outermost entry point on this
+// thread began, so every decision of one call (workspace layout, block widths, tile
+// shapes) reads the same table even while another thread publishes an override.
+const fx_tune& tune() { return t_pinned ? *t_pinned : *g_active.load(std::memory_order_acquire); }
+
+TunePin::TunePin() : own_(t_pinned == nullptr) {
+  if (own_) t_pinned = g_active.load(std::memory_order_acquire);
+}
+
+TunePin::~TunePin() {
+  if (own_) t_pinned = nullptr;
+}
 
 }  // namespace fx
 
@@ -89,13 +115,11 @@ int fx_tune_table(const char* arch, fx_tune* out) {
 
 int fx_tune_override(const fx_tune* t) {
   if (!t) {
-    g_has_override.store(false, std::memory_order_release);
+    g_active.store(&GFX950, std::memory_order_release);
     return FX_OK;
   }
   if (!valid(*t)) return FX_ERR_INVALID_ARGUMENT;
-  g_has_override.store(false, std::memory_order_release);
-  g_override = *t;
-  g_has_override.store(true, std::memory_order_release);
+  g_active.store(publish(*t), std::memory_order_release);
   return FX_OK;
 }
 

@@ -235,6 +235,11 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
 #define FX_NOALLOC_SCRATCH_BYTES (64u << 20)
 int fx_slogdet_f32_noalloc(const float* a, int64_t batch, int32_t n, float* sign, float* logabs,
                            fx_stream_t stream);
+/* Host-only plan query of fx_slogdet_f32_noalloc (no counterpart in the reference): the
+ * number of members per sub-batch it runs for (batch, n) -- batch itself when one sub-batch
+ * suffices, a multiple of 8 when at least 8 fit -- and 0 when it returns
+ * FX_ERR_UNSUPPORTED. */
+int64_t fx_slogdet_f32_noalloc_batch(int64_t batch, int32_t n);
 
 /* ---------------------------------------------------------------- slogpf
  * sign[b], logabs[b] of pf(S[b]), S = (a - a^T) / 2 if skew_symmetrize != 0, else

@@ -10,7 +10,8 @@ import torch
 import fermix_amd
 from fermix_amd import _kernels
 from oracle import generic as g
-from tests.tolerances import assert_grad, assert_grad_vs_fp32, lapack_inverse_f32, rel_fro
+from oracle import ref64
+from tests.tolerances import assert_grad, assert_grad_vs_fp32, assert_logabs, lapack_inverse_f32, rel_fro
 
 pytestmark = pytest.mark.gpu
 
@@ -23,20 +24,29 @@ def _np(x):
     return x.detach().cpu().numpy()
 
 
-@pytest.mark.parametrize("n", [1, 2, 5, 16, 17, 33, 48, 64, 100, 128, 129, 200, 256, 300, 320, 512])
-def test_slogdet_invT_vs_float64_and_oracle(dev, n):
+# The product mode (prec) changes the arithmetic only of the blocked kernels (n > 128):
+# both the IEEE fp32 MFMA mode and the split-bf16x3 mode are held to the same bars there.
+PRECS = {0: "ieee", 1: "bf16x3"}
+
+
+def _with_modes(ns):
+    return [(n, 1) for n in ns] + [(n, 0) for n in ns if n > 128]
+
+
+@pytest.mark.parametrize("n,x3", _with_modes([1, 2, 5, 16, 17, 33, 48, 64, 100, 128, 129, 200, 256, 300, 320, 512]))
+def test_slogdet_invT_vs_float64_and_oracle(dev, n, x3):
     B = 12 if n <= 256 else 4
     rng = np.random.default_rng(2000 + n)
     A = (rng.standard_normal((B, n, n)) / np.sqrt(n)).astype(np.float32)
-    print(f"invT n={n} B={B}", flush=True)
-    s, l, invT, _, _ = _kernels.slogdet_parts(_t(A, dev))
-    s0, l0 = fermix_amd.slogdet(_t(A, dev))
+    print(f"invT n={n} B={B} prec={PRECS[x3]}", flush=True)
+    s, l, invT, _, _ = _kernels.slogdet_parts(_t(A, dev), x3=x3)
+    s0, l0 = fermix_amd.slogdet(_t(A, dev), prec=PRECS[x3])
     assert torch.equal(s, s0) and torch.equal(l, l0), "parts primal != forward"
     invT = _np(invT)
     ref = np.linalg.inv(A.astype(np.float64)).transpose(0, 2, 1)
-    assert_grad(invT, ref, A, f"n={n} vs float64")
+    assert_grad(invT, ref, A, f"n={n} {PRECS[x3]} vs float64")
     _, _, invo, _, _, _ = g.lu_parts_generic(A)
-    assert_grad(invT, invo, A, f"n={n} vs oracle")
+    assert_grad(invT, invo, A, f"n={n} {PRECS[x3]} vs oracle")
 
 
 @pytest.mark.parametrize("n", [12, 40, 150])
@@ -101,45 +111,57 @@ def test_det_value_and_grad(dev):
     assert np.max(np.abs(_np(gr) - ref)) < 1e-4 * np.abs(ref).max()
 
 
-def test_c3_properties(dev):
-    """C3 size: B = 1024, n = 512, A iid N(0, 1/n). Primal bit-identical to the forward,
-    gradient finite, A^T invT = I on a subset in float64, a subset against the oracle."""
+@pytest.mark.parametrize("x3", [0, 1])
+def test_c3_properties(dev, x3):
+    """C3 size: B = 1024, n = 512, A iid N(0, 1/n), in both product modes. Primal
+    bit-identical to the forward, gradient finite, 18 members against float64 truth, the
+    oracle and float32 LAPACK (on average no less accurate than either), logabs and sign
+    of the same members against float64."""
     rng = np.random.default_rng(3)
     B, n = 1024, 512
     A = (rng.standard_normal((B, n, n), dtype=np.float32) * np.float32(1 / np.sqrt(n)))
     At = _t(A, dev)
-    s, l, invT, _, _ = _kernels.slogdet_parts(At)
-    s0, l0 = fermix_amd.slogdet(At)
+    what = f"C3 {PRECS[x3]}"
+    s, l, invT, _, _ = _kernels.slogdet_parts(At, x3=x3)
+    s0, l0 = fermix_amd.slogdet(At, prec=PRECS[x3])
     assert torch.equal(s, s0) and torch.equal(l, l0)
     assert bool(torch.isfinite(invT).all())
     idx = list(range(0, 1024, 64)) + [1, 1023]
     G = _np(invT[idx])
     ref = np.linalg.inv(A[idx].astype(np.float64)).transpose(0, 2, 1)
-    assert_grad(G, ref, A[idx], "C3 subset vs float64")
-    # no worse than twice the fp32 references on the same members: the oracle (the
-    # reference's generic path restated) and float32 LAPACK
+    assert_grad(G, ref, A[idx], f"{what} subset vs float64")
+    # no worse than the fp32 references on the same members: the oracle (the reference's
+    # generic path restated) and float32 LAPACK
     _, _, invo, _, _, _ = g.lu_parts_generic(A[idx])
-    assert_grad_vs_fp32(G, ref, rel_fro(invo, ref), "C3 subset vs the oracle's error")
+    assert_grad_vs_fp32(G, ref, rel_fro(invo, ref), f"{what} subset vs the oracle's error")
     inv32 = lapack_inverse_f32(A[idx]).transpose(0, 2, 1)
-    assert_grad_vs_fp32(G, ref, rel_fro(inv32, ref), "C3 subset vs fp32 LAPACK's error")
+    assert_grad_vs_fp32(G, ref, rel_fro(inv32, ref), f"{what} subset vs fp32 LAPACK's error")
+    s64, l64 = ref64.slogdet64(A[idx])
+    assert np.array_equal(_np(s)[idx], s64)
+    assert_logabs(_np(l)[idx], l64, n, f"{what} subset logabs vs float64", A[idx])
 
 
-@pytest.mark.parametrize("n", [2, 4, 6, 10, 16, 34, 64, 96, 128, 130, 256, 300, 512])
-def test_slogpf_grad_vs_float64_and_oracle(dev, n):
+@pytest.mark.parametrize("n,x3", _with_modes([2, 4, 6, 10, 16, 34, 64, 96, 128, 130, 256, 300, 512]))
+def test_slogpf_grad_vs_float64_and_oracle(dev, n, x3):
     B = 8 if n <= 256 else 3
     rng = np.random.default_rng(5000 + n)
     A = (rng.standard_normal((B, n, n)) / np.sqrt(n)).astype(np.float32)
     S = (A - A.transpose(0, 2, 1)).astype(np.float32)
-    print(f"slogpf grad n={n} B={B}", flush=True)
-    s, l, Sinv = _kernels.slogpf_parts(_t(S, dev), False)
-    s0, l0 = fermix_amd.slogpf(_t(S, dev), skew_symmetrize=False)
+    print(f"slogpf grad n={n} B={B} prec={PRECS[x3]}", flush=True)
+    s, l, Sinv = _kernels.slogpf_parts(_t(S, dev), False, x3=x3)
+    s0, l0 = fermix_amd.slogpf(_t(S, dev), skew_symmetrize=False, prec=PRECS[x3])
     assert torch.equal(s, s0) and torch.equal(l, l0), "parts primal != forward"
     Sinv = _np(Sinv)
     ref = np.linalg.inv(S.astype(np.float64))
-    assert_grad(Sinv, ref, S, f"n={n} vs float64")
+    assert_grad(Sinv, ref, S, f"n={n} {PRECS[x3]} vs float64")
     if n <= 256:
         _, _, So, _ = g.pf_parts_generic(S, False)
-        assert_grad(Sinv, So, S, f"n={n} vs oracle")
+        assert_grad(Sinv, So, S, f"n={n} {PRECS[x3]} vs oracle")
+    # the autograd route of the same mode: -S^-1 / 2 from the saved factors
+    Sg = _t(S, dev).requires_grad_()
+    _, la = fermix_amd.slogpf(Sg, skew_symmetrize=False, prec=PRECS[x3])
+    (gr,) = torch.autograd.grad(la.sum(), Sg)
+    assert torch.equal(gr, -0.5 * _t(Sinv, dev))
 
 
 def test_slogpf_autograd_and_singular(dev):
@@ -169,27 +191,32 @@ def test_slogpf_autograd_and_singular(dev):
     assert torch.equal(vs[0], s0) and torch.equal(vl[0], l0)
 
 
-def test_c4_properties(dev):
-    """C4 size: B = 64, n = 2048, S = A - A^T, A iid N(0, 1/n). Primal bit-identical to the
-    forward, gradient finite and skew, S S^-1 = I on a subset in float64."""
+@pytest.mark.parametrize("x3", [0, 1])
+def test_c4_properties(dev, x3):
+    """C4 size: B = 64, n = 2048, S = A - A^T, A iid N(0, 1/n), in both product modes.
+    Primal bit-identical to the forward, gradient finite and skew, 6 members against
+    float64 truth and float32 LAPACK (on average no less accurate), |pf|^2 = |det| of the
+    same members against float64."""
     rng = np.random.default_rng(4)
     B, n = 64, 2048
     A = rng.standard_normal((B, n, n), dtype=np.float32) * np.float32(1 / np.sqrt(n))
     S = A - A.transpose(0, 2, 1)
     del A
     St = _t(S, dev)
-    s, l, Sinv = _kernels.slogpf_parts(St, False)
-    s0, l0 = fermix_amd.slogpf(St, skew_symmetrize=False)
+    what = f"C4 {PRECS[x3]}"
+    s, l, Sinv = _kernels.slogpf_parts(St, False, x3=x3)
+    s0, l0 = fermix_amd.slogpf(St, skew_symmetrize=False, prec=PRECS[x3])
     assert torch.equal(s, s0) and torch.equal(l, l0)
     assert bool(torch.isfinite(Sinv).all())
     idx = [0, 1, 2, 31, 62, 63]
     G = _np(Sinv[idx])
     assert np.max(np.abs(G + G.transpose(0, 2, 1))) <= 1e-6 * np.abs(G).max()
     ref = np.linalg.inv(S[idx].astype(np.float64))
-    assert_grad(G, ref, S[idx], "C4 subset vs float64")
-    # no worse than twice a float32 LAPACK inverse of the same members
+    assert_grad(G, ref, S[idx], f"{what} subset vs float64")
     inv32 = lapack_inverse_f32(S[idx])
-    assert_grad_vs_fp32(G, ref, rel_fro(inv32, ref), "C4 subset vs fp32 LAPACK's error")
+    assert_grad_vs_fp32(G, ref, rel_fro(inv32, ref), f"{what} subset vs fp32 LAPACK's error")
+    _, ld64 = ref64.slogdet64(S[idx])
+    assert_logabs(_np(l)[idx], 0.5 * ld64, n, f"{what} subset log|pf| vs log|det| / 2 float64", S[idx])
 
 
 @pytest.mark.parametrize("n", [40, 129, 200, 512])

@@ -39,19 +39,19 @@ def _jmat(n, dev):
     return J
 
 
-@pytest.mark.parametrize("n", [4160, 8192])
-def test_slogdet_xxl(dev, n):
+@pytest.mark.parametrize("n,prec", [(4160, "bf16x3"), (4160, "ieee"), (8192, "bf16x3")])
+def test_slogdet_xxl(dev, n, prec):
     B = 2
     A64 = _near_identity(dev, B, n, 9600 + n)
     A64[1, :, n // 3] = 0.0  # exact zero pivot
     A = A64.to(torch.float32)
-    print(f"slogdet xxl n={n}", flush=True)
-    s, l = fermix_amd.slogdet(A)
+    print(f"slogdet xxl n={n} prec={prec}", flush=True)
+    s, l = fermix_amd.slogdet(A, prec=prec)
     s64, l64 = torch.linalg.slogdet(A.to(torch.float64))
     assert torch.equal(s.cpu().to(torch.float64), s64.cpu())
-    assert_logabs(l.cpu().numpy(), l64.cpu().numpy(), n, f"n={n} vs float64")
+    assert_logabs(l.cpu().numpy(), l64.cpu().numpy(), n, f"n={n} {prec} vs float64")
     # the gradient: A^-T of the regular member, and the primal of the parts run
-    sp, lp, invT, _, _ = _kernels.slogdet_parts(A[:1].contiguous())
+    sp, lp, invT, _, _ = _kernels.slogdet_parts(A[:1].contiguous(), x3=1 if prec == "bf16x3" else 0)
     assert torch.equal(sp, s[:1]) and torch.equal(lp, l[:1]), "parts primal != forward"
     err = _inv_residual(A[:1].transpose(1, 2), invT)
     print(f"  A^-T residual {err}", flush=True)

@@ -190,6 +190,28 @@ def test_noalloc_host_checks():
     for n in (4033, 4096):
         assert L.fx_slogdet_f32_noalloc(good, 4, n, good, good, None) == 4
     assert L.fx_slogdet_f32_noalloc(good, 4, 5000, good, good, None) == 4
+    # a misaligned matrix pointer is rejected before the first sub-batch is enqueued
+    assert L.fx_slogdet_f32_noalloc(good + 4, 7, 2049, good, good, None) == 1
+
+
+def test_noalloc_plan():
+    """The sub-batch plan of fx_slogdet_f32_noalloc (host-only): every n the entry point
+    accepts has a plan, each sub-batch's workspace fits the scratch array, and sub-batches
+    of 8 or more are multiples of 8. (For odd n a sub-batch may start 4-byte aligned only,
+    e.g. n = 2049 runs 3 + 3 + 1 members: the blocked LU reads such matrices with 4-byte
+    loads; tests/test_zz_no_alloc.py checks that case on the GPU.)"""
+    L = _lib.lib()
+    limit = 64 << 20
+    assert L.fx_slogdet_f32_noalloc_batch(7, 2049) == 3
+    assert L.fx_slogdet_f32_noalloc_batch(5, 100) == 5  # no workspace at all
+    assert L.fx_slogdet_f32_noalloc_batch(3, 4033) == 0
+    for n in list(range(129, 1500, 38)) + list(range(1401, 4033, 89)) + [2049, 2050, 4031, 4032]:
+        for batch in (1, 3, 7, 64, 1000):
+            m = L.fx_slogdet_f32_noalloc_batch(batch, n)
+            assert 1 <= m <= batch and L.fx_slogdet_f32_workspace(m, n) <= limit, (n, batch, m)
+            if m < batch:
+                assert m < 8 or m % 8 == 0, (n, batch, m)
+                assert L.fx_slogdet_f32_workspace(m + 1, n) > limit or m >= 8, (n, batch, m)
 
 
 def test_prec_argument_validated():
