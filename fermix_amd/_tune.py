@@ -45,8 +45,9 @@ class FermixTuneWarning(UserWarning):
 def check_prec(prec, dtype=None):
     """The mode a `prec` argument selects ("ieee" or "bf16x3"). The reduced-precision
     modes apply to the 32-bit kinds only (the reference rejects "tf32x3" for float64 /
-    complex128, src/fermix/_field.py:265-275); complex64 accepts them but runs no MFMA
-    product (its kernels are unblocked), so they do not change its results."""
+    complex128, src/fermix/_field.py:265-275); complex64 accepts them, but its products
+    (the blocked kernels above n = 64) run widened on the fp64 MFMA, so `prec` does not
+    change complex64 results."""
     if prec is None:
         return "ieee" if dtype in (torch.float64, torch.complex128) else DEFAULT_PREC
     if prec not in PREC:
