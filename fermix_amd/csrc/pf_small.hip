@@ -48,8 +48,11 @@ struct PfSmall {
 };
 static_assert(PfSmall<128>::LDS_BYTES <= 40960, "four n = 128 workgroups per CU");
 
-// Start of row p of the strictly lower triangle.
+// Start of row p of the strictly lower triangle (a 24-bit multiply: one VALU
+// instruction per lane).
 __device__ __forceinline__ int tri_row(int p) { return (int)(__umul24((unsigned)p, (unsigned)(p - 1)) >> 1); }
+// The same for a wave-uniform p (a scalar multiply, without the 24-bit operand masks).
+__device__ __forceinline__ int tri_row_u(int p) { return (p * (p - 1)) >> 1; }
 
 // Index of G element (row s, column k) in Gs.
 template <int N>
@@ -67,35 +70,43 @@ __device__ __forceinline__ int first_row(const unsigned long long (&b)[R]) {
 }
 
 // S0: first slot with rows >= r0 (rows l + 64 s with s < S0 are all finished).
+//
+// The step is one wave's instruction stream (one instruction per four cycles at best), so
+// it is written for few instructions: byte offsets precomputed per lane, the next row's
+// column and G row read before the pivot search (independent of it, so their LDS latency
+// overlaps the reduction), stores unpredicated where every lane row exists. Without FACT
+// the finished rows' tau / w are left as computed: they only enter the corrections of
+// finished rows, whose values nothing reads; FACT exports them, as zeros.
 template <int N, bool FACT, int S0>
 __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsigned char* src, int lane,
                                          PivotLog<PfSmall<N>::NPV>& piv_log, int& nsw,
                                          unsigned char* orig, float* gbuf_k, float* d_k) {
-  constexpr int R = PfSmall<N>::R, NTRI = PfSmall<N>::NTRI;
+  constexpr int R = PfSmall<N>::R;
+  constexpr bool ALL = N == 64 * R;  // every lane row exists
   // lane-derived addresses are recomputed per block instead of held across the loop
   asm volatile("" : "+v"(lane));
+  const char* const Tb = reinterpret_cast<const char*>(T);
   float G[R][16];
-  int pos[R], rop[R];
+  int pos[R], rop4[R], row4[R];
   bool valid[R];
 #pragma unroll
   for (int i = S0; i < R; ++i) {
     const int row = lane + 64 * i;
-    valid[i] = (row >= r0) && (row < N);
+    valid[i] = (row >= r0) && (ALL || row < N);
     pos[i] = valid[i] ? row : -1;  // finished / absent rows never match a position >= r0
-    rop[i] = row < N ? tri_row(row) : 0;
+    rop4[i] = (ALL || row < N) ? 4 * tri_row(row) : 0;
+    row4[i] = 4 * row;
 #pragma unroll
     for (int k = 0; k < 16; ++k) G[i][k] = 0.0f;
   }
   // M[row][q] of the block-start matrix for the lane's rows (value for row == q unused)
   auto column = [&](int q, float (&v)[R]) {
-    const int roq = tri_row(q);
+    const int q4 = 4 * q, roq4 = 4 * tri_row_u(q);
 #pragma unroll
     for (int i = S0; i < R; ++i) {
-      const int row = lane + 64 * i;
-      const bool below = row > q;
+      const bool below = row4[i] > q4;
       // row == q == N-1 addresses T[NTRI], the first entry of Gs (value unused)
-      const int e = below ? rop[i] + q : roq + row;
-      const float t = T[e];
+      const float t = *reinterpret_cast<const float*>(Tb + (below ? rop4[i] + q4 : roq4 + row4[i]));
       v[i] = below ? t : -t;
     }
   };
@@ -130,7 +141,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
       });
     }
   };
-  // Row a of step t and its current column x are carried from step t - 1: while step
+  // Row a of step t and its current column x are carried from step t - 1: before step
   // t - 1 searches its pivot, the row at position c + 2 is read and corrected with the
   // finished G columns; unless the pivot swap moved that row, only step t - 1's own term
   // is added afterwards (from the owner lane's registers, same order of operations).
@@ -140,13 +151,19 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
   static_for<0, 8>([&](auto tc) {
     constexpr int t = decltype(tc)::value;
     const int c = r0 + 2 * t;
+    // speculative next row a, its G row and column, read before the pivot search
+    const int qn = t < 7 ? row_at(c + 2) : 0;
+    float gn[16], xn[R];
+    if constexpr (t < 7) {
+      grow(qn, gn, tc);
+      column(qn, xn);
+    }
     unsigned key[R], kb = 0;
 #pragma unroll
     for (int i = S0; i < R; ++i) {
       key[i] = cand_key(x[i], pos[i] > c);
       kb = max(kb, key[i]);
     }
-    const int qn = t < 7 ? row_at(c + 2) : 0;  // speculative next row a
     const unsigned gk = wave_max_u32(kb);
     unsigned long long bp[R];
 #pragma unroll
@@ -160,11 +177,6 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
     float gp[16], y[R];
     grow(qp, gp, tc);
     column(qp, y);
-    float gn[16], xn[R];
-    if constexpr (t < 7) {
-      grow(qn, gn, tc);
-      column(qn, xn);
-    }
     correct(y, gp, tc);
     const int la = qa & 63, sa = qa >> 6;
     float yv = y[S0];  // M[a][p] = y at row a
@@ -183,10 +195,15 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
 #pragma unroll
     for (int i = S0; i < R; ++i) {
       const int row = lane + 64 * i;
-      const bool act = pos[i] > c + 1;
-      G[i][2 * t] = act ? -x[i] * inv : 0.0f;
-      G[i][2 * t + 1] = act ? y[i] : 0.0f;
-      if (row < N)
+      if constexpr (FACT) {
+        const bool act = pos[i] > c + 1;
+        G[i][2 * t] = act ? -x[i] * inv : 0.0f;
+        G[i][2 * t + 1] = act ? y[i] : 0.0f;
+      } else {
+        G[i][2 * t] = -x[i] * inv;
+        G[i][2 * t + 1] = y[i];
+      }
+      if (ALL || row < N)
         *reinterpret_cast<float2*>(Gs + g_idx<N>(row, 2 * t)) = make_float2(G[i][2 * t], G[i][2 * t + 1]);
     }
     wave_lds_fence();
