@@ -567,13 +567,23 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
   };
 
   // split-bf16x3 staging (X3): each thread holds two groups of four consecutive k -- of
-  // rows ra, ra + 64 of A (one 16-byte load each), or of columns 2 p, 2 p + 1 (p = tid %
-  // 64) of A^T / B (four 8-byte loads along k) -- fixed in registers when the stage is
-  // not plain, then split once into the planes
+  // rows ra, ra + 64 of A (one 16-byte load each), or of columns p, p + 64 (p = tid % 64)
+  // of A^T / B (eight 4-byte loads along k, each a 256-byte row segment per wave) -- fixed
+  // in registers when the stage is not plain, then split once into the planes. A wave's
+  // planes stores of A^T / B then cover 64 consecutive operand rows (32 bytes apart):
+  // with columns 2 p, 2 p + 1 per lane (one 8-byte load per k) they were 64 bytes apart,
+  // and twice as many lanes met in each LDS bank (C3 5.72 -> 5.42 ms, C4 13.85 -> 13.61
+  // ms). Four lanes per operand row (A's pattern, no bank met twice) lost more to the
+  // 64-byte load segments it needs than it gained (C3 5.74, C4 14.12 ms).
   auto xA = [&](int b) { return reinterpret_cast<__bf16*>(smem) + b * 3 * (XPA + XPB); };
   auto xB = [&](int b) { return reinterpret_cast<__bf16*>(smem) + b * 3 * (XPA + XPB) + 3 * XPA; };
   const int xp = tid & 63, xk = 4 * (tid >> 6);
-  const int xia = min(i0 + 2 * xp, d.M - 2), xjb = min(j0 + 2 * xp, d.N - 2);
+  int xia[2], xjb[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    xia[e] = min(i0 + xp + 64 * e, d.M - 1);
+    xjb[e] = min(j0 + xp + 64 * e, d.N - 1);
+  }
   // a stage's loaded values (a second set, with the loads two stages ahead, measured
   // 26 % slower on the n = 512 slogdet backward: 194 VGPRs leave two workgroups per CU
   // against three)
@@ -594,18 +604,18 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float2 x = *reinterpret_cast<const float2*>(A + min(k0 + xk + r, d.K - 1) * d.lda + xia);
-        R.a[0][r] = x.x;
-        R.a[1][r] = x.y;
+        const float* ar = A + min(k0 + xk + r, d.K - 1) * d.lda;
+        R.a[0][r] = ar[xia[0]];
+        R.a[1][r] = ar[xia[1]];
       }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int kr = min(k0 + xk + r, d.K - 1);
       if (BS) R.s[r] = d.bscale[bat * (d.K / 2) + (kr >> 1)];
-      const float2 y = *reinterpret_cast<const float2*>(B + (BS ? kr ^ 1 : kr) * d.ldb + xjb);
-      R.b[0][r] = y.x;
-      R.b[1][r] = y.y;
+      const float* br = B + (BS ? kr ^ 1 : kr) * d.ldb;
+      R.b[0][r] = br[xjb[0]];
+      R.b[1][r] = br[xjb[1]];
     }
   };
   // the stage's masks: each operand's triangle only where its stage meets the diagonal,
@@ -615,8 +625,8 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       // A: row gi, k from gk; B: column gj, k from k0 + xk
-      const int gi = TA ? i0 + 2 * xp + e : i0 + ra + 64 * e, gk = TA ? k0 + xk : k0 + ka;
-      const int gj = j0 + 2 * xp + e;
+      const int gi = TA ? i0 + xp + 64 * e : i0 + ra + 64 * e, gk = TA ? k0 + xk : k0 + ka;
+      const int gj = j0 + xp + 64 * e;
       float va4[4], vb4[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
