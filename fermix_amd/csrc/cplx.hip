@@ -39,7 +39,7 @@
 namespace fx {
 namespace {
 
-constexpr int CX_MAXN = 4096;
+constexpr int CX_MAXN = 8192;
 constexpr size_t CX_LDS_MAX = 60 * 1024;  // matrix bytes kept in LDS
 constexpr int CX_NT = 1024;
 // complex orders above this run the blocked kernels of lu64.hip (LU, solves, Parlett-Reid
@@ -738,9 +738,42 @@ size_t slogpf_ws(int64_t batch, int n) {
 }
 
 template <class T>
-int launch_pf(const T* a, int n, int skew, int64_t batch, T* sign, T* logabs, void* ws, size_t wsb, hipStream_t s) {
-  if (blocked<cx<T>>(n)) return blk_pr<cx<T>>((const cx<T>*)a, n, skew, batch, (cx<T>*)sign, logabs, ws, wsb, s);
+int launch_pf(const T* a, int n, int skew, int64_t batch, T* sign, T* logabs, void* ws, size_t wsb, hipStream_t s,
+              double* spread = nullptr) {
+  if (blocked<cx<T>>(n))
+    return blk_pr<cx<T>>((const cx<T>*)a, n, skew, batch, (cx<T>*)sign, logabs, ws, wsb, s, spread);
   return launch_cpr<T>(a, n, skew, batch, sign, logabs, ws, wsb, s);
+}
+
+// The blocked Pfaffian adjugate takes pf(S) S^-1 from an LU of S scaled by the
+// Parlett-Reid run's pf. That is accurate while S is well away from singular; near a
+// rank-(n - 2) S the LU's two small pivots and the Parlett-Reid run's small pair pivot
+// come from different factorisations, so the product is off by O(1). Members whose
+// Parlett-Reid pair pivots span more than this (log max |d| - log min |d|: |d_min| below
+// 2^-18 |d_max| in double precision, 2^-8 in single) take the pivot-replaced
+// Parlett-Reid formula instead (exact for singular S, as the reference's
+// src/fermix/_pfinv.py:196-269). Random members sit far inside it: |d_min| / |d_max| is
+// 0.03 .. 0.1 for N(0, 1/n) skew matrices at n = 256 .. 1024.
+template <class R>
+constexpr double pf_lu_spread_max() {
+  return (sizeof(R) == 8 ? 18.0 : 8.0) * 0.69314718055994531;
+}
+
+// gate[b] = sign[b] where the member takes the LU route (spread within the limit), else 0
+template <class F>
+__global__ void pf_gate_kernel(const F* __restrict__ sign, const double* __restrict__ spread, double lim,
+                               F* __restrict__ gate, int64_t batch) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  gate[b] = spread[b] <= lim ? sign[b] : Fd<F>::zero();
+}
+
+template <class F>
+int pf_gate(const F* sign, const double* spread, F* gate, int64_t batch, hipStream_t s) {
+  pf_gate_kernel<F><<<dim3((unsigned)((batch + 255) / 256)), 256, 0, s>>>(sign, spread,
+                                                                        pf_lu_spread_max<typename Fd<F>::R>(), gate,
+                                                                        batch);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
 // The Pfaffian adjugate's workspace: the Parlett-Reid matrix and then [T~ | I] (the same
@@ -800,8 +833,10 @@ size_t slogpf_parts_ws(int64_t batch, int n) {
   if (n > CX_MAXN || batch <= 0) return 0;
   const size_t scratch = align_up((size_t)batch * 3 * sizeof(T));
   if (blocked<cx<T>>(n)) {
+    // + the pivot spread and the route gate of the adjugate mode
     const size_t inv = align_up(blk_lu_inverse_workspace<cx<T>>(batch, n)) + scratch;
-    return align_up(slogpf_ws<T>(batch, n)) + std::max(inv, pf_adjugate_ws<cx<T>>(batch, n));
+    return align_up(slogpf_ws<T>(batch, n)) + std::max(inv, pf_adjugate_ws<cx<T>>(batch, n)) +
+           align_up((size_t)batch * sizeof(double)) + align_up((size_t)batch * sizeof(cx<T>));
   }
   const size_t inv = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n)) + scratch;
   return align_up(slogpf_ws<T>(batch, n)) + std::max(inv, pf_adjugate_ws<cx<T>>(batch, n));
@@ -828,21 +863,32 @@ int slogpf_parts(const T* a, int64_t batch, int n, int skew, int adjugate, T* si
   if (wsb < slogpf_parts_ws<T>(batch, n) || (!ws && slogpf_parts_ws<T>(batch, n))) return FX_ERR_WORKSPACE;
   const size_t pr = align_up(slogpf_ws<T>(batch, n));
   char* base = (char*)ws;
-  st = launch_pf<T>(a, n, skew != 0, batch, sign, logabs, base, pr, s);
+  const bool blk = blocked<cx<T>>(n);
+  const size_t lw = blk ? align_up(blk_lu_inverse_workspace<cx<T>>(batch, n)) : 0;
+  const size_t body = blk ? std::max(lw + align_up((size_t)batch * 3 * sizeof(T)), pf_adjugate_ws<cx<T>>(batch, n)) : 0;
+  double* spread = blk ? (double*)(base + pr + body) : nullptr;
+  st = launch_pf<T>(a, n, skew != 0, batch, sign, logabs, base, pr, s, spread);
   if (st != FX_OK) return st;
   if (adjugate && (n & 1)) return cx_zero<cx<T>>((cx<T>*)g, batch * (int64_t)n * n, s);
-  if (blocked<cx<T>>(n)) {
-    // S^-1 (adjugate: pf(S) S^-1 of the members with pf != 0) from the blocked LU solves,
-    // zero where pf = 0; the adjugate of those from the Parlett-Reid run below
+  if (blk) {
+    // S^-1 from the blocked LU solves, zero where pf = 0; adjugate: pf(S) S^-1 from the
+    // same solves for the members the gate passes, the pivot-replaced Parlett-Reid formula
+    // below for the others (pf = 0, or a pair pivot at round-off level)
     const cx<T>* A = (const cx<T>*)a;
     const cx<T>* sg = (const cx<T>*)sign;
-    const size_t lw = align_up(blk_lu_inverse_workspace<cx<T>>(batch, n));
     cx<T>* gsign = (cx<T>*)(base + pr + lw);
     T* glog = (T*)(gsign + batch);
-    st = blk_lu_inverse<cx<T>>(A, n, skew != 0, batch, gsign, glog, sg, adjugate ? sg : nullptr,
+    const cx<T>* gate = sg;
+    if (adjugate) {
+      cx<T>* gz = (cx<T>*)(base + pr + body + align_up((size_t)batch * sizeof(double)));
+      st = pf_gate<cx<T>>(sg, spread, gz, batch, s);
+      if (st != FX_OK) return st;
+      gate = gz;
+    }
+    st = blk_lu_inverse<cx<T>>(A, n, skew != 0, batch, gsign, glog, gate, adjugate ? sg : nullptr,
                                adjugate ? logabs : nullptr, (cx<T>*)g, 0, base + pr, lw, s);
     if (st != FX_OK || !adjugate) return st;
-    return pf_adjugate<cx<T>>(A, batch, n, skew != 0, (cx<T>*)g, base + pr, wsb - pr, s, sg);
+    return pf_adjugate<cx<T>>(A, batch, n, skew != 0, (cx<T>*)g, base + pr, body, s, gate);
   }
   if (adjugate)
     return pf_adjugate<cx<T>>((const cx<T>*)a, batch, n, skew != 0, (cx<T>*)g, base + pr, wsb - pr, s);
@@ -855,28 +901,33 @@ int slogpf_parts(const T* a, int64_t batch, int n, int skew, int adjugate, T* si
 }  // namespace
 
 // the float64 Pfaffian adjugate (fx_slogpf_parts_f64 with adjugate != 0): zero for odd n.
-// Above the register kernels (n > f64_reg_max_n) the members with pf != 0 (psign, the
-// Parlett-Reid run's sign, and plog its log|pf|) take pf(S) S^-1 from the blocked LU
-// solves, and only those with pf = 0 run the Parlett-Reid factor and Gauss-Jordan above.
-static size_t pf_adjugate_f64_lu_ws(int64_t batch, int n) {
-  return align_up(lu64_inverse_workspace(batch, n)) + align_up((size_t)batch * 2 * sizeof(double));
+// Above the register kernels (n > f64_reg_max_n) the members the gate passes (pf != 0 and
+// the pair pivots' spread within pf_lu_spread_max; psign, the Parlett-Reid run's sign,
+// plog its log|pf|, spread its pivot spread) take pf(S) S^-1 from the blocked LU solves,
+// and the others run the pivot-replaced Parlett-Reid factor and Gauss-Jordan above.
+static size_t pf_adjugate_f64_body(int64_t batch, int n) {
+  return std::max(pf_adjugate_ws<double>(batch, n),
+                  align_up(lu64_inverse_workspace(batch, n)) + align_up((size_t)batch * 2 * sizeof(double)));
 }
 size_t pf_adjugate_f64_ws(int64_t batch, int n) {
-  const size_t gj = pf_adjugate_ws<double>(batch, n);
-  if (n <= tune().f64_reg_max_n || batch <= 0 || (n & 1)) return gj;
-  return std::max(gj, pf_adjugate_f64_lu_ws(batch, n));
+  if (n <= tune().f64_reg_max_n || batch <= 0 || (n & 1)) return pf_adjugate_ws<double>(batch, n);
+  return pf_adjugate_f64_body(batch, n) + align_up((size_t)batch * sizeof(double));
 }
 int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, const double* psign,
-                    const double* plog, void* ws, size_t wsb, hipStream_t s) {
+                    const double* plog, const double* spread, void* ws, size_t wsb, hipStream_t s) {
   if (batch <= 0 || n == 0) return FX_OK;
   if (n & 1) return cx_zero<double>(g, batch * (int64_t)n * n, s);
   if (n <= tune().f64_reg_max_n) return pf_adjugate<double>(a, batch, n, skew, g, ws, wsb, s);
-  if (!ws || wsb < pf_adjugate_f64_ws(batch, n)) return FX_ERR_WORKSPACE;
+  if (!ws || !spread || wsb < pf_adjugate_f64_ws(batch, n)) return FX_ERR_WORKSPACE;
+  const size_t body = pf_adjugate_f64_body(batch, n);
   const size_t lw = align_up(lu64_inverse_workspace(batch, n));
   double* lsign = (double*)((char*)ws + lw);
-  const int r = launch_lu64_inverse(a, n, skew, batch, lsign, lsign + batch, psign, psign, plog, g, 0, ws, lw, s);
+  double* gate = (double*)((char*)ws + body);
+  int r = pf_gate<double>(psign, spread, gate, batch, s);
+  if (r == FX_OK)
+    r = launch_lu64_inverse(a, n, skew, batch, lsign, lsign + batch, gate, psign, plog, g, 0, ws, lw, s);
   if (r != FX_OK) return r;
-  return pf_adjugate<double>(a, batch, n, skew, g, ws, wsb, s, psign);
+  return pf_adjugate<double>(a, batch, n, skew, g, ws, body, s, gate);
 }
 
 }  // namespace fx

@@ -1,5 +1,5 @@
 // float64 path: slogdet / slogpf forward and their gradients (A^-T, S^-1) for
-// 0 <= n <= 4096: one workgroup per matrix up to n = 128, the blocked kernels of lu64.hip
+// 0 <= n <= 8192: one workgroup per matrix up to n = 128, the blocked kernels of lu64.hip
 // above.
 //
 // The reference takes float64 through the same entry points as float32 (dtype check
@@ -39,7 +39,7 @@
 namespace fx {
 namespace {
 
-constexpr int F64_MAXN = 4096;
+constexpr int F64_MAXN = 8192;
 constexpr size_t F64_LDS_MAX = 60 * 1024;  // matrix bytes kept in LDS
 
 size_t align_up_256(size_t x) { return (x + 255) / 256 * 256; }
@@ -456,8 +456,10 @@ int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, d
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
+// spread: the blocked run's pair-pivot spread (lu64.hip), left unwritten by the register
+// kernels
 int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
-                size_t ws_bytes, hipStream_t s) {
+                size_t ws_bytes, hipStream_t s, double* spread = nullptr) {
   if (n <= tune().f64_reg_max_n) {  // register-resident
     const dim3 grid((unsigned)batch);
     if (n <= tune().f64_strip16_max_n)
@@ -466,7 +468,7 @@ int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, d
       pfreg64_kernel<128, 32, 4><<<grid, 512, 0, s>>>(a, n, skew, sign, logabs);
     return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
   }
-  return launch_pr64_blocked(a, n, skew, batch, sign, logabs, ws, ws_bytes, s);  // lu64.hip
+  return launch_pr64_blocked(a, n, skew, batch, sign, logabs, ws, ws_bytes, s, spread);  // lu64.hip
 }
 
 // Workspace of the Gauss-Jordan path: none in registers (n <= f64_reg_max_n) or LDS.
@@ -555,7 +557,9 @@ size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n) {
   const size_t pr = fx_slogpf_f64_workspace(batch, n);
   const size_t inv = (lu64_path(n) ? align_up_256(lu64_inverse_workspace(batch, n)) : align_up_256(gj64_ws(batch, n, true))) +
                      align_up_256((size_t)batch * 2 * sizeof(double));
-  return align_up_256(pr) + std::max(inv, pf_adjugate_f64_ws(batch, n));
+  // + the blocked Parlett-Reid run's pair-pivot spread (the adjugate's route gate)
+  return align_up_256(pr) + std::max(inv, pf_adjugate_f64_ws(batch, n)) +
+         (lu64_path(n) ? align_up_256((size_t)batch * sizeof(double)) : 0);
 }
 
 int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
@@ -571,11 +575,14 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
   const size_t pr = align_up_256(fx_slogpf_f64_workspace(batch, n));
   const size_t gj = align_up_256(gj64_ws(batch, n, true));
   char* base = (char*)workspace;
-  st = launch_pr64(a, n, skew_symmetrize != 0, batch, sign, logabs, base, pr, s);
+  double* spread = lu64_path(n) ? (double*)(base + need - align_up_256((size_t)batch * sizeof(double))) : nullptr;
+  st = launch_pr64(a, n, skew_symmetrize != 0, batch, sign, logabs, base, pr, s, spread);
   if (st != FX_OK || n == 0) return st;
-  // the Pfaffian adjugate from its own Parlett-Reid run (cplx.hip)
+  // the Pfaffian adjugate (cplx.hip): the LU route, or the pivot-replaced Parlett-Reid
+  // formula for pf = 0 and numerically singular members
   if (adjugate)
-    return pf_adjugate_f64(a, batch, n, skew_symmetrize != 0, g, sign, logabs, base + pr, workspace_bytes - pr, s);
+    return pf_adjugate_f64(a, batch, n, skew_symmetrize != 0, g, sign, logabs, spread, base + pr,
+                           need - pr - (spread ? align_up_256((size_t)batch * sizeof(double)) : 0), s);
   // S^-1 by Gauss-Jordan (register kernels' orders) or the blocked LU solves on the same S,
   // zeroed where the Parlett-Reid run found pf = 0 (every member for odd n)
   if (lu64_path(n)) {

@@ -168,12 +168,12 @@ int launch_lu64_inverse(const double* A, int n, int skew, int64_t batch, double*
 // steps per panel, the trailing update on the fp64 MFMA
 size_t pr64_workspace(int64_t batch, int n);
 int launch_pr64_blocked(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
-                        size_t ws_bytes, hipStream_t s);
+                        size_t ws_bytes, hipStream_t s, double* spread = nullptr);
 
-// float64 Pfaffian adjugate pf(S) S^-1 (cplx.hip; zero for odd n); psign / plog: the
-// Parlett-Reid run's sign and log|pf| of the same S
+// float64 Pfaffian adjugate pf(S) S^-1 (cplx.hip; zero for odd n); psign / plog / spread:
+// the Parlett-Reid run's sign, log|pf| and pair-pivot spread (launch_pr64's) of the same S
 size_t pf_adjugate_f64_ws(int64_t batch, int n);
 int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, const double* psign,
-                    const double* plog, void* ws, size_t wsb, hipStream_t s);
+                    const double* plog, const double* spread, void* ws, size_t wsb, hipStream_t s);
 
 }  // namespace fx

@@ -103,7 +103,7 @@ __device__ __forceinline__ double half_diff(double v, double u) { return (v - u)
 // The blocked LU, its solves and the blocked Parlett-Reid for F = double, cx<float>,
 // cx<double> (lu64.hip): sign / logabs, and out = A^-T / A^-1 (times ssign exp(slog) when
 // ssign is given, zero where gate -- default: the factorisation's own sign -- is 0 or the
-// result is not finite); 0 < n <= 4096, every buffer of the batch.
+// result is not finite); 0 < n <= 8192, every buffer of the batch.
 template <class F>
 size_t blk_lu_workspace(int64_t batch, int n);
 template <class F>
@@ -119,6 +119,6 @@ template <class F>
 size_t blk_pr_workspace(int64_t batch, int n);
 template <class F>
 int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, typename Fd<F>::R* logabs, void* ws, size_t ws_bytes,
-           hipStream_t s);
+           hipStream_t s, double* spread = nullptr);
 
 }  // namespace fx

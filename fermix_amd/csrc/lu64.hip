@@ -1,5 +1,5 @@
 // Blocked LU with partial pivoting (sign, logabs) for the float64 and complex kinds above
-// the orders of their one-workgroup kernels, n <= 4096: the reference's `_lu_core` block
+// the orders of their one-workgroup kernels, n <= 8192: the reference's `_lu_core` block
 // loop (src/fermix/_lu.py:543-611: panel, row swaps, U rows, trailing GEMM) for the 64-bit
 // and complex fields, with the trailing update on the fp64 MFMA (v_mfma_f64_16x16x4f64;
 // a complex product as four real ones, complex64 operands widened to double). Every
@@ -605,10 +605,10 @@ constexpr int PRB = P64 / 2;  // pair steps per panel
 // rc: the current row c of the pair step; lacc / sacc / stat: log|pf| and the sign
 // (phase) so far and the zero-pivot flag (a flagged member skips its later panels).
 template <class F, int NT>
-__global__ __launch_bounds__(NT) void pr64_panel_kernel(F* __restrict__ W, int N, int r0, F* __restrict__ Ar,
+__global__ __launch_bounds__(NT) void pr64_panel_kernel(F* __restrict__ W, int N, int n, int r0, F* __restrict__ Ar,
                                                         F* __restrict__ Bk, F* __restrict__ rcg,
                                                         double* __restrict__ lacc, double2* __restrict__ sacc,
-                                                        int* __restrict__ stat) {
+                                                        int* __restrict__ stat, double2* __restrict__ lr) {
   using D = Fd<F>;
   __shared__ unsigned long long redk[2][NT / 64];
   __shared__ int redr[2][NT / 64];
@@ -622,6 +622,7 @@ __global__ __launch_bounds__(NT) void pr64_panel_kernel(F* __restrict__ W, int N
   F* rc = rcg + b * (int64_t)N;
   double lg = 0.0;  // thread 0's running sums, in pivot order
   double2 sg = make_double2(1.0, 0.0);
+  double lo = INFINITY, hi = -INFINITY;  // thread 0's range of log |d|
   bool sing = false;
   for (int p = 0; p < PRB; ++p) {
     const int c = r0 + 2 * p, q = c + 1;
@@ -700,13 +701,21 @@ __global__ __launch_bounds__(NT) void pr64_panel_kernel(F* __restrict__ W, int N
       Bb[(int64_t)p * N + x] = v;
       Bb[(int64_t)(PRB + p) * N + x] = u;
     }
-    if (tid == 0) D::acc(sg, lg, d);
+    if (tid == 0) {
+      D::acc(sg, lg, d);
+      if (c < n) {  // the pairs of the matrix, not of its padding
+        const double ld = log(D::mag(d));
+        lo = fmin(lo, ld);
+        hi = fmax(hi, ld);
+      }
+    }
     __syncthreads();
   }
   if (tid == 0) {
     if (sing) stat[b] = 1;
     lacc[b] += lg;
     sacc[b] = c2mul(sacc[b], sg);
+    lr[b] = make_double2(fmin(lr[b].x, lo), fmax(lr[b].y, hi));
   }
 }
 
@@ -716,9 +725,11 @@ __global__ __launch_bounds__(NT) void pr64_panel_kernel(F* __restrict__ W, int N
 // swap exchanges the two positions' registers through LDS, and the block is written once
 // at the end -- the arithmetic of pr64_panel_kernel element for element.
 template <class F, int NTR>
-__global__ __launch_bounds__(NTR) void pr64_panel_reg_kernel(F* __restrict__ W, int N, int r0, F* __restrict__ Ar,
+__global__ __launch_bounds__(NTR) void pr64_panel_reg_kernel(F* __restrict__ W, int N, int n, int r0,
+                                                             F* __restrict__ Ar,
                                                              F* __restrict__ Bk, double* __restrict__ lacc,
-                                                             double2* __restrict__ sacc, int* __restrict__ stat) {
+                                                             double2* __restrict__ sacc, int* __restrict__ stat,
+                                                             double2* __restrict__ lr) {
   using D = Fd<F>;
   __shared__ unsigned long long redk[2][NTR / 64];
   __shared__ int redr[2][NTR / 64];
@@ -737,6 +748,7 @@ __global__ __launch_bounds__(NTR) void pr64_panel_reg_kernel(F* __restrict__ W, 
   F rcx = D::zero();
   double lg = 0.0;  // thread 0's running sums, in pivot order
   double2 sg = make_double2(1.0, 0.0);
+  double lo = INFINITY, hi = -INFINITY;  // thread 0's range of log |d|
   bool sing = false;
   static_for<0, PRB>([&](auto pc) {
     constexpr int p = decltype(pc)::value;
@@ -823,7 +835,14 @@ __global__ __launch_bounds__(NTR) void pr64_panel_reg_kernel(F* __restrict__ W, 
     }
     u[p] = un;
     v[p] = vn;
-    if (tid == 0) D::acc(sg, lg, d);
+    if (tid == 0) {
+      D::acc(sg, lg, d);
+      if (c < n) {  // the pairs of the matrix, not of its padding
+        const double ld = log(D::mag(d));
+        lo = fmin(lo, ld);
+        hi = fmax(hi, ld);
+      }
+    }
     __syncthreads();
   });
   if (own && !sing) {
@@ -841,28 +860,33 @@ __global__ __launch_bounds__(NTR) void pr64_panel_reg_kernel(F* __restrict__ W, 
     if (sing) stat[b] = 1;
     lacc[b] += lg;
     sacc[b] = c2mul(sacc[b], sg);
+    lr[b] = make_double2(fmin(lr[b].x, lo), fmax(lr[b].y, hi));
   }
 }
 
 __global__ void pr64_init_kernel(double* __restrict__ lacc, double2* __restrict__ sacc, int* __restrict__ stat,
-                                 int64_t batch) {
+                                 double2* __restrict__ lr, int64_t batch) {
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= batch) return;
   lacc[b] = 0.0;
   sacc[b] = make_double2(1.0, 0.0);
   stat[b] = 0;
+  lr[b] = make_double2(INFINITY, -INFINITY);
 }
 
-// (sign, logabs): the running sums, (0, -inf) for flagged members and for odd n (odd)
+// (sign, logabs): the running sums, (0, -inf) for flagged members and for odd n (odd);
+// spread (when given): log max |d| - log min |d| over the pair pivots, +inf where pf = 0
 template <class F>
 __global__ void pr64_finish_kernel(const double* __restrict__ lacc, const double2* __restrict__ sacc,
-                                   const int* __restrict__ stat, int odd, F* __restrict__ sign,
-                                   RealOf<F>* __restrict__ logabs, int64_t batch) {
+                                   const int* __restrict__ stat, const double2* __restrict__ lr, int odd,
+                                   F* __restrict__ sign, RealOf<F>* __restrict__ logabs, double* __restrict__ spread,
+                                   int64_t batch) {
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= batch) return;
   const bool zero = odd || stat[b];
   sign[b] = zero ? Fd<F>::zero() : Fd<F>::from(sacc[b]);
   logabs[b] = zero ? RealOf<F>(-INFINITY) : RealOf<F>(lacc[b]);
+  if (spread) spread[b] = zero ? INFINITY : lr[b].y - lr[b].x;
 }
 
 template <class F>
@@ -874,6 +898,7 @@ struct Pr64Bufs {
   double* lacc;
   double2* sacc;
   int* stat;
+  double2* lr;  // (min, max) of log |d| over the pair pivots so far
 };
 
 template <class F>
@@ -891,6 +916,7 @@ Pr64Bufs<F> pr64_take(char* p, int64_t batch, int N) {
   f.lacc = (double*)take((size_t)batch * 8);
   f.sacc = (double2*)take((size_t)batch * 16);
   f.stat = (int*)take((size_t)batch * 4);
+  f.lr = (double2*)take((size_t)batch * 16);
   return f;
 }
 
@@ -907,7 +933,7 @@ size_t blk_lu_workspace(int64_t batch, int n) {
 template <class F>
 int blk_lu(const F* A, int n, int64_t batch, F* sign, RealOf<F>* logabs, void* ws, size_t ws_bytes, hipStream_t s) {
   if (batch <= 0) return FX_OK;
-  if (n <= 0 || n > 4096) return FX_ERR_UNSUPPORTED;
+  if (n <= 0 || n > 8192) return FX_ERR_UNSUPPORTED;
   if (!ws || ws_bytes < blk_lu_workspace<F>(batch, n)) return FX_ERR_WORKSPACE;
   const int N = lu64_padded(n);
   char* p = (char*)ws;
@@ -935,7 +961,7 @@ template <class F>
 int blk_lu_inverse(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logabs, const F* gate,
                    const F* ssign, const RealOf<F>* slog, F* out, int out_t, void* ws, size_t ws_bytes, hipStream_t s) {
   if (batch <= 0) return FX_OK;
-  if (n <= 0 || n > 4096) return FX_ERR_UNSUPPORTED;
+  if (n <= 0 || n > 8192) return FX_ERR_UNSUPPORTED;
   if (!ws || ws_bytes < blk_lu_inverse_workspace<F>(batch, n)) return FX_ERR_WORKSPACE;
   const int N = lu64_padded(n);
   char* p = (char*)ws;
@@ -972,20 +998,22 @@ size_t blk_pr_workspace(int64_t batch, int n) {
   const int N = lu64_padded(n);
   return al256((size_t)batch * N * N * sizeof(F)) + 2 * al256((size_t)batch * N * P64 * sizeof(F)) +
          al256((size_t)batch * N * sizeof(F)) + al256((size_t)batch * 8) + al256((size_t)batch * 16) +
-         al256((size_t)batch * 4);
+         al256((size_t)batch * 4) + al256((size_t)batch * 16);
 }
 
 // sign / logabs of pf(A) (skew: of (A - A^T) / 2) by the blocked Parlett-Reid: copy with
 // [[0, 1], [-1, 0]] padding to order N (a multiple of 32), 16 pair steps per panel
-// kernel, the K = 32 trailing update after each; (0, -inf) for odd n.
+// kernel, the K = 32 trailing update after each; (0, -inf) for odd n. spread (optional,
+// B doubles): log max |d| - log min |d| over the pair pivots of the matrix (not of its
+// padding), +inf where pf = 0.
 template <class F>
 int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logabs, void* ws, size_t ws_bytes,
-           hipStream_t s) {
+           hipStream_t s, double* spread) {
   if (batch <= 0) return FX_OK;
-  if (n <= 0 || n > 4096) return FX_ERR_UNSUPPORTED;
+  if (n <= 0 || n > 8192) return FX_ERR_UNSUPPORTED;
   const unsigned gb = (unsigned)((batch + 255) / 256);
   if (n & 1) {
-    pr64_finish_kernel<F><<<dim3(gb), 256, 0, s>>>(nullptr, nullptr, nullptr, 1, sign, logabs, batch);
+    pr64_finish_kernel<F><<<dim3(gb), 256, 0, s>>>(nullptr, nullptr, nullptr, nullptr, 1, sign, logabs, spread, batch);
     return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
   }
   if (!ws || ws_bytes < blk_pr_workspace<F>(batch, n)) return FX_ERR_WORKSPACE;
@@ -994,7 +1022,7 @@ int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logab
   const int64_t total = batch * (int64_t)N * N;
   lu64_copy_kernel<F><<<dim3(grid_of(total)), 256, 0, s>>>(A, n, skew, f.W, N, total, 1);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-  pr64_init_kernel<<<dim3(gb), 256, 0, s>>>(f.lacc, f.sacc, f.stat, batch);
+  pr64_init_kernel<<<dim3(gb), 256, 0, s>>>(f.lacc, f.sacc, f.stat, f.lr, batch);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
   const int64_t NN = (int64_t)N * N, NP = (int64_t)N * P64;
   for (int r0 = 0; r0 < N; r0 += P64) {
@@ -1004,12 +1032,12 @@ int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logab
     if constexpr (sizeof(F) == 8) {
       in_regs = N - r0 <= 512;
       if (in_regs)
-        pr64_panel_reg_kernel<F, 512><<<dim3((unsigned)batch), 512, 0, s>>>(f.W, N, r0, f.Ar, f.Bk, f.lacc, f.sacc,
-                                                                            f.stat);
+        pr64_panel_reg_kernel<F, 512><<<dim3((unsigned)batch), 512, 0, s>>>(f.W, N, n, r0, f.Ar, f.Bk, f.lacc, f.sacc,
+                                                                            f.stat, f.lr);
     }
     if (!in_regs)  // latency-bound column loops: more threads per matrix
-      pr64_panel_kernel<F, 1024><<<dim3((unsigned)batch), 1024, 0, s>>>(f.W, N, r0, f.Ar, f.Bk, f.rc, f.lacc, f.sacc,
-                                                                        f.stat);
+      pr64_panel_kernel<F, 1024><<<dim3((unsigned)batch), 1024, 0, s>>>(f.W, N, n, r0, f.Ar, f.Bk, f.rc, f.lacc, f.sacc,
+                                                                        f.stat, f.lr);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     const int r1 = r0 + P64;
     if (r1 >= N) break;
@@ -1018,7 +1046,7 @@ int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logab
                                         f.W + (int64_t)r1 * N + r1, N, NN, N - r1, N - r1, batch, s);
     if (st != FX_OK) return st;
   }
-  pr64_finish_kernel<F><<<dim3(gb), 256, 0, s>>>(f.lacc, f.sacc, f.stat, 0, sign, logabs, batch);
+  pr64_finish_kernel<F><<<dim3(gb), 256, 0, s>>>(f.lacc, f.sacc, f.stat, f.lr, 0, sign, logabs, spread, batch);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
@@ -1029,7 +1057,7 @@ int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logab
   template int blk_lu_inverse<F>(const F*, int, int, int64_t, F*, RealOf<F>*, const F*, const F*,                \
                                  const RealOf<F>*, F*, int, void*, size_t, hipStream_t);                         \
   template size_t blk_pr_workspace<F>(int64_t, int);                                                             \
-  template int blk_pr<F>(const F*, int, int, int64_t, F*, RealOf<F>*, void*, size_t, hipStream_t);
+  template int blk_pr<F>(const F*, int, int, int64_t, F*, RealOf<F>*, void*, size_t, hipStream_t, double*);
 FX_BLK_INST(double)
 FX_BLK_INST(cx<float>)
 FX_BLK_INST(cx<double>)
@@ -1049,8 +1077,8 @@ int launch_lu64_inverse(const double* A, int n, int skew, int64_t batch, double*
 }
 size_t pr64_workspace(int64_t batch, int n) { return blk_pr_workspace<double>(batch, n); }
 int launch_pr64_blocked(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
-                        size_t ws_bytes, hipStream_t s) {
-  return blk_pr<double>(A, n, skew, batch, sign, logabs, ws, ws_bytes, s);
+                        size_t ws_bytes, hipStream_t s, double* spread) {
+  return blk_pr<double>(A, n, skew, batch, sign, logabs, ws, ws_bytes, s, spread);
 }
 
 }  // namespace fx

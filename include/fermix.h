@@ -164,7 +164,7 @@ int32_t fx_pf_padded_size(int32_t n);
 /* ---------------------------------------------------------------- slogdet
  * sign[b], logabs[b] of det(a[b]) for b < batch: sign exactly +1 / -1, or 0 with
  * logabs = -inf for an exactly zero pivot. Sizes: every float32 entry point of this
- * header covers 0 <= n <= 8192 (the float64 and complex ones 0 <= n <= 4096) and returns
+ * header covers 0 <= n <= 8192 (the float64 and complex ones too) and returns
  * FX_ERR_UNSUPPORTED above. Above n = 4096 the LU panels spill registers and the
  * Parlett-Reid blocks are 8 columns wide (latency-bound; the trailing updates and GEMMs
  * are those of the smaller orders).
@@ -299,7 +299,7 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
  * The reference takes float64 through the same API (`_prep`, src/fermix/api.py:24-31,
  * with 64-bit fields, src/fermix/_field.py:20-120 and :265-275). These entry points are
  * the float64 counterparts of the ones above, with the same argument meaning, outputs
- * in float64 and 0 <= n <= 4096. For n <= fx_tune.f64_reg_max_n (128) one workgroup per
+ * in float64 and 0 <= n <= 8192. For n <= fx_tune.f64_reg_max_n (128) one workgroup per
  * matrix holds it in registers: an LU / Gauss-Jordan with partial pivoting
  * (`_slogdet_generic`, `_lu_parts_generic`, src/fermix/_fallback.py:36-97) and
  * Parlett-Reid (`_slogpf_generic`, :266-300), no workspace. Above, slogdet / det and the
@@ -333,9 +333,10 @@ int fx_slogpf_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmet
  * src/fermix/_fallback.py:101-192) from a Parlett-Reid run of its own (the smallest
  * pivot K by modulus, exact zero pivots and d_K replaced by 1) and one Gauss-Jordan
  * inverse of the replaced factorisation, a second exact zero pivot lifted to +1 and -1
- * (two inverses for those members); above n = 128 only the members with pf = 0 take that
- * route, the others pf(S) times S^-1 from the blocked LU solves; sign / logabs stay those
- * of the plain forward. */
+ * (two inverses for those members); above n = 128 only the members with pf = 0 or a
+ * numerically singular S (the forward's pair pivots spanning more than 2^18 in modulus)
+ * take that route, the others pf(S) times S^-1 from the blocked LU solves; sign / logabs
+ * stay those of the plain forward. */
 size_t fx_slogpf_parts_f64_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         double* sign, double* logabs, double* g, void* workspace, size_t workspace_bytes,
@@ -351,7 +352,7 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
  * of largest |re| + |im| (LAPACK's cabs1, the reference's `abs1`), sign = parity *
  * prod(d / |d|), logabs = sum log|d|, an exactly zero pivot gives sign 0 and logabs -inf;
  * inv_t = A^-T without conjugation (the holomorphic derivative of log det, as in
- * `_lu_parts_generic`, :63-97). 0 <= n <= 4096. Up to n = 64 one workgroup per matrix,
+ * `_lu_parts_generic`, :63-97). 0 <= n <= 8192. Up to n = 64 one workgroup per matrix,
  * the matrix in LDS when it fits (else one copy per member in the workspace; twice that
  * with the inverse); above, the blocked kernels of the float64 path on the complex field
  * (32-column LU panels, 16-pair Parlett-Reid panels, the trailing updates as four real
@@ -391,9 +392,10 @@ int fx_slogpf_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symme
  * src/fermix/_fallback.py:101-192) from a Parlett-Reid run of its own (the smallest
  * pivot K by modulus, exact zero pivots and d_K replaced by 1) and one Gauss-Jordan
  * inverse of the replaced factorisation, a second exact zero pivot lifted to +1 and -1
- * (two inverses for those members); above n = 128 only the members with pf = 0 take that
- * route, the others pf(S) times S^-1 from the blocked LU solves; sign / logabs stay those
- * of the plain forward. */
+ * (two inverses for those members); above n = 64 only the members with pf = 0 or a
+ * numerically singular S (the forward's pair pivots spanning more than 2^8 in modulus for
+ * complex64, 2^18 for complex128) take that route, the others pf(S) times S^-1 from the
+ * blocked LU solves; sign / logabs stay those of the plain forward. */
 size_t fx_slogpf_parts_c64_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
                         float* sign, float* logabs, float* g, void* workspace, size_t workspace_bytes,

@@ -186,3 +186,66 @@ def test_pf_adjugate_f64_blocked(dev):
         got = G1[i, jj]
         print(f"  G[{i}][{jj}] {got:.10g} vs {want:.10g}", flush=True)
         assert abs(got - want) <= 1e-9 * abs(want)
+
+
+def _rank_deficient_xjx(rng, n, dt):
+    """S = X J X^T with X = I + N(0, 1/(4n)) (complex: both parts) projected to rank n - 2
+    (its two smallest singular values set to zero): pf(S) = det(X) = 0 exactly, so the
+    stored S is singular up to its rounding and its adjugate pf(S) S^-1 is the rank-2
+    matrix of the (n - 2)-minor Pfaffians."""
+    X = rng.standard_normal((n, n))
+    if np.dtype(dt).kind == "c":
+        X = X + 1j * rng.standard_normal((n, n))
+    X = np.eye(n) + 0.5 * X / np.sqrt(n)
+    U, sv, Vt = np.linalg.svd(X)
+    sv[-2:] = 0.0
+    X = (U * sv) @ Vt
+    S = X @ _jmat(n) @ X.T
+    return (0.5 * (S - S.T)).astype(dt)
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+@pytest.mark.parametrize("n", [130, 256])
+def test_pf_adjugate_numerically_singular(dev, kind, n):
+    """A numerically singular member (S = X J X^T, X of rank n - 2: pf(S) at round-off
+    level) beside a regular one at the blocked sizes. pf(S) times an LU inverse of S would
+    be off by O(1) there (the LU's two small pivots and the Parlett-Reid run's small pair
+    pivot come from different factorisations); the member must take the pivot-replaced
+    formula. Entries against minor Pfaffians, G[i][j] = (-1)^(i+j) pf(S without i, j) for
+    i < j, at the largest entries and at random ones; S G = pf(S) I ~ 0 and G skew; the
+    regular member against pf(S) S^-1 in float64 / complex128."""
+    if kind == "c128" and n > 130:
+        pytest.skip("complex128 at n = 256 adds run time without a new code path")
+    dt, tol = KINDS[kind]
+    rng = np.random.default_rng(9700 + n)
+    S = np.stack([_rank_deficient_xjx(rng, n, dt), _near_j(rng, 1, n, dt)[0]])
+    print(f"pf adjugate numerically singular {kind} n={n}", flush=True)
+    St, sign, logabs, G = _pf_adj(S, dev)
+    s0, l0 = fermix_amd.slogpf(St, skew_symmetrize=False)
+    assert torch.equal(sign, s0) and torch.equal(logabs, l0)
+    assert np.all(np.isfinite(G))
+    W = _wide(S)
+    bar = tol * max(1.0, n / 16)
+    # the regular member: the LU route
+    ref = ref64.pf64(W[1]) * np.linalg.inv(W[1])
+    err = relerr(G[1], ref)
+    print(f"  regular relerr {err:.3g}", flush=True)
+    assert err < bar
+    G0 = _wide(G[0])
+    scale = np.abs(G0).max()
+    assert scale > 0
+    assert np.abs(G0 + G0.T).max() <= bar * scale
+    res = np.abs(W[0] @ G0).max() / (np.abs(W[0]).max() * scale * n)
+    print(f"  |S G| / (|S| |G| n) {res:.3g}", flush=True)
+    assert res < bar
+    iu, ju = np.triu_indices(n, 1)
+    order = np.argsort(-np.abs(G0[iu, ju]))
+    picks = list(order[:6]) + list(rng.choice(order[6:], 6, replace=False))
+    worst = 0.0
+    for t in picks:
+        i, j = int(iu[t]), int(ju[t])
+        keep = [x for x in range(n) if x not in (i, j)]
+        want = (-1.0) ** (i + j) * ref64.pf64(W[0][np.ix_(keep, keep)])
+        worst = max(worst, abs(G0[i, j] - want) / scale)
+    print(f"  minor Pfaffians: max |G - want| / max |G| {worst:.3g}", flush=True)
+    assert worst < bar

@@ -341,7 +341,7 @@ def test_complex_entry_points_host_checks():
         assert f(good, 2, 40, good + esz, good, ws, 1 << 40, None) == 1  # sign: one complex value
         assert f(good, -1, 40, good, good, ws, 1 << 40, None) == 1
         assert f(good, 0, 40, good, good, ws, 1 << 40, None) == 0
-        assert f(good, 2, 5000, good, good, ws, 1 << 40, None) == 4
+        assert f(good, 2, 8193, good, good, ws, 1 << 40, None) == 4
         assert getattr(L, f"fx_slogdet_parts_{k}")(good, 2, 40, good, good, bad, ws, 1 << 40, None) == 1
         assert getattr(L, f"fx_slogpf_{k}")(bad, 2, 40, 0, good, good, ws, 1 << 40, None) == 1
         assert getattr(L, f"fx_slogpf_parts_{k}")(good, 2, 40, 0, 0, good, good, bad, ws, 1 << 40, None) == 1
