@@ -215,7 +215,11 @@ def override(t=None, **changes):
 # n ranges -> kernel family (mirrors fx_slogdet_f32 / fx_slogpf_f32 dispatch)
 TINY_MAX_N = {"slogdet": 32, "slogpf": 16}  # several matrices per wave, one lane per row
 SMALL_MAX_N = 128  # largest n the fused one-workgroup-per-matrix kernels are built for
-LARGE_MAX_N = 8192  # blocked kernels (float32); larger n is unsupported
+LARGE_MAX_N = 8192  # blocked kernels (float32)
+# float32 above LARGE_MAX_N: the field-generic blocked kernels of the float64 path on
+# float storage (values and the gradients' parts runs, no packed factors); larger n is
+# unsupported
+GENERIC_MAX_N = 16384
 
 # The library's family override (read by every C entry point; a test hook like the
 # reference's OVERRIDE, src/fermix/_common.py:363-378, which its tests use to force a
@@ -238,7 +242,7 @@ def kernel_family(n, op="slogdet"):
     forced = os.environ.get(ENV, "")
     if forced in FAMILIES:
         if n > LARGE_MAX_N:
-            return "unsupported"
+            return "generic" if forced == "blocked" and n <= GENERIC_MAX_N else "unsupported"
         ok = {
             "tiny": n <= TINY_MAX_N[op],
             "fused": TINY_MAX_N[op] < n <= SMALL_MAX_N,
@@ -251,6 +255,8 @@ def kernel_family(n, op="slogdet"):
         return "fused-lds"
     if n <= LARGE_MAX_N:
         return "blocked"
+    if n <= GENERIC_MAX_N:
+        return "generic"
     return "unsupported"
 
 

@@ -69,11 +69,13 @@ static constexpr int PF_LARGE_MAX = PF_LARGE_MAXN;
 // Kernel families. The choice depends on n only (never on the batch), so a batched call
 // and a vmapped one run the same arithmetic: several matrices per wave (n <= 32 for the
 // LU, 16 for Parlett-Reid), one fused workgroup per matrix (n <= 128), blocked kernels
-// with workspace (n <= 8192). The environment variable FERMIX_AMD_KERNELS = tiny | fused
-// | blocked forces a family where it covers n (for cross-checks and tuning sweeps; an
-// uncovered n then reports FX_ERR_UNSUPPORTED). It is read on every call and the library
-// keeps no state of its own.
-enum { FAM_NONE = -1, FAM_TINY = 0, FAM_FUSED = 1, FAM_BLOCKED = 2 };
+// with workspace (n <= 8192), and above them the field-generic blocked kernels of the
+// float64 path on float storage (n <= GEN32_MAXN: values and the gradients' parts runs,
+// no packed factors). The environment variable FERMIX_AMD_KERNELS = tiny | fused |
+// blocked forces a family where it covers n (for cross-checks and tuning sweeps; an
+// uncovered n then reports FX_ERR_UNSUPPORTED; "blocked" keeps the generic family above
+// 8192). It is read on every call and the library keeps no state of its own.
+enum { FAM_NONE = -1, FAM_TINY = 0, FAM_FUSED = 1, FAM_BLOCKED = 2, FAM_GENERIC = 3 };
 
 static int family_override() {
   const char* e = getenv("FERMIX_AMD_KERNELS");
@@ -86,7 +88,11 @@ static int family_override() {
 
 // tiny_max: largest n of the tiny family for this factorisation; large_max: of the blocked.
 static int family(int n, int tiny_max, int large_max) {
-  if (n <= 0 || n > large_max) return FAM_NONE;
+  if (n <= 0 || n > GEN32_MAXN) return FAM_NONE;
+  if (n > large_max) {
+    const int o = family_override();
+    return o == FAM_NONE || o == FAM_BLOCKED ? FAM_GENERIC : FAM_NONE;
+  }
   switch (family_override()) {
     case FAM_TINY: return n <= tiny_max ? FAM_TINY : FAM_NONE;
     case FAM_FUSED: return (n > tiny_max && n <= SMALL_MAX) ? FAM_FUSED : FAM_NONE;
@@ -157,7 +163,7 @@ int32_t fx_lu_padded_size(int32_t n) {
   fx::TunePin pin_;
   if (n <= 0) return 0;
   const int f = lu_family(n);
-  if (f == FAM_NONE) return -1;
+  if (f == FAM_NONE || f == FAM_GENERIC) return -1;
   return f == FAM_BLOCKED ? lu_large_padded(n) : lu_small_padded(n);
 }
 
@@ -165,7 +171,7 @@ int32_t fx_pf_padded_size(int32_t n) {
   fx::TunePin pin_;
   if (n <= 0) return 0;
   const int f = pf_family(n);
-  if (f == FAM_NONE) return -1;
+  if (f == FAM_NONE || f == FAM_GENERIC) return -1;
   return f == FAM_BLOCKED ? pf_large_padded(n) : pf_small_padded(n);
 }
 
@@ -176,6 +182,7 @@ int32_t fx_pf_block_columns(int32_t n) {
 
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n) {
   fx::TunePin pin_;
+  if (batch > 0 && lu_family(n) == FAM_GENERIC) return gen32_slogdet_ws(batch, n);
   if (batch <= 0 || lu_family(n) != FAM_BLOCKED) return 0;
   return lu_large_workspace(chunk_batch(batch), n, false);
 }
@@ -197,6 +204,7 @@ int fx_slogdet_f32(const float* a, int64_t batch, int32_t n, float* sign, float*
         return launch_lu_large(a + b0 * n * n, n, nb, sign + b0, logabs + b0, workspace, workspace_bytes, false,
                                nullptr, nullptr, s, nullptr, nullptr, x3_of(prec), block_of(prec));
       });
+    case FAM_GENERIC: return gen32_slogdet(a, batch, n, sign, logabs, workspace, workspace_bytes, s);
     default: return FX_ERR_UNSUPPORTED;
   }
 }
@@ -227,6 +235,7 @@ size_t fx_slogdet_parts_f32_workspace(int64_t batch, int32_t n) {
   fx::TunePin pin_;
   const int fam = lu_family(n);
   if (batch <= 0 || fam == FAM_NONE) return 0;
+  if (fam == FAM_GENERIC) return gen32_slogdet_parts_ws(batch, n);
   return slogdet_parts_ws(chunk_batch(batch), n, fam);
 }
 
@@ -244,6 +253,10 @@ int fx_slogdet_parts_f32(const float* a, int64_t batch, int32_t n, int32_t zero_
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   const int fam = lu_family(n);
   if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (fam == FAM_GENERIC) {  // no packed factors, no unguarded inverse there
+    if (lu || !zero_singular) return FX_ERR_UNSUPPORTED;
+    return gen32_slogdet_parts(a, batch, n, sign, logabs, inv_t, workspace, workspace_bytes, s);
+  }
   if (!inv_t && fam != FAM_BLOCKED && lu)  // factors only: straight into the caller's buffers
     return lu_fused_factors(fam, a, n, batch, sign, logabs, lu, (int*)perm, s);
   if (inv_t && !lu && fam == FAM_TINY)  // one Gauss-Jordan pass, no workspace
@@ -301,7 +314,7 @@ int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign
   hipStream_t s = (hipStream_t)stream;
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   const int fam = lu_family(n);
-  if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (fam == FAM_NONE || fam == FAM_GENERIC) return FX_ERR_UNSUPPORTED;
   if (fam != FAM_BLOCKED) return lu_fused_factors(fam, a, n, batch, sign, logabs, lu, (int*)perm, s);
   const int N = fx_lu_padded_size(n);
   return for_chunks(batch, [&](int64_t b0, int64_t nb) {
@@ -312,7 +325,7 @@ int fx_slogdet_factors_f32(const float* a, int64_t batch, int32_t n, float* sign
 
 size_t fx_slogdet_inverse_f32_workspace(int64_t batch, int32_t n) {
   fx::TunePin pin_;
-  if (batch <= 0 || n <= 0 || lu_family(n) == FAM_NONE) return 0;
+  if (batch <= 0 || n <= 0 || lu_family(n) == FAM_NONE || lu_family(n) == FAM_GENERIC) return 0;
   const int N = fx_lu_padded_size(n);
   return lu_inverse_workspace(chunk_batch(batch), N, inv_padded(N) != N);
 }
@@ -326,7 +339,7 @@ int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, co
   if (!lu || !perm || !sign || !inv_t) return FX_ERR_INVALID_ARGUMENT;
   if (!al16(lu) || !al16(perm) || !al4(sign) || !al4(scale) || !al16(inv_t) || !al16(workspace))
     return FX_ERR_INVALID_ARGUMENT;
-  if (lu_family(n) == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (lu_family(n) == FAM_NONE || lu_family(n) == FAM_GENERIC) return FX_ERR_UNSUPPORTED;
   const size_t need = fx_slogdet_inverse_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_lu_padded_size(n);
@@ -340,6 +353,7 @@ int fx_slogdet_inverse_f32(float* lu, const int32_t* perm, const float* sign, co
 size_t fx_det_parts_f32_workspace(int64_t batch, int32_t n) {
   fx::TunePin pin_;
   if (batch <= 0 || lu_family(n) == FAM_NONE) return 0;
+  if (lu_family(n) == FAM_GENERIC) return gen32_det_parts_ws(batch, n);
   return fx_slogdet_parts_f32_workspace(batch, n) + align256(det_adjugate_workspace(chunk_batch(batch), n));
 }
 
@@ -354,6 +368,7 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
   if (n == 0) return fill2(sign, 1.0f, logabs, 0.0f, batch, s);
   const int fam = lu_family(n);
   if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (fam == FAM_GENERIC) return gen32_det_parts(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, s);
   const size_t need = fx_det_parts_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_lu_padded_size(n);
@@ -394,6 +409,7 @@ int fx_det_parts_f32(const float* a, int64_t batch, int32_t n, float* sign, floa
 
 size_t fx_slogpf_f32_workspace(int64_t batch, int32_t n) {
   fx::TunePin pin_;
+  if (batch > 0 && n % 2 == 0 && pf_family(n) == FAM_GENERIC) return gen32_slogpf_ws(batch, n);
   if (batch <= 0 || n % 2 || pf_family(n) != FAM_BLOCKED) return 0;
   return pf_large_workspace(chunk_batch(batch), n, false);
 }
@@ -417,6 +433,7 @@ int fx_slogpf_f32(const float* a, int64_t batch, int32_t n, int32_t skew_symmetr
   const int sk = skew_symmetrize ? 1 : 0;
   const int fam = pf_family(n);
   if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (fam == FAM_GENERIC) return gen32_slogpf(a, batch, n, sk, sign, logabs, workspace, workspace_bytes, s);
   if (fam != FAM_BLOCKED) return pf_fused(fam, a, n, sk, batch, sign, logabs, nullptr, nullptr, nullptr, s);
   return for_chunks(batch, [&](int64_t b0, int64_t nb) {
     return launch_pf_large(a + b0 * n * n, n, sk, nb, sign + b0, logabs + b0, nullptr, nullptr, nullptr, workspace,
@@ -443,7 +460,7 @@ int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew
   hipStream_t s = (hipStream_t)stream;
   const int sk = skew_symmetrize ? 1 : 0;
   const int fam = pf_family(n);
-  if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (fam == FAM_NONE || fam == FAM_GENERIC) return FX_ERR_UNSUPPORTED;
   if (fam != FAM_BLOCKED) return pf_fused(fam, a, n, sk, batch, sign, logabs, gbuf, d, (int*)perm, s);
   const int N = fx_pf_padded_size(n);
   return for_chunks(batch, [&](int64_t b0, int64_t nb) {
@@ -454,7 +471,7 @@ int fx_slogpf_factors_f32(const float* a, int64_t batch, int32_t n, int32_t skew
 
 size_t fx_slogpf_inverse_f32_workspace(int64_t batch, int32_t n) {
   fx::TunePin pin_;
-  if (batch <= 0 || n <= 0 || n % 2 || pf_family(n) == FAM_NONE) return 0;
+  if (batch <= 0 || n <= 0 || n % 2 || pf_family(n) == FAM_NONE || pf_family(n) == FAM_GENERIC) return 0;
   return pf_inverse_workspace(chunk_batch(batch), fx_pf_padded_size(n));
 }
 
@@ -470,7 +487,7 @@ int fx_slogpf_inverse_f32(const float* gbuf, const float* d, const int32_t* perm
   hipStream_t s = (hipStream_t)stream;
   if (n % 2 == 1) return fill(g, 0.0f, batch * (int64_t)n * n, s);
   if (!gbuf || !d || !perm) return FX_ERR_INVALID_ARGUMENT;
-  if (pf_family(n) == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (pf_family(n) == FAM_NONE || pf_family(n) == FAM_GENERIC) return FX_ERR_UNSUPPORTED;
   const size_t need = fx_slogpf_inverse_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_pf_padded_size(n);
@@ -493,6 +510,7 @@ size_t fx_slogpf_parts_f32_workspace(int64_t batch, int32_t n) {
   fx::TunePin pin_;
   const int fam = pf_family(n);
   if (batch <= 0 || n % 2 || fam == FAM_NONE) return 0;
+  if (fam == FAM_GENERIC) return gen32_slogpf_parts_ws(batch, n);
   return slogpf_parts_ws(chunk_batch(batch), n, fam);
 }
 
@@ -513,6 +531,9 @@ int fx_slogpf_parts_f32(const float* a, int64_t batch, int32_t n, int32_t skew_s
   }
   const int fam = pf_family(n);
   if (fam == FAM_NONE) return FX_ERR_UNSUPPORTED;
+  if (fam == FAM_GENERIC)
+    return gen32_slogpf_parts(a, batch, n, skew_symmetrize ? 1 : 0, adjugate ? 1 : 0, sign, logabs, g, workspace,
+                              workspace_bytes, s);
   const size_t need = fx_slogpf_parts_f32_workspace(batch, n);
   if (!workspace || workspace_bytes < need) return FX_ERR_WORKSPACE;
   const int N = fx_pf_padded_size(n);

@@ -569,6 +569,17 @@ template <>
 struct Kind<double> {
   using R = double;
 };
+template <>
+struct Kind<float> {
+  using R = float;
+};
+
+// the largest order of a field's entry points here: float32 reaches these templates only
+// above its own blocked kernels, up to the blocked kernels' float32 limit
+template <class F>
+constexpr int max_n() {
+  return sizeof(F) == 4 ? GEN32_MAXN : CX_MAXN;
+}
 
 template <class F>
 int launch_cgj(const void* a, int n, int skew, int64_t batch, void* sign, void* logabs, void* out, int mode,
@@ -612,7 +623,7 @@ int check_cx_args(const void* a, int64_t batch, int n, const void* sign, const v
                   const void* ws) {
   using R = typename Kind<F>::R;
   if (batch < 0 || n < 0) return FX_ERR_INVALID_ARGUMENT;
-  if (n > CX_MAXN) return FX_ERR_UNSUPPORTED;
+  if (n > max_n<F>()) return FX_ERR_UNSUPPORTED;
   if (batch > 0 && (!sign || !logabs || (n > 0 && !a))) return FX_ERR_INVALID_ARGUMENT;
   auto mis = [](const void* p, uintptr_t m) { return ((uintptr_t)p & m) != 0; };
   if (mis(a, 15) || mis(out, 15) || mis(ws, 15) || mis(sign, sizeof(F) - 1) || mis(logabs, sizeof(R) - 1))
@@ -640,19 +651,19 @@ int cx_empty(void* sign, void* logabs, int64_t batch, hipStream_t s) {
 
 template <class F>
 size_t slogdet_ws(int64_t batch, int n) {
-  if (n > CX_MAXN) return 0;
+  if (n > max_n<F>()) return 0;
   return blocked<F>(n) ? blk_lu_workspace<F>(batch, n) : cx_matrix_ws<F>(batch, n, n);
 }
 template <class F>
 size_t slogdet_parts_ws(int64_t batch, int n) {
-  if (n > CX_MAXN) return 0;
+  if (n > max_n<F>()) return 0;
   return blocked<F>(n) ? blk_lu_inverse_workspace<F>(batch, n) : cx_matrix_ws<F>(batch, n, 2 * n);
 }
 // det's gradient: blocked, the LU solves plus the Gauss-Jordan run for the singular members
 // (its [A | I] and its sign / logabs in scratch)
 template <class F>
 size_t det_parts_ws(int64_t batch, int n) {
-  if (n > CX_MAXN || !blocked<F>(n) || batch <= 0) return slogdet_parts_ws<F>(batch, n);
+  if (n > max_n<F>() || !blocked<F>(n) || batch <= 0) return slogdet_parts_ws<F>(batch, n);
   return align_up(blk_lu_inverse_workspace<F>(batch, n)) + align_up(cx_matrix_ws<F>(batch, n, 2 * n)) +
          align_up((size_t)batch * 2 * sizeof(F));
 }
@@ -780,7 +791,7 @@ int pf_gate(const F* sign, const double* spread, F* gate, int64_t batch, hipStre
 // bytes; none while they fit in LDS) and the per-member metadata.
 template <class F>
 size_t pf_adjugate_ws(int64_t batch, int n) {
-  if (batch <= 0 || n <= 0 || (n & 1) || n > CX_MAXN) return 0;
+  if (batch <= 0 || n <= 0 || (n & 1) || n > max_n<F>()) return 0;
   const size_t mats = std::max(cx_matrix_ws<F>(batch, n, n), cx_matrix_ws<F>(batch, n, 2 * n));
   return align_up(mats) + align_up((size_t)batch * pfa_layout<F>(n).stride);
 }
@@ -828,17 +839,59 @@ int pf_adjugate(const F* a, int64_t batch, int n, int skew, F* g, void* ws, size
   return FX_OK;
 }
 
+// The blocked parts run of a field (complex above CX_BLK_MIN, float32 above its own
+// blocked kernels): the blocked Parlett-Reid for sign / logabs and the pair pivots'
+// spread, then g: S^-1 from the blocked LU solves of the same S (zero where pf = 0), or the
+// Pfaffian adjugate pf(S) S^-1 -- from the same solves scaled by the Parlett-Reid pf for
+// the members the gate passes, from the pivot-replaced Parlett-Reid formula for the others
+// (pf = 0, or pair pivots spanning more than pf_lu_spread_max). Workspace: the
+// Parlett-Reid run's, then max(LU solves + their sign / logabs, the formula's), then the
+// spread and the gate.
+template <class F>
+size_t blk_pf_parts_body(int64_t batch, int n) {
+  using R = typename Fd<F>::R;
+  return std::max(align_up(blk_lu_inverse_workspace<F>(batch, n)) + align_up((size_t)batch * (sizeof(F) + sizeof(R))),
+                  pf_adjugate_ws<F>(batch, n));
+}
+template <class F>
+size_t blk_pf_parts_ws(int64_t batch, int n) {
+  if (batch <= 0 || n <= 0 || n > max_n<F>()) return 0;
+  return align_up(blk_pr_workspace<F>(batch, n)) + blk_pf_parts_body<F>(batch, n) +
+         align_up((size_t)batch * sizeof(double)) + align_up((size_t)batch * sizeof(F));
+}
+template <class F>
+int blk_pf_parts(const F* A, int64_t batch, int n, int skew, int adjugate, F* sign, typename Fd<F>::R* logabs, F* g,
+                 void* ws, size_t wsb, hipStream_t s) {
+  using R = typename Fd<F>::R;
+  if (!ws || wsb < blk_pf_parts_ws<F>(batch, n)) return FX_ERR_WORKSPACE;
+  const size_t pr = align_up(blk_pr_workspace<F>(batch, n));
+  const size_t body = blk_pf_parts_body<F>(batch, n);
+  const size_t lw = align_up(blk_lu_inverse_workspace<F>(batch, n));
+  char* base = (char*)ws;
+  double* spread = (double*)(base + pr + body);
+  F* gz = (F*)(base + pr + body + align_up((size_t)batch * sizeof(double)));
+  int st = blk_pr<F>(A, n, skew, batch, sign, logabs, base, pr, s, spread);
+  if (st != FX_OK) return st;
+  if (adjugate && (n & 1)) return cx_zero<F>(g, batch * (int64_t)n * n, s);
+  F* gsign = (F*)(base + pr + lw);
+  R* glog = (R*)(gsign + batch);
+  const F* gate = sign;
+  if (adjugate) {
+    st = pf_gate<F>(sign, spread, gz, batch, s);
+    if (st != FX_OK) return st;
+    gate = gz;
+  }
+  st = blk_lu_inverse<F>(A, n, skew, batch, gsign, glog, gate, adjugate ? sign : nullptr, adjugate ? logabs : nullptr,
+                         g, 0, base + pr, lw, s);
+  if (st != FX_OK || !adjugate) return st;
+  return pf_adjugate<F>(A, batch, n, skew, g, base + pr, body, s, gate);
+}
+
 template <class T>
 size_t slogpf_parts_ws(int64_t batch, int n) {
   if (n > CX_MAXN || batch <= 0) return 0;
-  const size_t scratch = align_up((size_t)batch * 3 * sizeof(T));
-  if (blocked<cx<T>>(n)) {
-    // + the pivot spread and the route gate of the adjugate mode
-    const size_t inv = align_up(blk_lu_inverse_workspace<cx<T>>(batch, n)) + scratch;
-    return align_up(slogpf_ws<T>(batch, n)) + std::max(inv, pf_adjugate_ws<cx<T>>(batch, n)) +
-           align_up((size_t)batch * sizeof(double)) + align_up((size_t)batch * sizeof(cx<T>));
-  }
-  const size_t inv = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n)) + scratch;
+  if (blocked<cx<T>>(n)) return blk_pf_parts_ws<cx<T>>(batch, n);
+  const size_t inv = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n)) + align_up((size_t)batch * 3 * sizeof(T));
   return align_up(slogpf_ws<T>(batch, n)) + std::max(inv, pf_adjugate_ws<cx<T>>(batch, n));
 }
 
@@ -860,36 +913,15 @@ int slogpf_parts(const T* a, int64_t batch, int n, int skew, int adjugate, T* si
   if (st != FX_OK || batch == 0) return st;
   if (!g) return slogpf<T>(a, batch, n, skew, sign, logabs, ws, wsb, s);
   if (n == 0) return cx_empty<cx<T>>(sign, logabs, batch, s);
+  if (blocked<cx<T>>(n))
+    return blk_pf_parts<cx<T>>((const cx<T>*)a, batch, n, skew != 0, adjugate, (cx<T>*)sign, logabs, (cx<T>*)g, ws,
+                               wsb, s);
   if (wsb < slogpf_parts_ws<T>(batch, n) || (!ws && slogpf_parts_ws<T>(batch, n))) return FX_ERR_WORKSPACE;
   const size_t pr = align_up(slogpf_ws<T>(batch, n));
   char* base = (char*)ws;
-  const bool blk = blocked<cx<T>>(n);
-  const size_t lw = blk ? align_up(blk_lu_inverse_workspace<cx<T>>(batch, n)) : 0;
-  const size_t body = blk ? std::max(lw + align_up((size_t)batch * 3 * sizeof(T)), pf_adjugate_ws<cx<T>>(batch, n)) : 0;
-  double* spread = blk ? (double*)(base + pr + body) : nullptr;
-  st = launch_pf<T>(a, n, skew != 0, batch, sign, logabs, base, pr, s, spread);
+  st = launch_pf<T>(a, n, skew != 0, batch, sign, logabs, base, pr, s);
   if (st != FX_OK) return st;
   if (adjugate && (n & 1)) return cx_zero<cx<T>>((cx<T>*)g, batch * (int64_t)n * n, s);
-  if (blk) {
-    // S^-1 from the blocked LU solves, zero where pf = 0; adjugate: pf(S) S^-1 from the
-    // same solves for the members the gate passes, the pivot-replaced Parlett-Reid formula
-    // below for the others (pf = 0, or a pair pivot at round-off level)
-    const cx<T>* A = (const cx<T>*)a;
-    const cx<T>* sg = (const cx<T>*)sign;
-    cx<T>* gsign = (cx<T>*)(base + pr + lw);
-    T* glog = (T*)(gsign + batch);
-    const cx<T>* gate = sg;
-    if (adjugate) {
-      cx<T>* gz = (cx<T>*)(base + pr + body + align_up((size_t)batch * sizeof(double)));
-      st = pf_gate<cx<T>>(sg, spread, gz, batch, s);
-      if (st != FX_OK) return st;
-      gate = gz;
-    }
-    st = blk_lu_inverse<cx<T>>(A, n, skew != 0, batch, gsign, glog, gate, adjugate ? sg : nullptr,
-                               adjugate ? logabs : nullptr, (cx<T>*)g, 0, base + pr, lw, s);
-    if (st != FX_OK || !adjugate) return st;
-    return pf_adjugate<cx<T>>(A, batch, n, skew != 0, (cx<T>*)g, base + pr, body, s, gate);
-  }
   if (adjugate)
     return pf_adjugate<cx<T>>((const cx<T>*)a, batch, n, skew != 0, (cx<T>*)g, base + pr, wsb - pr, s);
   const size_t gj = align_up(cx_matrix_ws<cx<T>>(batch, n, 2 * n));
@@ -928,6 +960,38 @@ int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, 
     r = launch_lu64_inverse(a, n, skew, batch, lsign, lsign + batch, gate, psign, plog, g, 0, ws, lw, s);
   if (r != FX_OK) return r;
   return pf_adjugate<double>(a, batch, n, skew, g, ws, body, s, gate);
+}
+
+// ---- float32 above its own blocked kernels (LU_LARGE_MAXN < n <= GEN32_MAXN): the
+// field-generic blocked kernels of lu64.hip on float storage (32-column panels, the
+// trailing products on the fp64 MFMA), with the entry points' argument checks done by the
+// caller. det's and pf's gradients as for the complex kinds: the LU solves for the regular
+// members, the Gauss-Jordan continuation / pivot-replaced Parlett-Reid formula (one
+// workgroup per member) for the exactly singular and, for pf, numerically singular ones.
+size_t gen32_slogdet_ws(int64_t batch, int n) { return blk_lu_workspace<float>(batch, n); }
+int gen32_slogdet(const float* a, int64_t batch, int n, float* sign, float* logabs, void* ws, size_t wsb,
+                  hipStream_t s) {
+  return blk_lu<float>(a, n, batch, sign, logabs, ws, wsb, s);
+}
+size_t gen32_slogdet_parts_ws(int64_t batch, int n) { return blk_lu_inverse_workspace<float>(batch, n); }
+int gen32_slogdet_parts(const float* a, int64_t batch, int n, float* sign, float* logabs, float* inv_t, void* ws,
+                        size_t wsb, hipStream_t s) {
+  return slogdet_parts<float>(a, batch, n, sign, logabs, inv_t, ws, wsb, s);
+}
+size_t gen32_det_parts_ws(int64_t batch, int n) { return det_parts_ws<float>(batch, n); }
+int gen32_det_parts(const float* a, int64_t batch, int n, float* sign, float* logabs, float* adj_t, void* ws,
+                    size_t wsb, hipStream_t s) {
+  return det_parts<float>(a, batch, n, sign, logabs, adj_t, ws, wsb, s);
+}
+size_t gen32_slogpf_ws(int64_t batch, int n) { return blk_pr_workspace<float>(batch, n); }
+int gen32_slogpf(const float* a, int64_t batch, int n, int skew, float* sign, float* logabs, void* ws, size_t wsb,
+                 hipStream_t s) {
+  return blk_pr<float>(a, n, skew, batch, sign, logabs, ws, wsb, s);
+}
+size_t gen32_slogpf_parts_ws(int64_t batch, int n) { return blk_pf_parts_ws<float>(batch, n); }
+int gen32_slogpf_parts(const float* a, int64_t batch, int n, int skew, int adjugate, float* sign, float* logabs,
+                       float* g, void* ws, size_t wsb, hipStream_t s) {
+  return blk_pf_parts<float>(a, batch, n, skew, adjugate, sign, logabs, g, ws, wsb, s);
 }
 
 }  // namespace fx

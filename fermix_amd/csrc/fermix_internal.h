@@ -176,4 +176,25 @@ size_t pf_adjugate_f64_ws(int64_t batch, int n);
 int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, const double* psign,
                     const double* plog, const double* spread, void* ws, size_t wsb, hipStream_t s);
 
+// float32 above LU_LARGE_MAXN / PF_LARGE_MAXN up to GEN32_MAXN (cplx.hip): the blocked
+// kernels of lu64.hip on float storage; the caller checks the arguments. slogdet_parts:
+// A^-T zero for singular members; det_parts: adj(A)^T; slogpf_parts: S^-1 (zero where
+// pf = 0) or, with adjugate, pf(S) S^-1.
+constexpr int GEN32_MAXN = 16384;
+size_t gen32_slogdet_ws(int64_t batch, int n);
+int gen32_slogdet(const float* a, int64_t batch, int n, float* sign, float* logabs, void* ws, size_t wsb,
+                  hipStream_t s);
+size_t gen32_slogdet_parts_ws(int64_t batch, int n);
+int gen32_slogdet_parts(const float* a, int64_t batch, int n, float* sign, float* logabs, float* inv_t, void* ws,
+                        size_t wsb, hipStream_t s);
+size_t gen32_det_parts_ws(int64_t batch, int n);
+int gen32_det_parts(const float* a, int64_t batch, int n, float* sign, float* logabs, float* adj_t, void* ws,
+                    size_t wsb, hipStream_t s);
+size_t gen32_slogpf_ws(int64_t batch, int n);
+int gen32_slogpf(const float* a, int64_t batch, int n, int skew, float* sign, float* logabs, void* ws, size_t wsb,
+                 hipStream_t s);
+size_t gen32_slogpf_parts_ws(int64_t batch, int n);
+int gen32_slogpf_parts(const float* a, int64_t batch, int n, int skew, int adjugate, float* sign, float* logabs,
+                       float* g, void* ws, size_t wsb, hipStream_t s);
+
 }  // namespace fx

@@ -6,6 +6,7 @@
 #pragma once
 
 #include "common.h"
+#include "fermix_internal.h"
 
 namespace fx {
 
@@ -89,6 +90,42 @@ struct Fd<double> {
   static __device__ __forceinline__ double scale(double a, double2 s) { return a * s.x; }
 };
 
+// float32 above the orders of the float32 blocked kernels: the generic blocked path of the
+// 64-bit kinds on float storage (the products of its GEMMs in fp64), with the float64
+// conventions (sign flipped per negative pivot, log|d| summed in double in pivot order)
+template <>
+struct Fd<float> {
+  using R = float;
+  static __device__ __forceinline__ float zero() { return 0.0f; }
+  static __device__ __forceinline__ float one() { return 1.0f; }
+  static __device__ __forceinline__ bool is0(float x) { return x == 0.0f; }
+  static __device__ __forceinline__ unsigned long long key(float x) { return key64((double)x); }
+  static __device__ __forceinline__ float mul(float a, float b) { return a * b; }
+  static __device__ __forceinline__ float fms(float r, float l, float p) { return fmaf(-l, p, r); }
+  static __device__ __forceinline__ float rcp(float x) { return x != 0.0f ? 1.0f / x : 0.0f; }
+  static __device__ __forceinline__ bool finite(float x) { return isfinite(x); }
+  static __device__ __forceinline__ void acc(double2& sgn, double& logabs, float x) {
+    logabs += log(fabs((double)x));
+    if (x < 0.0f) sgn.x = -sgn.x;
+  }
+  static __device__ __forceinline__ float from(double2 v) { return (float)v.x; }
+  static __device__ __forceinline__ double2 to2(float x) { return make_double2(x, 0.0); }
+  static __device__ __forceinline__ double mag(float x) { return fabs((double)x); }
+  static __device__ __forceinline__ float add(float a, float b) { return a + b; }
+  static __device__ __forceinline__ float sub(float a, float b) { return a - b; }
+  static __device__ __forceinline__ float neg(float a) { return -a; }
+  static __device__ __forceinline__ float div(float a, float b) { return a / b; }
+  static __device__ __forceinline__ float scale(float a, double2 s) { return (float)(a * s.x); }
+};
+
+// largest order of the blocked kernels of lu64.hip per field: float32 runs them only
+// above its own blocked kernels' 8192
+constexpr int BLK_MAXN = 8192;
+template <class F>
+constexpr int blk_max_n() {
+  return sizeof(F) == 4 ? GEN32_MAXN : BLK_MAXN;
+}
+
 __device__ __forceinline__ double2 c2mul(double2 a, double2 b) {
   return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
 }
@@ -99,11 +136,12 @@ __device__ __forceinline__ cx<T> half_diff(cx<T> v, cx<T> u) {
   return {(v.re - u.re) * T(0.5), (v.im - u.im) * T(0.5)};
 }
 __device__ __forceinline__ double half_diff(double v, double u) { return (v - u) * 0.5; }
+__device__ __forceinline__ float half_diff(float v, float u) { return (v - u) * 0.5f; }
 
 // The blocked LU, its solves and the blocked Parlett-Reid for F = double, cx<float>,
 // cx<double> (lu64.hip): sign / logabs, and out = A^-T / A^-1 (times ssign exp(slog) when
 // ssign is given, zero where gate -- default: the factorisation's own sign -- is 0 or the
-// result is not finite); 0 < n <= 8192, every buffer of the batch.
+// result is not finite); 0 < n <= blk_max_n<F>(), every buffer of the batch.
 template <class F>
 size_t blk_lu_workspace(int64_t batch, int n);
 template <class F>

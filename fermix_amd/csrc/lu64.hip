@@ -45,7 +45,7 @@ using RealOf = typename Fd<F>::R;
 
 template <class F>
 constexpr bool is_real() {
-  return sizeof(F) == sizeof(double) && sizeof(RealOf<F>) == sizeof(double);
+  return sizeof(F) == sizeof(RealOf<F>);
 }
 
 // W (B, N, N) = A (B, n, n) with identity padding (skew: (A - A^T) / 2), or, with pfpad
@@ -264,9 +264,10 @@ __global__ __launch_bounds__(NT64) void lu64_rows_kernel(const F* __restrict__ W
 // B[l / 16][l % 16]; accumulator element v of lane l is row l / 16 + 4 v, column l % 16
 // (measured with a one-wave probe: unlike the fp32 16x16x4 layout, a lane's four rows
 // are 4 apart). Serves the trailing update A22 -= L21 U12 and both solves' updates.
-__global__ __launch_bounds__(256) void lu64_gemm_kernel(const double* __restrict__ A, int lda, int64_t sA,
-                                                        const double* __restrict__ Bm, int ldb, int64_t sB,
-                                                        double* __restrict__ C, int ldc, int64_t sC, int M, int NC,
+template <class E>
+__global__ __launch_bounds__(256) void lu64_gemm_kernel(const E* __restrict__ A, int lda, int64_t sA,
+                                                        const E* __restrict__ Bm, int ldb, int64_t sB,
+                                                        E* __restrict__ C, int ldc, int64_t sC, int M, int NC,
                                                         int ntr, int ntc) {
   __shared__ double As[64][P64 + 1];
   __shared__ double Bs[P64][64 + 1];
@@ -274,15 +275,15 @@ __global__ __launch_bounds__(256) void lu64_gemm_kernel(const double* __restrict
   const int64_t b = blockIdx.x / nt;
   const int t = (int)(blockIdx.x - b * nt);
   const int i0 = 64 * (t / ntc), j0 = 64 * (t % ntc);
-  const double* Ab = A + b * sA;
-  const double* Bb = Bm + b * sB;
-  double* Cb = C + b * sC;
+  const E* Ab = A + b * sA;
+  const E* Bb = Bm + b * sB;
+  E* Cb = C + b * sC;
   const int tid = threadIdx.x;
   for (int e = tid; e < 64 * P64; e += 256) {
     const int i = e / P64, k = e % P64;
-    As[i][k] = i0 + i < M ? Ab[(int64_t)(i0 + i) * lda + k] : 0.0;
+    As[i][k] = i0 + i < M ? (double)Ab[(int64_t)(i0 + i) * lda + k] : 0.0;
     const int kk = e / 64, j = e % 64;
-    Bs[kk][j] = j0 + j < NC ? Bb[(int64_t)kk * ldb + j0 + j] : 0.0;
+    Bs[kk][j] = j0 + j < NC ? (double)Bb[(int64_t)kk * ldb + j0 + j] : 0.0;
   }
   __syncthreads();
   const int wave = tid >> 6, lane = tid & 63;
@@ -316,8 +317,8 @@ __global__ __launch_bounds__(256) void lu64_gemm_kernel(const double* __restrict
       for (int v = 0; v < 4; ++v) {
         const int row = i0 + wm + 16 * a + lk + 4 * v;
         if (row < M && col < NC) {
-          double* e = Cb + (int64_t)row * ldc + col;
-          *e = *e - acc[a][c][v];
+          E* e = Cb + (int64_t)row * ldc + col;
+          *e = E((double)*e - acc[a][c][v]);
         }
       }
     }
@@ -532,8 +533,7 @@ int lu64_gemm_strided(const F* A, int lda, int64_t sA, const F* Bm, int ldb, int
   const int ntr = (M + 63) / 64, ntc = (NC + 63) / 64;
   const dim3 grid((unsigned)(batch * ntr * ntc));
   if constexpr (is_real<F>())
-    lu64_gemm_kernel<<<grid, 256, 0, s>>>((const double*)A, lda, sA, (const double*)Bm, ldb, sB, (double*)C, ldc, sC,
-                                          M, NC, ntr, ntc);
+    lu64_gemm_kernel<F><<<grid, 256, 0, s>>>(A, lda, sA, Bm, ldb, sB, C, ldc, sC, M, NC, ntr, ntc);
   else
     lucx_gemm_kernel<RealOf<F>><<<grid, 256, 0, s>>>(A, lda, sA, Bm, ldb, sB, C, ldc, sC, M, NC, ntr, ntc);
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
@@ -565,7 +565,7 @@ int lu64_factor(const F* A, int n, int skew, int64_t batch, const Lu64Bufs<F>& f
     bool in_regs = N - r0 <= 512;  // the panel's rows in registers
     if (in_regs) {
       lu64_panel_reg_kernel<F, 512><<<dim3((unsigned)batch), 512, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
-    } else if constexpr (sizeof(F) == 8) {
+    } else if constexpr (sizeof(F) <= 8) {
       in_regs = N - r0 <= 1024;
       if (in_regs)
         lu64_panel_reg_kernel<F, 1024><<<dim3((unsigned)batch), 1024, 0, s>>>(f.W, N, r0, f.ipiv, f.dpiv, f.nsw);
@@ -933,7 +933,7 @@ size_t blk_lu_workspace(int64_t batch, int n) {
 template <class F>
 int blk_lu(const F* A, int n, int64_t batch, F* sign, RealOf<F>* logabs, void* ws, size_t ws_bytes, hipStream_t s) {
   if (batch <= 0) return FX_OK;
-  if (n <= 0 || n > 8192) return FX_ERR_UNSUPPORTED;
+  if (n <= 0 || n > blk_max_n<F>()) return FX_ERR_UNSUPPORTED;
   if (!ws || ws_bytes < blk_lu_workspace<F>(batch, n)) return FX_ERR_WORKSPACE;
   const int N = lu64_padded(n);
   char* p = (char*)ws;
@@ -961,7 +961,7 @@ template <class F>
 int blk_lu_inverse(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logabs, const F* gate,
                    const F* ssign, const RealOf<F>* slog, F* out, int out_t, void* ws, size_t ws_bytes, hipStream_t s) {
   if (batch <= 0) return FX_OK;
-  if (n <= 0 || n > 8192) return FX_ERR_UNSUPPORTED;
+  if (n <= 0 || n > blk_max_n<F>()) return FX_ERR_UNSUPPORTED;
   if (!ws || ws_bytes < blk_lu_inverse_workspace<F>(batch, n)) return FX_ERR_WORKSPACE;
   const int N = lu64_padded(n);
   char* p = (char*)ws;
@@ -1010,7 +1010,7 @@ template <class F>
 int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logabs, void* ws, size_t ws_bytes,
            hipStream_t s, double* spread) {
   if (batch <= 0) return FX_OK;
-  if (n <= 0 || n > 8192) return FX_ERR_UNSUPPORTED;
+  if (n <= 0 || n > blk_max_n<F>()) return FX_ERR_UNSUPPORTED;
   const unsigned gb = (unsigned)((batch + 255) / 256);
   if (n & 1) {
     pr64_finish_kernel<F><<<dim3(gb), 256, 0, s>>>(nullptr, nullptr, nullptr, nullptr, 1, sign, logabs, spread, batch);
@@ -1029,7 +1029,7 @@ int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logab
     // the panel's (U, V) in registers for 8-byte elements up to 512 rows (the 16-byte
     // complex128 entries, and 1024-thread workgroups, would spill)
     bool in_regs = false;
-    if constexpr (sizeof(F) == 8) {
+    if constexpr (sizeof(F) <= 8) {
       in_regs = N - r0 <= 512;
       if (in_regs)
         pr64_panel_reg_kernel<F, 512><<<dim3((unsigned)batch), 512, 0, s>>>(f.W, N, n, r0, f.Ar, f.Bk, f.lacc, f.sacc,
@@ -1059,6 +1059,7 @@ int blk_pr(const F* A, int n, int skew, int64_t batch, F* sign, RealOf<F>* logab
   template size_t blk_pr_workspace<F>(int64_t, int);                                                             \
   template int blk_pr<F>(const F*, int, int, int64_t, F*, RealOf<F>*, void*, size_t, hipStream_t, double*);
 FX_BLK_INST(double)
+FX_BLK_INST(float)
 FX_BLK_INST(cx<float>)
 FX_BLK_INST(cx<double>)
 #undef FX_BLK_INST

@@ -163,11 +163,17 @@ int32_t fx_pf_padded_size(int32_t n);
 
 /* ---------------------------------------------------------------- slogdet
  * sign[b], logabs[b] of det(a[b]) for b < batch: sign exactly +1 / -1, or 0 with
- * logabs = -inf for an exactly zero pivot. Sizes: every float32 entry point of this
- * header covers 0 <= n <= 8192 (the float64 and complex ones too) and returns
- * FX_ERR_UNSUPPORTED above. Above n = 4096 the LU panels spill registers and the
- * Parlett-Reid blocks are 8 columns wide (latency-bound; the trailing updates and GEMMs
- * are those of the smaller orders).
+ * logabs = -inf for an exactly zero pivot. Sizes: the float64 and complex entry points
+ * cover 0 <= n <= 8192, the float32 ones 0 <= n <= 16384, and return FX_ERR_UNSUPPORTED
+ * above. float32 above n = 4096: the LU panels spill registers and the Parlett-Reid
+ * blocks are 8 columns wide (latency-bound; the trailing updates and GEMMs are those of
+ * the smaller orders); above n = 8192: the field-generic blocked kernels of the float64
+ * path on float storage (32-column panels, the trailing products in fp64 on the MFMA,
+ * prec without effect), for the values and the parts runs (fx_slogdet_parts_f32 with
+ * zero_singular and no lu / perm, fx_det_parts_f32, fx_slogpf_parts_f32); the packed
+ * factor exports and their inverses (fx_slogdet_factors_f32, fx_slogdet_inverse_f32,
+ * fx_slogpf_factors_f32, fx_slogpf_inverse_f32, fx_lu_padded_size, fx_pf_padded_size)
+ * stop at 8192.
  * Replaces `_lu_core` (src/fermix/_lu.py:543-611) as called by `_slogdet_core`
  * (src/fermix/_diff.py:42-49); kernels K1-K4 of the reference (_lu.py:54-393). */
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n);

@@ -50,8 +50,12 @@ def test_host_only_calls():
     assert L.fx_slogdet_f32(None, 0, 4, None, None, 0, None, 0, None) == 0
     assert L.fx_det_parts_f32(None, -1, 4, None, None, None, 0, None, 0, None) == 1
     assert L.fx_det_parts_f32(None, 2, 4, None, None, None, 0, None, 0, None) == 1
-    assert L.fx_det_parts_f32_workspace(4, 8193) == 0 and L.fx_det_parts_f32_workspace(4, 8192) > 0
-    assert L.fx_slogpf_parts_f32_workspace(1, 8192) > 0 and L.fx_slogpf_parts_f32_workspace(1, 8194) == 0
+    assert L.fx_det_parts_f32_workspace(4, 16385) == 0 and L.fx_det_parts_f32_workspace(4, 8192) > 0
+    assert L.fx_det_parts_f32_workspace(4, 8193) > 0  # the generic blocked family above 8192
+    assert L.fx_slogpf_parts_f32_workspace(1, 16384) > 0 and L.fx_slogpf_parts_f32_workspace(1, 16386) == 0
+    # no packed factors above 8192
+    assert L.fx_lu_padded_size(8193) == -1 and L.fx_pf_padded_size(8194) == -1
+    assert L.fx_slogdet_factors_f32_workspace(1, 8193) == 0 and L.fx_slogpf_inverse_f32_workspace(1, 8194) == 0
     assert L.fx_det_parts_f32_workspace(4, 64) > L.fx_slogdet_parts_f32_workspace(4, 64)
 
 
@@ -123,7 +127,8 @@ def test_tune_table():
         _tune.check_prec("fp16")
     assert _tune.kernel_family(128) == "fused-lds"
     assert _tune.kernel_family(32) == "tiny-wave" and _tune.kernel_family(32, "slogpf") == "fused-lds"
-    assert _tune.kernel_family(8192, "slogpf") == "blocked" and _tune.kernel_family(8193) == "unsupported"
+    assert _tune.kernel_family(8192, "slogpf") == "blocked" and _tune.kernel_family(8193) == "generic"
+    assert _tune.kernel_family(16384) == "generic" and _tune.kernel_family(16385) == "unsupported"
 
 
 def test_misaligned_pointers_rejected():
