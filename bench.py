@@ -39,8 +39,8 @@ def _parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--only", default=None, help="comma list of workloads (c1,c2,c3,c4; f64 adds the float64 "
-                   "n = 128 workloads, blk the blocked float64 / complex ones at n = 512, both reported "
-                   "on stderr)")
+                   "n = 128 workloads, blk the blocked float64 / complex ones at n = 512, xxl the B = 1 "
+                   "orders 8192 / 16384, all reported on stderr)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (calibrates FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
@@ -298,6 +298,38 @@ def bench_blocked(steps, warmup):
     return out
 
 
+def bench_xxl(steps, warmup):
+    """B = 1 at the largest orders: float32 n = 8192 (its own blocked kernels) and
+    n = 16384 (the field-generic blocked kernels on float storage), float64 and complex128
+    at n = 8192: slogdet and slogpf forwards and the parts runs (with A^-T / S^-1) of
+    I + N(0, 1/(4n)) (complex: both parts), inputs generated on the GPU."""
+    import torch
+    from fermix_amd import _kernels
+
+    out = {}
+    for kind, n in [("f32", 8192), ("f32", 16384), ("f64", 8192), ("c128", 8192)]:
+        dt = {"f32": torch.float32, "f64": torch.float64, "c128": torch.complex128}[kind]
+        g = torch.Generator(device="cuda").manual_seed(n)
+        A = torch.randn((1, n, n), generator=g, dtype=dt, device="cuda") * (0.5 / np.sqrt(n))
+        A.diagonal(dim1=1, dim2=2).add_(1.0)
+        S = (A - A.transpose(1, 2)).contiguous()
+        esz = A.element_size()
+        for name, fn in [(f"xxl_{kind}_{n}_slogdet", lambda: _kernels.slogdet(A)),
+                         (f"xxl_{kind}_{n}_slogdet_parts", lambda: _kernels.slogdet_parts(A)),
+                         (f"xxl_{kind}_{n}_slogpf", lambda: _kernels.slogpf(S, False)),
+                         (f"xxl_{kind}_{n}_slogpf_parts", lambda: _kernels.slogpf_parts(S, False))]:
+            ms, wall = _time_gpu(fn, steps, warmup)
+            lu = name.endswith("slogdet") or name.endswith("slogdet_parts")
+            flops = (2.0 / 3.0 if lu else 1.0 / 3.0) * n ** 3 * (4 if kind == "c128" else 1)
+            if name.endswith("_parts"):
+                flops += 2.0 * n ** 3 * (4 if kind == "c128" else 1)
+            out[name] = dict(name=name, B=1, n=n, ms=ms, wall=wall, rate=1 / (ms * 1e-3), bytes=2 * esz * n * n,
+                             flops=flops, sample=None)
+        del A, S
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -381,6 +413,11 @@ def main():
             res[k] = r
             print(f"# {k}: {r['ms']:.4f} ms/step ({r['rate']:.4g} matrices/s)", file=sys.stderr,
                   flush=True)
+    if "xxl" in only:
+        for k, r in bench_xxl(max(2, args.steps // 10), 1).items():
+            res[k] = r
+            print(f"# {k}: {r['ms']:.2f} ms/step ({r['flops'] / (r['ms'] * 1e-3) / 1e12:.2f} TFLOP/s)",
+                  file=sys.stderr, flush=True)
     if "blk" in only:
         for k, r in bench_blocked(max(3, args.steps // 4), max(1, args.warmup // 2)).items():
             res[k] = r
@@ -393,7 +430,8 @@ def main():
         torch.cuda.synchronize()
         del x, y
     head = (res.get("c2") or res.get("c1") or res.get("c3") or res.get("c4")
-            or res.get("f64_slogpf_fwd") or res.get("blk_f64_slogdet_parts"))
+            or res.get("f64_slogpf_fwd") or res.get("blk_f64_slogdet_parts")
+            or res.get("xxl_f32_8192_slogdet"))
     achieved = head["bytes"] / (head["ms"] * 1e-3) / 1e9
     roofline = {
         "bound": "hbm",

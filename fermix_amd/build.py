@@ -4,6 +4,7 @@ library, no torch types). Run ``python -m fermix_amd.build``."""
 
 import concurrent.futures
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -47,11 +48,14 @@ def _compile(hipcc, src, obj):
 
 
 def _stale(src, obj, deps_mtime):
-    """True when obj is missing or older than its source or any shared header."""
+    """True when obj is missing or older than its source, any shared header or an
+    implementation file (.inc) the source includes."""
     if not os.path.exists(obj):
         return True
     t = os.path.getmtime(obj)
-    return t < os.path.getmtime(src) or t < deps_mtime
+    incs = re.findall(r'#include "([\w.]+\.inc)"', open(src).read())
+    inc_mtime = max((os.path.getmtime(os.path.join(CSRC, i)) for i in incs), default=0.0)
+    return t < os.path.getmtime(src) or t < deps_mtime or t < inc_mtime
 
 
 def build(verbose=False, jobs=None, incremental=False):

@@ -42,7 +42,7 @@ namespace {
 constexpr int CX_MAXN = 8192;
 constexpr size_t CX_LDS_MAX = 60 * 1024;  // matrix bytes kept in LDS
 constexpr int CX_NT = 1024;
-// complex orders above this run the blocked kernels of lu64.hip (LU, solves, Parlett-Reid
+// complex orders above this run the blocked kernels of lu64_impl.inc (LU, solves, Parlett-Reid
 // with the trailing updates on the fp64 MFMA); up to it, the one-workgroup kernels here
 constexpr int CX_BLK_MIN = 64;
 
@@ -963,7 +963,7 @@ int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, 
 }
 
 // ---- float32 above its own blocked kernels (LU_LARGE_MAXN < n <= GEN32_MAXN): the
-// field-generic blocked kernels of lu64.hip on float storage (32-column panels, the
+// field-generic blocked kernels of lu64_impl.inc on float storage (32-column panels, the
 // trailing products on the fp64 MFMA), with the entry points' argument checks done by the
 // caller. det's and pf's gradients as for the complex kinds: the LU solves for the regular
 // members, the Gauss-Jordan continuation / pivot-replaced Parlett-Reid formula (one

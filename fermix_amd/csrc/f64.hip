@@ -1,5 +1,5 @@
 // float64 path: slogdet / slogpf forward and their gradients (A^-T, S^-1) for
-// 0 <= n <= 8192: one workgroup per matrix up to n = 128, the blocked kernels of lu64.hip
+// 0 <= n <= 8192: one workgroup per matrix up to n = 128, the blocked kernels of lu64_impl.inc
 // above.
 //
 // The reference takes float64 through the same entry points as float32 (dtype check
@@ -17,7 +17,7 @@
 //    owners post the pivot candidates and the pivot row(s) through LDS, two barriers;
 //  - larger n, gj64_kernel<NT, INV>: the matrix in LDS when it fits in 60 KiB, else in a
 //    per-matrix slice of the workspace (rows served from L2); it serves the inverse and
-//    adjugate runs that the blocked kernels of lu64.hip (LU, Parlett-Reid and the solves,
+//    adjugate runs that the blocked kernels of lu64_impl.inc (LU, Parlett-Reid and the solves,
 //    used above 128 for sign / logabs and A^-T, S^-1) leave to it.
 // Gauss-Jordan (gj*): virtual partial pivoting (the pivot row of column j is the
 // unassigned row of largest |x|, lowest row index on ties). Without INV only the
@@ -28,7 +28,7 @@
 // Parlett-Reid (pfreg64_kernel): virtual pivoting (pair a = the lowest unassigned index,
 // p = argmax |S[p, a]|; pf = sgn(pi) prod d_k); it adds round(tau_r w_x) - round(w_r
 // tau_x) (no contraction), so the matrix stays exactly skew-symmetric. Above n = 128 the
-// blocked Parlett-Reid of lu64.hip swaps the pivot row / column into position c + 1 as the
+// blocked Parlett-Reid of lu64_impl.inc swaps the pivot row / column into position c + 1 as the
 // reference's generic path does. The register kernels are latency-bound per matrix
 // (barriers per column step).
 #include <algorithm>
@@ -456,7 +456,7 @@ int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, d
   return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
 }
 
-// spread: the blocked run's pair-pivot spread (lu64.hip), left unwritten by the register
+// spread: the blocked run's pair-pivot spread (lu64_impl.inc), left unwritten by the register
 // kernels
 int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
                 size_t ws_bytes, hipStream_t s, double* spread = nullptr) {
@@ -468,7 +468,7 @@ int launch_pr64(const double* a, int n, int skew, int64_t batch, double* sign, d
       pfreg64_kernel<128, 32, 4><<<grid, 512, 0, s>>>(a, n, skew, sign, logabs);
     return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
   }
-  return launch_pr64_blocked(a, n, skew, batch, sign, logabs, ws, ws_bytes, s, spread);  // lu64.hip
+  return launch_pr64_blocked(a, n, skew, batch, sign, logabs, ws, ws_bytes, s, spread);  // lu64_impl.inc
 }
 
 // Workspace of the Gauss-Jordan path: none in registers (n <= f64_reg_max_n) or LDS.
@@ -497,7 +497,7 @@ using namespace fx;
 extern "C" {
 
 
-// Above the register kernels the values come from the blocked LU (lu64.hip) and the
+// Above the register kernels the values come from the blocked LU (lu64_impl.inc) and the
 // gradient's A^-T from the blocked solves of the same factorisation, so that a gradient
 // call returns the forward's bits.
 static bool lu64_path(int n) { return n > tune().f64_reg_max_n; }

@@ -152,7 +152,7 @@ struct GemmDesc {
 // C = alpha op(A) op(B) + beta C for every (batch, second-batch) index.
 int launch_gemm(const GemmDesc& d, int64_t batch, int nb2, hipStream_t s);
 
-// float64 blocked LU (sign, logabs) for the orders above the register kernels (lu64.hip)
+// float64 blocked LU (sign, logabs) for the orders above the register kernels (lu64_impl.inc)
 size_t lu64_workspace(int64_t batch, int n);
 int launch_lu64(const double* A, int n, int64_t batch, double* sign, double* logabs, void* ws, size_t ws_bytes,
                 hipStream_t s);
@@ -164,7 +164,7 @@ size_t lu64_inverse_workspace(int64_t batch, int n);
 int launch_lu64_inverse(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs,
                         const double* gate, const double* ssign, const double* slog, double* out, int out_t,
                         void* ws, size_t ws_bytes, hipStream_t s);
-// float64 Parlett-Reid sign / logabs for n above the register kernels (lu64.hip): 16 pair
+// float64 Parlett-Reid sign / logabs for n above the register kernels (lu64_impl.inc): 16 pair
 // steps per panel, the trailing update on the fp64 MFMA
 size_t pr64_workspace(int64_t batch, int n);
 int launch_pr64_blocked(const double* A, int n, int skew, int64_t batch, double* sign, double* logabs, void* ws,
@@ -177,7 +177,7 @@ int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, 
                     const double* plog, const double* spread, void* ws, size_t wsb, hipStream_t s);
 
 // float32 above LU_LARGE_MAXN / PF_LARGE_MAXN up to GEN32_MAXN (cplx.hip): the blocked
-// kernels of lu64.hip on float storage; the caller checks the arguments. slogdet_parts:
+// kernels of lu64_impl.inc on float storage; the caller checks the arguments. slogdet_parts:
 // A^-T zero for singular members; det_parts: adj(A)^T; slogpf_parts: S^-1 (zero where
 // pf = 0) or, with adjugate, pf(S) S^-1.
 constexpr int GEN32_MAXN = 16384;

@@ -118,7 +118,7 @@ struct Fd<float> {
   static __device__ __forceinline__ float scale(float a, double2 s) { return (float)(a * s.x); }
 };
 
-// largest order of the blocked kernels of lu64.hip per field: float32 runs them only
+// largest order of the blocked kernels of lu64_impl.inc per field: float32 runs them only
 // above its own blocked kernels' 8192
 constexpr int BLK_MAXN = 8192;
 template <class F>
@@ -139,7 +139,7 @@ __device__ __forceinline__ double half_diff(double v, double u) { return (v - u)
 __device__ __forceinline__ float half_diff(float v, float u) { return (v - u) * 0.5f; }
 
 // The blocked LU, its solves and the blocked Parlett-Reid for F = double, cx<float>,
-// cx<double> (lu64.hip): sign / logabs, and out = A^-T / A^-1 (times ssign exp(slog) when
+// cx<double> (lu64_impl.inc): sign / logabs, and out = A^-T / A^-1 (times ssign exp(slog) when
 // ssign is given, zero where gate -- default: the factorisation's own sign -- is 0 or the
 // result is not finite); 0 < n <= blk_max_n<F>(), every buffer of the batch.
 template <class F>

@@ -1,0 +1,9 @@
+// The blocked LU / solves / Parlett-Reid of lu64_impl.inc instantiated for complex128
+// (one translation unit per field, compiled in parallel).
+#include "lu64_impl.inc"
+
+namespace fx {
+
+FX_BLK_INST(cx<double>)
+
+}  // namespace fx

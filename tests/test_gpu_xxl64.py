@@ -1,5 +1,6 @@
-"""GPU parity of the float64 / complex64 / complex128 blocked kernels (lu64.hip) at their
-largest order, n = 8192 (B = 1, 256 panels of 32 columns with the rows in memory): slogdet
+"""GPU parity of the float64 / complex64 / complex128 blocked kernels (lu64_impl.inc) at their
+largest order, n = 8192 (B = 1, 256 panels of 32 columns, the tall ones on several
+workgroups per matrix, lu64_panel_mwg_kernel): slogdet
 against torch.linalg.slogdet in float64 / complex128 on the GPU; A^-T, S^-1 and the
 Pfaffian adjugate pf(S) S^-1 through their float64 / complex128 residuals (M X - I, a
 bound on the relative error of X as M^-1); pf(X J X^T) = det(X), which ties the
