@@ -353,13 +353,16 @@ def test_complex_entry_points_host_checks():
         # the Pfaffian adjugate mode checks its workspace like the inverse mode
         assert getattr(L, f"fx_slogpf_parts_{k}")(good, 2, 300, 0, 1, good, good, good, ws, 256, None) == 2
         assert getattr(L, f"fx_slogdet_{k}_workspace")(4, 40) == 0
-        # n = 300 runs the blocked LU: one copy of padded order 320 plus its pivots (each
-        # buffer rounded up to 256 bytes); the inverse adds the solve's matrix and flags
+        # n = 300 runs the blocked LU: one copy of padded order 320 plus its pivots and the
+        # multi-workgroup panels' posts (G = 1 workgroup's worth per member at this order;
+        # each buffer rounded up to 256 bytes); the inverse adds the solve's matrix and flags
         w = getattr(L, f"fx_slogdet_{k}_workspace")(4, 300)
 
         def al(x):
             return (x + 255) // 256 * 256
 
         fz = 2 * esz
-        assert w == al(4 * 320 * 320 * fz) + al(4 * 320 * 4) + al(4 * 320 * fz) + al(4 * 10 * 4)
+        G = 1
+        sync = 2 * al(4 * 4) + al(4 * 2 * G * 8) + al(4 * 2 * G * 4) + al(4 * 2 * G * 32 * fz) + al(4 * 2 * 32 * fz)
+        assert w == al(4 * 320 * 320 * fz) + al(4 * 320 * 4) + al(4 * 320 * fz) + al(4 * 10 * 4) + sync
         assert getattr(L, f"fx_slogdet_parts_{k}_workspace")(4, 300) == w + al(4 * 320 * 320 * fz) + al(4 * 4)
