@@ -245,7 +245,8 @@ def cpu_library():
 
 def bench_f64(steps, warmup):
     """float64 counterparts of the n = 128 workloads (B = 4096, the C1 / C2 inputs in
-    float64): slogpf and slogdet forward, and slogdet forward + gradient."""
+    float64): slogpf and slogdet forward, and slogdet forward + gradient; and the slogdet
+    forward at n = 16 / 32, B = 65536, beside torch.linalg.slogdet."""
     import torch
     import fermix_amd
 
@@ -269,6 +270,16 @@ def bench_f64(steps, warmup):
         ms, wall = _time_gpu(fn, steps, warmup)
         out[name] = dict(name=name, B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
                          bytes=B * nbytes, sample=None)
+    # small orders, several matrices per wave, beside torch.linalg.slogdet (rocSOLVER)
+    for n_small in (16, 32):
+        Bs = 65536
+        As = torch.from_numpy(_inputs(Bs, n_small, 2).astype(np.float64)).cuda()
+        for name, fn in [(f"f64_slogdet_fwd_n{n_small}", lambda: fermix_amd.slogdet(As)),
+                         (f"torch_f64_slogdet_fwd_n{n_small}", lambda: torch.linalg.slogdet(As))]:
+            ms, wall = _time_gpu(fn, steps, warmup)
+            out[name] = dict(name=name, B=Bs, n=n_small, ms=ms, wall=wall, rate=Bs / (ms * 1e-3),
+                             bytes=Bs * (8 * n_small * n_small + 16), sample=None)
+        del As
     return out
 
 

@@ -192,6 +192,27 @@ __device__ __forceinline__ v4f mfma16(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Groups of G = 16 or 32 consecutive lanes of a wave (several small matrices per wave):
+// Maximum over the G-lane group (G = 16: DPP within a row; G = 32: one more exchange).
+template <int G>
+__device__ __forceinline__ unsigned group_max_u32(unsigned v) {
+  v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
+  v = max(v, dpp_u32<0x140>(v));  // row_mirror
+  if constexpr (G == 32) v = max(v, (unsigned)__shfl_xor((int)v, 16));
+  return v;
+}
+
+// Lowest lane of the group (relative index) whose predicate holds; gbase = first lane of
+// the group in the wave.
+template <int G>
+__device__ __forceinline__ int group_first(bool p, int gbase) {
+  const unsigned long long m = __ballot(p);
+  const unsigned bits = (unsigned)(m >> gbase) & (G == 32 ? 0xFFFFFFFFu : 0xFFFFu);
+  return bits ? (int)__builtin_ctz(bits) : G;
+}
+
 // Compiler-level ordering point for LDS traffic exchanged between the lanes of one
 // wave (the hardware executes one wave's LDS instructions in order).
 __device__ __forceinline__ void wave_lds_fence() {

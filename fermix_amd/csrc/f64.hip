@@ -425,10 +425,101 @@ size_t f64_lds_bytes(int n, int ld, bool lds, bool maps) {
   return bytes ? bytes : 16;
 }
 
+// slogdet forward for n <= TINY64_MAXN with several matrices per wave: G lanes per matrix
+// (16 for n <= 16, else 32), lane r of a group holding row r in registers, no workgroup
+// barrier. The arithmetic is gjreg64_kernel's forward element for element -- the same
+// pivots (the exact 64-bit argmax: the high words' maximum, then the low words' among the
+// lanes holding it, then the lowest such row), l = a[r][j] * (1 / piv) and one fma per
+// entry of the unassigned rows, the logs summed in pivot order, the sign from the
+// negative pivots and the permutation's parity -- so the gradient call
+// (gjreg64_kernel<..., true>) returns this forward's bits. The pivot row reaches the
+// group through LDS.
+constexpr int TINY64_MAXN = 32;
+
+template <int G>
+__global__ __launch_bounds__(256) void lutiny64_kernel(const double* __restrict__ a, int n, int64_t batch,
+                                                       double* __restrict__ sign_out,
+                                                       double* __restrict__ logabs_out) {
+  constexpr int MPW = 256 / G;  // matrices per workgroup
+  __shared__ double ubuf[256], pbuf[256];
+  __shared__ int ibuf[256];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int r = tid % G;       // row within the matrix
+  const int gbase = lane - r;  // first lane of the group
+  double* const ub = ubuf + (tid - r);  // the group's pivot row
+  double* const pv = pbuf + (tid - r);  // its pivots, in column order
+  int* const pi = ibuf + (tid - r);     // and their rows
+  const int64_t mi = (int64_t)blockIdx.x * MPW + tid / G;
+  const bool live = mi < batch;
+  const double* Ab = a + (live ? mi : 0) * (int64_t)n * n;
+  double M[G];
+  const int rr = min(r, n - 1);
+#pragma unroll
+  for (int c = 0; c < G; ++c) M[c] = Ab[(int64_t)rr * n + min(c, n - 1)];
+#pragma unroll
+  for (int c = 0; c < G; ++c) M[c] = (r < n && c < n) ? M[c] : 0.0;
+  bool asg = false, singular = false;
+  double sgn = 1.0;
+  static_for<0, G>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if (j < n) {
+      const unsigned long long k = (r < n && !asg) ? key64(M[j]) : 0ull;
+      const unsigned hi = (unsigned)(k >> 32), lo = (unsigned)k;
+      const unsigned mh = group_max_u32<G>(hi);
+      const unsigned ml = group_max_u32<G>(hi == mh ? lo : 0u);
+      const int p = group_first<G>(k != 0 && hi == mh && lo == ml, gbase);
+      const double piv = __shfl(M[j], gbase + p);
+      double rinv = 0.0;
+      if (piv == 0.0) {
+        singular = true;
+      } else {
+        rinv = 1.0 / piv;
+        if (piv < 0.0) sgn = -sgn;
+      }
+      if (r == p) {
+#pragma unroll
+        for (int c = j + 1; c < G; ++c) ub[c] = M[c];
+        pv[j] = piv;
+        pi[j] = p;
+      }
+      wave_lds_fence();
+      if (r < n && r != p && !asg) {
+        const double l = M[j] * rinv;
+#pragma unroll
+        for (int c = j + 1; c < G; ++c) M[c] = fma(-l, ub[c], M[c]);
+      }
+      if (r == p) asg = true;
+      wave_lds_fence();  // every read of ub precedes the next step's writes
+    }
+  });
+  if (live && r == 0) {
+    double logabs = 0.0;
+    if (!singular)
+      for (int j = 0; j < n; ++j) logabs += log(fabs(pv[j]));
+    unsigned seen = 0;  // parity of j -> pi[j] from its cycles
+    int cycles = 0;
+    for (int s0 = 0; s0 < n; ++s0) {
+      if ((seen >> s0) & 1u) continue;
+      ++cycles;
+      for (int u = s0; !((seen >> u) & 1u); u = pi[u]) seen |= 1u << u;
+    }
+    if ((n - cycles) & 1) sgn = -sgn;
+    sign_out[mi] = singular ? 0.0 : sgn;
+    logabs_out[mi] = singular ? -INFINITY : logabs;
+  }
+}
+
 int launch_gj64(const double* a, int n, int skew, int64_t batch, double* sign, double* logabs, double* out,
                 int out_t, const double* gate, void* ws, size_t ws_bytes, hipStream_t s) {
   const bool inv = out != nullptr;
   const int ld = inv ? 2 * n : n;
+  if (!inv && !skew && n >= 1 && n <= TINY64_MAXN) {  // several matrices per wave
+    if (n <= 16)
+      lutiny64_kernel<16><<<dim3((unsigned)((batch + 15) / 16)), 256, 0, s>>>(a, n, batch, sign, logabs);
+    else
+      lutiny64_kernel<32><<<dim3((unsigned)((batch + 7) / 8)), 256, 0, s>>>(a, n, batch, sign, logabs);
+    return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+  }
   if (n <= tune().f64_reg_max_n) {  // register-resident
     const dim3 grid((unsigned)batch);
     if (n <= tune().f64_strip16_max_n) {

@@ -27,16 +27,6 @@
 
 namespace fx {
 
-// Maximum over the G-lane group (G = 16: DPP within a row; G = 32: one more exchange).
-template <int G>
-__device__ __forceinline__ unsigned group_max_u32(unsigned v) {
-  v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
-  v = max(v, dpp_u32<0x140>(v));  // row_mirror
-  if constexpr (G == 32) v = max(v, (unsigned)__shfl_xor((int)v, 16));
-  return v;
-}
 
 template <int G>
 __device__ __forceinline__ float group_sum_f32(float v) {
@@ -48,14 +38,6 @@ __device__ __forceinline__ float group_sum_f32(float v) {
   return v;
 }
 
-// Lowest lane of the group (relative index) whose predicate holds; gbase = first lane of
-// the group in the wave.
-template <int G>
-__device__ __forceinline__ int group_first(bool p, int gbase) {
-  const unsigned long long m = __ballot(p);
-  const unsigned bits = (unsigned)(m >> gbase) & (G == 32 ? 0xFFFFFFFFu : 0xFFFFu);
-  return bits ? (int)__builtin_ctz(bits) : G;
-}
 
 // Row r of matrix Ab (n x n, row-major) into a[0..G): columns >= n and rows >= n are 0
 // (the callers write the padding). Every load is unconditional at a clamped, in-bounds
