@@ -284,10 +284,10 @@ def bench_f64(steps, warmup):
 
 
 def bench_blocked(steps, warmup):
-    """The blocked float64 / complex kernels (lu64.hip) at B = 32, n = 512: the value and
-    gradient factors (sign, logabs and A^-T or S^-1) of slogdet and slogpf in float64,
-    complex64 and complex128, on the C3-shaped inputs (complex: a second draw as the
-    imaginary part)."""
+    """The blocked float64 / complex kernels (lu64_impl.inc) at B = 32, n = 512: the value
+    and gradient factors (sign, logabs and A^-T or S^-1) of slogdet and slogpf in float64,
+    complex64 (both product modes) and complex128, on the C3-shaped inputs (complex: a
+    second draw as the imaginary part)."""
     import torch
     from fermix_amd import _kernels
 
@@ -300,8 +300,12 @@ def bench_blocked(steps, warmup):
         A = torch.from_numpy(np.ascontiguousarray(arr)).cuda()
         S = (A - A.transpose(1, 2)).contiguous()
         esz = A.element_size()
-        for name, fn in [(f"blk_{kind}_slogdet_parts", lambda: _kernels.slogdet_parts(A)),
-                         (f"blk_{kind}_slogpf_parts", lambda: _kernels.slogpf_parts(S, False))]:
+        runs = [(f"blk_{kind}_slogdet_parts", lambda: _kernels.slogdet_parts(A)),
+                (f"blk_{kind}_slogpf_parts", lambda: _kernels.slogpf_parts(S, False))]
+        if kind == "c64":  # complex64's fp32-product mode beside the default
+            runs += [("blk_c64_ieee_slogdet_parts", lambda: _kernels.slogdet_parts(A, x3=0)),
+                     ("blk_c64_ieee_slogpf_parts", lambda: _kernels.slogpf_parts(S, False, x3=0))]
+        for name, fn in runs:
             ms, wall = _time_gpu(fn, steps, warmup)
             out[name] = dict(name=name, B=B, n=n, ms=ms, wall=wall, rate=B / (ms * 1e-3),
                              bytes=B * 2 * esz * n * n, sample=None)

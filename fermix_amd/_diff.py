@@ -256,17 +256,17 @@ def slogdet(A, x3=DEFAULT_X3):
 
 class _SlogpfFwd(torch.autograd.Function):
     @staticmethod
-    def forward(A, skew):
-        return _kernels.slogpf(A, skew)
+    def forward(A, skew, x3):
+        return _kernels.slogpf(A, skew, x3=x3)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
         ctx.mark_non_differentiable(*output)
 
     @staticmethod
-    def vmap(info, in_dims, A, skew):
+    def vmap(info, in_dims, A, skew, x3):
         A2, vb = _fold(info, in_dims[:1], A)
-        s, l = _SlogpfFwd.apply(A2, skew)
+        s, l = _SlogpfFwd.apply(A2, skew, x3)
         if vb is None:
             return (s, l), (None, None)
         return (_unfold(s, vb), _unfold(l, vb)), (0, 0)
@@ -361,7 +361,7 @@ def slogpf(A, skew, x3=DEFAULT_X3):
         else:
             s, l, _ = _SlogpfParts.apply(A, skew, x3)
         return s, l
-    return _SlogpfFwd.apply(A, skew)
+    return _SlogpfFwd.apply(A, skew, x3)
 
 
 # ----------------------------------------------------------------- det / pf
@@ -455,7 +455,7 @@ def pf(A, skew, x3=DEFAULT_X3):
     if _wants_grad(A):
         p, _ = _PfParts.apply(A, skew, x3)
         return p
-    s, l = _SlogpfFwd.apply(A, skew)
+    s, l = _SlogpfFwd.apply(A, skew, x3)
     return s * torch.exp(l)
 
 

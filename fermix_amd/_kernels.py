@@ -4,7 +4,7 @@ tensors (float64 for the f64 entry points) on a ROCm device; no numerics happen 
 
 import torch
 
-from ._lib import FX_PREC_MASK, check, lib
+from ._lib import FX_PREC_BF16X3, FX_PREC_IEEE, FX_PREC_MASK, check, lib
 from ._tune import DEFAULT_PREC, prec_flag
 
 # the C ABI's prec word of the library's default product mode (the public API's default
@@ -59,10 +59,16 @@ def _cplx_input(A):
     return k
 
 
-def _cplx_call(A, name, skew=None, want_out=False, adjugate=False):
+def _cplx_prec(x3):
+    """complex64's prec argument: the fp32-accuracy mode (products on the fp64 MFMA) for a
+    bf16x3 word, fp32 MFMA products for an IEEE one."""
+    return FX_PREC_BF16X3 if int(x3) & FX_PREC_MASK else FX_PREC_IEEE
+
+
+def _cplx_call(A, name, skew=None, want_out=False, adjugate=False, x3=DEFAULT_X3):
     """complex64 / complex128: (sign, logabs[, out]) from fx_<name>_<kind>; sign complex
     (B,), logabs real (B,), out (B, n, n) complex (A^-T for slogdet_parts, S^-1 for
-    slogpf_parts)."""
+    slogpf_parts). complex64 passes its prec (from the C ABI's prec word x3)."""
     k = _cplx_input(A)
     A = _aligned(A)
     B, n, _ = A.shape
@@ -81,6 +87,8 @@ def _cplx_call(A, name, skew=None, want_out=False, adjugate=False):
     args += [_ptr(sign), _ptr(logabs)]
     if name.endswith("_parts"):
         args.append(_ptr(out))
+    if k == "c64":
+        args.append(_cplx_prec(x3))
     args += [_ptr(ws), wsb, _stream(A)]
     check(getattr(L, fn)(*args), fn)
     return (sign, logabs, out) if name.endswith("_parts") else (sign, logabs)
@@ -112,7 +120,7 @@ def slogdet(A, x3=DEFAULT_X3):
     """(sign, logabs) of each (n, n) matrix of A (B, n, n); x3: the C ABI's prec word
     (FX_PREC_BF16X3 products, FX_LU_BLOCK_* options; float32 only)."""
     if A.is_complex():
-        return _cplx_call(A, "slogdet")
+        return _cplx_call(A, "slogdet", x3=x3)
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape
@@ -137,7 +145,7 @@ def slogdet_parts(A, zero_singular=True, want_inv=True, want_lu=False, x3=DEFAUL
     if A.is_complex():
         if want_lu or not zero_singular:
             _no_f64(A, "the packed LU / unguarded inverse")
-        sign, logabs, invT = _cplx_call(A, "slogdet_parts", want_out=want_inv)
+        sign, logabs, invT = _cplx_call(A, "slogdet_parts", want_out=want_inv, x3=x3)
         return sign, logabs, invT, None, None
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
@@ -224,8 +232,9 @@ def det_parts(A, x3=DEFAULT_X3):
         adjT = torch.empty_like(A)
         L = lib()
         ws, wsb = _workspace(getattr(L, f"fx_det_parts_{k}_workspace")(B, n), dev)
+        prec = [_cplx_prec(x3)] if k == "c64" else []
         st = getattr(L, f"fx_det_parts_{k}")(
-            _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(adjT), _ptr(ws), wsb, _stream(A)
+            _ptr(A), B, n, _ptr(sign), _ptr(logabs), _ptr(adjT), *prec, _ptr(ws), wsb, _stream(A)
         )
         check(st, f"fx_det_parts_{k}")
         return sign, logabs, adjT
@@ -245,9 +254,11 @@ def det_parts(A, x3=DEFAULT_X3):
     return sign, logabs, adjT
 
 
-def slogpf(A, skew_symmetrize):
+def slogpf(A, skew_symmetrize, x3=DEFAULT_X3):
+    """(sign, logabs) of pf; x3 reaches only complex64 (the float32 forward's Parlett-Reid
+    update has no product mode)."""
     if A.is_complex():
-        return _cplx_call(A, "slogpf", skew=skew_symmetrize)
+        return _cplx_call(A, "slogpf", skew=skew_symmetrize, x3=x3)
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape
@@ -316,7 +327,7 @@ def slogpf_parts(A, skew_symmetrize, adjugate=False, x3=DEFAULT_X3):
     """(sign, logabs, G) of the (skew-symmetrised) batch from one Parlett-Reid run, G = S^-1
     or, with adjugate, pf(S) S^-1 (the Pfaffian adjugate)."""
     if A.is_complex():
-        return _cplx_call(A, "slogpf_parts", skew=skew_symmetrize, want_out=True, adjugate=adjugate)
+        return _cplx_call(A, "slogpf_parts", skew=skew_symmetrize, want_out=True, adjugate=adjugate, x3=x3)
     f64 = _check_input(A, f64_ok=True)
     A = _aligned(A)
     B, n, _ = A.shape

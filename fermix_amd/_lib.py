@@ -9,7 +9,10 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfermix_a
 
 FX_OK = 0
 
-# option bits of the prec argument of the slogdet / det entry points (include/fermix.h)
+# the prec argument (include/fermix.h): the product mode and, for the float32 slogdet /
+# det entry points, option bits
+FX_PREC_IEEE = 0
+FX_PREC_BF16X3 = 1
 FX_PREC_MASK = 0x0F
 FX_LU_BLOCK_64 = 0x100
 FX_LU_BLOCK_128 = 0x200
@@ -85,23 +88,26 @@ SIGNATURES = {
     "fx_slogpf_parts_f64_workspace": (_sz, [_i64, _i32]),
     "fx_slogpf_parts_f64": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _sz, _p]),
 }
-# complex64 / complex128: the float64 signatures with interleaved (re, im) buffers
+# complex64 / complex128: the float64 signatures with interleaved (re, im) buffers;
+# complex64's take the prec word before the workspace (PREC_ARG[_k]: the extra argument)
+PREC_ARG = {"c64": [_i32], "c128": []}
 for _k in ("c64", "c128"):
+    _q = PREC_ARG[_k]
     SIGNATURES.update({
         f"fx_slogdet_{_k}_workspace": (_sz, [_i64, _i32]),
-        f"fx_slogdet_{_k}": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _sz, _p]),
+        f"fx_slogdet_{_k}": (ctypes.c_int, [_p, _i64, _i32, _p, _p] + _q + [_p, _sz, _p]),
         f"fx_slogdet_parts_{_k}_workspace": (_sz, [_i64, _i32]),
-        f"fx_slogdet_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _sz, _p]),
+        f"fx_slogdet_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p] + _q + [_p, _sz, _p]),
         f"fx_slogpf_{_k}_workspace": (_sz, [_i64, _i32]),
-        f"fx_slogpf_{_k}": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _sz, _p]),
+        f"fx_slogpf_{_k}": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p] + _q + [_p, _sz, _p]),
         f"fx_slogpf_parts_{_k}_workspace": (_sz, [_i64, _i32]),
-        f"fx_slogpf_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _sz, _p]),
+        f"fx_slogpf_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _p, _p] + _q + [_p, _sz, _p]),
     })
 # det's gradient (the exact adjugate) for the 64-bit and complex kinds
 for _k in ("f64", "c64", "c128"):
     SIGNATURES.update({
         f"fx_det_parts_{_k}_workspace": (_sz, [_i64, _i32]),
-        f"fx_det_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _sz, _p]),
+        f"fx_det_parts_{_k}": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p] + PREC_ARG.get(_k, []) + [_p, _sz, _p]),
     })
 
 

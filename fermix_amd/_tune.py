@@ -45,9 +45,9 @@ class FermixTuneWarning(UserWarning):
 def check_prec(prec, dtype=None):
     """The mode a `prec` argument selects ("ieee" or "bf16x3"). The reduced-precision
     modes apply to the 32-bit kinds only (the reference rejects "tf32x3" for float64 /
-    complex128, src/fermix/_field.py:265-275); complex64 accepts them, but its products
-    (the blocked kernels above n = 64) run widened on the fp64 MFMA, so `prec` does not
-    change complex64 results."""
+    complex128, src/fermix/_field.py:265-275). For complex64 the fp32-accuracy mode
+    ("bf16x3" / "tf32x3", the default) forms the blocked kernels' products on the fp64
+    MFMA with the operands widened, "ieee" as four fp32 MFMA products per complex one."""
     if prec is None:
         return "ieee" if dtype in (torch.float64, torch.complex128) else DEFAULT_PREC
     if prec not in PREC:

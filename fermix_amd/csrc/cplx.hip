@@ -962,6 +962,12 @@ int pf_adjugate_f64(const double* a, int64_t batch, int n, int skew, double* g, 
   return pf_adjugate<double>(a, batch, n, skew, g, ws, body, s, gate);
 }
 
+// complex64's product mode, per thread and per call (FX_PREC_IEEE: fp32 products)
+static thread_local int t_cx32_ieee = 0;
+int cx32_ieee() { return t_cx32_ieee; }
+CxPrecPin::CxPrecPin(int ieee) : old_(t_cx32_ieee) { t_cx32_ieee = ieee; }
+CxPrecPin::~CxPrecPin() { t_cx32_ieee = old_; }
+
 // ---- float32 above its own blocked kernels (LU_LARGE_MAXN < n <= GEN32_MAXN): the
 // field-generic blocked kernels of lu64_impl.inc on float storage (32-column panels, the
 // trailing products on the fp64 MFMA), with the entry points' argument checks done by the
@@ -1003,9 +1009,15 @@ extern "C" {
 size_t fx_slogdet_c64_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogdet_ws<cx<float>>(batch, n); }
 size_t fx_slogdet_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogdet_ws<cx<double>>(batch, n); }
 
-int fx_slogdet_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, void* workspace,
-                   size_t workspace_bytes, fx_stream_t stream) {
+// complex64's prec: FX_PREC_BF16X3 (the fp32-accuracy mode) the products on the fp64
+// MFMA, FX_PREC_IEEE four fp32 MFMA products per complex one
+static bool bad_cx_prec(int32_t prec) { return prec != FX_PREC_IEEE && prec != FX_PREC_BF16X3; }
+
+int fx_slogdet_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, int32_t prec,
+                   void* workspace, size_t workspace_bytes, fx_stream_t stream) {
   fx::TunePin pin_;
+  if (bad_cx_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
+  fx::CxPrecPin pp_(prec == FX_PREC_IEEE);
   return slogdet<cx<float>>(a, batch, n, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_slogdet_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
@@ -1018,8 +1030,10 @@ size_t fx_slogdet_parts_c64_workspace(int64_t batch, int32_t n) { fx::TunePin pi
 size_t fx_slogdet_parts_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogdet_parts_ws<cx<double>>(batch, n); }
 
 int fx_slogdet_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* inv_t,
-                         void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+                         int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
   fx::TunePin pin_;
+  if (bad_cx_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
+  fx::CxPrecPin pp_(prec == FX_PREC_IEEE);
   return slogdet_parts<cx<float>>(a, batch, n, sign, logabs, inv_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_slogdet_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
@@ -1032,8 +1046,10 @@ size_t fx_slogpf_c64_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; ret
 size_t fx_slogpf_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogpf_ws<double>(batch, n); }
 
 int fx_slogpf_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign, float* logabs,
-                  void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+                  int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
   fx::TunePin pin_;
+  if (bad_cx_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
+  fx::CxPrecPin pp_(prec == FX_PREC_IEEE);
   return slogpf<float>(a, batch, n, skew_symmetrize, sign, logabs, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_slogpf_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign,
@@ -1047,9 +1063,11 @@ size_t fx_slogpf_parts_c64_workspace(int64_t batch, int32_t n) { fx::TunePin pin
 size_t fx_slogpf_parts_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return slogpf_parts_ws<double>(batch, n); }
 
 int fx_slogpf_parts_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
-                        float* sign, float* logabs, float* g, void* workspace, size_t workspace_bytes,
+                        float* sign, float* logabs, float* g, int32_t prec, void* workspace, size_t workspace_bytes,
                         fx_stream_t stream) {
   fx::TunePin pin_;
+  if (bad_cx_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
+  fx::CxPrecPin pp_(prec == FX_PREC_IEEE);
   return slogpf_parts<float>(a, batch, n, skew_symmetrize, adjugate, sign, logabs, g, workspace, workspace_bytes,
                              (hipStream_t)stream);
 }
@@ -1066,8 +1084,10 @@ size_t fx_det_parts_c128_workspace(int64_t batch, int32_t n) { fx::TunePin pin_;
 size_t fx_det_parts_f64_workspace(int64_t batch, int32_t n) { fx::TunePin pin_; return det_parts_f64_ws(batch, n); }
 
 int fx_det_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
-                     void* workspace, size_t workspace_bytes, fx_stream_t stream) {
+                     int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream) {
   fx::TunePin pin_;
+  if (bad_cx_prec(prec)) return FX_ERR_INVALID_ARGUMENT;
+  fx::CxPrecPin pp_(prec == FX_PREC_IEEE);
   return det_parts<cx<float>>(a, batch, n, sign, logabs, adj_t, workspace, workspace_bytes, (hipStream_t)stream);
 }
 int fx_det_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,

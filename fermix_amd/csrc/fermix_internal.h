@@ -197,4 +197,16 @@ size_t gen32_slogpf_parts_ws(int64_t batch, int n);
 int gen32_slogpf_parts(const float* a, int64_t batch, int n, int skew, int adjugate, float* sign, float* logabs,
                        float* g, void* ws, size_t wsb, hipStream_t s);
 
+// complex64's product mode for the calls of this thread: 1 while a complex64 entry point
+// called with FX_PREC_IEEE runs (the blocked products as fp32 MFMA products), else 0 (the
+// products on the fp64 MFMA, complex64 widened). CxPrecPin sets it for one call.
+int cx32_ieee();
+struct CxPrecPin {
+  explicit CxPrecPin(int ieee);
+  ~CxPrecPin();
+  CxPrecPin(const CxPrecPin&) = delete;
+  CxPrecPin& operator=(const CxPrecPin&) = delete;
+  int old_;
+};
+
 }  // namespace fx

@@ -362,10 +362,16 @@ int fx_slogpf_parts_f64(const double* a, int64_t batch, int32_t n, int32_t skew_
  * the matrix in LDS when it fits (else one copy per member in the workspace; twice that
  * with the inverse); above, the blocked kernels of the float64 path on the complex field
  * (32-column LU panels, 16-pair Parlett-Reid panels, the trailing updates as four real
- * fp64 MFMA products per complex one, complex64 operands widened to double in them). */
+ * MFMA products per complex one). The complex64 entry points take prec:
+ * FX_PREC_BF16X3 (the fp32-accuracy mode, the Python API's default as for float32) forms
+ * those products on the fp64 MFMA with the operands widened to double; FX_PREC_IEEE as
+ * four fp32 MFMA products (the reference's complex64 fp32-rate products, _field.py:173-190;
+ * the fp32 MFMA's rate and rounding). Any other value: FX_ERR_INVALID_ARGUMENT. Up to
+ * n = 64 (no blocked products) both give the same bits. complex128 has no prec (IEEE
+ * fp64). */
 size_t fx_slogdet_c64_workspace(int64_t batch, int32_t n);
-int fx_slogdet_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, void* workspace,
-                   size_t workspace_bytes, fx_stream_t stream);
+int fx_slogdet_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, int32_t prec,
+                   void* workspace, size_t workspace_bytes, fx_stream_t stream);
 size_t fx_slogdet_c128_workspace(int64_t batch, int32_t n);
 int fx_slogdet_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, void* workspace,
                     size_t workspace_bytes, fx_stream_t stream);
@@ -374,7 +380,7 @@ int fx_slogdet_c128(const double* a, int64_t batch, int32_t n, double* sign, dou
  * (NULL to skip), zero for members with an exactly zero pivot or a non-finite inverse. */
 size_t fx_slogdet_parts_c64_workspace(int64_t batch, int32_t n);
 int fx_slogdet_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* inv_t,
-                         void* workspace, size_t workspace_bytes, fx_stream_t stream);
+                         int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 size_t fx_slogdet_parts_c128_workspace(int64_t batch, int32_t n);
 int fx_slogdet_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* inv_t,
                           void* workspace, size_t workspace_bytes, fx_stream_t stream);
@@ -384,7 +390,7 @@ int fx_slogdet_parts_c128(const double* a, int64_t batch, int32_t n, double* sig
  * src/fermix/_fallback.py:266-300); odd n gives (0, -inf). */
 size_t fx_slogpf_c64_workspace(int64_t batch, int32_t n);
 int fx_slogpf_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, float* sign, float* logabs,
-                  void* workspace, size_t workspace_bytes, fx_stream_t stream);
+                  int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 size_t fx_slogpf_c128_workspace(int64_t batch, int32_t n);
 int fx_slogpf_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, double* sign,
                    double* logabs, void* workspace, size_t workspace_bytes, fx_stream_t stream);
@@ -404,7 +410,7 @@ int fx_slogpf_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symme
  * blocked LU solves; sign / logabs stay those of the plain forward. */
 size_t fx_slogpf_parts_c64_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_c64(const float* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
-                        float* sign, float* logabs, float* g, void* workspace, size_t workspace_bytes,
+                        float* sign, float* logabs, float* g, int32_t prec, void* workspace, size_t workspace_bytes,
                         fx_stream_t stream);
 size_t fx_slogpf_parts_c128_workspace(int64_t batch, int32_t n);
 int fx_slogpf_parts_c128(const double* a, int64_t batch, int32_t n, int32_t skew_symmetrize, int32_t adjugate,
@@ -429,7 +435,7 @@ int fx_det_parts_f64(const double* a, int64_t batch, int32_t n, double* sign, do
                      void* workspace, size_t workspace_bytes, fx_stream_t stream);
 size_t fx_det_parts_c64_workspace(int64_t batch, int32_t n);
 int fx_det_parts_c64(const float* a, int64_t batch, int32_t n, float* sign, float* logabs, float* adj_t,
-                     void* workspace, size_t workspace_bytes, fx_stream_t stream);
+                     int32_t prec, void* workspace, size_t workspace_bytes, fx_stream_t stream);
 size_t fx_det_parts_c128_workspace(int64_t batch, int32_t n);
 int fx_det_parts_c128(const double* a, int64_t batch, int32_t n, double* sign, double* logabs, double* adj_t,
                       void* workspace, size_t workspace_bytes, fx_stream_t stream);

@@ -231,3 +231,50 @@ def test_complex_blocked_large(dev, kind):
     zs, zl = fermix_amd.slogpf(Sz, skew_symmetrize=False)
     assert _np(zs)[0] == 0 and np.isneginf(_np(zl)[0])
     assert torch.equal(zs[1], ps[1]) and torch.equal(zl[1], pl[1])
+
+
+@pytest.mark.parametrize("n", [48, 130, 512])
+def test_complex64_product_modes(dev, n):
+    """complex64's two product modes of the blocked kernels: prec="ieee" (four fp32 MFMA
+    products per complex one) and the default fp32-accuracy mode (the products on the
+    fp64 MFMA, operands widened), each against complex128 numpy on X = I + N(0, 1/(4n)):
+    slogdet, A^-T through its residual, pf(X J X^T) = det X and S^-1 through its residual;
+    the parts calls' primal is bit-identical to the forward of the same mode. At n = 48
+    (one workgroup per matrix, no blocked products) the modes give the same bits."""
+    from fermix_amd import _kernels
+    from fermix_amd._tune import prec_flag
+
+    rng = np.random.default_rng(9850 + n)
+    X = (np.eye(n) + 0.5 * _crandn(rng, (3, n, n), np.complex128) / np.sqrt(n)).astype(np.complex64)
+    Xw = X.astype(np.complex128)
+    J = np.zeros((n, n))
+    J[np.arange(0, n, 2), np.arange(1, n, 2)] = 1.0
+    J[np.arange(1, n, 2), np.arange(0, n, 2)] = -1.0
+    S = Xw @ J @ np.swapaxes(Xw, 1, 2)
+    S = (0.5 * (S - np.swapaxes(S, 1, 2))).astype(np.complex64)
+    Xt, St = torch.from_numpy(X).to(dev), torch.from_numpy(S).to(dev)
+    sr, lr = np.linalg.slogdet(Xw)
+    tol, gtol = _tols("c64", n)
+    out = {}
+    for prec in ("ieee", "bf16x3"):
+        x3 = prec_flag(prec)
+        print(f"complex64 n={n} prec={prec}", flush=True)
+        s, l = fermix_amd.slogdet(Xt, prec=prec)
+        assert np.all(np.abs(_np(s) - sr) < tol) and np.all(np.abs(_np(l) - lr) < tol * max(1.0, np.abs(lr).max()))
+        sp, lp, invT = _kernels.slogdet_parts(Xt, x3=x3)[:3]
+        assert torch.equal(sp, s) and torch.equal(lp, l)
+        res = np.swapaxes(Xw, 1, 2) @ _np(invT).astype(np.complex128) - np.eye(n)
+        print(f"  A^-T residual {np.abs(res).max():.3g}", flush=True)
+        assert np.abs(res).max() < gtol
+        ps, pl = fermix_amd.slogpf(St, skew_symmetrize=False, prec=prec)
+        assert np.all(np.abs(_np(ps) - sr) < 10 * tol)
+        assert np.all(np.abs(_np(pl) - lr) < 10 * tol * max(1.0, np.abs(lr).max()))
+        qs, ql, Sinv = _kernels.slogpf_parts(St, False, x3=x3)
+        assert torch.equal(qs, ps) and torch.equal(ql, pl)
+        res = S.astype(np.complex128) @ _np(Sinv).astype(np.complex128) - np.eye(n)
+        print(f"  S^-1 residual {np.abs(res).max():.3g}", flush=True)
+        assert np.abs(res).max() < 10 * gtol
+        out[prec] = (_np(l), _np(invT))
+    if n <= 64:
+        assert np.array_equal(out["ieee"][0], out["bf16x3"][0])
+        assert np.array_equal(out["ieee"][1], out["bf16x3"][1])

@@ -41,7 +41,7 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_calls():
     L = _lib.lib()
-    assert L.fx_abi_version() == 201
+    assert L.fx_abi_version() == 202
     assert L.fx_status_string(0) == b"ok"
     assert L.fx_lu_padded_size(100) == 112
     assert L.fx_pf_padded_size(128) == 128
@@ -341,17 +341,20 @@ def test_complex_entry_points_host_checks():
     L = _lib.lib()
     good, bad, ws = 0x10000, 0x10008, 0x20000
     for k, esz in (("c64", 4), ("c128", 8)):
+        q = [_lib.FX_PREC_BF16X3] if k == "c64" else []  # complex64's prec argument
         f = getattr(L, f"fx_slogdet_{k}")
-        assert f(bad, 2, 40, good, good, ws, 1 << 40, None) == 1
-        assert f(good, 2, 40, good + esz, good, ws, 1 << 40, None) == 1  # sign: one complex value
-        assert f(good, -1, 40, good, good, ws, 1 << 40, None) == 1
-        assert f(good, 0, 40, good, good, ws, 1 << 40, None) == 0
-        assert f(good, 2, 8193, good, good, ws, 1 << 40, None) == 4
-        assert getattr(L, f"fx_slogdet_parts_{k}")(good, 2, 40, good, good, bad, ws, 1 << 40, None) == 1
-        assert getattr(L, f"fx_slogpf_{k}")(bad, 2, 40, 0, good, good, ws, 1 << 40, None) == 1
-        assert getattr(L, f"fx_slogpf_parts_{k}")(good, 2, 40, 0, 0, good, good, bad, ws, 1 << 40, None) == 1
+        assert f(bad, 2, 40, good, good, *q, ws, 1 << 40, None) == 1
+        assert f(good, 2, 40, good + esz, good, *q, ws, 1 << 40, None) == 1  # sign: one complex value
+        assert f(good, -1, 40, good, good, *q, ws, 1 << 40, None) == 1
+        assert f(good, 0, 40, good, good, *q, ws, 1 << 40, None) == 0
+        assert f(good, 2, 8193, good, good, *q, ws, 1 << 40, None) == 4
+        if k == "c64":  # an unknown product mode
+            assert f(good, 2, 40, good, good, 7, ws, 1 << 40, None) == 1
+        assert getattr(L, f"fx_slogdet_parts_{k}")(good, 2, 40, good, good, bad, *q, ws, 1 << 40, None) == 1
+        assert getattr(L, f"fx_slogpf_{k}")(bad, 2, 40, 0, good, good, *q, ws, 1 << 40, None) == 1
+        assert getattr(L, f"fx_slogpf_parts_{k}")(good, 2, 40, 0, 0, good, good, bad, *q, ws, 1 << 40, None) == 1
         # the Pfaffian adjugate mode checks its workspace like the inverse mode
-        assert getattr(L, f"fx_slogpf_parts_{k}")(good, 2, 300, 0, 1, good, good, good, ws, 256, None) == 2
+        assert getattr(L, f"fx_slogpf_parts_{k}")(good, 2, 300, 0, 1, good, good, good, *q, ws, 256, None) == 2
         assert getattr(L, f"fx_slogdet_{k}_workspace")(4, 40) == 0
         # n = 300 runs the blocked LU: one copy of padded order 320 plus its pivots and the
         # multi-workgroup panels' posts (G = 1 workgroup's worth per member at this order;
