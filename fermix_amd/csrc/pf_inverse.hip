@@ -188,8 +188,9 @@ __global__ void pf_reduce_bad_kernel(const int* __restrict__ flags, int ntiles, 
 // active members. One workgroup per RPW rows i < N: the source rows f of R are read
 // contiguously into LDS and the column permutation applied there; rows / columns >= n
 // are evaluated (flags[b][i] marks a non-finite value among the workgroup's rows) but
-// not stored.
-template <int RPW>
+// not stored. MAXJ >= N / 256: the columns per thread, a template parameter so that the
+// per-thread column tables (three registers per column) match N.
+template <int RPW, int MAXJ>
 __global__ __launch_bounds__(256) void pf_adj_gather_kernel(const float* __restrict__ R, int N,
                                                             const PfCoef* __restrict__ coef, float sg,
                                                             const float* __restrict__ vw,
@@ -218,7 +219,6 @@ __global__ __launch_bounds__(256) void pf_adj_gather_kernel(const float* __restr
   const float* Rb = R + b * (int64_t)N * N;
   // the column permutation and the correction vectors of this thread's outputs, loaded
   // with the rows (one round trip)
-  constexpr int MAXJ = PF_LARGE_MAXN / 256;
   int cj[MAXJ];
   float wj[MAXJ], vj[MAXJ];
 #pragma unroll
@@ -356,11 +356,20 @@ int launch_pf_inverse(const float* gbuf, int PB, const float* d, const int* perm
     hipLaunchKernelGGL(pf_wvec_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)batch), dim3(256), 0, s, R, N,
                        T, Ninv, coef, iperm, vw, active);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    // two rows per workgroup: measured 383 us at B = 64, N = 2048 against 520 (one), 463 (four)
+    // two rows per workgroup: measured 383 us at B = 64, N = 2048 against 520 (one), 463 (four);
+    // the column tables sized for N (sized for 8192 at every N: 673 us there)
     constexpr int RPW = 2;
-    hipLaunchKernelGGL((pf_adj_gather_kernel<RPW>), dim3((unsigned)((N + RPW - 1) / RPW), (unsigned)batch), dim3(256),
-                       RPW * N * sizeof(float), s, R, N, coef, sg, vw, iperm, n, flags, out, active, accumulate,
-                       scale);
+    const dim3 gg((unsigned)((N + RPW - 1) / RPW), (unsigned)batch);
+    const size_t gl = RPW * N * sizeof(float);
+    if (N <= 2048)
+      hipLaunchKernelGGL((pf_adj_gather_kernel<RPW, 8>), gg, dim3(256), gl, s, R, N, coef, sg, vw, iperm, n, flags, out,
+                         active, accumulate, scale);
+    else if (N <= 4096)
+      hipLaunchKernelGGL((pf_adj_gather_kernel<RPW, 16>), gg, dim3(256), gl, s, R, N, coef, sg, vw, iperm, n, flags,
+                         out, active, accumulate, scale);
+    else
+      hipLaunchKernelGGL((pf_adj_gather_kernel<RPW, PF_LARGE_MAXN / 256>), gg, dim3(256), gl, s, R, N, coef, sg, vw,
+                         iperm, n, flags, out, active, accumulate, scale);
     if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
     if (accumulate) return FX_OK;
     // inverse mode: members with d_K = 0 or a non-finite value anywhere are zeroed
