@@ -17,7 +17,7 @@ FX_PREC_MASK = 0x0F
 FX_LU_BLOCK_64 = 0x100
 FX_LU_BLOCK_128 = 0x200
 
-# fields of struct fx_tune, in order (int32 each; 3 reserved int32 follow)
+# fields of struct fx_tune, in order (int32 each)
 TUNE_FIELDS = (
     "fused_max_n",
     "lu_pair_above_n",
@@ -32,13 +32,16 @@ TUNE_FIELDS = (
     "gemm128_x3_tout",
     "f64_reg_max_n",
     "f64_strip16_max_n",
+    "pf_overlap_max_half",
+    "pf_overlap_min_work",
+    "lu_split_min_work",
 )
 
 
 class FxTune(ctypes.Structure):
     """struct fx_tune of include/fermix.h."""
 
-    _fields_ = [(f, ctypes.c_int32) for f in TUNE_FIELDS] + [("reserved", ctypes.c_int32 * 3)]
+    _fields_ = [(f, ctypes.c_int32) for f in TUNE_FIELDS]
 
 
 _p = ctypes.c_void_p

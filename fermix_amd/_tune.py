@@ -139,6 +139,14 @@ class Tune:
     # float64: registers for n <= f64_reg_max_n, 16-column strips for n <= f64_strip16_max_n
     f64_reg_max_n: int = 128
     f64_strip16_max_n: int = 64
+    # blocked float32 Parlett-Reid: two halves, one half's panels beside the other half's
+    # update in each launch, for halves of at most pf_overlap_max_half matrices and
+    # batch * N^2 >= pf_overlap_min_work * 2^20
+    pf_overlap_max_half: int = 32
+    pf_overlap_min_work: int = 256
+    # blocked float32 LU (N <= 4096): two halves on two streams for batch * N^2 >=
+    # lu_split_min_work * 2^20 (0: never)
+    lu_split_min_work: int = 128
 
 
 # per-architecture tables (the library holds gfx950 code only)

@@ -157,7 +157,7 @@ const char* fx_status_string(int status) {
   }
 }
 
-int fx_abi_version(void) { return 202; }
+int fx_abi_version(void) { return 203; }
 
 int32_t fx_lu_padded_size(int32_t n) {
   fx::TunePin pin_;

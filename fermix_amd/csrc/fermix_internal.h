@@ -2,6 +2,9 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <mutex>
+
 #include "../../include/fermix.h"
 
 namespace fx {
@@ -20,6 +23,35 @@ struct TunePin {
  private:
   bool own_;
 };
+
+// The device's second stream (side.hip) for a driver that runs two halves of a batch side
+// by side. With want and the stream available (not under graph capture), ok() holds and
+// the device's side stream is reserved until the destructor: fork() orders the side
+// stream after the work enqueued so far on s, join() (also run by the destructor) orders
+// s after the side stream's work.
+class SideStream {
+ public:
+  SideStream(hipStream_t s, bool want);
+  ~SideStream();
+  SideStream(const SideStream&) = delete;
+  SideStream& operator=(const SideStream&) = delete;
+  bool ok() const { return side_ != nullptr; }
+  hipStream_t side() const { return side_ ? *side_ : s_; }
+  int fork();
+  int join();
+
+ private:
+  hipStream_t s_;
+  hipStream_t* side_ = nullptr;
+  hipEvent_t* fork_ = nullptr;
+  hipEvent_t* join_ = nullptr;
+  bool forked_ = false;
+  std::unique_lock<std::mutex> lk_;
+};
+
+// Compute units of the current device (side.hip; queried once per device, 256 if the
+// query fails).
+int device_cus();
 
 // dst[i] = src[i] for i < count: count a multiple of 4, both pointers 16-byte aligned.
 int launch_copy(const float* src, float* dst, int64_t count, hipStream_t s);
@@ -61,10 +93,11 @@ int lu_large_padded(int n);
 size_t lu_large_workspace(int64_t batch, int n, bool parts, bool external = false);
 // x3 != 0 runs the trailing updates in the split-bf16x3 mode (FX_PREC_BF16X3); lu_block is
 // FX_LU_BLOCK_TABLE, FX_LU_BLOCK_64 or FX_LU_BLOCK_128 (block pairs from the table, never,
-// always).
+// always). split = false keeps every launch on s (no side stream).
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
                     size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s,
-                    float* W_ext = nullptr, int* g0_ext = nullptr, int x3 = 0, int lu_block = FX_LU_BLOCK_TABLE);
+                    float* W_ext = nullptr, int* g0_ext = nullptr, int x3 = 0, int lu_block = FX_LU_BLOCK_TABLE,
+                    bool split = true);
 
 // A^-T from the packed LU (B, N, N) and row map g0 (B, N) into invT (B, n, n); LU is
 // overwritten when in_place and N is a power-of-two multiple of 32 (inverse.hip).

@@ -896,63 +896,82 @@ static int launch_update(float* W, int N, int64_t batch, int r0, int ntr, int nt
 // panel moves the first block's L columns along with the rows it moves, so both blocks'
 // L columns are in the final row order for the U-row correction and the K = 128 update.
 // The panels' row maps alternate between srcs[0] (even blocks) and srcs[1] (odd); the
-// first pair, reading the input in place of a copy, composes both into srcs[2].
+//
+// The batch may be split over two streams (hv[0] on the caller's stream, hv[1] on the side
+// stream, ordered after hv[0]'s first panel): the blocks are enqueued alternately, half by
+// half, so a half's panel runs beside the other half's U rows and update.
+struct LuHalf {
+  float* W;
+  float* piv;
+  int* nsw;
+  int* srcs[3];
+  float* X;
+  int* g0;
+  const float* A_in;  // the input, read in place of a copy (direct), else nullptr
+  int64_t batch;
+  hipStream_t s;
+};
+
 template <int MR, int NT>
-static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int* const srcs[3], float* X,
-                      int* g0, bool fact, const float* A_in, hipStream_t s, int x3, bool paired) {
+static int run_blocks(int N, const LuHalf* hv, int nh, bool fact, int x3, bool paired, SideStream* side) {
   constexpr int PW = 64;
   const int nblk = N / PW;
   constexpr int MAXM = MR < 1024 ? 1024 : MR;
-  auto urow = [&](int r0, const int* src, int lfirst, int nleft, int nright, const float* A0, const int* rmap,
-                  int rc, int* comp) {
+  auto urow = [&](const LuHalf& H, int r0, const int* src, int lfirst, int nleft, int nright, const float* A0,
+                  const int* rmap, int rc, int* comp) {
     if (nleft + nright == 0) return FX_OK;
-    hipLaunchKernelGGL((lu_urow_kernel<PW, MAXM>), dim3(nleft + nright, (unsigned)batch), dim3(256), 0, s, W, N, r0,
-                       src, X, lfirst, nleft, A0, rmap, rc, comp);
+    hipLaunchKernelGGL((lu_urow_kernel<PW, MAXM>), dim3(nleft + nright, (unsigned)H.batch), dim3(256), 0, H.s, H.W,
+                       N, r0, src, H.X, lfirst, nleft, A0, rmap, rc, comp);
     return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
   };
   for (int blk = 0; blk < nblk; ++blk) {
-    const int r0 = blk * PW;
-    const int m = N - r0;
-    int* src = srcs[blk & 1];
-    const float* A0 = blk == 0 ? A_in : nullptr;  // input read in place of a copy
-    const int lmove = paired && (blk & 1);  // a pair's second panel moves the first block's L along
-    if (m <= 1024) {
-#define FX_PANEL_REG(T)                                                                                       \
-  hipLaunchKernelGGL((lu_panel_reg_kernel<T>), dim3((unsigned)batch), dim3(T), 0, s, W, N, r0, blk, piv, nsw, \
-                     nblk, src, X, g0, A0, lmove)
-      if (m <= 64) FX_PANEL_REG(64);
-      else if (m <= 128) FX_PANEL_REG(128);
-      else if (m <= 256) FX_PANEL_REG(256);
-      else if (m <= 512) FX_PANEL_REG(512);
-      else FX_PANEL_REG(1024);
+    for (int h = 0; h < nh; ++h) {
+      const LuHalf& H = hv[h];
+      const hipStream_t s = H.s;
+      const int r0 = blk * PW;
+      const int m = N - r0;
+      int* src = H.srcs[blk & 1];
+      const float* A0 = blk == 0 ? H.A_in : nullptr;  // input read in place of a copy
+      const int lmove = paired && (blk & 1);  // a pair's second panel moves the first block's L along
+      if (m <= 1024) {
+#define FX_PANEL_REG(T)                                                                                   \
+  hipLaunchKernelGGL((lu_panel_reg_kernel<T>), dim3((unsigned)H.batch), dim3(T), 0, s, H.W, N, r0, blk, \
+                     H.piv, H.nsw, nblk, src, H.X, H.g0, A0, lmove)
+        if (m <= 64) FX_PANEL_REG(64);
+        else if (m <= 128) FX_PANEL_REG(128);
+        else if (m <= 256) FX_PANEL_REG(256);
+        else if (m <= 512) FX_PANEL_REG(512);
+        else FX_PANEL_REG(1024);
 #undef FX_PANEL_REG
-    } else if constexpr (MR > 1024) {
-      hipLaunchKernelGGL((lu_panel_kernel<MR, PW, NT>), dim3((unsigned)batch), dim3(NT), 0, s, W, N, r0, blk, piv,
-                         nsw, nblk, src, X, g0, lmove);
+      } else if constexpr (MR > 1024) {
+        hipLaunchKernelGGL((lu_panel_kernel<MR, PW, NT>), dim3((unsigned)H.batch), dim3(NT), 0, s, H.W, N, r0, blk,
+                           H.piv, H.nsw, nblk, src, H.X, H.g0, lmove);
+      }
+      if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
+      if (blk == 0 && h == 0 && nh == 2 && side->fork() != FX_OK) return FX_ERR_LAUNCH;
+      const int nright = (N - r0 - PW) / 64;  // trailing strips / tile rows (N a multiple of 64)
+      int st;
+      if (!paired) {
+        st = urow(H, r0, src, 0, fact ? r0 / 64 : 0, nright, A0, nullptr, -1, nullptr);
+        if (st == FX_OK && nright > 0)
+          st = launch_update<1>(H.W, N, H.batch, r0, nright, nright, A0, A0 ? src : nullptr, s, x3);
+      } else if ((blk & 1) == 0) {
+        // first block of a pair: U rows, then the update of the next panel's columns only
+        st = urow(H, r0, src, 0, fact ? r0 / 64 : 0, nright, A0, nullptr, -1, nullptr);
+        if (st == FX_OK && nright > 0)
+          st = launch_update<1>(H.W, N, H.batch, r0, nright, 1, A0, A0 ? src : nullptr, s, x3);
+      } else {
+        // second block: U rows with the first block's deferred update, then both blocks'
+        // update of the trailing matrix; the first pair reads the input through both maps
+        const int rp = r0 - PW;
+        const float* Ain = blk == 1 ? H.A_in : nullptr;
+        st = urow(H, r0, src, 0, fact ? rp / 64 : 0, nright, Ain, Ain ? H.srcs[0] : nullptr, rp,
+                  Ain && nright > 0 ? H.srcs[2] : nullptr);
+        if (st == FX_OK && nright > 0)
+          st = launch_update<2>(H.W, N, H.batch, rp, nright, nright, Ain, Ain ? H.srcs[2] : nullptr, s, x3);
+      }
+      if (st != FX_OK) return st;
     }
-    if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;
-    const int nright = (N - r0 - PW) / 64;  // trailing strips / tile rows (N a multiple of 64)
-    int st;
-    if (!paired) {
-      st = urow(r0, src, 0, fact ? r0 / 64 : 0, nright, A0, nullptr, -1, nullptr);
-      if (st == FX_OK && nright > 0)
-        st = launch_update<1>(W, N, batch, r0, nright, nright, A0, A0 ? src : nullptr, s, x3);
-    } else if ((blk & 1) == 0) {
-      // first block of a pair: U rows, then the update of the next panel's columns only
-      st = urow(r0, src, 0, fact ? r0 / 64 : 0, nright, A0, nullptr, -1, nullptr);
-      if (st == FX_OK && nright > 0)
-        st = launch_update<1>(W, N, batch, r0, nright, 1, A0, A0 ? src : nullptr, s, x3);
-    } else {
-      // second block: U rows with the first block's deferred update, then both blocks'
-      // update of the trailing matrix; the first pair reads the input through both maps
-      const int rp = r0 - PW;
-      const float* Ain = blk == 1 ? A_in : nullptr;
-      st = urow(r0, src, 0, fact ? rp / 64 : 0, nright, Ain, Ain ? srcs[0] : nullptr, rp,
-                Ain && nright > 0 ? srcs[2] : nullptr);
-      if (st == FX_OK && nright > 0)
-        st = launch_update<2>(W, N, batch, rp, nright, nright, Ain, Ain ? srcs[2] : nullptr, s, x3);
-    }
-    if (st != FX_OK) return st;
   }
   return FX_OK;
 }
@@ -961,7 +980,7 @@ static int run_blocks(float* W, int N, int64_t batch, float* piv, int* nsw, int*
 // and the composed row map g0 (parts only) through *g0_out.
 int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* logabs, void* ws,
                     size_t ws_bytes, bool parts, float** W_out, int** g0_out, hipStream_t s, float* W_ext,
-                    int* g0_ext, int x3, int lu_block) {
+                    int* g0_ext, int x3, int lu_block, bool split) {
   const int N = lu_large_padded(n);
   const int PW = lu_panel_width(N);
   const int nblk = N / PW;
@@ -1005,16 +1024,40 @@ int launch_lu_large(const float* A, int n, int64_t batch, float* sign, float* lo
     const int64_t tot = batch * N;
     hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, g0, N, tot);
   }
+  // Batches with batch N^2 >= fx_tune.lu_split_min_work 2^20 run as two halves side by side
+  // (see run_blocks) for N <= 4096 (above, the halves' panels lose more than the overlap
+  // gains); every kernel works per matrix, so the results are the same bits. The
+  // no-allocation entry point passes split = false.
+  const bool halves = split && batch >= 2 && N <= 4096 && tn.lu_split_min_work > 0 &&
+                      (double)batch * N * N >= (double)tn.lu_split_min_work * (1 << 20);
+  SideStream side(s, halves);
+  const int nh = side.ok() ? 2 : 1;
+  const int64_t hb = (batch + nh - 1) / nh;
+  LuHalf hv[2];
+  for (int h = 0; h < nh; ++h) {
+    const int64_t b0 = h * hb;
+    LuHalf& H = hv[h];
+    H.W = W + b0 * (int64_t)N * N;
+    H.piv = piv + b0 * N;
+    H.nsw = nsw + b0 * nblk;
+    for (int k = 0; k < 3; ++k) H.srcs[k] = srcs[k] + b0 * N;
+    H.X = X + b0 * (PW / 16) * 256;
+    H.g0 = g0 ? g0 + b0 * N : nullptr;
+    H.A_in = direct ? A + b0 * (int64_t)N * N : nullptr;
+    H.batch = h + 1 < nh ? hb : batch - b0;
+    H.s = h == 0 ? s : side.side();
+  }
   int st;
   if (N <= 1024)
-    st = run_blocks<1024, 0>(W, N, batch, piv, nsw, srcs, X, g0, parts, direct ? A : nullptr, s, x3, paired);
+    st = run_blocks<1024, 0>(N, hv, nh, parts, x3, paired, &side);
   else if (N <= 2048)
-    st = run_blocks<2048, 512>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3, paired);
+    st = run_blocks<2048, 512>(N, hv, nh, parts, x3, paired, &side);
   else if (N <= 4096)
-    st = run_blocks<4096, 1024>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3, paired);
+    st = run_blocks<4096, 1024>(N, hv, nh, parts, x3, paired, &side);
   else
-    st = run_blocks<8192, 1024>(W, N, batch, piv, nsw, srcs, X, g0, parts, nullptr, s, x3, paired);
+    st = run_blocks<8192, 1024>(N, hv, nh, parts, x3, paired, &side);
   if (st != FX_OK) return st;
+  if (side.join() != FX_OK) return FX_ERR_LAUNCH;
   hipLaunchKernelGGL(lu_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, piv, nsw, N,
                      nblk, sign, logabs, batch);
   if (hipGetLastError() != hipSuccess) return FX_ERR_LAUNCH;

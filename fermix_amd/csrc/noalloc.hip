@@ -91,11 +91,13 @@ extern "C" int fx_slogdet_f32_noalloc(const float* a, int64_t batch, int32_t n, 
   // Sub-batches go straight to the blocked LU, which reads each member's rows with
   // 4-byte loads whenever the matrices are not 16-byte aligned: for odd n a sub-batch
   // starts at a + b0 n^2 floats, 4-byte aligned only (n^2 = 1 mod 4). Same arguments as
-  // fx_slogdet_f32 with FX_PREC_IEEE and the table's block choice, so bit-identical.
+  // fx_slogdet_f32 with FX_PREC_IEEE and the table's block choice, so bit-identical; all on
+  // the caller's stream (the side stream of a split batch is created on first use).
   for (int64_t b0 = 0; b0 < batch; b0 += m) {
     const int64_t nb = batch - b0 < m ? batch - b0 : m;
     const int r = launch_lu_large(a + b0 * n * n, n, nb, sign + b0, logabs + b0, ws, FX_NOALLOC_SCRATCH_BYTES,
-                                  false, nullptr, nullptr, (hipStream_t)stream, nullptr, nullptr, FX_PREC_IEEE, 0);
+                                  false, nullptr, nullptr, (hipStream_t)stream, nullptr, nullptr, FX_PREC_IEEE, 0,
+                                  false);
     if (r != FX_OK) return r;
   }
   return FX_OK;

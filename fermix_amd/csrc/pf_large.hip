@@ -157,20 +157,18 @@ __global__ __launch_bounds__(256) void pf_copy_pad_kernel(const float* __restric
   }
 }
 
+// The panel of matrix b (one workgroup of NT threads; pf_panel_kernel, pf_step_kernel).
 template <int NT, int R, int PB>
-__global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ M, int N, int r0, int nch,
-                                                      float* __restrict__ d_out,
-                                                      int* __restrict__ nsw_out,
-                                                      int* __restrict__ src_out,
-                                                      float* __restrict__ Gn,
-                                                      int* __restrict__ orig,
-                                                      float* __restrict__ gbuf, int full) {
+__device__ __forceinline__ void pf_panel_body(const float* __restrict__ M, int N, int r0, int nch,
+                                              float* __restrict__ d_out, int* __restrict__ nsw_out,
+                                              int* __restrict__ src_out, float* __restrict__ Gn,
+                                              int* __restrict__ orig, float* __restrict__ gbuf, int full,
+                                              int64_t b) {
   constexpr int NW = NT / 64;
   constexpr int CW = PB < 32 ? PB : 32;  // factor chunk width
   static_assert(PB % CW == 0 && PB / CW <= 2, "a block spans one or two chunks");
   __shared__ __align__(16) PfRowA rowa;
   __shared__ __align__(16) PfCand cand[2][NW];
-  const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = N - r0;
   // M[r0 + q][r0 + i] of the block-start matrix: the input itself in full storage (full:
@@ -380,6 +378,17 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
   }
 }
 
+template <int NT, int R, int PB>
+__global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ M, int N, int r0, int nch,
+                                                      float* __restrict__ d_out,
+                                                      int* __restrict__ nsw_out,
+                                                      int* __restrict__ src_out,
+                                                      float* __restrict__ Gn,
+                                                      int* __restrict__ orig,
+                                                      float* __restrict__ gbuf, int full) {
+  pf_panel_body<NT, R, PB>(M, N, r0, nch, d_out, nsw_out, src_out, Gn, orig, gbuf, full, blockIdx.x);
+}
+
 // M_new[p][q] = M_old[src p][src q] + sum_k G[p][k] (J G^T)[k][q] for the trailing
 // positions p > q >= r1 (lower tiles of T x T). Four waves, each owning a (T/2) x (T/2)
 // quarter as AW x AW 32x32 MFMA accumulators (the rows 8 (v / 4) + 4 lh + v % 4 of
@@ -389,20 +398,218 @@ __global__ __launch_bounds__(NT) void pf_panel_kernel(const float* __restrict__ 
 // column src q (a moved column's source is a block row, below every trailing row, so the
 // entry is stored there), a strip with a moved row (at most PB per block) entry by entry.
 // New entries: the strip layout, four rows of a column per 16-byte store.
+// Here in three phases on tile t of matrix b by the 256 threads tid of a workgroup:
+// stage (G rows and the permutation into LDS), a workgroup barrier, load (the old entries
+// into the accumulators), finish (G J G^T added, the lower entries stored). A workgroup
+// may hold several tiles (pf_step_kernel: each 256-thread group two, all staged before the
+// one barrier and all loaded before the first finish, for more loads in flight); an
+// inactive tile (act = false) takes part in the barrier only. lds: 2 PB (T + 4) floats.
+template <int PB, int T>
+struct PfTile {
+  static constexpr int H = T / 2, AW = H / 32;  // quarter size, accumulators per side
+  static constexpr int LDG = T + 4;
+  typedef float v16f __attribute__((ext_vector_type(16)));
+  int I, J, p0, q0;
+  int64_t b;
+  bool act;
+  float* Ga;  // the G rows of the tile rows, K-major
+  float* Hb;  // the (J G^T) columns of the tile columns, K-major
+  int* sp;
+  int* sq;
+  int* smv;  // strip of the tile rows with a moved row
+  v16f acc[AW][AW];
+
+  PfTile() = default;
+  __device__ __forceinline__ PfTile(int r1, int64_t b_, int t, bool act_, float* lds, int* sp_, int* sq_, int* smv_)
+      : b(b_), act(act_), Ga(lds), Hb(lds + PB * LDG), sp(sp_), sq(sq_), smv(smv_) {
+    I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
+    while ((I + 1) * (I + 2) / 2 <= t) ++I;
+    while (I * (I + 1) / 2 > t) --I;
+    J = t - I * (I + 1) / 2;
+    p0 = r1 + T * I;
+    q0 = r1 + T * J;
+  }
+
+  __device__ __forceinline__ void stage(int N, const int* __restrict__ src, const float* __restrict__ Gn, int tid);
+
+  __device__ __forceinline__ void load(const float* __restrict__ M, int N, const float* __restrict__ Min, int tid) {
+    if (!act) return;
+    const int wave = tid >> 6, lane = tid & 63;
+    const float* Mb = M + b * (int64_t)N * N;  // entries addressed by 32-bit offsets (N * N < 2^31)
+    // wave (wr, wc) owns an H x H quarter: the old entries M[src p][src q] (zeros for rows
+    // / columns beyond N and the upper half of a diagonal tile, which are never stored),
+    // loaded first, and G J G^T in AW x AW 32x32 accumulators of its own, added in fp32:
+    // the MFMAs truncate what they add below about three bits under the accumulator's
+    // last place, so small products added to the old entries one by one would lose more
+    const bool diag = I == J;
+    const int wr = (wave >> 1) * H, wc = (wave & 1) * H;
+    const int l32 = lane & 31, lh = lane >> 5;
+#pragma unroll
+    for (int a = 0; a < AW; ++a)
+#pragma unroll
+      for (int c = 0; c < AW; ++c) {
+        const int cl = wc + 32 * c + l32, q = q0 + cl;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int rl = wr + 32 * a + 8 * g + 4 * lh, p = p0 + rl;  // p % 4 == 0
+          float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          if (Min) {
+            // rows / columns beyond N hold index 0 in sp / sq: in-bounds reads
+            const float* Ab = Min + b * (int64_t)N * N;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] = Ab[(unsigned)(sp[rl + u] * N + sq[cl])];
+          } else if (p < N && q < N) {
+            const int scol = sq[cl];
+            if (!diag && !smv[rl >> 2]) {  // uniform per half-wave
+              const float4 y = *reinterpret_cast<const float4*>(Mb + l4(p, scol, N));
+              x[0] = y.x;
+              x[1] = y.y;
+              x[2] = y.z;
+              x[3] = y.w;
+            } else {
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                const int srow = sp[rl + u];
+                const float y = Mb[l4(max(srow, scol), min(srow, scol), N)];
+                x[u] = (diag && p + u <= q) ? 0.0f : (srow > scol ? y : -y);
+              }
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc[a][c][4 * g + u] = x[u];
+        }
+      }
+  }
+
+  __device__ __forceinline__ void finish(float* __restrict__ M, int N, int tid) {
+    if (!act) return;
+    const int wave = tid >> 6, lane = tid & 63;
+    const bool diag = I == J;
+    const int wr = (wave >> 1) * H, wc = (wave & 1) * H;
+    const int l32 = lane & 31, lh = lane >> 5;
+    float* Mb = M + b * (int64_t)N * N;
+    v16f prod[AW][AW];
+#pragma unroll
+    for (int a = 0; a < AW; ++a)
+#pragma unroll
+      for (int c = 0; c < AW; ++c)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) prod[a][c][v] = 0.0f;
+#pragma unroll
+    for (int kp = 0; kp < PB / 2; ++kp) {
+      float av[AW], bv[AW];
+#pragma unroll
+      for (int a = 0; a < AW; ++a) av[a] = Ga[(2 * kp + lh) * LDG + wr + 32 * a + l32];
+#pragma unroll
+      for (int c = 0; c < AW; ++c) bv[c] = Hb[(2 * kp + lh) * LDG + wc + 32 * c + l32];
+#pragma unroll
+      for (int a = 0; a < AW; ++a)
+#pragma unroll
+        for (int c = 0; c < AW; ++c)
+          prod[a][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[c], prod[a][c], 0, 0, 0);
+    }
+#pragma unroll
+    for (int a = 0; a < AW; ++a)
+#pragma unroll
+      for (int c = 0; c < AW; ++c)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[a][c][v] += prod[a][c][v];
+    // the lower entries: whole strips off the diagonal tiles (N is a multiple of 4, so a
+    // strip is inside the matrix or outside it), entry by entry below the diagonal of a
+    // diagonal tile
+#pragma unroll
+    for (int a = 0; a < AW; ++a)
+#pragma unroll
+      for (int c = 0; c < AW; ++c) {
+        const int q = q0 + wc + 32 * c + l32;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int p = p0 + wr + 32 * a + 8 * g + 4 * lh;  // a multiple of 4
+          if (p >= N || q >= N) continue;
+          float* dst = Mb + l4(p, q, N);
+          if (!diag) {
+            *reinterpret_cast<float4*>(dst) =
+                make_float4(acc[a][c][4 * g], acc[a][c][4 * g + 1], acc[a][c][4 * g + 2], acc[a][c][4 * g + 3]);
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              if (p + u > q) dst[u] = acc[a][c][4 * g + u];
+          }
+        }
+      }
+  }
+};
+
+// The staging registers of one tile: gload (its G rows and permutation entries, every
+// load issued before the first use) then lwrite (into the tile's LDS); stage is both.
+// pf_step_kernel issues a later tile's gload before finishing the current tile.
+template <int PB, int T>
+struct PfStage {
+  static constexpr int GE = T * PB / 256, LDG = T + 4;
+  float ga[GE], gb[GE];
+  int gsp, gsq;
+  bool gmv;
+
+  __device__ __forceinline__ void gload(const PfTile<PB, T>& x, int N, const int* __restrict__ src,
+                                        const float* __restrict__ Gn, int tid) {
+    if (!x.act) return;
+    const float* G = Gn + x.b * (int64_t)N * PB;
+    const int* sb = src + x.b * N;
+#pragma unroll
+    for (int i = 0; i < GE; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e / PB, k = e % PB;
+      const int p = min(x.p0 + r, N - 1), q = min(x.q0 + r, N - 1);
+      ga[i] = G[(unsigned)(p * PB + k)];
+      gb[i] = G[(unsigned)(q * PB + (k ^ 1))];
+    }
+    if (tid < T) {
+      gsp = x.p0 + tid < N ? sb[x.p0 + tid] : 0;
+      gsq = x.q0 + tid < N ? sb[x.q0 + tid] : 0;
+    } else if (tid < T + T / 4) {
+      const int r = x.p0 + 4 * (tid - T);  // rows beyond N (whole strips: N % 4 == 0) count as unmoved
+      bool mv = false;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) mv = mv || (r < N && sb[r + u] != r + u);
+      gmv = mv;
+    }
+  }
+
+  __device__ __forceinline__ void lwrite(const PfTile<PB, T>& x, int N, int tid) const {
+    if (!x.act) return;
+#pragma unroll
+    for (int i = 0; i < GE; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e / PB, k = e % PB;
+      x.Ga[k * LDG + r] = x.p0 + r < N ? ga[i] : 0.0f;
+      const float gq = x.q0 + r < N ? gb[i] : 0.0f;
+      x.Hb[k * LDG + r] = (k & 1) ? -gq : gq;
+    }
+    if (tid < T) {
+      x.sp[tid] = gsp;
+      x.sq[tid] = gsq;
+    } else if (tid < T + T / 4) {
+      x.smv[tid - T] = gmv;
+    }
+  }
+};
+
+template <int PB, int T>
+__device__ __forceinline__ void PfTile<PB, T>::stage(int N, const int* __restrict__ src, const float* __restrict__ Gn,
+                                                     int tid) {
+  PfStage<PB, T> g;
+  g.gload(*this, N, src, Gn, tid);
+  g.lwrite(*this, N, tid);
+}
+
 template <int PB, int T>
 __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, int N, int r1,
                                                         const int* __restrict__ src,
                                                         const float* __restrict__ Gn,
                                                         const float* __restrict__ Min) {
-  constexpr int H = T / 2, AW = H / 32;       // quarter size, accumulators per side
-  constexpr int LDG = T + 4;
-  typedef float v16f __attribute__((ext_vector_type(16)));
-  // Ga / Hb: the G rows of the tile rows / (J G^T) columns of the tile columns, K-major
-  __shared__ __align__(16) float lds[2 * PB * LDG];
+  __shared__ __align__(16) float lds[2 * PB * (T + 4)];
   __shared__ int sp[T], sq[T];
   __shared__ int smv[T / 4];  // strip of the tile rows with a moved row
-  float* Ga = lds;
-  float* Hb = lds + PB * LDG;
   int64_t b = blockIdx.y;
   int t = blockIdx.x;
   if (PB >= 64 && (gridDim.y & 7) == 0) {
@@ -414,137 +621,114 @@ __global__ __launch_bounds__(256) void pf_update_kernel(float* __restrict__ M, i
     t = (int)(slot % gridDim.x);
     b = (slot / gridDim.x) * 8 + (lin & 7);
   }
-  int I = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
-  while ((I + 1) * (I + 2) / 2 <= t) ++I;
-  while (I * (I + 1) / 2 > t) --I;
-  const int J = t - I * (I + 1) / 2;
-  const int p0 = r1 + T * I, q0 = r1 + T * J;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const float* G = Gn + b * (int64_t)N * PB;
-  const int* sb = src + b * N;
-  float* Mb = M + b * (int64_t)N * N;  // entries addressed by 32-bit offsets (N * N < 2^31)
-  // fixed trip count, so every load is issued before the first store
-  constexpr int GE = T * PB / 256;
-  float ga[GE], gb[GE];
-#pragma unroll
-  for (int i = 0; i < GE; ++i) {
-    const int e = tid + 256 * i;
-    const int r = e / PB, k = e % PB;
-    const int p = min(p0 + r, N - 1), q = min(q0 + r, N - 1);
-    ga[i] = G[(unsigned)(p * PB + k)];
-    gb[i] = G[(unsigned)(q * PB + (k ^ 1))];
+  PfTile<PB, T> x(r1, b, t, true, lds, sp, sq, smv);
+  x.stage(N, src, Gn, threadIdx.x);
+  __syncthreads();
+  x.load(M, N, Min, threadIdx.x);
+  x.finish(M, N, threadIdx.x);
+}
+
+// One launch of two independent pieces of work on two halves of a batch: the panels of one
+// half (workgroups 0 .. pa.batch - 1, one matrix each, pf_panel_body) and the trailing
+// update of the other half (the later workgroups, persistent, one per CU left over). The panel
+// workgroups come first in the dispatch order, so each finds an empty CU (a 1024-thread
+// panel needs one to itself) before the update tiles fill the GPU beside them; as
+// separate kernels on two streams the update's small workgroups keep every CU partly busy
+// and the panel waits for the whole update.
+struct PfPanelArgs {
+  const float* M;
+  int N, r0, nch, full;
+  float* d;
+  int* nsw;
+  int* src;
+  float* Gn;
+  int* orig;
+  float* gbuf;
+  int64_t batch;
+};
+struct PfUpdateArgs {
+  float* M;
+  int r1, ntiles;
+  const int* src;
+  const float* Gn;
+  const float* Min;
+  int64_t batch;
+};
+
+template <int NT, int R, int PBp, int PBu>
+__global__ __launch_bounds__(NT) void pf_step_kernel(PfPanelArgs pa, PfUpdateArgs ua) {
+  if ((int64_t)blockIdx.x < pa.batch) {
+    pf_panel_body<NT, R, PBp>(pa.M, pa.N, pa.r0, pa.nch, pa.d, pa.nsw, pa.src, pa.Gn, pa.orig, pa.gbuf, pa.full,
+                              blockIdx.x);
+    return;
   }
+  // The update workgroups (nU = gridDim.x - pa.batch, each holding a CU) are persistent:
+  // in iteration k, group sub of workgroup w updates the NL tiles ((k nU + w) NS + sub) NL
+  // + l. The loop keeps two stages per group in flight: stage k + 1's old entries (and,
+  // where the registers hold them, stage k + 2's G rows) are loaded while stage k is
+  // finished (LDS double-buffered; two barriers per iteration, the trip count uniform
+  // over the workgroup). In the 128 registers of a 1024-thread workgroup: NL = 1, the G
+  // rows ahead for PB <= 16 only (at PB = 32 they would spill). (Measured: 512-thread
+  // workgroups, whose panels hold 4 rows per lane and whose update groups then have the
+  // registers for two tiles per stage, ran the update part slower still: 8 waves per CU
+  // hide less latency than 16.)
+  constexpr int NS = NT / 256, NL = 1, T = PF_UPDATE_TILE;
+  constexpr bool GAHEAD = PBu <= 16;
+  __shared__ __align__(16) float lds[2][NS * NL][2 * PBu * (T + 4)];
+  __shared__ int sp[2][NS * NL][T], sq[2][NS * NL][T], smv[2][NS * NL][T / 4];
+  const int sub = threadIdx.x >> 8, tid = threadIdx.x & 255;
+  const int64_t w = (int64_t)blockIdx.x - pa.batch, nU = (int64_t)gridDim.x - pa.batch;
+  const int64_t tot = ua.batch * ua.ntiles;
+  const int64_t iters = (tot + nU * NS * NL - 1) / (nU * NS * NL);
+  auto tile = [&](int64_t k, int l) {
+    const int64_t f = ((k * nU + w) * NS + sub) * NL + l;
+    const bool act = k < iters && f < tot;
+    const int64_t b = act ? f / ua.ntiles : 0;
+    const int buf = (int)(k & 1), slot = sub * NL + l;
+    return PfTile<PBu, T>(ua.r1, b, act ? (int)(f - b * ua.ntiles) : 0, act, lds[buf][slot], sp[buf][slot],
+                          sq[buf][slot], smv[buf][slot]);
+  };
+  if (iters == 0) return;
+  const int N = pa.N;
+  typedef PfTile<PBu, T> Tile;
+  // stage slots A (even iterations) and B (odd); g holds stage k + 2's staging registers
+  // (the loops over l are unrolled, so the arrays stay in registers)
+  Tile ta[NL], tb[NL];
 #pragma unroll
-  for (int i = 0; i < GE; ++i) {
-    const int e = tid + 256 * i;
-    const int r = e / PB, k = e % PB;
-    Ga[k * LDG + r] = p0 + r < N ? ga[i] : 0.0f;
-    const float gq = q0 + r < N ? gb[i] : 0.0f;
-    Hb[k * LDG + r] = (k & 1) ? -gq : gq;
-  }
-  if (tid < T) {
-    sp[tid] = p0 + tid < N ? sb[p0 + tid] : 0;
-    sq[tid] = q0 + tid < N ? sb[q0 + tid] : 0;
-  } else if (tid < T + T / 4) {
-    const int r = p0 + 4 * (tid - T);  // rows beyond N (whole strips: N % 4 == 0) count as unmoved
-    bool mv = false;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) mv = mv || (r < N && sb[r + u] != r + u);
-    smv[tid - T] = mv;
+  for (int l = 0; l < NL; ++l) {
+    ta[l] = tile(0, l);
+    tb[l] = tile(1, l);
+    ta[l].stage(N, ua.src, ua.Gn, tid);
+    tb[l].stage(N, ua.src, ua.Gn, tid);
   }
   __syncthreads();
-  // wave (wr, wc) owns an H x H quarter: the old entries M[src p][src q] (zeros for rows
-  // / columns beyond N and the upper half of a diagonal tile, which are never stored),
-  // loaded first, and G J G^T in AW x AW 32x32 accumulators of its own, added in fp32:
-  // the MFMAs truncate what they add below about three bits under the accumulator's
-  // last place, so small products added to the old entries one by one would lose more
-  const bool diag = I == J;
-  const int wr = (wave >> 1) * H, wc = (wave & 1) * H;
-  const int l32 = lane & 31, lh = lane >> 5;
-  v16f acc[AW][AW], prod[AW][AW];
 #pragma unroll
-  for (int a = 0; a < AW; ++a)
+  for (int l = 0; l < NL; ++l) ta[l].load(ua.M, N, ua.Min, tid);
+  PfStage<PBu, T> g[NL];
+  // stage k in cur, k + 1 in nxt (loaded here); cur then takes stage k + 2
+  auto step = [&](Tile (&cur)[NL], Tile (&nxt)[NL], int64_t k) {
+    Tile nn[NL];
 #pragma unroll
-    for (int c = 0; c < AW; ++c) {
-      const int cl = wc + 32 * c + l32, q = q0 + cl;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int rl = wr + 32 * a + 8 * g + 4 * lh, p = p0 + rl;  // p % 4 == 0
-        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (Min) {
-          // rows / columns beyond N hold index 0 in sp / sq: in-bounds reads
-          const float* Ab = Min + b * (int64_t)N * N;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) x[u] = Ab[(unsigned)(sp[rl + u] * N + sq[cl])];
-        } else if (p < N && q < N) {
-          const int scol = sq[cl];
-          if (!diag && !smv[rl >> 2]) {  // uniform per half-wave
-            const float4 y = *reinterpret_cast<const float4*>(Mb + l4(p, scol, N));
-            x[0] = y.x;
-            x[1] = y.y;
-            x[2] = y.z;
-            x[3] = y.w;
-          } else {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int srow = sp[rl + u];
-              const float y = Mb[l4(max(srow, scol), min(srow, scol), N)];
-              x[u] = (diag && p + u <= q) ? 0.0f : (srow > scol ? y : -y);
-            }
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc[a][c][4 * g + u] = x[u];
-      }
+    for (int l = 0; l < NL; ++l) {
+      nxt[l].load(ua.M, N, ua.Min, tid);
+      nn[l] = tile(k + 2, l);
+      if constexpr (GAHEAD) g[l].gload(nn[l], N, ua.src, ua.Gn, tid);
     }
 #pragma unroll
-  for (int a = 0; a < AW; ++a)
+    for (int l = 0; l < NL; ++l) cur[l].finish(ua.M, N, tid);
+    __syncthreads();  // cur's buffers are free
 #pragma unroll
-    for (int c = 0; c < AW; ++c)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) prod[a][c][v] = 0.0f;
-#pragma unroll
-  for (int kp = 0; kp < PB / 2; ++kp) {
-    float av[AW], bv[AW];
-#pragma unroll
-    for (int a = 0; a < AW; ++a) av[a] = Ga[(2 * kp + lh) * LDG + wr + 32 * a + l32];
-#pragma unroll
-    for (int c = 0; c < AW; ++c) bv[c] = Hb[(2 * kp + lh) * LDG + wc + 32 * c + l32];
-#pragma unroll
-    for (int a = 0; a < AW; ++a)
-#pragma unroll
-      for (int c = 0; c < AW; ++c)
-        prod[a][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[c], prod[a][c], 0, 0, 0);
+    for (int l = 0; l < NL; ++l) {
+      cur[l] = nn[l];
+      if constexpr (!GAHEAD) g[l].gload(cur[l], N, ua.src, ua.Gn, tid);
+      g[l].lwrite(cur[l], N, tid);
+    }
+    __syncthreads();  // their rows visible
+  };
+  for (int64_t k = 0; k < iters; k += 2) {
+    step(ta, tb, k);
+    if (k + 1 < iters) step(tb, ta, k + 1);
   }
-#pragma unroll
-  for (int a = 0; a < AW; ++a)
-#pragma unroll
-    for (int c = 0; c < AW; ++c)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[a][c][v] += prod[a][c][v];
-  // the lower entries: whole strips off the diagonal tiles (N is a multiple of 4, so a
-  // strip is inside the matrix or outside it), entry by entry below the diagonal of a
-  // diagonal tile
-#pragma unroll
-  for (int a = 0; a < AW; ++a)
-#pragma unroll
-    for (int c = 0; c < AW; ++c) {
-      const int q = q0 + wc + 32 * c + l32;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int p = p0 + wr + 32 * a + 8 * g + 4 * lh;  // a multiple of 4
-        if (p >= N || q >= N) continue;
-        float* dst = Mb + l4(p, q, N);
-        if (!diag) {
-          *reinterpret_cast<float4*>(dst) =
-              make_float4(acc[a][c][4 * g], acc[a][c][4 * g + 1], acc[a][c][4 * g + 2], acc[a][c][4 * g + 3]);
-        } else {
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            if (p + u > q) dst[u] = acc[a][c][4 * g + u];
-        }
-      }
-    }
 }
 
 __global__ void pf_finish_kernel(const float* __restrict__ d, const int* __restrict__ nsw, int H, int nch,
@@ -638,6 +822,78 @@ static int pf_block(float* M, int N, int r0, int nch, int64_t batch, float* d, i
   return FX_OK;
 }
 
+// Rows per lane of the panels of PB-column blocks.
+static constexpr int pf_rows(int PB) { return PB == PFB_XXL ? 8 : PB == PFB_XL ? 4 : 2; }
+
+// One launch of pf_step_kernel: the panels of pa (1024 threads, their trailing order
+// m > 512 R) and the update of ua.
+template <int R, int PB>
+static int step_launch(const PfPanelArgs& pa, const PfUpdateArgs& ua, hipStream_t s) {
+  constexpr int NT = 1024;
+  static_assert(PB * R <= 64, "G[R][PB] fits the 128 VGPRs of a 1024-thread workgroup");
+  if (pa.batch > 0 && pa.N - pa.r0 <= 512 * R) return FX_ERR_UNSUPPORTED;
+  // update workgroups: one per CU the panels leave (at least a quarter of the device)
+  const int cus = device_cus();
+  int64_t nu = 0;
+  if (ua.batch * ua.ntiles > 0) nu = cus - pa.batch > cus / 4 ? cus - pa.batch : cus / 4;
+  const int64_t grid = pa.batch + nu;
+  if (grid > 0x7fffffff || grid == 0) return FX_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((pf_step_kernel<NT, R, PB, PB>), dim3((unsigned)grid), dim3(NT), 0, s, pa, ua);
+  return hipGetLastError() == hipSuccess ? FX_OK : FX_ERR_LAUNCH;
+}
+
+// The buffers of the matrices b0 .. b0 + batch - 1 of a run.
+struct PfPart {
+  float* M;
+  float* d;
+  int* nsw;
+  int* src;
+  float* G;  // this part's G region (widest block)
+  int* orig;
+  float* gbuf;
+  const float* A;  // the input, read in place by the first block (direct), else nullptr
+  int64_t batch;
+};
+
+// Panels of block (rp, PB) of part P (nullptr: none) and the update after block (ru, PB)
+// of part U (nullptr: none), in one launch of pf_step_kernel; both blocks PB columns wide
+// with 1024-thread panels.
+static int pf_pair(int N, int nch, const PfPart* P, int rp, const PfPart* U, int ru, int PB, hipStream_t s) {
+  if (U && ru + PB >= N) U = nullptr;  // the last block has no update
+  if (!P && !U) return FX_OK;
+  PfPanelArgs pa{};
+  PfUpdateArgs ua{};
+  pa.N = N;
+  if (P) {
+    pa.M = rp == 0 && P->A ? P->A : P->M;
+    pa.r0 = rp;
+    pa.nch = nch;
+    pa.full = rp == 0 && P->A;
+    pa.d = P->d;
+    pa.nsw = P->nsw;
+    pa.src = P->src;
+    pa.Gn = P->G;
+    pa.orig = P->orig;
+    pa.gbuf = P->gbuf;
+    pa.batch = P->batch;
+  }
+  if (U) {
+    constexpr int TU = PF_UPDATE_TILE;
+    const int nt = (N - ru - PB + TU - 1) / TU;
+    ua.M = U->M;
+    ua.r1 = ru + PB;
+    ua.ntiles = nt * (nt + 1) / 2;
+    ua.src = U->src;
+    ua.Gn = U->G;
+    ua.Min = ru == 0 ? U->A : nullptr;
+    ua.batch = U->batch;
+  }
+  if (PB == PFB) return step_launch<2, PFB>(pa, ua, s);
+  if (PB == PFB_XL) return step_launch<4, PFB_XL>(pa, ua, s);
+  if (PB == PFB_XXL) return step_launch<8, PFB_XXL>(pa, ua, s);
+  return FX_ERR_UNSUPPORTED;
+}
+
 // Forward (and, with gbuf/dout/perm, the factors: gbuf (B, N/PB, N, PB) by original row,
 // d (B, N/2), perm (B, N) final position -> original row).
 int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign, float* logabs,
@@ -675,15 +931,76 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     const int64_t tot = batch * N;
     hipLaunchKernelGGL(pf_iota_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, orig, N, tot);
   }
-  for (int r0 = 0; r0 < N;) {
-    const float* A0 = direct && r0 == 0 ? A : nullptr;
-    const int PB = pf_block_width(N, r0);
-    const int st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
-                   : PB == PFB ? pf_block<PFB, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
-                   : PB == PFB_XL ? pf_block<PFB_XL, 4>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
-                                  : pf_block<PFB_XXL, 8>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
+  const int maxw = pf_max_width(N);
+  const fx_tune& tn = tune();
+  const int64_t hb = (batch + 1) / 2;
+  const bool overlap = batch >= 2 && hb <= tn.pf_overlap_max_half &&
+                       (double)batch * N * N >= (double)tn.pf_overlap_min_work * (1 << 20);
+  if (!overlap) {
+    for (int r0 = 0; r0 < N;) {
+      const float* A0 = direct && r0 == 0 ? A : nullptr;
+      const int PB = pf_block_width(N, r0);
+      const int st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                     : PB == PFB ? pf_block<PFB, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                     : PB == PFB_XL ? pf_block<PFB_XL, 4>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                                    : pf_block<PFB_XXL, 8>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
+      if (st != FX_OK) return st;
+      r0 += PB;
+    }
+  } else {
+    // Small batches of large matrices (fx_tune.pf_overlap_*) run as two halves a and b, b
+    // one panel behind: each launch holds one half's panels and the other half's update
+    // (pf_step_kernel), so the panels (one latency-bound workgroup per matrix, on few
+    // CUs) run beside the updates (HBM-bound) where the whole batch would alternate
+    // between the two:
+    //   P(a, 0); P(b, 0) + U(a, 0); P(a, 1) + U(b, 0); P(b, 1) + U(a, 1); ...
+    // Every kernel works per matrix, so the results are the same bits. The update part
+    // runs in the panel's workgroup shape (1024 threads, 128 registers, one workgroup
+    // per CU), about 70 % as fast as pf_update_kernel, so the overlap pays where half an
+    // update takes about as long as a panel: measured B = 64, n = 2048 9.06 -> 8.76 ms,
+    // B = 16, n = 4096 28.5 -> 27.0 ms, B = 4, n = 8192 102.5 -> 94.6 ms; B = 8 or 128,
+    // n = 2048 lose (panels or updates alone dominate).
+    PfPart part[2];
+    for (int h = 0; h < 2; ++h) {
+      const int64_t b0 = h * hb;
+      part[h] = PfPart{M0 + b0 * NN, d + b0 * (N / 2), nsw + b0 * nch, src + b0 * N, Gn + b0 * N * maxw,
+                       orig ? orig + b0 * N : nullptr, gbuf ? gbuf + b0 * NN : nullptr,
+                       direct ? A + b0 * NN : nullptr, h ? batch - b0 : hb};
+    }
+    // the pipeline covers the blocks whose panels run 1024 threads (a CU each) and whose
+    // next block does too; the later blocks, whose panels take longer than half an
+    // update, run whole-batch
+    auto wide = [&](int r0) {
+      const int PB = pf_block_width(N, r0);
+      return r0 < N && N - r0 > 512 * pf_rows(PB) && PB * pf_rows(PB) <= 64 && pf_block_width(N, r0 + PB) == PB;
+    };
+    int st = FX_OK, r0 = 0;
+    if (wide(0)) {
+      const int PB = pf_block_width(N, 0);
+      st = pf_pair(N, nch, &part[0], 0, nullptr, 0, PB, s);
+      for (; st == FX_OK;) {
+        const int r1 = r0 + PB;
+        st = pf_pair(N, nch, &part[1], r0, &part[0], r0, PB, s);
+        if (st != FX_OK) break;
+        if (!wide(r1)) {
+          st = pf_pair(N, nch, nullptr, 0, &part[1], r0, PB, s);
+          r0 = r1;
+          break;
+        }
+        st = pf_pair(N, nch, &part[0], r1, &part[1], r0, PB, s);
+        r0 = r1;
+      }
+    }
+    for (; r0 < N && st == FX_OK;) {
+      const float* A0 = direct && r0 == 0 ? A : nullptr;
+      const int PB = pf_block_width(N, r0);
+      st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+           : PB == PFB ? pf_block<PFB, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+           : PB == PFB_XL ? pf_block<PFB_XL, 4>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                          : pf_block<PFB_XXL, 8>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
+      r0 += PB;
+    }
     if (st != FX_OK) return st;
-    r0 += PB;
   }
   hipLaunchKernelGGL(pf_finish_kernel, dim3((unsigned)((batch + 3) / 4)), dim3(256), 0, s, d, nsw, N / 2, nch,
                      sign, logabs, batch);

@@ -26,7 +26,17 @@
 //    4.56 -> 4.41; slogpf fwd + grad 1-4 %;
 //  - f64_reg_max_n 128 / f64_strip16_max_n 64: float64 matrices in registers for
 //    n <= 128 (slogdet n = 128 8.66 -> 3.16 ms against the LDS kernel), in 16-column strips
-//    for n <= 64 (n = 64 1.37 ms; at n = 128 they lose, 3.97 against 3.16 ms).
+//    for n <= 64 (n = 64 1.37 ms; at n = 128 they lose, 3.97 against 3.16 ms);
+//  - pf_overlap_max_half 32 / pf_overlap_min_work 256: the Parlett-Reid halves with one
+//    half's panels beside the other's update gain where half an update takes about as
+//    long as a panel (slogpf B = 64, n = 2048 9.06 -> 8.76 ms; B = 16, n = 4096 28.5 ->
+//    27.0; B = 4, n = 8192 102.5 -> 94.6) and lose where either dominates (B = 8 or 128,
+//    n = 2048: 3.79 -> 4.88, 15.2 -> 17.4 ms);
+//  - lu_split_min_work 128: the LU's halves on two streams (tails of one half's kernels
+//    beside the other's) gain from batch * N^2 >= 2^27 (slogdet + A^-T B = 1024, n = 512
+//    5.54 -> 5.37 ms; B = 16, n = 4096 38.9 -> 36.7) and lose below (B = 256, n = 512
+//    slogdet 0.88 -> 0.92 ms; B = 16, n = 2048 6.30 -> 6.54) and above N = 4096 (B = 4,
+//    n = 8192 153.3 -> 154.7).
 #include <atomic>
 #include <deque>
 #include <mutex>
@@ -52,7 +62,9 @@ constexpr fx_tune GFX950 = {
     /* gemm128_x3_tout */ 1,
     /* f64_reg_max_n */ 128,
     /* f64_strip16_max_n */ 64,
-    /* reserved */ {0, 0, 0},
+    /* pf_overlap_max_half */ 32,
+    /* pf_overlap_min_work */ 256,
+    /* lu_split_min_work */ 128,
 };
 
 // Every table an override publishes is kept, unchanged, until the process ends (a few
@@ -73,14 +85,13 @@ const fx_tune* publish(const fx_tune& t) {
 
 bool valid(const fx_tune& t) {
   auto in = [](int32_t v, int32_t lo, int32_t hi) { return v >= lo && v <= hi; };
-  for (int32_t r : t.reserved)
-    if (r != 0) return false;
   return in(t.fused_max_n, TINY_MAXN, 128) && in(t.lu_pair_above_n, 0, 1 << 30) &&
          in(t.lu_direct_max_n, 0, 1024) && in(t.pf_block64_min_n, 128, 1 << 30) &&
          in(t.pf_block64_max_m, 0, 1024) && in(t.gemm128_min_mn, 128, 1 << 30) &&
          in(t.gemm128_min_k, 64, 1 << 30) && in(t.gemm128_tout, 0, 1) &&
          in(t.gemm128_x3_min_mn, 128, 1 << 30) && in(t.gemm128_x3_min_k, 64, 1 << 30) && in(t.gemm128_x3_tout, 0, 1) && in(t.f64_reg_max_n, 0, 128) &&
-         in(t.f64_strip16_max_n, 0, 64);
+         in(t.f64_strip16_max_n, 0, 64) && in(t.pf_overlap_max_half, 0, 1 << 30) &&
+         in(t.pf_overlap_min_work, 0, 1 << 30) && in(t.lu_split_min_work, 0, 1 << 30);
 }
 
 }  // namespace

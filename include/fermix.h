@@ -130,7 +130,16 @@ typedef struct fx_tune {
    * larger n runs one workgroup per matrix in LDS or in the workspace */
   int32_t f64_reg_max_n;
   int32_t f64_strip16_max_n;
-  int32_t reserved[3]; /* zero */
+  /* blocked float32 Parlett-Reid: the batch runs as two halves, each launch holding one
+   * half's 1024-thread panels beside the other half's trailing update, when a half holds
+   * at most pf_overlap_max_half matrices and batch * N^2 >= pf_overlap_min_work * 2^20
+   * (the same bits as unsplit). >= 0 / >= 0 */
+  int32_t pf_overlap_max_half;
+  int32_t pf_overlap_min_work;
+  /* blocked float32 LU of padded order N <= 4096: batches of at least two matrices with
+   * batch * N^2 >= lu_split_min_work * 2^20 run as two halves on two streams (the same
+   * bits as unsplit); 0 never. >= 0 */
+  int32_t lu_split_min_work;
 } fx_tune;
 
 /* The table of an architecture ("gfx950"; FX_ERR_UNSUPPORTED for any other name: the

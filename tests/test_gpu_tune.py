@@ -182,3 +182,48 @@ def test_f64_override(dev, n):
         assert np.max(np.abs(_np(g) - inv)) / np.max(np.abs(inv)) < 1e-10, ov
         pl64 = 0.5 * np.linalg.slogdet(S)[1]
         assert np.all(np.abs(pl - pl64) < 1e-9 * np.maximum(1, np.abs(pl64))), ov
+
+
+def _vals_and_grad(fn, A):
+    X = A.clone().requires_grad_(True)
+    s, l = fn(X)
+    (g,) = torch.autograd.grad(l.sum(), X)
+    return s.detach(), l.detach(), g
+
+
+@pytest.mark.parametrize("n,B", [(300, 5), (640, 8), (1100, 3)])
+def test_lu_split_halves_bit_identical(dev, n, B):
+    """The LU's two batch halves on two streams (lu_split_min_work) give the unsplit bits:
+    values and A^-T, odd batches (unequal halves) included; and meet the float64 bar."""
+    A = _mats(n, B, 7400 + n)
+    At = _t(A, dev)
+    print(f"lu split n={n} B={B}", flush=True)
+    with _tune.override(lu_split_min_work=0):
+        ref = _vals_and_grad(fermix_amd.slogdet, At)
+    with _tune.override(lu_split_min_work=1):
+        out = _vals_and_grad(fermix_amd.slogdet, At)
+    for a, b in zip(ref, out):
+        assert torch.equal(a, b)
+    s64, l64 = ref64.slogdet64(A)
+    assert np.array_equal(_np(out[0]), s64)
+    assert_logabs(_np(out[1]), l64, n, "split", A)
+
+
+@pytest.mark.parametrize("n,B", [(1100, 3), (2100, 3), (4200, 2)])
+def test_pf_overlap_halves_bit_identical(dev, n, B):
+    """The Parlett-Reid halves with one half's panels beside the other half's update in each
+    launch (pf_overlap_*: 32-, 16- and 8-column blocks, N <= 2048 / 4096 / above) give the
+    unsplit bits: values, and S^-1 through the gradient; odd batches (unequal halves)
+    included; values against float64 (log|pf| = log|det| / 2)."""
+    A = _mats(n, B, 7500 + n)
+    S = (A - A.transpose(0, 2, 1)).astype(np.float32)
+    St = _t(S, dev)
+    print(f"pf overlap n={n} B={B}", flush=True)
+    with _tune.override(pf_overlap_max_half=0):
+        ref = _vals_and_grad(lambda X: fermix_amd.slogpf(X), St)
+    with _tune.override(pf_overlap_max_half=1 << 20, pf_overlap_min_work=0):
+        out = _vals_and_grad(lambda X: fermix_amd.slogpf(X), St)
+    for a, b in zip(ref, out):
+        assert torch.equal(a, b)
+    _, l64 = ref64.slogdet64(S)
+    assert_logabs(_np(out[1]), 0.5 * l64, n, "overlap", S)

@@ -41,7 +41,7 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_calls():
     L = _lib.lib()
-    assert L.fx_abi_version() == 202
+    assert L.fx_abi_version() == 203
     assert L.fx_status_string(0) == b"ok"
     assert L.fx_lu_padded_size(100) == 112
     assert L.fx_pf_padded_size(128) == 128
@@ -303,13 +303,15 @@ def test_tuning_override():
         dict(f64_reg_max_n=256),
         dict(f64_strip16_max_n=128),
         dict(lu_pair_above_n=-1),
+        dict(pf_overlap_max_half=-1),
+        dict(lu_split_min_work=-1),
     ):
         with pytest.raises(_lib.FermixLibraryError):
             _tune.set_override(dataclasses.replace(base, **bad))
         assert _tune.active() == base
     t = _lib.FxTune()
     assert L.fx_tune_active(t) == 0
-    t.reserved[2] = 1
+    t.pf_overlap_min_work = -1
     assert L.fx_tune_override(t) == 1 and _tune.active() == base
 
 
