@@ -17,8 +17,9 @@ fold into the kernels' batch, so vmap(f)(x) runs exactly the arithmetic of f(x))
   adjugate pf(S) S^-1 from the forward's own Parlett-Reid factors (finite for singular
   S); G is skew, so it is also the gradient w.r.t. ``a`` through S = (a - a^T)/2.
 
-float64 and complex inputs, and float32 above the float32 blocked kernels (n > 8192,
-where no packed factors are exported), take the parts route (A^-T / S^-1 formed with the
+float64 and complex inputs, and float32 where the field-generic kernels run (the LU above
+fx_tune.lu_generic_above_n, everything above 8192; no packed factors are exported
+there), take the parts route (A^-T / S^-1 formed with the
 primal by the field-generic blocked kernels); for complex kinds the sign is differentiable too, with
 the reference's conventions (see _log_tangents below). Their det derivative is the exact
 adjugate of the same Gauss-Jordan run (fx_det_parts_f64 / _c64 / _c128); their pf
@@ -243,7 +244,8 @@ def slogdet(A, x3=DEFAULT_X3):
     if _wants_grad(A):
         # n <= 32: one Gauss-Jordan pass forms A^-T with the factors; forward mode and
         # torch.func transforms: the parts call (their rules run on wrapped tensors)
-        if A.dtype == torch.float32 and 32 < A.shape[-1] <= _tune.LARGE_MAX_N and _plain_reverse(A):
+        if (A.dtype == torch.float32 and 32 < A.shape[-1] <= _tune.LARGE_MAX_N and _plain_reverse(A)
+                and _tune.kernel_family(A.shape[-1], "slogdet") != "generic"):
             s, l, _, _ = _SlogdetSplit.apply(A, x3)
         else:
             s, l, _ = _SlogdetParts.apply(A, x3)
@@ -356,7 +358,8 @@ def slogpf(A, skew, x3=DEFAULT_X3):
     update is memory-bound and runs in fp32 in both modes)."""
     if _wants_grad(A):
         n = A.shape[-1]
-        if A.dtype == torch.float32 and 0 < n <= _tune.LARGE_MAX_N and n % 2 == 0 and _plain_reverse(A):
+        if (A.dtype == torch.float32 and 0 < n <= _tune.LARGE_MAX_N and n % 2 == 0 and _plain_reverse(A)
+                and _tune.kernel_family(n, "slogpf") != "generic"):
             s, l, _, _, _ = _SlogpfSplit.apply(A, skew, x3)
         else:
             s, l, _ = _SlogpfParts.apply(A, skew, x3)

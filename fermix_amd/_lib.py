@@ -17,7 +17,7 @@ FX_PREC_MASK = 0x0F
 FX_LU_BLOCK_64 = 0x100
 FX_LU_BLOCK_128 = 0x200
 
-# fields of struct fx_tune, in order (int32 each)
+# fields of struct fx_tune, in order (int32 each; 3 reserved int32 follow)
 TUNE_FIELDS = (
     "fused_max_n",
     "lu_pair_above_n",
@@ -35,13 +35,14 @@ TUNE_FIELDS = (
     "pf_overlap_max_half",
     "pf_overlap_min_work",
     "lu_split_min_work",
+    "lu_generic_above_n",
 )
 
 
 class FxTune(ctypes.Structure):
     """struct fx_tune of include/fermix.h."""
 
-    _fields_ = [(f, ctypes.c_int32) for f in TUNE_FIELDS]
+    _fields_ = [(f, ctypes.c_int32) for f in TUNE_FIELDS] + [("reserved", ctypes.c_int32 * 3)]
 
 
 _p = ctypes.c_void_p

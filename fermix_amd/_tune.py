@@ -147,6 +147,8 @@ class Tune:
     # blocked float32 LU (N <= 4096): two halves on two streams for batch * N^2 >=
     # lu_split_min_work * 2^20 (0: never)
     lu_split_min_work: int = 128
+    # float32 LU: n above this runs the field-generic blocked kernels ("generic" family)
+    lu_generic_above_n: int = 4096
 
 
 # per-architecture tables (the library holds gfx950 code only)
@@ -233,7 +235,7 @@ GENERIC_MAX_N = 16384
 # reference's OVERRIDE, src/fermix/_common.py:363-378, which its tests use to force a
 # dispatch path, tests/test_fermix.py:720-762).
 ENV = "FERMIX_AMD_KERNELS"
-FAMILIES = {"tiny": "tiny-wave", "fused": "fused-lds", "blocked": "blocked"}
+FAMILIES = {"tiny": "tiny-wave", "fused": "fused-lds", "blocked": "blocked", "generic": "generic"}
 
 
 def _fused_max():
@@ -243,6 +245,13 @@ def _fused_max():
         return min(table().fused_max_n, SMALL_MAX_N)
 
 
+def _lu_generic_above():
+    try:
+        return active().lu_generic_above_n
+    except Exception:  # library not built: the table's value
+        return table().lu_generic_above_n
+
+
 def kernel_family(n, op="slogdet"):
     """Name of the kernel family the library runs for order n ("slogdet" / "slogpf", the
     same for their gradients), honouring the family override and the tuning values in
@@ -250,17 +259,20 @@ def kernel_family(n, op="slogdet"):
     forced = os.environ.get(ENV, "")
     if forced in FAMILIES:
         if n > LARGE_MAX_N:
-            return "generic" if forced == "blocked" and n <= GENERIC_MAX_N else "unsupported"
+            return "generic" if forced in ("blocked", "generic") and n <= GENERIC_MAX_N else "unsupported"
         ok = {
             "tiny": n <= TINY_MAX_N[op],
             "fused": TINY_MAX_N[op] < n <= SMALL_MAX_N,
             "blocked": True,
+            "generic": n > SMALL_MAX_N,
         }[forced]
         return FAMILIES[forced] if ok else "unsupported"
     if n <= TINY_MAX_N[op]:
         return "tiny-wave"
     if n <= _fused_max():
         return "fused-lds"
+    if op == "slogdet" and n > _lu_generic_above() and n <= GENERIC_MAX_N:
+        return "generic"
     if n <= LARGE_MAX_N:
         return "blocked"
     if n <= GENERIC_MAX_N:
@@ -270,7 +282,7 @@ def kernel_family(n, op="slogdet"):
 
 @contextlib.contextmanager
 def force_family(family):
-    """Force a kernel family ("tiny", "fused" or "blocked") for the calls made inside the
+    """Force a kernel family ("tiny", "fused", "blocked" or "generic") for the calls made inside the
     block (a size the family does not cover then raises FermixLibraryError). Sets the
     library's environment variable for the process and restores it on exit."""
     if family not in FAMILIES:

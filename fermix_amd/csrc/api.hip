@@ -83,6 +83,7 @@ static int family_override() {
   if (!strcmp(e, "tiny")) return FAM_TINY;
   if (!strcmp(e, "fused")) return FAM_FUSED;
   if (!strcmp(e, "blocked")) return FAM_BLOCKED;
+  if (!strcmp(e, "generic")) return FAM_GENERIC;
   return FAM_NONE;
 }
 
@@ -91,12 +92,13 @@ static int family(int n, int tiny_max, int large_max) {
   if (n <= 0 || n > GEN32_MAXN) return FAM_NONE;
   if (n > large_max) {
     const int o = family_override();
-    return o == FAM_NONE || o == FAM_BLOCKED ? FAM_GENERIC : FAM_NONE;
+    return o == FAM_NONE || o == FAM_BLOCKED || o == FAM_GENERIC ? FAM_GENERIC : FAM_NONE;
   }
   switch (family_override()) {
     case FAM_TINY: return n <= tiny_max ? FAM_TINY : FAM_NONE;
     case FAM_FUSED: return (n > tiny_max && n <= SMALL_MAX) ? FAM_FUSED : FAM_NONE;
     case FAM_BLOCKED: return FAM_BLOCKED;
+    case FAM_GENERIC: return n > SMALL_MAX ? FAM_GENERIC : FAM_NONE;
     default: break;
   }
   if (n <= tiny_max) return FAM_TINY;
@@ -104,7 +106,11 @@ static int family(int n, int tiny_max, int large_max) {
   return n <= fused_max ? FAM_FUSED : FAM_BLOCKED;
 }
 
-static int lu_family(int n) { return family(n, TINY_MAXN, LARGE_MAX); }
+// The LU's own blocked kernels stop at fx_tune.lu_generic_above_n unless a family is forced.
+static int lu_family(int n) {
+  const int f = family(n, TINY_MAXN, LARGE_MAX);
+  return f == FAM_BLOCKED && n > tune().lu_generic_above_n && family_override() == FAM_NONE ? FAM_GENERIC : f;
+}
 static int pf_family(int n) { return family(n, PF_TINY_MAXN, PF_LARGE_MAX); }
 
 // Alignment contract of the ABI: every matrix-shaped or workspace pointer is 16-byte

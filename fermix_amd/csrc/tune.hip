@@ -36,7 +36,13 @@
 //    beside the other's) gain from batch * N^2 >= 2^27 (slogdet + A^-T B = 1024, n = 512
 //    5.54 -> 5.37 ms; B = 16, n = 4096 38.9 -> 36.7) and lose below (B = 256, n = 512
 //    slogdet 0.88 -> 0.92 ms; B = 16, n = 2048 6.30 -> 6.54) and above N = 4096 (B = 4,
-//    n = 8192 153.3 -> 154.7).
+//    n = 8192 153.3 -> 154.7);
+//  - lu_generic_above_n 4096: above it the float32 LU's panels of more than 4096 rows
+//    spill their registers, and the field-generic kernels' multi-workgroup panels win:
+//    slogdet n = 6144 83.5 -> 55.2 ms, n = 8192 138 -> 83 ms, slogdet + A^-T 90.0 -> 82.9 /
+//    146 -> 142 ms; at n = 4160 the forward wins (43.5 -> 35.6) and the gradient is even
+//    (52.8 / 54.0). The Parlett-Reid keeps its own kernels to 8192 (its generic path is
+//    1.7-4x slower there).
 #include <atomic>
 #include <deque>
 #include <mutex>
@@ -65,6 +71,8 @@ constexpr fx_tune GFX950 = {
     /* pf_overlap_max_half */ 32,
     /* pf_overlap_min_work */ 256,
     /* lu_split_min_work */ 128,
+    /* lu_generic_above_n */ 4096,
+    /* reserved */ {0, 0, 0},
 };
 
 // Every table an override publishes is kept, unchanged, until the process ends (a few
@@ -85,13 +93,16 @@ const fx_tune* publish(const fx_tune& t) {
 
 bool valid(const fx_tune& t) {
   auto in = [](int32_t v, int32_t lo, int32_t hi) { return v >= lo && v <= hi; };
+  for (int32_t r : t.reserved)
+    if (r != 0) return false;
   return in(t.fused_max_n, TINY_MAXN, 128) && in(t.lu_pair_above_n, 0, 1 << 30) &&
          in(t.lu_direct_max_n, 0, 1024) && in(t.pf_block64_min_n, 128, 1 << 30) &&
          in(t.pf_block64_max_m, 0, 1024) && in(t.gemm128_min_mn, 128, 1 << 30) &&
          in(t.gemm128_min_k, 64, 1 << 30) && in(t.gemm128_tout, 0, 1) &&
          in(t.gemm128_x3_min_mn, 128, 1 << 30) && in(t.gemm128_x3_min_k, 64, 1 << 30) && in(t.gemm128_x3_tout, 0, 1) && in(t.f64_reg_max_n, 0, 128) &&
          in(t.f64_strip16_max_n, 0, 64) && in(t.pf_overlap_max_half, 0, 1 << 30) &&
-         in(t.pf_overlap_min_work, 0, 1 << 30) && in(t.lu_split_min_work, 0, 1 << 30);
+         in(t.pf_overlap_min_work, 0, 1 << 30) && in(t.lu_split_min_work, 0, 1 << 30) &&
+         in(t.lu_generic_above_n, 128, LU_LARGE_MAXN);
 }
 
 }  // namespace

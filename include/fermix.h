@@ -25,15 +25,20 @@
  *  - the return value is a status code (FX_OK on success); numerical edge cases are
  *    encoded in the values (an exactly zero pivot gives sign 0 and logabs -inf);
  *  - calls are reentrant; the library keeps no mutable global state apart from the
- *    once-per-device address of the scratch array of fx_slogdet_f32_noalloc and the
+ *    once-per-device address of the scratch array of fx_slogdet_f32_noalloc, the
+ *    once-per-device second stream (and its two events) on which the blocked LU runs
+ *    half of a large batch (ordered after the caller's stream and joined back to it
+ *    before the call returns; held under a per-device lock while in use) and the
  *    tuning-table override of fx_tune_override;
  *  - the kernel family is chosen from n alone (never from the batch): several matrices
  *    per wave (n <= 32 for slogdet, 16 for slogpf), one fused workgroup per matrix
  *    (n <= fx_tune.fused_max_n, 128 in the gfx950 table), blocked kernels with workspace
- *    (n <= 8192 for float32); the blocked kernels' own choices follow the tuning table below, whose
+ *    (float32: the Parlett-Reid to n = 8192, the LU to fx_tune.lu_generic_above_n, 4096,
+ *    then the field-generic blocked kernels to 16384); the blocked kernels' own choices follow the tuning table below, whose
  *    fx_tune_override is the reference's OVERRIDE hook. The environment variable
- *    FERMIX_AMD_KERNELS = tiny | fused | blocked, read on every call, forces a family
- *    where it covers n (FX_ERR_UNSUPPORTED elsewhere); the padded orders, block widths
+ *    FERMIX_AMD_KERNELS = tiny | fused | blocked | generic, read on every call, forces a
+ *    family where it covers n (generic: the field-generic blocked kernels that run
+ *    float32 above 8192, for any n > 128; FX_ERR_UNSUPPORTED elsewhere); the padded orders, block widths
  *    and workspace sizes reported below follow it, so query them under the same setting
  *    as the call (a test hook like the reference's OVERRIDE, src/fermix/_common.py:
  *    363-378).
@@ -140,6 +145,12 @@ typedef struct fx_tune {
    * batch * N^2 >= lu_split_min_work * 2^20 run as two halves on two streams (the same
    * bits as unsplit); 0 never. >= 0 */
   int32_t lu_split_min_work;
+  /* float32 LU (slogdet, det and their gradients): n > lu_generic_above_n runs the
+   * field-generic blocked kernels (multi-workgroup panels, fp64 MFMA products) in place
+   * of the float32 blocked ones, whose register panels spill for very tall panels (the
+   * reference's lu_generic_above_n, src/fermix/_common.py:126,211-281). 128 .. 8192 */
+  int32_t lu_generic_above_n;
+  int32_t reserved[3]; /* zero */
 } fx_tune;
 
 /* The table of an architecture ("gfx950"; FX_ERR_UNSUPPORTED for any other name: the
@@ -174,15 +185,16 @@ int32_t fx_pf_padded_size(int32_t n);
  * sign[b], logabs[b] of det(a[b]) for b < batch: sign exactly +1 / -1, or 0 with
  * logabs = -inf for an exactly zero pivot. Sizes: the float64 and complex entry points
  * cover 0 <= n <= 8192, the float32 ones 0 <= n <= 16384, and return FX_ERR_UNSUPPORTED
- * above. float32 above n = 4096: the LU panels spill registers and the Parlett-Reid
- * blocks are 8 columns wide (latency-bound; the trailing updates and GEMMs are those of
- * the smaller orders); above n = 8192: the field-generic blocked kernels of the float64
- * path on float storage (32-column panels, the trailing products in fp64 on the MFMA,
- * prec without effect), for the values and the parts runs (fx_slogdet_parts_f32 with
- * zero_singular and no lu / perm, fx_det_parts_f32, fx_slogpf_parts_f32); the packed
- * factor exports and their inverses (fx_slogdet_factors_f32, fx_slogdet_inverse_f32,
- * fx_slogpf_factors_f32, fx_slogpf_inverse_f32, fx_lu_padded_size, fx_pf_padded_size)
- * stop at 8192.
+ * above. float32 above n = 4096: the Parlett-Reid blocks are 8 columns wide (latency-bound;
+ * the trailing updates and GEMMs are those of the smaller orders); the LU above
+ * fx_tune.lu_generic_above_n (4096) and the Parlett-Reid above 8192 run the field-generic
+ * blocked kernels of the float64 path on float storage (32-column panels, tall ones on
+ * several workgroups per matrix, the trailing products in fp64 on the MFMA, prec without
+ * effect), for the values and the parts runs (fx_slogdet_parts_f32 with zero_singular and
+ * no lu / perm, fx_det_parts_f32, fx_slogpf_parts_f32); the packed factor exports and
+ * their inverses (fx_slogdet_factors_f32, fx_slogdet_inverse_f32, fx_lu_padded_size:
+ * above lu_generic_above_n; fx_slogpf_factors_f32, fx_slogpf_inverse_f32,
+ * fx_pf_padded_size: above 8192) return FX_ERR_UNSUPPORTED / 0 / -1 there.
  * Replaces `_lu_core` (src/fermix/_lu.py:543-611) as called by `_slogdet_core`
  * (src/fermix/_diff.py:42-49); kernels K1-K4 of the reference (_lu.py:54-393). */
 size_t fx_slogdet_f32_workspace(int64_t batch, int32_t n);

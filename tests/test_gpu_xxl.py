@@ -1,5 +1,6 @@
 """GPU parity above n = 4096 (the float32 blocked kernels up to n = 8192: LU panels of
-8192 rows, 8-column Parlett-Reid blocks), forward and gradients, against float64 truth
+8192 rows -- forced, the LU's default there being the field-generic kernels -- and
+8-column Parlett-Reid blocks), forward and gradients, against float64 truth
 formed on the GPU in float64 (slogdet by torch.linalg; the inverses through their float64
 residuals M X - I, which bound the relative error of X as M^-1). The inputs are well
 conditioned (I + N(0, 1/(4n)), and X J X^T for the Pfaffian, whose value is det(X) pf(J) =
@@ -11,7 +12,7 @@ import pytest
 import torch
 
 import fermix_amd
-from fermix_amd import _kernels
+from fermix_amd import _kernels, _tune
 from tests.tolerances import assert_logabs
 
 pytestmark = pytest.mark.gpu
@@ -39,13 +40,19 @@ def _jmat(n, dev):
     return J
 
 
-@pytest.mark.parametrize("n,prec", [(4160, "bf16x3"), (4160, "ieee"), (8192, "bf16x3")])
-def test_slogdet_xxl(dev, n, prec):
+@pytest.mark.parametrize("n,prec,family", [(4160, "bf16x3", None), (4160, "ieee", "blocked"), (8192, "bf16x3", None),
+                                           (8192, "bf16x3", "blocked")])
+def test_slogdet_xxl(dev, n, prec, family):
+    """Above lu_generic_above_n (4096) the LU runs the field-generic kernels; family
+    "blocked" keeps the float32 blocked LU (panels of up to 8192 rows) under test."""
+    if family:
+        with _tune.force_family(family):
+            return test_slogdet_xxl(dev, n, prec, None)
     B = 2
     A64 = _near_identity(dev, B, n, 9600 + n)
     A64[1, :, n // 3] = 0.0  # exact zero pivot
     A = A64.to(torch.float32)
-    print(f"slogdet xxl n={n} prec={prec}", flush=True)
+    print(f"slogdet xxl n={n} prec={prec} family={_tune.kernel_family(n)}", flush=True)
     s, l = fermix_amd.slogdet(A, prec=prec)
     s64, l64 = torch.linalg.slogdet(A.to(torch.float64))
     assert torch.equal(s.cpu().to(torch.float64), s64.cpu())

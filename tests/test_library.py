@@ -128,6 +128,18 @@ def test_tune_table():
     assert _tune.kernel_family(128) == "fused-lds"
     assert _tune.kernel_family(32) == "tiny-wave" and _tune.kernel_family(32, "slogpf") == "fused-lds"
     assert _tune.kernel_family(8192, "slogpf") == "blocked" and _tune.kernel_family(8193) == "generic"
+    # the LU's own blocked kernels stop at lu_generic_above_n (4096), the Parlett-Reid's at 8192
+    assert _tune.kernel_family(4096) == "blocked" and _tune.kernel_family(4097) == "generic"
+    assert _tune.kernel_family(4097, "slogpf") == "blocked"
+    L = _lib.lib()
+    assert L.fx_lu_padded_size(4096) == 4096 and L.fx_lu_padded_size(4097) == -1 and L.fx_pf_padded_size(4098) > 0
+    with _tune.override(lu_generic_above_n=8192):
+        assert _tune.kernel_family(4097) == "blocked" and L.fx_lu_padded_size(4097) > 0
+    with _tune.force_family("blocked"):
+        assert _tune.kernel_family(6000) == "blocked" and L.fx_lu_padded_size(6000) > 0
+    with _tune.force_family("generic"):
+        assert _tune.kernel_family(200) == "generic" and _tune.kernel_family(100) == "unsupported"
+        assert L.fx_lu_padded_size(200) == -1 and L.fx_slogdet_f32_workspace(2, 200) > 0
     assert _tune.kernel_family(16384) == "generic" and _tune.kernel_family(16385) == "unsupported"
 
 
@@ -305,13 +317,15 @@ def test_tuning_override():
         dict(lu_pair_above_n=-1),
         dict(pf_overlap_max_half=-1),
         dict(lu_split_min_work=-1),
+        dict(lu_generic_above_n=64),
+        dict(lu_generic_above_n=8193),
     ):
         with pytest.raises(_lib.FermixLibraryError):
             _tune.set_override(dataclasses.replace(base, **bad))
         assert _tune.active() == base
     t = _lib.FxTune()
     assert L.fx_tune_active(t) == 0
-    t.pf_overlap_min_work = -1
+    t.reserved[2] = 1
     assert L.fx_tune_override(t) == 1 and _tune.active() == base
 
 
