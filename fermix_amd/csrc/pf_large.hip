@@ -7,7 +7,7 @@
 // pair steps; PB = 64 once the trailing order m = N - r0 is at most 1024 for N >= 512 a
 // multiple of 64, else 32; 16 above N = 2048, 8 above N = 4096) at r0:
 //   1. pf_panel_kernel (one workgroup of NT = 256..1024 threads per matrix, each lane
-//      owning R = 2 or 4 of the m = N - r0 rows): the pair steps with the tau / w vectors
+//      owning R = 1, 2, 4 or 8 of the m = N - r0 rows): the pair steps with the tau / w vectors
 //      kept in registers as G (m x PB); column a and column p of the current matrix are read
 //      as rows of the block-start matrix (skew) plus the G corrections; each pair step
 //      has two workgroup barriers (the row at position c, the pivot). The permutation is
@@ -933,6 +933,11 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
   }
   const int maxw = pf_max_width(N);
   const fx_tune& tn = tune();
+  // 64-column blocks (m <= 1024): one row per lane (up to 1024 threads, G[1][64]) where the
+  // batch leaves CUs idle, two (half the threads, G[2][64]) where it fills the device:
+  // slogpf B = 16, n = 1024 1.455 -> 1.375 ms, B = 256, n = 1024 3.70 -> 3.57 ms, B = 64,
+  // n = 2048 8.37 -> 8.28 ms; B = 1024, n = 512 2.57 -> 2.84 ms (the same bits)
+  const bool rows1 = batch <= device_cus();
   const int64_t hb = (batch + 1) / 2;
   const bool overlap = batch >= 2 && hb <= tn.pf_overlap_max_half &&
                        (double)batch * N * N >= (double)tn.pf_overlap_min_work * (1 << 20);
@@ -940,7 +945,9 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     for (int r0 = 0; r0 < N;) {
       const float* A0 = direct && r0 == 0 ? A : nullptr;
       const int PB = pf_block_width(N, r0);
-      const int st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+      const int st =
+          PB == PFB_L ? (rows1 ? pf_block<PFB_L, 1>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                               : pf_block<PFB_L, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s))
                      : PB == PFB ? pf_block<PFB, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
                      : PB == PFB_XL ? pf_block<PFB_XL, 4>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
                                     : pf_block<PFB_XXL, 8>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
@@ -994,7 +1001,8 @@ int launch_pf_large(const float* A, int n, int skew, int64_t batch, float* sign,
     for (; r0 < N && st == FX_OK;) {
       const float* A0 = direct && r0 == 0 ? A : nullptr;
       const int PB = pf_block_width(N, r0);
-      st = PB == PFB_L ? pf_block<PFB_L, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+      st = PB == PFB_L ? (rows1 ? pf_block<PFB_L, 1>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
+                                : pf_block<PFB_L, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s))
            : PB == PFB ? pf_block<PFB, 2>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
            : PB == PFB_XL ? pf_block<PFB_XL, 4>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s)
                           : pf_block<PFB_XXL, 8>(M0, N, r0, nch, batch, d, nsw, src, Gn, orig, gbuf, A0, s);
