@@ -40,6 +40,10 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int GBK = 16;
 
+// Word 3 of a raw buffer descriptor on gfx9 (untyped 32-bit data, range-checked offsets).
+constexpr int BUF_RSRC_WORD3 = 0x00020000;
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
 // Element (r, c) of op(X) in the mask's global coordinates.
 __device__ __forceinline__ float mask_val(float v, int mask, int r, int c) {
   if (mask == MASK_LOWER_UNIT) return r > c ? v : (r == c ? 1.0f : 0.0f);
@@ -591,31 +595,46 @@ __global__ __launch_bounds__(256, X3 ? 2 : 4) void gemm128_kernel(GemmDesc d) {
     float a[2][4], b[2][4], s[4];
   };
   X3Regs rg0;
+  // The stage loads are raw buffer loads: each operand's base and extent in a descriptor
+  // (scalar registers), the thread's fixed byte offset in a vector register and the
+  // stage's row offset in a scalar one, so a load costs no address arithmetic and no
+  // clamp. A read past the operand's last element returns 0 (the descriptor's range
+  // check); whatever lies past M, N or K inside it, the edge path of put_x3 zeroes.
+  const unsigned extA = (unsigned)(TA ? (d.K - 1) * d.lda + d.M : (d.M - 1) * d.lda + d.K) * 4u;
+  const unsigned extB = (unsigned)((d.K - 1) * d.ldb + d.N) * 4u;
+  const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)extA, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)B, 0, (int)extB, BUF_RSRC_WORD3);
+  const int xkw = __builtin_amdgcn_readfirstlane(xk);  // wave-uniform
+  int oa[2], ob[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    oa[e] = 4 * (TA ? xkw * d.lda + xia[e] : aoff[e] + ka);
+    ob[e] = 4 * (xkw * d.ldb + xjb[e]);
+  }
   auto load_x3 = [&](int k0, X3Regs& R) {
     if (!TA) {
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        const float4 x = *reinterpret_cast<const float4*>(A + aoff[e] + min(k0 + ka, d.K - 4));
-        R.a[e][0] = x.x;
-        R.a[e][1] = x.y;
-        R.a[e][2] = x.z;
-        R.a[e][3] = x.w;
+        const v4u x = __builtin_amdgcn_raw_buffer_load_b128(rA, oa[e], 4 * k0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) R.a[e][r] = __uint_as_float(x[r]);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float* ar = A + min(k0 + xk + r, d.K - 1) * d.lda;
-        R.a[0][r] = ar[xia[0]];
-        R.a[1][r] = ar[xia[1]];
+        const int so = 4 * (k0 + r) * d.lda;
+        R.a[0][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rA, oa[0], so, 0));
+        R.a[1][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rA, oa[1], so, 0));
       }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int kr = min(k0 + xk + r, d.K - 1);
       if (BS) R.s[r] = d.bscale[bat * (d.K / 2) + (kr >> 1)];
-      const float* br = B + (BS ? kr ^ 1 : kr) * d.ldb;
-      R.b[0][r] = br[xjb[0]];
-      R.b[1][r] = br[xjb[1]];
+      // row k0 + xk + r (BS: its pair partner, (xk + r) ^ 1 as k0 and xk are even)
+      const int so = 4 * (k0 + (BS ? r ^ 1 : r)) * d.ldb;
+      R.b[0][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rB, ob[0], so, 0));
+      R.b[1][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rB, ob[1], so, 0));
     }
   };
   // the stage's masks: each operand's triangle only where its stage meets the diagonal,
