@@ -662,9 +662,9 @@ __global__ __launch_bounds__(NT) void pf_step_kernel(PfPanelArgs pa, PfUpdateArg
                               blockIdx.x);
     return;
   }
-  // The update workgroups (nU = gridDim.x - pa.batch, each holding a CU) are persistent:
-  // in iteration k, group sub of workgroup w updates the NL tiles ((k nU + w) NS + sub) NL
-  // + l. The loop keeps two stages per group in flight: stage k + 1's old entries (and,
+  // The update workgroups (the ids from pa.batch on, each holding a CU) are persistent: in
+  // iteration k, group sub of the w-th of the nU update workgroups of one XCD updates the
+  // NL tiles ((k nU + w) NS + sub) NL + l of that XCD's matrices. The loop keeps two stages per group in flight: stage k + 1's old entries (and,
   // where the registers hold them, stage k + 2's G rows) are loaded while stage k is
   // finished (LDS double-buffered; two barriers per iteration, the trip count uniform
   // over the workgroup). In the 128 registers of a 1024-thread workgroup: NL = 1, the G
@@ -677,15 +677,23 @@ __global__ __launch_bounds__(NT) void pf_step_kernel(PfPanelArgs pa, PfUpdateArg
   __shared__ __align__(16) float lds[2][NS * NL][2 * PBu * (T + 4)];
   __shared__ int sp[2][NS * NL][T], sq[2][NS * NL][T], smv[2][NS * NL][T / 4];
   const int sub = threadIdx.x >> 8, tid = threadIdx.x & 255;
-  const int64_t w = (int64_t)blockIdx.x - pa.batch, nU = (int64_t)gridDim.x - pa.batch;
-  const int64_t tot = ua.batch * ua.ntiles;
+  // Workgroups go to the XCDs round-robin by id, so the update workgroups with id = x mod
+  // 8 take the matrices b = x mod 8: a matrix's tiles then meet in one XCD's L2, which
+  // fetches its G rows once (spread over the XCDs, every L2 fetched them: 1.48x the
+  // matrix's read traffic at 32-column blocks).
+  const int x8 = (int)(blockIdx.x & 7);
+  const int64_t g_first = pa.batch + ((x8 - pa.batch % 8) + 8) % 8;  // first update id on XCD x8
+  const int64_t nU = ((int64_t)gridDim.x - g_first + 7) / 8, w = ((int64_t)blockIdx.x - g_first) / 8;
+  const int64_t nbx = (ua.batch - x8 + 7) / 8;  // matrices x8, x8 + 8, ...
+  const int64_t tot = nbx * ua.ntiles;
   const int64_t iters = (tot + nU * NS * NL - 1) / (nU * NS * NL);
   auto tile = [&](int64_t k, int l) {
     const int64_t f = ((k * nU + w) * NS + sub) * NL + l;
     const bool act = k < iters && f < tot;
-    const int64_t b = act ? f / ua.ntiles : 0;
+    const int64_t bx = act ? f / ua.ntiles : 0;
+    const int64_t b = x8 + 8 * bx;
     const int buf = (int)(k & 1), slot = sub * NL + l;
-    return PfTile<PBu, T>(ua.r1, b, act ? (int)(f - b * ua.ntiles) : 0, act, lds[buf][slot], sp[buf][slot],
+    return PfTile<PBu, T>(ua.r1, act ? b : 0, act ? (int)(f - bx * ua.ntiles) : 0, act, lds[buf][slot], sp[buf][slot],
                           sq[buf][slot], smv[buf][slot]);
   };
   if (iters == 0) return;
