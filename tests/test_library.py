@@ -385,3 +385,16 @@ def test_complex_entry_points_host_checks():
         sync = 2 * al(4 * 4) + al(4 * 2 * G * 8) + al(4 * 2 * G * 4) + al(4 * 2 * G * 32 * fz) + al(4 * 2 * 32 * fz)
         assert w == al(4 * 320 * 320 * fz) + al(4 * 320 * 4) + al(4 * 320 * fz) + al(4 * 10 * 4) + sync
         assert getattr(L, f"fx_slogdet_parts_{k}_workspace")(4, 300) == w + al(4 * 320 * 320 * fz) + al(4 * 4)
+
+
+def test_tune_struct_layout():
+    """The ctypes mirror of struct fx_tune has the header's fields in the header's order
+    and the same size (fx_tune_table writes the whole struct)."""
+    hdr = open(os.path.join(os.path.dirname(__file__), "..", "include", "fermix.h")).read()
+    body = re.search(r"typedef struct fx_tune \{(.*?)\} fx_tune;", hdr, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = re.findall(r"int32_t\s+(\w+)(?:\[(\d+)\])?;", body)
+    names = [f for f, n in fields if not n]
+    count = sum(int(n) if n else 1 for _, n in fields)
+    assert tuple(names) == _lib.TUNE_FIELDS
+    assert ctypes.sizeof(_lib.FxTune) == 4 * count
