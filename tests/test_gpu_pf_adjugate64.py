@@ -58,8 +58,6 @@ def test_pf_adjugate_regular(dev, kind, n):
     """pf(S) S^-1 against float64 / complex128; the primal bit-identical to the plain
     slogpf forward; the pf gradient (autograd, with skew_symmetrize on a skew input) is
     -pf(S) S^-1 / 2, conjugated for the complex kinds, and the jvp is sum(G * dS)."""
-    if kind == "c128" and n > 130:
-        pytest.skip("complex128 at n = 256 adds run time without a new code path")
     dt, tol = KINDS[kind]
     rng = np.random.default_rng(9300 + n)
     S = _near_j(rng, 3, n, dt)
@@ -214,8 +212,6 @@ def test_pf_adjugate_numerically_singular(dev, kind, n):
     formula. Entries against minor Pfaffians, G[i][j] = (-1)^(i+j) pf(S without i, j) for
     i < j, at the largest entries and at random ones; S G = pf(S) I ~ 0 and G skew; the
     regular member against pf(S) S^-1 in float64 / complex128."""
-    if kind == "c128" and n > 130:
-        pytest.skip("complex128 at n = 256 adds run time without a new code path")
     dt, tol = KINDS[kind]
     rng = np.random.default_rng(9700 + n)
     S = np.stack([_rank_deficient_xjx(rng, n, dt), _near_j(rng, 1, n, dt)[0]])
