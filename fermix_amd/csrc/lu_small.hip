@@ -14,8 +14,8 @@
 //   * wave 0 factors the m x 16 panel in registers (lane l owns rows R*l .. R*l+R-1):
 //     pivot = largest |a| among the unassigned rows (ties: lowest row), found with a
 //     DPP max over order-preserving integer keys; rows are pivoted virtually inside
-//     the panel and written back in the new order; it also forms X = L11^-1 (lane c
-//     holds column c) and the map src[new position] = old row;
+//     the panel and written back in the new order; it then forms X = L11^-1 from the
+//     stored L11 (lane c holds column c) and the map src[new position] = old row;
 //   * the trailing 16-column strips are gathered through src, U12 = X * A12 and
 //     A22 -= L21 * U12 run on fp32 MFMA 16x16x4, and the strip is stored in the new row
 //     order (each strip is read completely before it is written, and strips own
@@ -57,7 +57,6 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
 #pragma unroll
     for (int j = 0; j < 16; ++j) a[i][j] = valid[i] ? As[row * LDA + r0 + j] : 0.0f;
   }
-  float xcol[16];
   static_for<0, 16>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     const int posc = r0 + j;
@@ -71,9 +70,11 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
     const unsigned gk = wave_max_u32(kb);
     const int pl = first_lane(kb == gk);
     const int is = readlane_i(ib, pl);
-    // the pivot row (wave-uniform: `is` and `pl` are scalars), selected without branching
+    // the pivot row's columns j .. 15 (wave-uniform: `is` and `pl` are scalars), selected
+    // without branching; its columns < j (row j of L11) are read back from LDS for X after
+    // the panel, so no scalar register holds them across the step
     float u[16];
-    static_for<0, 16>([&](auto cc) {
+    static_for<j, 16>([&](auto cc) {
       float v = a[0][cc.value];
 #pragma unroll
       for (int i = 1; i < R; ++i) v = (is == i) ? a[i][cc.value] : v;
@@ -103,12 +104,8 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
         });
       }
     }
-    // row j of X = L11^-1: X[j][c] = -sum_{k<j} L11[j][k] X[k][c], X[j][j] = 1
-    float x = 0.0f;
-    static_for<0, j>([&](auto kc) { x = fmaf(-u[kc.value], xcol[kc.value], x); });
-    xcol[j] = (lane == j) ? 1.0f : x;
   });
-  // write the panel back in the new row order, the position map and X
+  // write the panel back in the new row order and the position map
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     if (valid[i]) {
@@ -117,9 +114,22 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
       src[pos[i]] = R * lane + i;
     }
   }
-  if (lane < 16) {
+  wave_lds_fence();
+  // X = L11^-1 from the unit lower L11 just stored (lane c holds column c):
+  // X[j][c] = -sum_{k<j} L11[j][k] X[k][c] in order of k, X[j][j] = 1
+  {
+    const float* L11 = As + r0 * LDA + r0;
+    float xcol[16];
+    static_for<0, 16>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      float x = 0.0f;
+      static_for<0, j>([&](auto kc) { x = fmaf(-L11[j * LDA + kc.value], xcol[kc.value], x); });
+      xcol[j] = (lane == j) ? 1.0f : x;
+    });
+    if (lane < 16) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) X[k * 16 + lane] = xcol[k];
+      for (int k = 0; k < 16; ++k) X[k * 16 + lane] = xcol[k];
+    }
   }
   if (FACT) {
     int pv[R];
