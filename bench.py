@@ -36,7 +36,10 @@ def _parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    # 100 untimed steps by default: after an idle period the GPU's clocks ramp up over the
+    # first ~60 steps of the n = 128 workloads (C2 0.1925 -> 0.1813 ms/step over the first
+    # 60 steps after 5 warm-up steps), so a short warm-up times the ramp, not the kernel
+    p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--only", default=None, help="comma list of workloads (c1,c2,c3,c4; f64 adds the float64 "
                    "n = 128 workloads, blk the blocked float64 / complex ones at n = 512, xxl the B = 1 "
