@@ -51,8 +51,9 @@ static_assert(PfSmall<128>::LDS_BYTES <= 40960, "four n = 128 workgroups per CU"
 // Start of row p of the strictly lower triangle (a 24-bit multiply: one VALU
 // instruction per lane).
 __device__ __forceinline__ int tri_row(int p) { return (int)(__umul24((unsigned)p, (unsigned)(p - 1)) >> 1); }
-// The same for a wave-uniform p (a scalar multiply, without the 24-bit operand masks).
-__device__ __forceinline__ int tri_row_u(int p) { return (p * (p - 1)) >> 1; }
+// Byte offset of row p: 4 p (p - 1) / 2 = p (2 p - 2), formed as one shift-add and one 24-bit
+// multiply (p (p - 1) is even, so no rounding or masking is involved).
+__device__ __forceinline__ unsigned tri_row_b(int p) { return __umul24((unsigned)p, (unsigned)(2 * p - 2)); }
 
 // Index of G element (row s, column k) in Gs.
 template <int N>
@@ -101,7 +102,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
   }
   // M[row][q] of the block-start matrix for the lane's rows (value for row == q unused)
   auto column = [&](int q, float (&v)[R]) {
-    const int q4 = 4 * q, roq4 = 4 * tri_row_u(q);
+    const int q4 = 4 * q, roq4 = q * (2 * q - 2);  // 4 tri_row(q)
 #pragma unroll
     for (int i = S0; i < R; ++i) {
       const bool below = row4[i] > q4;
@@ -413,23 +414,21 @@ __device__ __forceinline__ void pf_update(float* T, const float* Gs, const unsig
     unsigned sp4;
     float raw[4];
     float4 ga, gb;
-    unsigned below;
   };
   auto read_src = [&](Tile& x) {
     x.sp4 = *reinterpret_cast<const unsigned*>(src + x.P0 + 4 * g);
     x.sq = src[x.Q0 + li];
     x.sr = src[x.P0 + li];
   };
+  const char* const Tb = reinterpret_cast<const char*>(T);
   auto read_old = [&](Tile& x) {
-    x.below = 0;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       // branch-free addressing: the entry lives in the row of the larger index
       const int sv = (x.sp4 >> (8 * v)) & 0xFF;
       const int hi = max(sv, x.sq), lo = min(sv, x.sq);
       // p == q (diagonal tiles; never stored) may address T[NTRI], the first entry of Gs
-      x.raw[v] = T[tri_row(hi) + lo];
-      x.below |= (sv > x.sq ? 1u : 0u) << v;
+      x.raw[v] = *reinterpret_cast<const float*>(Tb + tri_row_b(hi) + 4 * lo);
     }
     x.ga = *reinterpret_cast<const float4*>(Gs + g_idx<N>(x.sr, 4 * g));
     x.gb = *reinterpret_cast<const float4*>(Gs + g_idx<N>(x.sq, 4 * g));
@@ -437,26 +436,29 @@ __device__ __forceinline__ void pf_update(float* T, const float* Gs, const unsig
   // MFMA step u contracts k = 4 g + u, so each lane's A and B operands are one 16-byte G
   // row group; (J G^T)[k] = G[k+1] (k even), -G[k-1] (k odd)
   auto finish = [&](const Tile& x) {
+    // the entry is stored at (row, column) when its row index is the larger, else negated
     v4f acc;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] = ((x.below >> v) & 1) ? x.raw[v] : -x.raw[v];
+    for (int v = 0; v < 4; ++v) acc[v] = (int)((x.sp4 >> (8 * v)) & 0xFF) > x.sq ? x.raw[v] : -x.raw[v];
     acc = mfma16(x.ga.x, x.gb.y, acc);
     acc = mfma16(x.ga.y, -x.gb.x, acc);
     acc = mfma16(x.ga.z, x.gb.w, acc);
     acc = mfma16(x.ga.w, -x.gb.z, acc);
     const int q = x.Q0 + li;
     const int p0 = x.P0 + 4 * g;
-    const int e0 = tri_row(p0) + q;  // tri_row(p0 + v) = tri_row(p0) + v p0 + v (v - 1) / 2
+    // tri_row(p0 + v) = tri_row(p0) + v p0 + v (v - 1) / 2, in bytes
+    char* const e0 = reinterpret_cast<char*>(T) + tri_row_b(p0) + 4 * q;
+    auto st = [&](int off, float val) { *reinterpret_cast<float*>(e0 + off) = val; };
     if (x.P0 != x.Q0) {
-      T[e0] = acc[0];
-      T[e0 + p0] = acc[1];
-      T[e0 + 2 * p0 + 1] = acc[2];
-      T[e0 + 3 * p0 + 3] = acc[3];
+      st(0, acc[0]);
+      st(4 * p0, acc[1]);
+      st(8 * p0 + 4, acc[2]);
+      st(12 * p0 + 12, acc[3]);
     } else {
-      if (p0 > q) T[e0] = acc[0];
-      if (p0 + 1 > q) T[e0 + p0] = acc[1];
-      if (p0 + 2 > q) T[e0 + 2 * p0 + 1] = acc[2];
-      if (p0 + 3 > q) T[e0 + 3 * p0 + 3] = acc[3];
+      if (p0 > q) st(0, acc[0]);
+      if (p0 + 1 > q) st(4 * p0, acc[1]);
+      if (p0 + 2 > q) st(8 * p0 + 4, acc[2]);
+      if (p0 + 3 > q) st(12 * p0 + 12, acc[3]);
     }
   };
   for (int t = wv; t < ntiles; t += 8) {
