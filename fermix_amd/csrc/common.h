@@ -27,11 +27,12 @@ constexpr int WAVE = 64;
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
-// Order-preserving key of a pivot candidate: |x| as unsigned bits plus one, 0 for "not a
-// candidate". Non-negative floats order like their bit patterns, so an integer max over
-// keys is an exact max over magnitudes (the +1 lifts |x| = 0 above "no candidate").
+// Order-preserving key of a pivot candidate: the bits of |x| with the top bit set (one OR:
+// setting the sign bit of x gives the same word), 0 for "not a candidate". Non-negative
+// floats order like their bit patterns, so an integer max over keys is an exact max over
+// magnitudes, and the top bit lifts |x| = 0 above "no candidate".
 __device__ __forceinline__ unsigned cand_key(float x, bool ok) {
-  return ok ? (__float_as_uint(fabsf(x)) + 1u) : 0u;
+  return ok ? (__float_as_uint(x) | 0x80000000u) : 0u;
 }
 
 template <int CTRL>
