@@ -35,7 +35,9 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 def _parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
+    # 200 timed steps by default: 20-step windows of the n = 128 workloads scatter by
+    # 2-4 % with the GPU's clock (0.1745-0.1826 ms/step for C2 in one process)
+    p.add_argument("--steps", type=int, default=200)
     # 100 untimed steps by default: after an idle period the GPU's clocks ramp up over the
     # first ~60 steps of the n = 128 workloads (C2 0.1925 -> 0.1813 ms/step over the first
     # 60 steps after 5 warm-up steps), so a short warm-up times the ramp, not the kernel
