@@ -138,7 +138,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
       static_for<0, U>([&](auto wc) {
         constexpr int u = decltype(wc)::value;
         v[i] = fmaf(G[i][2 * u], gq[2 * u + 1], v[i]);
-        v[i] = fmaf(-G[i][2 * u + 1], gq[2 * u], v[i]);
+        v[i] = fmaf(G[i][2 * u + 1], -gq[2 * u], v[i]);
       });
     }
   };
@@ -223,7 +223,7 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
 #pragma unroll
         for (int i = S0; i < R; ++i) {
           x[i] = fmaf(G[i][2 * t], h1, xn[i]);
-          x[i] = fmaf(-G[i][2 * t + 1], h0, x[i]);
+          x[i] = fmaf(G[i][2 * t + 1], -h0, x[i]);
         }
         qa = qn;
       } else {
@@ -445,7 +445,8 @@ __device__ __forceinline__ void pf_update(float* T, const float* Gs, const unsig
     acc = mfma16(x.ga.z, x.gb.w, acc);
     acc = mfma16(x.ga.w, -x.gb.z, acc);
     const int q = x.Q0 + li;
-    const int p0 = x.P0 + 4 * g;
+    int p0 = x.P0 + 4 * g;
+    asm volatile("" : "+v"(p0));  // no known-bits masking in front of the 24-bit multiply
     // tri_row(p0 + v) = tri_row(p0) + v p0 + v (v - 1) / 2, in bytes
     char* const e0 = reinterpret_cast<char*>(T) + tri_row_b(p0) + 4 * q;
     auto st = [&](int off, float val) { *reinterpret_cast<float*>(e0 + off) = val; };
@@ -455,10 +456,15 @@ __device__ __forceinline__ void pf_update(float* T, const float* Gs, const unsig
       st(8 * p0 + 4, acc[2]);
       st(12 * p0 + 12, acc[3]);
     } else {
-      if (p0 > q) st(0, acc[0]);
-      if (p0 + 1 > q) st(4 * p0, acc[1]);
-      if (p0 + 2 > q) st(8 * p0 + 4, acc[2]);
-      if (p0 + 3 > q) st(12 * p0 + 12, acc[3]);
+      // entries on or above the diagonal go to T[0] instead (M[1][0]: position 1 is
+      // finished before the first update, which starts at position 16, and never read
+      // again), so the stores need no per-element branch
+      char* const dead = reinterpret_cast<char*>(T);
+      auto sd = [&](bool keep, int off, float val) { *reinterpret_cast<float*>(keep ? e0 + off : dead) = val; };
+      sd(p0 > q, 0, acc[0]);
+      sd(p0 + 1 > q, 4 * p0, acc[1]);
+      sd(p0 + 2 > q, 8 * p0 + 4, acc[2]);
+      sd(p0 + 3 > q, 12 * p0 + 12, acc[3]);
     }
   };
   for (int t = wv; t < ntiles; t += 8) {
