@@ -155,13 +155,13 @@ __device__ __forceinline__ void lu_strip(float* As, int r0, int c0, const int* s
   const int col = c0 + li;
   float tb[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) tb[t] = As[src[r0 + 4 * t + g] * LDA + col];
+  for (int t = 0; t < 4; ++t) tb[t] = As[__umul24(src[r0 + 4 * t + g], LDA) + col];
   v4f ct[MAXT];
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     if (i < nt) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) ct[i][v] = As[src[r0 + 16 + 16 * i + 4 * g + v] * LDA + col];
+      for (int v = 0; v < 4; ++v) ct[i][v] = As[__umul24(src[r0 + 16 + 16 * i + 4 * g + v], LDA) + col];
     }
   }
   v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -170,15 +170,16 @@ __device__ __forceinline__ void lu_strip(float* As, int r0, int c0, const int* s
 #pragma unroll
   for (int v = 0; v < 4; ++v) As[(r0 + 4 * g + v) * LDA + col] = u[v];
   wave_lds_fence();
+  // -U12, negated once here rather than L21 in every product
   float ub[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) ub[t] = As[(r0 + 4 * t + g) * LDA + col];
+  for (int t = 0; t < 4; ++t) ub[t] = -As[(r0 + 4 * t + g) * LDA + col];
 #pragma unroll
   for (int i = 0; i < MAXT; ++i) {
     if (i < nt) {
       const int rb = r0 + 16 + 16 * i;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) ct[i] = mfma16(-As[(rb + li) * LDA + r0 + 4 * t + g], ub[t], ct[i]);
+      for (int t = 0; t < 4; ++t) ct[i] = mfma16(As[(rb + li) * LDA + r0 + 4 * t + g], ub[t], ct[i]);
 #pragma unroll
       for (int v = 0; v < 4; ++v) As[(rb + 4 * g + v) * LDA + col] = ct[i][v];
     }
@@ -199,7 +200,7 @@ __device__ __forceinline__ void lu_permute_strip(float* As, int r0, int c0, cons
 #pragma unroll
     for (int i = 0; i < MAXR; ++i) {
       const int p = r0 + g + 8 * i;
-      if (p < NR) v[i] = As[src[p] * LDA + col];
+      if (p < NR) v[i] = As[__umul24(src[p], LDA) + col];
     }
     wave_lds_fence();
 #pragma unroll
@@ -374,7 +375,7 @@ __global__ __launch_bounds__(256, 4) void lu_split_kernel(const float* __restric
     const int c = H + 16 * wave + li;
     auto elem = [&](int p) {
       const int r = perm[p];
-      return (r < n && c < n) ? Ab[r * n + c] : (r == c ? 1.0f : 0.0f);
+      return (r < n && c < n) ? Ab[__umul24(r, n) + c] : (r == c ? 1.0f : 0.0f);
     };
     v4f ap[NPH];
 #pragma unroll
@@ -385,19 +386,20 @@ __global__ __launch_bounds__(256, 4) void lu_split_kernel(const float* __restric
     for (int q = 0; q < NPS; ++q)
 #pragma unroll
       for (int v = 0; v < 4; ++v) Sc[q][v] = elem(H + 16 * q + 4 * g + v);
-    // U12 = L11^-1 (P A)12 block by block: U_s = X_s (A_s - sum_{t<s} L_st U_t)
-    v4f U[NPH];
+    // U12 = L11^-1 (P A)12 block by block: U_s = X_s (A_s - sum_{t<s} L_st U_t); the
+    // products take -U (nU, negated once per block) rather than -L in every product
+    v4f nU[NPH];
 #pragma unroll
     for (int s = 0; s < NPH; ++s) {
       v4f acc = ap[s];
 #pragma unroll
       for (int t = 0; t < s; ++t)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc = mfma16(-As[(16 * s + li) * LDH + 16 * t + 4 * g + v], U[t][v], acc);
+        for (int v = 0; v < 4; ++v) acc = mfma16(As[(16 * s + li) * LDH + 16 * t + 4 * g + v], nU[t][v], acc);
       v4f u = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int v = 0; v < 4; ++v) u = mfma16(Xall[s][li * 16 + 4 * g + v], acc[v], u);
-      U[s] = u;
+      nU[s] = -u;
       if (FACT) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) Lb[(16 * s + 4 * g + v) * N + c] = u[v];
@@ -410,7 +412,7 @@ __global__ __launch_bounds__(256, 4) void lu_split_kernel(const float* __restric
       for (int t = 0; t < NPH; ++t)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          Sc[q] = mfma16(-As[(H + 16 * q + li) * LDH + 16 * t + 4 * g + v], U[t][v], Sc[q]);
+          Sc[q] = mfma16(As[(H + 16 * q + li) * LDH + 16 * t + 4 * g + v], nU[t][v], Sc[q]);
   }
   __syncthreads();  // every wave is done with L
   if (wave < NPS) {
