@@ -638,7 +638,7 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
     // four 16-byte L21' reads per row block, one U12' row element per c.
     float uv[16];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) uv[c] = Wb[(int64_t)(rc + 16 * g + c) * N + cstart + col];
+    for (int c = 0; c < 16; ++c) uv[c] = -Wb[(int64_t)(rc + 16 * g + c) * N + cstart + col];  // -U12
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
       const float* Lr = Ls + (16 * s + li) * LDL + 16 * g;
@@ -652,7 +652,7 @@ __global__ __launch_bounds__(256, 4) void lu_urow_kernel(float* __restrict__ W, 
         lw[4 * q + 3] = t.w;
       }
 #pragma unroll
-      for (int c = 0; c < 16; ++c) a12[s] = mfma16(-lw[c], uv[c], a12[s]);
+      for (int c = 0; c < 16; ++c) a12[s] = mfma16(lw[c], uv[c], a12[s]);
     }
   }
   v4f U[NSUB];
