@@ -67,28 +67,30 @@ __device__ __forceinline__ void lu_panel(float* As, int r0, int* src, float* X, 
       const unsigned k = cand_key(a[i][j], valid[i] && pos[i] >= posc);
       if (k > kb) { kb = k; ib = i; }
     }
-    const unsigned gk = wave_max_u32(kb);
-    const int pl = first_lane(kb == gk);
-    const int is = readlane_i(ib, pl);
-    // the pivot row's columns j .. 15 (wave-uniform: `is` and `pl` are scalars), selected
-    // without branching; its columns < j (row j of L11) are read back from LDS for X after
-    // the panel, so no scalar register holds them across the step
-    float u[16];
+    // each lane's best slot's row (columns j .. 15) and position, selected before the
+    // reduction (off the dependency chain: the pivot lane's values are then one readlane
+    // away); the row's columns < j (row j of L11) are read back from LDS for X after the
+    // panel, so no scalar register holds them across the step
+    float brow[16];
+    int bpos = pos[0];
     static_for<j, 16>([&](auto cc) {
       float v = a[0][cc.value];
 #pragma unroll
-      for (int i = 1; i < R; ++i) v = (is == i) ? a[i][cc.value] : v;
-      u[cc.value] = readlane_f(v, pl);
+      for (int i = 1; i < R; ++i) v = (ib == i) ? a[i][cc.value] : v;
+      brow[cc.value] = v;
     });
-    int pv = pos[0];
 #pragma unroll
-    for (int i = 1; i < R; ++i) pv = (is == i) ? pos[i] : pv;
-    const int pp = readlane_i(pv, pl);
-    // swap positions posc <-> pp
+    for (int i = 1; i < R; ++i) bpos = (ib == i) ? pos[i] : bpos;
+    const unsigned gk = wave_max_u32(kb);
+    const int pl = first_lane(kb == gk);
+    float u[16];
+    static_for<j, 16>([&](auto cc) { u[cc.value] = readlane_f(brow[cc.value], pl); });
+    const int pp = readlane_i(bpos, pl);
+    // swap positions posc <-> pp (the pivot row is the pivot lane's best slot)
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       if (valid[i] && pos[i] == posc) pos[i] = pp;
-      if (lane == pl && i == is) pos[i] = posc;
+      if (lane == pl && i == ib) pos[i] = posc;
     }
     nsw += (pp != posc) ? 1 : 0;
     const float piv = u[j];
