@@ -79,6 +79,7 @@ def build(verbose=False, jobs=None, incremental=False):
     objs = [os.path.join(BUILD, os.path.basename(s)[:-4] + ".o") for s in srcs]
     headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
     headers.append(os.path.join(os.path.dirname(HERE), "include", "fermix.h"))
+    headers.append(os.path.abspath(__file__))  # the flags live here
     deps = max(os.path.getmtime(h) for h in headers if os.path.exists(h))
     todo = [(s, o) for s, o in zip(srcs, objs) if not incremental or _stale(s, o, deps)]
     jobs = jobs or min(max(1, len(todo)), max(1, (os.cpu_count() or 4)))
