@@ -165,16 +165,20 @@ __device__ __forceinline__ void pf_panel(const float* T, float* Gs, int r0, unsi
       key[i] = cand_key(x[i], pos[i] > c);
       kb = max(kb, key[i]);
     }
+    // the position of the lane's own candidate, selected before the reduction: on the
+    // pivot lane the winning slot is the lowest one holding the lane's maximum (if any
+    // row l < 64 holds the wave's maximum, the pivot is such a row; otherwise no slot-0
+    // key reaches it), so the pivot's position is one readlane once the lane is known
+    int bpos = pos[R - 1];
+#pragma unroll
+    for (int i = R - 2; i >= S0; --i) bpos = key[i] == kb ? pos[i] : bpos;
     const unsigned gk = wave_max_u32(kb);
     unsigned long long bp[R];
 #pragma unroll
     for (int i = S0; i < R; ++i) bp[i] = __ballot(key[i] == gk);
     const int qp = first_row<R, S0>(bp);
-    const int lp = qp & 63, sp = qp >> 6;
-    int pv = pos[S0];
-#pragma unroll
-    for (int i = S0 + 1; i < R; ++i) pv = (sp == i) ? pos[i] : pv;
-    const int pp = readlane_i(pv, lp);
+    const int lp = qp & 63;
+    const int pp = readlane_i(bpos, lp);
     float gp[16], y[R];
     grow(qp, gp, tc);
     column(qp, y);
