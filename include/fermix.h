@@ -4,8 +4,9 @@
  * This is the drop-in boundary for the hot path of ChenAo-Phys/fermix: each entry
  * point replaces the group of Pallas calls the reference issues through
  * `_pcall` (src/fermix/_field.py:357-389) for one role, cited per function below. The
- * reference binds its kernels inside JAX; the XLA FFI handler a maintainer would add on
- * top of this header is shown in INTEGRATION.md.
+ * reference binds its kernels inside JAX; a maintainer would bind this header from an
+ * XLA FFI handler (one typed-buffer handler per entry point, the stream taken from the
+ * call's platform stream).
  *
  * Conventions (all entry points):
  *  - matrices are row-major, contiguous, batch-major: a[b * n * n + i * n + j];

@@ -1,4 +1,4 @@
-"""GPU parity beyond the C4 regime: the LU path for
+"""GPU parity beyond the C4 regime (the larger orders): the LU path for
 1024 < n <= 4096 (panel factored in place in the work buffer) and the Parlett-Reid path
 for 2048 < n <= 4096 (16-column blocks), forward and gradients, against float64 truth.
 
